@@ -1,0 +1,34 @@
+"""Shared test helpers: build the oracle layer from the C1 golden fixture, tolerance checks."""
+import torch
+
+from oracle import moe_ref as R
+
+QUANT_CASES = ("normal", "outlier", "g32", "grid", "e20")
+LORA_NAMES = ("A_gate", "A_up", "A_down", "B_gate", "B_up", "B_down")
+
+
+def c1_layer(t, with_sel=True, deq_dtype=torch.float32) -> R.OracleLayer:
+    """The C1 layer exactly as tests/golden/make_golden.py handed it to the reference."""
+    frozen = {"gate_up": {k: t["bank.gate_up." + k] for k in ("q", "scale", "zero")},
+              "down": {k: t["bank.down." + k] for k in ("q", "scale", "zero")}}
+    L = R.OracleLayer(gate_w=t["in.gate_w"], frozen=frozen, int4=True, deq_dtype=deq_dtype, expert_group=32)
+    L.shared = {"gate_up": torch.cat((t["in.sh_gate"], t["in.sh_up"])), "down": t["in.sh_down"],
+                "gate_w": t["in.sh_gate_w"]}
+    if with_sel:
+        sel = t["in.sel_ids"]
+        L.sel_ids = sel.tolist()
+        L.sel_gate_up, L.sel_down = t["in.gate_up"][sel].clone(), t["in.down"][sel].clone()
+        L.ex_lora = {n: t["in.ex_" + n] for n in LORA_NAMES}
+        L.ex_scale = 2.0
+        L.sh_lora = {n: t["in.sh_" + n] for n in LORA_NAMES}
+        L.sh_scale = 2.0
+    return L
+
+
+def assert_close_bf16(out, ref, name="", rel=2e-2, cos=0.9999):
+    """The bf16 bar: ||out-ref||/||ref|| <= rel, max|out-ref| <= rel * max|ref| and cosine >= cos."""
+    e = R.rel_err(out, ref)
+    c = R.cosine(out, ref)
+    m = ((out.double() - ref.double()).abs().max() / ref.double().abs().max().clamp_min(1e-30)).item()
+    assert e <= rel and m <= rel and c >= cos, f"{name}: rel {e:.3e} max {m:.3e} cos {c:.6f}"
+    return e, m, c
