@@ -1,0 +1,169 @@
+/* C-ABI of the MI355X (gfx950) MoE-layer hot path of SMEL FT.
+ *
+ * Every entry point is stateless, allocates nothing, launches its kernels on the given HIP stream and never
+ * synchronizes the host. Pointers are device pointers unless noted; bf16 tensors are passed as uint16_t bit
+ * patterns. Return value: 0 on success, a positive hipError_t from the launch, or a negative SMEL_E* code for a
+ * rejected argument (smel_last_error() then holds a message; it is thread-local).
+ *
+ * Row space shared by the grouped GEMMs: rows [0, TK) are the routed slots in expert-sorted order (TK = T*topk),
+ * rows [TK, TK+T) are the shared expert's rows (one per token, token order) when the shared expert is fused in.
+ * order[row] is the flat slot p = t*topk + k of a routed row. "Groups" are the experts 0..E-1 plus, when present,
+ * the shared expert as group E; gkind[g] = (kind << 16) | index says where group g's weights live.
+ */
+#ifndef SMEL_MOE_H
+#define SMEL_MOE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMEL_EINVAL (-1)       /* bad pointer / size / stride */
+#define SMEL_EUNSUPPORTED (-2) /* shape outside what the kernels handle (message says which limit) */
+
+/* group kinds (gkind >> 16) */
+#define SMEL_KIND_INT4 0   /* frozen expert in the int4 bank (Int4Experts), index = expert id      */
+#define SMEL_KIND_BF16 1   /* frozen expert in a bf16 bank (BF16Experts), index = expert id        */
+#define SMEL_KIND_SEL 2    /* selected expert (bf16 copy + LoRA), index = slot j in sel_ids        */
+#define SMEL_KIND_SHARED 3 /* shared expert (bf16 + LoRA), index 0                                 */
+
+/* Weights of one projection (gate_up or down) for every group kind. Storage of one matrix is [R][C], C contiguous
+ * (gate_up: R = 2I, C = H; down: R = H, C = I), exactly the reference tensors. The forward GEMM contracts over C
+ * (out = x W^T), the backward GEMM over R (dx = dy W). */
+typedef struct smel_wset {
+  const uint8_t* q4;   /* int4 bank q  [E][R][C/2], low nibble = even column (smel/quant.py:42)     */
+  const uint16_t* s4;  /* int4 bank scale [E][R][C/group] bf16                                      */
+  const uint16_t* z4;  /* int4 bank zero  [E][R][C/group] bf16                                      */
+  const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down)                         */
+  const uint16_t* wsel;/* selected experts [n_sel][R][C] (LayerExperts.sel_gate_up / sel_down)      */
+  const uint16_t* wsh; /* shared expert [R][C]                                                      */
+  /* LoRA as a 32-wide K-extension of the GEMM (0-padded rank <= 16, built by smel_lora_prep):
+   *   forward  ext_*: [n][R][32]  (B factor per output row; gate_up: B_gate in cols 0..15, B_up in 16..31)
+   *   backward ext_*: [n][32][C]  (A factor rows; gate_up: A_gate rows 0..15, A_up rows 16..31) */
+  const uint16_t* ext_sel;
+  const uint16_t* ext_sh;
+  int64_t R, C;
+  int32_t group;       /* int4 group along C (a multiple of 32)                                        */
+  int32_t pad_;
+} smel_wset;
+
+const char* smel_last_error(void);
+int smel_abi_version(void);
+
+/* ---- (A7) replaces dequant_int4 / _dq4_kernel, smel/quant.py:51-84.
+ * q [rows][K/2], scale/zero [rows][K/group] -> out [rows][K]: w = RNE(q*s + z) (fp32 math). out_f32 = 1 writes fp32. */
+int smel_dequant_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, void* out, int64_t rows,
+                      int64_t K, int64_t group, int32_t out_f32, hipStream_t stream);
+
+/* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
+ * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the
+ * bf16-rounded logits), topv [T][K] bf16 (renormalised), topi [T][K] int64 and topi32 [T][K] int32 (descending,
+ * lower expert id first among equal logits), and, if shared_gate_w, sgate [T] fp32 = sigmoid(bf16(x . w_sg)). */
+int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T, int64_t H,
+               int64_t E, int64_t K, float* probs, uint16_t* topv, int64_t* topi, int32_t* topi32, float* sgate,
+               hipStream_t stream);
+
+/* Same selection from given bf16 logits [T][E] (bit-exact id checks against the CPU oracle). */
+int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, int64_t K, float* probs, uint16_t* topv,
+                      int64_t* topi, int32_t* topi32, hipStream_t stream);
+
+/* ---- (A3) replaces the dispatch of routed_experts, smel/moe.py:216-223 and the inverse of :249-250.
+ * ids [T*K] (int32 if ids_are_i64 == 0, else int64) -> counts [E], offsets [E+1], order [TK] (stable: experts
+ * ascending, slot p ascending within one), inv [TK], and the GEMM tile list: tiles [max_tiles][4] = {group, row0,
+ * row1, 0} over groups 0..E-1 (+ group E = shared rows [TK, TK+shared_rows) when shared_rows > 0), m_tile rows
+ * each; n_tiles [1] = how many are used. err [1] is set to 1 if an id is outside [0, E) (that slot is dropped).
+ * One workgroup; E <= 1024. */
+int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
+                  int32_t m_tile, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
+                  int32_t* n_tiles, int32_t* err, hipStream_t stream);
+/* Upper bound of the tile-list length for smel_dispatch (host-side, no GPU call). */
+int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared_rows, int32_t m_tile);
+
+/* ---- LoRA factor layouts (smel/lora.py:14-58 params, fp32) -> the bf16 K-extension operands.
+ * For n groups (n_sel selected slots, or 1 for the shared MLP) with rank r <= 16, hidden Hd, inter In, scale s:
+ *   fwd_gu  [n][2In][32]: B_gate in cols 0..r-1 of rows 0..In-1, B_up in cols 16..16+r-1 of rows In..2In-1
+ *   fwd_dn  [n][Hd][32] : B_down in cols 0..r-1
+ *   a_gu    [n][32][Hd] : A_gate rows 0..r-1, A_up rows 16..16+r-1   (XA = x a_gu^T; backward ext of gate_up)
+ *   a_dn    [n][32][In] : A_down rows 0..r-1                        (AD = act a_dn^T; backward ext of down)
+ *   bt_dn   [n][32][Hd] : B_down^T rows 0..r-1                       (DB = dy bt_dn^T)
+ *   bt_gu   [n][32][2In]: B_gate^T in rows 0..r-1 / cols 0..In-1, B_up^T in rows 16.. / cols In..2In-1
+ * Every other entry is 0. */
+int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, const float* B_up,
+                   const float* A_down, const float* B_down, int64_t n, int64_t r, int64_t Hd, int64_t In,
+                   uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
+                   uint16_t* bt_gu, hipStream_t stream);
+
+/* ---- (A11/A12) LoRA down-projections of the rows of LoRA groups (SEL / SHARED tiles of the tile list):
+ * ext[row][0:32] = bf16(scale_g * A_src[src(row)][0:Kd] . wcat_g[0:32][0:Kd]) where src(row) = token of the row if
+ * a_gather else row, wcat_g = wcat_sel + idx*32*Kd, scale_g = scale_sel (SEL) or wcat_sh, scale_sh (SHARED).
+ * Rows of other groups are left untouched. Kd must be a multiple of 32. */
+int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,
+                  const uint16_t* A_src, int64_t lda, int32_t a_gather, const int32_t* order, int64_t TK,
+                  int64_t topk, const uint16_t* wcat_sel, const uint16_t* wcat_sh, int64_t Kd, float scale_sel,
+                  float scale_sh, uint16_t* ext, hipStream_t stream);
+
+/* ---- (A5/A6/A11) grouped expert GEMM, forward: out = A W^T per group, W from w (int4 dequantized in registers,
+ * or bf16), plus the LoRA K-extension ext[row] . w.ext_*[n] for SEL/SHARED groups when ext != NULL.
+ * epilogue 0: out[slot(row)][n] = bf16(acc), n < R                                  (down projection)
+ * epilogue 1: gate/up pairs: g = bf16(acc[n]), u = bf16(acc[R/2 + n]), out[row][n] = bf16(act(g) u), n < R/2;
+ *             if hsave: hsave[row][n] = g, hsave[row][R/2 + n] = u                  (gate_up projection)
+ * A rows: A[token(row)] if a_gather else A[row]; K = w.C (multiple of 32). */
+int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
+                 int64_t max_tiles, const uint16_t* A, int64_t lda, int32_t a_gather, const int32_t* order,
+                 int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act, uint16_t* out,
+                 int64_t ldo, uint16_t* hsave, hipStream_t stream);
+
+/* ---- (A13) replaces the combine of routed_experts, smel/moe.py:248-252 (+ the shared add of :263):
+ * out[t] = bf16( sum_k fp32(topv[t,k]) * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Y[TK+t])] ), k in fixed order. */
+int smel_combine(const uint16_t* Y, const uint16_t* topv, const float* sgate, int64_t T, int64_t K, int64_t H,
+                 uint16_t* out, hipStream_t stream);
+
+/* ---- (A10/A11 backward) grouped GEMM, backward: acc = A W per group (contraction over w.R), int4 re-dequantized
+ * per group, plus ext[row] . w.ext_*[0:32][n] for SEL/SHARED groups when ext != NULL.
+ * epilogue 0: out[slot(row)][n] = bf16(acc), n < C                                   (dX of gate_up: dh W_gu)
+ * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] or sgate[t]; (g, u) = hsave[row];
+ *             out[row][n] = bf16(da u act'(g)), out[row][I+n] = bf16(da act(g));
+ *             dwp[row][blockIdx.y] = sum_n acc * bf16(act(g) u)   (d row weight, reduced later in fixed order)
+ * A rows: A[token(row)] if a_gather else A[row]; the GEMM K = w.R. */
+int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
+                 int64_t max_tiles, const uint16_t* A, int64_t lda, int32_t a_gather, const int32_t* order,
+                 int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
+                 const uint16_t* hsave, const uint16_t* topv, const float* sgate, uint16_t* out, int64_t ldo,
+                 float* dwp, hipStream_t stream);
+/* number of column blocks (dwp row width) smel_gmm_bwd uses for a given C */
+int64_t smel_gmm_bwd_nblocks(int64_t C);
+
+/* ---- (A15) router backward (autograd of route + renorm + the shared gate, smel/moe.py:162-167, 201):
+ * dtopv[t,k] = sum_j dwp[inv[t*K+k]][j]; d renorm; d gather; d softmax (probs) -> dlogits [T][ldl] bf16 with
+ * dlogits[t][E] = d shared-gate logit (sum_j dwp[TK+t][j] * sg (1-sg)) when sgate != NULL, zero padding to ldl.
+ * dtopv_out [T][K] fp32 (optional) receives dtopv. */
+int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs, const int32_t* topi32,
+                   const uint16_t* topv, const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK,
+                   uint16_t* dlogits, int64_t ldl, float* dtopv_out, hipStream_t stream);
+
+/* d(combine weight) of routed_experts when topv is an input: dtopv[p] = sum_j dwp[inv[p]][j], fp32 [TK]. */
+int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, float* dtopv, hipStream_t stream);
+
+/* ---- dX of the layer: dx[t] = bf16( sum_k DXS[t*K+k] + [DXS[TK+t]] + [DXR[t]] ), fixed order, fp32. */
+int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, int32_t with_shared, int64_t T, int64_t K, int64_t H,
+                   uint16_t* dx, hipStream_t stream);
+
+/* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP):
+ * for every LoRA group lora_groups[i] (expert id, or E for the shared rows [TK, TK+T)):
+ *   out[i][p][q] = sum_{rows of the group} alpha(row) * L[row][p] * Rm[src(row)][q],  p < 32, q < Q
+ * in a fixed order (rows in chunks of 256 into part, then the chunks in order). src(row) = token of the row if
+ * r_gather else row; alpha = the row weight (topv[p] / sgate[t]) if use_w, else 1.
+ * out [n_lora][32][Q] fp32; part [n_lora][part_chunks][32][Q] fp32 scratch with
+ * part_chunks = smel_lora_wgrad_part_chunks(max rows of one group). */
+int smel_lora_wgrad(const int32_t* lora_groups, int64_t n_lora, const int32_t* offsets, int64_t E, int64_t T,
+                    int64_t TK, int64_t topk, const int32_t* order, const uint16_t* L, const uint16_t* Rm,
+                    int64_t ldr, int32_t r_gather, int32_t use_w, const uint16_t* topv, const float* sgate,
+                    int64_t Q, float* part, int64_t part_chunks, float* out, hipStream_t stream);
+int64_t smel_lora_wgrad_part_chunks(int64_t max_group_rows);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,96 @@
+// Shared device helpers for the MoE-layer kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SMEL_DEV __device__ __forceinline__
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------------ bf16 <-> fp32
+SMEL_DEV float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+SMEL_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+SMEL_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 (gfx950 has a hardware conversion; NaN stays NaN).
+SMEL_DEV uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+SMEL_DEV uint32_t pack2bf(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// ------------------------------------------------------------------------------------------------ wave helpers
+SMEL_DEV int lane_id() { return __lane_id(); }
+
+SMEL_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+SMEL_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// sum over the 32 lanes that share lane/32 (the two halves of a wave reduce independently)
+SMEL_DEV float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ------------------------------------------------------------------------------------------------ MFMA
+// v_mfma_f32_32x32x16_bf16: lane l supplies A[i = l%32][k in K-set(l/32)] and B[k in K-set(l/32)][j = l%32]
+// (8 bf16 each); C lands as acc[r] = C[8*(r/4) + 4*(l/32) + r%4][l%32]. Which 8 k values a lane half carries is
+// our choice as long as A and B agree.
+SMEL_DEV f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+SMEL_DEV int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// ------------------------------------------------------------------------------------------------ int4 dequant
+// 8 nibbles of one uint32 (little-endian bytes; low nibble = even column) -> 4 packed bf16 pairs,
+// w = RNE_bf16(q*s + z) with fp32 arithmetic (q*s is exact, so fma and mul+add agree).
+SMEL_DEV void dq8(uint32_t b, float s, float z, uint32_t out[4]) {
+  const uint32_t lo = b & 0x0f0f0f0fu;          // columns 0,2,4,6
+  const uint32_t hi = (b >> 4) & 0x0f0f0f0fu;   // columns 1,3,5,7
+  out[0] = pack2bf(fmaf((float)(lo & 0xff), s, z), fmaf((float)(hi & 0xff), s, z));
+  out[1] = pack2bf(fmaf((float)((lo >> 8) & 0xff), s, z), fmaf((float)((hi >> 8) & 0xff), s, z));
+  out[2] = pack2bf(fmaf((float)((lo >> 16) & 0xff), s, z), fmaf((float)((hi >> 16) & 0xff), s, z));
+  out[3] = pack2bf(fmaf((float)(lo >> 24), s, z), fmaf((float)(hi >> 24), s, z));
+}
+
+// Nibble j (0..7) of b as float.
+SMEL_DEV float nib(uint32_t b, int j) { return (float)((b >> (4 * j)) & 0xfu); }
+
+// ------------------------------------------------------------------------------------------------ activations
+// act ids: 0 = silu, 1 = gelu_tanh (smel/moe.py:91-107)
+SMEL_DEV float act_f(float g, int act) {
+  if (act == 0) return g / (1.0f + __expf(-g));
+  const float c = 0.7978845608028654f;
+  const float t = tanhf(c * (g + 0.044715f * g * g * g));
+  return 0.5f * g * (1.0f + t);
+}
+SMEL_DEV void act_and_grad_f(float g, int act, float& a, float& da) {
+  if (act == 0) {
+    const float s = 1.0f / (1.0f + __expf(-g));
+    a = g * s;
+    da = s * (1.0f + g * (1.0f - s));
+    return;
+  }
+  const float c = 0.7978845608028654f;
+  const float t = tanhf(c * (g + 0.044715f * g * g * g));
+  a = 0.5f * g * (1.0f + t);
+  da = 0.5f * (1.0f + t) + 0.5f * g * (1.0f - t * t) * c * (1.0f + 3.0f * 0.044715f * g * g);
+}
+
+// ------------------------------------------------------------------------------------------------ row mapping
+// Rows of the grouped GEMMs: [0, TK) are the routed slots in expert-sorted order, [TK, TK + T) the shared expert
+// (one row per token, in token order). order[row] = flat slot p = t*K + k of a routed row.
+SMEL_DEV int row_token(int row, const int32_t* __restrict__ order, int TK, int topk) {
+  return row < TK ? order[row] / topk : row - TK;
+}
+SMEL_DEV int row_slot(int row, const int32_t* __restrict__ order, int TK) { return row < TK ? order[row] : row; }

@@ -1,0 +1,98 @@
+"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h).
+
+The library is the only compute path: if it is missing, or no GPU is visible, calls raise instead of falling back to
+anything else. Tensors go in as raw device pointers; every call runs on torch's current HIP stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmel_moe.so")
+
+KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
+
+vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
+
+
+class WSet(ctypes.Structure):
+    """smel_wset of include/smel_moe.h."""
+    _fields_ = [("q4", vp), ("s4", vp), ("z4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp), ("ext_sel", vp),
+                ("ext_sh", vp), ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "smel_last_error": (ctypes.c_char_p, []),
+    "smel_abi_version": (i32, []),
+    "smel_dequant_int4": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
+    "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp]),
+    "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
+    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
+    "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
+    "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i32, vp, i64, i64, vp, i32, i32, vp,
+                           i64, vp, vp]),
+    "smel_combine": (i32, [vp, vp, vp, i64, i64, i64, vp, vp]),
+    "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i32, vp, i64, i64, vp, i32, i32, vp,
+                           vp, vp, vp, i64, vp, vp]),
+    "smel_gmm_bwd_nblocks": (i64, [i64]),
+    "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, i64, vp, vp]),
+    "smel_dtopv": (i32, [vp, i64, vp, i64, vp, vp]),
+    "smel_dx_reduce": (i32, [vp, vp, i32, i64, i64, i64, vp, vp]),
+    "smel_lora_wgrad": (i32, [vp, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, i32, i32, vp, vp, i64, vp, i64, vp,
+                              vp]),
+    "smel_lora_wgrad_part_chunks": (i64, [i64]),
+}
+
+_lib = None
+
+
+class SmelError(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH):
+    """Load (once) and type the C-ABI library. Raises if it is missing: there is no other compute path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build the HIP extension first (python -c 'import __graft_entry__ as g; "
+                          f"g.build()')")
+    L = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def call(name: str, *args):
+    """Call an entry point that returns a status code; raise SmelError with the library's message on failure."""
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        msg = load().smel_last_error().decode(errors="replace")
+        raise SmelError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None):
+    """Device pointer of a tensor (None -> NULL). The tensor must stay alive for the duration of the launch."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def require_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("smel MoE kernels run on the GPU: every tensor must be on a cuda device")

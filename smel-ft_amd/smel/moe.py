@@ -1,0 +1,594 @@
+"""MoE layer of SMEL FT on MI355X kernels: the public API of the reference's smel/moe.py (drop-in for its callers,
+smel/layer_runner.py:243-291), every step a HIP kernel of libsmel_moe.so reached through the C-ABI.
+
+Forward (``moe_forward``): router (logits + softmax + top-k + renorm, and the shared-expert gate logit) -> stats hook ->
+stable counting-sort dispatch (device-side tile list, no host sync) -> LoRA down-projections of LoRA rows ->
+grouped gate_up GEMM (int4 dequant in registers / bf16 + LoRA K-extension, token gather fused, SiLU-gate epilogue)
+-> grouped down GEMM -> fixed-order fp32 combine of the K slots and the shared expert. The shared expert is the
+extra group E of the same grouped GEMMs (rows [TK, TK+T)).
+
+Backward: down-backward GEMM fused with the SiLU-gate backward, the topv / shared-gate scaling and the d(weight)
+partials -> gate_up-backward GEMM (int4 re-dequantized) -> router backward (renorm + softmax + shared gate) as a GEMM
+against the router weight -> fixed-order dX reduce; LoRA dA / dB as fixed-order row reductions. Bitwise
+run-to-run deterministic: no atomics anywhere.
+
+Differences from the reference's rounding points (all inside the bf16 tolerance): the LoRA scale is folded into the
+bf16 rank-r activations; LoRA terms accumulate in the same fp32 accumulator as the base GEMM; the combine adds the
+shared expert in fp32 before the single rounding; gradients are accumulated in fp32.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib as L
+from .quant import dequant_int4, quantize_int4
+
+M_TILE = 128      # rows per GEMM tile (the tile list of smel_dispatch)
+EXT = 32          # width of the LoRA K-extension (rank <= 16 for gate and up each)
+_ACT = {"silu": 0, "gelu_tanh": 1}
+_GELU_C = 0.7978845608028654
+
+
+# ------------------------------------------------------------------------------------------------ expert banks
+
+
+class BF16Experts:
+    """Frozen experts as fused 3-D tensors: gate_up [E, 2I, H], down [E, H, I] (smel/moe.py:18-32)."""
+
+    def __init__(self, gate_up: torch.Tensor, down: torch.Tensor):
+        self.gate_up, self.down = gate_up, down
+        self.num_experts = gate_up.shape[0]
+
+    def weights(self, e0: int, e1: int):
+        return self.gate_up[e0:e1], self.down[e0:e1]
+
+    def tensors(self):
+        return {"gate_up": self.gate_up, "down": self.down}
+
+    def nbytes(self):
+        return sum(t.numel() * t.element_size() for t in self.tensors().values())
+
+
+class Int4Experts:
+    """Frozen experts in group-wise int4 (smel/moe.py:35-55): dicts {"q", "scale", "zero"} for gate_up and down.
+    The grouped GEMMs read this format directly; ``weights`` (bf16 copies) exists for API compatibility only."""
+
+    def __init__(self, gu: dict, dn: dict, dtype=torch.bfloat16):
+        self.gu, self.dn, self.dtype = gu, dn, dtype
+        self.num_experts = gu["q"].shape[0]
+
+    @classmethod
+    def from_bf16(cls, gate_up, down, group=64):
+        return cls(quantize_int4(gate_up, group), quantize_int4(down, group), dtype=gate_up.dtype)
+
+    @staticmethod
+    def group_of(d: dict) -> int:
+        return d["q"].shape[-1] * 2 // d["scale"].shape[-1]
+
+    def weights(self, e0: int, e1: int):
+        gu = dequant_int4(self.gu["q"][e0:e1], self.gu["scale"][e0:e1], self.gu["zero"][e0:e1], self.dtype)
+        dn = dequant_int4(self.dn["q"][e0:e1], self.dn["scale"][e0:e1], self.dn["zero"][e0:e1], self.dtype)
+        return gu, dn
+
+    def tensors(self):
+        return {f"gate_up.{k}": v for k, v in self.gu.items()} | {f"down.{k}": v for k, v in self.dn.items()}
+
+    def nbytes(self):
+        return sum(t.numel() * t.element_size() for t in self.tensors().values())
+
+
+class LayerExperts:
+    """Routed experts of one layer (smel/moe.py:146-159): the frozen bank for all E experts plus trainable bf16
+    copies of the selected experts, whose bank copy is then ignored."""
+
+    def __init__(self, frozen, sel_ids=None, sel_gate_up=None, sel_down=None, group: int = 32, act: str = "silu"):
+        self.frozen = frozen
+        self.E = frozen.num_experts
+        self.group = group          # the reference's experts-dequantized-at-once knob; the kernels need none
+        self.act = act
+        self.sel_ids = None if sel_ids is None else torch.as_tensor(sel_ids, dtype=torch.long)
+        self.sel_gate_up, self.sel_down = sel_gate_up, sel_down
+        self._slot = {}
+        if self.sel_ids is not None:
+            self._slot = {int(e): j for j, e in enumerate(self.sel_ids.tolist())}
+        self._gkind = {}
+
+    def gkind(self, with_shared: bool, device) -> torch.Tensor:
+        """Per-group weight location: (kind << 16) | index, groups 0..E-1 (+ E = shared)."""
+        key = (with_shared, str(device))
+        if key not in self._gkind:
+            int4 = isinstance(self.frozen, Int4Experts)
+            k = []
+            for e in range(self.E):
+                if e in self._slot:
+                    k.append((L.KIND_SEL << 16) | self._slot[e])
+                else:
+                    k.append(((L.KIND_INT4 if int4 else L.KIND_BF16) << 16) | e)
+            if with_shared:
+                k.append(L.KIND_SHARED << 16)
+            self._gkind[key] = torch.tensor(k, dtype=torch.int32, device=device)
+        return self._gkind[key]
+
+
+# ------------------------------------------------------------------------------------------------ activations
+
+
+def act(x: torch.Tensor, name: str) -> torch.Tensor:
+    """smel/moe.py:91-96 (elementwise helper of the API; the kernels fuse their own)."""
+    if name == "silu":
+        return F.silu(x)
+    if name == "gelu_tanh":
+        return F.gelu(x, approximate="tanh")
+    raise ValueError(f"unknown activation {name}")
+
+
+def act_and_grad(g: torch.Tensor, name: str):
+    """smel/moe.py:99-107."""
+    if name == "silu":
+        sg = torch.sigmoid(g)
+        return g * sg, sg * (1 + g * (1 - sg))
+    if name == "gelu_tanh":
+        t = torch.tanh(_GELU_C * (g + 0.044715 * g ** 3))
+        return 0.5 * g * (1 + t), 0.5 * (1 + t) + 0.5 * g * (1 - t * t) * _GELU_C * (1 + 3 * 0.044715 * g * g)
+    raise ValueError(f"unknown activation {name}")
+
+
+# ------------------------------------------------------------------------------------------------ helpers
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"the MI355X MoE kernels compute in bf16; got {t.dtype}")
+    return t.contiguous()
+
+
+_dense_tiles_cache = {}
+
+
+def _dense_tiles(T: int, device):
+    """Tile list of one dense group of T rows (group 0), for the router-backward GEMM."""
+    key = (T, str(device))
+    if key not in _dense_tiles_cache:
+        n = (T + M_TILE - 1) // M_TILE
+        t = torch.zeros(max(n, 1), 4, dtype=torch.int32)
+        for i in range(n):
+            t[i, 0], t[i, 1], t[i, 2] = 0, i * M_TILE, min(T, (i + 1) * M_TILE)
+        _dense_tiles_cache[key] = (t.reshape(-1).to(device), torch.tensor([n], dtype=torch.int32, device=device),
+                                   n, torch.tensor([L.KIND_SHARED << 16], dtype=torch.int32, device=device))
+    return _dense_tiles_cache[key]
+
+
+def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> torch.Tensor:
+    """[Epad][H] bf16 = router rows, then the shared-gate row, zero-padded to a multiple of 32 rows: the weight of the
+    router-backward GEMM (dx += dlogits . W). Built per call (E x H bf16, about 1 MB)."""
+    E, H = gate_w.shape
+    Epad = (E + 1 + 31) // 32 * 32
+    w = torch.zeros(Epad, H, dtype=torch.bfloat16, device=gate_w.device)
+    w[:E] = gate_w
+    if sg_w is not None:
+        w[E] = sg_w.reshape(-1)
+    return w
+
+
+class _LoRABufs:
+    """bf16 K-extension layouts of one LoRA set (smel_lora_prep), built per call from the fp32 parameters."""
+
+    def __init__(self, lora, n: int, H: int, I: int, device):
+        self.scale = float(lora.scale)
+        self.r = lora.r
+        e = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=device)
+        self.fwd_gu, self.fwd_dn = e(n, 2 * I, EXT), e(n, H, EXT)
+        self.a_gu, self.a_dn = e(n, EXT, H), e(n, EXT, I)
+        self.bt_dn, self.bt_gu = e(n, EXT, H), e(n, EXT, 2 * I)
+        P = [getattr(lora, k).detach().float().contiguous() for k in
+             ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")]
+        L.call("smel_lora_prep", *[L.ptr(p) for p in P], n, lora.r, H, I, L.ptr(self.fwd_gu), L.ptr(self.fwd_dn),
+               L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu), L.stream())
+
+
+def _wset(ex: LayerExperts, which: str, sel_w, sh_w, ext_sel, ext_sh) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer."""
+    fz = ex.frozen
+    w = L.WSet()
+    if isinstance(fz, Int4Experts):
+        d = fz.gu if which == "gu" else fz.dn
+        w.q4, w.s4, w.z4 = L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"])
+        w.group = Int4Experts.group_of(d)
+        R = d["q"].shape[1]
+        C = d["q"].shape[2] * 2
+    else:
+        t = fz.gate_up if which == "gu" else fz.down
+        w.wb = L.ptr(t)
+        w.group = 32
+        R, C = t.shape[1], t.shape[2]
+    w.wsel = L.ptr(sel_w)
+    w.wsh = L.ptr(sh_w)
+    w.ext_sel = L.ptr(ext_sel)
+    w.ext_sh = L.ptr(ext_sh)
+    w.R, w.C = R, C
+    return w
+
+
+def _check_bank(ex: LayerExperts):
+    fz = ex.frozen
+    if isinstance(fz, Int4Experts):
+        for d in (fz.gu, fz.dn):
+            for k in ("q", "scale", "zero"):
+                L.require_device(d[k])
+                if not d[k].is_contiguous():
+                    raise ValueError(f"int4 bank tensor {k} must be contiguous")
+    else:
+        for t in (fz.gate_up, fz.down):
+            L.require_device(t)
+            _bf16(t)
+
+
+# ------------------------------------------------------------------------------------------------ router
+
+
+class _RouteFn(torch.autograd.Function):
+    """route (smel/moe.py:162-167) with topv differentiable w.r.t. x through the router softmax."""
+
+    @staticmethod
+    def forward(ctx, x, gate_w, top_k):
+        T, H = x.shape
+        E = gate_w.shape[0]
+        dev = x.device
+        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
+        topv = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
+        topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+        topi32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+        L.call("smel_route", L.ptr(x), L.ptr(gate_w), None, T, H, E, top_k, L.ptr(probs), L.ptr(topv), L.ptr(topi),
+               L.ptr(topi32), None, L.stream())
+        ctx.save_for_backward(probs, topi32, gate_w)
+        ctx.mark_non_differentiable(probs, topi)
+        return probs, topv, topi
+
+    @staticmethod
+    def backward(ctx, dprobs, dtopv, dtopi):
+        probs, topi32, gate_w = ctx.saved_tensors
+        T, E = probs.shape
+        K = topi32.shape[1]
+        dev = probs.device
+        if dtopv is None:
+            return None, None, None
+        dwp = dtopv.float().contiguous().reshape(-1, 1)
+        ident = torch.arange(T * K, dtype=torch.int32, device=dev)
+        wr = _router_ext_weight(gate_w, None)
+        Epad = wr.shape[0]
+        dl = torch.empty(T, Epad, dtype=torch.bfloat16, device=dev)
+        L.call("smel_route_bwd", L.ptr(dwp), 1, L.ptr(ident), L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
+               L.ptr(dl), Epad, None, L.stream())
+        dx = _router_dx(dl, wr, T)
+        return dx, None, None
+
+
+def _router_dx(dl: torch.Tensor, wr: torch.Tensor, T: int) -> torch.Tensor:
+    H = wr.shape[1]
+    tiles, ntiles, maxt, gk = _dense_tiles(T, dl.device)
+    dx = torch.empty(T, H, dtype=torch.bfloat16, device=dl.device)
+    w = L.WSet()
+    w.wsh = L.ptr(wr)
+    w.R, w.C, w.group = wr.shape[0], H, 32
+    L.call("smel_gmm_bwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dl), dl.shape[1], 0,
+           None, 0, 1, None, 0, 0, None, None, None, L.ptr(dx), H, None, L.stream())
+    return dx
+
+
+def route(x2d, gate_w, top_k):
+    """smel/moe.py:162-167 -> (probs fp32 [T,E], topv bf16 [T,K] renormalised, topi int64 [T,K])."""
+    L.require_device(x2d, gate_w)
+    return _RouteFn.apply(_bf16(x2d), _bf16(gate_w), int(top_k))
+
+
+def route_gemma4(h, W, top_k, eps):
+    """Gemma 4 router (smel/moe.py:170-180), torch ops on the GPU: weightless RMSNorm, router.scale, softmax, top-k,
+    renorm, per_expert_scale. Its HIP kernel is not built yet; this keeps the API whole for routed_experts callers."""
+    hf = h.float()
+    x = (hf * torch.pow(hf.pow(2).mean(-1, keepdim=True) + eps, -0.5)).type_as(h)
+    x = x * W["router.scale"] * h.shape[-1] ** -0.5
+    logits = F.linear(x, W["router.proj.weight"])
+    probs = torch.softmax(logits, dim=-1, dtype=torch.float32)
+    topv, topi = torch.topk(probs, top_k, dim=-1)
+    topv = topv / topv.sum(dim=-1, keepdim=True)
+    return probs, topv * W["router.per_expert_scale"][topi], topi
+
+
+# ------------------------------------------------------------------------------------------------ fused layer
+
+
+class _Ctx:
+    pass
+
+
+def _lora_groups(ex: LayerExperts, with_shared: bool, n_sel_lora: int, device):
+    ids = [int(e) for e in ex.sel_ids.tolist()][:n_sel_lora] if (ex.sel_ids is not None and n_sel_lora) else []
+    if with_shared:
+        ids.append(ex.E)
+    return torch.tensor(ids, dtype=torch.int32, device=device)
+
+
+def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
+                      need_grad: bool, c: _Ctx):
+    """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up [2I,H], down [H,I], sgate fp32 [T]) or None."""
+    T, H = x.shape
+    E = ex.E
+    dev = x.device
+    st = L.stream()
+    TK = T * K
+    rows_sh = T if shared is not None else 0
+    M = TK + rows_sh
+    maxt = L.load().smel_dispatch_max_tiles(TK, E, rows_sh, M_TILE)
+    i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
+    counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
+    tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
+    L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(counts), L.ptr(offsets),
+           L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), st)
+    gk = ex.gkind(shared is not None, dev)
+    sel_gu = sel_dn = None
+    if ex.sel_ids is not None and len(ex._slot):
+        sel_gu, sel_dn = _bf16(ex.sel_gate_up), _bf16(ex.sel_down)
+    I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
+    sh_gu = sh_dn = sgate = None
+    if shared is not None:
+        sh_gu, sh_dn, sgate = shared
+    lb_ex = _LoRABufs(lora_ex, len(ex._slot), H, I, dev) if (lora_ex is not None and sel_gu is not None) else None
+    lb_sh = _LoRABufs(lora_sh, 1, H, I, dev) if (lora_sh is not None and shared is not None) else None
+    any_lora = lb_ex is not None or lb_sh is not None
+    s_ex = lb_ex.scale if lb_ex else 0.0
+    s_sh = lb_sh.scale if lb_sh else 0.0
+    g = lambda b, n: getattr(b, n) if b is not None else None
+    bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+    ext_gu = ext_dn = None
+    if any_lora:
+        ext_gu = bf(M, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, 1, L.ptr(order), TK, K,
+               L.ptr(g(lb_ex, "a_gu")), L.ptr(g(lb_sh, "a_gu")), H, s_ex, s_sh, L.ptr(ext_gu), st)
+    actb = bf(M, I)
+    hsave = bf(M, 2 * I) if need_grad else None
+    w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"))
+    L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, 1,
+           L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave), st)
+    if any_lora:
+        ext_dn = bf(M, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(actb), I, 0, L.ptr(order), TK,
+               K, L.ptr(g(lb_ex, "a_dn")), L.ptr(g(lb_sh, "a_dn")), I, s_ex, s_sh, L.ptr(ext_dn), st)
+    Y = bf(M, H)
+    w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
+    L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, 0,
+           L.ptr(order), TK, K, L.ptr(ext_dn), 0, _ACT[ex.act], L.ptr(Y), H, None, st)
+    out = bf(T, H)
+    L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(sgate), T, K, H, L.ptr(out), st)
+    # everything the backward needs
+    c.T, c.H, c.I, c.E, c.K, c.TK, c.M, c.maxt = T, H, I, E, K, TK, M, maxt
+    c.ex, c.shared_w = ex, (sh_gu, sh_dn) if shared is not None else None
+    c.tensors = dict(x=x, topv=topv, sgate=sgate, counts=counts, offsets=offsets, order=order, inv=inv, tiles=tiles,
+                     ntiles=ntiles, err=err, gk=gk, act=actb, hsave=hsave, ext_gu=ext_gu, ext_dn=ext_dn,
+                     sel_gu=sel_gu, sel_dn=sel_dn)
+    c.lb_ex, c.lb_sh = lb_ex, lb_sh
+    c.lora_ex, c.lora_sh = lora_ex, lora_sh
+    return out
+
+
+def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
+    """Returns (dx_experts_plus_router, dtopv or None, {lora_param_name: grad}). ``router`` = (probs, topi32, wr) for
+    the fused layer (router + shared gate backward folded into the dX reduce)."""
+    t = c.tensors
+    T, H, I, E, K, TK, M, maxt = c.T, c.H, c.I, c.E, c.K, c.TK, c.M, c.maxt
+    dev = dout.device
+    st = L.stream()
+    ex = c.ex
+    dout = _bf16(dout)
+    lb_ex, lb_sh = c.lb_ex, c.lb_sh
+    g = lambda b, n: getattr(b, n) if b is not None else None
+    s_ex = lb_ex.scale if lb_ex else 0.0
+    s_sh = lb_sh.scale if lb_sh else 0.0
+    any_lora = lb_ex is not None or lb_sh is not None
+    bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+    sh_gu, sh_dn = c.shared_w if c.shared_w is not None else (None, None)
+    order, tiles, ntiles, gk = t["order"], t["tiles"], t["ntiles"], t["gk"]
+    # (1) LoRA down-projection of dout for the down backward: DB = s dout B_d (not yet scaled by the row weight)
+    ext_db = None
+    if any_lora:
+        ext_db = bf(M, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dout), H, 1, L.ptr(order), TK, K,
+               L.ptr(g(lb_ex, "bt_dn")), L.ptr(g(lb_sh, "bt_dn")), H, s_ex, s_sh, L.ptr(ext_db), st)
+    # (2) down backward + SiLU-gate backward + d(row weight) partials
+    nblk = L.load().smel_gmm_bwd_nblocks(I)
+    dh = bf(M, 2 * I)
+    dwp = torch.empty(M, nblk, dtype=torch.float32, device=dev)
+    w_dn = _wset(ex, "dn", t["sel_dn"], sh_dn, g(lb_ex, "a_dn"), g(lb_sh, "a_dn"))
+    L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, 1,
+           L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["topv"]),
+           L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st)
+    # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
+    ext_dxa = None
+    if any_lora:
+        ext_dxa = bf(M, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * I, 0, L.ptr(order), TK,
+               K, L.ptr(g(lb_ex, "bt_gu")), L.ptr(g(lb_sh, "bt_gu")), 2 * I, s_ex, s_sh, L.ptr(ext_dxa), st)
+    # (4) gate_up backward: per-slot dx rows
+    dxs = bf(M, H)
+    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "a_gu"), g(lb_sh, "a_gu"))
+    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, 0,
+           L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, L.ptr(dxs), H, None, st)
+    # (5) router backward (fused layer) or d topv (routed_experts)
+    dxr = None
+    dtopv = None
+    if router is not None:
+        probs, topi32, wr = router
+        Epad = wr.shape[0]
+        dl = bf(T, Epad)
+        L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32), L.ptr(t["topv"]),
+               L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, st)
+        dxr = _router_dx(dl, wr, T)
+    else:
+        dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
+        L.call("smel_dtopv", L.ptr(dwp), nblk, L.ptr(t["inv"]), TK, L.ptr(dtopv), st)
+    dx = bf(T, H)
+    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), int(t["sgate"] is not None), T, K, H, L.ptr(dx), st)
+    # (6) LoRA factor gradients
+    grads = {}
+    if any_lora:
+        n_sel = len(ex._slot) if lb_ex is not None else 0
+        groups = _lora_groups(ex, lb_sh is not None, n_sel, dev)
+        n_lora = groups.numel()
+        chunks = L.load().smel_lora_wgrad_part_chunks(T)
+        Qmax = max(H, 2 * I)
+        part = torch.empty(n_lora * chunks * EXT * Qmax, dtype=torch.float32, device=dev)
+
+        def wgrad(Lbuf, Rm, ldr, r_gather, use_w, Q):
+            out = torch.empty(n_lora, EXT, Q, dtype=torch.float32, device=dev)
+            L.call("smel_lora_wgrad", L.ptr(groups), n_lora, L.ptr(t["offsets"]), E, T, TK, K, L.ptr(order),
+                   L.ptr(Lbuf), L.ptr(Rm), ldr, r_gather, use_w, L.ptr(t["topv"]), L.ptr(t["sgate"]), Q, L.ptr(part),
+                   chunks, L.ptr(out), st)
+            return out
+
+        dA_gu = wgrad(ext_dxa, t["x"], H, 1, 0, H)          # [n, 32, H]: A_gate rows 0..r-1, A_up rows 16..
+        dB_gu = wgrad(t["ext_gu"], dh, 2 * I, 0, 0, 2 * I)   # [n, 32, 2I]
+        dA_dn = wgrad(ext_db, t["act"], I, 0, 1, I)         # [n, 32, I]
+        dB_dn = wgrad(t["ext_dn"], dout, H, 1, 1, H)         # [n, 32, H]
+        for tag, lb, j0, n in (("ex", lb_ex, 0, n_sel), ("sh", lb_sh, n_sel, 1 if lb_sh is not None else 0)):
+            if lb is None:
+                continue
+            r = lb.r
+            sl = slice(j0, j0 + n)
+            grads[tag] = {
+                "A_gate": dA_gu[sl, :r, :], "A_up": dA_gu[sl, 16:16 + r, :],
+                "B_gate": dB_gu[sl, :r, :I].transpose(1, 2), "B_up": dB_gu[sl, 16:16 + r, I:].transpose(1, 2),
+                "A_down": dA_dn[sl, :r, :], "B_down": dB_dn[sl, :r, :].transpose(1, 2)}
+    return dx, dtopv, grads
+
+
+_LORA_NAMES = ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")
+
+
+def _lora_leaves(lora):
+    return [getattr(lora, n) for n in _LORA_NAMES] if lora is not None else []
+
+
+def _shape_grads(grads: dict, tag: str, lora, squeeze: bool):
+    if lora is None:
+        return []
+    if tag not in grads:
+        return [None] * 6
+    out = []
+    for n in _LORA_NAMES:
+        gr = grads[tag][n]
+        gr = gr[0] if squeeze else gr
+        p = getattr(lora, n)
+        out.append(gr.contiguous().to(p.dtype).reshape(p.shape) if p.requires_grad else None)
+    return out
+
+
+class _MoELayerFn(torch.autograd.Function):
+    """The fused MoE layer (moe_forward): router + routed experts + shared expert, one forward and one backward."""
+
+    @staticmethod
+    def forward(ctx, x, plan, stats, *leaves):
+        T, H = x.shape
+        E, K = plan["ex"].E, plan["top_k"]
+        dev = x.device
+        fuse = plan["shared"] is not None
+        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
+        topv = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+        topi = torch.empty(T, K, dtype=torch.int64, device=dev)
+        topi32 = torch.empty(T, K, dtype=torch.int32, device=dev)
+        sgate = torch.empty(T, dtype=torch.float32, device=dev) if fuse else None
+        sgw = plan["shared"][2] if fuse else None
+        L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
+               L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.stream())
+        if stats is not None:
+            stats(probs, topv, topi)
+        c = _Ctx()
+        shared = (plan["shared"][0], plan["shared"][1], sgate) if fuse else None
+        out = _forward_pipeline(x, plan["ex"], K, topv, topi32, False, shared, plan["lora_ex"], plan["lora_sh"],
+                                plan["need_grad"], c)
+        if plan["need_grad"]:
+            c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw))
+            ctx.c = c
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        c = ctx.c
+        dx, _, grads = _backward_pipeline(c, dout, router=c.router)
+        g = _shape_grads(grads, "ex", c.lora_ex, False) + _shape_grads(grads, "sh", c.lora_sh, True)
+        ctx.c = None
+        return (dx, None, None, *g)
+
+
+class _RoutedFn(torch.autograd.Function):
+    """routed_experts (smel/moe.py:214-252) with given routing: differentiable w.r.t. x2d, topv and expert LoRA."""
+
+    @staticmethod
+    def forward(ctx, x, topv, topi, ex, lora, *leaves):
+        c = _Ctx()
+        K = topi.shape[1]
+        tv = topv.detach().to(torch.bfloat16).contiguous()
+        need = ctx.needs_input_grad[0] or ctx.needs_input_grad[1] or any(ctx.needs_input_grad[5:])
+        out = _forward_pipeline(x, ex, K, tv, topi.contiguous(), topi.dtype == torch.int64, None, lora, None, need, c)
+        if need:
+            ctx.c = c
+        ctx.topv_dtype = topv.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        c = ctx.c
+        dx, dtopv, grads = _backward_pipeline(c, dout, router=None)
+        g = _shape_grads(grads, "ex", c.lora_ex, False)
+        ctx.c = None
+        return (dx, dtopv.to(ctx.topv_dtype), None, None, None, *g)
+
+
+def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
+    """Weighted sum of the routed experts of every token (smel/moe.py:214-252)."""
+    L.require_device(x2d, topv, topi)
+    _check_bank(ex)
+    return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
+
+
+def _shared_weights(W: dict):
+    pre = "mlp.shared_expert."
+    if pre + "gate_proj.weight" not in W and pre + "gate_up_proj.weight" not in W:
+        return None
+    gu = W.get(pre + "gate_up_proj.weight")
+    if gu is None:
+        gu = torch.cat((W[pre + "gate_proj.weight"], W[pre + "up_proj.weight"]))
+    return _bf16(gu), _bf16(W[pre + "down_proj.weight"]), _bf16(W["mlp.shared_expert_gate.weight"].reshape(-1))
+
+
+def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=None):
+    """x2d [N, H] (already post-attention-normed) -> [N, H] bf16 (smel/moe.py:255-263): router, stats hook, routed
+    experts and the shared expert, fused into one forward/backward pipeline."""
+    L.require_device(x2d)
+    _check_bank(ex)
+    x = _bf16(x2d)
+    lora_ex = lora_layer.experts if lora_layer is not None else None
+    lora_sh = lora_layer.shared if lora_layer is not None else None
+    shared = _shared_weights(W)
+    if shared is not None:
+        I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
+        if shared[1].shape[1] != I:
+            raise NotImplementedError("fused shared expert needs shared intermediate == expert intermediate")
+    if lora_ex is not None and (ex.sel_ids is None or len(ex._slot) == 0):
+        lora_ex = None
+    plan = {"ex": ex, "top_k": int(top_k), "gate_w": _bf16(W["mlp.gate.weight"]), "shared": shared,
+            "lora_ex": lora_ex, "lora_sh": lora_sh if shared is not None else None}
+    leaves = _lora_leaves(plan["lora_ex"]) + _lora_leaves(plan["lora_sh"])
+    plan["need_grad"] = torch.is_grad_enabled() and (x2d.requires_grad or any(p.requires_grad for p in leaves))
+    return _MoELayerFn.apply(x, plan, stats, *leaves)
+
+
+class FrozenExpertsFn:
+    """API name of the reference's frozen-expert autograd Function (smel/moe.py:120-143). The kernels of this
+    package fuse it into the grouped GEMMs of ``routed_experts`` / ``moe_forward``; calling it directly is not
+    supported."""
+
+    @staticmethod
+    def apply(*args, **kwargs):
+        raise NotImplementedError("FrozenExpertsFn is fused into routed_experts / moe_forward on MI355X")

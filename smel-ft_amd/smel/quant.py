@@ -1,0 +1,76 @@
+"""int4 group-wise format of the frozen experts (API of smel/quant.py), dequant through the HIP kernel.
+
+Format (the reference's, smel/quant.py:14-44): q uint8 [..., K/2] with the even column in the low nibble, scale and
+zero bf16 [..., K/group], w = q*scale + zero. ``dequant_int4`` is the MI355X kernel (fp32 math, one
+round-to-nearest-even, as the reference's GPU kernel smel/quant.py:51-67). ``quantize_int4`` is the offline packer of
+the reference's pack stage (not on the hot path); it runs as torch ops on whatever device its input lives on.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+
+
+def _q4_candidate(wg, lo, hi):
+    scale = ((hi - lo) / 15).clamp_min(1e-8).to(torch.bfloat16).float()
+    zero = lo.to(torch.bfloat16).float()
+    q = torch.round((wg - zero) / scale).clamp_(0, 15)
+    return q, scale, zero
+
+
+def quantize_int4(w: torch.Tensor, group: int = 64, clip_search=(1.0, 0.95, 0.9, 0.85, 0.8)) -> dict:
+    """w [..., K] -> {"q": uint8 [..., K/2], "scale": bf16 [..., K/group], "zero": bf16 [..., K/group]}
+    (smel/quant.py:14-44): per group, the [min, max] range shrunk about its midpoint by the clip factor with the
+    smallest squared error (a later factor must be strictly better); 3-D inputs in slices of 16 experts."""
+    if w.dim() == 3 and w.shape[0] > 16:
+        parts = [quantize_int4(w[i:i + 16], group, clip_search) for i in range(0, w.shape[0], 16)]
+        return {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
+    K = w.shape[-1]
+    assert K % group == 0 and group % 2 == 0
+    wg = w.float().reshape(*w.shape[:-1], K // group, group)
+    lo0, hi0 = wg.amin(-1, keepdim=True), wg.amax(-1, keepdim=True)
+    mid = (lo0 + hi0) / 2
+    best = None
+    for c in clip_search or (1.0,):
+        q, s, z = _q4_candidate(wg, mid + (lo0 - mid) * c, mid + (hi0 - mid) * c)
+        err = (q * s + z - wg).pow(2).sum(-1, keepdim=True)
+        if best is None:
+            best = [err, q, s, z]
+            continue
+        take = err < best[0]
+        best = [torch.where(take, n, o) for n, o in zip((err, q, s, z), best)]
+    _, q, s, z = best
+    q = q.to(torch.uint8).reshape(*w.shape[:-1], K)
+    return {"q": (q[..., 0::2] | (q[..., 1::2] << 4)).contiguous(),
+            "scale": s.squeeze(-1).to(torch.bfloat16), "zero": z.squeeze(-1).to(torch.bfloat16)}
+
+
+def dequant_int4(q: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """int4 -> ``dtype`` (bf16 or fp32) on the GPU (smel/quant.py:74-84)."""
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"dequant_int4: unsupported output dtype {dtype}")
+    L.require_device(q, scale, zero)
+    q, scale, zero = q.contiguous(), scale.contiguous(), zero.contiguous()
+    K = q.shape[-1] * 2
+    G = scale.shape[-1]
+    out = torch.empty(*q.shape[:-1], K, device=q.device, dtype=dtype)
+    rows = q.numel() // max(1, q.shape[-1])
+    L.call("smel_dequant_int4", L.ptr(q), L.ptr(scale), L.ptr(zero), L.ptr(out), rows, K, K // G,
+           int(dtype == torch.float32), L.stream())
+    return out
+
+
+def dequant_int4_torch(q, scale, zero, dtype=torch.bfloat16):
+    """The reference's torch fallback semantics (smel/quant.py:87-94: product and add rounded in ``dtype``), kept
+    for API compatibility; not used by the kernels."""
+    K = q.shape[-1] * 2
+    G = scale.shape[-1]
+    w = torch.stack((q & 0xF, q >> 4), dim=-1).reshape(*q.shape[:-1], G, K // G).to(dtype)
+    w = w * scale.unsqueeze(-1).to(dtype) + zero.unsqueeze(-1).to(dtype)
+    return w.reshape(*q.shape[:-1], K)
+
+
+def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.float(), b.float()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()

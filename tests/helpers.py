@@ -32,3 +32,48 @@ def assert_close_bf16(out, ref, name="", rel=2e-2, cos=0.9999):
     m = ((out.double() - ref.double()).abs().max() / ref.double().abs().max().clamp_min(1e-30)).item()
     assert e <= rel and m <= rel and c >= cos, f"{name}: rel {e:.3e} max {m:.3e} cos {c:.6f}"
     return e, m, c
+
+
+def to_device_layer(ol: R.OracleLayer, device):
+    """The oracle's layer as the drop-in API's objects on ``device``: (W dict, LayerExperts, LayerLoRA or None)."""
+    from smel.lora import ExpertsLoRA, LayerLoRA, MLPLoRA
+    from smel.moe import BF16Experts, Int4Experts, LayerExperts
+
+    bf = lambda t: t.to(device=device, dtype=torch.bfloat16).contiguous()
+    W = {"mlp.gate.weight": bf(ol.gate_w)}
+    if ol.shared is not None:
+        Is = ol.shared["down"].shape[1]
+        W["mlp.shared_expert.gate_proj.weight"] = bf(ol.shared["gate_up"][:Is])
+        W["mlp.shared_expert.up_proj.weight"] = bf(ol.shared["gate_up"][Is:])
+        W["mlp.shared_expert.down_proj.weight"] = bf(ol.shared["down"])
+        W["mlp.shared_expert_gate.weight"] = bf(ol.shared["gate_w"])
+    if ol.int4:
+        dev = lambda d: {k: v.to(device).contiguous() for k, v in d.items()}
+        bank = Int4Experts(dev(ol.frozen["gate_up"]), dev(ol.frozen["down"]))
+    else:
+        bank = BF16Experts(bf(ol.frozen["gate_up"]), bf(ol.frozen["down"]))
+    if ol.sel_ids:
+        ex = LayerExperts(bank, ol.sel_ids, bf(ol.sel_gate_up), bf(ol.sel_down), group=32, act=ol.act)
+    else:
+        ex = LayerExperts(bank, group=32, act=ol.act)
+    lora = None
+    if ol.ex_lora is not None or ol.sh_lora is not None:
+        exl = shl = None
+        if ol.ex_lora is not None:
+            r, H = ol.ex_lora["A_gate"].shape[1:]
+            I = ol.ex_lora["A_down"].shape[2]
+            exl = ExpertsLoRA(ol.sel_ids, H, I, r, ol.ex_scale * r)
+            with torch.no_grad():
+                for n in LORA_NAMES:
+                    getattr(exl, n).copy_(ol.ex_lora[n])
+            exl = exl.to(device)
+        if ol.sh_lora is not None:
+            r, H = ol.sh_lora["A_gate"].shape
+            Is = ol.sh_lora["A_down"].shape[1]
+            shl = MLPLoRA(H, Is, r, ol.sh_scale * r)
+            with torch.no_grad():
+                for n in LORA_NAMES:
+                    getattr(shl, n).copy_(ol.sh_lora[n])
+            shl = shl.to(device)
+        lora = LayerLoRA(exl, shl)
+    return W, ex, lora

@@ -1,0 +1,69 @@
+"""The C-ABI library loads without a GPU, exports every entry point include/smel_moe.h declares, and its host-side
+argument checks reject bad shapes before any launch (CPU only: no kernel runs here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "smel_moe.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(smel_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_parses():
+    names = declared_functions()
+    assert "smel_gmm_fwd" in names and "smel_route" in names and len(names) >= 15
+
+
+def test_library_exports_every_declared_symbol():
+    from smel import _lib
+    L = _lib.load()
+    for n in declared_functions():
+        assert hasattr(L, n), n
+    # the Python binding types every declared symbol, and nothing undeclared
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_wset_layout_matches_header():
+    from smel import _lib
+    # 8 pointers, two int64, two int32
+    assert ctypes.sizeof(_lib.WSet) == 8 * 8 + 2 * 8 + 2 * 4
+
+
+def test_host_side_rejections():
+    """Shape checks happen on the host, before any launch, so they are safe without a GPU."""
+    from smel import _lib
+    L = _lib.load()
+    assert L.smel_dispatch_max_tiles(32736, 256, 4092, 128) == (32736 + 127) // 128 + 256 + 32 + 1
+    # route: too many experts
+    rc = L.smel_route(1, 1, None, 4, 64, 300, 8, 1, 1, 1, 1, None, None)
+    assert rc == -2 and b"E=300" in L.smel_last_error()
+    # route: hidden not a multiple of 64
+    assert L.smel_route(1, 1, None, 4, 96, 8, 2, 1, 1, 1, 1, None, None) == -2
+    # dequant: K not a multiple of the group
+    assert L.smel_dequant_int4(1, 1, 1, 1, 4, 96, 64, 0, None) == -1
+    # gmm: null weight set
+    assert L.smel_gmm_fwd(None, 1, 1, 1, 1, 1, 64, 0, None, 0, 1, None, 0, 0, 1, 64, None, None) == -1
+    w = _lib.WSet()
+    w.R, w.C, w.group = 64, 48, 64
+    assert L.smel_gmm_fwd(ctypes.byref(w), 1, 1, 1, 1, 16, 48, 0, None, 0, 1, None, 0, 0, 16, 64, None, None) == -2
+    with pytest.raises(_lib.SmelError):
+        _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, 32, 64, 64, None, None, None, None, None,
+                  None, None)
+
+
+def test_product_path_does_not_reach_the_oracle():
+    """Nothing under smel-ft_amd/ imports the oracle or the reference."""
+    pkg = os.path.join(ROOT, "smel-ft_amd")
+    for dp, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h")):
+                s = open(os.path.join(dp, f)).read()
+                assert "oracle" not in s.replace("Oracle", ""), f
+                assert "/root/reference" not in s, f
