@@ -73,12 +73,46 @@ def load(path: str = LIB_PATH):
     return L
 
 
-def call(name: str, *args):
-    """Call an entry point that returns a status code; raise SmelError with the library's message on failure."""
-    rc = getattr(load(), name)(*args)
+_timing = None   # list of (tag, start event, end event) while timing is on
+
+
+def call(name: str, *args, tag: str | None = None):
+    """Call an entry point that returns a status code; raise SmelError with the library's message on failure.
+    While :func:`timing` is active, the launch is bracketed by events on the current stream."""
+    fn = getattr(load(), name)
+    if _timing is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rc = fn(*args)
+        e1.record()
+        _timing.append((tag or name, e0, e1))
+    else:
+        rc = fn(*args)
     if rc != 0:
         msg = load().smel_last_error().decode(errors="replace")
         raise SmelError(f"{name} failed ({rc}): {msg}")
+
+
+class timing:
+    """Context manager: time every entry-point call (HIP events on the stream the kernels run on). After a device
+    synchronize, ``results()`` returns {tag: [milliseconds per call]}."""
+
+    def __enter__(self):
+        global _timing
+        _timing = []
+        self._rec = _timing
+        return self
+
+    def __exit__(self, *exc):
+        global _timing
+        _timing = None
+        return False
+
+    def results(self):
+        out = {}
+        for tag, e0, e1 in self._rec:
+            out.setdefault(tag, []).append(e0.elapsed_time(e1))
+        return out
 
 
 def ptr(t: torch.Tensor | None):
