@@ -109,9 +109,10 @@ int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tile
  * epilogue 0: out[slot(row)][n] = bf16(acc), n < R                                  (down projection)
  * epilogue 1: gate/up pairs: g = bf16(acc[n]), u = bf16(acc[R/2 + n]), out[row][n] = bf16(act(g) u), n < R/2;
  *             if hsave: hsave[row][n] = g, hsave[row][R/2 + n] = u                  (gate_up projection)
- * A rows: A[token(row)] if a_gather else A[row]; K = w.C (multiple of 32). */
+ * A rows: A[token(row)] if a_gather else A[row]; A holds a_rows rows; K = w.C (multiple of 32). */
 int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
-                 int64_t max_tiles, const uint16_t* A, int64_t lda, int32_t a_gather, const int32_t* order,
+                 int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
+                 const int32_t* order,
                  int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act, uint16_t* out,
                  int64_t ldo, uint16_t* hsave, hipStream_t stream);
 
@@ -126,9 +127,10 @@ int smel_combine(const uint16_t* Y, const uint16_t* topv, const float* sgate, in
  * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] or sgate[t]; (g, u) = hsave[row];
  *             out[row][n] = bf16(da u act'(g)), out[row][I+n] = bf16(da act(g));
  *             dwp[row][blockIdx.y] = sum_n acc * bf16(act(g) u)   (d row weight, reduced later in fixed order)
- * A rows: A[token(row)] if a_gather else A[row]; the GEMM K = w.R. */
+ * A rows: A[token(row)] if a_gather else A[row]; A holds a_rows rows; the GEMM K = w.R. */
 int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
-                 int64_t max_tiles, const uint16_t* A, int64_t lda, int32_t a_gather, const int32_t* order,
+                 int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
+                 const int32_t* order,
                  int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
                  const uint16_t* hsave, const uint16_t* topv, const float* sgate, uint16_t* out, int64_t ldo,
                  float* dwp, hipStream_t stream);

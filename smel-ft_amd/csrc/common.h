@@ -15,10 +15,12 @@ SMEL_DEV float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
 SMEL_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 SMEL_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Round-to-nearest-even fp32 -> bf16 (gfx950 has a hardware conversion; NaN stays NaN).
+// Round-to-nearest-even fp32 -> bf16 (gfx950 converts in hardware, two values per v_cvt_pk_bf16_f32; NaN stays NaN).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 SMEL_DEV uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 SMEL_DEV uint32_t pack2bf(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
 // ------------------------------------------------------------------------------------------------ wave helpers
@@ -52,15 +54,21 @@ SMEL_DEV f32x16_t mfma32(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) 
 SMEL_DEV int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
 // ------------------------------------------------------------------------------------------------ int4 dequant
+// Byte n of x as fp32 (v_cvt_f32_ubyteN: one instruction, no separate extract).
+SMEL_DEV float ub0(uint32_t x) { float f; asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(x)); return f; }
+SMEL_DEV float ub1(uint32_t x) { float f; asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(x)); return f; }
+SMEL_DEV float ub2(uint32_t x) { float f; asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(x)); return f; }
+SMEL_DEV float ub3(uint32_t x) { float f; asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(x)); return f; }
+
 // 8 nibbles of one uint32 (little-endian bytes; low nibble = even column) -> 4 packed bf16 pairs,
-// w = RNE_bf16(q*s + z) with fp32 arithmetic (q*s is exact, so fma and mul+add agree).
+// w = RNE_bf16(q*s + z) with fp32 arithmetic (q*s is exact, so fma and mul+add agree): 23 VALU ops for 8 weights.
 SMEL_DEV void dq8(uint32_t b, float s, float z, uint32_t out[4]) {
   const uint32_t lo = b & 0x0f0f0f0fu;          // columns 0,2,4,6
   const uint32_t hi = (b >> 4) & 0x0f0f0f0fu;   // columns 1,3,5,7
-  out[0] = pack2bf(fmaf((float)(lo & 0xff), s, z), fmaf((float)(hi & 0xff), s, z));
-  out[1] = pack2bf(fmaf((float)((lo >> 8) & 0xff), s, z), fmaf((float)((hi >> 8) & 0xff), s, z));
-  out[2] = pack2bf(fmaf((float)((lo >> 16) & 0xff), s, z), fmaf((float)((hi >> 16) & 0xff), s, z));
-  out[3] = pack2bf(fmaf((float)(lo >> 24), s, z), fmaf((float)(hi >> 24), s, z));
+  out[0] = pack2bf(fmaf(ub0(lo), s, z), fmaf(ub0(hi), s, z));
+  out[1] = pack2bf(fmaf(ub1(lo), s, z), fmaf(ub1(hi), s, z));
+  out[2] = pack2bf(fmaf(ub2(lo), s, z), fmaf(ub2(hi), s, z));
+  out[3] = pack2bf(fmaf(ub3(lo), s, z), fmaf(ub3(hi), s, z));
 }
 
 // Nibble j (0..7) of b as float.
@@ -86,6 +94,18 @@ SMEL_DEV void act_and_grad_f(float g, int act, float& a, float& da) {
   a = 0.5f * g * (1.0f + t);
   da = 0.5f * (1.0f + t) + 0.5f * g * (1.0f - t * t) * c * (1.0f + 3.0f * 0.044715f * g * g);
 }
+
+// ------------------------------------------------------------------------------------------------ buffer loads
+// Raw buffer loads: a load whose byte offset is outside [0, bytes) returns zeros, so rows past a tile's end and
+// columns past a matrix's end need no branch — their offset is set to OOB.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t OOB = 0x80000000u;
+SMEL_DEV rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0x7fffffffull ? 0x7fffffffu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+SMEL_DEV u32x4_t ld16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+SMEL_DEV uint32_t ld2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
 
 // ------------------------------------------------------------------------------------------------ row mapping
 // Rows of the grouped GEMMs: [0, TK) are the routed slots in expert-sorted order, [TK, TK + T) the shared expert

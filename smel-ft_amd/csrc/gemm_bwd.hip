@@ -5,8 +5,10 @@
 // k-contiguous bf16 for the MFMA B operand. Reference: FrozenExpertsFn.backward, smel/moe.py:128-143, and the
 // autograd of _selected_expert / lora_gate_up / lora_linear / the combine, smel/moe.py:204-252, smel/lora.py:61-83.
 //
-// Block = 4 waves, tile = up to 128 rows (4 slices of 32) x 256 columns (64 per wave). A rows staged in LDS (token
-// gather fused for the down backward, which reads dout rows); W step [64][256] staged transposed in LDS.
+// Block = 4 waves, tile = up to 128 rows (4 slices of 32) x 256 columns (64 per wave). Per 64-row step of W: the raw
+// A rows and raw W rows of the next step are loaded into registers while the current step's MFMAs run; then A is
+// written to LDS and W is dequantized (int4) and written transposed: thread (k pair, 32 columns) packs W[k][n] and
+// W[k+1][n] into one 32-bit LDS word of row n, so a wave's stores cover 32 consecutive words of a row.
 #include "abi_util.h"
 #include "common.h"
 
@@ -25,6 +27,7 @@ struct BwdArgs {
   const int32_t* n_tiles;
   const uint16_t* A;
   int64_t lda;
+  int64_t a_rows;
   const int32_t* order;
   const uint16_t* ext;
   const uint16_t* hsave;
@@ -37,114 +40,145 @@ struct BwdArgs {
   int Kd, N;   // Kd = w.R (contraction), N = w.C
 };
 
-// Stage W[k0 .. k0+63][n0 .. n0+255] of one group into Bt[n][k] (bf16, k contiguous). Thread -> (k pair, 32 cols).
+// Raw W data of one thread for one step: rows (ka, ka+1), 32 columns.
 template <bool Q4>
-SMEL_DEV void stage_w(const BwdArgs& a, int kind, int idx, int k0, int n0, uint16_t* Bt) {
-  const int tid = threadIdx.x;
-  const int kp = tid & 31, c32 = tid >> 5;
-  const int ka = k0 + 2 * kp;
-  const int nc = n0 + 32 * c32;
-  const smel_wset& w = a.w;
-  uint32_t* dst = reinterpret_cast<uint32_t*>(Bt + (32 * c32) * BS + 2 * kp);
-  const bool ok = ka + 1 < a.Kd && nc < a.N;   // Kd is a multiple of 32, so k pairs are whole
-  if (Q4) {
-    u32x4_t q0 = u32x4_t{}, q1 = u32x4_t{};
-    float s0 = 0.f, z0 = 0.f, s1 = 0.f, z1 = 0.f;
-    if (ok) {
-      const int64_t r0 = (int64_t)idx * w.R + ka;
-      q0 = *reinterpret_cast<const u32x4_t*>(w.q4 + r0 * (w.C / 2) + nc / 2);
-      q1 = *reinterpret_cast<const u32x4_t*>(w.q4 + (r0 + 1) * (w.C / 2) + nc / 2);
-      const int64_t g0 = r0 * (w.C / w.group) + nc / w.group;
-      const int64_t g1 = (r0 + 1) * (w.C / w.group) + nc / w.group;
-      s0 = bf2f(w.s4[g0]);
-      z0 = bf2f(w.z4[g0]);
-      s1 = bf2f(w.s4[g1]);
-      z1 = bf2f(w.z4[g1]);
-    }
-#pragma unroll
-    for (int wd = 0; wd < 4; ++wd) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v0 = fmaf(nib(q0[wd], j), s0, z0);
-        const float v1 = fmaf(nib(q1[wd], j), s1, z1);
-        dst[(8 * wd + j) * (BS / 2)] = pack2bf(v0, v1);
-      }
-    }
-  } else {
-    const uint16_t* base = kind == SMEL_KIND_BF16 ? w.wb : (kind == SMEL_KIND_SEL ? w.wsel : w.wsh);
-    const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
-    u32x4_t r0[4], r1[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r0[i] = r1[i] = u32x4_t{};
-    if (ok) {
-      const uint16_t* p0 = base + (mi * w.R + ka) * w.C + nc;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        r0[i] = *reinterpret_cast<const u32x4_t*>(p0 + 8 * i);
-        r1[i] = *reinterpret_cast<const u32x4_t*>(p0 + w.C + 8 * i);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t x0 = r0[i][j], x1 = r1[i][j];
-        dst[(8 * i + 2 * j) * (BS / 2)] = (x0 & 0xffffu) | (x1 << 16);
-        dst[(8 * i + 2 * j + 1) * (BS / 2)] = (x0 >> 16) | (x1 & 0xffff0000u);
-      }
-    }
-  }
-}
+struct WRegs;
+template <>
+struct WRegs<true> {
+  u32x4_t q[2];
+  uint32_t s[2], z[2];
+};
+template <>
+struct WRegs<false> {
+  u32x4_t v[2][4];
+};
 
-template <int EPI, bool Q4>
+template <int EPI, bool Q4, int NS>
 SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As, uint16_t* Bt) {
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
   const int nb = blockIdx.y;
   const int n0 = nb * NT;
   const int Kd = a.Kd;
+  const smel_wset& ws = a.w;
   const int cw = n0 + w * 64;                 // this wave's first column
   const bool fv0 = cw < a.N, fv1 = cw + 32 < a.N;
+  // ---- staging roles: A (tile row, 32-wide half), W (k pair, 32 columns)
   const int ar = tid >> 1, ap = tid & 1;
-  const uint16_t* arow = nullptr;
+  const int kp = tid & 31, c32 = tid >> 5;
+  const int nc = n0 + 32 * c32;
+  const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
+  uint32_t aoff = OOB;
   if (ar < nrows) {
     const int grow = row0 + ar;
     const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
-    arow = a.A + (int64_t)src * a.lda;
+    aoff = (uint32_t)src * (uint32_t)a.lda * 2 + 64 * ap;
   }
-  const int nslice = (nrows + 31) >> 5;
-  f32x16_t acc[4][2];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
+  rsrc_t rw, rs, rz;
+  uint32_t wrow;   // byte offset of column nc inside a row of this group's matrix
+  const int G = Q4 ? ws.C / ws.group : 0;
+  const bool cok = nc < a.N;
+  if constexpr (Q4) {
+    const int64_t mat = (int64_t)idx * ws.R;
+    rw = make_rsrc(ws.q4 + mat * (ws.C / 2), (uint64_t)ws.R * (ws.C / 2));
+    rs = make_rsrc(ws.s4 + mat * G, (uint64_t)ws.R * G * 2);
+    rz = make_rsrc(ws.z4 + mat * G, (uint64_t)ws.R * G * 2);
+    wrow = nc / 2;
+  } else {
+    const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
+    const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
+    rw = make_rsrc(base + mi * ws.R * ws.C, (uint64_t)ws.R * ws.C * 2);
+    rs = rz = rw;
+    wrow = nc * 2;
+  }
 
-  for (int k0 = 0; k0 < Kd; k0 += KT) {
-    {
-      const bool ok = arow && (k0 + 32 * ap + 32 <= Kd);
-      uint16_t* dst = As + ar * AS + 32 * ap;
+  f32x16_t acc[NS][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4_t*>(dst + 8 * i) =
-            ok ? *reinterpret_cast<const u32x4_t*>(arow + k0 + 32 * ap + 8 * i) : u32x4_t{};
+  for (int m = 0; m < NS; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
+
+  u32x4_t areg[4];
+  WRegs<Q4> wr;
+  auto load_step = [&](int k0) {
+    const uint32_t ao = (k0 + 32 * ap + 32 <= Kd) ? aoff + k0 * 2 : OOB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, ao + 16 * i);
+    const int ka = k0 + 2 * kp;
+    const bool ok = cok && ka + 1 < Kd;
+    if constexpr (Q4) {
+      const uint32_t rb = (uint32_t)ka * (ws.C / 2) + wrow;
+      wr.q[0] = ld16(rw, ok ? rb : OOB);
+      wr.q[1] = ld16(rw, ok ? rb + ws.C / 2 : OOB);
+      const uint32_t g = ((uint32_t)ka * G + nc / ws.group) * 2;
+      wr.s[0] = ld2(rs, ok ? g : OOB);
+      wr.z[0] = ld2(rz, ok ? g : OOB);
+      wr.s[1] = ld2(rs, ok ? g + G * 2 : OOB);
+      wr.z[1] = ld2(rz, ok ? g + G * 2 : OOB);
+    } else {
+      const uint32_t rb = (uint32_t)ka * ws.C * 2 + wrow;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wr.v[0][i] = ld16(rw, ok ? rb + 16 * i : OOB);
+        wr.v[1][i] = ld16(rw, ok ? rb + ws.C * 2 + 16 * i : OOB);
+      }
     }
-    stage_w<Q4>(a, kind, idx, k0, n0, Bt);
+  };
+  auto store_step = [&]() {
+    uint16_t* adst = As + ar * AS + 32 * ap;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(adst + 8 * i) = areg[i];
+    uint32_t* dst = reinterpret_cast<uint32_t*>(Bt + (32 * c32) * BS + 2 * kp);
+    if constexpr (Q4) {
+      const float s0 = bf2f(wr.s[0]), z0 = bf2f(wr.z[0]), s1 = bf2f(wr.s[1]), z1 = bf2f(wr.z[1]);
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        const uint32_t l0 = wr.q[0][wd] & 0x0f0f0f0fu, h0 = (wr.q[0][wd] >> 4) & 0x0f0f0f0fu;
+        const uint32_t l1 = wr.q[1][wd] & 0x0f0f0f0fu, h1 = (wr.q[1][wd] >> 4) & 0x0f0f0f0fu;
+        uint32_t* d = dst + (8 * wd) * (BS / 2);
+        d[0 * (BS / 2)] = pack2bf(fmaf(ub0(l0), s0, z0), fmaf(ub0(l1), s1, z1));
+        d[1 * (BS / 2)] = pack2bf(fmaf(ub0(h0), s0, z0), fmaf(ub0(h1), s1, z1));
+        d[2 * (BS / 2)] = pack2bf(fmaf(ub1(l0), s0, z0), fmaf(ub1(l1), s1, z1));
+        d[3 * (BS / 2)] = pack2bf(fmaf(ub1(h0), s0, z0), fmaf(ub1(h1), s1, z1));
+        d[4 * (BS / 2)] = pack2bf(fmaf(ub2(l0), s0, z0), fmaf(ub2(l1), s1, z1));
+        d[5 * (BS / 2)] = pack2bf(fmaf(ub2(h0), s0, z0), fmaf(ub2(h1), s1, z1));
+        d[6 * (BS / 2)] = pack2bf(fmaf(ub3(l0), s0, z0), fmaf(ub3(l1), s1, z1));
+        d[7 * (BS / 2)] = pack2bf(fmaf(ub3(h0), s0, z0), fmaf(ub3(h1), s1, z1));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t x0 = wr.v[0][i][j], x1 = wr.v[1][i][j];
+          dst[(8 * i + 2 * j) * (BS / 2)] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+          dst[(8 * i + 2 * j + 1) * (BS / 2)] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+        }
+      }
+    }
+  };
+
+  const int nk = (Kd + KT - 1) / KT;
+  load_step(0);
+  const uint16_t* Ab = As + r32 * AS + 32 * hi;
+  const uint16_t* Bb = Bt + (w * 64 + r32) * BS + 32 * hi;
+  for (int i = 0; i < nk; ++i) {
+    store_step();
     __syncthreads();
+    if (i + 1 < nk) load_step((i + 1) * KT);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(Bt + (w * 64 + r32) * BS + 32 * hi + 8 * s);
-      const u32x4_t b1 = *reinterpret_cast<const u32x4_t*>(Bt + (w * 64 + 32 + r32) * BS + 32 * hi + 8 * s);
+      const u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(Bb + 8 * s);
+      const u32x4_t b1 = *reinterpret_cast<const u32x4_t*>(Bb + 32 * BS + 8 * s);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (m < nslice) {
-          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(As + (m * 32 + r32) * AS + 32 * hi + 8 * s);
-          if (fv0) acc[m][0] = mfma32(af, b0, acc[m][0]);
-          if (fv1) acc[m][1] = mfma32(af, b1, acc[m][1]);
-        }
+      for (int m = 0; m < NS; ++m) {
+        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
+        acc[m][0] = mfma32(af, b0, acc[m][0]);
+        acc[m][1] = mfma32(af, b1, acc[m][1]);
       }
     }
     __syncthreads();
   }
   // ---- LoRA K-extension: ext[row][0:32] . Eb[0:32][n]
-  const uint16_t* eb = kind == SMEL_KIND_SEL ? (a.w.ext_sel ? a.w.ext_sel + (int64_t)idx * 32 * a.N : nullptr)
-                                               : (kind == SMEL_KIND_SHARED ? a.w.ext_sh : nullptr);
+  const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * 32 * a.N : nullptr)
+                                             : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
   if (a.ext && eb) {
     u32x4_t b0[2], b1[2];
 #pragma unroll
@@ -165,24 +199,22 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       b0[s] = u32x4_t{v0[0], v0[1], v0[2], v0[3]};
       b1[s] = u32x4_t{v1[0], v1[1], v1[2], v1[3]};
     }
+    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if (m >= nslice) continue;
+    for (int m = 0; m < NS; ++m) {
       const int row = m * 32 + r32;
-      const uint16_t* er = a.ext + (int64_t)(row0 + row) * 32;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const u32x4_t af = row < nrows ? *reinterpret_cast<const u32x4_t*>(er + 16 * hi + 8 * s) : u32x4_t{};
-        if (fv0) acc[m][0] = mfma32(af, b0[s], acc[m][0]);
-        if (fv1) acc[m][1] = mfma32(af, b1[s], acc[m][1]);
+        const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 32 * hi + 16 * s : OOB);
+        acc[m][0] = mfma32(af, b0[s], acc[m][0]);
+        acc[m][1] = mfma32(af, b1[s], acc[m][1]);
       }
     }
   }
   // ---- epilogue
   if (EPI == 0) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if (m >= nslice) continue;
+    for (int m = 0; m < NS; ++m) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m * 32 + acc_row(r, l);
@@ -195,18 +227,17 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     return;
   }
   // down backward: columns n < I of dh = [dg | du]
-  float* red = reinterpret_cast<float*>(As);   // [4 waves][MT]
+  float* red = reinterpret_cast<float*>(As);   // [4 waves][MT]; As is free after the last barrier
   const int I = a.N;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (m >= nslice) continue;   // block-uniform
+  for (int m = 0; m < NS; ++m) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m * 32 + acc_row(r, l);
       const bool rv = row < nrows;
       const int grow = row0 + row;
-      float wrow = 0.f;
-      if (rv) wrow = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
+      float wrow_ = 0.f;
+      if (rv) wrow_ = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
       float part = 0.f;
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
@@ -220,7 +251,7 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
           const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
           const float accv = acc[m][f][r];
           part += accv * abf;
-          const float da = wrow * accv;
+          const float da = wrow_ * accv;
           a.out[(int64_t)grow * a.ldo + n] = f2bf(da * u * dav);
           a.out[(int64_t)grow * a.ldo + I + n] = f2bf(da * av);
         }
@@ -236,20 +267,30 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   }
 }
 
+template <int EPI, bool Q4>
+SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As, uint16_t* Bt) {
+  switch ((nrows + 31) >> 5) {
+    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, As, Bt); break;
+    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, As, Bt); break;
+    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, As, Bt); break;
+    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, As, Bt); break;
+  }
+}
+
 template <int EPI>
-__global__ __launch_bounds__(256) void gmm_bwd_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[MT * AS];
   __shared__ __attribute__((aligned(16))) uint16_t Bt[NT * BS];
   if ((int)blockIdx.x >= a.n_tiles[0]) return;
   const int4 t = a.tiles[blockIdx.x];
   const int gk = a.gkind[t.x];
   const int kind = gk >> 16, idx = gk & 0xffff;
-  const int nrows = t.z - t.y;
+  const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4)
-    run_tile<EPI, true>(a, kind, idx, t.y, nrows, As, Bt);
+    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, As, Bt);
   else
-    run_tile<EPI, false>(a, kind, idx, t.y, nrows, As, Bt);
+    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, As, Bt);
 }
 
 }  // namespace
@@ -257,7 +298,7 @@ __global__ __launch_bounds__(256) void gmm_bwd_kernel(BwdArgs a) {
 extern "C" int64_t smel_gmm_bwd_nblocks(int64_t C) { return (C + NT - 1) / NT; }
 
 extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
-                            int64_t max_tiles, const uint16_t* A, int64_t lda, int32_t a_gather,
+                            int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
                             int32_t act, const uint16_t* hsave, const uint16_t* topv, const float* sgate,
                             uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
@@ -272,6 +313,8 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
                "gmm_bwd: epilogue %d needs hsave, dwp and topv", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_bwd: gather needs order");
+  SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: A larger than 2 GiB");
+  SMEL_REQUIRE(w->R * w->C * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: one weight matrix larger than 2 GiB");
   if (max_tiles == 0) return 0;
   BwdArgs a;
   a.w = *w;
@@ -280,6 +323,7 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   a.n_tiles = n_tiles;
   a.A = A;
   a.lda = lda;
+  a.a_rows = a_rows;
   a.order = order;
   a.ext = ext;
   a.hsave = hsave;

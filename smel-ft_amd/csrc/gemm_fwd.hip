@@ -27,6 +27,7 @@ struct FwdArgs {
   const int32_t* n_tiles;
   const uint16_t* A;
   int64_t lda;
+  int64_t a_rows;       // rows of A (bounds of the A buffer)
   const int32_t* order;
   const uint16_t* ext;
   uint16_t* out;
@@ -36,76 +37,27 @@ struct FwdArgs {
   int N, K;   // N = w.R (weight rows), K = w.C
 };
 
-struct BSrc {
-  const uint8_t* q;      // int4 row base (bytes), or nullptr
-  const uint16_t* sz_s;  // scale row base
-  const uint16_t* sz_z;  // zero row base
-  const uint16_t* wb;    // bf16 row base, or nullptr
+// Weight rows of one wave for one k-step: int4 (16 B = 32 nibbles per lane and fragment, plus its group's scale and
+// zero) or bf16 (64 B per lane and fragment).
+template <bool Q4>
+struct BRegs;
+template <>
+struct BRegs<true> {
+  u32x4_t q[2];
+  uint32_t s[2], z[2];
+};
+template <>
+struct BRegs<false> {
+  u32x4_t v[2][4];
 };
 
-template <bool Q4>
-SMEL_DEV BSrc weight_row(const FwdArgs& a, int kind, int idx, int n, bool valid) {
-  BSrc b{nullptr, nullptr, nullptr, nullptr};
-  if (!valid) return b;
-  const smel_wset& w = a.w;
-  if (Q4) {
-    const int64_t r = (int64_t)idx * w.R + n;
-    b.q = w.q4 + r * (w.C / 2);
-    b.sz_s = w.s4 + r * (w.C / w.group);
-    b.sz_z = w.z4 + r * (w.C / w.group);
-  } else {
-    const uint16_t* base = kind == SMEL_KIND_BF16 ? w.wb : (kind == SMEL_KIND_SEL ? w.wsel : w.wsh);
-    const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
-    b.wb = base + (mi * w.R + n) * w.C;
-  }
-  return b;
-}
-
-// Raw weight data of one fragment for one k-step.
-struct BRaw {
-  u32x4_t v[4];   // int4: v[0] holds 32 nibbles; bf16: v[0..3] hold 32 bf16
-  float s, z;
-};
-
-template <bool Q4>
-SMEL_DEV void load_b(const BSrc& b, int kk, int group, BRaw& r) {
-  if (Q4) {
-    if (b.q) {
-      r.v[0] = *reinterpret_cast<const u32x4_t*>(b.q + kk / 2);
-      r.s = bf2f(b.sz_s[kk / group]);
-      r.z = bf2f(b.sz_z[kk / group]);
-    } else {
-      r.v[0] = u32x4_t{};
-      r.s = r.z = 0.f;   // dequantizes to exact zeros
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      r.v[s] = b.wb ? *reinterpret_cast<const u32x4_t*>(b.wb + kk + 8 * s) : u32x4_t{};
-  }
-}
-
-template <bool Q4>
-SMEL_DEV void make_frags(const BRaw& r, u32x4_t f[4]) {
-  if (Q4) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      uint32_t o[4];
-      dq8(r.v[0][s], r.s, r.z, o);
-      f[s] = u32x4_t{o[0], o[1], o[2], o[3]};
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) f[s] = r.v[s];
-  }
-}
-
-template <int EPI, bool Q4>
+template <int EPI, bool Q4, int NS>
 SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As) {
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
   const int nb = blockIdx.y;
   const int K = a.K;
-  // ---- this wave's two weight rows (per lane)
+  const smel_wset& ws = a.w;
+  // ---- this wave's two weight rows (per lane): gate/up pair for epilogue 1, two adjacent 32-column blocks else
   int n0, n1;
   bool fv0, fv1;
   if (EPI == 1) {
@@ -121,97 +73,137 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     n0 = c0 + r32;
     n1 = c0 + 32 + r32;
   }
-  const BSrc bs0 = weight_row<Q4>(a, kind, idx, n0, fv0);
-  const BSrc bs1 = weight_row<Q4>(a, kind, idx, n1, fv1);
-  // ---- A staging: thread -> (tile row, 32-wide half of the k-step)
-  const int ar = tid >> 1, ap = tid & 1;
-  const uint16_t* arow = nullptr;
+  // ---- buffer resources: the weight matrix of this group, the A matrix
+  rsrc_t rw, rs, rz;
+  uint32_t wo0, wo1, so0 = 0, so1 = 0;
+  const int G = Q4 ? ws.C / ws.group : 0;
+  if constexpr (Q4) {
+    const int64_t mat = (int64_t)idx * ws.R;
+    rw = make_rsrc(ws.q4 + mat * (ws.C / 2), (uint64_t)ws.R * (ws.C / 2));
+    rs = make_rsrc(ws.s4 + mat * G, (uint64_t)ws.R * G * 2);
+    rz = make_rsrc(ws.z4 + mat * G, (uint64_t)ws.R * G * 2);
+    wo0 = fv0 ? (uint32_t)n0 * (ws.C / 2) : OOB;
+    wo1 = fv1 ? (uint32_t)n1 * (ws.C / 2) : OOB;
+    so0 = fv0 ? (uint32_t)n0 * G * 2 : OOB;
+    so1 = fv1 ? (uint32_t)n1 * G * 2 : OOB;
+  } else {
+    const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
+    const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
+    rw = make_rsrc(base + mi * ws.R * ws.C, (uint64_t)ws.R * ws.C * 2);
+    rs = rz = rw;
+    wo0 = fv0 ? (uint32_t)n0 * ws.C * 2 : OOB;
+    wo1 = fv1 ? (uint32_t)n1 * ws.C * 2 : OOB;
+  }
+  const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
+  const int ar = tid >> 1, ap = tid & 1;   // A staging: tile row, 32-wide half of the k-step
+  uint32_t aoff = OOB;
   if (ar < nrows) {
     const int grow = row0 + ar;
     const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
-    arow = a.A + (int64_t)src * a.lda;
+    aoff = (uint32_t)src * (uint32_t)a.lda * 2 + 64 * ap;
   }
-  const int nslice = (nrows + 31) >> 5;
-  f32x16_t acc[4][2];
+
+  f32x16_t acc[NS][2];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
+  for (int m = 0; m < NS; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
 
   u32x4_t areg[4];
+  BRegs<Q4> bc, bn;
   auto load_a = [&](int k0) {
-    const bool ok = arow && (k0 + 32 * ap + 32 <= K);
+    const uint32_t o = (k0 + 32 * ap + 32 <= K) ? aoff + k0 * 2 : OOB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) areg[i] = ok ? *reinterpret_cast<const u32x4_t*>(arow + k0 + 32 * ap + 8 * i) : u32x4_t{};
+    for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, o + 16 * i);
   };
   auto store_a = [&](int buf) {
     uint16_t* dst = As + buf * (MT * AS) + ar * AS + 32 * ap;
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(dst + 8 * i) = areg[i];
   };
-  BRaw braw[2];
-  auto load_bs = [&](int k0) {
+  auto load_b = [&](int k0, BRegs<Q4>& b) {
     const int kk = k0 + 32 * hi;
     const bool ok = kk + 32 <= K;
-    load_b<Q4>(ok ? bs0 : BSrc{nullptr, nullptr, nullptr, nullptr}, kk, a.w.group, braw[0]);
-    load_b<Q4>(ok ? bs1 : BSrc{nullptr, nullptr, nullptr, nullptr}, kk, a.w.group, braw[1]);
-  };
-
-  load_a(0);
-  store_a(0);
-  load_bs(0);
-  __syncthreads();
-  int buf = 0;
-  for (int k0 = 0; k0 < K; k0 += KT) {
-    u32x4_t bf0[4], bf1[4];
-    make_frags<Q4>(braw[0], bf0);
-    make_frags<Q4>(braw[1], bf1);
-    const bool more = k0 + KT < K;
-    if (more) {
-      load_a(k0 + KT);
-      load_bs(k0 + KT);
-    }
-    const uint16_t* Ab = As + buf * (MT * AS);
+    if constexpr (Q4) {
+      b.q[0] = ld16(rw, ok ? wo0 + kk / 2 : OOB);
+      b.q[1] = ld16(rw, ok ? wo1 + kk / 2 : OOB);
+      const uint32_t g2 = (kk / ws.group) * 2;
+      b.s[0] = ld2(rs, ok ? so0 + g2 : OOB);
+      b.z[0] = ld2(rz, ok ? so0 + g2 : OOB);
+      b.s[1] = ld2(rs, ok ? so1 + g2 : OOB);
+      b.z[1] = ld2(rz, ok ? so1 + g2 : OOB);
+    } else {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (m < nslice) {
-          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + (m * 32 + r32) * AS + 32 * hi + 8 * s);
-          if (fv0) acc[m][0] = mfma32(af, bf0[s], acc[m][0]);
-          if (fv1) acc[m][1] = mfma32(af, bf1[s], acc[m][1]);
-        }
+      for (int s = 0; s < 4; ++s) {
+        b.v[0][s] = ld16(rw, ok ? wo0 + kk * 2 + 16 * s : OOB);
+        b.v[1][s] = ld16(rw, ok ? wo1 + kk * 2 + 16 * s : OOB);
       }
     }
-    if (more) store_a(buf ^ 1);
+  };
+  auto frag = [&](const BRegs<Q4>& b, int f, int s) -> u32x4_t {
+    if constexpr (Q4) {
+      uint32_t o[4];
+      dq8(b.q[f][s], bf2f(b.s[f]), bf2f(b.z[f]), o);   // OOB rows load q = s = z = 0 -> exact zeros
+      return u32x4_t{o[0], o[1], o[2], o[3]};
+    } else {
+      return b.v[f][s];
+    }
+  };
+
+  const int nk = (K + KT - 1) / KT;
+  load_a(0);
+  load_b(0, bc);
+  store_a(0);
+  __syncthreads();
+  for (int i = 0; i < nk; ++i) {
+    const int buf = i & 1;
+    const bool more = i + 1 < nk;
+    if (more) {
+      load_a((i + 1) * KT);
+      load_b((i + 1) * KT, bn);
+    }
+    const uint16_t* Ab = As + buf * (MT * AS) + r32 * AS + 32 * hi;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4_t b0 = frag(bc, 0, s);
+      const u32x4_t b1 = frag(bc, 1, s);
+#pragma unroll
+      for (int m = 0; m < NS; ++m) {
+        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
+        acc[m][0] = mfma32(af, b0, acc[m][0]);
+        acc[m][1] = mfma32(af, b1, acc[m][1]);
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+      bc = bn;
+    }
     __syncthreads();
-    buf ^= 1;
   }
   // ---- LoRA K-extension: ext[row][0:32] . Bext[n][0:32]
-  const uint16_t* eb = kind == SMEL_KIND_SEL ? (a.w.ext_sel ? a.w.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
-                                               : (kind == SMEL_KIND_SHARED ? a.w.ext_sh : nullptr);
+  const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
+                                             : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
   if (a.ext && eb) {
+    const rsrc_t re = make_rsrc(eb, (uint64_t)a.N * 64);
+    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
     u32x4_t b0[2], b1[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      b0[s] = fv0 ? *reinterpret_cast<const u32x4_t*>(eb + (int64_t)n0 * 32 + 16 * hi + 8 * s) : u32x4_t{};
-      b1[s] = fv1 ? *reinterpret_cast<const u32x4_t*>(eb + (int64_t)n1 * 32 + 16 * hi + 8 * s) : u32x4_t{};
+      b0[s] = ld16(re, fv0 ? (uint32_t)n0 * 64 + 32 * hi + 16 * s : OOB);
+      b1[s] = ld16(re, fv1 ? (uint32_t)n1 * 64 + 32 * hi + 16 * s : OOB);
     }
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if (m >= nslice) continue;
+    for (int m = 0; m < NS; ++m) {
       const int row = m * 32 + r32;
-      const uint16_t* er = a.ext + (int64_t)(row0 + row) * 32;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const u32x4_t af = row < nrows ? *reinterpret_cast<const u32x4_t*>(er + 16 * hi + 8 * s) : u32x4_t{};
-        if (fv0) acc[m][0] = mfma32(af, b0[s], acc[m][0]);
-        if (fv1) acc[m][1] = mfma32(af, b1[s], acc[m][1]);
+        const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 32 * hi + 16 * s : OOB);
+        acc[m][0] = mfma32(af, b0[s], acc[m][0]);
+        acc[m][1] = mfma32(af, b1[s], acc[m][1]);
       }
     }
   }
   // ---- epilogue
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (m >= nslice) continue;
+  for (int m = 0; m < NS; ++m) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m * 32 + acc_row(r, l);
@@ -236,25 +228,35 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   }
 }
 
+template <int EPI, bool Q4>
+SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As) {
+  switch ((nrows + 31) >> 5) {
+    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, As); break;
+    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, As); break;
+    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, As); break;
+    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, As); break;
+  }
+}
+
 template <int EPI>
-__global__ __launch_bounds__(256) void gmm_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2 * MT * AS];
   if ((int)blockIdx.x >= a.n_tiles[0]) return;
   const int4 t = a.tiles[blockIdx.x];
   const int gk = a.gkind[t.x];
   const int kind = gk >> 16, idx = gk & 0xffff;
-  const int nrows = t.z - t.y;
+  const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4)
-    run_tile<EPI, true>(a, kind, idx, t.y, nrows, As);
+    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, As);
   else
-    run_tile<EPI, false>(a, kind, idx, t.y, nrows, As);
+    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, As);
 }
 
 }  // namespace
 
 extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
-                            int64_t max_tiles, const uint16_t* A, int64_t lda, int32_t a_gather,
+                            int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
                             int32_t act, uint16_t* out, int64_t ldo, uint16_t* hsave, hipStream_t stream) {
   SMEL_REQUIRE(w && gkind && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_fwd: null pointer");
@@ -269,6 +271,7 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_fwd: act %d", act);
+  SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_fwd: A larger than 2 GiB");
   if (max_tiles == 0) return 0;
   FwdArgs a;
   a.w = *w;
@@ -277,6 +280,7 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
   a.n_tiles = n_tiles;
   a.A = A;
   a.lda = lda;
+  a.a_rows = a_rows;
   a.order = order;
   a.ext = ext;
   a.out = out;

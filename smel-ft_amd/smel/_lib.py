@@ -35,11 +35,11 @@ SIGNATURES = {
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
     "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
-    "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i32, vp, i64, i64, vp, i32, i32, vp,
-                           i64, vp, vp]),
+    "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
+                           vp, i64, vp, vp]),
     "smel_combine": (i32, [vp, vp, vp, i64, i64, i64, vp, vp]),
-    "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i32, vp, i64, i64, vp, i32, i32, vp,
-                           vp, vp, vp, i64, vp, vp]),
+    "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
+                           vp, vp, vp, vp, i64, vp, vp]),
     "smel_gmm_bwd_nblocks": (i64, [i64]),
     "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, i64, vp, vp]),
     "smel_dtopv": (i32, [vp, i64, vp, i64, vp, vp]),

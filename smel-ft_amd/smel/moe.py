@@ -273,7 +273,7 @@ def _router_dx(dl: torch.Tensor, wr: torch.Tensor, T: int) -> torch.Tensor:
     w = L.WSet()
     w.wsh = L.ptr(wr)
     w.R, w.C, w.group = wr.shape[0], H, 32
-    L.call("smel_gmm_bwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dl), dl.shape[1], 0,
+    L.call("smel_gmm_bwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dl), dl.shape[1], T, 0,
            None, 0, 1, None, 0, 0, None, None, None, L.ptr(dx), H, None, L.stream(), tag="gemm_router_bwd")
     return dx
 
@@ -350,7 +350,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     actb = bf(M, I)
     hsave = bf(M, 2 * I) if need_grad else None
     w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"))
-    L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, 1,
+    L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_gu_fwd")
     if any_lora:
         ext_dn = bf(M, EXT)
@@ -358,7 +358,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
                K, L.ptr(g(lb_ex, "a_dn")), L.ptr(g(lb_sh, "a_dn")), I, s_ex, s_sh, L.ptr(ext_dn), st)
     Y = bf(M, H)
     w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
-    L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, 0,
+    L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dn), 0, _ACT[ex.act], L.ptr(Y), H, None, st, tag="gemm_dn_fwd")
     out = bf(T, H)
     L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(sgate), T, K, H, L.ptr(out), st)
@@ -401,7 +401,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     dh = bf(M, 2 * I)
     dwp = torch.empty(M, nblk, dtype=torch.float32, device=dev)
     w_dn = _wset(ex, "dn", t["sel_dn"], sh_dn, g(lb_ex, "a_dn"), g(lb_sh, "a_dn"))
-    L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, 1,
+    L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["topv"]),
            L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st, tag="gemm_dn_bwd")
     # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
@@ -413,7 +413,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     # (4) gate_up backward: per-slot dx rows
     dxs = bf(M, H)
     w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "a_gu"), g(lb_sh, "a_gu"))
-    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, 0,
+    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, L.ptr(dxs), H, None, st,
            tag="gemm_gu_bwd")
     # (5) router backward (fused layer) or d topv (routed_experts)

@@ -49,10 +49,10 @@ def test_host_side_rejections():
     # dequant: K not a multiple of the group
     assert L.smel_dequant_int4(1, 1, 1, 1, 4, 96, 64, 0, None) == -1
     # gmm: null weight set
-    assert L.smel_gmm_fwd(None, 1, 1, 1, 1, 1, 64, 0, None, 0, 1, None, 0, 0, 1, 64, None, None) == -1
+    assert L.smel_gmm_fwd(None, 1, 1, 1, 1, 1, 64, 4, 0, None, 0, 1, None, 0, 0, 1, 64, None, None) == -1
     w = _lib.WSet()
     w.R, w.C, w.group = 64, 48, 64
-    assert L.smel_gmm_fwd(ctypes.byref(w), 1, 1, 1, 1, 16, 48, 0, None, 0, 1, None, 0, 0, 16, 64, None, None) == -2
+    assert L.smel_gmm_fwd(ctypes.byref(w), 1, 1, 1, 1, 16, 48, 4, 0, None, 0, 1, None, 0, 0, 16, 64, None, None) == -2
     with pytest.raises(_lib.SmelError):
         _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, 32, 64, 64, None, None, None, None, None,
                   None, None)
