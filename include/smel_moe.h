@@ -97,12 +97,12 @@ int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, 
 
 /* ---- (A11/A12) LoRA down-projections of the rows of LoRA groups (SEL / SHARED tiles of the tile list):
  * ext[row][0:32] = bf16(scale_g * A_src[src(row)][0:Kd] . wcat_g[0:32][0:Kd]) where src(row) = token of the row if
- * a_gather else row, wcat_g = wcat_sel + idx*32*Kd, scale_g = scale_sel (SEL) or wcat_sh, scale_sh (SHARED).
- * Rows of other groups are left untouched. Kd must be a multiple of 32. */
+ * a_gather else row (A holds a_rows rows), wcat_g = wcat_sel + idx*32*Kd, scale_g = scale_sel (SEL) or wcat_sh,
+ * scale_sh (SHARED). Rows of other groups are left untouched. Kd must be a multiple of 32. */
 int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,
-                  const uint16_t* A_src, int64_t lda, int32_t a_gather, const int32_t* order, int64_t TK,
-                  int64_t topk, const uint16_t* wcat_sel, const uint16_t* wcat_sh, int64_t Kd, float scale_sel,
-                  float scale_sh, uint16_t* ext, hipStream_t stream);
+                  const uint16_t* A_src, int64_t lda, int64_t a_rows, int32_t a_gather, const int32_t* order,
+                  int64_t TK, int64_t topk, const uint16_t* wcat_sel, const uint16_t* wcat_sh, int64_t Kd,
+                  float scale_sel, float scale_sh, uint16_t* ext, hipStream_t stream);
 
 /* ---- (A5/A6/A11) grouped expert GEMM, forward: out = A W^T per group, W from w (int4 dequantized in registers,
  * or bf16), plus the LoRA K-extension ext[row] . w.ext_*[n] for SEL/SHARED groups when ext != NULL.
@@ -155,14 +155,14 @@ int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, int32_t with_shared
 /* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP):
  * for every LoRA group lora_groups[i] (expert id, or E for the shared rows [TK, TK+T)):
  *   out[i][p][q] = sum_{rows of the group} alpha(row) * L[row][p] * Rm[src(row)][q],  p < 32, q < Q
- * in a fixed order (rows in chunks of 256 into part, then the chunks in order). src(row) = token of the row if
- * r_gather else row; alpha = the row weight (topv[p] / sgate[t]) if use_w, else 1.
- * out [n_lora][32][Q] fp32; part [n_lora][part_chunks][32][Q] fp32 scratch with
- * part_chunks = smel_lora_wgrad_part_chunks(max rows of one group). */
+ * in a fixed order (MFMA over 64-row steps inside 1024-row chunks into part, then the chunks in order). src(row) =
+ * token of the row if r_gather else row; Rm holds r_rows rows; alpha = the row weight (topv[p] / sgate[t]) if use_w,
+ * else 1 (folded into L before its bf16 rounding). out [n_lora][32][Q] fp32; part [n_lora][part_chunks][32][Q] fp32
+ * scratch with part_chunks = smel_lora_wgrad_part_chunks(max rows of one group). Q must be a multiple of 16. */
 int smel_lora_wgrad(const int32_t* lora_groups, int64_t n_lora, const int32_t* offsets, int64_t E, int64_t T,
                     int64_t TK, int64_t topk, const int32_t* order, const uint16_t* L, const uint16_t* Rm,
-                    int64_t ldr, int32_t r_gather, int32_t use_w, const uint16_t* topv, const float* sgate,
-                    int64_t Q, float* part, int64_t part_chunks, float* out, hipStream_t stream);
+                    int64_t ldr, int64_t r_rows, int32_t r_gather, int32_t use_w, const uint16_t* topv,
+                    const float* sgate, int64_t Q, float* part, int64_t part_chunks, float* out, hipStream_t stream);
 int64_t smel_lora_wgrad_part_chunks(int64_t max_group_rows);
 
 #ifdef __cplusplus

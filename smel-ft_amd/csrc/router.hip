@@ -95,29 +95,47 @@ __global__ __launch_bounds__(256) void route_fwd(const uint16_t* __restrict__ x,
   const int ncol = E + (sg ? 1 : 0);
   const int nfrag = (ncol + 31) / 32;
   f32x16_t acc[3];
-  const uint16_t* brow[3];
+  uint32_t boff[3];
+  const rsrc_t rg = make_rsrc(gw, (uint64_t)E * H * 2);
+  const rsrc_t rsg = make_rsrc(sg, sg ? (uint64_t)H * 2 : 0);
+  bool bsg[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
     acc[i] = f32x16_t{};
     const int f = w + 4 * i;
     const int e = 32 * f + r32;
-    brow[i] = (f < nfrag) ? (e < E ? gw + (int64_t)e * H : (e == E && sg ? sg : nullptr)) : nullptr;
+    bsg[i] = f < nfrag && e == E && sg;
+    boff[i] = (f < nfrag && e < E) ? (uint32_t)e * H * 2 : (bsg[i] ? 0u : OOB);
   }
   const int t = t0 + r32;
-  const uint16_t* arow = t < T ? x + (int64_t)t * H : nullptr;
-  for (int k0 = 0; k0 < H; k0 += 64) {
-    u32x4_t a[4];
+  const rsrc_t rx = make_rsrc(x, (uint64_t)T * H * 2);
+  const uint32_t aoff = t < T ? (uint32_t)t * H * 2 : OOB;
+  // loads of step k0 + 64 are in flight while step k0 multiplies
+  u32x4_t a[4], b[3][4], an[4], bn[3][4];
+  auto load = [&](int k0, u32x4_t* av, u32x4_t (*bv)[4]) {
+    const uint32_t ko = (uint32_t)(k0 + 32 * hi) * 2;
+    const bool ok = k0 < H;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      a[s] = arow ? *reinterpret_cast<const u32x4_t*>(arow + k0 + 32 * hi + 8 * s) : u32x4_t{};
+    for (int s = 0; s < 4; ++s) av[s] = ld16(rx, ok ? aoff + ko + 16 * s : OOB);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) bv[i][s] = ld16(bsg[i] ? rsg : rg, ok ? boff[i] + ko + 16 * s : OOB);
+  };
+  load(0, a, b);
+  for (int k0 = 0; k0 < H; k0 += 64) {
+    load(k0 + 64, an, bn);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       if (w + 4 * i >= nfrag) continue;   // wave-uniform
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4_t b = brow[i] ? *reinterpret_cast<const u32x4_t*>(brow[i] + k0 + 32 * hi + 8 * s) : u32x4_t{};
-        acc[i] = mfma32(a[s], b, acc[i]);
-      }
+      for (int s = 0; s < 4; ++s) acc[i] = mfma32(a[s], b[i][s], acc[i]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      a[s] = an[s];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) b[i][s] = bn[i][s];
     }
   }
 #pragma unroll

@@ -34,7 +34,7 @@ SIGNATURES = {
     "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
     "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
-    "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
+    "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, i64, vp, vp]),
     "smel_combine": (i32, [vp, vp, vp, i64, i64, i64, vp, vp]),
@@ -44,8 +44,8 @@ SIGNATURES = {
     "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, i64, vp, vp]),
     "smel_dtopv": (i32, [vp, i64, vp, i64, vp, vp]),
     "smel_dx_reduce": (i32, [vp, vp, i32, i64, i64, i64, vp, vp]),
-    "smel_lora_wgrad": (i32, [vp, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, i32, i32, vp, vp, i64, vp, i64, vp,
-                              vp]),
+    "smel_lora_wgrad": (i32, [vp, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, i64, i32, i32, vp, vp, i64, vp, i64,
+                              vp, vp]),
     "smel_lora_wgrad_part_chunks": (i64, [i64]),
 }
 

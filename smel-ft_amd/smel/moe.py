@@ -345,7 +345,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     ext_gu = ext_dn = None
     if any_lora:
         ext_gu = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, 1, L.ptr(order), TK, K,
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, T, 1, L.ptr(order), TK, K,
                L.ptr(g(lb_ex, "a_gu")), L.ptr(g(lb_sh, "a_gu")), H, s_ex, s_sh, L.ptr(ext_gu), st)
     actb = bf(M, I)
     hsave = bf(M, 2 * I) if need_grad else None
@@ -354,7 +354,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
            L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_gu_fwd")
     if any_lora:
         ext_dn = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(actb), I, 0, L.ptr(order), TK,
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(actb), I, M, 0, L.ptr(order), TK,
                K, L.ptr(g(lb_ex, "a_dn")), L.ptr(g(lb_sh, "a_dn")), I, s_ex, s_sh, L.ptr(ext_dn), st)
     Y = bf(M, H)
     w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
@@ -394,7 +394,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     ext_db = None
     if any_lora:
         ext_db = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dout), H, 1, L.ptr(order), TK, K,
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dout), H, T, 1, L.ptr(order), TK, K,
                L.ptr(g(lb_ex, "bt_dn")), L.ptr(g(lb_sh, "bt_dn")), H, s_ex, s_sh, L.ptr(ext_db), st)
     # (2) down backward + SiLU-gate backward + d(row weight) partials
     nblk = L.load().smel_gmm_bwd_nblocks(I)
@@ -408,7 +408,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     ext_dxa = None
     if any_lora:
         ext_dxa = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * I, 0, L.ptr(order), TK,
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * I, M, 0, L.ptr(order), TK,
                K, L.ptr(g(lb_ex, "bt_gu")), L.ptr(g(lb_sh, "bt_gu")), 2 * I, s_ex, s_sh, L.ptr(ext_dxa), st)
     # (4) gate_up backward: per-slot dx rows
     dxs = bf(M, H)
@@ -444,8 +444,8 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
         def wgrad(Lbuf, Rm, ldr, r_gather, use_w, Q):
             out = torch.empty(n_lora, EXT, Q, dtype=torch.float32, device=dev)
             L.call("smel_lora_wgrad", L.ptr(groups), n_lora, L.ptr(t["offsets"]), E, T, TK, K, L.ptr(order),
-                   L.ptr(Lbuf), L.ptr(Rm), ldr, r_gather, use_w, L.ptr(t["topv"]), L.ptr(t["sgate"]), Q, L.ptr(part),
-                   chunks, L.ptr(out), st)
+                   L.ptr(Lbuf), L.ptr(Rm), ldr, Rm.shape[0], r_gather, use_w, L.ptr(t["topv"]), L.ptr(t["sgate"]), Q,
+                   L.ptr(part), chunks, L.ptr(out), st, tag="lora_wgrad")
             return out
 
         dA_gu = wgrad(ext_dxa, t["x"], H, 1, 0, H)          # [n, 32, H]: A_gate rows 0..r-1, A_up rows 16..
