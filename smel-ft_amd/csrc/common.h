@@ -107,6 +107,25 @@ SMEL_DEV rsrc_t make_rsrc(const void* base, uint64_t bytes) {
 SMEL_DEV u32x4_t ld16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 SMEL_DEV uint32_t ld2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
 
+// ------------------------------------------------------------------------------------------------ XCD-aware tiles
+// MI355X has 8 XCDs, each with its own L2; consecutive workgroup ids go to consecutive XCDs. A 1-D grid of
+// xcd_grid(max_tiles) * nblk workgroups is mapped so that XCD x owns a contiguous run of the tile list and runs the
+// nblk column blocks of each tile back to back: the blocks of one tile share its A rows in that XCD's L2, and the
+// tiles of one expert (adjacent in the list) share its weights there.
+constexpr int NXCD = 8;
+inline int64_t xcd_grid(int64_t max_tiles) { return (max_tiles + NXCD - 1) / NXCD * NXCD; }
+SMEL_DEV bool xcd_tile(int n_tiles, int nblk, int& tile, int& nb) {
+  const int b = blockIdx.x;
+  const int x = b % NXCD, j = b / NXCD;
+  const int per = (n_tiles + NXCD - 1) / NXCD;   // tiles per XCD
+  const int t0 = x * per;
+  const int cnt = min(per, n_tiles - t0);
+  if (cnt <= 0 || j >= cnt * nblk) return false;
+  tile = t0 + j / nblk;
+  nb = j % nblk;
+  return true;
+}
+
 // ------------------------------------------------------------------------------------------------ row mapping
 // Rows of the grouped GEMMs: [0, TK) are the routed slots in expert-sorted order, [TK, TK + T) the shared expert
 // (one row per token, in token order). order[row] = flat slot p = t*K + k of a routed row.

@@ -38,6 +38,7 @@ struct BwdArgs {
   float* dwp;
   int a_gather, TK, topk, act;
   int Kd, N;   // Kd = w.R (contraction), N = w.C
+  int nblk;    // column blocks per tile
 };
 
 // Raw W data of one thread for one step: rows (ka, ka+1), 32 columns.
@@ -54,9 +55,9 @@ struct WRegs<false> {
 };
 
 template <int EPI, bool Q4, int NS>
-SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As, uint16_t* Bt) {
+SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As,
+                       uint16_t* Bt) {
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
-  const int nb = blockIdx.y;
   const int n0 = nb * NT;
   const int Kd = a.Kd;
   const smel_wset& ws = a.w;
@@ -263,17 +264,18 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   __syncthreads();
   if (tid < MT && tid < nrows) {
     const float v = ((red[tid] + red[MT + tid]) + red[2 * MT + tid]) + red[3 * MT + tid];
-    a.dwp[(int64_t)(row0 + tid) * gridDim.y + nb] = v;
+    a.dwp[(int64_t)(row0 + tid) * a.nblk + nb] = v;
   }
 }
 
 template <int EPI, bool Q4>
-SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As, uint16_t* Bt) {
+SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As,
+                          uint16_t* Bt) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, As, Bt); break;
-    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, As, Bt); break;
-    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, As, Bt); break;
-    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, As, Bt); break;
+    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, nb, As, Bt); break;
+    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, nb, As, Bt); break;
+    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, nb, As, Bt); break;
+    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, nb, As, Bt); break;
   }
 }
 
@@ -281,16 +283,17 @@ template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[MT * AS];
   __shared__ __attribute__((aligned(16))) uint16_t Bt[NT * BS];
-  if ((int)blockIdx.x >= a.n_tiles[0]) return;
-  const int4 t = a.tiles[blockIdx.x];
+  int tile, nb;
+  if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
+  const int4 t = a.tiles[tile];
   const int gk = a.gkind[t.x];
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4)
-    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, As, Bt);
+    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, nb, As, Bt);
   else
-    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, As, Bt);
+    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, nb, As, Bt);
 }
 
 }  // namespace
@@ -338,7 +341,8 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   a.act = act;
   a.Kd = (int)w->R;
   a.N = (int)w->C;
-  dim3 grid((unsigned)max_tiles, (unsigned)smel_gmm_bwd_nblocks(w->C));
+  a.nblk = (int)smel_gmm_bwd_nblocks(w->C);
+  const unsigned grid = (unsigned)(xcd_grid(max_tiles) * a.nblk);
   if (epilogue == 1)
     gmm_bwd_kernel<1><<<grid, 256, 0, stream>>>(a);
   else

@@ -35,6 +35,7 @@ struct FwdArgs {
   uint16_t* hsave;
   int a_gather, TK, topk, act;
   int N, K;   // N = w.R (weight rows), K = w.C
+  int nblk;   // column blocks per tile
 };
 
 // Weight rows of one wave for one k-step: int4 (16 B = 32 nibbles per lane and fragment, plus its group's scale and
@@ -52,9 +53,8 @@ struct BRegs<false> {
 };
 
 template <int EPI, bool Q4, int NS>
-SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As) {
+SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As) {
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
-  const int nb = blockIdx.y;
   const int K = a.K;
   const smel_wset& ws = a.w;
   // ---- this wave's two weight rows (per lane): gate/up pair for epilogue 1, two adjacent 32-column blocks else
@@ -229,28 +229,29 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 }
 
 template <int EPI, bool Q4>
-SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, uint16_t* As) {
+SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, As); break;
-    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, As); break;
-    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, As); break;
-    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, As); break;
+    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, nb, As); break;
+    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, nb, As); break;
+    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, nb, As); break;
+    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, nb, As); break;
   }
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2 * MT * AS];
-  if ((int)blockIdx.x >= a.n_tiles[0]) return;
-  const int4 t = a.tiles[blockIdx.x];
+  int tile, nb;
+  if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
+  const int4 t = a.tiles[tile];
   const int gk = a.gkind[t.x];
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4)
-    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, As);
+    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, nb, As);
   else
-    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, As);
+    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, nb, As);
 }
 
 }  // namespace
@@ -292,12 +293,11 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
   a.act = act;
   a.N = (int)w->R;
   a.K = (int)w->C;
-  if (epilogue == 1) {
-    dim3 grid((unsigned)max_tiles, (unsigned)((w->R / 2 + 127) / 128));
+  a.nblk = (int)(epilogue == 1 ? (w->R / 2 + 127) / 128 : (w->R + 255) / 256);
+  const unsigned grid = (unsigned)(xcd_grid(max_tiles) * a.nblk);
+  if (epilogue == 1)
     gmm_fwd_kernel<1><<<grid, 256, 0, stream>>>(a);
-  } else {
-    dim3 grid((unsigned)max_tiles, (unsigned)((w->R + 255) / 256));
+  else
     gmm_fwd_kernel<0><<<grid, 256, 0, stream>>>(a);
-  }
   return smel::launch_status();
 }

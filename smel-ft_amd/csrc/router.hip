@@ -82,15 +82,16 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
   }
 }
 
-// One block = 32 tokens; wave w computes expert columns of fragments w, w+4, w+8 (32 columns each; the column E is
-// the shared-expert gate when sg != nullptr). H % 64 == 0.
-__global__ __launch_bounds__(256) void route_fwd(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gw,
+// One block = 32 tokens, 8 waves: wave w computes expert columns of fragments (w&3), (w&3)+4, (w&3)+8 (32 columns
+// each; the column E is the shared-expert gate when sg != nullptr) over the even (w < 4) or odd (w >= 4) 64-wide
+// k-steps; the two halves are added (odd into even, fixed order) through LDS. H % 64 == 0.
+__global__ __launch_bounds__(512) void route_fwd(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gw,
                                                  const uint16_t* __restrict__ sg, int T, int H, int E, int K,
                                                  float* __restrict__ probs, uint16_t* __restrict__ topv,
                                                  int64_t* __restrict__ topi, int32_t* __restrict__ topi32,
                                                  float* __restrict__ sgate) {
   __shared__ float lg[TB * LG_STRIDE];
-  const int l = lane_id(), w = threadIdx.x >> 6, hi = l >> 5, r32 = l & 31;
+  const int l = lane_id(), wv = threadIdx.x >> 6, w = wv & 3, kh = wv >> 2, hi = l >> 5, r32 = l & 31;
   const int t0 = blockIdx.x * TB;
   const int ncol = E + (sg ? 1 : 0);
   const int nfrag = (ncol + 31) / 32;
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void route_fwd(const uint16_t* __restrict__ x,
   const int t = t0 + r32;
   const rsrc_t rx = make_rsrc(x, (uint64_t)T * H * 2);
   const uint32_t aoff = t < T ? (uint32_t)t * H * 2 : OOB;
-  // loads of step k0 + 64 are in flight while step k0 multiplies
+  // loads of step k0 + 128 are in flight while step k0 multiplies
   u32x4_t a[4], b[3][4], an[4], bn[3][4];
   auto load = [&](int k0, u32x4_t* av, u32x4_t (*bv)[4]) {
     const uint32_t ko = (uint32_t)(k0 + 32 * hi) * 2;
@@ -122,9 +123,9 @@ __global__ __launch_bounds__(256) void route_fwd(const uint16_t* __restrict__ x,
 #pragma unroll
       for (int s = 0; s < 4; ++s) bv[i][s] = ld16(bsg[i] ? rsg : rg, ok ? boff[i] + ko + 16 * s : OOB);
   };
-  load(0, a, b);
-  for (int k0 = 0; k0 < H; k0 += 64) {
-    load(k0 + 64, an, bn);
+  load(64 * kh, a, b);
+  for (int k0 = 64 * kh; k0 < H; k0 += 128) {
+    load(k0 + 128, an, bn);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       if (w + 4 * i >= nfrag) continue;   // wave-uniform
@@ -138,16 +139,32 @@ __global__ __launch_bounds__(256) void route_fwd(const uint16_t* __restrict__ x,
       for (int i = 0; i < 3; ++i) b[i][s] = bn[i][s];
     }
   }
+  // odd-step partial sums -> LDS, then the even-step waves add them and round the logits to bf16
+  if (kh == 1) {
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int f = w + 4 * i;
-    if (f >= nfrag) continue;
+    for (int i = 0; i < 3; ++i) {
+      const int f = w + 4 * i;
+      if (f >= nfrag) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) lg[acc_row(r, l) * LG_STRIDE + 32 * f + r32] = bf2f(f2bf(acc[i][r]));
+      for (int r = 0; r < 16; ++r) lg[acc_row(r, l) * LG_STRIDE + 32 * f + r32] = acc[i][r];
+    }
   }
   __syncthreads();
-  for (int j = 0; j < TB / 4; ++j) {
-    const int row = w * (TB / 4) + j;
+  if (kh == 0) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int f = w + 4 * i;
+      if (f >= nfrag) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float* p = lg + acc_row(r, l) * LG_STRIDE + 32 * f + r32;
+        *p = bf2f(f2bf(acc[i][r] + *p));
+      }
+    }
+  }
+  __syncthreads();
+  for (int j = 0; j < TB / 8; ++j) {
+    const int row = wv * (TB / 8) + j;
     const int64_t tt = t0 + row;
     if (tt >= T) break;
     const float* lrow = lg + row * LG_STRIDE;
@@ -258,7 +275,7 @@ extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint1
   SMEL_REQUIRE(!shared_gate_w || sgate, SMEL_EINVAL, "route: sgate output needed with shared_gate_w");
   if (T == 0) return 0;
   SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32, SMEL_EINVAL, "route: null pointer");
-  route_fwd<<<(unsigned)((T + TB - 1) / TB), 256, 0, stream>>>(x, gate_w, shared_gate_w, (int)T, (int)H, (int)E,
+  route_fwd<<<(unsigned)((T + TB - 1) / TB), 512, 0, stream>>>(x, gate_w, shared_gate_w, (int)T, (int)H, (int)E,
                                                                  (int)K, probs, topv, topi, topi32, sgate);
   return smel::launch_status();
 }
