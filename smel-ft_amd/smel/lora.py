@@ -63,6 +63,30 @@ class MLPLoRA(nn.Module):
                 s * self.B_down.float() @ self.A_down.float())
 
 
+def lora_linear(x, w, A, B, scale):
+    """x w^T + scale (x A^T) B^T with the LoRA factors cast to x's dtype (smel/lora.py:61-69). A dense helper of the
+    API; the MoE layer itself runs its LoRA products inside the grouped-GEMM kernels."""
+    y = x @ w.t()
+    if A is None:
+        return y
+    if x.dim() == 2:
+        return torch.addmm(y, x @ A.to(x.dtype).t(), B.to(x.dtype).t(), alpha=scale)
+    return y + scale * ((x @ A.to(x.dtype).t()) @ B.to(x.dtype).t())
+
+
+def lora_gate_up(x, w_gate_up, A_gate, B_gate, A_up, B_up, scale):
+    """(gate, up) of a gated MLP from one stacked [2I, H] weight (smel/lora.py:72-83); dense helper of the API."""
+    I = w_gate_up.shape[0] // 2
+    base = x @ w_gate_up.t()
+    if A_gate is None:
+        return base[:, :I], base[:, I:]
+    r = A_gate.shape[0]
+    xa = x @ torch.cat((A_gate, A_up)).to(x.dtype).t()
+    g = torch.addmm(base[:, :I], xa[:, :r], B_gate.to(x.dtype).t(), alpha=scale)
+    u = torch.addmm(base[:, I:], xa[:, r:], B_up.to(x.dtype).t(), alpha=scale)
+    return g, u
+
+
 class LayerLoRA(nn.Module):
     def __init__(self, experts: ExpertsLoRA | None, shared: MLPLoRA | None):
         super().__init__()

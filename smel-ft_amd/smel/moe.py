@@ -553,6 +553,131 @@ def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
     return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
 
 
+class _MLPFn(torch.autograd.Function):
+    """Gated MLP with LoRA on gate/up/down (mlp_lora, smel/moe.py:183-194) as one dense group of the grouped GEMMs:
+    rows = tokens, weights = the stacked gate_up [2Is, H] and down [H, Is]."""
+
+    @staticmethod
+    def forward(ctx, x, w_gu, w_dn, lora, act_name, *leaves):
+        T, H = x.shape
+        Is = w_dn.shape[1]
+        dev = x.device
+        st = L.stream()
+        tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
+        lb = _LoRABufs(lora, 1, H, Is, dev) if lora is not None else None
+        bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+        g = lambda n: getattr(lb, n) if lb is not None else None
+        sc = lb.scale if lb is not None else 0.0
+        ext_gu = ext_dn = None
+        if lb is not None:
+            ext_gu = bf(T, EXT)
+            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, T, 0, None, 0, 1,
+                   None, L.ptr(lb.a_gu), H, 0.0, sc, L.ptr(ext_gu), st)
+        actb, hsave = bf(T, Is), bf(T, 2 * Is)
+        wg = _dense_wset(w_gu, g("fwd_gu"))
+        L.call("smel_gmm_fwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 0,
+               None, 0, 1, L.ptr(ext_gu), 1, _ACT[act_name], L.ptr(actb), Is, L.ptr(hsave), st, tag="gemm_mlp_gu_fwd")
+        if lb is not None:
+            ext_dn = bf(T, EXT)
+            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(actb), Is, T, 0, None, 0, 1,
+                   None, L.ptr(lb.a_dn), Is, 0.0, sc, L.ptr(ext_dn), st)
+        y = bf(T, H)
+        wd = _dense_wset(w_dn, g("fwd_dn"))
+        L.call("smel_gmm_fwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), Is, T, 0,
+               None, 0, 1, L.ptr(ext_dn), 0, _ACT[act_name], L.ptr(y), H, None, st, tag="gemm_mlp_dn_fwd")
+        ctx.save_for_backward(x, w_gu, w_dn, actb, hsave)
+        ctx.ext = (ext_gu, ext_dn)
+        ctx.lb, ctx.lora, ctx.act_name = lb, lora, act_name
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w_gu, w_dn, actb, hsave = ctx.saved_tensors
+        ext_gu, ext_dn = ctx.ext
+        lb, lora = ctx.lb, ctx.lora
+        dy = _bf16(dy)
+        T, H = x.shape
+        Is = w_dn.shape[1]
+        dev = x.device
+        st = L.stream()
+        tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
+        bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+        g = lambda n: getattr(lb, n) if lb is not None else None
+        sc = lb.scale if lb is not None else 0.0
+        ones = torch.ones(T, dtype=torch.float32, device=dev)       # row weight 1 (no combine weight here)
+        ext_db = ext_dxa = None
+        if lb is not None:
+            ext_db = bf(T, EXT)
+            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dy), H, T, 0, None, 0, 1,
+                   None, L.ptr(lb.bt_dn), H, 0.0, sc, L.ptr(ext_db), st)
+        nblk = L.load().smel_gmm_bwd_nblocks(Is)
+        dh = bf(T, 2 * Is)
+        dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
+        wd = _dense_wset(w_dn, g("a_dn"))
+        L.call("smel_gmm_bwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
+               None, 0, 1, L.ptr(ext_db), 1, _ACT[ctx.act_name], L.ptr(hsave), None, L.ptr(ones), L.ptr(dh), 2 * Is,
+               L.ptr(dwp), st, tag="gemm_mlp_dn_bwd")
+        if lb is not None:
+            ext_dxa = bf(T, EXT)
+            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * Is, T, 0, None, 0, 1,
+                   None, L.ptr(lb.bt_gu), 2 * Is, 0.0, sc, L.ptr(ext_dxa), st)
+        dx = bf(T, H)
+        wg = _dense_wset(w_gu, g("a_gu"))
+        L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
+               0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, L.ptr(dx), H, None, st, tag="gemm_mlp_gu_bwd")
+        grads = [None] * 6
+        if lb is not None:
+            zero = torch.zeros(2, dtype=torch.int32, device=dev)     # offsets of zero experts
+            groups = torch.zeros(1, dtype=torch.int32, device=dev)   # group 0 >= E = 0: rows [0, T)
+            chunks = L.load().smel_lora_wgrad_part_chunks(T)
+            part = torch.empty(chunks * EXT * max(H, 2 * Is), dtype=torch.float32, device=dev)
+
+            def wgrad(Lbuf, Rm, Q):
+                out = torch.empty(1, EXT, Q, dtype=torch.float32, device=dev)
+                L.call("smel_lora_wgrad", L.ptr(groups), 1, L.ptr(zero), 0, T, 0, 1, None, L.ptr(Lbuf), L.ptr(Rm),
+                       Rm.shape[1], Rm.shape[0], 0, 0, None, None, Q, L.ptr(part), chunks, L.ptr(out), st)
+                return out[0]
+
+            r = lb.r
+            dA_gu, dB_gu = wgrad(ext_dxa, x, H), wgrad(ext_gu, dh, 2 * Is)
+            dA_dn, dB_dn = wgrad(ext_db, actb, Is), wgrad(ext_dn, dy, H)
+            named = {"A_gate": dA_gu[:r], "A_up": dA_gu[16:16 + r], "B_gate": dB_gu[:r, :Is].t(),
+                     "B_up": dB_gu[16:16 + r, Is:].t(), "A_down": dA_dn[:r], "B_down": dB_dn[:r].t()}
+            grads = [named[n].contiguous().to(getattr(lora, n).dtype) if getattr(lora, n).requires_grad else None
+                     for n in _LORA_NAMES]
+        ctx.lb = ctx.lora = ctx.ext = None
+        return (dx, None, None, None, None, *grads)
+
+
+def _dense_wset(w: torch.Tensor, ext) -> L.WSet:
+    ws = L.WSet()
+    ws.wsh = L.ptr(w)
+    ws.ext_sh = L.ptr(ext)
+    ws.R, ws.C, ws.group = w.shape[0], w.shape[1], 32
+    return ws
+
+
+def mlp_lora(x, w_gate, w_up, w_down, lora, act_name="silu", w_gate_up=None):
+    """Gated MLP down(act(gate(x)) * up(x)) with optional LoRA on all three projections (smel/moe.py:183-194),
+    as the dense group of the grouped GEMM kernels. x [T, H] bf16; weights bf16."""
+    if act_name not in _ACT:
+        raise ValueError(f"unknown activation {act_name}")
+    L.require_device(x, w_down)
+    xs = x.reshape(-1, x.shape[-1])
+    gu = w_gate_up if w_gate_up is not None else torch.cat((w_gate, w_up))
+    y = _MLPFn.apply(_bf16(xs), _bf16(gu), _bf16(w_down), lora, act_name, *_lora_leaves(lora))
+    return y.reshape(*x.shape[:-1], y.shape[-1])
+
+
+def shared_mlp(x, W, lora):
+    """smel/moe.py:197-201: the shared expert times sigmoid(x w_sg^T). moe_forward fuses this into its grouped
+    GEMMs; this stand-alone form multiplies the gate with torch ops."""
+    pre = "mlp.shared_expert."
+    y = mlp_lora(x, W[pre + "gate_proj.weight"], W[pre + "up_proj.weight"], W[pre + "down_proj.weight"], lora,
+                 w_gate_up=W.get(pre + "gate_up_proj.weight"))
+    return y * torch.sigmoid(F.linear(x, W["mlp.shared_expert_gate.weight"]))
+
+
 def _shared_weights(W: dict):
     pre = "mlp.shared_expert."
     if pre + "gate_proj.weight" not in W and pre + "gate_up_proj.weight" not in W:

@@ -309,3 +309,60 @@ def test_route_api_backward():
     tvo = sel / sel.sum(-1, keepdim=True)
     (tvo * cot).sum().backward()
     assert_close_bf16(xg.grad.cpu(), xo.grad, "dx", rel=3e-2, cos=0.999)
+
+
+@pytest.mark.parametrize("act_name,T,H,Is,r", [("silu", 300, 256, 128, 8), ("gelu_tanh", 257, 512, 192, 16),
+                                               ("silu", 64, 128, 64, 0)])
+def test_mlp_lora_parity(act_name, T, H, Is, r):
+    """mlp_lora (smel/moe.py:183-194; Gemma-4's dense GeGLU MLP with act gelu_tanh) as the dense group."""
+    from smel.lora import MLPLoRA
+    from smel.moe import mlp_lora
+    _say(f"mlp_lora {act_name} T{T} H{H} Is{Is} r{r}")
+    gen = torch.Generator().manual_seed(T)
+    x = torch.randn(T, H, generator=gen).to(torch.bfloat16)
+    wg = (torch.randn(Is, H, generator=gen) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(Is, H, generator=gen) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(H, Is, generator=gen) * 0.02).to(torch.bfloat16)
+    lora = None
+    if r:
+        lora = MLPLoRA(H, Is, r, 2.0 * r)
+        with torch.no_grad():
+            for n in ("B_gate", "B_up", "B_down"):
+                getattr(lora, n).copy_(torch.randn(getattr(lora, n).shape, generator=gen) * 0.05)
+        lora = lora.to(DEV)
+    xg = x.to(DEV).requires_grad_(True)
+    y = mlp_lora(xg, wg.to(DEV), wu.to(DEV), wd.to(DEV), lora, act_name)
+    gy = (torch.randn(T, H, generator=gen) * 1e-2).to(torch.bfloat16)
+    y.backward(gy.to(DEV))
+    xo = x.float().requires_grad_(True)
+    L_o = {n: getattr(lora, n).detach().cpu().clone().requires_grad_(True) for n in LORA_NAMES} if r else None
+    yo = R.mlp_lora(xo, torch.cat((wg, wu)).float(), wd.float(), L_o, 2.0 if r else 0.0, act_name)
+    yo.backward(gy.float())
+    assert_close_bf16(y.detach().cpu(), yo.detach(), "y")
+    assert_close_bf16(xg.grad.cpu(), xo.grad, "dx")
+    if r:
+        for n in LORA_NAMES:
+            assert_close_bf16(getattr(lora, n).grad.cpu(), L_o[n].grad, n)
+
+
+def test_gelu_experts_parity():
+    """GELU-tanh routed experts (Gemma 4's act, smel/moe.py:91-107) through routed_experts."""
+    from smel.moe import routed_experts
+    _say("gelu experts")
+    x, ol = R.make_layer(T=180, H=256, E=16, I=128, K=4, n_sel=2, r=8, alpha=16.0, shared_inter=None, seed=6,
+                         act_name="gelu_tanh", lora_b_std=0.05)
+    W, ex, lora = to_device_layer(ol, DEV)
+    probs, topv, topi = R.route(x.float(), ol.gate_w.float(), 4)
+    tv = topv.to(torch.bfloat16)
+    xg = x.to(DEV).requires_grad_(True)
+    y = routed_experts(xg, tv.to(DEV), topi.to(DEV), ex, lora.experts)
+    gy = (torch.randn(x.shape, generator=torch.Generator().manual_seed(2)) * 1e-2).to(torch.bfloat16)
+    y.backward(gy.to(DEV))
+    xo = x.float().requires_grad_(True)
+    leaves = {n: ol.ex_lora[n].clone().requires_grad_(True) for n in LORA_NAMES}
+    yo = R.routed_experts(xo, tv.float(), topi, ol, leaves, torch.float32)
+    yo.backward(gy.float())
+    assert_close_bf16(y.detach().cpu(), yo.detach(), "y")
+    assert_close_bf16(xg.grad.cpu(), xo.grad, "dx")
+    for n in LORA_NAMES:
+        assert_close_bf16(getattr(lora.experts, n).grad.cpu(), leaves[n].grad, n)
