@@ -36,6 +36,7 @@ typedef struct smel_wset {
   const uint8_t* q4;   /* int4 bank q  [E][R][C/2], low nibble = even column (smel/quant.py:42)     */
   const uint16_t* s4;  /* int4 bank scale [E][R][C/group] bf16                                      */
   const uint16_t* z4;  /* int4 bank zero  [E][R][C/group] bf16                                      */
+  const uint32_t* sz4; /* the same scale/zero packed by smel_int4_pack_sz (forward GEMM operand)    */
   const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down)                         */
   const uint16_t* wsel;/* selected experts [n_sel][R][C] (LayerExperts.sel_gate_up / sel_down)      */
   const uint16_t* wsh; /* shared expert [R][C]                                                      */
@@ -56,6 +57,13 @@ int smel_abi_version(void);
  * q [rows][K/2], scale/zero [rows][K/group] -> out [rows][K]: w = RNE(q*s + z) (fp32 math). out_f32 = 1 writes fp32. */
 int smel_dequant_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, void* out, int64_t rows,
                       int64_t K, int64_t group, int32_t out_f32, hipStream_t stream);
+
+/* Derived operand layout of an int4 bank (no counterpart in the reference: the reference's scale/zero tensors stay
+ * the source of truth and are not modified). For rows r < rows and k-steps ks < ceil(K/64):
+ *   sz[(r*2 + h)*ceil(K/64) + ks] = scale | zero << 16   of the group holding column 64*ks + 32*h.
+ * One 16-byte load then gives a forward-GEMM lane its scales and zeros for 4 k-steps. */
+int smel_int4_pack_sz(const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K, int64_t group,
+                      uint32_t* sz, hipStream_t stream);
 
 /* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
  * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the

@@ -53,7 +53,41 @@ __global__ __launch_bounds__(256) void dequant_bytes(const uint8_t* __restrict__
   }
 }
 
+// sz[(r*2 + h)*nks + ks] = scale | zero << 16 of the group holding column 64*ks + 32*h.
+__global__ __launch_bounds__(256) void pack_sz(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
+                                               int64_t rows, int64_t K, int64_t group, int64_t nks,
+                                               uint32_t* __restrict__ out) {
+  const int64_t G = K / group;
+  const int64_t n = rows * 2 * nks;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t ks = i % nks;
+    const int64_t h = (i / nks) & 1;
+    const int64_t r = i / (2 * nks);
+    const int64_t k = 64 * ks + 32 * h;
+    uint32_t v = 0;
+    if (k < K) {
+      const int64_t gi = r * G + k / group;
+      v = (uint32_t)s[gi] | ((uint32_t)z[gi] << 16);
+    }
+    out[i] = v;
+  }
+}
+
 }  // namespace
+
+extern "C" int smel_int4_pack_sz(const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K, int64_t group,
+                                 uint32_t* sz, hipStream_t stream) {
+  SMEL_REQUIRE(rows >= 0 && K > 0 && group > 0 && K % group == 0 && group % 32 == 0, SMEL_EUNSUPPORTED,
+               "int4_pack_sz: K=%lld, group=%lld (group must be a multiple of 32 dividing K)", (long long)K,
+               (long long)group);
+  if (rows == 0) return 0;
+  SMEL_REQUIRE(scale && zero && sz, SMEL_EINVAL, "int4_pack_sz: null pointer");
+  const int64_t nks = (K + 63) / 64;
+  const int64_t n = rows * 2 * nks;
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 256 * 64);
+  pack_sz<<<blocks, 256, 0, stream>>>(scale, zero, rows, K, group, nks, sz);
+  return smel::launch_status();
+}
 
 extern "C" int smel_dequant_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, void* out,
                                  int64_t rows, int64_t K, int64_t group, int32_t out_f32, hipStream_t stream) {

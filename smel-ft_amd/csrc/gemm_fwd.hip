@@ -45,7 +45,7 @@ struct BRegs;
 template <>
 struct BRegs<true> {
   u32x4_t q[2];
-  uint32_t s[2], z[2];
+  u32x4_t sz[2];   // packed (scale, zero) of 4 consecutive k-steps (the 4-aligned run holding this step)
 };
 template <>
 struct BRegs<false> {
@@ -74,33 +74,39 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     n1 = c0 + 32 + r32;
   }
   // ---- buffer resources: the weight matrix of this group, the A matrix
-  rsrc_t rw, rs, rz;
+  rsrc_t rw, rsz;
   uint32_t wo0, wo1, so0 = 0, so1 = 0;
-  const int G = Q4 ? ws.C / ws.group : 0;
+  const int nks = (ws.C + 63) / 64;   // k-steps of one weight row (packed scale/zero entries per lane half)
   if constexpr (Q4) {
     const int64_t mat = (int64_t)idx * ws.R;
     rw = make_rsrc(ws.q4 + mat * (ws.C / 2), (uint64_t)ws.R * (ws.C / 2));
-    rs = make_rsrc(ws.s4 + mat * G, (uint64_t)ws.R * G * 2);
-    rz = make_rsrc(ws.z4 + mat * G, (uint64_t)ws.R * G * 2);
+    rsz = make_rsrc(ws.sz4 + mat * 2 * nks, (uint64_t)ws.R * 2 * nks * 4);
     wo0 = fv0 ? (uint32_t)n0 * (ws.C / 2) : OOB;
     wo1 = fv1 ? (uint32_t)n1 * (ws.C / 2) : OOB;
-    so0 = fv0 ? (uint32_t)n0 * G * 2 : OOB;
-    so1 = fv1 ? (uint32_t)n1 * G * 2 : OOB;
+    so0 = fv0 ? (uint32_t)(n0 * 2 + hi) * nks * 4 : OOB;
+    so1 = fv1 ? (uint32_t)(n1 * 2 + hi) * nks * 4 : OOB;
   } else {
     const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
     const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
     rw = make_rsrc(base + mi * ws.R * ws.C, (uint64_t)ws.R * ws.C * 2);
-    rs = rz = rw;
+    rsz = rw;
     wo0 = fv0 ? (uint32_t)n0 * ws.C * 2 : OOB;
     wo1 = fv1 ? (uint32_t)n1 * ws.C * 2 : OOB;
   }
   const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
-  const int ar = tid >> 1, ap = tid & 1;   // A staging: tile row, 32-wide half of the k-step
-  uint32_t aoff = OOB;
-  if (ar < nrows) {
-    const int grow = row0 + ar;
-    const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
-    aoff = (uint32_t)src * (uint32_t)a.lda * 2 + 64 * ap;
+  // A staging: 8 consecutive lanes read one row's 128 contiguous bytes of the k-step (16 B each), so a 16-lane
+  // quarter-wave touches 2 rows; thread t covers rows t/8 + 32 i, i = 0..3, at 16-byte chunk t%8.
+  const int ach = tid & 7, arow0 = tid >> 3;
+  uint32_t aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ar = arow0 + 32 * i;
+    aoff[i] = OOB;
+    if (ar < nrows) {
+      const int grow = row0 + ar;
+      const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
+      aoff[i] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * ach;
+    }
   }
 
   f32x16_t acc[NS][2];
@@ -110,14 +116,14 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   u32x4_t areg[4];
   BRegs<Q4> bc, bn;
   auto load_a = [&](int k0) {
-    const uint32_t o = (k0 + 32 * ap + 32 <= K) ? aoff + k0 * 2 : OOB;
+    const bool ok = k0 + 8 * ach + 8 <= K;   // K % 32 == 0: a 16-B chunk is all in or all out
 #pragma unroll
-    for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, o + 16 * i);
+    for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, ok ? aoff[i] + k0 * 2 : OOB);
   };
   auto store_a = [&](int buf) {
-    uint16_t* dst = As + buf * (MT * AS) + ar * AS + 32 * ap;
+    uint16_t* dst = As + buf * (MT * AS) + arow0 * AS + 8 * ach;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(dst + 8 * i) = areg[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(dst + 32 * i * AS) = areg[i];
   };
   auto load_b = [&](int k0, BRegs<Q4>& b) {
     const int kk = k0 + 32 * hi;
@@ -125,11 +131,11 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     if constexpr (Q4) {
       b.q[0] = ld16(rw, ok ? wo0 + kk / 2 : OOB);
       b.q[1] = ld16(rw, ok ? wo1 + kk / 2 : OOB);
-      const uint32_t g2 = (kk / ws.group) * 2;
-      b.s[0] = ld2(rs, ok ? so0 + g2 : OOB);
-      b.z[0] = ld2(rz, ok ? so0 + g2 : OOB);
-      b.s[1] = ld2(rs, ok ? so1 + g2 : OOB);
-      b.z[1] = ld2(rz, ok ? so1 + g2 : OOB);
+      const int ks = k0 / KT;
+      if ((ks & 3) == 0) {   // a new run of 4 k-steps: one 16-B load of packed (scale, zero) per fragment
+        b.sz[0] = ld16(rsz, so0 + ks * 4);
+        b.sz[1] = ld16(rsz, so1 + ks * 4);
+      }
     } else {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -138,10 +144,11 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     }
   };
-  auto frag = [&](const BRegs<Q4>& b, int f, int s) -> u32x4_t {
+  auto frag = [&](const BRegs<Q4>& b, int f, int s, int j) -> u32x4_t {
     if constexpr (Q4) {
+      const uint32_t p = j == 0 ? b.sz[f][0] : j == 1 ? b.sz[f][1] : j == 2 ? b.sz[f][2] : b.sz[f][3];
       uint32_t o[4];
-      dq8(b.q[f][s], bf2f(b.s[f]), bf2f(b.z[f]), o);   // OOB rows load q = s = z = 0 -> exact zeros
+      dq8(b.q[f][s], bf_lo(p), bf_hi(p), o);   // OOB rows load q = s = z = 0 -> exact zeros
       return u32x4_t{o[0], o[1], o[2], o[3]};
     } else {
       return b.v[f][s];
@@ -149,34 +156,111 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   };
 
   const int nk = (K + KT - 1) / KT;
-  load_a(0);
-  load_b(0, bc);
-  store_a(0);
-  __syncthreads();
-  for (int i = 0; i < nk; ++i) {
-    const int buf = i & 1;
-    const bool more = i + 1 < nk;
-    if (more) {
-      load_a((i + 1) * KT);
-      load_b((i + 1) * KT, bn);
-    }
-    const uint16_t* Ab = As + buf * (MT * AS) + r32 * AS + 32 * hi;
+  if constexpr (Q4 && EPI == 1) {
+    // int4 weights: a 4-deep ring of register sets (the loads of step i+4 are issued at step i, so an HBM fetch has
+    // about four steps to land); the loop is unrolled by 4 so each set keeps one role. Packed (scale, zero) runs of
+    // 4 steps are double-buffered (szc for the current run, szn loaded one run ahead). A: one step ahead via LDS.
+    u32x4_t q0[2], q1[2], q2[2], q3[2], szc[2], szn[2];
+    auto load_q = [&](int k0, u32x4_t* q) {
+      const int kk = k0 + 32 * hi;
+      const bool ok = k0 < K && kk + 32 <= K;
+      q[0] = ld16(rw, ok ? wo0 + kk / 2 : OOB);
+      q[1] = ld16(rw, ok ? wo1 + kk / 2 : OOB);
+    };
+    auto load_sz = [&](int ks, u32x4_t* z) {
+      const bool ok = ks < nks;
+      z[0] = ld16(rsz, ok ? so0 + ks * 4 : OOB);
+      z[1] = ld16(rsz, ok ? so1 + ks * 4 : OOB);
+    };
+    auto step = [&](int i, const u32x4_t* q, int j) {
+      const int buf = i & 1;
+      const bool more = i + 1 < nk;
+      if (more) load_a((i + 1) * KT);
+      const uint16_t* Ab = As + buf * (MT * AS) + r32 * AS + 32 * hi;
+      const uint32_t p0 = szc[0][j], p1 = szc[1][j];
+      const float s0 = bf_lo(p0), z0 = bf_hi(p0), s1 = bf_lo(p1), z1 = bf_hi(p1);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4_t b0 = frag(bc, 0, s);
-      const u32x4_t b1 = frag(bc, 1, s);
+      for (int s = 0; s < 4; ++s) {
+        uint32_t o0[4], o1[4];
+        dq8(q[0][s], s0, z0, o0);   // OOB rows load q = s = z = 0 -> exact zeros
+        dq8(q[1][s], s1, z1, o1);
+        const u32x4_t b0 = u32x4_t{o0[0], o0[1], o0[2], o0[3]};
+        const u32x4_t b1 = u32x4_t{o1[0], o1[1], o1[2], o1[3]};
 #pragma unroll
-      for (int m = 0; m < NS; ++m) {
-        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
-        acc[m][0] = mfma32(af, b0, acc[m][0]);
-        acc[m][1] = mfma32(af, b1, acc[m][1]);
+        for (int m = 0; m < NS; ++m) {
+          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
+          acc[m][0] = mfma32(af, b0, acc[m][0]);
+          acc[m][1] = mfma32(af, b1, acc[m][1]);
+        }
       }
-    }
-    if (more) {
-      store_a(buf ^ 1);
-      bc = bn;
-    }
+      if (more) store_a(buf ^ 1);
+      __syncthreads();
+    };
+    load_a(0);
+    load_q(0, q0);
+    load_q(KT, q1);
+    load_q(2 * KT, q2);
+    load_q(3 * KT, q3);
+    load_sz(0, szc);
+    load_sz(4, szn);
+    store_a(0);
     __syncthreads();
+    for (int i = 0; i < nk; i += 4) {
+      step(i, q0, 0);
+      load_q((i + 4) * KT, q0);
+      if (i + 1 >= nk) break;
+      step(i + 1, q1, 1);
+      load_q((i + 5) * KT, q1);
+      if (i + 2 >= nk) break;
+      step(i + 2, q2, 2);
+      load_q((i + 6) * KT, q2);
+      if (i + 3 >= nk) break;
+      step(i + 3, q3, 3);
+      load_q((i + 7) * KT, q3);
+      szc[0] = szn[0];
+      szc[1] = szn[1];
+      load_sz(i + 8, szn);
+    }
+  } else {
+    load_a(0);
+    load_b(0, bc);
+    store_a(0);
+    __syncthreads();
+    int buf = 0;
+    for (int i = 0; i < nk; ++i) {
+      const bool more = i + 1 < nk;
+      if (more) {
+        load_a((i + 1) * KT);
+        load_b((i + 1) * KT, bn);
+      }
+      const uint16_t* Ab = As + buf * (MT * AS) + r32 * AS + 32 * hi;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4_t b0 = frag(bc, 0, s, i & 3);
+        const u32x4_t b1 = frag(bc, 1, s, i & 3);
+#pragma unroll
+        for (int m = 0; m < NS; ++m) {
+          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
+          acc[m][0] = mfma32(af, b0, acc[m][0]);
+          acc[m][1] = mfma32(af, b1, acc[m][1]);
+        }
+      }
+      if (more) {
+        store_a(buf ^ 1);
+        if constexpr (Q4) {
+          bc.q[0] = bn.q[0];
+          bc.q[1] = bn.q[1];
+          if (((i + 1) & 3) == 0) {
+            bc.sz[0] = bn.sz[0];
+            bc.sz[1] = bn.sz[1];
+          }
+        } else {
+          bc = bn;
+        }
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
   }
   // ---- LoRA K-extension: ext[row][0:32] . Bext[n][0:32]
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
@@ -268,6 +352,7 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
                "gmm_fwd: N=%lld must be a multiple of 32 (64 for gate_up)", (long long)w->R);
   SMEL_REQUIRE(!w->q4 || (w->group % 32 == 0 && w->C % w->group == 0), SMEL_EUNSUPPORTED,
                "gmm_fwd: int4 group %d must be a multiple of 32 dividing K", w->group);
+  SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_fwd: an int4 bank needs its packed scale/zero (smel_int4_pack_sz)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_fwd: A rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");

@@ -20,8 +20,8 @@ vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_fl
 
 class WSet(ctypes.Structure):
     """smel_wset of include/smel_moe.h."""
-    _fields_ = [("q4", vp), ("s4", vp), ("z4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp), ("ext_sel", vp),
-                ("ext_sh", vp), ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
+    _fields_ = [("q4", vp), ("s4", vp), ("z4", vp), ("sz4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp),
+                ("ext_sel", vp), ("ext_sh", vp), ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
 
 
 # name -> (restype, argtypes)
@@ -29,6 +29,7 @@ SIGNATURES = {
     "smel_last_error": (ctypes.c_char_p, []),
     "smel_abi_version": (i32, []),
     "smel_dequant_int4": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
+    "smel_int4_pack_sz": (i32, [vp, vp, i64, i64, i64, vp, vp]),
     "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
     "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp]),

@@ -68,6 +68,21 @@ class Int4Experts:
     def group_of(d: dict) -> int:
         return d["q"].shape[-1] * 2 // d["scale"].shape[-1]
 
+    def packed_sz(self, which: str) -> torch.Tensor:
+        """Interleaved (scale, zero) operand of the forward GEMM for 'gu' or 'dn', built once per bank by
+        smel_int4_pack_sz (the bank is frozen; rebuild by deleting ``_sz`` after changing its tensors)."""
+        cache = self.__dict__.setdefault("_sz", {})
+        if which not in cache:
+            d = self.gu if which == "gu" else self.dn
+            E, R, half = d["q"].shape
+            K = half * 2
+            nks = (K + 63) // 64
+            sz = torch.empty(E, R, 2, nks, dtype=torch.int32, device=d["q"].device)
+            L.call("smel_int4_pack_sz", L.ptr(d["scale"]), L.ptr(d["zero"]), E * R, K, Int4Experts.group_of(d),
+                   L.ptr(sz), L.stream())
+            cache[which] = sz
+        return cache[which]
+
     def weights(self, e0: int, e1: int):
         gu = dequant_int4(self.gu["q"][e0:e1], self.gu["scale"][e0:e1], self.gu["zero"][e0:e1], self.dtype)
         dn = dequant_int4(self.dn["q"][e0:e1], self.dn["scale"][e0:e1], self.dn["zero"][e0:e1], self.dtype)
@@ -196,6 +211,7 @@ def _wset(ex: LayerExperts, which: str, sel_w, sh_w, ext_sel, ext_sh) -> L.WSet:
     if isinstance(fz, Int4Experts):
         d = fz.gu if which == "gu" else fz.dn
         w.q4, w.s4, w.z4 = L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"])
+        w.sz4 = L.ptr(fz.packed_sz(which))
         w.group = Int4Experts.group_of(d)
         R = d["q"].shape[1]
         C = d["q"].shape[2] * 2

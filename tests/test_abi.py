@@ -32,8 +32,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_wset_layout_matches_header():
     from smel import _lib
-    # 8 pointers, two int64, two int32
-    assert ctypes.sizeof(_lib.WSet) == 8 * 8 + 2 * 8 + 2 * 4
+    # 9 pointers, two int64, two int32
+    assert ctypes.sizeof(_lib.WSet) == 9 * 8 + 2 * 8 + 2 * 4
 
 
 def test_host_side_rejections():
