@@ -29,17 +29,16 @@ extern "C" {
 #define SMEL_KIND_SEL 2    /* selected expert (bf16 copy + LoRA), index = slot j in sel_ids        */
 #define SMEL_KIND_SHARED 3 /* shared expert (bf16 + LoRA), index 0                                 */
 
-/* Weights of one projection (gate_up or down) for every group kind. Storage of one matrix is [R][C], C contiguous
- * (gate_up: R = 2I, C = H; down: R = H, C = I), exactly the reference tensors. The forward GEMM contracts over C
- * (out = x W^T), the backward GEMM over R (dx = dy W). */
+/* Weights of one projection (gate_up or down) for every group kind. A matrix is [R][C] in the reference
+ * (gate_up: R = 2I, C = H; down: R = H, C = I; R a multiple of 32); the GEMMs read it in the fragment layout written
+ * by smel_pack_int4 / smel_pack_bf16 (below), one matrix after the other for a stacked bank. The forward GEMM
+ * contracts over C (out = x W^T), the backward GEMM over R (dx = dy W). */
 typedef struct smel_wset {
-  const uint8_t* q4;   /* int4 bank q  [E][R][C/2], low nibble = even column (smel/quant.py:42)     */
-  const uint16_t* s4;  /* int4 bank scale [E][R][C/group] bf16                                      */
-  const uint16_t* z4;  /* int4 bank zero  [E][R][C/group] bf16                                      */
-  const uint32_t* sz4; /* the same scale/zero packed by smel_int4_pack_sz (forward GEMM operand)    */
-  const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down)                         */
-  const uint16_t* wsel;/* selected experts [n_sel][R][C] (LayerExperts.sel_gate_up / sel_down)      */
-  const uint16_t* wsh; /* shared expert [R][C]                                                      */
+  const uint8_t* q4;   /* int4 bank [E][R][C] packed by smel_pack_int4 (q operand)                     */
+  const uint32_t* sz4; /* its scale/zero, packed by the same call                                      */
+  const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down), smel_pack_bf16            */
+  const uint16_t* wsel;/* selected experts [n_sel][R][C] (LayerExperts.sel_gate_up / sel_down), packed  */
+  const uint16_t* wsh; /* shared expert [R][C], packed                                                 */
   /* LoRA as a 32-wide K-extension of the GEMM (0-padded rank <= 16, built by smel_lora_prep):
    *   forward  ext_*: [n][R][32]  (B factor per output row; gate_up: B_gate in cols 0..15, B_up in 16..31)
    *   backward ext_*: [n][32][C]  (A factor rows; gate_up: A_gate rows 0..15, A_up rows 16..31) */
@@ -58,12 +57,25 @@ int smel_abi_version(void);
 int smel_dequant_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, void* out, int64_t rows,
                       int64_t K, int64_t group, int32_t out_f32, hipStream_t stream);
 
-/* Derived operand layout of an int4 bank (no counterpart in the reference: the reference's scale/zero tensors stay
- * the source of truth and are not modified). For rows r < rows and k-steps ks < ceil(K/64):
- *   sz[(r*2 + h)*ceil(K/64) + ks] = scale | zero << 16   of the group holding column 64*ks + 32*h.
- * One 16-byte load then gives a forward-GEMM lane its scales and zeros for 4 k-steps. */
-int smel_int4_pack_sz(const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K, int64_t group,
-                      uint32_t* sz, hipStream_t stream);
+/* ---- Weight layouts of the grouped GEMMs (no counterpart in the reference, whose q/scale/zero and bf16 tensors
+ * stay the source of truth and are not modified; a frozen bank is packed once when it is built).
+ * A matrix of `rows` rows (a stacked bank: E*R rows) and K columns is cut into fragments of 32 rows and k-steps of
+ * 64 columns; each (fragment f, k-step ks) is one 1-KB block per 64 lanes, lane 32*h + i holding row 32*f + i:
+ *   SMEL_PACK_Q4   block (f, ks):        16 B = the 32 nibbles of k in [64 ks + 32 h, +32)
+ *   SMEL_PACK_SZ   block (f, ks/4):      16 B = 4 words (ks%4 = 0..3), scale | zero << 16 of the group of 64 ks+32 h
+ *   SMEL_PACK_BF16 block (f, ks, s<4):   16 B = the 8 bf16 of k in [64 ks + 32 h + 8 s, +8)
+ * so a GEMM wave reads each block with one contiguous 1-KB load. Rows >= rows and columns >= K are zero.
+ * smel_packed_bytes gives the size of each (or -1 for a bad argument). */
+#define SMEL_PACK_Q4 0
+#define SMEL_PACK_SZ 1
+#define SMEL_PACK_BF16 2
+int64_t smel_packed_bytes(int32_t what, int64_t rows, int64_t K);
+/* q [rows][K/2], scale/zero [rows][K/group] bf16 (the Int4Experts dict of smel/moe.py:35-55, smel/quant.py:24-44)
+ * -> qf (SMEL_PACK_Q4), szf (SMEL_PACK_SZ). K a multiple of 32, group a multiple of 32 dividing K. */
+int smel_pack_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K,
+                   int64_t group, uint8_t* qf, uint32_t* szf, hipStream_t stream);
+/* w [rows][ld] bf16 (first K columns used) -> wf (SMEL_PACK_BF16). K and ld multiples of 8. */
+int smel_pack_bf16(const uint16_t* w, int64_t rows, int64_t K, int64_t ld, uint16_t* wf, hipStream_t stream);
 
 /* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
  * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the

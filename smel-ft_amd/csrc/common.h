@@ -106,6 +106,18 @@ SMEL_DEV rsrc_t make_rsrc(const void* base, uint64_t bytes) {
 }
 SMEL_DEV u32x4_t ld16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 SMEL_DEV uint32_t ld2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+SMEL_DEV uint32_t ld4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+
+// Loads straight into LDS (gfx950: 16 B per lane): lane i of the wave writes bytes [16 i, 16 i + 16) after the
+// wave-uniform LDS address `lds`; an out-of-range offset writes zeros. Completion is counted by vmcnt.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+SMEL_DEV void ld16_lds(rsrc_t r, const void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(lds), 16, off, 0, 0, 0);
+}
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
+#define SMEL_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+// ... and on LDS as well (lgkmcnt = 0): this wave's own LDS reads are done.
+#define SMEL_WAIT_VM_LDS(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
 
 // ------------------------------------------------------------------------------------------------ XCD-aware tiles
 // MI355X has 8 XCDs, each with its own L2; consecutive workgroup ids go to consecutive XCDs. A 1-D grid of

@@ -53,39 +53,103 @@ __global__ __launch_bounds__(256) void dequant_bytes(const uint8_t* __restrict__
   }
 }
 
-// sz[(r*2 + h)*nks + ks] = scale | zero << 16 of the group holding column 64*ks + 32*h.
-__global__ __launch_bounds__(256) void pack_sz(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
-                                               int64_t rows, int64_t K, int64_t group, int64_t nks,
-                                               uint32_t* __restrict__ out) {
-  const int64_t G = K / group;
-  const int64_t n = rows * 2 * nks;
+// ---- fragment layouts of the GEMM weight operands (one 1-KB block = what one wave loads with one 16-B load per
+// lane; lane l = 32 h + i holds row 32 f + i of fragment f, k-half h of a 64-wide k-step):
+//   int4 q : block (f, ks)       lane chunk = 32 nibbles, k = 64 ks + 32 h + [0, 32)
+//   sz     : block (f, ks / 4)   lane chunk = 4 words (ks % 4 = 0..3): scale | zero << 16 of the group of 64 ks + 32 h
+//   bf16   : block (f, ks, s)    lane chunk = 8 bf16, k = 64 ks + 32 h + 8 s + [0, 8)
+// Rows >= rows and k >= K are zero.
+
+__global__ __launch_bounds__(256) void pack_q4(const uint8_t* __restrict__ q, int64_t rows, int64_t K, int64_t nks,
+                                               u32x4_t* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t ks = i % nks;
-    const int64_t h = (i / nks) & 1;
-    const int64_t r = i / (2 * nks);
-    const int64_t k = 64 * ks + 32 * h;
-    uint32_t v = 0;
-    if (k < K) {
-      const int64_t gi = r * G + k / group;
-      v = (uint32_t)s[gi] | ((uint32_t)z[gi] << 16);
-    }
+    const int64_t lane = i & 63, blk = i >> 6;
+    const int64_t f = blk / nks, ks = blk - f * nks;
+    const int64_t r = 32 * f + (lane & 31), k = 64 * ks + 32 * (lane >> 5);
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (r < rows && k < K) v = *reinterpret_cast<const u32x4_t*>(q + r * (K / 2) + k / 2);
     out[i] = v;
   }
 }
 
+__global__ __launch_bounds__(256) void pack_sz(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
+                                               int64_t rows, int64_t K, int64_t group, int64_t nks4,
+                                               u32x4_t* __restrict__ out, int64_t n) {
+  const int64_t G = K / group;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t lane = i & 63, blk = i >> 6;
+    const int64_t f = blk / nks4, run = blk - f * nks4;
+    const int64_t r = 32 * f + (lane & 31);
+    uint32_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t k = 64 * (4 * run + j) + 32 * (lane >> 5);
+      v[j] = 0;
+      if (r < rows && k < K) {
+        const int64_t gi = r * G + k / group;
+        v[j] = (uint32_t)s[gi] | ((uint32_t)z[gi] << 16);
+      }
+    }
+    out[i] = u32x4_t{v[0], v[1], v[2], v[3]};
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_bf16(const uint16_t* __restrict__ w, int64_t rows, int64_t K, int64_t ld,
+                                                 int64_t nks, u32x4_t* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t lane = i & 63, blk = i >> 6;
+    const int64_t sub = blk & 3, fk = blk >> 2;
+    const int64_t f = fk / nks, ks = fk - f * nks;
+    const int64_t r = 32 * f + (lane & 31), k = 64 * ks + 32 * (lane >> 5) + 8 * sub;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (r < rows && k < K) v = *reinterpret_cast<const u32x4_t*>(w + r * ld + k);
+    out[i] = v;
+  }
+}
+
+inline int pack_blocks(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 256 * 64); }
+
 }  // namespace
 
-extern "C" int smel_int4_pack_sz(const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K, int64_t group,
-                                 uint32_t* sz, hipStream_t stream) {
-  SMEL_REQUIRE(rows >= 0 && K > 0 && group > 0 && K % group == 0 && group % 32 == 0, SMEL_EUNSUPPORTED,
-               "int4_pack_sz: K=%lld, group=%lld (group must be a multiple of 32 dividing K)", (long long)K,
-               (long long)group);
+extern "C" int64_t smel_packed_bytes(int32_t what, int64_t rows, int64_t K) {
+  if (rows < 0 || K <= 0) return -1;
+  const int64_t nf = (rows + 31) / 32, nks = (K + 63) / 64;
+  switch (what) {
+    case SMEL_PACK_Q4: return nf * nks * 1024;
+    case SMEL_PACK_SZ: return nf * ((nks + 3) / 4) * 1024;
+    case SMEL_PACK_BF16: return nf * nks * 4096;
+    default: return -1;
+  }
+}
+
+extern "C" int smel_pack_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K,
+                              int64_t group, uint8_t* qf, uint32_t* szf, hipStream_t stream) {
+  SMEL_REQUIRE(rows >= 0 && K > 0 && group > 0 && K % 32 == 0 && K % group == 0 && group % 32 == 0,
+               SMEL_EUNSUPPORTED, "pack_int4: K=%lld, group=%lld (K a multiple of 32, group a multiple of 32 dividing K)",
+               (long long)K, (long long)group);
   if (rows == 0) return 0;
-  SMEL_REQUIRE(scale && zero && sz, SMEL_EINVAL, "int4_pack_sz: null pointer");
-  const int64_t nks = (K + 63) / 64;
-  const int64_t n = rows * 2 * nks;
-  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 256 * 64);
-  pack_sz<<<blocks, 256, 0, stream>>>(scale, zero, rows, K, group, nks, sz);
+  SMEL_REQUIRE(q && scale && zero && qf && szf, SMEL_EINVAL, "pack_int4: null pointer");
+  SMEL_REQUIRE((uintptr_t)q % 16 == 0 && (uintptr_t)qf % 16 == 0 && (uintptr_t)szf % 16 == 0, SMEL_EUNSUPPORTED,
+               "pack_int4: q, qf and szf must be 16-byte aligned");
+  const int64_t nf = (rows + 31) / 32, nks = (K + 63) / 64, nks4 = (nks + 3) / 4;
+  const int64_t nq = nf * nks * 64, nsz = nf * nks4 * 64;
+  pack_q4<<<pack_blocks(nq), 256, 0, stream>>>(q, rows, K, nks, reinterpret_cast<u32x4_t*>(qf), nq);
+  pack_sz<<<pack_blocks(nsz), 256, 0, stream>>>(scale, zero, rows, K, group, nks4, reinterpret_cast<u32x4_t*>(szf),
+                                                nsz);
+  return smel::launch_status();
+}
+
+extern "C" int smel_pack_bf16(const uint16_t* w, int64_t rows, int64_t K, int64_t ld, uint16_t* wf,
+                              hipStream_t stream) {
+  SMEL_REQUIRE(rows >= 0 && K > 0 && K % 8 == 0 && ld >= K && ld % 8 == 0, SMEL_EUNSUPPORTED,
+               "pack_bf16: K=%lld, ld=%lld (K and ld multiples of 8, ld >= K)", (long long)K, (long long)ld);
+  if (rows == 0) return 0;
+  SMEL_REQUIRE(w && wf, SMEL_EINVAL, "pack_bf16: null pointer");
+  SMEL_REQUIRE((uintptr_t)w % 16 == 0 && (uintptr_t)wf % 16 == 0, SMEL_EUNSUPPORTED,
+               "pack_bf16: w and wf must be 16-byte aligned");
+  const int64_t nf = (rows + 31) / 32, nks = (K + 63) / 64;
+  const int64_t n = nf * nks * 4 * 64;
+  pack_bf16<<<pack_blocks(n), 256, 0, stream>>>(w, rows, K, ld, nks, reinterpret_cast<u32x4_t*>(wf), n);
   return smel::launch_status();
 }
 

@@ -74,22 +74,24 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
     aoff = (uint32_t)src * (uint32_t)a.lda * 2 + 64 * ap;
   }
-  rsrc_t rw, rs, rz;
-  uint32_t wrow;   // byte offset of column nc inside a row of this group's matrix
-  const int G = Q4 ? ws.C / ws.group : 0;
+  // W rows (ka, ka+1) = lanes (i, i+1) of fragment ka / 32 in the packed layout; columns [nc, nc+32) = half h of
+  // k-step ks of that layout.
+  const int pk = (a.N + 63) / 64, pk4 = (pk + 3) / 4, nfr = Kd / 32;   // k-steps of the packed layout (along C)
+  const int cks = nc / 64, ch = (nc / 32) & 1;
   const bool cok = nc < a.N;
+  rsrc_t rw, rsz;
+  uint32_t wbase, sbase = 0;   // byte offset of this thread's first chunk at k0 = 0
   if constexpr (Q4) {
-    const int64_t mat = (int64_t)idx * ws.R;
-    rw = make_rsrc(ws.q4 + mat * (ws.C / 2), (uint64_t)ws.R * (ws.C / 2));
-    rs = make_rsrc(ws.s4 + mat * G, (uint64_t)ws.R * G * 2);
-    rz = make_rsrc(ws.z4 + mat * G, (uint64_t)ws.R * G * 2);
-    wrow = nc / 2;
+    rw = make_rsrc(ws.q4 + (int64_t)idx * nfr * pk * 1024, (uint64_t)nfr * pk * 1024);
+    rsz = make_rsrc(ws.sz4 + (int64_t)idx * nfr * pk4 * 256, (uint64_t)nfr * pk4 * 1024);
+    wbase = (uint32_t)((cks * 64 + 32 * ch + (2 * kp) % 32) * 16);
+    sbase = (uint32_t)(((cks >> 2) * 64 + 32 * ch + (2 * kp) % 32) * 16 + 4 * (cks & 3));
   } else {
     const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
     const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
-    rw = make_rsrc(base + mi * ws.R * ws.C, (uint64_t)ws.R * ws.C * 2);
-    rs = rz = rw;
-    wrow = nc * 2;
+    rw = make_rsrc(base + mi * nfr * pk * 2048, (uint64_t)nfr * pk * 4096);
+    rsz = rw;
+    wbase = (uint32_t)((cks * 4 * 64 + 32 * ch + (2 * kp) % 32) * 16);
   }
 
   f32x16_t acc[NS][2];
@@ -104,21 +106,23 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, ao + 16 * i);
     const int ka = k0 + 2 * kp;
     const bool ok = cok && ka + 1 < Kd;
+    const int fr = ka / 32;
     if constexpr (Q4) {
-      const uint32_t rb = (uint32_t)ka * (ws.C / 2) + wrow;
-      wr.q[0] = ld16(rw, ok ? rb : OOB);
-      wr.q[1] = ld16(rw, ok ? rb + ws.C / 2 : OOB);
-      const uint32_t g = ((uint32_t)ka * G + nc / ws.group) * 2;
-      wr.s[0] = ld2(rs, ok ? g : OOB);
-      wr.z[0] = ld2(rz, ok ? g : OOB);
-      wr.s[1] = ld2(rs, ok ? g + G * 2 : OOB);
-      wr.z[1] = ld2(rz, ok ? g + G * 2 : OOB);
+      const uint32_t o = (uint32_t)fr * pk * 1024 + wbase;
+      wr.q[0] = ld16(rw, ok ? o : OOB);
+      wr.q[1] = ld16(rw, ok ? o + 16 : OOB);
+      const uint32_t so = (uint32_t)fr * pk4 * 1024 + sbase;
+      const uint32_t p0 = ld4(rsz, ok ? so : OOB), p1 = ld4(rsz, ok ? so + 16 : OOB);
+      wr.s[0] = p0 & 0xffffu;
+      wr.z[0] = p0 >> 16;
+      wr.s[1] = p1 & 0xffffu;
+      wr.z[1] = p1 >> 16;
     } else {
-      const uint32_t rb = (uint32_t)ka * ws.C * 2 + wrow;
+      const uint32_t o = (uint32_t)fr * pk * 4096 + wbase;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        wr.v[0][i] = ld16(rw, ok ? rb + 16 * i : OOB);
-        wr.v[1][i] = ld16(rw, ok ? rb + ws.C * 2 + 16 * i : OOB);
+        wr.v[0][i] = ld16(rw, ok ? o + 1024 * i : OOB);
+        wr.v[1][i] = ld16(rw, ok ? o + 1024 * i + 16 : OOB);
       }
     }
   };
@@ -312,6 +316,7 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
                "gmm_bwd: weight dims %lldx%lld must be multiples of 32", (long long)w->R, (long long)w->C);
   SMEL_REQUIRE(!w->q4 || (w->group % 32 == 0 && w->C % w->group == 0), SMEL_EUNSUPPORTED,
                "gmm_bwd: int4 group %d must be a multiple of 32 dividing the columns", w->group);
+  SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_bwd: an int4 bank needs its packed scale/zero (smel_pack_int4)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_bwd: A rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
                "gmm_bwd: epilogue %d needs hsave, dwp and topv", epilogue);

@@ -6,11 +6,17 @@
 // smel/moe.py:58-72, 110-117, 204-211 and smel/lora.py:61-83.
 //
 // Block = 4 waves, tile = up to 128 rows of one group (4 slices of 32) x (gate_up: 32 gate + 32 up columns per wave;
-// down: 64 columns per wave). A (activation rows) is staged through LDS, double-buffered, and shared by the 4 waves;
-// every wave streams its own weight rows straight into registers (16 B of int4 = 32 k per lane per step) and
-// dequantizes them there, so each weight element of a tile is read and dequantized once. MFMA 32x32x16 bf16.
-// Lane k-mapping inside a 64-wide step: lane half h = lane/32 carries k = 32h + 8s + [0,8) in substep s, for A and
-// B alike (one 16-B read per lane per operand).
+// down: 64 columns per wave). MFMA 32x32x16 bf16. Per 64-wide k-step:
+//  * A (activation rows, gathered by token) goes global -> LDS directly (16-B LDS-DMA loads, 1 KB per wave-load, no
+//    registers), into a ring of 4 stages; each 128-B row's 16-B chunks are XOR-swizzled so the fragment reads are
+//    bank-conflict free. Every wave reads all rows of a stage.
+//  * every wave streams its own two 32-row weight fragments straight into registers from the fragment layout of
+//    smel_pack_int4 / smel_pack_bf16 (one contiguous 1-KB load per fragment and k-step) and dequantizes int4 there,
+//    so each weight element of a tile is read and dequantized once.
+//  * loads run 3 k-steps ahead (int4: a 4-deep register ring; bf16: 1 step ahead, as its fragments are 4x larger).
+//    vmcnt retires in issue order, so each step issues its weight loads before its A loads and waits, before one
+//    barrier, for exactly the loads of the step it is about to use.
+// Lane k-mapping inside a k-step: lane half h = lane/32 carries k = 32h + 8s + [0,8) in substep s, for A and B alike.
 #include "abi_util.h"
 #include "common.h"
 
@@ -18,7 +24,11 @@ namespace {
 
 constexpr int MT = 128;
 constexpr int KT = 64;
-constexpr int AS = KT + 8;   // LDS row stride in bf16 (144 B: an odd number of 16-B units)
+constexpr int A_STAGE = MT * KT;   // bf16 elements of one A stage: row r at r * KT, no padding
+
+// Physical 16-B chunk of logical chunk c in A row r is c ^ swz(r): 8 (or 16) lanes reading consecutive rows at one
+// logical chunk then touch distinct banks, with 32 or with 64 four-byte banks.
+SMEL_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 struct FwdArgs {
   smel_wset w;
@@ -38,27 +48,15 @@ struct FwdArgs {
   int nblk;   // column blocks per tile
 };
 
-// Weight rows of one wave for one k-step: int4 (16 B = 32 nibbles per lane and fragment, plus its group's scale and
-// zero) or bf16 (64 B per lane and fragment).
-template <bool Q4>
-struct BRegs;
-template <>
-struct BRegs<true> {
-  u32x4_t q[2];
-  u32x4_t sz[2];   // packed (scale, zero) of 4 consecutive k-steps (the 4-aligned run holding this step)
-};
-template <>
-struct BRegs<false> {
-  u32x4_t v[2][4];
-};
-
 template <int EPI, bool Q4, int NS>
-SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As) {
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
+SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
+                       uint16_t* S2, uint16_t* S3) {
+  const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = a.K;
   const smel_wset& ws = a.w;
-  // ---- this wave's two weight rows (per lane): gate/up pair for epilogue 1, two adjacent 32-column blocks else
-  int n0, n1;
+  // ---- this wave's two 32-row weight fragments: gate/up pair for epilogue 1, two adjacent fragments else
+  int n0, n1, fr0, fr1;
   bool fv0, fv1;
   if (EPI == 1) {
     const int I = a.N / 2;
@@ -66,202 +64,177 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     fv0 = fv1 = c0 < I;
     n0 = c0 + r32;
     n1 = I + c0 + r32;
+    fr0 = c0 / 32;
+    fr1 = (I + c0) / 32;
   } else {
     const int c0 = nb * 256 + w * 64;
     fv0 = c0 < a.N;
     fv1 = c0 + 32 < a.N;
     n0 = c0 + r32;
     n1 = c0 + 32 + r32;
+    fr0 = c0 / 32;
+    fr1 = c0 / 32 + 1;
   }
-  // ---- buffer resources: the weight matrix of this group, the A matrix
+  const int nk = (K + KT - 1) / KT, nk4 = (nk + 3) / 4;
+  const int nfr = a.N / 32;   // fragments of one matrix
   rsrc_t rw, rsz;
-  uint32_t wo0, wo1, so0 = 0, so1 = 0;
-  const int nks = (ws.C + 63) / 64;   // k-steps of one weight row (packed scale/zero entries per lane half)
+  uint32_t wo0, wo1, so0 = OOB, so1 = OOB;
   if constexpr (Q4) {
-    const int64_t mat = (int64_t)idx * ws.R;
-    rw = make_rsrc(ws.q4 + mat * (ws.C / 2), (uint64_t)ws.R * (ws.C / 2));
-    rsz = make_rsrc(ws.sz4 + mat * 2 * nks, (uint64_t)ws.R * 2 * nks * 4);
-    wo0 = fv0 ? (uint32_t)n0 * (ws.C / 2) : OOB;
-    wo1 = fv1 ? (uint32_t)n1 * (ws.C / 2) : OOB;
-    so0 = fv0 ? (uint32_t)(n0 * 2 + hi) * nks * 4 : OOB;
-    so1 = fv1 ? (uint32_t)(n1 * 2 + hi) * nks * 4 : OOB;
+    rw = make_rsrc(ws.q4 + (int64_t)idx * nfr * nk * 1024, (uint64_t)nfr * nk * 1024);
+    rsz = make_rsrc(ws.sz4 + (int64_t)idx * nfr * nk4 * 256, (uint64_t)nfr * nk4 * 1024);
+    wo0 = fv0 ? (uint32_t)(fr0 * nk * 1024 + l * 16) : OOB;
+    wo1 = fv1 ? (uint32_t)(fr1 * nk * 1024 + l * 16) : OOB;
+    so0 = fv0 ? (uint32_t)(fr0 * nk4 * 1024 + l * 16) : OOB;
+    so1 = fv1 ? (uint32_t)(fr1 * nk4 * 1024 + l * 16) : OOB;
   } else {
     const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
     const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
-    rw = make_rsrc(base + mi * ws.R * ws.C, (uint64_t)ws.R * ws.C * 2);
+    rw = make_rsrc(base + mi * nfr * nk * 2048, (uint64_t)nfr * nk * 4096);
     rsz = rw;
-    wo0 = fv0 ? (uint32_t)n0 * ws.C * 2 : OOB;
-    wo1 = fv1 ? (uint32_t)n1 * ws.C * 2 : OOB;
+    wo0 = fv0 ? (uint32_t)(fr0 * nk * 4096 + l * 16) : OOB;
+    wo1 = fv1 ? (uint32_t)(fr1 * nk * 4096 + l * 16) : OOB;
   }
+  // ---- A staging: wave-load ii of wave w fills rows 8 g .. 8 g + 7 (g = 4 w + ii) of a stage, 1 KB; lane i writes
+  // physical chunk i % 8 of row 8 g + i / 8, i.e. logical chunk c = (i % 8) ^ swz(row).
   const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
-  // A staging: 8 consecutive lanes read one row's 128 contiguous bytes of the k-step (16 B each), so a 16-lane
-  // quarter-wave touches 2 rows; thread t covers rows t/8 + 32 i, i = 0..3, at 16-byte chunk t%8.
-  const int ach = tid & 7, arow0 = tid >> 3;
+  const int li = tid & 63;
   uint32_t aoff[4];
+  int akc[4];   // first k of this lane's chunk
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ar = arow0 + 32 * i;
-    aoff[i] = OOB;
-    if (ar < nrows) {
-      const int grow = row0 + ar;
+  for (int ii = 0; ii < 4; ++ii) {
+    const int g = 4 * w + ii;
+    const int row = 8 * g + (li >> 3);
+    const int c = (li & 7) ^ swz(row);
+    akc[ii] = 8 * c;
+    aoff[ii] = OOB;
+    if (row < nrows) {
+      const int grow = row0 + row;
       const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
-      aoff[i] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * ach;
+      aoff[ii] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * c;
     }
   }
+  auto issue_a = [&](int j, uint16_t* S) {
+    const int k0 = j * KT;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii)
+      ld16_lds(ra, S + (4 * w + ii) * 512, (k0 + akc[ii] + 8 <= K) ? aoff[ii] + k0 * 2 : OOB);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // A fragment reads: lane (r32, h) of slice m, substep s reads logical chunk 4 h + s of row 32 m + r32
+  uint32_t ard[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) ard[s] = r32 * KT + 8 * ((4 * hi + s) ^ swz(r32));
 
   f32x16_t acc[NS][2];
 #pragma unroll
   for (int m = 0; m < NS; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
 
-  u32x4_t areg[4];
-  BRegs<Q4> bc, bn;
-  auto load_a = [&](int k0) {
-    const bool ok = k0 + 8 * ach + 8 <= K;   // K % 32 == 0: a 16-B chunk is all in or all out
+  auto mma = [&](const uint16_t* S, int s, const u32x4_t& b0, const u32x4_t& b1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, ok ? aoff[i] + k0 * 2 : OOB);
-  };
-  auto store_a = [&](int buf) {
-    uint16_t* dst = As + buf * (MT * AS) + arow0 * AS + 8 * ach;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(dst + 32 * i * AS) = areg[i];
-  };
-  auto load_b = [&](int k0, BRegs<Q4>& b) {
-    const int kk = k0 + 32 * hi;
-    const bool ok = kk + 32 <= K;
-    if constexpr (Q4) {
-      b.q[0] = ld16(rw, ok ? wo0 + kk / 2 : OOB);
-      b.q[1] = ld16(rw, ok ? wo1 + kk / 2 : OOB);
-      const int ks = k0 / KT;
-      if ((ks & 3) == 0) {   // a new run of 4 k-steps: one 16-B load of packed (scale, zero) per fragment
-        b.sz[0] = ld16(rsz, so0 + ks * 4);
-        b.sz[1] = ld16(rsz, so1 + ks * 4);
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        b.v[0][s] = ld16(rw, ok ? wo0 + kk * 2 + 16 * s : OOB);
-        b.v[1][s] = ld16(rw, ok ? wo1 + kk * 2 + 16 * s : OOB);
-      }
-    }
-  };
-  auto frag = [&](const BRegs<Q4>& b, int f, int s, int j) -> u32x4_t {
-    if constexpr (Q4) {
-      const uint32_t p = j == 0 ? b.sz[f][0] : j == 1 ? b.sz[f][1] : j == 2 ? b.sz[f][2] : b.sz[f][3];
-      uint32_t o[4];
-      dq8(b.q[f][s], bf_lo(p), bf_hi(p), o);   // OOB rows load q = s = z = 0 -> exact zeros
-      return u32x4_t{o[0], o[1], o[2], o[3]};
-    } else {
-      return b.v[f][s];
+    for (int m = 0; m < NS; ++m) {
+      const u32x4_t af = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 32 * KT);
+      acc[m][0] = mfma32(af, b0, acc[m][0]);
+      acc[m][1] = mfma32(af, b1, acc[m][1]);
     }
   };
 
-  const int nk = (K + KT - 1) / KT;
-  if constexpr (Q4 && EPI == 1) {
-    // int4 weights: a 4-deep ring of register sets (the loads of step i+4 are issued at step i, so an HBM fetch has
-    // about four steps to land); the loop is unrolled by 4 so each set keeps one role. Packed (scale, zero) runs of
-    // 4 steps are double-buffered (szc for the current run, szn loaded one run ahead). A: one step ahead via LDS.
+  if constexpr (Q4) {
+    // Group of loads for step j: q (2), then, when j % 4 == 0, the packed (scale, zero) run of steps j..j+3 (2),
+    // then A (4). Groups j+1, j+2 are in flight while step j computes; group j+3 is issued after its barrier.
     u32x4_t q0[2], q1[2], q2[2], q3[2], szc[2], szn[2];
-    auto load_q = [&](int k0, u32x4_t* q) {
-      const int kk = k0 + 32 * hi;
-      const bool ok = k0 < K && kk + 32 <= K;
-      q[0] = ld16(rw, ok ? wo0 + kk / 2 : OOB);
-      q[1] = ld16(rw, ok ? wo1 + kk / 2 : OOB);
+    auto issue = [&](int j, u32x4_t* q, u32x4_t* z, uint16_t* S) {
+      const bool in = j < nk;
+      q[0] = ld16(rw, in ? wo0 + j * 1024 : OOB);
+      q[1] = ld16(rw, in ? wo1 + j * 1024 : OOB);
+      if (z) {
+        const bool zin = (j >> 2) < nk4;
+        z[0] = ld16(rsz, zin ? so0 + (j >> 2) * 1024 : OOB);
+        z[1] = ld16(rsz, zin ? so1 + (j >> 2) * 1024 : OOB);
+      }
+      issue_a(j, S);   // sched barriers keep the group's loads in this order, ahead of the step's compute
     };
-    auto load_sz = [&](int ks, u32x4_t* z) {
-      const bool ok = ks < nks;
-      z[0] = ld16(rsz, ok ? so0 + ks * 4 : OOB);
-      z[1] = ld16(rsz, ok ? so1 + ks * 4 : OOB);
-    };
-    auto step = [&](int i, const u32x4_t* q, int j) {
-      const int buf = i & 1;
-      const bool more = i + 1 < nk;
-      if (more) load_a((i + 1) * KT);
-      const uint16_t* Ab = As + buf * (MT * AS) + r32 * AS + 32 * hi;
-      const uint32_t p0 = szc[0][j], p1 = szc[1][j];
+    auto compute = [&](const uint16_t* S, const u32x4_t* q, int p) {
+      const uint32_t p0 = p == 0 ? szc[0][0] : p == 1 ? szc[0][1] : p == 2 ? szc[0][2] : szc[0][3];
+      const uint32_t p1 = p == 0 ? szc[1][0] : p == 1 ? szc[1][1] : p == 2 ? szc[1][2] : szc[1][3];
       const float s0 = bf_lo(p0), z0 = bf_hi(p0), s1 = bf_lo(p1), z1 = bf_hi(p1);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         uint32_t o0[4], o1[4];
-        dq8(q[0][s], s0, z0, o0);   // OOB rows load q = s = z = 0 -> exact zeros
+        dq8(q[0][s], s0, z0, o0);   // rows / k outside the matrix hold q = s = z = 0 -> exact zeros
         dq8(q[1][s], s1, z1, o1);
-        const u32x4_t b0 = u32x4_t{o0[0], o0[1], o0[2], o0[3]};
-        const u32x4_t b1 = u32x4_t{o1[0], o1[1], o1[2], o1[3]};
-#pragma unroll
-        for (int m = 0; m < NS; ++m) {
-          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
-          acc[m][0] = mfma32(af, b0, acc[m][0]);
-          acc[m][1] = mfma32(af, b1, acc[m][1]);
-        }
+        mma(S, s, u32x4_t{o0[0], o0[1], o0[2], o0[3]}, u32x4_t{o1[0], o1[1], o1[2], o1[3]});
       }
-      if (more) store_a(buf ^ 1);
-      __syncthreads();
     };
-    load_a(0);
-    load_q(0, q0);
-    load_q(KT, q1);
-    load_q(2 * KT, q2);
-    load_q(3 * KT, q3);
-    load_sz(0, szc);
-    load_sz(4, szn);
-    store_a(0);
-    __syncthreads();
+    issue(0, q0, szc, S0);
+    issue(1, q1, nullptr, S1);
+    issue(2, q2, nullptr, S2);
+    // ceil(nk / 4) * 4 steps, branch-free: a step past K loads zeros and adds nothing
     for (int i = 0; i < nk; i += 4) {
-      step(i, q0, 0);
-      load_q((i + 4) * KT, q0);
-      if (i + 1 >= nk) break;
-      step(i + 1, q1, 1);
-      load_q((i + 5) * KT, q1);
-      if (i + 2 >= nk) break;
-      step(i + 2, q2, 2);
-      load_q((i + 6) * KT, q2);
-      if (i + 3 >= nk) break;
-      step(i + 3, q3, 3);
-      load_q((i + 7) * KT, q3);
+      SMEL_WAIT_VM_LDS(12);
+      __builtin_amdgcn_s_barrier();
+      issue(i + 3, q3, nullptr, S3);
+      compute(S0, q0, 0);
+      SMEL_WAIT_VM_LDS(12);
+      __builtin_amdgcn_s_barrier();
+      issue(i + 4, q0, szn, S0);
+      compute(S1, q1, 1);
+      SMEL_WAIT_VM_LDS(14);
+      __builtin_amdgcn_s_barrier();
+      issue(i + 5, q1, nullptr, S1);
+      compute(S2, q2, 2);
+      SMEL_WAIT_VM_LDS(14);
+      __builtin_amdgcn_s_barrier();
+      issue(i + 6, q2, nullptr, S2);
+      compute(S3, q3, 3);
       szc[0] = szn[0];
       szc[1] = szn[1];
-      load_sz(i + 8, szn);
     }
   } else {
-    load_a(0);
-    load_b(0, bc);
-    store_a(0);
-    __syncthreads();
-    int buf = 0;
-    for (int i = 0; i < nk; ++i) {
-      const bool more = i + 1 < nk;
-      if (more) {
-        load_a((i + 1) * KT);
-        load_b((i + 1) * KT, bn);
-      }
-      const uint16_t* Ab = As + buf * (MT * AS) + r32 * AS + 32 * hi;
+    // bf16 weights: 8 loads per fragment pair and step, one step ahead in two alternating register sets; A three
+    // steps ahead. Issue order B(j+1), A(j+3): before step j only A(j+2) may still be in flight.
+    u32x4_t bA[2][4], bB[2][4];
+    auto issue_b = [&](int j, u32x4_t (*b)[4]) {
+      const bool in = j < nk;
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u32x4_t b0 = frag(bc, 0, s, i & 3);
-        const u32x4_t b1 = frag(bc, 1, s, i & 3);
+        b[0][s] = ld16(rw, in ? wo0 + j * 4096 + s * 1024 : OOB);
+        b[1][s] = ld16(rw, in ? wo1 + j * 4096 + s * 1024 : OOB);
+      }
+    };
+    auto compute = [&](const uint16_t* S, u32x4_t (*b)[4]) {
 #pragma unroll
-        for (int m = 0; m < NS; ++m) {
-          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
-          acc[m][0] = mfma32(af, b0, acc[m][0]);
-          acc[m][1] = mfma32(af, b1, acc[m][1]);
-        }
-      }
-      if (more) {
-        store_a(buf ^ 1);
-        if constexpr (Q4) {
-          bc.q[0] = bn.q[0];
-          bc.q[1] = bn.q[1];
-          if (((i + 1) & 3) == 0) {
-            bc.sz[0] = bn.sz[0];
-            bc.sz[1] = bn.sz[1];
-          }
-        } else {
-          bc = bn;
-        }
-      }
-      __syncthreads();
-      buf ^= 1;
+      for (int s = 0; s < 4; ++s) mma(S, s, b[0][s], b[1][s]);
+    };
+    issue_a(0, S0);
+    issue_a(1, S1);
+    issue_b(0, bA);
+    issue_a(2, S2);
+    for (int i = 0; i < nk; i += 4) {
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 1, bB);
+      issue_a(i + 3, S3);
+      compute(S0, bA);
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 2, bA);
+      issue_a(i + 4, S0);
+      compute(S1, bB);
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 3, bB);
+      issue_a(i + 5, S1);
+      compute(S2, bA);
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 4, bA);
+      issue_a(i + 6, S2);
+      compute(S3, bB);
     }
   }
+  SMEL_WAIT_VM(0);   // the ring's trailing (out-of-range) loads
   // ---- LoRA K-extension: ext[row][0:32] . Bext[n][0:32]
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
@@ -313,18 +286,22 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 }
 
 template <int EPI, bool Q4>
-SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As) {
+SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0,
+                          uint16_t* S1, uint16_t* S2, uint16_t* S3) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, nb, As); break;
-    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, nb, As); break;
-    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, nb, As); break;
-    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, nb, As); break;
+    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
   }
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2 * MT * AS];
+  __shared__ __attribute__((aligned(1024))) uint16_t S0[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S1[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S2[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S3[A_STAGE];
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
@@ -333,9 +310,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4)
-    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, nb, As);
+    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
   else
-    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, nb, As);
+    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
 }
 
 }  // namespace
@@ -352,7 +329,7 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
                "gmm_fwd: N=%lld must be a multiple of 32 (64 for gate_up)", (long long)w->R);
   SMEL_REQUIRE(!w->q4 || (w->group % 32 == 0 && w->C % w->group == 0), SMEL_EUNSUPPORTED,
                "gmm_fwd: int4 group %d must be a multiple of 32 dividing K", w->group);
-  SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_fwd: an int4 bank needs its packed scale/zero (smel_int4_pack_sz)");
+  SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_fwd: an int4 bank needs its packed scale/zero (smel_pack_int4)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_fwd: A rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");

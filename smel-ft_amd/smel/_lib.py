@@ -14,14 +14,16 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsmel_moe.so")
 
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
+PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
+ABI_VERSION = 2
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
 
 class WSet(ctypes.Structure):
     """smel_wset of include/smel_moe.h."""
-    _fields_ = [("q4", vp), ("s4", vp), ("z4", vp), ("sz4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp),
-                ("ext_sel", vp), ("ext_sh", vp), ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
+    _fields_ = [("q4", vp), ("sz4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp), ("ext_sel", vp), ("ext_sh", vp),
+                ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
 
 
 # name -> (restype, argtypes)
@@ -29,7 +31,9 @@ SIGNATURES = {
     "smel_last_error": (ctypes.c_char_p, []),
     "smel_abi_version": (i32, []),
     "smel_dequant_int4": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
-    "smel_int4_pack_sz": (i32, [vp, vp, i64, i64, i64, vp, vp]),
+    "smel_packed_bytes": (i64, [i32, i64, i64]),
+    "smel_pack_int4": (i32, [vp, vp, vp, i64, i64, i64, vp, vp, vp]),
+    "smel_pack_bf16": (i32, [vp, i64, i64, i64, vp, vp]),
     "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
     "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
@@ -70,6 +74,9 @@ def load(path: str = LIB_PATH):
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
+    if L.smel_abi_version() != ABI_VERSION:
+        raise ImportError(f"{path} has ABI version {L.smel_abi_version()}, this binding expects {ABI_VERSION}: "
+                          f"rebuild the HIP extension")
     _lib = L
     return L
 

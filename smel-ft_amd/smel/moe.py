@@ -32,6 +32,41 @@ _ACT = {"silu": 0, "gelu_tanh": 1}
 _GELU_C = 0.7978845608028654
 
 
+# ------------------------------------------------------------------------------------------------ weight layouts
+
+
+class PackedW:
+    """One bf16 weight matrix [R, C] (or a stack of them, R rows each) in the GEMMs' fragment layout
+    (smel_pack_bf16): ``t`` holds the packed bytes, ``R``/``C`` the shape of one matrix."""
+
+    __slots__ = ("t", "R", "C")
+
+    def __init__(self, t: torch.Tensor, R: int, C: int):
+        self.t, self.R, self.C = t, R, C
+
+
+def pack_bf16(*mats: torch.Tensor) -> PackedW:
+    """Pack bf16 matrices [..., R_i, C] (same C) stacked along rows into one fragment-layout buffer; every part but
+    the last needs a multiple of 32 rows. One matrix of the result has the rows of the last dimension-2 extent, i.e.
+    a [E, R, C] bank packs as E matrices of R rows, and pack_bf16(gate, up) as one [2I, C] matrix."""
+    C = mats[0].shape[-1]
+    rows = [m.numel() // C for m in mats]
+    if any(r % 32 for r in rows[:-1]):
+        raise ValueError("pack_bf16: every part but the last needs a multiple of 32 rows")
+    lib = L.load()
+    total = sum(rows)
+    out = torch.empty(lib.smel_packed_bytes(L.PACK_BF16, total, C) // 2, dtype=torch.bfloat16,
+                      device=mats[0].device)
+    off = 0
+    for m, r in zip(mats, rows):
+        m = _bf16(m)
+        dst = out.data_ptr() + lib.smel_packed_bytes(L.PACK_BF16, off, C)
+        L.call("smel_pack_bf16", L.ptr(m), r, C, C, dst, L.stream())
+        off += r
+    R = total if len(mats) > 1 else mats[0].shape[-2]
+    return PackedW(out, R, C)
+
+
 # ------------------------------------------------------------------------------------------------ expert banks
 
 
@@ -44,6 +79,13 @@ class BF16Experts:
 
     def weights(self, e0: int, e1: int):
         return self.gate_up[e0:e1], self.down[e0:e1]
+
+    def packed(self, which: str) -> PackedW:
+        """gate_up ('gu') or down ('dn') in the GEMMs' fragment layout, built once (the bank is frozen)."""
+        cache = self.__dict__.setdefault("_packed", {})
+        if which not in cache:
+            cache[which] = pack_bf16(_bf16(self.gate_up if which == "gu" else self.down))
+        return cache[which]
 
     def tensors(self):
         return {"gate_up": self.gate_up, "down": self.down}
@@ -68,19 +110,21 @@ class Int4Experts:
     def group_of(d: dict) -> int:
         return d["q"].shape[-1] * 2 // d["scale"].shape[-1]
 
-    def packed_sz(self, which: str) -> torch.Tensor:
-        """Interleaved (scale, zero) operand of the forward GEMM for 'gu' or 'dn', built once per bank by
-        smel_int4_pack_sz (the bank is frozen; rebuild by deleting ``_sz`` after changing its tensors)."""
-        cache = self.__dict__.setdefault("_sz", {})
+    def packed(self, which: str):
+        """(q, scale/zero) of 'gu' or 'dn' in the GEMMs' fragment layout (smel_pack_int4), built once per bank: the
+        bank is frozen (rebuild by deleting ``_packed`` after changing its tensors)."""
+        cache = self.__dict__.setdefault("_packed", {})
         if which not in cache:
             d = self.gu if which == "gu" else self.dn
             E, R, half = d["q"].shape
             K = half * 2
-            nks = (K + 63) // 64
-            sz = torch.empty(E, R, 2, nks, dtype=torch.int32, device=d["q"].device)
-            L.call("smel_int4_pack_sz", L.ptr(d["scale"]), L.ptr(d["zero"]), E * R, K, Int4Experts.group_of(d),
-                   L.ptr(sz), L.stream())
-            cache[which] = sz
+            lib = L.load()
+            qf = torch.empty(lib.smel_packed_bytes(L.PACK_Q4, E * R, K), dtype=torch.uint8, device=d["q"].device)
+            szf = torch.empty(lib.smel_packed_bytes(L.PACK_SZ, E * R, K) // 4, dtype=torch.int32,
+                              device=d["q"].device)
+            L.call("smel_pack_int4", L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"]), E * R, K,
+                   Int4Experts.group_of(d), L.ptr(qf), L.ptr(szf), L.stream())
+            cache[which] = (qf, szf)
         return cache[which]
 
     def weights(self, e0: int, e1: int):
@@ -110,6 +154,15 @@ class LayerExperts:
         if self.sel_ids is not None:
             self._slot = {int(e): j for j, e in enumerate(self.sel_ids.tolist())}
         self._gkind = {}
+
+    def packed_sel(self):
+        """(gate_up, down) of the selected experts in the GEMMs' fragment layout, built once (frozen base weights;
+        their LoRA is applied on top). None without selected experts."""
+        if self.sel_ids is None or not self._slot:
+            return None
+        if "_packed_sel" not in self.__dict__:
+            self._packed_sel = (pack_bf16(_bf16(self.sel_gate_up)), pack_bf16(_bf16(self.sel_down)))
+        return self._packed_sel
 
     def gkind(self, with_shared: bool, device) -> torch.Tensor:
         """Per-group weight location: (kind << 16) | index, groups 0..E-1 (+ E = shared)."""
@@ -176,16 +229,20 @@ def _dense_tiles(T: int, device):
     return _dense_tiles_cache[key]
 
 
-def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> torch.Tensor:
-    """[Epad][H] bf16 = router rows, then the shared-gate row, zero-padded to a multiple of 32 rows: the weight of the
-    router-backward GEMM (dx += dlogits . W). Built per call (E x H bf16, about 1 MB)."""
+def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> PackedW:
+    """The weight of the router-backward GEMM (dx += dlogits . W): router rows, then the shared-gate row, zero-padded
+    to a multiple of 32 rows ([Epad, H], Epad = R of the result), packed. Built per call (E x H bf16, about 1 MB)."""
     E, H = gate_w.shape
     Epad = (E + 1 + 31) // 32 * 32
-    w = torch.zeros(Epad, H, dtype=torch.bfloat16, device=gate_w.device)
-    w[:E] = gate_w
-    if sg_w is not None:
+    if sg_w is None:
+        pw = pack_bf16(gate_w)
+    else:
+        w = torch.empty(E + 1, H, dtype=torch.bfloat16, device=gate_w.device)
+        w[:E] = gate_w
         w[E] = sg_w.reshape(-1)
-    return w
+        pw = pack_bf16(w)
+    pw.R = Epad
+    return pw
 
 
 class _LoRABufs:
@@ -204,24 +261,24 @@ class _LoRABufs:
                L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu), L.stream())
 
 
-def _wset(ex: LayerExperts, which: str, sel_w, sh_w, ext_sel, ext_sh) -> L.WSet:
-    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer."""
+def _wset(ex: LayerExperts, which: str, sel_w: PackedW | None, sh_w: PackedW | None, ext_sel, ext_sh) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights)."""
     fz = ex.frozen
     w = L.WSet()
     if isinstance(fz, Int4Experts):
         d = fz.gu if which == "gu" else fz.dn
-        w.q4, w.s4, w.z4 = L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"])
-        w.sz4 = L.ptr(fz.packed_sz(which))
+        qf, szf = fz.packed(which)
+        w.q4, w.sz4 = L.ptr(qf), L.ptr(szf)
         w.group = Int4Experts.group_of(d)
         R = d["q"].shape[1]
         C = d["q"].shape[2] * 2
     else:
-        t = fz.gate_up if which == "gu" else fz.down
-        w.wb = L.ptr(t)
+        pw = fz.packed(which)
+        w.wb = L.ptr(pw.t)
         w.group = 32
-        R, C = t.shape[1], t.shape[2]
-    w.wsel = L.ptr(sel_w)
-    w.wsh = L.ptr(sh_w)
+        R, C = pw.R, pw.C
+    w.wsel = L.ptr(sel_w.t) if sel_w is not None else None
+    w.wsh = L.ptr(sh_w.t) if sh_w is not None else None
     w.ext_sel = L.ptr(ext_sel)
     w.ext_sh = L.ptr(ext_sh)
     w.R, w.C = R, C
@@ -274,7 +331,7 @@ class _RouteFn(torch.autograd.Function):
         dwp = dtopv.float().contiguous().reshape(-1, 1)
         ident = torch.arange(T * K, dtype=torch.int32, device=dev)
         wr = _router_ext_weight(gate_w, None)
-        Epad = wr.shape[0]
+        Epad = wr.R
         dl = torch.empty(T, Epad, dtype=torch.bfloat16, device=dev)
         L.call("smel_route_bwd", L.ptr(dwp), 1, L.ptr(ident), L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
                L.ptr(dl), Epad, None, L.stream())
@@ -282,13 +339,13 @@ class _RouteFn(torch.autograd.Function):
         return dx, None, None
 
 
-def _router_dx(dl: torch.Tensor, wr: torch.Tensor, T: int) -> torch.Tensor:
-    H = wr.shape[1]
+def _router_dx(dl: torch.Tensor, wr: PackedW, T: int) -> torch.Tensor:
+    H = wr.C
     tiles, ntiles, maxt, gk = _dense_tiles(T, dl.device)
     dx = torch.empty(T, H, dtype=torch.bfloat16, device=dl.device)
     w = L.WSet()
-    w.wsh = L.ptr(wr)
-    w.R, w.C, w.group = wr.shape[0], H, 32
+    w.wsh = L.ptr(wr.t)
+    w.R, w.C, w.group = wr.R, H, 32
     L.call("smel_gmm_bwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dl), dl.shape[1], T, 0,
            None, 0, 1, None, 0, 0, None, None, None, L.ptr(dx), H, None, L.stream(), tag="gemm_router_bwd")
     return dx
@@ -346,7 +403,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     gk = ex.gkind(shared is not None, dev)
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):
-        sel_gu, sel_dn = _bf16(ex.sel_gate_up), _bf16(ex.sel_down)
+        sel_gu, sel_dn = ex.packed_sel()
     I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
     sh_gu = sh_dn = sgate = None
     if shared is not None:
@@ -437,7 +494,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     dtopv = None
     if router is not None:
         probs, topi32, wr = router
-        Epad = wr.shape[0]
+        Epad = wr.R
         dl = bf(T, Epad)
         L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32), L.ptr(t["topv"]),
                L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, st)
@@ -576,7 +633,7 @@ class _MLPFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w_gu, w_dn, lora, act_name, *leaves):
         T, H = x.shape
-        Is = w_dn.shape[1]
+        Is = w_dn.C
         dev = x.device
         st = L.stream()
         tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
@@ -601,19 +658,21 @@ class _MLPFn(torch.autograd.Function):
         wd = _dense_wset(w_dn, g("fwd_dn"))
         L.call("smel_gmm_fwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), Is, T, 0,
                None, 0, 1, L.ptr(ext_dn), 0, _ACT[act_name], L.ptr(y), H, None, st, tag="gemm_mlp_dn_fwd")
-        ctx.save_for_backward(x, w_gu, w_dn, actb, hsave)
+        ctx.save_for_backward(x, actb, hsave)
+        ctx.w = (w_gu, w_dn)
         ctx.ext = (ext_gu, ext_dn)
         ctx.lb, ctx.lora, ctx.act_name = lb, lora, act_name
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x, w_gu, w_dn, actb, hsave = ctx.saved_tensors
+        x, actb, hsave = ctx.saved_tensors
+        w_gu, w_dn = ctx.w
         ext_gu, ext_dn = ctx.ext
         lb, lora = ctx.lb, ctx.lora
         dy = _bf16(dy)
         T, H = x.shape
-        Is = w_dn.shape[1]
+        Is = w_dn.C
         dev = x.device
         st = L.stream()
         tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
@@ -661,15 +720,15 @@ class _MLPFn(torch.autograd.Function):
                      "B_up": dB_gu[16:16 + r, Is:].t(), "A_down": dA_dn[:r], "B_down": dB_dn[:r].t()}
             grads = [named[n].contiguous().to(getattr(lora, n).dtype) if getattr(lora, n).requires_grad else None
                      for n in _LORA_NAMES]
-        ctx.lb = ctx.lora = ctx.ext = None
+        ctx.lb = ctx.lora = ctx.ext = ctx.w = None
         return (dx, None, None, None, None, *grads)
 
 
-def _dense_wset(w: torch.Tensor, ext) -> L.WSet:
+def _dense_wset(w: PackedW, ext) -> L.WSet:
     ws = L.WSet()
-    ws.wsh = L.ptr(w)
+    ws.wsh = L.ptr(w.t)
     ws.ext_sh = L.ptr(ext)
-    ws.R, ws.C, ws.group = w.shape[0], w.shape[1], 32
+    ws.R, ws.C, ws.group = w.R, w.C, 32
     return ws
 
 
@@ -680,8 +739,13 @@ def mlp_lora(x, w_gate, w_up, w_down, lora, act_name="silu", w_gate_up=None):
         raise ValueError(f"unknown activation {act_name}")
     L.require_device(x, w_down)
     xs = x.reshape(-1, x.shape[-1])
-    gu = w_gate_up if w_gate_up is not None else torch.cat((w_gate, w_up))
-    y = _MLPFn.apply(_bf16(xs), _bf16(gu), _bf16(w_down), lora, act_name, *_lora_leaves(lora))
+    if w_gate_up is not None:
+        pgu = pack_bf16(_bf16(w_gate_up))
+    else:
+        if w_gate.shape[0] % 32:
+            raise L.SmelError(f"mlp_lora: intermediate size {w_gate.shape[0]} must be a multiple of 32")
+        pgu = pack_bf16(_bf16(w_gate), _bf16(w_up))
+    y = _MLPFn.apply(_bf16(xs), pgu, pack_bf16(_bf16(w_down)), lora, act_name, *_lora_leaves(lora))
     return y.reshape(*x.shape[:-1], y.shape[-1])
 
 
@@ -695,13 +759,16 @@ def shared_mlp(x, W, lora):
 
 
 def _shared_weights(W: dict):
+    """(gate_up, down) of the shared expert packed (per call: the dict's tensors may change between calls), the
+    shared-gate row, and the shared intermediate size; None without a shared expert."""
     pre = "mlp.shared_expert."
     if pre + "gate_proj.weight" not in W and pre + "gate_up_proj.weight" not in W:
         return None
     gu = W.get(pre + "gate_up_proj.weight")
-    if gu is None:
-        gu = torch.cat((W[pre + "gate_proj.weight"], W[pre + "up_proj.weight"]))
-    return _bf16(gu), _bf16(W[pre + "down_proj.weight"]), _bf16(W["mlp.shared_expert_gate.weight"].reshape(-1))
+    dn = _bf16(W[pre + "down_proj.weight"])
+    pgu = pack_bf16(_bf16(gu)) if gu is not None else pack_bf16(_bf16(W[pre + "gate_proj.weight"]),
+                                                                  _bf16(W[pre + "up_proj.weight"]))
+    return pgu, pack_bf16(dn), _bf16(W["mlp.shared_expert_gate.weight"].reshape(-1)), dn.shape[1]
 
 
 def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=None):
@@ -715,7 +782,7 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
     shared = _shared_weights(W)
     if shared is not None:
         I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
-        if shared[1].shape[1] != I:
+        if shared[3] != I:
             raise NotImplementedError("fused shared expert needs shared intermediate == expert intermediate")
     if lora_ex is not None and (ex.sel_ids is None or len(ex._slot) == 0):
         lora_ex = None

@@ -32,8 +32,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_wset_layout_matches_header():
     from smel import _lib
-    # 9 pointers, two int64, two int32
-    assert ctypes.sizeof(_lib.WSet) == 9 * 8 + 2 * 8 + 2 * 4
+    # 7 pointers, two int64, two int32
+    assert ctypes.sizeof(_lib.WSet) == 7 * 8 + 2 * 8 + 2 * 4
 
 
 def test_host_side_rejections():
@@ -53,6 +53,13 @@ def test_host_side_rejections():
     w = _lib.WSet()
     w.R, w.C, w.group = 64, 48, 64
     assert L.smel_gmm_fwd(ctypes.byref(w), 1, 1, 1, 1, 16, 48, 4, 0, None, 0, 1, None, 0, 0, 16, 64, None, None) == -2
+    # packing: sizes and rejections
+    assert L.smel_packed_bytes(_lib.PACK_Q4, 64, 2048) == 2 * 32 * 1024
+    assert L.smel_packed_bytes(_lib.PACK_SZ, 64, 2048) == 2 * 8 * 1024
+    assert L.smel_packed_bytes(_lib.PACK_BF16, 33, 96) == 2 * 2 * 4096
+    assert L.smel_packed_bytes(7, 64, 64) == -1
+    assert L.smel_pack_int4(1, 1, 1, 64, 96, 64, 1, 1, None) == -2      # group does not divide K
+    assert L.smel_pack_bf16(1, 64, 60, 64, 1, None) == -2               # K not a multiple of 8
     with pytest.raises(_lib.SmelError):
         _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, 32, 64, 64, None, None, None, None, None,
                   None, None)

@@ -63,6 +63,63 @@ def test_dequant_random_bitexact(shape, group):
     assert np.array_equal(_u16(out), intref.dequant_bits(q.numpy(), _u16(s), _u16(z)))
 
 
+# ------------------------------------------------------------------------------------------------------- packing
+# The GEMMs read weights in the fragment layout of include/smel_moe.h (SMEL_PACK_*); these tests invert that layout
+# with numpy index arithmetic and require the round trip to be the identity, with zeros in the padding.
+
+
+def _unpack_q4(qf, szf, rows, K):
+    nf, nk = -(-rows // 32), -(-K // 64)
+    nk4 = -(-nk // 4)
+    q = qf.reshape(nf, nk, 2, 32, 16).transpose(0, 3, 1, 2, 4).reshape(nf * 32, nk * 32)
+    sz = szf.reshape(nf, nk4, 2, 32, 4).transpose(0, 3, 1, 4, 2).reshape(nf * 32, nk4 * 4, 2)
+    return q, sz
+
+
+@pytest.mark.parametrize("E,R,K,group", [(3, 64, 192, 64), (2, 32, 96, 32), (1, 96, 2048, 64)])
+def test_pack_int4_roundtrip(E, R, K, group):
+    L = _lib()
+    _say(f"pack int4 E{E} R{R} K{K} g{group}")
+    gen = torch.Generator().manual_seed(E * R + K)
+    q = torch.randint(0, 256, (E, R, K // 2), generator=gen, dtype=torch.uint8)
+    sc = torch.randint(0, 65536, (E, R, K // group), generator=gen, dtype=torch.int32).to(torch.int16)
+    ze = torch.randint(0, 65536, (E, R, K // group), generator=gen, dtype=torch.int32).to(torch.int16)
+    lib = L.load()
+    rows = E * R
+    qf = torch.empty(lib.smel_packed_bytes(L.PACK_Q4, rows, K), dtype=torch.uint8, device=DEV)
+    szf = torch.empty(lib.smel_packed_bytes(L.PACK_SZ, rows, K) // 4, dtype=torch.int32, device=DEV)
+    qd, sd, zd = q.to(DEV), sc.to(DEV), ze.to(DEV)
+    L.call("smel_pack_int4", L.ptr(qd), L.ptr(sd), L.ptr(zd), rows, K, group, L.ptr(qf), L.ptr(szf), L.stream())
+    uq, usz = _unpack_q4(qf.cpu().numpy(), szf.cpu().numpy().view(np.uint32), rows, K)
+    qn = q.reshape(rows, K // 2).numpy()
+    assert np.array_equal(uq[:, :K // 2], qn)
+    assert not uq[:, K // 2:].any()
+    s16 = sc.reshape(rows, -1).numpy().view(np.uint16).astype(np.uint32)
+    z16 = ze.reshape(rows, -1).numpy().view(np.uint16).astype(np.uint32)
+    nks = usz.shape[1]
+    col = 64 * np.arange(nks)[:, None] + 32 * np.arange(2)[None, :]          # [ks][h]
+    inside = col < K
+    g = np.minimum(col, K - 1) // group
+    want = np.where(inside[None], s16[:, g] | (z16[:, g] << 16), 0).astype(np.uint32)
+    assert np.array_equal(usz, want)
+
+
+@pytest.mark.parametrize("rows,K,ld", [(33, 72, 80), (64, 2048, 2048), (32, 32, 32)])
+def test_pack_bf16_roundtrip(rows, K, ld):
+    L = _lib()
+    _say(f"pack bf16 rows{rows} K{K} ld{ld}")
+    gen = torch.Generator().manual_seed(rows + K)
+    w = torch.randn(rows, ld, generator=gen).to(torch.bfloat16)
+    lib = L.load()
+    wf = torch.empty(lib.smel_packed_bytes(L.PACK_BF16, rows, K) // 2, dtype=torch.bfloat16, device=DEV)
+    wd = w.to(DEV)
+    L.call("smel_pack_bf16", L.ptr(wd), rows, K, ld, L.ptr(wf), L.stream())
+    nf, nk = -(-rows // 32), -(-K // 64)
+    u = _u16(wf).reshape(nf, nk, 4, 2, 32, 8).transpose(0, 4, 1, 3, 2, 5).reshape(nf * 32, nk * 64)
+    assert np.array_equal(u[:rows, :K], _u16(w)[:, :K])
+    assert not u[rows:].any() and not u[:, K:].any()
+
+
 # -------------------------------------------------------------------------------------------------------- router
 
 
