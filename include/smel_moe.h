@@ -146,7 +146,8 @@ int smel_combine(const uint16_t* Y, const uint16_t* topv, const float* sgate, in
  * epilogue 0: out[slot(row)][n] = bf16(acc), n < C                                   (dX of gate_up: dh W_gu)
  * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] or sgate[t]; (g, u) = hsave[row];
  *             out[row][n] = bf16(da u act'(g)), out[row][I+n] = bf16(da act(g));
- *             dwp[row][blockIdx.y] = sum_n acc * bf16(act(g) u)   (d row weight, reduced later in fixed order)
+ *             dwp[row][j] = sum over column block j of acc * bf16(act(g) u)   (d row weight, reduced later in
+ *             fixed order); dwp holds (rows) x smel_gmm_bwd_nblocks(C) floats
  * A rows: A[token(row)] if a_gather else A[row]; A holds a_rows rows; the GEMM K = w.R. */
 int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                  int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,

@@ -107,6 +107,8 @@ SMEL_DEV rsrc_t make_rsrc(const void* base, uint64_t bytes) {
 SMEL_DEV u32x4_t ld16(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 SMEL_DEV uint32_t ld2(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
 SMEL_DEV uint32_t ld4(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+SMEL_DEV u32x2_t ld8(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
 
 // Loads straight into LDS (gfx950: 16 B per lane): lane i of the wave writes bytes [16 i, 16 i + 16) after the
 // wave-uniform LDS address `lds`; an out-of-range offset writes zeros. Completion is counted by vmcnt.
@@ -118,6 +120,11 @@ SMEL_DEV void ld16_lds(rsrc_t r, const void* lds, uint32_t off) {
 #define SMEL_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 // ... and on LDS as well (lgkmcnt = 0): this wave's own LDS reads are done.
 #define SMEL_WAIT_VM_LDS(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+
+// Operand tiles in LDS hold rows of 64 bf16 (128 B) without padding; the physical 16-B chunk of logical chunk c of
+// row r is c ^ swz(r), so 8 (or 16) lanes reading consecutive rows at one logical chunk touch distinct banks with 32
+// (or 64) four-byte banks.
+SMEL_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // ------------------------------------------------------------------------------------------------ XCD-aware tiles
 // MI355X has 8 XCDs, each with its own L2; consecutive workgroup ids go to consecutive XCDs. A 1-D grid of

@@ -5,20 +5,24 @@
 // k-contiguous bf16 for the MFMA B operand. Reference: FrozenExpertsFn.backward, smel/moe.py:128-143, and the
 // autograd of _selected_expert / lora_gate_up / lora_linear / the combine, smel/moe.py:204-252, smel/lora.py:61-83.
 //
-// Block = 4 waves, tile = up to 128 rows (4 slices of 32) x 256 columns (64 per wave). Per 64-row step of W: the raw
-// A rows and raw W rows of the next step are loaded into registers while the current step's MFMAs run; then A is
-// written to LDS and W is dequantized (int4) and written transposed: thread (k pair, 32 columns) packs W[k][n] and
-// W[k+1][n] into one 32-bit LDS word of row n, so a wave's stores cover 32 consecutive words of a row.
+// Block = 4 waves in a 2 x 2 grid, tile = up to 128 rows x 128 columns, each wave 64 rows (2 slices of 32) x 64
+// columns (2 fragments). Per 64-row step of W (one barrier per step):
+//  * A rows (gathered by token for the down projection) go global -> LDS by LDS-DMA into a ring of 3 stages,
+//    2 steps ahead;
+//  * W is read from the fragment layout of smel_pack_int4 / smel_pack_bf16 into registers 3 steps ahead; one step
+//    ahead of its use, every thread dequantizes a row pair x 16 columns and writes them transposed (a 32-bit word =
+//    the two rows of one column) into one of two W^T buffers [column][k];
+//  * vmcnt retires in issue order: each step issues W before A and waits for exactly what the step uses.
 #include "abi_util.h"
 #include "common.h"
 
 namespace {
 
 constexpr int MT = 128;
-constexpr int NT = 256;
+constexpr int NT = 128;
 constexpr int KT = 64;
-constexpr int AS = KT + 8;   // A rows in LDS (bf16)
-constexpr int BS = KT + 8;   // transposed W rows in LDS (bf16)
+constexpr int A_STAGE = MT * KT;   // bf16 elements of one A stage
+constexpr int B_STAGE = NT * KT;   // bf16 elements of one W^T buffer: column n at n * KT
 
 struct BwdArgs {
   smel_wset w;
@@ -41,150 +45,204 @@ struct BwdArgs {
   int nblk;    // column blocks per tile
 };
 
-// Raw W data of one thread for one step: rows (ka, ka+1), 32 columns.
-template <bool Q4>
-struct WRegs;
-template <>
-struct WRegs<true> {
-  u32x4_t q[2];
-  uint32_t s[2], z[2];
-};
-template <>
-struct WRegs<false> {
-  u32x4_t v[2][4];
+// Raw W data of one thread for one step, rows (ka, ka+1) x 16 columns: bf16 in v[row][0..1] (8 columns each), or
+// int4: v[row][0] = the row's 16-B lane chunk of q (32 columns, this thread's 16 in words 2 hq, 2 hq + 1) and
+// v[row][1] = its 16-B chunk of packed scale/zero (this k-step's word at index cks % 4).
+struct WRegs {
+  u32x4_t v[2][2];
 };
 
-template <int EPI, bool Q4, int NS>
-SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As,
-                       uint16_t* Bt) {
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
+template <int EPI, int NSW>
+SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
+                       uint16_t* S2, uint16_t* B0, uint16_t* B1) {
+  const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = w >> 1, wc = w & 1;   // this wave: tile rows [64 wr, +64), columns [64 wc, +64)
   const int n0 = nb * NT;
   const int Kd = a.Kd;
   const smel_wset& ws = a.w;
-  const int cw = n0 + w * 64;                 // this wave's first column
+  const int cw = n0 + wc * 64;         // this wave's first column
   const bool fv0 = cw < a.N, fv1 = cw + 32 < a.N;
-  // ---- staging roles: A (tile row, 32-wide half), W (k pair, 32 columns)
-  const int ar = tid >> 1, ap = tid & 1;
-  const int kp = tid & 31, c32 = tid >> 5;
-  const int nc = n0 + 32 * c32;
-  const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
-  uint32_t aoff = OOB;
-  if (ar < nrows) {
-    const int grow = row0 + ar;
-    const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
-    aoff = (uint32_t)src * (uint32_t)a.lda * 2 + 64 * ap;
-  }
-  // W rows (ka, ka+1) = lanes (i, i+1) of fragment ka / 32 in the packed layout; columns [nc, nc+32) = half h of
-  // k-step ks of that layout.
-  const int pk = (a.N + 63) / 64, pk4 = (pk + 3) / 4, nfr = Kd / 32;   // k-steps of the packed layout (along C)
-  const int cks = nc / 64, ch = (nc / 32) & 1;
+  const int nk = (Kd + KT - 1) / KT;
+  // ---- W staging role: rows (k0 + 2 kp, +1) x columns [nc, nc + 16)
+  const int kp = tid & 31, cc = tid >> 5;
+  const int nc = n0 + 16 * cc;
   const bool cok = nc < a.N;
+  const int pk = (a.N + 63) / 64, pk4 = (pk + 3) / 4, nfr = Kd / 32;   // packed k-steps run along C here
+  const int cks = nc / 64, ch = (nc >> 5) & 1;
+  const int lane2 = 32 * ch + (2 * kp) % 32;   // packed lane of row ka (row ka + 1 is the next lane)
+  const bool q4 = kind == SMEL_KIND_INT4;   // uniform: the tile's group kind
+  const int hq = (nc >> 4) & 1;              // int4: which 8 bytes of the 16-B q chunk are this thread's
+  const int zw = cks & 3;                     // int4: word of the packed scale/zero chunk
   rsrc_t rw, rsz;
-  uint32_t wbase, sbase = 0;   // byte offset of this thread's first chunk at k0 = 0
-  if constexpr (Q4) {
+  uint32_t wbase, sbase, wstep, sstep;
+  if (q4) {
     rw = make_rsrc(ws.q4 + (int64_t)idx * nfr * pk * 1024, (uint64_t)nfr * pk * 1024);
     rsz = make_rsrc(ws.sz4 + (int64_t)idx * nfr * pk4 * 256, (uint64_t)nfr * pk4 * 1024);
-    wbase = (uint32_t)((cks * 64 + 32 * ch + (2 * kp) % 32) * 16);
-    sbase = (uint32_t)(((cks >> 2) * 64 + 32 * ch + (2 * kp) % 32) * 16 + 4 * (cks & 3));
+    wbase = (uint32_t)((cks * 64 + lane2) * 16);
+    sbase = (uint32_t)(((cks >> 2) * 64 + lane2) * 16);
+    wstep = pk * 1024;
+    sstep = pk4 * 1024;
   } else {
     const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
     const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
     rw = make_rsrc(base + mi * nfr * pk * 2048, (uint64_t)nfr * pk * 4096);
     rsz = rw;
-    wbase = (uint32_t)((cks * 4 * 64 + 32 * ch + (2 * kp) % 32) * 16);
+    wbase = (uint32_t)(((cks * 4 + ((nc >> 3) & 3)) * 64 + lane2) * 16);
+    sbase = wbase + 1024;   // the next 8 columns
+    wstep = sstep = pk * 4096;
   }
-
-  f32x16_t acc[NS][2];
-#pragma unroll
-  for (int m = 0; m < NS; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
-
-  u32x4_t areg[4];
-  WRegs<Q4> wr;
-  auto load_step = [&](int k0) {
-    const uint32_t ao = (k0 + 32 * ap + 32 <= Kd) ? aoff + k0 * 2 : OOB;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) areg[i] = ld16(ra, ao + 16 * i);
-    const int ka = k0 + 2 * kp;
-    const bool ok = cok && ka + 1 < Kd;
-    const int fr = ka / 32;
-    if constexpr (Q4) {
-      const uint32_t o = (uint32_t)fr * pk * 1024 + wbase;
-      wr.q[0] = ld16(rw, ok ? o : OOB);
-      wr.q[1] = ld16(rw, ok ? o + 16 : OOB);
-      const uint32_t so = (uint32_t)fr * pk4 * 1024 + sbase;
-      const uint32_t p0 = ld4(rsz, ok ? so : OOB), p1 = ld4(rsz, ok ? so + 16 : OOB);
-      wr.s[0] = p0 & 0xffffu;
-      wr.z[0] = p0 >> 16;
-      wr.s[1] = p1 & 0xffffu;
-      wr.z[1] = p1 >> 16;
-    } else {
-      const uint32_t o = (uint32_t)fr * pk * 4096 + wbase;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        wr.v[0][i] = ld16(rw, ok ? o + 1024 * i : OOB);
-        wr.v[1][i] = ld16(rw, ok ? o + 1024 * i + 16 : OOB);
-      }
-    }
+  // Four 16-B loads per thread and step for either kind, at addresses chosen above (no branch here: a branch
+  // between the two kinds' loads makes the compiler wait for the other branch's loads as well).
+  auto issue_w = [&](int j, WRegs& r) {
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t fr = (uint32_t)((j * KT + 2 * kp) / 32);
+    const bool ok = cok && j < nk;
+    const uint32_t o = fr * wstep + wbase, so = fr * sstep + sbase;
+    r.v[0][0] = ld16(rw, ok ? o : OOB);
+    r.v[0][1] = ld16(rsz, ok ? so : OOB);
+    r.v[1][0] = ld16(rw, ok ? o + 16 : OOB);
+    r.v[1][1] = ld16(rsz, ok ? so + 16 : OOB);
   };
-  auto store_step = [&]() {
-    uint16_t* adst = As + ar * AS + 32 * ap;
+  // W^T word of tile column n = 16 cc + c and k pair kp: element n * KT + 8 * ((kp / 4) ^ swz(n)) + 2 * (kp % 4);
+  // swz(16 cc + c) = swz(c), a constant per c.
+  uint32_t* const wt0 = reinterpret_cast<uint32_t*>(B0) + 16 * cc * (KT / 2) + (kp & 3);
+  uint32_t* const wt1 = reinterpret_cast<uint32_t*>(B1) + 16 * cc * (KT / 2) + (kp & 3);
+  const int kc = kp >> 2;
+  auto store_w = [&](const WRegs& r, uint32_t* wt) {
+    uint32_t word[16];
+    if (q4) {
+      const uint32_t p0 = zw == 0 ? r.v[0][1].x : zw == 1 ? r.v[0][1].y : zw == 2 ? r.v[0][1].z : r.v[0][1].w;
+      const uint32_t p1 = zw == 0 ? r.v[1][1].x : zw == 1 ? r.v[1][1].y : zw == 2 ? r.v[1][1].z : r.v[1][1].w;
+      const float s0 = bf_lo(p0), z0 = bf_hi(p0), s1 = bf_lo(p1), z1 = bf_hi(p1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(adst + 8 * i) = areg[i];
-    uint32_t* dst = reinterpret_cast<uint32_t*>(Bt + (32 * c32) * BS + 2 * kp);
-    if constexpr (Q4) {
-      const float s0 = bf2f(wr.s[0]), z0 = bf2f(wr.z[0]), s1 = bf2f(wr.s[1]), z1 = bf2f(wr.z[1]);
-#pragma unroll
-      for (int wd = 0; wd < 4; ++wd) {
-        const uint32_t l0 = wr.q[0][wd] & 0x0f0f0f0fu, h0 = (wr.q[0][wd] >> 4) & 0x0f0f0f0fu;
-        const uint32_t l1 = wr.q[1][wd] & 0x0f0f0f0fu, h1 = (wr.q[1][wd] >> 4) & 0x0f0f0f0fu;
-        uint32_t* d = dst + (8 * wd) * (BS / 2);
-        d[0 * (BS / 2)] = pack2bf(fmaf(ub0(l0), s0, z0), fmaf(ub0(l1), s1, z1));
-        d[1 * (BS / 2)] = pack2bf(fmaf(ub0(h0), s0, z0), fmaf(ub0(h1), s1, z1));
-        d[2 * (BS / 2)] = pack2bf(fmaf(ub1(l0), s0, z0), fmaf(ub1(l1), s1, z1));
-        d[3 * (BS / 2)] = pack2bf(fmaf(ub1(h0), s0, z0), fmaf(ub1(h1), s1, z1));
-        d[4 * (BS / 2)] = pack2bf(fmaf(ub2(l0), s0, z0), fmaf(ub2(l1), s1, z1));
-        d[5 * (BS / 2)] = pack2bf(fmaf(ub2(h0), s0, z0), fmaf(ub2(h1), s1, z1));
-        d[6 * (BS / 2)] = pack2bf(fmaf(ub3(l0), s0, z0), fmaf(ub3(l1), s1, z1));
-        d[7 * (BS / 2)] = pack2bf(fmaf(ub3(h0), s0, z0), fmaf(ub3(h1), s1, z1));
+      for (int d = 0; d < 2; ++d) {
+        const uint32_t q0 = hq ? r.v[0][0][2 + d] : r.v[0][0][d], q1 = hq ? r.v[1][0][2 + d] : r.v[1][0][d];
+        const uint32_t l0 = q0 & 0x0f0f0f0fu, h0 = (q0 >> 4) & 0x0f0f0f0fu;
+        const uint32_t l1 = q1 & 0x0f0f0f0fu, h1 = (q1 >> 4) & 0x0f0f0f0fu;
+        uint32_t* o = word + 8 * d;
+        o[0] = pack2bf(fmaf(ub0(l0), s0, z0), fmaf(ub0(l1), s1, z1));
+        o[1] = pack2bf(fmaf(ub0(h0), s0, z0), fmaf(ub0(h1), s1, z1));
+        o[2] = pack2bf(fmaf(ub1(l0), s0, z0), fmaf(ub1(l1), s1, z1));
+        o[3] = pack2bf(fmaf(ub1(h0), s0, z0), fmaf(ub1(h1), s1, z1));
+        o[4] = pack2bf(fmaf(ub2(l0), s0, z0), fmaf(ub2(l1), s1, z1));
+        o[5] = pack2bf(fmaf(ub2(h0), s0, z0), fmaf(ub2(h1), s1, z1));
+        o[6] = pack2bf(fmaf(ub3(l0), s0, z0), fmaf(ub3(l1), s1, z1));
+        o[7] = pack2bf(fmaf(ub3(h0), s0, z0), fmaf(ub3(h1), s1, z1));
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t x0 = wr.v[0][i][j], x1 = wr.v[1][i][j];
-          dst[(8 * i + 2 * j) * (BS / 2)] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-          dst[(8 * i + 2 * j + 1) * (BS / 2)] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+          const uint32_t x0 = r.v[0][d][j], x1 = r.v[1][d][j];
+          word[8 * d + 2 * j] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+          word[8 * d + 2 * j + 1] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) wt[c * (KT / 2) + 4 * (kc ^ swz(c))] = word[c];
+  };
+  // ---- A staging (as the forward kernel): wave-load ii of wave w fills rows 8 g .. 8 g + 7, g = 4 w + ii
+  const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
+  const int li = tid & 63;
+  uint32_t aoff[4];
+  int akc[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const int g = 4 * w + ii;
+    const int row = 8 * g + (li >> 3);
+    const int c = (li & 7) ^ swz(row);
+    akc[ii] = 8 * c;
+    aoff[ii] = OOB;
+    if (row < nrows) {
+      const int grow = row0 + row;
+      const int src = a.a_gather ? row_token(grow, a.order, a.TK, a.topk) : grow;
+      aoff[ii] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * c;
+    }
+  }
+  auto issue_a = [&](int j, uint16_t* S) {
+    const int k0 = j * KT;
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii)
+      ld16_lds(ra, S + (4 * w + ii) * 512, (k0 + akc[ii] + 8 <= Kd) ? aoff[ii] + k0 * 2 : OOB);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // fragment reads: A row 64 wr + 32 m + r32, W^T column 64 wc + 32 f + r32, logical chunk 4 h + s
+  uint32_t frd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) frd[s] = r32 * KT + 8 * ((4 * hi + s) ^ swz(r32));
+  const int abase = 64 * wr * KT, bbase = 64 * wc * KT;
+
+  f32x16_t acc[NSW > 0 ? NSW : 1][2];
+#pragma unroll
+  for (int m = 0; m < (NSW > 0 ? NSW : 1); ++m) acc[m][0] = acc[m][1] = f32x16_t{};
+
+  auto compute = [&](const uint16_t* Sa, const uint16_t* Bt) {
+    if constexpr (NSW > 0) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(Bt + bbase + frd[s]);
+        const u32x4_t b1 = *reinterpret_cast<const u32x4_t*>(Bt + bbase + 32 * KT + frd[s]);
+#pragma unroll
+        for (int m = 0; m < NSW; ++m) {
+          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Sa + abase + m * 32 * KT + frd[s]);
+          acc[m][0] = mfma32(af, b0, acc[m][0]);
+          acc[m][1] = mfma32(af, b1, acc[m][1]);
         }
       }
     }
   };
 
-  const int nk = (Kd + KT - 1) / KT;
-  load_step(0);
-  const uint16_t* Ab = As + r32 * AS + 32 * hi;
-  const uint16_t* Bb = Bt + (w * 64 + r32) * BS + 32 * hi;
-  for (int i = 0; i < nk; ++i) {
-    store_step();
-    __syncthreads();
-    if (i + 1 < nk) load_step((i + 1) * KT);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(Bb + 8 * s);
-      const u32x4_t b1 = *reinterpret_cast<const u32x4_t*>(Bb + 32 * BS + 8 * s);
-#pragma unroll
-      for (int m = 0; m < NS; ++m) {
-        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ab + m * 32 * AS + 8 * s);
-        acc[m][0] = mfma32(af, b0, acc[m][0]);
-        acc[m][1] = mfma32(af, b1, acc[m][1]);
+  // Ring positions of step j: A stage j % 3 (loaded 2 steps ahead), W^T buffer j % 2 (W(j+1) is dequantized into
+  // the other one during step j), W register set (j+1) % 6 dequantized and set (j+5) % 6 refilled (4 steps ahead).
+  WRegs w0, w1, w2, w3, w4, w5;
+  issue_w(0, w0);
+  issue_w(1, w1);
+  issue_w(2, w2);
+  issue_w(3, w3);
+  issue_a(0, S0);
+  issue_w(4, w4);
+  issue_a(1, S1);
+  store_w(w0, wt0);
+  auto step = [&](int j, uint16_t* Sa, uint16_t* Sa2, const uint16_t* Bc, uint32_t* wtn, const WRegs& wuse,
+                  WRegs& wiss) {
+    SMEL_WAIT_VM_LDS(8);   // A(j) and W(j+1) have landed: only step j-1's group may still be in flight
+    __builtin_amdgcn_s_barrier();
+    issue_w(j + 5, wiss);
+    issue_a(j + 2, Sa2);
+    store_w(wuse, wtn);    // W(j+1) -> the other W^T buffer
+    compute(Sa, Bc);
+  };
+  // whole rounds of 6 steps without exits (so the loop header keeps the waits above), then the remaining steps
+  int i = 0;
+  for (; i + 6 <= nk; i += 6) {
+    step(i, S0, S2, B0, wt1, w1, w5);
+    step(i + 1, S1, S0, B1, wt0, w2, w0);
+    step(i + 2, S2, S1, B0, wt1, w3, w1);
+    step(i + 3, S0, S2, B1, wt0, w4, w2);
+    step(i + 4, S1, S0, B0, wt1, w5, w3);
+    step(i + 5, S2, S1, B1, wt0, w0, w4);
+  }
+  if (i < nk) {
+    step(i, S0, S2, B0, wt1, w1, w5);
+    if (i + 1 < nk) {
+      step(i + 1, S1, S0, B1, wt0, w2, w0);
+      if (i + 2 < nk) {
+        step(i + 2, S2, S1, B0, wt1, w3, w1);
+        if (i + 3 < nk) {
+          step(i + 3, S0, S2, B1, wt0, w4, w2);
+          if (i + 4 < nk) step(i + 4, S1, S0, B0, wt1, w5, w3);
+        }
       }
     }
-    __syncthreads();
   }
+  SMEL_WAIT_VM_LDS(0);
+  __builtin_amdgcn_s_barrier();   // every wave is done with the ring: its LDS is reused below
   // ---- LoRA K-extension: ext[row][0:32] . Eb[0:32][n]
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * 32 * a.N : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
-  if (a.ext && eb) {
+  if (NSW > 0 && a.ext && eb) {
     u32x4_t b0[2], b1[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -206,8 +264,8 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     }
     const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
 #pragma unroll
-    for (int m = 0; m < NS; ++m) {
-      const int row = m * 32 + r32;
+    for (int m = 0; m < (NSW > 0 ? NSW : 1); ++m) {
+      const int row = 64 * wr + m * 32 + r32;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 32 * hi + 16 * s : OOB);
@@ -219,10 +277,10 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   // ---- epilogue
   if (EPI == 0) {
 #pragma unroll
-    for (int m = 0; m < NS; ++m) {
+    for (int m = 0; m < NSW; ++m) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m * 32 + acc_row(r, l);
+        const int row = 64 * wr + m * 32 + acc_row(r, l);
         if (row >= nrows) continue;
         const int64_t orow = (int64_t)row_slot(row0 + row, a.order, a.TK) * a.ldo;
         if (fv0) a.out[orow + cw + r32] = f2bf(acc[m][0][r]);
@@ -231,14 +289,14 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     }
     return;
   }
-  // down backward: columns n < I of dh = [dg | du]
-  float* red = reinterpret_cast<float*>(As);   // [4 waves][MT]; As is free after the last barrier
+  // down backward: columns n < I of dh = [dg | du]; per-row partial of sum_n dY.W[n] * act[n] over this block
+  float* red = reinterpret_cast<float*>(S0);   // [2 column halves][MT]
   const int I = a.N;
 #pragma unroll
-  for (int m = 0; m < NS; ++m) {
+  for (int m = 0; m < NSW; ++m) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = m * 32 + acc_row(r, l);
+      const int row = 64 * wr + m * 32 + acc_row(r, l);
       const bool rv = row < nrows;
       const int grow = row0 + row;
       float wrow_ = 0.f;
@@ -262,31 +320,33 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
         }
       }
       part = half_sum(part);
-      if (r32 == 0) red[w * MT + row] = part;
+      if (r32 == 0) red[wc * MT + row] = part;
     }
   }
   __syncthreads();
-  if (tid < MT && tid < nrows) {
-    const float v = ((red[tid] + red[MT + tid]) + red[2 * MT + tid]) + red[3 * MT + tid];
-    a.dwp[(int64_t)(row0 + tid) * a.nblk + nb] = v;
-  }
+  if (tid < MT && tid < nrows) a.dwp[(int64_t)(row0 + tid) * a.nblk + nb] = red[tid] + red[MT + tid];
 }
 
-template <int EPI, bool Q4>
-SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* As,
-                          uint16_t* Bt) {
-  switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, nb, As, Bt); break;
-    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, nb, As, Bt); break;
-    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, nb, As, Bt); break;
-    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, nb, As, Bt); break;
+template <int EPI>
+SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0,
+                          uint16_t* S1, uint16_t* S2, uint16_t* B0, uint16_t* B1) {
+  // slices of 32 rows this wave computes (its 64-row half of the tile); every wave stages and syncs alike
+  const int wr = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);
+  const int nsw = min(2, max(0, (nrows - 64 * wr + 31) >> 5));
+  switch (nsw) {
+    case 0: run_tile<EPI, 0>(a, kind, idx, row0, nrows, nb, S0, S1, S2, B0, B1); break;
+    case 1: run_tile<EPI, 1>(a, kind, idx, row0, nrows, nb, S0, S1, S2, B0, B1); break;
+    default: run_tile<EPI, 2>(a, kind, idx, row0, nrows, nb, S0, S1, S2, B0, B1); break;
   }
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_bwd_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[MT * AS];
-  __shared__ __attribute__((aligned(16))) uint16_t Bt[NT * BS];
+  __shared__ __attribute__((aligned(1024))) uint16_t S0[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S1[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S2[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t B0[B_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t B1[B_STAGE];
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
@@ -294,10 +354,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
-  if (kind == SMEL_KIND_INT4)
-    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, nb, As, Bt);
-  else
-    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, nb, As, Bt);
+  run_tile_ns<EPI>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, B0, B1);
 }
 
 }  // namespace

@@ -26,10 +26,6 @@ constexpr int MT = 128;
 constexpr int KT = 64;
 constexpr int A_STAGE = MT * KT;   // bf16 elements of one A stage: row r at r * KT, no padding
 
-// Physical 16-B chunk of logical chunk c in A row r is c ^ swz(r): 8 (or 16) lanes reading consecutive rows at one
-// logical chunk then touch distinct banks, with 32 or with 64 four-byte banks.
-SMEL_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
 struct FwdArgs {
   smel_wset w;
   const int32_t* gkind;
