@@ -112,6 +112,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE hot path here runs on one MI355X and has no multi-GPU path "
@@ -148,9 +149,34 @@ def main():
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms = dt / args.steps * 1e3
-    tok_s = cfg["T"] * args.steps / dt
-    log(f"step {ms:.3f} ms, {tok_s:.0f} tokens/s")
+    eager_ms = dt / args.steps * 1e3
+    log(f"eager step {eager_ms:.3f} ms, {cfg['T'] * args.steps / dt:.0f} tokens/s")
+    mode = "eager"
+    ms, tok_s = eager_ms, cfg["T"] * args.steps / dt
+    if not args.eager:
+        # The same step (forward + backward, every kernel) captured once in a HIP graph and replayed: this removes
+        # the host-side launch gaps between the ~40 kernels of a step. Capture on a side stream of default priority
+        # after a few warm-up steps there (allocator pools settle), as torch.cuda.graph expects.
+        gs = torch.cuda.Stream()
+        gs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(gs):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(gs)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        mode = "hip_graph"
+        ms, tok_s = dt / args.steps * 1e3, cfg["T"] * args.steps / dt
+        log(f"graph step {ms:.3f} ms, {tok_s:.0f} tokens/s")
     # per-launch timing of every entry point (events on the launching stream), a few extra steps
     n_prof = max(5, min(20, args.steps))
     with _lib.timing() as tm:
@@ -173,7 +199,8 @@ def main():
            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights ~N(0,0.02), x ~N(0,1))",
            "config": {"workload": "C3: Qwen3.6-35B-A3B MoE layer fwd+bwd, T=4092, H=2048, E=256, I=512, top-8, "
                                   "244 int4 g64 frozen + 12 bf16 LoRA r16 experts, shared 512 + LoRA r16",
-                      "tokens": cfg["T"], "selected_slots": S, "parallelism": "single GPU"},
+                      "tokens": cfg["T"], "selected_slots": S, "parallelism": "single GPU", "launch": mode},
+           "eager_ms_per_step": round(eager_ms, 4),
            "roofline": roof,
            "gemm_tflops_all": round(total_f / (sum(gemms.values()) * 1e-3) / 1e12, 2),
            "breakdown_ms": breakdown}

@@ -80,10 +80,14 @@ int smel_pack_bf16(const uint16_t* w, int64_t rows, int64_t K, int64_t ld, uint1
 /* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
  * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the
  * bf16-rounded logits), topv [T][K] bf16 (renormalised), topi [T][K] int64 and topi32 [T][K] int32 (descending,
- * lower expert id first among equal logits), and, if shared_gate_w, sgate [T] fp32 = sigmoid(bf16(x . w_sg)). */
+ * lower expert id first among equal logits), and, if shared_gate_w, sgate [T] fp32 = sigmoid(bf16(x . w_sg)).
+ * logits [T][smel_route_ld(E, shared_gate_w != NULL)] bf16 is the caller's workspace; it is left holding the
+ * bf16 logits (expert e in column e, the shared-gate logit in column ceil32(E)). */
 int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T, int64_t H,
                int64_t E, int64_t K, float* probs, uint16_t* topv, int64_t* topi, int32_t* topi32, float* sgate,
-               hipStream_t stream);
+               uint16_t* logits, hipStream_t stream);
+/* Row stride (elements) of smel_route's logits workspace (host-side, no GPU call); -1 for E <= 0. */
+int64_t smel_route_ld(int64_t E, int32_t with_shared_gate);
 
 /* Same selection from given bf16 logits [T][E] (bit-exact id checks against the CPU oracle). */
 int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, int64_t K, float* probs, uint16_t* topv,

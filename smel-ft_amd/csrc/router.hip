@@ -6,9 +6,7 @@
 
 namespace {
 
-constexpr int TB = 32;         // tokens per block (one 32-row MFMA slice)
-constexpr int MAXE = 256;      // experts handled by one block
-constexpr int LG_STRIDE = MAXE + 33;
+constexpr int MAXE = 256;      // experts handled by the selection (4 logits per lane)
 
 // Selection over one token's logits (held in LDS or global), by one wave. Writes probs, topv, topi, topi32.
 template <typename Get>
@@ -82,104 +80,113 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
   }
 }
 
-// One block = 32 tokens, 8 waves: wave w computes expert columns of fragments (w&3), (w&3)+4, (w&3)+8 (32 columns
-// each; the column E is the shared-expert gate when sg != nullptr) over the even (w < 4) or odd (w >= 4) 64-wide
-// k-steps; the two halves are added (odd into even, fixed order) through LDS. H % 64 == 0.
-__global__ __launch_bounds__(512) void route_fwd(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gw,
-                                                 const uint16_t* __restrict__ sg, int T, int H, int E, int K,
-                                                 float* __restrict__ probs, uint16_t* __restrict__ topv,
-                                                 int64_t* __restrict__ topi, int32_t* __restrict__ topi32,
-                                                 float* __restrict__ sgate) {
-  __shared__ float lg[TB * LG_STRIDE];
-  const int l = lane_id(), wv = threadIdx.x >> 6, w = wv & 3, kh = wv >> 2, hi = l >> 5, r32 = l & 31;
-  const int t0 = blockIdx.x * TB;
-  const int ncol = E + (sg ? 1 : 0);
-  const int nfrag = (ncol + 31) / 32;
-  f32x16_t acc[3];
-  uint32_t boff[3];
+// ---- logits GEMM: logits[t][c] = bf16(x[t] . w_c) for c < E (w_c = gate row c), at c = E32 = ceil32(E) the
+// shared-gate logit x[t] . w_sg (when sg), other columns 0. Block = 32 tokens x 64 columns (two 32-column MFMA
+// fragments); its 4 waves take the 64-wide k-steps j = w, w + 4, ... and add their partial sums through LDS in wave
+// order (fixed, so the result does not depend on timing). Grid = ceil(T / 32) x ceil(ldl / 64).
+constexpr int RT = 32;
+constexpr int RC = 64;
+constexpr int RW = 4;
+
+__global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ gw,
+                                                           const uint16_t* __restrict__ sg, int T, int H, int E,
+                                                           int ldl, uint16_t* __restrict__ logits) {
+  __shared__ float red[RW * RT * (RC + 4)];
+  const int l = lane_id(), hi = l >> 5, r32 = l & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t0 = blockIdx.x * RT, c0 = blockIdx.y * RC;
+  const int E32 = (E + 31) / 32 * 32;
+  // the two B fragments: expert rows, or the shared-gate row (its lane r32 = 0 only), or nothing
+  rsrc_t rb[2];
+  uint32_t boff[2];
+  bool fv[2];
   const rsrc_t rg = make_rsrc(gw, (uint64_t)E * H * 2);
-  const rsrc_t rsg = make_rsrc(sg, sg ? (uint64_t)H * 2 : 0);
-  bool bsg[3];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    acc[i] = f32x16_t{};
-    const int f = w + 4 * i;
-    const int e = 32 * f + r32;
-    bsg[i] = f < nfrag && e == E && sg;
-    boff[i] = (f < nfrag && e < E) ? (uint32_t)e * H * 2 : (bsg[i] ? 0u : OOB);
+  for (int f = 0; f < 2; ++f) {
+    const int cf = c0 + 32 * f;   // first column of the fragment (uniform)
+    const int c = cf + r32;
+    if (cf < E32) {
+      rb[f] = rg;
+      fv[f] = true;
+      boff[f] = c < E ? (uint32_t)c * H * 2 : OOB;
+    } else if (sg && cf == E32) {
+      rb[f] = make_rsrc(sg, (uint64_t)H * 2);
+      fv[f] = true;
+      boff[f] = r32 == 0 ? 0u : OOB;
+    } else {
+      rb[f] = rg;
+      fv[f] = false;
+      boff[f] = OOB;
+    }
   }
-  const int t = t0 + r32;
   const rsrc_t rx = make_rsrc(x, (uint64_t)T * H * 2);
-  const uint32_t aoff = t < T ? (uint32_t)t * H * 2 : OOB;
-  // loads of step k0 + 128 are in flight while step k0 multiplies
-  u32x4_t a[4], b[3][4], an[4], bn[3][4];
-  auto load = [&](int k0, u32x4_t* av, u32x4_t (*bv)[4]) {
-    const uint32_t ko = (uint32_t)(k0 + 32 * hi) * 2;
-    const bool ok = k0 < H;
+  const uint32_t aoff = t0 + r32 < T ? (uint32_t)(t0 + r32) * H * 2 : OOB;
+  const int nk = H / 64;
+  f32x16_t acc[2] = {f32x16_t{}, f32x16_t{}};
+  u32x4_t a0[4], b0[2][4], a1[4], b1[2][4];
+  auto load = [&](int j, u32x4_t* a, u32x4_t (*b)[4]) {
+    const bool ok = j < nk;
+    const uint32_t k2 = (uint32_t)(j * 64 + 32 * hi) * 2;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) av[s] = ld16(rx, ok ? aoff + ko + 16 * s : OOB);
+    for (int s = 0; s < 4; ++s) a[s] = ld16(rx, ok ? aoff + k2 + 16 * s : OOB);
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
+    for (int f = 0; f < 2; ++f)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) bv[i][s] = ld16(bsg[i] ? rsg : rg, ok ? boff[i] + ko + 16 * s : OOB);
+      for (int s = 0; s < 4; ++s) b[f][s] = ld16(rb[f], ok ? boff[f] + k2 + 16 * s : OOB);
   };
-  load(64 * kh, a, b);
-  for (int k0 = 64 * kh; k0 < H; k0 += 128) {
-    load(k0 + 128, an, bn);
+  auto mma = [&](const u32x4_t* a, u32x4_t (*b)[4]) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      if (w + 4 * i >= nfrag) continue;   // wave-uniform
+    for (int f = 0; f < 2; ++f) {
+      if (!fv[f]) continue;   // uniform
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc[i] = mfma32(a[s], b[i][s], acc[i]);
+      for (int s = 0; s < 4; ++s) acc[f] = mfma32(a[s], b[f][s], acc[f]);
     }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      a[s] = an[s];
-#pragma unroll
-      for (int i = 0; i < 3; ++i) b[i][s] = bn[i][s];
-    }
+  };
+  load(w, a0, b0);
+  for (int j = w; j < nk; j += 2 * RW) {
+    load(j + RW, a1, b1);
+    mma(a0, b0);
+    load(j + 2 * RW, a0, b0);
+    mma(a1, b1);
   }
-  // odd-step partial sums -> LDS, then the even-step waves add them and round the logits to bf16
-  if (kh == 1) {
+  float* mine = red + w * RT * (RC + 4);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int f = w + 4 * i;
-      if (f >= nfrag) continue;
+  for (int f = 0; f < 2; ++f)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) lg[acc_row(r, l) * LG_STRIDE + 32 * f + r32] = acc[i][r];
-    }
-  }
+    for (int r = 0; r < 16; ++r) mine[acc_row(r, l) * (RC + 4) + 32 * f + r32] = acc[f][r];
   __syncthreads();
-  if (kh == 0) {
+  // thread -> (row, 8 columns): sum the 4 partials in wave order, round to bf16, one 16-B store
+  const int row = threadIdx.x >> 3, col = 8 * (threadIdx.x & 7);
+  const int t = t0 + row, c = c0 + col;
+  if (t >= T || c >= ldl) return;
+  uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int f = w + 4 * i;
-      if (f >= nfrag) continue;
+  for (int i = 0; i < 4; ++i) {
+    float v[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float* p = lg + acc_row(r, l) * LG_STRIDE + 32 * f + r32;
-        *p = bf2f(f2bf(acc[i][r] + *p));
-      }
+    for (int h = 0; h < 2; ++h) {
+      const int cc = col + 2 * i + h;
+      float sum = red[row * (RC + 4) + cc];
+#pragma unroll
+      for (int ww = 1; ww < RW; ++ww) sum += red[ww * RT * (RC + 4) + row * (RC + 4) + cc];
+      v[h] = sum;
     }
+    o[i] = pack2bf(v[0], v[1]);
   }
-  __syncthreads();
-  for (int j = 0; j < TB / 8; ++j) {
-    const int row = wv * (TB / 8) + j;
-    const int64_t tt = t0 + row;
-    if (tt >= T) break;
-    const float* lrow = lg + row * LG_STRIDE;
-    select_topk([&](int e) { return lrow[e]; }, E, K, tt, probs, topv, topi, topi32);
-    if (sg && l == 0) sgate[tt] = 1.0f / (1.0f + expf(-lrow[E]));
-  }
+  *reinterpret_cast<u32x4_t*>(logits + (int64_t)t * ldl + c) = u32x4_t{o[0], o[1], o[2], o[3]};
 }
 
-__global__ __launch_bounds__(256) void route_from_logits(const uint16_t* __restrict__ logits, int T, int E, int K,
-                                                         float* __restrict__ probs, uint16_t* __restrict__ topv,
-                                                         int64_t* __restrict__ topi, int32_t* __restrict__ topi32) {
+// ---- selection: one wave per token over its bf16 logits row (probs, top-k, renorm; shared-gate sigmoid).
+__global__ __launch_bounds__(256) void route_select(const uint16_t* __restrict__ logits, int ldl, int T, int E, int K,
+                                                    int sg_col, float* __restrict__ probs,
+                                                    uint16_t* __restrict__ topv, int64_t* __restrict__ topi,
+                                                    int32_t* __restrict__ topi32, float* __restrict__ sgate) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const uint16_t* row = logits + t * E;
+  const uint16_t* row = logits + t * ldl;
   select_topk([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topi, topi32);
+  if (sgate && lane_id() == 0) sgate[t] = 1.0f / (1.0f + expf(-bf2f(row[sg_col])));
 }
 
 // Backward of route (+ shared gate): one wave per token.
@@ -265,18 +272,27 @@ extern "C" int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, in
   return smel::launch_status();
 }
 
+extern "C" int64_t smel_route_ld(int64_t E, int32_t with_shared_gate) {
+  return E <= 0 ? -1 : (E + 31) / 32 * 32 + (with_shared_gate ? 32 : 0);
+}
+
 extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T,
                           int64_t H, int64_t E, int64_t K, float* probs, uint16_t* topv, int64_t* topi,
-                          int32_t* topi32, float* sgate, hipStream_t stream) {
+                          int32_t* topi32, float* sgate, uint16_t* logits, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && H > 0 && E > 0 && K > 0, SMEL_EINVAL, "route: bad sizes");
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "route: E=%lld > %d experts", (long long)E, MAXE);
   SMEL_REQUIRE(K <= E && K <= 16, SMEL_EUNSUPPORTED, "route: top_k=%lld must be <= min(E, 16)", (long long)K);
   SMEL_REQUIRE(H % 64 == 0, SMEL_EUNSUPPORTED, "route: hidden %lld must be a multiple of 64", (long long)H);
   SMEL_REQUIRE(!shared_gate_w || sgate, SMEL_EINVAL, "route: sgate output needed with shared_gate_w");
+  SMEL_REQUIRE(T * H * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "route: x larger than 2 GiB");
   if (T == 0) return 0;
-  SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32, SMEL_EINVAL, "route: null pointer");
-  route_fwd<<<(unsigned)((T + TB - 1) / TB), 512, 0, stream>>>(x, gate_w, shared_gate_w, (int)T, (int)H, (int)E,
-                                                                 (int)K, probs, topv, topi, topi32, sgate);
+  SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32 && logits, SMEL_EINVAL, "route: null pointer");
+  const int64_t ldl = smel_route_ld(E, shared_gate_w != nullptr);
+  const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
+  route_logits_kernel<<<grid, 256, 0, stream>>>(x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
+  route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K,
+                                                            (int)((E + 31) / 32 * 32), probs, topv, topi, topi32,
+                                                            shared_gate_w ? sgate : nullptr);
   return smel::launch_status();
 }
 
@@ -288,8 +304,8 @@ extern "C" int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, i
                (long long)K);
   if (T == 0) return 0;
   SMEL_REQUIRE(logits && probs && topv && topi && topi32, SMEL_EINVAL, "route_logits: null pointer");
-  route_from_logits<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)T, (int)E, (int)K, probs, topv, topi,
-                                                                  topi32);
+  route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)E, (int)T, (int)E, (int)K, 0, probs, topv,
+                                                            topi, topi32, nullptr);
   return smel::launch_status();
 }
 

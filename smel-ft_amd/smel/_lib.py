@@ -34,7 +34,8 @@ SIGNATURES = {
     "smel_packed_bytes": (i64, [i32, i64, i64]),
     "smel_pack_int4": (i32, [vp, vp, vp, i64, i64, i64, vp, vp, vp]),
     "smel_pack_bf16": (i32, [vp, i64, i64, i64, vp, vp]),
-    "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp]),
+    "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_route_ld": (i64, [i64, i32]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
     "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),

@@ -314,8 +314,9 @@ class _RouteFn(torch.autograd.Function):
         topv = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
         topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
         topi32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+        lg = torch.empty(T, L.load().smel_route_ld(E, 0), dtype=torch.bfloat16, device=dev)
         L.call("smel_route", L.ptr(x), L.ptr(gate_w), None, T, H, E, top_k, L.ptr(probs), L.ptr(topv), L.ptr(topi),
-               L.ptr(topi32), None, L.stream())
+               L.ptr(topi32), None, L.ptr(lg), L.stream())
         ctx.save_for_backward(probs, topi32, gate_w)
         ctx.mark_non_differentiable(probs, topi)
         return probs, topv, topi
@@ -378,10 +379,16 @@ class _Ctx:
 
 
 def _lora_groups(ex: LayerExperts, with_shared: bool, n_sel_lora: int, device):
-    ids = [int(e) for e in ex.sel_ids.tolist()][:n_sel_lora] if (ex.sel_ids is not None and n_sel_lora) else []
-    if with_shared:
-        ids.append(ex.E)
-    return torch.tensor(ids, dtype=torch.int32, device=device)
+    """Group ids that carry LoRA (selected experts, then the shared expert as group E), cached on the layer so that
+    a step makes no host-to-device copy (and can be captured in a HIP graph)."""
+    cache = ex.__dict__.setdefault("_lora_groups", {})
+    key = (with_shared, n_sel_lora, str(device))
+    if key not in cache:
+        ids = [int(e) for e in ex.sel_ids.tolist()][:n_sel_lora] if (ex.sel_ids is not None and n_sel_lora) else []
+        if with_shared:
+            ids.append(ex.E)
+        cache[key] = torch.tensor(ids, dtype=torch.int32, device=device)
+    return cache[key]
 
 
 def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
@@ -573,8 +580,9 @@ class _MoELayerFn(torch.autograd.Function):
         topi32 = torch.empty(T, K, dtype=torch.int32, device=dev)
         sgate = torch.empty(T, dtype=torch.float32, device=dev) if fuse else None
         sgw = plan["shared"][2] if fuse else None
+        lg = torch.empty(T, L.load().smel_route_ld(E, int(fuse)), dtype=torch.bfloat16, device=dev)
         L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
-               L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.stream())
+               L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.stream())
         if stats is not None:
             stats(probs, topv, topi)
         c = _Ctx()

@@ -171,10 +171,21 @@ def test_route_fused(T, H, E, K, shared):
     topi32 = torch.empty(T, K, dtype=torch.int32, device=DEV)
     sgate = torch.empty(T, dtype=torch.float32, device=DEV)
     xd, gwd, sgd = x.to(DEV), gw.to(DEV), sg.to(DEV)
+    ldl = L.load().smel_route_ld(E, int(shared))
+    lgw = torch.full((T, ldl), float("nan"), dtype=torch.bfloat16, device=DEV)
     L.call("smel_route", L.ptr(xd), L.ptr(gwd), L.ptr(sgd) if shared else None, T, H, E, K, L.ptr(probs),
-           L.ptr(topv), L.ptr(topi), L.ptr(topi32), L.ptr(sgate) if shared else None, L.stream())
+           L.ptr(topv), L.ptr(topi), L.ptr(topi32), L.ptr(sgate) if shared else None, L.ptr(lgw), L.stream())
     logits = (x.double() @ gw.double().t())                   # exact dot products of the bf16 inputs
     lb = logits.float().to(torch.bfloat16).float()
+    # the workspace holds the kernel's bf16 logits: close to the exact ones, and the selection on them is exact
+    glog = lgw.float().cpu()
+    assert torch.allclose(glog[:, :E].double(), logits, rtol=1e-2, atol=2e-3)
+    _, sel_i = intref.topk(glog[:, :E].numpy(), K)
+    assert np.array_equal(topi.cpu().numpy(), sel_i)
+    assert torch.equal(topi32.cpu().long(), topi.cpu())
+    if shared:
+        e32 = (E + 31) // 32 * 32
+        assert torch.allclose(glog[:, e32].double(), x.double() @ sg.double(), rtol=1e-2, atol=2e-3)
     _, want_i = intref.topk(lb.numpy(), K)
     got = topi.cpu().numpy()
     bad = np.where((got != want_i).any(1))[0]
