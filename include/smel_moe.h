@@ -97,11 +97,14 @@ int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, int64_t K, f
  * ids [T*K] (int32 if ids_are_i64 == 0, else int64) -> counts [E], offsets [E+1], order [TK] (stable: experts
  * ascending, slot p ascending within one), inv [TK], and the GEMM tile list: tiles [max_tiles][4] = {group, row0,
  * row1, 0} over groups 0..E-1 (+ group E = shared rows [TK, TK+shared_rows) when shared_rows > 0), m_tile rows
- * each; n_tiles [1] = how many are used. err [1] is set to 1 if an id is outside [0, E) (that slot is dropped).
- * One workgroup; E <= 1024. */
+ * each; n_tiles [1] = how many are used. err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
+ * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
+ * workspace. E <= 512. */
 int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                   int32_t m_tile, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
-                  int32_t* n_tiles, int32_t* err, hipStream_t stream);
+                  int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream);
+/* int32 elements of smel_dispatch's workspace (host-side, no GPU call); -1 for bad sizes. */
+int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
 /* Upper bound of the tile-list length for smel_dispatch (host-side, no GPU call). */
 int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared_rows, int32_t m_tile);
 

@@ -2,16 +2,17 @@
 // smel/moe.py:216-223, and the inverse permutation of :249-250), plus the GEMM tile list. No host sync: counts and
 // offsets stay on the device and the grouped GEMMs read the tile list.
 //
-// One workgroup of 1024 threads (16 waves). Wave w owns the contiguous slot range [w*C, (w+1)*C). Pass 1 counts per
-// (wave, expert) in LDS; a scan over waves and experts gives each (wave, expert) its first output position; pass 2
-// walks the wave's range 64 slots at a time and ranks equal ids inside the step with ballots (a wave-level
-// multisplit), so slot order inside an expert is ascending p — exactly the stable sort.
+// Three launches over blocks of 1024 slots (one per thread): (1) per-block expert histograms; (2) one block turns
+// them into counts, offsets, each block's first output position per expert, and the tile list; (3) every block
+// ranks its slots again — inside a wave by ballots over the id bits (a wave-level multisplit), across its 16 waves
+// by a per-expert prefix — and scatters order / inv. Slots of one expert thus keep ascending p: the stable sort.
 #include "abi_util.h"
 #include "common.h"
 
 namespace {
 
-constexpr int NW = 16;        // waves
+constexpr int NW = 16;        // waves per block
+constexpr int DB = NW * 64;   // slots per block
 constexpr int MAXE = 512;
 
 SMEL_DEV int block_exclusive_scan(int v, int* wsum /* [NW] LDS */, int& total) {
@@ -35,82 +36,66 @@ SMEL_DEV int block_exclusive_scan(int v, int* wsum /* [NW] LDS */, int& total) {
   return base + inc - v;
 }
 
-__global__ __launch_bounds__(1024) void dispatch_kernel(const void* __restrict__ ids, int is64, int TK, int E,
-                                                        int shared_rows, int m_tile, int max_tiles,
-                                                        int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                        int32_t* __restrict__ order, int32_t* __restrict__ inv,
-                                                        int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles,
-                                                        int32_t* __restrict__ err) {
-  __shared__ int hist[NW * MAXE];   // per-wave counts, then per-wave write cursors
-  __shared__ int off_s[MAXE + 1];
-  __shared__ int wsum[NW];
-  __shared__ int bad;
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6;
-  auto id_at = [&](int p) -> int {
-    return is64 ? (int)static_cast<const int64_t*>(ids)[p] : static_cast<const int32_t*>(ids)[p];
-  };
-  for (int i = tid; i < NW * E; i += 1024) hist[i] = 0;
-  if (tid == 0) bad = 0;
+SMEL_DEV int id_at(const void* ids, int is64, int p) {
+  return is64 ? (int)static_cast<const int64_t*>(ids)[p] : static_cast<const int32_t*>(ids)[p];
+}
+
+// (1) hist[b][e] = slots of block b routed to expert e; bad[b] = 1 if block b holds an id outside [0, E)
+__global__ __launch_bounds__(1024) void dispatch_hist(const void* __restrict__ ids, int is64, int TK, int E,
+                                                      int32_t* __restrict__ hist, int32_t* __restrict__ bad) {
+  __shared__ int h[MAXE];
+  __shared__ int bad_s;
+  const int tid = threadIdx.x, b = blockIdx.x;
+  for (int e = tid; e < E; e += DB) h[e] = 0;
+  if (tid == 0) bad_s = 0;
   __syncthreads();
-  const int chunk = (TK + NW - 1) / NW;
-  const int p0 = min(TK, w * chunk), p1 = min(TK, p0 + chunk);
-  for (int p = p0 + l; p < p1; p += 64) {
-    const int e = id_at(p);
+  const int p = b * DB + tid;
+  if (p < TK) {
+    const int e = id_at(ids, is64, p);
     if (e >= 0 && e < E)
-      atomicAdd(&hist[w * E + e], 1);
+      atomicAdd(&h[e], 1);   // LDS counter: the total does not depend on the order
     else
-      bad = 1;
+      bad_s = 1;
   }
   __syncthreads();
-  // per expert: exclusive prefix over waves (in place), total count
-  int my_total = 0;
-  for (int e = tid; e < E; e += 1024) {
-    int run = 0;
-    for (int j = 0; j < NW; ++j) {
-      const int c = hist[j * E + e];
-      hist[j * E + e] = run;
-      run += c;
-    }
-    my_total = run;   // E <= 1024: one expert per thread
-  }
+  for (int e = tid; e < E; e += DB) hist[b * E + e] = h[e];
+  if (tid == 0) bad[b] = bad_s;
+}
+
+// (2) one block: counts, offsets, hist -> base[b][e] (first output position of block b's slots of expert e), tiles
+__global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int shared_rows, int m_tile,
+                                                      int max_tiles, int32_t* __restrict__ hist,
+                                                      const int32_t* __restrict__ bad, int32_t* __restrict__ counts,
+                                                      int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
+                                                      int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
+  __shared__ int wsum[NW];
+  __shared__ int off_s[MAXE + 1];
+  __shared__ int bad_s;
+  const int tid = threadIdx.x;
+  if (tid == 0) bad_s = 0;
+  int total = 0;
+  if (tid < E)
+    for (int b = 0; b < nb; ++b) total += hist[b * E + tid];
   int total_rows;
-  const int ex = block_exclusive_scan(tid < E ? my_total : 0, wsum, total_rows);
+  const int ex = block_exclusive_scan(tid < E ? total : 0, wsum, total_rows);
   if (tid < E) {
     off_s[tid] = ex;
-    counts[tid] = my_total;
+    counts[tid] = total;
     offsets[tid] = ex;
+    int run = ex;
+    for (int b = 0; b < nb; ++b) {
+      const int c = hist[b * E + tid];
+      hist[b * E + tid] = run;
+      run += c;
+    }
   }
   if (tid == 0) {
     off_s[E] = total_rows;
     offsets[E] = total_rows;
   }
+  for (int b = tid; b < nb; b += DB)
+    if (bad[b]) bad_s = 1;
   __syncthreads();
-  for (int i = tid; i < NW * E; i += 1024) hist[i] += off_s[i % E];
-  __syncthreads();
-  // pass 2: stable ranking inside 64-slot steps
-  int nbits = 1;
-  while ((1 << nbits) < E) ++nbits;
-  for (int base = p0; base < p1; base += 64) {
-    const int p = base + l;
-    int e = p < p1 ? id_at(p) : -1;
-    const bool ok = e >= 0 && e < E;
-    uint64_t m = __ballot(ok);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = ok && ((e >> b) & 1);
-      const uint64_t bb = __ballot(bit);
-      m &= bit ? bb : ~bb;
-    }
-    if (ok) {
-      const uint64_t lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
-      const int rank = __popcll(m & lt);
-      const int pos = hist[w * E + e] + rank;
-      order[pos] = p;
-      inv[p] = pos;
-      if ((m >> l) == 1ull) hist[w * E + e] += __popcll(m);   // highest lane of the group advances the cursor
-    } else if (p < p1) {
-      inv[p] = -1;
-    }
-  }
   // tile list over groups 0..E-1 (+ shared group E)
   const int G = E + (shared_rows > 0 ? 1 : 0);
   int nt = 0, rows = 0, row0 = 0;
@@ -133,7 +118,48 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const void* __restrict__
   }
   if (tid == 0) {
     n_tiles[0] = min(total_tiles, max_tiles);
-    err[0] = bad | (total_tiles > max_tiles ? 2 : 0);
+    err[0] = bad_s | (total_tiles > max_tiles ? 2 : 0);
+  }
+}
+
+// (3) stable scatter of block b's slots: order[pos] = p, inv[p] = pos (-1 for an id outside [0, E))
+__global__ __launch_bounds__(1024) void dispatch_scatter(const void* __restrict__ ids, int is64, int TK, int E,
+                                                         const int32_t* __restrict__ base,
+                                                         int32_t* __restrict__ order, int32_t* __restrict__ inv) {
+  __shared__ int cnt[NW * MAXE];   // per-wave counts, then per-wave first positions
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, b = blockIdx.x;
+  for (int i = tid; i < NW * E; i += DB) cnt[i] = 0;
+  __syncthreads();
+  const int p = b * DB + tid;
+  const int e = p < TK ? id_at(ids, is64, p) : -1;
+  const bool ok = e >= 0 && e < E;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  uint64_t m = __ballot(ok);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool v = ok && ((e >> bit) & 1);
+    const uint64_t bb = __ballot(v);
+    m &= v ? bb : ~bb;
+  }
+  const uint64_t lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  const int rank = ok ? __popcll(m & lt) : 0;
+  if (ok && (m >> l) == 1ull) cnt[w * E + e] = __popcll(m);   // the group's highest lane records its size
+  __syncthreads();
+  for (int x = tid; x < E; x += DB) {
+    int run = base[b * E + x];
+    for (int j = 0; j < NW; ++j) {
+      const int c = cnt[j * E + x];
+      cnt[j * E + x] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (ok) {
+    const int pos = cnt[w * E + e] + rank;
+    order[pos] = p;
+    inv[p] = pos;
+  } else if (p < TK) {
+    inv[p] = -1;
   }
 }
 
@@ -144,16 +170,37 @@ extern "C" int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared
   return (TK + m_tile - 1) / m_tile + E + (shared_rows + m_tile - 1) / m_tile + 1;
 }
 
+extern "C" int64_t smel_dispatch_ws_size(int64_t TK, int64_t E) {
+  if (TK < 0 || E <= 0) return -1;
+  const int64_t nb = (TK + DB - 1) / DB;
+  return nb * E + nb;
+}
+
 extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
                              int64_t shared_rows, int32_t m_tile, int32_t* counts, int32_t* offsets, int32_t* order,
-                             int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, hipStream_t stream) {
+                             int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, int32_t* ws,
+                             hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && shared_rows >= 0 && m_tile > 0, SMEL_EINVAL, "dispatch: bad sizes");
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "dispatch: E=%lld > %d experts", (long long)E, MAXE);
   SMEL_REQUIRE(T * K < (1ll << 30), SMEL_EUNSUPPORTED, "dispatch: T*K too large");
-  SMEL_REQUIRE(counts && offsets && tiles && n_tiles && err && (T == 0 || (ids && order && inv)), SMEL_EINVAL,
+  SMEL_REQUIRE(counts && offsets && tiles && n_tiles && err && (T == 0 || (ids && order && inv && ws)), SMEL_EINVAL,
                "dispatch: null pointer");
-  const int64_t mt = smel_dispatch_max_tiles(T * K, E, shared_rows, m_tile);
-  dispatch_kernel<<<1, 1024, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)(T * K), (int)E, (int)shared_rows, m_tile,
-                                          (int)mt, counts, offsets, order, inv, tiles, n_tiles, err);
+  const int64_t TK = T * K;
+  const int64_t mt = smel_dispatch_max_tiles(TK, E, shared_rows, m_tile);
+  const int nb = (int)((TK + DB - 1) / DB);
+  int32_t* hist = ws;
+  int32_t* bad = ws ? ws + (int64_t)nb * E : nullptr;
+  if (nb > 0) {
+    dispatch_hist<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)TK, (int)E, hist, bad);
+    const int st = smel::launch_status();
+    if (st) return st;
+  }
+  dispatch_scan<<<1, DB, 0, stream>>>(nb, (int)TK, (int)E, (int)shared_rows, m_tile, (int)mt, hist, bad, counts,
+                                      offsets, tiles, n_tiles, err);
+  if (nb > 0) {
+    const int st = smel::launch_status();
+    if (st) return st;
+    dispatch_scatter<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)TK, (int)E, hist, order, inv);
+  }
   return smel::launch_status();
 }

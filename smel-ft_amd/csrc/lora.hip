@@ -69,15 +69,19 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
 }
 
 // ext[row][0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles. Block = one 32-row
-// slice of a tile; its 4 waves take every 4th 64-wide k-step (loads of the next step in flight during the MFMAs) and
-// their partial sums are added in wave order through LDS.
-__global__ __launch_bounds__(256) void lora_ext_kernel(const int4* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
+// slice of a tile; its 8 waves take the 64-wide k-steps j = w, w + 8, ... issuing all loads of up to XPRE of their
+// steps before the MFMAs (one memory latency per XPRE steps, not one per step); the partial sums are added in wave
+// order through LDS.
+constexpr int XW = 8;
+constexpr int XPRE = 4;
+
+__global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
                                                        const int32_t* __restrict__ gkind, const uint16_t* __restrict__ A,
                                                        int64_t lda, int64_t a_rows, int a_gather,
                                                        const int32_t* __restrict__ order, int TK, int topk,
                                                        const uint16_t* __restrict__ wsel, const uint16_t* __restrict__ wsh,
                                                        int Kd, float ssel, float ssh, uint16_t* __restrict__ ext) {
-  __shared__ float red[4 * 64 * 16];
+  __shared__ float red[XW * 64 * 16];
   if ((int)blockIdx.x >= n_tiles[0]) return;
   const int4 t = tiles[blockIdx.x];
   const int gk = gkind[t.x];
@@ -99,36 +103,35 @@ __global__ __launch_bounds__(256) void lora_ext_kernel(const int4* __restrict__ 
     ao = (uint32_t)(a_gather ? row_token(grow, order, TK, topk) : grow) * (uint32_t)lda * 2;
   }
   const uint32_t bo = (uint32_t)r32 * Kd * 2;
+  const int nk = (Kd + 63) / 64;
   f32x16_t acc = f32x16_t{};
-  u32x4_t av[4], bv[4], an[4], bn[4];
-  auto load = [&](int k0, u32x4_t* x, u32x4_t* y) {
-    const int kk = k0 + 32 * hi;
-    const bool ok = k0 < Kd && kk + 32 <= Kd;
+  for (int j0 = w; j0 < nk; j0 += XW * XPRE) {
+    u32x4_t av[XPRE][4], bv[XPRE][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      x[s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
-      y[s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
+    for (int p = 0; p < XPRE; ++p) {
+      const int kk = (j0 + XW * p) * 64 + 32 * hi;
+      const bool ok = kk + 32 <= Kd;   // Kd % 32 == 0: a lane half's 32 k are all in or all out
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        av[p][s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
+        bv[p][s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
+      }
     }
-  };
-  int k0 = 64 * w;
-  load(k0, av, bv);
-  for (; k0 < Kd; k0 += 256) {
-    load(k0 + 256, an, bn);
+    __builtin_amdgcn_sched_barrier(0);   // every load of the batch is issued before the first MFMA waits
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc = mfma32(av[s], bv[s], acc);
+    for (int p = 0; p < XPRE; ++p)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      av[s] = an[s];
-      bv[s] = bn[s];
-    }
+      for (int s = 0; s < 4; ++s) acc = mfma32(av[p][s], bv[p][s], acc);
   }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) red[(w * 64 + l) * 16 + r] = acc[r];
+  for (int r = 0; r < 16; ++r) red[(w * 16 + r) * 64 + l] = acc[r];   // lane-contiguous: no bank conflicts
   __syncthreads();
   if (w == 0) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float v = ((red[l * 16 + r] + red[(64 + l) * 16 + r]) + red[(128 + l) * 16 + r]) + red[(192 + l) * 16 + r];
+      float v = red[r * 64 + l];
+#pragma unroll
+      for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
       const int orow = m * 32 + acc_row(r, l);
       if (orow < nrows) ext[(int64_t)(t.y + orow) * 32 + r32] = f2bf(scale * v);
     }
@@ -138,8 +141,10 @@ __global__ __launch_bounds__(256) void lora_ext_kernel(const int4* __restrict__ 
 // part[i][c][p][q] = sum over rows c*CH .. c*CH+CH-1 of group lora_groups[i]: alpha(row) L[row][p] Rm[src(row)][q],
 // as an MFMA GEMM with the row index as the contraction dim: per 64-row step, L and Rm are staged transposed in LDS
 // (k-pair packing: the values of rows 2j and 2j+1 share one 32-bit word), then each wave multiplies the 32 x 64 L^T
-// tile by its 64 x 32 slice of the Rm tile. Block = 4 waves = 32 p x 128 q.
-constexpr int WG_CH = 1024;   // rows per chunk
+// tile by its 64 x 32 slice of the Rm tile. Block = 4 waves = 32 p x 128 q. The LDS tiles are double-buffered and
+// the raw rows of step j+1 are loaded into registers before step j's MFMAs, so one barrier per step suffices and a
+// load's latency overlaps a step of work.
+constexpr int WG_CH = 256;    // rows per chunk
 constexpr int WG_QB = 128;    // columns per block
 constexpr int WG_S = 64 + 8;  // LDS row stride (bf16)
 
@@ -149,8 +154,8 @@ __global__ __launch_bounds__(256) void lora_wgrad_part(const int32_t* __restrict
                                                        int64_t ldr, int64_t r_rows, int r_gather, int use_w,
                                                        const uint16_t* __restrict__ topv, const float* __restrict__ sgate,
                                                        int Q, float* __restrict__ part, int chunks) {
-  __shared__ __attribute__((aligned(16))) uint16_t LT[32 * WG_S];
-  __shared__ __attribute__((aligned(16))) uint16_t RT[WG_QB * WG_S];
+  __shared__ __attribute__((aligned(16))) uint16_t LT[2][32 * WG_S];
+  __shared__ __attribute__((aligned(16))) uint16_t RT[2][WG_QB * WG_S];
   const int i = blockIdx.x, c = blockIdx.z;
   const int g = groups[i];
   const int r0 = g < E ? offsets[g] : TK;
@@ -161,8 +166,14 @@ __global__ __launch_bounds__(256) void lora_wgrad_part(const int32_t* __restrict
   const int q0 = blockIdx.y * WG_QB;
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
   const int kp = tid & 31, grp = tid >> 5;   // k pair, and 4 p's (L) / 16 q's (Rm) per thread
+  const int qq = q0 + 16 * grp;
+  const bool qok = qq < Q;
   const rsrc_t rr = make_rsrc(Rm, (uint64_t)r_rows * ldr * 2);
   f32x16_t acc = f32x16_t{};
+  // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights
+  uint2 lv0, lv1;
+  u32x4_t x0[2], x1[2];
+  float al0, al1;
   auto row_info = [&](int row, uint32_t& roff, float& alpha) {
     roff = OOB;
     alpha = 0.f;
@@ -180,50 +191,48 @@ __global__ __launch_bounds__(256) void lora_wgrad_part(const int32_t* __restrict
       roff = (uint32_t)src * (uint32_t)ldr * 2;
     }
   };
-  for (int k0 = a0; k0 < a1; k0 += 64) {
+  auto load = [&](int k0) {
     const int ra = k0 + 2 * kp;
     uint32_t o0, o1;
-    float al0, al1;
     row_info(ra, o0, al0);
     row_info(ra + 1, o1, al1);
-    // L^T: rows ra, ra+1, p = 4*grp .. 4*grp+3 (alpha folded in, fp32 then one bf16 rounding)
-    {
-      const uint2 v0 = ra < a1 ? *reinterpret_cast<const uint2*>(L + (int64_t)ra * 32 + 4 * grp) : make_uint2(0, 0);
-      const uint2 v1 = ra + 1 < a1 ? *reinterpret_cast<const uint2*>(L + (int64_t)(ra + 1) * 32 + 4 * grp)
-                                   : make_uint2(0, 0);
-      uint32_t* d = reinterpret_cast<uint32_t*>(LT + (4 * grp) * WG_S + 2 * kp);
-      d[0 * (WG_S / 2)] = pack2bf(al0 * bf_lo(v0.x), al1 * bf_lo(v1.x));
-      d[1 * (WG_S / 2)] = pack2bf(al0 * bf_hi(v0.x), al1 * bf_hi(v1.x));
-      d[2 * (WG_S / 2)] = pack2bf(al0 * bf_lo(v0.y), al1 * bf_lo(v1.y));
-      d[3 * (WG_S / 2)] = pack2bf(al0 * bf_hi(v0.y), al1 * bf_hi(v1.y));
-    }
-    // Rm^T: rows ra, ra+1, q = q0 + 16*grp .. +15
-    {
-      const int qq = q0 + 16 * grp;
-      const bool qok = qq < Q;
-      u32x4_t x0[2], x1[2];
+    lv0 = ra < a1 ? *reinterpret_cast<const uint2*>(L + (int64_t)ra * 32 + 4 * grp) : make_uint2(0, 0);
+    lv1 = ra + 1 < a1 ? *reinterpret_cast<const uint2*>(L + (int64_t)(ra + 1) * 32 + 4 * grp) : make_uint2(0, 0);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
-        x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+    for (int h = 0; h < 2; ++h) {
+      x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+      x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+    }
+  };
+  auto stage = [&](int buf) {
+    // L^T: alpha folded in (fp32, one bf16 rounding)
+    uint32_t* d = reinterpret_cast<uint32_t*>(LT[buf] + (4 * grp) * WG_S + 2 * kp);
+    d[0 * (WG_S / 2)] = pack2bf(al0 * bf_lo(lv0.x), al1 * bf_lo(lv1.x));
+    d[1 * (WG_S / 2)] = pack2bf(al0 * bf_hi(lv0.x), al1 * bf_hi(lv1.x));
+    d[2 * (WG_S / 2)] = pack2bf(al0 * bf_lo(lv0.y), al1 * bf_lo(lv1.y));
+    d[3 * (WG_S / 2)] = pack2bf(al0 * bf_hi(lv0.y), al1 * bf_hi(lv1.y));
+    uint32_t* e = reinterpret_cast<uint32_t*>(RT[buf] + (16 * grp) * WG_S + 2 * kp);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[(8 * h + 2 * j) * (WG_S / 2)] = __builtin_amdgcn_perm(x1[h][j], x0[h][j], 0x05040100u);
+        e[(8 * h + 2 * j + 1) * (WG_S / 2)] = __builtin_amdgcn_perm(x1[h][j], x0[h][j], 0x07060302u);
       }
-      uint32_t* d = reinterpret_cast<uint32_t*>(RT + (16 * grp) * WG_S + 2 * kp);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          d[(8 * h + 2 * j) * (WG_S / 2)] = __builtin_amdgcn_perm(x1[h][j], x0[h][j], 0x05040100u);
-          d[(8 * h + 2 * j + 1) * (WG_S / 2)] = __builtin_amdgcn_perm(x1[h][j], x0[h][j], 0x07060302u);
-        }
-    }
+  };
+  load(a0);
+  int buf = 0;
+  for (int k0 = a0; k0 < a1; k0 += 64) {
+    stage(buf);
+    if (k0 + 64 < a1) load(k0 + 64);
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT + r32 * WG_S + 32 * hi + 8 * s);
-      const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
+      const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT[buf] + r32 * WG_S + 32 * hi + 8 * s);
+      const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT[buf] + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
       acc = mfma32(af, bfr, acc);
     }
-    __syncthreads();
+    buf ^= 1;
   }
   const int q = q0 + 32 * w + r32;
   if (q < Q) {
@@ -277,7 +286,7 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "lora_ext: A larger than 2 GiB");
   if (max_tiles == 0) return 0;
   dim3 grid((unsigned)max_tiles, 4);
-  lora_ext_kernel<<<grid, 256, 0, stream>>>(reinterpret_cast<const int4*>(tiles), n_tiles, gkind, A_src, lda, a_rows,
+  lora_ext_kernel<<<grid, 512, 0, stream>>>(reinterpret_cast<const int4*>(tiles), n_tiles, gkind, A_src, lda, a_rows,
                                             a_gather, order, (int)TK, (int)topk, wcat_sel, wcat_sh, (int)Kd, scale_sel,
                                             scale_sh, ext);
   return smel::launch_status();

@@ -37,7 +37,8 @@ SIGNATURES = {
     "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_ld": (i64, [i64, i32]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
-    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_dispatch_ws_size": (i64, [i64, i64]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
     "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),

@@ -405,8 +405,9 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
+    dws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
     L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(counts), L.ptr(offsets),
-           L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), st)
+           L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st)
     gk = ex.gkind(shared is not None, dev)
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):

@@ -41,6 +41,7 @@ def test_host_side_rejections():
     from smel import _lib
     L = _lib.load()
     assert L.smel_dispatch_max_tiles(32736, 256, 4092, 128) == (32736 + 127) // 128 + 256 + 32 + 1
+    assert L.smel_dispatch_ws_size(32736, 256) == 32 * 256 + 32 and L.smel_dispatch_ws_size(0, 8) == 0
     # route: too many experts
     rc = L.smel_route(1, 1, None, 4, 64, 300, 8, 1, 1, 1, 1, None, 1, None)
     assert rc == -2 and b"E=300" in L.smel_last_error()

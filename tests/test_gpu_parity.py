@@ -212,8 +212,9 @@ def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128):
     i32 = lambda n: torch.full((n,), -7, dtype=torch.int32, device=DEV)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
+    ws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))   # garbage-filled: the kernels must not rely on zeros
     L.call("smel_dispatch", L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, shared_rows, m_tile, L.ptr(counts),
-           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.stream())
+           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(ws), L.stream())
     return [a.cpu().numpy() for a in (counts, offsets, order, inv, tiles, ntiles, err)]
 
 
