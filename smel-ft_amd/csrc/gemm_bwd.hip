@@ -274,57 +274,98 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     }
   }
-  // ---- epilogue
+  // ---- epilogue through LDS (the ring is free: see the barrier above): the wave results go into a row-major tile,
+  // then each thread handles 8 columns of whole rows with 16-B accesses (one address per 8 outputs).
+  const int ech = tid & 15;                // 8-column chunk of the block's 128 columns
+  const int col0 = n0 + 8 * ech;
   if (EPI == 0) {
+    // bf16 tile [128][128]: rows 0..63 in S0, 64..127 in S1; 16-B chunk c of row r at c ^ (r & 7)
 #pragma unroll
     for (int m = 0; m < NSW; ++m) {
+      uint16_t* D = wr == 0 ? S0 : S1;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = 64 * wr + m * 32 + acc_row(r, l);
-        if (row >= nrows) continue;
-        const int64_t orow = (int64_t)row_slot(row0 + row, a.order, a.TK) * a.ldo;
-        if (fv0) a.out[orow + cw + r32] = f2bf(acc[m][0][r]);
-        if (fv1) a.out[orow + cw + 32 + r32] = f2bf(acc[m][1][r]);
+        const int lr = m * 32 + acc_row(r, l);   // row inside this wave's 64-row half
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const int col = 64 * wc + 32 * f + r32;
+          D[lr * 128 + 8 * ((col >> 3) ^ (lr & 7)) + (col & 7)] = f2bf(acc[m][f][r]);
+        }
+      }
+    }
+    __syncthreads();
+    if (col0 < a.N) {
+      for (int row = tid >> 4; row < nrows; row += 16) {
+        const int lr = row & 63;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((row < 64 ? S0 : S1) + lr * 128 + 8 * (ech ^ (lr & 7)));
+        const int64_t orow = row_slot(row0 + row, a.order, a.TK);
+        *reinterpret_cast<u32x4_t*>(a.out + orow * a.ldo + col0) = v;
       }
     }
     return;
   }
-  // down backward: columns n < I of dh = [dg | du]; per-row partial of sum_n dY.W[n] * act[n] over this block
-  float* red = reinterpret_cast<float*>(S0);   // [2 column halves][MT]
-  const int I = a.N;
+  // down backward, columns n < I of dh = [dg | du]: fp32 tile [128][128], 32 rows per array (S0, S1, S2, B0); 16-B
+  // chunk c (4 floats) of row r at c ^ (r & 7). Then per row: da = w(row) acc, (g, u) = hsave, dg = da u act'(g),
+  // du = da act(g), and the row's partial of sum_n acc * bf16(act(g) u) over this block's columns -> dwp.
+  float* const Fa[4] = {reinterpret_cast<float*>(S0), reinterpret_cast<float*>(S1), reinterpret_cast<float*>(S2),
+                        reinterpret_cast<float*>(B0)};
 #pragma unroll
   for (int m = 0; m < NSW; ++m) {
+    float* D = wr == 0 ? Fa[m] : Fa[2 + m];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = 64 * wr + m * 32 + acc_row(r, l);
-      const bool rv = row < nrows;
-      const int grow = row0 + row;
-      float wrow_ = 0.f;
-      if (rv) wrow_ = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
-      float part = 0.f;
+      const int lr = acc_row(r, l);
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        const bool fv = f == 0 ? fv0 : fv1;
-        const int n = cw + 32 * f + r32;
-        if (rv && fv) {
-          const float g = bf2f(a.hsave[(int64_t)grow * 2 * I + n]);
-          const float u = bf2f(a.hsave[(int64_t)grow * 2 * I + I + n]);
-          float av, dav;
-          act_and_grad_f(g, a.act, av, dav);
-          const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
-          const float accv = acc[m][f][r];
-          part += accv * abf;
-          const float da = wrow_ * accv;
-          a.out[(int64_t)grow * a.ldo + n] = f2bf(da * u * dav);
-          a.out[(int64_t)grow * a.ldo + I + n] = f2bf(da * av);
-        }
+        const int col = 64 * wc + 32 * f + r32;
+        D[lr * 128 + 4 * ((col >> 2) ^ (lr & 7)) + (col & 3)] = acc[m][f][r];
       }
-      part = half_sum(part);
-      if (r32 == 0) red[wc * MT + row] = part;
     }
   }
   __syncthreads();
-  if (tid < MT && tid < nrows) a.dwp[(int64_t)(row0 + tid) * a.nblk + nb] = red[tid] + red[MT + tid];
+  const int I = a.N;
+  const bool cv = col0 < I;
+  for (int row = tid >> 4; row < nrows; row += 16) {   // 16 threads per row, uniform trip count per row group
+    const int lr = row & 31;
+    const int q = row >> 5;   // a select, not an indexed local array (which would live in scratch memory)
+    const float* D = (q == 0 ? Fa[0] : q == 1 ? Fa[1] : q == 2 ? Fa[2] : Fa[3]) + lr * 128;
+    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(D + 4 * ((2 * ech) ^ (lr & 7)));
+    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(D + 4 * ((2 * ech + 1) ^ (lr & 7)));
+    const int grow = row0 + row;
+    const float wrow_ = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
+    float part = 0.f;
+    if (cv) {
+      const u32x4_t g2 = *reinterpret_cast<const u32x4_t*>(a.hsave + (int64_t)grow * 2 * I + col0);
+      const u32x4_t u2 = *reinterpret_cast<const u32x4_t*>(a.hsave + (int64_t)grow * 2 * I + I + col0);
+      const float accv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      uint32_t og[4], ou[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float dgv[2], duv[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
+          const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
+          float av, dav;
+          act_and_grad_f(g, a.act, av, dav);
+          const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
+          const float acv = accv[2 * j + h];
+          part += acv * abf;
+          const float da = wrow_ * acv;
+          dgv[h] = da * u * dav;
+          duv[h] = da * av;
+        }
+        og[j] = pack2bf(dgv[0], dgv[1]);
+        ou[j] = pack2bf(duv[0], duv[1]);
+      }
+      *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + col0) = u32x4_t{og[0], og[1], og[2], og[3]};
+      *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + I + col0) = u32x4_t{ou[0], ou[1], ou[2], ou[3]};
+    }
+    // fixed-order sum over the row's 16 threads (lanes 16 q .. 16 q + 15 of a wave)
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) part += __shfl_xor(part, o, 64);
+    if (ech == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
+  }
 }
 
 template <int EPI>
@@ -375,6 +416,8 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
                "gmm_bwd: int4 group %d must be a multiple of 32 dividing the columns", w->group);
   SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_bwd: an int4 bank needs its packed scale/zero (smel_pack_int4)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_bwd: A rows must be 16-B aligned");
+  SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0, SMEL_EUNSUPPORTED,
+               "gmm_bwd: out / hsave rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
                "gmm_bwd: epilogue %d needs hsave, dwp and topv", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_bwd: gather needs order");

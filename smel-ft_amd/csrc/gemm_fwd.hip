@@ -254,28 +254,73 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     }
   }
-  // ---- epilogue
+  // ---- epilogue through LDS (the ring is free after the loop): every lane writes its bf16 results into a row-major
+  // tile, then each thread stores 16-B chunks of whole rows, i.e. one address per 8 outputs instead of one per
+  // output. Tile rows are 128 B-chunked and XOR-swizzled like the A stages (phys chunk = c ^ (row & 7)).
+  __syncthreads();   // every wave is done with the ring (its loads landed, its reads returned)
+  if constexpr (EPI == 1) {
+    // g tile [128][128] in S0 (rows 0..63) / S1, u tile in S2 / S3; column = 32 w + r32 inside the block's 128
+    const int col = 32 * w + r32;
 #pragma unroll
-  for (int m = 0; m < NS; ++m) {
+    for (int m = 0; m < NS; ++m) {
+      uint16_t* G = m < 2 ? S0 : S1;
+      uint16_t* U = m < 2 ? S2 : S3;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m * 32 + acc_row(r, l);
-      if (row >= nrows) continue;
-      const int grow = row0 + row;
-      if (EPI == 1) {
-        if (!fv0) continue;
-        const int I = a.N / 2;
-        const uint16_t gb = f2bf(acc[m][0][r]), ub = f2bf(acc[m][1][r]);
-        const float av = act_f(bf2f(gb), a.act) * bf2f(ub);
-        a.out[(int64_t)grow * a.ldo + n0] = f2bf(av);
+      for (int r = 0; r < 16; ++r) {
+        const int row = m * 32 + acc_row(r, l), lr = row & 63;
+        const int e = lr * 128 + 8 * ((col >> 3) ^ (row & 7)) + (col & 7);
+        G[e] = f2bf(acc[m][0][r]);
+        U[e] = f2bf(acc[m][1][r]);
+      }
+    }
+    __syncthreads();
+    // thread -> (row, 8-column chunk): 16 threads per row, 16 rows per pass
+    const int I = a.N / 2;
+    const int ch = tid & 15;
+    const int col0 = nb * 128 + 8 * ch;
+    if (col0 < I) {
+      for (int row = tid >> 4; row < nrows; row += 16) {
+        const int lr = row & 63;
+        const int e = lr * 128 + 8 * (ch ^ (row & 7));
+        const u32x4_t g = *reinterpret_cast<const u32x4_t*>((row < 64 ? S0 : S1) + e);
+        const u32x4_t u = *reinterpret_cast<const u32x4_t*>((row < 64 ? S2 : S3) + e);
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = pack2bf(act_f(bf_lo(g[j]), a.act) * bf_lo(u[j]), act_f(bf_hi(g[j]), a.act) * bf_hi(u[j]));
+        const int64_t grow = row0 + row;
+        *reinterpret_cast<u32x4_t*>(a.out + grow * a.ldo + col0) = u32x4_t{o[0], o[1], o[2], o[3]};
         if (a.hsave) {
-          a.hsave[(int64_t)grow * a.N + n0] = gb;
-          a.hsave[(int64_t)grow * a.N + I + n0] = ub;
+          *reinterpret_cast<u32x4_t*>(a.hsave + grow * a.N + col0) = g;
+          *reinterpret_cast<u32x4_t*>(a.hsave + grow * a.N + I + col0) = u;
         }
-      } else {
-        const int64_t orow = (int64_t)row_slot(grow, a.order, a.TK) * a.ldo;
-        if (fv0) a.out[orow + n0] = f2bf(acc[m][0][r]);
-        if (fv1) a.out[orow + n1] = f2bf(acc[m][1][r]);
+      }
+    }
+  } else {
+    // out tile [128][256]: rows 32 m .. 32 m + 31 in stage m; column = 64 w + 32 f + r32 inside the block's 256
+    uint16_t* const St[4] = {S0, S1, S2, S3};
+#pragma unroll
+    for (int m = 0; m < NS; ++m) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = acc_row(r, l);   // row inside the stage (= row & 31)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const int col = 64 * w + 32 * f + r32;
+          St[m][lr * 256 + 8 * ((col >> 3) ^ (lr & 7)) + (col & 7)] = f2bf(acc[m][f][r]);
+        }
+      }
+    }
+    __syncthreads();
+    // thread -> (row, 8-column chunk): 32 threads per row, 8 rows per pass; rows go to their slot's output row
+    const int ch = tid & 31;
+    const int col0 = nb * 256 + 8 * ch;
+    if (col0 < a.N) {
+      for (int row = tid >> 5; row < nrows; row += 8) {
+        const int lr = row & 31;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(St[row >> 5] + lr * 256 + 8 * (ch ^ (lr & 7)));
+        const int64_t orow = row_slot(row0 + row, a.order, a.TK);
+        *reinterpret_cast<u32x4_t*>(a.out + orow * a.ldo + col0) = v;
       }
     }
   }
@@ -327,6 +372,8 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
                "gmm_fwd: int4 group %d must be a multiple of 32 dividing K", w->group);
   SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_fwd: an int4 bank needs its packed scale/zero (smel_pack_int4)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_fwd: A rows must be 16-B aligned");
+  SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0, SMEL_EUNSUPPORTED,
+               "gmm_fwd: out / hsave rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_fwd: act %d", act);
