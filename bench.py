@@ -1,11 +1,22 @@
-"""Benchmark of the MoE-layer hot path on one MI355X: forward with autograd + backward of the Qwen3.6-35B-A3B-shaped
-MoE layer (T=4092, hidden 2048, 256 experts, top-8, expert intermediate 512, 244 frozen
-int4 group-64 experts + 12 selected bf16 experts with LoRA r=16 alpha=32, shared expert 512 with LoRA r=16,
-upstream grad ~N(0, 1e-3)). Synthetic data, random weights of that shape (weights ~N(0, 0.02), x ~N(0, 1)).
+"""Benchmark of the MoE-layer hot path on one MI355X.
 
-One JSON line on stdout: tokens/s of the whole layer step, the roofline of the dominant kernel (HIP-event timed
-launches inside this run) and the CPU baseline (the oracle's restatement of the reference's CPU torch path, timed on
-this host's cores on one full pass of the same layer).
+Default (the driver's line): forward with autograd + backward of the Qwen3.6-35B-A3B-shaped MoE layer (BASELINE.json
+configs[2], "C3": T=4092, hidden 2048, 256 experts, top-8, expert intermediate 512, 244 frozen int4 group-64 experts
++ 12 selected bf16 experts with LoRA r=16 alpha=32, shared expert 512 with LoRA r=16, upstream grad ~N(0, 1e-3)).
+Synthetic data, random weights of that shape (weights ~N(0, 0.02), x ~N(0, 1)).
+
+Other workloads of BASELINE.json (``--workload``), each printing one JSON line of its own:
+  c2  forward only (no autograd) of the same layer with all 256 experts frozen int4 and no LoRA;
+  c4  Gemma-4-26B-A4B-style MoE block fwd+bwd: route_gemma4 on the residual stream, 128 GELU-tanh
+      experts (I=704, 12 selected bf16 + LoRA r16, the rest int4), the dense GeGLU MLP (2112) with LoRA r16, T=4096;
+      the block's RMSNorms are outside this path and replaced by separate synthetic inputs;
+  c5  the Qwen layer under skewed routing: T=32768 as 8 micro-batches of 4096, router biased to a
+      Zipf(1.2) expert popularity (realised top-12 gate-mass share reported), the 12 most popular experts selected.
+
+Every line carries tokens/s of the whole step, the roofline of the dominant kernel (HIP-event timed launches inside
+this run: algorithmic FLOPs and bytes per launch against MI355X's dense bf16 MFMA and HBM peaks, the binding one
+reported) and, for C3, the CPU baseline (the oracle's restatement of the reference's CPU torch path, timed on this
+host's cores on one full pass of the same layer).
 """
 import argparse
 import json
@@ -23,50 +34,347 @@ METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 HBM_PEAK = 8.0e12            # B/s, MI355X
 MFMA_BF16_PEAK = 2.5e15      # FLOP/s, MI355X dense bf16
 
-C3 = dict(T=4092, H=2048, E=256, I=512, K=8, Is=512, r=16, alpha=32.0, n_sel=12, group=64)
+QWEN = dict(T=4092, H=2048, E=256, I=512, K=8, Is=512, r=16, alpha=32.0, n_sel=12, group=64, act="silu")
+GEMMA = dict(T=4096, H=2816, E=128, I=704, K=8, Is=2112, r=16, alpha=32.0, n_sel=12, group=64, act="gelu_tanh")
+C5_BIAS = 0.45               # Zipf bias scale giving a ~50% top-12 gate-mass share (calibrated on the GPU)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_layer(device, cfg=C3, seed=0):
-    """The C3 layer with the drop-in API's own types; the frozen bank is quantized on the GPU by smel.quant."""
+# ------------------------------------------------------------------------------------------------- layer builders
+
+
+def _rnd(g, device, *s, std=0.02):
+    return (torch.randn(*s, generator=g, device=device) * std).to(torch.bfloat16)
+
+
+def build_qwen_layer(device, cfg=QWEN, seed=0, n_sel=None, lora=True, zipf=None):
+    """The Qwen layer with the drop-in API's own types; the frozen bank is quantized on the GPU by smel.quant.
+    ``zipf`` = bias scale c: expert e (in a random popularity order) gets logit bias -1.2 c ln(rank), injected
+    through the API's inputs: x has a unit mean component and router row e adds bias_e / H to every entry (rows
+    centred first, so the bias is the only mean term)."""
     from smel.lora import ExpertsLoRA, LayerLoRA, MLPLoRA
     from smel.moe import Int4Experts, LayerExperts
     g = torch.Generator(device=device).manual_seed(seed)
     T, H, E, I, Is, r = cfg["T"], cfg["H"], cfg["E"], cfg["I"], cfg["Is"], cfg["r"]
-    bf = torch.bfloat16
-
-    def rnd(*s, std=0.02):
-        return (torch.randn(*s, generator=g, device=device) * std).to(bf)
-
-    x = torch.randn(T, H, generator=g, device=device).to(bf)
-    W = {"mlp.gate.weight": rnd(E, H),
-         "mlp.shared_expert.gate_proj.weight": rnd(Is, H), "mlp.shared_expert.up_proj.weight": rnd(Is, H),
-         "mlp.shared_expert.down_proj.weight": rnd(H, Is), "mlp.shared_expert_gate.weight": rnd(1, H)}
-    gu, dn = rnd(E, 2 * I, H), rnd(E, H, I)
+    n_sel = cfg["n_sel"] if n_sel is None else n_sel
+    x = torch.randn(T, H, generator=g, device=device)
+    gate = torch.randn(E, H, generator=g, device=device) * 0.02
+    popular = None
+    if zipf is not None:
+        perm = torch.randperm(E, generator=torch.Generator().manual_seed(seed + 1))
+        rank = torch.empty(E, dtype=torch.long)
+        rank[perm] = torch.arange(E)
+        bias = -1.2 * zipf * torch.log(rank.double() + 1.0)
+        gate = gate - gate.mean(1, keepdim=True) + (bias / H).float().to(device)[:, None]
+        x = x + 1.0
+        popular = perm[:n_sel].tolist()
+    x = x.to(torch.bfloat16)
+    W = {"mlp.gate.weight": gate.to(torch.bfloat16),
+         "mlp.shared_expert.gate_proj.weight": _rnd(g, device, Is, H),
+         "mlp.shared_expert.up_proj.weight": _rnd(g, device, Is, H),
+         "mlp.shared_expert.down_proj.weight": _rnd(g, device, H, Is),
+         "mlp.shared_expert_gate.weight": _rnd(g, device, 1, H)}
+    gu, dn = _rnd(g, device, E, 2 * I, H), _rnd(g, device, E, H, I)
     bank = Int4Experts.from_bf16(gu, dn, cfg["group"])
-    sel = list(range(0, E, E // cfg["n_sel"]))[: cfg["n_sel"]]        # scripts/bench/bench_layer.py:70
-    ex = LayerExperts(bank, sel, gu[sel].clone(), dn[sel].clone(), group=32)
+    if n_sel:
+        sel = popular if popular is not None else list(range(0, E, E // n_sel))[:n_sel]   # bench_layer.py:70
+        ex = LayerExperts(bank, sel, gu[sel].clone(), dn[sel].clone(), group=32, act=cfg["act"])
+    else:
+        sel = []
+        ex = LayerExperts(bank, group=32, act=cfg["act"])
+    del gu, dn
+    torch.manual_seed(seed)
+    lo = None
+    if lora:
+        lo = LayerLoRA(ExpertsLoRA(sel, H, I, r, cfg["alpha"]) if sel else None,
+                       MLPLoRA(H, Is, r, cfg["alpha"])).to(device)
+    gy = (torch.randn(T, H, generator=g, device=device) * 1e-3).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    return x, W, ex, lo, gy
+
+
+def build_gemma_block(device, cfg=GEMMA, seed=0):
+    """The Gemma-4-style MoE block's inputs and weights: residual stream h (router input), the experts' input xe and
+    the dense MLP's input xm (the RMSNorm outputs of the reference's block, synthetic here), router tensors as
+    smel/tiny.py:74-77 draws them, 128 experts (12 selected bf16 + LoRA, the rest int4), dense GeGLU MLP + LoRA."""
+    from smel.lora import ExpertsLoRA, LayerLoRA, MLPLoRA
+    from smel.moe import Int4Experts, LayerExperts
+    g = torch.Generator(device=device).manual_seed(seed)
+    T, H, E, I, Is, r = cfg["T"], cfg["H"], cfg["E"], cfg["I"], cfg["Is"], cfg["r"]
+    h = (torch.randn(T, H, generator=g, device=device) * 3.0).to(torch.bfloat16)
+    xe = torch.randn(T, H, generator=g, device=device).to(torch.bfloat16)
+    xm = torch.randn(T, H, generator=g, device=device).to(torch.bfloat16)
+    W = {"router.scale": (1.0 + 0.2 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16),
+         "router.proj.weight": _rnd(g, device, E, H),
+         "router.per_expert_scale": (0.5 + torch.rand(E, generator=g, device=device)).to(torch.bfloat16),
+         "mlp.gate_up_proj.weight": _rnd(g, device, 2 * Is, H), "mlp.down_proj.weight": _rnd(g, device, H, Is)}
+    W["mlp.gate_proj.weight"] = W["mlp.gate_up_proj.weight"][:Is]
+    W["mlp.up_proj.weight"] = W["mlp.gate_up_proj.weight"][Is:]
+    gu, dn = _rnd(g, device, E, 2 * I, H), _rnd(g, device, E, H, I)
+    bank = Int4Experts.from_bf16(gu, dn, cfg["group"])
+    sel = list(range(0, E, E // cfg["n_sel"]))[: cfg["n_sel"]]
+    ex = LayerExperts(bank, sel, gu[sel].clone(), dn[sel].clone(), group=32, act=cfg["act"])
     del gu, dn
     torch.manual_seed(seed)
     lora = LayerLoRA(ExpertsLoRA(sel, H, I, r, cfg["alpha"]), MLPLoRA(H, Is, r, cfg["alpha"])).to(device)
-    gy = (torch.randn(T, H, generator=g, device=device) * 1e-3).to(bf)
+    gy = (torch.randn(T, H, generator=g, device=device) * 1e-3).to(torch.bfloat16)
     torch.cuda.synchronize()
-    return x, W, ex, lora, gy
+    return h, xe, xm, W, ex, lora, gy
 
 
-def gemm_flops(tag, cfg, S):
-    """Algorithmic FLOPs of one launch of each grouped GEMM (routed + shared rows, LoRA at its real rank r)."""
-    T, H, E, I, K, r = cfg["T"], cfg["H"], cfg["E"], cfg["I"], cfg["K"], cfg["r"]
-    M = T * K + T          # routed slots + shared-expert rows
-    Lr = S + T             # rows with LoRA (selected-expert slots + shared rows)
-    return {"gemm_gu_fwd": 2 * M * H * 2 * I + 2 * Lr * r * 2 * I,
-            "gemm_dn_fwd": 2 * M * I * H + 2 * Lr * r * H,
-            "gemm_dn_bwd": 2 * M * H * I + 2 * Lr * r * I,
-            "gemm_gu_bwd": 2 * M * 2 * I * H + 2 * Lr * 2 * r * H,
-            "gemm_router_bwd": 2 * T * (E + 1) * H}.get(tag)
+# ------------------------------------------------------------------------------------------ algorithmic work model
+
+
+def kernel_work(tag, c, S):
+    """(algorithmic FLOPs, algorithmic HBM bytes) of one launch of a kernel, from the layer's shape ``c`` and the
+    number S of slots routed to selected experts. Bytes = every operand read once and every result written once:
+    frozen int4 experts (q + bf16 scale/zero) except the selected ones, selected / shared bf16 weights, activations
+    (the gathered token rows counted once per token), the LoRA K-extension rows, the saved pre-activations."""
+    T, H, E, I, K, r = c["T"], c["H"], c["E"], c["I"], c["K"], c["r"]
+    g = c["group"]
+    n_sel = c.get("n_sel_used", c["n_sel"])
+    Msh = T if c.get("fused_shared") else 0
+    M = T * K + Msh
+    Lr = S + Msh
+    nfz = E - n_sel
+    gu_w = nfz * (2 * I * H // 2 + 2 * I * (H // g) * 4) + n_sel * 2 * I * H * 2 + (2 * I * H * 2 if Msh else 0)
+    dn_w = nfz * (H * I // 2 + H * (I // g) * 4) + n_sel * H * I * 2 + (H * I * 2 if Msh else 0)
+    ext = M * 32 * 2 if (Lr and r) else 0
+    nblk = -(-I // 128)
+    Epad = -(-(E + (1 if Msh else 0)) // 32) * 32
+    Is = c.get("Is", I)
+    w = {"gemm_gu_fwd": (2 * M * H * 2 * I + 2 * Lr * r * 2 * I, gu_w + T * H * 2 + ext + M * I * 2 + M * 2 * I * 2),
+         "gemm_dn_fwd": (2 * M * I * H + 2 * Lr * r * H, dn_w + M * I * 2 + ext + M * H * 2),
+         "gemm_dn_bwd": (2 * M * H * I + 2 * Lr * r * I,
+                         dn_w + T * H * 2 + M * 2 * I * 2 + ext + M * 2 * I * 2 + M * nblk * 4),
+         "gemm_gu_bwd": (2 * M * 2 * I * H + 2 * Lr * 2 * r * H, gu_w + M * 2 * I * 2 + ext + M * H * 2),
+         "gemm_router_bwd": (2 * T * Epad * H, T * Epad * 2 + Epad * H * 2 + T * H * 2),
+         "gemm_mlp_gu_fwd": (2 * T * H * 2 * Is + 2 * T * r * 2 * Is,
+                             2 * Is * H * 2 + T * H * 2 + T * 64 + T * Is * 2 + T * 2 * Is * 2),
+         "gemm_mlp_dn_fwd": (2 * T * Is * H + 2 * T * r * H, H * Is * 2 + T * Is * 2 + T * 64 + T * H * 2),
+         "gemm_mlp_dn_bwd": (2 * T * H * Is + 2 * T * r * Is, H * Is * 2 + T * H * 2 + 2 * T * 2 * Is * 2 + T * 64),
+         "gemm_mlp_gu_bwd": (2 * T * 2 * Is * H + 2 * T * 2 * r * H,
+                             2 * Is * H * 2 + T * 2 * Is * 2 + T * 64 + T * H * 2),
+         "smel_combine": (0, M * H * 2 + T * K * 2 + T * 4 + T * H * 2),
+         "smel_dx_reduce": (0, M * H * 2 + 2 * T * H * 2)}
+    return w.get(tag)
+
+
+def roofline(breakdown, c, S):
+    """The dominant (longest average launch) kernel with a work model: its roofline time max(F / P_mfma,
+    B / BW_hbm) decides the bound; achieved = that kernel's F or B over its HIP-event-timed launch."""
+    known = {k: v for k, v in breakdown.items() if kernel_work(k, c, S)}
+    dom = max(known, key=known.get)
+    F, B = kernel_work(dom, c, S)
+    t = known[dom] * 1e-3
+    if F / MFMA_BF16_PEAK >= B / HBM_PEAK:
+        out = {"kernel": dom, "bound": "mfma", "achieved": round(F / t / 1e12, 2), "peak": MFMA_BF16_PEAK / 1e12,
+               "unit": "TFLOP/s", "frac": round(F / t / MFMA_BF16_PEAK, 4)}
+    else:
+        out = {"kernel": dom, "bound": "hbm", "achieved": round(B / t / 1e9, 1), "peak": HBM_PEAK / 1e9,
+               "unit": "GB/s", "frac": round(B / t / HBM_PEAK, 4)}
+    out.update({"traffic": measured_traffic(dom), "flops_per_launch": F, "bytes_per_launch": B,
+                "avg_launch_ms": known[dom], "mfma_frac": round(F / t / MFMA_BF16_PEAK, 4),
+                "hbm_frac": round(B / t / HBM_PEAK, 4)})
+    return out
+
+
+def measured_traffic(kernel_tag):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary (profiles/traffic.json: FETCH_SIZE
+    and WRITE_SIZE per dispatch, scaled by the same counters on a copy of known size), or None if not measured."""
+    try:
+        d = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))
+    except (OSError, ValueError):
+        return None
+    k = d.get("kernels", {}).get(kernel_tag)
+    return None if k is None else k.get("hbm_bytes_per_launch")
+
+
+# ---------------------------------------------------------------------------------------------------- timing
+
+
+def time_step(step, steps, warmup, graph):
+    """Eager timing of ``steps`` steps after ``warmup``, then (graph=True) the same step captured once in a HIP
+    graph and replayed (removes the host launch gaps between the step's kernels). Returns (mode, ms, eager_ms)."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) / steps * 1e3
+    log(f"eager step {eager_ms:.3f} ms")
+    if not graph:
+        return "eager", eager_ms, eager_ms
+    # capture on a side stream of default priority after a few warm-up steps there (allocator pools settle)
+    gs = torch.cuda.Stream()
+    gs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(gs):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(gs)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    log(f"graph step {ms:.3f} ms")
+    return "hip_graph", ms, eager_ms
+
+
+def breakdown_of(step, n):
+    """Per-launch milliseconds of every entry point (events on the launching stream) over n extra steps."""
+    from smel import _lib
+    with _lib.timing() as tm:
+        for _ in range(n):
+            step()
+    torch.cuda.synchronize()
+    res = tm.results()
+    return {k: round(statistics.mean(v), 4) for k, v in sorted(res.items(), key=lambda kv: -sum(kv[1]))}
+
+
+def emit(metric, tokens, args, timing, workload, extra_cfg, roof, breakdown, cpu=None, **extra):
+    mode, ms, eager_ms = timing
+    out = {"metric": metric, "value": round(tokens / ms * 1e3, 1), "unit": "tokens/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (random weights ~N(0,0.02), x ~N(0,1))",
+           "config": {"workload": workload, "tokens": tokens, "parallelism": "single GPU", "launch": mode,
+                      **extra_cfg},
+           "eager_ms_per_step": round(eager_ms, 4), "roofline": roof, "breakdown_ms": breakdown,
+           "cpu_baseline": cpu}
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+# ------------------------------------------------------------------------------------------------- workloads
+
+QWEN_NAMES = {
+    "c3": ("C3: Qwen3.6-35B-A3B MoE layer fwd+bwd, T=4092, H=2048, E=256, I=512, top-8, 244 int4 g64 frozen + 12 bf16 "
+           "LoRA r16 experts, shared 512 + LoRA r16"),
+    "c2": ("C2: Qwen3.6-35B-A3B MoE layer forward only, T=4092, H=2048, E=256, I=512, top-8, all 256 experts int4 "
+           "g64, shared expert 512 (no LoRA)"),
+    "c5": ("C5: Qwen3.6 MoE layer fwd+bwd under Zipf(1.2)-biased routing, T=32768 as 8 micro-batches of 4096, the 12 "
+           "most popular experts bf16 + LoRA r16, shared 512 + LoRA r16")}
+QWEN_METRICS = {"c2": "MoE layer forward tokens/s (Qwen3.6 shape, T=4092)",
+                "c5": "MoE layer fwd+bwd tokens/s under Zipf-skewed routing (Qwen3.6 shape, 8 x 4096 tokens)"}
+
+
+def run_qwen(args, dev, mode):
+    """c3 (default): fwd+bwd with LoRA; c2: forward only, all experts int4, no LoRA; c5: c3 under Zipf routing,
+    8 micro-batches of 4096 tokens per step."""
+    from smel.moe import moe_forward
+    cfg = dict(QWEN)
+    fwd_only = mode == "c2"
+    nmb = 1
+    if mode == "c5":
+        cfg["T"] = 4096
+        nmb = 8
+    log(f"building the {mode} layer (int4 quantization on the GPU) ...")
+    x, W, ex, lora, gy = build_qwen_layer(dev, cfg, n_sel=0 if fwd_only else None, lora=not fwd_only,
+                                          zipf=C5_BIAS if mode == "c5" else None)
+    T = cfg["T"]
+    xs, gys = [x], [gy]
+    if nmb > 1:   # micro-batches: the same layer on 8 different token sets
+        g = torch.Generator(device=dev).manual_seed(7)
+        for _ in range(nmb - 1):
+            xs.append((x.float() + 0.5 * torch.randn(x.shape, generator=g, device=dev)).to(torch.bfloat16))
+            gys.append((torch.randn(gy.shape, generator=g, device=dev) * 1e-3).to(torch.bfloat16))
+    xgs = [xi.clone().requires_grad_(not fwd_only) for xi in xs]
+    params = list(lora.parameters()) if lora is not None else []
+    seen = []
+
+    def step(stats=None):
+        if fwd_only:
+            with torch.no_grad():
+                for xi in xgs:
+                    moe_forward(xi, W, ex, cfg["K"], None, stats=stats)
+            return
+        for p in params:
+            p.grad = None
+        for xi, gi in zip(xgs, gys):
+            xi.grad = None
+            moe_forward(xi, W, ex, cfg["K"], lora, stats=stats).backward(gi)
+
+    step(stats=lambda p, v, i: seen.append((v.float(), i)))
+    sel = torch.zeros(cfg["E"], dtype=torch.bool, device=dev)
+    if ex.sel_ids is not None:
+        sel[ex.sel_ids.to(dev)] = True
+    S = int(sum(int(sel[i].sum()) for _, i in seen) / len(seen))
+    extra = {}
+    if mode == "c5":
+        mass = torch.zeros(cfg["E"], dtype=torch.float64, device=dev)
+        cnt = torch.zeros(cfg["E"], dtype=torch.float64, device=dev)
+        for v, i in seen:
+            mass.index_add_(0, i.reshape(-1), v.reshape(-1).double())
+            cnt.index_add_(0, i.reshape(-1), torch.ones(i.numel(), dtype=torch.float64, device=dev))
+        share = float(mass.sort(descending=True).values[:12].sum() / mass.sum())
+        sel_share = float(mass[sel].sum() / mass.sum())
+        extra = {"top12_gate_mass_share": round(share, 4), "selected_gate_mass_share": round(sel_share, 4),
+                 "rows_per_expert_max": int(cnt.max()) // nmb, "rows_per_expert_min": int(cnt.min()) // nmb}
+        log(f"zipf routing: top-12 gate-mass share {share:.3f}, selected {sel_share:.3f}, "
+            f"rows/expert per micro-batch {int(cnt.min()) // nmb}..{int(cnt.max()) // nmb}")
+    log(f"slots routed to the selected experts per micro-batch: S={S} (S/T={S / T:.3f})")
+    timing = time_step(step, args.steps, args.warmup, not args.eager)
+    bd = breakdown_of(step, max(3, min(20, args.steps)))
+    log("per-launch ms:", json.dumps(bd))
+    c = dict(cfg, fused_shared=True, n_sel_used=0 if fwd_only else cfg["n_sel"])
+    if fwd_only:
+        c["r"] = 0
+    roof = roofline(bd, c, S)
+    cpu = None
+    if mode == "c3" and not args.no_cpu_baseline:
+        log("timing the CPU baseline (one full pass of the oracle) ...")
+        cpu = cpu_baseline(x, W, ex, lora, gy, cfg)
+    emit(METRIC if mode == "c3" else QWEN_METRICS[mode], T * nmb, args, timing, QWEN_NAMES[mode],
+         {"selected_slots": S, "micro_batches": nmb}, roof, bd, cpu, **extra)
+
+
+def run_gemma(args, dev):
+    from smel.moe import mlp_lora, route_gemma4, routed_experts
+    cfg = GEMMA
+    log("building the c4 Gemma-4-style block (int4 quantization on the GPU) ...")
+    h, xe, xm, W, ex, lora, gy = build_gemma_block(dev, cfg)
+    hg, xeg, xmg = (t.clone().requires_grad_(True) for t in (h, xe, xm))
+    params = list(lora.parameters())
+    seen = {}
+
+    def step(stats=None):
+        for t in (hg, xeg, xmg):
+            t.grad = None
+        for p in params:
+            p.grad = None
+        m = mlp_lora(xmg, W["mlp.gate_proj.weight"], W["mlp.up_proj.weight"], W["mlp.down_proj.weight"],
+                     lora.shared, cfg["act"], W["mlp.gate_up_proj.weight"])
+        probs, topv, topi = route_gemma4(hg, W, cfg["K"], 1e-6)
+        if stats is not None:
+            stats(probs, topv, topi)
+        e = routed_experts(xeg, topv, topi, ex, lora.experts)
+        (m + e).backward(gy)
+
+    step(stats=lambda p, v, i: seen.update(topi=i))
+    sel = torch.zeros(cfg["E"], dtype=torch.bool, device=dev)
+    sel[ex.sel_ids.to(dev)] = True
+    S = int(sel[seen["topi"]].sum())
+    log(f"slots routed to the selected experts: S={S} (S/T={S / cfg['T']:.3f})")
+    timing = time_step(step, args.steps, args.warmup, not args.eager)
+    bd = breakdown_of(step, max(3, min(20, args.steps)))
+    log("per-launch ms:", json.dumps(bd))
+    roof = roofline(bd, dict(cfg, fused_shared=False), S)
+    emit("MoE block fwd+bwd tokens/s (Gemma-4-26B-A4B shape, T=4096)", cfg["T"], args, timing,
+         "C4: Gemma-4-26B-A4B-style MoE block fwd+bwd: route_gemma4, 128 GELU-tanh experts I=704 top-8 (116 int4 g64 + "
+         "12 bf16 LoRA r16), dense GeGLU MLP 2112 + LoRA r16, T=4096, H=2816 (block RMSNorms excluded)",
+         {"selected_slots": S}, roof, bd, None)
 
 
 def cpu_baseline(x, W, ex, lora, gy, cfg):
@@ -91,16 +399,29 @@ def cpu_baseline(x, W, ex, lora, gy, cfg):
     t0 = time.perf_counter()
     R.moe_forward_backward(c(x), ol, cfg["K"], c(gy), dtype=torch.float32)
     dt = time.perf_counter() - t0
-    return {"value": cfg["T"] / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+    return {"value": round(cfg["T"] / dt, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"1 fwd+bwd pass of the full C3 layer (T={cfg['T']}), fp32, {dt:.1f} s, "
                       f"torch threads={cores}, cpu={_cpu_model()}"}
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """A device-to-device copy of exactly COPY_BYTES bytes (read COPY_BYTES, write COPY_BYTES), 5 launches."""
+    src = torch.randint(0, 255, (COPY_BYTES,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 5 copies of {COPY_BYTES} bytes")
+
+
 def _cpu_model():
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
     except OSError:
         pass
     return "unknown"
@@ -111,105 +432,27 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5"), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of COPY_BYTES bytes 5 times (the reference point that scales "
+                         "the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE hot path here runs on one MI355X and has no multi-GPU path "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     from smel import _lib
-    from smel.moe import moe_forward
     _lib.load()
     dev = torch.device("cuda:0")
-    cfg = C3
-    log("building the C3 layer (int4 quantization on the GPU) ...")
-    x, W, ex, lora, gy = build_layer(dev, cfg)
-    xg = x.clone().requires_grad_(True)
-    params = list(lora.parameters())
-    seen = {}
-
-    def step(stats=None):
-        xg.grad = None
-        for p in params:
-            p.grad = None
-        y = moe_forward(xg, W, ex, cfg["K"], lora, stats=stats)
-        y.backward(gy)
-
-    step(stats=lambda p, v, i: seen.update(topi=i))
-    sel = torch.zeros(cfg["E"], dtype=torch.bool, device=dev)
-    sel[ex.sel_ids.to(dev)] = True
-    S = int(sel[seen["topi"]].sum())
-    log(f"slots routed to the selected experts: S={S} (S/T={S / cfg['T']:.3f})")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    eager_ms = dt / args.steps * 1e3
-    log(f"eager step {eager_ms:.3f} ms, {cfg['T'] * args.steps / dt:.0f} tokens/s")
-    mode = "eager"
-    ms, tok_s = eager_ms, cfg["T"] * args.steps / dt
-    if not args.eager:
-        # The same step (forward + backward, every kernel) captured once in a HIP graph and replayed: this removes
-        # the host-side launch gaps between the ~40 kernels of a step. Capture on a side stream of default priority
-        # after a few warm-up steps there (allocator pools settle), as torch.cuda.graph expects.
-        gs = torch.cuda.Stream()
-        gs.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(gs):
-            for _ in range(3):
-                step()
-        torch.cuda.current_stream().wait_stream(gs)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            step()
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
-        mode = "hip_graph"
-        ms, tok_s = dt / args.steps * 1e3, cfg["T"] * args.steps / dt
-        log(f"graph step {ms:.3f} ms, {tok_s:.0f} tokens/s")
-    # per-launch timing of every entry point (events on the launching stream), a few extra steps
-    n_prof = max(5, min(20, args.steps))
-    with _lib.timing() as tm:
-        for _ in range(n_prof):
-            step()
-    torch.cuda.synchronize()
-    res = tm.results()
-    breakdown = {k: round(statistics.mean(v), 4) for k, v in sorted(res.items(), key=lambda kv: -sum(kv[1]))}
-    log("per-launch ms:", json.dumps(breakdown))
-    gemms = {k: v for k, v in breakdown.items() if gemm_flops(k, cfg, S)}
-    dom = max(gemms, key=gemms.get)
-    F = gemm_flops(dom, cfg, S)
-    achieved = F / (gemms[dom] * 1e-3)
-    roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": MFMA_BF16_PEAK / 1e12,
-            "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK, 4), "traffic": None,
-            "flops_per_launch": F, "avg_launch_ms": gemms[dom]}
-    total_f = sum(gemm_flops(k, cfg, S) for k in gemms)
-    out = {"metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random weights ~N(0,0.02), x ~N(0,1))",
-           "config": {"workload": "C3: Qwen3.6-35B-A3B MoE layer fwd+bwd, T=4092, H=2048, E=256, I=512, top-8, "
-                                  "244 int4 g64 frozen + 12 bf16 LoRA r16 experts, shared 512 + LoRA r16",
-                      "tokens": cfg["T"], "selected_slots": S, "parallelism": "single GPU", "launch": mode},
-           "eager_ms_per_step": round(eager_ms, 4),
-           "roofline": roof,
-           "gemm_tflops_all": round(total_f / (sum(gemms.values()) * 1e-3) / 1e12, 2),
-           "breakdown_ms": breakdown}
-    if not args.no_cpu_baseline:
-        log("timing the CPU baseline (one full pass of the oracle) ...")
-        out["cpu_baseline"] = cpu_baseline(x, W, ex, lora, gy, cfg)
+    if args.workload == "c4":
+        run_gemma(args, dev)
     else:
-        out["cpu_baseline"] = None
-    print(json.dumps(out), flush=True)
+        run_qwen(args, dev, args.workload)
 
 
 if __name__ == "__main__":

@@ -93,6 +93,22 @@ int64_t smel_route_ld(int64_t E, int32_t with_shared_gate);
 int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, int64_t K, float* probs, uint16_t* topv,
                       int64_t* topi, int32_t* topi32, hipStream_t stream);
 
+/* ---- (A2) replaces route_gemma4, smel/moe.py:170-180 (the Gemma 4 router on the residual stream).
+ * h [T][H] bf16, router_scale [H], proj_w [E][H], per_expert_scale [E] bf16 (E <= 256, H a multiple of 64):
+ *   xn = bf16(bf16(bf16(h r) * router_scale) * H^-1/2), r = rstd[t] = (mean_j h[t][j]^2 + eps)^-1/2 (fp32),
+ *   logits = bf16(xn proj_w^T), probs = softmax (fp32), top-k as smel_route, topv [T][K] fp32 = renormalised value
+ *   * per_expert_scale[id]. xn [T][H], rstd [T] and logits [T][smel_route_ld(E, 0)] are caller workspaces, left
+ *   holding those values (the backward reads rstd). */
+int smel_route_gemma4(const uint16_t* h, const uint16_t* router_scale, const uint16_t* proj_w,
+                      const uint16_t* per_expert_scale, int64_t T, int64_t H, int64_t E, int64_t K, float eps,
+                      float* probs, float* topv, int64_t* topi, int32_t* topi32, uint16_t* xn, float* rstd,
+                      uint16_t* logits, hipStream_t stream);
+/* Backward of the router input of smel_route_gemma4 (autograd of smel/moe.py:172-174): dxn [T][H] bf16 = dL/dxn
+ * (the router GEMM's dX) -> dh [T][H] bf16 = g r - h r^3 sum_j(g h)/H with g = bf16(bf16(dxn H^-1/2) router_scale).
+ * The d(topv) -> dlogits step is smel_route_bwd with inv = NULL and per_expert_scale. */
+int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scale, const float* rstd,
+                                  const uint16_t* dxn, int64_t T, int64_t H, uint16_t* dh, hipStream_t stream);
+
 /* ---- (A3) replaces the dispatch of routed_experts, smel/moe.py:216-223 and the inverse of :249-250.
  * ids [T*K] (int32 if ids_are_i64 == 0, else int64) -> counts [E], offsets [E+1], order [TK] (stable: experts
  * ascending, slot p ascending within one), inv [TK], and the GEMM tile list: tiles [max_tiles][4] = {group, row0,
@@ -168,10 +184,13 @@ int64_t smel_gmm_bwd_nblocks(int64_t C);
 /* ---- (A15) router backward (autograd of route + renorm + the shared gate, smel/moe.py:162-167, 201):
  * dtopv[t,k] = sum_j dwp[inv[t*K+k]][j]; d renorm; d gather; d softmax (probs) -> dlogits [T][ldl] bf16 with
  * dlogits[t][E] = d shared-gate logit (sum_j dwp[TK+t][j] * sg (1-sg)) when sgate != NULL, zero padding to ldl.
- * dtopv_out [T][K] fp32 (optional) receives dtopv. */
+ * dtopv_out [T][K] fp32 (optional) receives dtopv. inv = NULL: dwp rows are the slots t*K+k themselves (TK = T*K).
+ * per_expert_scale [E] bf16 (optional, route_gemma4): the routed value was renorm * per_expert_scale[id], so dtopv
+ * is multiplied by it before the renorm backward. */
 int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs, const int32_t* topi32,
                    const uint16_t* topv, const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK,
-                   uint16_t* dlogits, int64_t ldl, float* dtopv_out, hipStream_t stream);
+                   uint16_t* dlogits, int64_t ldl, float* dtopv_out, const uint16_t* per_expert_scale,
+                   hipStream_t stream);
 
 /* d(combine weight) of routed_experts when topv is an input: dtopv[p] = sum_j dwp[inv[p]][j], fp32 [TK]. */
 int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, float* dtopv, hipStream_t stream);

@@ -1,6 +1,8 @@
 // Router: logits = x W_r^T (bf16 MFMA, fp32 accumulation, bf16-rounded like F.linear in bf16), softmax in fp32,
 // top-k (descending, lower expert id first among equal logits), renormalisation; and its backward.
 // Reference: route, smel/moe.py:162-167; the shared-expert gate logit of shared_mlp, smel/moe.py:201.
+#include <math.h>
+
 #include "abi_util.h"
 #include "common.h"
 
@@ -8,10 +10,12 @@ namespace {
 
 constexpr int MAXE = 256;      // experts handled by the selection (4 logits per lane)
 
-// Selection over one token's logits (held in LDS or global), by one wave. Writes probs, topv, topi, topi32.
+// Selection over one token's logits (held in LDS or global), by one wave. Writes probs, topi, topi32 and topv: bf16
+// (route), or fp32 times per_expert_scale[id] when topv_f32 is given (route_gemma4).
 template <typename Get>
 SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict__ probs, uint16_t* __restrict__ topv,
-                          int64_t* __restrict__ topi, int32_t* __restrict__ topi32) {
+                          int64_t* __restrict__ topi, int32_t* __restrict__ topi32, float* __restrict__ topv_f32,
+                          const uint16_t* __restrict__ pes) {
   const int l = lane_id();
   float v[MAXE / 64];
 #pragma unroll
@@ -74,7 +78,10 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
         p = pk[k];
         i = ik[k];
       }
-    topv[t * K + l] = f2bf(p / psum);
+    if (topv_f32)
+      topv_f32[t * K + l] = pes ? (p / psum) * bf2f(pes[i]) : p / psum;   // route_gemma4: fp32, x per-expert scale
+    else
+      topv[t * K + l] = f2bf(p / psum);
     topi[t * K + l] = i;
     topi32[t * K + l] = i;
   }
@@ -181,11 +188,12 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
 __global__ __launch_bounds__(256) void route_select(const uint16_t* __restrict__ logits, int ldl, int T, int E, int K,
                                                     int sg_col, float* __restrict__ probs,
                                                     uint16_t* __restrict__ topv, int64_t* __restrict__ topi,
-                                                    int32_t* __restrict__ topi32, float* __restrict__ sgate) {
+                                                    int32_t* __restrict__ topi32, float* __restrict__ sgate,
+                                                    float* __restrict__ topv_f32, const uint16_t* __restrict__ pes) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const uint16_t* row = logits + t * ldl;
-  select_topk([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topi, topi32);
+  select_topk([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topi, topi32, topv_f32, pes);
   if (sgate && lane_id() == 0) sgate[t] = 1.0f / (1.0f + expf(-bf2f(row[sg_col])));
 }
 
@@ -199,7 +207,7 @@ __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, 
                                                  const int32_t* __restrict__ topi32, const uint16_t* __restrict__ topv,
                                                  const float* __restrict__ sgate, int T, int K, int E, int TK,
                                                  uint16_t* __restrict__ dlogits, int ldl,
-                                                 float* __restrict__ dtopv_out) {
+                                                 float* __restrict__ dtopv_out, const uint16_t* __restrict__ pes) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int l = lane_id();
@@ -207,13 +215,15 @@ __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, 
   float dtv = 0.f, p = 0.f;
   int idx = -1;
   if (l < K) {
-    const int row = inv[t * K + l];   // -1 for a slot the dispatch dropped (id out of range)
+    // -1 for a slot the dispatch dropped (id out of range); no inv = dwp rows are the slots themselves
+    const int row = inv ? inv[t * K + l] : (int)(t * K + l);
     if (row >= 0)
       for (int j = 0; j < nblk; ++j) dtv += dwp[(int64_t)row * nblk + j];
     idx = topi32[t * K + l];
     if (idx >= 0 && idx < E) p = probs[t * E + idx];
     else idx = -1;
     if (dtopv_out) dtopv_out[t * K + l] = dtv;
+    if (pes && idx >= 0) dtv *= bf2f(pes[idx]);   // route_gemma4's topv = renorm * per_expert_scale[i]
   }
   // S = sum_k p_k ; topv_k = p_k / S (recomputed in fp32, not the bf16-rounded copy)
   float S = 0.f, dot = 0.f;
@@ -248,6 +258,86 @@ __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, 
     dlogits[t * ldl + e] = f2bf(g);
   }
   (void)topv;
+}
+
+// ---- Gemma 4 router input (smel/moe.py:170-180): one wave per token of the residual stream h [T][H]:
+//   r = (mean(h^2) + eps)^-1/2 (fp32), xn = bf16(bf16(bf16(h r) * router.scale) * H^-1/2)  (the reference's roundings:
+//   .type_as(h), then two bf16 products); rstd[t] = r is kept for the backward.
+__global__ __launch_bounds__(256) void route_prenorm(const uint16_t* __restrict__ h, const uint16_t* __restrict__ scale,
+                                                     int T, int H, float eps, float hs, uint16_t* __restrict__ xn,
+                                                     float* __restrict__ rstd) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int l = lane_id();
+  const u32x4_t* row = reinterpret_cast<const u32x4_t*>(h + t * H);
+  const int nc = H / 8;
+  float ss = 0.f;
+  for (int c = l; c < nc; c += 64) {
+    const u32x4_t v = row[c];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf_lo(v[j]), b = bf_hi(v[j]);
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)H + eps);
+  const u32x4_t* sc = reinterpret_cast<const u32x4_t*>(scale);
+  u32x4_t* out = reinterpret_cast<u32x4_t*>(xn + t * H);
+  for (int c = l; c < nc; c += 64) {
+    const u32x4_t v = row[c], g = sc[c];
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = bf2f(f2bf(bf2f(f2bf(bf_lo(v[j]) * r)) * bf_lo(g[j]))) * hs;
+      const float b = bf2f(f2bf(bf2f(f2bf(bf_hi(v[j]) * r)) * bf_hi(g[j]))) * hs;
+      o[j] = pack2bf(a, b);
+    }
+    out[c] = u32x4_t{o[0], o[1], o[2], o[3]};
+  }
+  if (l == 0) rstd[t] = r;
+}
+
+// Backward of route_prenorm given dxn = dL/dxn [T][H] bf16 (the router GEMM's dX): g = bf16(bf16(dxn H^-1/2) scale)
+// (the bf16 products' backward), then the RMSNorm backward in fp32: dh = g r - h r^3 sum(g h) / H.
+__global__ __launch_bounds__(256) void route_prenorm_bwd(const uint16_t* __restrict__ h,
+                                                         const uint16_t* __restrict__ scale,
+                                                         const float* __restrict__ rstd,
+                                                         const uint16_t* __restrict__ dxn, int T, int H, float hs,
+                                                         uint16_t* __restrict__ dh) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int l = lane_id();
+  const u32x4_t* hr = reinterpret_cast<const u32x4_t*>(h + t * H);
+  const u32x4_t* dr = reinterpret_cast<const u32x4_t*>(dxn + t * H);
+  const u32x4_t* sc = reinterpret_cast<const u32x4_t*>(scale);
+  const int nc = H / 8;
+  auto gval = [&](uint32_t d, uint32_t s, int hi_half) {
+    const float dv = hi_half ? bf_hi(d) : bf_lo(d), sv = hi_half ? bf_hi(s) : bf_lo(s);
+    return bf2f(f2bf(bf2f(f2bf(dv * hs)) * sv));
+  };
+  float dot = 0.f;
+  for (int c = l; c < nc; c += 64) {
+    const u32x4_t v = hr[c], d = dr[c], g = sc[c];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dot = fmaf(gval(d[j], g[j], 0), bf_lo(v[j]), dot);
+      dot = fmaf(gval(d[j], g[j], 1), bf_hi(v[j]), dot);
+    }
+  }
+  dot = wave_sum(dot);
+  const float r = rstd[t];
+  const float c3 = r * r * r * dot / (float)H;
+  u32x4_t* out = reinterpret_cast<u32x4_t*>(dh + t * H);
+  for (int c = l; c < nc; c += 64) {
+    const u32x4_t v = hr[c], d = dr[c], g = sc[c];
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack2bf(gval(d[j], g[j], 0) * r - bf_lo(v[j]) * c3, gval(d[j], g[j], 1) * r - bf_hi(v[j]) * c3);
+    out[c] = u32x4_t{o[0], o[1], o[2], o[3]};
+  }
 }
 
 __global__ __launch_bounds__(256) void dtopv_kernel(const float* __restrict__ dwp, int nblk,
@@ -292,7 +382,7 @@ extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint1
   route_logits_kernel<<<grid, 256, 0, stream>>>(x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
   route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K,
                                                             (int)((E + 31) / 32 * 32), probs, topv, topi, topi32,
-                                                            shared_gate_w ? sgate : nullptr);
+                                                            shared_gate_w ? sgate : nullptr, nullptr, nullptr);
   return smel::launch_status();
 }
 
@@ -305,19 +395,57 @@ extern "C" int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, i
   if (T == 0) return 0;
   SMEL_REQUIRE(logits && probs && topv && topi && topi32, SMEL_EINVAL, "route_logits: null pointer");
   route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)E, (int)T, (int)E, (int)K, 0, probs, topv,
-                                                            topi, topi32, nullptr);
+                                                            topi, topi32, nullptr, nullptr, nullptr);
   return smel::launch_status();
 }
 
 extern "C" int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs,
                               const int32_t* topi32, const uint16_t* topv, const float* sgate, int64_t T, int64_t K,
                               int64_t E, int64_t TK, uint16_t* dlogits, int64_t ldl, float* dtopv_out,
-                              hipStream_t stream) {
+                              const uint16_t* per_expert_scale, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && K <= 16 && E > 0 && nblk > 0, SMEL_EINVAL, "route_bwd: bad sizes");
   SMEL_REQUIRE(ldl >= E + (sgate ? 1 : 0), SMEL_EINVAL, "route_bwd: ldl %lld too small", (long long)ldl);
   if (T == 0) return 0;
-  SMEL_REQUIRE(dwp && inv && probs && topi32 && dlogits, SMEL_EINVAL, "route_bwd: null pointer");
+  SMEL_REQUIRE(dwp && probs && topi32 && dlogits, SMEL_EINVAL, "route_bwd: null pointer");
+  SMEL_REQUIRE(inv || TK == T * K, SMEL_EINVAL, "route_bwd: without inv, dwp rows are the T*K slots");
   route_bwd<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(dwp, (int)nblk, inv, probs, topi32, topv, sgate, (int)T,
-                                                         (int)K, (int)E, (int)TK, dlogits, (int)ldl, dtopv_out);
+                                                         (int)K, (int)E, (int)TK, dlogits, (int)ldl, dtopv_out,
+                                                         per_expert_scale);
+  return smel::launch_status();
+}
+
+extern "C" int smel_route_gemma4(const uint16_t* h, const uint16_t* router_scale, const uint16_t* proj_w,
+                                 const uint16_t* per_expert_scale, int64_t T, int64_t H, int64_t E, int64_t K,
+                                 float eps, float* probs, float* topv, int64_t* topi, int32_t* topi32, uint16_t* xn,
+                                 float* rstd, uint16_t* logits, hipStream_t stream) {
+  SMEL_REQUIRE(T >= 0 && H > 0 && E > 0 && K > 0, SMEL_EINVAL, "route_gemma4: bad sizes");
+  SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "route_gemma4: E=%lld > %d experts", (long long)E, MAXE);
+  SMEL_REQUIRE(K <= E && K <= 16, SMEL_EUNSUPPORTED, "route_gemma4: top_k=%lld must be <= min(E, 16)",
+               (long long)K);
+  SMEL_REQUIRE(H % 64 == 0, SMEL_EUNSUPPORTED, "route_gemma4: hidden %lld must be a multiple of 64", (long long)H);
+  SMEL_REQUIRE(T * H * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "route_gemma4: h larger than 2 GiB");
+  if (T == 0) return 0;
+  SMEL_REQUIRE(h && router_scale && proj_w && per_expert_scale && probs && topv && topi && topi32 && xn && rstd &&
+                   logits,
+               SMEL_EINVAL, "route_gemma4: null pointer");
+  const int64_t ldl = smel_route_ld(E, 0);
+  const unsigned tg = (unsigned)((T + 3) / 4);
+  // H^-1/2 as the reference's Python float (a double) rounded to fp32 for the bf16 product
+  route_prenorm<<<tg, 256, 0, stream>>>(h, router_scale, (int)T, (int)H, eps, (float)pow((double)H, -0.5), xn, rstd);
+  const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
+  route_logits_kernel<<<grid, 256, 0, stream>>>(xn, proj_w, nullptr, (int)T, (int)H, (int)E, (int)ldl, logits);
+  route_select<<<tg, 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K, 0, probs, nullptr, topi, topi32,
+                                       nullptr, topv, per_expert_scale);
+  return smel::launch_status();
+}
+
+extern "C" int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scale, const float* rstd,
+                                             const uint16_t* dxn, int64_t T, int64_t H, uint16_t* dh,
+                                             hipStream_t stream) {
+  SMEL_REQUIRE(T >= 0 && H > 0 && H % 8 == 0, SMEL_EINVAL, "route_gemma4_prenorm_bwd: bad sizes");
+  if (T == 0) return 0;
+  SMEL_REQUIRE(h && router_scale && rstd && dxn && dh, SMEL_EINVAL, "route_gemma4_prenorm_bwd: null pointer");
+  route_prenorm_bwd<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(h, router_scale, rstd, dxn, (int)T, (int)H,
+                                                                  (float)pow((double)H, -0.5), dh);
   return smel::launch_status();
 }

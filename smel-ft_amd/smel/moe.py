@@ -261,32 +261,35 @@ class _LoRABufs:
                L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu), L.stream())
 
 
-def _wset(ex: LayerExperts, which: str, sel_w: PackedW | None, sh_w: PackedW | None, ext_sel, ext_sh) -> L.WSet:
-    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights)."""
-    fz = ex.frozen
+def _bank_wset(fz, which: str) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of a frozen bank (packed weights)."""
     w = L.WSet()
     if isinstance(fz, Int4Experts):
         d = fz.gu if which == "gu" else fz.dn
         qf, szf = fz.packed(which)
         w.q4, w.sz4 = L.ptr(qf), L.ptr(szf)
         w.group = Int4Experts.group_of(d)
-        R = d["q"].shape[1]
-        C = d["q"].shape[2] * 2
+        w.R, w.C = d["q"].shape[1], d["q"].shape[2] * 2
     else:
         pw = fz.packed(which)
         w.wb = L.ptr(pw.t)
         w.group = 32
-        R, C = pw.R, pw.C
+        w.R, w.C = pw.R, pw.C
+    return w
+
+
+def _wset(ex: LayerExperts, which: str, sel_w: PackedW | None, sh_w: PackedW | None, ext_sel, ext_sh) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights)."""
+    w = _bank_wset(ex.frozen, which)
     w.wsel = L.ptr(sel_w.t) if sel_w is not None else None
     w.wsh = L.ptr(sh_w.t) if sh_w is not None else None
     w.ext_sel = L.ptr(ext_sel)
     w.ext_sh = L.ptr(ext_sh)
-    w.R, w.C = R, C
     return w
 
 
-def _check_bank(ex: LayerExperts):
-    fz = ex.frozen
+def _check_bank(ex):
+    fz = ex.frozen if isinstance(ex, LayerExperts) else ex
     if isinstance(fz, Int4Experts):
         for d in (fz.gu, fz.dn):
             for k in ("q", "scale", "zero"):
@@ -330,12 +333,11 @@ class _RouteFn(torch.autograd.Function):
         if dtopv is None:
             return None, None, None
         dwp = dtopv.float().contiguous().reshape(-1, 1)
-        ident = torch.arange(T * K, dtype=torch.int32, device=dev)
         wr = _router_ext_weight(gate_w, None)
         Epad = wr.R
         dl = torch.empty(T, Epad, dtype=torch.bfloat16, device=dev)
-        L.call("smel_route_bwd", L.ptr(dwp), 1, L.ptr(ident), L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
-               L.ptr(dl), Epad, None, L.stream())
+        L.call("smel_route_bwd", L.ptr(dwp), 1, None, L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
+               L.ptr(dl), Epad, None, None, L.stream())
         dx = _router_dx(dl, wr, T)
         return dx, None, None
 
@@ -358,17 +360,55 @@ def route(x2d, gate_w, top_k):
     return _RouteFn.apply(_bf16(x2d), _bf16(gate_w), int(top_k))
 
 
+class _RouteGemma4Fn(torch.autograd.Function):
+    """route_gemma4 (smel/moe.py:170-180): topv differentiable w.r.t. h through the per-expert scale, the renorm, the
+    softmax, the router GEMM and the weightless RMSNorm."""
+
+    @staticmethod
+    def forward(ctx, h, scale, proj, pes, top_k, eps):
+        T, H = h.shape
+        E = proj.shape[0]
+        dev = h.device
+        probs = torch.empty(T, E, dtype=torch.float32, device=dev)
+        topv = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+        topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+        topi32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+        xn = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        rstd = torch.empty(T, dtype=torch.float32, device=dev)
+        lg = torch.empty(T, L.load().smel_route_ld(E, 0), dtype=torch.bfloat16, device=dev)
+        L.call("smel_route_gemma4", L.ptr(h), L.ptr(scale), L.ptr(proj), L.ptr(pes), T, H, E, top_k, eps,
+               L.ptr(probs), L.ptr(topv), L.ptr(topi), L.ptr(topi32), L.ptr(xn), L.ptr(rstd), L.ptr(lg), L.stream())
+        ctx.save_for_backward(h, scale, proj, pes, probs, topi32, rstd)
+        ctx.mark_non_differentiable(probs, topi)
+        return probs, topv, topi
+
+    @staticmethod
+    def backward(ctx, dprobs, dtopv, dtopi):
+        if dtopv is None:
+            return None, None, None, None, None, None
+        h, scale, proj, pes, probs, topi32, rstd = ctx.saved_tensors
+        T, H = h.shape
+        E, K = probs.shape[1], topi32.shape[1]
+        dev = h.device
+        wr = _router_ext_weight(proj, None)
+        dl = torch.empty(T, wr.R, dtype=torch.bfloat16, device=dev)
+        dw = dtopv.float().contiguous()
+        L.call("smel_route_bwd", L.ptr(dw), 1, None, L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
+               L.ptr(dl), wr.R, None, L.ptr(pes), L.stream())
+        dxn = _router_dx(dl, wr, T)
+        dh = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        L.call("smel_route_gemma4_prenorm_bwd", L.ptr(h), L.ptr(scale), L.ptr(rstd), L.ptr(dxn), T, H, L.ptr(dh),
+               L.stream())
+        return dh, None, None, None, None, None
+
+
 def route_gemma4(h, W, top_k, eps):
-    """Gemma 4 router (smel/moe.py:170-180), torch ops on the GPU: weightless RMSNorm, router.scale, softmax, top-k,
-    renorm, per_expert_scale. Its HIP kernel is not built yet; this keeps the API whole for routed_experts callers."""
-    hf = h.float()
-    x = (hf * torch.pow(hf.pow(2).mean(-1, keepdim=True) + eps, -0.5)).type_as(h)
-    x = x * W["router.scale"] * h.shape[-1] ** -0.5
-    logits = F.linear(x, W["router.proj.weight"])
-    probs = torch.softmax(logits, dim=-1, dtype=torch.float32)
-    topv, topi = torch.topk(probs, top_k, dim=-1)
-    topv = topv / topv.sum(dim=-1, keepdim=True)
-    return probs, topv * W["router.per_expert_scale"][topi], topi
+    """Gemma 4 router on the residual stream (smel/moe.py:170-180) -> (probs fp32 [T,E], topv fp32 [T,K] =
+    renormalised top-k x per_expert_scale, topi int64 [T,K]): weightless RMSNorm, x router.scale x H^-0.5, logits,
+    softmax, top-k, renorm, scale, as HIP kernels (differentiable w.r.t. h)."""
+    L.require_device(h)
+    return _RouteGemma4Fn.apply(_bf16(h), _bf16(W["router.scale"]).reshape(-1), _bf16(W["router.proj.weight"]),
+                                _bf16(W["router.per_expert_scale"]).reshape(-1), int(top_k), float(eps))
 
 
 # ------------------------------------------------------------------------------------------------ fused layer
@@ -505,7 +545,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
         Epad = wr.R
         dl = bf(T, Epad)
         L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32), L.ptr(t["topv"]),
-               L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, st)
+               L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, None, st)
         dxr = _router_dx(dl, wr, T)
     else:
         dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
@@ -802,11 +842,95 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
     return _MoELayerFn.apply(x, plan, stats, *leaves)
 
 
-class FrozenExpertsFn:
-    """API name of the reference's frozen-expert autograd Function (smel/moe.py:120-143). The kernels of this
-    package fuse it into the grouped GEMMs of ``routed_experts`` / ``moe_forward``; calling it directly is not
-    supported."""
+def _count_tiles(counts: list, device):
+    """Tile list of 128-row tiles over contiguous row groups of the given (host) sizes: rows of group e are
+    [sum(counts[:e]), +counts[e]). Returns (tiles, n_tiles, max_tiles) as the grouped GEMMs take them."""
+    tl, row = [], 0
+    for e, c in enumerate(counts):
+        for r0 in range(row, row + c, M_TILE):
+            tl.append((e, r0, min(row + c, r0 + M_TILE), 0))
+        row += c
+    n = len(tl)
+    t = torch.tensor(tl or [(0, 0, 0, 0)], dtype=torch.int32).reshape(-1).to(device)
+    return t, torch.tensor([n], dtype=torch.int32).to(device), n
+
+
+def _bank_gkind(bank, device) -> torch.Tensor:
+    """Group kinds of a bare frozen bank: group e = expert e of the bank."""
+    cache = bank.__dict__.setdefault("_gkind_plain", {})
+    if str(device) not in cache:
+        kind = L.KIND_INT4 if isinstance(bank, Int4Experts) else L.KIND_BF16
+        cache[str(device)] = torch.tensor([(kind << 16) | e for e in range(bank.num_experts)], dtype=torch.int32,
+                                          device=device)
+    return cache[str(device)]
+
+
+class FrozenExpertsFn(torch.autograd.Function):
+    """Frozen experts over rows already sorted by expert (smel/moe.py:110-143): ``apply(xs, counts, bank, group,
+    act_name)`` with ``counts`` the host list of rows per expert. Forward = the grouped gate_up GEMM (int4 dequant in
+    registers or bf16 bank, act-gate epilogue) and the grouped down GEMM; backward = the down-backward GEMM fused with
+    the act-gate backward and the gate_up-backward GEMM (weights re-dequantized, no weight gradients). ``group`` (the
+    reference's experts-dequantized-at-once knob) is accepted and not needed. The gate/up pre-activations are kept
+    from the forward (bf16, the values the reference recomputes) instead of being recomputed."""
 
     @staticmethod
-    def apply(*args, **kwargs):
-        raise NotImplementedError("FrozenExpertsFn is fused into routed_experts / moe_forward on MI355X")
+    def forward(ctx, xs, counts, bank, group, act_name="silu"):
+        if act_name not in _ACT:
+            raise ValueError(f"unknown activation {act_name}")
+        L.require_device(xs)
+        _check_bank(bank)
+        xs = _bf16(xs)
+        counts = [int(c) for c in counts]
+        rows, H = xs.shape
+        if len(counts) != bank.num_experts or sum(counts) != rows or min(counts, default=0) < 0:
+            raise ValueError(f"FrozenExpertsFn: counts (sum {sum(counts)}, {len(counts)} experts) do not match "
+                             f"xs rows {rows} / bank experts {bank.num_experts}")
+        dev = xs.device
+        st = L.stream()
+        w_gu, w_dn = _bank_wset(bank, "gu"), _bank_wset(bank, "dn")
+        I = w_dn.C
+        bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+        out = bf(rows, H)
+        ctx.plan = None
+        if rows == 0:
+            return out
+        tiles, ntiles, maxt = _count_tiles(counts, dev)
+        gk = _bank_gkind(bank, dev)
+        actb, hsave = bf(rows, I), bf(rows, 2 * I)
+        L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(xs), H, rows,
+               0, None, 0, 1, None, 1, _ACT[act_name], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_frozen_gu_fwd")
+        L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, rows,
+               0, None, 0, 1, None, 0, _ACT[act_name], L.ptr(out), H, None, st, tag="gemm_frozen_dn_fwd")
+        ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, act_name)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        if ctx.plan is None:
+            return torch.zeros_like(dy), None, None, None, None
+        bank, tiles, ntiles, maxt, gk, hsave, act_name = ctx.plan
+        ctx.plan = None
+        dy = _bf16(dy)
+        rows, H = dy.shape
+        dev = dy.device
+        st = L.stream()
+        w_gu, w_dn = _bank_wset(bank, "gu"), _bank_wset(bank, "dn")
+        I = w_dn.C
+        nblk = L.load().smel_gmm_bwd_nblocks(I)
+        dh = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=dev)
+        dwp = torch.empty(rows, nblk, dtype=torch.float32, device=dev)
+        ones = torch.ones(rows, dtype=torch.float32, device=dev)    # row weight 1 (no combine weight here)
+        L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, rows, 0,
+               None, 0, 1, None, 1, _ACT[act_name], L.ptr(hsave), None, L.ptr(ones), L.ptr(dh), 2 * I, L.ptr(dwp),
+               st, tag="gemm_frozen_dn_bwd")
+        dx = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
+        L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I,
+               rows, 0, None, 0, 1, None, 0, _ACT[act_name], None, None, None, L.ptr(dx), H, None, st,
+               tag="gemm_frozen_gu_bwd")
+        return dx, None, None, None, None
+
+
+def frozen_experts_forward(xs, counts, bank, group, act_name="silu"):
+    """smel/moe.py:110-117 (no autograd)."""
+    with torch.no_grad():
+        return FrozenExpertsFn.apply(xs, counts, bank, group, act_name)

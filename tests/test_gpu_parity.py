@@ -435,3 +435,114 @@ def test_gelu_experts_parity():
     assert_close_bf16(xg.grad.cpu(), xo.grad, "dx")
     for n in LORA_NAMES:
         assert_close_bf16(getattr(lora.experts, n).grad.cpu(), leaves[n].grad, n)
+
+
+@pytest.mark.parametrize("int4,act_name,counts", [
+    (True, "silu", [9, 0, 12, 7, 15, 7]),                        # the reference's own counts (test_gemma4.py:157)
+    (False, "gelu_tanh", [9, 0, 12, 7, 15, 7]),
+    (True, "silu", [0, 300, 1, 129, 0, 0, 64, 128]),              # tiles split at 128 rows, empty experts
+    (True, "gelu_tanh", [0, 0, 0, 0, 0, 0]),                      # no rows at all
+])
+def test_frozen_experts_fn(int4, act_name, counts):
+    """FrozenExpertsFn.apply(xs, counts, bank, group, act) (smel/moe.py:120-143) on rows sorted by expert, forward
+    and dX, against the oracle's restatement of the reference's per-group dequant / recompute backward."""
+    from smel.moe import FrozenExpertsFn
+    E = len(counts)
+    _say(f"FrozenExpertsFn int4={int4} {act_name} counts={counts}")
+    _, ol = R.make_layer(T=8, H=128, E=E, I=64, K=1, int4=int4, act_name=act_name, seed=11)
+    _, bank_dev, _ = to_device_layer(ol, DEV)
+    bank = bank_dev.frozen
+    N = sum(counts)
+    gen = torch.Generator().manual_seed(N + E)
+    xs = torch.randn(N, 128, generator=gen).to(torch.bfloat16)
+    gy = (torch.randn(N, 128, generator=gen) * 1e-2).to(torch.bfloat16)
+    xg = xs.to(DEV).requires_grad_(True)
+    y = FrozenExpertsFn.apply(xg, counts, bank, 2, act_name)
+    y.backward(gy.to(DEV))
+    torch.cuda.synchronize()
+    assert y.shape == (N, 128) and xg.grad.shape == (N, 128)
+    if N == 0:
+        return
+    xo = xs.float().requires_grad_(True)
+    yo = R._FrozenExperts.apply(xo, counts, ol, torch.float32)
+    yo.backward(gy.float())
+    assert_close_bf16(y.detach().cpu(), yo.detach(), "y")
+    assert_close_bf16(xg.grad.cpu(), xo.grad, "dx")
+
+
+# ------------------------------------------------------------------------------------------------- Gemma 4 router
+
+
+def _gemma_router_inputs(T, H, E, seed):
+    gen = torch.Generator().manual_seed(seed)
+    h = (torch.randn(T, H, generator=gen) * 3.0).to(torch.bfloat16)                 # residual stream
+    W = {"router.scale": (1.0 + 0.2 * torch.randn(H, generator=gen)).to(torch.bfloat16),   # tiny.py:74-77
+         "router.proj.weight": (torch.randn(E, H, generator=gen) * 0.5).to(torch.bfloat16),
+         "router.per_expert_scale": (0.5 + torch.rand(E, generator=gen)).to(torch.bfloat16)}
+    return h, W
+
+
+@pytest.mark.parametrize("T,H,E,K", [(4096, 2816, 128, 8), (128, 64, 8, 2), (333, 256, 32, 4), (1, 128, 256, 16)])
+def test_route_gemma4_forward(T, H, E, K):
+    """smel_route_gemma4 (smel/moe.py:170-180): the router input xn against the oracle's bf16 roundings (at most two
+    bf16 ulps apart, where the fp32 rstd of the two differs in its last bits), the logits within bf16 tolerance, and
+    probs / topv / ids bit-for-bit what the oracle's selection gives on the kernel's own logits."""
+    L = _lib()
+    _say(f"route_gemma4 T{T} H{H} E{E} K{K}")
+    eps = 1e-6
+    h, W = _gemma_router_inputs(T, H, E, T + H)
+    d = {k: v.to(DEV) for k, v in W.items()}
+    hd = h.to(DEV)
+    f = lambda *s, dt=torch.float32: torch.empty(*s, dtype=dt, device=DEV)
+    probs, topv, topi, topi32 = f(T, E), f(T, K), f(T, K, dt=torch.int64), f(T, K, dt=torch.int32)
+    xn, rstd = f(T, H, dt=torch.bfloat16), f(T)
+    ldl = L.load().smel_route_ld(E, 0)
+    lg = f(T, ldl, dt=torch.bfloat16)
+    L.call("smel_route_gemma4", L.ptr(hd), L.ptr(d["router.scale"]), L.ptr(d["router.proj.weight"]),
+           L.ptr(d["router.per_expert_scale"]), T, H, E, K, eps, L.ptr(probs), L.ptr(topv), L.ptr(topi),
+           L.ptr(topi32), L.ptr(xn), L.ptr(rstd), L.ptr(lg), L.stream())
+    torch.cuda.synchronize()
+    # router input: the oracle's expression on the CPU
+    hf = h.float()
+    r = torch.pow(hf.pow(2).mean(-1, keepdim=True) + eps, -0.5)
+    xo = (hf * r).to(torch.bfloat16) * W["router.scale"] * H ** -0.5
+    assert torch.allclose(rstd.cpu(), r[:, 0], rtol=1e-6, atol=0)
+    diff = (xn.cpu().float() - xo.float()).abs()
+    ulp = xo.float().abs() * 2 ** -6
+    assert bool((diff <= ulp + 1e-30).all())
+    assert (diff > 0).float().mean().item() < 1e-3
+    # logits of the kernel's own xn: fp32-accumulated dot products, rounded once
+    lref = (xn.cpu().double() @ W["router.proj.weight"].double().t())
+    glog = lg.cpu().float()[:, :E]
+    assert torch.allclose(glog.double(), lref, rtol=1e-2, atol=1e-2)
+    # selection on identical logits: the oracle's softmax / top-k / renorm / per-expert scale
+    po = torch.softmax(glog, -1, dtype=torch.float32)
+    vo, io = R.topk_lowest_index(po, K)
+    assert torch.equal(topi.cpu(), io) and torch.equal(topi32.cpu().long(), io)
+    to = vo / vo.sum(-1, keepdim=True) * W["router.per_expert_scale"][io]
+    assert torch.allclose(probs.cpu(), po, rtol=1e-5, atol=1e-7)
+    assert torch.allclose(topv.cpu(), to, rtol=1e-5, atol=1e-7)
+
+
+def test_route_gemma4_backward():
+    """route_gemma4 through the API: d topv flows back to h through the per-expert scale, renorm, softmax, router
+    GEMM, the two bf16 scalings and the weightless RMSNorm; vs fp32 autograd of the reference formula, same ids."""
+    from smel.moe import route_gemma4
+    _say("route_gemma4 backward")
+    T, H, E, K, eps = 200, 256, 32, 4, 1e-6
+    h, W = _gemma_router_inputs(T, H, E, 21)
+    hg = h.to(DEV).requires_grad_(True)
+    probs, topv, topi = route_gemma4(hg, {k: v.to(DEV) for k, v in W.items()}, K, eps)
+    assert topv.dtype == torch.float32 and probs.dtype == torch.float32 and topi.dtype == torch.int64
+    cot = torch.randn(T, K, generator=torch.Generator().manual_seed(3))
+    (topv * cot.to(DEV)).sum().backward()
+    ho = h.float().requires_grad_(True)
+    r = torch.pow(ho.pow(2).mean(-1, keepdim=True) + eps, -0.5)
+    x = ho * r * W["router.scale"].float() * H ** -0.5
+    po = torch.softmax(x @ W["router.proj.weight"].float().t(), -1)
+    ti = topi.cpu()
+    sel = po.gather(1, ti)
+    tvo = sel / sel.sum(-1, keepdim=True) * W["router.per_expert_scale"].float()[ti]
+    (tvo * cot).sum().backward()
+    assert torch.allclose(topv.detach().cpu(), tvo.detach(), rtol=3e-2, atol=1e-3)
+    assert_close_bf16(hg.grad.cpu(), ho.grad, "dh", rel=3e-2, cos=0.999)
