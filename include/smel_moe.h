@@ -30,18 +30,19 @@ extern "C" {
 #define SMEL_KIND_SHARED 3 /* shared expert (bf16 + LoRA), index 0                                 */
 
 /* Weights of one projection (gate_up or down) for every group kind. A matrix is [R][C] in the reference
- * (gate_up: R = 2I, C = H; down: R = H, C = I; R a multiple of 32); the GEMMs read it in the fragment layout written
- * by smel_pack_int4 / smel_pack_bf16 (below), one matrix after the other for a stacked bank. The forward GEMM
- * contracts over C (out = x W^T), the backward GEMM over R (dx = dy W). */
+ * (gate_up: R = 2I, C = H; down: R = H, C = I; R a multiple of 32). The forward GEMM contracts over C (out = x W^T)
+ * and reads the fragment layout of smel_pack_int4 / smel_pack_bf16; the backward GEMM contracts over R (dx = dy W)
+ * and reads the transposed fragment layout of smel_pack_int4_t / smel_pack_bf16_t (below), one matrix after the
+ * other for a stacked bank. */
 typedef struct smel_wset {
-  const uint8_t* q4;   /* int4 bank [E][R][C] packed by smel_pack_int4 (q operand)                     */
+  const uint8_t* q4;   /* int4 bank [E][R][C] packed by smel_pack_int4 (forward) / _int4_t (backward)   */
   const uint32_t* sz4; /* its scale/zero, packed by the same call                                      */
-  const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down), smel_pack_bf16            */
+  const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down), smel_pack_bf16(_t)        */
   const uint16_t* wsel;/* selected experts [n_sel][R][C] (LayerExperts.sel_gate_up / sel_down), packed  */
   const uint16_t* wsh; /* shared expert [R][C], packed                                                 */
   /* LoRA as a 32-wide K-extension of the GEMM (0-padded rank <= 16, built by smel_lora_prep):
    *   forward  ext_*: [n][R][32]  (B factor per output row; gate_up: B_gate in cols 0..15, B_up in 16..31)
-   *   backward ext_*: [n][32][C]  (A factor rows; gate_up: A_gate rows 0..15, A_up rows 16..31) */
+   *   backward ext_*: [n][C][32]  (A factor per output column; gate_up: A_gate in 0..15, A_up in 16..31) */
   const uint16_t* ext_sel;
   const uint16_t* ext_sh;
   int64_t R, C;
@@ -76,6 +77,24 @@ int smel_pack_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero
                    int64_t group, uint8_t* qf, uint32_t* szf, hipStream_t stream);
 /* w [rows][ld] bf16 (first K columns used) -> wf (SMEL_PACK_BF16). K and ld multiples of 8. */
 int smel_pack_bf16(const uint16_t* w, int64_t rows, int64_t K, int64_t ld, uint16_t* wf, hipStream_t stream);
+
+/* Transposed fragment layouts, read by smel_gmm_bwd (no counterpart in the reference either; the same source tensors,
+ * one more derived copy per frozen bank, int4 stays int4). For n_mats matrices [R][C] (the contraction runs over R):
+ * with p = a pair of 32 columns, ks = a 64-row step, lane l = 16 kq + i, substep s, 16-column fragment fr:
+ *   SMEL_PACK_Q4   block (mat, p, ks) 1 KB:  lane chunk word 2 fr + s = the 8 nibbles (low first) of column
+ *                                             32 p + 16 fr + i at rows 64 ks + 32 s + 8 kq + [0, 8)
+ *   SMEL_PACK_SZ   block (mat, g, ks) 256 B: word 16 kq + 8 s + t = scale | zero << 16 of row 64 ks + 32 s + 8 kq + t
+ *                                             in column group g (C / group groups)
+ *   SMEL_PACK_BF16 block (mat, p, ks, 2 fr + s) 1 KB: lane chunk = the 8 bf16 of that column at those rows
+ * Rows >= R are zero. smel_packed_t_bytes gives the size of each (-1 for a bad argument). */
+int64_t smel_packed_t_bytes(int32_t what, int64_t n_mats, int64_t R, int64_t C, int64_t group);
+/* q [n_mats][R][C/2], scale/zero [n_mats][R][C/group] -> qt, szt. C a multiple of 32, group a multiple of 32
+ * dividing C. */
+int smel_pack_int4_t(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t n_mats, int64_t R,
+                     int64_t C, int64_t group, uint8_t* qt, uint32_t* szt, hipStream_t stream);
+/* w [n_mats][R][ld] bf16 (first C columns) -> wt. C a multiple of 32. */
+int smel_pack_bf16_t(const uint16_t* w, int64_t n_mats, int64_t R, int64_t C, int64_t ld, uint16_t* wt,
+                     hipStream_t stream);
 
 /* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
  * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the
@@ -128,15 +147,17 @@ int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared_rows, int3
  * For n groups (n_sel selected slots, or 1 for the shared MLP) with rank r <= 16, hidden Hd, inter In, scale s:
  *   fwd_gu  [n][2In][32]: B_gate in cols 0..r-1 of rows 0..In-1, B_up in cols 16..16+r-1 of rows In..2In-1
  *   fwd_dn  [n][Hd][32] : B_down in cols 0..r-1
- *   a_gu    [n][32][Hd] : A_gate rows 0..r-1, A_up rows 16..16+r-1   (XA = x a_gu^T; backward ext of gate_up)
- *   a_dn    [n][32][In] : A_down rows 0..r-1                        (AD = act a_dn^T; backward ext of down)
+ *   a_gu    [n][32][Hd] : A_gate rows 0..r-1, A_up rows 16..16+r-1   (XA = x a_gu^T)
+ *   a_dn    [n][32][In] : A_down rows 0..r-1                        (AD = act a_dn^T)
  *   bt_dn   [n][32][Hd] : B_down^T rows 0..r-1                       (DB = dy bt_dn^T)
  *   bt_gu   [n][32][2In]: B_gate^T in rows 0..r-1 / cols 0..In-1, B_up^T in rows 16.. / cols In..2In-1
+ *   at_gu   [n][Hd][32] : a_gu transposed (backward ext of gate_up)
+ *   at_dn   [n][In][32] : a_dn transposed (backward ext of down)
  * Every other entry is 0. */
 int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, const float* B_up,
                    const float* A_down, const float* B_down, int64_t n, int64_t r, int64_t Hd, int64_t In,
                    uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
-                   uint16_t* bt_gu, hipStream_t stream);
+                   uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn, hipStream_t stream);
 
 /* ---- (A11/A12) LoRA down-projections of the rows of LoRA groups (SEL / SHARED tiles of the tile list):
  * ext[row][0:32] = bf16(scale_g * A_src[src(row)][0:Kd] . wcat_g[0:32][0:Kd]) where src(row) = token of the row if
@@ -164,8 +185,9 @@ int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
 int smel_combine(const uint16_t* Y, const uint16_t* topv, const float* sgate, int64_t T, int64_t K, int64_t H,
                  uint16_t* out, hipStream_t stream);
 
-/* ---- (A10/A11 backward) grouped GEMM, backward: acc = A W per group (contraction over w.R), int4 re-dequantized
- * per group, plus ext[row] . w.ext_*[0:32][n] for SEL/SHARED groups when ext != NULL.
+/* ---- (A10/A11 backward) grouped GEMM, backward: acc = A W per group (contraction over w.R), W in the transposed
+ * layouts (smel_pack_int4_t / smel_pack_bf16_t), int4 re-dequantized in registers, plus ext[row] . w.ext_*[n][0:32]
+ * for SEL/SHARED groups when ext != NULL. acc is rounded to bf16 before the epilogue (the reference's bf16 GEMM output).
  * epilogue 0: out[slot(row)][n] = bf16(acc), n < C                                   (dX of gate_up: dh W_gu)
  * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] or sgate[t]; (g, u) = hsave[row];
  *             out[row][n] = bf16(da u act'(g)), out[row][I+n] = bf16(da act(g));

@@ -107,6 +107,87 @@ __global__ __launch_bounds__(256) void pack_bf16(const uint16_t* __restrict__ w,
   }
 }
 
+// ---- transposed fragment layouts (the backward GEMM's weight operand: contraction over the matrix's rows R, output
+// columns C; v_mfma_f32_16x16x32_bf16 with lane l = 16 kq + i holding column i of a 16-column fragment and, in
+// substep s of a 64-row step, rows k = 32 s + 8 kq + [0, 8)):
+//   int4 q : block (e, p, ks) = 1 KB, column pair p = 32 columns; lane chunk = 4 words, word (2 fr + s) = the 8
+//            nibbles (row order, low nibble first) of column 32 p + 16 fr + i at rows 64 ks + 32 s + 8 kq + [0, 8)
+//   sz     : block (e, g, ks) = 256 B, group g of C; word 16 kq + 8 s + t = scale | zero << 16 of row
+//            64 ks + 32 s + 8 kq + t (a lane reads the 64 B of its kq)
+//   bf16   : block (e, p, ks, 2 fr + s) = 1 KB; lane chunk = the 8 bf16 of column 32 p + 16 fr + i at those rows
+// Rows >= R and columns >= C are zero.
+
+__global__ __launch_bounds__(256) void pack_q4_t(const uint8_t* __restrict__ q, int64_t R, int64_t C, int64_t np,
+                                                 int64_t nks, u32x4_t* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t lane = i & 63, blk = i >> 6;
+    const int64_t ks = blk % nks, ep = blk / nks;
+    const int64_t p = ep % np, e = ep / np;
+    const int kq = (int)(lane >> 4), li = (int)(lane & 15);
+    uint32_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int fr = j >> 1, sub = j & 1;
+      const int64_t col = 32 * p + 16 * fr + li;
+      const int64_t k0 = 64 * ks + 32 * sub + 8 * kq;
+      uint32_t word = 0;
+      if (col < C) {
+        for (int t = 0; t < 8; ++t) {
+          const int64_t k = k0 + t;
+          if (k < R) {
+            const uint32_t b = q[(e * R + k) * (C / 2) + col / 2];
+            word |= ((col & 1) ? (b >> 4) : (b & 15u)) << (4 * t);
+          }
+        }
+      }
+      v[j] = word;
+    }
+    out[i] = u32x4_t{v[0], v[1], v[2], v[3]};
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_sz_t(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
+                                                 int64_t R, int64_t G, int64_t nks, uint32_t* __restrict__ out,
+                                                 int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t pos = i & 63, blk = i >> 6;
+    const int64_t ks = blk % nks, eg = blk / nks;
+    const int64_t g = eg % G, e = eg / G;
+    const int64_t kq = pos >> 4, sub = (pos >> 3) & 1, t = pos & 7;
+    const int64_t k = 64 * ks + 32 * sub + 8 * kq + t;
+    uint32_t v = 0;
+    if (k < R) {
+      const int64_t gi = (e * R + k) * G + g;
+      v = (uint32_t)s[gi] | ((uint32_t)z[gi] << 16);
+    }
+    out[i] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_bf16_t(const uint16_t* __restrict__ w, int64_t R, int64_t C, int64_t ld,
+                                                   int64_t np, int64_t nks, u32x4_t* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t lane = i & 63, blk = i >> 6;
+    const int j = (int)(blk & 3);
+    const int64_t pk = blk >> 2;
+    const int64_t ks = pk % nks, ep = pk / nks;
+    const int64_t p = ep % np, e = ep / np;
+    const int fr = j >> 1, sub = j & 1;
+    const int kq = (int)(lane >> 4), li = (int)(lane & 15);
+    const int64_t col = 32 * p + 16 * fr + li;
+    const int64_t k0 = 64 * ks + 32 * sub + 8 * kq;
+    uint32_t v[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint32_t lo = 0, hi = 0;
+      if (col < C && k0 + 2 * t < R) lo = w[(e * R + k0 + 2 * t) * ld + col];
+      if (col < C && k0 + 2 * t + 1 < R) hi = w[(e * R + k0 + 2 * t + 1) * ld + col];
+      v[t] = lo | (hi << 16);
+    }
+    out[i] = u32x4_t{v[0], v[1], v[2], v[3]};
+  }
+}
+
 inline int pack_blocks(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 256 * 64); }
 
 }  // namespace
@@ -120,6 +201,45 @@ extern "C" int64_t smel_packed_bytes(int32_t what, int64_t rows, int64_t K) {
     case SMEL_PACK_BF16: return nf * nks * 4096;
     default: return -1;
   }
+}
+
+extern "C" int64_t smel_packed_t_bytes(int32_t what, int64_t n_mats, int64_t R, int64_t C, int64_t group) {
+  if (n_mats < 0 || R <= 0 || C <= 0) return -1;
+  const int64_t np = (C + 31) / 32, nks = (R + 63) / 64;
+  switch (what) {
+    case SMEL_PACK_Q4: return n_mats * np * nks * 1024;
+    case SMEL_PACK_SZ: return (group > 0 && C % group == 0) ? n_mats * (C / group) * nks * 256 : -1;
+    case SMEL_PACK_BF16: return n_mats * np * nks * 4096;
+    default: return -1;
+  }
+}
+
+extern "C" int smel_pack_int4_t(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t n_mats,
+                                int64_t R, int64_t C, int64_t group, uint8_t* qt, uint32_t* szt, hipStream_t stream) {
+  SMEL_REQUIRE(n_mats >= 0 && R > 0 && C > 0 && group > 0 && C % 32 == 0 && C % group == 0 && group % 32 == 0,
+               SMEL_EUNSUPPORTED, "pack_int4_t: C=%lld, group=%lld (C a multiple of 32, group a multiple of 32 "
+               "dividing C)", (long long)C, (long long)group);
+  if (n_mats == 0) return 0;
+  SMEL_REQUIRE(q && scale && zero && qt && szt, SMEL_EINVAL, "pack_int4_t: null pointer");
+  SMEL_REQUIRE((uintptr_t)qt % 16 == 0, SMEL_EUNSUPPORTED, "pack_int4_t: qt must be 16-byte aligned");
+  const int64_t np = C / 32, nks = (R + 63) / 64, G = C / group;
+  const int64_t nq = n_mats * np * nks * 64, nsz = n_mats * G * nks * 64;
+  pack_q4_t<<<pack_blocks(nq), 256, 0, stream>>>(q, R, C, np, nks, reinterpret_cast<u32x4_t*>(qt), nq);
+  pack_sz_t<<<pack_blocks(nsz), 256, 0, stream>>>(scale, zero, R, G, nks, szt, nsz);
+  return smel::launch_status();
+}
+
+extern "C" int smel_pack_bf16_t(const uint16_t* w, int64_t n_mats, int64_t R, int64_t C, int64_t ld, uint16_t* wt,
+                                hipStream_t stream) {
+  SMEL_REQUIRE(n_mats >= 0 && R > 0 && C > 0 && C % 32 == 0 && ld >= C, SMEL_EUNSUPPORTED,
+               "pack_bf16_t: C=%lld, ld=%lld (C a multiple of 32, ld >= C)", (long long)C, (long long)ld);
+  if (n_mats == 0) return 0;
+  SMEL_REQUIRE(w && wt, SMEL_EINVAL, "pack_bf16_t: null pointer");
+  SMEL_REQUIRE((uintptr_t)wt % 16 == 0, SMEL_EUNSUPPORTED, "pack_bf16_t: wt must be 16-byte aligned");
+  const int64_t np = C / 32, nks = (R + 63) / 64;
+  const int64_t n = n_mats * np * nks * 4 * 64;
+  pack_bf16_t<<<pack_blocks(n), 256, 0, stream>>>(w, R, C, ld, np, nks, reinterpret_cast<u32x4_t*>(wt), n);
+  return smel::launch_status();
 }
 
 extern "C" int smel_pack_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t rows, int64_t K,

@@ -1,28 +1,36 @@
 // Grouped expert GEMM, backward (acc = A W per group, contraction over the weight's row dim): dA of the down
 // projection (fused with the SiLU-gate backward, the d(combine weight) partials and the topv / shared-gate scaling)
-// and dX of the gate_up projection. Frozen int4 experts are re-dequantized group by group; the int4 groups run along
-// the output columns here, so each 64-row step of the weight is dequantized cooperatively into LDS, transposed to
-// k-contiguous bf16 for the MFMA B operand. Reference: FrozenExpertsFn.backward, smel/moe.py:128-143, and the
-// autograd of _selected_expert / lora_gate_up / lora_linear / the combine, smel/moe.py:204-252, smel/lora.py:61-83.
+// and dX of the gate_up projection. Frozen int4 experts are re-dequantized step by step in registers. Reference:
+// FrozenExpertsFn.backward, smel/moe.py:128-143, and the autograd of _selected_expert / lora_gate_up / lora_linear /
+// the combine, smel/moe.py:204-252, smel/lora.py:61-83.
 //
-// Block = 4 waves in a 2 x 2 grid, tile = up to 128 rows x 128 columns, each wave 64 rows (2 slices of 32) x 64
-// columns (2 fragments). Per 64-row step of W (one barrier per step):
-//  * A rows (gathered by token for the down projection) go global -> LDS by LDS-DMA into a ring of 3 stages,
-//    2 steps ahead;
-//  * W is read from the fragment layout of smel_pack_int4 / smel_pack_bf16 into registers 3 steps ahead; one step
-//    ahead of its use, every thread dequantizes a row pair x 16 columns and writes them transposed (a 32-bit word =
-//    the two rows of one column) into one of two W^T buffers [column][k];
-//  * vmcnt retires in issue order: each step issues W before A and waits for exactly what the step uses.
+// The weights come in the transposed fragment layout of smel_pack_int4_t / smel_pack_bf16_t, so every wave streams its
+// own 64 output columns straight into registers (one 16-B load per lane, column pair and 64-row step for int4) and
+// dequantizes them there, as the forward kernel does; the int4 scale / zero vary along the contraction here, so each
+// lane needs one (scale, zero) word per row it holds: those 64-word runs go global -> LDS by LDS-DMA beside the A rows.
+//
+// Block = 4 waves, tile = up to 128 rows of one group (4 slices of 32) x 256 columns (64 per wave).
+// MFMA v_mfma_f32_16x16x32_bf16: lane l = 16 kq + i carries, in substep s of a 64-wide k-step, k = 32 s + 8 kq +
+// [0, 8) for A and B alike (so a lane needs 16 scale/zero words per k-step, not 32 as with 32x32x16), and
+// accumulates D[4 kq + r][i]. Per k-step:
+//  * A rows (gathered by token for the down projection) go global -> LDS (16-B LDS-DMA) into a ring of 4 stages,
+//    XOR-swizzled as in the forward kernel; each wave DMAs its own scale/zero words (4 B per lane) into the stage;
+//  * weights run 3 k-steps ahead (int4: a 4-deep register ring of 2 loads; bf16: 1 step ahead, 8 loads);
+//  * vmcnt retires in issue order: each step issues its weight loads before its LDS-DMAs and waits for exactly the
+//    loads of the step it is about to use.
 #include "abi_util.h"
 #include "common.h"
 
 namespace {
 
 constexpr int MT = 128;
-constexpr int NT = 128;
 constexpr int KT = 64;
-constexpr int A_STAGE = MT * KT;   // bf16 elements of one A stage
-constexpr int B_STAGE = NT * KT;   // bf16 elements of one W^T buffer: column n at n * KT
+constexpr int NB = 256;            // output columns per block
+constexpr int A_BYTES = MT * KT * 2;         // A rows of one stage
+constexpr int Q_BYTES = 4 * 2 * 1024;        // int4 q of one stage: 4 waves x 2 column pairs
+constexpr int Z_BYTES = 4 * 2 * 256;         // scale/zero of one stage: 4 waves x 2 groups x 64 rows
+constexpr int Q_STAGE = A_BYTES + Q_BYTES + Z_BYTES;
+constexpr int SMEM_BYTES = 3 * Q_STAGE > 4 * A_BYTES ? 3 * Q_STAGE : 4 * A_BYTES;
 
 struct BwdArgs {
   smel_wset w;
@@ -45,115 +53,83 @@ struct BwdArgs {
   int nblk;    // column blocks per tile
 };
 
-// Raw W data of one thread for one step, rows (ka, ka+1) x 16 columns: bf16 in v[row][0..1] (8 columns each), or
-// int4: v[row][0] = the row's 16-B lane chunk of q (32 columns, this thread's 16 in words 2 hq, 2 hq + 1) and
-// v[row][1] = its 16-B chunk of packed scale/zero (this k-step's word at index cks % 4).
-struct WRegs {
-  u32x4_t v[2][2];
-};
+SMEL_DEV f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
 
-template <int EPI, int NSW>
-SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
-                       uint16_t* S2, uint16_t* B0, uint16_t* B1) {
-  const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
+// 8 nibbles of one word (rows k0 .. k0+7, low nibble first) with per-row scale sc[t] / zero ze[t] -> 4 packed bf16
+// pairs in row order, w = RNE(q*s + z) with fp32 arithmetic (the reference's dequant value).
+SMEL_DEV void dq8r(uint32_t b, const float* sc, const float* ze, uint32_t out[4]) {
+  const uint32_t lo = b & 0x0f0f0f0fu;          // rows 0,2,4,6
+  const uint32_t hi = (b >> 4) & 0x0f0f0f0fu;   // rows 1,3,5,7
+  out[0] = pack2bf(fmaf(ub0(lo), sc[0], ze[0]), fmaf(ub0(hi), sc[1], ze[1]));
+  out[1] = pack2bf(fmaf(ub1(lo), sc[2], ze[2]), fmaf(ub1(hi), sc[3], ze[3]));
+  out[2] = pack2bf(fmaf(ub2(lo), sc[4], ze[4]), fmaf(ub2(hi), sc[5], ze[5]));
+  out[3] = pack2bf(fmaf(ub3(lo), sc[6], ze[6]), fmaf(ub3(hi), sc[7], ze[7]));
+}
+
+// 4-byte-per-lane LDS-DMA: lane i writes bytes [4 i, 4 i + 4) after the wave-uniform LDS address.
+SMEL_DEV void ld4_lds(rsrc_t r, const void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(lds), 4, off, 0, 0, 0);
+}
+
+template <int EPI, bool Q4, int NS, bool SZ2>
+SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint8_t* smem) {
+  // LDS rings. int4: 3 stages of [A rows 16 KB | q of 4 waves x 2 column pairs, 8 KB | scale/zero of 4 waves x 2
+  // groups, 2 KB]. bf16: 4 stages of A rows (the weights go to registers). The epilogue reuses the first 64 KB.
+  auto St = [&](int st) {
+    return reinterpret_cast<uint16_t*>(smem + st * (Q4 ? Q_STAGE : A_BYTES));
+  };
+  auto Qt = [&](int st) { return smem + st * Q_STAGE + A_BYTES; };
+  auto Zt = [&](int st) { return reinterpret_cast<uint32_t*>(smem + st * Q_STAGE + A_BYTES + Q_BYTES); };
+  auto Et = [&](int m) { return reinterpret_cast<uint16_t*>(smem + m * A_BYTES); };
+  const int tid = threadIdx.x, l = lane_id(), kq = l >> 4, li = l & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = w >> 1, wc = w & 1;   // this wave: tile rows [64 wr, +64), columns [64 wc, +64)
-  const int n0 = nb * NT;
-  const int Kd = a.Kd;
+  const int Kd = a.Kd, N = a.N;
   const smel_wset& ws = a.w;
-  const int cw = n0 + wc * 64;         // this wave's first column
-  const bool fv0 = cw < a.N, fv1 = cw + 32 < a.N;
+  const int cw = nb * NB + w * 64;   // this wave's first output column
   const int nk = (Kd + KT - 1) / KT;
-  // ---- W staging role: rows (k0 + 2 kp, +1) x columns [nc, nc + 16)
-  const int kp = tid & 31, cc = tid >> 5;
-  const int nc = n0 + 16 * cc;
-  const bool cok = nc < a.N;
-  const int pk = (a.N + 63) / 64, pk4 = (pk + 3) / 4, nfr = Kd / 32;   // packed k-steps run along C here
-  const int cks = nc / 64, ch = (nc >> 5) & 1;
-  const int lane2 = 32 * ch + (2 * kp) % 32;   // packed lane of row ka (row ka + 1 is the next lane)
-  const bool q4 = kind == SMEL_KIND_INT4;   // uniform: the tile's group kind
-  const int hq = (nc >> 4) & 1;              // int4: which 8 bytes of the 16-B q chunk are this thread's
-  const int zw = cks & 3;                     // int4: word of the packed scale/zero chunk
-  rsrc_t rw, rsz;
-  uint32_t wbase, sbase, wstep, sstep;
-  if (q4) {
-    rw = make_rsrc(ws.q4 + (int64_t)idx * nfr * pk * 1024, (uint64_t)nfr * pk * 1024);
-    rsz = make_rsrc(ws.sz4 + (int64_t)idx * nfr * pk4 * 256, (uint64_t)nfr * pk4 * 1024);
-    wbase = (uint32_t)((cks * 64 + lane2) * 16);
-    sbase = (uint32_t)(((cks >> 2) * 64 + lane2) * 16);
-    wstep = pk * 1024;
-    sstep = pk4 * 1024;
+  const int np = N / 32;             // column pairs of one matrix
+  const int p0 = cw / 32;
+  // Weight / scale-zero offsets need no validity flags: each descriptor covers exactly the rest of one matrix, so a
+  // column pair or group past its end reads as zero (hardware out-of-range handling). The second column pair gets a
+  // descriptor of its own (scalar registers) at the first pair's lane offset, which saves a vector register.
+  rsrc_t rw, rw1, rsz, rsz1;
+  uint32_t wo, so = 0;
+  if constexpr (Q4) {
+    const int G = N / ws.group;
+    const uint8_t* qb = ws.q4 + (int64_t)idx * np * nk * 1024;
+    const int64_t qbytes = (int64_t)np * nk * 1024;
+    rw = make_rsrc(qb, (uint64_t)qbytes);
+    rw1 = make_rsrc(qb + (int64_t)nk * 1024, (uint64_t)(qbytes - (int64_t)nk * 1024));
+    const uint32_t* zb = ws.sz4 + (int64_t)idx * G * nk * 64;
+    const int64_t zbytes = (int64_t)G * nk * 256;
+    const int64_t zstep = (int64_t)((cw + 32) / ws.group - cw / ws.group) * nk * 256;   // 0 or one group
+    rsz = make_rsrc(zb, (uint64_t)zbytes);
+    rsz1 = make_rsrc(reinterpret_cast<const uint8_t*>(zb) + zstep, (uint64_t)(zbytes - zstep));
+    wo = (uint32_t)(p0 * nk * 1024 + l * 16);
+    so = (uint32_t)((cw / ws.group) * nk * 256 + 4 * l);
   } else {
     const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
     const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
-    rw = make_rsrc(base + mi * nfr * pk * 2048, (uint64_t)nfr * pk * 4096);
-    rsz = rw;
-    wbase = (uint32_t)(((cks * 4 + ((nc >> 3) & 3)) * 64 + lane2) * 16);
-    sbase = wbase + 1024;   // the next 8 columns
-    wstep = sstep = pk * 4096;
+    const uint16_t* wb = base + mi * np * nk * 2048;
+    const int64_t wbytes = (int64_t)np * nk * 4096;
+    rw = make_rsrc(wb, (uint64_t)wbytes);
+    rw1 = make_rsrc(wb + (int64_t)nk * 2048, (uint64_t)(wbytes - (int64_t)nk * 4096));
+    rsz = rsz1 = rw;
+    wo = (uint32_t)(p0 * nk * 4096 + l * 16);
   }
-  // Four 16-B loads per thread and step for either kind, at addresses chosen above (no branch here: a branch
-  // between the two kinds' loads makes the compiler wait for the other branch's loads as well).
-  auto issue_w = [&](int j, WRegs& r) {
-    __builtin_amdgcn_sched_barrier(0);
-    const uint32_t fr = (uint32_t)((j * KT + 2 * kp) / 32);
-    const bool ok = cok && j < nk;
-    const uint32_t o = fr * wstep + wbase, so = fr * sstep + sbase;
-    r.v[0][0] = ld16(rw, ok ? o : OOB);
-    r.v[0][1] = ld16(rsz, ok ? so : OOB);
-    r.v[1][0] = ld16(rw, ok ? o + 16 : OOB);
-    r.v[1][1] = ld16(rsz, ok ? so + 16 : OOB);
-  };
-  // W^T word of tile column n = 16 cc + c and k pair kp: element n * KT + 8 * ((kp / 4) ^ swz(n)) + 2 * (kp % 4);
-  // swz(16 cc + c) = swz(c), a constant per c.
-  uint32_t* const wt0 = reinterpret_cast<uint32_t*>(B0) + 16 * cc * (KT / 2) + (kp & 3);
-  uint32_t* const wt1 = reinterpret_cast<uint32_t*>(B1) + 16 * cc * (KT / 2) + (kp & 3);
-  const int kc = kp >> 2;
-  auto store_w = [&](const WRegs& r, uint32_t* wt) {
-    uint32_t word[16];
-    if (q4) {
-      const uint32_t p0 = zw == 0 ? r.v[0][1].x : zw == 1 ? r.v[0][1].y : zw == 2 ? r.v[0][1].z : r.v[0][1].w;
-      const uint32_t p1 = zw == 0 ? r.v[1][1].x : zw == 1 ? r.v[1][1].y : zw == 2 ? r.v[1][1].z : r.v[1][1].w;
-      const float s0 = bf_lo(p0), z0 = bf_hi(p0), s1 = bf_lo(p1), z1 = bf_hi(p1);
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        const uint32_t q0 = hq ? r.v[0][0][2 + d] : r.v[0][0][d], q1 = hq ? r.v[1][0][2 + d] : r.v[1][0][d];
-        const uint32_t l0 = q0 & 0x0f0f0f0fu, h0 = (q0 >> 4) & 0x0f0f0f0fu;
-        const uint32_t l1 = q1 & 0x0f0f0f0fu, h1 = (q1 >> 4) & 0x0f0f0f0fu;
-        uint32_t* o = word + 8 * d;
-        o[0] = pack2bf(fmaf(ub0(l0), s0, z0), fmaf(ub0(l1), s1, z1));
-        o[1] = pack2bf(fmaf(ub0(h0), s0, z0), fmaf(ub0(h1), s1, z1));
-        o[2] = pack2bf(fmaf(ub1(l0), s0, z0), fmaf(ub1(l1), s1, z1));
-        o[3] = pack2bf(fmaf(ub1(h0), s0, z0), fmaf(ub1(h1), s1, z1));
-        o[4] = pack2bf(fmaf(ub2(l0), s0, z0), fmaf(ub2(l1), s1, z1));
-        o[5] = pack2bf(fmaf(ub2(h0), s0, z0), fmaf(ub2(h1), s1, z1));
-        o[6] = pack2bf(fmaf(ub3(l0), s0, z0), fmaf(ub3(l1), s1, z1));
-        o[7] = pack2bf(fmaf(ub3(h0), s0, z0), fmaf(ub3(h1), s1, z1));
-      }
-    } else {
-#pragma unroll
-      for (int d = 0; d < 2; ++d)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t x0 = r.v[0][d][j], x1 = r.v[1][d][j];
-          word[8 * d + 2 * j] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-          word[8 * d + 2 * j + 1] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < 16; ++c) wt[c * (KT / 2) + 4 * (kc ^ swz(c))] = word[c];
-  };
-  // ---- A staging (as the forward kernel): wave-load ii of wave w fills rows 8 g .. 8 g + 7, g = 4 w + ii
+  // ---- A staging: wave-load ii of wave w fills rows 8 g .. 8 g + 7 (g = 4 w + ii) of a stage, 1 KB; lane i writes
+  // physical chunk i % 8 of row 8 g + i / 8, i.e. logical chunk c = (i % 8) ^ swz(row). Kd is a multiple of 64, so a
+  // k-step is all in or all out.
   const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
-  const int li = tid & 63;
   uint32_t aoff[4];
-  int akc[4];
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
     const int g = 4 * w + ii;
-    const int row = 8 * g + (li >> 3);
-    const int c = (li & 7) ^ swz(row);
-    akc[ii] = 8 * c;
+    const int row = 8 * g + (l >> 3);
+    const int c = (l & 7) ^ swz(row);
     aoff[ii] = OOB;
     if (row < nrows) {
       const int grow = row0 + row;
@@ -161,183 +137,232 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       aoff[ii] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * c;
     }
   }
-  auto issue_a = [&](int j, uint16_t* S) {
-    const int k0 = j * KT;
+  // All loads of step j into stage st: int4 -> q (2 x 1 KB per wave), scale/zero (256 B per group), A (4 x 1 KB);
+  // bf16 -> A only.
+  auto issue_lds = [&](int j, int st) {
+    const bool in = j < nk;
+    const uint32_t k2 = (uint32_t)j * KT * 2;
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (Q4) {
+      ld16_lds(rw, Qt(st) + w * 2048, in ? wo + j * 1024 : OOB);
+      ld16_lds(rw1, Qt(st) + w * 2048 + 1024, in ? wo + j * 1024 : OOB);
+      ld4_lds(rsz, Zt(st) + w * 128, in ? so + j * 256 : OOB);
+      if constexpr (SZ2) ld4_lds(rsz1, Zt(st) + w * 128 + 64, in ? so + j * 256 : OOB);
+    }
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii)
-      ld16_lds(ra, S + (4 * w + ii) * 512, (k0 + akc[ii] + 8 <= Kd) ? aoff[ii] + k0 * 2 : OOB);
+    for (int ii = 0; ii < 4; ++ii) ld16_lds(ra, St(st) + (4 * w + ii) * 512, in ? aoff[ii] + k2 : OOB);
     __builtin_amdgcn_sched_barrier(0);
   };
-  // fragment reads: A row 64 wr + 32 m + r32, W^T column 64 wc + 32 f + r32, logical chunk 4 h + s
-  uint32_t frd[4];
+  // A fragment reads: lane (kq, li) of row-fragment rf, substep s reads logical chunk 4 s + kq of row 16 rf + li
+  // (swz of that row depends on li only)
+  uint32_t ard[2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) frd[s] = r32 * KT + 8 * ((4 * hi + s) ^ swz(r32));
-  const int abase = 64 * wr * KT, bbase = 64 * wc * KT;
+  for (int s = 0; s < 2; ++s) ard[s] = li * KT + 8 * ((4 * s + kq) ^ swz(li));
 
-  f32x16_t acc[NSW > 0 ? NSW : 1][2];
+  constexpr int NRF = 2 * NS;   // 16-row fragments
+  f32x4_t acc[NRF][4];
 #pragma unroll
-  for (int m = 0; m < (NSW > 0 ? NSW : 1); ++m) acc[m][0] = acc[m][1] = f32x16_t{};
+  for (int m = 0; m < NRF; ++m)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[m][f] = f32x4_t{};
 
-  auto compute = [&](const uint16_t* Sa, const uint16_t* Bt) {
-    if constexpr (NSW > 0) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(Bt + bbase + frd[s]);
-        const u32x4_t b1 = *reinterpret_cast<const u32x4_t*>(Bt + bbase + 32 * KT + frd[s]);
-#pragma unroll
-        for (int m = 0; m < NSW; ++m) {
-          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Sa + abase + m * 32 * KT + frd[s]);
-          acc[m][0] = mfma32(af, b0, acc[m][0]);
-          acc[m][1] = mfma32(af, b1, acc[m][1]);
-        }
-      }
-    }
-  };
-
-  // Ring positions of step j: A stage j % 3 (loaded 2 steps ahead), W^T buffer j % 2 (W(j+1) is dequantized into
-  // the other one during step j), W register set (j+1) % 6 dequantized and set (j+5) % 6 refilled (4 steps ahead).
-  WRegs w0, w1, w2, w3, w4, w5;
-  issue_w(0, w0);
-  issue_w(1, w1);
-  issue_w(2, w2);
-  issue_w(3, w3);
-  issue_a(0, S0);
-  issue_w(4, w4);
-  issue_a(1, S1);
-  store_w(w0, wt0);
-  auto step = [&](int j, uint16_t* Sa, uint16_t* Sa2, const uint16_t* Bc, uint32_t* wtn, const WRegs& wuse,
-                  WRegs& wiss) {
-    SMEL_WAIT_VM_LDS(8);   // A(j) and W(j+1) have landed: only step j-1's group may still be in flight
-    __builtin_amdgcn_s_barrier();
-    issue_w(j + 5, wiss);
-    issue_a(j + 2, Sa2);
-    store_w(wuse, wtn);    // W(j+1) -> the other W^T buffer
-    compute(Sa, Bc);
-  };
-  // whole rounds of 6 steps without exits (so the loop header keeps the waits above), then the remaining steps
-  int i = 0;
-  for (; i + 6 <= nk; i += 6) {
-    step(i, S0, S2, B0, wt1, w1, w5);
-    step(i + 1, S1, S0, B1, wt0, w2, w0);
-    step(i + 2, S2, S1, B0, wt1, w3, w1);
-    step(i + 3, S0, S2, B1, wt0, w4, w2);
-    step(i + 4, S1, S0, B0, wt1, w5, w3);
-    step(i + 5, S2, S1, B1, wt0, w0, w4);
-  }
-  if (i < nk) {
-    step(i, S0, S2, B0, wt1, w1, w5);
-    if (i + 1 < nk) {
-      step(i + 1, S1, S0, B1, wt0, w2, w0);
-      if (i + 2 < nk) {
-        step(i + 2, S2, S1, B0, wt1, w3, w1);
-        if (i + 3 < nk) {
-          step(i + 3, S0, S2, B1, wt0, w4, w2);
-          if (i + 4 < nk) step(i + 4, S1, S0, B0, wt1, w5, w3);
-        }
-      }
-    }
-  }
-  SMEL_WAIT_VM_LDS(0);
-  __builtin_amdgcn_s_barrier();   // every wave is done with the ring: its LDS is reused below
-  // ---- LoRA K-extension: ext[row][0:32] . Eb[0:32][n]
-  const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * 32 * a.N : nullptr)
-                                             : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
-  if (NSW > 0 && a.ext && eb) {
-    u32x4_t b0[2], b1[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      uint32_t v0[4] = {0, 0, 0, 0}, v1[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = 16 * hi + 8 * s + 2 * j;
-        if (fv0) {
-          const uint16_t* p = eb + (int64_t)k * a.N + cw + r32;
-          v0[j] = (uint32_t)p[0] | ((uint32_t)p[a.N] << 16);
-        }
-        if (fv1) {
-          const uint16_t* p = eb + (int64_t)k * a.N + cw + 32 + r32;
-          v1[j] = (uint32_t)p[0] | ((uint32_t)p[a.N] << 16);
-        }
-      }
-      b0[s] = u32x4_t{v0[0], v0[1], v0[2], v0[3]};
-      b1[s] = u32x4_t{v1[0], v1[1], v1[2], v1[3]};
-    }
-    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
-#pragma unroll
-    for (int m = 0; m < (NSW > 0 ? NSW : 1); ++m) {
-      const int row = 64 * wr + m * 32 + r32;
+  if constexpr (Q4) {
+    // One substep: the 2 NS A fragments, this lane's q words and its 8 scale/zero words come from the stage; then
+    // column fragment f+1 is dequantized (VALU) while the 2 NS MFMAs of fragment f run, so the two pipes overlap
+    // inside a wave.
+    auto compute = [&](int st) {
+      const uint16_t* S = St(st);
+      const uint32_t* Z = Zt(st) + w * 128 + 16 * kq;
+      const u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(Qt(st) + w * 2048 + l * 16);
+      const u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(Qt(st) + w * 2048 + 1024 + l * 16);
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 32 * hi + 16 * s : OOB);
-        acc[m][0] = mfma32(af, b0[s], acc[m][0]);
-        acc[m][1] = mfma32(af, b1[s], acc[m][1]);
+        float sc[8], ze[8];
+        auto unpack = [&](const uint32_t* zp) {
+          const u32x4_t za = *reinterpret_cast<const u32x4_t*>(zp);
+          const u32x4_t zb = *reinterpret_cast<const u32x4_t*>(zp + 4);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            sc[t] = bf_lo(za[t]);
+            ze[t] = bf_hi(za[t]);
+            sc[4 + t] = bf_lo(zb[t]);
+            ze[4 + t] = bf_hi(zb[t]);
+          }
+        };
+        auto dq = [&](int f) {
+          const int fr = f & 1;
+          if (SZ2 && f == 2) unpack(Z + 64 + 8 * s);
+          const uint32_t qw = (f < 2 ? q0 : q1)[2 * fr + s];
+          uint32_t o[4];
+          dq8r(qw, sc, ze, o);   // rows / columns outside the matrix hold q = s = z = 0
+          return u32x4_t{o[0], o[1], o[2], o[3]};
+        };
+        unpack(Z + 8 * s);
+        // first half of the row fragments: fragment f+1 dequantized while fragment f's MFMAs run; second half: the
+        // four finished B fragments again (16 A registers live instead of 32)
+        constexpr int H1 = (NRF + 1) / 2;
+        u32x4_t af[H1], b[4];
+#pragma unroll
+        for (int m = 0; m < H1; ++m) af[m] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
+        b[0] = dq(0);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          if (f < 3) b[f + 1] = dq(f + 1);
+#pragma unroll
+          for (int m = 0; m < H1; ++m) acc[m][f] = mfma16(af[m], b[f], acc[m][f]);
+        }
+        if constexpr (NRF > H1) {
+#pragma unroll
+          for (int m = H1; m < NRF; ++m)
+            af[m - H1] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
+#pragma unroll
+          for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int m = H1; m < NRF; ++m) acc[m][f] = mfma16(af[m - H1], b[f], acc[m][f]);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // one substep's fragments live at a time (256-VGPR budget)
       }
+    };
+    // 3-stage ring, every operand by LDS-DMA, two steps ahead: before step j only step j+1's loads may be in flight.
+    constexpr int NV = 3 + (SZ2 ? 2 : 1) + 4;   // vector-memory ops per step
+    auto step = [&](int j, int st) {
+      SMEL_WAIT_VM_LDS(NV);
+      __builtin_amdgcn_s_barrier();
+      issue_lds(j + 2, st == 0 ? 2 : st - 1);
+      compute(st);
+    };
+    issue_lds(0, 0);
+    issue_lds(1, 1);
+    int i = 0;
+    for (; i + 3 <= nk; i += 3) {   // whole rounds of 3 steps, then the 0-2 remaining ones
+      step(i, 0);
+      step(i + 1, 1);
+      step(i + 2, 2);
+    }
+    if (i < nk) {
+      step(i, 0);
+      if (i + 1 < nk) step(i + 1, 1);
+    }
+  } else {
+    auto mma = [&](const uint16_t* S, int s, const u32x4_t* b) {
+#pragma unroll
+      for (int m = 0; m < NRF; ++m) {
+        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) acc[m][f] = mfma16(af, b[f], acc[m][f]);
+      }
+    };
+    // bf16 weights: 8 loads per wave and step (2 pairs x 2 fragments x 2 substeps), one step ahead in two
+    // alternating register sets; A three steps ahead in a 4-stage ring. Issue order W(j+1), A(j+3): before step j
+    // only A(j+2)'s 4 loads may still be in flight.
+    u32x4_t bA[2][4], bB[2][4];   // [substep][column fragment]
+    auto issue_b = [&](int j, u32x4_t (*b)[4]) {
+      const bool in = j < nk;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr) {
+          b[s][fr] = ld16(rw, in ? wo + j * 4096 + (2 * fr + s) * 1024 : OOB);
+          b[s][2 + fr] = ld16(rw1, in ? wo + j * 4096 + (2 * fr + s) * 1024 : OOB);
+        }
+    };
+    auto compute = [&](int st, u32x4_t (*b)[4]) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) mma(St(st), s, b[s]);
+    };
+    issue_lds(0, 0);
+    issue_lds(1, 1);
+    issue_b(0, bA);
+    issue_lds(2, 2);
+    for (int i = 0; i < nk; i += 4) {
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 1, bB);
+      issue_lds(i + 3, 3);
+      compute(0, bA);
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 2, bA);
+      issue_lds(i + 4, 0);
+      compute(1, bB);
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 3, bB);
+      issue_lds(i + 5, 1);
+      compute(2, bA);
+      SMEL_WAIT_VM_LDS(4);
+      __builtin_amdgcn_s_barrier();
+      issue_b(i + 4, bA);
+      issue_lds(i + 6, 2);
+      compute(3, bB);
     }
   }
-  // ---- epilogue through LDS (the ring is free: see the barrier above): the wave results go into a row-major tile,
-  // then each thread handles 8 columns of whole rows with 16-B accesses (one address per 8 outputs).
-  const int ech = tid & 15;                // 8-column chunk of the block's 128 columns
-  const int col0 = n0 + 8 * ech;
-  if (EPI == 0) {
-    // bf16 tile [128][128]: rows 0..63 in S0, 64..127 in S1; 16-B chunk c of row r at c ^ (r & 7)
+  SMEL_WAIT_VM(0);   // the ring's trailing (out-of-range) loads
+  // ---- LoRA K-extension: ext[row][0:32] . Eb[n][0:32] (one 32-wide substep)
+  const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * N * 32 : nullptr)
+                                             : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
+  if (a.ext && eb) {
+    const rsrc_t re = make_rsrc(eb, (uint64_t)N * 64);
+    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
+    u32x4_t b[4];
 #pragma unroll
-    for (int m = 0; m < NSW; ++m) {
-      uint16_t* D = wr == 0 ? S0 : S1;
+    for (int f = 0; f < 4; ++f) {
+      const int n = cw + 16 * f + li;
+      b[f] = ld16(re, (cw + 16 * f < N) ? (uint32_t)n * 64 + 16 * kq : OOB);
+    }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lr = m * 32 + acc_row(r, l);   // row inside this wave's 64-row half
+    for (int m = 0; m < NRF; ++m) {
+      const int row = m * 16 + li;
+      const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 16 * kq : OOB);
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const int col = 64 * wc + 32 * f + r32;
-          D[lr * 128 + 8 * ((col >> 3) ^ (lr & 7)) + (col & 7)] = f2bf(acc[m][f][r]);
-        }
+      for (int f = 0; f < 4; ++f) acc[m][f] = mfma16(af, b[f], acc[m][f]);
+    }
+  }
+  // ---- epilogue through LDS (the ring is free after the loop): every lane writes its results, rounded to bf16, into a
+  // row-major tile [128][256] (rows 32 m .. 32 m + 31 in stage m; 16-B chunk c of row r at c ^ (r & 7)), then each
+  // thread handles 8 columns of whole rows with 16-B accesses.
+  __syncthreads();   // every wave is done with the ring (its loads landed, its reads returned)
+#pragma unroll
+  for (int m = 0; m < NRF; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * m + 4 * kq + r;   // D[4 kq + r][li] of the fragment
+      const int lr = row & 31;
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int col = 64 * w + 16 * f + li;
+        Et(row >> 5)[lr * 256 + 8 * ((col >> 3) ^ (lr & 7)) + (col & 7)] = f2bf(acc[m][f][r]);
       }
     }
-    __syncthreads();
-    if (col0 < a.N) {
-      for (int row = tid >> 4; row < nrows; row += 16) {
-        const int lr = row & 63;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>((row < 64 ? S0 : S1) + lr * 128 + 8 * (ech ^ (lr & 7)));
+  __syncthreads();
+  // thread -> (row, 8-column chunk): 32 threads per row, 8 rows per pass
+  const int ch = tid & 31;
+  const int col0 = nb * NB + 8 * ch;
+  if (EPI == 0) {
+    if (col0 < N) {
+      for (int row = tid >> 5; row < nrows; row += 8) {
+        const int lr = row & 31;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
         const int64_t orow = row_slot(row0 + row, a.order, a.TK);
         *reinterpret_cast<u32x4_t*>(a.out + orow * a.ldo + col0) = v;
       }
     }
     return;
   }
-  // down backward, columns n < I of dh = [dg | du]: fp32 tile [128][128], 32 rows per array (S0, S1, S2, B0); 16-B
-  // chunk c (4 floats) of row r at c ^ (r & 7). Then per row: da = w(row) acc, (g, u) = hsave, dg = da u act'(g),
+  // down backward, columns n < I of dh = [dg | du]: per row, da = w(row) acc, (g, u) = hsave, dg = da u act'(g),
   // du = da act(g), and the row's partial of sum_n acc * bf16(act(g) u) over this block's columns -> dwp.
-  float* const Fa[4] = {reinterpret_cast<float*>(S0), reinterpret_cast<float*>(S1), reinterpret_cast<float*>(S2),
-                        reinterpret_cast<float*>(B0)};
-#pragma unroll
-  for (int m = 0; m < NSW; ++m) {
-    float* D = wr == 0 ? Fa[m] : Fa[2 + m];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = acc_row(r, l);
-#pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const int col = 64 * wc + 32 * f + r32;
-        D[lr * 128 + 4 * ((col >> 2) ^ (lr & 7)) + (col & 3)] = acc[m][f][r];
-      }
-    }
-  }
-  __syncthreads();
-  const int I = a.N;
+  const int I = N;
   const bool cv = col0 < I;
-  for (int row = tid >> 4; row < nrows; row += 16) {   // 16 threads per row, uniform trip count per row group
+  for (int row = tid >> 5; row < nrows; row += 8) {   // 32 threads per row, uniform trip count per row group
     const int lr = row & 31;
-    const int q = row >> 5;   // a select, not an indexed local array (which would live in scratch memory)
-    const float* D = (q == 0 ? Fa[0] : q == 1 ? Fa[1] : q == 2 ? Fa[2] : Fa[3]) + lr * 128;
-    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(D + 4 * ((2 * ech) ^ (lr & 7)));
-    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(D + 4 * ((2 * ech + 1) ^ (lr & 7)));
+    const u32x4_t av = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
     const int grow = row0 + row;
     const float wrow_ = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
     float part = 0.f;
     if (cv) {
       const u32x4_t g2 = *reinterpret_cast<const u32x4_t*>(a.hsave + (int64_t)grow * 2 * I + col0);
       const u32x4_t u2 = *reinterpret_cast<const u32x4_t*>(a.hsave + (int64_t)grow * 2 * I + I + col0);
-      const float accv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
       uint32_t og[4], ou[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -346,14 +371,14 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
         for (int h = 0; h < 2; ++h) {
           const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
           const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
-          float av, dav;
-          act_and_grad_f(g, a.act, av, dav);
+          const float acv = h ? bf_hi(av[j]) : bf_lo(av[j]);
+          float avl, dav;
+          act_and_grad_f(g, a.act, avl, dav);
           const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
-          const float acv = accv[2 * j + h];
           part += acv * abf;
           const float da = wrow_ * acv;
           dgv[h] = da * u * dav;
-          duv[h] = da * av;
+          duv[h] = da * avl;
         }
         og[j] = pack2bf(dgv[0], dgv[1]);
         ou[j] = pack2bf(duv[0], duv[1]);
@@ -361,33 +386,26 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + col0) = u32x4_t{og[0], og[1], og[2], og[3]};
       *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + I + col0) = u32x4_t{ou[0], ou[1], ou[2], ou[3]};
     }
-    // fixed-order sum over the row's 16 threads (lanes 16 q .. 16 q + 15 of a wave)
+    // fixed-order sum over the row's 32 threads (lanes 32 h .. 32 h + 31 of a wave)
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) part += __shfl_xor(part, o, 64);
-    if (ech == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
+    for (int o = 1; o < 32; o <<= 1) part += __shfl_xor(part, o, 64);
+    if (ch == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
   }
 }
 
-template <int EPI>
-SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0,
-                          uint16_t* S1, uint16_t* S2, uint16_t* B0, uint16_t* B1) {
-  // slices of 32 rows this wave computes (its 64-row half of the tile); every wave stages and syncs alike
-  const int wr = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);
-  const int nsw = min(2, max(0, (nrows - 64 * wr + 31) >> 5));
-  switch (nsw) {
-    case 0: run_tile<EPI, 0>(a, kind, idx, row0, nrows, nb, S0, S1, S2, B0, B1); break;
-    case 1: run_tile<EPI, 1>(a, kind, idx, row0, nrows, nb, S0, S1, S2, B0, B1); break;
-    default: run_tile<EPI, 2>(a, kind, idx, row0, nrows, nb, S0, S1, S2, B0, B1); break;
+template <int EPI, bool Q4, bool SZ2>
+SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint8_t* smem) {
+  switch ((nrows + 31) >> 5) {
+    case 1: run_tile<EPI, Q4, 1, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
+    case 2: run_tile<EPI, Q4, 2, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
+    case 3: run_tile<EPI, Q4, 3, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
+    default: run_tile<EPI, Q4, 4, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
   }
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_bwd_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t S0[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S1[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S2[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t B0[B_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t B1[B_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM_BYTES];
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
@@ -395,12 +413,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
-  run_tile_ns<EPI>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, B0, B1);
+  if (kind == SMEL_KIND_INT4) {
+    if (a.w.group % 64)   // the 64 columns of a wave span two scale/zero groups
+      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, smem);
+    else
+      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, smem);
+  } else {
+    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, smem);
+  }
 }
 
 }  // namespace
 
-extern "C" int64_t smel_gmm_bwd_nblocks(int64_t C) { return (C + NT - 1) / NT; }
+extern "C" int64_t smel_gmm_bwd_nblocks(int64_t C) { return (C + NB - 1) / NB; }
 
 extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                             int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
@@ -410,17 +435,19 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(w && gkind && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->R && topk > 0, SMEL_EINVAL,
                "gmm_bwd: bad sizes");
-  SMEL_REQUIRE(w->R % 32 == 0 && w->C % 32 == 0, SMEL_EUNSUPPORTED,
-               "gmm_bwd: weight dims %lldx%lld must be multiples of 32", (long long)w->R, (long long)w->C);
+  SMEL_REQUIRE(w->R % 64 == 0 && w->C % 32 == 0, SMEL_EUNSUPPORTED,
+               "gmm_bwd: weight dims %lldx%lld must be multiples of 64 x 32", (long long)w->R, (long long)w->C);
   SMEL_REQUIRE(!w->q4 || (w->group % 32 == 0 && w->C % w->group == 0), SMEL_EUNSUPPORTED,
                "gmm_bwd: int4 group %d must be a multiple of 32 dividing the columns", w->group);
-  SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL, "gmm_bwd: an int4 bank needs its packed scale/zero (smel_pack_int4)");
+  SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL,
+               "gmm_bwd: an int4 bank needs its transposed scale/zero (smel_pack_int4_t)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_bwd: A rows must be 16-B aligned");
   SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0, SMEL_EUNSUPPORTED,
                "gmm_bwd: out / hsave rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
                "gmm_bwd: epilogue %d needs hsave, dwp and topv", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_bwd: gather needs order");
+  SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_bwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: A larger than 2 GiB");
   SMEL_REQUIRE(w->R * w->C * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: one weight matrix larger than 2 GiB");
   if (max_tiles == 0) return 0;

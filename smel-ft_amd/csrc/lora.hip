@@ -12,7 +12,8 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
                                                         int n, int r, int Hd, int In, uint16_t* __restrict__ fwd_gu,
                                                         uint16_t* __restrict__ fwd_dn, uint16_t* __restrict__ a_gu,
                                                         uint16_t* __restrict__ a_dn, uint16_t* __restrict__ bt_dn,
-                                                        uint16_t* __restrict__ bt_gu) {
+                                                        uint16_t* __restrict__ bt_gu, uint16_t* __restrict__ at_gu,
+                                                        uint16_t* __restrict__ at_dn) {
   const int which = blockIdx.y;
   int64_t total;
   switch (which) {
@@ -21,7 +22,9 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
     case 2: total = (int64_t)n * 32 * Hd; break;
     case 3: total = (int64_t)n * 32 * In; break;
     case 4: total = (int64_t)n * 32 * Hd; break;
-    default: total = (int64_t)n * 32 * 2 * In; break;
+    case 5: total = (int64_t)n * 32 * 2 * In; break;
+    case 6: total = (int64_t)n * Hd * 32; break;
+    default: total = (int64_t)n * In * 32; break;
   }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     float v = 0.f;
@@ -57,13 +60,28 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
       const int g = i / ((int64_t)Hd * 32);
       if (j < r) v = Bd[((int64_t)g * Hd + h) * r + j];
       bt_dn[i] = f2bf(v);
-    } else {                     // bt_gu [n][32][2In]
+    } else if (which == 5) {     // bt_gu [n][32][2In]
       const int c = i % (2 * In);
       const int j = (i / (2 * In)) % 32;
       const int g = i / ((int64_t)2 * In * 32);
       if (j < r && c < In) v = Bg[((int64_t)g * In + c) * r + j];
       if (j >= 16 && j < 16 + r && c >= In) v = Bu[((int64_t)g * In + c - In) * r + j - 16];
       bt_gu[i] = f2bf(v);
+    } else if (which == 6) {     // at_gu [n][Hd][32]: a_gu transposed (the backward GEMM's K-extension)
+      const int j = i % 32;
+      const int64_t hg = i / 32;
+      const int h = hg % Hd;
+      const int g = hg / Hd;
+      if (j < r) v = Ag[((int64_t)g * r + j) * Hd + h];
+      if (j >= 16 && j < 16 + r) v = Au[((int64_t)g * r + j - 16) * Hd + h];
+      at_gu[i] = f2bf(v);
+    } else {                     // at_dn [n][In][32]: a_dn transposed
+      const int j = i % 32;
+      const int64_t cg = i / 32;
+      const int c = cg % In;
+      const int g = cg / In;
+      if (j < r) v = Ad[((int64_t)g * r + j) * In + c];
+      at_dn[i] = f2bf(v);
     }
   }
 }
@@ -262,15 +280,15 @@ __global__ __launch_bounds__(256) void lora_wgrad_sum(const int32_t* __restrict_
 extern "C" int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, const float* B_up,
                               const float* A_down, const float* B_down, int64_t n, int64_t r, int64_t Hd, int64_t In,
                               uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
-                              uint16_t* bt_gu, hipStream_t stream) {
+                              uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn, hipStream_t stream) {
   SMEL_REQUIRE(n >= 0 && r > 0 && Hd > 0 && In > 0, SMEL_EINVAL, "lora_prep: bad sizes");
   SMEL_REQUIRE(r <= 16, SMEL_EUNSUPPORTED, "lora_prep: rank %lld > 16", (long long)r);
   if (n == 0) return 0;
   SMEL_REQUIRE(A_gate && B_gate && A_up && B_up && A_down && B_down && fwd_gu && fwd_dn && a_gu && a_dn && bt_dn &&
-                   bt_gu, SMEL_EINVAL, "lora_prep: null pointer");
-  dim3 grid(256, 6);
+                   bt_gu && at_gu && at_dn, SMEL_EINVAL, "lora_prep: null pointer");
+  dim3 grid(256, 8);
   lora_prep_kernel<<<grid, 256, 0, stream>>>(A_gate, B_gate, A_up, B_up, A_down, B_down, (int)n, (int)r, (int)Hd,
-                                             (int)In, fwd_gu, fwd_dn, a_gu, a_dn, bt_dn, bt_gu);
+                                             (int)In, fwd_gu, fwd_dn, a_gu, a_dn, bt_dn, bt_gu, at_gu, at_dn);
   return smel::launch_status();
 }
 

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(HERE, "libsmel_moe.so")
 
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -34,13 +34,16 @@ SIGNATURES = {
     "smel_packed_bytes": (i64, [i32, i64, i64]),
     "smel_pack_int4": (i32, [vp, vp, vp, i64, i64, i64, vp, vp, vp]),
     "smel_pack_bf16": (i32, [vp, i64, i64, i64, vp, vp]),
+    "smel_packed_t_bytes": (i64, [i32, i64, i64, i64, i64]),
+    "smel_pack_int4_t": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp]),
+    "smel_pack_bf16_t": (i32, [vp, i64, i64, i64, i64, vp, vp]),
     "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_ld": (i64, [i64, i32]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
     "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_ws_size": (i64, [i64, i64]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
-    "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, i64, vp, vp]),

@@ -19,6 +19,7 @@ shared expert in fp32 before the single rounding; gradients are accumulated in f
 from __future__ import annotations
 
 import ctypes
+from collections import OrderedDict
 
 import torch
 import torch.nn.functional as F
@@ -67,6 +68,38 @@ def pack_bf16(*mats: torch.Tensor) -> PackedW:
     return PackedW(out, R, C)
 
 
+def pack_bf16_t(w: torch.Tensor) -> PackedW:
+    """Pack bf16 matrices [..., R, C] (a [E, R, C] bank: E matrices) into the backward GEMM's transposed fragment
+    layout (smel_pack_bf16_t)."""
+    w = _bf16(w)
+    R, C = w.shape[-2], w.shape[-1]
+    n = w.numel() // (R * C)
+    lib = L.load()
+    out = torch.empty(lib.smel_packed_t_bytes(L.PACK_BF16, n, R, C, 0) // 2, dtype=torch.bfloat16, device=w.device)
+    L.call("smel_pack_bf16_t", L.ptr(w), n, R, C, C, L.ptr(out), L.stream())
+    return PackedW(out, R, C)
+
+
+_PACK_CACHE: "OrderedDict" = OrderedDict()
+_PACK_CACHE_MAX = 32
+
+
+def _cached(kind: str, build, *mats: torch.Tensor):
+    """Packed form of per-call weights (shared expert, router, dense MLP) reused while the source tensors are
+    unchanged: keyed by storage address, version counter (bumped by any in-place write, views included), shape and
+    strides. The entry holds the sources, so their addresses cannot be reused while it lives."""
+    key = (kind,) + tuple((m.data_ptr(), m._version, tuple(m.shape), tuple(m.stride()), str(m.device)) for m in mats)
+    hit = _PACK_CACHE.get(key)
+    if hit is not None:
+        _PACK_CACHE.move_to_end(key)
+        return hit[1]
+    val = build()
+    _PACK_CACHE[key] = (mats, val)
+    while len(_PACK_CACHE) > _PACK_CACHE_MAX:
+        _PACK_CACHE.popitem(last=False)
+    return val
+
+
 # ------------------------------------------------------------------------------------------------ expert banks
 
 
@@ -85,6 +118,13 @@ class BF16Experts:
         cache = self.__dict__.setdefault("_packed", {})
         if which not in cache:
             cache[which] = pack_bf16(_bf16(self.gate_up if which == "gu" else self.down))
+        return cache[which]
+
+    def packed_t(self, which: str) -> PackedW:
+        """The same in the backward GEMM's transposed layout, built once."""
+        cache = self.__dict__.setdefault("_packed_t", {})
+        if which not in cache:
+            cache[which] = pack_bf16_t(self.gate_up if which == "gu" else self.down)
         return cache[which]
 
     def tensors(self):
@@ -127,6 +167,24 @@ class Int4Experts:
             cache[which] = (qf, szf)
         return cache[which]
 
+    def packed_t(self, which: str):
+        """(q, scale/zero) of 'gu' or 'dn' in the backward GEMM's transposed layout (smel_pack_int4_t), built once
+        per bank: one more int4 copy (not a bf16 one) that the backward streams straight into registers."""
+        cache = self.__dict__.setdefault("_packed_t", {})
+        if which not in cache:
+            d = self.gu if which == "gu" else self.dn
+            E, R, half = d["q"].shape
+            C = half * 2
+            g = Int4Experts.group_of(d)
+            lib = L.load()
+            qt = torch.empty(lib.smel_packed_t_bytes(L.PACK_Q4, E, R, C, g), dtype=torch.uint8, device=d["q"].device)
+            szt = torch.empty(lib.smel_packed_t_bytes(L.PACK_SZ, E, R, C, g) // 4, dtype=torch.int32,
+                              device=d["q"].device)
+            L.call("smel_pack_int4_t", L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"]), E, R, C, g, L.ptr(qt),
+                   L.ptr(szt), L.stream())
+            cache[which] = (qt, szt)
+        return cache[which]
+
     def weights(self, e0: int, e1: int):
         gu = dequant_int4(self.gu["q"][e0:e1], self.gu["scale"][e0:e1], self.gu["zero"][e0:e1], self.dtype)
         dn = dequant_int4(self.dn["q"][e0:e1], self.dn["scale"][e0:e1], self.dn["zero"][e0:e1], self.dtype)
@@ -163,6 +221,14 @@ class LayerExperts:
         if "_packed_sel" not in self.__dict__:
             self._packed_sel = (pack_bf16(_bf16(self.sel_gate_up)), pack_bf16(_bf16(self.sel_down)))
         return self._packed_sel
+
+    def packed_sel_t(self):
+        """The same in the backward GEMM's transposed layout, built once."""
+        if self.sel_ids is None or not self._slot:
+            return None
+        if "_packed_sel_t" not in self.__dict__:
+            self._packed_sel_t = (pack_bf16_t(self.sel_gate_up), pack_bf16_t(self.sel_down))
+        return self._packed_sel_t
 
     def gkind(self, with_shared: bool, device) -> torch.Tensor:
         """Per-group weight location: (kind << 16) | index, groups 0..E-1 (+ E = shared)."""
@@ -230,19 +296,23 @@ def _dense_tiles(T: int, device):
 
 
 def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> PackedW:
-    """The weight of the router-backward GEMM (dx += dlogits . W): router rows, then the shared-gate row, zero-padded
-    to a multiple of 32 rows ([Epad, H], Epad = R of the result), packed. Built per call (E x H bf16, about 1 MB)."""
+    """The weight of the router-backward GEMM (dx += dlogits . W): router rows, then the shared-gate row, as one
+    [E(+1), H] matrix in the transposed layout, its contraction dim padded to a multiple of 64 (R of the result)."""
     E, H = gate_w.shape
-    Epad = (E + 1 + 31) // 32 * 32
-    if sg_w is None:
-        pw = pack_bf16(gate_w)
-    else:
-        w = torch.empty(E + 1, H, dtype=torch.bfloat16, device=gate_w.device)
-        w[:E] = gate_w
-        w[E] = sg_w.reshape(-1)
-        pw = pack_bf16(w)
-    pw.R = Epad
-    return pw
+    Epad = (E + (1 if sg_w is not None else 0) + 63) // 64 * 64
+
+    def build():
+        if sg_w is None:
+            pw = pack_bf16_t(gate_w)
+        else:
+            w = torch.empty(E + 1, H, dtype=torch.bfloat16, device=gate_w.device)
+            w[:E] = gate_w
+            w[E] = sg_w.reshape(-1)
+            pw = pack_bf16_t(w)
+        pw.R = Epad
+        return pw
+
+    return _cached("router_t", build, *((gate_w,) if sg_w is None else (gate_w, sg_w)))
 
 
 class _LoRABufs:
@@ -255,32 +325,36 @@ class _LoRABufs:
         self.fwd_gu, self.fwd_dn = e(n, 2 * I, EXT), e(n, H, EXT)
         self.a_gu, self.a_dn = e(n, EXT, H), e(n, EXT, I)
         self.bt_dn, self.bt_gu = e(n, EXT, H), e(n, EXT, 2 * I)
+        self.at_gu, self.at_dn = e(n, H, EXT), e(n, I, EXT)
         P = [getattr(lora, k).detach().float().contiguous() for k in
              ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")]
         L.call("smel_lora_prep", *[L.ptr(p) for p in P], n, lora.r, H, I, L.ptr(self.fwd_gu), L.ptr(self.fwd_dn),
-               L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu), L.stream())
+               L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu), L.ptr(self.at_gu),
+               L.ptr(self.at_dn), L.stream())
 
 
-def _bank_wset(fz, which: str) -> L.WSet:
-    """smel_wset for the gate_up ('gu') or down ('dn') projection of a frozen bank (packed weights)."""
+def _bank_wset(fz, which: str, t: bool = False) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of a frozen bank (packed weights; t = the backward
+    GEMM's transposed layout)."""
     w = L.WSet()
     if isinstance(fz, Int4Experts):
         d = fz.gu if which == "gu" else fz.dn
-        qf, szf = fz.packed(which)
+        qf, szf = fz.packed_t(which) if t else fz.packed(which)
         w.q4, w.sz4 = L.ptr(qf), L.ptr(szf)
         w.group = Int4Experts.group_of(d)
         w.R, w.C = d["q"].shape[1], d["q"].shape[2] * 2
     else:
-        pw = fz.packed(which)
+        pw = fz.packed_t(which) if t else fz.packed(which)
         w.wb = L.ptr(pw.t)
         w.group = 32
         w.R, w.C = pw.R, pw.C
     return w
 
 
-def _wset(ex: LayerExperts, which: str, sel_w: PackedW | None, sh_w: PackedW | None, ext_sel, ext_sh) -> L.WSet:
-    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights)."""
-    w = _bank_wset(ex.frozen, which)
+def _wset(ex: LayerExperts, which: str, sel_w: PackedW | None, sh_w: PackedW | None, ext_sel, ext_sh,
+          t: bool = False) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights; t = transposed)."""
+    w = _bank_wset(ex.frozen, which, t)
     w.wsel = L.ptr(sel_w.t) if sel_w is not None else None
     w.wsh = L.ptr(sh_w.t) if sh_w is not None else None
     w.ext_sel = L.ptr(ext_sel)
@@ -433,7 +507,8 @@ def _lora_groups(ex: LayerExperts, with_shared: bool, n_sel_lora: int, device):
 
 def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
                       need_grad: bool, c: _Ctx):
-    """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up [2I,H], down [H,I], sgate fp32 [T]) or None."""
+    """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up, down, sgate fp32 [T], gate_up^T, down^T) or None
+    (packed forward and transposed layouts of the shared expert's [2I,H] / [H,I] weights)."""
     T, H = x.shape
     E = ex.E
     dev = x.device
@@ -453,9 +528,9 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     if ex.sel_ids is not None and len(ex._slot):
         sel_gu, sel_dn = ex.packed_sel()
     I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
-    sh_gu = sh_dn = sgate = None
+    sh_gu = sh_dn = sgate = sh_gu_t = sh_dn_t = None
     if shared is not None:
-        sh_gu, sh_dn, sgate = shared
+        sh_gu, sh_dn, sgate, sh_gu_t, sh_dn_t = shared
     lb_ex = _LoRABufs(lora_ex, len(ex._slot), H, I, dev) if (lora_ex is not None and sel_gu is not None) else None
     lb_sh = _LoRABufs(lora_sh, 1, H, I, dev) if (lora_sh is not None and shared is not None) else None
     any_lora = lb_ex is not None or lb_sh is not None
@@ -485,10 +560,11 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(sgate), T, K, H, L.ptr(out), st)
     # everything the backward needs
     c.T, c.H, c.I, c.E, c.K, c.TK, c.M, c.maxt = T, H, I, E, K, TK, M, maxt
-    c.ex, c.shared_w = ex, (sh_gu, sh_dn) if shared is not None else None
+    c.ex, c.shared_w = ex, (sh_gu_t, sh_dn_t) if shared is not None else None
+    sel_t = ex.packed_sel_t() if (need_grad and sel_gu is not None) else None
     c.tensors = dict(x=x, topv=topv, sgate=sgate, counts=counts, offsets=offsets, order=order, inv=inv, tiles=tiles,
                      ntiles=ntiles, err=err, gk=gk, act=actb, hsave=hsave, ext_gu=ext_gu, ext_dn=ext_dn,
-                     sel_gu=sel_gu, sel_dn=sel_dn)
+                     sel_gu=sel_t[0] if sel_t else None, sel_dn=sel_t[1] if sel_t else None)
     c.lb_ex, c.lb_sh = lb_ex, lb_sh
     c.lora_ex, c.lora_sh = lora_ex, lora_sh
     return out
@@ -521,7 +597,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     nblk = L.load().smel_gmm_bwd_nblocks(I)
     dh = bf(M, 2 * I)
     dwp = torch.empty(M, nblk, dtype=torch.float32, device=dev)
-    w_dn = _wset(ex, "dn", t["sel_dn"], sh_dn, g(lb_ex, "a_dn"), g(lb_sh, "a_dn"))
+    w_dn = _wset(ex, "dn", t["sel_dn"], sh_dn, g(lb_ex, "at_dn"), g(lb_sh, "at_dn"), t=True)
     L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["topv"]),
            L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st, tag="gemm_dn_bwd")
@@ -533,7 +609,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
                K, L.ptr(g(lb_ex, "bt_gu")), L.ptr(g(lb_sh, "bt_gu")), 2 * I, s_ex, s_sh, L.ptr(ext_dxa), st)
     # (4) gate_up backward: per-slot dx rows
     dxs = bf(M, H)
-    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "a_gu"), g(lb_sh, "a_gu"))
+    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True)
     L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, L.ptr(dxs), H, None, st,
            tag="gemm_gu_bwd")
@@ -627,7 +703,7 @@ class _MoELayerFn(torch.autograd.Function):
         if stats is not None:
             stats(probs, topv, topi)
         c = _Ctx()
-        shared = (plan["shared"][0], plan["shared"][1], sgate) if fuse else None
+        shared = (plan["shared"][0], plan["shared"][1], sgate, plan["shared"][4], plan["shared"][5]) if fuse else None
         out = _forward_pipeline(x, plan["ex"], K, topv, topi32, False, shared, plan["lora_ex"], plan["lora_sh"],
                                 plan["need_grad"], c)
         if plan["need_grad"]:
@@ -677,11 +753,13 @@ def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
 
 class _MLPFn(torch.autograd.Function):
     """Gated MLP with LoRA on gate/up/down (mlp_lora, smel/moe.py:183-194) as one dense group of the grouped GEMMs:
-    rows = tokens, weights = the stacked gate_up [2Is, H] and down [H, Is]."""
+    rows = tokens, weights = the stacked gate_up [2Is, H] and down [H, Is], each given as (forward layout, transposed
+    layout) packs."""
 
     @staticmethod
-    def forward(ctx, x, w_gu, w_dn, lora, act_name, *leaves):
+    def forward(ctx, x, w_gu2, w_dn2, lora, act_name, *leaves):
         T, H = x.shape
+        w_gu, w_dn = w_gu2[0], w_dn2[0]
         Is = w_dn.C
         dev = x.device
         st = L.stream()
@@ -708,7 +786,7 @@ class _MLPFn(torch.autograd.Function):
         L.call("smel_gmm_fwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), Is, T, 0,
                None, 0, 1, L.ptr(ext_dn), 0, _ACT[act_name], L.ptr(y), H, None, st, tag="gemm_mlp_dn_fwd")
         ctx.save_for_backward(x, actb, hsave)
-        ctx.w = (w_gu, w_dn)
+        ctx.w = (w_gu2[1], w_dn2[1])
         ctx.ext = (ext_gu, ext_dn)
         ctx.lb, ctx.lora, ctx.act_name = lb, lora, act_name
         return y
@@ -737,7 +815,7 @@ class _MLPFn(torch.autograd.Function):
         nblk = L.load().smel_gmm_bwd_nblocks(Is)
         dh = bf(T, 2 * Is)
         dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
-        wd = _dense_wset(w_dn, g("a_dn"))
+        wd = _dense_wset(w_dn, g("at_dn"))
         L.call("smel_gmm_bwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
                None, 0, 1, L.ptr(ext_db), 1, _ACT[ctx.act_name], L.ptr(hsave), None, L.ptr(ones), L.ptr(dh), 2 * Is,
                L.ptr(dwp), st, tag="gemm_mlp_dn_bwd")
@@ -746,7 +824,7 @@ class _MLPFn(torch.autograd.Function):
             L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * Is, T, 0, None, 0, 1,
                    None, L.ptr(lb.bt_gu), 2 * Is, 0.0, sc, L.ptr(ext_dxa), st)
         dx = bf(T, H)
-        wg = _dense_wset(w_gu, g("a_gu"))
+        wg = _dense_wset(w_gu, g("at_gu"))
         L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
                0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, L.ptr(dx), H, None, st, tag="gemm_mlp_gu_bwd")
         grads = [None] * 6
@@ -789,12 +867,16 @@ def mlp_lora(x, w_gate, w_up, w_down, lora, act_name="silu", w_gate_up=None):
     L.require_device(x, w_down)
     xs = x.reshape(-1, x.shape[-1])
     if w_gate_up is not None:
-        pgu = pack_bf16(_bf16(w_gate_up))
+        gus = (_bf16(w_gate_up),)
+        pgu = (_cached("f", lambda: pack_bf16(gus[0]), *gus), _cached("t", lambda: pack_bf16_t(gus[0]), *gus))
     else:
         if w_gate.shape[0] % 32:
             raise L.SmelError(f"mlp_lora: intermediate size {w_gate.shape[0]} must be a multiple of 32")
-        pgu = pack_bf16(_bf16(w_gate), _bf16(w_up))
-    y = _MLPFn.apply(_bf16(xs), pgu, pack_bf16(_bf16(w_down)), lora, act_name, *_lora_leaves(lora))
+        gus = (_bf16(w_gate), _bf16(w_up))
+        pgu = (_cached("f", lambda: pack_bf16(*gus), *gus), _cached("t", lambda: pack_bf16_t(torch.cat(gus)), *gus))
+    dn = _bf16(w_down)
+    pdn = (_cached("f", lambda: pack_bf16(dn), dn), _cached("t", lambda: pack_bf16_t(dn), dn))
+    y = _MLPFn.apply(_bf16(xs), pgu, pdn, lora, act_name, *_lora_leaves(lora))
     return y.reshape(*x.shape[:-1], y.shape[-1])
 
 
@@ -808,16 +890,25 @@ def shared_mlp(x, W, lora):
 
 
 def _shared_weights(W: dict):
-    """(gate_up, down) of the shared expert packed (per call: the dict's tensors may change between calls), the
-    shared-gate row, and the shared intermediate size; None without a shared expert."""
+    """(gate_up, down) of the shared expert packed, the shared-gate row, the shared intermediate size, and (gate_up,
+    down) in the backward's transposed layout; None without a shared expert. Packs are reused while the dict's
+    tensors are unchanged."""
     pre = "mlp.shared_expert."
     if pre + "gate_proj.weight" not in W and pre + "gate_up_proj.weight" not in W:
         return None
     gu = W.get(pre + "gate_up_proj.weight")
     dn = _bf16(W[pre + "down_proj.weight"])
-    pgu = pack_bf16(_bf16(gu)) if gu is not None else pack_bf16(_bf16(W[pre + "gate_proj.weight"]),
-                                                                  _bf16(W[pre + "up_proj.weight"]))
-    return pgu, pack_bf16(dn), _bf16(W["mlp.shared_expert_gate.weight"].reshape(-1)), dn.shape[1]
+    if gu is not None:
+        gus = (_bf16(gu),)
+        pgu = _cached("f", lambda: pack_bf16(gus[0]), *gus)
+        pgu_t = _cached("t", lambda: pack_bf16_t(gus[0]), *gus)
+    else:
+        gus = (_bf16(W[pre + "gate_proj.weight"]), _bf16(W[pre + "up_proj.weight"]))
+        pgu = _cached("f", lambda: pack_bf16(*gus), *gus)
+        pgu_t = _cached("t", lambda: pack_bf16_t(torch.cat(gus)), *gus)
+    pdn = _cached("f", lambda: pack_bf16(dn), dn)
+    pdn_t = _cached("t", lambda: pack_bf16_t(dn), dn)
+    return pgu, pdn, _bf16(W["mlp.shared_expert_gate.weight"].reshape(-1)), dn.shape[1], pgu_t, pdn_t
 
 
 def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=None):
@@ -914,7 +1005,7 @@ class FrozenExpertsFn(torch.autograd.Function):
         rows, H = dy.shape
         dev = dy.device
         st = L.stream()
-        w_gu, w_dn = _bank_wset(bank, "gu"), _bank_wset(bank, "dn")
+        w_gu, w_dn = _bank_wset(bank, "gu", t=True), _bank_wset(bank, "dn", t=True)
         I = w_dn.C
         nblk = L.load().smel_gmm_bwd_nblocks(I)
         dh = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=dev)

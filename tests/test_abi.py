@@ -64,7 +64,14 @@ def test_host_side_rejections():
     assert L.smel_pack_bf16(1, 64, 60, 64, 1, None) == -2               # K not a multiple of 8
     with pytest.raises(_lib.SmelError):
         _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, 32, 64, 64, None, None, None, None, None,
-                  None, None)
+                  None, None, None, None)
+    # transposed layouts (backward GEMM operand): sizes and rejections
+    assert L.smel_packed_t_bytes(_lib.PACK_Q4, 2, 1024, 2048, 64) == 2 * 64 * 16 * 1024
+    assert L.smel_packed_t_bytes(_lib.PACK_SZ, 2, 1024, 2048, 64) == 2 * 32 * 16 * 256
+    assert L.smel_packed_t_bytes(_lib.PACK_BF16, 1, 288, 2048, 0) == 64 * 5 * 4096
+    assert L.smel_packed_t_bytes(_lib.PACK_SZ, 1, 64, 96, 64) == -1      # group does not divide C
+    assert L.smel_pack_int4_t(1, 1, 1, 1, 64, 96, 64, 1, 1, None) == -2  # group does not divide C
+    assert L.smel_pack_bf16_t(1, 1, 64, 48, 64, 1, None) == -2           # C not a multiple of 32
 
 
 def test_product_path_does_not_reach_the_oracle():

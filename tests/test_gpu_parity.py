@@ -120,6 +120,75 @@ def test_pack_bf16_roundtrip(rows, K, ld):
     assert not u[rows:].any() and not u[:, K:].any()
 
 
+# The backward GEMM's transposed layouts (SMEL_PACK_* of smel_pack_int4_t / smel_pack_bf16_t), inverted the same way.
+
+
+def _t_index(E, R, C):
+    """(row, col) of every packed element of the transposed q / bf16 layouts, in packed order
+    [e][p][ks][kq][i][fr][s][t] (bf16: [e][p][ks][fr][s][kq][i][t])."""
+    nks = -(-R // 64)
+    p, ks, kq, i, fr, s, t = np.meshgrid(np.arange(C // 32), np.arange(nks), np.arange(4), np.arange(16),
+                                         np.arange(2), np.arange(2), np.arange(8), indexing="ij")
+    return 64 * ks + 32 * s + 8 * kq + t, 32 * p + 16 * fr + i
+
+
+@pytest.mark.parametrize("E,R,C,group", [(3, 128, 192, 64), (2, 96, 64, 32), (1, 1024, 2048, 64)])
+def test_pack_int4_t_roundtrip(E, R, C, group):
+    L = _lib()
+    _say(f"pack int4 transposed E{E} R{R} C{C} g{group}")
+    gen = torch.Generator().manual_seed(E * R + C + 1)
+    q = torch.randint(0, 256, (E, R, C // 2), generator=gen, dtype=torch.uint8)
+    sc = torch.randint(0, 65536, (E, R, C // group), generator=gen, dtype=torch.int32).to(torch.int16)
+    ze = torch.randint(0, 65536, (E, R, C // group), generator=gen, dtype=torch.int32).to(torch.int16)
+    lib = L.load()
+    qt = torch.empty(lib.smel_packed_t_bytes(L.PACK_Q4, E, R, C, group), dtype=torch.uint8, device=DEV)
+    szt = torch.empty(lib.smel_packed_t_bytes(L.PACK_SZ, E, R, C, group) // 4, dtype=torch.int32, device=DEV)
+    qd, sd, zd = q.to(DEV), sc.to(DEV), ze.to(DEV)
+    L.call("smel_pack_int4_t", L.ptr(qd), L.ptr(sd), L.ptr(zd), E, R, C, group, L.ptr(qt), L.ptr(szt), L.stream())
+    nks = -(-R // 64)
+    # dense nibbles of the source: low nibble = even column
+    qn = q.numpy()
+    dense = np.stack((qn & 15, qn >> 4), axis=-1).reshape(E, R, C)
+    words = qt.cpu().numpy().view(np.uint32).reshape(E, C // 32, nks, 4, 16, 2, 2)   # [e][p][ks][kq][i][fr][s]
+    nib = (words[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 15              # [..., t]
+    row, col = _t_index(E, R, C)
+    ok = row < R
+    for e in range(E):
+        got = nib[e]
+        assert np.array_equal(got[ok], dense[e][row[ok], col[ok]])
+        assert not got[~ok].any()
+    s16 = sc.numpy().view(np.uint16).astype(np.uint32)
+    z16 = ze.numpy().view(np.uint16).astype(np.uint32)
+    sw = szt.cpu().numpy().view(np.uint32).reshape(E, C // group, nks, 4, 2, 8)       # [e][g][ks][kq][s][t]
+    ks, kq, ss, t = np.meshgrid(np.arange(nks), np.arange(4), np.arange(2), np.arange(8), indexing="ij")
+    r = 64 * ks + 32 * ss + 8 * kq + t
+    for e in range(E):
+        for g in range(C // group):
+            want = np.where(r < R, s16[e][np.minimum(r, R - 1), g] | (z16[e][np.minimum(r, R - 1), g] << 16), 0)
+            assert np.array_equal(sw[e, g], want.astype(np.uint32))
+
+
+@pytest.mark.parametrize("E,R,C", [(2, 96, 64), (1, 288, 2048), (12, 512, 2048)])
+def test_pack_bf16_t_roundtrip(E, R, C):
+    L = _lib()
+    _say(f"pack bf16 transposed E{E} R{R} C{C}")
+    gen = torch.Generator().manual_seed(E + R + C)
+    w = torch.randn(E, R, C, generator=gen).to(torch.bfloat16)
+    lib = L.load()
+    wt = torch.empty(lib.smel_packed_t_bytes(L.PACK_BF16, E, R, C, 0) // 2, dtype=torch.bfloat16, device=DEV)
+    wd = w.to(DEV)
+    L.call("smel_pack_bf16_t", L.ptr(wd), E, R, C, C, L.ptr(wt), L.stream())
+    nks = -(-R // 64)
+    u = _u16(wt).reshape(E, C // 32, nks, 2, 2, 4, 16, 8)                            # [e][p][ks][fr][s][kq][i][t]
+    u = u.transpose(0, 1, 2, 5, 6, 3, 4, 7)                                           # -> [e][p][ks][kq][i][fr][s][t]
+    row, col = _t_index(E, R, C)
+    ok = row < R
+    src = _u16(w)
+    for e in range(E):
+        assert np.array_equal(u[e][ok], src[e][row[ok], col[ok]])
+        assert not u[e][~ok].any()
+
+
 # -------------------------------------------------------------------------------------------------------- router
 
 
@@ -546,3 +615,69 @@ def test_route_gemma4_backward():
     (tvo * cot).sum().backward()
     assert torch.allclose(topv.detach().cpu(), tvo.detach(), rtol=3e-2, atol=1e-3)
     assert_close_bf16(hg.grad.cpu(), ho.grad, "dh", rel=3e-2, cos=0.999)
+
+
+# ------------------------------------------------------------------------------------------ skewed routing (C5 kind)
+
+
+def _skewed_layer(seed=0):
+    """A layer whose router prefers a few experts (Zipf(1.2) logit bias through the inputs, as bench.py's C5 does):
+    hot experts span many 128-row tiles, some experts get no rows; the 4 most popular are the selected ones."""
+    T, H, E, I, K = 1500, 256, 32, 128, 4
+    x, ol = R.make_layer(T=T, H=H, E=E, I=I, K=K, n_sel=0, r=8, alpha=16.0, shared_inter=I, seed=seed,
+                         lora_b_std=0.05)
+    g = torch.Generator().manual_seed(seed + 100)
+    perm = torch.randperm(E, generator=g)
+    rank = torch.empty(E, dtype=torch.long)
+    rank[perm] = torch.arange(E)
+    bias = -1.2 * 0.6 * torch.log(rank.double() + 1.0)
+    gw = ol.gate_w.float()
+    ol.gate_w = (gw - gw.mean(1, keepdim=True) + (bias / H).float()[:, None]).to(torch.bfloat16)
+    x = (x.float() + 1.0).to(torch.bfloat16)
+    sel = perm[:4].tolist()
+    # selected experts: bf16 copies of the bank's dequantized weights + LoRA
+    wgu, wdn = ol.frozen_weights(0, E, torch.float32)
+    ol.sel_ids = sel
+    ol.sel_gate_up, ol.sel_down = wgu[sel].to(torch.bfloat16), wdn[sel].to(torch.bfloat16)
+    ex_l = {}
+    for n, shp, fan in (("A_gate", (4, 8, H), H), ("A_up", (4, 8, H), H), ("A_down", (4, 8, I), I)):
+        ex_l[n] = (torch.rand(*shp, generator=g) * 2 - 1) / fan ** 0.5
+    for n, shp in (("B_gate", (4, I, 8)), ("B_up", (4, I, 8)), ("B_down", (4, H, 8))):
+        ex_l[n] = torch.randn(*shp, generator=g) * 0.05
+    ol.ex_lora, ol.ex_scale = ex_l, 2.0
+    return x, ol, K
+
+
+def test_layer_skewed_parity_and_determinism():
+    from smel.moe import moe_forward
+    _say("skewed routing layer")
+    x, ol, K = _skewed_layer()
+    W, ex, lora = to_device_layer(ol, DEV)
+    gy = (torch.randn(x.shape, generator=torch.Generator().manual_seed(5)) * 1e-2).to(torch.bfloat16)
+    outs = []
+    for _ in range(3):
+        xg = x.to(DEV).requires_grad_(True)
+        for m in (lora.experts, lora.shared):
+            for n in LORA_NAMES:
+                getattr(m, n).grad = None
+        seen = {}
+        y = moe_forward(xg, W, ex, K, lora, stats=lambda p, v, i: seen.update(i=i.clone()))
+        y.backward(gy.to(DEV))
+        torch.cuda.synchronize()
+        grads = {f"{t}_{n}": getattr(m, n).grad.detach().cpu().clone() for t, m in (("ex", lora.experts),
+                                                                                    ("sh", lora.shared))
+                 for n in LORA_NAMES}
+        outs.append((y.detach().cpu(), xg.grad.cpu(), grads, seen["i"].cpu()))
+    counts = torch.bincount(outs[0][3].reshape(-1), minlength=32)
+    _say(f"  rows per expert: max {int(counts.max())}, min {int(counts.min())}, empty {int((counts == 0).sum())}")
+    assert int(counts.max()) > 3 * 128          # hot experts span several tiles
+    for o in outs[1:]:                           # bitwise repeatable
+        assert torch.equal(o[0].view(torch.int16), outs[0][0].view(torch.int16))
+        assert torch.equal(o[1].view(torch.int16), outs[0][1].view(torch.int16))
+        for k in o[2]:
+            assert torch.equal(o[2][k], outs[0][2][k]), k
+    y, dx, grads = R.moe_forward_backward(x, ol, K, gy, forced_topi=outs[0][3], dtype=torch.float32)
+    assert_close_bf16(outs[0][0], y, "y")
+    assert_close_bf16(outs[0][1], dx, "dx")
+    for k, v in grads.items():
+        assert_close_bf16(outs[0][2][k], v, k)
