@@ -221,18 +221,38 @@ int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, f
 int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, int32_t with_shared, int64_t T, int64_t K, int64_t H,
                    uint16_t* dx, hipStream_t stream);
 
-/* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP):
- * for every LoRA group lora_groups[i] (expert id, or E for the shared rows [TK, TK+T)):
- *   out[i][p][q] = sum_{rows of the group} alpha(row) * L[row][p] * Rm[src(row)][q],  p < 32, q < Q
- * in a fixed order (MFMA over 64-row steps inside 1024-row chunks into part, then the chunks in order). src(row) =
- * token of the row if r_gather else row; Rm holds r_rows rows; alpha = the row weight (topv[p] / sgate[t]) if use_w,
- * else 1 (folded into L before its bf16 rounding). out [n_lora][32][Q] fp32; part [n_lora][part_chunks][32][Q] fp32
- * scratch with part_chunks = smel_lora_wgrad_part_chunks(max rows of one group). Q must be a multiple of 16. */
-int smel_lora_wgrad(const int32_t* lora_groups, int64_t n_lora, const int32_t* offsets, int64_t E, int64_t T,
-                    int64_t TK, int64_t topk, const int32_t* order, const uint16_t* L, const uint16_t* Rm,
-                    int64_t ldr, int64_t r_rows, int32_t r_gather, int32_t use_w, const uint16_t* topv,
-                    const float* sgate, int64_t Q, float* part, int64_t part_chunks, float* out, hipStream_t stream);
-int64_t smel_lora_wgrad_part_chunks(int64_t max_group_rows);
+/* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP), up to four
+ * products in one launch. For job j and every LoRA group lora_groups[i] (expert id, or E for the shared rows
+ * [TK, TK+T)):
+ *   R[p][q] = sum_{rows of the group} alpha(row) * L[row][p] * Rm[src(row)][q],  p < 32, q < Q
+ * summed in one fixed order (deterministic). src(row) = token of the row if r_gather else row; Rm holds r_rows rows;
+ * alpha = the row weight (topv[p] / sgate[t]) if use_w, else 1 (folded into L before its bf16 rounding).
+ * Each R[p][q] with p in [p0, p0+np) and q in [q0, q0+nq) of a destination is stored (fp32) at
+ *   ptr[slot * s_idx + (p - p0) * s_p + (q - q0) * s_q],
+ * dest[0][h] for groups i < n_sel (slot = i, the selected experts' LoRA tensors), dest[1][h] for the others (slot 0,
+ * the shared MLP's), h = 0, 1 for the two halves (gate / up) of a gate_up product; ptr NULL = not stored. Q must be a
+ * multiple of 16. */
+typedef struct smel_wg_dest {
+  float* ptr;
+  int64_t s_idx, s_p, s_q;
+  int32_t p0, np, q0, nq;
+} smel_wg_dest;
+typedef struct smel_wg_job {
+  const uint16_t* L;   /* [rows][32] bf16: the LoRA K-extension rows of the direction */
+  const uint16_t* Rm;  /* right operand rows, ldr elements apart                     */
+  int64_t ldr, r_rows;
+  int32_t r_gather, use_w;
+  int64_t Q;
+  smel_wg_dest dest[2][2];
+} smel_wg_job;
+/* Groups of more than 512 rows are cut into 512-row chunks whose fp32 partial tiles go to the caller's workspace ws
+ * (ws_floats >= smel_lora_wgrad_ws_floats(jobs, n_jobs, n_lora, max_rows), max_rows >= the rows of all LoRA groups
+ * together) and are summed in chunk order by a second launch. */
+int64_t smel_lora_wgrad_ws_floats(const smel_wg_job* jobs, int32_t n_jobs, int64_t n_lora, int64_t max_rows);
+int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const int32_t* lora_groups, int64_t n_lora,
+                    int64_t n_sel, const int32_t* offsets, int64_t E, int64_t T, int64_t TK, int64_t topk,
+                    const int32_t* order, const uint16_t* topv, const float* sgate, int64_t max_rows, float* ws,
+                    int64_t ws_floats, hipStream_t stream);
 
 #ifdef __cplusplus
 }

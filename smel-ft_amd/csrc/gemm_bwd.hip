@@ -224,7 +224,7 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     };
     // 3-stage ring, every operand by LDS-DMA, two steps ahead: before step j only step j+1's loads may be in flight.
-    constexpr int NV = 3 + (SZ2 ? 2 : 1) + 4;   // vector-memory ops per step
+    constexpr int NV = 2 + (SZ2 ? 2 : 1) + 4;   // vector-memory ops per step: 2 q, 1-2 scale/zero, 4 A
     auto step = [&](int j, int st) {
       SMEL_WAIT_VM_LDS(NV);
       __builtin_amdgcn_s_barrier();

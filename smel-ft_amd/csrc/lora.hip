@@ -156,123 +156,237 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
   }
 }
 
-// part[i][c][p][q] = sum over rows c*CH .. c*CH+CH-1 of group lora_groups[i]: alpha(row) L[row][p] Rm[src(row)][q],
-// as an MFMA GEMM with the row index as the contraction dim: per 64-row step, L and Rm are staged transposed in LDS
-// (k-pair packing: the values of rows 2j and 2j+1 share one 32-bit word), then each wave multiplies the 32 x 64 L^T
-// tile by its 64 x 32 slice of the Rm tile. Block = 4 waves = 32 p x 128 q. The LDS tiles are double-buffered and
-// the raw rows of step j+1 are loaded into registers before step j's MFMAs, so one barrier per step suffices and a
-// load's latency overlaps a step of work.
-constexpr int WG_CH = 256;    // rows per chunk
+// LoRA factor gradients, all four products of a backward in one launch. Block = (job, LoRA group i, 128-column
+// block): out[p][q] = sum over ALL rows of group i of alpha(row) L[row][p] Rm[src(row)][q], p < 32, as an MFMA GEMM
+// with the row index as the contraction dim: per 64-row step, L and Rm are staged transposed in LDS (k-pair packing:
+// the values of rows 2j and 2j+1 share one 32-bit word), then each wave multiplies the 32 x 64 L^T tile by its 64 x 32
+// slice of the Rm tile. The LDS tiles are double-buffered and the raw rows of step j+1 are loaded into registers
+// before step j's MFMAs, so one barrier per step suffices. Rows are summed in one fixed order (deterministic), and
+// each (p, q) goes straight to the gradient tensor the job's destination descriptor names.
 constexpr int WG_QB = 128;    // columns per block
 constexpr int WG_S = 64 + 8;  // LDS row stride (bf16)
+constexpr int WG_PF = 4;      // 64-row steps in flight
+constexpr int WG_CH = 512;    // rows per chunk block
+constexpr int WG_MAXG = 256;  // LoRA groups per call
+constexpr int WG_WIN = WG_CH; // rows per index window
 
-__global__ __launch_bounds__(256) void lora_wgrad_part(const int32_t* __restrict__ groups, const int32_t* __restrict__ offsets,
-                                                       int E, int T, int TK, int topk, const int32_t* __restrict__ order,
-                                                       const uint16_t* __restrict__ L, const uint16_t* __restrict__ Rm,
-                                                       int64_t ldr, int64_t r_rows, int r_gather, int use_w,
-                                                       const uint16_t* __restrict__ topv, const float* __restrict__ sgate,
-                                                       int Q, float* __restrict__ part, int chunks) {
+struct WgArgs {
+  smel_wg_job job[4];
+  int item0[5];                // first block of each job
+  int qb0[4];                  // first 128-column block of each job in the partial-tile space
+  int tot;                     // partial-tile slots per column block
+  float* ws;                   // partial tiles [sum of column blocks][tot][32 * 128]
+  const int32_t* groups;
+  int n_lora, n_sel;
+  const int32_t* offsets;
+  int E, T, TK, topk;
+  const int32_t* order;
+  const uint16_t* topv;
+  const float* sgate;
+};
+
+// The LoRA groups' first row G0, row count GN and first chunk slot GC (GC[n] = slots used), into LDS: thread i loads
+// group i's offsets (all groups at once, one memory latency). Returns the number of groups.
+SMEL_DEV int wg_table(const WgArgs& a, int* G0, int* GN, int* GC) {
+  const int tid = threadIdx.x;
+  if (tid < a.n_lora) {
+    const int g = a.groups[tid];
+    G0[tid] = g < a.E ? a.offsets[g] : a.TK;
+    GN[tid] = g < a.E ? a.offsets[g + 1] - a.offsets[g] : a.T;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    // the host's row bound caps the slots (monotone, <= tot): nothing is read or written out of range
+    int c = 0;
+    for (int i = 0; i < a.n_lora; ++i) {
+      GC[i] = min(c, a.tot);
+      c += max(1, (GN[i] + WG_CH - 1) / WG_CH);
+    }
+    GC[a.n_lora] = min(c, a.tot);
+  }
+  __syncthreads();
+  return a.n_lora;
+}
+
+// R[p][q] of one 32 x 32 wave tile (acc of wave w, lane l; column block q0) -> the job's destination for group i's
+// class (selected slot i, or the shared set) and p-range.
+SMEL_DEV void wg_store(const smel_wg_job& J, int n_sel, int i, int q0, int w, int l, const f32x16_t& acc) {
+  const int q = q0 + 32 * w + (l & 31);
+  if (q >= J.Q) return;
+  const int cls = i < n_sel ? 0 : 1;
+  const int64_t slot = cls == 0 ? i : 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const smel_wg_dest& d = J.dest[cls][h];
+    if (!d.ptr || q < d.q0 || q >= d.q0 + d.nq) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int p = acc_row(r, l);
+      if (p >= d.p0 && p < d.p0 + d.np)
+        d.ptr[slot * d.s_idx + (int64_t)(p - d.p0) * d.s_p + (int64_t)(q - d.q0) * d.s_q] = acc[r];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t LT[2][32 * WG_S];
   __shared__ __attribute__((aligned(16))) uint16_t RT[2][WG_QB * WG_S];
-  const int i = blockIdx.x, c = blockIdx.z;
-  const int g = groups[i];
-  const int r0 = g < E ? offsets[g] : TK;
-  const int r1 = g < E ? offsets[g + 1] : TK + T;
-  const int a0 = r0 + c * WG_CH;
-  if (a0 >= r1) return;
-  const int a1 = min(r1, a0 + WG_CH);
-  const int q0 = blockIdx.y * WG_QB;
+  __shared__ uint32_t TOFF[WG_WIN];
+  __shared__ float TAL[WG_WIN];
+  __shared__ int G0[WG_MAXG], GN[WG_MAXG], GC[WG_MAXG + 1];
+  int jb = 0;
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    if ((int)blockIdx.x >= a.item0[j]) jb = j;
+  const smel_wg_job& J = a.job[jb];
+  const int item = blockIdx.x - a.item0[jb];
+  const int sl = item % a.tot, qb = item / a.tot;   // chunk slot, column block
+  // the groups' rows, loaded in parallel (one memory latency), and their chunk slots: group i owns slots
+  // [GC[i], GC[i+1]), one per 512-row chunk (at least one)
+  const int ng = wg_table(a, G0, GN, GC);
+  if (sl >= GC[ng]) return;
+  int i = 0;
+  while (GC[i + 1] <= sl) ++i;
+  const int c = sl - GC[i];
+  const int nch = GC[i + 1] - GC[i];
+  const int g0 = G0[i], g1 = G0[i] + GN[i];
+  // this block: rows [a0, a1) = chunk c of the group
+  const int a0 = g0 + c * WG_CH;
+  const int a1 = min(g1, a0 + WG_CH);
+  const int q0 = qb * WG_QB;
+  const int Q = (int)J.Q;
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
   const int kp = tid & 31, grp = tid >> 5;   // k pair, and 4 p's (L) / 16 q's (Rm) per thread
   const int qq = q0 + 16 * grp;
   const bool qok = qq < Q;
-  const rsrc_t rr = make_rsrc(Rm, (uint64_t)r_rows * ldr * 2);
+  const rsrc_t rr = make_rsrc(J.Rm, (uint64_t)J.r_rows * J.ldr * 2);
+  const int64_t ldr = J.ldr;
+  const int r_gather = J.r_gather, use_w = J.use_w;
+  const uint16_t* __restrict__ Lp = J.L;
   f32x16_t acc = f32x16_t{};
-  // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights
-  uint2 lv0, lv1;
-  u32x4_t x0[2], x1[2];
-  float al0, al1;
-  auto row_info = [&](int row, uint32_t& roff, float& alpha) {
-    roff = OOB;
-    alpha = 0.f;
-    if (row < a1) {
+  // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights;
+  // WG_PF steps are in flight (a register ring rotated by unrolling): a long group (the shared MLP's T rows) is bound
+  // by the load latency, not by its few MFMAs.
+  struct Raw {
+    uint2 lv0, lv1;
+    u32x4_t x0[2], x1[2];
+    float al0, al1;
+  };
+  Raw rw[WG_PF];
+  // per window of WG_WIN rows: source-row byte offset and row weight of every row, built once into LDS so that the
+  // prefetched loads depend on LDS reads only (a load whose address came from a global load would make the wait for
+  // it drain every load in flight, vmcnt retiring in order)
+  auto build = [&](int w0, int w1) {
+    for (int row = w0 + tid; row < w1; row += 256) {
       int src = row;
-      alpha = 1.f;
-      if (row < TK) {
-        const int p = order[row];
-        if (r_gather) src = p / topk;
-        if (use_w) alpha = bf2f(topv[p]);
+      float alpha = 1.f;
+      if (row < a.TK) {
+        const int p = a.order[row];
+        if (r_gather) src = p / a.topk;
+        if (use_w) alpha = bf2f(a.topv[p]);
       } else {
-        if (r_gather) src = row - TK;
-        if (use_w) alpha = sgate[row - TK];
+        if (r_gather) src = row - a.TK;
+        if (use_w) alpha = a.sgate[row - a.TK];
       }
-      roff = (uint32_t)src * (uint32_t)ldr * 2;
+      TOFF[row - w0] = (uint32_t)src * (uint32_t)ldr * 2;
+      TAL[row - w0] = alpha;
     }
   };
-  auto load = [&](int k0) {
+  const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * 64);   // L rows [0, a1): a row past the group reads zeros
+  // branch-free: rows past the window get an out-of-range offset (zeros) and weight 0
+  auto load = [&](int k0, int w0, int w1, Raw& R) {
     const int ra = k0 + 2 * kp;
-    uint32_t o0, o1;
-    row_info(ra, o0, al0);
-    row_info(ra + 1, o1, al1);
-    lv0 = ra < a1 ? *reinterpret_cast<const uint2*>(L + (int64_t)ra * 32 + 4 * grp) : make_uint2(0, 0);
-    lv1 = ra + 1 < a1 ? *reinterpret_cast<const uint2*>(L + (int64_t)(ra + 1) * 32 + 4 * grp) : make_uint2(0, 0);
+    const bool v0 = ra < w1, v1 = ra + 1 < w1;
+    const int t0 = v0 ? ra - w0 : 0, t1 = v1 ? ra + 1 - w0 : 0;
+    const uint32_t o0 = v0 ? TOFF[t0] : OOB, o1 = v1 ? TOFF[t1] : OOB;
+    R.al0 = v0 ? TAL[t0] : 0.f;
+    R.al1 = v1 ? TAL[t1] : 0.f;
+    const u32x2_t l0 = ld8(rl, v0 ? (uint32_t)ra * 64 + 8 * grp : OOB);
+    const u32x2_t l1 = ld8(rl, v1 ? (uint32_t)(ra + 1) * 64 + 8 * grp : OOB);
+    R.lv0 = make_uint2(l0.x, l0.y);
+    R.lv1 = make_uint2(l1.x, l1.y);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
-      x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+      R.x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+      R.x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
     }
   };
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, const Raw& R) {
     // L^T: alpha folded in (fp32, one bf16 rounding)
     uint32_t* d = reinterpret_cast<uint32_t*>(LT[buf] + (4 * grp) * WG_S + 2 * kp);
-    d[0 * (WG_S / 2)] = pack2bf(al0 * bf_lo(lv0.x), al1 * bf_lo(lv1.x));
-    d[1 * (WG_S / 2)] = pack2bf(al0 * bf_hi(lv0.x), al1 * bf_hi(lv1.x));
-    d[2 * (WG_S / 2)] = pack2bf(al0 * bf_lo(lv0.y), al1 * bf_lo(lv1.y));
-    d[3 * (WG_S / 2)] = pack2bf(al0 * bf_hi(lv0.y), al1 * bf_hi(lv1.y));
+    d[0 * (WG_S / 2)] = pack2bf(R.al0 * bf_lo(R.lv0.x), R.al1 * bf_lo(R.lv1.x));
+    d[1 * (WG_S / 2)] = pack2bf(R.al0 * bf_hi(R.lv0.x), R.al1 * bf_hi(R.lv1.x));
+    d[2 * (WG_S / 2)] = pack2bf(R.al0 * bf_lo(R.lv0.y), R.al1 * bf_lo(R.lv1.y));
+    d[3 * (WG_S / 2)] = pack2bf(R.al0 * bf_hi(R.lv0.y), R.al1 * bf_hi(R.lv1.y));
     uint32_t* e = reinterpret_cast<uint32_t*>(RT[buf] + (16 * grp) * WG_S + 2 * kp);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        e[(8 * h + 2 * j) * (WG_S / 2)] = __builtin_amdgcn_perm(x1[h][j], x0[h][j], 0x05040100u);
-        e[(8 * h + 2 * j + 1) * (WG_S / 2)] = __builtin_amdgcn_perm(x1[h][j], x0[h][j], 0x07060302u);
+        e[(8 * h + 2 * j) * (WG_S / 2)] = __builtin_amdgcn_perm(R.x1[h][j], R.x0[h][j], 0x05040100u);
+        e[(8 * h + 2 * j + 1) * (WG_S / 2)] = __builtin_amdgcn_perm(R.x1[h][j], R.x0[h][j], 0x07060302u);
       }
   };
-  load(a0);
-  int buf = 0;
-  for (int k0 = a0; k0 < a1; k0 += 64) {
-    stage(buf);
-    if (k0 + 64 < a1) load(k0 + 64);
+  for (int w0 = a0; w0 < a1; w0 += WG_WIN) {   // uniform
+    const int w1 = min(a1, w0 + WG_WIN);
+    __syncthreads();   // the previous window's table and tiles are no longer read
+    build(w0, w1);
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT[buf] + r32 * WG_S + 32 * hi + 8 * s);
-      const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT[buf] + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
-      acc = mfma32(af, bfr, acc);
-    }
-    buf ^= 1;
-  }
-  const int q = q0 + 32 * w + r32;
-  if (q < Q) {
-    float* dst = part + ((int64_t)i * chunks + c) * 32 * Q + q;
+    for (int u = 0; u < WG_PF; ++u) load(w0 + 64 * u, w0, w1, rw[u]);
+    for (int k0 = w0; k0 < w1; k0 += 64 * WG_PF) {
+      // WG_PF steps per round, branch-free (a step past the window stages zeros and adds nothing), so the compiler's
+      // wait for a ring slot counts exactly the loads issued after it
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dst[(int64_t)acc_row(r, l) * Q] = acc[r];
+      for (int u = 0; u < WG_PF; ++u) {
+        const int kk = k0 + 64 * u;
+        const int buf = u & 1;
+        stage(buf, rw[u]);
+        load(kk + 64 * WG_PF, w0, w1, rw[u]);   // past the window: out-of-range loads, zeros
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT[buf] + r32 * WG_S + 32 * hi + 8 * s);
+          const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT[buf] + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
+          acc = mfma32(af, bfr, acc);
+        }
+      }
+    }
   }
+  if (nch == 1) {
+    wg_store(J, a.n_sel, i, q0, w, l, acc);
+    return;
+  }
+  // a group of several chunks: this chunk's partial tile, summed in chunk order by lora_wgrad_reduce
+  float* tile = a.ws + ((int64_t)(a.qb0[jb] + qb) * a.tot + sl) * (32 * WG_QB);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = acc[r];
 }
 
-__global__ __launch_bounds__(256) void lora_wgrad_sum(const int32_t* __restrict__ groups,
-                                                      const int32_t* __restrict__ offsets, int E, int T, int TK,
-                                                      int Q, const float* __restrict__ part, int chunks,
-                                                      float* __restrict__ out) {
-  const int i = blockIdx.y;
-  const int g = groups[i];
-  const int rows = g < E ? offsets[g + 1] - offsets[g] : T;
-  const int nch = min((rows + WG_CH - 1) / WG_CH, chunks);
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < (int64_t)32 * Q; e += (int64_t)gridDim.x * blockDim.x) {
-    float v = 0.f;
-    for (int c = 0; c < nch; ++c) v += part[((int64_t)i * chunks + c) * 32 * Q + e];
-    out[(int64_t)i * 32 * Q + e] = v;
-  }
+// The multi-chunk groups: sum the partial tiles in chunk order, store like lora_wgrad_kernel. Block = (job, column
+// block, group).
+__global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
+  __shared__ int G0[WG_MAXG], GN[WG_MAXG], GC[WG_MAXG + 1];
+  int jb = 0;
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    if ((int)blockIdx.x >= a.qb0[j] * a.n_lora) jb = j;
+  const smel_wg_job& J = a.job[jb];
+  const int item = blockIdx.x - a.qb0[jb] * a.n_lora;
+  const int qb = item / a.n_lora, i = item - qb * a.n_lora;
+  const int ng = wg_table(a, G0, GN, GC);
+  if (i >= ng) return;
+  const int nch = GC[i + 1] - GC[i];
+  if (nch <= 1) return;
+  const int tid = threadIdx.x;
+  const float* tile = a.ws + ((int64_t)(a.qb0[jb] + qb) * a.tot + GC[i]) * (32 * WG_QB);
+  f32x16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = tile[r * 256 + tid];
+  for (int cc = 1; cc < nch; ++cc)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += tile[(int64_t)cc * (32 * WG_QB) + r * 256 + tid];
+  wg_store(J, a.n_sel, i, qb * WG_QB, tid >> 6, lane_id(), acc);
 }
 
 }  // namespace
@@ -310,29 +424,78 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
   return smel::launch_status();
 }
 
-extern "C" int64_t smel_lora_wgrad_part_chunks(int64_t max_group_rows) {
-  return (max_group_rows + WG_CH - 1) / WG_CH;
+namespace {
+int64_t wg_qblocks(const smel_wg_job* jobs, int n_jobs) {
+  int64_t n = 0;
+  for (int j = 0; j < n_jobs; ++j) n += (jobs[j].Q + WG_QB - 1) / WG_QB;
+  return n;
+}
+int64_t wg_tot(int64_t n_lora, int64_t max_rows) { return n_lora + (max_rows + WG_CH - 1) / WG_CH; }
+}  // namespace
+
+extern "C" int64_t smel_lora_wgrad_ws_floats(const smel_wg_job* jobs, int32_t n_jobs, int64_t n_lora,
+                                             int64_t max_rows) {
+  if (!jobs || n_jobs < 0 || n_jobs > 4 || n_lora < 0 || max_rows < 0) return -1;
+  return wg_qblocks(jobs, n_jobs) * wg_tot(n_lora, max_rows) * 32 * WG_QB;
 }
 
-extern "C" int smel_lora_wgrad(const int32_t* lora_groups, int64_t n_lora, const int32_t* offsets, int64_t E,
-                               int64_t T, int64_t TK, int64_t topk, const int32_t* order, const uint16_t* L,
-                               const uint16_t* Rm, int64_t ldr, int64_t r_rows, int32_t r_gather, int32_t use_w,
-                               const uint16_t* topv, const float* sgate, int64_t Q, float* part,
-                               int64_t part_chunks, float* out, hipStream_t stream) {
-  SMEL_REQUIRE(n_lora >= 0 && Q > 0 && part_chunks >= 0, SMEL_EINVAL, "lora_wgrad: bad sizes");
-  if (n_lora == 0 || part_chunks == 0) return 0;
-  SMEL_REQUIRE(lora_groups && offsets && L && Rm && part && out, SMEL_EINVAL, "lora_wgrad: null pointer");
-  SMEL_REQUIRE(!(r_gather || use_w) || order || TK == 0, SMEL_EINVAL, "lora_wgrad: needs order");
-  SMEL_REQUIRE(ldr % 8 == 0 && Q % 16 == 0 && ((uintptr_t)Rm % 16) == 0, SMEL_EUNSUPPORTED,
-               "lora_wgrad: Rm rows must be 16-B aligned and Q a multiple of 16");
-  SMEL_REQUIRE(r_rows * ldr * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "lora_wgrad: Rm larger than 2 GiB");
-  dim3 g1((unsigned)n_lora, (unsigned)((Q + WG_QB - 1) / WG_QB), (unsigned)part_chunks);
-  lora_wgrad_part<<<g1, 256, 0, stream>>>(lora_groups, offsets, (int)E, (int)T, (int)TK, (int)topk, order, L, Rm, ldr,
-                                          r_rows, r_gather, use_w, topv, sgate, (int)Q, part, (int)part_chunks);
+extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const int32_t* lora_groups, int64_t n_lora,
+                               int64_t n_sel, const int32_t* offsets, int64_t E, int64_t T, int64_t TK, int64_t topk,
+                               const int32_t* order, const uint16_t* topv, const float* sgate, int64_t max_rows,
+                               float* ws, int64_t ws_floats, hipStream_t stream) {
+  SMEL_REQUIRE(jobs && n_jobs >= 0 && n_jobs <= 4 && n_lora >= 0 && n_sel >= 0 && n_sel <= n_lora && max_rows >= 0,
+               SMEL_EINVAL, "lora_wgrad: bad job / group counts");
+  if (n_jobs == 0 || n_lora == 0) return 0;
+  SMEL_REQUIRE(lora_groups && offsets, SMEL_EINVAL, "lora_wgrad: null pointer");
+  SMEL_REQUIRE(n_lora <= WG_MAXG, SMEL_EUNSUPPORTED, "lora_wgrad: %lld LoRA groups > %d", (long long)n_lora, WG_MAXG);
+  SMEL_REQUIRE(ws && ws_floats >= smel_lora_wgrad_ws_floats(jobs, n_jobs, n_lora, max_rows), SMEL_EINVAL,
+               "lora_wgrad: workspace smaller than smel_lora_wgrad_ws_floats");
+  WgArgs a;
+  a.tot = (int)wg_tot(n_lora, max_rows);
+  a.ws = ws;
+  int items = 0, qbs = 0;
+  for (int j = 0; j < 4; ++j) {
+    a.item0[j] = items;
+    a.qb0[j] = qbs;
+    if (j < n_jobs) {
+      const smel_wg_job& J = jobs[j];
+      SMEL_REQUIRE(J.L && J.Rm && J.Q > 0, SMEL_EINVAL, "lora_wgrad: job %d: null operand or Q", j);
+      SMEL_REQUIRE(!(J.r_gather || J.use_w) || order || TK == 0, SMEL_EINVAL, "lora_wgrad: job %d needs order", j);
+      SMEL_REQUIRE(J.ldr % 8 == 0 && J.Q % 16 == 0 && ((uintptr_t)J.Rm % 16) == 0, SMEL_EUNSUPPORTED,
+                   "lora_wgrad: job %d: Rm rows must be 16-B aligned and Q a multiple of 16", j);
+      SMEL_REQUIRE(J.r_rows * J.ldr * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "lora_wgrad: job %d: Rm larger than 2 GiB",
+                   j);
+      for (int c = 0; c < 2; ++c)
+        for (int h = 0; h < 2; ++h) {
+          const smel_wg_dest& d = J.dest[c][h];
+          SMEL_REQUIRE(!d.ptr || (d.p0 >= 0 && d.np >= 0 && d.p0 + d.np <= 32 && d.q0 >= 0 && d.nq >= 0 &&
+                                  d.q0 + d.nq <= J.Q),
+                       SMEL_EINVAL, "lora_wgrad: job %d: destination [%d][%d] outside the 32 x Q result", j, c, h);
+        }
+      a.job[j] = J;
+      const int nqb = (int)((J.Q + WG_QB - 1) / WG_QB);
+      items += nqb * a.tot;
+      qbs += nqb;
+    } else {
+      a.job[j] = smel_wg_job{};
+      a.job[j].Q = WG_QB;
+    }
+  }
+  a.item0[4] = items;
+  a.groups = lora_groups;
+  a.n_lora = (int)n_lora;
+  a.n_sel = (int)n_sel;
+  a.offsets = offsets;
+  a.E = (int)E;
+  a.T = (int)T;
+  a.TK = (int)TK;
+  a.topk = (int)topk;
+  a.order = order;
+  a.topv = topv;
+  a.sgate = sgate;
+  lora_wgrad_kernel<<<(unsigned)items, 256, 0, stream>>>(a);
   int st = smel::launch_status();
   if (st) return st;
-  dim3 g2((unsigned)std::min<int64_t>((32 * Q + 255) / 256, 1024), (unsigned)n_lora);
-  lora_wgrad_sum<<<g2, 256, 0, stream>>>(lora_groups, offsets, (int)E, (int)T, (int)TK, (int)Q, part,
-                                         (int)part_chunks, out);
+  lora_wgrad_reduce<<<(unsigned)(qbs * n_lora), 256, 0, stream>>>(a);
   return smel::launch_status();
 }

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(HERE, "libsmel_moe.so")
 
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -24,6 +24,18 @@ class WSet(ctypes.Structure):
     """smel_wset of include/smel_moe.h."""
     _fields_ = [("q4", vp), ("sz4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp), ("ext_sel", vp), ("ext_sh", vp),
                 ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
+
+
+class WgDest(ctypes.Structure):
+    """smel_wg_dest of include/smel_moe.h."""
+    _fields_ = [("ptr", vp), ("s_idx", i64), ("s_p", i64), ("s_q", i64), ("p0", i32), ("np", i32), ("q0", i32),
+                ("nq", i32)]
+
+
+class WgJob(ctypes.Structure):
+    """smel_wg_job of include/smel_moe.h."""
+    _fields_ = [("L", vp), ("Rm", vp), ("ldr", i64), ("r_rows", i64), ("r_gather", i32), ("use_w", i32), ("Q", i64),
+                ("dest", (WgDest * 2) * 2)]
 
 
 # name -> (restype, argtypes)
@@ -56,9 +68,9 @@ SIGNATURES = {
     "smel_route_gemma4_prenorm_bwd": (i32, [vp, vp, vp, vp, i64, i64, vp, vp]),
     "smel_dtopv": (i32, [vp, i64, vp, i64, vp, vp]),
     "smel_dx_reduce": (i32, [vp, vp, i32, i64, i64, i64, vp, vp]),
-    "smel_lora_wgrad": (i32, [vp, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, i64, i32, i32, vp, vp, i64, vp, i64,
-                              vp, vp]),
-    "smel_lora_wgrad_part_chunks": (i64, [i64]),
+    "smel_lora_wgrad": (i32, [ctypes.POINTER(WgJob), i32, vp, i64, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp,
+                              i64, vp]),
+    "smel_lora_wgrad_ws_floats": (i64, [ctypes.POINTER(WgJob), i32, i64, i64]),
 }
 
 _lib = None

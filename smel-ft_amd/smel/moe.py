@@ -628,36 +628,25 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
         L.call("smel_dtopv", L.ptr(dwp), nblk, L.ptr(t["inv"]), TK, L.ptr(dtopv), st)
     dx = bf(T, H)
     L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), int(t["sgate"] is not None), T, K, H, L.ptr(dx), st)
-    # (6) LoRA factor gradients
+    # (6) LoRA factor gradients: one launch for the four products, written into parameter-shaped fp32 tensors
     grads = {}
     if any_lora:
         n_sel = len(ex._slot) if lb_ex is not None else 0
         groups = _lora_groups(ex, lb_sh is not None, n_sel, dev)
-        n_lora = groups.numel()
-        chunks = L.load().smel_lora_wgrad_part_chunks(T)
-        Qmax = max(H, 2 * I)
-        part = torch.empty(n_lora * chunks * EXT * Qmax, dtype=torch.float32, device=dev)
-
-        def wgrad(Lbuf, Rm, ldr, r_gather, use_w, Q):
-            out = torch.empty(n_lora, EXT, Q, dtype=torch.float32, device=dev)
-            L.call("smel_lora_wgrad", L.ptr(groups), n_lora, L.ptr(t["offsets"]), E, T, TK, K, L.ptr(order),
-                   L.ptr(Lbuf), L.ptr(Rm), ldr, Rm.shape[0], r_gather, use_w, L.ptr(t["topv"]), L.ptr(t["sgate"]), Q,
-                   L.ptr(part), chunks, L.ptr(out), st, tag="lora_wgrad")
-            return out
-
-        dA_gu = wgrad(ext_dxa, t["x"], H, 1, 0, H)          # [n, 32, H]: A_gate rows 0..r-1, A_up rows 16..
-        dB_gu = wgrad(t["ext_gu"], dh, 2 * I, 0, 0, 2 * I)   # [n, 32, 2I]
-        dA_dn = wgrad(ext_db, t["act"], I, 0, 1, I)         # [n, 32, I]
-        dB_dn = wgrad(t["ext_dn"], dout, H, 1, 1, H)         # [n, 32, H]
-        for tag, lb, j0, n in (("ex", lb_ex, 0, n_sel), ("sh", lb_sh, n_sel, 1 if lb_sh is not None else 0)):
-            if lb is None:
-                continue
-            r = lb.r
-            sl = slice(j0, j0 + n)
-            grads[tag] = {
-                "A_gate": dA_gu[sl, :r, :], "A_up": dA_gu[sl, 16:16 + r, :],
-                "B_gate": dB_gu[sl, :r, :I].transpose(1, 2), "B_up": dB_gu[sl, 16:16 + r, I:].transpose(1, 2),
-                "A_down": dA_dn[sl, :r, :], "B_down": dB_dn[sl, :r, :].transpose(1, 2)}
+        sets = ((c.lora_ex if lb_ex is not None else None), (c.lora_sh if lb_sh is not None else None))
+        gx, gs = (_alloc_lora_grads(m, dev) for m in sets)
+        jobs = _wgrad_jobs(H, I, (gx, gs), sets, (ext_dxa, t["x"], T, 1, 0), (t["ext_gu"], dh, M, 0, 0),
+                           (ext_db, t["act"], M, 0, 1), (t["ext_dn"], dout, T, 1, 1))
+        # rows of all LoRA groups: a token routes at most min(K, n_sel) slots to selected experts, + the shared rows
+        max_rows = (min(K, n_sel) * T if lb_ex is not None else 0) + (T if lb_sh is not None else 0)
+        ws = _wgrad_ws(jobs, groups.numel(), max_rows, dev)
+        L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK, K,
+               L.ptr(order), L.ptr(t["topv"]), L.ptr(t["sgate"]), max_rows, L.ptr(ws), ws.numel(), st,
+               tag="lora_wgrad")
+        if gx is not None:
+            grads["ex"] = gx
+        if gs is not None:
+            grads["sh"] = gs
     return dx, dtopv, grads
 
 
@@ -668,18 +657,70 @@ def _lora_leaves(lora):
     return [getattr(lora, n) for n in _LORA_NAMES] if lora is not None else []
 
 
-def _shape_grads(grads: dict, tag: str, lora, squeeze: bool):
+def _shape_grads(grads: dict, tag: str, lora, squeeze: bool = False):
+    """The parameter-shaped LoRA gradients of one set (None where a parameter needs none)."""
     if lora is None:
         return []
     if tag not in grads:
         return [None] * 6
-    out = []
-    for n in _LORA_NAMES:
-        gr = grads[tag][n]
-        gr = gr[0] if squeeze else gr
-        p = getattr(lora, n)
-        out.append(gr.contiguous().to(p.dtype).reshape(p.shape) if p.requires_grad else None)
-    return out
+    return [grads[tag].get(n) for n in _LORA_NAMES]
+
+
+def _alloc_lora_grads(lora, device):
+    """fp32 gradient tensors shaped like the LoRA parameters that require a gradient (each element is written by the
+    weight-gradient kernel), or None without the set."""
+    if lora is None:
+        return None
+    return {n: torch.empty(getattr(lora, n).shape, dtype=torch.float32, device=device)
+            for n in _LORA_NAMES if getattr(lora, n).requires_grad}
+
+
+def _wgrad_ws(jobs, n_lora: int, max_rows: int, device) -> torch.Tensor:
+    """fp32 workspace of smel_lora_wgrad (partial tiles of the groups longer than one 512-row chunk)."""
+    n = L.load().smel_lora_wgrad_ws_floats(jobs, 4, n_lora, max_rows)
+    return torch.empty(max(n, 1), dtype=torch.float32, device=device)
+
+
+def _wgrad_jobs(H, I, grads, sets, j_agu, j_bgu, j_adn, j_bdn):
+    """The four smel_wg_job of a backward (dA of gate/up, dB of gate/up, dA of down, dB of down). Each j_* =
+    (L rows, Rm, Rm rows, r_gather, use_w). Destinations: class 0 = the selected experts' ExpertsLoRA (slot = its
+    index), class 1 = the shared MLPLoRA; gate/up products split in two halves (rows 0..15 / 16..31 of the rank
+    dimension, columns 0..I-1 / I..2I-1 for the B factors)."""
+    jobs = (L.WgJob * 4)()
+    Qs = (H, 2 * I, I, H)
+    for j, (spec, Q) in enumerate(zip((j_agu, j_bgu, j_adn, j_bdn), Qs)):
+        Lb, Rm, rows, gather, use_w = spec
+        J = jobs[j]
+        J.L, J.Rm, J.ldr, J.r_rows, J.r_gather, J.use_w, J.Q = L.ptr(Lb), L.ptr(Rm), Rm.shape[1], rows, gather, use_w, Q
+        for cls in range(2):
+            g, m = grads[cls], sets[cls]
+            if g is None:
+                continue
+            r = m.r
+            lead = 1 if cls == 0 else 0
+
+            def dest(h, name, p0, q0, nq, col_major):
+                t = g.get(name)
+                if t is None:
+                    return
+                d = J.dest[cls][h]
+                d.ptr = L.ptr(t)
+                d.s_idx = t.stride(0) if lead else 0
+                # A factors [.., r, Q] (p rows, q contiguous); B factors [.., Q, r] (q rows, p contiguous)
+                d.s_p, d.s_q = (1, t.stride(lead)) if col_major else (t.stride(lead), 1)
+                d.p0, d.np, d.q0, d.nq = p0, r, q0, nq
+
+            if j == 0:
+                dest(0, "A_gate", 0, 0, H, False)
+                dest(1, "A_up", 16, 0, H, False)
+            elif j == 1:
+                dest(0, "B_gate", 0, 0, I, True)
+                dest(1, "B_up", 16, I, I, True)
+            elif j == 2:
+                dest(0, "A_down", 0, 0, I, False)
+            else:
+                dest(0, "B_down", 0, 0, H, True)
+    return jobs
 
 
 class _MoELayerFn(torch.autograd.Function):
@@ -715,7 +756,7 @@ class _MoELayerFn(torch.autograd.Function):
     def backward(ctx, dout):
         c = ctx.c
         dx, _, grads = _backward_pipeline(c, dout, router=c.router)
-        g = _shape_grads(grads, "ex", c.lora_ex, False) + _shape_grads(grads, "sh", c.lora_sh, True)
+        g = _shape_grads(grads, "ex", c.lora_ex) + _shape_grads(grads, "sh", c.lora_sh)
         ctx.c = None
         return (dx, None, None, *g)
 
@@ -739,7 +780,7 @@ class _RoutedFn(torch.autograd.Function):
     def backward(ctx, dout):
         c = ctx.c
         dx, dtopv, grads = _backward_pipeline(c, dout, router=None)
-        g = _shape_grads(grads, "ex", c.lora_ex, False)
+        g = _shape_grads(grads, "ex", c.lora_ex)
         ctx.c = None
         return (dx, dtopv.to(ctx.topv_dtype), None, None, None, *g)
 
@@ -831,22 +872,13 @@ class _MLPFn(torch.autograd.Function):
         if lb is not None:
             zero = torch.zeros(2, dtype=torch.int32, device=dev)     # offsets of zero experts
             groups = torch.zeros(1, dtype=torch.int32, device=dev)   # group 0 >= E = 0: rows [0, T)
-            chunks = L.load().smel_lora_wgrad_part_chunks(T)
-            part = torch.empty(chunks * EXT * max(H, 2 * Is), dtype=torch.float32, device=dev)
-
-            def wgrad(Lbuf, Rm, Q):
-                out = torch.empty(1, EXT, Q, dtype=torch.float32, device=dev)
-                L.call("smel_lora_wgrad", L.ptr(groups), 1, L.ptr(zero), 0, T, 0, 1, None, L.ptr(Lbuf), L.ptr(Rm),
-                       Rm.shape[1], Rm.shape[0], 0, 0, None, None, Q, L.ptr(part), chunks, L.ptr(out), st)
-                return out[0]
-
-            r = lb.r
-            dA_gu, dB_gu = wgrad(ext_dxa, x, H), wgrad(ext_gu, dh, 2 * Is)
-            dA_dn, dB_dn = wgrad(ext_db, actb, Is), wgrad(ext_dn, dy, H)
-            named = {"A_gate": dA_gu[:r], "A_up": dA_gu[16:16 + r], "B_gate": dB_gu[:r, :Is].t(),
-                     "B_up": dB_gu[16:16 + r, Is:].t(), "A_down": dA_dn[:r], "B_down": dB_dn[:r].t()}
-            grads = [named[n].contiguous().to(getattr(lora, n).dtype) if getattr(lora, n).requires_grad else None
-                     for n in _LORA_NAMES]
+            gs = _alloc_lora_grads(lora, dev)
+            jobs = _wgrad_jobs(H, Is, (None, gs), (None, lora), (ext_dxa, x, T, 0, 0), (ext_gu, dh, T, 0, 0),
+                               (ext_db, actb, T, 0, 0), (ext_dn, dy, T, 0, 0))
+            ws = _wgrad_ws(jobs, 1, T, dev)
+            L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), 1, 0, L.ptr(zero), 0, T, 0, 1, None, None, None, T,
+                   L.ptr(ws), ws.numel(), st, tag="lora_wgrad")
+            grads = [gs.get(n) for n in _LORA_NAMES]
         ctx.lb = ctx.lora = ctx.ext = ctx.w = None
         return (dx, None, None, None, None, *grads)
 

@@ -36,6 +36,45 @@ def test_wset_layout_matches_header():
     assert ctypes.sizeof(_lib.WSet) == 7 * 8 + 2 * 8 + 2 * 4
 
 
+PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "smel_moe.h"
+#define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+int main() {
+  printf("smel_wset %zu\nsmel_wg_dest %zu\nsmel_wg_job %zu\n", sizeof(smel_wset), sizeof(smel_wg_dest),
+         sizeof(smel_wg_job));
+  F(smel_wset, R) F(smel_wset, group) F(smel_wg_dest, s_idx) F(smel_wg_dest, p0) F(smel_wg_dest, nq)
+  F(smel_wg_job, ldr) F(smel_wg_job, r_gather) F(smel_wg_job, Q) F(smel_wg_job, dest)
+  return 0;
+}
+"""
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """The ctypes mirrors of the header's structs have the C compiler's sizes and field offsets."""
+    import shutil
+    import subprocess
+    from smel import _lib
+    cxx = shutil.which("g++")
+    if cxx is None or not os.path.exists("/opt/rocm/include/hip/hip_runtime.h"):
+        pytest.skip("no host compiler / HIP headers")
+    src = tmp_path / "probe.cpp"
+    src.write_text(PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run([cxx, "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-I" + os.path.join(ROOT, "include"),
+                    str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                       text=True).stdout.splitlines())
+    mirror = {"smel_wset": _lib.WSet, "smel_wg_dest": _lib.WgDest, "smel_wg_job": _lib.WgJob}
+    for key, val in got.items():
+        if "." in key:
+            t, f = key.split(".")
+            assert getattr(mirror[t], f).offset == int(val), key
+        else:
+            assert ctypes.sizeof(mirror[key]) == int(val), key
+
+
 def test_host_side_rejections():
     """Shape checks happen on the host, before any launch, so they are safe without a GPU."""
     from smel import _lib
@@ -65,6 +104,16 @@ def test_host_side_rejections():
     with pytest.raises(_lib.SmelError):
         _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, 32, 64, 64, None, None, None, None, None,
                   None, None, None, None)
+    # LoRA weight gradients: a destination outside the 32 x Q result is rejected on the host
+    jobs = (_lib.WgJob * 4)()
+    jobs[0].L, jobs[0].Rm, jobs[0].ldr, jobs[0].r_rows, jobs[0].Q = 1, 16, 64, 4, 64
+    jobs[0].dest[1][0].ptr, jobs[0].dest[1][0].p0, jobs[0].dest[1][0].np, jobs[0].dest[1][0].nq = 16, 20, 16, 64
+    assert L.smel_lora_wgrad_ws_floats(jobs, 1, 1, 4) == 1 * (1 + 1) * 32 * 128
+    assert L.smel_lora_wgrad(jobs, 1, 1, 1, 0, 1, 0, 4, 0, 1, None, None, None, 4, 1, 1 << 20, None) == -1
+    assert b"destination" in L.smel_last_error()
+    jobs[0].dest[1][0].ptr = None
+    assert L.smel_lora_wgrad(jobs, 1, 1, 1, 0, 1, 0, 4, 0, 1, None, None, None, 4, 1, 16, None) == -1
+    assert b"workspace" in L.smel_last_error()
     # transposed layouts (backward GEMM operand): sizes and rejections
     assert L.smel_packed_t_bytes(_lib.PACK_Q4, 2, 1024, 2048, 64) == 2 * 64 * 16 * 1024
     assert L.smel_packed_t_bytes(_lib.PACK_SZ, 2, 1024, 2048, 64) == 2 * 32 * 16 * 256
