@@ -131,7 +131,7 @@ def build_gemma_block(device, cfg=GEMMA, seed=0):
 def kernel_work(tag, c, S):
     """(algorithmic FLOPs, algorithmic HBM bytes) of one launch of a kernel, from the layer's shape ``c`` and the
     number S of slots routed to selected experts. Bytes = every operand read once and every result written once:
-    frozen int4 experts (q + bf16 scale/zero) except the selected ones, selected / shared bf16 weights, activations
+    frozen int4 experts (q + scale/zero in the layout the kernel reads) except the selected ones, selected / shared bf16 weights, activations
     (the gathered token rows counted once per token), the LoRA K-extension rows, the saved pre-activations."""
     T, H, E, I, K, r = c["T"], c["H"], c["E"], c["I"], c["K"], c["r"]
     g = c["group"]
@@ -140,8 +140,14 @@ def kernel_work(tag, c, S):
     M = T * K + Msh
     Lr = S + Msh
     nfz = E - n_sel
-    gu_w = nfz * (2 * I * H // 2 + 2 * I * (H // g) * 4) + n_sel * 2 * I * H * 2 + (2 * I * H * 2 if Msh else 0)
-    dn_w = nfz * (H * I // 2 + H * (I // g) * 4) + n_sel * H * I * 2 + (H * I * 2 if Msh else 0)
+    # forward layouts: scale/zero as bf16 pairs (4 B per group); the backward's transposed layout keeps them as fp32
+    # pairs (8 B per group)
+    def bank(nq, ngroups, nbf, szb):
+        return nfz * (nq // 2 + ngroups * szb) + n_sel * nbf * 2 + (nbf * 2 if Msh else 0)
+    gu_w = bank(2 * I * H, 2 * I * (H // g), 2 * I * H, 4)
+    dn_w = bank(H * I, H * (I // g), H * I, 4)
+    gu_wt = bank(2 * I * H, 2 * I * (H // g), 2 * I * H, 8)
+    dn_wt = bank(H * I, H * (I // g), H * I, 8)
     ext = M * 32 * 2 if (Lr and r) else 0
     nblk = -(-I // 128)
     Epad = -(-(E + (1 if Msh else 0)) // 32) * 32
@@ -149,8 +155,8 @@ def kernel_work(tag, c, S):
     w = {"gemm_gu_fwd": (2 * M * H * 2 * I + 2 * Lr * r * 2 * I, gu_w + T * H * 2 + ext + M * I * 2 + M * 2 * I * 2),
          "gemm_dn_fwd": (2 * M * I * H + 2 * Lr * r * H, dn_w + M * I * 2 + ext + M * H * 2),
          "gemm_dn_bwd": (2 * M * H * I + 2 * Lr * r * I,
-                         dn_w + T * H * 2 + M * 2 * I * 2 + ext + M * 2 * I * 2 + M * nblk * 4),
-         "gemm_gu_bwd": (2 * M * 2 * I * H + 2 * Lr * 2 * r * H, gu_w + M * 2 * I * 2 + ext + M * H * 2),
+                         dn_wt + T * H * 2 + M * 2 * I * 2 + ext + M * 2 * I * 2 + M * nblk * 4),
+         "gemm_gu_bwd": (2 * M * 2 * I * H + 2 * Lr * 2 * r * H, gu_wt + M * 2 * I * 2 + ext + M * H * 2),
          "gemm_router_bwd": (2 * T * Epad * H, T * Epad * 2 + Epad * H * 2 + T * H * 2),
          "gemm_mlp_gu_fwd": (2 * T * H * 2 * Is + 2 * T * r * 2 * Is,
                              2 * Is * H * 2 + T * H * 2 + T * 64 + T * Is * 2 + T * 2 * Is * 2),

@@ -47,8 +47,9 @@ typedef struct smel_wset {
   const uint16_t* ext_sh;
   int64_t R, C;
   int32_t group;       /* int4 group along C (a multiple of 32)                                        */
-  int32_t pad_;
+  int32_t flags;       /* SMEL_WSET_FAST_DQ: every scale/zero group of q4 passed smel_int4_fast_ok       */
 } smel_wset;
+#define SMEL_WSET_FAST_DQ 1
 
 const char* smel_last_error(void);
 int smel_abi_version(void);
@@ -83,18 +84,24 @@ int smel_pack_bf16(const uint16_t* w, int64_t rows, int64_t K, int64_t ld, uint1
  * with p = a pair of 32 columns, ks = a 64-row step, lane l = 16 kq + i, substep s, 16-column fragment fr:
  *   SMEL_PACK_Q4   block (mat, p, ks) 1 KB:  lane chunk word 2 fr + s = the 8 nibbles (low first) of column
  *                                             32 p + 16 fr + i at rows 64 ks + 32 s + 8 kq + [0, 8)
- *   SMEL_PACK_SZ   block (mat, g, ks) 256 B: word 16 kq + 8 s + t = scale | zero << 16 of row 64 ks + 32 s + 8 kq + t
- *                                             in column group g (C / group groups)
+ *   SMEL_PACK_SZ   block (mat, g, ks) 512 B: fp32 pair 16 kq + 8 s + t = (scale, zero') of row 64 ks + 32 s + 8 kq + t
+ *                                             in column group g (C / group groups); zero' = fp32(zero - 1024 scale)
+ *                                             when packed with fast = 1, else zero
  *   SMEL_PACK_BF16 block (mat, p, ks, 2 fr + s) 1 KB: lane chunk = the 8 bf16 of that column at those rows
  * Rows >= R are zero. smel_packed_t_bytes gives the size of each (-1 for a bad argument). */
 int64_t smel_packed_t_bytes(int32_t what, int64_t n_mats, int64_t R, int64_t C, int64_t group);
 /* q [n_mats][R][C/2], scale/zero [n_mats][R][C/group] -> qt, szt. C a multiple of 32, group a multiple of 32
  * dividing C. */
 int smel_pack_int4_t(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t n_mats, int64_t R,
-                     int64_t C, int64_t group, uint8_t* qt, uint32_t* szt, hipStream_t stream);
+                     int64_t C, int64_t group, int32_t fast, uint8_t* qt, float* szt, hipStream_t stream);
 /* w [n_mats][R][ld] bf16 (first C columns) -> wt. C a multiple of 32. */
 int smel_pack_bf16_t(const uint16_t* w, int64_t n_mats, int64_t R, int64_t C, int64_t ld, uint16_t* wt,
                      hipStream_t stream);
+/* Scale / zero groups [n] bf16 (any bank's scale and zero tensors) -> *ok = 1 if every group has z - 1024 s, z - 64 s
+ * and s / 16 exactly representable as normal (or zero) fp32 values, else 0. Such a bank dequantizes with the cheaper
+ * fp16-magic form in the GEMMs (same values, bit for bit); pack it with fast = 1 and set SMEL_WSET_FAST_DQ.
+ * ok is device memory; the result is there when the stream reaches it. */
+int smel_int4_fast_ok(const uint16_t* scale, const uint16_t* zero, int64_t n, int32_t* ok, hipStream_t stream);
 
 /* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
  * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the

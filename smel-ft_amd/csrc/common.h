@@ -74,6 +74,44 @@ SMEL_DEV void dq8(uint32_t b, float s, float z, uint32_t out[4]) {
 // Nibble j (0..7) of b as float.
 SMEL_DEV float nib(uint32_t b, int j) { return (float)((b >> (4 * j)) & 0xfu); }
 
+// ---- The same value in 17 instead of 23 VALU ops (banks whose scale/zero pass smel_int4_fast_ok).
+// A nibble q ORed into the low mantissa bits of the fp16 1024.0 (0x6400) is the fp16 value 1024 + q, and in bits 4..7
+// it is 1024 + 16 q: exact. v_fma_mix_f32 multiplies that fp16 half (either half of a register, no extraction) by an
+// fp32 operand and adds an fp32 operand, rounded once:
+//   fma(1024 + q, s, z - 1024 s)       = fl(q s + z)
+//   fma(1024 + 16 q, s / 16, z - 64 s) = fl(q s + z)
+// whenever z - 1024 s, z - 64 s and s / 16 are exact fp32 values (both sides then round the same real number), which
+// smel_int4_fast_ok checks for every group of a bank when it is packed. One AND-OR per two weights replaces the
+// nibble split and the byte-to-float conversions of dq8.
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+SMEL_DEV float h_lo(uint32_t x) { return (float)__builtin_bit_cast(h2_t, x)[0]; }
+SMEL_DEV float h_hi(uint32_t x) { return (float)__builtin_bit_cast(h2_t, x)[1]; }
+// fp16 pair (1024, 1024) in a vector register: v_and_or_b32 takes the mask from a scalar register and this constant
+// from a vector one (one scalar operand per instruction), so it must not be folded into a literal.
+SMEL_DEV uint32_t f16_magic() {
+  uint32_t m;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
+}
+struct FastSZ {
+  float a0, c0, a1, c1;   // s, z - 1024 s, s / 16, z - 64 s
+};
+SMEL_DEV FastSZ fast_sz(float s, float z) {
+  return FastSZ{s, fmaf(-1024.f, s, z), s * 0.0625f, fmaf(-64.f, s, z)};
+}
+// dq8 for a fast bank: nibbles t = 0..7 of b (bits 4t) are columns 0..7.
+SMEL_DEV void dq8f(uint32_t b, const FastSZ& p, uint32_t magic, uint32_t out[4]) {
+  const uint32_t b8 = b >> 8;
+  const uint32_t x0 = (b & 0x000F000Fu) | magic;    // columns 0, 4 at 1024 + q
+  const uint32_t x1 = (b & 0x00F000F0u) | magic;    // columns 1, 5 at 1024 + 16 q
+  const uint32_t x2 = (b8 & 0x000F000Fu) | magic;   // columns 2, 6
+  const uint32_t x3 = (b8 & 0x00F000F0u) | magic;   // columns 3, 7
+  out[0] = pack2bf(fmaf(h_lo(x0), p.a0, p.c0), fmaf(h_lo(x1), p.a1, p.c1));
+  out[1] = pack2bf(fmaf(h_lo(x2), p.a0, p.c0), fmaf(h_lo(x3), p.a1, p.c1));
+  out[2] = pack2bf(fmaf(h_hi(x0), p.a0, p.c0), fmaf(h_hi(x1), p.a1, p.c1));
+  out[3] = pack2bf(fmaf(h_hi(x2), p.a0, p.c0), fmaf(h_hi(x3), p.a1, p.c1));
+}
+
 // ------------------------------------------------------------------------------------------------ activations
 // act ids: 0 = silu, 1 = gelu_tanh (smel/moe.py:91-107)
 SMEL_DEV float act_f(float g, int act) {

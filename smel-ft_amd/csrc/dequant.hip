@@ -112,8 +112,11 @@ __global__ __launch_bounds__(256) void pack_bf16(const uint16_t* __restrict__ w,
 // substep s of a 64-row step, rows k = 32 s + 8 kq + [0, 8)):
 //   int4 q : block (e, p, ks) = 1 KB, column pair p = 32 columns; lane chunk = 4 words, word (2 fr + s) = the 8
 //            nibbles (row order, low nibble first) of column 32 p + 16 fr + i at rows 64 ks + 32 s + 8 kq + [0, 8)
-//   sz     : block (e, g, ks) = 256 B, group g of C; word 16 kq + 8 s + t = scale | zero << 16 of row
-//            64 ks + 32 s + 8 kq + t (a lane reads the 64 B of its kq)
+//   sz     : block (e, g, ks) = 512 B, group g of C; fp32 pair 16 kq + 8 s + t = (scale, zero') of row
+//            64 ks + 32 s + 8 kq + t (a lane reads the 64 B of its kq and substep); zero' = zero - 1024 scale for a
+//            fast bank (the constant of the fp16-magic dequant, exact by smel_int4_fast_ok), else zero. fp32 here
+//            because these values change along the contraction, so each lane needs eight pairs per substep: stored
+//            ready to use, they cost no unpacking
 //   bf16   : block (e, p, ks, 2 fr + s) = 1 KB; lane chunk = the 8 bf16 of column 32 p + 16 fr + i at those rows
 // Rows >= R and columns >= C are zero.
 
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(256) void pack_q4_t(const uint8_t* __restrict__ q, 
 }
 
 __global__ __launch_bounds__(256) void pack_sz_t(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
-                                                 int64_t R, int64_t G, int64_t nks, uint32_t* __restrict__ out,
+                                                 int64_t R, int64_t G, int64_t nks, int fast, float2* __restrict__ out,
                                                  int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t pos = i & 63, blk = i >> 6;
@@ -155,12 +158,37 @@ __global__ __launch_bounds__(256) void pack_sz_t(const uint16_t* __restrict__ s,
     const int64_t g = eg % G, e = eg / G;
     const int64_t kq = pos >> 4, sub = (pos >> 3) & 1, t = pos & 7;
     const int64_t k = 64 * ks + 32 * sub + 8 * kq + t;
-    uint32_t v = 0;
+    float2 v = make_float2(0.f, 0.f);
     if (k < R) {
       const int64_t gi = (e * R + k) * G + g;
-      v = (uint32_t)s[gi] | ((uint32_t)z[gi] << 16);
+      const float sc = bf2f(s[gi]), ze = bf2f(z[gi]);
+      v = make_float2(sc, fast ? fmaf(-1024.f, sc, ze) : ze);
     }
     out[i] = v;
+  }
+}
+
+// fp32 value d, exactly: a normal or zero fp32?
+SMEL_DEV bool f32_exact(double d) {
+  const float f = (float)d;
+  return (double)f == d && (d == 0.0 || (fabs(d) >= 1.1754943508222875e-38 && fabs(d) <= 3.4028234663852886e38));
+}
+// z - m exactly an fp32 (z, m bf16 values, m possibly scaled by a power of two): with exponents at most 40 apart the
+// difference (at most 49 significant bits) is exact in double, so the fp32 round trip decides; further apart, the
+// exact difference needs more than 24 bits unless one side is zero.
+SMEL_DEV bool diff_exact(double z, double m) {
+  if (z == 0.0 || m == 0.0) return f32_exact(z - m);
+  if (abs(ilogb(z) - ilogb(m)) > 40) return false;
+  return f32_exact(z - m);
+}
+__global__ __launch_bounds__(256) void fast_ok_init(int32_t* ok) { *ok = 1; }
+__global__ __launch_bounds__(256) void fast_ok_check(const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
+                                                     int64_t n, int32_t* ok) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const double sc = bf2f(s[i]), ze = bf2f(z[i]);
+    const bool good = f32_exact(sc) && f32_exact(sc / 16.0) && diff_exact(ze, 1024.0 * sc) &&
+                      diff_exact(ze, 64.0 * sc) && f32_exact(1024.0 * sc);
+    if (!good) *ok = 0;   // every writer stores the same value
   }
 }
 
@@ -208,24 +236,37 @@ extern "C" int64_t smel_packed_t_bytes(int32_t what, int64_t n_mats, int64_t R, 
   const int64_t np = (C + 31) / 32, nks = (R + 63) / 64;
   switch (what) {
     case SMEL_PACK_Q4: return n_mats * np * nks * 1024;
-    case SMEL_PACK_SZ: return (group > 0 && C % group == 0) ? n_mats * (C / group) * nks * 256 : -1;
+    case SMEL_PACK_SZ: return (group > 0 && C % group == 0) ? n_mats * (C / group) * nks * 512 : -1;
     case SMEL_PACK_BF16: return n_mats * np * nks * 4096;
     default: return -1;
   }
 }
 
 extern "C" int smel_pack_int4_t(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, int64_t n_mats,
-                                int64_t R, int64_t C, int64_t group, uint8_t* qt, uint32_t* szt, hipStream_t stream) {
+                                int64_t R, int64_t C, int64_t group, int32_t fast, uint8_t* qt, float* szt,
+                                hipStream_t stream) {
   SMEL_REQUIRE(n_mats >= 0 && R > 0 && C > 0 && group > 0 && C % 32 == 0 && C % group == 0 && group % 32 == 0,
                SMEL_EUNSUPPORTED, "pack_int4_t: C=%lld, group=%lld (C a multiple of 32, group a multiple of 32 "
                "dividing C)", (long long)C, (long long)group);
   if (n_mats == 0) return 0;
   SMEL_REQUIRE(q && scale && zero && qt && szt, SMEL_EINVAL, "pack_int4_t: null pointer");
-  SMEL_REQUIRE((uintptr_t)qt % 16 == 0, SMEL_EUNSUPPORTED, "pack_int4_t: qt must be 16-byte aligned");
+  SMEL_REQUIRE((uintptr_t)qt % 16 == 0 && (uintptr_t)szt % 8 == 0, SMEL_EUNSUPPORTED,
+               "pack_int4_t: qt must be 16-byte and szt 8-byte aligned");
+  SMEL_REQUIRE(fast == 0 || fast == 1, SMEL_EINVAL, "pack_int4_t: fast %d", fast);
   const int64_t np = C / 32, nks = (R + 63) / 64, G = C / group;
   const int64_t nq = n_mats * np * nks * 64, nsz = n_mats * G * nks * 64;
   pack_q4_t<<<pack_blocks(nq), 256, 0, stream>>>(q, R, C, np, nks, reinterpret_cast<u32x4_t*>(qt), nq);
-  pack_sz_t<<<pack_blocks(nsz), 256, 0, stream>>>(scale, zero, R, G, nks, szt, nsz);
+  pack_sz_t<<<pack_blocks(nsz), 256, 0, stream>>>(scale, zero, R, G, nks, fast, reinterpret_cast<float2*>(szt), nsz);
+  return smel::launch_status();
+}
+
+extern "C" int smel_int4_fast_ok(const uint16_t* scale, const uint16_t* zero, int64_t n, int32_t* ok,
+                                 hipStream_t stream) {
+  SMEL_REQUIRE(n >= 0 && ok && (n == 0 || (scale && zero)), SMEL_EINVAL, "int4_fast_ok: null pointer or n < 0");
+  fast_ok_init<<<1, 1, 0, stream>>>(ok);
+  int st = smel::launch_status();
+  if (st || n == 0) return st;
+  fast_ok_check<<<pack_blocks(n), 256, 0, stream>>>(scale, zero, n, ok);
   return smel::launch_status();
 }
 

@@ -5,9 +5,9 @@
 // the combine, smel/moe.py:204-252, smel/lora.py:61-83.
 //
 // The weights come in the transposed fragment layout of smel_pack_int4_t / smel_pack_bf16_t, so every wave streams its
-// own 64 output columns straight into registers (one 16-B load per lane, column pair and 64-row step for int4) and
-// dequantizes them there, as the forward kernel does; the int4 scale / zero vary along the contraction here, so each
-// lane needs one (scale, zero) word per row it holds: those 64-word runs go global -> LDS by LDS-DMA beside the A rows.
+// own 64 output columns (int4: through the LDS ring by LDS-DMA) and dequantizes them in registers, as the forward
+// kernel does; the int4 scale / zero vary along the contraction here, so each lane needs one (scale, zero) pair per
+// row it holds: those 64-pair runs (fp32, ready to use) go global -> LDS by LDS-DMA beside the A rows.
 //
 // Block = 4 waves, tile = up to 128 rows of one group (4 slices of 32) x 256 columns (64 per wave).
 // MFMA v_mfma_f32_16x16x32_bf16: lane l = 16 kq + i carries, in substep s of a 64-wide k-step, k = 32 s + 8 kq +
@@ -28,9 +28,12 @@ constexpr int KT = 64;
 constexpr int NB = 256;            // output columns per block
 constexpr int A_BYTES = MT * KT * 2;         // A rows of one stage
 constexpr int Q_BYTES = 4 * 2 * 1024;        // int4 q of one stage: 4 waves x 2 column pairs
-constexpr int Z_BYTES = 4 * 2 * 256;         // scale/zero of one stage: 4 waves x 2 groups x 64 rows
-constexpr int Q_STAGE = A_BYTES + Q_BYTES + Z_BYTES;
-constexpr int SMEM_BYTES = 3 * Q_STAGE > 4 * A_BYTES ? 3 * Q_STAGE : 4 * A_BYTES;
+// scale/zero of one stage: 4 waves x 64 rows x (scale, zero) fp32, per group (two groups per wave when the int4 group
+// is 32 wide: SZ2)
+constexpr int z_bytes(bool sz2) { return 4 * 512 * (sz2 ? 2 : 1); }
+constexpr int q_stage(bool sz2) { return A_BYTES + Q_BYTES + z_bytes(sz2); }
+constexpr int smem_bytes(bool sz2) { return 3 * q_stage(sz2) > 4 * A_BYTES ? 3 * q_stage(sz2) : 4 * A_BYTES; }
+static_assert(smem_bytes(false) <= 80 * 1024, "two blocks per CU");
 
 struct BwdArgs {
   smel_wset w;
@@ -68,21 +71,36 @@ SMEL_DEV void dq8r(uint32_t b, const float* sc, const float* ze, uint32_t out[4]
   out[2] = pack2bf(fmaf(ub2(lo), sc[4], ze[4]), fmaf(ub2(hi), sc[5], ze[5]));
   out[3] = pack2bf(fmaf(ub3(lo), sc[6], ze[6]), fmaf(ub3(hi), sc[7], ze[7]));
 }
+// The same for a fast bank (ze[t] = zero - 1024 scale, see dq8f): (b >> 4j) & 0x000F000F holds rows j and j + 4 as
+// fp16 1024 + q; 19 VALU ops for 8 weights instead of 23.
+SMEL_DEV void dq8rf(uint32_t b, const float* sc, const float* ze, uint32_t magic, uint32_t out[4]) {
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t x = ((b >> (4 * j)) & 0x000F000Fu) | magic;
+    r[j] = fmaf(h_lo(x), sc[j], ze[j]);
+    r[j + 4] = fmaf(h_hi(x), sc[j + 4], ze[j + 4]);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) out[t] = pack2bf(r[2 * t], r[2 * t + 1]);
+}
 
 // 4-byte-per-lane LDS-DMA: lane i writes bytes [4 i, 4 i + 4) after the wave-uniform LDS address.
 SMEL_DEV void ld4_lds(rsrc_t r, const void* lds, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(lds), 4, off, 0, 0, 0);
 }
 
-template <int EPI, bool Q4, int NS, bool SZ2>
+template <int EPI, bool Q4, int NS, bool SZ2, bool FAST>
 SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint8_t* smem) {
-  // LDS rings. int4: 3 stages of [A rows 16 KB | q of 4 waves x 2 column pairs, 8 KB | scale/zero of 4 waves x 2
-  // groups, 2 KB]. bf16: 4 stages of A rows (the weights go to registers). The epilogue reuses the first 64 KB.
+  // LDS rings. int4: 3 stages of [A rows 16 KB | q of 4 waves x 2 column pairs, 8 KB | scale/zero pairs of 4 waves x
+  // 64 rows (x 2 groups for SZ2), 2 KB (4 KB)]. bf16: 4 stages of A rows (the weights go to registers). The epilogue
+  // reuses the first 64 KB.
+  constexpr int QS = q_stage(SZ2), ZW = SZ2 ? 1024 : 512;   // stage bytes, scale/zero bytes per wave
   auto St = [&](int st) {
-    return reinterpret_cast<uint16_t*>(smem + st * (Q4 ? Q_STAGE : A_BYTES));
+    return reinterpret_cast<uint16_t*>(smem + st * (Q4 ? QS : A_BYTES));
   };
-  auto Qt = [&](int st) { return smem + st * Q_STAGE + A_BYTES; };
-  auto Zt = [&](int st) { return reinterpret_cast<uint32_t*>(smem + st * Q_STAGE + A_BYTES + Q_BYTES); };
+  auto Qt = [&](int st) { return smem + st * QS + A_BYTES; };
+  auto Zt = [&](int st) { return smem + st * QS + A_BYTES + Q_BYTES; };
   auto Et = [&](int m) { return reinterpret_cast<uint16_t*>(smem + m * A_BYTES); };
   const int tid = threadIdx.x, l = lane_id(), kq = l >> 4, li = l & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -103,13 +121,13 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     const int64_t qbytes = (int64_t)np * nk * 1024;
     rw = make_rsrc(qb, (uint64_t)qbytes);
     rw1 = make_rsrc(qb + (int64_t)nk * 1024, (uint64_t)(qbytes - (int64_t)nk * 1024));
-    const uint32_t* zb = ws.sz4 + (int64_t)idx * G * nk * 64;
-    const int64_t zbytes = (int64_t)G * nk * 256;
-    const int64_t zstep = (int64_t)((cw + 32) / ws.group - cw / ws.group) * nk * 256;   // 0 or one group
+    const uint8_t* zb = reinterpret_cast<const uint8_t*>(ws.sz4) + (int64_t)idx * G * nk * 512;
+    const int64_t zbytes = (int64_t)G * nk * 512;
+    const int64_t zstep = (int64_t)((cw + 32) / ws.group - cw / ws.group) * nk * 512;   // 0 or one group
     rsz = make_rsrc(zb, (uint64_t)zbytes);
-    rsz1 = make_rsrc(reinterpret_cast<const uint8_t*>(zb) + zstep, (uint64_t)(zbytes - zstep));
+    rsz1 = make_rsrc(zb + zstep, (uint64_t)(zbytes - zstep));
     wo = (uint32_t)(p0 * nk * 1024 + l * 16);
-    so = (uint32_t)((cw / ws.group) * nk * 256 + 4 * l);
+    so = (uint32_t)((cw / ws.group) * nk * 512 + 4 * l);
   } else {
     const uint16_t* base = kind == SMEL_KIND_BF16 ? ws.wb : (kind == SMEL_KIND_SEL ? ws.wsel : ws.wsh);
     const int64_t mi = kind == SMEL_KIND_SHARED ? 0 : idx;
@@ -137,8 +155,8 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       aoff[ii] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * c;
     }
   }
-  // All loads of step j into stage st: int4 -> q (2 x 1 KB per wave), scale/zero (256 B per group), A (4 x 1 KB);
-  // bf16 -> A only.
+  // All loads of step j into stage st: int4 -> q (2 x 1 KB per wave), scale/zero pairs (2 x 256 B per group), A
+  // (4 x 1 KB); bf16 -> A only.
   auto issue_lds = [&](int j, int st) {
     const bool in = j < nk;
     const uint32_t k2 = (uint32_t)j * KT * 2;
@@ -146,8 +164,12 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     if constexpr (Q4) {
       ld16_lds(rw, Qt(st) + w * 2048, in ? wo + j * 1024 : OOB);
       ld16_lds(rw1, Qt(st) + w * 2048 + 1024, in ? wo + j * 1024 : OOB);
-      ld4_lds(rsz, Zt(st) + w * 128, in ? so + j * 256 : OOB);
-      if constexpr (SZ2) ld4_lds(rsz1, Zt(st) + w * 128 + 64, in ? so + j * 256 : OOB);
+      ld4_lds(rsz, Zt(st) + w * ZW, in ? so + j * 512 : OOB);
+      ld4_lds(rsz, Zt(st) + w * ZW + 256, in ? so + j * 512 + 256 : OOB);
+      if constexpr (SZ2) {
+        ld4_lds(rsz1, Zt(st) + w * ZW + 512, in ? so + j * 512 : OOB);
+        ld4_lds(rsz1, Zt(st) + w * ZW + 768, in ? so + j * 512 + 256 : OOB);
+      }
     }
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) ld16_lds(ra, St(st) + (4 * w + ii) * 512, in ? aoff[ii] + k2 : OOB);
@@ -167,37 +189,40 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     for (int f = 0; f < 4; ++f) acc[m][f] = f32x4_t{};
 
   if constexpr (Q4) {
-    // One substep: the 2 NS A fragments, this lane's q words and its 8 scale/zero words come from the stage; then
+    // One substep: the 2 NS A fragments, this lane's q words and its 8 scale/zero pairs come from the stage; then
     // column fragment f+1 is dequantized (VALU) while the 2 NS MFMAs of fragment f run, so the two pipes overlap
     // inside a wave.
+    const uint32_t magic = FAST ? f16_magic() : 0u;
     auto compute = [&](int st) {
       const uint16_t* S = St(st);
-      const uint32_t* Z = Zt(st) + w * 128 + 16 * kq;
+      const float* Z = reinterpret_cast<const float*>(Zt(st) + w * ZW) + 32 * kq;
       const u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(Qt(st) + w * 2048 + l * 16);
       const u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(Qt(st) + w * 2048 + 1024 + l * 16);
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         float sc[8], ze[8];
-        auto unpack = [&](const uint32_t* zp) {
-          const u32x4_t za = *reinterpret_cast<const u32x4_t*>(zp);
-          const u32x4_t zb = *reinterpret_cast<const u32x4_t*>(zp + 4);
+        auto unpack = [&](const float* zp) {   // 8 (scale, zero) pairs, used as they are
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            sc[t] = bf_lo(za[t]);
-            ze[t] = bf_hi(za[t]);
-            sc[4 + t] = bf_lo(zb[t]);
-            ze[4 + t] = bf_hi(zb[t]);
+          for (int v = 0; v < 4; ++v) {
+            const f32x4_t z4 = *reinterpret_cast<const f32x4_t*>(zp + 4 * v);
+            sc[2 * v] = z4[0];
+            ze[2 * v] = z4[1];
+            sc[2 * v + 1] = z4[2];
+            ze[2 * v + 1] = z4[3];
           }
         };
         auto dq = [&](int f) {
           const int fr = f & 1;
-          if (SZ2 && f == 2) unpack(Z + 64 + 8 * s);
+          if (SZ2 && f == 2) unpack(Z + 128 + 16 * s);
           const uint32_t qw = (f < 2 ? q0 : q1)[2 * fr + s];
           uint32_t o[4];
-          dq8r(qw, sc, ze, o);   // rows / columns outside the matrix hold q = s = z = 0
+          if constexpr (FAST)
+            dq8rf(qw, sc, ze, magic, o);
+          else
+            dq8r(qw, sc, ze, o);   // rows / columns outside the matrix hold q = s = z = 0
           return u32x4_t{o[0], o[1], o[2], o[3]};
         };
-        unpack(Z + 8 * s);
+        unpack(Z + 16 * s);
         // first half of the row fragments: fragment f+1 dequantized while fragment f's MFMAs run; second half: the
         // four finished B fragments again (16 A registers live instead of 32)
         constexpr int H1 = (NRF + 1) / 2;
@@ -224,7 +249,7 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     };
     // 3-stage ring, every operand by LDS-DMA, two steps ahead: before step j only step j+1's loads may be in flight.
-    constexpr int NV = 2 + (SZ2 ? 2 : 1) + 4;   // vector-memory ops per step: 2 q, 1-2 scale/zero, 4 A
+    constexpr int NV = 2 + (SZ2 ? 4 : 2) + 4;   // vector-memory ops per step: 2 q, 2-4 scale/zero, 4 A
     auto step = [&](int j, int st) {
       SMEL_WAIT_VM_LDS(NV);
       __builtin_amdgcn_s_barrier();
@@ -393,19 +418,18 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   }
 }
 
-template <int EPI, bool Q4, bool SZ2>
+template <int EPI, bool Q4, bool SZ2, bool FAST>
 SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint8_t* smem) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
-    case 2: run_tile<EPI, Q4, 2, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
-    case 3: run_tile<EPI, Q4, 3, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
-    default: run_tile<EPI, Q4, 4, SZ2>(a, kind, idx, row0, nrows, nb, smem); break;
+    case 1: run_tile<EPI, Q4, 1, SZ2, FAST>(a, kind, idx, row0, nrows, nb, smem); break;
+    case 2: run_tile<EPI, Q4, 2, SZ2, FAST>(a, kind, idx, row0, nrows, nb, smem); break;
+    case 3: run_tile<EPI, Q4, 3, SZ2, FAST>(a, kind, idx, row0, nrows, nb, smem); break;
+    default: run_tile<EPI, Q4, 4, SZ2, FAST>(a, kind, idx, row0, nrows, nb, smem); break;
   }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_bwd_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM_BYTES];
+template <int EPI, bool SZ2>
+SMEL_DEV void gmm_bwd_body(const BwdArgs& a, uint8_t* smem) {
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
@@ -414,13 +438,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4) {
-    if (a.w.group % 64)   // the 64 columns of a wave span two scale/zero groups
-      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, smem);
+    if (a.w.flags & SMEL_WSET_FAST_DQ)
+      run_tile_ns<EPI, true, SZ2, true>(a, kind, idx, t.y, nrows, nb, smem);
     else
-      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, smem);
+      run_tile_ns<EPI, true, SZ2, false>(a, kind, idx, t.y, nrows, nb, smem);
   } else {
-    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, smem);
+    run_tile_ns<EPI, false, false, false>(a, kind, idx, t.y, nrows, nb, smem);
   }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_bwd_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[smem_bytes(false)];
+  gmm_bwd_body<EPI, false>(a, smem);
+}
+
+// An int4 group of 32 columns (the 64 columns of a wave span two scale/zero groups): the larger ring allows one
+// block per CU.
+template <int EPI>
+__global__ __launch_bounds__(256) void gmm_bwd_kernel_sz2(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[smem_bytes(true)];
+  gmm_bwd_body<EPI, true>(a, smem);
 }
 
 }  // namespace
@@ -475,9 +513,17 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   a.N = (int)w->C;
   a.nblk = (int)smel_gmm_bwd_nblocks(w->C);
   const unsigned grid = (unsigned)(xcd_grid(max_tiles) * a.nblk);
-  if (epilogue == 1)
-    gmm_bwd_kernel<1><<<grid, 256, 0, stream>>>(a);
-  else
-    gmm_bwd_kernel<0><<<grid, 256, 0, stream>>>(a);
+  const bool sz2 = w->q4 && w->group % 64 != 0;
+  if (sz2) {
+    if (epilogue == 1)
+      gmm_bwd_kernel_sz2<1><<<grid, 256, 0, stream>>>(a);
+    else
+      gmm_bwd_kernel_sz2<0><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (epilogue == 1)
+      gmm_bwd_kernel<1><<<grid, 256, 0, stream>>>(a);
+    else
+      gmm_bwd_kernel<0><<<grid, 256, 0, stream>>>(a);
+  }
   return smel::launch_status();
 }

@@ -12,7 +12,8 @@
 //    bank-conflict free. Every wave reads all rows of a stage.
 //  * every wave streams its own two 32-row weight fragments straight into registers from the fragment layout of
 //    smel_pack_int4 / smel_pack_bf16 (one contiguous 1-KB load per fragment and k-step) and dequantizes int4 there,
-//    so each weight element of a tile is read and dequantized once.
+//    so each weight element of a tile is read and dequantized once (dq8, or dq8f for a bank with the
+//    SMEL_WSET_FAST_DQ flag: the same values in fewer instructions).
 //  * loads run 3 k-steps ahead (int4: a 4-deep register ring; bf16: 1 step ahead, as its fragments are 4x larger).
 //    vmcnt retires in issue order, so each step issues its weight loads before its A loads and waits, before one
 //    barrier, for exactly the loads of the step it is about to use.
@@ -44,7 +45,7 @@ struct FwdArgs {
   int nblk;   // column blocks per tile
 };
 
-template <int EPI, bool Q4, int NS>
+template <int EPI, bool Q4, int NS, bool FAST>
 SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
                        uint16_t* S2, uint16_t* S3) {
   const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
@@ -150,15 +151,22 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       }
       issue_a(j, S);   // sched barriers keep the group's loads in this order, ahead of the step's compute
     };
+    const uint32_t magic = FAST ? f16_magic() : 0u;
     auto compute = [&](const uint16_t* S, const u32x4_t* q, int p) {
       const uint32_t p0 = p == 0 ? szc[0][0] : p == 1 ? szc[0][1] : p == 2 ? szc[0][2] : szc[0][3];
       const uint32_t p1 = p == 0 ? szc[1][0] : p == 1 ? szc[1][1] : p == 2 ? szc[1][2] : szc[1][3];
       const float s0 = bf_lo(p0), z0 = bf_hi(p0), s1 = bf_lo(p1), z1 = bf_hi(p1);
+      const FastSZ f0 = fast_sz(s0, z0), f1 = fast_sz(s1, z1);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         uint32_t o0[4], o1[4];
-        dq8(q[0][s], s0, z0, o0);   // rows / k outside the matrix hold q = s = z = 0 -> exact zeros
-        dq8(q[1][s], s1, z1, o1);
+        if constexpr (FAST) {
+          dq8f(q[0][s], f0, magic, o0);
+          dq8f(q[1][s], f1, magic, o1);
+        } else {
+          dq8(q[0][s], s0, z0, o0);   // rows / k outside the matrix hold q = s = z = 0 -> exact zeros
+          dq8(q[1][s], s1, z1, o1);
+        }
         mma(S, s, u32x4_t{o0[0], o0[1], o0[2], o0[3]}, u32x4_t{o1[0], o1[1], o1[2], o1[3]});
       }
     };
@@ -326,14 +334,14 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   }
 }
 
-template <int EPI, bool Q4>
+template <int EPI, bool Q4, bool FAST>
 SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0,
                           uint16_t* S1, uint16_t* S2, uint16_t* S3) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
-    case 2: run_tile<EPI, Q4, 2>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
-    case 3: run_tile<EPI, Q4, 3>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
-    default: run_tile<EPI, Q4, 4>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    case 1: run_tile<EPI, Q4, 1, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    default: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
   }
 }
 
@@ -350,10 +358,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
-  if (kind == SMEL_KIND_INT4)
-    run_tile_ns<EPI, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
-  else
-    run_tile_ns<EPI, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+  if (kind == SMEL_KIND_INT4) {
+    if (a.w.flags & SMEL_WSET_FAST_DQ)
+      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+    else
+      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+  } else {
+    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+  }
 }
 
 }  // namespace

@@ -15,7 +15,8 @@ LIB_PATH = os.path.join(HERE, "libsmel_moe.so")
 
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
-ABI_VERSION = 5
+WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
+ABI_VERSION = 6
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -23,7 +24,7 @@ vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_fl
 class WSet(ctypes.Structure):
     """smel_wset of include/smel_moe.h."""
     _fields_ = [("q4", vp), ("sz4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp), ("ext_sel", vp), ("ext_sh", vp),
-                ("R", i64), ("C", i64), ("group", i32), ("pad_", i32)]
+                ("R", i64), ("C", i64), ("group", i32), ("flags", i32)]
 
 
 class WgDest(ctypes.Structure):
@@ -47,7 +48,8 @@ SIGNATURES = {
     "smel_pack_int4": (i32, [vp, vp, vp, i64, i64, i64, vp, vp, vp]),
     "smel_pack_bf16": (i32, [vp, i64, i64, i64, vp, vp]),
     "smel_packed_t_bytes": (i64, [i32, i64, i64, i64, i64]),
-    "smel_pack_int4_t": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp]),
+    "smel_pack_int4_t": (i32, [vp, vp, vp, i64, i64, i64, i64, i32, vp, vp, vp]),
+    "smel_int4_fast_ok": (i32, [vp, vp, i64, vp, vp]),
     "smel_pack_bf16_t": (i32, [vp, i64, i64, i64, i64, vp, vp]),
     "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_ld": (i64, [i64, i32]),

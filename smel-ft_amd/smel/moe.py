@@ -167,9 +167,22 @@ class Int4Experts:
             cache[which] = (qf, szf)
         return cache[which]
 
+    def fast_dq(self, which: str) -> bool:
+        """Whether every scale/zero group of 'gu' or 'dn' admits the GEMMs' cheaper exact dequant form
+        (smel_int4_fast_ok; checked once per bank, one host sync)."""
+        cache = self.__dict__.setdefault("_fast_dq", {})
+        if which not in cache:
+            d = self.gu if which == "gu" else self.dn
+            ok = torch.zeros(1, dtype=torch.int32, device=d["q"].device)
+            L.call("smel_int4_fast_ok", L.ptr(d["scale"]), L.ptr(d["zero"]), d["scale"].numel(), L.ptr(ok),
+                   L.stream())
+            cache[which] = bool(ok.item())
+        return cache[which]
+
     def packed_t(self, which: str):
         """(q, scale/zero) of 'gu' or 'dn' in the backward GEMM's transposed layout (smel_pack_int4_t), built once
-        per bank: one more int4 copy (not a bf16 one) that the backward streams straight into registers."""
+        per bank: one more int4 copy (not a bf16 one) that the backward streams straight into registers; its
+        scale/zero are fp32 pairs (zero pre-shifted for the fast dequant form when fast_dq holds)."""
         cache = self.__dict__.setdefault("_packed_t", {})
         if which not in cache:
             d = self.gu if which == "gu" else self.dn
@@ -178,10 +191,10 @@ class Int4Experts:
             g = Int4Experts.group_of(d)
             lib = L.load()
             qt = torch.empty(lib.smel_packed_t_bytes(L.PACK_Q4, E, R, C, g), dtype=torch.uint8, device=d["q"].device)
-            szt = torch.empty(lib.smel_packed_t_bytes(L.PACK_SZ, E, R, C, g) // 4, dtype=torch.int32,
+            szt = torch.empty(lib.smel_packed_t_bytes(L.PACK_SZ, E, R, C, g) // 4, dtype=torch.float32,
                               device=d["q"].device)
-            L.call("smel_pack_int4_t", L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"]), E, R, C, g, L.ptr(qt),
-                   L.ptr(szt), L.stream())
+            L.call("smel_pack_int4_t", L.ptr(d["q"]), L.ptr(d["scale"]), L.ptr(d["zero"]), E, R, C, g,
+                   int(self.fast_dq(which)), L.ptr(qt), L.ptr(szt), L.stream())
             cache[which] = (qt, szt)
         return cache[which]
 
@@ -342,6 +355,7 @@ def _bank_wset(fz, which: str, t: bool = False) -> L.WSet:
         qf, szf = fz.packed_t(which) if t else fz.packed(which)
         w.q4, w.sz4 = L.ptr(qf), L.ptr(szf)
         w.group = Int4Experts.group_of(d)
+        w.flags = L.WSET_FAST_DQ if fz.fast_dq(which) else 0
         w.R, w.C = d["q"].shape[1], d["q"].shape[2] * 2
     else:
         pw = fz.packed_t(which) if t else fz.packed(which)

@@ -44,7 +44,7 @@ PROBE = r"""
 int main() {
   printf("smel_wset %zu\nsmel_wg_dest %zu\nsmel_wg_job %zu\n", sizeof(smel_wset), sizeof(smel_wg_dest),
          sizeof(smel_wg_job));
-  F(smel_wset, R) F(smel_wset, group) F(smel_wg_dest, s_idx) F(smel_wg_dest, p0) F(smel_wg_dest, nq)
+  F(smel_wset, R) F(smel_wset, group) F(smel_wset, flags) F(smel_wg_dest, s_idx) F(smel_wg_dest, p0) F(smel_wg_dest, nq)
   F(smel_wg_job, ldr) F(smel_wg_job, r_gather) F(smel_wg_job, Q) F(smel_wg_job, dest)
   return 0;
 }
@@ -116,10 +116,12 @@ def test_host_side_rejections():
     assert b"workspace" in L.smel_last_error()
     # transposed layouts (backward GEMM operand): sizes and rejections
     assert L.smel_packed_t_bytes(_lib.PACK_Q4, 2, 1024, 2048, 64) == 2 * 64 * 16 * 1024
-    assert L.smel_packed_t_bytes(_lib.PACK_SZ, 2, 1024, 2048, 64) == 2 * 32 * 16 * 256
+    assert L.smel_packed_t_bytes(_lib.PACK_SZ, 2, 1024, 2048, 64) == 2 * 32 * 16 * 512
     assert L.smel_packed_t_bytes(_lib.PACK_BF16, 1, 288, 2048, 0) == 64 * 5 * 4096
     assert L.smel_packed_t_bytes(_lib.PACK_SZ, 1, 64, 96, 64) == -1      # group does not divide C
-    assert L.smel_pack_int4_t(1, 1, 1, 1, 64, 96, 64, 1, 1, None) == -2  # group does not divide C
+    assert L.smel_pack_int4_t(1, 1, 1, 1, 64, 96, 64, 0, 1, 1, None) == -2  # group does not divide C
+    assert L.smel_pack_int4_t(1, 1, 1, 1, 64, 128, 64, 2, 16, 16, None) == -1   # fast is 0 or 1
+    assert L.smel_int4_fast_ok(None, None, 4, None, None) == -1
     assert L.smel_pack_bf16_t(1, 1, 64, 48, 64, 1, None) == -2           # C not a multiple of 32
 
 

@@ -132,19 +132,31 @@ def _t_index(E, R, C):
     return 64 * ks + 32 * s + 8 * kq + t, 32 * p + 16 * fr + i
 
 
-@pytest.mark.parametrize("E,R,C,group", [(3, 128, 192, 64), (2, 96, 64, 32), (1, 1024, 2048, 64)])
-def test_pack_int4_t_roundtrip(E, R, C, group):
+def _realistic_sz(gen, shape):
+    """Scale / zero as the reference's quantizer makes them (zero = group minimum, scale = range / 15) in bf16."""
+    s = (torch.rand(*shape, generator=gen) * 0.004 + 1e-4).to(torch.bfloat16)
+    z = (-7.5 * s.float() * (0.6 + 0.8 * torch.rand(*shape, generator=gen))).to(torch.bfloat16)
+    return s, z
+
+
+@pytest.mark.parametrize("E,R,C,group,fast", [(3, 128, 192, 64, 0), (2, 96, 64, 32, 0), (1, 1024, 2048, 64, 0),
+                                              (2, 128, 256, 64, 1), (2, 64, 96, 32, 1)])
+def test_pack_int4_t_roundtrip(E, R, C, group, fast):
     L = _lib()
-    _say(f"pack int4 transposed E{E} R{R} C{C} g{group}")
+    _say(f"pack int4 transposed E{E} R{R} C{C} g{group} fast{fast}")
     gen = torch.Generator().manual_seed(E * R + C + 1)
     q = torch.randint(0, 256, (E, R, C // 2), generator=gen, dtype=torch.uint8)
-    sc = torch.randint(0, 65536, (E, R, C // group), generator=gen, dtype=torch.int32).to(torch.int16)
-    ze = torch.randint(0, 65536, (E, R, C // group), generator=gen, dtype=torch.int32).to(torch.int16)
+    if fast:
+        sc, ze = (t.view(torch.int16) for t in _realistic_sz(gen, (E, R, C // group)))
+    else:   # any bit patterns: the pairs are bf16 -> fp32 copies
+        sc = torch.randint(0, 65536, (E, R, C // group), generator=gen, dtype=torch.int32).to(torch.int16)
+        ze = torch.randint(0, 65536, (E, R, C // group), generator=gen, dtype=torch.int32).to(torch.int16)
     lib = L.load()
     qt = torch.empty(lib.smel_packed_t_bytes(L.PACK_Q4, E, R, C, group), dtype=torch.uint8, device=DEV)
     szt = torch.empty(lib.smel_packed_t_bytes(L.PACK_SZ, E, R, C, group) // 4, dtype=torch.int32, device=DEV)
     qd, sd, zd = q.to(DEV), sc.to(DEV), ze.to(DEV)
-    L.call("smel_pack_int4_t", L.ptr(qd), L.ptr(sd), L.ptr(zd), E, R, C, group, L.ptr(qt), L.ptr(szt), L.stream())
+    L.call("smel_pack_int4_t", L.ptr(qd), L.ptr(sd), L.ptr(zd), E, R, C, group, fast, L.ptr(qt), L.ptr(szt),
+           L.stream())
     nks = -(-R // 64)
     # dense nibbles of the source: low nibble = even column
     qn = q.numpy()
@@ -157,15 +169,81 @@ def test_pack_int4_t_roundtrip(E, R, C, group):
         got = nib[e]
         assert np.array_equal(got[ok], dense[e][row[ok], col[ok]])
         assert not got[~ok].any()
-    s16 = sc.numpy().view(np.uint16).astype(np.uint32)
-    z16 = ze.numpy().view(np.uint16).astype(np.uint32)
-    sw = szt.cpu().numpy().view(np.uint32).reshape(E, C // group, nks, 4, 2, 8)       # [e][g][ks][kq][s][t]
+    s32 = sc.numpy().view(np.uint16).astype(np.uint32) << 16
+    z32 = ze.numpy().view(np.uint16).astype(np.uint32) << 16
+    if fast:   # zero' = fp32(zero - 1024 scale), exact in double for these magnitudes, rounded once
+        zf = z32.view(np.float32).astype(np.float64) - 1024.0 * s32.view(np.float32).astype(np.float64)
+        z32 = zf.astype(np.float32).view(np.uint32)
+    pw = szt.cpu().numpy().view(np.uint32).reshape(E, C // group, nks, 4, 2, 8, 2)    # [e][g][ks][kq][s][t][pair]
     ks, kq, ss, t = np.meshgrid(np.arange(nks), np.arange(4), np.arange(2), np.arange(8), indexing="ij")
     r = 64 * ks + 32 * ss + 8 * kq + t
+    rc = np.minimum(r, R - 1)
     for e in range(E):
         for g in range(C // group):
-            want = np.where(r < R, s16[e][np.minimum(r, R - 1), g] | (z16[e][np.minimum(r, R - 1), g] << 16), 0)
-            assert np.array_equal(sw[e, g], want.astype(np.uint32))
+            assert np.array_equal(pw[e, g, ..., 0], np.where(r < R, s32[e][rc, g], 0).astype(np.uint32))
+            assert np.array_equal(pw[e, g, ..., 1], np.where(r < R, z32[e][rc, g], 0).astype(np.uint32))
+
+
+def test_int4_fast_ok():
+    """The exactness check of the fast dequant form: reference-style groups pass; a zero far below the scale, a
+    zero far above it and a scale whose 1024 multiple overflows each fail it."""
+    L = _lib()
+    gen = torch.Generator().manual_seed(11)
+    s, z = _realistic_sz(gen, (64, 32))
+    ok = torch.zeros(1, dtype=torch.int32, device=DEV)
+
+    def check(s_, z_):
+        sd, zd = s_.to(DEV), z_.to(DEV)   # kept alive until the kernel has read them
+        L.call("smel_int4_fast_ok", L.ptr(sd), L.ptr(zd), s_.numel(), L.ptr(ok), L.stream())
+        return int(ok.item())
+
+    assert check(s, z) == 1
+    assert check(s, torch.zeros_like(z)) == 1                         # zero = 0: z - 1024 s is -1024 s, exact
+    for s_val, z_val in ((1e-3, 2.0 ** -60), (1e-8, 2.0 ** 20), (2.0 ** 120, 1.0)):
+        s2, z2 = s.clone(), z.clone()
+        s2[5, 7], z2[5, 7] = s_val, z_val
+        assert check(s2, z2) == 0, (s_val, z_val)
+
+
+@pytest.mark.parametrize("group,fast", [(64, True), (64, False), (32, True), (32, False)])
+def test_gemm_dequant_bitexact(group, fast):
+    """The grouped GEMMs' in-loop dequant reproduces the reference's bf16 weights bit for bit: with identity blocks
+    as A, the forward GEMM returns W^T and the backward GEMM W of every expert exactly (one nonzero product per
+    output, rounded to bf16 from an exact bf16 value). Both the fast dequant form and the plain one, for 64- and
+    32-wide groups."""
+    from smel.moe import Int4Experts, _bank_gkind, _bank_wset, _count_tiles
+    L = _lib()
+    _say(f"gemm dequant bit-exact g{group} fast{fast}")
+    E, R, C = 3, 128, 256
+    gen = torch.Generator().manual_seed(group + fast)
+    q = torch.randint(0, 256, (E, R, C // 2), generator=gen, dtype=torch.uint8)
+    s, z = _realistic_sz(gen, (E, R, C // group))
+    if not fast:
+        z[1, 3, 0] = 2.0 ** -60   # one group outside the fast form's exactness condition
+    d = {"q": q.to(DEV), "scale": s.to(DEV), "zero": z.to(DEV)}
+    bank = Int4Experts(d, d)
+    assert bank.fast_dq("gu") == fast
+    want = intref.dequant_bits(q.numpy(), _u16(s), _u16(z)).reshape(E, R, C)
+    gk = _bank_gkind(bank, DEV)
+    # forward: rows e*C + k carry e_k -> out[e*C + k][n] = W_e[n][k]
+    w = _bank_wset(bank, "gu")
+    A = torch.eye(C, dtype=torch.bfloat16).repeat(E, 1).to(DEV)
+    order = torch.arange(E * C, dtype=torch.int32, device=DEV)
+    tiles, nt, maxt = _count_tiles([C] * E, DEV)
+    out = torch.empty(E * C, R, dtype=torch.bfloat16, device=DEV)
+    L.call("smel_gmm_fwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(nt), maxt, L.ptr(A), C, E * C, 0,
+           L.ptr(order), E * C, 1, None, 0, 0, L.ptr(out), R, None, L.stream())
+    got = _u16(out).reshape(E, C, R)
+    assert np.array_equal(got, want.transpose(0, 2, 1))
+    # backward (transposed layout): rows e*R + r carry e_r -> out[e*R + r][n] = W_e[r][n]
+    wt = _bank_wset(bank, "gu", t=True)
+    At = torch.eye(R, dtype=torch.bfloat16).repeat(E, 1).to(DEV)
+    order_t = torch.arange(E * R, dtype=torch.int32, device=DEV)
+    tiles, nt, maxt = _count_tiles([R] * E, DEV)
+    out_t = torch.empty(E * R, C, dtype=torch.bfloat16, device=DEV)
+    L.call("smel_gmm_bwd", ctypes.byref(wt), L.ptr(gk), L.ptr(tiles), L.ptr(nt), maxt, L.ptr(At), R, E * R, 0,
+           L.ptr(order_t), E * R, 1, None, 0, 0, None, None, None, L.ptr(out_t), C, None, L.stream())
+    assert np.array_equal(_u16(out_t).reshape(E, R, C), want)
 
 
 @pytest.mark.parametrize("E,R,C", [(2, 96, 64), (1, 288, 2048), (12, 512, 2048)])
