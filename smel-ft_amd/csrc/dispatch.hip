@@ -14,6 +14,7 @@ namespace {
 constexpr int NW = 16;        // waves per block
 constexpr int DB = NW * 64;   // slots per block
 constexpr int MAXE = 512;
+constexpr int HCH = 12288;    // histogram entries per LDS chunk of dispatch_scan (48 KB)
 
 SMEL_DEV int block_exclusive_scan(int v, int* wsum /* [NW] LDS */, int& total) {
   const int l = lane_id(), w = threadIdx.x >> 6;
@@ -71,23 +72,42 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   __shared__ int wsum[NW];
   __shared__ int off_s[MAXE + 1];
   __shared__ int bad_s;
+  __shared__ int hs[HCH];
   const int tid = threadIdx.x;
   if (tid == 0) bad_s = 0;
+  // the histograms go through LDS in chunks of whole blocks, loaded by all threads at once (one memory latency per
+  // chunk instead of one per block and expert column)
+  const int ch = HCH / E;   // blocks per chunk
   int total = 0;
-  if (tid < E)
-    for (int b = 0; b < nb; ++b) total += hist[b * E + tid];
+  for (int b0 = 0; b0 < nb; b0 += ch) {
+    const int n = min(ch, nb - b0) * E;
+    __syncthreads();
+    for (int i = tid; i < n; i += DB) hs[i] = hist[b0 * E + i];
+    __syncthreads();
+    if (tid < E)
+      for (int b = 0; b < n / E; ++b) total += hs[b * E + tid];
+  }
   int total_rows;
   const int ex = block_exclusive_scan(tid < E ? total : 0, wsum, total_rows);
   if (tid < E) {
     off_s[tid] = ex;
     counts[tid] = total;
     offsets[tid] = ex;
-    int run = ex;
-    for (int b = 0; b < nb; ++b) {
-      const int c = hist[b * E + tid];
-      hist[b * E + tid] = run;
-      run += c;
-    }
+  }
+  int run = ex;
+  for (int b0 = 0; b0 < nb; b0 += ch) {
+    const int n = min(ch, nb - b0) * E;
+    __syncthreads();
+    for (int i = tid; i < n; i += DB) hs[i] = hist[b0 * E + i];
+    __syncthreads();
+    if (tid < E)
+      for (int b = 0; b < n / E; ++b) {
+        const int c = hs[b * E + tid];
+        hs[b * E + tid] = run;
+        run += c;
+      }
+    __syncthreads();
+    for (int i = tid; i < n; i += DB) hist[b0 * E + i] = hs[i];
   }
   if (tid == 0) {
     off_s[E] = total_rows;

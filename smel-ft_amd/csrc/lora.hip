@@ -14,76 +14,75 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
                                                         uint16_t* __restrict__ a_dn, uint16_t* __restrict__ bt_dn,
                                                         uint16_t* __restrict__ bt_gu, uint16_t* __restrict__ at_gu,
                                                         uint16_t* __restrict__ at_dn) {
+  // 32-bit index arithmetic (every layout has fewer than 2^31 elements: checked by the host) and two adjacent
+  // outputs per thread (every innermost dimension is even), stored as one 32-bit word
   const int which = blockIdx.y;
-  int64_t total;
+  const uint32_t I2 = 2u * In, H = Hd, Iu = In, R = r;
+  uint32_t total;
+  uint16_t* out;
   switch (which) {
-    case 0: total = (int64_t)n * 2 * In * 32; break;
-    case 1: total = (int64_t)n * Hd * 32; break;
-    case 2: total = (int64_t)n * 32 * Hd; break;
-    case 3: total = (int64_t)n * 32 * In; break;
-    case 4: total = (int64_t)n * 32 * Hd; break;
-    case 5: total = (int64_t)n * 32 * 2 * In; break;
-    case 6: total = (int64_t)n * Hd * 32; break;
-    default: total = (int64_t)n * In * 32; break;
+    case 0: total = n * I2 * 32u; out = fwd_gu; break;
+    case 1: total = n * H * 32u; out = fwd_dn; break;
+    case 2: total = n * 32u * H; out = a_gu; break;
+    case 3: total = n * 32u * Iu; out = a_dn; break;
+    case 4: total = n * 32u * H; out = bt_dn; break;
+    case 5: total = n * 32u * I2; out = bt_gu; break;
+    case 6: total = n * H * 32u; out = at_gu; break;
+    default: total = n * Iu * 32u; out = at_dn; break;
   }
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+  auto val = [&](uint32_t i) -> float {
     float v = 0.f;
-    if (which == 0) {            // fwd_gu [n][2In][32]
-      const int c = i % 32;
-      const int64_t rowg = i / 32;
-      const int row = rowg % (2 * In);
-      const int g = rowg / (2 * In);
-      if (row < In && c < r) v = Bg[((int64_t)g * In + row) * r + c];
-      if (row >= In && c >= 16 && c < 16 + r) v = Bu[((int64_t)g * In + row - In) * r + c - 16];
-      fwd_gu[i] = f2bf(v);
-    } else if (which == 1) {     // fwd_dn [n][Hd][32]
-      const int c = i % 32;
-      const int64_t rowg = i / 32;
-      if (c < r) v = Bd[rowg * r + c];
-      fwd_dn[i] = f2bf(v);
-    } else if (which == 2) {     // a_gu [n][32][Hd]
-      const int h = i % Hd;
-      const int j = (i / Hd) % 32;
-      const int g = i / ((int64_t)Hd * 32);
-      if (j < r) v = Ag[((int64_t)g * r + j) * Hd + h];
-      if (j >= 16 && j < 16 + r) v = Au[((int64_t)g * r + j - 16) * Hd + h];
-      a_gu[i] = f2bf(v);
-    } else if (which == 3) {     // a_dn [n][32][In]
-      const int c = i % In;
-      const int j = (i / In) % 32;
-      const int g = i / ((int64_t)In * 32);
-      if (j < r) v = Ad[((int64_t)g * r + j) * In + c];
-      a_dn[i] = f2bf(v);
-    } else if (which == 4) {     // bt_dn [n][32][Hd] = B_down^T
-      const int h = i % Hd;
-      const int j = (i / Hd) % 32;
-      const int g = i / ((int64_t)Hd * 32);
-      if (j < r) v = Bd[((int64_t)g * Hd + h) * r + j];
-      bt_dn[i] = f2bf(v);
-    } else if (which == 5) {     // bt_gu [n][32][2In]
-      const int c = i % (2 * In);
-      const int j = (i / (2 * In)) % 32;
-      const int g = i / ((int64_t)2 * In * 32);
-      if (j < r && c < In) v = Bg[((int64_t)g * In + c) * r + j];
-      if (j >= 16 && j < 16 + r && c >= In) v = Bu[((int64_t)g * In + c - In) * r + j - 16];
-      bt_gu[i] = f2bf(v);
-    } else if (which == 6) {     // at_gu [n][Hd][32]: a_gu transposed (the backward GEMM's K-extension)
-      const int j = i % 32;
-      const int64_t hg = i / 32;
-      const int h = hg % Hd;
-      const int g = hg / Hd;
-      if (j < r) v = Ag[((int64_t)g * r + j) * Hd + h];
-      if (j >= 16 && j < 16 + r) v = Au[((int64_t)g * r + j - 16) * Hd + h];
-      at_gu[i] = f2bf(v);
-    } else {                     // at_dn [n][In][32]: a_dn transposed
-      const int j = i % 32;
-      const int64_t cg = i / 32;
-      const int c = cg % In;
-      const int g = cg / In;
-      if (j < r) v = Ad[((int64_t)g * r + j) * In + c];
-      at_dn[i] = f2bf(v);
+    switch (which) {
+      case 0: {   // fwd_gu [n][2In][32]
+        const uint32_t c = i & 31u, rowg = i >> 5, row = rowg % I2, g = rowg / I2;
+        if (row < Iu && c < R) v = Bg[(g * Iu + row) * R + c];
+        if (row >= Iu && c >= 16u && c < 16u + R) v = Bu[(g * Iu + row - Iu) * R + c - 16u];
+        break;
+      }
+      case 1: {   // fwd_dn [n][Hd][32]
+        const uint32_t c = i & 31u;
+        if (c < R) v = Bd[(i >> 5) * R + c];
+        break;
+      }
+      case 2: {   // a_gu [n][32][Hd]
+        const uint32_t h = i % H, jg = i / H, j = jg & 31u, g = jg >> 5;
+        if (j < R) v = Ag[(g * R + j) * H + h];
+        if (j >= 16u && j < 16u + R) v = Au[(g * R + j - 16u) * H + h];
+        break;
+      }
+      case 3: {   // a_dn [n][32][In]
+        const uint32_t c = i % Iu, jg = i / Iu, j = jg & 31u, g = jg >> 5;
+        if (j < R) v = Ad[(g * R + j) * Iu + c];
+        break;
+      }
+      case 4: {   // bt_dn [n][32][Hd] = B_down^T
+        const uint32_t h = i % H, jg = i / H, j = jg & 31u, g = jg >> 5;
+        if (j < R) v = Bd[(g * H + h) * R + j];
+        break;
+      }
+      case 5: {   // bt_gu [n][32][2In]
+        const uint32_t c = i % I2, jg = i / I2, j = jg & 31u, g = jg >> 5;
+        if (j < R && c < Iu) v = Bg[(g * Iu + c) * R + j];
+        if (j >= 16u && j < 16u + R && c >= Iu) v = Bu[(g * Iu + c - Iu) * R + j - 16u];
+        break;
+      }
+      case 6: {   // at_gu [n][Hd][32]: a_gu transposed (the backward GEMM's K-extension)
+        const uint32_t j = i & 31u, hg = i >> 5, h = hg % H, g = hg / H;
+        if (j < R) v = Ag[(g * R + j) * H + h];
+        if (j >= 16u && j < 16u + R) v = Au[(g * R + j - 16u) * H + h];
+        break;
+      }
+      default: {  // at_dn [n][In][32]: a_dn transposed
+        const uint32_t j = i & 31u, cg = i >> 5, c = cg % Iu, g = cg / Iu;
+        if (j < R) v = Ad[(g * R + j) * Iu + c];
+        break;
+      }
     }
-  }
+    return v;
+  };
+  uint32_t* o32 = reinterpret_cast<uint32_t*>(out);
+  for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < total / 2u; p += gridDim.x * blockDim.x)
+    o32[p] = pack2bf(val(2u * p), val(2u * p + 1u));
 }
 
 // ext[row][0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles. Block = one 32-row
@@ -400,6 +399,10 @@ extern "C" int smel_lora_prep(const float* A_gate, const float* B_gate, const fl
   if (n == 0) return 0;
   SMEL_REQUIRE(A_gate && B_gate && A_up && B_up && A_down && B_down && fwd_gu && fwd_dn && a_gu && a_dn && bt_dn &&
                    bt_gu && at_gu && at_dn, SMEL_EINVAL, "lora_prep: null pointer");
+  SMEL_REQUIRE(n * 32 * std::max(Hd, 2 * In) < (1ll << 31), SMEL_EUNSUPPORTED, "lora_prep: layouts too large");
+  SMEL_REQUIRE(((uintptr_t)fwd_gu | (uintptr_t)fwd_dn | (uintptr_t)a_gu | (uintptr_t)a_dn | (uintptr_t)bt_dn |
+                (uintptr_t)bt_gu | (uintptr_t)at_gu | (uintptr_t)at_dn) % 4 == 0, SMEL_EUNSUPPORTED,
+               "lora_prep: outputs must be 4-byte aligned");
   dim3 grid(256, 8);
   lora_prep_kernel<<<grid, 256, 0, stream>>>(A_gate, B_gate, A_up, B_up, A_down, B_down, (int)n, (int)r, (int)Hd,
                                              (int)In, fwd_gu, fwd_dn, a_gu, a_dn, bt_dn, bt_gu, at_gu, at_dn);

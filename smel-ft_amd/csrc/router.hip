@@ -40,32 +40,32 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
     const int e = l + 64 * j;
     if (e < E) probs[t * E + e] = ex[j] * inv_s;
   }
-  // top-k: K rounds of a (value desc, index asc) arg-max across the wave
-  unsigned taken = 0;
+  // top-k: K rounds of a wave-wide max over 32-bit keys (bf16 logit in an order-preserving form above 0xffff - e):
+  // one compare per step for (value desc, index asc); a taken expert's key becomes 0
+  uint32_t key[MAXE / 64];
+#pragma unroll
+  for (int j = 0; j < MAXE / 64; ++j) {
+    const int e = l + 64 * j;
+    uint32_t b = __float_as_uint(v[j]) >> 16;   // the logit's bf16 bits
+    if (b == 0x8000u) b = 0u;                   // -0 ties with +0
+    const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+    key[j] = e < E ? (ord << 16) | (0xffffu - (uint32_t)e) : 0u;
+  }
   float pk[16];
   int ik[16];
   float psum = 0.f;
   for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    uint32_t best = key[0];
 #pragma unroll
-    for (int j = 0; j < MAXE / 64; ++j) {
-      const int e = l + 64 * j;
-      if (e < E && !(taken >> j & 1u) && (v[j] > bv || (v[j] == bv && e < bi))) {
-        bv = v[j];
-        bi = e;
-      }
-    }
+    for (int j = 1; j < MAXE / 64; ++j) best = max(best, key[j]);
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == l) taken |= 1u << (bi >> 6);
+    for (int o = 32; o >= 1; o >>= 1) best = max(best, (uint32_t)__shfl_xor((int)best, o, 64));
+    const int bi = (int)(0xffffu - (best & 0xffffu));
+#pragma unroll
+    for (int j = 0; j < MAXE / 64; ++j)
+      if (bi == l + 64 * j) key[j] = 0u;
+    const uint32_t ob = best >> 16;
+    const float bv = __uint_as_float(((ob & 0x8000u) ? (ob & 0x7fffu) : (~ob & 0xffffu)) << 16);
     ik[k] = bi;
     pk[k] = expf(bv - m) * inv_s;   // the same expression as probs[t][bi]
     psum += pk[k];
@@ -95,6 +95,7 @@ constexpr int RT = 32;
 constexpr int RC = 64;
 constexpr int RW = 4;
 
+template <int NSTEP>
 __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ gw,
                                                            const uint16_t* __restrict__ sg, int T, int H, int E,
@@ -131,7 +132,9 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
   const uint32_t aoff = t0 + r32 < T ? (uint32_t)(t0 + r32) * H * 2 : OOB;
   const int nk = H / 64;
   f32x16_t acc[2] = {f32x16_t{}, f32x16_t{}};
-  u32x4_t a0[4], b0[2][4], a1[4], b1[2][4];
+  // the wave's k-steps j = w, w + 4, ...: four in flight in a ring of register sets (loads of step i + 4 are issued
+  // right after step i's MFMAs), so a block waits for about two memory latencies instead of one per step
+  u32x4_t A[4][4], B[4][2][4];
   auto load = [&](int j, u32x4_t* a, u32x4_t (*b)[4]) {
     const bool ok = j < nk;
     const uint32_t k2 = (uint32_t)(j * 64 + 32 * hi) * 2;
@@ -144,18 +147,32 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
   };
   auto mma = [&](const u32x4_t* a, u32x4_t (*b)[4]) {
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      if (!fv[f]) continue;   // uniform
+    for (int f = 0; f < 2; ++f)   // an unused fragment loads zeros (no branch: a branch here costs the ring)
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc[f] = mfma32(a[s], b[f][s], acc[f]);
-    }
   };
-  load(w, a0, b0);
-  for (int j = w; j < nk; j += 2 * RW) {
-    load(j + RW, a1, b1);
-    mma(a0, b0);
-    load(j + 2 * RW, a0, b0);
-    mma(a1, b1);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) load(w + RW * u, A[u], B[u]);
+  __builtin_amdgcn_sched_barrier(0);
+  // straight-line code (NSTEP >= the wave's steps; steps past nk load zeros and add nothing), so the compiler's
+  // wait counts follow the ring exactly; a loop makes it drain all loads at every back edge
+  if constexpr (NSTEP > 0) {
+#pragma unroll
+    for (int i = 0; i < NSTEP; ++i) {
+      __builtin_amdgcn_sched_barrier(0);   // keep the four sets in flight (no sinking of loads toward their use)
+      mma(A[i & 3], B[i & 3]);
+      if (i + 4 < NSTEP) load(w + RW * (i + 4), A[i & 3], B[i & 3]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  } else {   // any hidden size
+    const int nsteps = (nk + RW - 1) / RW;
+    for (int i = 0; i < nsteps; i += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        mma(A[u], B[u]);
+        load(w + RW * (i + u + 4), A[u], B[u]);
+      }
+    }
   }
   float* mine = red + w * RT * (RC + 4);
 #pragma unroll
@@ -351,6 +368,22 @@ __global__ __launch_bounds__(256) void dtopv_kernel(const float* __restrict__ dw
   out[p] = v;
 }
 
+// route_logits_kernel with the smallest unrolled step count that covers H (64-wide k-steps, RW waves)
+void launch_logits(dim3 grid, hipStream_t stream, const uint16_t* x, const uint16_t* gw, const uint16_t* sg, int T,
+                   int H, int E, int ldl, uint16_t* logits) {
+  const int steps = (H / 64 + RW - 1) / RW;
+  if (steps <= 4)
+    route_logits_kernel<4><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+  else if (steps <= 8)
+    route_logits_kernel<8><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+  else if (steps <= 12)
+    route_logits_kernel<12><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+  else if (steps <= 16)
+    route_logits_kernel<16><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+  else
+    route_logits_kernel<0><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+}
+
 }  // namespace
 
 extern "C" int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, float* dtopv,
@@ -379,7 +412,7 @@ extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint1
   SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32 && logits, SMEL_EINVAL, "route: null pointer");
   const int64_t ldl = smel_route_ld(E, shared_gate_w != nullptr);
   const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
-  route_logits_kernel<<<grid, 256, 0, stream>>>(x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
+  launch_logits(grid, stream, x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
   route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K,
                                                             (int)((E + 31) / 32 * 32), probs, topv, topi, topi32,
                                                             shared_gate_w ? sgate : nullptr, nullptr, nullptr);
@@ -433,7 +466,7 @@ extern "C" int smel_route_gemma4(const uint16_t* h, const uint16_t* router_scale
   // H^-1/2 as the reference's Python float (a double) rounded to fp32 for the bf16 product
   route_prenorm<<<tg, 256, 0, stream>>>(h, router_scale, (int)T, (int)H, eps, (float)pow((double)H, -0.5), xn, rstd);
   const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
-  route_logits_kernel<<<grid, 256, 0, stream>>>(xn, proj_w, nullptr, (int)T, (int)H, (int)E, (int)ldl, logits);
+  launch_logits(grid, stream, xn, proj_w, nullptr, (int)T, (int)H, (int)E, (int)ldl, logits);
   route_select<<<tg, 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K, 0, probs, nullptr, topi, topi32,
                                        nullptr, topv, per_expert_scale);
   return smel::launch_status();

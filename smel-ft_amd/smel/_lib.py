@@ -11,7 +11,8 @@ import os
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsmel_moe.so")
+# SMEL_MOE_LIB names another build of the same library (e.g. one compiled with different flags)
+LIB_PATH = os.environ.get("SMEL_MOE_LIB") or os.path.join(HERE, "libsmel_moe.so")
 
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2

@@ -328,6 +328,40 @@ def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> Packe
     return _cached("router_t", build, *((gate_w,) if sg_w is None else (gate_w, sg_w)))
 
 
+_SIDE_STREAMS = {}
+
+
+def _side_stream(dev, i: int) -> torch.cuda.Stream:
+    """Side stream i of a device (default priority), for launches that do not depend on the main stream's latest
+    work: they overlap it, and the main stream waits for them before using their results (an event join, which a
+    HIP graph capture records as a fork / join of the step graph)."""
+    key = (str(dev), i)
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
+    return _SIDE_STREAMS[key]
+
+
+class _Fork:
+    """``with _Fork(dev, i) as s:`` launches on side stream i after the current stream's work so far; ``join()``
+    makes the current (main) stream wait for everything launched there."""
+
+    def __init__(self, dev, i: int):
+        self.main = torch.cuda.current_stream(dev)
+        self.side = _side_stream(dev, i)
+        self.side.wait_stream(self.main)
+        self._ctx = torch.cuda.stream(self.side)
+
+    def __enter__(self):
+        self._ctx.__enter__()
+        return self.side
+
+    def __exit__(self, *exc):
+        return self._ctx.__exit__(*exc)
+
+    def join(self):
+        self.main.wait_stream(self.side)
+
+
 class _LoRABufs:
     """bf16 K-extension layouts of one LoRA set (smel_lora_prep), built per call from the fp32 parameters."""
 
@@ -430,10 +464,11 @@ class _RouteFn(torch.autograd.Function):
         return dx, None, None
 
 
-def _router_dx(dl: torch.Tensor, wr: PackedW, T: int) -> torch.Tensor:
+def _router_dx(dl: torch.Tensor, wr: PackedW, T: int, dx: torch.Tensor | None = None) -> torch.Tensor:
     H = wr.C
     tiles, ntiles, maxt, gk = _dense_tiles(T, dl.device)
-    dx = torch.empty(T, H, dtype=torch.bfloat16, device=dl.device)
+    if dx is None:
+        dx = torch.empty(T, H, dtype=torch.bfloat16, device=dl.device)
     w = L.WSet()
     w.wsh = L.ptr(wr.t)
     w.R, w.C, w.group = wr.R, H, 32
@@ -519,10 +554,24 @@ def _lora_groups(ex: LayerExperts, with_shared: bool, n_sel_lora: int, device):
     return cache[key]
 
 
+def _expert_I(ex: LayerExperts) -> int:
+    return (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
+
+
+def _prep_lora(ex: LayerExperts, lora_ex, lora_sh, with_shared: bool, H: int, dev):
+    """The bf16 LoRA layouts of the selected experts and the shared MLP (lora_prep launches on the current stream)."""
+    I = _expert_I(ex)
+    has_sel = ex.sel_ids is not None and len(ex._slot)
+    lb_ex = _LoRABufs(lora_ex, len(ex._slot), H, I, dev) if (lora_ex is not None and has_sel) else None
+    lb_sh = _LoRABufs(lora_sh, 1, H, I, dev) if (lora_sh is not None and with_shared) else None
+    return lb_ex, lb_sh
+
+
 def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
-                      need_grad: bool, c: _Ctx):
+                      need_grad: bool, c: _Ctx, prep=None):
     """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up, down, sgate fp32 [T], gate_up^T, down^T) or None
-    (packed forward and transposed layouts of the shared expert's [2I,H] / [H,I] weights)."""
+    (packed forward and transposed layouts of the shared expert's [2I,H] / [H,I] weights). ``prep`` = (_Fork,
+    (lb_ex, lb_sh)) when the LoRA layouts were launched on a side stream (joined before their first use)."""
     T, H = x.shape
     E = ex.E
     dev = x.device
@@ -535,18 +584,23 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
     dws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
+    if prep is None:   # LoRA layouts on a side stream, overlapping the dispatch
+        fork = _Fork(dev, 0)
+        with fork:
+            bufs = _prep_lora(ex, lora_ex, lora_sh, shared is not None, H, dev)
+        prep = (fork, bufs)
     L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(counts), L.ptr(offsets),
            L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st)
     gk = ex.gkind(shared is not None, dev)
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):
         sel_gu, sel_dn = ex.packed_sel()
-    I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
+    I = _expert_I(ex)
     sh_gu = sh_dn = sgate = sh_gu_t = sh_dn_t = None
     if shared is not None:
         sh_gu, sh_dn, sgate, sh_gu_t, sh_dn_t = shared
-    lb_ex = _LoRABufs(lora_ex, len(ex._slot), H, I, dev) if (lora_ex is not None and sel_gu is not None) else None
-    lb_sh = _LoRABufs(lora_sh, 1, H, I, dev) if (lora_sh is not None and shared is not None) else None
+    fork, (lb_ex, lb_sh) = prep
+    fork.join()
     any_lora = lb_ex is not None or lb_sh is not None
     s_ex = lb_ex.scale if lb_ex else 0.0
     s_sh = lb_sh.scale if lb_sh else 0.0
@@ -615,35 +669,34 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["topv"]),
            L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st, tag="gemm_dn_bwd")
+    # (5, side stream 0) router backward (fused layer) or d topv (routed_experts): needs only dwp, so it overlaps
+    # steps (3) and (4)
+    dxr = None
+    dtopv = None
+    side_r = _Fork(dev, 0)
+    if router is not None:
+        probs, topi32, wr = router
+        Epad = wr.R
+        dl = bf(T, Epad)
+        dxr = bf(T, H)
+        with side_r:
+            L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32),
+                   L.ptr(t["topv"]), L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, None, L.stream())
+            _router_dx(dl, wr, T, dxr)
+    else:
+        dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
+        with side_r:
+            L.call("smel_dtopv", L.ptr(dwp), nblk, L.ptr(t["inv"]), TK, L.ptr(dtopv), L.stream())
     # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
     ext_dxa = None
     if any_lora:
         ext_dxa = bf(M, EXT)
         L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * I, M, 0, L.ptr(order), TK,
                K, L.ptr(g(lb_ex, "bt_gu")), L.ptr(g(lb_sh, "bt_gu")), 2 * I, s_ex, s_sh, L.ptr(ext_dxa), st)
-    # (4) gate_up backward: per-slot dx rows
-    dxs = bf(M, H)
-    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True)
-    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
-           L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, L.ptr(dxs), H, None, st,
-           tag="gemm_gu_bwd")
-    # (5) router backward (fused layer) or d topv (routed_experts)
-    dxr = None
-    dtopv = None
-    if router is not None:
-        probs, topi32, wr = router
-        Epad = wr.R
-        dl = bf(T, Epad)
-        L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32), L.ptr(t["topv"]),
-               L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, None, st)
-        dxr = _router_dx(dl, wr, T)
-    else:
-        dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
-        L.call("smel_dtopv", L.ptr(dwp), nblk, L.ptr(t["inv"]), TK, L.ptr(dtopv), st)
-    dx = bf(T, H)
-    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), int(t["sgate"] is not None), T, K, H, L.ptr(dx), st)
-    # (6) LoRA factor gradients: one launch for the four products, written into parameter-shaped fp32 tensors
+    # (6, side stream 1) LoRA factor gradients: one launch for the four products, written into parameter-shaped fp32
+    # tensors; every operand is ready here, so it overlaps the gate_up backward
     grads = {}
+    side_w = None
     if any_lora:
         n_sel = len(ex._slot) if lb_ex is not None else 0
         groups = _lora_groups(ex, lb_sh is not None, n_sel, dev)
@@ -654,13 +707,26 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
         # rows of all LoRA groups: a token routes at most min(K, n_sel) slots to selected experts, + the shared rows
         max_rows = (min(K, n_sel) * T if lb_ex is not None else 0) + (T if lb_sh is not None else 0)
         ws = _wgrad_ws(jobs, groups.numel(), max_rows, dev)
-        L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK, K,
-               L.ptr(order), L.ptr(t["topv"]), L.ptr(t["sgate"]), max_rows, L.ptr(ws), ws.numel(), st,
-               tag="lora_wgrad")
+        side_w = _Fork(dev, 1)
+        with side_w:
+            L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK,
+                   K, L.ptr(order), L.ptr(t["topv"]), L.ptr(t["sgate"]), max_rows, L.ptr(ws), ws.numel(), L.stream(),
+                   tag="lora_wgrad")
         if gx is not None:
             grads["ex"] = gx
         if gs is not None:
             grads["sh"] = gs
+    # (4) gate_up backward: per-slot dx rows
+    dxs = bf(M, H)
+    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True)
+    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
+           L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, L.ptr(dxs), H, None, st,
+           tag="gemm_gu_bwd")
+    side_r.join()
+    dx = bf(T, H)
+    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), int(t["sgate"] is not None), T, K, H, L.ptr(dx), st)
+    if side_w is not None:
+        side_w.join()
     return dx, dtopv, grads
 
 
@@ -753,6 +819,9 @@ class _MoELayerFn(torch.autograd.Function):
         sgate = torch.empty(T, dtype=torch.float32, device=dev) if fuse else None
         sgw = plan["shared"][2] if fuse else None
         lg = torch.empty(T, L.load().smel_route_ld(E, int(fuse)), dtype=torch.bfloat16, device=dev)
+        fork = _Fork(dev, 0)   # LoRA layouts overlap the router and the dispatch
+        with fork:
+            bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"], fuse, H, dev)
         L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
                L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.stream())
         if stats is not None:
@@ -760,7 +829,7 @@ class _MoELayerFn(torch.autograd.Function):
         c = _Ctx()
         shared = (plan["shared"][0], plan["shared"][1], sgate, plan["shared"][4], plan["shared"][5]) if fuse else None
         out = _forward_pipeline(x, plan["ex"], K, topv, topi32, False, shared, plan["lora_ex"], plan["lora_sh"],
-                                plan["need_grad"], c)
+                                plan["need_grad"], c, prep=(fork, bufs))
         if plan["need_grad"]:
             c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw))
             ctx.c = c
