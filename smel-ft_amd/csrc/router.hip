@@ -88,117 +88,112 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
 }
 
 // ---- logits GEMM: logits[t][c] = bf16(x[t] . w_c) for c < E (w_c = gate row c), at c = E32 = ceil32(E) the
-// shared-gate logit x[t] . w_sg (when sg), other columns 0. Block = 32 tokens x 64 columns (two 32-column MFMA
-// fragments); its 4 waves take the 64-wide k-steps j = w, w + 4, ... and add their partial sums through LDS in wave
-// order (fixed, so the result does not depend on timing). Grid = ceil(T / 32) x ceil(ldl / 64).
-constexpr int RT = 32;
-constexpr int RC = 64;
-constexpr int RW = 4;
+// shared-gate logit x[t] . w_sg (when sg), other columns 0. Block = 64 tokens x 96 columns, 4 waves; wave w takes
+// tokens 16 w .. 16 w + 15 against all 96 columns (v_mfma_f32_16x16x32_bf16, 6 column fragments) over the whole
+// hidden dim, so no partial sums are reduced. Per 64-wide k-step the block stages the 96 weight rows once in LDS
+// (LDS-DMA, 4-stage ring, XOR-swizzled 16-B chunks) and each wave loads its own 16 x rows into registers three steps
+// ahead: x is read once per column block and the weights once per 64 tokens. Grid = ceil(T / 64) x ceil(ldl / 96).
+constexpr int RT = 64;
+constexpr int RC = 96;
+constexpr int RKT = 64;
+constexpr int RSTAGE = RC * RKT;   // bf16 elements of one weight stage (12 KB)
 
-template <int NSTEP>
+SMEL_DEV f32x4_t mfma16r(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
+
 __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ gw,
                                                            const uint16_t* __restrict__ sg, int T, int H, int E,
                                                            int ldl, uint16_t* __restrict__ logits) {
-  __shared__ float red[RW * RT * (RC + 4)];
-  const int l = lane_id(), hi = l >> 5, r32 = l & 31;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ __attribute__((aligned(1024))) uint16_t WS[4][RSTAGE];
+  const int tid = threadIdx.x, l = lane_id(), kq = l >> 4, li = l & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = blockIdx.x * RT, c0 = blockIdx.y * RC;
   const int E32 = (E + 31) / 32 * 32;
-  // the two B fragments: expert rows, or the shared-gate row (its lane r32 = 0 only), or nothing
-  rsrc_t rb[2];
-  uint32_t boff[2];
-  bool fv[2];
+  const int nk = H / RKT;
+  // weight staging: wave-load ii of wave w fills weight rows 8 g .. 8 g + 7 (g = 3 w + ii) of a stage; lane i writes
+  // physical chunk i % 8 of row 8 g + i / 8 = logical chunk (i % 8) ^ swz(row). A group of 8 rows is all gate rows or
+  // all past E32 (E32 and c0 are multiples of 8), so one descriptor serves the wave-load.
   const rsrc_t rg = make_rsrc(gw, (uint64_t)E * H * 2);
+  const rsrc_t rsg = make_rsrc(sg ? sg : gw, sg ? (uint64_t)H * 2 : 0);
+  rsrc_t rb[3];
+  uint32_t boff[3];
 #pragma unroll
-  for (int f = 0; f < 2; ++f) {
-    const int cf = c0 + 32 * f;   // first column of the fragment (uniform)
-    const int c = cf + r32;
-    if (cf < E32) {
-      rb[f] = rg;
-      fv[f] = true;
-      boff[f] = c < E ? (uint32_t)c * H * 2 : OOB;
-    } else if (sg && cf == E32) {
-      rb[f] = make_rsrc(sg, (uint64_t)H * 2);
-      fv[f] = true;
-      boff[f] = r32 == 0 ? 0u : OOB;
-    } else {
-      rb[f] = rg;
-      fv[f] = false;
-      boff[f] = OOB;
-    }
+  for (int ii = 0; ii < 3; ++ii) {
+    const int row = 8 * (3 * w + ii) + (l >> 3);
+    const int c = c0 + row;
+    const int ch = (l & 7) ^ swz(row);
+    const bool gate = c0 + 8 * (3 * w + ii) < E32;   // uniform
+    rb[ii] = gate ? rg : rsg;
+    boff[ii] = gate ? (c < E ? (uint32_t)c * H * 2 + 16 * ch : OOB) : ((sg && c == E32) ? 16u * ch : OOB);
   }
+  // x rows of this wave: lane (kq, li) holds token 16 w + li, k = 32 s + 8 kq + [0, 8) in substep s
   const rsrc_t rx = make_rsrc(x, (uint64_t)T * H * 2);
-  const uint32_t aoff = t0 + r32 < T ? (uint32_t)(t0 + r32) * H * 2 : OOB;
-  const int nk = H / 64;
-  f32x16_t acc[2] = {f32x16_t{}, f32x16_t{}};
-  // the wave's k-steps j = w, w + 4, ...: four in flight in a ring of register sets (loads of step i + 4 are issued
-  // right after step i's MFMAs), so a block waits for about two memory latencies instead of one per step
-  u32x4_t A[4][4], B[4][2][4];
-  auto load = [&](int j, u32x4_t* a, u32x4_t (*b)[4]) {
-    const bool ok = j < nk;
-    const uint32_t k2 = (uint32_t)(j * 64 + 32 * hi) * 2;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) a[s] = ld16(rx, ok ? aoff + k2 + 16 * s : OOB);
-#pragma unroll
-    for (int f = 0; f < 2; ++f)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) b[f][s] = ld16(rb[f], ok ? boff[f] + k2 + 16 * s : OOB);
-  };
-  auto mma = [&](const u32x4_t* a, u32x4_t (*b)[4]) {
-#pragma unroll
-    for (int f = 0; f < 2; ++f)   // an unused fragment loads zeros (no branch: a branch here costs the ring)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc[f] = mfma32(a[s], b[f][s], acc[f]);
-  };
-#pragma unroll
-  for (int u = 0; u < 4; ++u) load(w + RW * u, A[u], B[u]);
-  __builtin_amdgcn_sched_barrier(0);
-  // straight-line code (NSTEP >= the wave's steps; steps past nk load zeros and add nothing), so the compiler's
-  // wait counts follow the ring exactly; a loop makes it drain all loads at every back edge
-  if constexpr (NSTEP > 0) {
-#pragma unroll
-    for (int i = 0; i < NSTEP; ++i) {
-      __builtin_amdgcn_sched_barrier(0);   // keep the four sets in flight (no sinking of loads toward their use)
-      mma(A[i & 3], B[i & 3]);
-      if (i + 4 < NSTEP) load(w + RW * (i + 4), A[i & 3], B[i & 3]);
-    }
+  const int tok = t0 + 16 * w + li;
+  const uint32_t xoff = tok < T ? (uint32_t)tok * H * 2 + 16 * kq : OOB;
+  auto issue = [&](int j, u32x4_t* xa) {
+    const bool in = j < nk;
+    const uint32_t k2 = (uint32_t)j * RKT * 2;
     __builtin_amdgcn_sched_barrier(0);
-  } else {   // any hidden size
-    const int nsteps = (nk + RW - 1) / RW;
-    for (int i = 0; i < nsteps; i += 4) {
+    xa[0] = ld16(rx, in ? xoff + k2 : OOB);
+    xa[1] = ld16(rx, in ? xoff + k2 + 64 : OOB);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        mma(A[u], B[u]);
-        load(w + RW * (i + u + 4), A[u], B[u]);
-      }
+    for (int ii = 0; ii < 3; ++ii) ld16_lds(rb[ii], &WS[j & 3][(3 * w + ii) * 512], in ? boff[ii] + k2 : OOB);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // weight fragment reads: column fragment f, substep s, lane (kq, li) -> row 16 f + li, logical chunk 4 s + kq
+  uint32_t brd[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) brd[s] = li * RKT + 8 * ((4 * s + kq) ^ swz(li));
+  f32x4_t acc[6];
+#pragma unroll
+  for (int f = 0; f < 6; ++f) acc[f] = f32x4_t{};
+  u32x4_t X0[2], X1[2], X2[2], X3[2];
+  auto compute = [&](int j, const u32x4_t* xa) {
+    const uint16_t* S = WS[j & 3];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int f = 0; f < 6; ++f)
+        acc[f] = mfma16r(xa[s], *reinterpret_cast<const u32x4_t*>(S + brd[s] + f * 16 * RKT), acc[f]);
+  };
+  // three steps ahead; per step and wave 2 x loads (registers) + 3 weight DMAs: before step j only steps j+1 and
+  // j+2 (10 operations) may still be in flight
+  issue(0, X0);
+  issue(1, X1);
+  issue(2, X2);
+  for (int j = 0; j < nk; j += 4) {
+    SMEL_WAIT_VM_LDS(10);
+    __builtin_amdgcn_s_barrier();
+    issue(j + 3, X3);
+    compute(j, X0);
+    SMEL_WAIT_VM_LDS(10);
+    __builtin_amdgcn_s_barrier();
+    issue(j + 4, X0);
+    compute(j + 1, X1);
+    SMEL_WAIT_VM_LDS(10);
+    __builtin_amdgcn_s_barrier();
+    issue(j + 5, X1);
+    compute(j + 2, X2);
+    SMEL_WAIT_VM_LDS(10);
+    __builtin_amdgcn_s_barrier();
+    issue(j + 6, X2);
+    compute(j + 3, X3);
+  }
+  SMEL_WAIT_VM(0);   // the trailing (out-of-range) loads
+  // D[4 kq + r][li] of fragment f: token 16 w + 4 kq + r, column c0 + 16 f + li
+#pragma unroll
+  for (int f = 0; f < 6; ++f) {
+    const int c = c0 + 16 * f + li;
+    if (c >= ldl) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 16 * w + 4 * kq + r;
+      if (t < T) logits[(int64_t)t * ldl + c] = f2bf(acc[f][r]);
     }
   }
-  float* mine = red + w * RT * (RC + 4);
-#pragma unroll
-  for (int f = 0; f < 2; ++f)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mine[acc_row(r, l) * (RC + 4) + 32 * f + r32] = acc[f][r];
-  __syncthreads();
-  // thread -> (row, 8 columns): sum the 4 partials in wave order, round to bf16, one 16-B store
-  const int row = threadIdx.x >> 3, col = 8 * (threadIdx.x & 7);
-  const int t = t0 + row, c = c0 + col;
-  if (t >= T || c >= ldl) return;
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float v[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int cc = col + 2 * i + h;
-      float sum = red[row * (RC + 4) + cc];
-#pragma unroll
-      for (int ww = 1; ww < RW; ++ww) sum += red[ww * RT * (RC + 4) + row * (RC + 4) + cc];
-      v[h] = sum;
-    }
-    o[i] = pack2bf(v[0], v[1]);
-  }
-  *reinterpret_cast<u32x4_t*>(logits + (int64_t)t * ldl + c) = u32x4_t{o[0], o[1], o[2], o[3]};
 }
 
 // ---- selection: one wave per token over its bf16 logits row (probs, top-k, renorm; shared-gate sigmoid).
@@ -368,21 +363,12 @@ __global__ __launch_bounds__(256) void dtopv_kernel(const float* __restrict__ dw
   out[p] = v;
 }
 
-// route_logits_kernel with the smallest unrolled step count that covers H (64-wide k-steps, RW waves)
-void launch_logits(dim3 grid, hipStream_t stream, const uint16_t* x, const uint16_t* gw, const uint16_t* sg, int T,
-                   int H, int E, int ldl, uint16_t* logits) {
-  const int steps = (H / 64 + RW - 1) / RW;
-  if (steps <= 4)
-    route_logits_kernel<4><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
-  else if (steps <= 8)
-    route_logits_kernel<8><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
-  else if (steps <= 12)
-    route_logits_kernel<12><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
-  else if (steps <= 16)
-    route_logits_kernel<16><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
-  else
-    route_logits_kernel<0><<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+void launch_logits(hipStream_t stream, const uint16_t* x, const uint16_t* gw, const uint16_t* sg, int T, int H, int E,
+                   int ldl, uint16_t* logits) {
+  const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
+  route_logits_kernel<<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
 }
+
 
 }  // namespace
 
@@ -411,8 +397,7 @@ extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint1
   if (T == 0) return 0;
   SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32 && logits, SMEL_EINVAL, "route: null pointer");
   const int64_t ldl = smel_route_ld(E, shared_gate_w != nullptr);
-  const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
-  launch_logits(grid, stream, x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
+  launch_logits(stream, x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
   route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K,
                                                             (int)((E + 31) / 32 * 32), probs, topv, topi, topi32,
                                                             shared_gate_w ? sgate : nullptr, nullptr, nullptr);
@@ -465,8 +450,7 @@ extern "C" int smel_route_gemma4(const uint16_t* h, const uint16_t* router_scale
   const unsigned tg = (unsigned)((T + 3) / 4);
   // H^-1/2 as the reference's Python float (a double) rounded to fp32 for the bf16 product
   route_prenorm<<<tg, 256, 0, stream>>>(h, router_scale, (int)T, (int)H, eps, (float)pow((double)H, -0.5), xn, rstd);
-  const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
-  launch_logits(grid, stream, xn, proj_w, nullptr, (int)T, (int)H, (int)E, (int)ldl, logits);
+  launch_logits(stream, xn, proj_w, nullptr, (int)T, (int)H, (int)E, (int)ldl, logits);
   route_select<<<tg, 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K, 0, probs, nullptr, topi, topi32,
                                        nullptr, topv, per_expert_scale);
   return smel::launch_status();
