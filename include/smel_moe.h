@@ -8,7 +8,9 @@
  * Row space shared by the grouped GEMMs: rows [0, TK) are the routed slots in expert-sorted order (TK = T*topk),
  * rows [TK, TK+T) are the shared expert's rows (one per token, token order) when the shared expert is fused in.
  * order[row] is the flat slot p = t*topk + k of a routed row. "Groups" are the experts 0..E-1 plus, when present,
- * the shared expert as group E; gkind[g] = (kind << 16) | index says where group g's weights live.
+ * the shared expert as group E; gkind[g] = (kind << 16) | index says where group g's weights live. A tile list entry
+ * is {group, row0, row1, gk}: the GEMM / LoRA entry points take gk from there when their gkind argument is NULL
+ * (smel_dispatch fills it when given gkind), which saves a dependent load per workgroup.
  */
 #ifndef SMEL_MOE_H
 #define SMEL_MOE_H
@@ -138,13 +140,14 @@ int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scal
 /* ---- (A3) replaces the dispatch of routed_experts, smel/moe.py:216-223 and the inverse of :249-250.
  * ids [T*K] (int32 if ids_are_i64 == 0, else int64) -> counts [E], offsets [E+1], order [TK] (stable: experts
  * ascending, slot p ascending within one), inv [TK], and the GEMM tile list: tiles [max_tiles][4] = {group, row0,
- * row1, 0} over groups 0..E-1 (+ group E = shared rows [TK, TK+shared_rows) when shared_rows > 0), m_tile rows
- * each; n_tiles [1] = how many are used. err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
+ * row1, gk} over groups 0..E-1 (+ group E = shared rows [TK, TK+shared_rows) when shared_rows > 0), m_tile rows
+ * each, gk = gkind[group] when gkind [E (+1)] is given (the GEMMs then need no gkind argument), else 0; n_tiles [1]
+ * = how many are used. err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
  * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
  * workspace. E <= 512. */
 int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
-                  int32_t m_tile, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
-                  int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream);
+                  int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
+                  int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream);
 /* int32 elements of smel_dispatch's workspace (host-side, no GPU call); -1 for bad sizes. */
 int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
 /* Upper bound of the tile-list length for smel_dispatch (host-side, no GPU call). */

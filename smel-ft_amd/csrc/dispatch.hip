@@ -65,7 +65,8 @@ __global__ __launch_bounds__(1024) void dispatch_hist(const void* __restrict__ i
 
 // (2) one block: counts, offsets, hist -> base[b][e] (first output position of block b's slots of expert e), tiles
 __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int shared_rows, int m_tile,
-                                                      int max_tiles, int32_t* __restrict__ hist,
+                                                      int max_tiles, const int32_t* __restrict__ gkind,
+                                                      int32_t* __restrict__ hist,
                                                       const int32_t* __restrict__ bad, int32_t* __restrict__ counts,
                                                       int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
                                                       int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
       tl.x = tid;
       tl.y = row0 + i * m_tile;
       tl.z = min(row0 + rows, row0 + (i + 1) * m_tile);
-      tl.w = 0;
+      tl.w = gkind ? gkind[tid] : 0;
       reinterpret_cast<int4*>(tiles)[tbase + i] = tl;
     }
   }
@@ -197,7 +198,8 @@ extern "C" int64_t smel_dispatch_ws_size(int64_t TK, int64_t E) {
 }
 
 extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
-                             int64_t shared_rows, int32_t m_tile, int32_t* counts, int32_t* offsets, int32_t* order,
+                             int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
+                             int32_t* offsets, int32_t* order,
                              int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, int32_t* ws,
                              hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && shared_rows >= 0 && m_tile > 0, SMEL_EINVAL, "dispatch: bad sizes");
@@ -215,8 +217,8 @@ extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, in
     const int st = smel::launch_status();
     if (st) return st;
   }
-  dispatch_scan<<<1, DB, 0, stream>>>(nb, (int)TK, (int)E, (int)shared_rows, m_tile, (int)mt, hist, bad, counts,
-                                      offsets, tiles, n_tiles, err);
+  dispatch_scan<<<1, DB, 0, stream>>>(nb, (int)TK, (int)E, (int)shared_rows, m_tile, (int)mt, gkind, hist, bad,
+                                      counts, offsets, tiles, n_tiles, err);
   if (nb > 0) {
     const int st = smel::launch_status();
     if (st) return st;

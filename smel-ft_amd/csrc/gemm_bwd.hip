@@ -433,7 +433,7 @@ SMEL_DEV void gmm_bwd_body(const BwdArgs& a, uint8_t* smem) {
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
-  const int gk = a.gkind[t.x];
+  const int gk = a.gkind ? a.gkind[t.x] : t.w;   // the tile list may carry the group kind itself
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
@@ -470,7 +470,7 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
                             int32_t act, const uint16_t* hsave, const uint16_t* topv, const float* sgate,
                             uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
-  SMEL_REQUIRE(w && gkind && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
+  SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->R && topk > 0, SMEL_EINVAL,
                "gmm_bwd: bad sizes");
   SMEL_REQUIRE(w->R % 64 == 0 && w->C % 32 == 0, SMEL_EUNSUPPORTED,

@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
-  const int gk = a.gkind[t.x];
+  const int gk = a.gkind ? a.gkind[t.x] : t.w;   // the tile list may carry the group kind itself
   const int kind = gk >> 16, idx = gk & 0xffff;
   const int nrows = min(t.z - t.y, MT);
   if (nrows <= 0) return;
@@ -374,7 +374,7 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
                             int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
                             int32_t act, uint16_t* out, int64_t ldo, uint16_t* hsave, hipStream_t stream) {
-  SMEL_REQUIRE(w && gkind && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_fwd: null pointer");
+  SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_fwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->C && topk > 0, SMEL_EINVAL,
                "gmm_fwd: bad sizes");
   SMEL_REQUIRE(w->C % 32 == 0, SMEL_EUNSUPPORTED, "gmm_fwd: K=%lld must be a multiple of 32", (long long)w->C);

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
   __shared__ float red[XW * 64 * 16];
   if ((int)blockIdx.x >= n_tiles[0]) return;
   const int4 t = tiles[blockIdx.x];
-  const int gk = gkind[t.x];
+  const int gk = gkind ? gkind[t.x] : t.w;
   const int kind = gk >> 16, idx = gk & 0xffff;
   if (kind != SMEL_KIND_SEL && kind != SMEL_KIND_SHARED) return;
   const int m = blockIdx.y;
@@ -414,7 +414,7 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
                              const int32_t* order, int64_t TK, int64_t topk, const uint16_t* wcat_sel,
                              const uint16_t* wcat_sh, int64_t Kd, float scale_sel, float scale_sh, uint16_t* ext,
                              hipStream_t stream) {
-  SMEL_REQUIRE(tiles && n_tiles && gkind && A_src && ext, SMEL_EINVAL, "lora_ext: null pointer");
+  SMEL_REQUIRE(tiles && n_tiles && A_src && ext, SMEL_EINVAL, "lora_ext: null pointer");
   SMEL_REQUIRE(Kd > 0 && Kd % 32 == 0, SMEL_EUNSUPPORTED, "lora_ext: K %lld must be a multiple of 32", (long long)Kd);
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A_src % 16) == 0, SMEL_EUNSUPPORTED, "lora_ext: A rows must be 16-B aligned");
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "lora_ext: gather needs order");

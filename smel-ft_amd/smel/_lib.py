@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("SMEL_MOE_LIB") or os.path.join(HERE, "libsmel_moe.so"
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -55,7 +55,7 @@ SIGNATURES = {
     "smel_route": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_ld": (i64, [i64, i32]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
-    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_ws_size": (i64, [i64, i64]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
     "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),

@@ -302,7 +302,7 @@ def _dense_tiles(T: int, device):
         n = (T + M_TILE - 1) // M_TILE
         t = torch.zeros(max(n, 1), 4, dtype=torch.int32)
         for i in range(n):
-            t[i, 0], t[i, 1], t[i, 2] = 0, i * M_TILE, min(T, (i + 1) * M_TILE)
+            t[i, 0], t[i, 1], t[i, 2], t[i, 3] = 0, i * M_TILE, min(T, (i + 1) * M_TILE), L.KIND_SHARED << 16
         _dense_tiles_cache[key] = (t.reshape(-1).to(device), torch.tensor([n], dtype=torch.int32, device=device),
                                    n, torch.tensor([L.KIND_SHARED << 16], dtype=torch.int32, device=device))
     return _dense_tiles_cache[key]
@@ -589,9 +589,10 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
         with fork:
             bufs = _prep_lora(ex, lora_ex, lora_sh, shared is not None, H, dev)
         prep = (fork, bufs)
-    L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(counts), L.ptr(offsets),
-           L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st)
-    gk = ex.gkind(shared is not None, dev)
+    gk_groups = ex.gkind(shared is not None, dev)
+    L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(gk_groups), L.ptr(counts),
+           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st)
+    gk = None   # the tile list carries each tile's group kind
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):
         sel_gu, sel_dn = ex.packed_sel()

@@ -352,7 +352,7 @@ def test_route_fused(T, H, E, K, shared):
 # ------------------------------------------------------------------------------------------------------ dispatch
 
 
-def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128):
+def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128, gkind=None):
     L = _lib()
     TK = T * K
     maxt = L.load().smel_dispatch_max_tiles(TK, E, shared_rows, m_tile)
@@ -360,8 +360,10 @@ def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128):
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
     ws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))   # garbage-filled: the kernels must not rely on zeros
-    L.call("smel_dispatch", L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, shared_rows, m_tile, L.ptr(counts),
-           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(ws), L.stream())
+    gk = torch.tensor(gkind, dtype=torch.int32, device=DEV) if gkind is not None else None
+    L.call("smel_dispatch", L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, shared_rows, m_tile, L.ptr(gk),
+           L.ptr(counts), L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err),
+           L.ptr(ws), L.stream())
     return [a.cpu().numpy() for a in (counts, offsets, order, inv, tiles, ntiles, err)]
 
 
@@ -397,13 +399,18 @@ def test_dispatch_bitexact(T, K, E, shared, kind):
         topi = topi.reshape(T, K).astype(np.int64)
     sh = T if shared else 0
     for dt in (torch.int32, torch.int64):
-        counts, offsets, order, inv, tiles, ntiles, err = _dispatch(torch.from_numpy(topi).to(DEV, dt), T, K, E, sh)
+        # with int64 ids, also hand over group kinds: the tile list then carries them in its fourth field
+        gkind = [(g * 7919) & 0x3ffff for g in range(E + 1)] if dt == torch.int64 else None
+        counts, offsets, order, inv, tiles, ntiles, err = _dispatch(torch.from_numpy(topi).to(DEV, dt), T, K, E, sh,
+                                                                    gkind=gkind)
         c0, o0, ord0, inv0 = intref.dispatch(topi, E)
         assert err[0] == 0
         assert np.array_equal(counts, c0) and np.array_equal(offsets, o0)
         if T:
             assert np.array_equal(order, ord0) and np.array_equal(inv, inv0)
         want = _expected_tiles(o0, E, T * K, sh, 128)
+        if gkind is not None:
+            want[:, 3] = np.asarray(gkind, np.int32)[want[:, 0]]
         assert ntiles[0] == len(want)
         assert np.array_equal(tiles.reshape(-1, 4)[:len(want)], want)
 
