@@ -106,6 +106,17 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Kd = a.Kd, N = a.N;
   const smel_wset& ws = a.w;
+  // What the epilogue needs per tile row, fetched now (thread t < MT: row t) so that no load sits between its
+  // stores: the output slot for the gate_up backward, the combine weight for the down backward.
+  int ep_slot = 0;
+  float ep_w = 0.f;
+  if (tid < nrows) {
+    const int grow = row0 + tid;
+    if (EPI == 0)
+      ep_slot = row_slot(grow, a.order, a.TK);
+    else
+      ep_w = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
+  }
   const int cw = nb * NB + w * 64;   // this wave's first output column
   const int nk = (Kd + KT - 1) / KT;
   const int np = N / 32;             // column pairs of one matrix
@@ -360,6 +371,14 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
         Et(row >> 5)[lr * 256 + 8 * ((col >> 3) ^ (lr & 7)) + (col & 7)] = f2bf(acc[m][f][r]);
       }
     }
+  // per-row slot / weight table right after the staged tile (inside the ring, free now)
+  int* const rowmap = reinterpret_cast<int*>(smem + 4 * A_BYTES);
+  if (tid < MT) {
+    if (EPI == 0)
+      rowmap[tid] = ep_slot;
+    else
+      reinterpret_cast<float*>(rowmap)[tid] = ep_w;
+  }
   __syncthreads();
   // thread -> (row, 8-column chunk): 32 threads per row, 8 rows per pass
   const int ch = tid & 31;
@@ -369,7 +388,7 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       for (int row = tid >> 5; row < nrows; row += 8) {
         const int lr = row & 31;
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
-        const int64_t orow = row_slot(row0 + row, a.order, a.TK);
+        const int64_t orow = rowmap[row];
         *reinterpret_cast<u32x4_t*>(a.out + orow * a.ldo + col0) = v;
       }
     }
@@ -379,42 +398,61 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   // du = da act(g), and the row's partial of sum_n acc * bf16(act(g) u) over this block's columns -> dwp.
   const int I = N;
   const bool cv = col0 < I;
-  for (int row = tid >> 5; row < nrows; row += 8) {   // 32 threads per row, uniform trip count per row group
-    const int lr = row & 31;
-    const u32x4_t av = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
-    const int grow = row0 + row;
-    const float wrow_ = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
-    float part = 0.f;
-    if (cv) {
-      const u32x4_t g2 = *reinterpret_cast<const u32x4_t*>(a.hsave + (int64_t)grow * 2 * I + col0);
-      const u32x4_t u2 = *reinterpret_cast<const u32x4_t*>(a.hsave + (int64_t)grow * 2 * I + I + col0);
-      uint32_t og[4], ou[4];
+  const float* const wmap = reinterpret_cast<const float*>(rowmap);
+  // 32 threads per row, 8 rows per pass; the saved (g, u) of 8 passes are loaded before any of them is used, so the
+  // stores of one batch never wait for the loads of the next row
+  constexpr int PB = 8;
+  for (int rb = tid >> 5; rb < nrows; rb += 8 * PB) {
+    u32x4_t g2s[PB], u2s[PB];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float dgv[2], duv[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
-          const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
-          const float acv = h ? bf_hi(av[j]) : bf_lo(av[j]);
-          float avl, dav;
-          act_and_grad_f(g, a.act, avl, dav);
-          const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
-          part += acv * abf;
-          const float da = wrow_ * acv;
-          dgv[h] = da * u * dav;
-          duv[h] = da * avl;
-        }
-        og[j] = pack2bf(dgv[0], dgv[1]);
-        ou[j] = pack2bf(duv[0], duv[1]);
+    for (int p = 0; p < PB; ++p) {
+      const int64_t grow = row0 + rb + 8 * p;
+      g2s[p] = u2s[p] = u32x4_t{};
+      if (cv && rb + 8 * p < nrows) {
+        g2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + col0);
+        u2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + I + col0);
       }
-      *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + col0) = u32x4_t{og[0], og[1], og[2], og[3]};
-      *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + I + col0) = u32x4_t{ou[0], ou[1], ou[2], ou[3]};
     }
-    // fixed-order sum over the row's 32 threads (lanes 32 h .. 32 h + 31 of a wave)
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) part += __shfl_xor(part, o, 64);
-    if (ch == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
+    for (int p = 0; p < PB; ++p) {
+      const int row = rb + 8 * p;
+      if (row >= nrows) break;   // uniform over the row's 32 threads
+      const int lr = row & 31;
+      const u32x4_t av = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
+      const int grow = row0 + row;
+      const float wrow_ = wmap[row];
+      float part = 0.f;
+      if (cv) {
+        const u32x4_t g2 = g2s[p];
+        const u32x4_t u2 = u2s[p];
+        uint32_t og[4], ou[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float dgv[2], duv[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
+            const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
+            const float acv = h ? bf_hi(av[j]) : bf_lo(av[j]);
+            float avl, dav;
+            act_and_grad_f(g, a.act, avl, dav);
+            const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
+            part += acv * abf;
+            const float da = wrow_ * acv;
+            dgv[h] = da * u * dav;
+            duv[h] = da * avl;
+          }
+          og[j] = pack2bf(dgv[0], dgv[1]);
+          ou[j] = pack2bf(duv[0], duv[1]);
+        }
+        *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + col0) = u32x4_t{og[0], og[1], og[2], og[3]};
+        *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + I + col0) = u32x4_t{ou[0], ou[1], ou[2], ou[3]};
+      }
+      // fixed-order sum over the row's 32 threads (lanes 32 h .. 32 h + 31 of a wave)
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) part += __shfl_xor(part, o, 64);
+      if (ch == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
+    }
   }
 }
 

@@ -47,11 +47,15 @@ struct FwdArgs {
 
 template <int EPI, bool Q4, int NS, bool FAST>
 SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
-                       uint16_t* S2, uint16_t* S3) {
+                       uint16_t* S2, uint16_t* S3, int* rowmap) {
   const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = a.K;
   const smel_wset& ws = a.w;
+  // output slot of tile row t (thread t < MT) for the down projection, fetched now so that no load sits between the
+  // epilogue's stores
+  int ep_slot = 0;
+  if (EPI == 0 && tid < nrows) ep_slot = row_slot(row0 + tid, a.order, a.TK);
   // ---- this wave's two 32-row weight fragments: gate/up pair for epilogue 1, two adjacent fragments else
   int n0, n1, fr0, fr1;
   bool fv0, fv1;
@@ -307,6 +311,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   } else {
     // out tile [128][256]: rows 32 m .. 32 m + 31 in stage m; column = 64 w + 32 f + r32 inside the block's 256
     uint16_t* const St[4] = {S0, S1, S2, S3};
+    if (tid < MT) rowmap[tid] = ep_slot;
 #pragma unroll
     for (int m = 0; m < NS; ++m) {
 #pragma unroll
@@ -327,7 +332,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       for (int row = tid >> 5; row < nrows; row += 8) {
         const int lr = row & 31;
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(St[row >> 5] + lr * 256 + 8 * (ch ^ (lr & 7)));
-        const int64_t orow = row_slot(row0 + row, a.order, a.TK);
+        const int64_t orow = rowmap[row];
         *reinterpret_cast<u32x4_t*>(a.out + orow * a.ldo + col0) = v;
       }
     }
@@ -336,12 +341,12 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 
 template <int EPI, bool Q4, bool FAST>
 SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0,
-                          uint16_t* S1, uint16_t* S2, uint16_t* S3) {
+                          uint16_t* S1, uint16_t* S2, uint16_t* S3, int* rowmap) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
-    case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
-    case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
-    default: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3); break;
+    case 1: run_tile<EPI, Q4, 1, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
+    case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
+    case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
+    default: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
   }
 }
 
@@ -351,6 +356,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(1024))) uint16_t S1[A_STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t S2[A_STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t S3[A_STAGE];
+  __shared__ int rowmap[MT];
   int tile, nb;
   if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
   const int4 t = a.tiles[tile];
@@ -360,11 +366,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4) {
     if (a.w.flags & SMEL_WSET_FAST_DQ)
-      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap);
     else
-      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap);
   } else {
-    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3);
+    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap);
   }
 }
 
