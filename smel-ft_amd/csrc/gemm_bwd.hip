@@ -5,9 +5,9 @@
 // the combine, smel/moe.py:204-252, smel/lora.py:61-83.
 //
 // The weights come in the transposed fragment layout of smel_pack_int4_t / smel_pack_bf16_t, so every wave streams its
-// own 64 output columns (int4: through the LDS ring by LDS-DMA) and dequantizes them in registers, as the forward
-// kernel does; the int4 scale / zero vary along the contraction here, so each lane needs one (scale, zero) pair per
-// row it holds: those 64-pair runs (fp32, ready to use) go global -> LDS by LDS-DMA beside the A rows.
+// own 64 output columns straight into registers and dequantizes them there, as the forward kernel does; the int4
+// scale / zero vary along the contraction here, so each lane needs one (scale, zero) pair per row it holds: those
+// 64-pair runs (fp32, ready to use) go global -> LDS by LDS-DMA beside the A rows.
 //
 // Block = 4 waves, tile = up to 128 rows of one group (4 slices of 32) x 256 columns (64 per wave).
 // MFMA v_mfma_f32_16x16x32_bf16: lane l = 16 kq + i carries, in substep s of a 64-wide k-step, k = 32 s + 8 kq +
@@ -15,7 +15,8 @@
 // accumulates D[4 kq + r][i]. Per k-step:
 //  * A rows (gathered by token for the down projection) go global -> LDS (16-B LDS-DMA) into a ring of 4 stages,
 //    XOR-swizzled as in the forward kernel; each wave DMAs its own scale/zero words (4 B per lane) into the stage;
-//  * weights run 3 k-steps ahead (int4: a 4-deep register ring of 2 loads; bf16: 1 step ahead, 8 loads);
+//  * int4: weights (a 4-deep register ring of 2 loads), scale/zero and A all run 3 k-steps ahead; bf16: weights 1
+//    step ahead (8 loads), A 3 steps ahead;
 //  * vmcnt retires in issue order: each step issues its weight loads before its LDS-DMAs and waits for exactly the
 //    loads of the step it is about to use.
 #include "abi_util.h"
@@ -27,13 +28,13 @@ constexpr int MT = 128;
 constexpr int KT = 64;
 constexpr int NB = 256;            // output columns per block
 constexpr int A_BYTES = MT * KT * 2;         // A rows of one stage
-constexpr int Q_BYTES = 4 * 2 * 1024;        // int4 q of one stage: 4 waves x 2 column pairs
 // scale/zero of one stage: 4 waves x 64 rows x (scale, zero) fp32, per group (two groups per wave when the int4 group
 // is 32 wide: SZ2)
 constexpr int z_bytes(bool sz2) { return 4 * 512 * (sz2 ? 2 : 1); }
-constexpr int q_stage(bool sz2) { return A_BYTES + Q_BYTES + z_bytes(sz2); }
-constexpr int smem_bytes(bool sz2) { return 3 * q_stage(sz2) > 4 * A_BYTES ? 3 * q_stage(sz2) : 4 * A_BYTES; }
-static_assert(smem_bytes(false) <= 80 * 1024, "two blocks per CU");
+constexpr int q_stage(bool sz2) { return A_BYTES + z_bytes(sz2); }
+// 4 stages; the epilogue's staged tile (4 x A_BYTES) and its 512-B row table fit inside
+constexpr int smem_bytes(bool sz2) { return 4 * q_stage(sz2); }
+static_assert(smem_bytes(false) <= 80 * 1024 && 4 * A_BYTES + 512 <= smem_bytes(false), "two blocks per CU");
 
 struct BwdArgs {
   smel_wset w;
@@ -92,15 +93,13 @@ SMEL_DEV void ld4_lds(rsrc_t r, const void* lds, uint32_t off) {
 
 template <int EPI, bool Q4, int NS, bool SZ2, bool FAST>
 SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint8_t* smem) {
-  // LDS rings. int4: 3 stages of [A rows 16 KB | q of 4 waves x 2 column pairs, 8 KB | scale/zero pairs of 4 waves x
-  // 64 rows (x 2 groups for SZ2), 2 KB (4 KB)]. bf16: 4 stages of A rows (the weights go to registers). The epilogue
-  // reuses the first 64 KB.
+  // LDS rings of 4 stages. int4: [A rows 16 KB | scale/zero pairs of 4 waves x 64 rows (x 2 groups for SZ2), 2 KB
+  // (4 KB)]; bf16: A rows. The weights go to registers. The epilogue reuses the first 64 KB.
   constexpr int QS = q_stage(SZ2), ZW = SZ2 ? 1024 : 512;   // stage bytes, scale/zero bytes per wave
   auto St = [&](int st) {
     return reinterpret_cast<uint16_t*>(smem + st * (Q4 ? QS : A_BYTES));
   };
-  auto Qt = [&](int st) { return smem + st * QS + A_BYTES; };
-  auto Zt = [&](int st) { return smem + st * QS + A_BYTES + Q_BYTES; };
+  auto Zt = [&](int st) { return smem + st * QS + A_BYTES; };
   auto Et = [&](int m) { return reinterpret_cast<uint16_t*>(smem + m * A_BYTES); };
   const int tid = threadIdx.x, l = lane_id(), kq = l >> 4, li = l & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -166,15 +165,15 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       aoff[ii] = (uint32_t)src * (uint32_t)a.lda * 2 + 16 * c;
     }
   }
-  // All loads of step j into stage st: int4 -> q (2 x 1 KB per wave), scale/zero pairs (2 x 256 B per group), A
-  // (4 x 1 KB); bf16 -> A only.
-  auto issue_lds = [&](int j, int st) {
+  // All loads of step j: int4 -> q (2 x 16 B per lane) into the registers qd, scale/zero pairs (2 x 256 B per group)
+  // into stage st; A (4 x 1 KB) into stage st.
+  auto issue_lds = [&](int j, int st, u32x4_t* qd) {
     const bool in = j < nk;
     const uint32_t k2 = (uint32_t)j * KT * 2;
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (Q4) {
-      ld16_lds(rw, Qt(st) + w * 2048, in ? wo + j * 1024 : OOB);
-      ld16_lds(rw1, Qt(st) + w * 2048 + 1024, in ? wo + j * 1024 : OOB);
+      qd[0] = ld16(rw, in ? wo + j * 1024 : OOB);
+      qd[1] = ld16(rw1, in ? wo + j * 1024 : OOB);
       ld4_lds(rsz, Zt(st) + w * ZW, in ? so + j * 512 : OOB);
       ld4_lds(rsz, Zt(st) + w * ZW + 256, in ? so + j * 512 + 256 : OOB);
       if constexpr (SZ2) {
@@ -200,84 +199,106 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     for (int f = 0; f < 4; ++f) acc[m][f] = f32x4_t{};
 
   if constexpr (Q4) {
-    // One substep: the 2 NS A fragments, this lane's q words and its 8 scale/zero pairs come from the stage; then
-    // column fragment f+1 is dequantized (VALU) while the 2 NS MFMAs of fragment f run, so the two pipes overlap
-    // inside a wave.
+    // One k-step = 2 substeps of 32. The A fragments, this lane's q words and its scale/zero pairs come from the
+    // stage. The compiler would run a substep's four dequants (VALU) back to back and then its MFMAs, so the order is
+    // fixed by sched_barrier fences: each group of MFMAs on column fragment f runs beside half of the dequant of
+    // fragment f+1, and the second half of substep 0 (MFMAs only) also prepares substep 1's scale/zero and first
+    // fragment. 16 A registers live at a time (first half rows, then second half rows).
     const uint32_t magic = FAST ? f16_magic() : 0u;
-    auto compute = [&](int st) {
+    auto compute = [&](int st, const u32x4_t* qv) {
       const uint16_t* S = St(st);
       const float* Z = reinterpret_cast<const float*>(Zt(st) + w * ZW) + 32 * kq;
-      const u32x4_t q0 = *reinterpret_cast<const u32x4_t*>(Qt(st) + w * 2048 + l * 16);
-      const u32x4_t q1 = *reinterpret_cast<const u32x4_t*>(Qt(st) + w * 2048 + 1024 + l * 16);
+      const u32x4_t q0 = qv[0], q1 = qv[1];
+      float sc[8], ze[8];
+      u32x4_t b[4];
+      auto unpack = [&](const float* zp) {   // 8 (scale, zero) pairs, used as they are
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const f32x4_t z4 = *reinterpret_cast<const f32x4_t*>(zp + 4 * v);
+          sc[2 * v] = z4[0];
+          ze[2 * v] = z4[1];
+          sc[2 * v + 1] = z4[2];
+          ze[2 * v + 1] = z4[3];
+        }
+      };
+      // half h of column fragment f's dequant in substep s. Fast bank: B words h and h + 2 (rows 2h, 2h+1 and
+      // 2h+4, 2h+5, the same arithmetic as dq8rf); exact path: the whole fragment with h = 0.
+      auto dqh = [&](int s, int f, int h) {
+        const uint32_t qw = (f < 2 ? q0 : q1)[2 * (f & 1) + s];
+        if constexpr (FAST) {
+          const uint32_t x0 = ((qw >> (8 * h)) & 0x000F000Fu) | magic;
+          const uint32_t x1 = ((qw >> (8 * h + 4)) & 0x000F000Fu) | magic;
+          const int j = 2 * h;
+          b[f][h] = pack2bf(fmaf(h_lo(x0), sc[j], ze[j]), fmaf(h_lo(x1), sc[j + 1], ze[j + 1]));
+          b[f][h + 2] = pack2bf(fmaf(h_hi(x0), sc[j + 4], ze[j + 4]), fmaf(h_hi(x1), sc[j + 5], ze[j + 5]));
+        } else if (h == 0) {
+          uint32_t o[4];
+          dq8r(qw, sc, ze, o);   // rows / columns outside the matrix hold q = s = z = 0
+          b[f] = u32x4_t{o[0], o[1], o[2], o[3]};
+        }
+      };
+      constexpr int H1 = (NRF + 1) / 2, HA = (H1 + 1) / 2;   // first-half row fragments, in two MFMA groups
+      unpack(Z);
+      dqh(0, 0, 0);
+      dqh(0, 0, 1);
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        float sc[8], ze[8];
-        auto unpack = [&](const float* zp) {   // 8 (scale, zero) pairs, used as they are
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const f32x4_t z4 = *reinterpret_cast<const f32x4_t*>(zp + 4 * v);
-            sc[2 * v] = z4[0];
-            ze[2 * v] = z4[1];
-            sc[2 * v + 1] = z4[2];
-            ze[2 * v + 1] = z4[3];
-          }
-        };
-        auto dq = [&](int f) {
-          const int fr = f & 1;
-          if (SZ2 && f == 2) unpack(Z + 128 + 16 * s);
-          const uint32_t qw = (f < 2 ? q0 : q1)[2 * fr + s];
-          uint32_t o[4];
-          if constexpr (FAST)
-            dq8rf(qw, sc, ze, magic, o);
-          else
-            dq8r(qw, sc, ze, o);   // rows / columns outside the matrix hold q = s = z = 0
-          return u32x4_t{o[0], o[1], o[2], o[3]};
-        };
-        unpack(Z + 16 * s);
-        // first half of the row fragments: fragment f+1 dequantized while fragment f's MFMAs run; second half: the
-        // four finished B fragments again (16 A registers live instead of 32)
-        constexpr int H1 = (NRF + 1) / 2;
-        u32x4_t af[H1], b[4];
+        u32x4_t af[H1];
 #pragma unroll
         for (int m = 0; m < H1; ++m) af[m] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
-        b[0] = dq(0);
 #pragma unroll
         for (int f = 0; f < 4; ++f) {
-          if (f < 3) b[f + 1] = dq(f + 1);
+          if (SZ2 && f == 1) unpack(Z + 128 + 16 * s);   // fragments 2, 3 are the wave's second scale/zero group
 #pragma unroll
-          for (int m = 0; m < H1; ++m) acc[m][f] = mfma16(af[m], b[f], acc[m][f]);
+          for (int m = 0; m < HA; ++m) acc[m][f] = mfma16(af[m], b[f], acc[m][f]);
+          if (f < 3) dqh(s, f + 1, 0);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int m = HA; m < H1; ++m) acc[m][f] = mfma16(af[m], b[f], acc[m][f]);
+          if (f < 3) dqh(s, f + 1, 1);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (NRF > H1) {
 #pragma unroll
-          for (int m = H1; m < NRF; ++m)
-            af[m - H1] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
+        for (int m = H1; m < NRF; ++m) af[m - H1] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
 #pragma unroll
-          for (int f = 0; f < 4; ++f)
+        for (int f = 0; f < 4; ++f) {
 #pragma unroll
-            for (int m = H1; m < NRF; ++m) acc[m][f] = mfma16(af[m - H1], b[f], acc[m][f]);
+          for (int m = H1; m < NRF; ++m) acc[m][f] = mfma16(af[m - H1], b[f], acc[m][f]);
+          if (s == 0) {   // substep 1's first fragment: b[0] is free once these MFMAs on it are issued
+            if (f == 0) unpack(Z + 16);
+            if (f == 1) dqh(1, 0, 0);
+            if (f == 2) dqh(1, 0, 1);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);   // one substep's fragments live at a time (256-VGPR budget)
       }
     };
-    // 3-stage ring, every operand by LDS-DMA, two steps ahead: before step j only step j+1's loads may be in flight.
+    // 4-stage ring (q: 4 register sets), three steps ahead: before step j, steps j+1 and j+2 may be in flight.
     constexpr int NV = 2 + (SZ2 ? 4 : 2) + 4;   // vector-memory ops per step: 2 q, 2-4 scale/zero, 4 A
+    u32x4_t qa[2], qb[2], qc[2], qe[2];
+    u32x4_t* const qs[4] = {qa, qb, qc, qe};
     auto step = [&](int j, int st) {
-      SMEL_WAIT_VM_LDS(NV);
+      SMEL_WAIT_VM_LDS(2 * NV);
       __builtin_amdgcn_s_barrier();
-      issue_lds(j + 2, st == 0 ? 2 : st - 1);
-      compute(st);
+      issue_lds(j + 3, (st + 3) & 3, qs[(st + 3) & 3]);
+      compute(st, qs[st]);
     };
-    issue_lds(0, 0);
-    issue_lds(1, 1);
+    issue_lds(0, 0, qa);
+    issue_lds(1, 1, qb);
+    issue_lds(2, 2, qc);
     int i = 0;
-    for (; i + 3 <= nk; i += 3) {   // whole rounds of 3 steps, then the 0-2 remaining ones
+    for (; i + 4 <= nk; i += 4) {   // whole rounds of 4 steps, then the 0-3 remaining ones
       step(i, 0);
       step(i + 1, 1);
       step(i + 2, 2);
+      step(i + 3, 3);
     }
     if (i < nk) {
       step(i, 0);
-      if (i + 1 < nk) step(i + 1, 1);
+      if (i + 1 < nk) {
+        step(i + 1, 1);
+        if (i + 2 < nk) step(i + 2, 2);
+      }
     }
   } else {
     auto mma = [&](const uint16_t* S, int s, const u32x4_t* b) {
@@ -307,30 +328,30 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
 #pragma unroll
       for (int s = 0; s < 2; ++s) mma(St(st), s, b[s]);
     };
-    issue_lds(0, 0);
-    issue_lds(1, 1);
+    issue_lds(0, 0, nullptr);
+    issue_lds(1, 1, nullptr);
     issue_b(0, bA);
-    issue_lds(2, 2);
+    issue_lds(2, 2, nullptr);
     for (int i = 0; i < nk; i += 4) {
       SMEL_WAIT_VM_LDS(4);
       __builtin_amdgcn_s_barrier();
       issue_b(i + 1, bB);
-      issue_lds(i + 3, 3);
+      issue_lds(i + 3, 3, nullptr);
       compute(0, bA);
       SMEL_WAIT_VM_LDS(4);
       __builtin_amdgcn_s_barrier();
       issue_b(i + 2, bA);
-      issue_lds(i + 4, 0);
+      issue_lds(i + 4, 0, nullptr);
       compute(1, bB);
       SMEL_WAIT_VM_LDS(4);
       __builtin_amdgcn_s_barrier();
       issue_b(i + 3, bB);
-      issue_lds(i + 5, 1);
+      issue_lds(i + 5, 1, nullptr);
       compute(2, bA);
       SMEL_WAIT_VM_LDS(4);
       __builtin_amdgcn_s_barrier();
       issue_b(i + 4, bA);
-      issue_lds(i + 6, 2);
+      issue_lds(i + 6, 2, nullptr);
       compute(3, bB);
     }
   }
