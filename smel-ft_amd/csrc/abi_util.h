@@ -18,6 +18,19 @@ inline int launch_status() {
   }
   return 0;
 }
+
+// Compute units of the current device, queried once per device (the grid of the persistent kernels).
+inline int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 }  // namespace smel
 
 #define SMEL_REQUIRE(cond, code, ...)  \

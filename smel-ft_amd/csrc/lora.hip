@@ -85,73 +85,112 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
     o32[p] = pack2bf(val(2u * p), val(2u * p + 1u));
 }
 
-// ext[row][0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles. Block = one 32-row
-// slice of a tile; its 8 waves take the 64-wide k-steps j = w, w + 8, ... issuing all loads of up to XPRE of their
-// steps before the MFMAs (one memory latency per XPRE steps, not one per step); the partial sums are added in wave
-// order through LDS.
+// ext[row][0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles. Persistent: one block
+// per CU first builds, in LDS, the list of this call's tiles that carry a LoRA (the tile list holds each tile's kind;
+// all tile entries are loaded at once, one memory latency), then takes the (LoRA tile, 32-row slice) items
+// blockIdx.x, blockIdx.x + gridDim.x, ... A slice's 8 waves take the 64-wide k-steps j = w, w + 8, ..., issuing all
+// loads of up to XPRE of their steps before the MFMAs (one memory latency per XPRE steps, not one per step); the
+// partial sums are added in wave order through LDS.
 constexpr int XW = 8;
 constexpr int XPRE = 4;
+constexpr int XT_PER = 8;              // tile entries each thread scans
+constexpr int XLT = 512 * XT_PER;      // tiles one call may hold
 
 __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
                                                        const int32_t* __restrict__ gkind, const uint16_t* __restrict__ A,
                                                        int64_t lda, int64_t a_rows, int a_gather,
                                                        const int32_t* __restrict__ order, int TK, int topk,
                                                        const uint16_t* __restrict__ wsel, const uint16_t* __restrict__ wsh,
-                                                       int Kd, float ssel, float ssh, uint16_t* __restrict__ ext) {
+                                                       int Kd, float ssel, float ssh, uint16_t* __restrict__ ext,
+                                                       int max_tiles) {
   __shared__ float red[XW * 64 * 16];
-  if ((int)blockIdx.x >= n_tiles[0]) return;
-  const int4 t = tiles[blockIdx.x];
-  const int gk = gkind ? gkind[t.x] : t.w;
-  const int kind = gk >> 16, idx = gk & 0xffff;
-  if (kind != SMEL_KIND_SEL && kind != SMEL_KIND_SHARED) return;
-  const int m = blockIdx.y;
-  const int nrows = min(t.z - t.y, 128);
-  if (m * 32 >= nrows) return;
-  const uint16_t* wc = kind == SMEL_KIND_SEL ? (wsel ? wsel + (int64_t)idx * 32 * Kd : nullptr) : wsh;
-  if (!wc) return;   // this group has no LoRA
-  const int l = lane_id(), w = threadIdx.x >> 6, hi = l >> 5, r32 = l & 31;
-  const float scale = kind == SMEL_KIND_SEL ? ssel : ssh;
-  const int row = m * 32 + r32;
-  const rsrc_t ra = make_rsrc(A, (uint64_t)a_rows * lda * 2);
-  const rsrc_t rb = make_rsrc(wc, (uint64_t)32 * Kd * 2);
-  uint32_t ao = OOB;
-  if (row < nrows) {
-    const int grow = t.y + row;
-    ao = (uint32_t)(a_gather ? row_token(grow, order, TK, topk) : grow) * (uint32_t)lda * 2;
+  __shared__ int lt[XLT];
+  __shared__ int wcnt[XT_PER][XW];
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
+  // ---- the LoRA tiles of this call, in tile order
+  const int nt = min(n_tiles[0], max_tiles);
+  bool fl[XT_PER];
+#pragma unroll
+  for (int p = 0; p < XT_PER; ++p) {
+    const int i = p * 512 + tid;
+    fl[p] = false;
+    if (i < nt) {
+      const int4 t = tiles[i];
+      const int kind = (gkind ? gkind[t.x] : t.w) >> 16;
+      fl[p] = (kind == SMEL_KIND_SEL && wsel) || (kind == SMEL_KIND_SHARED && wsh);
+    }
   }
-  const uint32_t bo = (uint32_t)r32 * Kd * 2;
+  uint64_t msk[XT_PER];
+#pragma unroll
+  for (int p = 0; p < XT_PER; ++p) {
+    msk[p] = __ballot(fl[p]);
+    if (l == 0) wcnt[p][w] = __popcll(msk[p]);
+  }
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int p = 0; p < XT_PER; ++p) {
+    int off = total;
+#pragma unroll
+    for (int v = 0; v < XW; ++v) {
+      off += v < w ? wcnt[p][v] : 0;
+      total += wcnt[p][v];
+    }
+    if (fl[p]) lt[off + __popcll(msk[p] & ((1ull << l) - 1ull))] = p * 512 + tid;
+  }
+  __syncthreads();
+  // ---- (tile, slice) items
+  const rsrc_t ra = make_rsrc(A, (uint64_t)a_rows * lda * 2);
   const int nk = (Kd + 63) / 64;
-  f32x16_t acc = f32x16_t{};
-  for (int j0 = w; j0 < nk; j0 += XW * XPRE) {
-    u32x4_t av[XPRE][4], bv[XPRE][4];
+  for (int item = blockIdx.x; item < 4 * total; item += gridDim.x) {
+    const int4 t = tiles[lt[item >> 2]];
+    const int kind = (gkind ? gkind[t.x] : t.w) >> 16, idx = (gkind ? gkind[t.x] : t.w) & 0xffff;
+    const int m = item & 3;
+    const int nrows = min(t.z - t.y, 128);
+    if (m * 32 >= nrows) continue;   // uniform over the block
+    const uint16_t* wc = kind == SMEL_KIND_SEL ? wsel + (int64_t)idx * 32 * Kd : wsh;
+    const float scale = kind == SMEL_KIND_SEL ? ssel : ssh;
+    const int row = m * 32 + r32;
+    const rsrc_t rb = make_rsrc(wc, (uint64_t)32 * Kd * 2);
+    uint32_t ao = OOB;
+    if (row < nrows) {
+      const int grow = t.y + row;
+      ao = (uint32_t)(a_gather ? row_token(grow, order, TK, topk) : grow) * (uint32_t)lda * 2;
+    }
+    const uint32_t bo = (uint32_t)r32 * Kd * 2;
+    f32x16_t acc = f32x16_t{};
+    for (int j0 = w; j0 < nk; j0 += XW * XPRE) {
+      u32x4_t av[XPRE][4], bv[XPRE][4];
 #pragma unroll
-    for (int p = 0; p < XPRE; ++p) {
-      const int kk = (j0 + XW * p) * 64 + 32 * hi;
-      const bool ok = kk + 32 <= Kd;   // Kd % 32 == 0: a lane half's 32 k are all in or all out
+      for (int p = 0; p < XPRE; ++p) {
+        const int kk = (j0 + XW * p) * 64 + 32 * hi;
+        const bool ok = kk + 32 <= Kd;   // Kd % 32 == 0: a lane half's 32 k are all in or all out
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        av[p][s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
-        bv[p][s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
+        for (int s = 0; s < 4; ++s) {
+          av[p][s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
+          bv[p][s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);   // every load of the batch is issued before the first MFMA waits
+#pragma unroll
+      for (int p = 0; p < XPRE; ++p)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma32(av[p][s], bv[p][s], acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(w * 16 + r) * 64 + l] = acc[r];   // lane-contiguous: no bank conflicts
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = red[r * 64 + l];
+#pragma unroll
+        for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
+        const int orow = m * 32 + acc_row(r, l);
+        if (orow < nrows) ext[(int64_t)(t.y + orow) * 32 + r32] = f2bf(scale * v);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);   // every load of the batch is issued before the first MFMA waits
-#pragma unroll
-    for (int p = 0; p < XPRE; ++p)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc = mfma32(av[p][s], bv[p][s], acc);
-  }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) red[(w * 16 + r) * 64 + l] = acc[r];   // lane-contiguous: no bank conflicts
-  __syncthreads();
-  if (w == 0) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = red[r * 64 + l];
-#pragma unroll
-      for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
-      const int orow = m * 32 + acc_row(r, l);
-      if (orow < nrows) ext[(int64_t)(t.y + orow) * 32 + r32] = f2bf(scale * v);
-    }
+    __syncthreads();   // red is reused by the next item
   }
 }
 
@@ -419,11 +458,12 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A_src % 16) == 0, SMEL_EUNSUPPORTED, "lora_ext: A rows must be 16-B aligned");
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "lora_ext: gather needs order");
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "lora_ext: A larger than 2 GiB");
-  if (max_tiles == 0) return 0;
-  dim3 grid((unsigned)max_tiles, 4);
-  lora_ext_kernel<<<grid, 512, 0, stream>>>(reinterpret_cast<const int4*>(tiles), n_tiles, gkind, A_src, lda, a_rows,
-                                            a_gather, order, (int)TK, (int)topk, wcat_sel, wcat_sh, (int)Kd, scale_sel,
-                                            scale_sh, ext);
+  SMEL_REQUIRE(max_tiles <= XLT, SMEL_EUNSUPPORTED, "lora_ext: at most %d tiles per call (got %lld)", XLT,
+               (long long)max_tiles);
+  if (max_tiles == 0 || (!wcat_sel && !wcat_sh)) return 0;
+  lora_ext_kernel<<<smel::cu_count(), 512, 0, stream>>>(reinterpret_cast<const int4*>(tiles), n_tiles, gkind, A_src,
+                                                        lda, a_rows, a_gather, order, (int)TK, (int)topk, wcat_sel,
+                                                        wcat_sh, (int)Kd, scale_sel, scale_sh, ext, (int)max_tiles);
   return smel::launch_status();
 }
 
