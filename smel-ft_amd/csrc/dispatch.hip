@@ -76,9 +76,16 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   __shared__ int hs[HCH];
   const int tid = threadIdx.x;
   if (tid == 0) bad_s = 0;
+  // the bad-id flags and the group kinds are needed only at the end: their loads go out with the first histogram
+  // chunk's
+  int badv = 0;
+  for (int b = tid; b < nb; b += DB) badv |= bad[b];
+  const int G = E + (shared_rows > 0 ? 1 : 0);   // groups: the experts, then the shared expert
+  const int gkv = (gkind && tid < G) ? gkind[tid] : 0;
   // the histograms go through LDS in chunks of whole blocks, loaded by all threads at once (one memory latency per
-  // chunk instead of one per block and expert column)
+  // chunk instead of one per block and expert column); with a single chunk the second pass reuses it
   const int ch = HCH / E;   // blocks per chunk
+  const bool one = nb <= ch;
   int total = 0;
   for (int b0 = 0; b0 < nb; b0 += ch) {
     const int n = min(ch, nb - b0) * E;
@@ -98,9 +105,11 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   int run = ex;
   for (int b0 = 0; b0 < nb; b0 += ch) {
     const int n = min(ch, nb - b0) * E;
-    __syncthreads();
-    for (int i = tid; i < n; i += DB) hs[i] = hist[b0 * E + i];
-    __syncthreads();
+    if (!one) {
+      __syncthreads();
+      for (int i = tid; i < n; i += DB) hs[i] = hist[b0 * E + i];
+      __syncthreads();
+    }
     if (tid < E)
       for (int b = 0; b < n / E; ++b) {
         const int c = hs[b * E + tid];
@@ -114,11 +123,9 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
     off_s[E] = total_rows;
     offsets[E] = total_rows;
   }
-  for (int b = tid; b < nb; b += DB)
-    if (bad[b]) bad_s = 1;
+  if (badv) bad_s = 1;
   __syncthreads();
   // tile list over groups 0..E-1 (+ shared group E)
-  const int G = E + (shared_rows > 0 ? 1 : 0);
   int nt = 0, rows = 0, row0 = 0;
   if (tid < G) {
     rows = tid < E ? off_s[tid + 1] - off_s[tid] : shared_rows;
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
       tl.x = tid;
       tl.y = row0 + i * m_tile;
       tl.z = min(row0 + rows, row0 + (i + 1) * m_tile);
-      tl.w = gkind ? gkind[tid] : 0;
+      tl.w = gkv;
       reinterpret_cast<int4*>(tiles)[tbase + i] = tl;
     }
   }
