@@ -19,6 +19,7 @@ shared expert in fp32 before the single rounding; gradients are accumulated in f
 from __future__ import annotations
 
 import ctypes
+import os
 from collections import OrderedDict
 
 import torch
@@ -329,6 +330,9 @@ def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> Packe
 
 
 _SIDE_STREAMS = {}
+# Side streams in use: 0 = router backward, 1 = LoRA factor gradients, 2 = the forward's LoRA layouts.
+# SMEL_SIDE_STREAMS="0,1" (say) keeps only those; a fork that is off runs its launches on the main stream, in order.
+_SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1,2").split(",") if v.strip())
 
 
 def _side_stream(dev, i: int) -> torch.cuda.Stream:
@@ -347,8 +351,9 @@ class _Fork:
 
     def __init__(self, dev, i: int):
         self.main = torch.cuda.current_stream(dev)
-        self.side = _side_stream(dev, i)
-        self.side.wait_stream(self.main)
+        self.side = _side_stream(dev, i) if i in _SIDE_ON else self.main
+        if self.side is not self.main:
+            self.side.wait_stream(self.main)
         self._ctx = torch.cuda.stream(self.side)
 
     def __enter__(self):
@@ -359,7 +364,8 @@ class _Fork:
         return self._ctx.__exit__(*exc)
 
     def join(self):
-        self.main.wait_stream(self.side)
+        if self.side is not self.main:
+            self.main.wait_stream(self.side)
 
 
 class _LoRABufs:
@@ -585,7 +591,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
     dws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
     if prep is None:   # LoRA layouts on a side stream, overlapping the dispatch
-        fork = _Fork(dev, 0)
+        fork = _Fork(dev, 2)
         with fork:
             bufs = _prep_lora(ex, lora_ex, lora_sh, shared is not None, H, dev)
         prep = (fork, bufs)
@@ -820,7 +826,7 @@ class _MoELayerFn(torch.autograd.Function):
         sgate = torch.empty(T, dtype=torch.float32, device=dev) if fuse else None
         sgw = plan["shared"][2] if fuse else None
         lg = torch.empty(T, L.load().smel_route_ld(E, int(fuse)), dtype=torch.bfloat16, device=dev)
-        fork = _Fork(dev, 0)   # LoRA layouts overlap the router and the dispatch
+        fork = _Fork(dev, 2)   # LoRA layouts overlap the router and the dispatch
         with fork:
             bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"], fuse, H, dev)
         L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
