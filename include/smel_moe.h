@@ -142,7 +142,8 @@ int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scal
  * ascending, slot p ascending within one), inv [TK], and the GEMM tile list: tiles [max_tiles][4] = {group, row0,
  * row1, gk} over groups 0..E-1 (+ group E = shared rows [TK, TK+shared_rows) when shared_rows > 0), m_tile rows
  * each, gk = gkind[group] when gkind [E (+1)] is given (the GEMMs then need no gkind argument), else 0; n_tiles [1]
- * = how many are used. err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
+ * = how many are used. Order: the tiles of more than m_tile / 2 rows in group order, then the shorter (last) tiles
+ * in group order. err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
  * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
  * workspace. E <= 512. */
 int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,

@@ -166,19 +166,17 @@ SMEL_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // ------------------------------------------------------------------------------------------------ XCD-aware tiles
 // MI355X has 8 XCDs, each with its own L2; consecutive workgroup ids go to consecutive XCDs. A 1-D grid of
-// xcd_grid(max_tiles) * nblk workgroups is mapped so that XCD x owns a contiguous run of the tile list and runs the
-// nblk column blocks of each tile back to back: the blocks of one tile share its A rows in that XCD's L2, and the
-// tiles of one expert (adjacent in the list) share its weights there.
+// xcd_grid(max_tiles) * nblk workgroups are mapped so that the nblk column blocks of one tile run back to back on one
+// XCD (workgroups go to the XCDs round robin: block b to XCD b % 8): they share the tile's A rows in that XCD's L2.
+// Tiles are taken in list order, tile t on XCD t % 8.
 constexpr int NXCD = 8;
 inline int64_t xcd_grid(int64_t max_tiles) { return (max_tiles + NXCD - 1) / NXCD * NXCD; }
 SMEL_DEV bool xcd_tile(int n_tiles, int nblk, int& tile, int& nb) {
   const int b = blockIdx.x;
   const int x = b % NXCD, j = b / NXCD;
-  const int per = (n_tiles + NXCD - 1) / NXCD;   // tiles per XCD
-  const int t0 = x * per;
-  const int cnt = min(per, n_tiles - t0);
-  if (cnt <= 0 || j >= cnt * nblk) return false;
-  tile = t0 + j / nblk;
+  const int t = (j / nblk) * NXCD + x;
+  if (t >= n_tiles) return false;
+  tile = t;
   nb = j % nblk;
   return true;
 }

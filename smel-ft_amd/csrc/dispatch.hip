@@ -125,23 +125,30 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   }
   if (badv) bad_s = 1;
   __syncthreads();
-  // tile list over groups 0..E-1 (+ shared group E)
-  int nt = 0, rows = 0, row0 = 0;
+  // tile list over groups 0..E-1 (+ shared group E): the tiles of more than m_tile / 2 rows first (in group order),
+  // then the shorter last tiles of the groups (in group order). The grouped GEMMs start tiles in list order, so the
+  // short tiles fill the last round of workgroups instead of holding long ones back.
+  int nt = 0, rows = 0, row0 = 0, nlong = 0;
   if (tid < G) {
     rows = tid < E ? off_s[tid + 1] - off_s[tid] : shared_rows;
     row0 = tid < E ? off_s[tid] : TK;
     nt = (rows + m_tile - 1) / m_tile;
+    nlong = nt - ((nt > 0 && rows - (nt - 1) * m_tile <= m_tile / 2) ? 1 : 0);
   }
-  int total_tiles;
-  const int tbase = block_exclusive_scan(nt, wsum, total_tiles);
+  int n_long, n_short;
+  const int lbase = block_exclusive_scan(nlong, wsum, n_long);
+  const int sbase = block_exclusive_scan(nt - nlong, wsum, n_short);
+  const int total_tiles = n_long + n_short;
   if (tid < G) {
-    for (int i = 0; i < nt && tbase + i < max_tiles; ++i) {
+    for (int i = 0; i < nt; ++i) {
+      const int pos = i < nlong ? lbase + i : n_long + sbase;   // only a group's last tile can be short
+      if (pos >= max_tiles) continue;
       int4 tl;
       tl.x = tid;
       tl.y = row0 + i * m_tile;
       tl.z = min(row0 + rows, row0 + (i + 1) * m_tile);
       tl.w = gkv;
-      reinterpret_cast<int4*>(tiles)[tbase + i] = tl;
+      reinterpret_cast<int4*>(tiles)[pos] = tl;
     }
   }
   if (tid == 0) {

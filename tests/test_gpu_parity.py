@@ -368,12 +368,15 @@ def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128, gkind=None):
 
 
 def _expected_tiles(offsets, E, TK, shared_rows, m_tile):
+    """m_tile-row tiles of every group; those of more than m_tile / 2 rows first, then the short ones, each part in
+    group order."""
     out = []
     for g in range(E + (1 if shared_rows else 0)):
         r0 = offsets[g] if g < E else TK
         n = (offsets[g + 1] - offsets[g]) if g < E else shared_rows
         for i in range(0, n, m_tile):
             out.append((g, r0 + i, r0 + min(n, i + m_tile), 0))
+    out = [t for t in out if t[2] - t[1] > m_tile // 2] + [t for t in out if t[2] - t[1] <= m_tile // 2]
     return np.array(out, dtype=np.int32).reshape(-1, 4)
 
 
