@@ -194,8 +194,10 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
   }
 }
 
-// LoRA factor gradients, all four products of a backward in one launch. Block = (job, LoRA group i, 128-column
-// block): out[p][q] = sum over ALL rows of group i of alpha(row) L[row][p] Rm[src(row)][q], p < 32, as an MFMA GEMM
+// LoRA factor gradients, all four products of a backward in one launch. Item = (128-column block of a job, 512-row
+// chunk slot of a LoRA group); persistent blocks (at most two per CU) take the items that are in use, counted on the
+// device from the group offsets. out[p][q] = sum over ALL rows of group i of alpha(row) L[row][p] Rm[src(row)][q],
+// p < 32, as an MFMA GEMM
 // with the row index as the contraction dim: per 64-row step, L and Rm are staged transposed in LDS (k-pair packing:
 // the values of rows 2j and 2j+1 share one 32-bit word), then each wave multiplies the 32 x 64 L^T tile by its 64 x 32
 // slice of the Rm tile. The LDS tiles are double-buffered and the raw rows of step j+1 are loaded into registers
@@ -210,8 +212,8 @@ constexpr int WG_WIN = WG_CH; // rows per index window
 
 struct WgArgs {
   smel_wg_job job[4];
-  int item0[5];                // first block of each job
   int qb0[4];                  // first 128-column block of each job in the partial-tile space
+  int nqb;                     // 128-column blocks of all jobs
   int tot;                     // partial-tile slots per column block
   float* ws;                   // partial tiles [sum of column blocks][tot][32 * 128]
   const int32_t* groups;
@@ -272,159 +274,163 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
   __shared__ uint32_t TOFF[WG_WIN];
   __shared__ float TAL[WG_WIN];
   __shared__ int G0[WG_MAXG], GN[WG_MAXG], GC[WG_MAXG + 1];
-  int jb = 0;
-#pragma unroll
-  for (int j = 1; j < 4; ++j)
-    if ((int)blockIdx.x >= a.item0[j]) jb = j;
-  const smel_wg_job& J = a.job[jb];
-  const int item = blockIdx.x - a.item0[jb];
-  const int sl = item % a.tot, qb = item / a.tot;   // chunk slot, column block
   // the groups' rows, loaded in parallel (one memory latency), and their chunk slots: group i owns slots
   // [GC[i], GC[i+1]), one per 512-row chunk (at least one)
   const int ng = wg_table(a, G0, GN, GC);
-  if (sl >= GC[ng]) return;
-  int i = 0;
-  while (GC[i + 1] <= sl) ++i;
-  const int c = sl - GC[i];
-  const int nch = GC[i + 1] - GC[i];
-  const int g0 = G0[i], g1 = G0[i] + GN[i];
-  // this block: rows [a0, a1) = chunk c of the group
-  const int a0 = g0 + c * WG_CH;
-  const int a1 = min(g1, a0 + WG_CH);
-  const int q0 = qb * WG_QB;
-  const int Q = (int)J.Q;
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
-  const int kp = tid & 31, grp = tid >> 5;   // k pair, and 4 p's (L) / 16 q's (Rm) per thread
-  const int qq = q0 + 16 * grp;
-  const bool qok = qq < Q;
-  const rsrc_t rr = make_rsrc(J.Rm, (uint64_t)J.r_rows * J.ldr * 2);
-  const int64_t ldr = J.ldr;
-  const int r_gather = J.r_gather, use_w = J.use_w;
-  const uint16_t* __restrict__ Lp = J.L;
-  f32x16_t acc = f32x16_t{};
-  // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights;
-  // WG_PF steps are in flight (a register ring rotated by unrolling): a long group (the shared MLP's T rows) is bound
-  // by the load latency, not by its few MFMAs.
-  struct Raw {
-    uint2 lv0, lv1;
-    u32x4_t x0[2], x1[2];
-    float al0, al1;
-  };
-  Raw rw[WG_PF];
-  // per window of WG_WIN rows: source-row byte offset and row weight of every row, built once into LDS so that the
-  // prefetched loads depend on LDS reads only (a load whose address came from a global load would make the wait for
-  // it drain every load in flight, vmcnt retiring in order)
-  auto build = [&](int w0, int w1) {
-    for (int row = w0 + tid; row < w1; row += 256) {
-      int src = row;
-      float alpha = 1.f;
-      if (row < a.TK) {
-        const int p = a.order[row];
-        if (r_gather) src = p / a.topk;
-        if (use_w) alpha = bf2f(a.topv[p]);
-      } else {
-        if (r_gather) src = row - a.TK;
-        if (use_w) alpha = a.sgate[row - a.TK];
+  const int used = GC[ng];
+  // persistent: items (column block of all jobs, chunk slot), the slots in use only
+  for (int it = blockIdx.x; it < a.nqb * used; it += gridDim.x) {   // uniform
+    const int qbg = it / used, sl = it - qbg * used;
+    int jb = 0;
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (qbg >= a.qb0[j]) jb = j;
+    const smel_wg_job& J = a.job[jb];
+    const int qb = qbg - a.qb0[jb];
+    int i = 0;
+    while (GC[i + 1] <= sl) ++i;
+    const int c = sl - GC[i];
+    const int nch = GC[i + 1] - GC[i];
+    const int g0 = G0[i], g1 = G0[i] + GN[i];
+    // this block: rows [a0, a1) = chunk c of the group
+    const int a0 = g0 + c * WG_CH;
+    const int a1 = min(g1, a0 + WG_CH);
+    const int q0 = qb * WG_QB;
+    const int Q = (int)J.Q;
+    const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
+    const int kp = tid & 31, grp = tid >> 5;   // k pair, and 4 p's (L) / 16 q's (Rm) per thread
+    const int qq = q0 + 16 * grp;
+    const bool qok = qq < Q;
+    const rsrc_t rr = make_rsrc(J.Rm, (uint64_t)J.r_rows * J.ldr * 2);
+    const int64_t ldr = J.ldr;
+    const int r_gather = J.r_gather, use_w = J.use_w;
+    const uint16_t* __restrict__ Lp = J.L;
+    f32x16_t acc = f32x16_t{};
+    // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights;
+    // WG_PF steps are in flight (a register ring rotated by unrolling): a long group (the shared MLP's T rows) is bound
+    // by the load latency, not by its few MFMAs.
+    struct Raw {
+      uint2 lv0, lv1;
+      u32x4_t x0[2], x1[2];
+      float al0, al1;
+    };
+    Raw rw[WG_PF];
+    // per window of WG_WIN rows: source-row byte offset and row weight of every row, built once into LDS so that the
+    // prefetched loads depend on LDS reads only (a load whose address came from a global load would make the wait for
+    // it drain every load in flight, vmcnt retiring in order)
+    auto build = [&](int w0, int w1) {
+      for (int row = w0 + tid; row < w1; row += 256) {
+        int src = row;
+        float alpha = 1.f;
+        if (row < a.TK) {
+          const int p = a.order[row];
+          if (r_gather) src = p / a.topk;
+          if (use_w) alpha = bf2f(a.topv[p]);
+        } else {
+          if (r_gather) src = row - a.TK;
+          if (use_w) alpha = a.sgate[row - a.TK];
+        }
+        TOFF[row - w0] = (uint32_t)src * (uint32_t)ldr * 2;
+        TAL[row - w0] = alpha;
       }
-      TOFF[row - w0] = (uint32_t)src * (uint32_t)ldr * 2;
-      TAL[row - w0] = alpha;
-    }
-  };
-  const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * 64);   // L rows [0, a1): a row past the group reads zeros
-  // branch-free: rows past the window get an out-of-range offset (zeros) and weight 0
-  auto load = [&](int k0, int w0, int w1, Raw& R) {
-    const int ra = k0 + 2 * kp;
-    const bool v0 = ra < w1, v1 = ra + 1 < w1;
-    const int t0 = v0 ? ra - w0 : 0, t1 = v1 ? ra + 1 - w0 : 0;
-    const uint32_t o0 = v0 ? TOFF[t0] : OOB, o1 = v1 ? TOFF[t1] : OOB;
-    R.al0 = v0 ? TAL[t0] : 0.f;
-    R.al1 = v1 ? TAL[t1] : 0.f;
-    const u32x2_t l0 = ld8(rl, v0 ? (uint32_t)ra * 64 + 8 * grp : OOB);
-    const u32x2_t l1 = ld8(rl, v1 ? (uint32_t)(ra + 1) * 64 + 8 * grp : OOB);
-    R.lv0 = make_uint2(l0.x, l0.y);
-    R.lv1 = make_uint2(l1.x, l1.y);
+    };
+    const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * 64);   // L rows [0, a1): a row past the group reads zeros
+    // branch-free: rows past the window get an out-of-range offset (zeros) and weight 0
+    auto load = [&](int k0, int w0, int w1, Raw& R) {
+      const int ra = k0 + 2 * kp;
+      const bool v0 = ra < w1, v1 = ra + 1 < w1;
+      const int t0 = v0 ? ra - w0 : 0, t1 = v1 ? ra + 1 - w0 : 0;
+      const uint32_t o0 = v0 ? TOFF[t0] : OOB, o1 = v1 ? TOFF[t1] : OOB;
+      R.al0 = v0 ? TAL[t0] : 0.f;
+      R.al1 = v1 ? TAL[t1] : 0.f;
+      const u32x2_t l0 = ld8(rl, v0 ? (uint32_t)ra * 64 + 8 * grp : OOB);
+      const u32x2_t l1 = ld8(rl, v1 ? (uint32_t)(ra + 1) * 64 + 8 * grp : OOB);
+      R.lv0 = make_uint2(l0.x, l0.y);
+      R.lv1 = make_uint2(l1.x, l1.y);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      R.x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
-      R.x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
-    }
-  };
-  auto stage = [&](int buf, const Raw& R) {
-    // L^T: alpha folded in (fp32, one bf16 rounding)
-    uint32_t* d = reinterpret_cast<uint32_t*>(LT[buf] + (4 * grp) * WG_S + 2 * kp);
-    d[0 * (WG_S / 2)] = pack2bf(R.al0 * bf_lo(R.lv0.x), R.al1 * bf_lo(R.lv1.x));
-    d[1 * (WG_S / 2)] = pack2bf(R.al0 * bf_hi(R.lv0.x), R.al1 * bf_hi(R.lv1.x));
-    d[2 * (WG_S / 2)] = pack2bf(R.al0 * bf_lo(R.lv0.y), R.al1 * bf_lo(R.lv1.y));
-    d[3 * (WG_S / 2)] = pack2bf(R.al0 * bf_hi(R.lv0.y), R.al1 * bf_hi(R.lv1.y));
-    uint32_t* e = reinterpret_cast<uint32_t*>(RT[buf] + (16 * grp) * WG_S + 2 * kp);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        e[(8 * h + 2 * j) * (WG_S / 2)] = __builtin_amdgcn_perm(R.x1[h][j], R.x0[h][j], 0x05040100u);
-        e[(8 * h + 2 * j + 1) * (WG_S / 2)] = __builtin_amdgcn_perm(R.x1[h][j], R.x0[h][j], 0x07060302u);
+      for (int h = 0; h < 2; ++h) {
+        R.x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+        R.x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
       }
-  };
-  for (int w0 = a0; w0 < a1; w0 += WG_WIN) {   // uniform
-    const int w1 = min(a1, w0 + WG_WIN);
-    __syncthreads();   // the previous window's table and tiles are no longer read
-    build(w0, w1);
-    __syncthreads();
+    };
+    auto stage = [&](int buf, const Raw& R) {
+      // L^T: alpha folded in (fp32, one bf16 rounding)
+      uint32_t* d = reinterpret_cast<uint32_t*>(LT[buf] + (4 * grp) * WG_S + 2 * kp);
+      d[0 * (WG_S / 2)] = pack2bf(R.al0 * bf_lo(R.lv0.x), R.al1 * bf_lo(R.lv1.x));
+      d[1 * (WG_S / 2)] = pack2bf(R.al0 * bf_hi(R.lv0.x), R.al1 * bf_hi(R.lv1.x));
+      d[2 * (WG_S / 2)] = pack2bf(R.al0 * bf_lo(R.lv0.y), R.al1 * bf_lo(R.lv1.y));
+      d[3 * (WG_S / 2)] = pack2bf(R.al0 * bf_hi(R.lv0.y), R.al1 * bf_hi(R.lv1.y));
+      uint32_t* e = reinterpret_cast<uint32_t*>(RT[buf] + (16 * grp) * WG_S + 2 * kp);
 #pragma unroll
-    for (int u = 0; u < WG_PF; ++u) load(w0 + 64 * u, w0, w1, rw[u]);
-    for (int k0 = w0; k0 < w1; k0 += 64 * WG_PF) {
-      // WG_PF steps per round, branch-free (a step past the window stages zeros and adds nothing), so the compiler's
-      // wait for a ring slot counts exactly the loads issued after it
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int u = 0; u < WG_PF; ++u) {
-        const int kk = k0 + 64 * u;
-        const int buf = u & 1;
-        stage(buf, rw[u]);
-        load(kk + 64 * WG_PF, w0, w1, rw[u]);   // past the window: out-of-range loads, zeros
-        __syncthreads();
+        for (int j = 0; j < 4; ++j) {
+          e[(8 * h + 2 * j) * (WG_S / 2)] = __builtin_amdgcn_perm(R.x1[h][j], R.x0[h][j], 0x05040100u);
+          e[(8 * h + 2 * j + 1) * (WG_S / 2)] = __builtin_amdgcn_perm(R.x1[h][j], R.x0[h][j], 0x07060302u);
+        }
+    };
+    for (int w0 = a0; w0 < a1; w0 += WG_WIN) {   // uniform
+      const int w1 = min(a1, w0 + WG_WIN);
+      __syncthreads();   // the previous window's table and tiles are no longer read
+      build(w0, w1);
+      __syncthreads();
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT[buf] + r32 * WG_S + 32 * hi + 8 * s);
-          const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT[buf] + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
-          acc = mfma32(af, bfr, acc);
+      for (int u = 0; u < WG_PF; ++u) load(w0 + 64 * u, w0, w1, rw[u]);
+      for (int k0 = w0; k0 < w1; k0 += 64 * WG_PF) {
+        // WG_PF steps per round, branch-free (a step past the window stages zeros and adds nothing), so the compiler's
+        // wait for a ring slot counts exactly the loads issued after it
+#pragma unroll
+        for (int u = 0; u < WG_PF; ++u) {
+          const int kk = k0 + 64 * u;
+          const int buf = u & 1;
+          stage(buf, rw[u]);
+          load(kk + 64 * WG_PF, w0, w1, rw[u]);   // past the window: out-of-range loads, zeros
+          __syncthreads();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT[buf] + r32 * WG_S + 32 * hi + 8 * s);
+            const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT[buf] + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
+            acc = mfma32(af, bfr, acc);
+          }
         }
       }
     }
-  }
-  if (nch == 1) {
-    wg_store(J, a.n_sel, i, q0, w, l, acc);
-    return;
-  }
-  // a group of several chunks: this chunk's partial tile, summed in chunk order by lora_wgrad_reduce
-  float* tile = a.ws + ((int64_t)(a.qb0[jb] + qb) * a.tot + sl) * (32 * WG_QB);
+    if (nch == 1) {
+      wg_store(J, a.n_sel, i, q0, w, l, acc);
+    } else {
+      // a group of several chunks: this chunk's partial tile, summed in chunk order by lora_wgrad_reduce
+      float* tile = a.ws + ((int64_t)(a.qb0[jb] + qb) * a.tot + sl) * (32 * WG_QB);
 #pragma unroll
-  for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = acc[r];
+      for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = acc[r];
+    }
+  }
 }
 
-// The multi-chunk groups: sum the partial tiles in chunk order, store like lora_wgrad_kernel. Block = (job, column
-// block, group).
+// The multi-chunk groups: sum the partial tiles in chunk order, store like lora_wgrad_kernel. Block = one column block
+// of all jobs; it takes every group of more than one chunk.
 __global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
   __shared__ int G0[WG_MAXG], GN[WG_MAXG], GC[WG_MAXG + 1];
+  const int qbg = blockIdx.x;
   int jb = 0;
 #pragma unroll
   for (int j = 1; j < 4; ++j)
-    if ((int)blockIdx.x >= a.qb0[j] * a.n_lora) jb = j;
+    if (qbg >= a.qb0[j]) jb = j;
   const smel_wg_job& J = a.job[jb];
-  const int item = blockIdx.x - a.qb0[jb] * a.n_lora;
-  const int qb = item / a.n_lora, i = item - qb * a.n_lora;
+  const int qb = qbg - a.qb0[jb];
   const int ng = wg_table(a, G0, GN, GC);
-  if (i >= ng) return;
-  const int nch = GC[i + 1] - GC[i];
-  if (nch <= 1) return;
   const int tid = threadIdx.x;
-  const float* tile = a.ws + ((int64_t)(a.qb0[jb] + qb) * a.tot + GC[i]) * (32 * WG_QB);
-  f32x16_t acc;
+  for (int i = 0; i < ng; ++i) {   // uniform
+    const int nch = GC[i + 1] - GC[i];
+    if (nch <= 1) continue;
+    const float* tile = a.ws + ((int64_t)qbg * a.tot + GC[i]) * (32 * WG_QB);
+    f32x16_t acc;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = tile[r * 256 + tid];
-  for (int cc = 1; cc < nch; ++cc)
+    for (int r = 0; r < 16; ++r) acc[r] = tile[r * 256 + tid];
+    for (int cc = 1; cc < nch; ++cc)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] += tile[(int64_t)cc * (32 * WG_QB) + r * 256 + tid];
-  wg_store(J, a.n_sel, i, qb * WG_QB, tid >> 6, lane_id(), acc);
+      for (int r = 0; r < 16; ++r) acc[r] += tile[(int64_t)cc * (32 * WG_QB) + r * 256 + tid];
+    wg_store(J, a.n_sel, i, qb * WG_QB, tid >> 6, lane_id(), acc);
+  }
 }
 
 }  // namespace
@@ -496,9 +502,8 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   WgArgs a;
   a.tot = (int)wg_tot(n_lora, max_rows);
   a.ws = ws;
-  int items = 0, qbs = 0;
+  int qbs = 0;
   for (int j = 0; j < 4; ++j) {
-    a.item0[j] = items;
     a.qb0[j] = qbs;
     if (j < n_jobs) {
       const smel_wg_job& J = jobs[j];
@@ -516,15 +521,13 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
                        SMEL_EINVAL, "lora_wgrad: job %d: destination [%d][%d] outside the 32 x Q result", j, c, h);
         }
       a.job[j] = J;
-      const int nqb = (int)((J.Q + WG_QB - 1) / WG_QB);
-      items += nqb * a.tot;
-      qbs += nqb;
+      qbs += (int)((J.Q + WG_QB - 1) / WG_QB);
     } else {
       a.job[j] = smel_wg_job{};
       a.job[j].Q = WG_QB;
     }
   }
-  a.item0[4] = items;
+  a.nqb = qbs;
   a.groups = lora_groups;
   a.n_lora = (int)n_lora;
   a.n_sel = (int)n_sel;
@@ -536,9 +539,11 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   a.order = order;
   a.topv = topv;
   a.sgate = sgate;
-  lora_wgrad_kernel<<<(unsigned)items, 256, 0, stream>>>(a);
+  // persistent blocks over the (column block, chunk slot) items in use: at most two per CU
+  const int64_t bound = (int64_t)qbs * a.tot;
+  lora_wgrad_kernel<<<(unsigned)std::min<int64_t>(bound, 2 * smel::cu_count()), 256, 0, stream>>>(a);
   int st = smel::launch_status();
   if (st) return st;
-  lora_wgrad_reduce<<<(unsigned)(qbs * n_lora), 256, 0, stream>>>(a);
+  lora_wgrad_reduce<<<(unsigned)qbs, 256, 0, stream>>>(a);
   return smel::launch_status();
 }
