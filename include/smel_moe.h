@@ -86,9 +86,10 @@ int smel_pack_bf16(const uint16_t* w, int64_t rows, int64_t K, int64_t ld, uint1
  * with p = a pair of 32 columns, ks = a 64-row step, lane l = 16 kq + i, substep s, 16-column fragment fr:
  *   SMEL_PACK_Q4   block (mat, p, ks) 1 KB:  lane chunk word 2 fr + s = the 8 nibbles (low first) of column
  *                                             32 p + 16 fr + i at rows 64 ks + 32 s + 8 kq + [0, 8)
- *   SMEL_PACK_SZ   block (mat, g, ks) 512 B: fp32 pair 16 kq + 8 s + t = (scale, zero') of row 64 ks + 32 s + 8 kq + t
- *                                             in column group g (C / group groups); zero' = fp32(zero - 1024 scale)
- *                                             when packed with fast = 1, else zero
+ *   SMEL_PACK_SZ   block (mat, g, ks) 512 B: fp32 pair 16 kq + 8 s + t = (scale, zero) of row 64 ks + 32 s + 8 kq + t
+ *                                             in column group g (C / group groups); packed with fast = 1 the pair
+ *                                             is (scale, zero - 1024 scale) for even t and (scale / 16,
+ *                                             zero - 64 scale) for odd t, each an exact fp32 value
  *   SMEL_PACK_BF16 block (mat, p, ks, 2 fr + s) 1 KB: lane chunk = the 8 bf16 of that column at those rows
  * Rows >= R are zero. smel_packed_t_bytes gives the size of each (-1 for a bad argument). */
 int64_t smel_packed_t_bytes(int32_t what, int64_t n_mats, int64_t R, int64_t C, int64_t group);

@@ -162,7 +162,14 @@ __global__ __launch_bounds__(256) void pack_sz_t(const uint16_t* __restrict__ s,
     if (k < R) {
       const int64_t gi = (e * R + k) * G + g;
       const float sc = bf2f(s[gi]), ze = bf2f(z[gi]);
-      v = make_float2(sc, fast ? fmaf(-1024.f, sc, ze) : ze);
+      // fast: the backward reads rows t = 0, 2, 4, 6 of a word as fp16 1024 + q and rows 1, 3, 5, 7 as 1024 + 16 q
+      // (a nibble in bits 4..7 needs no shift): (s, z - 1024 s), resp. (s / 16, z - 64 s)
+      if (!fast)
+        v = make_float2(sc, ze);
+      else if (t & 1)
+        v = make_float2(sc * 0.0625f, fmaf(-64.f, sc, ze));
+      else
+        v = make_float2(sc, fmaf(-1024.f, sc, ze));
     }
     out[i] = v;
   }

@@ -72,20 +72,6 @@ SMEL_DEV void dq8r(uint32_t b, const float* sc, const float* ze, uint32_t out[4]
   out[2] = pack2bf(fmaf(ub2(lo), sc[4], ze[4]), fmaf(ub2(hi), sc[5], ze[5]));
   out[3] = pack2bf(fmaf(ub3(lo), sc[6], ze[6]), fmaf(ub3(hi), sc[7], ze[7]));
 }
-// The same for a fast bank (ze[t] = zero - 1024 scale, see dq8f): (b >> 4j) & 0x000F000F holds rows j and j + 4 as
-// fp16 1024 + q; 19 VALU ops for 8 weights instead of 23.
-SMEL_DEV void dq8rf(uint32_t b, const float* sc, const float* ze, uint32_t magic, uint32_t out[4]) {
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t x = ((b >> (4 * j)) & 0x000F000Fu) | magic;
-    r[j] = fmaf(h_lo(x), sc[j], ze[j]);
-    r[j + 4] = fmaf(h_hi(x), sc[j + 4], ze[j + 4]);
-  }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) out[t] = pack2bf(r[2 * t], r[2 * t + 1]);
-}
-
 // 4-byte-per-lane LDS-DMA: lane i writes bytes [4 i, 4 i + 4) after the wave-uniform LDS address.
 SMEL_DEV void ld4_lds(rsrc_t r, const void* lds, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)(lds), 4, off, 0, 0, 0);
@@ -222,12 +208,15 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
         }
       };
       // half h of column fragment f's dequant in substep s. Fast bank: B words h and h + 2 (rows 2h, 2h+1 and
-      // 2h+4, 2h+5, the same arithmetic as dq8rf); exact path: the whole fragment with h = 0.
+      // 2h+4, 2h+5): byte h of each half-word holds rows 2h (+4) in its low nibble, read as fp16 1024 + q with the
+      // pair (s, z - 1024 s), and rows 2h+1 (+5) in its high nibble, read in place as fp16 1024 + 16 q with the pair
+      // (s / 16, z - 64 s): 17 VALU per 8 weights. Exact path: the whole fragment with h = 0.
       auto dqh = [&](int s, int f, int h) {
         const uint32_t qw = (f < 2 ? q0 : q1)[2 * (f & 1) + s];
         if constexpr (FAST) {
-          const uint32_t x0 = ((qw >> (8 * h)) & 0x000F000Fu) | magic;
-          const uint32_t x1 = ((qw >> (8 * h + 4)) & 0x000F000Fu) | magic;
+          const uint32_t qb = h ? qw >> 8 : qw;
+          const uint32_t x0 = (qb & 0x000F000Fu) | magic;
+          const uint32_t x1 = (qb & 0x00F000F0u) | magic;
           const int j = 2 * h;
           b[f][h] = pack2bf(fmaf(h_lo(x0), sc[j], ze[j]), fmaf(h_lo(x1), sc[j + 1], ze[j + 1]));
           b[f][h + 2] = pack2bf(fmaf(h_hi(x0), sc[j + 4], ze[j + 4]), fmaf(h_hi(x1), sc[j + 5], ze[j + 5]));

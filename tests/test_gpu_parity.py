@@ -171,17 +171,23 @@ def test_pack_int4_t_roundtrip(E, R, C, group, fast):
         assert not got[~ok].any()
     s32 = sc.numpy().view(np.uint16).astype(np.uint32) << 16
     z32 = ze.numpy().view(np.uint16).astype(np.uint32) << 16
-    if fast:   # zero' = fp32(zero - 1024 scale), exact in double for these magnitudes, rounded once
-        zf = z32.view(np.float32).astype(np.float64) - 1024.0 * s32.view(np.float32).astype(np.float64)
-        z32 = zf.astype(np.float32).view(np.uint32)
     pw = szt.cpu().numpy().view(np.uint32).reshape(E, C // group, nks, 4, 2, 8, 2)    # [e][g][ks][kq][s][t][pair]
     ks, kq, ss, t = np.meshgrid(np.arange(nks), np.arange(4), np.arange(2), np.arange(8), indexing="ij")
     r = 64 * ks + 32 * ss + 8 * kq + t
     rc = np.minimum(r, R - 1)
     for e in range(E):
         for g in range(C // group):
-            assert np.array_equal(pw[e, g, ..., 0], np.where(r < R, s32[e][rc, g], 0).astype(np.uint32))
-            assert np.array_equal(pw[e, g, ..., 1], np.where(r < R, z32[e][rc, g], 0).astype(np.uint32))
+            if fast:   # even rows (s, z - 1024 s), odd rows (s / 16, z - 64 s): exact in double, rounded once
+                sv = s32[e][rc, g].view(np.float32).astype(np.float64)
+                zv = z32[e][rc, g].view(np.float32).astype(np.float64)
+                sv, zv = np.where(t % 2 == 1, sv / 16.0, sv), np.where(t % 2 == 1, zv - 64.0 * sv, zv - 1024.0 * sv)
+                sb, zb = sv.astype(np.float32).view(np.uint32), zv.astype(np.float32).view(np.uint32)
+            else:      # bit copies (any pattern, NaN payloads included)
+                sb, zb = s32[e][rc, g], z32[e][rc, g]
+            want_s = np.where(r < R, sb, 0).astype(np.uint32)
+            want_z = np.where(r < R, zb, 0).astype(np.uint32)
+            assert np.array_equal(pw[e, g, ..., 0], want_s)
+            assert np.array_equal(pw[e, g, ..., 1], want_z)
 
 
 def test_int4_fast_ok():
