@@ -114,15 +114,18 @@ SMEL_DEV void dq8f(uint32_t b, const FastSZ& p, uint32_t magic, uint32_t out[4])
 
 // ------------------------------------------------------------------------------------------------ activations
 // act ids: 0 = silu, 1 = gelu_tanh (smel/moe.py:91-107)
+// e^x as one v_exp_f32 (2^x; results below the normal range flush to 0, which cannot change 1 + e^x)
+SMEL_DEV float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+// SiLU as g * sigmoid(g), the sigmoid by v_rcp_f32 (1 ulp): the results are rounded to bf16 next
 SMEL_DEV float act_f(float g, int act) {
-  if (act == 0) return g / (1.0f + __expf(-g));
+  if (act == 0) return g * __builtin_amdgcn_rcpf(1.0f + exp_fast(-g));
   const float c = 0.7978845608028654f;
   const float t = tanhf(c * (g + 0.044715f * g * g * g));
   return 0.5f * g * (1.0f + t);
 }
 SMEL_DEV void act_and_grad_f(float g, int act, float& a, float& da) {
-  if (act == 0) {
-    const float s = 1.0f / (1.0f + __expf(-g));
+  if (act == 0) {   // the same sigmoid as act_f
+    const float s = __builtin_amdgcn_rcpf(1.0f + exp_fast(-g));
     a = g * s;
     da = s * (1.0f + g * (1.0f - s));
     return;

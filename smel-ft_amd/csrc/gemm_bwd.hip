@@ -19,6 +19,7 @@
 //    step ahead (8 loads), A 3 steps ahead;
 //  * vmcnt retires in issue order: each step issues its weight loads before its LDS-DMAs and waits for exactly the
 //    loads of the step it is about to use.
+
 #include "abi_util.h"
 #include "common.h"
 
@@ -47,6 +48,7 @@ struct BwdArgs {
   const int32_t* order;
   const uint16_t* ext;
   const uint16_t* hsave;
+  const uint16_t* actsave;   // the forward's bf16 act(g) u rows (epilogue 1)
   const uint16_t* topv;
   const float* sgate;
   uint16_t* out;
@@ -409,59 +411,63 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   const int I = N;
   const bool cv = col0 < I;
   const float* const wmap = reinterpret_cast<const float*>(rowmap);
-  // 32 threads per row, 8 rows per pass; the saved (g, u) of 8 passes are loaded before any of them is used, so the
-  // stores of one batch never wait for the loads of the next row
+  // 32 threads per row, 8 rows per pass; the saved (g, u) and act(g) u of PB passes are loaded before any of them is
+  // used, so the stores of one batch never wait for the loads of the next row.
   constexpr int PB = 8;
-  for (int rb = tid >> 5; rb < nrows; rb += 8 * PB) {
-    u32x4_t g2s[PB], u2s[PB];
+  const int act = a.act;
+  {
+    for (int rb = tid >> 5; rb < nrows; rb += 8 * PB) {
+      u32x4_t g2s[PB], u2s[PB], a2s[PB];
 #pragma unroll
-    for (int p = 0; p < PB; ++p) {
-      const int64_t grow = row0 + rb + 8 * p;
-      g2s[p] = u2s[p] = u32x4_t{};
-      if (cv && rb + 8 * p < nrows) {
-        g2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + col0);
-        u2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + I + col0);
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < PB; ++p) {
-      const int row = rb + 8 * p;
-      if (row >= nrows) break;   // uniform over the row's 32 threads
-      const int lr = row & 31;
-      const u32x4_t av = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
-      const int grow = row0 + row;
-      const float wrow_ = wmap[row];
-      float part = 0.f;
-      if (cv) {
-        const u32x4_t g2 = g2s[p];
-        const u32x4_t u2 = u2s[p];
-        uint32_t og[4], ou[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float dgv[2], duv[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
-            const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
-            const float acv = h ? bf_hi(av[j]) : bf_lo(av[j]);
-            float avl, dav;
-            act_and_grad_f(g, a.act, avl, dav);
-            const float abf = bf2f(f2bf(act_f(g, a.act) * u));   // the forward's rounded activation
-            part += acv * abf;
-            const float da = wrow_ * acv;
-            dgv[h] = da * u * dav;
-            duv[h] = da * avl;
-          }
-          og[j] = pack2bf(dgv[0], dgv[1]);
-          ou[j] = pack2bf(duv[0], duv[1]);
+      for (int p = 0; p < PB; ++p) {
+        const int64_t grow = row0 + rb + 8 * p;
+        g2s[p] = u2s[p] = a2s[p] = u32x4_t{};
+        if (cv && rb + 8 * p < nrows) {
+          g2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + col0);
+          u2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + I + col0);
+          a2s[p] = *reinterpret_cast<const u32x4_t*>(a.actsave + grow * I + col0);
         }
-        *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + col0) = u32x4_t{og[0], og[1], og[2], og[3]};
-        *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + I + col0) = u32x4_t{ou[0], ou[1], ou[2], ou[3]};
       }
-      // fixed-order sum over the row's 32 threads (lanes 32 h .. 32 h + 31 of a wave)
 #pragma unroll
-      for (int o = 1; o < 32; o <<= 1) part += __shfl_xor(part, o, 64);
-      if (ch == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
+      for (int p = 0; p < PB; ++p) {
+        const int row = rb + 8 * p;
+        if (row >= nrows) break;   // uniform over the row's 32 threads
+        const int lr = row & 31;
+        const u32x4_t av = *reinterpret_cast<const u32x4_t*>(Et(row >> 5) + lr * 256 + 8 * (ch ^ (lr & 7)));
+        const int grow = row0 + row;
+        const float wrow_ = wmap[row];
+        float part = 0.f;
+        if (cv) {
+          const u32x4_t g2 = g2s[p], u2 = u2s[p], a2 = a2s[p];
+          uint32_t og[4], ou[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float dgv[2], duv[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
+              const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
+              const float acv = h ? bf_hi(av[j]) : bf_lo(av[j]);
+              float avl, dav;
+              act_and_grad_f(g, act, avl, dav);
+              const float abf = h ? bf_hi(a2[j]) : bf_lo(a2[j]);   // the forward's rounded activation
+              part += acv * abf;
+              const float da = wrow_ * acv;
+              dgv[h] = da * u * dav;
+              duv[h] = da * avl;
+            }
+            og[j] = pack2bf(dgv[0], dgv[1]);
+            ou[j] = pack2bf(duv[0], duv[1]);
+          }
+          *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + col0) = u32x4_t{og[0], og[1], og[2], og[3]};
+          *reinterpret_cast<u32x4_t*>(a.out + (int64_t)grow * a.ldo + I + col0) =
+              u32x4_t{ou[0], ou[1], ou[2], ou[3]};
+        }
+        // fixed-order sum over the row's 32 threads (lanes 32 h .. 32 h + 31 of a wave)
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) part += __shfl_xor(part, o, 64);
+        if (ch == 0) a.dwp[(int64_t)grow * a.nblk + nb] = part;
+      }
     }
   }
 }
@@ -516,8 +522,8 @@ extern "C" int64_t smel_gmm_bwd_nblocks(int64_t C) { return (C + NB - 1) / NB; }
 extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                             int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
-                            int32_t act, const uint16_t* hsave, const uint16_t* topv, const float* sgate,
-                            uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
+                            int32_t act, const uint16_t* hsave, const uint16_t* actsave, const uint16_t* topv,
+                            const float* sgate, uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
   SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->R && topk > 0, SMEL_EINVAL,
                "gmm_bwd: bad sizes");
@@ -528,10 +534,11 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL,
                "gmm_bwd: an int4 bank needs its transposed scale/zero (smel_pack_int4_t)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_bwd: A rows must be 16-B aligned");
-  SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0, SMEL_EUNSUPPORTED,
-               "gmm_bwd: out / hsave rows must be 16-B aligned");
-  SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
-               "gmm_bwd: epilogue %d needs hsave, dwp and topv", epilogue);
+  SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0 &&
+                   ((uintptr_t)actsave % 16) == 0, SMEL_EUNSUPPORTED,
+               "gmm_bwd: out / hsave / actsave rows must be 16-B aligned");
+  SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && actsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
+               "gmm_bwd: epilogue %d needs hsave, actsave, dwp and topv", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_bwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_bwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: A larger than 2 GiB");
@@ -548,6 +555,7 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   a.order = order;
   a.ext = ext;
   a.hsave = hsave;
+  a.actsave = epilogue == 1 ? actsave : nullptr;
   a.topv = topv;
   a.sgate = sgate;
   a.out = out;

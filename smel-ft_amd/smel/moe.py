@@ -479,7 +479,7 @@ def _router_dx(dl: torch.Tensor, wr: PackedW, T: int, dx: torch.Tensor | None = 
     w.wsh = L.ptr(wr.t)
     w.R, w.C, w.group = wr.R, H, 32
     L.call("smel_gmm_bwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dl), dl.shape[1], T, 0,
-           None, 0, 1, None, 0, 0, None, None, None, L.ptr(dx), H, None, L.stream(), tag="gemm_router_bwd")
+           None, 0, 1, None, 0, 0, None, None, None, None, L.ptr(dx), H, None, L.stream(), tag="gemm_router_bwd")
     return dx
 
 
@@ -674,7 +674,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     dwp = torch.empty(M, nblk, dtype=torch.float32, device=dev)
     w_dn = _wset(ex, "dn", t["sel_dn"], sh_dn, g(lb_ex, "at_dn"), g(lb_sh, "at_dn"), t=True)
     L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
-           L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["topv"]),
+           L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["act"]), L.ptr(t["topv"]),
            L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st, tag="gemm_dn_bwd")
     # (5, side stream 0) router backward (fused layer) or d topv (routed_experts): needs only dwp, so it overlaps
     # steps (3) and (4)
@@ -727,7 +727,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
     dxs = bf(M, H)
     w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True)
     L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
-           L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, L.ptr(dxs), H, None, st,
+           L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, None, L.ptr(dxs), H, None, st,
            tag="gemm_gu_bwd")
     side_r.join()
     dx = bf(T, H)
@@ -948,8 +948,8 @@ class _MLPFn(torch.autograd.Function):
         dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
         wd = _dense_wset(w_dn, g("at_dn"))
         L.call("smel_gmm_bwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
-               None, 0, 1, L.ptr(ext_db), 1, _ACT[ctx.act_name], L.ptr(hsave), None, L.ptr(ones), L.ptr(dh), 2 * Is,
-               L.ptr(dwp), st, tag="gemm_mlp_dn_bwd")
+               None, 0, 1, L.ptr(ext_db), 1, _ACT[ctx.act_name], L.ptr(hsave), L.ptr(actb), None, L.ptr(ones),
+               L.ptr(dh), 2 * Is, L.ptr(dwp), st, tag="gemm_mlp_dn_bwd")
         if lb is not None:
             ext_dxa = bf(T, EXT)
             L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * Is, T, 0, None, 0, 1,
@@ -957,7 +957,8 @@ class _MLPFn(torch.autograd.Function):
         dx = bf(T, H)
         wg = _dense_wset(w_gu, g("at_gu"))
         L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
-               0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, L.ptr(dx), H, None, st, tag="gemm_mlp_gu_bwd")
+               0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H, None, st,
+               tag="gemm_mlp_gu_bwd")
         grads = [None] * 6
         if lb is not None:
             zero = torch.zeros(2, dtype=torch.int32, device=dev)     # offsets of zero experts
@@ -1114,14 +1115,14 @@ class FrozenExpertsFn(torch.autograd.Function):
                0, None, 0, 1, None, 1, _ACT[act_name], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_frozen_gu_fwd")
         L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, rows,
                0, None, 0, 1, None, 0, _ACT[act_name], L.ptr(out), H, None, st, tag="gemm_frozen_dn_fwd")
-        ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, act_name)
+        ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, actb, act_name)
         return out
 
     @staticmethod
     def backward(ctx, dy):
         if ctx.plan is None:
             return torch.zeros_like(dy), None, None, None, None
-        bank, tiles, ntiles, maxt, gk, hsave, act_name = ctx.plan
+        bank, tiles, ntiles, maxt, gk, hsave, actb, act_name = ctx.plan
         ctx.plan = None
         dy = _bf16(dy)
         rows, H = dy.shape
@@ -1134,11 +1135,11 @@ class FrozenExpertsFn(torch.autograd.Function):
         dwp = torch.empty(rows, nblk, dtype=torch.float32, device=dev)
         ones = torch.ones(rows, dtype=torch.float32, device=dev)    # row weight 1 (no combine weight here)
         L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, rows, 0,
-               None, 0, 1, None, 1, _ACT[act_name], L.ptr(hsave), None, L.ptr(ones), L.ptr(dh), 2 * I, L.ptr(dwp),
-               st, tag="gemm_frozen_dn_bwd")
+               None, 0, 1, None, 1, _ACT[act_name], L.ptr(hsave), L.ptr(actb), None, L.ptr(ones), L.ptr(dh), 2 * I,
+               L.ptr(dwp), st, tag="gemm_frozen_dn_bwd")
         dx = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
         L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I,
-               rows, 0, None, 0, 1, None, 0, _ACT[act_name], None, None, None, L.ptr(dx), H, None, st,
+               rows, 0, None, 0, 1, None, 0, _ACT[act_name], None, None, None, None, L.ptr(dx), H, None, st,
                tag="gemm_frozen_gu_bwd")
         return dx, None, None, None, None
 
