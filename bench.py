@@ -12,6 +12,9 @@ Other workloads of BASELINE.json (``--workload``), each printing one JSON line o
       the block's RMSNorms are outside this path and replaced by separate synthetic inputs;
   c5  the Qwen layer under skewed routing: T=32768 as 8 micro-batches of 4096, router biased to a
       Zipf(1.2) expert popularity (realised top-12 gate-mass share reported), the 12 most popular experts selected.
+  norms  the RMSNorm family around the block (include/smel_norm.h), forward + backward at the Qwen3.6 block's
+      shapes for T=4092: input norm and residual add + post-attention norm [T, 2048], q / k head norms
+      [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128].
 
 Every line carries tokens/s of the whole step, the roofline of the dominant kernel (HIP-event timed launches inside
 this run: algorithmic FLOPs and bytes per launch against MI355X's dense bf16 MFMA and HBM peaks, the binding one
@@ -132,7 +135,8 @@ def kernel_work(tag, c, S):
     """(algorithmic FLOPs, algorithmic HBM bytes) of one launch of a kernel, from the layer's shape ``c`` and the
     number S of slots routed to selected experts. Bytes = every operand read once and every result written once:
     frozen int4 experts (q + scale/zero in the layout the kernel reads) except the selected ones, selected / shared bf16 weights, activations
-    (the gathered token rows counted once per token), the LoRA K-extension rows, the saved pre-activations."""
+    (the gathered token rows counted once per token), the LoRA K-extension rows, the saved pre-activations and (down
+    backward) the saved activation."""
     T, H, E, I, K, r = c["T"], c["H"], c["E"], c["I"], c["K"], c["r"]
     g = c["group"]
     n_sel = c.get("n_sel_used", c["n_sel"])
@@ -155,7 +159,7 @@ def kernel_work(tag, c, S):
     w = {"gemm_gu_fwd": (2 * M * H * 2 * I + 2 * Lr * r * 2 * I, gu_w + T * H * 2 + ext + M * I * 2 + M * 2 * I * 2),
          "gemm_dn_fwd": (2 * M * I * H + 2 * Lr * r * H, dn_w + M * I * 2 + ext + M * H * 2),
          "gemm_dn_bwd": (2 * M * H * I + 2 * Lr * r * I,
-                         dn_wt + T * H * 2 + M * 2 * I * 2 + ext + M * 2 * I * 2 + M * nblk * 4),
+                         dn_wt + T * H * 2 + M * 2 * I * 2 + M * I * 2 + ext + M * 2 * I * 2 + M * nblk * 4),
          "gemm_gu_bwd": (2 * M * 2 * I * H + 2 * Lr * 2 * r * H, gu_wt + M * 2 * I * 2 + ext + M * H * 2),
          "gemm_router_bwd": (2 * T * Epad * H, T * Epad * 2 + Epad * H * 2 + T * H * 2),
          "gemm_mlp_gu_fwd": (2 * T * H * 2 * Is + 2 * T * r * 2 * Is,
@@ -433,12 +437,110 @@ def _cpu_model():
     return "unknown"
 
 
+NORM_SHAPES = dict(T=4092, H=2048, NQ=16, NKV=2, HD=256, NV=32, VD=128)
+
+
+def run_norms(args, dev):
+    """One step = forward and backward of every RMSNorm of a Qwen3.6 block (smel/layer_runner.py:174-175, 212,
+    285-290 call them): C-ABI launches on preallocated buffers, each tagged for the per-kernel breakdown."""
+    from smel import _lib
+    c = NORM_SHAPES
+    T, H, HD, VD = c["T"], c["H"], c["HD"], c["VD"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    rn = lambda *sh, s=1.0: (torch.randn(*sh, generator=g, device=dev) * s).to(torch.bfloat16)
+    P = _lib.ptr
+    bufs = {"h": rn(T, H), "a": rn(T, H), "qg": rn(T, c["NQ"], 2 * HD), "k": rn(T, c["NKV"], HD),
+            "o": rn(T * c["NV"], VD), "z": rn(T * c["NV"], VD)}
+    w = {"in": rn(H, s=0.1), "post": rn(H, s=0.1), "q": rn(HD, s=0.1), "k": rn(HD, s=0.1),
+         "g": (1 + 0.1 * torch.randn(VD, generator=g, device=dev)).to(torch.bfloat16)}
+    # (tag, rows, cols, row stride, input, weight) of the plain norms; outputs and gradients preallocated
+    plain = [("in_norm", T, H, H, bufs["h"], w["in"]), ("q_norm", T * c["NQ"], HD, 2 * HD, bufs["qg"], w["q"]),
+             ("k_norm", T * c["NKV"], HD, HD, bufs["k"], w["k"])]
+    out = {tag: (torch.empty(R, C, device=dev, dtype=torch.bfloat16), torch.empty(R, device=dev),
+                 rn(R, C), torch.empty(R, C, device=dev, dtype=torch.bfloat16)) for tag, R, C, _, _, _ in plain}
+    s_, y_, dx_ = (torch.empty(T, H, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    r_add = torch.empty(T, device=dev)
+    dy_add, ds_add = rn(T, H), rn(T, H)
+    Rg = T * c["NV"]
+    yg, dxg, dzg = (torch.empty(Rg, VD, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    r_g, do_g = torch.empty(Rg, device=dev), rn(Rg, VD)
+    EPS = 1e-6
+
+    def step():
+        st = _lib.stream()   # the current stream: a side stream while the step is captured
+        for tag, R, C, ld, x, wt in plain:
+            y, r, dy, dx = out[tag]
+            _lib.call("smel_rmsnorm_fwd", P(x), R, C, ld, P(wt), 2, EPS, 0, P(y), P(r), st, tag=tag + "_fwd")
+        _lib.call("smel_add_rmsnorm_fwd", P(bufs["h"]), P(bufs["a"]), T, H, P(w["post"]), 2, EPS, 0, P(s_), P(y_),
+                  P(r_add), st, tag="add_norm_fwd")
+        _lib.call("smel_gated_rmsnorm_fwd", P(bufs["o"]), P(bufs["z"]), Rg, VD, P(w["g"]), EPS, 0, P(yg), P(r_g),
+                  st, tag="gated_norm_fwd")
+        _lib.call("smel_gated_rmsnorm_bwd", P(do_g), P(bufs["o"]), P(bufs["z"]), Rg, VD, P(w["g"]), P(r_g), 0,
+                  P(dxg), P(dzg), st, tag="gated_norm_bwd")
+        _lib.call("smel_rmsnorm_bwd", P(dy_add), P(s_), T, H, H, P(w["post"]), 2, P(r_add), P(ds_add), 0, P(dx_),
+                  st, tag="add_norm_bwd")
+        for tag, R, C, ld, x, wt in plain:
+            y, r, dy, dx = out[tag]
+            _lib.call("smel_rmsnorm_bwd", P(dy), P(x), R, C, ld, P(wt), 2, P(r), None, 0, P(dx), st,
+                      tag=tag + "_bwd")
+
+    # algorithmic HBM bytes per launch: every operand read once, every result written once (bf16 rows, bf16
+    # weight, fp32 rstd)
+    nbytes = {}
+    for tag, R, C, _, _, _ in plain:
+        nbytes[tag + "_fwd"] = 2 * R * C * 2 + C * 2 + R * 4
+        nbytes[tag + "_bwd"] = 3 * R * C * 2 + C * 2 + R * 4
+    nbytes["add_norm_fwd"] = 4 * T * H * 2 + H * 2 + T * 4
+    nbytes["add_norm_bwd"] = 4 * T * H * 2 + H * 2 + T * 4
+    nbytes["gated_norm_fwd"] = 3 * Rg * VD * 2 + VD * 2 + Rg * 4
+    nbytes["gated_norm_bwd"] = 5 * Rg * VD * 2 + VD * 2 + Rg * 4
+    timing = time_step(step, args.steps, args.warmup, graph=not args.eager)
+    bd = breakdown_of(step, 20)
+    dom = max(bd, key=bd.get)
+    B, t = nbytes[dom], bd[dom] * 1e-3
+    roof = {"kernel": dom, "bound": "hbm", "achieved": round(B / t / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": round(B / t / HBM_PEAK, 4), "traffic": measured_traffic(dom), "bytes_per_launch": B,
+            "avg_launch_ms": bd[dom],
+            "step_bytes": sum(nbytes.values()),
+            "step_frac": round(sum(nbytes.values()) / (timing[1] * 1e-3) / HBM_PEAK, 4)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = norms_cpu_baseline(bufs, w, plain, dict(dy=out, dy_add=dy_add, ds_add=ds_add, do_g=do_g), c)
+    emit("RMSNorm family fwd+bwd tokens/s (Qwen3.6 block norms, T=4092)", T, args, timing, "norms",
+         {"shapes": "in/post norm [T,2048], q norm [T,16,256] of [T,16,512], k norm [T,2,256], gated [T*32,128]"},
+         roof, bd, cpu)
+
+
+def norms_cpu_baseline(bufs, w, plain, grads, c):
+    """The oracle's numpy restatement of the reference's norm kernels (fp32, one thread) on the same step."""
+    from oracle import norm_ref as N
+    f = lambda t: t.detach().float().cpu().numpy()
+    T, H, HD, VD = c["T"], c["H"], c["HD"], c["VD"]
+    xs = {"in_norm": f(bufs["h"]), "q_norm": f(bufs["qg"])[..., :HD].reshape(-1, HD),
+          "k_norm": f(bufs["k"]).reshape(-1, HD)}
+    ins = {"post": f(w["post"]), "g": f(w["g"])}
+    dys = {tag: f(grads["dy"][tag][2]) for tag in xs}
+    a, o, z, dyo = f(bufs["a"]), f(bufs["o"]), f(bufs["z"]), f(grads["do_g"])
+    dy_add, ds_add = f(grads["dy_add"]), f(grads["ds_add"])
+    t0 = time.perf_counter()
+    for tag, _, _, _, _, wt in plain:
+        _, r = N.rmsnorm_fwd(xs[tag], f(wt), 1e-6, 2)
+        N.rmsnorm_bwd(dys[tag], xs[tag], f(wt), 2, r)
+    s, _, r = N.add_rmsnorm_fwd(xs["in_norm"], a, ins["post"], 1e-6, 2)
+    N.rmsnorm_bwd(dy_add, s, ins["post"], 2, r, ds_add)
+    _, r = N.gated_fwd(o, z, ins["g"], 1e-6)
+    N.gated_bwd(dyo, o, z, ins["g"], r)
+    dt = time.perf_counter() - t0
+    return {"value": round(T / dt, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 fwd+bwd pass of the same norms (T={T}), numpy fp32, {dt:.2f} s, cpu={_cpu_model()}"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5"), default="c3")
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms"), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -457,6 +559,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "c4":
         run_gemma(args, dev)
+    elif args.workload == "norms":
+        run_norms(args, dev)
     else:
         run_qwen(args, dev, args.workload)
 

@@ -1,4 +1,4 @@
-"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h).
+"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h and include/smel_norm.h).
 
 The library is the only compute path: if it is missing, or no GPU is visible, calls raise instead of falling back to
 anything else. Tensors go in as raw device pointers; every call runs on torch's current HIP stream.
@@ -74,6 +74,12 @@ SIGNATURES = {
     "smel_lora_wgrad": (i32, [ctypes.POINTER(WgJob), i32, vp, i64, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp,
                               i64, vp]),
     "smel_lora_wgrad_ws_floats": (i64, [ctypes.POINTER(WgJob), i32, i64, i64]),
+    # include/smel_norm.h
+    "smel_rmsnorm_fwd": (i32, [vp, i64, i64, i64, vp, i32, f32, i32, vp, vp, vp]),
+    "smel_rmsnorm_bwd": (i32, [vp, vp, i64, i64, i64, vp, i32, vp, vp, i32, vp, vp]),
+    "smel_add_rmsnorm_fwd": (i32, [vp, vp, i64, i64, vp, i32, f32, i32, vp, vp, vp, vp]),
+    "smel_gated_rmsnorm_fwd": (i32, [vp, vp, i64, i64, vp, f32, i32, vp, vp, vp]),
+    "smel_gated_rmsnorm_bwd": (i32, [vp, vp, vp, i64, i64, vp, vp, i32, vp, vp, vp]),
 }
 
 _lib = None

@@ -1,4 +1,4 @@
-"""The C-ABI library loads without a GPU, exports every entry point include/smel_moe.h declares, and its host-side
+"""The C-ABI library loads without a GPU, exports every entry point include/*.h declares, and its host-side
 argument checks reject bad shapes before any launch (CPU only: no kernel runs here)."""
 import ctypes
 import os
@@ -7,11 +7,12 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "smel_moe.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def declared_functions():
-    src = open(HEADER).read()
+    src = "\n".join(open(h).read() for h in HEADERS)
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(smel_\w+)\s*\(", src, flags=re.M)))
 
