@@ -12,6 +12,10 @@ Other workloads of BASELINE.json (``--workload``), each printing one JSON line o
       the block's RMSNorms are outside this path and replaced by separate synthetic inputs;
   c5  the Qwen layer under skewed routing: T=32768 as 8 micro-batches of 4096, router biased to a
       Zipf(1.2) expert popularity (realised top-12 gate-mass share reported), the 12 most popular experts selected.
+  stream  the C3 layer with its weights (int4 bank, selected experts, router, shared expert) staged from pinned host
+      memory into two device slots per layer (include/smel_stream.h): host -> device bandwidth with one and two copy
+      streams, and the layer-major loop over 4 layer ids (each layer's upload and packing overlapping the previous
+      layer's fwd+bwd) against the resident layer;
   norms  the RMSNorm family around the block (include/smel_norm.h), forward + backward at the Qwen3.6 block's
       shapes for T=4092: input norm and residual add + post-attention norm [T, 2048], q / k head norms
       [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128].
@@ -535,12 +539,116 @@ def norms_cpu_baseline(bufs, w, plain, grads, c):
             "sample": f"1 fwd+bwd pass of the same norms (T={T}), numpy fp32, {dt:.2f} s, cpu={_cpu_model()}"}
 
 
+PCIE_GEN5_X16 = 64e9   # B/s per direction, the host link's nominal peak
+
+
+def run_stream(args, dev):
+    """Layer-major streaming of the C3 layer (smel/stream.py:39-114 in the reference; bench_layer.py:119-127 times
+    the bank's host -> device copy from pinned memory)."""
+    from smel import stream
+    from smel.moe import moe_forward
+    cfg = dict(QWEN)
+    log("building the C3 layer ...")
+    x, W, ex, lora, gy = build_qwen_layer(dev, cfg)
+    t = {f"experts.gate_up.{k}": v for k, v in ex.frozen.gu.items()}
+    t.update({f"experts.down.{k}": v for k, v in ex.frozen.dn.items()})
+    t.update({"experts.sel.ids": ex.sel_ids.cpu(), "experts.sel.gate_up": ex.sel_gate_up,
+              "experts.sel.down": ex.sel_down})
+    t.update({k: v for k, v in W.items() if not k.endswith("gate_up_proj.weight")})
+    t = {k: v.detach().cpu() for k, v in t.items()}
+    NL = 4
+    xg = x.clone().requires_grad_(True)
+    params = list(lora.parameters())
+
+    def layer_step(LW):
+        for p in params:
+            p.grad = None
+        xg.grad = None
+        moe_forward(xg, LW.W, LW.experts, cfg["K"], lora).backward(gy)
+
+    res = {}
+    for ns in (1, 2):
+        stream.N_COPY_STREAMS = ns
+        src = stream.PinnedSource({0: t}, max_on_gpu=2)
+        P = src.pinned[0]
+        src.pinned = {l: P for l in range(NL)}
+        src.get(0)                                  # first upload: the one host sync (fast-dequant check)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 6
+        e0.record()
+        for i in range(1, reps + 1):
+            src.get(i % NL)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_stage = e0.elapsed_time(e1) / reps
+        res[ns] = ms_stage
+        log(f"{ns} copy stream(s): stage (copy + pack) {ms_stage:.2f} ms per layer, {P.nbytes / 1e6:.1f} MB, "
+            f"{P.nbytes / ms_stage / 1e6:.1f} GB/s")
+        src.close()
+    ns = 2 if res[2] <= res[1] else 1
+    stream.N_COPY_STREAMS = ns
+    src = stream.PinnedSource({0: t}, max_on_gpu=2)
+    P = src.pinned[0]
+    src.pinned = {l: P for l in range(NL)}
+    LW = src.get(0)
+    layer_step(LW)
+    torch.cuda.synchronize()
+    # copy-only rate: the same bytes without packing, pinned -> the slot arena
+    import ctypes
+    from smel import _lib
+    slot = src.slots[0]
+    evs = [stream._Event() for _ in range(ns)]
+    streams = (ctypes.c_void_p * ns)(*[c.cuda_stream for c in src.copy[:ns]])
+    done = (ctypes.c_void_p * ns)(*[e.h for e in evs])
+    reg = (_lib.H2DRegion * 1)(_lib.H2DRegion(slot.arena.data_ptr(), P.host.data_ptr(), P.nbytes))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        _lib.call("smel_h2d_regions", reg, 1, stream.CHUNK_BYTES, streams, done, ns, None)
+    torch.cuda.synchronize()
+    ms_copy = (time.perf_counter() - t0) / 5 * 1e3
+    torch.autograd.graph.increment_version(slot.arena)
+    src.close()
+    src = stream.PinnedSource({0: t}, max_on_gpu=2)
+    src.pinned = {l: P for l in range(NL)}
+    P.fast = dict(P.fast)
+
+    def step():
+        for l in range(NL):
+            LW = src.get(l)
+            src.prefetch((l + 1) % NL)
+            layer_step(LW)
+
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup // 5)):
+        step()
+    torch.cuda.synchronize()
+    n = max(1, args.steps // 10)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        step()
+    torch.cuda.synchronize()
+    ms_layer = (time.perf_counter() - t0) / n / NL * 1e3
+    resident = time_step(lambda: layer_step(LW), 10, 3, graph=False)[1]
+    log(f"streamed layer {ms_layer:.2f} ms, resident (eager) {resident:.3f} ms, copy {ms_copy:.2f} ms")
+    rate = P.nbytes / (ms_copy * 1e-3)
+    roof = {"kernel": "h2d_copy", "bound": "pcie", "achieved": round(rate / 1e9, 1), "peak": PCIE_GEN5_X16 / 1e9,
+            "unit": "GB/s", "frac": round(rate / PCIE_GEN5_X16, 4), "traffic": None, "bytes_per_launch": P.nbytes,
+            "avg_launch_ms": round(ms_copy, 3)}
+    emit("streamed MoE layer fwd+bwd tokens/s (C3, weights staged from pinned host memory per layer)", cfg["T"],
+         args, ("eager_layer_major", ms_layer, ms_layer), "stream",
+         {"layer_bytes": P.nbytes, "layer_ids": NL, "copy_streams": ns, "chunk_bytes": stream.CHUNK_BYTES},
+         roof, {"stage_ms_1_stream": round(res[1], 3), "stage_ms_2_streams": round(res[2], 3),
+                "copy_ms": round(ms_copy, 3), "resident_layer_ms": round(resident, 3)}, None)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms"), default="c3")
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream"), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -561,6 +669,8 @@ def main():
         run_gemma(args, dev)
     elif args.workload == "norms":
         run_norms(args, dev)
+    elif args.workload == "stream":
+        run_stream(args, dev)
     else:
         run_qwen(args, dev, args.workload)
 

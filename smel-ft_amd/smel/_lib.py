@@ -1,4 +1,4 @@
-"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h and include/smel_norm.h).
+"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h, smel_norm.h and smel_stream.h).
 
 The library is the only compute path: if it is missing, or no GPU is visible, calls raise instead of falling back to
 anything else. Tensors go in as raw device pointers; every call runs on torch's current HIP stream.
@@ -38,6 +38,11 @@ class WgJob(ctypes.Structure):
     """smel_wg_job of include/smel_moe.h."""
     _fields_ = [("L", vp), ("Rm", vp), ("ldr", i64), ("r_rows", i64), ("r_gather", i32), ("use_w", i32), ("Q", i64),
                 ("dest", (WgDest * 2) * 2)]
+
+
+class H2DRegion(ctypes.Structure):
+    """smel_h2d_region of include/smel_stream.h."""
+    _fields_ = [("dst", vp), ("src", vp), ("bytes", i64)]
 
 
 # name -> (restype, argtypes)
@@ -80,6 +85,12 @@ SIGNATURES = {
     "smel_add_rmsnorm_fwd": (i32, [vp, vp, i64, i64, vp, i32, f32, i32, vp, vp, vp, vp]),
     "smel_gated_rmsnorm_fwd": (i32, [vp, vp, i64, i64, vp, f32, i32, vp, vp, vp]),
     "smel_gated_rmsnorm_bwd": (i32, [vp, vp, vp, i64, i64, vp, vp, i32, vp, vp, vp]),
+    # include/smel_stream.h
+    "smel_event_create": (i32, [ctypes.POINTER(vp)]),
+    "smel_event_destroy": (i32, [vp]),
+    "smel_event_record": (i32, [vp, vp]),
+    "smel_stream_wait": (i32, [vp, vp]),
+    "smel_h2d_regions": (i32, [ctypes.POINTER(H2DRegion), i32, i64, ctypes.POINTER(vp), ctypes.POINTER(vp), i32, vp]),
 }
 
 _lib = None

@@ -1,0 +1,340 @@
+"""Layer weight sources with prefetch for the layer-major runner (the reference's smel/stream.py:1-214), built on
+the stager of include/smel_stream.h.
+
+A layer's tensors live in one pinned host arena (``PinnedLayer``: the reference's tensor names, 256-byte aligned
+offsets, the dense gate and up projections next to each other). ``prefetch(l)`` copies the arena into a device slot
+on copy streams (chunked over two DMA queues), then, on the first copy stream, packs the frozen int4 bank and the
+selected experts into the grouped GEMMs' layouts, so the layer arrives ready to run; ``get(l)`` makes the current
+(compute) stream wait on the stage's event. The host never blocks on a copy (the reference's worker thread waits on
+every upload's event, smel/stream.py:62). The one host synchronisation is the exact-fast-dequant check of an int4
+bank, once per pinned layer on its first upload (the answer is kept with the pinned layer).
+
+Differences from the reference, by design: a slot is reused once ``max_on_gpu`` other layers were fetched after it,
+so a ``LayerWeights`` from ``get(l)`` is valid until then (the layer-major runner uses a layer before fetching the
+next ones); device memory is a fixed set of slots (no allocator churn per layer).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import time
+from collections import OrderedDict
+
+import torch
+
+from . import _lib as L
+from .moe import BF16Experts, Int4Experts, LayerExperts
+
+ALIGN = 256
+CHUNK_BYTES = 8 << 20
+N_COPY_STREAMS = 2
+
+
+class LayerWeights:
+    """Device tensors of one decoder layer: dense part (names relative to the layer) + routed experts
+    (smel/layer_runner.py:265-278). Gate and up of the dense / shared MLP are presented stacked as
+    ``*gate_up_proj.weight`` with the old names as views; when they are adjacent in memory (as a ``PinnedLayer``
+    stages them) the stacked tensor is a view too, otherwise one concatenation."""
+
+    def __init__(self, idx: int, ltype: str, W: dict, experts: LayerExperts):
+        W = dict(W)
+        for pre in ("mlp.shared_expert.", "mlp."):
+            g, u = W.get(pre + "gate_proj.weight"), W.get(pre + "up_proj.weight")
+            if g is not None and u is not None and g.shape == u.shape and g.dtype == u.dtype:
+                if (g.is_contiguous() and u.is_contiguous() and g.untyped_storage().data_ptr()
+                        == u.untyped_storage().data_ptr() and u.data_ptr() == g.data_ptr() + g.numel() * g.element_size()):
+                    gu = torch.as_strided(g, (2 * g.shape[0],) + tuple(g.shape[1:]), g.stride())
+                else:
+                    gu = torch.cat((g, u))
+                W[pre + "gate_up_proj.weight"], W[pre + "gate_proj.weight"], W[pre + "up_proj.weight"] = \
+                    gu, gu[:g.shape[0]], gu[g.shape[0]:]
+        self.idx, self.ltype, self.W, self.experts = idx, ltype, W, experts
+
+
+def build_layer(idx, ltype, t: dict, sel_ids=None, group=32, frozen_dtype=torch.bfloat16, act="silu"):
+    """t: device tensors of one layer, names relative to the layer: bf16 fused experts ('mlp.experts.gate_up_proj' /
+    'down_proj') or the packed int4 bank ('experts.gate_up.q', ...) + 'experts.sel.*' (smel/stream.py:16-36)."""
+    dense = {k: v for k, v in t.items() if not k.startswith(("mlp.experts.", "experts."))}
+    if "mlp.experts.gate_up_proj" in t:
+        gu, dn = t["mlp.experts.gate_up_proj"], t["mlp.experts.down_proj"]
+        frozen = BF16Experts(gu, dn)
+        sgu = sdn = None
+        if sel_ids is not None and len(sel_ids):
+            ids = torch.as_tensor(sel_ids, device=gu.device)
+            sgu, sdn = gu[ids].clone(), dn[ids].clone()
+    else:
+        gq = {k[len("experts.gate_up."):]: v for k, v in t.items() if k.startswith("experts.gate_up.")}
+        dq = {k[len("experts.down."):]: v for k, v in t.items() if k.startswith("experts.down.")}
+        frozen = Int4Experts(gq, dq, dtype=frozen_dtype)
+        sgu, sdn = t.get("experts.sel.gate_up"), t.get("experts.sel.down")
+        if sel_ids is None and "experts.sel.ids" in t:
+            sel_ids = t["experts.sel.ids"].tolist()
+    if sgu is None:
+        sel_ids = None
+    return LayerWeights(idx, ltype, dense, LayerExperts(frozen, sel_ids, sgu, sdn, group=group, act=act))
+
+
+def _order(names):
+    """Staging order: every name in sorted order, except that an MLP's up projection follows its gate projection."""
+    out = []
+    for k in sorted(names):
+        if k.endswith("up_proj.weight") and k.replace("up_proj", "gate_proj") in names:
+            continue
+        out.append(k)
+        if k.endswith("gate_proj.weight") and k.replace("gate_proj", "up_proj") in names:
+            out.append(k.replace("gate_proj", "up_proj"))
+    return out
+
+
+def arena_layout(t: dict):
+    """{name: (offset, shape, dtype, nbytes)} and the total size of a layer's arena (offsets aligned to ALIGN except
+    an up projection, which directly follows its gate projection when that keeps its alignment)."""
+    meta, off = OrderedDict(), 0
+    for k in _order(list(t)):
+        v = t[k]
+        nb = v.numel() * v.element_size()
+        glued = k.endswith("up_proj.weight") and k.replace("up_proj", "gate_proj") in meta
+        if not glued or off % v.element_size():
+            off = -(-off // ALIGN) * ALIGN
+        meta[k] = (off, tuple(v.shape), v.dtype, nb)
+        off += nb
+    return meta, -(-off // ALIGN) * ALIGN
+
+
+class PinnedLayer:
+    """One layer's tensors copied once into a pinned host arena (page-locked: the DMA engines read it directly)."""
+
+    def __init__(self, t: dict):
+        self.meta, self.nbytes = arena_layout(t)
+        self.host = torch.empty(max(self.nbytes, ALIGN), dtype=torch.uint8, pin_memory=True)
+        for k, (off, _, _, nb) in self.meta.items():
+            if nb:
+                self.host[off:off + nb].copy_(t[k].detach().contiguous().reshape(-1).view(torch.uint8))
+        ids = t.get("experts.sel.ids")
+        self.sel_ids = None if ids is None else [int(i) for i in ids.tolist()]
+        self.fast = {}   # int4 bank: {'gu' | 'dn': exact fast dequant form holds}, filled at the first upload
+
+
+class _Slot:
+    def __init__(self, nbytes, device):
+        self.arena = torch.empty(max(nbytes, ALIGN), dtype=torch.uint8, device=device)
+        self.free = _Event()                 # recorded on the compute stream when the slot is given up
+        self.free_used = False
+        self.done = [_Event() for _ in range(N_COPY_STREAMS)]
+        self.ready = _Event()
+        self.layer = None
+        self.LW = None
+
+
+class _Event:
+    """A timing-free HIP event owned by the library (smel_event_create)."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        L.call("smel_event_create", ctypes.byref(h))
+        self.h = h
+
+    def __del__(self):
+        try:
+            if self.h:
+                L.load().smel_event_destroy(self.h)
+        except Exception:   # interpreter shutdown
+            pass
+
+
+class _StagedSource:
+    """prefetch(l) / get(l) -> LayerWeights / close() / stats, as the reference's _StreamingSource
+    (smel/stream.py:39-114), over the device slots of the stager. Subclasses give _pinned(l) -> PinnedLayer and
+    _ltype(l)."""
+
+    def __init__(self, device="cuda", resident=False, max_on_gpu=2, group=32, act="silu"):
+        self.device = torch.device(device)
+        L.require_device(torch.empty(0, device=self.device))
+        self.resident, self.max_on_gpu, self.group, self.act = resident, max(1, max_on_gpu), group, act
+        self.slots = []                     # _Slot, in least-recently-used order at the front
+        self.copy = [torch.cuda.Stream(self.device) for _ in range(N_COPY_STREAMS)]   # default priority
+        self.stats = {"load_s": 0.0, "wait_s": 0.0, "bytes": 0, "loads": 0}
+        self.cache = {}                     # l -> LayerWeights staged (views into a slot)
+
+    # -- subclass hooks
+    def _pinned(self, l) -> PinnedLayer:
+        raise NotImplementedError
+
+    def _ltype(self, l) -> str:
+        return "linear_attention"
+
+    # --
+    def _slot_for(self, l, nbytes):
+        for s in self.slots:
+            if s.layer == l:
+                return s, True
+        if self.resident or len(self.slots) < self.max_on_gpu:
+            s = _Slot(nbytes, self.device)
+            self.slots.append(s)
+            return s, False
+        s = self.slots[0]                   # least recently used
+        if s.arena.numel() < nbytes:
+            s.arena = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        # every kernel that reads the evicted layer was enqueued on the current stream before this point
+        L.call("smel_event_record", s.free.h, L.stream())
+        s.free_used = True
+        self.cache.pop(s.layer, None)
+        s.layer, s.LW = None, None
+        return s, False
+
+    def prefetch(self, l):
+        """Stage layer l in a device slot (copies and packing on the copy streams; returns at once)."""
+        if l in self.cache:
+            return
+        t0 = time.perf_counter()
+        P = self._pinned(l)
+        s, hit = self._slot_for(l, P.nbytes)
+        if hit:
+            return
+        regions = (L.H2DRegion * 1)(L.H2DRegion(s.arena.data_ptr(), P.host.data_ptr(), P.nbytes))
+        streams = (ctypes.c_void_p * N_COPY_STREAMS)(*[c.cuda_stream for c in self.copy])
+        done = (ctypes.c_void_p * N_COPY_STREAMS)(*[d.h for d in s.done])
+        # the copy streams start after work already enqueued on the current stream that may read the slot
+        L.call("smel_h2d_regions", regions, 1, CHUNK_BYTES, streams, done, N_COPY_STREAMS,
+               s.free.h if s.free_used else None)
+        torch.autograd.graph.increment_version(s.arena)   # packed-layout caches keyed on the old bytes miss
+        t = {k: s.arena[off:off + nb].view(dt).view(shape) for k, (off, shape, dt, nb) in P.meta.items()}
+        c0 = self.copy[0]
+        for d in s.done[1:]:
+            L.call("smel_stream_wait", c0.cuda_stream, d.h)
+        with torch.cuda.stream(c0):
+            LW = build_layer(l, self._ltype(l), t, P.sel_ids, self.group, act=self.act)
+            self._pack(LW.experts, P)
+        L.call("smel_event_record", s.ready.h, c0.cuda_stream)
+        s.layer, s.LW = l, LW
+        self.cache[l] = LW
+        self.slots.remove(s)
+        self.slots.append(s)
+        self.stats["load_s"] += time.perf_counter() - t0
+        self.stats["bytes"] += P.nbytes
+        self.stats["loads"] += 1
+
+    @staticmethod
+    def _pack(ex: LayerExperts, P: PinnedLayer):
+        """The GEMMs' packed layouts of the staged bank and selected experts, on the current (copy) stream."""
+        fz = ex.frozen
+        if isinstance(fz, Int4Experts):
+            if P.fast:
+                fz._fast_dq = dict(P.fast)
+            for which in ("gu", "dn"):
+                P.fast[which] = fz.fast_dq(which)    # a host synchronisation only the first time
+                fz.packed(which)
+                fz.packed_t(which)
+        ex.packed_sel()
+        ex.packed_sel_t()
+
+    @staticmethod
+    def _stage_tensors(LW: LayerWeights):
+        """Every tensor of a staged layer; those made on the copy stream (packed layouts, stacked or selected
+        copies) must not be reused by the allocator before the compute stream is done with them."""
+        ex = LW.experts
+        out = [v for v in LW.W.values() if isinstance(v, torch.Tensor)]
+        out += [v for v in (ex.sel_gate_up, ex.sel_down) if isinstance(v, torch.Tensor)]
+        fz = ex.frozen
+        for name in ("_packed", "_packed_t"):
+            for v in fz.__dict__.get(name, {}).values():
+                out += [x for x in v if isinstance(x, torch.Tensor)]
+        for name in ("_packed_sel", "_packed_sel_t"):
+            for p in ex.__dict__.get(name) or ():
+                out.append(p.t)
+        return out
+
+    def get(self, l) -> LayerWeights:
+        """The staged layer l (staged now if it was not prefetched); the current stream waits for its stage."""
+        t0 = time.perf_counter()
+        if l not in self.cache:
+            self.prefetch(l)
+        s = next(x for x in self.slots if x.layer == l)
+        cur = L.stream()
+        L.call("smel_stream_wait", cur, s.ready.h)
+        cs = torch.cuda.current_stream(self.device)
+        for x in self._stage_tensors(s.LW):   # made on the copy stream, read on this one
+            x.record_stream(cs)
+        self.slots.remove(s)
+        self.slots.append(s)
+        self.stats["wait_s"] += time.perf_counter() - t0
+        return s.LW
+
+    def close(self):
+        torch.cuda.synchronize(self.device)
+        self.cache.clear()
+        self.slots.clear()
+
+
+class DictSource:
+    """Already materialized LayerWeights (tests / fully resident block), smel/stream.py:200-214."""
+
+    def __init__(self, layers: dict):
+        self.layers = layers
+        self.stats = {"load_s": 0.0, "wait_s": 0.0, "bytes": 0, "loads": 0}
+
+    def get(self, l):
+        return self.layers[l]
+
+    def prefetch(self, l):
+        pass
+
+    def close(self):
+        pass
+
+
+class PinnedSource(_StagedSource):
+    """Layers given as dicts of CPU tensors (e.g. ``pack_layer`` outputs), pinned once at construction."""
+
+    def __init__(self, layers: dict, ltypes=None, device="cuda", resident=False, max_on_gpu=2, group=32,
+                 act="silu"):
+        super().__init__(device, resident, max_on_gpu, group, act)
+        self.pinned = {l: PinnedLayer(t) for l, t in layers.items()}
+        self.ltypes = ltypes or {}
+
+    def _pinned(self, l):
+        return self.pinned[l]
+
+    def _ltype(self, l):
+        return self.ltypes.get(l, "linear_attention")
+
+
+class PackedSource(_StagedSource):
+    """Layers from the packed block, one ``layer_{l:02d}.safetensors`` per layer (smel/stream.py:142-197). With
+    pin=True every layer is read once into pinned RAM (up to pin_budget_gb); the rest are read and pinned at each
+    upload. ``dims`` needs ``layer_types`` and ``act``."""
+
+    def __init__(self, packed_dir, dims, layers, device="cuda", resident=False, pin=False, group=32,
+                 pin_budget_gb=9.0, preloaded=None, selection=None, ckpt=None, max_on_gpu=2):
+        if selection is not None or ckpt is not None:
+            raise NotImplementedError("re-selecting experts from the original checkpoint is outside this build")
+        super().__init__(device, resident, max_on_gpu, group, getattr(dims, "act", "silu"))
+        self.dir, self.d = packed_dir, dims
+        self.preloaded = preloaded or {}
+        self.pinned, self.pinned_gb = {}, 0.0
+        if pin:
+            used = 0
+            for l in layers:
+                P = PinnedLayer(self._read(l))
+                if (used + P.nbytes) / 2**30 > pin_budget_gb:
+                    break
+                self.pinned[l] = P
+                self.preloaded.pop(l, None)
+                used += P.nbytes
+            self.pinned_gb = used / 2**30
+
+    def _path(self, l):
+        return os.path.join(self.dir, f"layer_{l:02d}.safetensors")
+
+    def _read(self, l):
+        if l in self.preloaded:
+            return self.preloaded[l]
+        from safetensors import safe_open
+        with safe_open(self._path(l), "pt") as f:
+            return {k: f.get_tensor(k) for k in f.keys()}
+
+    def _pinned(self, l):
+        return self.pinned[l] if l in self.pinned else PinnedLayer(self._read(l))
+
+    def _ltype(self, l):
+        return self.d.layer_types[l]
