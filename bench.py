@@ -16,6 +16,8 @@ Other workloads of BASELINE.json (``--workload``), each printing one JSON line o
       memory into two device slots per layer (include/smel_stream.h): host -> device bandwidth with one and two copy
       streams, and the layer-major loop over 4 layer ids (each layer's upload and packing overlapping the previous
       layer's fwd+bwd) against the resident layer;
+  quant  the GPU int4 quantizer (the pack stage's producer of the on-disk format) on the C2 bank: 256 experts,
+      gate_up [256, 1024, 2048] and down [256, 2048, 512] bf16, group 64, the reference's five clip factors;
   norms  the RMSNorm family around the block (include/smel_norm.h), forward + backward at the Qwen3.6 block's
       shapes for T=4092: input norm and residual add + post-attention norm [T, 2048], q / k head norms
       [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128].
@@ -643,12 +645,57 @@ def run_stream(args, dev):
                 "copy_ms": round(ms_copy, 3), "resident_layer_ms": round(resident, 3)}, None)
 
 
+def run_quant(args, dev):
+    """quantize_int4 (smel/quant.py:14-44) of a whole C2-shaped bank on the GPU: HIP kernel time per bank, and the
+    same algorithm as torch ops on the host CPU (sampled) as the baseline."""
+    from smel import quant
+    c = QWEN
+    E, H, I = c["E"], c["H"], c["I"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    gu = (torch.randn(E, 2 * I, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    dn = (torch.randn(E, H, I, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    def step():
+        quant.quantize_int4(gu, 64)
+        quant.quantize_int4(dn, 64)
+
+    timing = time_step(step, max(3, args.steps // 10), 2, graph=False)
+    bd = breakdown_of(step, 3)
+    ms = timing[1]
+    nbytes = (gu.numel() + dn.numel()) * 2 + (gu.numel() + dn.numel()) // 2 + (gu.numel() + dn.numel()) // 64 * 4
+    cpu = None
+    if not args.no_cpu_baseline:
+        w = gu[:1].cpu()
+        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        t0 = time.perf_counter()
+        quant._quantize_int4_host(w, 64)
+        dt = time.perf_counter() - t0
+        per_bank_s = dt * E * 1.5
+        cpu = {"value": round(1 / per_bank_s, 4), "unit": "banks/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"1 expert's gate_up ({2 * I}x{H}) by the torch restatement on the CPU in "
+                                         f"{dt:.2f} s, scaled to the bank (x{E * 1.5:.0f}), cpu={_cpu_model()}"}
+    t = bd.get("smel_quantize_int4", ms / 2)
+    roof = {"kernel": "quantize_int4_reg_kernel<64>", "bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
+            "traffic": None, "bytes_per_launch": nbytes // 2, "avg_launch_ms": t,
+            "note": "VALU-bound: 5 candidates x (2 divisions + 10 operations) per weight"}
+    out_ms = {"hip_bank_ms": round(ms, 3)}
+    log(f"bank quantized in {ms:.2f} ms")
+    print(json.dumps({"metric": "int4 bank quantization banks/s (C2 bank: 256 experts, group 64, 5 clip factors)",
+                      "value": round(1e3 / ms, 2), "unit": "banks/s", "n_gpus": 1, "steps": timing and args.steps,
+                      "warmup": 2, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+                      "vs_baseline": None, "dtype": "f32", "data": "synthetic bf16 weights ~N(0, 0.02)",
+                      "config": {"workload": "quant", "experts": E, "gate_up": [2 * I, H], "down": [H, I],
+                                 "group": 64}, "roofline": roof, "breakdown_ms": {**bd, **out_ms},
+                      "cpu_baseline": cpu}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream"), default="c3")
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream", "quant"), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -671,6 +718,8 @@ def main():
         run_norms(args, dev)
     elif args.workload == "stream":
         run_stream(args, dev)
+    elif args.workload == "quant":
+        run_quant(args, dev)
     else:
         run_qwen(args, dev, args.workload)
 

@@ -61,6 +61,14 @@ int smel_abi_version(void);
 int smel_dequant_int4(const uint8_t* q, const uint16_t* scale, const uint16_t* zero, void* out, int64_t rows,
                       int64_t K, int64_t group, int32_t out_f32, hipStream_t stream);
 
+/* ---- (A8) replaces quantize_int4, smel/quant.py:5-44 (the on-disk format's producer, run on the GPU).
+ * w [rows][K] (w_dtype 0 bf16, 1 fp32, 2 fp16) -> q [rows][K/2] (even column in the low nibble), scale/zero bf16
+ * [rows][K/group]. Per group: the range [min, max] shrunk about its midpoint by each of the n_clip (1..8) factors in
+ * clip[] (host array) in turn, the candidate with the smallest sum of squared errors kept (later ones only if strictly
+ * better); every step is the reference's fp32 operation, the error sum in index order. group even, K % group == 0. */
+int smel_quantize_int4(const void* w, int32_t w_dtype, int64_t rows, int64_t K, int32_t group, const float* clip,
+                       int32_t n_clip, uint8_t* q, uint16_t* scale, uint16_t* zero, hipStream_t stream);
+
 /* ---- Weight layouts of the grouped GEMMs (no counterpart in the reference, whose q/scale/zero and bf16 tensors
  * stay the source of truth and are not modified; a frozen bank is packed once when it is built).
  * A matrix of `rows` rows (a stacked bank: E*R rows) and K columns is cut into fragments of 32 rows and k-steps of

@@ -50,6 +50,7 @@ SIGNATURES = {
     "smel_last_error": (ctypes.c_char_p, []),
     "smel_abi_version": (i32, []),
     "smel_dequant_int4": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
+    "smel_quantize_int4": (i32, [vp, i32, i64, i64, i32, ctypes.POINTER(f32), i32, vp, vp, vp, vp]),
     "smel_packed_bytes": (i64, [i32, i64, i64]),
     "smel_pack_int4": (i32, [vp, vp, vp, i64, i64, i64, vp, vp, vp]),
     "smel_pack_bf16": (i32, [vp, i64, i64, i64, vp, vp]),

@@ -3,7 +3,9 @@
 Format (the reference's, smel/quant.py:14-44): q uint8 [..., K/2] with the even column in the low nibble, scale and
 zero bf16 [..., K/group], w = q*scale + zero. ``dequant_int4`` is the MI355X kernel (fp32 math, one
 round-to-nearest-even, as the reference's GPU kernel smel/quant.py:51-67). ``quantize_int4`` is the offline packer of
-the reference's pack stage (not on the hot path); it runs as torch ops on whatever device its input lives on.
+the reference's pack stage (not on the hot path): a GPU input runs the HIP kernel ``smel_quantize_int4`` (one thread
+per group, the reference's fp32 steps in its order); a host input (a pack stage on a machine without the GPU) runs
+the same steps as torch ops on the CPU.
 """
 from __future__ import annotations
 
@@ -19,12 +21,35 @@ def _q4_candidate(wg, lo, hi):
     return q, scale, zero
 
 
+_QDT = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}
+
+
 def quantize_int4(w: torch.Tensor, group: int = 64, clip_search=(1.0, 0.95, 0.9, 0.85, 0.8)) -> dict:
     """w [..., K] -> {"q": uint8 [..., K/2], "scale": bf16 [..., K/group], "zero": bf16 [..., K/group]}
     (smel/quant.py:14-44): per group, the [min, max] range shrunk about its midpoint by the clip factor with the
-    smallest squared error (a later factor must be strictly better); 3-D inputs in slices of 16 experts."""
+    smallest squared error (a later factor must be strictly better). GPU inputs: one HIP launch for the whole
+    tensor; host inputs: torch ops, 3-D inputs in slices of 16 experts as the reference."""
+    if not w.is_cuda:
+        return _quantize_int4_host(w, group, clip_search)
+    K = w.shape[-1]
+    assert K % group == 0 and group % 2 == 0
+    clip = list(clip_search or (1.0,))
+    if w.dtype not in _QDT:
+        w = w.float()
+    wc = w.contiguous()
+    rows = wc.numel() // K
+    q = torch.empty(*w.shape[:-1], K // 2, dtype=torch.uint8, device=w.device)
+    scale = torch.empty(*w.shape[:-1], K // group, dtype=torch.bfloat16, device=w.device)
+    zero = torch.empty_like(scale)
+    cf = (L.f32 * len(clip))(*clip)
+    L.call("smel_quantize_int4", L.ptr(wc), _QDT[wc.dtype], rows, K, group, cf, len(clip), L.ptr(q), L.ptr(scale),
+           L.ptr(zero), L.stream())
+    return {"q": q, "scale": scale, "zero": zero}
+
+
+def _quantize_int4_host(w: torch.Tensor, group: int = 64, clip_search=(1.0, 0.95, 0.9, 0.85, 0.8)) -> dict:
     if w.dim() == 3 and w.shape[0] > 16:
-        parts = [quantize_int4(w[i:i + 16], group, clip_search) for i in range(0, w.shape[0], 16)]
+        parts = [_quantize_int4_host(w[i:i + 16], group, clip_search) for i in range(0, w.shape[0], 16)]
         return {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
     K = w.shape[-1]
     assert K % group == 0 and group % 2 == 0

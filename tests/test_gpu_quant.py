@@ -1,0 +1,80 @@
+"""GPU int4 quantizer (smel_quantize_int4 through smel.quant.quantize_int4) against the reference's own bytes and
+against the reference's algorithm in torch ops (smel/quant.py:5-44).
+
+Bar: the reference's golden bytes (tests/golden/quant_int4.safetensors, written by the reference's quantize_int4)
+bit for bit. On larger random banks, every group's q equals clamp(rint((w - zero) / scale), 0, 15) for the scale
+and zero it chose, and scale / zero equal those of the torch restatement except where two clip candidates' error
+sums agree to within fp32 rounding (the reference leaves the order of that sum to its library): there the fp64
+errors of both choices must agree to 2e-5 relative, and at most 1 group in 10^3 may be such a tie."""
+import os
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_int4.safetensors")
+CASES = ("normal", "outlier", "g32", "grid", "e20")
+
+
+@pytest.fixture(scope="module")
+def quant():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from smel import quant
+    return quant
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_golden_bytes(quant, case):
+    from safetensors.torch import load_file
+    g = load_file(GOLDEN)
+    w = g[f"quant.{case}.w"].cuda()
+    pk = quant.quantize_int4(w, 32 if case == "g32" else 64)
+    assert torch.equal(pk["q"].cpu(), g[f"quant.{case}.q"])
+    assert torch.equal(pk["scale"].cpu().view(torch.int16), g[f"quant.{case}.scale"].view(torch.int16))
+    assert torch.equal(pk["zero"].cpu().view(torch.int16), g[f"quant.{case}.zero"].view(torch.int16))
+
+
+def unpack(q):
+    return torch.stack((q & 15, q >> 4), -1).reshape(*q.shape[:-1], q.shape[-1] * 2).float()
+
+
+def group_err64(w, q, s, z, group):
+    wg = w.double().reshape(*w.shape[:-1], -1, group)
+    qg = q.double().reshape(wg.shape)
+    return ((qg * s.double()[..., None] + z.double()[..., None] - wg) ** 2).sum(-1)
+
+
+@pytest.mark.parametrize("dtype,group,shape", [(torch.bfloat16, 64, (8, 512, 2048)), (torch.float32, 32, (4, 256, 512)),
+                                               (torch.bfloat16, 128, (4, 512, 1024)), (torch.float16, 64, (2, 64, 640))])
+def test_random_banks(quant, dtype, group, shape):
+    print(f"quant {dtype} g{group} {shape}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(group)
+    w = (torch.randn(*shape, generator=g, device="cuda") * 0.02).to(dtype)
+    w[0, 0, :group] = 0.0                                   # a constant group: scale clamps to 1e-8
+    w[0, 1, :group] *= 50                                    # an outlier group
+    got = quant.quantize_int4(w, group)
+    ref = quant._quantize_int4_host(w.cpu(), group)
+    s, z = got["scale"].cpu().float(), got["zero"].cpu().float()
+    # q is exactly the rounding of w for the chosen (scale, zero)
+    wg = w.cpu().float().reshape(*shape[:-1], -1, group)
+    qx = torch.round((wg - z[..., None]) / s[..., None]).clamp_(0, 15).reshape(*shape)
+    assert torch.equal(unpack(got["q"].cpu()), qx)
+    diff = (got["scale"].cpu().view(torch.int16) != ref["scale"].view(torch.int16)) | \
+           (got["zero"].cpu().view(torch.int16) != ref["zero"].view(torch.int16))
+    n = int(diff.sum())
+    assert n <= max(1, diff.numel() // 1000), f"{n} of {diff.numel()} groups chose another clip factor"
+    if n:
+        e_got = group_err64(w.cpu(), unpack(got["q"].cpu()), got["scale"].cpu().float(), got["zero"].cpu().float(),
+                            group)[diff]
+        e_ref = group_err64(w.cpu(), unpack(ref["q"]), ref["scale"].float(), ref["zero"].float(), group)[diff]
+        assert torch.all((e_got - e_ref).abs() <= 2e-5 * torch.maximum(e_got, e_ref)), (e_got, e_ref)
+    same = ~diff
+    qa = got["q"].cpu().reshape(*shape[:-1], -1, group // 2)[same]
+    qb = ref["q"].reshape(*shape[:-1], -1, group // 2)[same]
+    assert torch.equal(qa, qb)
+
+
+def test_bad_group_is_an_assertion(quant):
+    with pytest.raises(AssertionError):
+        quant.quantize_int4(torch.randn(2, 48, device="cuda"), 64)
