@@ -18,6 +18,8 @@ Other workloads of BASELINE.json (``--workload``), each printing one JSON line o
       layer's fwd+bwd) against the resident layer;
   quant  the GPU int4 quantizer (the pack stage's producer of the on-disk format) on the C2 bank: 256 experts,
       gate_up [256, 1024, 2048] and down [256, 2048, 512] bf16, group 64, the reference's five clip factors;
+  ce  the single-pass chunked cross-entropy (loss + dh) over a Qwen3.6-sized head: 4092 tokens, hidden 2048, vocabulary
+      248320, bf16, token chunk 1024, vocabulary chunk 32768;
   norms  the RMSNorm family around the block (include/smel_norm.h), forward + backward at the Qwen3.6 block's
       shapes for T=4092: input norm and residual add + post-attention norm [T, 2048], q / k head norms
       [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128].
@@ -690,12 +692,53 @@ def run_quant(args, dev):
                       "cpu_baseline": cpu}), flush=True)
 
 
+CE_SHAPE = dict(T=4092, H=2048, V=248320, token_chunk=1024, vocab_chunk=32768)
+
+
+def run_ce(args, dev):
+    """chunked_ce (smel/loss.py:149-156) loss and gradient for one sequence of the Qwen3.6 shape: per vocabulary
+    chunk two library GEMMs (logits, p W) and the HIP online-softmax / accumulator kernels."""
+    from smel import loss as LS
+    c = CE_SHAPE
+    T, H, V = c["T"], c["H"], c["V"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16).requires_grad_(True)
+    W = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    tgt = torch.randint(0, V, (T,), generator=g, device=dev)
+    head = LS.LMHead(weight=W, vocab_chunk=c["vocab_chunk"])
+
+    def step():
+        h.grad = None
+        LS.chunked_ce(h, head, tgt, denom=float(T), token_chunk=c["token_chunk"]).backward()
+
+    timing = time_step(step, max(3, args.steps // 10), 2, graph=False)
+    bd = breakdown_of(step, 2)
+    ms = timing[1]
+    flops = 4 * T * V * H                         # logits GEMM + gradient GEMM, 2 T V H each
+    roof = {"kernel": "whole step (library GEMMs + smel_ce_chunk_update / smel_ce_acc_update)", "bound": "mfma",
+            "achieved": round(flops / (ms * 1e-3) / 1e12, 1), "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+            "frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4), "traffic": None, "flops_per_step": flops}
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import loss_ref as LR
+        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        ns = 32
+        t0 = time.perf_counter()
+        LR.full_ce(h[:ns].float(), W.float(), tgt[:ns], 0.0, float(T))
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(ns / dt, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{ns} tokens through the full-logit fp64 oracle (loss + gradient) in {dt:.2f} s, "
+                         f"cpu={_cpu_model()}"}
+    emit("chunked CE loss+grad tokens/s (Qwen3.6 head: hidden 2048, vocabulary 248320)", T, args, timing, "ce",
+         dict(c), roof, bd, cpu)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream", "quant"), default="c3")
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream", "quant", "ce"), default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -720,6 +763,8 @@ def main():
         run_stream(args, dev)
     elif args.workload == "quant":
         run_quant(args, dev)
+    elif args.workload == "ce":
+        run_ce(args, dev)
     else:
         run_qwen(args, dev, args.workload)
 

@@ -11,6 +11,7 @@ Modules
                      smel/quant.py; autograd gives the backward, as in the reference's CPU path.
 ``oracle.norm_ref``  numpy fp32 restatement of the RMSNorm kernels of smel/norm.py (plain, residual add + norm,
                      gated; forward and backward) and of the torch code layer_runner.py runs instead of them.
+``oracle.loss_ref``  the chunked cross-entropy's result from the full logits in fp64 (torch on the CPU).
 ``oracle.intref``    numpy restatement of the integer/byte parts (nibble unpacking, bf16 round-to-nearest-even,
                      stable counting-sort dispatch, lowest-index top-k) and a ctypes loader for the C restatement
                      ``oracle/c/oracle.c`` of the same functions.

@@ -1,4 +1,4 @@
-"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h, smel_norm.h and smel_stream.h).
+"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h, smel_norm.h, smel_stream.h and smel_loss.h).
 
 The library is the only compute path: if it is missing, or no GPU is visible, calls raise instead of falling back to
 anything else. Tensors go in as raw device pointers; every call runs on torch's current HIP stream.
@@ -92,6 +92,9 @@ SIGNATURES = {
     "smel_event_record": (i32, [vp, vp]),
     "smel_stream_wait": (i32, [vp, vp]),
     "smel_h2d_regions": (i32, [ctypes.POINTER(H2DRegion), i32, i64, ctypes.POINTER(vp), ctypes.POINTER(vp), i32, vp]),
+    # include/smel_loss.h
+    "smel_ce_chunk_update": (i32, [vp, i64, i64, i64, i64, vp, f32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp]),
+    "smel_ce_acc_update": (i32, [vp, vp, vp, i32, i64, i64, i32, vp]),
 }
 
 _lib = None

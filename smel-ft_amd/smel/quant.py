@@ -99,3 +99,16 @@ def dequant_int4_torch(q, scale, zero, dtype=torch.bfloat16):
 def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
     a, b = a.float(), b.float()
     return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def quantize_int8_rows(w: torch.Tensor):
+    """Symmetric per-row int8 of a dense matrix (lm_head), smel/quant.py:97-101: scale = max(|w|) / 127 (at least
+    1e-12), q = clamp(round(w / scale), -127, 127); scale stored as bf16."""
+    s = (w.float().abs().amax(-1, keepdim=True) / 127).clamp_min(1e-12)
+    q = torch.round(w.float() / s).clamp_(-127, 127).to(torch.int8)
+    return {"q": q, "scale": s.squeeze(-1).to(torch.bfloat16)}
+
+
+def dequant_int8_rows(q, scale, dtype=torch.bfloat16):
+    """q * scale in `dtype` (smel/quant.py:104-105)."""
+    return q.to(dtype) * scale.unsqueeze(-1).to(dtype)
