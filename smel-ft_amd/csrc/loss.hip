@@ -145,6 +145,30 @@ __global__ __launch_bounds__(256) void ce_acc_update_kernel(float* __restrict__ 
   acc[i] = acc[i] * r[i / H] + v;
 }
 
+// the same for 16-bit products with H % 8 == 0 and 16-byte aligned buffers: 8 elements per thread
+template <int DT>
+__global__ __launch_bounds__(256) void ce_acc_update8_kernel(float* __restrict__ acc, const float* __restrict__ r,
+                                                             const void* __restrict__ pw, int64_t n, int64_t H,
+                                                             int parts) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i >= n * H) return;
+  float v[8];
+  ld8<DT>(pw, i, v);
+  for (int k = 1; k < parts; ++k) {
+    float u[8];
+    ld8<DT>(pw, (int64_t)k * n * H + i, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += u[e];
+  }
+  const float rr = r[i / H];
+  f32x4_t* const a4 = reinterpret_cast<f32x4_t*>(acc + i);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const f32x4_t a = a4[h];
+    a4[h] = f32x4_t{a[0] * rr + v[4 * h], a[1] * rr + v[4 * h + 1], a[2] * rr + v[4 * h + 2], a[3] * rr + v[4 * h + 3]};
+  }
+}
+
 }  // namespace
 
 extern "C" int smel_ce_chunk_update(const void* logits, int64_t n, int64_t vc, int64_t ld, int64_t v0,
@@ -187,10 +211,15 @@ extern "C" int smel_ce_acc_update(float* acc, const float* r, const void* pw, in
   SMEL_REQUIRE(dtype >= 0 && dtype <= 2, SMEL_EINVAL, "ce_acc_update: dtype %d", dtype);
   if (n == 0) return 0;
   SMEL_REQUIRE(acc && r && pw, SMEL_EINVAL, "ce_acc_update: null pointer");
-  const int64_t blocks = (n * H + 255) / 256;
+  const bool vec = dtype != 1 && H % 8 == 0 && (uintptr_t)acc % 16 == 0 && (uintptr_t)pw % 16 == 0;
+  const int64_t blocks = vec ? (n * H / 8 + 255) / 256 : (n * H + 255) / 256;
   SMEL_REQUIRE(blocks < (int64_t)1 << 31, SMEL_EUNSUPPORTED, "ce_acc_update: too large");
   const dim3 g((unsigned)blocks), b(256);
-  if (dtype == 0)
+  if (vec && dtype == 0)
+    ce_acc_update8_kernel<0><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
+  else if (vec)
+    ce_acc_update8_kernel<2><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
+  else if (dtype == 0)
     ce_acc_update_kernel<0><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
   else if (dtype == 1)
     ce_acc_update_kernel<1><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
