@@ -249,6 +249,9 @@ int launch_dt(NormArgs& p, hipStream_t stream) {
   p.lpr = 1;
   while (p.lpr < nch && p.lpr < 64) p.lpr *= 2;
   if (nch > 4 * 64) p.lpr = 256;
+  // forward passes of short rows (head dims): two chunks per thread (measured 2-7% faster; the backward, which
+  // holds two or three tensors per chunk, is faster with one)
+  if ((MODE == M_FWD || MODE == M_ADD || MODE == M_GFWD) && p.lpr >= 16 && nch <= 64) p.lpr /= 2;
   while (cpl * p.lpr < nch) cpl *= 2;
   const int64_t rows_per_block = 256 / p.lpr;
   const int64_t blocks = (p.rows + rows_per_block - 1) / rows_per_block;
