@@ -7,9 +7,10 @@ Synthetic data, random weights of that shape (weights ~N(0, 0.02), x ~N(0, 1)).
 
 Other workloads of BASELINE.json (``--workload``), each printing one JSON line of its own:
   c2  forward only (no autograd) of the same layer with all 256 experts frozen int4 and no LoRA (configs[1]);
-  c4  Gemma-4-26B-A4B-style MoE block fwd+bwd: route_gemma4 on the residual stream, 128 GELU-tanh
-      experts (I=704, 12 selected bf16 + LoRA r16, the rest int4), the dense GeGLU MLP (2112) with LoRA r16, T=4096;
-      the block's RMSNorms are outside this path and replaced by separate synthetic inputs;
+  c4  Gemma-4-26B-A4B-style MoE block fwd+bwd: the Gemma 4 layer from the attention output on
+      (smel/layer_runner.py:243-262): six RMSNorms, route_gemma4 on the residual stream, 128 GELU-tanh experts
+      (I=704, 12 selected bf16 + LoRA r16, the rest int4), the dense GeGLU MLP (2112) with LoRA r16, the residual
+      adds and the layer scalar, T=4096 as 8 packed sequences (the block is token-wise: cu_seqlens change nothing);
   c5  the Qwen layer under skewed routing: T=32768 as 8 micro-batches of 4096, router biased to a
       Zipf(1.2) expert popularity (realised top-12 gate-mass share reported), the 12 most popular experts selected.
   stream  the C3 layer with its weights (int4 bank, selected experts, router, shared expert) staged from pinned host
@@ -61,6 +62,17 @@ def _rnd(g, device, *s, std=0.02):
     return (torch.randn(*s, generator=g, device=device) * std).to(torch.bfloat16)
 
 
+def _randomize_lora_b(lora, g, std=0.02):
+    """LoRA B factors ~N(0, std) instead of the init's zeros, so that every LoRA product and gradient of the step is
+    non-trivial (dA is exactly 0 while B = 0); the work is the same either way."""
+    with torch.no_grad():
+        for m in (lora.experts, lora.shared):
+            if m is not None:
+                for n in ("B_gate", "B_up", "B_down"):
+                    p = getattr(m, n)
+                    p.copy_(torch.randn(p.shape, generator=g, device=p.device) * std)
+
+
 def build_qwen_layer(device, cfg=QWEN, seed=0, n_sel=None, lora=True, zipf=None):
     """The Qwen layer with the drop-in API's own types; the frozen bank is quantized on the GPU by smel.quant.
     ``zipf`` = bias scale c: expert e (in a random popularity order) gets logit bias -1.2 c ln(rank), injected
@@ -102,26 +114,33 @@ def build_qwen_layer(device, cfg=QWEN, seed=0, n_sel=None, lora=True, zipf=None)
     if lora:
         lo = LayerLoRA(ExpertsLoRA(sel, H, I, r, cfg["alpha"]) if sel else None,
                        MLPLoRA(H, Is, r, cfg["alpha"])).to(device)
+        _randomize_lora_b(lo, g)
     gy = (torch.randn(T, H, generator=g, device=device) * 1e-3).to(torch.bfloat16)
     torch.cuda.synchronize()
     return x, W, ex, lo, gy
 
 
+GEMMA_NORMS = ("post_attention_layernorm", "pre_feedforward_layernorm", "post_feedforward_layernorm_1",
+               "pre_feedforward_layernorm_2", "post_feedforward_layernorm_2", "post_feedforward_layernorm")
+
+
 def build_gemma_block(device, cfg=GEMMA, seed=0):
-    """The Gemma-4-style MoE block's inputs and weights: residual stream h (router input), the experts' input xe and
-    the dense MLP's input xm (the RMSNorm outputs of the reference's block, synthetic here), router tensors as
-    smel/tiny.py:74-77 draws them, 128 experts (12 selected bf16 + LoRA, the rest int4), dense GeGLU MLP + LoRA."""
+    """The Gemma-4-style block's inputs and weights: residual stream h and attention output a, the six norm weights
+    (~1 + N(0, 0.2)) and the layer scalar, router tensors as smel/tiny.py:74-77 draws them, 128 experts (12 selected
+    bf16 + LoRA, the rest int4), dense GeGLU MLP + LoRA. Returns (h, a, W, LayerExperts, LayerLoRA, upstream grad)."""
     from smel.lora import ExpertsLoRA, LayerLoRA, MLPLoRA
     from smel.moe import Int4Experts, LayerExperts
     g = torch.Generator(device=device).manual_seed(seed)
     T, H, E, I, Is, r = cfg["T"], cfg["H"], cfg["E"], cfg["I"], cfg["Is"], cfg["r"]
     h = (torch.randn(T, H, generator=g, device=device) * 3.0).to(torch.bfloat16)
-    xe = torch.randn(T, H, generator=g, device=device).to(torch.bfloat16)
-    xm = torch.randn(T, H, generator=g, device=device).to(torch.bfloat16)
-    W = {"router.scale": (1.0 + 0.2 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16),
-         "router.proj.weight": _rnd(g, device, E, H),
-         "router.per_expert_scale": (0.5 + torch.rand(E, generator=g, device=device)).to(torch.bfloat16),
-         "mlp.gate_up_proj.weight": _rnd(g, device, 2 * Is, H), "mlp.down_proj.weight": _rnd(g, device, H, Is)}
+    a = torch.randn(T, H, generator=g, device=device).to(torch.bfloat16)
+    W = {f"{n}.weight": (1.0 + 0.2 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16)
+         for n in GEMMA_NORMS}
+    W.update({"router.scale": (1.0 + 0.2 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16),
+              "router.proj.weight": _rnd(g, device, E, H),
+              "router.per_expert_scale": (0.5 + torch.rand(E, generator=g, device=device)).to(torch.bfloat16),
+              "mlp.gate_up_proj.weight": _rnd(g, device, 2 * Is, H), "mlp.down_proj.weight": _rnd(g, device, H, Is),
+              "layer_scalar": torch.full((1,), 0.8, device=device).to(torch.bfloat16)})
     W["mlp.gate_proj.weight"] = W["mlp.gate_up_proj.weight"][:Is]
     W["mlp.up_proj.weight"] = W["mlp.gate_up_proj.weight"][Is:]
     gu, dn = _rnd(g, device, E, 2 * I, H), _rnd(g, device, E, H, I)
@@ -131,9 +150,42 @@ def build_gemma_block(device, cfg=GEMMA, seed=0):
     del gu, dn
     torch.manual_seed(seed)
     lora = LayerLoRA(ExpertsLoRA(sel, H, I, r, cfg["alpha"]), MLPLoRA(H, Is, r, cfg["alpha"])).to(device)
+    _randomize_lora_b(lora, g)
     gy = (torch.randn(T, H, generator=g, device=device) * 1e-3).to(torch.bfloat16)
     torch.cuda.synchronize()
-    return h, xe, xm, W, ex, lora, gy
+    return h, a, W, ex, lora, gy
+
+
+def gemma_block(h, a, W, ex, lora, top_k, eps=1e-6, stats=None):
+    """The Gemma 4 layer from the attention output on, through the drop-in API (smel/layer_runner.py:243-262: norm
+    and MoE calls in the reference's order): every norm and MoE step is a HIP launch; the residual adds and the
+    layer-scalar product are torch element-wise ops."""
+    from smel.moe import mlp_lora, route_gemma4, routed_experts
+    from smel.norm import add_rmsnorm, rmsnorm
+    nw = lambda n: W[n + ".weight"]
+    h2, xm = add_rmsnorm(h, rmsnorm(a, nw("post_attention_layernorm"), eps, False), nw("pre_feedforward_layernorm"),
+                         eps, False)
+    m = mlp_lora(xm, W["mlp.gate_proj.weight"], W["mlp.up_proj.weight"], W["mlp.down_proj.weight"], lora.shared,
+                 ex.act, W["mlp.gate_up_proj.weight"])
+    m = rmsnorm(m, nw("post_feedforward_layernorm_1"), eps, False)
+    probs, topv, topi = route_gemma4(h2, W, top_k, eps)
+    if stats is not None:
+        stats(probs, topv, topi)
+    e = routed_experts(rmsnorm(h2, nw("pre_feedforward_layernorm_2"), eps, False), topv, topi, ex, lora.experts)
+    e = rmsnorm(e, nw("post_feedforward_layernorm_2"), eps, False)
+    _, y = add_rmsnorm(m, e, nw("post_feedforward_layernorm"), eps, False)
+    return (h2 + y) * W["layer_scalar"]
+
+
+def c5_microbatches(x, gy, n, device):
+    """The C5 step's n micro-batches of the same layer: the first is (x, gy), the others x + 0.5 N(0, 1) with fresh
+    upstream gradients (the same Zipf-biased router sees each)."""
+    xs, gys = [x], [gy]
+    g = torch.Generator(device=device).manual_seed(7)
+    for _ in range(n - 1):
+        xs.append((x.float() + 0.5 * torch.randn(x.shape, generator=g, device=device)).to(torch.bfloat16))
+        gys.append((torch.randn(gy.shape, generator=g, device=device) * 1e-3).to(torch.bfloat16))
+    return xs, gys
 
 
 # ------------------------------------------------------------------------------------------ algorithmic work model
@@ -142,7 +194,8 @@ def build_gemma_block(device, cfg=GEMMA, seed=0):
 def kernel_work(tag, c, S):
     """(algorithmic FLOPs, algorithmic HBM bytes) of one launch of a kernel, from the layer's shape ``c`` and the
     number S of slots routed to selected experts. Bytes = every operand read once and every result written once:
-    frozen int4 experts (q + scale/zero in the layout the kernel reads) except the selected ones, selected / shared bf16 weights, activations
+    frozen int4 experts (q + bf16 scale/zero, the reference's format) except the selected ones, selected / shared
+    bf16 weights, activations
     (the gathered token rows counted once per token), the LoRA K-extension rows, the saved pre-activations and (down
     backward) the saved activation."""
     T, H, E, I, K, r = c["T"], c["H"], c["E"], c["I"], c["K"], c["r"]
@@ -152,14 +205,12 @@ def kernel_work(tag, c, S):
     M = T * K + Msh
     Lr = S + Msh
     nfz = E - n_sel
-    # forward layouts: scale/zero as bf16 pairs (4 B per group); the backward's transposed layout keeps them as fp32
-    # pairs (8 B per group)
-    def bank(nq, ngroups, nbf, szb):
-        return nfz * (nq // 2 + ngroups * szb) + n_sel * nbf * 2 + (nbf * 2 if Msh else 0)
-    gu_w = bank(2 * I * H, 2 * I * (H // g), 2 * I * H, 4)
-    dn_w = bank(H * I, H * (I // g), H * I, 4)
-    gu_wt = bank(2 * I * H, 2 * I * (H // g), 2 * I * H, 8)
-    dn_wt = bank(H * I, H * (I // g), H * I, 8)
+    # int4 weights counted in the reference's format (smel/quant.py:24-44: two nibbles per byte, a bf16 scale and a
+    # bf16 zero per group = 4 B), whatever layout a kernel reads them in
+    def bank(nq, ngroups, nbf):
+        return nfz * (nq // 2 + ngroups * 4) + n_sel * nbf * 2 + (nbf * 2 if Msh else 0)
+    gu_w = gu_wt = bank(2 * I * H, 2 * I * (H // g), 2 * I * H)
+    dn_w = dn_wt = bank(H * I, H * (I // g), H * I)
     ext = M * 32 * 2 if (Lr and r) else 0
     nblk = -(-I // 128)
     Epad = -(-(E + (1 if Msh else 0)) // 32) * 32
@@ -302,12 +353,7 @@ def run_qwen(args, dev, mode):
     x, W, ex, lora, gy = build_qwen_layer(dev, cfg, n_sel=0 if fwd_only else None, lora=not fwd_only,
                                           zipf=C5_BIAS if mode == "c5" else None)
     T = cfg["T"]
-    xs, gys = [x], [gy]
-    if nmb > 1:   # micro-batches: the same layer on 8 different token sets
-        g = torch.Generator(device=dev).manual_seed(7)
-        for _ in range(nmb - 1):
-            xs.append((x.float() + 0.5 * torch.randn(x.shape, generator=g, device=dev)).to(torch.bfloat16))
-            gys.append((torch.randn(gy.shape, generator=g, device=dev) * 1e-3).to(torch.bfloat16))
+    xs, gys = c5_microbatches(x, gy, nmb, dev)   # nmb = 1: just (x, gy)
     xgs = [xi.clone().requires_grad_(not fwd_only) for xi in xs]
     params = list(lora.parameters()) if lora is not None else []
     seen = []
@@ -351,34 +397,27 @@ def run_qwen(args, dev, mode):
         c["r"] = 0
     roof = roofline(bd, c, S)
     cpu = None
-    if mode == "c3" and not args.no_cpu_baseline:
-        log("timing the CPU baseline (one full pass of the oracle) ...")
-        cpu = cpu_baseline(x, W, ex, lora, gy, cfg)
+    if mode in ("c3", "c2") and not args.no_cpu_baseline:
+        log("timing the CPU baseline (the oracle: 1 warmup + median of 5 full passes) ...")
+        cpu = cpu_baseline(x, W, ex, lora, gy, cfg, fwd_only)
     emit(METRIC if mode == "c3" else QWEN_METRICS[mode], T * nmb, args, timing, QWEN_NAMES[mode],
          {"selected_slots": S, "micro_batches": nmb}, roof, bd, cpu, **extra)
 
 
 def run_gemma(args, dev):
-    from smel.moe import mlp_lora, route_gemma4, routed_experts
     cfg = GEMMA
     log("building the c4 Gemma-4-style block (int4 quantization on the GPU) ...")
-    h, xe, xm, W, ex, lora, gy = build_gemma_block(dev, cfg)
-    hg, xeg, xmg = (t.clone().requires_grad_(True) for t in (h, xe, xm))
+    h, a, W, ex, lora, gy = build_gemma_block(dev, cfg)
+    hg, ag = (t.clone().requires_grad_(True) for t in (h, a))
     params = list(lora.parameters())
     seen = {}
 
     def step(stats=None):
-        for t in (hg, xeg, xmg):
+        for t in (hg, ag):
             t.grad = None
         for p in params:
             p.grad = None
-        m = mlp_lora(xmg, W["mlp.gate_proj.weight"], W["mlp.up_proj.weight"], W["mlp.down_proj.weight"],
-                     lora.shared, cfg["act"], W["mlp.gate_up_proj.weight"])
-        probs, topv, topi = route_gemma4(hg, W, cfg["K"], 1e-6)
-        if stats is not None:
-            stats(probs, topv, topi)
-        e = routed_experts(xeg, topv, topi, ex, lora.experts)
-        (m + e).backward(gy)
+        gemma_block(hg, ag, W, ex, lora, cfg["K"], stats=stats).backward(gy)
 
     step(stats=lambda p, v, i: seen.update(topi=i))
     sel = torch.zeros(cfg["E"], dtype=torch.bool, device=dev)
@@ -390,36 +429,64 @@ def run_gemma(args, dev):
     log("per-launch ms:", json.dumps(bd))
     roof = roofline(bd, dict(cfg, fused_shared=False), S)
     emit("MoE block fwd+bwd tokens/s (Gemma-4-26B-A4B shape, T=4096)", cfg["T"], args, timing,
-         "C4: Gemma-4-26B-A4B-style MoE block fwd+bwd: route_gemma4, 128 GELU-tanh experts I=704 top-8 (116 int4 g64 + "
-         "12 bf16 LoRA r16), dense GeGLU MLP 2112 + LoRA r16, T=4096, H=2816 (block RMSNorms excluded)",
+         "C4: Gemma-4-26B-A4B-style MoE block fwd+bwd from the attention output on: 6 RMSNorms, route_gemma4, 128 "
+         "GELU-tanh experts I=704 top-8 (116 int4 g64 + 12 bf16 LoRA r16), dense GeGLU MLP 2112 + LoRA r16, residual "
+         "adds and layer scalar, T=4096, H=2816",
          {"selected_slots": S}, roof, bd, None)
 
 
-def cpu_baseline(x, W, ex, lora, gy, cfg):
-    """The oracle (CPU restatement of the reference's CPU torch path, fp32) on one full pass of the same layer."""
+def _cpu_threads():
+    """Threads for the CPU baseline: every CPU this process may run on, capped at the job's CPU share when the
+    environment states one (OMP_NUM_THREADS on the GPU boxes), since more threads than that share oversubscribe."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(share)) if share.isdigit() and int(share) > 0 else n
+
+
+def _physical_cores():
+    """Distinct (physical id, core id) pairs of /proc/cpuinfo, or None."""
+    try:
+        cores, phys = set(), "0"
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("physical id"):
+                phys = ln.split(":", 1)[1].strip()
+            elif ln.startswith("core id"):
+                cores.add((phys, ln.split(":", 1)[1].strip()))
+        return len(cores) or None
+    except OSError:
+        return None
+
+
+def cpu_baseline(x, W, ex, lora, gy, cfg, fwd_only=False):
+    """The oracle (CPU restatement of the reference's CPU torch path, fp32) on the same layer: 1 warmup pass, then
+    the median of 5 timed passes (forward only for C2, forward with autograd + backward for C3)."""
     from oracle import moe_ref as R
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
-    c = lambda t: t.detach().cpu()
-    fz = {"gate_up": {k: c(v) for k, v in ex.frozen.gu.items()}, "down": {k: c(v) for k, v in ex.frozen.dn.items()}}
-    names = ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")
-    Is = cfg["Is"]
-    ol = R.OracleLayer(gate_w=c(W["mlp.gate.weight"]), frozen=fz, int4=True, sel_ids=[int(e) for e in ex.sel_ids],
-                       sel_gate_up=c(ex.sel_gate_up), sel_down=c(ex.sel_down),
-                       ex_lora={n: c(getattr(lora.experts, n)) for n in names}, ex_scale=lora.experts.scale,
-                       shared={"gate_up": torch.cat((c(W["mlp.shared_expert.gate_proj.weight"]),
-                                                     c(W["mlp.shared_expert.up_proj.weight"]))),
-                               "down": c(W["mlp.shared_expert.down_proj.weight"]),
-                               "gate_w": c(W["mlp.shared_expert_gate.weight"])},
-                       sh_lora={n: c(getattr(lora.shared, n)) for n in names}, sh_scale=lora.shared.scale,
-                       deq_dtype=torch.bfloat16)
-    assert ol.shared["down"].shape[1] == Is
-    t0 = time.perf_counter()
-    R.moe_forward_backward(c(x), ol, cfg["K"], c(gy), dtype=torch.float32)
-    dt = time.perf_counter() - t0
-    return {"value": round(cfg["T"] / dt, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"1 fwd+bwd pass of the full C3 layer (T={cfg['T']}), fp32, {dt:.1f} s, "
-                      f"torch threads={cores}, cpu={_cpu_model()}"}
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    ol = R.OracleLayer.from_api(W, ex, lora)
+    ol.deq_dtype = torch.bfloat16
+    assert ol.shared is not None and ol.shared["down"].shape[1] == cfg["Is"]
+    xc, gc = x.detach().cpu(), gy.detach().cpu()
+
+    def one():
+        if fwd_only:
+            with torch.no_grad():
+                R.moe_forward(xc, ol, cfg["K"], dtype=torch.float32)
+        else:
+            R.moe_forward_backward(xc, ol, cfg["K"], gc, dtype=torch.float32)
+
+    one()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        one()
+        ts.append(time.perf_counter() - t0)
+    dt = statistics.median(ts)
+    what = "forward" if fwd_only else "fwd+bwd"
+    return {"value": round(cfg["T"] / dt, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{what} of the full layer (T={cfg['T']}) by the oracle, fp32: 1 warmup + median of 5 passes "
+                      f"= {dt:.2f} s (range {min(ts):.2f}-{max(ts):.2f}); torch threads={threads}; host: "
+                      f"{os.cpu_count()} logical CPUs, {_physical_cores()} physical cores, {_cpu_model()}"}
 
 
 COPY_BYTES = 1 << 30
@@ -668,7 +735,7 @@ def run_quant(args, dev):
     cpu = None
     if not args.no_cpu_baseline:
         w = gu[:1].cpu()
-        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        torch.set_num_threads(_cpu_threads())
         t0 = time.perf_counter()
         quant._quantize_int4_host(w, 64)
         dt = time.perf_counter() - t0
@@ -721,7 +788,7 @@ def run_ce(args, dev):
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import loss_ref as LR
-        torch.set_num_threads(min(16, os.cpu_count() or 1))
+        torch.set_num_threads(_cpu_threads())
         ns = 32
         t0 = time.perf_counter()
         LR.full_ce(h[:ns].float(), W.float(), tgt[:ns], 0.0, float(T))

@@ -115,23 +115,24 @@ int smel_pack_bf16_t(const uint16_t* w, int64_t n_mats, int64_t R, int64_t C, in
 int smel_int4_fast_ok(const uint16_t* scale, const uint16_t* zero, int64_t n, int32_t* ok, hipStream_t stream);
 
 /* ---- (A1) replaces route, smel/moe.py:162-167, plus the shared-expert gate logit of smel/moe.py:201.
- * x [T][H], gate_w [E][H] bf16 (E <= 256), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the
+ * x [T][H], gate_w [E][H] bf16 (E <= 512), shared_gate_w [H] or NULL. Writes probs [T][E] fp32 (softmax of the
  * bf16-rounded logits), topv [T][K] bf16 (renormalised), topi [T][K] int64 and topi32 [T][K] int32 (descending,
  * lower expert id first among equal logits), and, if shared_gate_w, sgate [T] fp32 = sigmoid(bf16(x . w_sg)).
+ * topv32 [T][K] (optional) receives fp32(topv), the combine weight of the reference (topv.float(), :252).
  * logits [T][smel_route_ld(E, shared_gate_w != NULL)] bf16 is the caller's workspace; it is left holding the
  * bf16 logits (expert e in column e, the shared-gate logit in column ceil32(E)). */
 int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T, int64_t H,
-               int64_t E, int64_t K, float* probs, uint16_t* topv, int64_t* topi, int32_t* topi32, float* sgate,
-               uint16_t* logits, hipStream_t stream);
+               int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi, int32_t* topi32,
+               float* sgate, uint16_t* logits, hipStream_t stream);
 /* Row stride (elements) of smel_route's logits workspace (host-side, no GPU call); -1 for E <= 0. */
 int64_t smel_route_ld(int64_t E, int32_t with_shared_gate);
 
-/* Same selection from given bf16 logits [T][E] (bit-exact id checks against the CPU oracle). */
+/* Same selection from given bf16 logits [T][E], E <= 512 (bit-exact id checks against the CPU oracle). */
 int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, int64_t K, float* probs, uint16_t* topv,
                       int64_t* topi, int32_t* topi32, hipStream_t stream);
 
 /* ---- (A2) replaces route_gemma4, smel/moe.py:170-180 (the Gemma 4 router on the residual stream).
- * h [T][H] bf16, router_scale [H], proj_w [E][H], per_expert_scale [E] bf16 (E <= 256, H a multiple of 64):
+ * h [T][H] bf16, router_scale [H], proj_w [E][H], per_expert_scale [E] bf16 (E <= 512, H a multiple of 64):
  *   xn = bf16(bf16(bf16(h r) * router_scale) * H^-1/2), r = rstd[t] = (mean_j h[t][j]^2 + eps)^-1/2 (fp32),
  *   logits = bf16(xn proj_w^T), probs = softmax (fp32), top-k as smel_route, topv [T][K] fp32 = renormalised value
  *   * per_expert_scale[id]. xn [T][H], rstd [T] and logits [T][smel_route_ld(E, 0)] are caller workspaces, left
@@ -201,15 +202,17 @@ int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
                  int64_t ldo, uint16_t* hsave, hipStream_t stream);
 
 /* ---- (A13) replaces the combine of routed_experts, smel/moe.py:248-252 (+ the shared add of :263):
- * out[t] = bf16( sum_k fp32(topv[t,k]) * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Y[TK+t])] ), k in fixed order. */
-int smel_combine(const uint16_t* Y, const uint16_t* topv, const float* sgate, int64_t T, int64_t K, int64_t H,
-                 uint16_t* out, hipStream_t stream);
+ * out[t] = bf16( sum_k topv[t,k] * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Y[TK+t])] ), k in fixed order, topv fp32.
+ * inv [T*K] (optional, smel_dispatch's): a slot with inv < 0 (an expert id out of range, dropped by the dispatch)
+ * adds nothing. */
+int smel_combine(const uint16_t* Y, const float* topv, const int32_t* inv, const float* sgate, int64_t T, int64_t K,
+                 int64_t H, uint16_t* out, hipStream_t stream);
 
 /* ---- (A10/A11 backward) grouped GEMM, backward: acc = A W per group (contraction over w.R), W in the transposed
  * layouts (smel_pack_int4_t / smel_pack_bf16_t), int4 re-dequantized in registers, plus ext[row] . w.ext_*[n][0:32]
  * for SEL/SHARED groups when ext != NULL. acc is rounded to bf16 before the epilogue (the reference's bf16 GEMM output).
  * epilogue 0: out[slot(row)][n] = bf16(acc), n < C                                   (dX of gate_up: dh W_gu)
- * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] or sgate[t]; (g, u) = hsave[row];
+ * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] (fp32) or sgate[t]; (g, u) = hsave[row];
  *             out[row][n] = bf16(da u act'(g)), out[row][I+n] = bf16(da act(g));
  *             dwp[row][j] = sum over column block j of acc * bf16(act(g) u)   (d row weight, reduced later in
  *             fixed order); dwp holds (rows) x smel_gmm_bwd_nblocks(C) floats; bf16(act(g) u) is read from actsave
@@ -219,7 +222,7 @@ int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
                  int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                  const int32_t* order,
                  int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
-                 const uint16_t* hsave, const uint16_t* actsave, const uint16_t* topv, const float* sgate,
+                 const uint16_t* hsave, const uint16_t* actsave, const float* topv, const float* sgate,
                  uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream);
 /* number of column blocks (dwp row width) smel_gmm_bwd uses for a given C */
 int64_t smel_gmm_bwd_nblocks(int64_t C);
@@ -231,23 +234,23 @@ int64_t smel_gmm_bwd_nblocks(int64_t C);
  * per_expert_scale [E] bf16 (optional, route_gemma4): the routed value was renorm * per_expert_scale[id], so dtopv
  * is multiplied by it before the renorm backward. */
 int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs, const int32_t* topi32,
-                   const uint16_t* topv, const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK,
-                   uint16_t* dlogits, int64_t ldl, float* dtopv_out, const uint16_t* per_expert_scale,
-                   hipStream_t stream);
+                   const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK, uint16_t* dlogits, int64_t ldl,
+                   float* dtopv_out, const uint16_t* per_expert_scale, hipStream_t stream);
 
 /* d(combine weight) of routed_experts when topv is an input: dtopv[p] = sum_j dwp[inv[p]][j], fp32 [TK]. */
 int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, float* dtopv, hipStream_t stream);
 
-/* ---- dX of the layer: dx[t] = bf16( sum_k DXS[t*K+k] + [DXS[TK+t]] + [DXR[t]] ), fixed order, fp32. */
-int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, int32_t with_shared, int64_t T, int64_t K, int64_t H,
-                   uint16_t* dx, hipStream_t stream);
+/* ---- dX of the layer: dx[t] = bf16( sum_k DXS[t*K+k] + [DXS[TK+t]] + [DXR[t]] ), fixed order, fp32; slots with
+ * inv < 0 (inv optional, as in smel_combine) add nothing. */
+int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, const int32_t* inv, int32_t with_shared, int64_t T,
+                   int64_t K, int64_t H, uint16_t* dx, hipStream_t stream);
 
 /* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP), up to four
  * products in one launch. For job j and every LoRA group lora_groups[i] (expert id, or E for the shared rows
  * [TK, TK+T)):
  *   R[p][q] = sum_{rows of the group} alpha(row) * L[row][p] * Rm[src(row)][q],  p < 32, q < Q
  * summed in one fixed order (deterministic). src(row) = token of the row if r_gather else row; Rm holds r_rows rows;
- * alpha = the row weight (topv[p] / sgate[t]) if use_w, else 1 (folded into L before its bf16 rounding).
+ * alpha = the row weight (topv[p] fp32 / sgate[t]) if use_w, else 1 (folded into L before its bf16 rounding).
  * Each R[p][q] with p in [p0, p0+np) and q in [q0, q0+nq) of a destination is stored (fp32) at
  *   ptr[slot * s_idx + (p - p0) * s_p + (q - q0) * s_q],
  * dest[0][h] for groups i < n_sel (slot = i, the selected experts' LoRA tensors), dest[1][h] for the others (slot 0,
@@ -272,7 +275,7 @@ typedef struct smel_wg_job {
 int64_t smel_lora_wgrad_ws_floats(const smel_wg_job* jobs, int32_t n_jobs, int64_t n_lora, int64_t max_rows);
 int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const int32_t* lora_groups, int64_t n_lora,
                     int64_t n_sel, const int32_t* offsets, int64_t E, int64_t T, int64_t TK, int64_t topk,
-                    const int32_t* order, const uint16_t* topv, const float* sgate, int64_t max_rows, float* ws,
+                    const int32_t* order, const float* topv, const float* sgate, int64_t max_rows, float* ws,
                     int64_t ws_floats, hipStream_t stream);
 
 #ifdef __cplusplus

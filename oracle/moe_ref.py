@@ -19,6 +19,8 @@ PINNED — what checks each function against something other than its own formul
   act / act_and_grad .... torch.autograd.gradcheck in fp64 + torch.nn.functional [::test_act_grad]
   lora_linear/_gate_up .. plain fp64 formula and its autograd [::test_lora_plain_formula]
   routed_experts ........ golden reference output (C1) [::test_routed_golden]
+  gemma4_moe_block ...... composed of the pinned parts (route_gemma4, mlp_lora, routed_experts) and the pinned torch
+                          RMSNorm of norm_ref; fp64 per-token brute force of the whole block [::test_gemma4_block]
   moe_forward + backward  golden reference y, dX, LoRA dA/dB (C1, with and without selected experts), fp64
                           brute force per token [::test_moe_golden, ::test_moe_bruteforce]
 """
@@ -136,15 +138,20 @@ def route(x2d, gate_w, top_k, logits=None):
     return probs, topv.to(logits.dtype), topi
 
 
-def route_gemma4(h, W, top_k, eps):
+def route_gemma4(h, W, top_k, eps, forced_topi=None):
     """smel/moe.py:170-180: weightless RMSNorm of the residual stream in fp32, x router.scale x H^-0.5, logits,
-    softmax fp32, top-k, renormalise, x per_expert_scale of the chosen experts."""
+    softmax fp32, top-k, renormalise, x per_expert_scale of the chosen experts. ``forced_topi`` replaces the chosen
+    ids (topv stays differentiable through the softmax), as :func:`moe_forward` forces routing."""
     hf = h.float()
     x = (hf * torch.pow(hf.pow(2).mean(-1, keepdim=True) + eps, -0.5)).type_as(h)
     x = x * W["router.scale"] * h.shape[-1] ** -0.5
     logits = F.linear(x, W["router.proj.weight"])
     probs = torch.softmax(logits, dim=-1, dtype=torch.float32)
-    topv, topi = topk_lowest_index(probs, top_k)
+    if forced_topi is None:
+        topv, topi = topk_lowest_index(probs, top_k)
+    else:
+        topi = forced_topi.long()
+        topv = probs.gather(1, topi)
     topv = topv / topv.sum(dim=-1, keepdim=True)
     return probs, topv * W["router.per_expert_scale"][topi], topi
 
@@ -268,6 +275,38 @@ class OracleLayer:
     @property
     def E(self):
         return self.gate_w.shape[0]
+
+    @classmethod
+    def from_api(cls, W: dict, ex, lora=None, router_key: str = "mlp.gate.weight"):
+        """The layer held by the drop-in API's objects (the W dict of smel/moe.py:255-263, a LayerExperts and a
+        LayerLoRA; device tensors are copied to the CPU): the oracle then computes on exactly the weights a GPU layer
+        was built with. The LoRA of ``lora.shared`` is kept in ``sh_lora`` also without a shared expert (Gemma 4's
+        dense MLP takes the layer's shared LoRA, smel/layer_runner.py:249-254)."""
+        c = lambda t: t.detach().cpu()
+        fz = ex.frozen
+        int4 = hasattr(fz, "gu")
+        frozen = ({"gate_up": {k: c(v) for k, v in fz.gu.items()}, "down": {k: c(v) for k, v in fz.dn.items()}}
+                  if int4 else {"gate_up": c(fz.gate_up), "down": c(fz.down)})
+        sel = [int(e) for e in ex.sel_ids] if ex.sel_ids is not None else []
+        L = cls(gate_w=c(W[router_key]), frozen=frozen, int4=int4, sel_ids=sel, act=ex.act,
+                deq_dtype=getattr(fz, "dtype", torch.bfloat16))
+        names = ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")
+        if sel:
+            L.sel_gate_up, L.sel_down = c(ex.sel_gate_up), c(ex.sel_down)
+            if lora is not None and lora.experts is not None:
+                L.ex_lora = {n: c(getattr(lora.experts, n)).float() for n in names}
+                L.ex_scale = float(lora.experts.scale)
+        pre = "mlp.shared_expert."
+        if pre + "down_proj.weight" in W:
+            gu = W.get(pre + "gate_up_proj.weight")
+            if gu is None:
+                gu = torch.cat((W[pre + "gate_proj.weight"], W[pre + "up_proj.weight"]))
+            L.shared = {"gate_up": c(gu), "down": c(W[pre + "down_proj.weight"]),
+                        "gate_w": c(W["mlp.shared_expert_gate.weight"]).reshape(1, -1)}
+        if lora is not None and lora.shared is not None:
+            L.sh_lora = {n: c(getattr(lora.shared, n)).float() for n in names}
+            L.sh_scale = float(lora.shared.scale)
+        return L
 
     def frozen_weights(self, e0, e1, dtype):
         """Int4Experts.weights / BF16Experts.weights (smel/moe.py:25-26, 46-49) in the compute dtype."""
@@ -454,6 +493,64 @@ def moe_forward_backward(x2d, layer: OracleLayer, top_k, gy, forced_topi=None, d
         layer.ex_lora, layer.sh_lora = saved
     return y.detach(), x.grad.detach(), {k: v.grad.detach() if v.grad is not None else torch.zeros_like(v)
                                          for k, v in leaves.items()}
+
+
+# ------------------------------------------------------------------------------------ Gemma 4 MoE block (C4)
+
+GEMMA4_NORMS = ("post_attention_layernorm", "pre_feedforward_layernorm", "post_feedforward_layernorm_1",
+                "pre_feedforward_layernorm_2", "post_feedforward_layernorm_2", "post_feedforward_layernorm")
+
+
+def gemma4_moe_block(h, a, W: dict, layer: OracleLayer, top_k: int, eps: float, forced_topi=None,
+                     dtype=torch.float32):
+    """The Gemma 4 decoder layer from the attention output on (smel/layer_runner.py:243-262): the residual add with
+    the post-attention norm, the pre-feed-forward norm, the dense GeGLU MLP with the layer's shared LoRA
+    (smel/moe.py:183-194) and its post norm, route_gemma4 on the residual stream, the experts on their own pre norm
+    and their post norm, the final norm of the sum, the residual add and the layer scalar. Every norm is the
+    reference's torch RMSNorm with a plain weight (plus_one=False). h: residual stream, a: attention output.
+    Returns (out, (probs, topv, topi))."""
+    from .norm_ref import torch_rmsnorm
+
+    wt = lambda k: W[k].to(dtype)
+    rn = lambda x, name: torch_rmsnorm(x, wt(name + ".weight"), eps, plus_one=False)
+    h = h.to(dtype)
+    h2 = h + rn(a.to(dtype), "post_attention_layernorm")
+    xm = rn(h2, "pre_feedforward_layernorm")
+    gu = W.get("mlp.gate_up_proj.weight")
+    if gu is None:
+        gu = torch.cat((W["mlp.gate_proj.weight"], W["mlp.up_proj.weight"]))
+    m = mlp_lora(xm, gu.to(dtype), wt("mlp.down_proj.weight"), layer.sh_lora, layer.sh_scale, layer.act)
+    m = rn(m, "post_feedforward_layernorm_1")
+    rw = {k: wt(k) for k in ("router.scale", "router.proj.weight", "router.per_expert_scale")}
+    probs, topv, topi = route_gemma4(h2, rw, top_k, eps, forced_topi)
+    e = routed_experts(rn(h2, "pre_feedforward_layernorm_2"), topv, topi, layer, layer.ex_lora, dtype)
+    e = rn(e, "post_feedforward_layernorm_2")
+    out = (h2 + rn(m + e, "post_feedforward_layernorm")) * wt("layer_scalar")
+    return out, (probs, topv, topi)
+
+
+def gemma4_block_forward_backward(h, a, W: dict, layer: OracleLayer, top_k, eps, gy, forced_topi=None,
+                                  dtype=torch.float32):
+    """Forward with autograd + backward of :func:`gemma4_moe_block`. Returns (out, dh, da, {name: grad}) with the
+    LoRA gradients keyed ``ex_*`` (experts) and ``sh_*`` (the dense MLP)."""
+    hh = h.to(dtype).clone().requires_grad_(True)
+    aa = a.to(dtype).clone().requires_grad_(True)
+    leaves = {}
+    saved = (layer.ex_lora, layer.sh_lora)
+    for tag in ("ex", "sh"):
+        L = getattr(layer, tag + "_lora")
+        if L is None:
+            continue
+        new = {k: v.detach().to(dtype).clone().requires_grad_(True) for k, v in L.items()}
+        leaves.update({f"{tag}_{k}": v for k, v in new.items()})
+        setattr(layer, tag + "_lora", new)
+    try:
+        out, _ = gemma4_moe_block(hh, aa, W, layer, top_k, eps, forced_topi, dtype)
+        out.backward(gy.to(dtype))
+    finally:
+        layer.ex_lora, layer.sh_lora = saved
+    return out.detach(), hh.grad.detach(), aa.grad.detach(), {
+        k: v.grad.detach() if v.grad is not None else torch.zeros_like(v) for k, v in leaves.items()}
 
 
 # --------------------------------------------------------------------------------------- synthetic layers (C1-C5)

@@ -161,6 +161,18 @@ SMEL_DEV void ld16_lds(rsrc_t r, const void* lds, uint32_t off) {
 #define SMEL_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 // ... and on LDS as well (lgkmcnt = 0): this wave's own LDS reads are done.
 #define SMEL_WAIT_VM_LDS(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+// The same waits with the count checked at compile time. A pipelined main loop computes N from the per-group load
+// counts its issue code is written with (constexpr), so a count cannot drift from the loads actually issued.
+template <int N>
+SMEL_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt counts 0..63 outstanding vector-memory operations");
+  SMEL_WAIT_VM(N);
+}
+template <int N>
+SMEL_DEV void wait_vm_lds() {
+  static_assert(N >= 0 && N < 64, "vmcnt counts 0..63 outstanding vector-memory operations");
+  SMEL_WAIT_VM_LDS(N);
+}
 
 // Operand tiles in LDS hold rows of 64 bf16 (128 B) without padding; the physical 16-B chunk of logical chunk c of
 // row r is c ^ swz(r), so 8 (or 16) lanes reading consecutive rows at one logical chunk touch distinct banks with 32

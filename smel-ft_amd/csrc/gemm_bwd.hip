@@ -37,6 +37,18 @@ constexpr int q_stage(bool sz2) { return A_BYTES + z_bytes(sz2); }
 constexpr int smem_bytes(bool sz2) { return 4 * q_stage(sz2); }
 static_assert(smem_bytes(false) <= 80 * 1024 && 4 * A_BYTES + 512 <= smem_bytes(false), "two blocks per CU");
 
+// Vector-memory operations per wave in each issue group of the main loops; the issue code below is written with
+// these counts and every wait is computed from them (vmcnt retires in issue order).
+constexpr int VM_A = A_BYTES / (4 * 1024);                 // A rows of a stage: 1-KB LDS-DMA wave-loads, 4 waves
+constexpr int VM_Q = 2;                                     // int4: 16-B words of the two column pairs
+constexpr int vm_sz(bool sz2) { return sz2 ? 4 : 2; }       // int4: 256-B scale/zero runs, per group
+constexpr int vm_q4(bool sz2) { return VM_Q + vm_sz(sz2) + VM_A; }
+constexpr int VM_B = 2 * 4;                                 // bf16: 2 substeps x 4 column fragments
+// int4: steps j+1 and j+2 may be in flight while step j computes; bf16: issue order ... W(j+1), A(j+3), so before
+// step j only A(j+2) may be
+constexpr int q4_wait(bool sz2) { return 2 * vm_q4(sz2); }
+constexpr int BF_WAIT = VM_A;
+
 struct BwdArgs {
   smel_wset w;
   const int32_t* gkind;
@@ -49,7 +61,7 @@ struct BwdArgs {
   const uint16_t* ext;
   const uint16_t* hsave;
   const uint16_t* actsave;   // the forward's bf16 act(g) u rows (epilogue 1)
-  const uint16_t* topv;
+  const float* topv;
   const float* sgate;
   uint16_t* out;
   int64_t ldo;
@@ -102,7 +114,7 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     if (EPI == 0)
       ep_slot = row_slot(grow, a.order, a.TK);
     else
-      ep_w = grow < a.TK ? bf2f(a.topv[a.order[grow]]) : a.sgate[grow - a.TK];
+      ep_w = grow < a.TK ? a.topv[a.order[grow]] : a.sgate[grow - a.TK];
   }
   const int cw = nb * NB + w * 64;   // this wave's first output column
   const int nk = (Kd + KT - 1) / KT;
@@ -140,10 +152,10 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   // physical chunk i % 8 of row 8 g + i / 8, i.e. logical chunk c = (i % 8) ^ swz(row). Kd is a multiple of 64, so a
   // k-step is all in or all out.
   const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
-  uint32_t aoff[4];
+  uint32_t aoff[VM_A];
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const int g = 4 * w + ii;
+  for (int ii = 0; ii < VM_A; ++ii) {
+    const int g = VM_A * w + ii;
     const int row = 8 * g + (l >> 3);
     const int c = (l & 7) ^ swz(row);
     aoff[ii] = OOB;
@@ -160,17 +172,16 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     const uint32_t k2 = (uint32_t)j * KT * 2;
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (Q4) {
+      static_assert(VM_Q == 2, "one word per column pair, 2 pairs");
       qd[0] = ld16(rw, in ? wo + j * 1024 : OOB);
       qd[1] = ld16(rw1, in ? wo + j * 1024 : OOB);
-      ld4_lds(rsz, Zt(st) + w * ZW, in ? so + j * 512 : OOB);
-      ld4_lds(rsz, Zt(st) + w * ZW + 256, in ? so + j * 512 + 256 : OOB);
-      if constexpr (SZ2) {
-        ld4_lds(rsz1, Zt(st) + w * ZW + 512, in ? so + j * 512 : OOB);
-        ld4_lds(rsz1, Zt(st) + w * ZW + 768, in ? so + j * 512 + 256 : OOB);
-      }
+      // vm_sz(SZ2) runs of 256 B: (scale, zero) of the 64 rows, per group of the wave's columns
+#pragma unroll
+      for (int z = 0; z < vm_sz(SZ2); ++z)
+        ld4_lds(z < 2 ? rsz : rsz1, Zt(st) + w * ZW + 256 * z, in ? so + j * 512 + 256 * (z & 1) : OOB);
     }
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) ld16_lds(ra, St(st) + (4 * w + ii) * 512, in ? aoff[ii] + k2 : OOB);
+    for (int ii = 0; ii < VM_A; ++ii) ld16_lds(ra, St(st) + (VM_A * w + ii) * 512, in ? aoff[ii] + k2 : OOB);
     __builtin_amdgcn_sched_barrier(0);
   };
   // A fragment reads: lane (kq, li) of row-fragment rf, substep s reads logical chunk 4 s + kq of row 16 rf + li
@@ -265,11 +276,10 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     };
     // 4-stage ring (q: 4 register sets), three steps ahead: before step j, steps j+1 and j+2 may be in flight.
-    constexpr int NV = 2 + (SZ2 ? 4 : 2) + 4;   // vector-memory ops per step: 2 q, 2-4 scale/zero, 4 A
-    u32x4_t qa[2], qb[2], qc[2], qe[2];
+    u32x4_t qa[VM_Q], qb[VM_Q], qc[VM_Q], qe[VM_Q];
     u32x4_t* const qs[4] = {qa, qb, qc, qe};
     auto step = [&](int j, int st) {
-      SMEL_WAIT_VM_LDS(2 * NV);
+      wait_vm_lds<q4_wait(SZ2)>();
       __builtin_amdgcn_s_barrier();
       issue_lds(j + 3, (st + 3) & 3, qs[(st + 3) & 3]);
       compute(st, qs[st]);
@@ -304,6 +314,7 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     // alternating register sets; A three steps ahead in a 4-stage ring. Issue order W(j+1), A(j+3): before step j
     // only A(j+2)'s 4 loads may still be in flight.
     u32x4_t bA[2][4], bB[2][4];   // [substep][column fragment]
+    static_assert(VM_B == 2 * 4, "2 substeps x 4 column fragments");
     auto issue_b = [&](int j, u32x4_t (*b)[4]) {
       const bool in = j < nk;
       __builtin_amdgcn_sched_barrier(0);
@@ -324,29 +335,29 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     issue_b(0, bA);
     issue_lds(2, 2, nullptr);
     for (int i = 0; i < nk; i += 4) {
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 1, bB);
       issue_lds(i + 3, 3, nullptr);
       compute(0, bA);
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 2, bA);
       issue_lds(i + 4, 0, nullptr);
       compute(1, bB);
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 3, bB);
       issue_lds(i + 5, 1, nullptr);
       compute(2, bA);
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 4, bA);
       issue_lds(i + 6, 2, nullptr);
       compute(3, bB);
     }
   }
-  SMEL_WAIT_VM(0);   // the ring's trailing (out-of-range) loads
+  wait_vm<0>();   // the ring's trailing (out-of-range) loads
   // ---- LoRA K-extension: ext[row][0:32] . Eb[n][0:32] (one 32-wide substep)
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
@@ -522,7 +533,7 @@ extern "C" int64_t smel_gmm_bwd_nblocks(int64_t C) { return (C + NB - 1) / NB; }
 extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                             int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
-                            int32_t act, const uint16_t* hsave, const uint16_t* actsave, const uint16_t* topv,
+                            int32_t act, const uint16_t* hsave, const uint16_t* actsave, const float* topv,
                             const float* sgate, uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
   SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->R && topk > 0, SMEL_EINVAL,

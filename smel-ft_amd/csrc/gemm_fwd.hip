@@ -27,6 +27,19 @@ constexpr int MT = 128;
 constexpr int KT = 64;
 constexpr int A_STAGE = MT * KT;   // bf16 elements of one A stage: row r at r * KT, no padding
 
+// Vector-memory operations per wave in each issue group of the main loops; the issue code below is written with
+// these counts and every wait is computed from them (vmcnt retires in issue order).
+constexpr int VM_A = A_STAGE * 2 / (4 * 1024);   // A rows of a stage: 1-KB LDS-DMA wave-loads, 4 waves
+constexpr int VM_Q = 2;                           // int4: one 16-B word per weight fragment, 2 fragments
+constexpr int VM_SZ = 2;                          // int4: the packed scale/zero run of 4 k-steps, per fragment
+constexpr int VM_B = 2 * 4;                       // bf16: 4 substep chunks per fragment, 2 fragments
+// int4: the group of step j carries the scale/zero run iff j % 4 == 0; while step j (round position pos = j % 4)
+// computes, the groups of steps j+1 and j+2 may still be in flight
+constexpr int q4_group(int j) { return VM_Q + (j % 4 == 0 ? VM_SZ : 0) + VM_A; }
+constexpr int q4_wait(int pos) { return q4_group(pos + 1) + q4_group(pos + 2); }
+// bf16: issue order ... B(j+1), A(j+3): before step j only the last group, A(j+2), may be in flight
+constexpr int BF_WAIT = VM_A;
+
 struct FwdArgs {
   smel_wset w;
   const int32_t* gkind;
@@ -99,11 +112,11 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   // physical chunk i % 8 of row 8 g + i / 8, i.e. logical chunk c = (i % 8) ^ swz(row).
   const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
   const int li = tid & 63;
-  uint32_t aoff[4];
-  int akc[4];   // first k of this lane's chunk
+  uint32_t aoff[VM_A];
+  int akc[VM_A];   // first k of this lane's chunk
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const int g = 4 * w + ii;
+  for (int ii = 0; ii < VM_A; ++ii) {
+    const int g = VM_A * w + ii;
     const int row = 8 * g + (li >> 3);
     const int c = (li & 7) ^ swz(row);
     akc[ii] = 8 * c;
@@ -118,8 +131,8 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     const int k0 = j * KT;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii)
-      ld16_lds(ra, S + (4 * w + ii) * 512, (k0 + akc[ii] + 8 <= K) ? aoff[ii] + k0 * 2 : OOB);
+    for (int ii = 0; ii < VM_A; ++ii)
+      ld16_lds(ra, S + (VM_A * w + ii) * 512, (k0 + akc[ii] + 8 <= K) ? aoff[ii] + k0 * 2 : OOB);
     __builtin_amdgcn_sched_barrier(0);
   };
   // A fragment reads: lane (r32, h) of slice m, substep s reads logical chunk 4 h + s of row 32 m + r32
@@ -143,15 +156,17 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   if constexpr (Q4) {
     // Group of loads for step j: q (2), then, when j % 4 == 0, the packed (scale, zero) run of steps j..j+3 (2),
     // then A (4). Groups j+1, j+2 are in flight while step j computes; group j+3 is issued after its barrier.
-    u32x4_t q0[2], q1[2], q2[2], q3[2], szc[2], szn[2];
+    static_assert(VM_Q == 2 && VM_SZ == 2, "one q word and one scale/zero run per fragment, 2 fragments");
+    u32x4_t q0[VM_Q], q1[VM_Q], q2[VM_Q], q3[VM_Q], szc[VM_SZ], szn[VM_SZ];
+    const uint32_t wof[VM_Q] = {wo0, wo1}, sof[VM_SZ] = {so0, so1};
     auto issue = [&](int j, u32x4_t* q, u32x4_t* z, uint16_t* S) {
       const bool in = j < nk;
-      q[0] = ld16(rw, in ? wo0 + j * 1024 : OOB);
-      q[1] = ld16(rw, in ? wo1 + j * 1024 : OOB);
-      if (z) {
+#pragma unroll
+      for (int f = 0; f < VM_Q; ++f) q[f] = ld16(rw, in ? wof[f] + j * 1024 : OOB);
+      if (z) {   // exactly the steps with j % 4 == 0 (q4_group)
         const bool zin = (j >> 2) < nk4;
-        z[0] = ld16(rsz, zin ? so0 + (j >> 2) * 1024 : OOB);
-        z[1] = ld16(rsz, zin ? so1 + (j >> 2) * 1024 : OOB);
+#pragma unroll
+        for (int f = 0; f < VM_SZ; ++f) z[f] = ld16(rsz, zin ? sof[f] + (j >> 2) * 1024 : OOB);
       }
       issue_a(j, S);   // sched barriers keep the group's loads in this order, ahead of the step's compute
     };
@@ -179,19 +194,19 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     issue(2, q2, nullptr, S2);
     // ceil(nk / 4) * 4 steps, branch-free: a step past K loads zeros and adds nothing
     for (int i = 0; i < nk; i += 4) {
-      SMEL_WAIT_VM_LDS(12);
+      wait_vm_lds<q4_wait(0)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 3, q3, nullptr, S3);
       compute(S0, q0, 0);
-      SMEL_WAIT_VM_LDS(12);
+      wait_vm_lds<q4_wait(1)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 4, q0, szn, S0);
       compute(S1, q1, 1);
-      SMEL_WAIT_VM_LDS(14);
+      wait_vm_lds<q4_wait(2)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 5, q1, nullptr, S1);
       compute(S2, q2, 2);
-      SMEL_WAIT_VM_LDS(14);
+      wait_vm_lds<q4_wait(3)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 6, q2, nullptr, S2);
       compute(S3, q3, 3);
@@ -201,6 +216,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   } else {
     // bf16 weights: 8 loads per fragment pair and step, one step ahead in two alternating register sets; A three
     // steps ahead. Issue order B(j+1), A(j+3): before step j only A(j+2) may still be in flight.
+    static_assert(VM_B == 2 * 4, "2 fragments x 4 substep chunks");
     u32x4_t bA[2][4], bB[2][4];
     auto issue_b = [&](int j, u32x4_t (*b)[4]) {
       const bool in = j < nk;
@@ -220,29 +236,29 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     issue_b(0, bA);
     issue_a(2, S2);
     for (int i = 0; i < nk; i += 4) {
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 1, bB);
       issue_a(i + 3, S3);
       compute(S0, bA);
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 2, bA);
       issue_a(i + 4, S0);
       compute(S1, bB);
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 3, bB);
       issue_a(i + 5, S1);
       compute(S2, bA);
-      SMEL_WAIT_VM_LDS(4);
+      wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 4, bA);
       issue_a(i + 6, S2);
       compute(S3, bB);
     }
   }
-  SMEL_WAIT_VM(0);   // the ring's trailing (out-of-range) loads
+  wait_vm<0>();   // the ring's trailing (out-of-range) loads
   // ---- LoRA K-extension: ext[row][0:32] . Bext[n][0:32]
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);

@@ -221,7 +221,7 @@ struct WgArgs {
   const int32_t* offsets;
   int E, T, TK, topk;
   const int32_t* order;
-  const uint16_t* topv;
+  const float* topv;
   const float* sgate;
 };
 
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
         if (row < a.TK) {
           const int p = a.order[row];
           if (r_gather) src = p / a.topk;
-          if (use_w) alpha = bf2f(a.topv[p]);
+          if (use_w) alpha = a.topv[p];
         } else {
           if (r_gather) src = row - a.TK;
           if (use_w) alpha = a.sgate[row - a.TK];
@@ -490,7 +490,7 @@ extern "C" int64_t smel_lora_wgrad_ws_floats(const smel_wg_job* jobs, int32_t n_
 
 extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const int32_t* lora_groups, int64_t n_lora,
                                int64_t n_sel, const int32_t* offsets, int64_t E, int64_t T, int64_t TK, int64_t topk,
-                               const int32_t* order, const uint16_t* topv, const float* sgate, int64_t max_rows,
+                               const int32_t* order, const float* topv, const float* sgate, int64_t max_rows,
                                float* ws, int64_t ws_floats, hipStream_t stream) {
   SMEL_REQUIRE(jobs && n_jobs >= 0 && n_jobs <= 4 && n_lora >= 0 && n_sel >= 0 && n_sel <= n_lora && max_rows >= 0,
                SMEL_EINVAL, "lora_wgrad: bad job / group counts");

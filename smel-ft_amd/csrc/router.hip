@@ -8,43 +8,44 @@
 
 namespace {
 
-constexpr int MAXE = 256;      // experts handled by the selection (4 logits per lane)
+constexpr int MAXE = 512;      // experts handled by the selection (up to 8 logits per lane)
 
-// Selection over one token's logits (held in LDS or global), by one wave. Writes probs, topi, topi32 and topv: bf16
-// (route), or fp32 times per_expert_scale[id] when topv_f32 is given (route_gemma4).
-template <typename Get>
+// Selection over one token's logits (held in LDS or global), by one wave; NPL = logits per lane (E <= 64 NPL).
+// Writes probs, topi, topi32 and the renormalised values: topv bf16 and topv32 = the same rounded value as fp32
+// (route), or topv_f32 = fp32 value times per_expert_scale[id] (route_gemma4).
+template <int NPL, typename Get>
 SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict__ probs, uint16_t* __restrict__ topv,
-                          int64_t* __restrict__ topi, int32_t* __restrict__ topi32, float* __restrict__ topv_f32,
-                          const uint16_t* __restrict__ pes) {
+                          float* __restrict__ topv32, int64_t* __restrict__ topi, int32_t* __restrict__ topi32,
+                          float* __restrict__ topv_f32, const uint16_t* __restrict__ pes) {
   const int l = lane_id();
-  float v[MAXE / 64];
+  float v[NPL];
 #pragma unroll
-  for (int j = 0; j < MAXE / 64; ++j) {
+  for (int j = 0; j < NPL; ++j) {
     const int e = l + 64 * j;
     v[j] = e < E ? logit(e) : -INFINITY;
   }
   float m = v[0];
 #pragma unroll
-  for (int j = 1; j < MAXE / 64; ++j) m = fmaxf(m, v[j]);
+  for (int j = 1; j < NPL; ++j) m = fmaxf(m, v[j]);
   m = wave_max(m);
-  float ex[MAXE / 64], s = 0.f;
+  float ex[NPL], s = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXE / 64; ++j) {
+  for (int j = 0; j < NPL; ++j) {
     ex[j] = (l + 64 * j) < E ? expf(v[j] - m) : 0.f;
     s += ex[j];
   }
   s = wave_sum(s);
   const float inv_s = 1.0f / s;
 #pragma unroll
-  for (int j = 0; j < MAXE / 64; ++j) {
+  for (int j = 0; j < NPL; ++j) {
     const int e = l + 64 * j;
     if (e < E) probs[t * E + e] = ex[j] * inv_s;
   }
   // top-k: K rounds of a wave-wide max over 32-bit keys (bf16 logit in an order-preserving form above 0xffff - e):
   // one compare per step for (value desc, index asc); a taken expert's key becomes 0
-  uint32_t key[MAXE / 64];
+  uint32_t key[NPL];
 #pragma unroll
-  for (int j = 0; j < MAXE / 64; ++j) {
+  for (int j = 0; j < NPL; ++j) {
     const int e = l + 64 * j;
     uint32_t b = __float_as_uint(v[j]) >> 16;   // the logit's bf16 bits
     if (b == 0x8000u) b = 0u;                   // -0 ties with +0
@@ -57,12 +58,12 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
   for (int k = 0; k < K; ++k) {
     uint32_t best = key[0];
 #pragma unroll
-    for (int j = 1; j < MAXE / 64; ++j) best = max(best, key[j]);
+    for (int j = 1; j < NPL; ++j) best = max(best, key[j]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) best = max(best, (uint32_t)__shfl_xor((int)best, o, 64));
     const int bi = (int)(0xffffu - (best & 0xffffu));
 #pragma unroll
-    for (int j = 0; j < MAXE / 64; ++j)
+    for (int j = 0; j < NPL; ++j)
       if (bi == l + 64 * j) key[j] = 0u;
     const uint32_t ob = best >> 16;
     const float bv = __uint_as_float(((ob & 0x8000u) ? (ob & 0x7fffu) : (~ob & 0xffffu)) << 16);
@@ -78,10 +79,13 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
         p = pk[k];
         i = ik[k];
       }
-    if (topv_f32)
+    if (topv_f32) {
       topv_f32[t * K + l] = pes ? (p / psum) * bf2f(pes[i]) : p / psum;   // route_gemma4: fp32, x per-expert scale
-    else
-      topv[t * K + l] = f2bf(p / psum);
+    } else {
+      const uint16_t b = f2bf(p / psum);
+      topv[t * K + l] = b;
+      if (topv32) topv32[t * K + l] = bf2f(b);   // the combine weight the reference uses: fp32 of the bf16 value
+    }
     topi[t * K + l] = i;
     topi32[t * K + l] = i;
   }
@@ -97,6 +101,11 @@ constexpr int RT = 64;
 constexpr int RC = 96;
 constexpr int RKT = 64;
 constexpr int RSTAGE = RC * RKT;   // bf16 elements of one weight stage (12 KB)
+// Vector-memory operations per wave in each issue group of the logits loop (the issue code is written with these
+// counts; the wait is computed from them): 2 x-row loads into registers, 3 weight-row LDS-DMAs
+constexpr int RVM_X = 2;
+constexpr int RVM_W = RSTAGE * 2 / (4 * 1024);
+constexpr int R_WAIT = 2 * (RVM_X + RVM_W);   // steps j+1 and j+2 may be in flight while step j computes
 
 SMEL_DEV f32x4_t mfma16r(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
@@ -118,14 +127,14 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
   // all past E32 (E32 and c0 are multiples of 8), so one descriptor serves the wave-load.
   const rsrc_t rg = make_rsrc(gw, (uint64_t)E * H * 2);
   const rsrc_t rsg = make_rsrc(sg ? sg : gw, sg ? (uint64_t)H * 2 : 0);
-  rsrc_t rb[3];
-  uint32_t boff[3];
+  rsrc_t rb[RVM_W];
+  uint32_t boff[RVM_W];
 #pragma unroll
-  for (int ii = 0; ii < 3; ++ii) {
-    const int row = 8 * (3 * w + ii) + (l >> 3);
+  for (int ii = 0; ii < RVM_W; ++ii) {
+    const int row = 8 * (RVM_W * w + ii) + (l >> 3);
     const int c = c0 + row;
     const int ch = (l & 7) ^ swz(row);
-    const bool gate = c0 + 8 * (3 * w + ii) < E32;   // uniform
+    const bool gate = c0 + 8 * (RVM_W * w + ii) < E32;   // uniform
     rb[ii] = gate ? rg : rsg;
     boff[ii] = gate ? (c < E ? (uint32_t)c * H * 2 + 16 * ch : OOB) : ((sg && c == E32) ? 16u * ch : OOB);
   }
@@ -137,10 +146,11 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
     const bool in = j < nk;
     const uint32_t k2 = (uint32_t)j * RKT * 2;
     __builtin_amdgcn_sched_barrier(0);
-    xa[0] = ld16(rx, in ? xoff + k2 : OOB);
-    xa[1] = ld16(rx, in ? xoff + k2 + 64 : OOB);
 #pragma unroll
-    for (int ii = 0; ii < 3; ++ii) ld16_lds(rb[ii], &WS[j & 3][(3 * w + ii) * 512], in ? boff[ii] + k2 : OOB);
+    for (int s = 0; s < RVM_X; ++s) xa[s] = ld16(rx, in ? xoff + k2 + 64 * s : OOB);
+#pragma unroll
+    for (int ii = 0; ii < RVM_W; ++ii)
+      ld16_lds(rb[ii], &WS[j & 3][(RVM_W * w + ii) * 512], in ? boff[ii] + k2 : OOB);
     __builtin_amdgcn_sched_barrier(0);
   };
   // weight fragment reads: column fragment f, substep s, lane (kq, li) -> row 16 f + li, logical chunk 4 s + kq
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
   f32x4_t acc[6];
 #pragma unroll
   for (int f = 0; f < 6; ++f) acc[f] = f32x4_t{};
-  u32x4_t X0[2], X1[2], X2[2], X3[2];
+  u32x4_t X0[RVM_X], X1[RVM_X], X2[RVM_X], X3[RVM_X];
   auto compute = [&](int j, const u32x4_t* xa) {
     const uint16_t* S = WS[j & 3];
 #pragma unroll
@@ -165,24 +175,24 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
   issue(1, X1);
   issue(2, X2);
   for (int j = 0; j < nk; j += 4) {
-    SMEL_WAIT_VM_LDS(10);
+    wait_vm_lds<R_WAIT>();
     __builtin_amdgcn_s_barrier();
     issue(j + 3, X3);
     compute(j, X0);
-    SMEL_WAIT_VM_LDS(10);
+    wait_vm_lds<R_WAIT>();
     __builtin_amdgcn_s_barrier();
     issue(j + 4, X0);
     compute(j + 1, X1);
-    SMEL_WAIT_VM_LDS(10);
+    wait_vm_lds<R_WAIT>();
     __builtin_amdgcn_s_barrier();
     issue(j + 5, X1);
     compute(j + 2, X2);
-    SMEL_WAIT_VM_LDS(10);
+    wait_vm_lds<R_WAIT>();
     __builtin_amdgcn_s_barrier();
     issue(j + 6, X2);
     compute(j + 3, X3);
   }
-  SMEL_WAIT_VM(0);   // the trailing (out-of-range) loads
+  wait_vm<0>();   // the trailing (out-of-range) loads
   // D[4 kq + r][li] of fragment f: token 16 w + 4 kq + r, column c0 + 16 f + li
 #pragma unroll
   for (int f = 0; f < 6; ++f) {
@@ -197,16 +207,31 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
 }
 
 // ---- selection: one wave per token over its bf16 logits row (probs, top-k, renorm; shared-gate sigmoid).
+template <int NPL>
 __global__ __launch_bounds__(256) void route_select(const uint16_t* __restrict__ logits, int ldl, int T, int E, int K,
                                                     int sg_col, float* __restrict__ probs,
-                                                    uint16_t* __restrict__ topv, int64_t* __restrict__ topi,
-                                                    int32_t* __restrict__ topi32, float* __restrict__ sgate,
-                                                    float* __restrict__ topv_f32, const uint16_t* __restrict__ pes) {
+                                                    uint16_t* __restrict__ topv, float* __restrict__ topv32,
+                                                    int64_t* __restrict__ topi, int32_t* __restrict__ topi32,
+                                                    float* __restrict__ sgate, float* __restrict__ topv_f32,
+                                                    const uint16_t* __restrict__ pes) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const uint16_t* row = logits + t * ldl;
-  select_topk([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topi, topi32, topv_f32, pes);
+  select_topk<NPL>([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topv32, topi, topi32, topv_f32, pes);
   if (sgate && lane_id() == 0) sgate[t] = 1.0f / (1.0f + expf(-bf2f(row[sg_col])));
+}
+
+// The selection launch for E experts: 4 logits per lane up to 256 experts, 8 up to 512.
+void launch_select(hipStream_t stream, const uint16_t* logits, int ldl, int T, int E, int K, int sg_col, float* probs,
+                   uint16_t* topv, float* topv32, int64_t* topi, int32_t* topi32, float* sgate, float* topv_f32,
+                   const uint16_t* pes) {
+  const unsigned grid = (unsigned)((T + 3) / 4);
+  if (E <= 256)
+    route_select<4><<<grid, 256, 0, stream>>>(logits, ldl, T, E, K, sg_col, probs, topv, topv32, topi, topi32, sgate,
+                                               topv_f32, pes);
+  else
+    route_select<8><<<grid, 256, 0, stream>>>(logits, ldl, T, E, K, sg_col, probs, topv, topv32, topi, topi32, sgate,
+                                               topv_f32, pes);
 }
 
 // Backward of route (+ shared gate): one wave per token.
@@ -216,8 +241,8 @@ __global__ __launch_bounds__(256) void route_select(const uint16_t* __restrict__
 //   shared gate: dlogit_sg = (sum_j dwp[TK+t][j]) * sg (1 - sg)
 __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, int nblk,
                                                  const int32_t* __restrict__ inv, const float* __restrict__ probs,
-                                                 const int32_t* __restrict__ topi32, const uint16_t* __restrict__ topv,
-                                                 const float* __restrict__ sgate, int T, int K, int E, int TK,
+                                                 const int32_t* __restrict__ topi32, const float* __restrict__ sgate, int T,
+                                                 int K, int E, int TK,
                                                  uint16_t* __restrict__ dlogits, int ldl,
                                                  float* __restrict__ dtopv_out, const uint16_t* __restrict__ pes) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -269,7 +294,6 @@ __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, 
     }
     dlogits[t * ldl + e] = f2bf(g);
   }
-  (void)topv;
 }
 
 // ---- Gemma 4 router input (smel/moe.py:170-180): one wave per token of the residual stream h [T][H]:
@@ -386,7 +410,7 @@ extern "C" int64_t smel_route_ld(int64_t E, int32_t with_shared_gate) {
 }
 
 extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T,
-                          int64_t H, int64_t E, int64_t K, float* probs, uint16_t* topv, int64_t* topi,
+                          int64_t H, int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi,
                           int32_t* topi32, float* sgate, uint16_t* logits, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && H > 0 && E > 0 && K > 0, SMEL_EINVAL, "route: bad sizes");
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "route: E=%lld > %d experts", (long long)E, MAXE);
@@ -398,9 +422,8 @@ extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint1
   SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32 && logits, SMEL_EINVAL, "route: null pointer");
   const int64_t ldl = smel_route_ld(E, shared_gate_w != nullptr);
   launch_logits(stream, x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
-  route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K,
-                                                            (int)((E + 31) / 32 * 32), probs, topv, topi, topi32,
-                                                            shared_gate_w ? sgate : nullptr, nullptr, nullptr);
+  launch_select(stream, logits, (int)ldl, (int)T, (int)E, (int)K, (int)((E + 31) / 32 * 32), probs, topv, topv32,
+                topi, topi32, shared_gate_w ? sgate : nullptr, nullptr, nullptr);
   return smel::launch_status();
 }
 
@@ -412,22 +435,22 @@ extern "C" int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, i
                (long long)K);
   if (T == 0) return 0;
   SMEL_REQUIRE(logits && probs && topv && topi && topi32, SMEL_EINVAL, "route_logits: null pointer");
-  route_select<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(logits, (int)E, (int)T, (int)E, (int)K, 0, probs, topv,
-                                                            topi, topi32, nullptr, nullptr, nullptr);
+  launch_select(stream, logits, (int)E, (int)T, (int)E, (int)K, 0, probs, topv, nullptr, topi, topi32, nullptr,
+                nullptr, nullptr);
   return smel::launch_status();
 }
 
 extern "C" int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs,
-                              const int32_t* topi32, const uint16_t* topv, const float* sgate, int64_t T, int64_t K,
-                              int64_t E, int64_t TK, uint16_t* dlogits, int64_t ldl, float* dtopv_out,
-                              const uint16_t* per_expert_scale, hipStream_t stream) {
+                              const int32_t* topi32, const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK,
+                              uint16_t* dlogits, int64_t ldl, float* dtopv_out, const uint16_t* per_expert_scale,
+                              hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && K <= 16 && E > 0 && nblk > 0, SMEL_EINVAL, "route_bwd: bad sizes");
   SMEL_REQUIRE(ldl >= E + (sgate ? 1 : 0), SMEL_EINVAL, "route_bwd: ldl %lld too small", (long long)ldl);
   if (T == 0) return 0;
   SMEL_REQUIRE(dwp && probs && topi32 && dlogits, SMEL_EINVAL, "route_bwd: null pointer");
   SMEL_REQUIRE(inv || TK == T * K, SMEL_EINVAL, "route_bwd: without inv, dwp rows are the T*K slots");
-  route_bwd<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(dwp, (int)nblk, inv, probs, topi32, topv, sgate, (int)T,
-                                                         (int)K, (int)E, (int)TK, dlogits, (int)ldl, dtopv_out,
+  route_bwd<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(dwp, (int)nblk, inv, probs, topi32, sgate, (int)T, (int)K,
+                                                         (int)E, (int)TK, dlogits, (int)ldl, dtopv_out,
                                                          per_expert_scale);
   return smel::launch_status();
 }
@@ -451,8 +474,8 @@ extern "C" int smel_route_gemma4(const uint16_t* h, const uint16_t* router_scale
   // H^-1/2 as the reference's Python float (a double) rounded to fp32 for the bf16 product
   route_prenorm<<<tg, 256, 0, stream>>>(h, router_scale, (int)T, (int)H, eps, (float)pow((double)H, -0.5), xn, rstd);
   launch_logits(stream, xn, proj_w, nullptr, (int)T, (int)H, (int)E, (int)ldl, logits);
-  route_select<<<tg, 256, 0, stream>>>(logits, (int)ldl, (int)T, (int)E, (int)K, 0, probs, nullptr, topi, topi32,
-                                       nullptr, topv, per_expert_scale);
+  launch_select(stream, logits, (int)ldl, (int)T, (int)E, (int)K, 0, probs, nullptr, nullptr, topi, topi32, nullptr,
+                topv, per_expert_scale);
   return smel::launch_status();
 }
 

@@ -446,8 +446,8 @@ class _RouteFn(torch.autograd.Function):
         topi = torch.empty(T, top_k, dtype=torch.int64, device=dev)
         topi32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
         lg = torch.empty(T, L.load().smel_route_ld(E, 0), dtype=torch.bfloat16, device=dev)
-        L.call("smel_route", L.ptr(x), L.ptr(gate_w), None, T, H, E, top_k, L.ptr(probs), L.ptr(topv), L.ptr(topi),
-               L.ptr(topi32), None, L.ptr(lg), L.stream())
+        L.call("smel_route", L.ptr(x), L.ptr(gate_w), None, T, H, E, top_k, L.ptr(probs), L.ptr(topv), None,
+               L.ptr(topi), L.ptr(topi32), None, L.ptr(lg), L.stream())
         ctx.save_for_backward(probs, topi32, gate_w)
         ctx.mark_non_differentiable(probs, topi)
         return probs, topv, topi
@@ -464,7 +464,7 @@ class _RouteFn(torch.autograd.Function):
         wr = _router_ext_weight(gate_w, None)
         Epad = wr.R
         dl = torch.empty(T, Epad, dtype=torch.bfloat16, device=dev)
-        L.call("smel_route_bwd", L.ptr(dwp), 1, None, L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
+        L.call("smel_route_bwd", L.ptr(dwp), 1, None, L.ptr(probs), L.ptr(topi32), None, T, K, E, T * K,
                L.ptr(dl), Epad, None, None, L.stream())
         dx = _router_dx(dl, wr, T)
         return dx, None, None
@@ -522,7 +522,7 @@ class _RouteGemma4Fn(torch.autograd.Function):
         wr = _router_ext_weight(proj, None)
         dl = torch.empty(T, wr.R, dtype=torch.bfloat16, device=dev)
         dw = dtopv.float().contiguous()
-        L.call("smel_route_bwd", L.ptr(dw), 1, None, L.ptr(probs), L.ptr(topi32), None, None, T, K, E, T * K,
+        L.call("smel_route_bwd", L.ptr(dw), 1, None, L.ptr(probs), L.ptr(topi32), None, T, K, E, T * K,
                L.ptr(dl), wr.R, None, L.ptr(pes), L.stream())
         dxn = _router_dx(dl, wr, T)
         dh = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
@@ -632,7 +632,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dn), 0, _ACT[ex.act], L.ptr(Y), H, None, st, tag="gemm_dn_fwd")
     out = bf(T, H)
-    L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(sgate), T, K, H, L.ptr(out), st)
+    L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(inv), L.ptr(sgate), T, K, H, L.ptr(out), st)
     # everything the backward needs
     c.T, c.H, c.I, c.E, c.K, c.TK, c.M, c.maxt = T, H, I, E, K, TK, M, maxt
     c.ex, c.shared_w = ex, (sh_gu_t, sh_dn_t) if shared is not None else None
@@ -688,7 +688,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
         dxr = bf(T, H)
         with side_r:
             L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32),
-                   L.ptr(t["topv"]), L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, None, L.stream())
+                   L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, None, L.stream())
             _router_dx(dl, wr, T, dxr)
     else:
         dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
@@ -731,7 +731,8 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
            tag="gemm_gu_bwd")
     side_r.join()
     dx = bf(T, H)
-    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), int(t["sgate"] is not None), T, K, H, L.ptr(dx), st)
+    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), L.ptr(t["inv"]), int(t["sgate"] is not None), T, K, H, L.ptr(dx),
+           st)
     if side_w is not None:
         side_w.join()
     return dx, dtopv, grads
@@ -821,6 +822,7 @@ class _MoELayerFn(torch.autograd.Function):
         fuse = plan["shared"] is not None
         probs = torch.empty(T, E, dtype=torch.float32, device=dev)
         topv = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+        topv32 = torch.empty(T, K, dtype=torch.float32, device=dev)   # fp32 of topv: the combine weight
         topi = torch.empty(T, K, dtype=torch.int64, device=dev)
         topi32 = torch.empty(T, K, dtype=torch.int32, device=dev)
         sgate = torch.empty(T, dtype=torch.float32, device=dev) if fuse else None
@@ -830,12 +832,12 @@ class _MoELayerFn(torch.autograd.Function):
         with fork:
             bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"], fuse, H, dev)
         L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
-               L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.stream())
+               L.ptr(topv32), L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.stream())
         if stats is not None:
             stats(probs, topv, topi)
         c = _Ctx()
         shared = (plan["shared"][0], plan["shared"][1], sgate, plan["shared"][4], plan["shared"][5]) if fuse else None
-        out = _forward_pipeline(x, plan["ex"], K, topv, topi32, False, shared, plan["lora_ex"], plan["lora_sh"],
+        out = _forward_pipeline(x, plan["ex"], K, topv32, topi32, False, shared, plan["lora_ex"], plan["lora_sh"],
                                 plan["need_grad"], c, prep=(fork, bufs))
         if plan["need_grad"]:
             c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw))
@@ -858,7 +860,7 @@ class _RoutedFn(torch.autograd.Function):
     def forward(ctx, x, topv, topi, ex, lora, *leaves):
         c = _Ctx()
         K = topi.shape[1]
-        tv = topv.detach().to(torch.bfloat16).contiguous()
+        tv = topv.detach().float().contiguous()   # fp32 combine weights: the reference's topv.float() (:252)
         need = ctx.needs_input_grad[0] or ctx.needs_input_grad[1] or any(ctx.needs_input_grad[5:])
         out = _forward_pipeline(x, ex, K, tv, topi.contiguous(), topi.dtype == torch.int64, None, lora, None, need, c)
         if need:
@@ -875,10 +877,23 @@ class _RoutedFn(torch.autograd.Function):
         return (dx, dtopv.to(ctx.topv_dtype), None, None, None, *g)
 
 
+def _check_ids(topi: torch.Tensor, E: int):
+    """Expert ids handed in by a caller must lie in [0, E), where the reference's bincount / indexing
+    (smel/moe.py:216-223) fails otherwise: checked here with one host synchronisation. Inside a HIP-graph capture
+    (no synchronisation possible) the check is skipped; the dispatch then drops a slot whose id is out of range
+    (inv = -1) and the combine, the dX reduce and the d(topv) reduction treat it as a zero row, so the output and
+    the gradients stay defined."""
+    if topi.numel() == 0 or torch.cuda.is_current_stream_capturing():
+        return
+    if bool(((topi < 0) | (topi >= E)).any()):
+        raise IndexError(f"routed_experts: expert ids must lie in [0, {E})")
+
+
 def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
     """Weighted sum of the routed experts of every token (smel/moe.py:214-252)."""
     L.require_device(x2d, topv, topi)
     _check_bank(ex)
+    _check_ids(topi, ex.E)
     return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
 
 

@@ -83,10 +83,10 @@ def test_host_side_rejections():
     assert L.smel_dispatch_max_tiles(32736, 256, 4092, 128) == (32736 + 127) // 128 + 256 + 32 + 1
     assert L.smel_dispatch_ws_size(32736, 256) == 32 * 256 + 32 and L.smel_dispatch_ws_size(0, 8) == 0
     # route: too many experts
-    rc = L.smel_route(1, 1, None, 4, 64, 300, 8, 1, 1, 1, 1, None, 1, None)
-    assert rc == -2 and b"E=300" in L.smel_last_error()
+    rc = L.smel_route(1, 1, None, 4, 64, 600, 8, 1, 1, None, 1, 1, None, 1, None)
+    assert rc == -2 and b"E=600" in L.smel_last_error()
     # route: hidden not a multiple of 64
-    assert L.smel_route(1, 1, None, 4, 96, 8, 2, 1, 1, 1, 1, None, 1, None) == -2
+    assert L.smel_route(1, 1, None, 4, 96, 8, 2, 1, 1, None, 1, 1, None, 1, None) == -2
     assert L.smel_route_ld(256, 1) == 288 and L.smel_route_ld(250, 0) == 256
     # dequant: K not a multiple of the group
     assert L.smel_dequant_int4(1, 1, 1, 1, 4, 96, 64, 0, None) == -1

@@ -288,7 +288,8 @@ def _route_logits(logits, K):
     return probs, topv, topi, topi32
 
 
-@pytest.mark.parametrize("T,E,K", [(4092, 256, 8), (128, 8, 2), (513, 128, 8), (1, 64, 1), (33, 256, 16)])
+@pytest.mark.parametrize("T,E,K", [(4092, 256, 8), (128, 8, 2), (513, 128, 8), (1, 64, 1), (33, 256, 16),
+                                   (700, 512, 8), (50, 257, 16)])
 def test_route_ids_bitexact_given_logits(T, E, K):
     _say(f"route_logits T{T} E{E} K{K}")
     gen = torch.Generator().manual_seed(T + E)
@@ -308,7 +309,8 @@ def test_route_ids_bitexact_given_logits(T, E, K):
 
 
 @pytest.mark.parametrize("T,H,E,K,shared", [(4092, 2048, 256, 8, True), (128, 64, 8, 2, True),
-                                            (300, 256, 16, 4, False), (7, 128, 100, 3, True)])
+                                            (300, 256, 16, 4, False), (7, 128, 100, 3, True),
+                                            (500, 256, 512, 8, True), (64, 128, 300, 16, False)])
 def test_route_fused(T, H, E, K, shared):
     """Fused logits GEMM + selection: ids agree with the oracle except at bf16 near-ties of the logits, whose rate is
     reported; probs / topv / shared gate within tolerance."""
@@ -320,6 +322,7 @@ def test_route_fused(T, H, E, K, shared):
     sg = (torch.randn(H, generator=gen) * 0.02).to(torch.bfloat16)
     probs = torch.empty(T, E, dtype=torch.float32, device=DEV)
     topv = torch.empty(T, K, dtype=torch.bfloat16, device=DEV)
+    topv32 = torch.empty(T, K, dtype=torch.float32, device=DEV)
     topi = torch.empty(T, K, dtype=torch.int64, device=DEV)
     topi32 = torch.empty(T, K, dtype=torch.int32, device=DEV)
     sgate = torch.empty(T, dtype=torch.float32, device=DEV)
@@ -327,7 +330,9 @@ def test_route_fused(T, H, E, K, shared):
     ldl = L.load().smel_route_ld(E, int(shared))
     lgw = torch.full((T, ldl), float("nan"), dtype=torch.bfloat16, device=DEV)
     L.call("smel_route", L.ptr(xd), L.ptr(gwd), L.ptr(sgd) if shared else None, T, H, E, K, L.ptr(probs),
-           L.ptr(topv), L.ptr(topi), L.ptr(topi32), L.ptr(sgate) if shared else None, L.ptr(lgw), L.stream())
+           L.ptr(topv), L.ptr(topv32), L.ptr(topi), L.ptr(topi32), L.ptr(sgate) if shared else None, L.ptr(lgw),
+           L.stream())
+    assert torch.equal(topv32.cpu(), topv.float().cpu())       # the fp32 copy is the bf16 value itself
     logits = (x.double() @ gw.double().t())                   # exact dot products of the bf16 inputs
     lb = logits.float().to(torch.bfloat16).float()
     # the workspace holds the kernel's bf16 logits: close to the exact ones, and the selection on them is exact
@@ -520,6 +525,40 @@ def test_routed_experts_parity():
     assert_close_bf16(tvg.grad.cpu(), tvo.grad, "dtopv")
     for n in LORA_NAMES:
         assert_close_bf16(getattr(lora.experts, n).grad.cpu(), leaves[n].grad, n)
+
+
+def test_routed_experts_bad_ids():
+    """Expert ids outside [0, E) given to routed_experts: eager calls raise (the reference's bincount / indexing
+    fails there); under HIP-graph capture the dispatch drops those slots and the combine treats them as zero rows, so
+    the output equals the oracle's with those routing weights set to zero (no uninitialised rows are read)."""
+    from smel.moe import routed_experts
+    _say("routed_experts bad ids")
+    x, ol = R.make_layer(T=96, H=128, E=8, I=64, K=2, n_sel=2, r=4, alpha=8.0, shared_inter=None, seed=8,
+                         lora_b_std=0.05)
+    W, ex, lora = to_device_layer(ol, DEV)
+    probs, topv, topi = R.route(x.float(), ol.gate_w.float(), 2)
+    bad = topi.clone()
+    bad[3, 1], bad[40, 0], bad[77, 1] = 8, -1, 1000
+    xd, tvd, bd = x.to(DEV), topv.float().to(DEV), bad.to(DEV)
+    with pytest.raises(IndexError):
+        routed_experts(xd, tvd, bd, ex, lora.experts)
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        routed_experts(xd, tvd, topi.to(DEV), ex, lora.experts)    # warm-up: packs and caches outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = routed_experts(xd, tvd, bd, ex, lora.experts)
+        for _ in range(2):
+            g.replay()
+            torch.cuda.synchronize()
+            keep = (bad >= 0) & (bad < 8)
+            tv0 = torch.where(keep, topv.float(), torch.zeros_like(topv.float()))
+            ids0 = torch.where(keep, bad, torch.zeros_like(bad))
+            leaves = {n: ol.ex_lora[n].clone() for n in LORA_NAMES}
+            yo = R.routed_experts(x.float(), tv0, ids0, ol, leaves, torch.float32)
+            assert torch.isfinite(y.float()).all()
+            assert_close_bf16(y.cpu(), yo, "y")
 
 
 def test_route_api_backward():

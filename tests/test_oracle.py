@@ -1,5 +1,7 @@
 """Pins the CPU oracle: against the reference's own golden vectors (tests/golden, written by the reference code),
 against closed forms and brute force, and the C restatement against the numpy one. CPU only."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -263,3 +265,94 @@ def test_moe_stats_hook_and_forced_routes(golden_c1):
     R.moe_forward(t["in.x"], L, 2, stats=stats, forced_topi=forced)
     assert torch.equal(seen["i"], forced)
     assert torch.allclose(seen["v"].sum(-1), torch.ones(128))
+
+
+def _tiny_gemma(seed=3):
+    """A tiny Gemma-4-style block: 8 GELU-tanh experts (2 selected with LoRA), a dense GeGLU MLP with LoRA, router
+    tensors as smel/tiny.py:74-77 draws them, plain-weight norms, a layer scalar."""
+    T, H, E, I, K, Is, r = 24, 64, 8, 32, 2, 48, 4
+    x, L = R.make_layer(T=T, H=H, E=E, I=I, K=K, n_sel=2, r=r, alpha=8.0, shared_inter=None, group=32, seed=seed,
+                        act_name="gelu_tanh", lora_b_std=0.05)
+    g = torch.Generator().manual_seed(seed + 1)
+    rn = lambda *s, std=1.0: torch.randn(*s, generator=g) * std
+    W = {f"{n}.weight": (1.0 + 0.2 * rn(H)).to(torch.bfloat16) for n in R.GEMMA4_NORMS}
+    W.update({"router.scale": (1.0 + 0.2 * rn(H)).to(torch.bfloat16),
+              "router.proj.weight": rn(E, H, std=0.3).to(torch.bfloat16),
+              "router.per_expert_scale": (0.5 + torch.rand(E, generator=g)).to(torch.bfloat16),
+              "mlp.gate_up_proj.weight": rn(2 * Is, H, std=0.1).to(torch.bfloat16),
+              "mlp.down_proj.weight": rn(H, Is, std=0.1).to(torch.bfloat16),
+              "layer_scalar": torch.tensor([0.75], dtype=torch.bfloat16)})
+    L.sh_lora = {"A_gate": rn(r, H, std=0.1), "A_up": rn(r, H, std=0.1), "A_down": rn(r, Is, std=0.1),
+                 "B_gate": rn(Is, r, std=0.1), "B_up": rn(Is, r, std=0.1), "B_down": rn(H, r, std=0.1)}
+    L.sh_scale = 2.0
+    h = (rn(T, H) * 3.0).to(torch.bfloat16)
+    return h, x, W, L, K
+
+
+def _gemma_block_bruteforce(h, a, W, L, topi, eps):
+    """Token by token and slot by slot from the formulas of smel/layer_runner.py:243-262, fp64 throughout."""
+    d = lambda t: t.double()
+    norm = lambda v, w: v / torch.sqrt((v * v).mean() + eps) * d(w)
+    gelu = lambda v: 0.5 * v * (1 + torch.tanh(math.sqrt(2 / math.pi) * (v + 0.044715 * v ** 3)))
+    gu_all, dn_all = L.frozen_weights(0, L.E, torch.float64)
+    sel = {int(e): j for j, e in enumerate(L.sel_ids)}
+    S = {k: d(v) for k, v in L.sh_lora.items()}
+    Wgu, Wd = d(W["mlp.gate_up_proj.weight"]), d(W["mlp.down_proj.weight"])
+    Is = Wd.shape[1]
+    H = h.shape[1]
+    out = []
+    for t in range(h.shape[0]):
+        h2 = d(h[t]) + norm(d(a[t]), W["post_attention_layernorm.weight"])
+        xm = norm(h2, W["pre_feedforward_layernorm.weight"])
+        g = Wgu[:Is] @ xm + L.sh_scale * S["B_gate"] @ (S["A_gate"] @ xm)
+        u = Wgu[Is:] @ xm + L.sh_scale * S["B_up"] @ (S["A_up"] @ xm)
+        act = gelu(g) * u
+        m = norm(Wd @ act + L.sh_scale * S["B_down"] @ (S["A_down"] @ act), W["post_feedforward_layernorm_1.weight"])
+        rx = h2 / torch.sqrt((h2 * h2).mean() + eps) * d(W["router.scale"]) * H ** -0.5
+        p = torch.softmax(d(W["router.proj.weight"]) @ rx, -1)
+        ids = topi[t].tolist()
+        v = p[ids] / p[ids].sum() * d(W["router.per_expert_scale"])[ids]
+        xe = norm(h2, W["pre_feedforward_layernorm_2.weight"])
+        e = torch.zeros(H, dtype=torch.float64)
+        for k, ei in enumerate(ids):
+            if ei in sel:
+                j = sel[ei]
+                X = {n: d(L.ex_lora[n][j]) for n in L.ex_lora}
+                gu, dn = d(L.sel_gate_up[j]), d(L.sel_down[j])
+                I = dn.shape[1]
+                ge = gu[:I] @ xe + L.ex_scale * X["B_gate"] @ (X["A_gate"] @ xe)
+                ue = gu[I:] @ xe + L.ex_scale * X["B_up"] @ (X["A_up"] @ xe)
+                ae = gelu(ge) * ue
+                y = dn @ ae + L.ex_scale * X["B_down"] @ (X["A_down"] @ ae)
+            else:
+                I = dn_all.shape[2]
+                ge, ue = gu_all[ei][:I] @ xe, gu_all[ei][I:] @ xe
+                y = dn_all[ei] @ (gelu(ge) * ue)
+            e += v[k] * y
+        e = norm(e, W["post_feedforward_layernorm_2.weight"])
+        out.append((h2 + norm(m + e, W["post_feedforward_layernorm.weight"])) * d(W["layer_scalar"]))
+    return torch.stack(out)
+
+
+def test_gemma4_block():
+    """The composed Gemma 4 block against a token-by-token fp64 evaluation of the same formulas (same routing); the
+    block's norms compute in fp32 as the reference's torch RMSNorm does, hence 1e-5. A plus-one norm weight (the
+    Qwen form) or a router without its per-expert scale is shown to fail the same bound."""
+    h, a, W, L, K = _tiny_gemma()
+    eps = 1e-6
+    out, (probs, topv, topi) = R.gemma4_moe_block(h, a, W, L, K, eps, dtype=torch.float64)
+    ref = _gemma_block_bruteforce(h, a, W, L, topi, eps)
+    assert R.rel_err(out, ref) < 1e-5
+    W2 = dict(W, **{"post_feedforward_layernorm_2.weight": (W["post_feedforward_layernorm_2.weight"].float() + 1)
+                    .to(torch.bfloat16)})
+    assert R.rel_err(_gemma_block_bruteforce(h, a, W2, L, topi, eps), ref) > 1e-3
+    W3 = dict(W, **{"router.per_expert_scale": torch.ones_like(W["router.per_expert_scale"])})
+    assert R.rel_err(_gemma_block_bruteforce(h, a, W3, L, topi, eps), ref) > 1e-3
+    # forced routing reproduces the free choice, and the fp32 autograd wrapper runs end to end
+    out_f, _ = R.gemma4_moe_block(h, a, W, L, K, eps, forced_topi=topi, dtype=torch.float64)
+    assert torch.equal(out_f, out)
+    gy = torch.randn(out.shape, generator=torch.Generator().manual_seed(0))
+    y32, dh, da, grads = R.gemma4_block_forward_backward(h, a, W, L, K, eps, gy, forced_topi=topi)
+    assert R.rel_err(y32, ref) < 1e-5 and dh.shape == h.shape and da.shape == a.shape
+    assert set(grads) == {f"{t}_{n}" for t in ("ex", "sh") for n in L.ex_lora}
+    assert all(float(v.abs().sum()) > 0 for v in grads.values())
