@@ -161,6 +161,18 @@ int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, in
                   int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream);
 /* int32 elements of smel_dispatch's workspace (host-side, no GPU call); -1 for bad sizes. */
 int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
+/* smel_dispatch without the workspace argument; it allocates nothing. No counterpart in the reference: it exists
+ * for callers that cannot allocate device memory (code under HIP-graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The workspace is a fixed array of smel_dispatch_noalloc_max_ws() int32 held by the library on
+ * every GPU it runs on until the process ends; calls whose smel_dispatch_ws_size(T*K, E) exceeds it are rejected
+ * (SMEL_EUNSUPPORTED). Every call on one GPU shares that GPU's array and each call rewrites all of the part it uses
+ * before reading it, so nothing carries over between calls, but calls that overlap in time on one GPU (different
+ * streams, or threads without ordering) race: order them on one stream. Results are those of smel_dispatch. */
+int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
+                          int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
+                          int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, hipStream_t stream);
+/* int32 capacity of smel_dispatch_noalloc's built-in workspace (host-side, no GPU call). */
+int64_t smel_dispatch_noalloc_max_ws(void);
 /* Upper bound of the tile-list length for smel_dispatch (host-side, no GPU call). */
 int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared_rows, int32_t m_tile);
 

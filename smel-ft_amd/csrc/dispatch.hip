@@ -6,8 +6,16 @@
 // them into counts, offsets, each block's first output position per expert, and the tile list; (3) every block
 // ranks its slots again — inside a wave by ballots over the id bits (a wave-level multisplit), across its 16 waves
 // by a per-expert prefix — and scatters order / inv. Slots of one expert thus keep ascending p: the stable sort.
+#include <mutex>
+
 #include "abi_util.h"
 #include "common.h"
+
+// Workspace of smel_dispatch_noalloc (the allocation-free variant below): one copy of this array on every GPU the
+// library runs on, held until the process ends. In host code the name is a host-side stand-in, not a device
+// address: kernels only ever receive the address hipGetSymbolAddress returns for the current device.
+constexpr int64_t SCRATCH_INTS = 1 << 18;   // 1 MiB: nb * (E + 1) ints for nb = ceil(T*K / 1024) blocks
+static __device__ __align__(256) int32_t scratch[SCRATCH_INTS];
 
 namespace {
 
@@ -200,6 +208,37 @@ __global__ __launch_bounds__(1024) void dispatch_scatter(const void* __restrict_
 
 }  // namespace
 
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch[MAX_DEVICES] = {};
+
+// Device address of the current device's `scratch` array, looked up on the first call on that device (with it
+// current) and kept; nullptr with the error message set if the lookup fails.
+int32_t* scratch_on_device() {
+  int dev = -1;
+  const hipError_t e0 = hipGetDevice(&dev);
+  if (e0 != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    smel::set_error("dispatch_noalloc: no usable current device (%s)", hipGetErrorString(e0));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      smel::set_error("dispatch_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                      hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[dev] = static_cast<int32_t*>(p);
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+
 extern "C" int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared_rows, int32_t m_tile) {
   if (m_tile <= 0) return 0;
   return (TK + m_tile - 1) / m_tile + E + (shared_rows + m_tile - 1) / m_tile + 1;
@@ -239,4 +278,22 @@ extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, in
     dispatch_scatter<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)TK, (int)E, hist, order, inv);
   }
   return smel::launch_status();
+}
+
+extern "C" int64_t smel_dispatch_noalloc_max_ws(void) { return SCRATCH_INTS; }
+
+extern "C" int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
+                                     int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
+                                     int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
+                                     int32_t* n_tiles, int32_t* err, hipStream_t stream) {
+  SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && T * K < (1ll << 30), SMEL_EINVAL, "dispatch_noalloc: bad sizes");
+  const int64_t need = smel_dispatch_ws_size(T * K, E);
+  SMEL_REQUIRE(need >= 0 && need <= SCRATCH_INTS, SMEL_EUNSUPPORTED,
+               "dispatch_noalloc: T*K=%lld slots over E=%lld experts need %lld workspace ints, more than the %lld of "
+               "the built-in scratch array (use smel_dispatch with a workspace)",
+               (long long)(T * K), (long long)E, (long long)need, (long long)SCRATCH_INTS);
+  int32_t* ws = scratch_on_device();
+  if (!ws) return SMEL_EINVAL;
+  return smel_dispatch(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
+                       n_tiles, err, ws, stream);
 }

@@ -64,6 +64,8 @@ SIGNATURES = {
     "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_ws_size": (i64, [i64, i64]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
+    "smel_dispatch_noalloc": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_dispatch_noalloc_max_ws": (i64, []),
     "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
