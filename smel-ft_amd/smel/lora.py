@@ -1,93 +1,101 @@
-"""LoRA parameter containers of the selected experts and the shared MLP (the types of smel/lora.py:14-58, 86-90).
+"""LoRA parameter sets of the selected routed experts and of the shared / dense MLP: the adapter format of the
+reference's smel/lora.py (classes ExpertsLoRA, MLPLoRA, LayerLoRA, BlockLoRA; parameters A_gate, B_gate, A_up,
+B_up, A_down, B_down in that order, fp32, A [.., r, in] uniform in +-1/sqrt(in) (kaiming_uniform with a = sqrt(5)),
+B [.., out, r] zero), so adapters written by either load into the other.
 
-Parameters are fp32 nn.Parameters with the reference's shapes and init (A: kaiming_uniform(a=sqrt(5)) per [r, in]
-matrix, B: zeros); slot j of ExpertsLoRA belongs to expert ``expert_ids[j]``. The LoRA products themselves run inside
-the MoE kernels (a 32-wide K-extension of the expert GEMMs), see ``smel.moe``.
+The MoE layer never multiplies these factors in Python: smel.moe lays them out as a 32-wide K-extension of the
+grouped-GEMM kernels. ``lora_linear`` / ``lora_gate_up`` are the dense helpers of the API (torch ops).
 """
 from __future__ import annotations
 
+import json
 import math
+import os
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
-
-def _init_a(t: torch.Tensor):
-    for m in t.reshape(-1, *t.shape[-2:]):
-        nn.init.kaiming_uniform_(m, a=math.sqrt(5))
+_PROJ = ("gate", "up", "down")
 
 
-class ExpertsLoRA(nn.Module):
-    """LoRA of k selected experts: A_gate/A_up [k, r, H], B_gate/B_up [k, I, r], A_down [k, r, I], B_down [k, H, r]."""
+def _uniform_fan_in(a: torch.Tensor) -> torch.Tensor:
+    """Every [r, in] matrix of ``a`` uniform in +-1/sqrt(in): kaiming_uniform_ with a = sqrt(5) gives
+    gain sqrt(2 / (1 + 5)) and bound gain * sqrt(3 / in), which is that."""
+    bound = 1.0 / math.sqrt(a.shape[-1])
+    with torch.no_grad():
+        for m in a.view(-1, *a.shape[-2:]):
+            m.uniform_(-bound, bound)
+    return a
+
+
+class _LoRASet(nn.Module):
+    """The six factors of a gated MLP's LoRA, with ``lead`` leading dims (() for one MLP, (k,) for k experts):
+    A_p [*lead, r, in_p], B_p [*lead, out_p, r] for p = gate, up (in = hidden, out = inter) and down (in = inter,
+    out = hidden); scale = alpha / r."""
+
+    def __init__(self, lead: tuple, hidden: int, inter: int, r: int, alpha: float):
+        super().__init__()
+        self.r, self.alpha, self.scale = r, alpha, alpha / r
+        io = {"gate": (hidden, inter), "up": (hidden, inter), "down": (inter, hidden)}
+        for p in _PROJ:
+            fan_in, fan_out = io[p]
+            setattr(self, f"A_{p}", nn.Parameter(_uniform_fan_in(torch.empty(*lead, r, fan_in))))
+            setattr(self, f"B_{p}", nn.Parameter(torch.zeros(*lead, fan_out, r)))
+
+    def _deltas(self, idx):
+        """scale B_p A_p for the three projections at index ``idx`` of the leading dims (fp32)."""
+        return tuple(torch.matmul(getattr(self, f"B_{p}")[idx].float(), getattr(self, f"A_{p}")[idx].float())
+                     .mul_(self.scale) for p in _PROJ)
+
+
+class ExpertsLoRA(_LoRASet):
+    """LoRA of k selected experts of one layer (smel/lora.py:14-36): slot j belongs to expert ``expert_ids[j]``."""
 
     def __init__(self, expert_ids, hidden: int, inter: int, r: int = 16, alpha: float = 32.0):
-        super().__init__()
-        k = len(expert_ids)
-        self.register_buffer("expert_ids", torch.as_tensor(list(expert_ids), dtype=torch.long), persistent=True)
-        self.r, self.alpha, self.scale = r, alpha, alpha / r
-        self.A_gate = nn.Parameter(torch.empty(k, r, hidden))
-        self.B_gate = nn.Parameter(torch.zeros(k, inter, r))
-        self.A_up = nn.Parameter(torch.empty(k, r, hidden))
-        self.B_up = nn.Parameter(torch.zeros(k, inter, r))
-        self.A_down = nn.Parameter(torch.empty(k, r, inter))
-        self.B_down = nn.Parameter(torch.zeros(k, hidden, r))
-        for a in (self.A_gate, self.A_up, self.A_down):
-            _init_a(a.data)
+        ids = [int(e) for e in expert_ids]
+        super().__init__((len(ids),), hidden, inter, r, alpha)
+        self.register_buffer("expert_ids", torch.tensor(ids, dtype=torch.long), persistent=True)
 
     def delta(self, j: int):
-        s = self.scale
-        return (s * self.B_gate[j].float() @ self.A_gate[j].float(),
-                s * self.B_up[j].float() @ self.A_up[j].float(),
-                s * self.B_down[j].float() @ self.A_down[j].float())
+        """Dense weight deltas of slot j: (d_gate [I, H], d_up [I, H], d_down [H, I]), fp32."""
+        return self._deltas(j)
 
 
-class MLPLoRA(nn.Module):
-    """LoRA of a plain gated MLP (the shared expert / Gemma's dense MLP): A_* [r, in], B_* [out, r]."""
+class MLPLoRA(_LoRASet):
+    """LoRA of one gated MLP: the shared expert, or Gemma 4's dense MLP (smel/lora.py:39-58)."""
 
     def __init__(self, hidden: int, inter: int, r: int = 16, alpha: float = 32.0):
-        super().__init__()
-        self.r, self.alpha, self.scale = r, alpha, alpha / r
-        self.A_gate = nn.Parameter(torch.empty(r, hidden))
-        self.B_gate = nn.Parameter(torch.zeros(inter, r))
-        self.A_up = nn.Parameter(torch.empty(r, hidden))
-        self.B_up = nn.Parameter(torch.zeros(inter, r))
-        self.A_down = nn.Parameter(torch.empty(r, inter))
-        self.B_down = nn.Parameter(torch.zeros(hidden, r))
-        for a in (self.A_gate, self.A_up, self.A_down):
-            _init_a(a.data)
+        super().__init__((), hidden, inter, r, alpha)
 
     def delta(self):
-        s = self.scale
-        return (s * self.B_gate.float() @ self.A_gate.float(),
-                s * self.B_up.float() @ self.A_up.float(),
-                s * self.B_down.float() @ self.A_down.float())
+        return self._deltas(())
 
 
 def lora_linear(x, w, A, B, scale):
-    """x w^T + scale (x A^T) B^T with the LoRA factors cast to x's dtype (smel/lora.py:61-69). A dense helper of the
-    API; the MoE layer itself runs its LoRA products inside the grouped-GEMM kernels."""
-    y = x @ w.t()
+    """x w^T + scale (x A^T) B^T with the LoRA factors in x's dtype (smel/lora.py:61-69)."""
+    y = F.linear(x, w)
     if A is None:
         return y
-    if x.dim() == 2:
-        return torch.addmm(y, x @ A.to(x.dtype).t(), B.to(x.dtype).t(), alpha=scale)
-    return y + scale * ((x @ A.to(x.dtype).t()) @ B.to(x.dtype).t())
+    return torch.add(y, F.linear(F.linear(x, A.to(x.dtype)), B.to(x.dtype)), alpha=scale)
 
 
 def lora_gate_up(x, w_gate_up, A_gate, B_gate, A_up, B_up, scale):
-    """(gate, up) of a gated MLP from one stacked [2I, H] weight (smel/lora.py:72-83); dense helper of the API."""
+    """(gate, up) of a gated MLP from its stacked [2I, H] weight (smel/lora.py:72-83). Both low-rank products run
+    as one: x [A_gate; A_up]^T gives the 2r-wide projection, and the block-diagonal [[B_gate, 0], [0, B_up]] maps it
+    to the stacked 2I outputs, added to the base GEMM's."""
+    h = F.linear(x, w_gate_up)
+    if A_gate is not None:
+        dt = x.dtype
+        low = F.linear(x, torch.cat((A_gate, A_up)).to(dt))
+        h = torch.add(h, F.linear(low, torch.block_diag(B_gate, B_up).to(dt)), alpha=scale)
     I = w_gate_up.shape[0] // 2
-    base = x @ w_gate_up.t()
-    if A_gate is None:
-        return base[:, :I], base[:, I:]
-    r = A_gate.shape[0]
-    xa = x @ torch.cat((A_gate, A_up)).to(x.dtype).t()
-    g = torch.addmm(base[:, :I], xa[:, :r], B_gate.to(x.dtype).t(), alpha=scale)
-    u = torch.addmm(base[:, I:], xa[:, r:], B_up.to(x.dtype).t(), alpha=scale)
-    return g, u
+    return h[..., :I], h[..., I:]
 
 
 class LayerLoRA(nn.Module):
+    """The LoRA of one layer: ``experts`` (ExpertsLoRA or None) and ``shared`` (MLPLoRA or None)."""
+
     def __init__(self, experts: ExpertsLoRA | None, shared: MLPLoRA | None):
         super().__init__()
         self.experts = experts
@@ -95,21 +103,34 @@ class LayerLoRA(nn.Module):
 
 
 class BlockLoRA(nn.Module):
-    """All LoRA modules of a block of layers, keyed by absolute layer index (smel/lora.py:93-125)."""
+    """The LoRA of a block of layers, keyed by absolute layer index (smel/lora.py:93-125)."""
 
     def __init__(self, layers: dict):
         super().__init__()
         self.layers = nn.ModuleDict({str(k): v for k, v in layers.items()})
 
     def get(self, l: int):
-        return self.layers[str(l)] if str(l) in self.layers else None
+        key = str(l)
+        return self.layers[key] if key in self.layers else None
 
     @classmethod
     def build(cls, selection: dict, hidden: int, inter: int, shared_inter: int, r: int, alpha: float,
               shared: bool = True):
-        layers = {}
-        for l, ids in selection.items():
+        """selection {layer: [expert ids]} -> one LayerLoRA per layer (no ExpertsLoRA for an empty selection)."""
+        def layer(ids):
             ex = ExpertsLoRA(ids, hidden, inter, r, alpha) if len(ids) else None
-            sh = MLPLoRA(hidden, shared_inter, r, alpha) if shared else None
-            layers[int(l)] = LayerLoRA(ex, sh)
-        return cls(layers)
+            return LayerLoRA(ex, MLPLoRA(hidden, shared_inter, r, alpha) if shared else None)
+        return cls({int(l): layer(ids) for l, ids in selection.items()})
+
+    @classmethod
+    def load(cls, path, dims, device="cuda"):
+        """An adapter folder (adapter_config.json + adapter.safetensors, the reference trainer's output format) ->
+        (BlockLoRA on ``device``, the config dict). ``dims`` supplies hidden, moe_inter and shared_inter."""
+        from safetensors.torch import load_file
+        with open(os.path.join(path, "adapter_config.json")) as f:
+            meta = json.load(f)
+        sel = {int(l): ids for l, ids in meta["experts"].items()}
+        block = cls.build(sel, dims.hidden, dims.moe_inter, dims.shared_inter, meta["r"], meta["alpha"],
+                          shared=meta["shared_lora"])
+        block.load_state_dict(load_file(os.path.join(path, "adapter.safetensors")))
+        return block.to(device), meta

@@ -99,3 +99,71 @@ def test_repeatable_and_empty(lm):
     assert torch.equal(a, b) and torch.equal(ga, h.grad)
     e = loss_mod.chunked_ce(h[:0], head, tgt[:0], denom=1.0)
     assert e.item() == 0.0
+
+
+def rounded_full_ce(h, W, tgt, softcap):
+    """Comparator written for these tests: the full logits rounded to h's dtype (the library GEMM's output), capped
+    in fp32, the exact softmax from their log-sum-exp, the softmax terms rounded to h's dtype before they meet W (the
+    reference's p.to(h.dtype) @ W). Targets outside [0, V) contribute no target logit and no target row."""
+    V = W.shape[0]
+    z = (h @ W.t()).float()
+    dz = torch.ones_like(z)
+    if softcap:
+        t = torch.tanh(z / softcap)
+        z, dz = softcap * t, 1 - t * t
+    lse = torch.logsumexp(z, -1)
+    ok = (tgt >= 0) & (tgt < V)
+    idx = torch.where(ok, tgt, torch.zeros_like(tgt))
+    zt = torch.where(ok, z.gather(1, idx[:, None])[:, 0], torch.zeros_like(lse))
+    p = torch.exp(z - lse[:, None])
+    p[torch.arange(len(tgt), device=h.device)[ok], idx[ok]] -= 1.0
+    g = ((p * dz).to(h.dtype) @ W).float()
+    return (lse - zt).sum(), g
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("softcap", [0.0, 30.0])
+def test_split_k_gradient_chunks(lm, dtype, softcap):
+    """Vocabulary chunks of 4096 columns take the 8-slice split-K gradient GEMM ([parts][n][vc/parts] softmax terms,
+    per-slice products summed in fixed order by smel_ce_acc_update); the last chunk (100 columns) falls back to one
+    slice. Loss and gradient against the fp64 full-logit oracle and the rounded full-logit comparator."""
+    loss_mod, _ = lm
+    print(f"split-K CE {dtype} softcap {softcap}", flush=True)
+    torch.manual_seed(4)
+    n, H, V = 300, 256, 2 * 4096 + 100
+    h = (torch.randn(n, H, device="cuda") * 0.5).to(dtype)
+    W = (torch.randn(V, H, device="cuda") * 0.2).to(dtype)
+    tgt = torch.randint(0, V, (n,), device="cuda")
+    tgt[:4] = torch.tensor([0, 4095, 4096, V - 1])                      # chunk edges and the short last chunk
+    head = loss_mod.LMHead(weight=W, vocab_chunk=4096, softcap=softcap)
+    assert [loss_mod._split_parts(v1 - v0) for v0, v1 in head.chunks()] == [8, 8, 1]
+    l1, g1 = loss_mod._ce_chunk(h, head, tgt, True)
+    l64, g64 = LR.full_ce(h, W, tgt, softcap)
+    lc, gc = rounded_full_ce(h, W, tgt, softcap)
+    tol_l, tol_g = (1e-3, 3e-2) if dtype == torch.bfloat16 else (1e-5, 1e-4)
+    assert abs(l1.item() - float(l64)) / abs(float(l64)) < tol_l
+    assert (g1.double().cpu() - g64).norm() / g64.norm() < tol_g
+    assert abs(l1.item() - lc.item()) / abs(lc.item()) < tol_l
+    assert (g1 - gc).norm() / gc.norm() < (2e-2 if dtype == torch.bfloat16 else 1e-4)
+    l2, g2 = loss_mod._ce_chunk_two_pass(h, head, tgt, True)           # the same sums without any rescaling
+    assert abs(l1.item() - l2.item()) / abs(l2.item()) < tol_l
+    assert (g1 - g2).norm() / g2.norm() < (2e-2 if dtype == torch.bfloat16 else 1e-5)
+
+
+def test_targets_outside_the_vocabulary(lm):
+    """A target outside [0, V) (e.g. an ignore index of -100 that a caller did not filter) matches no row: its loss
+    term is the log-sum-exp alone and its gradient has no target row, as in the reference's _ce_chunk; no row of W is
+    gathered for it."""
+    loss_mod, _ = lm
+    torch.manual_seed(5)
+    n, H, V = 40, 64, 900
+    h = torch.randn(n, H, device="cuda") * 0.5
+    W = torch.randn(V, H, device="cuda") * 0.2
+    tgt = torch.randint(0, V, (n,), device="cuda")
+    tgt[3], tgt[7], tgt[11] = -100, V, V + 1000
+    for softcap in (0.0, 30.0):
+        head = loss_mod.LMHead(weight=W, vocab_chunk=256, softcap=softcap)
+        l1, g1 = loss_mod._ce_chunk(h, head, tgt, True)
+        lc, gc = rounded_full_ce(h, W, tgt, softcap)
+        assert abs(l1.item() - lc.item()) < 1e-4 * abs(lc.item())
+        assert (g1 - gc).norm() / gc.norm() < 1e-4
