@@ -214,11 +214,12 @@ int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
                  int64_t ldo, uint16_t* hsave, hipStream_t stream);
 
 /* ---- (A13) replaces the combine of routed_experts, smel/moe.py:248-252 (+ the shared add of :263):
- * out[t] = bf16( sum_k topv[t,k] * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Y[TK+t])] ), k in fixed order, topv fp32.
- * inv [T*K] (optional, smel_dispatch's): a slot with inv < 0 (an expert id out of range, dropped by the dispatch)
- * adds nothing. */
-int smel_combine(const uint16_t* Y, const float* topv, const int32_t* inv, const float* sgate, int64_t T, int64_t K,
-                 int64_t H, uint16_t* out, hipStream_t stream);
+ * out[t] = bf16( sum_k topv[t,k] * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Ysh[t])] ), k in fixed order, topv fp32;
+ * the shared expert's row Ysh[t] is Y[TK+t] (the fused shared expert) when Ysh is NULL, else row t of Ysh [T][H]
+ * (a shared expert of another intermediate size, run as its own GEMMs). inv [T*K] (optional, smel_dispatch's): a slot
+ * with inv < 0 (an expert id out of range, dropped by the dispatch) adds nothing. */
+int smel_combine(const uint16_t* Y, const float* topv, const int32_t* inv, const float* sgate, const uint16_t* Ysh,
+                 int64_t T, int64_t K, int64_t H, uint16_t* out, hipStream_t stream);
 
 /* ---- (A10/A11 backward) grouped GEMM, backward: acc = A W per group (contraction over w.R), W in the transposed
  * layouts (smel_pack_int4_t / smel_pack_bf16_t), int4 re-dequantized in registers, plus ext[row] . w.ext_*[n][0:32]
@@ -241,21 +242,24 @@ int64_t smel_gmm_bwd_nblocks(int64_t C);
 
 /* ---- (A15) router backward (autograd of route + renorm + the shared gate, smel/moe.py:162-167, 201):
  * dtopv[t,k] = sum_j dwp[inv[t*K+k]][j]; d renorm; d gather; d softmax (probs) -> dlogits [T][ldl] bf16 with
- * dlogits[t][E] = d shared-gate logit (sum_j dwp[TK+t][j] * sg (1-sg)) when sgate != NULL, zero padding to ldl.
+ * dlogits[t][E] = d shared-gate logit (sum_j dwp[TK+t][j] * sg (1-sg), or with dwp_sh != NULL sum_j dwp_sh[t][j] over
+ * its nblk_sh columns: the shared expert run as its own GEMMs) when sgate != NULL, zero padding to ldl.
  * dtopv_out [T][K] fp32 (optional) receives dtopv. inv = NULL: dwp rows are the slots t*K+k themselves (TK = T*K).
  * per_expert_scale [E] bf16 (optional, route_gemma4): the routed value was renorm * per_expert_scale[id], so dtopv
  * is multiplied by it before the renorm backward. */
 int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs, const int32_t* topi32,
-                   const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK, uint16_t* dlogits, int64_t ldl,
-                   float* dtopv_out, const uint16_t* per_expert_scale, hipStream_t stream);
+                   const float* sgate, const float* dwp_sh, int64_t nblk_sh, int64_t T, int64_t K, int64_t E,
+                   int64_t TK, uint16_t* dlogits, int64_t ldl, float* dtopv_out, const uint16_t* per_expert_scale,
+                   hipStream_t stream);
 
 /* d(combine weight) of routed_experts when topv is an input: dtopv[p] = sum_j dwp[inv[p]][j], fp32 [TK]. */
 int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, float* dtopv, hipStream_t stream);
 
-/* ---- dX of the layer: dx[t] = bf16( sum_k DXS[t*K+k] + [DXS[TK+t]] + [DXR[t]] ), fixed order, fp32; slots with
- * inv < 0 (inv optional, as in smel_combine) add nothing. */
-int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, const int32_t* inv, int32_t with_shared, int64_t T,
-                   int64_t K, int64_t H, uint16_t* dx, hipStream_t stream);
+/* ---- dX of the layer: dx[t] = bf16( sum_k DXS[t*K+k] + [shared row] + [DXR[t]] ), fixed order, fp32; the shared row
+ * (with_shared) is DXS[TK+t], or DXSH[t] when dxsh is given; slots with inv < 0 (inv optional, as in smel_combine)
+ * add nothing. */
+int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, const int32_t* inv, int32_t with_shared,
+                   const uint16_t* dxsh, int64_t T, int64_t K, int64_t H, uint16_t* dx, hipStream_t stream);
 
 /* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP), up to four
  * products in one launch. For job j and every LoRA group lora_groups[i] (expert id, or E for the shared rows

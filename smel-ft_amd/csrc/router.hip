@@ -241,8 +241,9 @@ void launch_select(hipStream_t stream, const uint16_t* logits, int ldl, int T, i
 //   shared gate: dlogit_sg = (sum_j dwp[TK+t][j]) * sg (1 - sg)
 __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, int nblk,
                                                  const int32_t* __restrict__ inv, const float* __restrict__ probs,
-                                                 const int32_t* __restrict__ topi32, const float* __restrict__ sgate, int T,
-                                                 int K, int E, int TK,
+                                                 const int32_t* __restrict__ topi32, const float* __restrict__ sgate,
+                                                 const float* __restrict__ dwp_sh, int nblk_sh, int T, int K, int E,
+                                                 int TK,
                                                  uint16_t* __restrict__ dlogits, int ldl,
                                                  float* __restrict__ dtopv_out, const uint16_t* __restrict__ pes) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -288,7 +289,10 @@ __global__ __launch_bounds__(256) void route_bwd(const float* __restrict__ dwp, 
       g = probs[t * E + e] * (dpe - pdp);
     } else if (e == E && sgate) {
       float ds = 0.f;
-      for (int j = 0; j < nblk; ++j) ds += dwp[(int64_t)(TK + t) * nblk + j];
+      if (dwp_sh)   // the shared expert ran as its own GEMMs: its row-weight partials, [T][nblk_sh]
+        for (int j = 0; j < nblk_sh; ++j) ds += dwp_sh[t * nblk_sh + j];
+      else
+        for (int j = 0; j < nblk; ++j) ds += dwp[(int64_t)(TK + t) * nblk + j];
       const float sgv = sgate[t];
       g = ds * sgv * (1.0f - sgv);
     }
@@ -441,17 +445,18 @@ extern "C" int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, i
 }
 
 extern "C" int smel_route_bwd(const float* dwp, int64_t nblk, const int32_t* inv, const float* probs,
-                              const int32_t* topi32, const float* sgate, int64_t T, int64_t K, int64_t E, int64_t TK,
-                              uint16_t* dlogits, int64_t ldl, float* dtopv_out, const uint16_t* per_expert_scale,
-                              hipStream_t stream) {
+                              const int32_t* topi32, const float* sgate, const float* dwp_sh, int64_t nblk_sh,
+                              int64_t T, int64_t K, int64_t E, int64_t TK, uint16_t* dlogits, int64_t ldl,
+                              float* dtopv_out, const uint16_t* per_expert_scale, hipStream_t stream) {
+  SMEL_REQUIRE(!dwp_sh || nblk_sh > 0, SMEL_EINVAL, "route_bwd: nblk_sh must be positive with dwp_sh");
   SMEL_REQUIRE(T >= 0 && K > 0 && K <= 16 && E > 0 && nblk > 0, SMEL_EINVAL, "route_bwd: bad sizes");
   SMEL_REQUIRE(ldl >= E + (sgate ? 1 : 0), SMEL_EINVAL, "route_bwd: ldl %lld too small", (long long)ldl);
   if (T == 0) return 0;
   SMEL_REQUIRE(dwp && probs && topi32 && dlogits, SMEL_EINVAL, "route_bwd: null pointer");
   SMEL_REQUIRE(inv || TK == T * K, SMEL_EINVAL, "route_bwd: without inv, dwp rows are the T*K slots");
-  route_bwd<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(dwp, (int)nblk, inv, probs, topi32, sgate, (int)T, (int)K,
-                                                         (int)E, (int)TK, dlogits, (int)ldl, dtopv_out,
-                                                         per_expert_scale);
+  route_bwd<<<(unsigned)((T + 3) / 4), 256, 0, stream>>>(dwp, (int)nblk, inv, probs, topi32, sgate, dwp_sh,
+                                                         (int)nblk_sh, (int)T, (int)K, (int)E, (int)TK, dlogits,
+                                                         (int)ldl, dtopv_out, per_expert_scale);
   return smel::launch_status();
 }
 

@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("SMEL_MOE_LIB") or os.path.join(HERE, "libsmel_moe.so"
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -70,15 +70,15 @@ SIGNATURES = {
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, i64, vp, vp]),
-    "smel_combine": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
+    "smel_combine": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp]),
     "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, vp, vp, vp, vp, i64, vp, vp]),
     "smel_gmm_bwd_nblocks": (i64, [i64]),
-    "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, i64, i64, i64, i64, vp, i64, vp, vp, vp]),
+    "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp, vp, vp]),
     "smel_route_gemma4": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_gemma4_prenorm_bwd": (i32, [vp, vp, vp, vp, i64, i64, vp, vp]),
     "smel_dtopv": (i32, [vp, i64, vp, i64, vp, vp]),
-    "smel_dx_reduce": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
+    "smel_dx_reduce": (i32, [vp, vp, vp, i32, vp, i64, i64, i64, vp, vp]),
     "smel_lora_wgrad": (i32, [ctypes.POINTER(WgJob), i32, vp, i64, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp,
                               i64, vp]),
     "smel_lora_wgrad_ws_floats": (i64, [ctypes.POINTER(WgJob), i32, i64, i64]),

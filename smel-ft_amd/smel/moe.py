@@ -464,7 +464,7 @@ class _RouteFn(torch.autograd.Function):
         wr = _router_ext_weight(gate_w, None)
         Epad = wr.R
         dl = torch.empty(T, Epad, dtype=torch.bfloat16, device=dev)
-        L.call("smel_route_bwd", L.ptr(dwp), 1, None, L.ptr(probs), L.ptr(topi32), None, T, K, E, T * K,
+        L.call("smel_route_bwd", L.ptr(dwp), 1, None, L.ptr(probs), L.ptr(topi32), None, None, 0, T, K, E, T * K,
                L.ptr(dl), Epad, None, None, L.stream())
         dx = _router_dx(dl, wr, T)
         return dx, None, None
@@ -522,7 +522,7 @@ class _RouteGemma4Fn(torch.autograd.Function):
         wr = _router_ext_weight(proj, None)
         dl = torch.empty(T, wr.R, dtype=torch.bfloat16, device=dev)
         dw = dtopv.float().contiguous()
-        L.call("smel_route_bwd", L.ptr(dw), 1, None, L.ptr(probs), L.ptr(topi32), None, T, K, E, T * K,
+        L.call("smel_route_bwd", L.ptr(dw), 1, None, L.ptr(probs), L.ptr(topi32), None, None, 0, T, K, E, T * K,
                L.ptr(dl), wr.R, None, L.ptr(pes), L.stream())
         dxn = _router_dx(dl, wr, T)
         dh = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
@@ -574,10 +574,12 @@ def _prep_lora(ex: LayerExperts, lora_ex, lora_sh, with_shared: bool, H: int, de
 
 
 def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
-                      need_grad: bool, c: _Ctx, prep=None):
+                      need_grad: bool, c: _Ctx, prep=None, shared_rows=None):
     """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up, down, sgate fp32 [T], gate_up^T, down^T) or None
     (packed forward and transposed layouts of the shared expert's [2I,H] / [H,I] weights). ``prep`` = (_Fork,
-    (lb_ex, lb_sh)) when the LoRA layouts were launched on a side stream (joined before their first use)."""
+    (lb_ex, lb_sh)) when the LoRA layouts were launched on a side stream (joined before their first use).
+    ``shared_rows`` = (sgate fp32 [T], y_shared bf16 [T, H]) adds a shared expert computed elsewhere (one whose
+    intermediate size differs from the experts') to the combine."""
     T, H = x.shape
     E = ex.E
     dev = x.device
@@ -632,7 +634,10 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dn), 0, _ACT[ex.act], L.ptr(Y), H, None, st, tag="gemm_dn_fwd")
     out = bf(T, H)
-    L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(inv), L.ptr(sgate), T, K, H, L.ptr(out), st)
+    ysh = None
+    if shared_rows is not None:
+        sgate, ysh = shared_rows
+    L.call("smel_combine", L.ptr(Y), L.ptr(topv), L.ptr(inv), L.ptr(sgate), L.ptr(ysh), T, K, H, L.ptr(out), st)
     # everything the backward needs
     c.T, c.H, c.I, c.E, c.K, c.TK, c.M, c.maxt = T, H, I, E, K, TK, M, maxt
     c.ex, c.shared_w = ex, (sh_gu_t, sh_dn_t) if shared is not None else None
@@ -645,9 +650,11 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     return out
 
 
-def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
+def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=None):
     """Returns (dx_experts_plus_router, dtopv or None, {lora_param_name: grad}). ``router`` = (probs, topi32, wr) for
-    the fused layer (router + shared gate backward folded into the dX reduce)."""
+    the fused layer (router + shared gate backward folded into the dX reduce). ``shared_split`` = (dwp_sh, nblk_sh,
+    dx_sh) of a shared expert that ran as its own GEMMs: its row-weight partials (for the shared gate's gradient) and
+    its dX rows."""
     t = c.tensors
     T, H, I, E, K, TK, M, maxt = c.T, c.H, c.I, c.E, c.K, c.TK, c.M, c.maxt
     dev = dout.device
@@ -687,8 +694,9 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
         dl = bf(T, Epad)
         dxr = bf(T, H)
         with side_r:
+            dwp_sh, nblk_sh = (shared_split[0], shared_split[1]) if shared_split is not None else (None, 0)
             L.call("smel_route_bwd", L.ptr(dwp), nblk, L.ptr(t["inv"]), L.ptr(probs), L.ptr(topi32),
-                   L.ptr(t["sgate"]), T, K, E, TK, L.ptr(dl), Epad, None, None, L.stream())
+                   L.ptr(t["sgate"]), L.ptr(dwp_sh), nblk_sh, T, K, E, TK, L.ptr(dl), Epad, None, None, L.stream())
             _router_dx(dl, wr, T, dxr)
     else:
         dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
@@ -731,8 +739,9 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None):
            tag="gemm_gu_bwd")
     side_r.join()
     dx = bf(T, H)
-    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), L.ptr(t["inv"]), int(t["sgate"] is not None), T, K, H, L.ptr(dx),
-           st)
+    dxsh = shared_split[2] if shared_split is not None else None
+    L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), L.ptr(t["inv"]), int(t["sgate"] is not None), L.ptr(dxsh), T,
+           K, H, L.ptr(dx), st)
     if side_w is not None:
         side_w.join()
     return dx, dtopv, grads
@@ -812,43 +821,67 @@ def _wgrad_jobs(H, I, grads, sets, j_agu, j_bgu, j_adn, j_bdn):
 
 
 class _MoELayerFn(torch.autograd.Function):
-    """The fused MoE layer (moe_forward): router + routed experts + shared expert, one forward and one backward."""
+    """The fused MoE layer (moe_forward): router + routed experts + shared expert, one forward and one backward. A
+    shared expert whose intermediate size equals the experts' is group E of the expert GEMMs; another size runs as its
+    own dense-group GEMMs (row weight = the shared gate) and joins in the combine and the dX reduce."""
 
     @staticmethod
     def forward(ctx, x, plan, stats, *leaves):
         T, H = x.shape
         E, K = plan["ex"].E, plan["top_k"]
         dev = x.device
-        fuse = plan["shared"] is not None
+        has_sh = plan["shared"] is not None
+        split = has_sh and plan["split_shared"]
+        fuse = has_sh and not split
         probs = torch.empty(T, E, dtype=torch.float32, device=dev)
         topv = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
         topv32 = torch.empty(T, K, dtype=torch.float32, device=dev)   # fp32 of topv: the combine weight
         topi = torch.empty(T, K, dtype=torch.int64, device=dev)
         topi32 = torch.empty(T, K, dtype=torch.int32, device=dev)
-        sgate = torch.empty(T, dtype=torch.float32, device=dev) if fuse else None
-        sgw = plan["shared"][2] if fuse else None
-        lg = torch.empty(T, L.load().smel_route_ld(E, int(fuse)), dtype=torch.bfloat16, device=dev)
+        sgate = torch.empty(T, dtype=torch.float32, device=dev) if has_sh else None
+        sgw = plan["shared"][2] if has_sh else None
+        lg = torch.empty(T, L.load().smel_route_ld(E, int(has_sh)), dtype=torch.bfloat16, device=dev)
         fork = _Fork(dev, 2)   # LoRA layouts overlap the router and the dispatch
         with fork:
-            bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"], fuse, H, dev)
+            bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"] if fuse else None, fuse, H, dev)
         L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
                L.ptr(topv32), L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.stream())
         if stats is not None:
             stats(probs, topv, topi)
         c = _Ctx()
         shared = (plan["shared"][0], plan["shared"][1], sgate, plan["shared"][4], plan["shared"][5]) if fuse else None
-        out = _forward_pipeline(x, plan["ex"], K, topv32, topi32, False, shared, plan["lora_ex"], plan["lora_sh"],
-                                plan["need_grad"], c, prep=(fork, bufs))
+        shared_rows = None
+        if split:
+            pgu, pdn, _, Is, pgu_t, pdn_t = plan["shared"]
+            lsh = plan["lora_sh"]
+            lb_sh = _LoRABufs(lsh, 1, H, Is, dev) if lsh is not None else None
+            ysh, sv = _dense_mlp_fwd(x, pgu, pdn, lb_sh, "silu", tag="gemm_shared")
+            shared_rows = (sgate, ysh)
+            c.split = (sv, pgu_t, pdn_t, lsh, sgate)
+        out = _forward_pipeline(x, plan["ex"], K, topv32, topi32, False, shared, plan["lora_ex"],
+                                plan["lora_sh"] if fuse else None, plan["need_grad"], c, prep=(fork, bufs),
+                                shared_rows=shared_rows)
         if plan["need_grad"]:
             c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw))
+            c.plan_lora_sh = plan["lora_sh"]
             ctx.c = c
         return out
 
     @staticmethod
     def backward(ctx, dout):
         c = ctx.c
-        dx, _, grads = _backward_pipeline(c, dout, router=c.router)
-        g = _shape_grads(grads, "ex", c.lora_ex) + _shape_grads(grads, "sh", c.lora_sh)
+        split = getattr(c, "split", None)
+        shared_split = None
+        grads_sh = None
+        if split is not None:
+            sv, pgu_t, pdn_t, lsh, sgate = split
+            dx_sh, grads_sh, dwp_sh, nblk_sh = _dense_mlp_bwd(sv, dout, pgu_t, pdn_t, lsh, "silu", sgate,
+                                                              tag="gemm_shared")
+            shared_split = (dwp_sh, nblk_sh, dx_sh)
+        dx, _, grads = _backward_pipeline(c, dout, router=c.router, shared_split=shared_split)
+        if grads_sh is not None:
+            grads["sh"] = grads_sh
+        g = _shape_grads(grads, "ex", c.lora_ex) + _shape_grads(grads, "sh", c.plan_lora_sh)
         ctx.c = None
         return (dx, None, None, *g)
 
@@ -897,6 +930,95 @@ def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
     return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
 
 
+class _DenseSaved:
+    """What the backward of a dense gated MLP needs from its forward."""
+    __slots__ = ("x", "actb", "hsave", "ext_gu", "ext_dn", "lb")
+
+
+def _dense_mlp_fwd(x, w_gu: PackedW, w_dn: PackedW, lb, act_name: str, tag: str = "gemm_mlp"):
+    """Gated MLP y = down(act(gate(x)) * up(x)) (+ LoRA on all three as the K-extension) as one dense group of the
+    grouped GEMMs (rows = tokens). Returns (y [T, H] bf16, _DenseSaved)."""
+    T, H = x.shape
+    Is = w_dn.C
+    dev = x.device
+    st = L.stream()
+    tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
+    bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+    g = lambda n: getattr(lb, n) if lb is not None else None
+    sc = lb.scale if lb is not None else 0.0
+    sv = _DenseSaved()
+    sv.x, sv.lb, sv.ext_gu, sv.ext_dn = x, lb, None, None
+    if lb is not None:
+        sv.ext_gu = bf(T, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, T, 0, None, 0, 1,
+               None, L.ptr(lb.a_gu), H, 0.0, sc, L.ptr(sv.ext_gu), st)
+    sv.actb, sv.hsave = bf(T, Is), bf(T, 2 * Is)
+    wg = _dense_wset(w_gu, g("fwd_gu"))
+    L.call("smel_gmm_fwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 0,
+           None, 0, 1, L.ptr(sv.ext_gu), 1, _ACT[act_name], L.ptr(sv.actb), Is, L.ptr(sv.hsave), st,
+           tag=tag + "_gu_fwd")
+    if lb is not None:
+        sv.ext_dn = bf(T, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(sv.actb), Is, T, 0, None, 0, 1,
+               None, L.ptr(lb.a_dn), Is, 0.0, sc, L.ptr(sv.ext_dn), st)
+    y = bf(T, H)
+    wd = _dense_wset(w_dn, g("fwd_dn"))
+    L.call("smel_gmm_fwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(sv.actb), Is, T, 0,
+           None, 0, 1, L.ptr(sv.ext_dn), 0, _ACT[act_name], L.ptr(y), H, None, st, tag=tag + "_dn_fwd")
+    return y, sv
+
+
+def _dense_mlp_bwd(sv: _DenseSaved, dy, w_gu_t: PackedW, w_dn_t: PackedW, lora, act_name: str, row_w,
+                   tag: str = "gemm_mlp"):
+    """Backward of _dense_mlp_fwd for the output row_w[t] * y[t] (row_w fp32 [T]: ones for a plain MLP, the shared
+    gate for the shared expert): returns (dx [T, H] bf16, {LoRA name: grad} or None, dwp [T][nblk] fp32 = the
+    per-column-block partials of <y[t], dy[t]>, i.e. d loss / d row_w[t], nblk)."""
+    x, lb = sv.x, sv.lb
+    dy = _bf16(dy)
+    T, H = x.shape
+    Is = w_dn_t.C
+    dev = x.device
+    st = L.stream()
+    tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
+    bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+    g = lambda n: getattr(lb, n) if lb is not None else None
+    sc = lb.scale if lb is not None else 0.0
+    ext_db = ext_dxa = None
+    if lb is not None:
+        ext_db = bf(T, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dy), H, T, 0, None, 0, 1,
+               None, L.ptr(lb.bt_dn), H, 0.0, sc, L.ptr(ext_db), st)
+    nblk = L.load().smel_gmm_bwd_nblocks(Is)
+    dh = bf(T, 2 * Is)
+    dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
+    wd = _dense_wset(w_dn_t, g("at_dn"))
+    L.call("smel_gmm_bwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
+           None, 0, 1, L.ptr(ext_db), 1, _ACT[act_name], L.ptr(sv.hsave), L.ptr(sv.actb), None, L.ptr(row_w),
+           L.ptr(dh), 2 * Is, L.ptr(dwp), st, tag=tag + "_dn_bwd")
+    if lb is not None:
+        ext_dxa = bf(T, EXT)
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * Is, T, 0, None, 0, 1,
+               None, L.ptr(lb.bt_gu), 2 * Is, 0.0, sc, L.ptr(ext_dxa), st)
+    dx = bf(T, H)
+    wg = _dense_wset(w_gu_t, g("at_gu"))
+    L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
+           0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H, None, st,
+           tag=tag + "_gu_bwd")
+    grads = None
+    if lb is not None:
+        zero = torch.zeros(2, dtype=torch.int32, device=dev)     # offsets of zero experts
+        groups = torch.zeros(1, dtype=torch.int32, device=dev)   # group 0 >= E = 0: rows [0, T)
+        gs = _alloc_lora_grads(lora, dev)
+        # the down projection's products take the row weight (dh already carries it)
+        jobs = _wgrad_jobs(H, Is, (None, gs), (None, lora), (ext_dxa, x, T, 0, 0), (sv.ext_gu, dh, T, 0, 0),
+                           (ext_db, sv.actb, T, 0, 1), (sv.ext_dn, dy, T, 0, 1))
+        ws = _wgrad_ws(jobs, 1, T, dev)
+        L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), 1, 0, L.ptr(zero), 0, T, 0, 1, None, None, L.ptr(row_w),
+               T, L.ptr(ws), ws.numel(), st, tag="lora_wgrad")
+        grads = gs
+    return dx, grads, dwp, nblk
+
+
 class _MLPFn(torch.autograd.Function):
     """Gated MLP with LoRA on gate/up/down (mlp_lora, smel/moe.py:183-194) as one dense group of the grouped GEMMs:
     rows = tokens, weights = the stacked gate_up [2Is, H] and down [H, Is], each given as (forward layout, transposed
@@ -904,88 +1026,18 @@ class _MLPFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_gu2, w_dn2, lora, act_name, *leaves):
-        T, H = x.shape
-        w_gu, w_dn = w_gu2[0], w_dn2[0]
-        Is = w_dn.C
-        dev = x.device
-        st = L.stream()
-        tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
-        lb = _LoRABufs(lora, 1, H, Is, dev) if lora is not None else None
-        bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
-        g = lambda n: getattr(lb, n) if lb is not None else None
-        sc = lb.scale if lb is not None else 0.0
-        ext_gu = ext_dn = None
-        if lb is not None:
-            ext_gu = bf(T, EXT)
-            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, T, 0, None, 0, 1,
-                   None, L.ptr(lb.a_gu), H, 0.0, sc, L.ptr(ext_gu), st)
-        actb, hsave = bf(T, Is), bf(T, 2 * Is)
-        wg = _dense_wset(w_gu, g("fwd_gu"))
-        L.call("smel_gmm_fwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 0,
-               None, 0, 1, L.ptr(ext_gu), 1, _ACT[act_name], L.ptr(actb), Is, L.ptr(hsave), st, tag="gemm_mlp_gu_fwd")
-        if lb is not None:
-            ext_dn = bf(T, EXT)
-            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(actb), Is, T, 0, None, 0, 1,
-                   None, L.ptr(lb.a_dn), Is, 0.0, sc, L.ptr(ext_dn), st)
-        y = bf(T, H)
-        wd = _dense_wset(w_dn, g("fwd_dn"))
-        L.call("smel_gmm_fwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), Is, T, 0,
-               None, 0, 1, L.ptr(ext_dn), 0, _ACT[act_name], L.ptr(y), H, None, st, tag="gemm_mlp_dn_fwd")
-        ctx.save_for_backward(x, actb, hsave)
-        ctx.w = (w_gu2[1], w_dn2[1])
-        ctx.ext = (ext_gu, ext_dn)
-        ctx.lb, ctx.lora, ctx.act_name = lb, lora, act_name
+        lb = _LoRABufs(lora, 1, x.shape[1], w_dn2[0].C, x.device) if lora is not None else None
+        y, sv = _dense_mlp_fwd(x, w_gu2[0], w_dn2[0], lb, act_name)
+        ctx.sv, ctx.w, ctx.lora, ctx.act_name = sv, (w_gu2[1], w_dn2[1]), lora, act_name
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x, actb, hsave = ctx.saved_tensors
-        w_gu, w_dn = ctx.w
-        ext_gu, ext_dn = ctx.ext
-        lb, lora = ctx.lb, ctx.lora
-        dy = _bf16(dy)
-        T, H = x.shape
-        Is = w_dn.C
-        dev = x.device
-        st = L.stream()
-        tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
-        bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
-        g = lambda n: getattr(lb, n) if lb is not None else None
-        sc = lb.scale if lb is not None else 0.0
-        ones = torch.ones(T, dtype=torch.float32, device=dev)       # row weight 1 (no combine weight here)
-        ext_db = ext_dxa = None
-        if lb is not None:
-            ext_db = bf(T, EXT)
-            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dy), H, T, 0, None, 0, 1,
-                   None, L.ptr(lb.bt_dn), H, 0.0, sc, L.ptr(ext_db), st)
-        nblk = L.load().smel_gmm_bwd_nblocks(Is)
-        dh = bf(T, 2 * Is)
-        dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
-        wd = _dense_wset(w_dn, g("at_dn"))
-        L.call("smel_gmm_bwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
-               None, 0, 1, L.ptr(ext_db), 1, _ACT[ctx.act_name], L.ptr(hsave), L.ptr(actb), None, L.ptr(ones),
-               L.ptr(dh), 2 * Is, L.ptr(dwp), st, tag="gemm_mlp_dn_bwd")
-        if lb is not None:
-            ext_dxa = bf(T, EXT)
-            L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * Is, T, 0, None, 0, 1,
-                   None, L.ptr(lb.bt_gu), 2 * Is, 0.0, sc, L.ptr(ext_dxa), st)
-        dx = bf(T, H)
-        wg = _dense_wset(w_gu, g("at_gu"))
-        L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
-               0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H, None, st,
-               tag="gemm_mlp_gu_bwd")
-        grads = [None] * 6
-        if lb is not None:
-            zero = torch.zeros(2, dtype=torch.int32, device=dev)     # offsets of zero experts
-            groups = torch.zeros(1, dtype=torch.int32, device=dev)   # group 0 >= E = 0: rows [0, T)
-            gs = _alloc_lora_grads(lora, dev)
-            jobs = _wgrad_jobs(H, Is, (None, gs), (None, lora), (ext_dxa, x, T, 0, 0), (ext_gu, dh, T, 0, 0),
-                               (ext_db, actb, T, 0, 0), (ext_dn, dy, T, 0, 0))
-            ws = _wgrad_ws(jobs, 1, T, dev)
-            L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), 1, 0, L.ptr(zero), 0, T, 0, 1, None, None, None, T,
-                   L.ptr(ws), ws.numel(), st, tag="lora_wgrad")
-            grads = [gs.get(n) for n in _LORA_NAMES]
-        ctx.lb = ctx.lora = ctx.ext = ctx.w = None
+        sv, (w_gu_t, w_dn_t), lora = ctx.sv, ctx.w, ctx.lora
+        ones = torch.ones(sv.x.shape[0], dtype=torch.float32, device=dy.device)   # row weight 1
+        dx, gs, _, _ = _dense_mlp_bwd(sv, dy, w_gu_t, w_dn_t, lora, ctx.act_name, ones)
+        grads = [gs.get(n) for n in _LORA_NAMES] if gs is not None else [None] * 6
+        ctx.sv = ctx.w = ctx.lora = None
         return (dx, None, None, None, None, *grads)
 
 
@@ -1058,14 +1110,12 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
     lora_ex = lora_layer.experts if lora_layer is not None else None
     lora_sh = lora_layer.shared if lora_layer is not None else None
     shared = _shared_weights(W)
-    if shared is not None:
-        I = (ex.frozen.dn["q"].shape[2] * 2) if isinstance(ex.frozen, Int4Experts) else ex.frozen.down.shape[2]
-        if shared[3] != I:
-            raise NotImplementedError("fused shared expert needs shared intermediate == expert intermediate")
+    # a shared expert of the experts' intermediate size is fused into the expert GEMMs; another runs on its own
+    split = shared is not None and shared[3] != _expert_I(ex)
     if lora_ex is not None and (ex.sel_ids is None or len(ex._slot) == 0):
         lora_ex = None
     plan = {"ex": ex, "top_k": int(top_k), "gate_w": _bf16(W["mlp.gate.weight"]), "shared": shared,
-            "lora_ex": lora_ex, "lora_sh": lora_sh if shared is not None else None}
+            "split_shared": split, "lora_ex": lora_ex, "lora_sh": lora_sh if shared is not None else None}
     leaves = _lora_leaves(plan["lora_ex"]) + _lora_leaves(plan["lora_sh"])
     plan["need_grad"] = torch.is_grad_enabled() and (x2d.requires_grad or any(p.requires_grad for p in leaves))
     return _MoELayerFn.apply(x, plan, stats, *leaves)

@@ -452,6 +452,14 @@ LAYERS = {
                       lora_b_std=0.05),
     "no_shared": dict(T=190, H=128, E=8, I=64, K=2, n_sel=2, r=4, alpha=8.0, shared_inter=None, group=32,
                       lora_b_std=0.05),
+    # a shared expert of another intermediate size than the experts' runs as its own GEMMs (smel/moe.py:197-201)
+    "shared_wide": dict(T=300, H=256, E=16, I=128, K=4, n_sel=3, r=8, alpha=16.0, shared_inter=192, group=64,
+                        lora_b_std=0.05),
+    "shared_narrow": dict(T=260, H=128, E=8, I=128, K=2, n_sel=2, r=4, alpha=8.0, shared_inter=64, group=64,
+                          lora_b_std=0.05),
+    # more than 256 experts (the router's 8-logits-per-lane selection)
+    "e512": dict(T=200, H=128, E=512, I=64, K=8, n_sel=3, r=4, alpha=8.0, shared_inter=64, group=64,
+                 lora_b_std=0.05),
 }
 
 
