@@ -716,7 +716,7 @@ def run_stream(args, dev):
 
 def run_quant(args, dev):
     """quantize_int4 (smel/quant.py:14-44) of a whole C2-shaped bank on the GPU: HIP kernel time per bank, and the
-    same algorithm as torch ops on the host CPU (sampled) as the baseline."""
+    oracle's restatement of the same algorithm as torch ops on the host CPU (sampled) as the baseline."""
     from smel import quant
     c = QWEN
     E, H, I = c["E"], c["H"], c["I"]
@@ -734,14 +734,15 @@ def run_quant(args, dev):
     nbytes = (gu.numel() + dn.numel()) * 2 + (gu.numel() + dn.numel()) // 2 + (gu.numel() + dn.numel()) // 64 * 4
     cpu = None
     if not args.no_cpu_baseline:
+        from oracle import moe_ref as R
         w = gu[:1].cpu()
         torch.set_num_threads(_cpu_threads())
         t0 = time.perf_counter()
-        quant._quantize_int4_host(w, 64)
+        R.quantize_int4(w, 64)
         dt = time.perf_counter() - t0
         per_bank_s = dt * E * 1.5
         cpu = {"value": round(1 / per_bank_s, 4), "unit": "banks/s", "cores": torch.get_num_threads(),
-               "kind": "port", "sample": f"1 expert's gate_up ({2 * I}x{H}) by the torch restatement on the CPU in "
+               "kind": "port", "sample": f"1 expert's gate_up ({2 * I}x{H}) by the oracle (torch ops) on the CPU in "
                                          f"{dt:.2f} s, scaled to the bank (x{E * 1.5:.0f}), cpu={_cpu_model()}"}
     t = bd.get("smel_quantize_int4", ms / 2)
     roof = {"kernel": "quantize_int4_reg_kernel<64>", "bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),

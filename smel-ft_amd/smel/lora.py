@@ -44,9 +44,11 @@ class _LoRASet(nn.Module):
             setattr(self, f"B_{p}", nn.Parameter(torch.zeros(*lead, fan_out, r)))
 
     def _deltas(self, idx):
-        """scale B_p A_p for the three projections at index ``idx`` of the leading dims (fp32)."""
-        return tuple(torch.matmul(getattr(self, f"B_{p}")[idx].float(), getattr(self, f"A_{p}")[idx].float())
-                     .mul_(self.scale) for p in _PROJ)
+        """(scale B_p) A_p for the three projections at index ``idx`` of the leading dims (fp32; B is scaled before
+        the product, the order of smel/lora.py:31-36, so merged weights round as the reference's)."""
+        def one(p):
+            return torch.matmul(getattr(self, f"B_{p}")[idx].float() * self.scale, getattr(self, f"A_{p}")[idx].float())
+        return tuple(one(p) for p in _PROJ)
 
 
 class ExpertsLoRA(_LoRASet):

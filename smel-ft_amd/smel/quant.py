@@ -3,9 +3,9 @@
 Format (the reference's, smel/quant.py:14-44): q uint8 [..., K/2] with the even column in the low nibble, scale and
 zero bf16 [..., K/group], w = q*scale + zero. ``dequant_int4`` is the MI355X kernel (fp32 math, one
 round-to-nearest-even, as the reference's GPU kernel smel/quant.py:51-67). ``quantize_int4`` is the offline packer of
-the reference's pack stage (not on the hot path): a GPU input runs the HIP kernel ``smel_quantize_int4`` (one thread
-per group, the reference's fp32 steps in its order); a host input (a pack stage on a machine without the GPU) runs
-the same steps as torch ops on the CPU.
+the reference's pack stage (not on the hot path): it always runs the HIP kernel ``smel_quantize_int4`` (one thread
+per group, the reference's fp32 steps in its order); a host tensor is copied to the current GPU for it and the
+result copied back, so there is no CPU quantizer in this package.
 """
 from __future__ import annotations
 
@@ -14,25 +14,20 @@ import torch
 from . import _lib as L
 
 
-def _q4_candidate(wg, lo, hi):
-    scale = ((hi - lo) / 15).clamp_min(1e-8).to(torch.bfloat16).float()
-    zero = lo.to(torch.bfloat16).float()
-    q = torch.round((wg - zero) / scale).clamp_(0, 15)
-    return q, scale, zero
-
-
 _QDT = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}
 
 
 def quantize_int4(w: torch.Tensor, group: int = 64, clip_search=(1.0, 0.95, 0.9, 0.85, 0.8)) -> dict:
     """w [..., K] -> {"q": uint8 [..., K/2], "scale": bf16 [..., K/group], "zero": bf16 [..., K/group]}
     (smel/quant.py:14-44): per group, the [min, max] range shrunk about its midpoint by the clip factor with the
-    smallest squared error (a later factor must be strictly better). GPU inputs: one HIP launch for the whole
-    tensor; host inputs: torch ops, 3-D inputs in slices of 16 experts as the reference."""
-    if not w.is_cuda:
-        return _quantize_int4_host(w, group, clip_search)
+    smallest squared error (a later factor must be strictly better). One HIP launch for the whole tensor; a host
+    tensor goes through the current GPU and the result comes back on the host."""
     K = w.shape[-1]
-    assert K % group == 0 and group % 2 == 0
+    assert K % group == 0 and group % 2 == 0, f"K={K} must be a multiple of the (even) group {group}"
+    if not w.is_cuda:
+        if not torch.cuda.is_available():
+            raise RuntimeError("quantize_int4 runs on the GPU (HIP kernel smel_quantize_int4); no GPU is visible")
+        return {k: v.cpu() for k, v in quantize_int4(w.cuda(), group, clip_search).items()}
     clip = list(clip_search or (1.0,))
     if w.dtype not in _QDT:
         w = w.float()
@@ -41,34 +36,11 @@ def quantize_int4(w: torch.Tensor, group: int = 64, clip_search=(1.0, 0.95, 0.9,
     q = torch.empty(*w.shape[:-1], K // 2, dtype=torch.uint8, device=w.device)
     scale = torch.empty(*w.shape[:-1], K // group, dtype=torch.bfloat16, device=w.device)
     zero = torch.empty_like(scale)
-    cf = (L.f32 * len(clip))(*clip)
-    L.call("smel_quantize_int4", L.ptr(wc), _QDT[wc.dtype], rows, K, group, cf, len(clip), L.ptr(q), L.ptr(scale),
-           L.ptr(zero), L.stream())
+    if rows:
+        cf = (L.f32 * len(clip))(*clip)
+        L.call("smel_quantize_int4", L.ptr(wc), _QDT[wc.dtype], rows, K, group, cf, len(clip), L.ptr(q),
+               L.ptr(scale), L.ptr(zero), L.stream())
     return {"q": q, "scale": scale, "zero": zero}
-
-
-def _quantize_int4_host(w: torch.Tensor, group: int = 64, clip_search=(1.0, 0.95, 0.9, 0.85, 0.8)) -> dict:
-    if w.dim() == 3 and w.shape[0] > 16:
-        parts = [_quantize_int4_host(w[i:i + 16], group, clip_search) for i in range(0, w.shape[0], 16)]
-        return {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
-    K = w.shape[-1]
-    assert K % group == 0 and group % 2 == 0
-    wg = w.float().reshape(*w.shape[:-1], K // group, group)
-    lo0, hi0 = wg.amin(-1, keepdim=True), wg.amax(-1, keepdim=True)
-    mid = (lo0 + hi0) / 2
-    best = None
-    for c in clip_search or (1.0,):
-        q, s, z = _q4_candidate(wg, mid + (lo0 - mid) * c, mid + (hi0 - mid) * c)
-        err = (q * s + z - wg).pow(2).sum(-1, keepdim=True)
-        if best is None:
-            best = [err, q, s, z]
-            continue
-        take = err < best[0]
-        best = [torch.where(take, n, o) for n, o in zip((err, q, s, z), best)]
-    _, q, s, z = best
-    q = q.to(torch.uint8).reshape(*w.shape[:-1], K)
-    return {"q": (q[..., 0::2] | (q[..., 1::2] << 4)).contiguous(),
-            "scale": s.squeeze(-1).to(torch.bfloat16), "zero": z.squeeze(-1).to(torch.bfloat16)}
 
 
 def dequant_int4(q: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:

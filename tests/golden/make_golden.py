@@ -7,11 +7,14 @@ bit-exactly:
 * ``quantize_int4`` (smel/quant.py:14-44): exact q/scale/zero bytes depend on the clip-search tie rule and on the
   fp32 reduction order of the squared error;
 * the composite ``moe_forward`` / ``routed_experts`` result and its autograd gradients at the tiny config C1
-  (smel/moe.py:214-263), as an end-to-end regression value for the oracle.
+  (smel/moe.py:214-263), as an end-to-end regression value for the oracle;
+* ``pack_layer`` / ``merge_experts`` / ``merge_mlp`` (smel/pack.py:8-45) on a small layer dict: the packed format's
+  names, dtypes and bytes, and the merged weights' bits.
 
 Everything is generated on the CPU in fp32 with fixed seeds and stored as safetensors (inputs and outputs, so the
-tests never re-run this script). Run:  python tests/golden/make_golden.py
+tests never re-run this script). Run:  python tests/golden/make_golden.py [quant] [c1] [pack]  (default: all)
 """
+import json
 import os
 import sys
 
@@ -28,6 +31,12 @@ def _import_reference():
     from smel import moe as ref_moe  # noqa: E402
     from smel import quant as ref_quant  # noqa: E402
     return ref_moe, ref_quant, ref_lora
+
+
+def _import_reference_pack():
+    sys.path.insert(0, REF_ROOT)
+    from smel import pack as ref_pack  # noqa: E402
+    return ref_pack
 
 
 def c1_inputs(seed=0):
@@ -77,7 +86,70 @@ def quant_cases():
     return cases
 
 
-def main():
+def pack_inputs(seed=11):
+    """One layer's tensors as a checkpoint holds them (names relative to the layer): dense weights in fp32, bf16 and
+    fp16, SSM parameters A_log / dt_bias (kept fp32), an int64 buffer, and 20 fused bf16 experts (H=64, I=64, more
+    than 16 so the quantizer's 16-expert slices show), plus LoRA factors for the merge (r=4, alpha=6: scale 1.5)."""
+    g = torch.Generator().manual_seed(seed)
+    H, I, E, Is, r = 64, 64, 20, 96, 4
+    t = {"input_layernorm.weight": 1 + 0.1 * torch.randn(H, generator=g),
+         "linear_attn.A_log": torch.randn(4, generator=g),
+         "linear_attn.dt_bias": torch.randn(4, generator=g),
+         "linear_attn.in_proj.weight": (torch.randn(3 * H, H, generator=g) * 0.02).bfloat16(),
+         "mlp.gate.weight": torch.randn(E, H, generator=g) * 0.02,
+         "mlp.shared_expert.gate_proj.weight": (torch.randn(Is, H, generator=g) * 0.02).bfloat16(),
+         "mlp.shared_expert.up_proj.weight": (torch.randn(Is, H, generator=g) * 0.02).bfloat16(),
+         "mlp.shared_expert.down_proj.weight": (torch.randn(H, Is, generator=g) * 0.02).bfloat16(),
+         "mlp.shared_expert_gate.weight": (torch.randn(1, H, generator=g) * 0.02).half(),
+         "conv1d.position_ids": torch.arange(7, dtype=torch.int64),
+         "mlp.experts.gate_up_proj": (torch.randn(E, 2 * I, H, generator=g) * 0.02).bfloat16(),
+         "mlp.experts.down_proj": (torch.randn(E, H, I, generator=g) * 0.02).bfloat16()}
+    lo = {}
+    for pre, lead, inter in (("ex_", (2,), I), ("sh_", (), Is)):
+        for n, shp in (("A_gate", (r, H)), ("A_up", (r, H)), ("A_down", (r, inter))):
+            lo[pre + n] = (torch.rand(*lead, *shp, generator=g) * 2 - 1) / shp[-1] ** 0.5
+        for n, shp in (("B_gate", (inter, r)), ("B_up", (inter, r)), ("B_down", (H, r))):
+            lo[pre + n] = torch.randn(*lead, *shp, generator=g) * 0.05
+    return t, lo, [3, 17]
+
+
+def write_pack():
+    ref_pack = _import_reference_pack()
+    from smel import lora as ref_lora  # noqa: E402  (already on sys.path)
+    t, lo, sel = pack_inputs()
+    out = {"in." + k: v.clone() for k, v in t.items()}
+    out.update({"lora." + k: v.clone() for k, v in lo.items()})
+    order = {}
+    for tag, ids, grp in (("sel", sel, 64), ("nosel", None, 32)):
+        pk = ref_pack.pack_layer(t, ids, grp)
+        order[tag] = list(pk)
+        out.update({f"{tag}.{k}": v.clone() for k, v in pk.items()})
+    exl = ref_lora.ExpertsLoRA(sel, 64, 64, 4, 6.0)
+    shl = ref_lora.MLPLoRA(64, 96, 4, 6.0)
+    with torch.no_grad():
+        for n in ("A_gate", "A_up", "A_down", "B_gate", "B_up", "B_down"):
+            getattr(exl, n).copy_(lo["ex_" + n])
+            getattr(shl, n).copy_(lo["sh_" + n])
+    gu, dn = ref_pack.merge_experts(t["mlp.experts.gate_up_proj"], t["mlp.experts.down_proj"], exl)
+    # only the selected experts' rows change; the other rows equal the input's
+    out["merge.gate_up_sel"], out["merge.down_sel"] = gu[sel].clone(), dn[sel].clone()
+    assert torch.equal(gu[[e for e in range(20) if e not in sel]],
+                       t["mlp.experts.gate_up_proj"][[e for e in range(20) if e not in sel]])
+    p = "mlp.shared_expert."
+    for n, w in zip(("gate", "up", "down"), ref_pack.merge_mlp(t[p + "gate_proj.weight"], t[p + "up_proj.weight"],
+                                                               t[p + "down_proj.weight"], shl)):
+        out["merge.sh_" + n] = w
+    path = os.path.join(HERE, "pack_layer.safetensors")
+    save_file(out, path, metadata={"order": json.dumps(order)})
+    os.chmod(path, 0o644)
+
+
+def main(parts):
+    if "pack" in parts:
+        write_pack()
+    if "quant" not in parts and "c1" not in parts:
+        print("wrote", sorted(os.listdir(HERE)))
+        return
     ref_moe, ref_quant, ref_lora = _import_reference()
     torch.manual_seed(0)
     out = {}
@@ -162,4 +234,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(set(sys.argv[1:]) or {"quant", "c1", "pack"})

@@ -1,15 +1,17 @@
 """GPU int4 quantizer (smel_quantize_int4 through smel.quant.quantize_int4) against the reference's own bytes and
-against the reference's algorithm in torch ops (smel/quant.py:5-44).
+against the oracle's restatement of the reference's algorithm in torch ops (oracle/moe_ref.py, smel/quant.py:5-44).
 
 Bar: the reference's golden bytes (tests/golden/quant_int4.safetensors, written by the reference's quantize_int4)
 bit for bit. On larger random banks, every group's q equals clamp(rint((w - zero) / scale), 0, 15) for the scale
-and zero it chose, and scale / zero equal those of the torch restatement except where two clip candidates' error
+and zero it chose, and scale / zero equal those of the oracle's restatement except where two clip candidates' error
 sums agree to within fp32 rounding (the reference leaves the order of that sum to its library): there the fp64
 errors of both choices must agree to 2e-5 relative, and at most 1 group in 10^3 may be such a tie."""
 import os
 
 import pytest
 import torch
+
+from oracle import moe_ref as R
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_int4.safetensors")
@@ -54,7 +56,7 @@ def test_random_banks(quant, dtype, group, shape):
     w[0, 0, :group] = 0.0                                   # a constant group: scale clamps to 1e-8
     w[0, 1, :group] *= 50                                    # an outlier group
     got = quant.quantize_int4(w, group)
-    ref = quant._quantize_int4_host(w.cpu(), group)
+    ref = R.quantize_int4(w.cpu(), group)
     s, z = got["scale"].cpu().float(), got["zero"].cpu().float()
     # q is exactly the rounding of w for the chosen (scale, zero)
     wg = w.cpu().float().reshape(*shape[:-1], -1, group)
@@ -78,3 +80,13 @@ def test_random_banks(quant, dtype, group, shape):
 def test_bad_group_is_an_assertion(quant):
     with pytest.raises(AssertionError):
         quant.quantize_int4(torch.randn(2, 48, device="cuda"), 64)
+
+
+def test_host_tensor_goes_through_the_gpu(quant):
+    """A host tensor is quantized by the same kernel and comes back on the host, equal to the device result."""
+    w = torch.randn(3, 8, 128) * 0.02
+    a, b = quant.quantize_int4(w, 64), quant.quantize_int4(w.cuda(), 64)
+    for k in ("q", "scale", "zero"):
+        assert not a[k].is_cuda and torch.equal(a[k], b[k].cpu())
+    e = quant.quantize_int4(torch.empty(0, 64, device="cuda"), 64)
+    assert e["q"].shape == (0, 32) and e["scale"].shape == (0, 1)

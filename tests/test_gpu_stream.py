@@ -14,24 +14,22 @@ H, E, I, K, T = 256, 16, 128, 4, 256
 def mods():
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")
-    from smel import moe, quant, stream
-    return moe, quant, stream
+    from smel import moe, pack, stream
+    return moe, pack, stream
 
 
-def make_layer(quant, seed):
+def make_layer(pack, seed):
+    """One packed layer (pack_layer's format, on the host) with two selected experts."""
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(seed)
     rn = lambda *s: (torch.randn(*s, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     gu, dn = rn(E, 2 * I, H), rn(E, H, I)
     sel = [1, 5 + seed % 3]
-    t = {f"experts.gate_up.{k}": v for k, v in quant.quantize_int4(gu, 64).items()}
-    t.update({f"experts.down.{k}": v for k, v in quant.quantize_int4(dn, 64).items()})
-    t.update({"experts.sel.ids": torch.tensor(sel), "experts.sel.gate_up": gu[sel].clone(),
-              "experts.sel.down": dn[sel].clone(), "mlp.gate.weight": rn(E, H),
-              "mlp.shared_expert.gate_proj.weight": rn(I, H), "mlp.shared_expert.up_proj.weight": rn(I, H),
-              "mlp.shared_expert.down_proj.weight": rn(H, I), "mlp.shared_expert_gate.weight": rn(1, H),
-              "self_attn.q_norm.weight": rn(64)})
-    return {k: v.cpu() for k, v in t.items()}
+    t = {"mlp.experts.gate_up_proj": gu, "mlp.experts.down_proj": dn, "mlp.gate.weight": rn(E, H),
+         "mlp.shared_expert.gate_proj.weight": rn(I, H), "mlp.shared_expert.up_proj.weight": rn(I, H),
+         "mlp.shared_expert.down_proj.weight": rn(H, I), "mlp.shared_expert_gate.weight": rn(1, H),
+         "self_attn.q_norm.weight": rn(64)}
+    return {k: v.cpu() for k, v in pack.pack_layer(t, sel, 64).items()}
 
 
 def run(moe, LW, x, gy):
@@ -42,8 +40,8 @@ def run(moe, LW, x, gy):
 
 
 def test_staged_layers_match_resident(mods):
-    moe, quant, stream = mods
-    layers = {l: make_layer(quant, l) for l in range(3)}
+    moe, pack, stream = mods
+    layers = {l: make_layer(pack, l) for l in range(3)}
     resident = {}
     for l, t in layers.items():
         dt = {k: v.cuda() for k, v in t.items()}
