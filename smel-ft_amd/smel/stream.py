@@ -155,6 +155,9 @@ class _StagedSource:
         self.copy = [torch.cuda.Stream(self.device) for _ in range(N_COPY_STREAMS)]   # default priority
         self.stats = {"load_s": 0.0, "wait_s": 0.0, "bytes": 0, "loads": 0}
         self.cache = {}                     # l -> LayerWeights staged (views into a slot)
+        # (PinnedLayer, event after its stage): a host arena made for one upload stays referenced until its copies
+        # are done, since the DMA reads it behind torch's back and torch would otherwise recycle the pinned block
+        self._in_flight = []
 
     # -- subclass hooks
     def _pinned(self, l) -> PinnedLayer:
@@ -162,6 +165,10 @@ class _StagedSource:
 
     def _ltype(self, l) -> str:
         return "linear_attention"
+
+    def _sel_ids(self, l, P: PinnedLayer):
+        """The selected experts of layer l: those the layer's own tensors name (``experts.sel.ids``)."""
+        return P.sel_ids
 
     # --
     def _slot_for(self, l, nbytes):
@@ -203,9 +210,12 @@ class _StagedSource:
         for d in s.done[1:]:
             L.call("smel_stream_wait", c0.cuda_stream, d.h)
         with torch.cuda.stream(c0):
-            LW = build_layer(l, self._ltype(l), t, P.sel_ids, self.group, act=self.act)
+            LW = build_layer(l, self._ltype(l), t, self._sel_ids(l, P), self.group, act=self.act)
             self._pack(LW.experts, P)
         L.call("smel_event_record", s.ready.h, c0.cuda_stream)
+        staged = torch.cuda.Event()
+        staged.record(c0)                   # c0 has waited on every copy stream's part of this upload
+        self._in_flight = [(p, e) for p, e in self._in_flight if not e.query()] + [(P, staged)]
         s.layer, s.LW = l, LW
         self.cache[l] = LW
         self.slots.remove(s)
@@ -262,6 +272,7 @@ class _StagedSource:
 
     def close(self):
         torch.cuda.synchronize(self.device)
+        self._in_flight.clear()
         self.cache.clear()
         self.slots.clear()
 
@@ -299,6 +310,58 @@ class PinnedSource(_StagedSource):
         return self.ltypes.get(l, "linear_attention")
 
 
+def _selected_rows(selection: dict, layers, ckpt) -> dict:
+    """{l: the packed layer's experts.sel.* tensors} for a new selection, from the original checkpoint's fused bf16
+    expert tensors (only the selected rows are read)."""
+    rows = {}
+    for l in layers:
+        ids = [int(e) for e in selection.get(l, [])]
+        if not ids:
+            continue
+        if ckpt is None:
+            raise ValueError("PackedSource: a new selection needs ckpt= to read the selected experts' bf16 rows")
+        part = {"experts.sel.ids": torch.tensor(ids, dtype=torch.long)}
+        for field, short in (("gate_up", "mlp.experts.gate_up_proj"), ("down", "mlp.experts.down_proj")):
+            part[f"experts.sel.{field}"] = ckpt.get_rows(ckpt.full_name(l, short), ids).contiguous()
+        rows[l] = part
+    return rows
+
+
+class CheckpointSource(_StagedSource):
+    """Layers straight from the original checkpoint (smel/stream.py:117-139): ``ckpt`` gives layer(l) (the layer's
+    tensors under layer-relative names, bf16 experts fused) and ``dims`` (layer_types, act). frozen="bf16" streams
+    the dense and expert tensors in ``dtype`` (SSM A_log / dt_bias and non-floating tensors as they are);
+    frozen="int4" packs each layer with pack_layer (int4 bank from the GPU quantizer, group ``quant_group``) before
+    it is pinned. The checkpoint reader itself is the caller's."""
+
+    def __init__(self, ckpt, device="cuda", dtype=torch.bfloat16, selection=None, resident=False, group=32,
+                 frozen="bf16", quant_group=64, max_on_gpu=2):
+        if frozen not in ("bf16", "int4"):
+            raise ValueError(f"frozen must be 'bf16' or 'int4', got {frozen!r}")
+        super().__init__(device, resident, max_on_gpu, group, getattr(ckpt.dims, "act", "silu"))
+        self.ckpt, self.d, self.dtype = ckpt, ckpt.dims, dtype
+        self.selection = selection or {}
+        self.frozen, self.quant_group = frozen, quant_group
+
+    def _host_layer(self, l) -> dict:
+        from .pack import _dense_part, pack_layer
+        t = self.ckpt.layer(l)
+        if self.frozen == "int4":
+            return pack_layer(t, self.selection.get(l), self.quant_group, self.dtype)
+        return {**_dense_part(t, self.dtype), **{k: v.to(self.dtype).contiguous() for k, v in t.items()
+                                                 if k.startswith("mlp.experts.")}}
+
+    def _pinned(self, l):
+        return PinnedLayer(self._host_layer(l))
+
+    def _sel_ids(self, l, P: PinnedLayer):
+        ids = self.selection.get(l)
+        return P.sel_ids if P.sel_ids is not None else (list(ids) if ids else None)
+
+    def _ltype(self, l):
+        return self.d.layer_types[l]
+
+
 class PackedSource(_StagedSource):
     """Layers from the packed block, one ``layer_{l:02d}.safetensors`` per layer (smel/stream.py:142-197). With
     pin=True every layer is read once into pinned RAM (up to pin_budget_gb); the rest are read and pinned at each
@@ -306,10 +369,13 @@ class PackedSource(_StagedSource):
 
     def __init__(self, packed_dir, dims, layers, device="cuda", resident=False, pin=False, group=32,
                  pin_budget_gb=9.0, preloaded=None, selection=None, ckpt=None, max_on_gpu=2):
-        if selection is not None or ckpt is not None:
-            raise NotImplementedError("re-selecting experts from the original checkpoint is outside this build")
+        """selection {l: [expert ids]} + ckpt: train another expert set on the same packed block. The int4 bank holds
+        every expert, so only the new selection's bf16 rows are read, once, from the original checkpoint (``ckpt``
+        with full_name(l, short) and get_rows(name, ids), the reference's Checkpoint interface); the packed block's
+        own ``experts.sel.*`` are then ignored, and a layer left out of ``selection`` trains no routed expert."""
         super().__init__(device, resident, max_on_gpu, group, getattr(dims, "act", "silu"))
         self.dir, self.d = packed_dir, dims
+        self.sel_rows = None if selection is None else _selected_rows(selection, layers, ckpt)
         self.preloaded = preloaded or {}
         self.pinned, self.pinned_gb = {}, 0.0
         if pin:
@@ -328,10 +394,16 @@ class PackedSource(_StagedSource):
 
     def _read(self, l):
         if l in self.preloaded:
-            return self.preloaded[l]
-        from safetensors import safe_open
-        with safe_open(self._path(l), "pt") as f:
-            return {k: f.get_tensor(k) for k in f.keys()}
+            t = self.preloaded[l]
+        else:
+            from safetensors import safe_open
+            with safe_open(self._path(l), "pt") as f:
+                t = {k: f.get_tensor(k) for k in f.keys()}
+        if self.sel_rows is None:
+            return t
+        t = {k: v for k, v in t.items() if not k.startswith("experts.sel.")}
+        t.update(self.sel_rows.get(l, {}))
+        return t
 
     def _pinned(self, l):
         return self.pinned[l] if l in self.pinned else PinnedLayer(self._read(l))
