@@ -23,11 +23,14 @@ Other workloads of BASELINE.json (``--workload``), each printing one JSON line o
       248320, bf16, token chunk 1024, vocabulary chunk 32768;
   norms  the RMSNorm family around the block (include/smel_norm.h), forward + backward at the Qwen3.6 block's
       shapes for T=4092: input norm and residual add + post-attention norm [T, 2048], q / k head norms
-      [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128].
+      [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128];
+  peaks  the achievable MFMA rate and HBM bandwidth of this GPU by kernels that do nothing else
+      (include/smel_probe.h), and hipBLASLt's bf16 GEMM for comparison.
 
 Every line carries tokens/s of the whole step, the roofline of the dominant kernel (HIP-event timed launches inside
 this run: algorithmic FLOPs and bytes per launch against MI355X's dense bf16 MFMA and HBM peaks, the binding one
-reported) and, for C3, the CPU baseline (the oracle's restatement of the reference's CPU torch path, timed on this
+reported; beside it the fraction of the achievable peak measured by the probes of ``--workload peaks``, its HBM
+traffic and MFMA-busy share from the committed rocprofv3 --pmc summaries) and, for C3 and C2, the CPU baseline (the oracle's restatement of the reference's CPU torch path, timed on this
 host's cores on one full pass of the same layer).
 """
 import argparse
@@ -232,9 +235,11 @@ def kernel_work(tag, c, S):
     return w.get(tag)
 
 
-def roofline(breakdown, c, S):
+def roofline(breakdown, c, S, pmc=False):
     """The dominant (longest average launch) kernel with a work model: its roofline time max(F / P_mfma,
-    B / BW_hbm) decides the bound; achieved = that kernel's F or B over its HIP-event-timed launch."""
+    B / BW_hbm) decides the bound; achieved = that kernel's F or B over its HIP-event-timed launch. pmc: the
+    workload is the one the committed rocprofv3 --pmc summaries were taken on (C3), so its HBM traffic and MFMA-busy
+    share are reported from them."""
     known = {k: v for k, v in breakdown.items() if kernel_work(k, c, S)}
     dom = max(known, key=known.get)
     F, B = kernel_work(dom, c, S)
@@ -245,18 +250,34 @@ def roofline(breakdown, c, S):
     else:
         out = {"kernel": dom, "bound": "hbm", "achieved": round(B / t / 1e9, 1), "peak": HBM_PEAK / 1e9,
                "unit": "GB/s", "frac": round(B / t / HBM_PEAK, 4)}
-    out.update({"traffic": measured_traffic(dom), "flops_per_launch": F, "bytes_per_launch": B,
+    out.update({"traffic": measured_traffic(dom) if pmc else None, "flops_per_launch": F, "bytes_per_launch": B,
                 "avg_launch_ms": known[dom], "mfma_frac": round(F / t / MFMA_BF16_PEAK, 4),
                 "hbm_frac": round(B / t / HBM_PEAK, 4)})
+    pk = _profile("peaks.json")
+    if pk:
+        m = pk["measured"]
+        ach = m["mfma_loop_tflops"] * 1e12 if out["bound"] == "mfma" else m["read_gbps"] * 1e9
+        out.update({"achievable_peak": round(ach / (1e12 if out["bound"] == "mfma" else 1e9), 1),
+                    "frac_of_achievable": round((F if out["bound"] == "mfma" else B) / t / ach, 4)})
+    busy = (_profile("mfma.json") or {}).get("kernels", {}).get(dom) if pmc else None
+    if busy:
+        out["mfma_busy_pmc"] = busy["mfma_busy"]
     return out
+
+
+def _profile(name):
+    """A committed measurement summary from profiles/ (JSON), or None."""
+    try:
+        return json.load(open(os.path.join(ROOT, "profiles", name)))
+    except (OSError, ValueError):
+        return None
 
 
 def measured_traffic(kernel_tag):
     """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary (profiles/traffic.json: FETCH_SIZE
     and WRITE_SIZE per dispatch, scaled by the same counters on a copy of known size), or None if not measured."""
-    try:
-        d = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))
-    except (OSError, ValueError):
+    d = _profile("traffic.json")
+    if d is None:
         return None
     k = d.get("kernels", {}).get(kernel_tag)
     return None if k is None else k.get("hbm_bytes_per_launch")
@@ -302,12 +323,20 @@ def time_step(step, steps, warmup, graph):
 
 
 def breakdown_of(step, n):
-    """Per-launch milliseconds of every entry point (events on the launching stream) over n extra steps."""
+    """Per-launch milliseconds of every entry point over n extra eager steps, by HIP events on the launching stream.
+    The side-stream forks of the step run on the main stream for this (launch order kept), so each event pair
+    brackets one launch with nothing beside it: the launch's own duration, as a kernel trace shows it. (With the
+    forks on, a launch's start event also counts the wait for compute units that the forked kernels hold.)"""
     from smel import _lib
-    with _lib.timing() as tm:
-        for _ in range(n):
-            step()
-    torch.cuda.synchronize()
+    from smel import moe
+    forks, moe._SIDE_ON = moe._SIDE_ON, frozenset()
+    try:
+        with _lib.timing() as tm:
+            for _ in range(n):
+                step()
+        torch.cuda.synchronize()
+    finally:
+        moe._SIDE_ON = forks
     res = tm.results()
     return {k: round(statistics.mean(v), 4) for k, v in sorted(res.items(), key=lambda kv: -sum(kv[1]))}
 
@@ -395,7 +424,7 @@ def run_qwen(args, dev, mode):
     c = dict(cfg, fused_shared=True, n_sel_used=0 if fwd_only else cfg["n_sel"])
     if fwd_only:
         c["r"] = 0
-    roof = roofline(bd, c, S)
+    roof = roofline(bd, c, S, pmc=mode == "c3")
     cpu = None
     if mode in ("c3", "c2") and not args.no_cpu_baseline:
         log("timing the CPU baseline (the oracle: 1 warmup + median of 5 full passes) ...")
@@ -500,6 +529,61 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     log(f"copy calibration: 5 copies of {COPY_BYTES} bytes")
+
+
+def run_peaks(args, dev):
+    """The achievable peaks of this GPU, by kernels that do nothing else (include/smel_probe.h): the MFMA-only loop
+    (v_mfma_f32_32x32x16_bf16, eight independent accumulators per wave, 2 workgroups of 4 waves per CU), a streaming
+    read and a device copy of 2 GiB (16 bytes per lane, grid-stride, over a sweep of grid sizes: the best is kept),
+    and the platform library's bf16 GEMM (torch.mm on hipBLASLt, 8192^3) for comparison. HIP events on the launching
+    stream, best of 5 launches after one warmup."""
+    from smel import _lib as L
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def best_ms(fn, reps=5):
+        fn()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        return min(ts)
+
+    blocks, iters = 2 * cus, 4000
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    ms = best_ms(lambda: L.call("smel_probe_mfma", L.ptr(out), blocks, iters, L.stream()))
+    mfma = blocks * 4 * iters * 8 * 32768 / (ms * 1e-3)
+    log(f"MFMA loop: {mfma / 1e12:.1f} TFLOP/s")
+    nbytes = 2 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    reads, copies = {}, {}
+    for grid in (1024, 2048, 4096, 8192):
+        sink = torch.empty(grid * 256, dtype=torch.int32, device=dev)
+        reads[grid] = nbytes / (best_ms(lambda: L.call("smel_probe_read", L.ptr(src), nbytes, L.ptr(sink), grid,
+                                                       L.stream())) * 1e-3)
+        copies[grid] = 2 * nbytes / (best_ms(lambda: L.call("smel_probe_copy", L.ptr(src), L.ptr(dst), nbytes, grid,
+                                                            L.stream())) * 1e-3)
+    del src, dst
+    n = 8192
+    a = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    b = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+    gemm = 2 * n ** 3 / (best_ms(lambda: torch.mm(a, b, out=c)) * 1e-3)
+    rg, cg = max(reads, key=reads.get), max(copies, key=copies.get)
+    res = {"mfma_loop_tflops": round(mfma / 1e12, 1), "hipblaslt_bf16_gemm_8192_tflops": round(gemm / 1e12, 1),
+           "read_gbps": round(reads[rg] / 1e9), "read_grid": rg, "copy_gbps": round(copies[cg] / 1e9), "copy_grid": cg,
+           "read_gbps_by_grid": {k: round(v / 1e9) for k, v in reads.items()},
+           "copy_gbps_by_grid": {k: round(v / 1e9) for k, v in copies.items()}, "compute_units": cus}
+    print(json.dumps({"metric": "achievable peaks of this GPU (MFMA-only loop, streaming read, device copy)",
+                      "value": res["mfma_loop_tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": 5, "warmup": 1,
+                      "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                      "dtype": "bf16", "data": "synthetic", "config": {"workload": "peaks", "copy_bytes": nbytes},
+                      "published": {"mfma_bf16_tflops": MFMA_BF16_PEAK / 1e12, "hbm_gbps": HBM_PEAK / 1e9},
+                      "measured": res}), flush=True)
 
 
 def _cpu_model():
@@ -806,7 +890,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream", "quant", "ce"), default="c3")
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream", "quant", "ce", "peaks"),
+                    default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -833,6 +918,8 @@ def main():
         run_quant(args, dev)
     elif args.workload == "ce":
         run_ce(args, dev)
+    elif args.workload == "peaks":
+        run_peaks(args, dev)
     else:
         run_qwen(args, dev, args.workload)
 

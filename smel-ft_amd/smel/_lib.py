@@ -17,7 +17,7 @@ LIB_PATH = os.environ.get("SMEL_MOE_LIB") or os.path.join(HERE, "libsmel_moe.so"
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -97,6 +97,10 @@ SIGNATURES = {
     # include/smel_loss.h
     "smel_ce_chunk_update": (i32, [vp, i64, i64, i64, i64, vp, f32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp]),
     "smel_ce_acc_update": (i32, [vp, vp, vp, i32, i64, i64, i32, vp]),
+    # include/smel_probe.h
+    "smel_probe_mfma": (i32, [vp, i32, i32, vp]),
+    "smel_probe_read": (i32, [vp, i64, vp, i32, vp]),
+    "smel_probe_copy": (i32, [vp, vp, i64, i32, vp]),
 }
 
 _lib = None
