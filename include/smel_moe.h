@@ -42,16 +42,23 @@ typedef struct smel_wset {
   const uint16_t* wb;  /* bf16 bank [E][R][C] (BF16Experts.gate_up / .down), smel_pack_bf16(_t)        */
   const uint16_t* wsel;/* selected experts [n_sel][R][C] (LayerExperts.sel_gate_up / sel_down), packed  */
   const uint16_t* wsh; /* shared expert [R][C], packed                                                 */
-  /* LoRA as a 32-wide K-extension of the GEMM (0-padded rank <= 16, built by smel_lora_prep):
-   *   forward  ext_*: [n][R][32]  (B factor per output row; gate_up: B_gate in cols 0..15, B_up in 16..31)
-   *   backward ext_*: [n][C][32]  (A factor per output column; gate_up: A_gate in 0..15, A_up in 16..31) */
+  /* LoRA as a K-extension of the GEMM (0-padded, built by smel_lora_prep), in 32-wide planes:
+   *   forward  ext_*: [n][R][32]          (B factor per output row; gate_up with one plane: B_gate in cols 0..15,
+   *                                        B_up in 16..31; with two planes: each in cols 0..r-1 of its own rows)
+   *   backward ext_*: [n][planes][C][32]  (A factor per output column; gate_up with one plane: A_gate in 0..15, A_up
+   *                                        in 16..31; with two planes: A_gate in plane 0, A_up in plane 1)
+   * The ext rows passed to the GEMMs are [rows][32 * planes]. Two planes (SMEL_WSET_EXT2, gate_up LoRA of rank
+   * 17..32): the forward's gate columns take plane 0 of the ext rows and its up columns plane 1; the backward adds
+   * both planes' products. */
   const uint16_t* ext_sel;
   const uint16_t* ext_sh;
   int64_t R, C;
   int32_t group;       /* int4 group along C (a multiple of 32)                                        */
-  int32_t flags;       /* SMEL_WSET_FAST_DQ: every scale/zero group of q4 passed smel_int4_fast_ok       */
+  int32_t flags;       /* SMEL_WSET_FAST_DQ: every scale/zero group of q4 passed smel_int4_fast_ok;
+                        * SMEL_WSET_EXT2: the LoRA K-extension has two planes (see above)                */
 } smel_wset;
 #define SMEL_WSET_FAST_DQ 1
+#define SMEL_WSET_EXT2 2
 
 const char* smel_last_error(void);
 int smel_abi_version(void);
@@ -177,29 +184,35 @@ int64_t smel_dispatch_noalloc_max_ws(void);
 int64_t smel_dispatch_max_tiles(int64_t TK, int64_t E, int64_t shared_rows, int32_t m_tile);
 
 /* ---- LoRA factor layouts (smel/lora.py:14-58 params, fp32) -> the bf16 K-extension operands.
- * For n groups (n_sel selected slots, or 1 for the shared MLP) with rank r <= 16, hidden Hd, inter In, scale s:
- *   fwd_gu  [n][2In][32]: B_gate in cols 0..r-1 of rows 0..In-1, B_up in cols 16..16+r-1 of rows In..2In-1
+ * For n groups (n_sel selected slots, or 1 for the shared MLP) with rank r, hidden Hd, inter In, and `planes` 32-wide
+ * planes for the gate_up side (1: r <= 16, gate and up packed in one plane; 2: r <= 32, gate in plane 0 and up in
+ * plane 1; the down side always has one plane, r <= 32):
+ *   planes = 1                                              planes = 2
+ *   fwd_gu  [n][2In][32]: B_gate cols 0..r-1 of rows < In,   B_gate / B_up in cols 0..r-1 of their rows
+ *                         B_up cols 16..16+r-1 of rows >= In
+ *   a_gu    [n][32][Hd] : A_gate rows 0..r-1, A_up 16..       [2][n][32][Hd]: A_gate in plane 0, A_up in plane 1
+ *   bt_gu   [n][32][2In]: B_gate^T rows 0.. / cols < In,     [2][n][32][2In]: plane 0 B_gate^T (cols < In), plane 1
+ *                         B_up^T rows 16.. / cols >= In                        B_up^T (cols >= In)
+ *   at_gu   [n][Hd][32] : a_gu transposed                    [n][2][Hd][32]: A_gate^T in plane 0, A_up^T in plane 1
  *   fwd_dn  [n][Hd][32] : B_down in cols 0..r-1
- *   a_gu    [n][32][Hd] : A_gate rows 0..r-1, A_up rows 16..16+r-1   (XA = x a_gu^T)
  *   a_dn    [n][32][In] : A_down rows 0..r-1                        (AD = act a_dn^T)
  *   bt_dn   [n][32][Hd] : B_down^T rows 0..r-1                       (DB = dy bt_dn^T)
- *   bt_gu   [n][32][2In]: B_gate^T in rows 0..r-1 / cols 0..In-1, B_up^T in rows 16.. / cols In..2In-1
- *   at_gu   [n][Hd][32] : a_gu transposed (backward ext of gate_up)
  *   at_dn   [n][In][32] : a_dn transposed (backward ext of down)
- * Every other entry is 0. */
+ * Every other entry is 0. The LoRA of smel/lora.py takes any rank; ranks above 32 are rejected here. */
 int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, const float* B_up,
-                   const float* A_down, const float* B_down, int64_t n, int64_t r, int64_t Hd, int64_t In,
-                   uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
+                   const float* A_down, const float* B_down, int64_t n, int64_t r, int32_t planes, int64_t Hd,
+                   int64_t In, uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
                    uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn, hipStream_t stream);
 
 /* ---- (A11/A12) LoRA down-projections of the rows of LoRA groups (SEL / SHARED tiles of the tile list):
- * ext[row][0:32] = bf16(scale_g * A_src[src(row)][0:Kd] . wcat_g[0:32][0:Kd]) where src(row) = token of the row if
- * a_gather else row (A holds a_rows rows), wcat_g = wcat_sel + idx*32*Kd, scale_g = scale_sel (SEL) or wcat_sh,
- * scale_sh (SHARED). Rows of other groups are left untouched. Kd must be a multiple of 32. */
+ * ext[row * ldx + 0:32] = bf16(scale_g * A_src[src(row)][0:Kd] . wcat_g[0:32][0:Kd]) where src(row) = token of the row
+ * if a_gather else row (A holds a_rows rows), wcat_g = wcat_sel + idx*32*Kd, scale_g = scale_sel (SEL) or wcat_sh,
+ * scale_sh (SHARED). One call fills one 32-wide plane: ldx = 32 * planes, ext offset by 32 per plane. Rows of other
+ * groups are left untouched. Kd must be a multiple of 32. */
 int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,
                   const uint16_t* A_src, int64_t lda, int64_t a_rows, int32_t a_gather, const int32_t* order,
                   int64_t TK, int64_t topk, const uint16_t* wcat_sel, const uint16_t* wcat_sh, int64_t Kd,
-                  float scale_sel, float scale_sh, uint16_t* ext, hipStream_t stream);
+                  float scale_sel, float scale_sh, uint16_t* ext, int64_t ldx, hipStream_t stream);
 
 /* ---- (A5/A6/A11) grouped expert GEMM, forward: out = A W^T per group, W from w (int4 dequantized in registers,
  * or bf16), plus the LoRA K-extension ext[row] . w.ext_*[n] for SEL/SHARED groups when ext != NULL.
@@ -261,10 +274,10 @@ int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, f
 int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, const int32_t* inv, int32_t with_shared,
                    const uint16_t* dxsh, int64_t T, int64_t K, int64_t H, uint16_t* dx, hipStream_t stream);
 
-/* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP), up to four
- * products in one launch. For job j and every LoRA group lora_groups[i] (expert id, or E for the shared rows
- * [TK, TK+T)):
- *   R[p][q] = sum_{rows of the group} alpha(row) * L[row][p] * Rm[src(row)][q],  p < 32, q < Q
+/* ---- LoRA weight gradients (autograd of smel/lora.py:61-83 for the selected experts and the shared MLP), up to six
+ * products in one launch (four; six when the gate_up side has two planes, one job per plane). For job j and every
+ * LoRA group lora_groups[i] (expert id, or E for the shared rows [TK, TK+T)):
+ *   R[p][q] = sum_{rows of the group} alpha(row) * L[row * ldl + p] * Rm[src(row)][q],  p < 32, q < Q
  * summed in one fixed order (deterministic). src(row) = token of the row if r_gather else row; Rm holds r_rows rows;
  * alpha = the row weight (topv[p] fp32 / sgate[t]) if use_w, else 1 (folded into L before its bf16 rounding).
  * Each R[p][q] with p in [p0, p0+np) and q in [q0, q0+nq) of a destination is stored (fp32) at
@@ -278,11 +291,12 @@ typedef struct smel_wg_dest {
   int32_t p0, np, q0, nq;
 } smel_wg_dest;
 typedef struct smel_wg_job {
-  const uint16_t* L;   /* [rows][32] bf16: the LoRA K-extension rows of the direction */
-  const uint16_t* Rm;  /* right operand rows, ldr elements apart                     */
+  const uint16_t* L;   /* bf16 LoRA K-extension rows of the direction, ldl elements apart (32 p's used)   */
+  const uint16_t* Rm;  /* right operand rows, ldr elements apart                                          */
   int64_t ldr, r_rows;
   int32_t r_gather, use_w;
   int64_t Q;
+  int64_t ldl;         /* 32 or 64 (a plane of two-plane ext rows; L then points at the plane's column 0) */
   smel_wg_dest dest[2][2];
 } smel_wg_job;
 /* Groups of more than 512 rows are cut into 512-row chunks whose fp32 partial tiles go to the caller's workspace ws

@@ -558,11 +558,12 @@ def gemma4_block_forward_backward(h, a, W: dict, layer: OracleLayer, top_k, eps,
 
 def make_layer(T, H, E, I, K, n_sel=0, r=16, alpha=32.0, shared_inter=None, group=64, down_group=None,
                int4=True, seed=0, sel_ids=None, act_name="silu", lora_b_std=0.02, dtype=torch.bfloat16,
-               router_std=0.02):
+               router_std=0.02, r_shared=None):
     """Synthetic MoE layer of the given shape (the benchmark configs): weights ~N(0, 0.02) in ``dtype``, router
     ~N(0, router_std), frozen experts quantized with :func:`quantize_int4`, selected ids spread as the reference's
     layer benchmark picks them (scripts/bench/bench_layer.py:70) unless given, LoRA A ~ U(+-1/sqrt(in)) and
-    B ~ N(0, lora_b_std). Returns (x [T,H], OracleLayer)."""
+    B ~ N(0, lora_b_std), rank r (the shared MLP's r_shared when given; scale alpha / rank). Returns
+    (x [T,H], OracleLayer)."""
     g = torch.Generator().manual_seed(seed)
 
     def rnd(*s, std=0.02):
@@ -582,7 +583,7 @@ def make_layer(T, H, E, I, K, n_sel=0, r=16, alpha=32.0, shared_inter=None, grou
     layer = OracleLayer(gate_w=gate_w, frozen=frozen, int4=int4, sel_ids=sel_ids, act=act_name,
                         deq_dtype=torch.bfloat16)
 
-    def lora_set(k, inter, lead):
+    def lora_set(k, inter, lead, r=r):
         shp = (lambda *s: (k, *s)) if lead else (lambda *s: s)
         out = {}
         for n, s, fan in (("A_gate", shp(r, H), H), ("A_up", shp(r, H), H), ("A_down", shp(r, inter), inter)):
@@ -598,8 +599,9 @@ def make_layer(T, H, E, I, K, n_sel=0, r=16, alpha=32.0, shared_inter=None, grou
     if shared_inter:
         layer.shared = {"gate_up": rnd(2 * shared_inter, H), "down": rnd(H, shared_inter),
                         "gate_w": rnd(1, H)}
-        layer.sh_lora = lora_set(0, shared_inter, False) if r else None
-        layer.sh_scale = alpha / r if r else 0.0
+        rs = r if r_shared is None else r_shared
+        layer.sh_lora = lora_set(0, shared_inter, False, rs) if rs else None
+        layer.sh_scale = alpha / rs if rs else 0.0
     return x, layer
 
 

@@ -358,24 +358,29 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     }
   }
   wait_vm<0>();   // the ring's trailing (out-of-range) loads
-  // ---- LoRA K-extension: ext[row][0:32] . Eb[n][0:32] (one 32-wide substep)
-  const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * N * 32 : nullptr)
+  // ---- LoRA K-extension: ext[row][32 c : 32 c + 32] . Eb[c][n][0:32], one 32-wide substep per plane c (two planes
+  // for a gate_up LoRA of rank 17..32: the gate and the up products add up)
+  const int planes = (ws.flags & SMEL_WSET_EXT2) ? 2 : 1;   // uniform
+  const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * planes * N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
   if (a.ext && eb) {
-    const rsrc_t re = make_rsrc(eb, (uint64_t)N * 64);
-    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
-    u32x4_t b[4];
+    const uint32_t xb = 64u * planes;   // ext row bytes
+    const rsrc_t re = make_rsrc(eb, (uint64_t)planes * N * 64);
+    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * (xb / 2), (uint64_t)nrows * xb);
+    for (int c = 0; c < planes; ++c) {
+      u32x4_t b[4];
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int n = cw + 16 * f + li;
-      b[f] = ld16(re, (cw + 16 * f < N) ? (uint32_t)n * 64 + 16 * kq : OOB);
-    }
+      for (int f = 0; f < 4; ++f) {
+        const int n = cw + 16 * f + li;
+        b[f] = ld16(re, (cw + 16 * f < N) ? (uint32_t)(c * N + n) * 64 + 16 * kq : OOB);
+      }
 #pragma unroll
-    for (int m = 0; m < NRF; ++m) {
-      const int row = m * 16 + li;
-      const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 16 * kq : OOB);
+      for (int m = 0; m < NRF; ++m) {
+        const int row = m * 16 + li;
+        const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * xb + 64 * c + 16 * kq : OOB);
 #pragma unroll
-      for (int f = 0; f < 4; ++f) acc[m][f] = mfma16(af, b[f], acc[m][f]);
+        for (int f = 0; f < 4; ++f) acc[m][f] = mfma16(af, b[f], acc[m][f]);
+      }
     }
   }
   // ---- epilogue through LDS (the ring is free after the loop): every lane writes its results, rounded to bf16, into a
@@ -551,6 +556,8 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && actsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
                "gmm_bwd: epilogue %d needs hsave, actsave, dwp and topv", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_bwd: gather needs order");
+  SMEL_REQUIRE(!(w->flags & SMEL_WSET_EXT2) || epilogue == 0, SMEL_EINVAL,
+               "gmm_bwd: a two-plane LoRA extension belongs to the gate_up backward (epilogue 0)");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_bwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: A larger than 2 GiB");
   SMEL_REQUIRE(w->R * w->C * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: one weight matrix larger than 2 GiB");

@@ -259,12 +259,15 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     }
   }
   wait_vm<0>();   // the ring's trailing (out-of-range) loads
-  // ---- LoRA K-extension: ext[row][0:32] . Bext[n][0:32]
+  // ---- LoRA K-extension: ext[row][0:32] . Bext[n][0:32]. Two planes (gate_up LoRA of rank 17..32): ext rows are
+  // 64 wide, the gate fragment (0) takes plane 0 and the up fragment (1) plane 1.
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
   if (a.ext && eb) {
+    const bool two = (ws.flags & SMEL_WSET_EXT2) != 0;   // uniform
+    const uint32_t xb = two ? 128u : 64u;                 // ext row bytes
     const rsrc_t re = make_rsrc(eb, (uint64_t)a.N * 64);
-    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * 32, (uint64_t)nrows * 64);
+    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * (xb / 2), (uint64_t)nrows * xb);
     u32x4_t b0[2], b1[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -276,9 +279,11 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       const int row = m * 32 + r32;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * 64 + 32 * hi + 16 * s : OOB);
+        const uint32_t o = row < nrows ? (uint32_t)row * xb + 32 * hi + 16 * s : OOB;
+        const u32x4_t af = ld16(rx, o);
+        const u32x4_t af1 = two ? ld16(rx, o == OOB ? OOB : o + 64) : af;
         acc[m][0] = mfma32(af, b0[s], acc[m][0]);
-        acc[m][1] = mfma32(af, b1[s], acc[m][1]);
+        acc[m][1] = mfma32(af1, b1[s], acc[m][1]);
       }
     }
   }
@@ -409,6 +414,8 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0, SMEL_EUNSUPPORTED,
                "gmm_fwd: out / hsave rows must be 16-B aligned");
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
+  SMEL_REQUIRE(!(w->flags & SMEL_WSET_EXT2) || epilogue == 1, SMEL_EINVAL,
+               "gmm_fwd: a two-plane LoRA extension belongs to the gate_up projection (epilogue 1)");
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_fwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_fwd: A larger than 2 GiB");

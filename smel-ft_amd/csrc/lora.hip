@@ -9,34 +9,45 @@ namespace {
 __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ Ag, const float* __restrict__ Bg,
                                                         const float* __restrict__ Au, const float* __restrict__ Bu,
                                                         const float* __restrict__ Ad, const float* __restrict__ Bd,
-                                                        int n, int r, int Hd, int In, uint16_t* __restrict__ fwd_gu,
-                                                        uint16_t* __restrict__ fwd_dn, uint16_t* __restrict__ a_gu,
-                                                        uint16_t* __restrict__ a_dn, uint16_t* __restrict__ bt_dn,
-                                                        uint16_t* __restrict__ bt_gu, uint16_t* __restrict__ at_gu,
-                                                        uint16_t* __restrict__ at_dn) {
+                                                        int n, int r, int planes, int Hd, int In,
+                                                        uint16_t* __restrict__ fwd_gu, uint16_t* __restrict__ fwd_dn,
+                                                        uint16_t* __restrict__ a_gu, uint16_t* __restrict__ a_dn,
+                                                        uint16_t* __restrict__ bt_dn, uint16_t* __restrict__ bt_gu,
+                                                        uint16_t* __restrict__ at_gu, uint16_t* __restrict__ at_dn) {
   // 32-bit index arithmetic (every layout has fewer than 2^31 elements: checked by the host) and two adjacent
   // outputs per thread (every innermost dimension is even), stored as one 32-bit word
   const int which = blockIdx.y;
-  const uint32_t I2 = 2u * In, H = Hd, Iu = In, R = r;
+  const uint32_t I2 = 2u * In, H = Hd, Iu = In, R = r, P = planes, N = n;
+  // gate_up side: with one plane, gate ranks sit at 0..r-1 and up ranks at 16..16+r-1 of it; with two planes, each
+  // projection has its own plane and its ranks at 0..r-1. (plane, j) -> rank of gate / up, or -1.
+  auto gate_rank = [&](uint32_t plane, uint32_t j) -> int { return (plane == 0u && j < R) ? (int)j : -1; };
+  auto up_rank = [&](uint32_t plane, uint32_t j) -> int {
+    if (P == 1u) return (j >= 16u && j < 16u + R) ? (int)(j - 16u) : -1;
+    return (plane == 1u && j < R) ? (int)j : -1;
+  };
   uint32_t total;
   uint16_t* out;
   switch (which) {
-    case 0: total = n * I2 * 32u; out = fwd_gu; break;
-    case 1: total = n * H * 32u; out = fwd_dn; break;
-    case 2: total = n * 32u * H; out = a_gu; break;
-    case 3: total = n * 32u * Iu; out = a_dn; break;
-    case 4: total = n * 32u * H; out = bt_dn; break;
-    case 5: total = n * 32u * I2; out = bt_gu; break;
-    case 6: total = n * H * 32u; out = at_gu; break;
-    default: total = n * Iu * 32u; out = at_dn; break;
+    case 0: total = N * I2 * 32u; out = fwd_gu; break;
+    case 1: total = N * H * 32u; out = fwd_dn; break;
+    case 2: total = P * N * 32u * H; out = a_gu; break;
+    case 3: total = N * 32u * Iu; out = a_dn; break;
+    case 4: total = N * 32u * H; out = bt_dn; break;
+    case 5: total = P * N * 32u * I2; out = bt_gu; break;
+    case 6: total = N * P * H * 32u; out = at_gu; break;
+    default: total = N * Iu * 32u; out = at_dn; break;
   }
   auto val = [&](uint32_t i) -> float {
     float v = 0.f;
     switch (which) {
-      case 0: {   // fwd_gu [n][2In][32]
+      case 0: {   // fwd_gu [n][2In][32]: row < In gate (plane 0), row >= In up (its own plane's ranks)
         const uint32_t c = i & 31u, rowg = i >> 5, row = rowg % I2, g = rowg / I2;
-        if (row < Iu && c < R) v = Bg[(g * Iu + row) * R + c];
-        if (row >= Iu && c >= 16u && c < 16u + R) v = Bu[(g * Iu + row - Iu) * R + c - 16u];
+        if (row < Iu) {
+          if (c < R) v = Bg[(g * Iu + row) * R + c];
+        } else {
+          const int k = up_rank(P - 1u, c);
+          if (k >= 0) v = Bu[(g * Iu + row - Iu) * R + k];
+        }
         break;
       }
       case 1: {   // fwd_dn [n][Hd][32]
@@ -44,10 +55,11 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
         if (c < R) v = Bd[(i >> 5) * R + c];
         break;
       }
-      case 2: {   // a_gu [n][32][Hd]
-        const uint32_t h = i % H, jg = i / H, j = jg & 31u, g = jg >> 5;
-        if (j < R) v = Ag[(g * R + j) * H + h];
-        if (j >= 16u && j < 16u + R) v = Au[(g * R + j - 16u) * H + h];
+      case 2: {   // a_gu [planes][n][32][Hd]
+        const uint32_t h = i % H, jg = i / H, j = jg & 31u, pg = jg >> 5, plane = pg / N, g = pg - plane * N;
+        const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
+        if (kg >= 0) v = Ag[(g * R + kg) * H + h];
+        if (ku >= 0) v = Au[(g * R + ku) * H + h];
         break;
       }
       case 3: {   // a_dn [n][32][In]
@@ -60,16 +72,18 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
         if (j < R) v = Bd[(g * H + h) * R + j];
         break;
       }
-      case 5: {   // bt_gu [n][32][2In]
-        const uint32_t c = i % I2, jg = i / I2, j = jg & 31u, g = jg >> 5;
-        if (j < R && c < Iu) v = Bg[(g * Iu + c) * R + j];
-        if (j >= 16u && j < 16u + R && c >= Iu) v = Bu[(g * Iu + c - Iu) * R + j - 16u];
+      case 5: {   // bt_gu [planes][n][32][2In]: gate ranks on columns < In, up ranks on columns >= In
+        const uint32_t c = i % I2, jg = i / I2, j = jg & 31u, pg = jg >> 5, plane = pg / N, g = pg - plane * N;
+        const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
+        if (kg >= 0 && c < Iu) v = Bg[(g * Iu + c) * R + kg];
+        if (ku >= 0 && c >= Iu) v = Bu[(g * Iu + c - Iu) * R + ku];
         break;
       }
-      case 6: {   // at_gu [n][Hd][32]: a_gu transposed (the backward GEMM's K-extension)
-        const uint32_t j = i & 31u, hg = i >> 5, h = hg % H, g = hg / H;
-        if (j < R) v = Ag[(g * R + j) * H + h];
-        if (j >= 16u && j < 16u + R) v = Au[(g * R + j - 16u) * H + h];
+      case 6: {   // at_gu [n][planes][Hd][32]: a_gu transposed (the backward GEMM's K-extension)
+        const uint32_t j = i & 31u, hg = i >> 5, h = hg % H, pg = hg / H, plane = pg % P, g = pg / P;
+        const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
+        if (kg >= 0) v = Ag[(g * R + kg) * H + h];
+        if (ku >= 0) v = Au[(g * R + ku) * H + h];
         break;
       }
       default: {  // at_dn [n][In][32]: a_dn transposed
@@ -85,12 +99,12 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
     o32[p] = pack2bf(val(2u * p), val(2u * p + 1u));
 }
 
-// ext[row][0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles. Persistent: one block
-// per CU first builds, in LDS, the list of this call's tiles that carry a LoRA (the tile list holds each tile's kind;
-// all tile entries are loaded at once, one memory latency), then takes the (LoRA tile, 32-row slice) items
-// blockIdx.x, blockIdx.x + gridDim.x, ... A slice's 8 waves take the 64-wide k-steps j = w, w + 8, ..., issuing all
-// loads of up to XPRE of their steps before the MFMAs (one memory latency per XPRE steps, not one per step); the
-// partial sums are added in wave order through LDS.
+// ext[row * ldx + 0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles (one 32-wide
+// plane per call). Persistent: one block per CU first builds, in LDS, the list of this call's tiles that carry a LoRA
+// (the tile list holds each tile's kind; all tile entries are loaded at once, one memory latency), then takes the
+// (LoRA tile, 32-row slice) items blockIdx.x, blockIdx.x + gridDim.x, ... A slice's 8 waves take the 64-wide k-steps
+// j = w, w + 8, ..., issuing all loads of up to XPRE of their steps before the MFMAs (one memory latency per XPRE
+// steps, not one per step); the partial sums are added in wave order through LDS.
 constexpr int XW = 8;
 constexpr int XPRE = 4;
 constexpr int XT_PER = 8;              // tile entries each thread scans
@@ -102,7 +116,7 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
                                                        const int32_t* __restrict__ order, int TK, int topk,
                                                        const uint16_t* __restrict__ wsel, const uint16_t* __restrict__ wsh,
                                                        int Kd, float ssel, float ssh, uint16_t* __restrict__ ext,
-                                                       int max_tiles) {
+                                                       int ldx, int max_tiles) {
   __shared__ float red[XW * 64 * 16];
   __shared__ int lt[XLT];
   __shared__ int wcnt[XT_PER][XW];
@@ -187,21 +201,21 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
 #pragma unroll
         for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
         const int orow = m * 32 + acc_row(r, l);
-        if (orow < nrows) ext[(int64_t)(t.y + orow) * 32 + r32] = f2bf(scale * v);
+        if (orow < nrows) ext[(int64_t)(t.y + orow) * ldx + r32] = f2bf(scale * v);
       }
     }
     __syncthreads();   // red is reused by the next item
   }
 }
 
-// LoRA factor gradients, all four products of a backward in one launch. Item = (128-column block of a job, 512-row
-// chunk slot of a LoRA group); persistent blocks (at most two per CU) take the items that are in use, counted on the
-// device from the group offsets. out[p][q] = sum over ALL rows of group i of alpha(row) L[row][p] Rm[src(row)][q],
-// p < 32, as an MFMA GEMM
-// with the row index as the contraction dim: per 64-row step, L and Rm are staged transposed in LDS (k-pair packing:
-// the values of rows 2j and 2j+1 share one 32-bit word), then each wave multiplies the 32 x 64 L^T tile by its 64 x 32
-// slice of the Rm tile. The LDS tiles are double-buffered and the raw rows of step j+1 are loaded into registers
-// before step j's MFMAs, so one barrier per step suffices. Rows are summed in one fixed order (deterministic), and
+// LoRA factor gradients, all products of a backward (four, or six with two-plane gate_up operands) in one launch.
+// Item = (128-column block of a job, 512-row chunk slot of a LoRA group); persistent blocks (at most two per CU) take
+// the items that are in use, counted on the device from the group offsets. out[p][q] = sum over ALL rows of group i
+// of alpha(row) L[row * ldl + p] Rm[src(row)][q], p < 32, as an MFMA GEMM with the row index as the contraction dim:
+// per 64-row step, L and Rm are staged transposed in LDS (k-pair packing: the values of rows 2j and 2j+1 share one
+// 32-bit word), then each wave multiplies the 32 x 64 L^T tile by its 64 x 32 slice of the Rm tile. The LDS tiles
+// are double-buffered and the raw rows of step j+1 are loaded into registers before step j's MFMAs, so one barrier
+// per step suffices. Rows are summed in one fixed order (deterministic), and
 // each (p, q) goes straight to the gradient tensor the job's destination descriptor names.
 constexpr int WG_QB = 128;    // columns per block
 constexpr int WG_S = 64 + 8;  // LDS row stride (bf16)
@@ -209,10 +223,11 @@ constexpr int WG_PF = 4;      // 64-row steps in flight
 constexpr int WG_CH = 512;    // rows per chunk block
 constexpr int WG_MAXG = 256;  // LoRA groups per call
 constexpr int WG_WIN = WG_CH; // rows per index window
+constexpr int WG_MAXJ = 6;    // jobs per launch (four, or six with two-plane gate_up operands)
 
 struct WgArgs {
-  smel_wg_job job[4];
-  int qb0[4];                  // first 128-column block of each job in the partial-tile space
+  smel_wg_job job[WG_MAXJ];
+  int qb0[WG_MAXJ];            // first 128-column block of each job in the partial-tile space
   int nqb;                     // 128-column blocks of all jobs
   int tot;                     // partial-tile slots per column block
   float* ws;                   // partial tiles [sum of column blocks][tot][32 * 128]
@@ -283,7 +298,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     const int qbg = it / used, sl = it - qbg * used;
     int jb = 0;
 #pragma unroll
-    for (int j = 1; j < 4; ++j)
+    for (int j = 1; j < WG_MAXJ; ++j)
       if (qbg >= a.qb0[j]) jb = j;
     const smel_wg_job& J = a.job[jb];
     const int qb = qbg - a.qb0[jb];
@@ -334,7 +349,8 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
         TAL[row - w0] = alpha;
       }
     };
-    const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * 64);   // L rows [0, a1): a row past the group reads zeros
+    const uint32_t ldl2 = (uint32_t)J.ldl * 2;              // L row pitch in bytes
+    const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * ldl2);  // L rows [0, a1): a row past the group reads zeros
     // branch-free: rows past the window get an out-of-range offset (zeros) and weight 0
     auto load = [&](int k0, int w0, int w1, Raw& R) {
       const int ra = k0 + 2 * kp;
@@ -343,8 +359,8 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
       const uint32_t o0 = v0 ? TOFF[t0] : OOB, o1 = v1 ? TOFF[t1] : OOB;
       R.al0 = v0 ? TAL[t0] : 0.f;
       R.al1 = v1 ? TAL[t1] : 0.f;
-      const u32x2_t l0 = ld8(rl, v0 ? (uint32_t)ra * 64 + 8 * grp : OOB);
-      const u32x2_t l1 = ld8(rl, v1 ? (uint32_t)(ra + 1) * 64 + 8 * grp : OOB);
+      const u32x2_t l0 = ld8(rl, v0 ? (uint32_t)ra * ldl2 + 8 * grp : OOB);
+      const u32x2_t l1 = ld8(rl, v1 ? (uint32_t)(ra + 1) * ldl2 + 8 * grp : OOB);
       R.lv0 = make_uint2(l0.x, l0.y);
       R.lv1 = make_uint2(l1.x, l1.y);
 #pragma unroll
@@ -413,7 +429,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
   const int qbg = blockIdx.x;
   int jb = 0;
 #pragma unroll
-  for (int j = 1; j < 4; ++j)
+  for (int j = 1; j < WG_MAXJ; ++j)
     if (qbg >= a.qb0[j]) jb = j;
   const smel_wg_job& J = a.job[jb];
   const int qb = qbg - a.qb0[jb];
@@ -436,21 +452,25 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
 }  // namespace
 
 extern "C" int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, const float* B_up,
-                              const float* A_down, const float* B_down, int64_t n, int64_t r, int64_t Hd, int64_t In,
-                              uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
-                              uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn, hipStream_t stream) {
+                              const float* A_down, const float* B_down, int64_t n, int64_t r, int32_t planes,
+                              int64_t Hd, int64_t In, uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu,
+                              uint16_t* a_dn, uint16_t* bt_dn, uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn,
+                              hipStream_t stream) {
   SMEL_REQUIRE(n >= 0 && r > 0 && Hd > 0 && In > 0, SMEL_EINVAL, "lora_prep: bad sizes");
-  SMEL_REQUIRE(r <= 16, SMEL_EUNSUPPORTED, "lora_prep: rank %lld > 16", (long long)r);
+  SMEL_REQUIRE(planes == 1 || planes == 2, SMEL_EINVAL, "lora_prep: planes %d (1 or 2)", planes);
+  SMEL_REQUIRE(r <= 16 * planes, SMEL_EUNSUPPORTED, "lora_prep: rank %lld > %d (%d plane%s)", (long long)r,
+               16 * planes, planes, planes == 1 ? "; 2 planes take up to 32" : "s");
   if (n == 0) return 0;
   SMEL_REQUIRE(A_gate && B_gate && A_up && B_up && A_down && B_down && fwd_gu && fwd_dn && a_gu && a_dn && bt_dn &&
                    bt_gu && at_gu && at_dn, SMEL_EINVAL, "lora_prep: null pointer");
-  SMEL_REQUIRE(n * 32 * std::max(Hd, 2 * In) < (1ll << 31), SMEL_EUNSUPPORTED, "lora_prep: layouts too large");
+  SMEL_REQUIRE(n * planes * 32 * std::max(Hd, 2 * In) < (1ll << 31), SMEL_EUNSUPPORTED,
+               "lora_prep: layouts too large");
   SMEL_REQUIRE(((uintptr_t)fwd_gu | (uintptr_t)fwd_dn | (uintptr_t)a_gu | (uintptr_t)a_dn | (uintptr_t)bt_dn |
                 (uintptr_t)bt_gu | (uintptr_t)at_gu | (uintptr_t)at_dn) % 4 == 0, SMEL_EUNSUPPORTED,
                "lora_prep: outputs must be 4-byte aligned");
   dim3 grid(256, 8);
-  lora_prep_kernel<<<grid, 256, 0, stream>>>(A_gate, B_gate, A_up, B_up, A_down, B_down, (int)n, (int)r, (int)Hd,
-                                             (int)In, fwd_gu, fwd_dn, a_gu, a_dn, bt_dn, bt_gu, at_gu, at_dn);
+  lora_prep_kernel<<<grid, 256, 0, stream>>>(A_gate, B_gate, A_up, B_up, A_down, B_down, (int)n, (int)r, planes,
+                                             (int)Hd, (int)In, fwd_gu, fwd_dn, a_gu, a_dn, bt_dn, bt_gu, at_gu, at_dn);
   return smel::launch_status();
 }
 
@@ -458,8 +478,9 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
                              const uint16_t* A_src, int64_t lda, int64_t a_rows, int32_t a_gather,
                              const int32_t* order, int64_t TK, int64_t topk, const uint16_t* wcat_sel,
                              const uint16_t* wcat_sh, int64_t Kd, float scale_sel, float scale_sh, uint16_t* ext,
-                             hipStream_t stream) {
+                             int64_t ldx, hipStream_t stream) {
   SMEL_REQUIRE(tiles && n_tiles && A_src && ext, SMEL_EINVAL, "lora_ext: null pointer");
+  SMEL_REQUIRE(ldx == 32 || ldx == 64, SMEL_EINVAL, "lora_ext: ext row stride %lld (32 or 64)", (long long)ldx);
   SMEL_REQUIRE(Kd > 0 && Kd % 32 == 0, SMEL_EUNSUPPORTED, "lora_ext: K %lld must be a multiple of 32", (long long)Kd);
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A_src % 16) == 0, SMEL_EUNSUPPORTED, "lora_ext: A rows must be 16-B aligned");
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "lora_ext: gather needs order");
@@ -469,7 +490,8 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
   if (max_tiles == 0 || (!wcat_sel && !wcat_sh)) return 0;
   lora_ext_kernel<<<smel::cu_count(), 512, 0, stream>>>(reinterpret_cast<const int4*>(tiles), n_tiles, gkind, A_src,
                                                         lda, a_rows, a_gather, order, (int)TK, (int)topk, wcat_sel,
-                                                        wcat_sh, (int)Kd, scale_sel, scale_sh, ext, (int)max_tiles);
+                                                        wcat_sh, (int)Kd, scale_sel, scale_sh, ext, (int)ldx,
+                                                        (int)max_tiles);
   return smel::launch_status();
 }
 
@@ -484,7 +506,7 @@ int64_t wg_tot(int64_t n_lora, int64_t max_rows) { return n_lora + (max_rows + W
 
 extern "C" int64_t smel_lora_wgrad_ws_floats(const smel_wg_job* jobs, int32_t n_jobs, int64_t n_lora,
                                              int64_t max_rows) {
-  if (!jobs || n_jobs < 0 || n_jobs > 4 || n_lora < 0 || max_rows < 0) return -1;
+  if (!jobs || n_jobs < 0 || n_jobs > WG_MAXJ || n_lora < 0 || max_rows < 0) return -1;
   return wg_qblocks(jobs, n_jobs) * wg_tot(n_lora, max_rows) * 32 * WG_QB;
 }
 
@@ -492,7 +514,8 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
                                int64_t n_sel, const int32_t* offsets, int64_t E, int64_t T, int64_t TK, int64_t topk,
                                const int32_t* order, const float* topv, const float* sgate, int64_t max_rows,
                                float* ws, int64_t ws_floats, hipStream_t stream) {
-  SMEL_REQUIRE(jobs && n_jobs >= 0 && n_jobs <= 4 && n_lora >= 0 && n_sel >= 0 && n_sel <= n_lora && max_rows >= 0,
+  SMEL_REQUIRE(jobs && n_jobs >= 0 && n_jobs <= WG_MAXJ && n_lora >= 0 && n_sel >= 0 && n_sel <= n_lora &&
+                   max_rows >= 0,
                SMEL_EINVAL, "lora_wgrad: bad job / group counts");
   if (n_jobs == 0 || n_lora == 0) return 0;
   SMEL_REQUIRE(lora_groups && offsets, SMEL_EINVAL, "lora_wgrad: null pointer");
@@ -503,11 +526,13 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   a.tot = (int)wg_tot(n_lora, max_rows);
   a.ws = ws;
   int qbs = 0;
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < WG_MAXJ; ++j) {
     a.qb0[j] = qbs;
     if (j < n_jobs) {
       const smel_wg_job& J = jobs[j];
       SMEL_REQUIRE(J.L && J.Rm && J.Q > 0, SMEL_EINVAL, "lora_wgrad: job %d: null operand or Q", j);
+      SMEL_REQUIRE((J.ldl == 32 || J.ldl == 64) && ((uintptr_t)J.L % 8) == 0, SMEL_EINVAL,
+                   "lora_wgrad: job %d: L row stride %lld (32 or 64) or L not 8-B aligned", j, (long long)J.ldl);
       SMEL_REQUIRE(!(J.r_gather || J.use_w) || order || TK == 0, SMEL_EINVAL, "lora_wgrad: job %d needs order", j);
       SMEL_REQUIRE(J.ldr % 8 == 0 && J.Q % 16 == 0 && ((uintptr_t)J.Rm % 16) == 0, SMEL_EUNSUPPORTED,
                    "lora_wgrad: job %d: Rm rows must be 16-B aligned and Q a multiple of 16", j);
@@ -525,6 +550,7 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
     } else {
       a.job[j] = smel_wg_job{};
       a.job[j].Q = WG_QB;
+      a.job[j].ldl = 32;
     }
   }
   a.nqb = qbs;

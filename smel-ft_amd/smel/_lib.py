@@ -17,7 +17,8 @@ LIB_PATH = os.environ.get("SMEL_MOE_LIB") or os.path.join(HERE, "libsmel_moe.so"
 KIND_INT4, KIND_BF16, KIND_SEL, KIND_SHARED = 0, 1, 2, 3
 PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
-ABI_VERSION = 11
+WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
+ABI_VERSION = 12
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -37,7 +38,7 @@ class WgDest(ctypes.Structure):
 class WgJob(ctypes.Structure):
     """smel_wg_job of include/smel_moe.h."""
     _fields_ = [("L", vp), ("Rm", vp), ("ldr", i64), ("r_rows", i64), ("r_gather", i32), ("use_w", i32), ("Q", i64),
-                ("dest", (WgDest * 2) * 2)]
+                ("ldl", i64), ("dest", (WgDest * 2) * 2)]
 
 
 class H2DRegion(ctypes.Structure):
@@ -66,8 +67,8 @@ SIGNATURES = {
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
     "smel_dispatch_noalloc": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_noalloc_max_ws": (i64, []),
-    "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
-    "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, vp]),
+    "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, i64, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, i64, vp, vp]),
     "smel_combine": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp]),

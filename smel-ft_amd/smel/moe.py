@@ -29,7 +29,18 @@ from . import _lib as L
 from .quant import dequant_int4, quantize_int4
 
 M_TILE = 128      # rows per GEMM tile (the tile list of smel_dispatch)
-EXT = 32          # width of the LoRA K-extension (rank <= 16 for gate and up each)
+EXT = 32          # width of one plane of the LoRA K-extension
+MAX_LORA_RANK = 32
+
+
+def _lora_planes(*sets) -> int:
+    """32-wide K-extension planes of the gate_up side for the LoRA sets one launch serves: one (gate and up packed,
+    ranks 0..15 / 16..31: rank <= 16) or two (gate in plane 0, up in plane 1: rank <= 32). The down side always has
+    one plane."""
+    r = max((m.r for m in sets if m is not None), default=0)
+    if r > MAX_LORA_RANK:
+        raise L.SmelError(f"LoRA rank {r} is above the kernels' {MAX_LORA_RANK}")
+    return 2 if r > EXT // 2 else 1
 _ACT = {"silu": 0, "gelu_tanh": 1}
 _GELU_C = 0.7978845608028654
 
@@ -369,21 +380,47 @@ class _Fork:
 
 
 class _LoRABufs:
-    """bf16 K-extension layouts of one LoRA set (smel_lora_prep), built per call from the fp32 parameters."""
+    """bf16 K-extension layouts of one LoRA set (smel_lora_prep), built per call from the fp32 parameters. The
+    gate_up side has ``planes`` 32-wide planes (a_gu, bt_gu: plane-major, one [n][32][K] matrix per plane; at_gu:
+    [n][planes][H][32])."""
 
-    def __init__(self, lora, n: int, H: int, I: int, device):
+    def __init__(self, lora, n: int, H: int, I: int, device, planes: int = 1):
         self.scale = float(lora.scale)
         self.r = lora.r
+        self.planes = planes
         e = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=device)
         self.fwd_gu, self.fwd_dn = e(n, 2 * I, EXT), e(n, H, EXT)
-        self.a_gu, self.a_dn = e(n, EXT, H), e(n, EXT, I)
-        self.bt_dn, self.bt_gu = e(n, EXT, H), e(n, EXT, 2 * I)
-        self.at_gu, self.at_dn = e(n, H, EXT), e(n, I, EXT)
+        self.a_gu, self.a_dn = e(planes, n, EXT, H), e(n, EXT, I)
+        self.bt_dn, self.bt_gu = e(n, EXT, H), e(planes, n, EXT, 2 * I)
+        self.at_gu, self.at_dn = e(n, planes, H, EXT), e(n, I, EXT)
         P = [getattr(lora, k).detach().float().contiguous() for k in
              ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")]
-        L.call("smel_lora_prep", *[L.ptr(p) for p in P], n, lora.r, H, I, L.ptr(self.fwd_gu), L.ptr(self.fwd_dn),
-               L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu), L.ptr(self.at_gu),
-               L.ptr(self.at_dn), L.stream())
+        L.call("smel_lora_prep", *[L.ptr(p) for p in P], n, lora.r, planes, H, I, L.ptr(self.fwd_gu),
+               L.ptr(self.fwd_dn), L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu),
+               L.ptr(self.at_gu), L.ptr(self.at_dn), L.stream())
+
+
+_PLANE_MAJOR = ("a_gu", "bt_gu")   # layouts with a leading plane dimension (lora_ext operands)
+
+
+def _lora_ext(tl, A, lda, a_rows, gather, order, TK, K, lb_ex, lb_sh, name: str, Kd: int, planes: int, M: int, dev,
+              st):
+    """ext rows [M][32 * planes] of one direction: smel_lora_ext once per plane (``name`` = the layout the rows are
+    projected on; the down side's layouts have one plane). ``tl`` = (tiles, n_tiles, max_tiles, gkind)."""
+    tiles, ntiles, maxt, gk = tl
+    ext = torch.empty(M, EXT * planes, dtype=torch.bfloat16, device=dev)
+    s_ex = lb_ex.scale if lb_ex is not None else 0.0
+    s_sh = lb_sh.scale if lb_sh is not None else 0.0
+    for c in range(planes):
+        def w(lb):
+            if lb is None:
+                return None
+            t = getattr(lb, name)
+            return t[c] if name in _PLANE_MAJOR else t
+        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(A), lda, a_rows, gather,
+               L.ptr(order), TK, K, L.ptr(w(lb_ex)), L.ptr(w(lb_sh)), Kd, s_ex, s_sh, ext.data_ptr() + 2 * EXT * c,
+               EXT * planes, st)
+    return ext
 
 
 def _bank_wset(fz, which: str, t: bool = False) -> L.WSet:
@@ -406,13 +443,16 @@ def _bank_wset(fz, which: str, t: bool = False) -> L.WSet:
 
 
 def _wset(ex: LayerExperts, which: str, sel_w: PackedW | None, sh_w: PackedW | None, ext_sel, ext_sh,
-          t: bool = False) -> L.WSet:
-    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights; t = transposed)."""
+          t: bool = False, planes: int = 1) -> L.WSet:
+    """smel_wset for the gate_up ('gu') or down ('dn') projection of the layer (packed weights; t = transposed;
+    planes = the gate_up LoRA K-extension's planes)."""
     w = _bank_wset(ex.frozen, which, t)
     w.wsel = L.ptr(sel_w.t) if sel_w is not None else None
     w.wsh = L.ptr(sh_w.t) if sh_w is not None else None
     w.ext_sel = L.ptr(ext_sel)
     w.ext_sh = L.ptr(ext_sh)
+    if which == "gu" and planes == 2:
+        w.flags |= L.WSET_EXT2
     return w
 
 
@@ -565,11 +605,15 @@ def _expert_I(ex: LayerExperts) -> int:
 
 
 def _prep_lora(ex: LayerExperts, lora_ex, lora_sh, with_shared: bool, H: int, dev):
-    """The bf16 LoRA layouts of the selected experts and the shared MLP (lora_prep launches on the current stream)."""
+    """The bf16 LoRA layouts of the selected experts and the shared MLP (lora_prep launches on the current stream),
+    with the gate_up planes both sets need."""
     I = _expert_I(ex)
     has_sel = ex.sel_ids is not None and len(ex._slot)
-    lb_ex = _LoRABufs(lora_ex, len(ex._slot), H, I, dev) if (lora_ex is not None and has_sel) else None
-    lb_sh = _LoRABufs(lora_sh, 1, H, I, dev) if (lora_sh is not None and with_shared) else None
+    use_ex = lora_ex if (lora_ex is not None and has_sel) else None
+    use_sh = lora_sh if (lora_sh is not None and with_shared) else None
+    planes = _lora_planes(use_ex, use_sh)
+    lb_ex = _LoRABufs(use_ex, len(ex._slot), H, I, dev, planes) if use_ex is not None else None
+    lb_sh = _LoRABufs(use_sh, 1, H, I, dev, planes) if use_sh is not None else None
     return lb_ex, lb_sh
 
 
@@ -611,24 +655,20 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     fork, (lb_ex, lb_sh) = prep
     fork.join()
     any_lora = lb_ex is not None or lb_sh is not None
-    s_ex = lb_ex.scale if lb_ex else 0.0
-    s_sh = lb_sh.scale if lb_sh else 0.0
+    planes = (lb_ex or lb_sh).planes if any_lora else 1
     g = lambda b, n: getattr(b, n) if b is not None else None
     bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
+    tl = (tiles, ntiles, maxt, gk)
     ext_gu = ext_dn = None
     if any_lora:
-        ext_gu = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, T, 1, L.ptr(order), TK, K,
-               L.ptr(g(lb_ex, "a_gu")), L.ptr(g(lb_sh, "a_gu")), H, s_ex, s_sh, L.ptr(ext_gu), st)
+        ext_gu = _lora_ext(tl, x, H, T, 1, order, TK, K, lb_ex, lb_sh, "a_gu", H, planes, M, dev, st)
     actb = bf(M, I)
     hsave = bf(M, 2 * I) if need_grad else None
-    w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"))
+    w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"), planes=planes)
     L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_gu_fwd")
     if any_lora:
-        ext_dn = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(actb), I, M, 0, L.ptr(order), TK,
-               K, L.ptr(g(lb_ex, "a_dn")), L.ptr(g(lb_sh, "a_dn")), I, s_ex, s_sh, L.ptr(ext_dn), st)
+        ext_dn = _lora_ext(tl, actb, I, M, 0, order, TK, K, lb_ex, lb_sh, "a_dn", I, 1, M, dev, st)
     Y = bf(M, H)
     w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
     L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
@@ -663,18 +703,16 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     dout = _bf16(dout)
     lb_ex, lb_sh = c.lb_ex, c.lb_sh
     g = lambda b, n: getattr(b, n) if b is not None else None
-    s_ex = lb_ex.scale if lb_ex else 0.0
-    s_sh = lb_sh.scale if lb_sh else 0.0
     any_lora = lb_ex is not None or lb_sh is not None
+    planes = (lb_ex or lb_sh).planes if any_lora else 1
     bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
     sh_gu, sh_dn = c.shared_w if c.shared_w is not None else (None, None)
     order, tiles, ntiles, gk = t["order"], t["tiles"], t["ntiles"], t["gk"]
+    tl = (tiles, ntiles, maxt, gk)
     # (1) LoRA down-projection of dout for the down backward: DB = s dout B_d (not yet scaled by the row weight)
     ext_db = None
     if any_lora:
-        ext_db = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dout), H, T, 1, L.ptr(order), TK, K,
-               L.ptr(g(lb_ex, "bt_dn")), L.ptr(g(lb_sh, "bt_dn")), H, s_ex, s_sh, L.ptr(ext_db), st)
+        ext_db = _lora_ext(tl, dout, H, T, 1, order, TK, K, lb_ex, lb_sh, "bt_dn", H, 1, M, dev, st)
     # (2) down backward + SiLU-gate backward + d(row weight) partials
     nblk = L.load().smel_gmm_bwd_nblocks(I)
     dh = bf(M, 2 * I)
@@ -705,9 +743,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
     ext_dxa = None
     if any_lora:
-        ext_dxa = bf(M, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * I, M, 0, L.ptr(order), TK,
-               K, L.ptr(g(lb_ex, "bt_gu")), L.ptr(g(lb_sh, "bt_gu")), 2 * I, s_ex, s_sh, L.ptr(ext_dxa), st)
+        ext_dxa = _lora_ext(tl, dh, 2 * I, M, 0, order, TK, K, lb_ex, lb_sh, "bt_gu", 2 * I, planes, M, dev, st)
     # (6, side stream 1) LoRA factor gradients: one launch for the four products, written into parameter-shaped fp32
     # tensors; every operand is ready here, so it overlaps the gate_up backward
     grads = {}
@@ -717,14 +753,14 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
         groups = _lora_groups(ex, lb_sh is not None, n_sel, dev)
         sets = ((c.lora_ex if lb_ex is not None else None), (c.lora_sh if lb_sh is not None else None))
         gx, gs = (_alloc_lora_grads(m, dev) for m in sets)
-        jobs = _wgrad_jobs(H, I, (gx, gs), sets, (ext_dxa, t["x"], T, 1, 0), (t["ext_gu"], dh, M, 0, 0),
-                           (ext_db, t["act"], M, 0, 1), (t["ext_dn"], dout, T, 1, 1))
+        jobs, nj = _wgrad_jobs(H, I, (gx, gs), sets, (ext_dxa, t["x"], T, 1, 0), (t["ext_gu"], dh, M, 0, 0),
+                               (ext_db, t["act"], M, 0, 1), (t["ext_dn"], dout, T, 1, 1), planes)
         # rows of all LoRA groups: a token routes at most min(K, n_sel) slots to selected experts, + the shared rows
         max_rows = (min(K, n_sel) * T if lb_ex is not None else 0) + (T if lb_sh is not None else 0)
-        ws = _wgrad_ws(jobs, groups.numel(), max_rows, dev)
+        ws = _wgrad_ws(jobs, nj, groups.numel(), max_rows, dev)
         side_w = _Fork(dev, 1)
         with side_w:
-            L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK,
+            L.call("smel_lora_wgrad", jobs, nj, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK,
                    K, L.ptr(order), L.ptr(t["topv"]), L.ptr(t["sgate"]), max_rows, L.ptr(ws), ws.numel(), L.stream(),
                    tag="lora_wgrad")
         if gx is not None:
@@ -733,7 +769,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
             grads["sh"] = gs
     # (4) gate_up backward: per-slot dx rows
     dxs = bf(M, H)
-    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True)
+    w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True, planes=planes)
     L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, None, L.ptr(dxs), H, None, st,
            tag="gemm_gu_bwd")
@@ -772,52 +808,51 @@ def _alloc_lora_grads(lora, device):
             for n in _LORA_NAMES if getattr(lora, n).requires_grad}
 
 
-def _wgrad_ws(jobs, n_lora: int, max_rows: int, device) -> torch.Tensor:
+def _wgrad_ws(jobs, n_jobs: int, n_lora: int, max_rows: int, device) -> torch.Tensor:
     """fp32 workspace of smel_lora_wgrad (partial tiles of the groups longer than one 512-row chunk)."""
-    n = L.load().smel_lora_wgrad_ws_floats(jobs, 4, n_lora, max_rows)
+    n = L.load().smel_lora_wgrad_ws_floats(jobs, n_jobs, n_lora, max_rows)
     return torch.empty(max(n, 1), dtype=torch.float32, device=device)
 
 
-def _wgrad_jobs(H, I, grads, sets, j_agu, j_bgu, j_adn, j_bdn):
-    """The four smel_wg_job of a backward (dA of gate/up, dB of gate/up, dA of down, dB of down). Each j_* =
-    (L rows, Rm, Rm rows, r_gather, use_w). Destinations: class 0 = the selected experts' ExpertsLoRA (slot = its
-    index), class 1 = the shared MLPLoRA; gate/up products split in two halves (rows 0..15 / 16..31 of the rank
-    dimension, columns 0..I-1 / I..2I-1 for the B factors)."""
-    jobs = (L.WgJob * 4)()
-    Qs = (H, 2 * I, I, H)
-    for j, (spec, Q) in enumerate(zip((j_agu, j_bgu, j_adn, j_bdn), Qs)):
-        Lb, Rm, rows, gather, use_w = spec
-        J = jobs[j]
-        J.L, J.Rm, J.ldr, J.r_rows, J.r_gather, J.use_w, J.Q = L.ptr(Lb), L.ptr(Rm), Rm.shape[1], rows, gather, use_w, Q
+def _wgrad_jobs(H, I, grads, sets, j_agu, j_bgu, j_adn, j_bdn, planes: int = 1):
+    """The smel_wg_job list of a backward: dA and dB of gate/up, dA and dB of down. Each j_* = (L rows, Rm, Rm rows,
+    r_gather, use_w). Destinations: class 0 = the selected experts' ExpertsLoRA (slot = its index), class 1 = the
+    shared MLPLoRA. With one gate_up plane a gate/up product is one job whose result splits in two halves (ranks
+    0..15 / 16..31; the B factors' columns 0..I-1 / I..2I-1); with two planes it is one job per plane (L = that
+    plane's 32 columns of the 64-wide ext rows; the up B job reads the up half of dh only). Returns (jobs, count)."""
+    gate_up = []   # (L byte offset, ldl, Rm byte offset, Q, [(half, param, p0, q0, nq, col_major)])
+    if planes == 1:
+        gate_up.append((j_agu, 0, EXT, 0, H, [(0, "A_gate", 0, 0, H, False), (1, "A_up", EXT // 2, 0, H, False)]))
+        gate_up.append((j_bgu, 0, EXT, 0, 2 * I,
+                        [(0, "B_gate", 0, 0, I, True), (1, "B_up", EXT // 2, I, I, True)]))
+    else:
+        w = 2 * EXT
+        gate_up.append((j_agu, 0, w, 0, H, [(0, "A_gate", 0, 0, H, False)]))
+        gate_up.append((j_agu, 2 * EXT, w, 0, H, [(0, "A_up", 0, 0, H, False)]))
+        gate_up.append((j_bgu, 0, w, 0, I, [(0, "B_gate", 0, 0, I, True)]))
+        gate_up.append((j_bgu, 2 * EXT, w, 2 * I, I, [(0, "B_up", 0, 0, I, True)]))
+    specs = gate_up + [(j_adn, 0, EXT, 0, I, [(0, "A_down", 0, 0, I, False)]),
+                       (j_bdn, 0, EXT, 0, H, [(0, "B_down", 0, 0, H, True)])]
+    jobs = (L.WgJob * len(specs))()
+    for J, ((Lb, Rm, rows, gather, use_w), l_off, ldl, r_off, Q, dests) in zip(jobs, specs):
+        J.L, J.Rm = Lb.data_ptr() + l_off, Rm.data_ptr() + r_off
+        J.ldl, J.ldr, J.r_rows, J.r_gather, J.use_w, J.Q = ldl, Rm.shape[1], rows, gather, use_w, Q
         for cls in range(2):
             g, m = grads[cls], sets[cls]
             if g is None:
                 continue
-            r = m.r
             lead = 1 if cls == 0 else 0
-
-            def dest(h, name, p0, q0, nq, col_major):
+            for h, name, p0, q0, nq, col_major in dests:
                 t = g.get(name)
                 if t is None:
-                    return
+                    continue
                 d = J.dest[cls][h]
                 d.ptr = L.ptr(t)
                 d.s_idx = t.stride(0) if lead else 0
                 # A factors [.., r, Q] (p rows, q contiguous); B factors [.., Q, r] (q rows, p contiguous)
                 d.s_p, d.s_q = (1, t.stride(lead)) if col_major else (t.stride(lead), 1)
-                d.p0, d.np, d.q0, d.nq = p0, r, q0, nq
-
-            if j == 0:
-                dest(0, "A_gate", 0, 0, H, False)
-                dest(1, "A_up", 16, 0, H, False)
-            elif j == 1:
-                dest(0, "B_gate", 0, 0, I, True)
-                dest(1, "B_up", 16, I, I, True)
-            elif j == 2:
-                dest(0, "A_down", 0, 0, I, False)
-            else:
-                dest(0, "B_down", 0, 0, H, True)
-    return jobs
+                d.p0, d.np, d.q0, d.nq = p0, m.r, q0, nq
+    return jobs, len(specs)
 
 
 class _MoELayerFn(torch.autograd.Function):
@@ -854,7 +889,7 @@ class _MoELayerFn(torch.autograd.Function):
         if split:
             pgu, pdn, _, Is, pgu_t, pdn_t = plan["shared"]
             lsh = plan["lora_sh"]
-            lb_sh = _LoRABufs(lsh, 1, H, Is, dev) if lsh is not None else None
+            lb_sh = _LoRABufs(lsh, 1, H, Is, dev, _lora_planes(lsh)) if lsh is not None else None
             ysh, sv = _dense_mlp_fwd(x, pgu, pdn, lb_sh, "silu", tag="gemm_shared")
             shared_rows = (sgate, ysh)
             c.split = (sv, pgu_t, pdn_t, lsh, sgate)
@@ -943,24 +978,21 @@ def _dense_mlp_fwd(x, w_gu: PackedW, w_dn: PackedW, lb, act_name: str, tag: str 
     dev = x.device
     st = L.stream()
     tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
+    tl = (tiles, ntiles, maxt, gk)
     bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
     g = lambda n: getattr(lb, n) if lb is not None else None
-    sc = lb.scale if lb is not None else 0.0
+    planes = lb.planes if lb is not None else 1
     sv = _DenseSaved()
     sv.x, sv.lb, sv.ext_gu, sv.ext_dn = x, lb, None, None
     if lb is not None:
-        sv.ext_gu = bf(T, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(x), H, T, 0, None, 0, 1,
-               None, L.ptr(lb.a_gu), H, 0.0, sc, L.ptr(sv.ext_gu), st)
+        sv.ext_gu = _lora_ext(tl, x, H, T, 0, None, 0, 1, None, lb, "a_gu", H, planes, T, dev, st)
     sv.actb, sv.hsave = bf(T, Is), bf(T, 2 * Is)
-    wg = _dense_wset(w_gu, g("fwd_gu"))
+    wg = _dense_wset(w_gu, g("fwd_gu"), planes)
     L.call("smel_gmm_fwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 0,
            None, 0, 1, L.ptr(sv.ext_gu), 1, _ACT[act_name], L.ptr(sv.actb), Is, L.ptr(sv.hsave), st,
            tag=tag + "_gu_fwd")
     if lb is not None:
-        sv.ext_dn = bf(T, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(sv.actb), Is, T, 0, None, 0, 1,
-               None, L.ptr(lb.a_dn), Is, 0.0, sc, L.ptr(sv.ext_dn), st)
+        sv.ext_dn = _lora_ext(tl, sv.actb, Is, T, 0, None, 0, 1, None, lb, "a_dn", Is, 1, T, dev, st)
     y = bf(T, H)
     wd = _dense_wset(w_dn, g("fwd_dn"))
     L.call("smel_gmm_fwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(sv.actb), Is, T, 0,
@@ -980,14 +1012,13 @@ def _dense_mlp_bwd(sv: _DenseSaved, dy, w_gu_t: PackedW, w_dn_t: PackedW, lora, 
     dev = x.device
     st = L.stream()
     tiles, ntiles, maxt, gk = _dense_tiles(T, dev)
+    tl = (tiles, ntiles, maxt, gk)
     bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
     g = lambda n: getattr(lb, n) if lb is not None else None
-    sc = lb.scale if lb is not None else 0.0
+    planes = lb.planes if lb is not None else 1
     ext_db = ext_dxa = None
     if lb is not None:
-        ext_db = bf(T, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dy), H, T, 0, None, 0, 1,
-               None, L.ptr(lb.bt_dn), H, 0.0, sc, L.ptr(ext_db), st)
+        ext_db = _lora_ext(tl, dy, H, T, 0, None, 0, 1, None, lb, "bt_dn", H, 1, T, dev, st)
     nblk = L.load().smel_gmm_bwd_nblocks(Is)
     dh = bf(T, 2 * Is)
     dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
@@ -996,11 +1027,9 @@ def _dense_mlp_bwd(sv: _DenseSaved, dy, w_gu_t: PackedW, w_dn_t: PackedW, lora, 
            None, 0, 1, L.ptr(ext_db), 1, _ACT[act_name], L.ptr(sv.hsave), L.ptr(sv.actb), None, L.ptr(row_w),
            L.ptr(dh), 2 * Is, L.ptr(dwp), st, tag=tag + "_dn_bwd")
     if lb is not None:
-        ext_dxa = bf(T, EXT)
-        L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(dh), 2 * Is, T, 0, None, 0, 1,
-               None, L.ptr(lb.bt_gu), 2 * Is, 0.0, sc, L.ptr(ext_dxa), st)
+        ext_dxa = _lora_ext(tl, dh, 2 * Is, T, 0, None, 0, 1, None, lb, "bt_gu", 2 * Is, planes, T, dev, st)
     dx = bf(T, H)
-    wg = _dense_wset(w_gu_t, g("at_gu"))
+    wg = _dense_wset(w_gu_t, g("at_gu"), planes)
     L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
            0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H, None, st,
            tag=tag + "_gu_bwd")
@@ -1010,10 +1039,10 @@ def _dense_mlp_bwd(sv: _DenseSaved, dy, w_gu_t: PackedW, w_dn_t: PackedW, lora, 
         groups = torch.zeros(1, dtype=torch.int32, device=dev)   # group 0 >= E = 0: rows [0, T)
         gs = _alloc_lora_grads(lora, dev)
         # the down projection's products take the row weight (dh already carries it)
-        jobs = _wgrad_jobs(H, Is, (None, gs), (None, lora), (ext_dxa, x, T, 0, 0), (sv.ext_gu, dh, T, 0, 0),
-                           (ext_db, sv.actb, T, 0, 1), (sv.ext_dn, dy, T, 0, 1))
-        ws = _wgrad_ws(jobs, 1, T, dev)
-        L.call("smel_lora_wgrad", jobs, 4, L.ptr(groups), 1, 0, L.ptr(zero), 0, T, 0, 1, None, None, L.ptr(row_w),
+        jobs, nj = _wgrad_jobs(H, Is, (None, gs), (None, lora), (ext_dxa, x, T, 0, 0), (sv.ext_gu, dh, T, 0, 0),
+                               (ext_db, sv.actb, T, 0, 1), (sv.ext_dn, dy, T, 0, 1), planes)
+        ws = _wgrad_ws(jobs, nj, 1, T, dev)
+        L.call("smel_lora_wgrad", jobs, nj, L.ptr(groups), 1, 0, L.ptr(zero), 0, T, 0, 1, None, None, L.ptr(row_w),
                T, L.ptr(ws), ws.numel(), st, tag="lora_wgrad")
         grads = gs
     return dx, grads, dwp, nblk
@@ -1026,7 +1055,7 @@ class _MLPFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_gu2, w_dn2, lora, act_name, *leaves):
-        lb = _LoRABufs(lora, 1, x.shape[1], w_dn2[0].C, x.device) if lora is not None else None
+        lb = _LoRABufs(lora, 1, x.shape[1], w_dn2[0].C, x.device, _lora_planes(lora)) if lora is not None else None
         y, sv = _dense_mlp_fwd(x, w_gu2[0], w_dn2[0], lb, act_name)
         ctx.sv, ctx.w, ctx.lora, ctx.act_name = sv, (w_gu2[1], w_dn2[1]), lora, act_name
         return y
@@ -1041,11 +1070,14 @@ class _MLPFn(torch.autograd.Function):
         return (dx, None, None, None, None, *grads)
 
 
-def _dense_wset(w: PackedW, ext) -> L.WSet:
+def _dense_wset(w: PackedW, ext, planes: int = 1) -> L.WSet:
+    """smel_wset of a dense MLP projection (the shared group); planes = 2 for a two-plane gate_up LoRA."""
     ws = L.WSet()
     ws.wsh = L.ptr(w.t)
     ws.ext_sh = L.ptr(ext)
     ws.R, ws.C, ws.group = w.R, w.C, 32
+    if planes == 2:
+        ws.flags |= L.WSET_EXT2
     return ws
 
 

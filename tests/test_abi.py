@@ -102,12 +102,20 @@ def test_host_side_rejections():
     assert L.smel_packed_bytes(7, 64, 64) == -1
     assert L.smel_pack_int4(1, 1, 1, 64, 96, 64, 1, 1, None) == -2      # group does not divide K
     assert L.smel_pack_bf16(1, 64, 60, 64, 1, None) == -2               # K not a multiple of 8
-    with pytest.raises(_lib.SmelError):
-        _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, 32, 64, 64, None, None, None, None, None,
-                  None, None, None, None)
-    # LoRA weight gradients: a destination outside the 32 x Q result is rejected on the host
+    # LoRA layouts: rank above 16 with one gate_up plane, above 32 with two, a third plane
+    for r, planes in ((17, 1), (33, 2), (8, 3)):
+        with pytest.raises(_lib.SmelError):
+            _lib.call("smel_lora_prep", None, None, None, None, None, None, 2, r, planes, 64, 64, None, None, None,
+                      None, None, None, None, None, None)
+    with pytest.raises(_lib.SmelError):   # ext row stride other than one or two planes
+        _lib.call("smel_lora_ext", 8, 8, 1, None, 16, 64, 4, 0, None, 0, 1, None, 16, 64, 1.0, 1.0, 16, 48, None)
+    # LoRA weight gradients: an L row stride other than 32 / 64, and a destination outside the 32 x Q result, are
+    # rejected on the host
     jobs = (_lib.WgJob * 4)()
-    jobs[0].L, jobs[0].Rm, jobs[0].ldr, jobs[0].r_rows, jobs[0].Q = 1, 16, 64, 4, 64
+    jobs[0].L, jobs[0].Rm, jobs[0].ldr, jobs[0].r_rows, jobs[0].Q, jobs[0].ldl = 8, 16, 64, 4, 64, 48
+    assert L.smel_lora_wgrad(jobs, 1, 1, 1, 0, 1, 0, 4, 0, 1, None, None, None, 4, 1, 1 << 20, None) == -1
+    assert b"stride" in L.smel_last_error()
+    jobs[0].ldl = 64
     jobs[0].dest[1][0].ptr, jobs[0].dest[1][0].p0, jobs[0].dest[1][0].np, jobs[0].dest[1][0].nq = 16, 20, 16, 64
     assert L.smel_lora_wgrad_ws_floats(jobs, 1, 1, 4) == 1 * (1 + 1) * 32 * 128
     assert L.smel_lora_wgrad(jobs, 1, 1, 1, 0, 1, 0, 4, 0, 1, None, None, None, 4, 1, 1 << 20, None) == -1

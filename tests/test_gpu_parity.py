@@ -460,6 +460,14 @@ LAYERS = {
     # more than 256 experts (the router's 8-logits-per-lane selection)
     "e512": dict(T=200, H=128, E=512, I=64, K=8, n_sel=3, r=4, alpha=8.0, shared_inter=64, group=64,
                  lora_b_std=0.05),
+    # LoRA ranks above 16: the gate_up K-extension in two 32-wide planes (gate, up); mixed ranks in one launch (the
+    # rank-8 shared set laid out in two planes too); a split shared expert with its own two-plane extension
+    "r32": dict(T=400, H=256, E=16, I=128, K=4, n_sel=3, r=32, alpha=64.0, shared_inter=128, group=64,
+                lora_b_std=0.05),
+    "r24_mixed": dict(T=333, H=256, E=16, I=128, K=4, n_sel=4, r=24, alpha=48.0, shared_inter=128, group=64,
+                      lora_b_std=0.05, r_shared=8),
+    "r32_shared_split": dict(T=260, H=256, E=16, I=128, K=4, n_sel=2, r=32, alpha=32.0, shared_inter=192, group=64,
+                             lora_b_std=0.05),
 }
 
 
@@ -591,7 +599,8 @@ def test_route_api_backward():
 
 
 @pytest.mark.parametrize("act_name,T,H,Is,r", [("silu", 300, 256, 128, 8), ("gelu_tanh", 257, 512, 192, 16),
-                                               ("silu", 64, 128, 64, 0)])
+                                               ("silu", 64, 128, 64, 0), ("gelu_tanh", 190, 256, 128, 32),
+                                               ("silu", 140, 128, 64, 20)])
 def test_mlp_lora_parity(act_name, T, H, Is, r):
     """mlp_lora (smel/moe.py:183-194; Gemma-4's dense GeGLU MLP with act gelu_tanh) as the dense group."""
     from smel.lora import MLPLoRA
