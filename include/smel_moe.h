@@ -59,6 +59,10 @@ typedef struct smel_wset {
 } smel_wset;
 #define SMEL_WSET_FAST_DQ 1
 #define SMEL_WSET_EXT2 2
+/* SMEL_WSET_XCD_CHUNK: the GEMM's tile list is in group order (smel_dispatch's tiles_grouped) and each of the 8
+ * XCDs takes a contiguous chunk of it, so a group's tiles run side by side on one XCD and share its L2 (its weights
+ * are streamed once for all of them); without it, tile t runs on XCD t % 8 in list order. */
+#define SMEL_WSET_XCD_CHUNK 4
 
 const char* smel_last_error(void);
 int smel_abi_version(void);
@@ -160,12 +164,14 @@ int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scal
  * row1, gk} over groups 0..E-1 (+ group E = shared rows [TK, TK+shared_rows) when shared_rows > 0), m_tile rows
  * each, gk = gkind[group] when gkind [E (+1)] is given (the GEMMs then need no gkind argument), else 0; n_tiles [1]
  * = how many are used. Order: the tiles of more than m_tile / 2 rows in group order, then the shorter (last) tiles
- * in group order. err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
+ * in group order. tiles_grouped (optional, [max_tiles][4]): the same tiles in group order (for SMEL_WSET_XCD_CHUNK).
+ * err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
  * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
  * workspace. E <= 512. */
 int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                   int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
-                  int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream);
+                  int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t* ws,
+                  hipStream_t stream);
 /* int32 elements of smel_dispatch's workspace (host-side, no GPU call); -1 for bad sizes. */
 int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
 /* smel_dispatch without the workspace argument; it allocates nothing. No counterpart in the reference: it exists
@@ -177,7 +183,8 @@ int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
  * streams, or threads without ordering) race: order them on one stream. Results are those of smel_dispatch. */
 int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                           int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
-                          int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, hipStream_t stream);
+                          int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err,
+                          hipStream_t stream);
 /* int32 capacity of smel_dispatch_noalloc's built-in workspace (host-side, no GPU call). */
 int64_t smel_dispatch_noalloc_max_ws(void);
 /* Upper bound of the tile-list length for smel_dispatch (host-side, no GPU call). */

@@ -183,9 +183,23 @@ SMEL_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 // MI355X has 8 XCDs, each with its own L2; consecutive workgroup ids go to consecutive XCDs. A 1-D grid of
 // xcd_grid(max_tiles) * nblk workgroups are mapped so that the nblk column blocks of one tile run back to back on one
 // XCD (workgroups go to the XCDs round robin: block b to XCD b % 8): they share the tile's A rows in that XCD's L2.
-// Tiles are taken in list order, tile t on XCD t % 8.
+// xcd_tile: tiles are taken in list order, tile t on XCD t % 8. xcd_tile_chunk: XCD x takes the contiguous chunk
+// [x c, (x + 1) c) of the list (c = ceil(n_tiles / 8)) in order, so with a list in group order the tiles of one group
+// run side by side on one XCD and share its weights in that XCD's L2.
 constexpr int NXCD = 8;
 inline int64_t xcd_grid(int64_t max_tiles) { return (max_tiles + NXCD - 1) / NXCD * NXCD; }
+SMEL_DEV bool xcd_tile_chunk(int n_tiles, int nblk, int& tile, int& nb) {
+  const int b = blockIdx.x;
+  const int x = b % NXCD, j = b / NXCD;
+  const int chunk = (n_tiles + NXCD - 1) / NXCD;
+  const int r = j / nblk;
+  if (r >= chunk) return false;
+  const int t = x * chunk + r;
+  if (t >= n_tiles) return false;
+  tile = t;
+  nb = j % nblk;
+  return true;
+}
 SMEL_DEV bool xcd_tile(int n_tiles, int nblk, int& tile, int& nb) {
   const int b = blockIdx.x;
   const int x = b % NXCD, j = b / NXCD;

@@ -77,7 +77,8 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
                                                       int32_t* __restrict__ hist,
                                                       const int32_t* __restrict__ bad, int32_t* __restrict__ counts,
                                                       int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
-                                                      int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
+                                                      int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles,
+                                                      int32_t* __restrict__ err) {
   __shared__ int wsum[NW];
   __shared__ int off_s[MAXE + 1];
   __shared__ int bad_s;
@@ -135,7 +136,8 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   __syncthreads();
   // tile list over groups 0..E-1 (+ shared group E): the tiles of more than m_tile / 2 rows first (in group order),
   // then the shorter last tiles of the groups (in group order). The grouped GEMMs start tiles in list order, so the
-  // short tiles fill the last round of workgroups instead of holding long ones back.
+  // short tiles fill the last round of workgroups instead of holding long ones back. tiles_g (optional): the same
+  // tiles in group order, a group's tiles next to each other.
   int nt = 0, rows = 0, row0 = 0, nlong = 0;
   if (tid < G) {
     rows = tid < E ? off_s[tid + 1] - off_s[tid] : shared_rows;
@@ -157,6 +159,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
       tl.z = min(row0 + rows, row0 + (i + 1) * m_tile);
       tl.w = gkv;
       reinterpret_cast<int4*>(tiles)[pos] = tl;
+      if (tiles_g) reinterpret_cast<int4*>(tiles_g)[lbase + sbase + i] = tl;
     }
   }
   if (tid == 0) {
@@ -252,9 +255,8 @@ extern "C" int64_t smel_dispatch_ws_size(int64_t TK, int64_t E) {
 
 extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
                              int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
-                             int32_t* offsets, int32_t* order,
-                             int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* err, int32_t* ws,
-                             hipStream_t stream) {
+                             int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles, int32_t* tiles_grouped,
+                             int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && shared_rows >= 0 && m_tile > 0, SMEL_EINVAL, "dispatch: bad sizes");
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "dispatch: E=%lld > %d experts", (long long)E, MAXE);
   SMEL_REQUIRE(T * K < (1ll << 30), SMEL_EUNSUPPORTED, "dispatch: T*K too large");
@@ -271,7 +273,7 @@ extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, in
     if (st) return st;
   }
   dispatch_scan<<<1, DB, 0, stream>>>(nb, (int)TK, (int)E, (int)shared_rows, m_tile, (int)mt, gkind, hist, bad,
-                                      counts, offsets, tiles, n_tiles, err);
+                                      counts, offsets, tiles, tiles_grouped, n_tiles, err);
   if (nb > 0) {
     const int st = smel::launch_status();
     if (st) return st;
@@ -285,7 +287,7 @@ extern "C" int64_t smel_dispatch_noalloc_max_ws(void) { return SCRATCH_INTS; }
 extern "C" int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
                                      int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
                                      int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
-                                     int32_t* n_tiles, int32_t* err, hipStream_t stream) {
+                                     int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && T * K < (1ll << 30), SMEL_EINVAL, "dispatch_noalloc: bad sizes");
   const int64_t need = smel_dispatch_ws_size(T * K, E);
   SMEL_REQUIRE(need >= 0 && need <= SCRATCH_INTS, SMEL_EUNSUPPORTED,
@@ -295,5 +297,5 @@ extern "C" int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64
   int32_t* ws = scratch_on_device();
   if (!ws) return SMEL_EINVAL;
   return smel_dispatch(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
-                       n_tiles, err, ws, stream);
+                       tiles_grouped, n_tiles, err, ws, stream);
 }

@@ -501,7 +501,9 @@ SMEL_DEV void run_tile_ns(const BwdArgs& a, int kind, int idx, int row0, int nro
 template <int EPI, bool SZ2>
 SMEL_DEV void gmm_bwd_body(const BwdArgs& a, uint8_t* smem) {
   int tile, nb;
-  if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
+  if (!((a.w.flags & SMEL_WSET_XCD_CHUNK) ? xcd_tile_chunk(a.n_tiles[0], a.nblk, tile, nb)
+                                          : xcd_tile(a.n_tiles[0], a.nblk, tile, nb)))
+    return;
   const int4 t = a.tiles[tile];
   const int gk = a.gkind ? a.gkind[t.x] : t.w;   // the tile list may carry the group kind itself
   const int kind = gk >> 16, idx = gk & 0xffff;

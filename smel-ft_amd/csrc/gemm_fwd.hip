@@ -379,7 +379,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(1024))) uint16_t S3[A_STAGE];
   __shared__ int rowmap[MT];
   int tile, nb;
-  if (!xcd_tile(a.n_tiles[0], a.nblk, tile, nb)) return;
+  if (!((a.w.flags & SMEL_WSET_XCD_CHUNK) ? xcd_tile_chunk(a.n_tiles[0], a.nblk, tile, nb)
+                                          : xcd_tile(a.n_tiles[0], a.nblk, tile, nb)))
+    return;
   const int4 t = a.tiles[tile];
   const int gk = a.gkind ? a.gkind[t.x] : t.w;   // the tile list may carry the group kind itself
   const int kind = gk >> 16, idx = gk & 0xffff;

@@ -634,7 +634,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     maxt = L.load().smel_dispatch_max_tiles(TK, E, rows_sh, M_TILE)
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
-    tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
+    tiles, tiles_g, ntiles, err = i32(maxt * 4), i32(maxt * 4), i32(1), i32(1)
     dws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
     if prep is None:   # LoRA layouts on a side stream, overlapping the dispatch
         fork = _Fork(dev, 2)
@@ -643,7 +643,8 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
         prep = (fork, bufs)
     gk_groups = ex.gkind(shared is not None, dev)
     L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(gk_groups), L.ptr(counts),
-           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st)
+           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err),
+           L.ptr(dws), st)
     gk = None   # the tile list carries each tile's group kind
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):
@@ -664,8 +665,11 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
         ext_gu = _lora_ext(tl, x, H, T, 1, order, TK, K, lb_ex, lb_sh, "a_gu", H, planes, M, dev, st)
     actb = bf(M, I)
     hsave = bf(M, 2 * I) if need_grad else None
+    # the gate_up GEMMs take the tiles in group order, a chunk per XCD (an expert's tiles share its weights in L2);
+    # the down GEMMs the long-tiles-first order (short tiles fill the last round)
     w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"), planes=planes)
-    L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
+    w_gu.flags |= L.WSET_XCD_CHUNK
+    L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_g), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_gu_fwd")
     if any_lora:
         ext_dn = _lora_ext(tl, actb, I, M, 0, order, TK, K, lb_ex, lb_sh, "a_dn", I, 1, M, dev, st)
@@ -683,8 +687,8 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     c.ex, c.shared_w = ex, (sh_gu_t, sh_dn_t) if shared is not None else None
     sel_t = ex.packed_sel_t() if (need_grad and sel_gu is not None) else None
     c.tensors = dict(x=x, topv=topv, sgate=sgate, counts=counts, offsets=offsets, order=order, inv=inv, tiles=tiles,
-                     ntiles=ntiles, err=err, gk=gk, act=actb, hsave=hsave, ext_gu=ext_gu, ext_dn=ext_dn,
-                     sel_gu=sel_t[0] if sel_t else None, sel_dn=sel_t[1] if sel_t else None)
+                     tiles_g=tiles_g, ntiles=ntiles, err=err, gk=gk, act=actb, hsave=hsave, ext_gu=ext_gu,
+                     ext_dn=ext_dn, sel_gu=sel_t[0] if sel_t else None, sel_dn=sel_t[1] if sel_t else None)
     c.lb_ex, c.lb_sh = lb_ex, lb_sh
     c.lora_ex, c.lora_sh = lora_ex, lora_sh
     return out
@@ -770,8 +774,9 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     # (4) gate_up backward: per-slot dx rows
     dxs = bf(M, H)
     w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True, planes=planes)
-    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I, M, 0,
-           L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, None, L.ptr(dxs), H, None, st,
+    w_gu.flags |= L.WSET_XCD_CHUNK
+    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(t["tiles_g"]), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I,
+           M, 0, L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, None, L.ptr(dxs), H, None, st,
            tag="gemm_gu_bwd")
     side_r.join()
     dx = bf(T, H)

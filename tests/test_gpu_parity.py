@@ -369,25 +369,28 @@ def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128, gkind=None):
     maxt = L.load().smel_dispatch_max_tiles(TK, E, shared_rows, m_tile)
     i32 = lambda n: torch.full((n,), -7, dtype=torch.int32, device=DEV)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
-    tiles, ntiles, err = i32(maxt * 4), i32(1), i32(1)
+    tiles, tiles_g, ntiles, err = i32(maxt * 4), i32(maxt * 4), i32(1), i32(1)
     ws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))   # garbage-filled: the kernels must not rely on zeros
     gk = torch.tensor(gkind, dtype=torch.int32, device=DEV) if gkind is not None else None
     L.call("smel_dispatch", L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, shared_rows, m_tile, L.ptr(gk),
-           L.ptr(counts), L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(ntiles), L.ptr(err),
-           L.ptr(ws), L.stream())
-    return [a.cpu().numpy() for a in (counts, offsets, order, inv, tiles, ntiles, err)]
+           L.ptr(counts), L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(tiles_g), L.ptr(ntiles),
+           L.ptr(err), L.ptr(ws), L.stream())
+    out = [a.cpu().numpy() for a in (counts, offsets, order, inv, tiles, ntiles, err)]
+    _dispatch.grouped = tiles_g.cpu().numpy()
+    return out
 
 
-def _expected_tiles(offsets, E, TK, shared_rows, m_tile):
+def _expected_tiles(offsets, E, TK, shared_rows, m_tile, grouped=False):
     """m_tile-row tiles of every group; those of more than m_tile / 2 rows first, then the short ones, each part in
-    group order."""
+    group order (grouped: all in group order)."""
     out = []
     for g in range(E + (1 if shared_rows else 0)):
         r0 = offsets[g] if g < E else TK
         n = (offsets[g + 1] - offsets[g]) if g < E else shared_rows
         for i in range(0, n, m_tile):
             out.append((g, r0 + i, r0 + min(n, i + m_tile), 0))
-    out = [t for t in out if t[2] - t[1] > m_tile // 2] + [t for t in out if t[2] - t[1] <= m_tile // 2]
+    if not grouped:
+        out = [t for t in out if t[2] - t[1] > m_tile // 2] + [t for t in out if t[2] - t[1] <= m_tile // 2]
     return np.array(out, dtype=np.int32).reshape(-1, 4)
 
 
@@ -423,10 +426,13 @@ def test_dispatch_bitexact(T, K, E, shared, kind):
         if T:
             assert np.array_equal(order, ord0) and np.array_equal(inv, inv0)
         want = _expected_tiles(o0, E, T * K, sh, 128)
+        want_g = _expected_tiles(o0, E, T * K, sh, 128, grouped=True)
         if gkind is not None:
             want[:, 3] = np.asarray(gkind, np.int32)[want[:, 0]]
+            want_g[:, 3] = np.asarray(gkind, np.int32)[want_g[:, 0]]
         assert ntiles[0] == len(want)
         assert np.array_equal(tiles.reshape(-1, 4)[:len(want)], want)
+        assert np.array_equal(_dispatch.grouped.reshape(-1, 4)[:len(want)], want_g)
 
 
 def test_dispatch_flags_bad_ids():

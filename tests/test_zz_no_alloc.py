@@ -16,10 +16,10 @@ def _run(entry, ids, T, K, E, shared_rows, gkind):
     TK = T * K
     maxt = lib.smel_dispatch_max_tiles(TK, E, shared_rows, 128)
     i32 = lambda n, v=-7: torch.full((max(n, 1),), v, dtype=torch.int32, device=DEV)   # poisoned outputs
-    out = dict(counts=i32(E), offsets=i32(E + 1), order=i32(TK), inv=i32(TK), tiles=i32(maxt * 4), ntiles=i32(1),
-               err=i32(1))
+    out = dict(counts=i32(E), offsets=i32(E + 1), order=i32(TK), inv=i32(TK), tiles=i32(maxt * 4),
+               tiles_g=i32(maxt * 4), ntiles=i32(1), err=i32(1))
     args = [L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, shared_rows, 128, L.ptr(gkind)] + \
-           [L.ptr(out[k]) for k in ("counts", "offsets", "order", "inv", "tiles", "ntiles", "err")]
+           [L.ptr(out[k]) for k in ("counts", "offsets", "order", "inv", "tiles", "tiles_g", "ntiles", "err")]
     if entry == "smel_dispatch":
         ws = torch.empty(max(1, lib.smel_dispatch_ws_size(TK, E)), dtype=torch.int32, device=DEV)
         L.call(entry, *args, L.ptr(ws), L.stream())
@@ -29,6 +29,7 @@ def _run(entry, ids, T, K, E, shared_rows, gkind):
     n = int(out["ntiles"][0])
     res = {k: v.cpu().numpy() for k, v in out.items()}
     res["tiles"] = res["tiles"][:4 * n]
+    res["tiles_g"] = res["tiles_g"][:4 * n]
     return res
 
 
@@ -57,5 +58,5 @@ def test_noalloc_dispatch_matches_workspace_dispatch(dtype):
     # too large for the scratch array: rejected on the host, before any launch
     big_T = 65536
     assert lib.smel_dispatch_ws_size(big_T * 8, 512) > lib.smel_dispatch_noalloc_max_ws()
-    rc = lib.smel_dispatch_noalloc(1, 0, big_T, 8, 512, 0, 128, None, 1, 1, 1, 1, 1, 1, 1, None)
+    rc = lib.smel_dispatch_noalloc(1, 0, big_T, 8, 512, 0, 128, None, 1, 1, 1, 1, 1, None, 1, 1, None)
     assert rc == -2 and b"scratch" in lib.smel_last_error()
