@@ -210,6 +210,15 @@ int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, 
                    const float* A_down, const float* B_down, int64_t n, int64_t r, int32_t planes, int64_t Hd,
                    int64_t In, uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu, uint16_t* a_dn, uint16_t* bt_dn,
                    uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn, hipStream_t stream);
+/* The same layouts for up to two LoRA sets of one layer (the selected experts' and the shared MLP's, same Hd, In and
+ * planes) in one launch; a set with n = 0 is skipped. */
+typedef struct smel_lora_set {
+  const float *A_gate, *B_gate, *A_up, *B_up, *A_down, *B_down;
+  int64_t n, r;
+  uint16_t *fwd_gu, *fwd_dn, *a_gu, *a_dn, *bt_dn, *bt_gu, *at_gu, *at_dn;
+} smel_lora_set;
+int smel_lora_prep_sets(const smel_lora_set* sets, int32_t n_sets, int32_t planes, int64_t Hd, int64_t In,
+                        hipStream_t stream);
 
 /* ---- (A11/A12) LoRA down-projections of the rows of LoRA groups (SEL / SHARED tiles of the tile list):
  * ext[row * ldx + 0:32] = bf16(scale_g * A_src[src(row)][0:Kd] . wcat_g[0:32][0:Kd]) where src(row) = token of the row

@@ -6,14 +6,30 @@
 
 namespace {
 
-__global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ Ag, const float* __restrict__ Bg,
-                                                        const float* __restrict__ Au, const float* __restrict__ Bu,
-                                                        const float* __restrict__ Ad, const float* __restrict__ Bd,
-                                                        int n, int r, int planes, int Hd, int In,
-                                                        uint16_t* __restrict__ fwd_gu, uint16_t* __restrict__ fwd_dn,
-                                                        uint16_t* __restrict__ a_gu, uint16_t* __restrict__ a_dn,
-                                                        uint16_t* __restrict__ bt_dn, uint16_t* __restrict__ bt_gu,
-                                                        uint16_t* __restrict__ at_gu, uint16_t* __restrict__ at_dn) {
+constexpr int PREP_MAX_SETS = 2;
+struct PrepArgs {
+  smel_lora_set set[PREP_MAX_SETS];
+  int planes, Hd, In;
+};
+
+// grid (256, 8 layouts, sets): blockIdx.z picks the LoRA set, blockIdx.y the layout
+__global__ __launch_bounds__(256) void lora_prep_kernel(PrepArgs pa) {
+  const smel_lora_set& S = pa.set[blockIdx.z];
+  const float* __restrict__ Ag = S.A_gate;
+  const float* __restrict__ Bg = S.B_gate;
+  const float* __restrict__ Au = S.A_up;
+  const float* __restrict__ Bu = S.B_up;
+  const float* __restrict__ Ad = S.A_down;
+  const float* __restrict__ Bd = S.B_down;
+  uint16_t* __restrict__ fwd_gu = S.fwd_gu;
+  uint16_t* __restrict__ fwd_dn = S.fwd_dn;
+  uint16_t* __restrict__ a_gu = S.a_gu;
+  uint16_t* __restrict__ a_dn = S.a_dn;
+  uint16_t* __restrict__ bt_dn = S.bt_dn;
+  uint16_t* __restrict__ bt_gu = S.bt_gu;
+  uint16_t* __restrict__ at_gu = S.at_gu;
+  uint16_t* __restrict__ at_dn = S.at_dn;
+  const int n = (int)S.n, r = (int)S.r, planes = pa.planes, Hd = pa.Hd, In = pa.In;
   // 32-bit index arithmetic (every layout has fewer than 2^31 elements: checked by the host) and two adjacent
   // outputs per thread (every innermost dimension is even), stored as one 32-bit word
   const int which = blockIdx.y;
@@ -451,27 +467,46 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
 
 }  // namespace
 
+extern "C" int smel_lora_prep_sets(const smel_lora_set* sets, int32_t n_sets, int32_t planes, int64_t Hd,
+                                   int64_t In, hipStream_t stream) {
+  SMEL_REQUIRE(sets && n_sets >= 1 && n_sets <= PREP_MAX_SETS, SMEL_EINVAL, "lora_prep: %d sets (1 or 2)", n_sets);
+  SMEL_REQUIRE(Hd > 0 && In > 0, SMEL_EINVAL, "lora_prep: bad sizes");
+  SMEL_REQUIRE(planes == 1 || planes == 2, SMEL_EINVAL, "lora_prep: planes %d (1 or 2)", planes);
+  PrepArgs pa{};
+  pa.planes = planes;
+  pa.Hd = (int)Hd;
+  pa.In = (int)In;
+  int nz = 0;
+  for (int i = 0; i < n_sets; ++i) {
+    const smel_lora_set& S = sets[i];
+    SMEL_REQUIRE(S.n >= 0 && S.r > 0, SMEL_EINVAL, "lora_prep: set %d: bad sizes", i);
+    SMEL_REQUIRE(S.r <= 16 * planes, SMEL_EUNSUPPORTED, "lora_prep: set %d: rank %lld > %d (%d plane%s)", i,
+                 (long long)S.r, 16 * planes, planes, planes == 1 ? "; 2 planes take up to 32" : "s");
+    if (S.n == 0) continue;
+    SMEL_REQUIRE(S.A_gate && S.B_gate && S.A_up && S.B_up && S.A_down && S.B_down && S.fwd_gu && S.fwd_dn && S.a_gu &&
+                     S.a_dn && S.bt_dn && S.bt_gu && S.at_gu && S.at_dn,
+                 SMEL_EINVAL, "lora_prep: set %d: null pointer", i);
+    SMEL_REQUIRE(S.n * planes * 32 * std::max(Hd, 2 * In) < (1ll << 31), SMEL_EUNSUPPORTED,
+                 "lora_prep: set %d: layouts too large", i);
+    SMEL_REQUIRE(((uintptr_t)S.fwd_gu | (uintptr_t)S.fwd_dn | (uintptr_t)S.a_gu | (uintptr_t)S.a_dn |
+                  (uintptr_t)S.bt_dn | (uintptr_t)S.bt_gu | (uintptr_t)S.at_gu | (uintptr_t)S.at_dn) % 4 == 0,
+                 SMEL_EUNSUPPORTED, "lora_prep: set %d: outputs must be 4-byte aligned", i);
+    pa.set[nz++] = S;   // empty sets are left out of the launch
+  }
+  if (nz == 0) return 0;
+  dim3 grid(256, 8, nz);
+  lora_prep_kernel<<<grid, 256, 0, stream>>>(pa);
+  return smel::launch_status();
+}
+
 extern "C" int smel_lora_prep(const float* A_gate, const float* B_gate, const float* A_up, const float* B_up,
                               const float* A_down, const float* B_down, int64_t n, int64_t r, int32_t planes,
                               int64_t Hd, int64_t In, uint16_t* fwd_gu, uint16_t* fwd_dn, uint16_t* a_gu,
                               uint16_t* a_dn, uint16_t* bt_dn, uint16_t* bt_gu, uint16_t* at_gu, uint16_t* at_dn,
                               hipStream_t stream) {
-  SMEL_REQUIRE(n >= 0 && r > 0 && Hd > 0 && In > 0, SMEL_EINVAL, "lora_prep: bad sizes");
-  SMEL_REQUIRE(planes == 1 || planes == 2, SMEL_EINVAL, "lora_prep: planes %d (1 or 2)", planes);
-  SMEL_REQUIRE(r <= 16 * planes, SMEL_EUNSUPPORTED, "lora_prep: rank %lld > %d (%d plane%s)", (long long)r,
-               16 * planes, planes, planes == 1 ? "; 2 planes take up to 32" : "s");
-  if (n == 0) return 0;
-  SMEL_REQUIRE(A_gate && B_gate && A_up && B_up && A_down && B_down && fwd_gu && fwd_dn && a_gu && a_dn && bt_dn &&
-                   bt_gu && at_gu && at_dn, SMEL_EINVAL, "lora_prep: null pointer");
-  SMEL_REQUIRE(n * planes * 32 * std::max(Hd, 2 * In) < (1ll << 31), SMEL_EUNSUPPORTED,
-               "lora_prep: layouts too large");
-  SMEL_REQUIRE(((uintptr_t)fwd_gu | (uintptr_t)fwd_dn | (uintptr_t)a_gu | (uintptr_t)a_dn | (uintptr_t)bt_dn |
-                (uintptr_t)bt_gu | (uintptr_t)at_gu | (uintptr_t)at_dn) % 4 == 0, SMEL_EUNSUPPORTED,
-               "lora_prep: outputs must be 4-byte aligned");
-  dim3 grid(256, 8);
-  lora_prep_kernel<<<grid, 256, 0, stream>>>(A_gate, B_gate, A_up, B_up, A_down, B_down, (int)n, (int)r, planes,
-                                             (int)Hd, (int)In, fwd_gu, fwd_dn, a_gu, a_dn, bt_dn, bt_gu, at_gu, at_dn);
-  return smel::launch_status();
+  const smel_lora_set S{A_gate, B_gate, A_up, B_up, A_down, B_down, n, r, fwd_gu, fwd_dn, a_gu, a_dn,
+                        bt_dn, bt_gu, at_gu, at_dn};
+  return smel_lora_prep_sets(&S, 1, planes, Hd, In, stream);
 }
 
 extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,

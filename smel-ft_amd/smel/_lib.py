@@ -19,7 +19,7 @@ PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -40,6 +40,13 @@ class WgJob(ctypes.Structure):
     """smel_wg_job of include/smel_moe.h."""
     _fields_ = [("L", vp), ("Rm", vp), ("ldr", i64), ("r_rows", i64), ("r_gather", i32), ("use_w", i32), ("Q", i64),
                 ("ldl", i64), ("dest", (WgDest * 2) * 2)]
+
+
+class LoraSet(ctypes.Structure):
+    """smel_lora_set of include/smel_moe.h: one LoRA set's fp32 factors and its bf16 layouts."""
+    _fields_ = [(n, vp) for n in ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")] + \
+               [("n", i64), ("r", i64)] + \
+               [(n, vp) for n in ("fwd_gu", "fwd_dn", "a_gu", "a_dn", "bt_dn", "bt_gu", "at_gu", "at_dn")]
 
 
 class H2DRegion(ctypes.Structure):
@@ -69,6 +76,7 @@ SIGNATURES = {
     "smel_dispatch_noalloc": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_dispatch_noalloc_max_ws": (i64, []),
     "smel_lora_prep": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_lora_prep_sets": (i32, [ctypes.POINTER(LoraSet), i32, i32, i64, i64, vp]),
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, i64, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, i64, vp, vp]),

@@ -341,9 +341,10 @@ def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> Packe
 
 
 _SIDE_STREAMS = {}
-# Side streams in use: 0 = router backward, 1 = LoRA factor gradients, 2 = the forward's LoRA layouts.
-# SMEL_SIDE_STREAMS="0,1" (say) keeps only those; a fork that is off runs its launches on the main stream, in order.
-_SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1,2").split(",") if v.strip())
+# Side streams: 0 = router backward, 1 = LoRA factor gradients, 2 = the forward's LoRA layouts. The default keeps
+# 0 and 1: the layouts of both LoRA sets are one ~16 us launch, less than a fork and join of a graph costs there.
+# SMEL_SIDE_STREAMS="0,1,2" (say) picks others; a fork that is off runs its launches on the main stream, in order.
+_SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1").split(",") if v.strip())
 
 
 def _side_stream(dev, i: int) -> torch.cuda.Stream:
@@ -384,20 +385,37 @@ class _LoRABufs:
     gate_up side has ``planes`` 32-wide planes (a_gu, bt_gu: plane-major, one [n][32][K] matrix per plane; at_gu:
     [n][planes][H][32])."""
 
-    def __init__(self, lora, n: int, H: int, I: int, device, planes: int = 1):
+    def __init__(self, lora, n: int, H: int, I: int, device, planes: int = 1, prep: bool = True):
         self.scale = float(lora.scale)
         self.r = lora.r
         self.planes = planes
+        self.H, self.I = H, I
         e = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=device)
         self.fwd_gu, self.fwd_dn = e(n, 2 * I, EXT), e(n, H, EXT)
         self.a_gu, self.a_dn = e(planes, n, EXT, H), e(n, EXT, I)
         self.bt_dn, self.bt_gu = e(n, EXT, H), e(planes, n, EXT, 2 * I)
         self.at_gu, self.at_dn = e(n, planes, H, EXT), e(n, I, EXT)
-        P = [getattr(lora, k).detach().float().contiguous() for k in
-             ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")]
-        L.call("smel_lora_prep", *[L.ptr(p) for p in P], n, lora.r, planes, H, I, L.ptr(self.fwd_gu),
-               L.ptr(self.fwd_dn), L.ptr(self.a_gu), L.ptr(self.a_dn), L.ptr(self.bt_dn), L.ptr(self.bt_gu),
-               L.ptr(self.at_gu), L.ptr(self.at_dn), L.stream())
+        self.factors = [getattr(lora, k).detach().float().contiguous() for k in
+                        ("A_gate", "B_gate", "A_up", "B_up", "A_down", "B_down")]
+        self.n = n
+        if prep:
+            _prep_sets([self])
+
+    def lora_set(self) -> L.LoraSet:
+        s = L.LoraSet(*[L.ptr(p) for p in self.factors], self.n, self.r)
+        for k in ("fwd_gu", "fwd_dn", "a_gu", "a_dn", "bt_dn", "bt_gu", "at_gu", "at_dn"):
+            setattr(s, k, L.ptr(getattr(self, k)))
+        return s
+
+
+def _prep_sets(bufs) -> None:
+    """smel_lora_prep_sets: the bf16 layouts of one or two LoRA sets (same shapes and planes) in one launch."""
+    bufs = [b for b in bufs if b is not None]
+    if not bufs:
+        return
+    arr = (L.LoraSet * len(bufs))(*[b.lora_set() for b in bufs])
+    b0 = bufs[0]
+    L.call("smel_lora_prep_sets", arr, len(bufs), b0.planes, b0.H, b0.I, L.stream(), tag="smel_lora_prep")
 
 
 _PLANE_MAJOR = ("a_gu", "bt_gu")   # layouts with a leading plane dimension (lora_ext operands)
@@ -612,8 +630,9 @@ def _prep_lora(ex: LayerExperts, lora_ex, lora_sh, with_shared: bool, H: int, de
     use_ex = lora_ex if (lora_ex is not None and has_sel) else None
     use_sh = lora_sh if (lora_sh is not None and with_shared) else None
     planes = _lora_planes(use_ex, use_sh)
-    lb_ex = _LoRABufs(use_ex, len(ex._slot), H, I, dev, planes) if use_ex is not None else None
-    lb_sh = _LoRABufs(use_sh, 1, H, I, dev, planes) if use_sh is not None else None
+    lb_ex = _LoRABufs(use_ex, len(ex._slot), H, I, dev, planes, prep=False) if use_ex is not None else None
+    lb_sh = _LoRABufs(use_sh, 1, H, I, dev, planes, prep=False) if use_sh is not None else None
+    _prep_sets([lb_ex, lb_sh])   # both sets in one launch
     return lb_ex, lb_sh
 
 

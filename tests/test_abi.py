@@ -43,10 +43,11 @@ PROBE = r"""
 #include "smel_moe.h"
 #define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
 int main() {
-  printf("smel_wset %zu\nsmel_wg_dest %zu\nsmel_wg_job %zu\n", sizeof(smel_wset), sizeof(smel_wg_dest),
-         sizeof(smel_wg_job));
+  printf("smel_wset %zu\nsmel_wg_dest %zu\nsmel_wg_job %zu\nsmel_lora_set %zu\n", sizeof(smel_wset),
+         sizeof(smel_wg_dest), sizeof(smel_wg_job), sizeof(smel_lora_set));
   F(smel_wset, R) F(smel_wset, group) F(smel_wset, flags) F(smel_wg_dest, s_idx) F(smel_wg_dest, p0) F(smel_wg_dest, nq)
-  F(smel_wg_job, ldr) F(smel_wg_job, r_gather) F(smel_wg_job, Q) F(smel_wg_job, dest)
+  F(smel_wg_job, ldr) F(smel_wg_job, r_gather) F(smel_wg_job, Q) F(smel_wg_job, ldl) F(smel_wg_job, dest)
+  F(smel_lora_set, n) F(smel_lora_set, r) F(smel_lora_set, fwd_gu) F(smel_lora_set, at_dn)
   return 0;
 }
 """
@@ -67,7 +68,8 @@ def test_struct_layouts_match_header(tmp_path):
                     str(src), "-o", str(exe)], check=True, capture_output=True)
     got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
                                                        text=True).stdout.splitlines())
-    mirror = {"smel_wset": _lib.WSet, "smel_wg_dest": _lib.WgDest, "smel_wg_job": _lib.WgJob}
+    mirror = {"smel_wset": _lib.WSet, "smel_wg_dest": _lib.WgDest, "smel_wg_job": _lib.WgJob,
+              "smel_lora_set": _lib.LoraSet}
     for key, val in got.items():
         if "." in key:
             t, f = key.split(".")
