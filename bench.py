@@ -849,7 +849,9 @@ CE_SHAPE = dict(T=4092, H=2048, V=248320, token_chunk=1024, vocab_chunk=32768)
 
 def run_ce(args, dev):
     """chunked_ce (smel/loss.py:149-156) loss and gradient for one sequence of the Qwen3.6 shape: per vocabulary
-    chunk two library GEMMs (logits, p W) and the HIP online-softmax / accumulator kernels."""
+    chunk the logits GEMM with the online softmax in its epilogue (smel_ce_logits), the statistics fold
+    (smel_ce_stats) and the gradient GEMM p W (smel_ce_grad), both GEMMs on MFMA; the roofline line is the whole
+    step's MFMA rate, with each GEMM's own rate per launch beside it."""
     from smel import loss as LS
     c = CE_SHAPE
     T, H, V = c["T"], c["H"], c["V"]
@@ -867,9 +869,14 @@ def run_ce(args, dev):
     bd = breakdown_of(step, 2)
     ms = timing[1]
     flops = 4 * T * V * H                         # logits GEMM + gradient GEMM, 2 T V H each
-    roof = {"kernel": "whole step (library GEMMs + smel_ce_chunk_update / smel_ce_acc_update)", "bound": "mfma",
+    chunks, _ = head._kernel_chunks()
+    per_launch = 2 * T * V * H / len(chunks)      # one GEMM of one vocabulary chunk, averaged over the chunks
+    per_kernel = {k: round(per_launch / (bd[k] * 1e-3) / 1e12, 1) for k in ("smel_ce_logits", "smel_ce_grad")
+                  if k in bd}
+    roof = {"kernel": "whole step (smel_ce_logits + smel_ce_grad on MFMA, smel_ce_stats / _finish)", "bound": "mfma",
             "achieved": round(flops / (ms * 1e-3) / 1e12, 1), "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-            "frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4), "traffic": None, "flops_per_step": flops}
+            "frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4), "traffic": None, "flops_per_step": flops,
+            "per_launch_tflops": per_kernel}
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import loss_ref as LR

@@ -1,28 +1,481 @@
-// Single-pass chunked cross-entropy over a frozen lm_head (smel/loss.py:50-92): the per-chunk online softmax state
-// and the gradient terms, between the two GEMMs of each (token chunk, vocabulary chunk) step.
+// Single-pass chunked cross-entropy over a frozen lm_head (smel/loss.py:50-156), both GEMMs on MFMA.
 //
-//   ce_chunk_update  (one block per token row): z = cap(logit) (cap = c tanh(z / c), or none), chunk max cm,
-//                    new running max nm = max(m, cm), rescale r = exp(m - nm), softmax terms e = exp(z - nm),
-//                    s = s r + sum(e), p = e (1 - (z / c)^2 with the cap) written in the rows' dtype for the
-//                    gradient GEMM p W, and the target's capped logit and cap derivative when it lies in the chunk
-//                    (smel/loss.py:62-84; no host synchronisation: the reference's `inside.any()` / `nonzero`
-//                    become a comparison in the kernel)
-//   ce_acc_update    acc = acc r + (p W) (smel/loss.py:85): one pass over the fp32 accumulator, summing the parts of
-//                    the gradient GEMM in fixed order. The gradient GEMM p W has a long K (the vocabulary chunk) and
-//                    a small output ([tokens, H]: 32 tiles of 256 x 256 at 1024 tokens, too few for 256 CUs), so p is
-//                    written split into `parts` column slices [parts][n][vc / parts] and multiplied slice by slice
-//                    in one batched GEMM (a split K)
-// fp32 math; the GEMM outputs arrive rounded to the rows' dtype, as the reference's `(h @ W.t()).float()`.
-// 16-bit rows move through 16-byte loads and stores (8 values per thread and step) when the chunk allows it.
+// Per vocabulary chunk [v0, v0 + vc) and pass of n token rows:
+//   ce_logits  (MFMA, 256 vocabulary x 256 token tile): z = h W_c^T rounded to the rows' dtype (the reference's
+//              `(h @ W.t())`), capped (z -> c tanh(z / c)), and per window of 128 columns and token row the
+//              window's maximum rounded up to a whole power of two, e = ceil(max z * log2 e), the sum of
+//              exp(z - e ln 2) and the softmax terms p = exp(z - e ln 2) (times the cap derivative 1 - (z / c)^2) in
+//              the rows' dtype, [n][vc] row-major; the target's capped logit and cap derivative where the target
+//              lies in the tile. The logits never reach memory.
+//   ce_stats   per row: chunk maximum E = max e, chunk sum, the running maximum nE = max(m, E) and sum
+//              s = s 2^(m - nE) + sum_w s_w 2^(e_w - nE), the accumulator's rescale r = 2^(m - nE), and per window
+//              the shift nE - e_w of its softmax terms. Every rescale is an exact power of two.
+//   ce_grad    (MFMA, 256 hidden x 128 token tile, K = the chunk's columns): acc = r acc + sum_v p'_v W_v with
+//              p' = p 2^-(shift): each 16-byte fragment of p is shifted in registers as it leaves LDS (bf16: one
+//              saturating 16-bit subtract of the exponent per value pair; fp16 / fp32: ldexp), so the products are
+//              the reference's `p.to(h.dtype) @ W` terms at the running maximum (smel/loss.py:85).
+//   ce_finish  per row: loss = nE ln 2 + log s - z_target, gradient row = acc / s - d_target W[target]
+//              (smel/loss.py:87-92), scaled and stored in the requested dtype; ce_loss_sum adds the rows' losses
+//              in fixed order.
+// The head operand of ce_grad is the head transposed ([H][V], one copy per frozen head, made by ce_transpose), so
+// both GEMMs read K-contiguous rows. No atomics: every output element has one writer and fixed-order sums.
+#include <algorithm>
+
 #include "../../include/smel_loss.h"
 #include "abi_util.h"
 #include "common.h"
 
 namespace {
 
+constexpr int KB = 128;     // bytes of one k-step of an operand row: 64 16-bit or 32 fp32 values
+constexpr int WIN = 128;    // vocabulary columns of one statistics window
+constexpr int VT = 256;     // vocabulary columns of a logits tile (two windows)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+constexpr int SHIFT_ZERO = 255;   // a shift that turns every softmax term of the window into zero
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+template <int DT>
+constexpr int ebytes() {
+  return DT == 1 ? 4 : 2;
+}
+
+// One 16-byte chunk per lane of A and B into a 32x32 fp32 accumulator: 16-bit types in one 32x32x16 MFMA; fp32 in
+// four 32x32x2 MFMAs, the j-th value of both chunks in the j-th (the k order inside a chunk is the same for A and B).
+template <int DT>
+SMEL_DEV void mma(f32x16_t& c, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (DT == 0) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                0, 0, 0);
+  } else if constexpr (DT == 2) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                               0, 0);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[j]), __uint_as_float(b[j]), c, 0, 0, 0);
+  }
+}
+
+// fp32 value rounded to the rows' dtype and back (the reference's 16-bit GEMM output)
+template <int DT>
+SMEL_DEV float round_t(float v) {
+  if constexpr (DT == 0) return bf2f(f2bf(v));
+  else if constexpr (DT == 2) return (float)(_Float16)v;
+  else return v;
+}
+// two values in the rows' dtype, packed (16-bit) — fp32 keeps them apart
+SMEL_DEV uint32_t pack2h(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+// 16-byte chunk of softmax terms times 2^-sh (sh >= 0). bf16 (all terms are >= 0 and at most ~1): subtracting
+// sh << 7 from the bit pattern moves the exponent, exactly for every result in the normal range; the saturating
+// subtract turns a result below it into zero or a value under 2^-126. fp16 / fp32: ldexp, exact.
+// The results go to a separate vector: hipcc of ROCm 7.2 miscompiles an in-place update v[i] = f(bit_cast(v[i])) of
+// an ext-vector element in an unrolled loop (every later element got the first element's result).
+template <int DT>
+SMEL_DEV u32x4_t shift_chunk(const u32x4_t v, uint32_t sh) {
+  if (sh == 0) return v;
+  u32x4_t o;
+  if constexpr (DT == 0) {
+    const unsigned short d = (unsigned short)(sh << 7);
+    const u16x2_t dd = {d, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = v[i];
+      o[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2_t, x), dd));
+    }
+  } else if constexpr (DT == 2) {
+    const int e = -(int)sh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = v[i];
+      o[i] = pack2h(ldexpf(h_lo(x), e), ldexpf(h_hi(x), e));
+    }
+  } else {
+    const int e = -(int)sh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = v[i];
+      o[i] = __float_as_uint(ldexpf(__uint_as_float(x), e));
+    }
+  }
+  return o;
+}
+
+// ------------------------------------------------------------------------------------------------ GEMM main loop
+// C[i][j] += sum_k A[i][k] B[j][k] over one tile: A 256 rows, B 64 NB rows, both K-contiguous (row pitch in bytes
+// given by the caller's offsets). 4 waves: wave w computes A rows 128 (w & 1) + [0, 128) x B rows 32 NB (w >> 1) +
+// [0, 32 NB) as 4 x NB MFMA tiles of 32 x 32. Per k-step (128 bytes of every row) the operands go global -> LDS
+// directly (16-byte LDS-DMA loads, 1 KB per wave-load: 8 rows), into a ring of NST stages loaded NST - 1 steps
+// ahead; the 16-byte chunks of each 128-byte LDS row are XOR-swizzled (chunk c of row r at c ^ swz(r)), so the
+// fragment reads of 32 consecutive rows hit distinct banks. Lane half h carries chunk 4 h + s of substep s, for A
+// and B alike.
+template <int NB, int NST>
+struct Ring {
+  static constexpr int A_BYTES = 256 * KB, B_BYTES = 64 * NB * KB, STAGE = A_BYTES + B_BYTES, BYTES = NST * STAGE;
+  static constexpr int VM_A = 256 / 8 / 4, VM_B = 64 * NB / 8 / 4;   // wave-loads per wave and stage
+  static constexpr int VM_STEP = VM_A + VM_B;
+};
+
+// Lane row and swizzled chunk of wave-load ii (of a wave whose loads start at group g0 = VM * w, an even number):
+// row 8 (g0 + ii) + lane / 8, logical chunk (lane % 8) ^ swz(row) = (lane % 8) ^ (lane / 8) ^ (ii % 2).
+SMEL_DEV uint32_t ld_chunk_bytes(int lane, int ii) { return 16u * (uint32_t)((lane & 7) ^ (lane >> 3) ^ (ii & 1)); }
+
+// Row offsets (bytes from the operand base) of this lane's wave-loads, OOB for rows at or past `valid`.
+template <int VM>
+SMEL_DEV void row_offsets(uint32_t (&off)[VM], int w, int lane, int valid, uint32_t pitch_bytes) {
+#pragma unroll
+  for (int ii = 0; ii < VM; ++ii) {
+    const int row = 8 * (VM * w + ii) + (lane >> 3);
+    off[ii] = row < valid ? (uint32_t)row * pitch_bytes : OOB;
+  }
+}
+
+// The main loop over kbytes (a multiple of 16) of every row. `pre(j)` runs for step j + 1 before that step's
+// operand loads are issued (it may issue its own loads: they retire before the next step's wait); `fix(n, j, v)`
+// transforms a B fragment of tile column n in step j as it leaves LDS.
+template <int DT, int NB, int NST, class Pre, class Fix>
+SMEL_DEV void nt_loop(f32x16_t (&acc)[4][NB], uint8_t* smem, rsrc_t ra, const uint32_t (&aoff)[Ring<NB, NST>::VM_A],
+                      rsrc_t rb, const uint32_t (&boff)[Ring<NB, NST>::VM_B], int kbytes, Pre&& pre, Fix&& fix) {
+  using R = Ring<NB, NST>;
+  const int lane = lane_id(), h = lane >> 5, r32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = w & 1, wn = w >> 1;
+  const uint32_t cb0 = ld_chunk_bytes(lane, 0), cb1 = ld_chunk_bytes(lane, 1);
+  const int nk = (kbytes + KB - 1) / KB;
+  auto issue = [&](int j) {
+    uint8_t* S = smem + (j % NST) * R::STAGE;
+    const uint32_t k0 = (uint32_t)j * KB;
+    const bool tail = (int)k0 + KB > kbytes;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ii = 0; ii < R::VM_A; ++ii) {
+      const uint32_t cb = (ii & 1) ? cb1 : cb0;
+      const bool ok = !tail || (int)(k0 + cb) + 16 <= kbytes;
+      ld16_lds(ra, S + (R::VM_A * w + ii) * 1024, ok ? aoff[ii] + k0 + cb : OOB);
+    }
+#pragma unroll
+    for (int ii = 0; ii < R::VM_B; ++ii) {
+      const uint32_t cb = (ii & 1) ? cb1 : cb0;
+      const bool ok = !tail || (int)(k0 + cb) + 16 <= kbytes;
+      ld16_lds(rb, S + R::A_BYTES + (R::VM_B * w + ii) * 1024, ok ? boff[ii] + k0 + cb : OOB);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // fragment read offsets inside a stage: substep s reads logical chunk 4 h + s of its rows
+  uint32_t pcb[4];
+  const int sw = swz(r32);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) pcb[s] = (uint32_t)r32 * KB + 16u * (uint32_t)((4 * h + s) ^ sw);
+  pre(-1);
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nk) issue(s);
+  for (int j = 0; j < nk; ++j) {
+    if (j + NST - 2 < nk) wait_vm<(NST - 2) * R::VM_STEP>();
+    else wait_vm<0>();
+    __syncthreads();
+    if (j + 1 < nk) pre(j);
+    if (j + NST - 1 < nk) issue(j + NST - 1);
+    const uint8_t* A = smem + (j % NST) * R::STAGE + wm * 128 * KB;
+    const uint8_t* B = smem + (j % NST) * R::STAGE + R::A_BYTES + wn * 32 * NB * KB;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t af[4], bf[NB];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) af[m] = *reinterpret_cast<const u32x4_t*>(A + m * 32 * KB + pcb[s]);
+#pragma unroll
+      for (int n = 0; n < NB; ++n) bf[n] = fix(n, j, *reinterpret_cast<const u32x4_t*>(B + n * 32 * KB + pcb[s]));
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) mma<DT>(acc[m][n], af[m], bf[n]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ ce_logits
+struct LogitsArgs {
+  const void* W;        // head rows of the chunk (row 0 = vocabulary id v0), pitch ldw elements
+  const void* h;        // token rows, pitch ldh elements
+  const int64_t* tgt;   // target id per token row
+  void* P;              // softmax terms [n][ldp] in the rows' dtype, or null (statistics only)
+  float *win_e, *win_s; // [nwin][ldn] window maxima (power-of-two exponents) and sums
+  float *tz, *td;       // target logit and cap derivative per row (written where the target lies in the chunk)
+  int64_t ldw, ldh, ldp, ldn, v0;
+  int vc, n, K;         // chunk columns, token rows, hidden size
+  float cap;
+  int n_vt, n_tt;       // 256-column vocabulary tiles, 256-row token tiles
+};
+
+template <int DT, bool CAP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void ce_logits_kernel(LogitsArgs a) {
+  using R = Ring<4, 2>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES];
+  // blocks b, b + 8, ... run on one XCD: it takes vocabulary tiles x, x + 8, ... with all token tiles of each in a
+  // row, so one vocabulary tile's head rows are read from that XCD's L2 by all its token tiles
+  const int b = blockIdx.x, x = b % NXCD, jj = b / NXCD;
+  const int tt = jj % a.n_tt, vt = (jj / a.n_tt) * NXCD + x;
+  if (vt >= a.n_vt) return;
+  constexpr int E = ebytes<DT>();
+  const int lane = lane_id(), h = lane >> 5, r32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = w & 1, wn = w >> 1;
+  const int a0 = vt * VT, b0 = tt * 256;
+  const int kbytes = a.K * E;
+  const int a_valid = min(VT, a.vc - a0), b_valid = min(256, a.n - b0);
+  const rsrc_t ra = make_rsrc(static_cast<const uint8_t*>(a.W) + (int64_t)a0 * a.ldw * E,
+                              (uint64_t)(a_valid - 1) * a.ldw * E + kbytes);
+  const rsrc_t rb = make_rsrc(static_cast<const uint8_t*>(a.h) + (int64_t)b0 * a.ldh * E,
+                              (uint64_t)(b_valid - 1) * a.ldh * E + kbytes);
+  uint32_t aoff[R::VM_A], boff[R::VM_B];
+  row_offsets(aoff, w, lane, a_valid, (uint32_t)(a.ldw * E));
+  row_offsets(boff, w, lane, b_valid, (uint32_t)(a.ldh * E));
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[m][n] = f32x16_t{};
+  nt_loop<DT, 4, 2>(acc, smem, ra, aoff, rb, boff, kbytes, [](int) {},
+                    [](int, int, const u32x4_t& v) { return v; });
+  __syncthreads();   // every wave is done with the operand ring: the epilogue may use the LDS
+
+  // ---- epilogue. acc[m][n][r] = z at vocabulary column c0 + 32 m + 8 (r / 4) + 4 h + r % 4 of token row
+  // b0 + 128 wn + 32 n + r32: each token row's 128 columns of this wave (one window) are 64 values in this lane and
+  // 64 in lane ^ 32.
+  const int c0 = a0 + 128 * wm;              // first chunk column of the window
+  const int win = vt * 2 + wm;
+  const int ncol = a.vc - c0;                // valid columns of the window (may be <= 0 or > 128)
+  const float cap = a.cap;
+  const float inv_cap = cap != 0.f ? 1.f / cap : 0.f;
+  auto col_of = [&](int m, int r) { return 32 * m + 8 * (r >> 2) + 4 * h + (r & 3); };
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int tok = b0 + 128 * wn + 32 * n + r32;
+    const bool tok_ok = tok < a.n;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float z = round_t<DT>(acc[m][n][r]);
+        if constexpr (CAP) z = cap * tanhf(z * inv_cap);
+        if (ncol < 128 && col_of(m, r) >= ncol) z = -INFINITY;
+        acc[m][n][r] = z;
+        mx = fmaxf(mx, z);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float e = mx == -INFINITY ? -INFINITY : ceilf(mx * LOG2E);
+    const float ne = mx == -INFINITY ? 0.f : -e;
+    float sum = 0.f;
+    uint8_t* prow = a.P ? static_cast<uint8_t*>(a.P) + ((int64_t)tok * a.ldp + c0) * E : nullptr;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float z = acc[m][n][4 * q + i];
+          const bool live = z != -INFINITY;
+          const float ez = live ? __builtin_amdgcn_exp2f(fmaf(z, LOG2E, ne)) : 0.f;
+          sum += ez;
+          p[i] = CAP && live ? ez * (1.f - (z * inv_cap) * (z * inv_cap)) : ez;
+        }
+        if (prow && tok_ok) {
+          uint8_t* dst = prow + (32 * m + 8 * q + 4 * h) * E;
+          if constexpr (DT == 0) {
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2bf(p[0], p[1]), pack2bf(p[2], p[3])};
+          } else if constexpr (DT == 2) {
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2h(p[0], p[1]), pack2h(p[2], p[3])};
+          } else {
+            *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{p[0], p[1], p[2], p[3]};
+          }
+        }
+      }
+    sum += __shfl_xor(sum, 32, 64);
+    if (h == 0 && tok_ok) {
+      a.win_e[(int64_t)win * a.ldn + tok] = e;
+      a.win_s[(int64_t)win * a.ldn + tok] = sum;
+    }
+    // the target: at most one window of the whole vocabulary holds it; a wave with such a row puts its capped
+    // logits of this slice in LDS ([32 rows][129], free after the main loop) and the row's lane h = 0 reads its one
+    const int64_t tc64 = tok_ok ? a.tgt[tok] - a.v0 - c0 : -1;
+    const bool here = tc64 >= 0 && tc64 < 128 && tc64 < ncol;
+    if (__builtin_amdgcn_ballot_w64(here)) {
+      float* zb = reinterpret_cast<float*>(smem) + w * (32 * 129) + r32 * 129;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) zb[col_of(m, r)] = acc[m][n][r];
+      __builtin_amdgcn_wave_barrier();
+      const bool mine = here && h == 0;
+      const float zt = mine ? zb[(int)tc64] : 0.f;
+      __builtin_amdgcn_wave_barrier();
+      if (mine) {
+        a.tz[tok] = zt;
+        a.td[tok] = CAP ? 1.f - (zt * inv_cap) * (zt * inv_cap) : 1.f;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ ce_grad
+struct GradArgs {
+  const void* WT;        // transposed head [H][ldwt], column 0 = vocabulary id v0 of the chunk
+  const void* P;         // softmax terms [n][ldp]
+  const uint8_t* shift;  // [nwin][ldn]
+  const float* r;        // accumulator rescale per row
+  float* acc;            // [n][H] fp32
+  int64_t ldwt, ldp, ldn;
+  int H, n, kbytes, first;
+  int n_ht, n_tt;        // 256-row hidden tiles, 128-row token tiles
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void ce_grad_kernel(GradArgs a) {
+  using R = Ring<2, 3>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES];
+  // XCD x takes a contiguous run of the tile list (token-major): the hidden tiles of one token tile run side by
+  // side on one XCD and read that token tile's softmax terms from its L2
+  const int n_tiles = a.n_ht * a.n_tt;
+  int tile, unused;
+  if (!xcd_tile_chunk(n_tiles, 1, tile, unused)) return;
+  const int tt = tile / a.n_ht, ht = tile % a.n_ht;
+  constexpr int E = ebytes<DT>();
+  const int lane = lane_id(), h = lane >> 5, r32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = w & 1, wn = w >> 1;
+  const int a0 = ht * 256, b0 = tt * 128;
+  const int a_valid = min(256, a.H - a0), b_valid = min(128, a.n - b0);
+  const rsrc_t ra = make_rsrc(static_cast<const uint8_t*>(a.WT) + (int64_t)a0 * a.ldwt * E,
+                              (uint64_t)(a_valid - 1) * a.ldwt * E + a.kbytes);
+  const rsrc_t rb = make_rsrc(static_cast<const uint8_t*>(a.P) + (int64_t)b0 * a.ldp * E,
+                              (uint64_t)(b_valid - 1) * a.ldp * E + a.kbytes);
+  uint32_t aoff[R::VM_A], boff[R::VM_B];
+  row_offsets(aoff, w, lane, a_valid, (uint32_t)(a.ldwt * E));
+  row_offsets(boff, w, lane, b_valid, (uint32_t)(a.ldp * E));
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) acc[m][n] = f32x16_t{};
+  // shifts of this lane's two token rows: the window of step j is j * KB / (WIN * E)
+  constexpr int STEPS_PER_WIN = WIN * E / KB;
+  const int tok0 = b0 + 64 * wn + r32;
+  uint32_t sh_cur[2] = {0, 0}, sh_next[2] = {0, 0};
+  auto load_sh = [&](int win, uint32_t (&dst)[2]) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int tok = tok0 + 32 * n;
+      dst[n] = tok < a.n ? (uint32_t)a.shift[(int64_t)win * a.ldn + tok] : (uint32_t)SHIFT_ZERO;
+    }
+  };
+  auto pre = [&](int j) {   // j = -1: before the first step; else during step j, for step j + 1
+    if (j < 0) {
+      load_sh(0, sh_cur);
+    } else if ((j + 1) % STEPS_PER_WIN == 0) {
+      load_sh((j + 1) / STEPS_PER_WIN, sh_next);
+    }
+  };
+  int cur_win = 0;
+  auto fix = [&](int n, int j, const u32x4_t& v) {
+    const int wj = j / STEPS_PER_WIN;
+    if (n == 0 && wj != cur_win) {
+      cur_win = wj;
+      sh_cur[0] = sh_next[0];
+      sh_cur[1] = sh_next[1];
+    }
+    return shift_chunk<DT>(v, sh_cur[n]);
+  };
+  nt_loop<DT, 2, 3>(acc, smem, ra, aoff, rb, boff, a.kbytes, pre, fix);
+
+  // ---- epilogue: acc[m][n][r] = term of hidden column a0 + 128 wm + 32 m + 8 (r / 4) + 4 h + r % 4 and token
+  // row tok0 + 32 n: 16-byte runs of 4 columns, added to r acc (or written on the first chunk)
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const int tok = tok0 + 32 * n;
+    if (tok >= a.n) continue;
+    const float rr = a.first ? 0.f : a.r[tok];
+    float* row = a.acc + (int64_t)tok * a.H;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = a0 + 128 * wm + 32 * m + 8 * q + 4 * h;
+        if (col >= a.H) continue;
+        f32x4_t* dst = reinterpret_cast<f32x4_t*>(row + col);
+        f32x4_t v = {acc[m][n][4 * q], acc[m][n][4 * q + 1], acc[m][n][4 * q + 2], acc[m][n][4 * q + 3]};
+        if (!a.first) {
+          const f32x4_t o = *dst;
+          v = f32x4_t{fmaf(o[0], rr, v[0]), fmaf(o[1], rr, v[1]), fmaf(o[2], rr, v[2]), fmaf(o[3], rr, v[3])};
+        }
+        *dst = v;
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ small kernels
+__global__ __launch_bounds__(256) void ce_begin_kernel(float* m, float* s, float* tz, float* td, const float* m0,
+                                                       int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  m[i] = m0 ? m0[i] : -INFINITY;
+  s[i] = 0.f;
+  tz[i] = 0.f;
+  td[i] = 1.f;
+}
+
+SMEL_DEV float pow2i(float e) { return ldexpf(1.f, (int)e); }
+
+// 64 rows per block, 4 threads per row (windows w = q mod 4), partial results combined in fixed order
+__global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__ win_e, const float* __restrict__ win_s,
+                                                       int nwin, int64_t ldn, int64_t n, float* m, float* s,
+                                                       uint8_t* shift, float* r_out) {
+  __shared__ float red[4][64];
+  const int q = threadIdx.x >> 6, t = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 64 + t;
+  const bool ok = row < n;
+  float E = -INFINITY;
+  if (ok)
+    for (int w = q; w < nwin; w += 4) E = fmaxf(E, win_e[(int64_t)w * ldn + row]);
+  red[q][t] = E;
+  __syncthreads();
+  E = fmaxf(fmaxf(red[0][t], red[1][t]), fmaxf(red[2][t], red[3][t]));
+  __syncthreads();
+  const float mo = ok ? m[row] : -INFINITY;
+  const float nE = fmaxf(mo, E);   // finite: every chunk has a valid column
+  float S = 0.f;
+  if (ok)
+    for (int w = q; w < nwin; w += 4) {
+      const float e = win_e[(int64_t)w * ldn + row];
+      int sh = SHIFT_ZERO;
+      if (e != -INFINITY) {
+        const float d = nE - e;
+        sh = d < (float)SHIFT_ZERO ? (int)d : SHIFT_ZERO;
+        S += ldexpf(win_s[(int64_t)w * ldn + row], -(int)fminf(d, 300.f));
+      }
+      shift[(int64_t)w * ldn + row] = (uint8_t)sh;
+    }
+  red[q][t] = S;
+  __syncthreads();
+  if (q == 0 && ok) {
+    S = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+    const float r = mo == -INFINITY ? 0.f : ldexpf(1.f, -(int)fminf(nE - mo, 300.f));
+    s[row] = s[row] * r + S;
+    m[row] = nE;
+    r_out[row] = r;
+  }
+}
+
 template <int DT>
 SMEL_DEV float ld_t(const void* p, int64_t i) {
-  if constexpr (DT == 0) return __uint_as_float((uint32_t) static_cast<const uint16_t*>(p)[i] << 16);
+  if constexpr (DT == 0) return bf2f(static_cast<const uint16_t*>(p)[i]);
   else if constexpr (DT == 1) return static_cast<const float*>(p)[i];
   else return (float)static_cast<const _Float16*>(p)[i];
 }
@@ -33,197 +486,259 @@ SMEL_DEV void st_t(void* p, int64_t i, float v) {
   else static_cast<_Float16*>(p)[i] = (_Float16)v;
 }
 
-SMEL_DEV float capf(float z, float c) { return c != 0.f ? c * tanhf(z / c) : z; }
-
-// block-wide reduction of 256 threads: fixed order (xor butterfly per wave, then the four wave values in order)
-template <bool MAX>
-SMEL_DEV float block_reduce(float v, float* red) {
-  for (int o = 1; o < 64; o <<= 1) {
-    const float u = __shfl_xor(v, o, 64);
-    v = MAX ? fmaxf(v, u) : v + u;
-  }
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return MAX ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : ((red[0] + red[1]) + red[2]) + red[3];
-}
-
-// 8 values of a 16-bit row from one 16-byte load
-template <int DT>
-SMEL_DEV void ld8(const void* p, int64_t i, float v[8]) {
-  const u32x4_t q = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[2 * k] = DT == 0 ? bf_lo(q[k]) : h_lo(q[k]);
-    v[2 * k + 1] = DT == 0 ? bf_hi(q[k]) : h_hi(q[k]);
-  }
-}
-
-// VEC: 16-bit rows whose chunk width, row stride and base pointers are multiples of 8 elements / 16 bytes
-template <int DT, bool VEC>
-__global__ __launch_bounds__(256) void ce_chunk_update_kernel(const void* __restrict__ lg, int64_t ld, int vc,
-                                                              int64_t v0, const int64_t* __restrict__ tgt, float cap,
-                                                              int need_grad, float* m, float* s, float* tgt_logit,
-                                                              float* tgt_d, void* p, float* r_out, int64_t n, int sw) {
-  __shared__ float red[4];
+// one block per row: loss and (with acc) the gradient row; trows (optional) holds the target rows already in the
+// rows' dtype, else they are read from W at the target id
+template <int DT, int GT>
+__global__ __launch_bounds__(256) void ce_finish_kernel(const float* __restrict__ m, const float* __restrict__ s,
+                                                        const float* __restrict__ tz, const float* __restrict__ td,
+                                                        const float* __restrict__ acc, const void* __restrict__ W,
+                                                        int64_t ldw, const void* __restrict__ trows,
+                                                        const int64_t* __restrict__ tgt, int64_t V, int64_t H,
+                                                        float gscale, void* g, int64_t ldg, float* loss_rows) {
   const int64_t row = blockIdx.x;
-  const int64_t base = row * ld;
-  // p in the split layout [vc / sw][n][sw]: column j of the row goes to part j / sw, column j % sw
-  auto p_at = [&](int j) { return (int64_t)(j / sw) * n * sw + row * (int64_t)sw + (j % sw); };
-  float cm = -INFINITY;
-  if constexpr (VEC) {
-    for (int c = threadIdx.x; c < vc / 8; c += 256) {
-      float v[8];
-      ld8<DT>(lg, base + 8 * c, v);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) cm = fmaxf(cm, capf(v[k], cap));
-    }
-  } else {
-    for (int j = threadIdx.x; j < vc; j += 256) cm = fmaxf(cm, capf(ld_t<DT>(lg, base + j), cap));
-  }
-  cm = block_reduce<true>(cm, red);
-  const float m_old = m[row];
-  const float nm = fmaxf(m_old, cm);
-  const float r = expf(m_old - nm);   // exp(-inf) = 0 on the first chunk
-  float sum = 0.f;
-  if constexpr (VEC) {
-    for (int c = threadIdx.x; c < vc / 8; c += 256) {
-      float v[8];
-      ld8<DT>(lg, base + 8 * c, v);
-      uint32_t o[4];
-#pragma unroll
-      for (int k = 0; k < 8; k += 2) {
-        float q2[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const float z = capf(v[k + u], cap);
-          const float e = expf(z - nm);
-          sum += e;
-          q2[u] = cap != 0.f ? e * (1.f - (z / cap) * (z / cap)) : e;
-        }
-        o[k / 2] = DT == 0 ? pack2bf(q2[0], q2[1])
-                           : (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q2[0]) |
-                                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q2[1]) << 16);
-      }
-      if (need_grad)
-        *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p) + p_at(8 * c)) =
-            u32x4_t{o[0], o[1], o[2], o[3]};
-    }
-  } else {
-    for (int j = threadIdx.x; j < vc; j += 256) {
-      const float z = capf(ld_t<DT>(lg, base + j), cap);
-      const float e = expf(z - nm);
-      sum += e;
-      if (need_grad) {
-        const float q = cap != 0.f ? e * (1.f - (z / cap) * (z / cap)) : e;
-        st_t<DT>(p, p_at(j), q);
-      }
-    }
-  }
-  sum = block_reduce<false>(sum, red);
-  if (threadIdx.x == 0) {
-    s[row] = s[row] * r + sum;
-    m[row] = nm;
-    r_out[row] = r;
-    const int64_t t = tgt[row] - v0;
-    if (t >= 0 && t < vc) {
-      const float z = capf(ld_t<DT>(lg, base + t), cap);
-      tgt_logit[row] = z;
-      if (cap != 0.f) tgt_d[row] = 1.f - (z / cap) * (z / cap);
-    }
+  const float sr = s[row];
+  const int64_t t = tgt[row];
+  const bool ok = t >= 0 && t < V;
+  if (threadIdx.x == 0) loss_rows[row] = (m[row] * LN2 + logf(sr)) - tz[row];
+  if (!acc) return;
+  const float inv = 1.f / sr, d = ok ? td[row] : 0.f;
+  const void* wsrc = trows ? trows : W;
+  const int64_t wrow = trows ? row * H : (ok ? t : 0) * ldw;
+  for (int64_t c = threadIdx.x; c < H; c += 256) {
+    const float wv = ok ? ld_t<DT>(wsrc, wrow + c) : 0.f;
+    const float v = acc[row * H + c] * inv - d * wv;
+    st_t<GT>(g, row * ldg + c, v * gscale);
   }
 }
 
-template <int DT>
-__global__ __launch_bounds__(256) void ce_acc_update_kernel(float* __restrict__ acc, const float* __restrict__ r,
-                                                            const void* __restrict__ pw, int64_t n, int64_t H,
-                                                            int parts) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n * H) return;
-  float v = ld_t<DT>(pw, i);
-  for (int k = 1; k < parts; ++k) v += ld_t<DT>(pw, (int64_t)k * n * H + i);   // the split products, in order
-  acc[i] = acc[i] * r[i / H] + v;
+// total (+)= scale * sum of the rows' losses, in fixed order (one block)
+__global__ __launch_bounds__(256) void ce_loss_sum_kernel(const float* __restrict__ loss_rows, int64_t n, float scale,
+                                                          int accumulate, float* total) {
+  __shared__ float red[256];
+  float v = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 256) v += loss_rows[i];
+  red[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *total = (accumulate ? *total : 0.f) + red[0] * scale;
 }
 
-// the same for 16-bit products with H % 8 == 0 and 16-byte aligned buffers: 8 elements per thread
+// x *= *go for n values of the rows' dtype (the backward's incoming gradient, a device scalar)
 template <int DT>
-__global__ __launch_bounds__(256) void ce_acc_update8_kernel(float* __restrict__ acc, const float* __restrict__ r,
-                                                             const void* __restrict__ pw, int64_t n, int64_t H,
-                                                             int parts) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-  if (i >= n * H) return;
-  float v[8];
-  ld8<DT>(pw, i, v);
-  for (int k = 1; k < parts; ++k) {
-    float u[8];
-    ld8<DT>(pw, (int64_t)k * n * H + i, u);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] += u[e];
+__global__ __launch_bounds__(256) void ce_scale_kernel(void* x, int64_t n, const float* __restrict__ go) {
+  const float f = *go;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    st_t<DT>(x, i, ld_t<DT>(x, i) * f);
+}
+
+// dst [C][ldd] = src [R][C] (pitch lds) transposed, 64 x 64 tiles through LDS; dst columns R .. ldd - 1 zeroed
+template <int E>
+__global__ __launch_bounds__(256) void ce_transpose_kernel(const uint8_t* __restrict__ src, int64_t R, int64_t C,
+                                                           int64_t lds, uint8_t* __restrict__ dst, int64_t ldd) {
+  __shared__ uint8_t tile[64][64 * E + 4];
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int rr = i / 64, cc = i % 64;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    uint8_t* t = &tile[rr][cc * E];
+    if (r < R && c < C) {
+      for (int b = 0; b < E; ++b) t[b] = src[(r * lds + c) * E + b];
+    } else {
+      for (int b = 0; b < E; ++b) t[b] = 0;
+    }
   }
-  const float rr = r[i / H];
-  f32x4_t* const a4 = reinterpret_cast<f32x4_t*>(acc + i);
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const f32x4_t a = a4[h];
-    a4[h] = f32x4_t{a[0] * rr + v[4 * h], a[1] * rr + v[4 * h + 1], a[2] * rr + v[4 * h + 2], a[3] * rr + v[4 * h + 3]};
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int cc = i / 64, rr = i % 64;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    if (c < C && r < ldd)
+      for (int b = 0; b < E; ++b) dst[(c * ldd + r) * E + b] = tile[rr][cc * E + b];
   }
 }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
-extern "C" int smel_ce_chunk_update(const void* logits, int64_t n, int64_t vc, int64_t ld, int64_t v0,
-                                    const int64_t* tgt, float softcap, int32_t dtype, int32_t need_grad, float* m,
-                                    float* s, float* tgt_logit, float* tgt_d, void* p, int32_t p_parts, float* r,
-                                    hipStream_t stream) {
-  SMEL_REQUIRE(p_parts >= 1 && vc % p_parts == 0, SMEL_EINVAL, "ce_chunk_update: %d parts do not divide %lld columns",
-               p_parts, (long long)vc);
-  SMEL_REQUIRE(n >= 0 && vc >= 1 && vc <= INT32_MAX && ld >= vc, SMEL_EINVAL,
-               "ce_chunk_update: bad sizes n=%lld vc=%lld ld=%lld", (long long)n, (long long)vc, (long long)ld);
-  SMEL_REQUIRE(dtype >= 0 && dtype <= 2, SMEL_EINVAL, "ce_chunk_update: dtype %d (0 bf16, 1 fp32, 2 fp16)", dtype);
-  SMEL_REQUIRE(n < (int64_t)1 << 31, SMEL_EUNSUPPORTED, "ce_chunk_update: %lld rows", (long long)n);
+// ------------------------------------------------------------------------------------------------ C-ABI
+#define SMEL_DT_OK(dt) ((dt) >= 0 && (dt) <= 2)
+
+extern "C" int smel_ce_begin(float* m, float* s, float* tz, float* td, const float* m0, int64_t n,
+                             hipStream_t stream) {
+  SMEL_REQUIRE(n >= 0, SMEL_EINVAL, "ce_begin: n=%lld", (long long)n);
   if (n == 0) return 0;
-  SMEL_REQUIRE(logits && tgt && m && s && tgt_logit && tgt_d && r && (!need_grad || p), SMEL_EINVAL,
-               "ce_chunk_update: null pointer");
-  const dim3 g((unsigned)n), b(256);
-  const int sw = (int)(vc / p_parts);
-  const bool vec = dtype != 1 && sw % 8 == 0 && ld % 8 == 0 && (uintptr_t)logits % 16 == 0 &&
-                   (!need_grad || (uintptr_t)p % 16 == 0);
-#define SMEL_CE_LAUNCH(D, V)                                                                                     \
-  ce_chunk_update_kernel<D, V><<<g, b, 0, stream>>>(logits, ld, (int)vc, v0, tgt, softcap, need_grad, m, s, tgt_logit, \
-                                                    tgt_d, p, r, n, sw)
-  if (dtype == 0 && vec)
-    SMEL_CE_LAUNCH(0, true);
-  else if (dtype == 0)
-    SMEL_CE_LAUNCH(0, false);
-  else if (dtype == 2 && vec)
-    SMEL_CE_LAUNCH(2, true);
-  else if (dtype == 2)
-    SMEL_CE_LAUNCH(2, false);
-  else
-    SMEL_CE_LAUNCH(1, false);
-#undef SMEL_CE_LAUNCH
+  SMEL_REQUIRE(m && s && tz && td, SMEL_EINVAL, "ce_begin: null pointer");
+  ce_begin_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(m, s, tz, td, m0, n);
   return smel::launch_status();
 }
 
-extern "C" int smel_ce_acc_update(float* acc, const float* r, const void* pw, int32_t parts, int64_t n, int64_t H,
-                                  int32_t dtype, hipStream_t stream) {
-  SMEL_REQUIRE(n >= 0 && H >= 1 && parts >= 1, SMEL_EINVAL, "ce_acc_update: bad sizes");
-  SMEL_REQUIRE(dtype >= 0 && dtype <= 2, SMEL_EINVAL, "ce_acc_update: dtype %d", dtype);
+extern "C" int smel_ce_logits(const void* W, int64_t ldw, int64_t vc, int64_t v0, const void* h, int64_t ldh,
+                              int64_t n, int64_t H, const int64_t* tgt, float softcap, int32_t dtype, void* P,
+                              int64_t ldp, float* win_e, float* win_s, int64_t ldn, float* tz, float* td,
+                              hipStream_t stream) {
+  SMEL_REQUIRE(SMEL_DT_OK(dtype), SMEL_EINVAL, "ce_logits: dtype %d (0 bf16, 1 fp32, 2 fp16)", dtype);
+  const int E = dtype == 1 ? 4 : 2;
+  SMEL_REQUIRE(n >= 0 && vc >= 1 && H >= 1 && v0 >= 0, SMEL_EINVAL, "ce_logits: bad sizes n=%lld vc=%lld H=%lld",
+               (long long)n, (long long)vc, (long long)H);
   if (n == 0) return 0;
-  SMEL_REQUIRE(acc && r && pw, SMEL_EINVAL, "ce_acc_update: null pointer");
-  const bool vec = dtype != 1 && H % 8 == 0 && (uintptr_t)acc % 16 == 0 && (uintptr_t)pw % 16 == 0;
-  const int64_t blocks = vec ? (n * H / 8 + 255) / 256 : (n * H + 255) / 256;
-  SMEL_REQUIRE(blocks < (int64_t)1 << 31, SMEL_EUNSUPPORTED, "ce_acc_update: too large");
+  SMEL_REQUIRE(W && h && tgt && win_e && win_s && tz && td, SMEL_EINVAL, "ce_logits: null pointer");
+  SMEL_REQUIRE((H * E) % 16 == 0 && (ldw * E) % 16 == 0 && (ldh * E) % 16 == 0 && ldw >= H && ldh >= H &&
+                   aligned16(W) && aligned16(h),
+               SMEL_EUNSUPPORTED, "ce_logits: rows must be 16-byte aligned runs (H=%lld, ldw=%lld, ldh=%lld)",
+               (long long)H, (long long)ldw, (long long)ldh);
+  const int64_t vcp = (vc + VT - 1) / VT * VT;
+  SMEL_REQUIRE(!P || (ldp >= vcp && (ldp * E) % 16 == 0 && aligned16(P)), SMEL_EINVAL,
+               "ce_logits: softmax rows need %lld columns, 16-byte aligned (ldp=%lld)", (long long)vcp, (long long)ldp);
+  SMEL_REQUIRE(ldn >= n, SMEL_EINVAL, "ce_logits: statistics pitch %lld < %lld rows", (long long)ldn, (long long)n);
+  SMEL_REQUIRE((ldw * E) * 256 < ((int64_t)1 << 31) && (ldh * E) * 256 < ((int64_t)1 << 31) && vc < INT32_MAX &&
+                   n < INT32_MAX,
+               SMEL_EUNSUPPORTED, "ce_logits: tile offsets exceed 31 bits");
+  LogitsArgs a;
+  a.W = W;
+  a.h = h;
+  a.tgt = tgt;
+  a.P = P;
+  a.win_e = win_e;
+  a.win_s = win_s;
+  a.tz = tz;
+  a.td = td;
+  a.ldw = ldw;
+  a.ldh = ldh;
+  a.ldp = ldp;
+  a.ldn = ldn;
+  a.v0 = v0;
+  a.vc = (int)vc;
+  a.n = (int)n;
+  a.K = (int)H;
+  a.cap = softcap;
+  a.n_vt = (int)(vcp / VT);
+  a.n_tt = (int)((n + 255) / 256);
+  const int64_t blocks = xcd_grid(a.n_vt) * a.n_tt;
+  SMEL_REQUIRE(blocks < INT32_MAX, SMEL_EUNSUPPORTED, "ce_logits: grid too large");
   const dim3 g((unsigned)blocks), b(256);
-  if (vec && dtype == 0)
-    ce_acc_update8_kernel<0><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
-  else if (vec)
-    ce_acc_update8_kernel<2><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
-  else if (dtype == 0)
-    ce_acc_update_kernel<0><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
-  else if (dtype == 1)
-    ce_acc_update_kernel<1><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
-  else
-    ce_acc_update_kernel<2><<<g, b, 0, stream>>>(acc, r, pw, n, H, parts);
+  const bool cap = softcap != 0.f;
+  if (dtype == 0 && cap) ce_logits_kernel<0, true><<<g, b, 0, stream>>>(a);
+  else if (dtype == 0) ce_logits_kernel<0, false><<<g, b, 0, stream>>>(a);
+  else if (dtype == 1 && cap) ce_logits_kernel<1, true><<<g, b, 0, stream>>>(a);
+  else if (dtype == 1) ce_logits_kernel<1, false><<<g, b, 0, stream>>>(a);
+  else if (cap) ce_logits_kernel<2, true><<<g, b, 0, stream>>>(a);
+  else ce_logits_kernel<2, false><<<g, b, 0, stream>>>(a);
+  return smel::launch_status();
+}
+
+extern "C" int smel_ce_stats(const float* win_e, const float* win_s, int64_t nwin, int64_t ldn, int64_t n, float* m,
+                             float* s, uint8_t* shift, float* r, hipStream_t stream) {
+  SMEL_REQUIRE(n >= 0 && nwin >= 1 && ldn >= n, SMEL_EINVAL, "ce_stats: bad sizes");
+  if (n == 0) return 0;
+  SMEL_REQUIRE(win_e && win_s && m && s && shift && r, SMEL_EINVAL, "ce_stats: null pointer");
+  SMEL_REQUIRE(nwin < INT32_MAX, SMEL_EUNSUPPORTED, "ce_stats: too many windows");
+  ce_stats_kernel<<<dim3((unsigned)((n + 63) / 64)), dim3(256), 0, stream>>>(win_e, win_s, (int)nwin, ldn, n, m, s,
+                                                                           shift, r);
+  return smel::launch_status();
+}
+
+extern "C" int smel_ce_grad(const void* WT, int64_t ldwt, int64_t H, const void* P, int64_t ldp, int64_t vc,
+                            const uint8_t* shift, int64_t ldn, const float* r, int64_t n, int32_t dtype, int32_t first,
+                            float* acc, hipStream_t stream) {
+  SMEL_REQUIRE(SMEL_DT_OK(dtype), SMEL_EINVAL, "ce_grad: dtype %d (0 bf16, 1 fp32, 2 fp16)", dtype);
+  const int E = dtype == 1 ? 4 : 2;
+  SMEL_REQUIRE(n >= 0 && vc >= 1 && H >= 1 && ldn >= n, SMEL_EINVAL, "ce_grad: bad sizes");
+  if (n == 0) return 0;
+  SMEL_REQUIRE(WT && P && shift && acc && (first || r), SMEL_EINVAL, "ce_grad: null pointer");
+  const int64_t kbytes = (vc * E + 15) / 16 * 16;
+  SMEL_REQUIRE(H % 4 == 0 && aligned16(acc) && aligned16(WT) && aligned16(P) && (ldwt * E) % 16 == 0 &&
+                   (ldp * E) % 16 == 0 && ldp * E >= kbytes && ldwt * E >= kbytes,
+               SMEL_EUNSUPPORTED, "ce_grad: rows must be 16-byte aligned runs covering the chunk (H=%lld)",
+               (long long)H);
+  SMEL_REQUIRE((ldwt * E) * 256 < ((int64_t)1 << 31) && (ldp * E) * 128 < ((int64_t)1 << 31) && H < INT32_MAX &&
+                   n < INT32_MAX,
+               SMEL_EUNSUPPORTED, "ce_grad: tile offsets exceed 31 bits");
+  GradArgs a;
+  a.WT = WT;
+  a.P = P;
+  a.shift = shift;
+  a.r = r;
+  a.acc = acc;
+  a.ldwt = ldwt;
+  a.ldp = ldp;
+  a.ldn = ldn;
+  a.H = (int)H;
+  a.n = (int)n;
+  a.kbytes = (int)kbytes;
+  a.first = first ? 1 : 0;
+  a.n_ht = (int)((H + 255) / 256);
+  a.n_tt = (int)((n + 127) / 128);
+  const int64_t tiles = (int64_t)a.n_ht * a.n_tt;
+  SMEL_REQUIRE(tiles < INT32_MAX, SMEL_EUNSUPPORTED, "ce_grad: grid too large");
+  const dim3 g((unsigned)xcd_grid(tiles)), b(256);
+  if (dtype == 0) ce_grad_kernel<0><<<g, b, 0, stream>>>(a);
+  else if (dtype == 1) ce_grad_kernel<1><<<g, b, 0, stream>>>(a);
+  else ce_grad_kernel<2><<<g, b, 0, stream>>>(a);
+  return smel::launch_status();
+}
+
+extern "C" int smel_ce_finish(const float* m, const float* s, const float* tz, const float* td, const float* acc,
+                              const void* W, int64_t ldw, const void* trows, const int64_t* tgt, int64_t V, int64_t n,
+                              int64_t H, int32_t dtype, float gscale, void* g, int64_t ldg, int32_t g_dtype,
+                              float* loss_rows, hipStream_t stream) {
+  SMEL_REQUIRE(SMEL_DT_OK(dtype) && SMEL_DT_OK(g_dtype), SMEL_EINVAL, "ce_finish: dtype %d / %d", dtype, g_dtype);
+  SMEL_REQUIRE(n >= 0 && H >= 1 && V >= 1, SMEL_EINVAL, "ce_finish: bad sizes");
+  if (n == 0) return 0;
+  SMEL_REQUIRE(m && s && tz && td && tgt && loss_rows && (!acc || (g && ldg >= H && (W || trows))), SMEL_EINVAL,
+               "ce_finish: null pointer");
+  SMEL_REQUIRE(n < INT32_MAX, SMEL_EUNSUPPORTED, "ce_finish: too many rows");
+  const dim3 gr((unsigned)n), b(256);
+#define SMEL_FIN(D, G) \
+  ce_finish_kernel<D, G><<<gr, b, 0, stream>>>(m, s, tz, td, acc, W, ldw, trows, tgt, V, H, gscale, g, ldg, loss_rows)
+#define SMEL_FIN_G(D)            \
+  if (g_dtype == 0) SMEL_FIN(D, 0); \
+  else if (g_dtype == 1) SMEL_FIN(D, 1); \
+  else SMEL_FIN(D, 2);
+  if (dtype == 0) {
+    SMEL_FIN_G(0)
+  } else if (dtype == 1) {
+    SMEL_FIN_G(1)
+  } else {
+    SMEL_FIN_G(2)
+  }
+#undef SMEL_FIN_G
+#undef SMEL_FIN
+  return smel::launch_status();
+}
+
+extern "C" int smel_ce_loss_sum(const float* loss_rows, int64_t n, float scale, int32_t accumulate, float* total,
+                                hipStream_t stream) {
+  SMEL_REQUIRE(n >= 0 && total && (n == 0 || loss_rows), SMEL_EINVAL, "ce_loss_sum: bad arguments");
+  ce_loss_sum_kernel<<<dim3(1), dim3(256), 0, stream>>>(loss_rows, n, scale, accumulate, total);
+  return smel::launch_status();
+}
+
+extern "C" int smel_ce_scale(void* x, int64_t n, int32_t dtype, const float* go, hipStream_t stream) {
+  SMEL_REQUIRE(SMEL_DT_OK(dtype) && n >= 0, SMEL_EINVAL, "ce_scale: dtype %d, n %lld", dtype, (long long)n);
+  if (n == 0) return 0;
+  SMEL_REQUIRE(x && go, SMEL_EINVAL, "ce_scale: null pointer");
+  const dim3 g((unsigned)std::min<int64_t>((n + 255) / 256, 4096)), b(256);
+  if (dtype == 0) ce_scale_kernel<0><<<g, b, 0, stream>>>(x, n, go);
+  else if (dtype == 1) ce_scale_kernel<1><<<g, b, 0, stream>>>(x, n, go);
+  else ce_scale_kernel<2><<<g, b, 0, stream>>>(x, n, go);
+  return smel::launch_status();
+}
+
+extern "C" int smel_ce_transpose(const void* src, int64_t R, int64_t C, int64_t lds, void* dst, int64_t ldd,
+                                 int32_t dtype, hipStream_t stream) {
+  SMEL_REQUIRE(SMEL_DT_OK(dtype), SMEL_EINVAL, "ce_transpose: dtype %d", dtype);
+  SMEL_REQUIRE(R >= 0 && C >= 0 && lds >= C && ldd >= R, SMEL_EINVAL, "ce_transpose: bad sizes");
+  if (R == 0 || C == 0) return 0;
+  SMEL_REQUIRE(src && dst, SMEL_EINVAL, "ce_transpose: null pointer");
+  const int64_t gx = (ldd + 63) / 64, gy = (C + 63) / 64;
+  SMEL_REQUIRE(gx < INT32_MAX && gy < 65536, SMEL_EUNSUPPORTED, "ce_transpose: too large");
+  const dim3 g((unsigned)gx, (unsigned)gy), b(256);
+  const auto* s8 = static_cast<const uint8_t*>(src);
+  auto* d8 = static_cast<uint8_t*>(dst);
+  if (dtype == 1) ce_transpose_kernel<4><<<g, b, 0, stream>>>(s8, R, C, lds, d8, ldd);
+  else ce_transpose_kernel<2><<<g, b, 0, stream>>>(s8, R, C, lds, d8, ldd);
   return smel::launch_status();
 }

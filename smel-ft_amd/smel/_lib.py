@@ -19,7 +19,7 @@ PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -105,8 +105,14 @@ SIGNATURES = {
     "smel_stream_wait": (i32, [vp, vp]),
     "smel_h2d_regions": (i32, [ctypes.POINTER(H2DRegion), i32, i64, ctypes.POINTER(vp), ctypes.POINTER(vp), i32, vp]),
     # include/smel_loss.h
-    "smel_ce_chunk_update": (i32, [vp, i64, i64, i64, i64, vp, f32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp]),
-    "smel_ce_acc_update": (i32, [vp, vp, vp, i32, i64, i64, i32, vp]),
+    "smel_ce_begin": (i32, [vp, vp, vp, vp, vp, i64, vp]),
+    "smel_ce_logits": (i32, [vp, i64, i64, i64, vp, i64, i64, i64, vp, f32, i32, vp, i64, vp, vp, i64, vp, vp, vp]),
+    "smel_ce_stats": (i32, [vp, vp, i64, i64, i64, vp, vp, vp, vp, vp]),
+    "smel_ce_grad": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, vp, i64, i32, i32, vp, vp]),
+    "smel_ce_finish": (i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, f32, vp, i64, i32, vp, vp]),
+    "smel_ce_loss_sum": (i32, [vp, i64, f32, i32, vp, vp]),
+    "smel_ce_scale": (i32, [vp, i64, i32, vp, vp]),
+    "smel_ce_transpose": (i32, [vp, i64, i64, i64, vp, i64, i32, vp]),
     # include/smel_probe.h
     "smel_probe_mfma": (i32, [vp, i32, i32, vp]),
     "smel_probe_read": (i32, [vp, i64, vp, i32, vp]),

@@ -3,14 +3,19 @@ the [tokens, vocabulary] logits: the API of the reference's smel/loss.py (``LMHe
 ``_ce_chunk_two_pass``; same arguments and results), on the HIP kernels of include/smel_loss.h.
 
 Structure here:
-  * an LMHead reads its rows through a row source (dense rows, or int8 rows dequantized per vocabulary chunk);
-  * a token chunk is one sweep over the vocabulary chunks. Per vocabulary chunk: the logits GEMM h W_c^T (a library
-    GEMM through torch), ``smel_ce_chunk_update`` (softcap, the online maximum and sum, the target's capped logit and
-    cap derivative, the softmax terms in the rows' dtype; no host synchronisation), the gradient GEMM p W_c as a
-    split K over column slices of the chunk, and ``smel_ce_acc_update`` (rescale and add in fp32);
-  * the per-row state (maximum, sum, rescale, target logit and derivative, fp32 accumulator) is allocated once per
-    call for the largest token chunk and reused by every chunk; the gradient rows go straight into one [N, H] output
-    already divided by ``denom``.
+  * a pass covers a block of token rows; per vocabulary chunk, ``smel_ce_logits`` runs the logits GEMM on MFMA and,
+    in its epilogue, the online softmax bookkeeping per 128-column window (maximum rounded up to a power of two, sum
+    of exponentials, the softmax terms written in the rows' dtype, the target's logit), ``smel_ce_stats`` folds the
+    windows into each row's running maximum and sum (every rescale an exact power of two) and ``smel_ce_grad`` runs
+    the gradient GEMM p W on MFMA, shifting each fragment of p to the running maximum as it is loaded and adding into
+    the fp32 accumulator rescaled by the same power of two; ``smel_ce_finish`` writes the loss rows and the gradient
+    rows (acc / s - d W[target], scaled), ``smel_ce_loss_sum`` their sum;
+  * the gradient GEMM reads the head transposed ([H][V]): a dense head whose dtype is the rows' is transposed once
+    and kept with the head (it is frozen); other heads (int8, or another dtype) are converted per vocabulary chunk,
+    as the reference's ``rows()`` does, and that chunk is transposed;
+  * vocabulary chunks are ``vocab_chunk`` rounded up to 256 columns (the logits tile), and a pass takes
+    max(token_chunk, 4096) rows: the rows are independent, so the results are those of the reference's chunking;
+    the softmax terms of a pass take rows x chunk values of the rows' dtype (256 MB at 4096 x 32768 bf16).
 The gradient is computed in the forward (lm_head is frozen) and handed back by the backward, as in the reference.
 """
 from __future__ import annotations
@@ -21,14 +26,20 @@ from . import _lib as L
 from .quant import dequant_int8_rows, quantize_int8_rows
 
 _DT = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}
-SPLIT_PARTS = 8        # column slices of a vocabulary chunk in the gradient GEMM (its [tokens, H] output is small)
+TILE_V = 256           # vocabulary columns of a logits tile; chunks are whole tiles
+WIN = 128              # columns of one statistics window
+ROWS_PER_PASS = 4096   # token rows of one pass at least (the GEMMs' row tiles fill the GPU from there on)
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
 
 
 # --------------------------------------------------------------------------------------------------- the head
 
 
 class _DenseRows:
-    """Rows of a bf16 / fp32 head weight [V, H]."""
+    """Rows of a bf16 / fp16 / fp32 head weight [V, H]."""
 
     def __init__(self, w: torch.Tensor):
         self.w = w
@@ -41,6 +52,16 @@ class _DenseRows:
 
     def take(self, idx: torch.Tensor, dtype) -> torch.Tensor:
         return self.w.index_select(0, idx).to(dtype)
+
+    def native(self, dtype):
+        """The weight itself when the kernels can read it as rows of `dtype` in place, else None."""
+        w = self.w
+        if w.dtype != dtype or not w.is_cuda or w.stride(1) != 1:
+            return None
+        e = w.element_size()
+        if (w.shape[1] * e) % 16 or (w.stride(0) * e) % 16 or w.data_ptr() % 16:
+            return None
+        return w
 
     def moved(self, device):
         return _DenseRows(self.w.to(device))
@@ -61,6 +82,9 @@ class _Int8Rows:
     def take(self, idx: torch.Tensor, dtype) -> torch.Tensor:
         return dequant_int8_rows(self.q["q"].index_select(0, idx), self.q["scale"].index_select(0, idx), dtype)
 
+    def native(self, dtype):
+        return None
+
     def moved(self, device):
         return _Int8Rows({k: v.to(device) for k, v in self.q.items()})
 
@@ -79,6 +103,7 @@ class LMHead:
         self.vocab = self._src.n()
         self.vocab_chunk = vocab_chunk
         self.softcap = float(softcap or 0.0)
+        self._wt = {}    # dtype -> (key, transposed head [H][Vp]) for a dense head read in place
 
     @classmethod
     def from_weight(cls, w, int8=False, vocab_chunk=32768, softcap=0.0):
@@ -112,131 +137,172 @@ class LMHead:
             out[:, v0:v1] = self.cap(torch.mm(h, self.rows(v0, v1, h.dtype).t()).float())
         return out
 
+    # ---- what the kernels read
+    def _kernel_chunks(self):
+        """Vocabulary chunks of the kernels: vocab_chunk rounded up to whole logits tiles."""
+        step = _round_up(max(1, min(self.vocab_chunk, self.vocab)), TILE_V)
+        return [(v0, min(self.vocab, v0 + step)) for v0 in range(0, self.vocab, step)], step
 
-# ------------------------------------------------------------------------------------------- one token chunk
+    def _transposed(self, w: torch.Tensor) -> torch.Tensor:
+        """The head [V, H] transposed to [H, Vp] (Vp = V rounded up to 8, zero columns past V), made once."""
+        key = (w.data_ptr(), w._version, tuple(w.shape), w.dtype)
+        got = self._wt.get(w.dtype)
+        if got is not None and got[0] == key:
+            return got[1]
+        V, H = w.shape
+        wt = torch.empty(H, _round_up(V, 8), dtype=w.dtype, device=w.device)
+        L.call("smel_ce_transpose", L.ptr(w), V, H, w.stride(0), L.ptr(wt), wt.stride(0), _DT[w.dtype], L.stream())
+        self._wt[w.dtype] = (key, wt)
+        return wt
 
 
-def _split_parts(vc: int) -> int:
-    """Column slices of a vocabulary chunk of vc columns for the split-K gradient GEMM: SPLIT_PARTS when every slice
-    is at least 256 columns of whole 8-column groups, else 1."""
-    return SPLIT_PARTS if vc % (8 * SPLIT_PARTS) == 0 and vc >= 256 * SPLIT_PARTS else 1
+# ------------------------------------------------------------------------------------------------ one pass
 
 
-class _RowState:
-    """Per-row state of one token chunk, allocated for up to ``cap`` rows and reused chunk after chunk."""
+class _Pass:
+    """Scratch of one pass over n token rows: per-row state, window statistics, softmax terms, accumulator."""
 
-    def __init__(self, cap: int, H: int, need_grad: bool, device):
+    def __init__(self, n: int, H: int, vcp: int, dtype, need_grad: bool, device):
         f = lambda *s: torch.empty(*s, dtype=torch.float32, device=device)
-        self.m, self.s, self.r, self.tl, self.td = f(cap), f(cap), f(cap), f(cap), f(cap)
-        self.acc = f(cap, H) if need_grad else None
-
-    def start(self, n: int, m0: torch.Tensor | None = None):
-        """Views for n rows, reset for a sweep (m0: a preset running maximum, the two-pass form's second pass)."""
-        v = [t[:n] for t in (self.m, self.s, self.r, self.tl, self.td)]
-        m, s, r, tl, td = v
-        if m0 is None:
-            m.fill_(-float("inf"))
-        else:
-            m.copy_(m0)
-        s.zero_()
-        tl.zero_()
-        td.fill_(1.0)
-        acc = None
-        if self.acc is not None:
-            acc = self.acc[:n]
-            acc.zero_()
-        return m, s, r, tl, td, acc
+        nwin = vcp // WIN
+        self.n = n
+        self.m, self.s, self.tz, self.td, self.r, self.loss = (f(n) for _ in range(6))
+        self.win_e, self.win_s = f(nwin, n), f(nwin, n)
+        self.shift = torch.empty(nwin, n, dtype=torch.uint8, device=device)
+        self.P = torch.empty(n, vcp, dtype=dtype, device=device) if need_grad else None
+        self.acc = f(n, H) if need_grad else None
 
 
-def _sweep(h, head: LMHead, tgt, need_grad: bool, st: _RowState, m0=None):
-    """One pass over the vocabulary for the rows h [n, H]: returns (m, s, tgt_logit, tgt_d, acc) after the last
-    chunk (acc = sum_v softmax-term_v W_v, scaled to the final maximum; None without need_grad)."""
+def _sweep(h, head: LMHead, tgt, need_grad: bool, ps: _Pass, m0=None):
+    """One pass over the vocabulary for the rows h [n, H]: the per-row state and (need_grad) the accumulator."""
     n, H = h.shape
-    dt = _DT[h.dtype]
-    m, s, r, tl, td, acc = st.start(n, m0)
-    stream = L.stream()
-    for v0, v1 in head.chunks():
-        W = head.rows(v0, v1, h.dtype).contiguous()
+    dt, st, p = _DT[h.dtype], L.stream(), L.ptr
+    L.call("smel_ce_begin", p(ps.m), p(ps.s), p(ps.tz), p(ps.td), p(m0), n, st)
+    native = head._src.native(h.dtype)
+    chunks, _ = head._kernel_chunks()
+    for i, (v0, v1) in enumerate(chunks):
         vc = v1 - v0
-        lg = torch.mm(h, W.t())                         # rounded to the rows' dtype, as the reference's h @ W.t()
-        parts = _split_parts(vc) if need_grad else 1
-        p = torch.empty(parts, n, vc // parts, dtype=h.dtype, device=h.device) if need_grad else None
-        L.call("smel_ce_chunk_update", L.ptr(lg), n, vc, lg.stride(0), v0, L.ptr(tgt), head.softcap, dt,
-               int(need_grad), L.ptr(m), L.ptr(s), L.ptr(tl), L.ptr(td), L.ptr(p), parts, L.ptr(r), stream)
+        if native is not None:
+            W, ldw = native[v0:v1], native.stride(0)
+        else:
+            W = head.rows(v0, v1, h.dtype).contiguous()
+            ldw = W.stride(0)
+        nwin = _round_up(vc, TILE_V) // WIN
+        P = ps.P if need_grad else None
+        L.call("smel_ce_logits", p(W), ldw, vc, v0, p(h), h.stride(0), n, H, p(tgt), head.softcap, dt, p(P),
+               P.stride(0) if need_grad else 0, p(ps.win_e), p(ps.win_s), n, p(ps.tz), p(ps.td), st)
+        L.call("smel_ce_stats", p(ps.win_e), p(ps.win_s), nwin, n, n, p(ps.m), p(ps.s), p(ps.shift), p(ps.r), st)
         if need_grad:
-            pw = torch.bmm(p, W.view(parts, vc // parts, H))   # slice k: p_k W_k, [parts, n, H]
-            L.call("smel_ce_acc_update", L.ptr(acc), L.ptr(r), L.ptr(pw), parts, n, H, dt, stream)
-    return m, s, tl, td, acc
+            if native is not None:
+                wt = head._transposed(native)
+                WT, ldwt = wt[:, v0:], wt.stride(0)
+            else:
+                WT = torch.empty(H, _round_up(vc, 8), dtype=h.dtype, device=h.device)
+                L.call("smel_ce_transpose", p(W), vc, H, ldw, p(WT), WT.stride(0), dt, st)
+                ldwt = WT.stride(0)
+            L.call("smel_ce_grad", p(WT), ldwt, H, p(ps.P), ps.P.stride(0), vc, p(ps.shift), n, p(ps.r), n, dt,
+                   int(i == 0), p(ps.acc), st)
 
 
-def _finish(h, head: LMHead, tgt, m, s, tl, td, acc):
-    """loss_sum = sum (lse - target logit); gradient rows = acc / s - tgt_d W[tgt] (a target outside [0, V) matches
-    no row of the head: its logit and row count as zero, as in the reference's _ce_chunk)."""
-    loss = (m + torch.log(s) - tl).sum()
-    if acc is None:
-        return loss, None
-    ok = (tgt >= 0) & (tgt < head.vocab)
-    rows = head.rows_at(torch.where(ok, tgt, torch.zeros_like(tgt)), h.dtype).float()
-    return loss, acc / s[:, None] - (td * ok)[:, None] * rows
+def _finish(h, head: LMHead, tgt, ps: _Pass, need_grad: bool, gscale: float = 1.0, g=None):
+    """Loss rows into ps.loss and (need_grad) gradient rows gscale (acc / s - d W[target]) into g (default: a new
+    fp32 [n, H]); a target outside [0, V) matches no row of the head (its logit and row count as zero, as in the
+    reference's _ce_chunk)."""
+    n, H = h.shape
+    dt, p = _DT[h.dtype], L.ptr
+    W, ldw, trows = None, 0, None
+    if need_grad:
+        native = head._src.native(h.dtype)
+        if native is not None:
+            W, ldw = native, native.stride(0)
+        else:
+            ok = (tgt >= 0) & (tgt < head.vocab)
+            trows = head.rows_at(torch.where(ok, tgt, torch.zeros_like(tgt)), h.dtype).contiguous()
+        if g is None:
+            g = torch.empty(n, H, dtype=torch.float32, device=h.device)
+    L.call("smel_ce_finish", p(ps.m), p(ps.s), p(ps.tz), p(ps.td), p(ps.acc), p(W), ldw, p(trows), p(tgt), head.vocab,
+           n, H, dt, float(gscale), p(g), g.stride(0) if g is not None else 0, _DT[g.dtype] if g is not None else 0,
+           p(ps.loss), L.stream())
+    return g
 
 
 def _prep(h, tgt):
     L.require_device(h)
     if h.dtype not in _DT:
         raise ValueError(f"chunked CE takes bf16 / fp16 / fp32 rows, got {h.dtype}")
-    return h.contiguous(), tgt.to(device=h.device, dtype=torch.int64).contiguous()
+    h = h.contiguous()
+    if (h.shape[1] * h.element_size()) % 16:
+        raise ValueError(f"chunked CE takes rows of whole 16-byte runs (hidden size {h.shape[1]} in {h.dtype})")
+    return h, tgt.to(device=h.device, dtype=torch.int64).contiguous()
+
+
+def _loss_sum(ps: _Pass, total: torch.Tensor, scale: float, accumulate: bool):
+    L.call("smel_ce_loss_sum", L.ptr(ps.loss), ps.n, float(scale), int(accumulate), L.ptr(total), L.stream())
+
+
+def _one_chunk(h, head: LMHead, tgt, need_grad, two_pass: bool):
+    h, tgt = _prep(h, tgt)
+    n, H = h.shape
+    _, vcp = head._kernel_chunks()
+    total = torch.empty((), dtype=torch.float32, device=h.device)
+    ps = _Pass(n, H, vcp, h.dtype, need_grad, h.device)
+    m0 = None
+    if two_pass:
+        _sweep(h, head, tgt, False, ps)
+        m0 = ps.m.clone()
+    _sweep(h, head, tgt, need_grad, ps, m0=m0)
+    g = _finish(h, head, tgt, ps, need_grad)
+    _loss_sum(ps, total, 1.0, False)
+    return total, g
 
 
 def _ce_chunk(h, head: LMHead, tgt, need_grad):
-    """Loss sum and (optionally) d loss_sum / d h of one token chunk in ONE pass over the vocabulary
+    """Loss sum and (optionally) d loss_sum / d h (fp32) of one token chunk in ONE pass over the vocabulary
     (smel/loss.py:55-92): the gradient terms are accumulated under the same running maximum as the log-sum-exp and
-    rescaled with it. The split-K gradient GEMM rounds each slice's product to the rows' dtype before the fp32 sum,
-    where the reference rounds the one product."""
-    h, tgt = _prep(h, tgt)
-    st = _RowState(h.shape[0], h.shape[1], need_grad, h.device)
-    return _finish(h, head, tgt, *_sweep(h, head, tgt, need_grad, st))
+    rescaled with it."""
+    return _one_chunk(h, head, tgt, need_grad, False)
 
 
 def _ce_chunk_two_pass(h, head: LMHead, tgt, need_grad):
     """The same quantities in two passes over the vocabulary (the comparator of smel/loss.py:95-127): the first pass
     finds each row's final maximum, the second runs with that maximum preset, so no partial sum or gradient term is
     ever rescaled."""
-    h, tgt = _prep(h, tgt)
-    st = _RowState(h.shape[0], h.shape[1], need_grad, h.device)
-    m = _sweep(h, head, tgt, False, st)[0].clone()
-    if not need_grad:
-        return _finish(h, head, tgt, m, st.s[:h.shape[0]], st.tl[:h.shape[0]], st.td[:h.shape[0]], None)
-    return _finish(h, head, tgt, *_sweep(h, head, tgt, True, st, m0=m))
+    return _one_chunk(h, head, tgt, need_grad, True)
 
 
 # ------------------------------------------------------------------------------------------------ the loss
 
 
 class _ChunkedCE(torch.autograd.Function):
-    """sum_t CE / denom over token chunks (smel/loss.py:130-146); the gradient rows, already divided by denom, are
+    """sum_t CE / denom over token passes (smel/loss.py:130-146); the gradient rows, already divided by denom, are
     written into one output during the forward and returned, times the incoming gradient, by the backward."""
 
     @staticmethod
     def forward(ctx, h, head, tgt, denom, token_chunk, need_grad):
         h, tgt = _prep(h, tgt)
         N, H = h.shape
-        st = _RowState(min(N, token_chunk), H, need_grad, h.device)
+        rows = min(N, max(int(token_chunk), ROWS_PER_PASS))
+        _, vcp = head._kernel_chunks()
         grad = torch.empty_like(h) if need_grad else None
-        total = torch.zeros((), dtype=torch.float32, device=h.device)
-        for t0 in range(0, N, token_chunk):
-            t1 = min(N, t0 + token_chunk)
-            loss, g = _finish(h[t0:t1], head, tgt[t0:t1], *_sweep(h[t0:t1], head, tgt[t0:t1], need_grad, st))
-            total += loss
-            if need_grad:
-                grad[t0:t1] = g / denom
+        total = torch.empty((), dtype=torch.float32, device=h.device)
+        ps = _Pass(rows, H, vcp, h.dtype, need_grad, h.device)
+        for t0 in range(0, N, rows):
+            t1 = min(N, t0 + rows)
+            if t1 - t0 != ps.n:
+                ps = _Pass(t1 - t0, H, vcp, h.dtype, need_grad, h.device)
+            _sweep(h[t0:t1], head, tgt[t0:t1], need_grad, ps)
+            _finish(h[t0:t1], head, tgt[t0:t1], ps, need_grad, 1.0 / denom, grad[t0:t1] if need_grad else None)
+            _loss_sum(ps, total, 1.0 / denom, t0 > 0)
         ctx.grad = grad
-        return total / denom
+        return total
 
     @staticmethod
     def backward(ctx, go):
         g = ctx.grad
         ctx.grad = None
-        return g * go.to(g.dtype), None, None, None, None, None
+        go = go.to(device=g.device, dtype=torch.float32).contiguous()
+        L.call("smel_ce_scale", L.ptr(g), g.numel(), _DT[g.dtype], L.ptr(go), L.stream())
+        return g, None, None, None, None, None
 
 
 def chunked_ce(h, head: LMHead, tgt, denom: float, token_chunk: int = 1024, need_grad: bool = True):

@@ -123,20 +123,19 @@ def rounded_full_ce(h, W, tgt, softcap):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("softcap", [0.0, 30.0])
-def test_split_k_gradient_chunks(lm, dtype, softcap):
-    """Vocabulary chunks of 4096 columns take the 8-slice split-K gradient GEMM ([parts][n][vc/parts] softmax terms,
-    per-slice products summed in fixed order by smel_ce_acc_update); the last chunk (100 columns) falls back to one
-    slice. Loss and gradient against the fp64 full-logit oracle and the rounded full-logit comparator."""
+def test_several_vocabulary_chunks(lm, dtype, softcap):
+    """Vocabulary chunks of 4096 columns (16 logits tiles, 32 statistics windows) and a short last chunk of 100
+    columns (one partly filled tile): the running maximum moves between chunks, so the accumulator and the window
+    shifts are rescaled. Loss and gradient against the fp64 full-logit oracle and the rounded full-logit comparator."""
     loss_mod, _ = lm
-    print(f"split-K CE {dtype} softcap {softcap}", flush=True)
+    print(f"multi-chunk CE {dtype} softcap {softcap}", flush=True)
     torch.manual_seed(4)
     n, H, V = 300, 256, 2 * 4096 + 100
     h = (torch.randn(n, H, device="cuda") * 0.5).to(dtype)
     W = (torch.randn(V, H, device="cuda") * 0.2).to(dtype)
     tgt = torch.randint(0, V, (n,), device="cuda")
-    tgt[:4] = torch.tensor([0, 4095, 4096, V - 1])                      # chunk edges and the short last chunk
+    tgt[:6] = torch.tensor([0, 127, 128, 4095, 4096, V - 1])           # window, tile, chunk edges, the last column
     head = loss_mod.LMHead(weight=W, vocab_chunk=4096, softcap=softcap)
-    assert [loss_mod._split_parts(v1 - v0) for v0, v1 in head.chunks()] == [8, 8, 1]
     l1, g1 = loss_mod._ce_chunk(h, head, tgt, True)
     l64, g64 = LR.full_ce(h, W, tgt, softcap)
     lc, gc = rounded_full_ce(h, W, tgt, softcap)
@@ -148,6 +147,87 @@ def test_split_k_gradient_chunks(lm, dtype, softcap):
     l2, g2 = loss_mod._ce_chunk_two_pass(h, head, tgt, True)           # the same sums without any rescaling
     assert abs(l1.item() - l2.item()) / abs(l2.item()) < tol_l
     assert (g1 - g2).norm() / g2.norm() < (2e-2 if dtype == torch.bfloat16 else 1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_wide_logit_range(lm, dtype):
+    """Head rows of very different norms: windows whose maxima lie 100-400 below the row's maximum get shifts past
+    the bf16 / fp32 range (their terms become zero, as exp underflows in the reference), others small shifts; a few
+    rows put their target in such a window (a large loss). bf16 against the rounded full-logit comparator (logits of
+    a few hundred carry bf16 steps of 0.5-2 in both), fp32 against the fp64 oracle."""
+    loss_mod, _ = lm
+    print(f"wide-range CE {dtype}", flush=True)
+    torch.manual_seed(6)
+    n, H, V = 96, 128, 3000
+    h = torch.randn(n, H, device="cuda").to(dtype)
+    scale = torch.ones(V, 1, device="cuda")
+    scale[0:128] = 40.0            # window 0: logits of a few hundred
+    scale[1024:1152] = 8.0         # a window at a moderate offset
+    W = (torch.randn(V, H, device="cuda") * 0.1 * scale).to(dtype)
+    tgt = torch.randint(0, V, (n,), device="cuda")
+    tgt[:4] = torch.tensor([5, 1030, 2999, 700])
+    head = loss_mod.LMHead(weight=W, vocab_chunk=1024)
+    l1, g1 = loss_mod._ce_chunk(h, head, tgt, True)
+    if dtype == torch.bfloat16:
+        lc, gc = rounded_full_ce(h, W, tgt, 0.0)
+        assert abs(l1.item() - lc.item()) / abs(lc.item()) < 1e-4
+        assert (g1 - gc).norm() / gc.norm() < 2e-2
+    else:
+        l64, g64 = LR.full_ce(h, W, tgt)
+        assert abs(l1.item() - float(l64)) / abs(float(l64)) < 1e-5
+        assert (g1.double().cpu() - g64).norm() / g64.norm() < 1e-4
+
+
+def test_several_row_passes(lm, monkeypatch):
+    """Passes of 64 rows (the pass size lowered for the test): the loss accumulates over the passes and each pass
+    writes its own gradient rows; equal to one pass over all rows."""
+    loss_mod, _ = lm
+    torch.manual_seed(7)
+    n, H, V = 200, 64, 1500
+    h = (torch.randn(n, H, device="cuda") * 0.5).bfloat16()
+    W = (torch.randn(V, H, device="cuda") * 0.2).bfloat16()
+    tgt = torch.randint(0, V, (n,), device="cuda")
+    head = loss_mod.LMHead(weight=W, vocab_chunk=512)
+    one = h.clone().requires_grad_(True)
+    l_one = loss_mod.chunked_ce(one, head, tgt, denom=float(n))
+    l_one.backward()
+    monkeypatch.setattr(loss_mod, "ROWS_PER_PASS", 64)
+    many = h.clone().requires_grad_(True)
+    l_many = loss_mod.chunked_ce(many, head, tgt, denom=float(n), token_chunk=16)
+    (l_many * 2.0).backward()                                      # the incoming gradient scales the rows
+    assert abs(l_one.item() - l_many.item()) < 1e-5 * abs(l_one.item())
+    assert torch.equal(many.grad.float(), (2.0 * one.grad.float()).bfloat16().float())
+    l64, g64 = LR.full_ce(h, W, tgt, denom=float(n))
+    assert abs(l_many.item() - float(l64)) / abs(float(l64)) < 1e-3
+
+
+def test_qwen_head_full_size(lm):
+    """The bench's shape (4092 rows, hidden 2048, vocabulary 248320, chunks of 32768, bf16): loss and gradient of
+    chunked_ce against the rounded full-logit comparator run in fp32 torch on the GPU (the [4092, 248320] logits fit
+    in memory there), and the same call twice gives bitwise equal results."""
+    loss_mod, _ = lm
+    print("CE full size", flush=True)
+    torch.manual_seed(8)
+    T, H, V = 4092, 2048, 248320
+    h = torch.randn(T, H, device="cuda").bfloat16()
+    W = (torch.randn(V, H, device="cuda") * 0.02).bfloat16()
+    tgt = torch.randint(0, V, (T,), device="cuda")
+    head = loss_mod.LMHead(weight=W)
+    x = h.clone().requires_grad_(True)
+    loss = loss_mod.chunked_ce(x, head, tgt, denom=float(T))
+    loss.backward()
+    g1 = x.grad.clone()
+    x.grad = None
+    loss2 = loss_mod.chunked_ce(x, head, tgt, denom=float(T))
+    loss2.backward()
+    assert torch.equal(loss, loss2) and torch.equal(g1, x.grad)
+    lc, gc = rounded_full_ce(h, W, tgt, 0.0)
+    lc, gc = lc / T, gc / T
+    rel_l = abs(loss.item() - lc.item()) / abs(lc.item())
+    rel_g = ((g1.float() - gc).norm() / gc.norm()).item()
+    cos = torch.nn.functional.cosine_similarity(g1.float().flatten(), gc.flatten(), dim=0).item()
+    print(f"full-size CE: loss rel err {rel_l:.2e}, grad rel err {rel_g:.2e}, cos {cos:.6f}", flush=True)
+    assert rel_l < 1e-4 and rel_g < 2e-2 and cos > 0.9999
 
 
 def test_targets_outside_the_vocabulary(lm):

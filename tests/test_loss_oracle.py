@@ -42,17 +42,27 @@ def test_softcap_gradient_finite_differences():
 
 
 def test_ce_entry_points_reject_bad_arguments():
+    """Host-side checks of include/smel_loss.h: bad sizes, dtypes and layouts are refused before any launch."""
     from smel import _lib
     L = _lib.load()
-    fake = ctypes.c_void_p(1 << 20)   # never dereferenced
-    EINVAL = -1
-    cu = L.smel_ce_chunk_update
-    assert cu(fake, 4, 0, 0, 0, fake, 0.0, 0, 1, fake, fake, fake, fake, fake, 1, fake, None) == EINVAL  # vc 0
-    assert cu(fake, 4, 8, 4, 0, fake, 0.0, 0, 1, fake, fake, fake, fake, fake, 1, fake, None) == EINVAL  # ld < vc
-    assert cu(fake, 4, 8, 8, 0, fake, 0.0, 3, 1, fake, fake, fake, fake, fake, 1, fake, None) == EINVAL  # dtype
-    assert cu(fake, 4, 8, 8, 0, fake, 0.0, 0, 1, fake, fake, fake, fake, None, 1, fake, None) == EINVAL  # no p
-    assert cu(fake, 4, 8, 8, 0, fake, 0.0, 0, 1, fake, fake, fake, fake, fake, 3, fake, None) == EINVAL  # 3 parts
-    assert cu(fake, 0, 8, 8, 0, fake, 0.0, 0, 1, fake, fake, fake, fake, fake, 2, fake, None) == 0       # no rows
-    assert L.smel_ce_acc_update(fake, fake, None, 1, 4, 8, 0, None) == EINVAL
-    assert L.smel_ce_acc_update(fake, fake, fake, 1, 4, 0, 0, None) == EINVAL
-    assert L.smel_ce_acc_update(fake, fake, fake, 0, 4, 8, 0, None) == EINVAL
+    fake = ctypes.c_void_p(1 << 20)   # 16-byte aligned, never dereferenced
+    EINVAL, EUNSUP = -1, -2
+    lg = L.smel_ce_logits   # W ldw vc v0 h ldh n H tgt cap dtype P ldp win_e win_s ldn tz td stream
+    ok = (fake, 64, 300, 0, fake, 64, 4, 64, fake, 0.0, 0, fake, 512, fake, fake, 4, fake, fake)
+    assert lg(*ok[:10], 3, *ok[11:], None) == EINVAL                       # dtype
+    assert lg(*ok[:2], 0, *ok[3:], None) == EINVAL                          # empty chunk
+    assert lg(*ok[:7], 12, *ok[8:], None) == EUNSUP                         # 24-byte bf16 rows
+    assert lg(*ok[:12], 300, *ok[13:], None) == EINVAL                      # softmax rows shorter than 512
+    assert lg(*ok[:15], 3, *ok[16:], None) == EINVAL                        # statistics pitch below n
+    assert lg(*ok[:6], 0, *ok[7:], None) == 0                               # no rows: nothing to do
+    gr = L.smel_ce_grad     # WT ldwt H P ldp vc shift ldn r n dtype first acc stream
+    assert gr(fake, 512, 66, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, None) == EUNSUP   # H % 4
+    assert gr(fake, 512, 64, None, 512, 300, fake, 4, fake, 4, 0, 0, fake, None) == EINVAL   # no softmax terms
+    assert gr(fake, 256, 64, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, None) == EUNSUP   # head rows too short
+    assert gr(fake, 512, 64, fake, 512, 300, fake, 4, None, 4, 0, 0, fake, None) == EINVAL   # no rescale
+    assert L.smel_ce_stats(fake, fake, 0, 4, 4, fake, fake, fake, fake, None) == EINVAL         # no windows
+    assert L.smel_ce_finish(fake, fake, fake, fake, None, None, 0, None, fake, 10, 4, 64, 5, 1.0, None, 0, 0,
+                            fake, None) == EINVAL                                               # dtype
+    assert L.smel_ce_transpose(fake, 4, 64, 32, fake, 8, 0, None) == EINVAL                    # pitch < columns
+    assert L.smel_ce_scale(fake, 8, 3, fake, None) == EINVAL
+    assert L.smel_ce_loss_sum(fake, 4, 1.0, 0, None, None) == EINVAL
