@@ -41,19 +41,23 @@ int smel_ce_logits(const void* W, int64_t ldw, int64_t vc, int64_t v0, const voi
 int smel_ce_stats(const float* win_e, const float* win_s, int64_t nwin, int64_t ldn, int64_t n, float* m, float* s,
                   uint8_t* shift, float* r, hipStream_t stream);
 
-/* acc [n][H] fp32 = (first ? 0 : r acc) + sum_v (P[v] 2^-shift) W[v] over the chunk's vc columns, with the head
- * transposed: WT [H][ldwt], column 0 = vocabulary id v0 (ldwt covers vc rounded up to 16 bytes).
- * smel/loss.py:83-85 (`acc * r + p.to(h.dtype) @ W`), the product on MFMA. */
+/* The gradient GEMM of vocabulary chunk number `chunk` (0, 1, ... in order) over its vc columns, with the head
+ * transposed: WT [H][ldwt], column 0 = vocabulary id v0 (ldwt covers vc rounded up to 16 bytes). The chunk's columns
+ * are split in two halves: acc [n][H] fp32 = (chunk == 0 ? 0 : r (acc + part[(chunk - 1) % 2])) + sum over the
+ * first half of (P[v] 2^-shift) W[v], and part[chunk % 2] = the same sum over the second half (part: [2][n][H]
+ * fp32; the gradient sum after the last chunk is acc + part[last % 2]). smel/loss.py:83-85
+ * (`acc * r + p.to(h.dtype) @ W`), the product on MFMA. */
 int smel_ce_grad(const void* WT, int64_t ldwt, int64_t H, const void* P, int64_t ldp, int64_t vc,
-                 const uint8_t* shift, int64_t ldn, const float* r, int64_t n, int32_t dtype, int32_t first,
-                 float* acc, hipStream_t stream);
+                 const uint8_t* shift, int64_t ldn, const float* r, int64_t n, int32_t dtype, int32_t chunk,
+                 float* acc, float* part, hipStream_t stream);
 
-/* Per row: loss_rows = m ln 2 + log s - tz; with acc, g [n][ldg] in g_dtype = gscale (acc / s - td W[tgt]) (no
- * target row when tgt is outside [0, V)), the target row read from trows [n][H] when given, else from W [V][ldw].
- * smel/loss.py:86-92. */
-int smel_ce_finish(const float* m, const float* s, const float* tz, const float* td, const float* acc, const void* W,
-                   int64_t ldw, const void* trows, const int64_t* tgt, int64_t V, int64_t n, int64_t H, int32_t dtype,
-                   float gscale, void* g, int64_t ldg, int32_t g_dtype, float* loss_rows, hipStream_t stream);
+/* Per row: loss_rows = m ln 2 + log s - tz; with acc, g [n][ldg] in g_dtype = gscale ((acc + part) / s - td W[tgt])
+ * (part: the last chunk's partial [n][H], may be null; no target row when tgt is outside [0, V)), the target row
+ * read from trows [n][H] when given, else from W [V][ldw]. smel/loss.py:86-92. */
+int smel_ce_finish(const float* m, const float* s, const float* tz, const float* td, const float* acc,
+                   const float* part, const void* W, int64_t ldw, const void* trows, const int64_t* tgt, int64_t V,
+                   int64_t n, int64_t H, int32_t dtype, float gscale, void* g, int64_t ldg, int32_t g_dtype,
+                   float* loss_rows, hipStream_t stream);
 
 /* total = (accumulate ? total : 0) + scale * sum of loss_rows, in fixed order (smel/loss.py:136-140). */
 int smel_ce_loss_sum(const float* loss_rows, int64_t n, float scale, int32_t accumulate, float* total,

@@ -27,8 +27,22 @@
 
 namespace {
 
-constexpr int KB = 128;     // bytes of one k-step of an operand row: 64 16-bit or 32 fp32 values
 constexpr int WIN = 128;    // vocabulary columns of one statistics window
+// k-step bytes and ring stages of the two GEMMs (the logits GEMM's stage: 256 + 256 rows, the gradient GEMM's:
+// 256 + 128 rows)
+#ifndef SMEL_CE_LG_KB
+#define SMEL_CE_LG_KB 128
+#define SMEL_CE_LG_NST 2
+#define SMEL_CE_GR_KB 128
+#define SMEL_CE_GR_NST 2
+#endif
+#ifndef SMEL_CE_LG_NW
+#define SMEL_CE_LG_NW 8
+#endif
+#ifndef SMEL_CE_GR_NW
+#define SMEL_CE_GR_NW 8
+#endif
+
 constexpr int VT = 256;     // vocabulary columns of a logits tile (two windows)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
@@ -79,7 +93,6 @@ SMEL_DEV uint32_t pack2h(float lo, float hi) {
 // an ext-vector element in an unrolled loop (every later element got the first element's result).
 template <int DT>
 SMEL_DEV u32x4_t shift_chunk(const u32x4_t v, uint32_t sh) {
-  if (sh == 0) return v;
   u32x4_t o;
   if constexpr (DT == 0) {
     const unsigned short d = (unsigned short)(sh << 7);
@@ -110,91 +123,130 @@ SMEL_DEV u32x4_t shift_chunk(const u32x4_t v, uint32_t sh) {
 // ------------------------------------------------------------------------------------------------ GEMM main loop
 // C[i][j] += sum_k A[i][k] B[j][k] over one tile: A 256 rows, B 64 NB rows, both K-contiguous (row pitch in bytes
 // given by the caller's offsets). 4 waves: wave w computes A rows 128 (w & 1) + [0, 128) x B rows 32 NB (w >> 1) +
-// [0, 32 NB) as 4 x NB MFMA tiles of 32 x 32. Per k-step (128 bytes of every row) the operands go global -> LDS
-// directly (16-byte LDS-DMA loads, 1 KB per wave-load: 8 rows), into a ring of NST stages loaded NST - 1 steps
-// ahead; the 16-byte chunks of each 128-byte LDS row are XOR-swizzled (chunk c of row r at c ^ swz(r)), so the
-// fragment reads of 32 consecutive rows hit distinct banks. Lane half h carries chunk 4 h + s of substep s, for A
-// and B alike.
-template <int NB, int NST>
+// [0, 32 NB) as 4 x NB MFMA tiles of 32 x 32. Per k-step (KB bytes of every row: 128 or 64) the operands go
+// global -> LDS directly (16-byte LDS-DMA loads, 1 KB per wave-load), into a ring of NST stages loaded NST - 1 steps
+// ahead. The 16-byte chunks of each LDS row are XOR-swizzled (logical chunk c of row r at phys(c, r)) so that the
+// fragment reads of 8 or 16 consecutive rows at one logical chunk hit distinct banks (32 or 64 four-byte banks).
+// Lane half h carries chunk NSUB h + s in substep s, for A and B alike.
+template <int KB_, int NB, int NST, int NW = 4>
 struct Ring {
-  static constexpr int A_BYTES = 256 * KB, B_BYTES = 64 * NB * KB, STAGE = A_BYTES + B_BYTES, BYTES = NST * STAGE;
-  static constexpr int VM_A = 256 / 8 / 4, VM_B = 64 * NB / 8 / 4;   // wave-loads per wave and stage
+  static constexpr int KB = KB_;            // bytes of one k-step of a row
+  static constexpr int NSTAGE = NST;
+  static constexpr int NWAVES = NW;         // 2 x NW / 2 waves: A halves x B parts
+  static constexpr int RPW = 1024 / KB;     // rows of one 1-KB wave-load
+  static constexpr int CPR = KB / 16;       // 16-byte chunks per row
+  static constexpr int NSUB = CPR / 2;      // MFMA substeps per k-step
+  static constexpr int B_ROWS = 32 * NB * (NW / 2);
+  static constexpr int A_BYTES = 256 * KB, B_BYTES = B_ROWS * KB, STAGE = A_BYTES + B_BYTES, BYTES = NST * STAGE;
+  static constexpr int VM_A = 256 / RPW / NW, VM_B = B_ROWS / RPW / NW;   // wave-loads per wave and stage
+  static_assert(VM_A % 2 == 0 && VM_B % 2 == 0, "even wave-load counts (the 128-byte swizzle parity)");
   static constexpr int VM_STEP = VM_A + VM_B;
+  static_assert(KB == 128 || KB == 64, "k-steps of 128 or 64 bytes");
+  // the row swizzle: 128-byte rows (8 chunks) c ^ (r % 8) ^ (r / 8 % 2); 64-byte rows (4 chunks)
+  // c ^ ((r / 2 ^ r / 4) % 4); both depend on r % 16 only
+  static SMEL_DEV int phys(int c, int r) {
+    if constexpr (KB == 128) return c ^ (r & 7) ^ ((r >> 3) & 1);
+    else return c ^ (((r >> 1) ^ (r >> 2)) & 3);
+  }
+  // wave-load ii of wave w (rows RPW g .. RPW g + RPW - 1, g = VM w + ii): this lane's row in the operand tile and
+  // the byte offset of the logical chunk it loads (physical chunk lane % CPR of that row)
+  static SMEL_DEV int ld_row(int vm, int w, int ii, int lane) { return RPW * (vm * w + ii) + lane / CPR; }
+  static SMEL_DEV uint32_t ld_chunk(int vm, int w, int ii, int lane) {
+    return 16u * (uint32_t)phys(lane % CPR, ld_row(vm, w, ii, lane));
+  }
 };
 
-// Lane row and swizzled chunk of wave-load ii (of a wave whose loads start at group g0 = VM * w, an even number):
-// row 8 (g0 + ii) + lane / 8, logical chunk (lane % 8) ^ swz(row) = (lane % 8) ^ (lane / 8) ^ (ii % 2).
-SMEL_DEV uint32_t ld_chunk_bytes(int lane, int ii) { return 16u * (uint32_t)((lane & 7) ^ (lane >> 3) ^ (ii & 1)); }
-
 // Row offsets (bytes from the operand base) of this lane's wave-loads, OOB for rows at or past `valid`.
-template <int VM>
+template <class R, int VM>
 SMEL_DEV void row_offsets(uint32_t (&off)[VM], int w, int lane, int valid, uint32_t pitch_bytes) {
 #pragma unroll
   for (int ii = 0; ii < VM; ++ii) {
-    const int row = 8 * (VM * w + ii) + (lane >> 3);
+    const int row = R::ld_row(VM, w, ii, lane);
     off[ii] = row < valid ? (uint32_t)row * pitch_bytes : OOB;
   }
 }
 
-// The main loop over kbytes (a multiple of 16) of every row. `pre(j)` runs for step j + 1 before that step's
-// operand loads are issued (it may issue its own loads: they retire before the next step's wait); `fix(n, j, v)`
-// transforms a B fragment of tile column n in step j as it leaves LDS.
-template <int DT, int NB, int NST, class Pre, class Fix>
-SMEL_DEV void nt_loop(f32x16_t (&acc)[4][NB], uint8_t* smem, rsrc_t ra, const uint32_t (&aoff)[Ring<NB, NST>::VM_A],
-                      rsrc_t rb, const uint32_t (&boff)[Ring<NB, NST>::VM_B], int kbytes, Pre&& pre, Fix&& fix) {
-  using R = Ring<NB, NST>;
+// The main loop over kbytes (a multiple of 16) of every row, in the k-step order rot, rot + 1, ..., nk - 1, 0, ...,
+// rot - 1: a tile's sum over k is then taken in an order fixed by `rot`, and tiles running side by side with different
+// rotations read different 128-byte columns of their rows at any moment (with row pitches that are multiples of
+// 2 KB, the rows of one column all fall on one L2 channel). `pre(kk, first)` runs before the operand loads of the
+// step after the current one are issued (kk = that step's k-step index; first: before the loop, for the first
+// step) and may issue its own loads: they retire before the next step's wait. `fix(n, kk, v)` transforms a B fragment
+// of tile column n in k-step kk as it leaves LDS.
+template <int DT, class R, int NB, class Pre, class Fix>
+SMEL_DEV void nt_loop(f32x16_t (&acc)[4][NB], uint8_t* smem, rsrc_t ra, const uint32_t (&aoff)[R::VM_A], rsrc_t rb,
+                      const uint32_t (&boff)[R::VM_B], int kbytes, int rot, Pre&& pre, Fix&& fix) {
+  constexpr int KB = R::KB, NST = R::NSTAGE;
   const int lane = lane_id(), h = lane >> 5, r32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = w & 1, wn = w >> 1;
-  const uint32_t cb0 = ld_chunk_bytes(lane, 0), cb1 = ld_chunk_bytes(lane, 1);
   const int nk = (kbytes + KB - 1) / KB;
+  if (nk <= 0) return;   // an empty K range (a half of a one-step chunk): the tile's sum is zero
+  rot = __builtin_amdgcn_readfirstlane(rot % nk);
+  auto kstep = [&](int j) { return j + rot < nk ? j + rot : j + rot - nk; };
   auto issue = [&](int j) {
     uint8_t* S = smem + (j % NST) * R::STAGE;
-    const uint32_t k0 = (uint32_t)j * KB;
+    const uint32_t k0 = (uint32_t)kstep(j) * KB;
     const bool tail = (int)k0 + KB > kbytes;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ii = 0; ii < R::VM_A; ++ii) {
-      const uint32_t cb = (ii & 1) ? cb1 : cb0;
+      const uint32_t cb = R::ld_chunk(R::VM_A, w, ii, lane);
       const bool ok = !tail || (int)(k0 + cb) + 16 <= kbytes;
       ld16_lds(ra, S + (R::VM_A * w + ii) * 1024, ok ? aoff[ii] + k0 + cb : OOB);
     }
 #pragma unroll
     for (int ii = 0; ii < R::VM_B; ++ii) {
-      const uint32_t cb = (ii & 1) ? cb1 : cb0;
+      const uint32_t cb = R::ld_chunk(R::VM_B, w, ii, lane);
       const bool ok = !tail || (int)(k0 + cb) + 16 <= kbytes;
       ld16_lds(rb, S + R::A_BYTES + (R::VM_B * w + ii) * 1024, ok ? boff[ii] + k0 + cb : OOB);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // fragment read offsets inside a stage: substep s reads logical chunk 4 h + s of its rows
-  uint32_t pcb[4];
-  const int sw = swz(r32);
+  // fragment read offsets inside a stage: substep s reads logical chunk NSUB h + s of its rows
+  uint32_t pcb[R::NSUB];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) pcb[s] = (uint32_t)r32 * KB + 16u * (uint32_t)((4 * h + s) ^ sw);
-  pre(-1);
+  for (int s = 0; s < R::NSUB; ++s) pcb[s] = (uint32_t)r32 * KB + 16u * (uint32_t)R::phys(R::NSUB * h + s, r32);
+  pre(kstep(0), true);
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s)
     if (s < nk) issue(s);
   for (int j = 0; j < nk; ++j) {
-    if (j + NST - 2 < nk) wait_vm<(NST - 2) * R::VM_STEP>();
-    else wait_vm<0>();
-    __syncthreads();
-    if (j + 1 < nk) pre(j);
+    // this wave's loads of step j have landed (later steps' may still be in flight: no __syncthreads, which would
+    // wait for all of them) and its LDS reads of the stage the next issue overwrites have returned; then the barrier
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + NST - 2 < nk) wait_vm_lds<(NST - 2) * R::VM_STEP>();
+    else wait_vm_lds<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < nk) pre(kstep(j + 1), false);
     if (j + NST - 1 < nk) issue(j + NST - 1);
+    const int kk = kstep(j);
     const uint8_t* A = smem + (j % NST) * R::STAGE + wm * 128 * KB;
     const uint8_t* B = smem + (j % NST) * R::STAGE + R::A_BYTES + wn * 32 * NB * KB;
+    // fragments in two register sets: those of substep s + 1 are read from LDS before the MFMAs of substep s are
+    // issued (the order is pinned), so their LDS latency runs under those MFMAs
+    u32x4_t af[2][4], bf[2][NB];
+    auto read = [&](int s, int set) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      u32x4_t af[4], bf[NB];
+      for (int m = 0; m < 4; ++m) af[set][m] = *reinterpret_cast<const u32x4_t*>(A + m * 32 * KB + pcb[s]);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) af[m] = *reinterpret_cast<const u32x4_t*>(A + m * 32 * KB + pcb[s]);
+      for (int n = 0; n < NB; ++n) bf[set][n] = *reinterpret_cast<const u32x4_t*>(B + n * 32 * KB + pcb[s]);
+    };
+    read(0, 0);
 #pragma unroll
-      for (int n = 0; n < NB; ++n) bf[n] = fix(n, j, *reinterpret_cast<const u32x4_t*>(B + n * 32 * KB + pcb[s]));
+    for (int s = 0; s < R::NSUB; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < R::NSUB) read(s + 1, cur ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      u32x4_t bx[NB];
+#pragma unroll
+      for (int n = 0; n < NB; ++n) bx[n] = fix(n, kk, bf[cur][n]);
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int n = 0; n < NB; ++n) mma<DT>(acc[m][n], af[m], bf[n]);
+        for (int n = 0; n < NB; ++n) mma<DT>(acc[m][n], af[cur][m], bx[n]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -213,9 +265,13 @@ struct LogitsArgs {
   int n_vt, n_tt;       // 256-column vocabulary tiles, 256-row token tiles
 };
 
+constexpr int LG_NW = SMEL_CE_LG_NW, LG_NB = 8 / (LG_NW / 2);   // waves; token slices of 32 per wave
+
 template <int DT, bool CAP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void ce_logits_kernel(LogitsArgs a) {
-  using R = Ring<4, 2>;
+__global__ __launch_bounds__(64 * LG_NW) __attribute__((amdgpu_waves_per_eu(LG_NW / 4, LG_NW / 4))) void
+ce_logits_kernel(LogitsArgs a) {
+  using R = Ring<SMEL_CE_LG_KB, LG_NB, SMEL_CE_LG_NST, LG_NW>;
+  static_assert(R::B_ROWS == 256, "256-row token tiles");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES];
   // blocks b, b + 8, ... run on one XCD: it takes vocabulary tiles x, x + 8, ... with all token tiles of each in a
   // row, so one vocabulary tile's head rows are read from that XCD's L2 by all its token tiles
@@ -234,19 +290,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const rsrc_t rb = make_rsrc(static_cast<const uint8_t*>(a.h) + (int64_t)b0 * a.ldh * E,
                               (uint64_t)(b_valid - 1) * a.ldh * E + kbytes);
   uint32_t aoff[R::VM_A], boff[R::VM_B];
-  row_offsets(aoff, w, lane, a_valid, (uint32_t)(a.ldw * E));
-  row_offsets(boff, w, lane, b_valid, (uint32_t)(a.ldh * E));
-  f32x16_t acc[4][4];
+  row_offsets<R>(aoff, w, lane, a_valid, (uint32_t)(a.ldw * E));
+  row_offsets<R>(boff, w, lane, b_valid, (uint32_t)(a.ldh * E));
+  f32x16_t acc[4][LG_NB];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[m][n] = f32x16_t{};
-  nt_loop<DT, 4, 2>(acc, smem, ra, aoff, rb, boff, kbytes, [](int) {},
+    for (int n = 0; n < LG_NB; ++n) acc[m][n] = f32x16_t{};
+  nt_loop<DT, R, LG_NB>(acc, smem, ra, aoff, rb, boff, kbytes, 5 * (b / NXCD), [](int, bool) {},
                     [](int, int, const u32x4_t& v) { return v; });
   __syncthreads();   // every wave is done with the operand ring: the epilogue may use the LDS
 
   // ---- epilogue. acc[m][n][r] = z at vocabulary column c0 + 32 m + 8 (r / 4) + 4 h + r % 4 of token row
-  // b0 + 128 wn + 32 n + r32: each token row's 128 columns of this wave (one window) are 64 values in this lane and
+  // b0 + 32 NB wn + 32 n + r32: each token row's 128 columns of this wave (one window) are 64 values in this lane and
   // 64 in lane ^ 32.
   const int c0 = a0 + 128 * wm;              // first chunk column of the window
   const int win = vt * 2 + wm;
@@ -255,8 +311,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const float inv_cap = cap != 0.f ? 1.f / cap : 0.f;
   auto col_of = [&](int m, int r) { return 32 * m + 8 * (r >> 2) + 4 * h + (r & 3); };
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    const int tok = b0 + 128 * wn + 32 * n + r32;
+  for (int n = 0; n < LG_NB; ++n) {
+    const int tok = b0 + 32 * LG_NB * wn + 32 * n + r32;
     const bool tok_ok = tok < a.n;
     float mx = -INFINITY;
 #pragma unroll
@@ -304,11 +360,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       a.win_s[(int64_t)win * a.ldn + tok] = sum;
     }
     // the target: at most one window of the whole vocabulary holds it; a wave with such a row puts its capped
-    // logits of this slice in LDS ([32 rows][129], free after the main loop) and the row's lane h = 0 reads its one
+    // logits of this slice in LDS ([32 rows][128], free after the main loop) and the row's lane h = 0 reads its one
     const int64_t tc64 = tok_ok ? a.tgt[tok] - a.v0 - c0 : -1;
     const bool here = tc64 >= 0 && tc64 < 128 && tc64 < ncol;
     if (__builtin_amdgcn_ballot_w64(here)) {
-      float* zb = reinterpret_cast<float*>(smem) + w * (32 * 129) + r32 * 129;
+      static_assert(LG_NW * 32 * 128 * 4 <= R::BYTES, "target scratch in the operand ring");
+      float* zb = reinterpret_cast<float*>(smem) + w * (32 * 128) + r32 * 128;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -326,94 +383,123 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // ------------------------------------------------------------------------------------------------ ce_grad
+// Tiles of 256 hidden x 256 token rows (the tile size sets the FLOPs per byte loaded, which bounds these GEMMs), the
+// chunk's K range split in two halves so that 4092 x 2048 outputs still give 256 workgroups: the first half adds
+// into the accumulator, acc = r (acc + part_prev) + sum_first_half, the second half writes its sum to a partial
+// buffer part[c % 2] (c = chunk index; the next chunk's first half folds it in, the finish adds the last one).
 struct GradArgs {
   const void* WT;        // transposed head [H][ldwt], column 0 = vocabulary id v0 of the chunk
   const void* P;         // softmax terms [n][ldp]
   const uint8_t* shift;  // [nwin][ldn]
   const float* r;        // accumulator rescale per row
   float* acc;            // [n][H] fp32
+  float* part;           // [2][n][H] fp32 partials of the second halves
   int64_t ldwt, ldp, ldn;
-  int H, n, kbytes, first;
-  int n_ht, n_tt;        // 256-row hidden tiles, 128-row token tiles
+  int H, n, kbytes, first, parity;
+  int n_ht, n_tt;        // 256-row hidden tiles, 256-row token tiles
 };
 
+constexpr int GR_NW = SMEL_CE_GR_NW, GR_NB = 8 / (GR_NW / 2);
+
 template <int DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void ce_grad_kernel(GradArgs a) {
-  using R = Ring<2, 3>;
+__global__ __launch_bounds__(64 * GR_NW) __attribute__((amdgpu_waves_per_eu(GR_NW / 4, GR_NW / 4))) void
+ce_grad_kernel(GradArgs a) {
+  using R = Ring<SMEL_CE_GR_KB, GR_NB, SMEL_CE_GR_NST, GR_NW>;
+  static_assert(R::B_ROWS == 256, "256-row token tiles");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES];
-  // XCD x takes a contiguous run of the tile list (token-major): the hidden tiles of one token tile run side by
-  // side on one XCD and read that token tile's softmax terms from its L2
+  // the list (half, token tile, hidden tile), XCD x a contiguous run of it: one XCD's tiles share their token
+  // tiles' softmax terms and the hidden tiles' head columns of one K half in its L2
   const int n_tiles = a.n_ht * a.n_tt;
-  int tile, unused;
-  if (!xcd_tile_chunk(n_tiles, 1, tile, unused)) return;
+  int item, unused;
+  if (!xcd_tile_chunk(2 * n_tiles, 1, item, unused)) return;
+  const int half = item / n_tiles, tile = item % n_tiles;
   const int tt = tile / a.n_ht, ht = tile % a.n_ht;
   constexpr int E = ebytes<DT>();
   const int lane = lane_id(), h = lane >> 5, r32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = w & 1, wn = w >> 1;
-  const int a0 = ht * 256, b0 = tt * 128;
-  const int a_valid = min(256, a.H - a0), b_valid = min(128, a.n - b0);
+  const int a0 = ht * 256, b0 = tt * 256;
+  const int a_valid = min(256, a.H - a0), b_valid = min(256, a.n - b0);
+  // the halves: k-steps [0, nk / 2) and [nk / 2, nk) of the chunk
+  const int nk = (a.kbytes + R::KB - 1) / R::KB;
+  const int klo = half ? (nk / 2) * R::KB : 0;
+  const int kbytes = half ? a.kbytes - klo : (nk / 2) * R::KB;
   const rsrc_t ra = make_rsrc(static_cast<const uint8_t*>(a.WT) + (int64_t)a0 * a.ldwt * E,
                               (uint64_t)(a_valid - 1) * a.ldwt * E + a.kbytes);
   const rsrc_t rb = make_rsrc(static_cast<const uint8_t*>(a.P) + (int64_t)b0 * a.ldp * E,
                               (uint64_t)(b_valid - 1) * a.ldp * E + a.kbytes);
   uint32_t aoff[R::VM_A], boff[R::VM_B];
-  row_offsets(aoff, w, lane, a_valid, (uint32_t)(a.ldwt * E));
-  row_offsets(boff, w, lane, b_valid, (uint32_t)(a.ldp * E));
-  f32x16_t acc[4][2];
+  row_offsets<R>(aoff, w, lane, a_valid, (uint32_t)(a.ldwt * E));
+  row_offsets<R>(boff, w, lane, b_valid, (uint32_t)(a.ldp * E));
+#pragma unroll
+  for (int ii = 0; ii < R::VM_A; ++ii) aoff[ii] += (uint32_t)klo;   // an OOB offset stays past the buffer
+#pragma unroll
+  for (int ii = 0; ii < R::VM_B; ++ii) boff[ii] += (uint32_t)klo;
+  f32x16_t acc[4][GR_NB];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int n = 0; n < 2; ++n) acc[m][n] = f32x16_t{};
-  // shifts of this lane's two token rows: the window of step j is j * KB / (WIN * E)
-  constexpr int STEPS_PER_WIN = WIN * E / KB;
-  const int tok0 = b0 + 64 * wn + r32;
-  uint32_t sh_cur[2] = {0, 0}, sh_next[2] = {0, 0};
-  auto load_sh = [&](int win, uint32_t (&dst)[2]) {
+    for (int n = 0; n < GR_NB; ++n) acc[m][n] = f32x16_t{};
+  // shifts of this lane's token rows: the window of k-step kk (of the chunk) is kk * KB / (WIN * E)
+  constexpr int STEPS_PER_WIN = WIN * E / R::KB;
+  const int kbase = klo / R::KB;
+  const int tok0 = b0 + 32 * GR_NB * wn + r32;
+  uint32_t sh_cur[GR_NB], sh_next[GR_NB];
+  auto load_sh = [&](int win, uint32_t (&dst)[GR_NB]) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
+    for (int n = 0; n < GR_NB; ++n) {
       const int tok = tok0 + 32 * n;
       dst[n] = tok < a.n ? (uint32_t)a.shift[(int64_t)win * a.ldn + tok] : (uint32_t)SHIFT_ZERO;
     }
   };
-  auto pre = [&](int j) {   // j = -1: before the first step; else during step j, for step j + 1
-    if (j < 0) {
-      load_sh(0, sh_cur);
-    } else if ((j + 1) % STEPS_PER_WIN == 0) {
-      load_sh((j + 1) / STEPS_PER_WIN, sh_next);
+  int cur_win = 0;
+  auto pre = [&](int kk, bool first) {   // the shifts of k-step kk's window, loaded where a window starts
+    const int kg = kbase + kk;
+    if (first) {
+      cur_win = kg / STEPS_PER_WIN;
+      load_sh(cur_win, sh_cur);
+    } else if (kg % STEPS_PER_WIN == 0) {
+      load_sh(kg / STEPS_PER_WIN, sh_next);
     }
   };
-  int cur_win = 0;
-  auto fix = [&](int n, int j, const u32x4_t& v) {
-    const int wj = j / STEPS_PER_WIN;
+  auto fix = [&](int n, int kk, const u32x4_t& v) {
+    const int wj = (kbase + kk) / STEPS_PER_WIN;
     if (n == 0 && wj != cur_win) {
       cur_win = wj;
-      sh_cur[0] = sh_next[0];
-      sh_cur[1] = sh_next[1];
+#pragma unroll
+      for (int q = 0; q < GR_NB; ++q) sh_cur[q] = sh_next[q];
     }
     return shift_chunk<DT>(v, sh_cur[n]);
   };
-  nt_loop<DT, 2, 3>(acc, smem, ra, aoff, rb, boff, a.kbytes, pre, fix);
+  nt_loop<DT, R, GR_NB>(acc, smem, ra, aoff, rb, boff, kbytes, 5 * (int)(blockIdx.x / NXCD), pre, fix);
 
   // ---- epilogue: acc[m][n][r] = term of hidden column a0 + 128 wm + 32 m + 8 (r / 4) + 4 h + r % 4 and token
-  // row tok0 + 32 n: 16-byte runs of 4 columns, added to r acc (or written on the first chunk)
+  // row tok0 + 32 n: 16-byte runs of 4 columns
+  const size_t nh = (size_t)a.n * a.H;
+  const float* prev = a.part + (size_t)(a.parity ^ 1) * nh;
+  float* mine = a.part + (size_t)a.parity * nh;
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+  for (int n = 0; n < GR_NB; ++n) {
     const int tok = tok0 + 32 * n;
     if (tok >= a.n) continue;
     const float rr = a.first ? 0.f : a.r[tok];
-    float* row = a.acc + (int64_t)tok * a.H;
+    const size_t row = (size_t)tok * a.H;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int col = a0 + 128 * wm + 32 * m + 8 * q + 4 * h;
         if (col >= a.H) continue;
-        f32x4_t* dst = reinterpret_cast<f32x4_t*>(row + col);
         f32x4_t v = {acc[m][n][4 * q], acc[m][n][4 * q + 1], acc[m][n][4 * q + 2], acc[m][n][4 * q + 3]};
+        if (half) {
+          *reinterpret_cast<f32x4_t*>(mine + row + col) = v;
+          continue;
+        }
+        f32x4_t* dst = reinterpret_cast<f32x4_t*>(a.acc + row + col);
         if (!a.first) {
-          const f32x4_t o = *dst;
-          v = f32x4_t{fmaf(o[0], rr, v[0]), fmaf(o[1], rr, v[1]), fmaf(o[2], rr, v[2]), fmaf(o[3], rr, v[3])};
+          const f32x4_t o = *dst, p = *reinterpret_cast<const f32x4_t*>(prev + row + col);
+          v = f32x4_t{fmaf(o[0] + p[0], rr, v[0]), fmaf(o[1] + p[1], rr, v[1]), fmaf(o[2] + p[2], rr, v[2]),
+                      fmaf(o[3] + p[3], rr, v[3])};
         }
         *dst = v;
       }
@@ -433,26 +519,29 @@ __global__ __launch_bounds__(256) void ce_begin_kernel(float* m, float* s, float
 
 SMEL_DEV float pow2i(float e) { return ldexpf(1.f, (int)e); }
 
-// 64 rows per block, 4 threads per row (windows w = q mod 4), partial results combined in fixed order
+// 16 rows per block, 16 threads per row (windows w = q mod 16): per-thread partial maxima and sums combined in fixed
+// order through LDS
+constexpr int ST_ROWS = 16, ST_Q = 16;
 __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__ win_e, const float* __restrict__ win_s,
                                                        int nwin, int64_t ldn, int64_t n, float* m, float* s,
                                                        uint8_t* shift, float* r_out) {
-  __shared__ float red[4][64];
-  const int q = threadIdx.x >> 6, t = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 64 + t;
+  __shared__ float red[ST_Q][ST_ROWS];
+  const int q = threadIdx.x / ST_ROWS, t = threadIdx.x % ST_ROWS;
+  const int64_t row = (int64_t)blockIdx.x * ST_ROWS + t;
   const bool ok = row < n;
   float E = -INFINITY;
   if (ok)
-    for (int w = q; w < nwin; w += 4) E = fmaxf(E, win_e[(int64_t)w * ldn + row]);
+    for (int w = q; w < nwin; w += ST_Q) E = fmaxf(E, win_e[(int64_t)w * ldn + row]);
   red[q][t] = E;
   __syncthreads();
-  E = fmaxf(fmaxf(red[0][t], red[1][t]), fmaxf(red[2][t], red[3][t]));
+#pragma unroll
+  for (int k = 0; k < ST_Q; ++k) E = fmaxf(E, red[k][t]);
   __syncthreads();
   const float mo = ok ? m[row] : -INFINITY;
   const float nE = fmaxf(mo, E);   // finite: every chunk has a valid column
   float S = 0.f;
   if (ok)
-    for (int w = q; w < nwin; w += 4) {
+    for (int w = q; w < nwin; w += ST_Q) {
       const float e = win_e[(int64_t)w * ldn + row];
       int sh = SHIFT_ZERO;
       if (e != -INFINITY) {
@@ -465,7 +554,9 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__
   red[q][t] = S;
   __syncthreads();
   if (q == 0 && ok) {
-    S = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+    S = 0.f;
+#pragma unroll
+    for (int k = 0; k < ST_Q; ++k) S += red[k][t];
     const float r = mo == -INFINITY ? 0.f : ldexpf(1.f, -(int)fminf(nE - mo, 300.f));
     s[row] = s[row] * r + S;
     m[row] = nE;
@@ -491,7 +582,8 @@ SMEL_DEV void st_t(void* p, int64_t i, float v) {
 template <int DT, int GT>
 __global__ __launch_bounds__(256) void ce_finish_kernel(const float* __restrict__ m, const float* __restrict__ s,
                                                         const float* __restrict__ tz, const float* __restrict__ td,
-                                                        const float* __restrict__ acc, const void* __restrict__ W,
+                                                        const float* __restrict__ acc,
+                                                        const float* __restrict__ part, const void* __restrict__ W,
                                                         int64_t ldw, const void* __restrict__ trows,
                                                         const int64_t* __restrict__ tgt, int64_t V, int64_t H,
                                                         float gscale, void* g, int64_t ldg, float* loss_rows) {
@@ -506,7 +598,7 @@ __global__ __launch_bounds__(256) void ce_finish_kernel(const float* __restrict_
   const int64_t wrow = trows ? row * H : (ok ? t : 0) * ldw;
   for (int64_t c = threadIdx.x; c < H; c += 256) {
     const float wv = ok ? ld_t<DT>(wsrc, wrow + c) : 0.f;
-    const float v = acc[row * H + c] * inv - d * wv;
+    const float v = (acc[row * H + c] + (part ? part[row * H + c] : 0.f)) * inv - d * wv;
     st_t<GT>(g, row * ldg + c, v * gscale);
   }
 }
@@ -618,7 +710,7 @@ extern "C" int smel_ce_logits(const void* W, int64_t ldw, int64_t vc, int64_t v0
   a.n_tt = (int)((n + 255) / 256);
   const int64_t blocks = xcd_grid(a.n_vt) * a.n_tt;
   SMEL_REQUIRE(blocks < INT32_MAX, SMEL_EUNSUPPORTED, "ce_logits: grid too large");
-  const dim3 g((unsigned)blocks), b(256);
+  const dim3 g((unsigned)blocks), b(64 * LG_NW);
   const bool cap = softcap != 0.f;
   if (dtype == 0 && cap) ce_logits_kernel<0, true><<<g, b, 0, stream>>>(a);
   else if (dtype == 0) ce_logits_kernel<0, false><<<g, b, 0, stream>>>(a);
@@ -635,25 +727,25 @@ extern "C" int smel_ce_stats(const float* win_e, const float* win_s, int64_t nwi
   if (n == 0) return 0;
   SMEL_REQUIRE(win_e && win_s && m && s && shift && r, SMEL_EINVAL, "ce_stats: null pointer");
   SMEL_REQUIRE(nwin < INT32_MAX, SMEL_EUNSUPPORTED, "ce_stats: too many windows");
-  ce_stats_kernel<<<dim3((unsigned)((n + 63) / 64)), dim3(256), 0, stream>>>(win_e, win_s, (int)nwin, ldn, n, m, s,
-                                                                           shift, r);
+  ce_stats_kernel<<<dim3((unsigned)((n + ST_ROWS - 1) / ST_ROWS)), dim3(256), 0, stream>>>(win_e, win_s, (int)nwin,
+                                                                                        ldn, n, m, s, shift, r);
   return smel::launch_status();
 }
 
 extern "C" int smel_ce_grad(const void* WT, int64_t ldwt, int64_t H, const void* P, int64_t ldp, int64_t vc,
-                            const uint8_t* shift, int64_t ldn, const float* r, int64_t n, int32_t dtype, int32_t first,
-                            float* acc, hipStream_t stream) {
+                            const uint8_t* shift, int64_t ldn, const float* r, int64_t n, int32_t dtype, int32_t chunk,
+                            float* acc, float* part, hipStream_t stream) {
   SMEL_REQUIRE(SMEL_DT_OK(dtype), SMEL_EINVAL, "ce_grad: dtype %d (0 bf16, 1 fp32, 2 fp16)", dtype);
   const int E = dtype == 1 ? 4 : 2;
-  SMEL_REQUIRE(n >= 0 && vc >= 1 && H >= 1 && ldn >= n, SMEL_EINVAL, "ce_grad: bad sizes");
+  SMEL_REQUIRE(n >= 0 && vc >= 1 && H >= 1 && ldn >= n && chunk >= 0, SMEL_EINVAL, "ce_grad: bad sizes");
   if (n == 0) return 0;
-  SMEL_REQUIRE(WT && P && shift && acc && (first || r), SMEL_EINVAL, "ce_grad: null pointer");
+  SMEL_REQUIRE(WT && P && shift && acc && part && (chunk == 0 || r), SMEL_EINVAL, "ce_grad: null pointer");
   const int64_t kbytes = (vc * E + 15) / 16 * 16;
-  SMEL_REQUIRE(H % 4 == 0 && aligned16(acc) && aligned16(WT) && aligned16(P) && (ldwt * E) % 16 == 0 &&
-                   (ldp * E) % 16 == 0 && ldp * E >= kbytes && ldwt * E >= kbytes,
+  SMEL_REQUIRE(H % 4 == 0 && aligned16(acc) && aligned16(part) && aligned16(WT) && aligned16(P) &&
+                   (ldwt * E) % 16 == 0 && (ldp * E) % 16 == 0 && ldp * E >= kbytes && ldwt * E >= kbytes,
                SMEL_EUNSUPPORTED, "ce_grad: rows must be 16-byte aligned runs covering the chunk (H=%lld)",
                (long long)H);
-  SMEL_REQUIRE((ldwt * E) * 256 < ((int64_t)1 << 31) && (ldp * E) * 128 < ((int64_t)1 << 31) && H < INT32_MAX &&
+  SMEL_REQUIRE((ldwt * E) * 256 < ((int64_t)1 << 31) && (ldp * E) * 256 < ((int64_t)1 << 31) && H < INT32_MAX &&
                    n < INT32_MAX,
                SMEL_EUNSUPPORTED, "ce_grad: tile offsets exceed 31 bits");
   GradArgs a;
@@ -662,18 +754,20 @@ extern "C" int smel_ce_grad(const void* WT, int64_t ldwt, int64_t H, const void*
   a.shift = shift;
   a.r = r;
   a.acc = acc;
+  a.part = part;
   a.ldwt = ldwt;
   a.ldp = ldp;
   a.ldn = ldn;
   a.H = (int)H;
   a.n = (int)n;
   a.kbytes = (int)kbytes;
-  a.first = first ? 1 : 0;
+  a.first = chunk == 0;
+  a.parity = chunk & 1;
   a.n_ht = (int)((H + 255) / 256);
-  a.n_tt = (int)((n + 127) / 128);
-  const int64_t tiles = (int64_t)a.n_ht * a.n_tt;
-  SMEL_REQUIRE(tiles < INT32_MAX, SMEL_EUNSUPPORTED, "ce_grad: grid too large");
-  const dim3 g((unsigned)xcd_grid(tiles)), b(256);
+  a.n_tt = (int)((n + 255) / 256);
+  const int64_t items = 2 * (int64_t)a.n_ht * a.n_tt;
+  SMEL_REQUIRE(items < INT32_MAX, SMEL_EUNSUPPORTED, "ce_grad: grid too large");
+  const dim3 g((unsigned)xcd_grid(items)), b(64 * GR_NW);
   if (dtype == 0) ce_grad_kernel<0><<<g, b, 0, stream>>>(a);
   else if (dtype == 1) ce_grad_kernel<1><<<g, b, 0, stream>>>(a);
   else ce_grad_kernel<2><<<g, b, 0, stream>>>(a);
@@ -681,7 +775,7 @@ extern "C" int smel_ce_grad(const void* WT, int64_t ldwt, int64_t H, const void*
 }
 
 extern "C" int smel_ce_finish(const float* m, const float* s, const float* tz, const float* td, const float* acc,
-                              const void* W, int64_t ldw, const void* trows, const int64_t* tgt, int64_t V, int64_t n,
+                              const float* part, const void* W, int64_t ldw, const void* trows, const int64_t* tgt, int64_t V, int64_t n,
                               int64_t H, int32_t dtype, float gscale, void* g, int64_t ldg, int32_t g_dtype,
                               float* loss_rows, hipStream_t stream) {
   SMEL_REQUIRE(SMEL_DT_OK(dtype) && SMEL_DT_OK(g_dtype), SMEL_EINVAL, "ce_finish: dtype %d / %d", dtype, g_dtype);
@@ -692,7 +786,8 @@ extern "C" int smel_ce_finish(const float* m, const float* s, const float* tz, c
   SMEL_REQUIRE(n < INT32_MAX, SMEL_EUNSUPPORTED, "ce_finish: too many rows");
   const dim3 gr((unsigned)n), b(256);
 #define SMEL_FIN(D, G) \
-  ce_finish_kernel<D, G><<<gr, b, 0, stream>>>(m, s, tz, td, acc, W, ldw, trows, tgt, V, H, gscale, g, ldg, loss_rows)
+  ce_finish_kernel<D, G><<<gr, b, 0, stream>>>(m, s, tz, td, acc, part, W, ldw, trows, tgt, V, H, gscale, g, ldg, \
+                                               loss_rows)
 #define SMEL_FIN_G(D)            \
   if (g_dtype == 0) SMEL_FIN(D, 0); \
   else if (g_dtype == 1) SMEL_FIN(D, 1); \

@@ -108,8 +108,8 @@ SIGNATURES = {
     "smel_ce_begin": (i32, [vp, vp, vp, vp, vp, i64, vp]),
     "smel_ce_logits": (i32, [vp, i64, i64, i64, vp, i64, i64, i64, vp, f32, i32, vp, i64, vp, vp, i64, vp, vp, vp]),
     "smel_ce_stats": (i32, [vp, vp, i64, i64, i64, vp, vp, vp, vp, vp]),
-    "smel_ce_grad": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, vp, i64, i32, i32, vp, vp]),
-    "smel_ce_finish": (i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, f32, vp, i64, i32, vp, vp]),
+    "smel_ce_grad": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, vp, i64, i32, i32, vp, vp, vp]),
+    "smel_ce_finish": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, f32, vp, i64, i32, vp, vp]),
     "smel_ce_loss_sum": (i32, [vp, i64, f32, i32, vp, vp]),
     "smel_ce_scale": (i32, [vp, i64, i32, vp, vp]),
     "smel_ce_transpose": (i32, [vp, i64, i64, i64, vp, i64, i32, vp]),

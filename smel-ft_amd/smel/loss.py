@@ -8,8 +8,9 @@ Structure here:
     of exponentials, the softmax terms written in the rows' dtype, the target's logit), ``smel_ce_stats`` folds the
     windows into each row's running maximum and sum (every rescale an exact power of two) and ``smel_ce_grad`` runs
     the gradient GEMM p W on MFMA, shifting each fragment of p to the running maximum as it is loaded and adding into
-    the fp32 accumulator rescaled by the same power of two; ``smel_ce_finish`` writes the loss rows and the gradient
-    rows (acc / s - d W[target], scaled), ``smel_ce_loss_sum`` their sum;
+    the fp32 accumulator rescaled by the same power of two (the chunk's columns in two halves, the second half's sum
+    kept apart and folded in by the next chunk); ``smel_ce_finish`` writes the loss rows and the gradient rows
+    (acc / s - d W[target], scaled), ``smel_ce_loss_sum`` their sum;
   * the gradient GEMM reads the head transposed ([H][V]): a dense head whose dtype is the rows' is transposed once
     and kept with the head (it is frozen); other heads (int8, or another dtype) are converted per vocabulary chunk,
     as the reference's ``rows()`` does, and that chunk is transposed;
@@ -171,6 +172,8 @@ class _Pass:
         self.shift = torch.empty(nwin, n, dtype=torch.uint8, device=device)
         self.P = torch.empty(n, vcp, dtype=dtype, device=device) if need_grad else None
         self.acc = f(n, H) if need_grad else None
+        self.part = f(2, n, H) if need_grad else None     # the second K halves' partials, by chunk parity
+        self.last = 0                                       # chunks of the last sweep
 
 
 def _sweep(h, head: LMHead, tgt, need_grad: bool, ps: _Pass, m0=None):
@@ -201,7 +204,8 @@ def _sweep(h, head: LMHead, tgt, need_grad: bool, ps: _Pass, m0=None):
                 L.call("smel_ce_transpose", p(W), vc, H, ldw, p(WT), WT.stride(0), dt, st)
                 ldwt = WT.stride(0)
             L.call("smel_ce_grad", p(WT), ldwt, H, p(ps.P), ps.P.stride(0), vc, p(ps.shift), n, p(ps.r), n, dt,
-                   int(i == 0), p(ps.acc), st)
+                   i, p(ps.acc), p(ps.part), st)
+    ps.last = len(chunks) - 1
 
 
 def _finish(h, head: LMHead, tgt, ps: _Pass, need_grad: bool, gscale: float = 1.0, g=None):
@@ -220,9 +224,10 @@ def _finish(h, head: LMHead, tgt, ps: _Pass, need_grad: bool, gscale: float = 1.
             trows = head.rows_at(torch.where(ok, tgt, torch.zeros_like(tgt)), h.dtype).contiguous()
         if g is None:
             g = torch.empty(n, H, dtype=torch.float32, device=h.device)
-    L.call("smel_ce_finish", p(ps.m), p(ps.s), p(ps.tz), p(ps.td), p(ps.acc), p(W), ldw, p(trows), p(tgt), head.vocab,
-           n, H, dt, float(gscale), p(g), g.stride(0) if g is not None else 0, _DT[g.dtype] if g is not None else 0,
-           p(ps.loss), L.stream())
+    part = ps.part[ps.last % 2] if need_grad else None
+    L.call("smel_ce_finish", p(ps.m), p(ps.s), p(ps.tz), p(ps.td), p(ps.acc), p(part), p(W), ldw, p(trows), p(tgt),
+           head.vocab, n, H, dt, float(gscale), p(g), g.stride(0) if g is not None else 0,
+           _DT[g.dtype] if g is not None else 0, p(ps.loss), L.stream())
     return g
 
 

@@ -55,13 +55,14 @@ def test_ce_entry_points_reject_bad_arguments():
     assert lg(*ok[:12], 300, *ok[13:], None) == EINVAL                      # softmax rows shorter than 512
     assert lg(*ok[:15], 3, *ok[16:], None) == EINVAL                        # statistics pitch below n
     assert lg(*ok[:6], 0, *ok[7:], None) == 0                               # no rows: nothing to do
-    gr = L.smel_ce_grad     # WT ldwt H P ldp vc shift ldn r n dtype first acc stream
-    assert gr(fake, 512, 66, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, None) == EUNSUP   # H % 4
-    assert gr(fake, 512, 64, None, 512, 300, fake, 4, fake, 4, 0, 0, fake, None) == EINVAL   # no softmax terms
-    assert gr(fake, 256, 64, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, None) == EUNSUP   # head rows too short
-    assert gr(fake, 512, 64, fake, 512, 300, fake, 4, None, 4, 0, 0, fake, None) == EINVAL   # no rescale
+    gr = L.smel_ce_grad     # WT ldwt H P ldp vc shift ldn r n dtype chunk acc part stream
+    assert gr(fake, 512, 66, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, fake, None) == EUNSUP   # H % 4
+    assert gr(fake, 512, 64, None, 512, 300, fake, 4, fake, 4, 0, 0, fake, fake, None) == EINVAL   # no softmax terms
+    assert gr(fake, 256, 64, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, fake, None) == EUNSUP  # head rows short
+    assert gr(fake, 512, 64, fake, 512, 300, fake, 4, None, 4, 0, 1, fake, fake, None) == EINVAL   # no rescale
+    assert gr(fake, 512, 64, fake, 512, 300, fake, 4, fake, 4, 0, 0, fake, None, None) == EINVAL   # no partials
     assert L.smel_ce_stats(fake, fake, 0, 4, 4, fake, fake, fake, fake, None) == EINVAL         # no windows
-    assert L.smel_ce_finish(fake, fake, fake, fake, None, None, 0, None, fake, 10, 4, 64, 5, 1.0, None, 0, 0,
+    assert L.smel_ce_finish(fake, fake, fake, fake, None, None, None, 0, None, fake, 10, 4, 64, 5, 1.0, None, 0, 0,
                             fake, None) == EINVAL                                               # dtype
     assert L.smel_ce_transpose(fake, 4, 64, 32, fake, 8, 0, None) == EINVAL                    # pitch < columns
     assert L.smel_ce_scale(fake, 8, 3, fake, None) == EINVAL
