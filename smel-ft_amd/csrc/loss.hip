@@ -1,24 +1,27 @@
 // Single-pass chunked cross-entropy over a frozen lm_head (smel/loss.py:50-156), both GEMMs on MFMA.
 //
 // Per vocabulary chunk [v0, v0 + vc) and pass of n token rows:
-//   ce_logits  (MFMA, 256 vocabulary x 256 token tile): z = h W_c^T rounded to the rows' dtype (the reference's
-//              `(h @ W.t())`), capped (z -> c tanh(z / c)), and per window of 128 columns and token row the
-//              window's maximum rounded up to a whole power of two, e = ceil(max z * log2 e), the sum of
+//   ce_logits  (MFMA, 256 vocabulary x 256 token tile, 8 waves): z = h W_c^T rounded to the rows' dtype (the
+//              reference's `(h @ W.t())`), capped (z -> c tanh(z / c)), and per window of 128 columns and token row
+//              the window's maximum rounded up to a whole power of two, e = ceil(max z * log2 e), the sum of
 //              exp(z - e ln 2) and the softmax terms p = exp(z - e ln 2) (times the cap derivative 1 - (z / c)^2) in
 //              the rows' dtype, [n][vc] row-major; the target's capped logit and cap derivative where the target
 //              lies in the tile. The logits never reach memory.
 //   ce_stats   per row: chunk maximum E = max e, chunk sum, the running maximum nE = max(m, E) and sum
 //              s = s 2^(m - nE) + sum_w s_w 2^(e_w - nE), the accumulator's rescale r = 2^(m - nE), and per window
 //              the shift nE - e_w of its softmax terms. Every rescale is an exact power of two.
-//   ce_grad    (MFMA, 256 hidden x 128 token tile, K = the chunk's columns): acc = r acc + sum_v p'_v W_v with
+//   ce_grad    (MFMA, 256 hidden x 256 token tile, 8 waves, the chunk's columns in two K halves):
+//              acc = r (acc + part_prev) + sum_v p'_v W_v over the first half, part = the second half's sum, with
 //              p' = p 2^-(shift): each 16-byte fragment of p is shifted in registers as it leaves LDS (bf16: one
 //              saturating 16-bit subtract of the exponent per value pair; fp16 / fp32: ldexp), so the products are
 //              the reference's `p.to(h.dtype) @ W` terms at the running maximum (smel/loss.py:85).
-//   ce_finish  per row: loss = nE ln 2 + log s - z_target, gradient row = acc / s - d_target W[target]
+//   ce_finish  per row: loss = nE ln 2 + log s - z_target, gradient row = (acc + part) / s - d_target W[target]
 //              (smel/loss.py:87-92), scaled and stored in the requested dtype; ce_loss_sum adds the rows' losses
 //              in fixed order.
 // The head operand of ce_grad is the head transposed ([H][V], one copy per frozen head, made by ce_transpose), so
 // both GEMMs read K-contiguous rows. No atomics: every output element has one writer and fixed-order sums.
+// Both GEMMs are bound by the rate at which a CU brings operands in from L2 (about 14 B per clock here), so their
+// tiles are the largest the registers hold (256 x 256, 131 FLOP per loaded byte in bf16).
 #include <algorithm>
 
 #include "../../include/smel_loss.h"
@@ -28,8 +31,8 @@
 namespace {
 
 constexpr int WIN = 128;    // vocabulary columns of one statistics window
-// k-step bytes and ring stages of the two GEMMs (the logits GEMM's stage: 256 + 256 rows, the gradient GEMM's:
-// 256 + 128 rows)
+// build-time tuning of the two GEMMs: k-step bytes, ring stages (a stage holds 256 + 256 rows) and waves per block;
+// deeper rings and 64-byte k-steps measured no faster
 #ifndef SMEL_CE_LG_KB
 #define SMEL_CE_LG_KB 128
 #define SMEL_CE_LG_NST 2
@@ -273,9 +276,9 @@ ce_logits_kernel(LogitsArgs a) {
   using R = Ring<SMEL_CE_LG_KB, LG_NB, SMEL_CE_LG_NST, LG_NW>;
   static_assert(R::B_ROWS == 256, "256-row token tiles");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES];
+  const int b = blockIdx.x, x = b % NXCD, jj = b / NXCD;
   // blocks b, b + 8, ... run on one XCD: it takes vocabulary tiles x, x + 8, ... with all token tiles of each in a
   // row, so one vocabulary tile's head rows are read from that XCD's L2 by all its token tiles
-  const int b = blockIdx.x, x = b % NXCD, jj = b / NXCD;
   const int tt = jj % a.n_tt, vt = (jj / a.n_tt) * NXCD + x;
   if (vt >= a.n_vt) return;
   constexpr int E = ebytes<DT>();
