@@ -23,6 +23,7 @@
 // Both GEMMs are bound by the rate at which a CU brings operands in from L2 (about 14 B per clock here), so their
 // tiles are the largest the registers hold (256 x 256, 131 FLOP per loaded byte in bf16).
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/smel_loss.h"
 #include "abi_util.h"
@@ -295,6 +296,14 @@ ce_logits_kernel(LogitsArgs a) {
   uint32_t aoff[R::VM_A], boff[R::VM_B];
   row_offsets<R>(aoff, w, lane, a_valid, (uint32_t)(a.ldw * E));
   row_offsets<R>(boff, w, lane, b_valid, (uint32_t)(a.ldh * E));
+  // this lane's token rows' targets, loaded before the main loop (the epilogue would wait on them)
+  int tg[LG_NB];   // target - v0 - c0 (the window's first column), -1 when outside [0, 2^31)
+#pragma unroll
+  for (int n = 0; n < LG_NB; ++n) {
+    const int tok = b0 + 32 * LG_NB * wn + 32 * n + r32;
+    const int64_t t = tok < a.n ? a.tgt[tok] - a.v0 - (a0 + 128 * wm) : -1;
+    tg[n] = t >= 0 && t < INT32_MAX ? (int)t : -1;
+  }
   f32x16_t acc[4][LG_NB];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
@@ -313,8 +322,9 @@ ce_logits_kernel(LogitsArgs a) {
   const float cap = a.cap;
   const float inv_cap = cap != 0.f ? 1.f / cap : 0.f;
   auto col_of = [&](int m, int r) { return 32 * m + 8 * (r >> 2) + 4 * h + (r & 3); };
-#pragma unroll
-  for (int n = 0; n < LG_NB; ++n) {
+  // FULL: every column of the window lies in the chunk (all tiles but the chunk's last): no masking
+  auto slice = [&](int n, auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
     const int tok = b0 + 32 * LG_NB * wn + 32 * n + r32;
     const bool tok_ok = tok < a.n;
     float mx = -INFINITY;
@@ -324,7 +334,8 @@ ce_logits_kernel(LogitsArgs a) {
       for (int r = 0; r < 16; ++r) {
         float z = round_t<DT>(acc[m][n][r]);
         if constexpr (CAP) z = cap * tanhf(z * inv_cap);
-        if (ncol < 128 && col_of(m, r) >= ncol) z = -INFINITY;
+        if constexpr (!FULL)
+          if (col_of(m, r) >= ncol) z = -INFINITY;
         acc[m][n][r] = z;
         mx = fmaxf(mx, z);
       }
@@ -341,10 +352,12 @@ ce_logits_kernel(LogitsArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float z = acc[m][n][4 * q + i];
-          const bool live = z != -INFINITY;
-          const float ez = live ? __builtin_amdgcn_exp2f(fmaf(z, LOG2E, ne)) : 0.f;
+          float ez;
+          if constexpr (FULL) ez = __builtin_amdgcn_exp2f(fmaf(z, LOG2E, ne));
+          else ez = z != -INFINITY ? __builtin_amdgcn_exp2f(fmaf(z, LOG2E, ne)) : 0.f;
           sum += ez;
-          p[i] = CAP && live ? ez * (1.f - (z * inv_cap) * (z * inv_cap)) : ez;
+          if constexpr (CAP) p[i] = (FULL || z != -INFINITY) ? ez * (1.f - (z * inv_cap) * (z * inv_cap)) : 0.f;
+          else p[i] = ez;
         }
         if (prow && tok_ok) {
           uint8_t* dst = prow + (32 * m + 8 * q + 4 * h) * E;
@@ -364,7 +377,7 @@ ce_logits_kernel(LogitsArgs a) {
     }
     // the target: at most one window of the whole vocabulary holds it; a wave with such a row puts its capped
     // logits of this slice in LDS ([32 rows][128], free after the main loop) and the row's lane h = 0 reads its one
-    const int64_t tc64 = tok_ok ? a.tgt[tok] - a.v0 - c0 : -1;
+    const int tc64 = tok_ok ? tg[n] : -1;
     const bool here = tc64 >= 0 && tc64 < 128 && tc64 < ncol;
     if (__builtin_amdgcn_ballot_w64(here)) {
       static_assert(LG_NW * 32 * 128 * 4 <= R::BYTES, "target scratch in the operand ring");
@@ -382,6 +395,13 @@ ce_logits_kernel(LogitsArgs a) {
         a.td[tok] = CAP ? 1.f - (zt * inv_cap) * (zt * inv_cap) : 1.f;
       }
     }
+  };
+  if (ncol >= 128) {
+#pragma unroll
+    for (int n = 0; n < LG_NB; ++n) slice(n, std::true_type{});
+  } else {
+#pragma unroll
+    for (int n = 0; n < LG_NB; ++n) slice(n, std::false_type{});
   }
 }
 
