@@ -344,6 +344,10 @@ ce_logits_kernel(LogitsArgs a) {
     const float ne = mx == -INFINITY ? 0.f : -e;
     float sum = 0.f;
     uint8_t* prow = a.P ? static_cast<uint8_t*>(a.P) + ((int64_t)tok * a.ldp + c0) * E : nullptr;
+    // 16-bit terms go through this wave's LDS region first ([32 rows][272 B]), then out as whole 256-byte row
+    // segments (16 lanes per row, 16 B each); fp32 terms are stored directly
+    uint8_t* stg = smem + w * 16384;
+    constexpr int SP = 272;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -359,17 +363,27 @@ ce_logits_kernel(LogitsArgs a) {
           if constexpr (CAP) p[i] = (FULL || z != -INFINITY) ? ez * (1.f - (z * inv_cap) * (z * inv_cap)) : 0.f;
           else p[i] = ez;
         }
-        if (prow && tok_ok) {
-          uint8_t* dst = prow + (32 * m + 8 * q + 4 * h) * E;
-          if constexpr (DT == 0) {
-            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2bf(p[0], p[1]), pack2bf(p[2], p[3])};
-          } else if constexpr (DT == 2) {
-            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2h(p[0], p[1]), pack2h(p[2], p[3])};
-          } else {
-            *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{p[0], p[1], p[2], p[3]};
-          }
+        if constexpr (DT == 1) {
+          if (prow && tok_ok)
+            *reinterpret_cast<f32x4_t*>(prow + (32 * m + 8 * q + 4 * h) * E) = f32x4_t{p[0], p[1], p[2], p[3]};
+        } else {
+          uint8_t* d = stg + r32 * SP + (32 * m + 8 * q + 4 * h) * 2;
+          if constexpr (DT == 0) *reinterpret_cast<u32x2_t*>(d) = u32x2_t{pack2bf(p[0], p[1]), pack2bf(p[2], p[3])};
+          else *reinterpret_cast<u32x2_t*>(d) = u32x2_t{pack2h(p[0], p[1]), pack2h(p[2], p[3])};
         }
       }
+    if constexpr (DT != 1) {
+      if (a.P) {   // the slice's 32 token rows x 256 B: chunk k = 64 j + lane is row k / 16, 16-byte piece k % 16
+        const int tok_s = b0 + 32 * LG_NB * wn + 32 * n;
+        uint8_t* pbase = static_cast<uint8_t*>(a.P) + ((int64_t)tok_s * a.ldp + c0) * E;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int k = 64 * j + lane, row = k >> 4, piece = k & 15;
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stg + row * SP + piece * 16);
+          if (tok_s + row < a.n) *reinterpret_cast<u32x4_t*>(pbase + (int64_t)row * a.ldp * E + piece * 16) = v;
+        }
+      }
+    }
     sum += __shfl_xor(sum, 32, 64);
     if (h == 0 && tok_ok) {
       a.win_e[(int64_t)win * a.ldn + tok] = e;
@@ -380,8 +394,8 @@ ce_logits_kernel(LogitsArgs a) {
     const int tc64 = tok_ok ? tg[n] : -1;
     const bool here = tc64 >= 0 && tc64 < 128 && tc64 < ncol;
     if (__builtin_amdgcn_ballot_w64(here)) {
-      static_assert(LG_NW * 32 * 128 * 4 <= R::BYTES, "target scratch in the operand ring");
-      float* zb = reinterpret_cast<float*>(smem) + w * (32 * 128) + r32 * 128;
+      static_assert(LG_NW * 16384 <= R::BYTES, "per-wave staging / target scratch in the operand ring");
+      float* zb = reinterpret_cast<float*>(smem + w * 16384) + r32 * 128;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
