@@ -556,9 +556,10 @@ __global__ __launch_bounds__(256) void ce_begin_kernel(float* m, float* s, float
 
 SMEL_DEV float pow2i(float e) { return ldexpf(1.f, (int)e); }
 
-// 16 rows per block, 16 threads per row (windows w = q mod 16): per-thread partial maxima and sums combined in fixed
-// order through LDS
-constexpr int ST_ROWS = 16, ST_Q = 16;
+// 16 rows per block, 16 threads per row (windows w = q mod 16): each thread loads its windows' maxima and sums once
+// (up to ST_W of them in registers, any further ones again from memory), partial maxima and sums are combined in
+// fixed order through LDS
+constexpr int ST_ROWS = 16, ST_Q = 16, ST_W = 16;
 __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__ win_e, const float* __restrict__ win_s,
                                                        int nwin, int64_t ldn, int64_t n, float* m, float* s,
                                                        uint8_t* shift, float* r_out) {
@@ -566,9 +567,18 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__
   const int q = threadIdx.x / ST_ROWS, t = threadIdx.x % ST_ROWS;
   const int64_t row = (int64_t)blockIdx.x * ST_ROWS + t;
   const bool ok = row < n;
+  float ev[ST_W], sv[ST_W];
   float E = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < ST_W; ++i) {
+    const int w = q + ST_Q * i;
+    const bool in = ok && w < nwin;
+    ev[i] = in ? win_e[(int64_t)w * ldn + row] : -INFINITY;
+    sv[i] = in ? win_s[(int64_t)w * ldn + row] : 0.f;
+    E = fmaxf(E, ev[i]);
+  }
   if (ok)
-    for (int w = q; w < nwin; w += ST_Q) E = fmaxf(E, win_e[(int64_t)w * ldn + row]);
+    for (int w = q + ST_Q * ST_W; w < nwin; w += ST_Q) E = fmaxf(E, win_e[(int64_t)w * ldn + row]);
   red[q][t] = E;
   __syncthreads();
 #pragma unroll
@@ -577,17 +587,23 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__
   const float mo = ok ? m[row] : -INFINITY;
   const float nE = fmaxf(mo, E);   // finite: every chunk has a valid column
   float S = 0.f;
-  if (ok)
-    for (int w = q; w < nwin; w += ST_Q) {
-      const float e = win_e[(int64_t)w * ldn + row];
-      int sh = SHIFT_ZERO;
-      if (e != -INFINITY) {
-        const float d = nE - e;
-        sh = d < (float)SHIFT_ZERO ? (int)d : SHIFT_ZERO;
-        S += ldexpf(win_s[(int64_t)w * ldn + row], -(int)fminf(d, 300.f));
-      }
-      shift[(int64_t)w * ldn + row] = (uint8_t)sh;
+  auto fold = [&](int w, float e, float sw) {
+    int sh = SHIFT_ZERO;
+    if (e != -INFINITY) {
+      const float d = nE - e;
+      sh = d < (float)SHIFT_ZERO ? (int)d : SHIFT_ZERO;
+      S += ldexpf(sw, -(int)fminf(d, 300.f));
     }
+    shift[(int64_t)w * ldn + row] = (uint8_t)sh;
+  };
+  if (ok) {
+#pragma unroll
+    for (int i = 0; i < ST_W; ++i) {
+      const int w = q + ST_Q * i;
+      if (w < nwin) fold(w, ev[i], sv[i]);
+    }
+    for (int w = q + ST_Q * ST_W; w < nwin; w += ST_Q) fold(w, win_e[(int64_t)w * ldn + row], win_s[(int64_t)w * ldn + row]);
+  }
   red[q][t] = S;
   __syncthreads();
   if (q == 0 && ok) {
