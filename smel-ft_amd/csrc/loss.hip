@@ -437,13 +437,14 @@ struct GradArgs {
 };
 
 constexpr int GR_NW = SMEL_CE_GR_NW, GR_NB = 8 / (GR_NW / 2);
+constexpr int GR_SP = 528;   // epilogue staging row pitch: 128 fp32 + 16 B (rows start on different banks)
 
 template <int DT>
 __global__ __launch_bounds__(64 * GR_NW) __attribute__((amdgpu_waves_per_eu(GR_NW / 4, GR_NW / 4))) void
 ce_grad_kernel(GradArgs a) {
   using R = Ring<SMEL_CE_GR_KB, GR_NB, SMEL_CE_GR_NST, GR_NW>;
   static_assert(R::B_ROWS == 256, "256-row token tiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[R::BYTES > GR_NW * 32 * GR_SP ? R::BYTES : GR_NW * 32 * GR_SP];
   // the list (half, token tile, hidden tile), XCD x a contiguous run of it: one XCD's tiles share their token
   // tiles' softmax terms and the hidden tiles' head columns of one K half in its L2
   const int n_tiles = a.n_ht * a.n_tt;
@@ -511,35 +512,43 @@ ce_grad_kernel(GradArgs a) {
   nt_loop<DT, R, GR_NB>(acc, smem, ra, aoff, rb, boff, kbytes, 5 * (int)(blockIdx.x / NXCD), pre, fix);
 
   // ---- epilogue: acc[m][n][r] = term of hidden column a0 + 128 wm + 32 m + 8 (r / 4) + 4 h + r % 4 and token
-  // row tok0 + 32 n: 16-byte runs of 4 columns
+  // row tok0 + 32 n. Per token slice the wave stages its 32 rows x 128 columns in LDS (the ring is free) and writes
+  // them out as whole 512-byte row segments (32 lanes per row, 16 B each), the accumulator update alike.
+  __syncthreads();
+  uint8_t* stg = smem + w * (32 * GR_SP);
   const size_t nh = (size_t)a.n * a.H;
   const float* prev = a.part + (size_t)(a.parity ^ 1) * nh;
   float* mine = a.part + (size_t)a.parity * nh;
+  const int col0 = a0 + 128 * wm;
 #pragma unroll
   for (int n = 0; n < GR_NB; ++n) {
-    const int tok = tok0 + 32 * n;
-    if (tok >= a.n) continue;
-    const float rr = a.first ? 0.f : a.r[tok];
-    const size_t row = (size_t)tok * a.H;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = a0 + 128 * wm + 32 * m + 8 * q + 4 * h;
-        if (col >= a.H) continue;
-        f32x4_t v = {acc[m][n][4 * q], acc[m][n][4 * q + 1], acc[m][n][4 * q + 2], acc[m][n][4 * q + 3]};
-        if (half) {
-          *reinterpret_cast<f32x4_t*>(mine + row + col) = v;
-          continue;
-        }
-        f32x4_t* dst = reinterpret_cast<f32x4_t*>(a.acc + row + col);
-        if (!a.first) {
-          const f32x4_t o = *dst, p = *reinterpret_cast<const f32x4_t*>(prev + row + col);
-          v = f32x4_t{fmaf(o[0] + p[0], rr, v[0]), fmaf(o[1] + p[1], rr, v[1]), fmaf(o[2] + p[2], rr, v[2]),
-                      fmaf(o[3] + p[3], rr, v[3])};
-        }
-        *dst = v;
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4_t*>(stg + r32 * GR_SP + (32 * m + 8 * q + 4 * h) * 4) =
+            f32x4_t{acc[m][n][4 * q], acc[m][n][4 * q + 1], acc[m][n][4 * q + 2], acc[m][n][4 * q + 3]};
+    const int tok_s = b0 + 32 * GR_NB * wn + 32 * n;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int k = 64 * jj + lane, row = k >> 5, piece = k & 31;
+      const int tok = tok_s + row, col = col0 + 4 * piece;
+      f32x4_t v = *reinterpret_cast<const f32x4_t*>(stg + row * GR_SP + piece * 16);
+      if (tok >= a.n || col >= a.H) continue;
+      const size_t at = (size_t)tok * a.H + col;
+      if (half) {
+        *reinterpret_cast<f32x4_t*>(mine + at) = v;
+        continue;
       }
+      if (!a.first) {
+        const float rr = a.r[tok];
+        const f32x4_t o = *reinterpret_cast<const f32x4_t*>(a.acc + at);
+        const f32x4_t pp = *reinterpret_cast<const f32x4_t*>(prev + at);
+        v = f32x4_t{fmaf(o[0] + pp[0], rr, v[0]), fmaf(o[1] + pp[1], rr, v[1]), fmaf(o[2] + pp[2], rr, v[2]),
+                    fmaf(o[3] + pp[3], rr, v[3])};
+      }
+      *reinterpret_cast<f32x4_t*>(a.acc + at) = v;
+    }
   }
 }
 
