@@ -95,8 +95,9 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
 // shared-gate logit x[t] . w_sg (when sg), other columns 0. Block = 64 tokens x 96 columns, 4 waves; wave w takes
 // tokens 16 w .. 16 w + 15 against all 96 columns (v_mfma_f32_16x16x32_bf16, 6 column fragments) over the whole
 // hidden dim, so no partial sums are reduced. Per 64-wide k-step the block stages the 96 weight rows once in LDS
-// (LDS-DMA, 4-stage ring, XOR-swizzled 16-B chunks) and each wave loads its own 16 x rows into registers three steps
-// ahead: x is read once per column block and the weights once per 64 tokens. Grid = ceil(T / 64) x ceil(ldl / 96).
+// (LDS-DMA, 8-stage ring, XOR-swizzled 16-B chunks) and each wave loads its own 16 x rows into registers seven steps
+// ahead (a step's MFMA work is short next to a load's latency, so the depth sets the kernel's speed): x is read once
+// per column block and the weights once per 64 tokens. Grid = ceil(T / 64) x ceil(ldl / 96).
 constexpr int RT = 64;
 constexpr int RC = 96;
 constexpr int RKT = 64;
@@ -105,7 +106,8 @@ constexpr int RSTAGE = RC * RKT;   // bf16 elements of one weight stage (12 KB)
 // counts; the wait is computed from them): 2 x-row loads into registers, 3 weight-row LDS-DMAs
 constexpr int RVM_X = 2;
 constexpr int RVM_W = RSTAGE * 2 / (4 * 1024);
-constexpr int R_WAIT = 2 * (RVM_X + RVM_W);   // steps j+1 and j+2 may be in flight while step j computes
+constexpr int RNST = 8;                        // ring stages: loads run RNST - 1 steps ahead
+constexpr int R_WAIT = (RNST - 2) * (RVM_X + RVM_W);   // steps j+1 .. j+RNST-2 may be in flight while step j computes
 
 SMEL_DEV f32x4_t mfma16r(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
                                                            const uint16_t* __restrict__ gw,
                                                            const uint16_t* __restrict__ sg, int T, int H, int E,
                                                            int ldl, uint16_t* __restrict__ logits) {
-  __shared__ __attribute__((aligned(1024))) uint16_t WS[4][RSTAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t WS[RNST][RSTAGE];
   const int tid = threadIdx.x, l = lane_id(), kq = l >> 4, li = l & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = blockIdx.x * RT, c0 = blockIdx.y * RC;
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
     for (int s = 0; s < RVM_X; ++s) xa[s] = ld16(rx, in ? xoff + k2 + 64 * s : OOB);
 #pragma unroll
     for (int ii = 0; ii < RVM_W; ++ii)
-      ld16_lds(rb[ii], &WS[j & 3][(RVM_W * w + ii) * 512], in ? boff[ii] + k2 : OOB);
+      ld16_lds(rb[ii], &WS[j % RNST][(RVM_W * w + ii) * 512], in ? boff[ii] + k2 : OOB);
     __builtin_amdgcn_sched_barrier(0);
   };
   // weight fragment reads: column fragment f, substep s, lane (kq, li) -> row 16 f + li, logical chunk 4 s + kq
@@ -160,37 +162,27 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
   f32x4_t acc[6];
 #pragma unroll
   for (int f = 0; f < 6; ++f) acc[f] = f32x4_t{};
-  u32x4_t X0[RVM_X], X1[RVM_X], X2[RVM_X], X3[RVM_X];
+  u32x4_t X[RNST][RVM_X];   // x rows of the steps in flight, register set j % RNST
   auto compute = [&](int j, const u32x4_t* xa) {
-    const uint16_t* S = WS[j & 3];
+    const uint16_t* S = WS[j % RNST];
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int f = 0; f < 6; ++f)
         acc[f] = mfma16r(xa[s], *reinterpret_cast<const u32x4_t*>(S + brd[s] + f * 16 * RKT), acc[f]);
   };
-  // three steps ahead; per step and wave 2 x loads (registers) + 3 weight DMAs: before step j only steps j+1 and
-  // j+2 (10 operations) may still be in flight
-  issue(0, X0);
-  issue(1, X1);
-  issue(2, X2);
-  for (int j = 0; j < nk; j += 4) {
-    wait_vm_lds<R_WAIT>();
-    __builtin_amdgcn_s_barrier();
-    issue(j + 3, X3);
-    compute(j, X0);
-    wait_vm_lds<R_WAIT>();
-    __builtin_amdgcn_s_barrier();
-    issue(j + 4, X0);
-    compute(j + 1, X1);
-    wait_vm_lds<R_WAIT>();
-    __builtin_amdgcn_s_barrier();
-    issue(j + 5, X1);
-    compute(j + 2, X2);
-    wait_vm_lds<R_WAIT>();
-    __builtin_amdgcn_s_barrier();
-    issue(j + 6, X2);
-    compute(j + 3, X3);
+  // RNST - 1 steps ahead; per step and wave 2 x loads (registers) + 3 weight DMAs: before step j only steps
+  // j+1 .. j+RNST-2 may still be in flight
+#pragma unroll
+  for (int s = 0; s < RNST - 1; ++s) issue(s, X[s]);
+  for (int j = 0; j < nk; j += RNST) {
+#pragma unroll
+    for (int u = 0; u < RNST; ++u) {
+      wait_vm_lds<R_WAIT>();
+      __builtin_amdgcn_s_barrier();
+      issue(j + u + RNST - 1, X[(u + RNST - 1) % RNST]);
+      compute(j + u, X[u]);
+    }
   }
   wait_vm<0>();   // the trailing (out-of-range) loads
   // D[4 kq + r][li] of fragment f: token 16 w + 4 kq + r, column c0 + 16 f + li
