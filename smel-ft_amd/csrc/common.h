@@ -173,6 +173,14 @@ SMEL_DEV void wait_vm_lds() {
   static_assert(N >= 0 && N < 64, "vmcnt counts 0..63 outstanding vector-memory operations");
   SMEL_WAIT_VM_LDS(N);
 }
+// Workgroup barrier for hand-offs through LDS only: it orders the block's LDS accesses around the barrier and waits
+// for none of the wave's global loads or stores. (__syncthreads also waits for every outstanding global access, a
+// whole memory round trip after a store.) Only for code whose threads exchange nothing through global memory.
+SMEL_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // Operand tiles in LDS hold rows of 64 bf16 (128 B) without padding; the physical 16-B chunk of logical chunk c of
 // row r is c ^ swz(r), so 8 (or 16) lanes reading consecutive rows at one logical chunk touch distinct banks with 32

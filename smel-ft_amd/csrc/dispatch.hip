@@ -2,10 +2,11 @@
 // smel/moe.py:216-223, and the inverse permutation of :249-250), plus the GEMM tile list. No host sync: counts and
 // offsets stay on the device and the grouped GEMMs read the tile list.
 //
-// Three launches over blocks of 1024 slots (one per thread): (1) per-block expert histograms; (2) one block turns
-// them into counts, offsets, each block's first output position per expert, and the tile list; (3) every block
-// ranks its slots again — inside a wave by ballots over the id bits (a wave-level multisplit), across its 16 waves
-// by a per-expert prefix — and scatters order / inv. Slots of one expert thus keep ascending p: the stable sort.
+// Launches over blocks of 1024 slots (one per thread): (1) per-block expert histograms; (2) one block turns them into
+// counts, offsets, each block's first output position per expert, and the tile list; (3) every block ranks its slots
+// again — inside a wave by ballots over the id bits (a wave-level multisplit), across its 16 waves by a per-expert
+// prefix — and scatters order / inv. Slots of one expert thus keep ascending p: the stable sort. With at most 64
+// blocks (T * K <= 65536 slots) (2) and (3) are one launch: each block folds every block's histogram itself.
 #include <mutex>
 
 #include "abi_util.h"
@@ -33,20 +34,107 @@ SMEL_DEV int block_exclusive_scan(int v, int* wsum /* [NW] LDS */, int& total) {
     if (l >= o) inc += y;
   }
   if (l == 63) wsum[w] = inc;
-  __syncthreads();
+  lds_barrier();
   int base = 0, tot = 0;
   for (int j = 0; j < NW; ++j) {
     const int s = wsum[j];
     if (j < w) base += s;
     tot += s;
   }
-  __syncthreads();
+  lds_barrier();
   total = tot;
   return base + inc - v;
 }
 
 SMEL_DEV int id_at(const void* ids, int is64, int p) {
   return is64 ? (int)static_cast<const int64_t*>(ids)[p] : static_cast<const int32_t*>(ids)[p];
+}
+
+// Tile list over groups 0..E-1 (+ shared group E): the tiles of more than m_tile / 2 rows first (in group order), then
+// the shorter last tiles of the groups (in group order). The grouped GEMMs start tiles in list order, so the short
+// tiles fill the last round of workgroups instead of holding long ones back. tiles_g (optional): the same tiles in
+// group order, a group's tiles next to each other.
+// Group g = tid: rows from row0, nt tiles of which nlong long; lbase / sbase = its first position among the long /
+// short tiles; n_long / n_short = the totals. The groups' values go through LDS, then thread q writes long tile q and
+// short tile q (its group found by a binary search over the first positions), so no thread loops over a large
+// group's tiles. Every thread of the block calls it (one barrier inside).
+struct TileLds {
+  int lb[MAXE + 1], sb[MAXE + 1], row0[MAXE + 1], rows[MAXE + 1], nt[MAXE + 1], gk[MAXE + 1];
+};
+SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt, int lbase, int sbase, int n_long,
+                          int n_short, int m_tile, int max_tiles, int gkv, int bad, int32_t* __restrict__ tiles,
+                          int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
+  if (tid < G) {
+    t.lb[tid] = lbase;
+    t.sb[tid] = sbase;
+    t.row0[tid] = row0;
+    t.rows[tid] = rows;
+    t.nt[tid] = nt;
+    t.gk[tid] = gkv;
+  }
+  lds_barrier();
+  // the last group whose first position is <= q: the group of position q (groups without such tiles share their
+  // first position with the next group)
+  auto group_of = [&](const int* first, int q) {
+    int lo = 0, hi = G - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (first[mid] <= q)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    return lo;
+  };
+  auto put = [&](int g, int i, int pos) {
+    if (pos >= max_tiles) return;
+    const int r0 = t.row0[g];
+    int4 tl;
+    tl.x = g;
+    tl.y = r0 + i * m_tile;
+    tl.z = min(r0 + t.rows[g], r0 + (i + 1) * m_tile);
+    tl.w = t.gk[g];
+    reinterpret_cast<int4*>(tiles)[pos] = tl;
+    const int gpos = t.lb[g] + t.sb[g] + i;   // a group's tiles next to each other
+    if (tiles_g && gpos < max_tiles) reinterpret_cast<int4*>(tiles_g)[gpos] = tl;
+  };
+  for (int q = tid; q < n_long; q += DB) {
+    const int g = group_of(t.lb, q);
+    put(g, q - t.lb[g], q);
+  }
+  for (int q = tid; q < n_short; q += DB) {   // only a group's last tile can be short
+    const int g = group_of(t.sb, q);
+    put(g, t.nt[g] - 1, n_long + q);
+  }
+  if (tid == 0) {
+    const int total_tiles = n_long + n_short;
+    n_tiles[0] = min(total_tiles, max_tiles);
+    err[0] = bad | (total_tiles > max_tiles ? 2 : 0);
+  }
+}
+SMEL_DEV int tiles_of(int rows, int m_tile) { return (rows + m_tile - 1) / m_tile; }
+SMEL_DEV int long_tiles_of(int rows, int m_tile) {   // tiles of more than m_tile / 2 rows
+  const int nt = tiles_of(rows, m_tile);
+  return nt - ((nt > 0 && rows - (nt - 1) * m_tile <= m_tile / 2) ? 1 : 0);
+}
+
+// The tile list from the offsets off_s[0..E] (LDS). Called by every thread of one block (block scans inside).
+SMEL_DEV void write_tiles(TileLds& tl, int tid, int E, int TK, int shared_rows, int m_tile, int max_tiles, int gkv,
+                          const int* off_s, int bad, int* wsum, int32_t* __restrict__ tiles,
+                          int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
+  const int G = E + (shared_rows > 0 ? 1 : 0);
+  int nt = 0, rows = 0, row0 = 0, nlong = 0;
+  if (tid < G) {
+    rows = tid < E ? off_s[tid + 1] - off_s[tid] : shared_rows;
+    row0 = tid < E ? off_s[tid] : TK;
+    nt = tiles_of(rows, m_tile);
+    nlong = long_tiles_of(rows, m_tile);
+  }
+  int n_long, n_short;
+  const int lbase = block_exclusive_scan(nlong, wsum, n_long);
+  const int sbase = block_exclusive_scan(nt - nlong, wsum, n_short);
+  store_tiles(tl, tid, G, rows, row0, nt, lbase, sbase, n_long, n_short, m_tile, max_tiles, gkv, bad, tiles, tiles_g,
+              n_tiles, err);
 }
 
 // (1) hist[b][e] = slots of block b routed to expert e; bad[b] = 1 if block b holds an id outside [0, E)
@@ -57,7 +145,7 @@ __global__ __launch_bounds__(1024) void dispatch_hist(const void* __restrict__ i
   const int tid = threadIdx.x, b = blockIdx.x;
   for (int e = tid; e < E; e += DB) h[e] = 0;
   if (tid == 0) bad_s = 0;
-  __syncthreads();
+  lds_barrier();
   const int p = b * DB + tid;
   if (p < TK) {
     const int e = id_at(ids, is64, p);
@@ -66,7 +154,7 @@ __global__ __launch_bounds__(1024) void dispatch_hist(const void* __restrict__ i
     else
       bad_s = 1;
   }
-  __syncthreads();
+  lds_barrier();
   for (int e = tid; e < E; e += DB) hist[b * E + e] = h[e];
   if (tid == 0) bad[b] = bad_s;
 }
@@ -83,6 +171,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   __shared__ int off_s[MAXE + 1];
   __shared__ int bad_s;
   __shared__ int hs[HCH];
+  __shared__ TileLds tl;
   const int tid = threadIdx.x;
   if (tid == 0) bad_s = 0;
   // the bad-id flags and the group kinds are needed only at the end: their loads go out with the first histogram
@@ -98,9 +187,9 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   int total = 0;
   for (int b0 = 0; b0 < nb; b0 += ch) {
     const int n = min(ch, nb - b0) * E;
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < n; i += DB) hs[i] = hist[b0 * E + i];
-    __syncthreads();
+    lds_barrier();
     if (tid < E)
       for (int b = 0; b < n / E; ++b) total += hs[b * E + tid];
   }
@@ -115,9 +204,9 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   for (int b0 = 0; b0 < nb; b0 += ch) {
     const int n = min(ch, nb - b0) * E;
     if (!one) {
-      __syncthreads();
+      lds_barrier();
       for (int i = tid; i < n; i += DB) hs[i] = hist[b0 * E + i];
-      __syncthreads();
+      lds_barrier();
     }
     if (tid < E)
       for (int b = 0; b < n / E; ++b) {
@@ -125,7 +214,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
         hs[b * E + tid] = run;
         run += c;
       }
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < n; i += DB) hist[b0 * E + i] = hs[i];
   }
   if (tid == 0) {
@@ -133,51 +222,20 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
     offsets[E] = total_rows;
   }
   if (badv) bad_s = 1;
-  __syncthreads();
-  // tile list over groups 0..E-1 (+ shared group E): the tiles of more than m_tile / 2 rows first (in group order),
-  // then the shorter last tiles of the groups (in group order). The grouped GEMMs start tiles in list order, so the
-  // short tiles fill the last round of workgroups instead of holding long ones back. tiles_g (optional): the same
-  // tiles in group order, a group's tiles next to each other.
-  int nt = 0, rows = 0, row0 = 0, nlong = 0;
-  if (tid < G) {
-    rows = tid < E ? off_s[tid + 1] - off_s[tid] : shared_rows;
-    row0 = tid < E ? off_s[tid] : TK;
-    nt = (rows + m_tile - 1) / m_tile;
-    nlong = nt - ((nt > 0 && rows - (nt - 1) * m_tile <= m_tile / 2) ? 1 : 0);
-  }
-  int n_long, n_short;
-  const int lbase = block_exclusive_scan(nlong, wsum, n_long);
-  const int sbase = block_exclusive_scan(nt - nlong, wsum, n_short);
-  const int total_tiles = n_long + n_short;
-  if (tid < G) {
-    for (int i = 0; i < nt; ++i) {
-      const int pos = i < nlong ? lbase + i : n_long + sbase;   // only a group's last tile can be short
-      if (pos >= max_tiles) continue;
-      int4 tl;
-      tl.x = tid;
-      tl.y = row0 + i * m_tile;
-      tl.z = min(row0 + rows, row0 + (i + 1) * m_tile);
-      tl.w = gkv;
-      reinterpret_cast<int4*>(tiles)[pos] = tl;
-      if (tiles_g) reinterpret_cast<int4*>(tiles_g)[lbase + sbase + i] = tl;
-    }
-  }
-  if (tid == 0) {
-    n_tiles[0] = min(total_tiles, max_tiles);
-    err[0] = bad_s | (total_tiles > max_tiles ? 2 : 0);
-  }
+  lds_barrier();
+  write_tiles(tl, tid, E, TK, shared_rows, m_tile, max_tiles, gkv, off_s, bad_s, wsum, tiles, tiles_g, n_tiles, err);
 }
 
-// (3) stable scatter of block b's slots: order[pos] = p, inv[p] = pos (-1 for an id outside [0, E))
-__global__ __launch_bounds__(1024) void dispatch_scatter(const void* __restrict__ ids, int is64, int TK, int E,
-                                                         const int32_t* __restrict__ base,
-                                                         int32_t* __restrict__ order, int32_t* __restrict__ inv) {
-  __shared__ int cnt[NW * MAXE];   // per-wave counts, then per-wave first positions
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, b = blockIdx.x;
+// Stable scatter of block b's slots: order[pos] = p, inv[p] = pos (-1 for an id outside [0, E)); base(x) = the first
+// output position of this block's slots of expert x. Every thread of the block calls it.
+// e = the thread's slot id (loaded by the caller, -1 past TK).
+template <typename Base>
+SMEL_DEV void scatter_block(int e, int TK, int E, int b, Base base, int* cnt /* [NW * MAXE] LDS */,
+                            int32_t* __restrict__ order, int32_t* __restrict__ inv) {
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6;
   for (int i = tid; i < NW * E; i += DB) cnt[i] = 0;
-  __syncthreads();
+  lds_barrier();
   const int p = b * DB + tid;
-  const int e = p < TK ? id_at(ids, is64, p) : -1;
   const bool ok = e >= 0 && e < E;
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
@@ -190,16 +248,161 @@ __global__ __launch_bounds__(1024) void dispatch_scatter(const void* __restrict_
   const uint64_t lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
   const int rank = ok ? __popcll(m & lt) : 0;
   if (ok && (m >> l) == 1ull) cnt[w * E + e] = __popcll(m);   // the group's highest lane records its size
-  __syncthreads();
+  lds_barrier();
   for (int x = tid; x < E; x += DB) {
-    int run = base[b * E + x];
+    int run = base(x);
     for (int j = 0; j < NW; ++j) {
       const int c = cnt[j * E + x];
       cnt[j * E + x] = run;
       run += c;
     }
   }
-  __syncthreads();
+  lds_barrier();
+  if (ok) {
+    const int pos = cnt[w * E + e] + rank;
+    order[pos] = p;
+    inv[p] = pos;
+  } else if (p < TK) {
+    inv[p] = -1;
+  }
+}
+
+// (3) the scatter after dispatch_scan: base[b][e] comes from the scan
+__global__ __launch_bounds__(1024) void dispatch_scatter(const void* __restrict__ ids, int is64, int TK, int E,
+                                                         const int32_t* __restrict__ base,
+                                                         int32_t* __restrict__ order, int32_t* __restrict__ inv) {
+  __shared__ int cnt[NW * MAXE];   // per-wave counts, then per-wave first positions
+  const int b = blockIdx.x, p = b * DB + threadIdx.x;
+  const int e = p < TK ? id_at(ids, is64, p) : -1;
+  scatter_block(e, TK, E, b, [&](int x) { return base[b * E + x]; }, cnt, order, inv);
+}
+
+// Exclusive scan of three values at once over the block (the latency of one scan); tot = the block totals. wsum is
+// not reused afterwards, so there is no trailing barrier.
+struct I3 {
+  int a, b, c;
+};
+SMEL_DEV I3 block_exclusive_scan3(I3 v, I3* wsum /* [NW] LDS */, I3& tot) {
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  I3 inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int ya = __shfl_up(inc.a, o, 64), yb = __shfl_up(inc.b, o, 64), yc = __shfl_up(inc.c, o, 64);
+    if (l >= o) {
+      inc.a += ya;
+      inc.b += yb;
+      inc.c += yc;
+    }
+  }
+  if (l == 63) wsum[w] = inc;
+  lds_barrier();
+  I3 base{0, 0, 0}, t{0, 0, 0};
+  for (int j = 0; j < NW; ++j) {
+    const I3 s = wsum[j];
+    if (j < w) {
+      base.a += s.a;
+      base.b += s.b;
+      base.c += s.c;
+    }
+    t.a += s.a;
+    t.b += s.b;
+    t.c += s.c;
+  }
+  tot = t;
+  return I3{base.a + inc.a - v.a, base.b + inc.b - v.b, base.c + inc.c - v.c};
+}
+
+// (2+3) for at most SCAN_FUSE_NB blocks, the scan and the scatter in one launch: every block folds all blocks'
+// histograms itself (the totals, and the prefix over the blocks before it, per expert) and scatters its slots; block
+// 0 also writes counts, offsets, the tile lists, n_tiles and err. No block waits for another. Order of the work: every
+// load first (the slot id, the histograms), the ranking of the block's slots, one scan of (offsets, long tiles, short
+// tiles), then only stores and LDS traffic (so no wait on a load queued behind a store).
+constexpr int SCAN_FUSE_NB = 64;
+__global__ __launch_bounds__(1024) void dispatch_scan_scatter(const void* __restrict__ ids, int is64, int nb, int TK,
+                                                              int E, int shared_rows, int m_tile, int max_tiles,
+                                                              const int32_t* __restrict__ gkind,
+                                                              const int32_t* __restrict__ hist,
+                                                              const int32_t* __restrict__ bad,
+                                                              int32_t* __restrict__ counts,
+                                                              int32_t* __restrict__ offsets,
+                                                              int32_t* __restrict__ tiles,
+                                                              int32_t* __restrict__ tiles_g,
+                                                              int32_t* __restrict__ n_tiles,
+                                                              int32_t* __restrict__ err, int32_t* __restrict__ order,
+                                                              int32_t* __restrict__ inv) {
+  __shared__ int cnt[NW * MAXE];   // per-wave counts, then per-wave first positions
+  __shared__ I3 wsum[NW];
+  __shared__ int bad_s;
+  __shared__ TileLds tl;
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, b = blockIdx.x;
+  const bool lead = b == 0;   // uniform
+  const int G = E + (shared_rows > 0 ? 1 : 0);
+  const int p = b * DB + tid;
+  const int e = p < TK ? id_at(ids, is64, p) : -1;
+  int badv = 0, gkv = 0;
+  if (lead) {
+    for (int bb = tid; bb < nb; bb += DB) badv |= bad[bb];
+    gkv = (gkind && tid < G) ? gkind[tid] : 0;
+  }
+  int c[SCAN_FUSE_NB];
+  if (tid < E) {
+#pragma unroll
+    for (int i = 0; i < SCAN_FUSE_NB; ++i) {   // branch-free: rows past nb re-read the last one and count zero
+      const int v = hist[min(i, nb - 1) * E + tid];
+      c[i] = i < nb ? v : 0;
+    }
+  }
+  for (int i = tid; i < NW * E; i += DB) cnt[i] = 0;
+  if (tid == 0) bad_s = 0;
+  lds_barrier();
+  // rank of the slot among the block's slots of its expert: inside the wave by ballots over the id bits, the wave's
+  // count per expert recorded by the group's highest lane
+  const bool ok = e >= 0 && e < E;
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  uint64_t m = __ballot(ok);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool v = ok && ((e >> bit) & 1);
+    const uint64_t bb = __ballot(v);
+    m &= v ? bb : ~bb;
+  }
+  const uint64_t lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  const int rank = ok ? __popcll(m & lt) : 0;
+  if (ok && (m >> l) == 1ull) cnt[w * E + e] = __popcll(m);
+  if (badv) bad_s = 1;
+  // per expert: the total over all blocks, the prefix over blocks 0 .. b-1; per group: its tiles
+  int total = 0, pre = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int i = 0; i < SCAN_FUSE_NB; ++i) {
+      total += c[i];
+      pre += i < b ? c[i] : 0;
+    }
+  }
+  const int rows = tid < E ? total : (tid < G ? shared_rows : 0);
+  const int nt = tiles_of(rows, m_tile), nlong = long_tiles_of(rows, m_tile);
+  I3 tot;
+  const I3 ex = block_exclusive_scan3(I3{tid < E ? total : 0, nlong, nt - nlong}, wsum, tot);   // its barrier also
+                                                                                                // completes cnt, bad_s
+  if (lead) {
+    if (tid < E) {
+      counts[tid] = total;
+      offsets[tid] = ex.a;
+    }
+    if (tid == 0) offsets[E] = tot.a;
+    store_tiles(tl, tid, G, rows, tid < E ? ex.a : TK, nt, ex.b, ex.c, tot.b, tot.c, m_tile, max_tiles, gkv, bad_s,
+                tiles, tiles_g, n_tiles, err);
+  }
+  // first output position of wave j's slots of expert tid
+  if (tid < E) {
+    int run = ex.a + pre;
+    for (int j = 0; j < NW; ++j) {
+      const int cj = cnt[j * E + tid];
+      cnt[j * E + tid] = run;
+      run += cj;
+    }
+  }
+  lds_barrier();
   if (ok) {
     const int pos = cnt[w * E + e] + rank;
     order[pos] = p;
@@ -271,6 +474,12 @@ extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, in
     dispatch_hist<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)TK, (int)E, hist, bad);
     const int st = smel::launch_status();
     if (st) return st;
+  }
+  if (nb > 0 && nb <= SCAN_FUSE_NB) {
+    dispatch_scan_scatter<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, nb, (int)TK, (int)E, (int)shared_rows,
+                                                 m_tile, (int)mt, gkind, hist, bad, counts, offsets, tiles,
+                                                 tiles_grouped, n_tiles, err, order, inv);
+    return smel::launch_status();
   }
   dispatch_scan<<<1, DB, 0, stream>>>(nb, (int)TK, (int)E, (int)shared_rows, m_tile, (int)mt, gkind, hist, bad,
                                       counts, offsets, tiles, tiles_grouped, n_tiles, err);

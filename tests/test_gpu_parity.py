@@ -404,7 +404,10 @@ def _zipf_topi(T, K, E, s, gen):
 @pytest.mark.parametrize("T,K,E,shared,kind", [(4092, 8, 256, True, "uniform"), (128, 2, 8, True, "uniform"),
                                                (4096, 8, 256, False, "zipf"), (1, 8, 256, True, "uniform"),
                                                (0, 8, 256, True, "uniform"), (1000, 1, 3, False, "uniform"),
-                                               (257, 4, 512, True, "zipf")])
+                                               (257, 4, 512, True, "zipf"),
+                                               # 64 blocks of 1024 slots: the last size with the scan and the
+                                               # scatter in one launch; 71 blocks: three launches
+                                               (8192, 8, 128, False, "uniform"), (9000, 8, 256, True, "zipf")])
 def test_dispatch_bitexact(T, K, E, shared, kind):
     _say(f"dispatch T{T} K{K} E{E} {kind}")
     gen = torch.Generator().manual_seed(T * 7 + E)
