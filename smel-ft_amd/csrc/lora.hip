@@ -7,112 +7,148 @@
 namespace {
 
 constexpr int PREP_MAX_SETS = 2;
+constexpr int PCH = 128;   // columns (A factors) or rows (B factors) of one chunk
+// block kinds: the A factors of gate / up (over Hd), A_down (over In), the B factors of gate / up (rows of In),
+// B_down (rows of Hd)
+enum { PK_AGU = 0, PK_ADN = 1, PK_BGU = 2, PK_BDN = 3, PK_N = 4 };
 struct PrepArgs {
   smel_lora_set set[PREP_MAX_SETS];
+  int first[PREP_MAX_SETS * PK_N + 1];   // first block of each (set, kind), then the total
   int planes, Hd, In;
 };
 
-// grid (256, 8 layouts, sets): blockIdx.z picks the LoRA set, blockIdx.y the layout
+// One block = one chunk of PCH columns (A factors) or rows (B factors) of one expert's fp32 factor(s). The chunk goes
+// to LDS as [factor][rank][column] in one round of coalesced loads (every load issued before the first is used); the
+// block then writes every layout that draws on it, the plain and the transposed one, two bf16 per 32-bit store with
+// consecutive threads on consecutive words.
 __global__ __launch_bounds__(256) void lora_prep_kernel(PrepArgs pa) {
-  const smel_lora_set& S = pa.set[blockIdx.z];
-  const float* __restrict__ Ag = S.A_gate;
-  const float* __restrict__ Bg = S.B_gate;
-  const float* __restrict__ Au = S.A_up;
-  const float* __restrict__ Bu = S.B_up;
-  const float* __restrict__ Ad = S.A_down;
-  const float* __restrict__ Bd = S.B_down;
-  uint16_t* __restrict__ fwd_gu = S.fwd_gu;
-  uint16_t* __restrict__ fwd_dn = S.fwd_dn;
-  uint16_t* __restrict__ a_gu = S.a_gu;
-  uint16_t* __restrict__ a_dn = S.a_dn;
-  uint16_t* __restrict__ bt_dn = S.bt_dn;
-  uint16_t* __restrict__ bt_gu = S.bt_gu;
-  uint16_t* __restrict__ at_gu = S.at_gu;
-  uint16_t* __restrict__ at_dn = S.at_dn;
-  const int n = (int)S.n, r = (int)S.r, planes = pa.planes, Hd = pa.Hd, In = pa.In;
-  // 32-bit index arithmetic (every layout has fewer than 2^31 elements: checked by the host) and two adjacent
-  // outputs per thread (every innermost dimension is even), stored as one 32-bit word
-  const int which = blockIdx.y;
-  const uint32_t I2 = 2u * In, H = Hd, Iu = In, R = r, P = planes, N = n;
+  __shared__ float sa[2][32][PCH + 1];   // odd row length: the transposed reads and writes are conflict free
+  const int tid = threadIdx.x, bid = blockIdx.x;
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < PREP_MAX_SETS * PK_N; ++i)
+    if (bid >= pa.first[i]) si = i;
+  const smel_lora_set& S = pa.set[si / PK_N];
+  const int kind = si % PK_N;
+  const int n = (int)S.n, R = (int)S.r, P = pa.planes, Hd = pa.Hd, In = pa.In;
+  const int X = (kind == PK_AGU || kind == PK_BDN) ? Hd : In;   // the dimension the chunks run over
+  const int nch = (X + PCH - 1) / PCH;
+  const int loc = bid - pa.first[si], g = loc / nch, x0 = (loc % nch) * PCH, w = min(PCH, X - x0);
+  const int nf = (kind == PK_AGU || kind == PK_BGU) ? 2 : 1;   // factors in the chunk (gate and up)
   // gate_up side: with one plane, gate ranks sit at 0..r-1 and up ranks at 16..16+r-1 of it; with two planes, each
   // projection has its own plane and its ranks at 0..r-1. (plane, j) -> rank of gate / up, or -1.
-  auto gate_rank = [&](uint32_t plane, uint32_t j) -> int { return (plane == 0u && j < R) ? (int)j : -1; };
-  auto up_rank = [&](uint32_t plane, uint32_t j) -> int {
-    if (P == 1u) return (j >= 16u && j < 16u + R) ? (int)(j - 16u) : -1;
-    return (plane == 1u && j < R) ? (int)j : -1;
+  auto gate_rank = [&](int plane, int j) -> int { return (plane == 0 && j < R) ? j : -1; };
+  auto up_rank = [&](int plane, int j) -> int {
+    if (P == 1) return (j >= 16 && j < 16 + R) ? j - 16 : -1;
+    return (plane == 1 && j < R) ? j : -1;
   };
-  uint32_t total;
-  uint16_t* out;
-  switch (which) {
-    case 0: total = N * I2 * 32u; out = fwd_gu; break;
-    case 1: total = N * H * 32u; out = fwd_dn; break;
-    case 2: total = P * N * 32u * H; out = a_gu; break;
-    case 3: total = N * 32u * Iu; out = a_dn; break;
-    case 4: total = N * 32u * H; out = bt_dn; break;
-    case 5: total = P * N * 32u * I2; out = bt_gu; break;
-    case 6: total = N * P * H * 32u; out = at_gu; break;
-    default: total = N * Iu * 32u; out = at_dn; break;
-  }
-  auto val = [&](uint32_t i) -> float {
-    float v = 0.f;
-    switch (which) {
-      case 0: {   // fwd_gu [n][2In][32]: row < In gate (plane 0), row >= In up (its own plane's ranks)
-        const uint32_t c = i & 31u, rowg = i >> 5, row = rowg % I2, g = rowg / I2;
-        if (row < Iu) {
-          if (c < R) v = Bg[(g * Iu + row) * R + c];
-        } else {
-          const int k = up_rank(P - 1u, c);
-          if (k >= 0) v = Bu[(g * Iu + row - Iu) * R + k];
+  // ---- load, 16 B per lane: A factors [n][R][X] as (factor, rank, 4 columns) items, B factors [n][X][R] as the
+  // chunk's w * R contiguous floats per factor; into sa[f][k][c]
+  {
+    const bool isA = kind == PK_AGU || kind == PK_ADN;
+    const float* f0 = kind == PK_AGU ? S.A_gate : kind == PK_ADN ? S.A_down : kind == PK_BGU ? S.B_gate : S.B_down;
+    const float* f1 = kind == PK_AGU ? S.A_up : S.B_up;
+    constexpr int NI = 2 * 32 * PCH / 4 / 256;   // 16-B items per thread
+    f32x4_t v[NI];
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const int q = u * 256 + tid, f = q / (8 * PCH), e = q % (8 * PCH);   // e: item inside one factor's chunk
+      const float* src = f ? f1 : f0;
+      bool ok;
+      int64_t off;
+      if (isA) {   // e = (rank k, 4-column group)
+        const int k = e / (PCH / 4), c = 4 * (e % (PCH / 4));
+        ok = f < nf && k < R && c < w;
+        off = ((int64_t)g * R + k) * X + x0 + c;
+      } else {     // e = float quad of the chunk's rows
+        ok = f < nf && 4 * e < w * R;
+        off = ((int64_t)g * X + x0) * R + 4 * e;
+      }
+      v[u] = ok ? *reinterpret_cast<const f32x4_t*>(src + off) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    // B chunks hold ranks past R in no float: their slots must read 0
+    if (!isA)
+      for (int q = tid; q < 2 * 32 * PCH; q += 256) sa[q / (32 * PCH)][(q / PCH) % 32][q % PCH] = 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const int q = u * 256 + tid, f = q / (8 * PCH), e = q % (8 * PCH);
+      if (isA) {
+        const int k = e / (PCH / 4), c = 4 * (e % (PCH / 4));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sa[f][k][c + t] = v[u][t];
+      } else if (4 * e < w * R) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int x = 4 * e + t;   // float x of the chunk = row x / R, rank x % R
+          sa[f][x % R][x / R] = v[u][t];
         }
-        break;
-      }
-      case 1: {   // fwd_dn [n][Hd][32]
-        const uint32_t c = i & 31u;
-        if (c < R) v = Bd[(i >> 5) * R + c];
-        break;
-      }
-      case 2: {   // a_gu [planes][n][32][Hd]
-        const uint32_t h = i % H, jg = i / H, j = jg & 31u, pg = jg >> 5, plane = pg / N, g = pg - plane * N;
-        const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
-        if (kg >= 0) v = Ag[(g * R + kg) * H + h];
-        if (ku >= 0) v = Au[(g * R + ku) * H + h];
-        break;
-      }
-      case 3: {   // a_dn [n][32][In]
-        const uint32_t c = i % Iu, jg = i / Iu, j = jg & 31u, g = jg >> 5;
-        if (j < R) v = Ad[(g * R + j) * Iu + c];
-        break;
-      }
-      case 4: {   // bt_dn [n][32][Hd] = B_down^T
-        const uint32_t h = i % H, jg = i / H, j = jg & 31u, g = jg >> 5;
-        if (j < R) v = Bd[(g * H + h) * R + j];
-        break;
-      }
-      case 5: {   // bt_gu [planes][n][32][2In]: gate ranks on columns < In, up ranks on columns >= In
-        const uint32_t c = i % I2, jg = i / I2, j = jg & 31u, pg = jg >> 5, plane = pg / N, g = pg - plane * N;
-        const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
-        if (kg >= 0 && c < Iu) v = Bg[(g * Iu + c) * R + kg];
-        if (ku >= 0 && c >= Iu) v = Bu[(g * Iu + c - Iu) * R + ku];
-        break;
-      }
-      case 6: {   // at_gu [n][planes][Hd][32]: a_gu transposed (the backward GEMM's K-extension)
-        const uint32_t j = i & 31u, hg = i >> 5, h = hg % H, pg = hg / H, plane = pg % P, g = pg / P;
-        const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
-        if (kg >= 0) v = Ag[(g * R + kg) * H + h];
-        if (ku >= 0) v = Au[(g * R + ku) * H + h];
-        break;
-      }
-      default: {  // at_dn [n][In][32]: a_dn transposed
-        const uint32_t j = i & 31u, cg = i >> 5, c = cg % Iu, g = cg / Iu;
-        if (j < R) v = Ad[(g * R + j) * Iu + c];
-        break;
       }
     }
-    return v;
+  }
+  __syncthreads();
+  // slot j of plane `plane` of the gate_up layouts: the gate or up factor's value at chunk column c, or 0
+  auto gu = [&](int plane, int j, int c) -> float {
+    const int kg = gate_rank(plane, j), ku = up_rank(plane, j);
+    return kg >= 0 ? sa[0][kg][c] : (ku >= 0 ? sa[1][ku][c] : 0.f);
   };
-  uint32_t* o32 = reinterpret_cast<uint32_t*>(out);
-  for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < total / 2u; p += gridDim.x * blockDim.x)
-    o32[p] = pack2bf(val(2u * p), val(2u * p + 1u));
+  auto one = [&](int j, int c) -> float { return j < R ? sa[0][j][c] : 0.f; };
+  // 16-B stores of 8 bf16. [..][X] rows (32 slots per plane): item (plane, slot j, 8 columns); [X][32] rows: item
+  // (plane, column, 8 slots)
+  auto pack8 = [&](float a0, float a1, float a2, float a3, float a4, float a5, float a6, float a7) {
+    return u32x4_t{pack2bf(a0, a1), pack2bf(a2, a3), pack2bf(a4, a5), pack2bf(a6, a7)};
+  };
+  auto rows_along_x = [&](uint16_t* dst, int planes_, int64_t plane_stride, int64_t row0, int ldx, auto value) {
+    for (int q = tid; q < planes_ * 32 * (PCH / 8); q += 256) {
+      const int c = 8 * (q % (PCH / 8)), j = (q / (PCH / 8)) % 32, pl = q / (32 * (PCH / 8));
+      if (c < w)
+        *reinterpret_cast<u32x4_t*>(dst + pl * plane_stride + (row0 + j) * (int64_t)ldx + x0 + c) =
+            pack8(value(pl, j, c), value(pl, j, c + 1), value(pl, j, c + 2), value(pl, j, c + 3), value(pl, j, c + 4),
+                  value(pl, j, c + 5), value(pl, j, c + 6), value(pl, j, c + 7));
+    }
+  };
+  auto slots_along_row = [&](uint16_t* dst, int planes_, int64_t plane_stride, int64_t xrow0, auto value) {
+    for (int q = tid; q < planes_ * PCH * 4; q += 256) {
+      const int j = 8 * (q % 4), c = (q / 4) % PCH, pl = q / (PCH * 4);
+      if (c < w)
+        *reinterpret_cast<u32x4_t*>(dst + pl * plane_stride + (xrow0 + x0 + c) * 32 + j) =
+            pack8(value(pl, j, c), value(pl, j + 1, c), value(pl, j + 2, c), value(pl, j + 3, c), value(pl, j + 4, c),
+                  value(pl, j + 5, c), value(pl, j + 6, c), value(pl, j + 7, c));
+    }
+  };
+  switch (kind) {
+    case PK_AGU:
+      // a_gu [planes][n][32][Hd] and at_gu [n][planes][Hd][32]
+      rows_along_x(S.a_gu, P, (int64_t)n * 32 * Hd, (int64_t)g * 32, Hd,
+                   [&](int pl, int j, int c) { return gu(pl, j, c); });
+      slots_along_row(S.at_gu, P, (int64_t)Hd * 32, (int64_t)g * P * Hd,
+                      [&](int pl, int j, int c) { return gu(pl, j, c); });
+      break;
+    case PK_ADN:
+      // a_dn [n][32][In] and at_dn [n][In][32]
+      rows_along_x(S.a_dn, 1, 0, (int64_t)g * 32, In, [&](int, int j, int c) { return one(j, c); });
+      slots_along_row(S.at_dn, 1, 0, (int64_t)g * In, [&](int, int j, int c) { return one(j, c); });
+      break;
+    case PK_BGU:
+      // fwd_gu [n][2In][32]: gate rows < In (ranks at slots 0..r-1), up rows >= In (plane 1 with two planes, else
+      // the up slots of the one plane); bt_gu [planes][n][32][2In]: gate columns < In, up columns >= In
+      slots_along_row(S.fwd_gu, 2, (int64_t)In * 32, (int64_t)g * 2 * In, [&](int half, int j, int c) {
+        if (!half) return one(j, c);
+        const int k = up_rank(P - 1, j);
+        return k >= 0 ? sa[1][k][c] : 0.f;
+      });
+      for (int half = 0; half < 2; ++half)
+        rows_along_x(S.bt_gu + half * In, P, (int64_t)n * 32 * 2 * In, (int64_t)g * 32, 2 * In, [&](int pl, int j, int c) {
+          const int k = half ? up_rank(pl, j) : gate_rank(pl, j);
+          return k >= 0 ? sa[half][k][c] : 0.f;
+        });
+      break;
+    default:
+      // fwd_dn [n][Hd][32] and bt_dn [n][32][Hd]
+      slots_along_row(S.fwd_dn, 1, 0, (int64_t)g * Hd, [&](int, int j, int c) { return one(j, c); });
+      rows_along_x(S.bt_dn, 1, 0, (int64_t)g * 32, Hd, [&](int, int j, int c) { return one(j, c); });
+      break;
+  }
 }
 
 // ext[row * ldx + 0:32] = bf16(scale * A_src[src(row)] . wcat^T) for the rows of SEL / SHARED tiles (one 32-wide
@@ -489,13 +525,29 @@ extern "C" int smel_lora_prep_sets(const smel_lora_set* sets, int32_t n_sets, in
     SMEL_REQUIRE(S.n * planes * 32 * std::max(Hd, 2 * In) < (1ll << 31), SMEL_EUNSUPPORTED,
                  "lora_prep: set %d: layouts too large", i);
     SMEL_REQUIRE(((uintptr_t)S.fwd_gu | (uintptr_t)S.fwd_dn | (uintptr_t)S.a_gu | (uintptr_t)S.a_dn |
-                  (uintptr_t)S.bt_dn | (uintptr_t)S.bt_gu | (uintptr_t)S.at_gu | (uintptr_t)S.at_dn) % 4 == 0,
-                 SMEL_EUNSUPPORTED, "lora_prep: set %d: outputs must be 4-byte aligned", i);
+                  (uintptr_t)S.bt_dn | (uintptr_t)S.bt_gu | (uintptr_t)S.at_gu | (uintptr_t)S.at_dn) % 16 == 0,
+                 SMEL_EUNSUPPORTED, "lora_prep: set %d: outputs must be 16-byte aligned", i);
+    SMEL_REQUIRE(((uintptr_t)S.A_gate | (uintptr_t)S.B_gate | (uintptr_t)S.A_up | (uintptr_t)S.B_up |
+                  (uintptr_t)S.A_down | (uintptr_t)S.B_down) % 16 == 0,
+                 SMEL_EUNSUPPORTED, "lora_prep: set %d: factors must be 16-byte aligned", i);
     pa.set[nz++] = S;   // empty sets are left out of the launch
   }
   if (nz == 0) return 0;
-  dim3 grid(256, 8, nz);
-  lora_prep_kernel<<<grid, 256, 0, stream>>>(pa);
+  SMEL_REQUIRE(Hd % 32 == 0 && In % 32 == 0, SMEL_EUNSUPPORTED,
+               "lora_prep: Hd=%lld and In=%lld must be multiples of 32 (as the GEMMs' dimensions)", (long long)Hd,
+               (long long)In);
+  // blocks: per set, n experts x chunks of each kind
+  const int64_t ch_h = (Hd + PCH - 1) / PCH, ch_i = (In + PCH - 1) / PCH;
+  int64_t b = 0;
+  for (int i = 0; i < PREP_MAX_SETS; ++i)
+    for (int k = 0; k < PK_N; ++k) {
+      pa.first[i * PK_N + k] = (int)b;
+      if (i < nz) b += pa.set[i].n * ((k == PK_AGU || k == PK_BDN) ? ch_h : ch_i);
+    }
+  pa.first[PREP_MAX_SETS * PK_N] = (int)b;
+  SMEL_REQUIRE(b < (1ll << 31), SMEL_EUNSUPPORTED, "lora_prep: too many blocks");
+  if (b == 0) return 0;
+  lora_prep_kernel<<<(unsigned)b, 256, 0, stream>>>(pa);
   return smel::launch_status();
 }
 
