@@ -170,20 +170,24 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
                                                        int Kd, float ssel, float ssh, uint16_t* __restrict__ ext,
                                                        int ldx, int max_tiles) {
   __shared__ float red[XW * 64 * 16];
-  __shared__ int lt[XLT];
+  __shared__ int4 lt[XLT];   // the call's LoRA tiles (whole entries: no second load per item)
   __shared__ int wcnt[XT_PER][XW];
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
   // ---- the LoRA tiles of this call, in tile order
   const int nt = min(n_tiles[0], max_tiles);
   bool fl[XT_PER];
+  int4 te[XT_PER];
 #pragma unroll
   for (int p = 0; p < XT_PER; ++p) {
     const int i = p * 512 + tid;
     fl[p] = false;
+    te[p] = int4{0, 0, 0, 0};
     if (i < nt) {
-      const int4 t = tiles[i];
-      const int kind = (gkind ? gkind[t.x] : t.w) >> 16;
+      int4 t = tiles[i];
+      if (gkind) t.w = gkind[t.x];   // the group kind, in the entry's fourth field from here on
+      const int kind = t.w >> 16;
       fl[p] = (kind == SMEL_KIND_SEL && wsel) || (kind == SMEL_KIND_SHARED && wsh);
+      te[p] = t;
     }
   }
   uint64_t msk[XT_PER];
@@ -202,15 +206,15 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
       off += v < w ? wcnt[p][v] : 0;
       total += wcnt[p][v];
     }
-    if (fl[p]) lt[off + __popcll(msk[p] & ((1ull << l) - 1ull))] = p * 512 + tid;
+    if (fl[p]) lt[off + __popcll(msk[p] & ((1ull << l) - 1ull))] = te[p];
   }
   __syncthreads();
   // ---- (tile, slice) items
   const rsrc_t ra = make_rsrc(A, (uint64_t)a_rows * lda * 2);
   const int nk = (Kd + 63) / 64;
   for (int item = blockIdx.x; item < 4 * total; item += gridDim.x) {
-    const int4 t = tiles[lt[item >> 2]];
-    const int kind = (gkind ? gkind[t.x] : t.w) >> 16, idx = (gkind ? gkind[t.x] : t.w) & 0xffff;
+    const int4 t = lt[item >> 2];
+    const int kind = t.w >> 16, idx = t.w & 0xffff;
     const int m = item & 3;
     const int nrows = min(t.z - t.y, 128);
     if (m * 32 >= nrows) continue;   // uniform over the block
@@ -227,15 +231,20 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
     f32x16_t acc = f32x16_t{};
     for (int j0 = w; j0 < nk; j0 += XW * XPRE) {
       u32x4_t av[XPRE][4], bv[XPRE][4];
+      // the factor rows first: they do not wait for the row's token (a gathered row's address does)
 #pragma unroll
       for (int p = 0; p < XPRE; ++p) {
         const int kk = (j0 + XW * p) * 64 + 32 * hi;
         const bool ok = kk + 32 <= Kd;   // Kd % 32 == 0: a lane half's 32 k are all in or all out
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          av[p][s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
-          bv[p][s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
-        }
+        for (int s = 0; s < 4; ++s) bv[p][s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
+      }
+#pragma unroll
+      for (int p = 0; p < XPRE; ++p) {
+        const int kk = (j0 + XW * p) * 64 + 32 * hi;
+        const bool ok = kk + 32 <= Kd;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) av[p][s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
       }
       __builtin_amdgcn_sched_barrier(0);   // every load of the batch is issued before the first MFMA waits
 #pragma unroll
@@ -245,18 +254,19 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[(w * 16 + r) * 64 + l] = acc[r];   // lane-contiguous: no bank conflicts
-    __syncthreads();
-    if (w == 0) {
+    lds_barrier();
+    // wave w sums accumulator registers 2w and 2w + 1 over the waves, in wave order, and stores those rows
+    static_assert(2 * XW == 16, "two accumulator registers per wave");
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = red[r * 64 + l];
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = 2 * w + rr;
+      float v = red[r * 64 + l];
 #pragma unroll
-        for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
-        const int orow = m * 32 + acc_row(r, l);
-        if (orow < nrows) ext[(int64_t)(t.y + orow) * ldx + r32] = f2bf(scale * v);
-      }
+      for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
+      const int orow = m * 32 + acc_row(r, l);
+      if (orow < nrows) ext[(int64_t)(t.y + orow) * ldx + r32] = f2bf(scale * v);
     }
-    __syncthreads();   // red is reused by the next item
+    lds_barrier();   // red is reused by the next item
   }
 }
 
