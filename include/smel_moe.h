@@ -135,6 +135,13 @@ int smel_int4_fast_ok(const uint16_t* scale, const uint16_t* zero, int64_t n, in
 int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T, int64_t H,
                int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi, int32_t* topi32,
                float* sgate, uint16_t* logits, hipStream_t stream);
+/* smel_route that also counts the dispatch's histograms of its own topi (route followed by the dispatch of
+ * routed_experts, smel/moe.py:162-167 then :216-223): disp_ws [smel_dispatch_ws_size(T*K, E)] int32 is the workspace
+ * the following smel_dispatch_counted of the same topi takes; it is cleared here and left holding the per-block expert
+ * counts, so the dispatch skips its histogram launch. Results otherwise those of smel_route. */
+int smel_route_counted(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T, int64_t H,
+                       int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi,
+                       int32_t* topi32, float* sgate, uint16_t* logits, int32_t* disp_ws, hipStream_t stream);
 /* Row stride (elements) of smel_route's logits workspace (host-side, no GPU call); -1 for E <= 0. */
 int64_t smel_route_ld(int64_t E, int32_t with_shared_gate);
 
@@ -174,6 +181,12 @@ int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, in
                   hipStream_t stream);
 /* int32 elements of smel_dispatch's workspace (host-side, no GPU call); -1 for bad sizes. */
 int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
+/* smel_dispatch of the ids that smel_route_counted selected, with the workspace it filled: the histogram launch is
+ * skipped (same results as smel_dispatch; ws must come from smel_route_counted of exactly these ids). */
+int smel_dispatch_counted(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
+                          int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
+                          int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err,
+                          int32_t* ws, hipStream_t stream);
 /* smel_dispatch without the workspace argument; it allocates nothing. No counterpart in the reference: it exists
  * for callers that cannot allocate device memory (code under HIP-graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). The workspace is a fixed array of smel_dispatch_noalloc_max_ws() int32 held by the library on

@@ -195,6 +195,9 @@ SMEL_DEV int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 // [x c, (x + 1) c) of the list (c = ceil(n_tiles / 8)) in order, so with a list in group order the tiles of one group
 // run side by side on one XCD and share its weights in that XCD's L2.
 constexpr int NXCD = 8;
+// Slots per block of the dispatch's per-block expert histograms (the dispatch workspace holds [blocks][E] counts,
+// then one bad-id flag per block); smel_route_counted writes the same histograms.
+constexpr int DISPATCH_SLOTS = 1024;
 inline int64_t xcd_grid(int64_t max_tiles) { return (max_tiles + NXCD - 1) / NXCD * NXCD; }
 SMEL_DEV bool xcd_tile_chunk(int n_tiles, int nblk, int& tile, int& nb) {
   const int b = blockIdx.x;

@@ -22,6 +22,7 @@ namespace {
 
 constexpr int NW = 16;        // waves per block
 constexpr int DB = NW * 64;   // slots per block
+static_assert(DB == DISPATCH_SLOTS, "the histogram blocks smel_route_counted fills");
 constexpr int MAXE = 512;
 constexpr int HCH = 12288;    // histogram entries per LDS chunk of dispatch_scan (48 KB)
 
@@ -456,10 +457,11 @@ extern "C" int64_t smel_dispatch_ws_size(int64_t TK, int64_t E) {
   return nb * E + nb;
 }
 
-extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
-                             int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
-                             int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles, int32_t* tiles_grouped,
-                             int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream) {
+namespace {
+int dispatch_impl(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
+                  int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inv,
+                  int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t* ws, bool counted,
+                  hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && shared_rows >= 0 && m_tile > 0, SMEL_EINVAL, "dispatch: bad sizes");
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "dispatch: E=%lld > %d experts", (long long)E, MAXE);
   SMEL_REQUIRE(T * K < (1ll << 30), SMEL_EUNSUPPORTED, "dispatch: T*K too large");
@@ -470,7 +472,7 @@ extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, in
   const int nb = (int)((TK + DB - 1) / DB);
   int32_t* hist = ws;
   int32_t* bad = ws ? ws + (int64_t)nb * E : nullptr;
-  if (nb > 0) {
+  if (nb > 0 && !counted) {
     dispatch_hist<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)TK, (int)E, hist, bad);
     const int st = smel::launch_status();
     if (st) return st;
@@ -489,6 +491,24 @@ extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, in
     dispatch_scatter<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, (int)TK, (int)E, hist, order, inv);
   }
   return smel::launch_status();
+}
+}  // namespace
+
+extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
+                             int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
+                             int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles, int32_t* tiles_grouped,
+                             int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream) {
+  return dispatch_impl(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
+                       tiles_grouped, n_tiles, err, ws, false, stream);
+}
+
+extern "C" int smel_dispatch_counted(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
+                                     int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
+                                     int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
+                                     int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t* ws,
+                                     hipStream_t stream) {
+  return dispatch_impl(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
+                       tiles_grouped, n_tiles, err, ws, true, stream);
 }
 
 extern "C" int64_t smel_dispatch_noalloc_max_ws(void) { return SCRATCH_INTS; }

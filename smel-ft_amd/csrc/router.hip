@@ -16,7 +16,8 @@ constexpr int MAXE = 512;      // experts handled by the selection (up to 8 logi
 template <int NPL, typename Get>
 SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict__ probs, uint16_t* __restrict__ topv,
                           float* __restrict__ topv32, int64_t* __restrict__ topi, int32_t* __restrict__ topi32,
-                          float* __restrict__ topv_f32, const uint16_t* __restrict__ pes) {
+                          float* __restrict__ topv_f32, const uint16_t* __restrict__ pes,
+                          int32_t* __restrict__ hist) {
   const int l = lane_id();
   float v[NPL];
 #pragma unroll
@@ -88,6 +89,8 @@ SMEL_DEV void select_topk(Get logit, int E, int K, int64_t t, float* __restrict_
     }
     topi[t * K + l] = i;
     topi32[t * K + l] = i;
+    // the dispatch's per-block histogram: an integer count, the same whatever order the adds land in
+    if (hist) atomicAdd(&hist[(int)((t * K + l) / DISPATCH_SLOTS) * E + i], 1);
   }
 }
 
@@ -117,8 +120,13 @@ SMEL_DEV f32x4_t mfma16r(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
 __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ gw,
                                                            const uint16_t* __restrict__ sg, int T, int H, int E,
-                                                           int ldl, uint16_t* __restrict__ logits) {
+                                                           int ldl, uint16_t* __restrict__ logits,
+                                                           int32_t* __restrict__ zero_ws, int zero_n) {
   __shared__ __attribute__((aligned(1024))) uint16_t WS[RNST][RSTAGE];
+  if (zero_ws) {   // the dispatch workspace the selection counts into (the selection runs after this launch)
+    const int nblk = gridDim.x * gridDim.y, b = blockIdx.y * gridDim.x + blockIdx.x;
+    for (int i = b * 256 + (int)threadIdx.x; i < zero_n; i += nblk * 256) zero_ws[i] = 0;
+  }
   const int tid = threadIdx.x, l = lane_id(), kq = l >> 4, li = l & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = blockIdx.x * RT, c0 = blockIdx.y * RC;
@@ -205,25 +213,26 @@ __global__ __launch_bounds__(256) void route_select(const uint16_t* __restrict__
                                                     uint16_t* __restrict__ topv, float* __restrict__ topv32,
                                                     int64_t* __restrict__ topi, int32_t* __restrict__ topi32,
                                                     float* __restrict__ sgate, float* __restrict__ topv_f32,
-                                                    const uint16_t* __restrict__ pes) {
+                                                    const uint16_t* __restrict__ pes, int32_t* __restrict__ hist) {
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const uint16_t* row = logits + t * ldl;
-  select_topk<NPL>([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topv32, topi, topi32, topv_f32, pes);
+  select_topk<NPL>([&](int e) { return bf2f(row[e]); }, E, K, t, probs, topv, topv32, topi, topi32, topv_f32, pes,
+                   hist);
   if (sgate && lane_id() == 0) sgate[t] = 1.0f / (1.0f + expf(-bf2f(row[sg_col])));
 }
 
 // The selection launch for E experts: 4 logits per lane up to 256 experts, 8 up to 512.
 void launch_select(hipStream_t stream, const uint16_t* logits, int ldl, int T, int E, int K, int sg_col, float* probs,
                    uint16_t* topv, float* topv32, int64_t* topi, int32_t* topi32, float* sgate, float* topv_f32,
-                   const uint16_t* pes) {
+                   const uint16_t* pes, int32_t* hist = nullptr) {
   const unsigned grid = (unsigned)((T + 3) / 4);
   if (E <= 256)
     route_select<4><<<grid, 256, 0, stream>>>(logits, ldl, T, E, K, sg_col, probs, topv, topv32, topi, topi32, sgate,
-                                               topv_f32, pes);
+                                               topv_f32, pes, hist);
   else
     route_select<8><<<grid, 256, 0, stream>>>(logits, ldl, T, E, K, sg_col, probs, topv, topv32, topi, topi32, sgate,
-                                               topv_f32, pes);
+                                               topv_f32, pes, hist);
 }
 
 // Backward of route (+ shared gate): one wave per token.
@@ -384,9 +393,9 @@ __global__ __launch_bounds__(256) void dtopv_kernel(const float* __restrict__ dw
 }
 
 void launch_logits(hipStream_t stream, const uint16_t* x, const uint16_t* gw, const uint16_t* sg, int T, int H, int E,
-                   int ldl, uint16_t* logits) {
+                   int ldl, uint16_t* logits, int32_t* zero_ws = nullptr, int zero_n = 0) {
   const dim3 grid((unsigned)((T + RT - 1) / RT), (unsigned)((ldl + RC - 1) / RC));
-  route_logits_kernel<<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits);
+  route_logits_kernel<<<grid, 256, 0, stream>>>(x, gw, sg, T, H, E, ldl, logits, zero_ws, zero_n);
 }
 
 
@@ -405,22 +414,44 @@ extern "C" int64_t smel_route_ld(int64_t E, int32_t with_shared_gate) {
   return E <= 0 ? -1 : (E + 31) / 32 * 32 + (with_shared_gate ? 32 : 0);
 }
 
-extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T,
-                          int64_t H, int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi,
-                          int32_t* topi32, float* sgate, uint16_t* logits, hipStream_t stream) {
+namespace {
+int route_impl(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T, int64_t H,
+               int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi, int32_t* topi32,
+               float* sgate, uint16_t* logits, int32_t* disp_ws, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && H > 0 && E > 0 && K > 0, SMEL_EINVAL, "route: bad sizes");
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "route: E=%lld > %d experts", (long long)E, MAXE);
   SMEL_REQUIRE(K <= E && K <= 16, SMEL_EUNSUPPORTED, "route: top_k=%lld must be <= min(E, 16)", (long long)K);
   SMEL_REQUIRE(H % 64 == 0, SMEL_EUNSUPPORTED, "route: hidden %lld must be a multiple of 64", (long long)H);
   SMEL_REQUIRE(!shared_gate_w || sgate, SMEL_EINVAL, "route: sgate output needed with shared_gate_w");
   SMEL_REQUIRE(T * H * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "route: x larger than 2 GiB");
+  SMEL_REQUIRE(T * K < (1ll << 30), SMEL_EUNSUPPORTED, "route: T*K too large");
   if (T == 0) return 0;
   SMEL_REQUIRE(x && gate_w && probs && topv && topi && topi32 && logits, SMEL_EINVAL, "route: null pointer");
   const int64_t ldl = smel_route_ld(E, shared_gate_w != nullptr);
-  launch_logits(stream, x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits);
+  // the dispatch workspace: [ceil(T K / 1024)][E] histogram counts, then one bad-id flag per block (smel_dispatch)
+  const int64_t nb = (T * K + DISPATCH_SLOTS - 1) / DISPATCH_SLOTS;
+  launch_logits(stream, x, gate_w, shared_gate_w, (int)T, (int)H, (int)E, (int)ldl, logits, disp_ws,
+                (int)(disp_ws ? nb * E + nb : 0));
   launch_select(stream, logits, (int)ldl, (int)T, (int)E, (int)K, (int)((E + 31) / 32 * 32), probs, topv, topv32,
-                topi, topi32, shared_gate_w ? sgate : nullptr, nullptr, nullptr);
+                topi, topi32, shared_gate_w ? sgate : nullptr, nullptr, nullptr, disp_ws);
   return smel::launch_status();
+}
+}  // namespace
+
+extern "C" int smel_route(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w, int64_t T,
+                          int64_t H, int64_t E, int64_t K, float* probs, uint16_t* topv, float* topv32, int64_t* topi,
+                          int32_t* topi32, float* sgate, uint16_t* logits, hipStream_t stream) {
+  return route_impl(x, gate_w, shared_gate_w, T, H, E, K, probs, topv, topv32, topi, topi32, sgate, logits, nullptr,
+                    stream);
+}
+
+extern "C" int smel_route_counted(const uint16_t* x, const uint16_t* gate_w, const uint16_t* shared_gate_w,
+                                  int64_t T, int64_t H, int64_t E, int64_t K, float* probs, uint16_t* topv,
+                                  float* topv32, int64_t* topi, int32_t* topi32, float* sgate, uint16_t* logits,
+                                  int32_t* disp_ws, hipStream_t stream) {
+  SMEL_REQUIRE(disp_ws || T == 0, SMEL_EINVAL, "route_counted: null dispatch workspace");
+  return route_impl(x, gate_w, shared_gate_w, T, H, E, K, probs, topv, topv32, topi, topi32, sgate, logits, disp_ws,
+                    stream);
 }
 
 extern "C" int smel_route_logits(const uint16_t* logits, int64_t T, int64_t E, int64_t K, float* probs,

@@ -637,12 +637,13 @@ def _prep_lora(ex: LayerExperts, lora_ex, lora_sh, with_shared: bool, H: int, de
 
 
 def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
-                      need_grad: bool, c: _Ctx, prep=None, shared_rows=None):
+                      need_grad: bool, c: _Ctx, prep=None, shared_rows=None, counted_ws=None):
     """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up, down, sgate fp32 [T], gate_up^T, down^T) or None
     (packed forward and transposed layouts of the shared expert's [2I,H] / [H,I] weights). ``prep`` = (_Fork,
     (lb_ex, lb_sh)) when the LoRA layouts were launched on a side stream (joined before their first use).
     ``shared_rows`` = (sgate fp32 [T], y_shared bf16 [T, H]) adds a shared expert computed elsewhere (one whose
-    intermediate size differs from the experts') to the combine."""
+    intermediate size differs from the experts') to the combine. ``counted_ws`` = the dispatch workspace that
+    smel_route_counted filled for these ids (the dispatch then skips its histogram launch)."""
     T, H = x.shape
     E = ex.E
     dev = x.device
@@ -654,16 +655,16 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, tiles_g, ntiles, err = i32(maxt * 4), i32(maxt * 4), i32(1), i32(1)
-    dws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
+    dws = counted_ws if counted_ws is not None else i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
     if prep is None:   # LoRA layouts on a side stream, overlapping the dispatch
         fork = _Fork(dev, 2)
         with fork:
             bufs = _prep_lora(ex, lora_ex, lora_sh, shared is not None, H, dev)
         prep = (fork, bufs)
     gk_groups = ex.gkind(shared is not None, dev)
-    L.call("smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K, E, rows_sh, M_TILE, L.ptr(gk_groups), L.ptr(counts),
-           L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err),
-           L.ptr(dws), st)
+    L.call("smel_dispatch_counted" if counted_ws is not None else "smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K,
+           E, rows_sh, M_TILE, L.ptr(gk_groups), L.ptr(counts), L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles),
+           L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st, tag="smel_dispatch")
     gk = None   # the tile list carries each tile's group kind
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):
@@ -903,8 +904,11 @@ class _MoELayerFn(torch.autograd.Function):
         fork = _Fork(dev, 2)   # LoRA layouts overlap the router and the dispatch
         with fork:
             bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"] if fuse else None, fuse, H, dev)
-        L.call("smel_route", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs), L.ptr(topv),
-               L.ptr(topv32), L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.stream())
+        # the router also counts the dispatch's per-block histograms of its picks into the dispatch workspace
+        dws = torch.empty(max(1, L.load().smel_dispatch_ws_size(T * K, E)), dtype=torch.int32, device=dev)
+        L.call("smel_route_counted", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs),
+               L.ptr(topv), L.ptr(topv32), L.ptr(topi), L.ptr(topi32), L.ptr(sgate), L.ptr(lg), L.ptr(dws), L.stream(),
+               tag="smel_route")
         if stats is not None:
             stats(probs, topv, topi)
         c = _Ctx()
@@ -919,7 +923,7 @@ class _MoELayerFn(torch.autograd.Function):
             c.split = (sv, pgu_t, pdn_t, lsh, sgate)
         out = _forward_pipeline(x, plan["ex"], K, topv32, topi32, False, shared, plan["lora_ex"],
                                 plan["lora_sh"] if fuse else None, plan["need_grad"], c, prep=(fork, bufs),
-                                shared_rows=shared_rows)
+                                shared_rows=shared_rows, counted_ws=dws)
         if plan["need_grad"]:
             c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw))
             c.plan_lora_sh = plan["lora_sh"]

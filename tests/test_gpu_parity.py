@@ -360,6 +360,55 @@ def test_route_fused(T, H, E, K, shared):
         assert torch.allclose(sgate.cpu(), ref, rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("T,H,E,K,shared", [(4092, 2048, 256, 8, True), (77, 128, 16, 3, False),
+                                           (1300, 256, 512, 8, True)])
+def test_route_counted_then_dispatch_counted(T, H, E, K, shared):
+    """smel_route_counted + smel_dispatch_counted (the router counting the dispatch's histograms) against smel_route +
+    smel_dispatch: every output bit for bit, with the workspace starting as garbage."""
+    L = _lib()
+    lib = L.load()
+    _say(f"route/dispatch counted T{T} H{H} E{E} K{K}")
+    gen = torch.Generator().manual_seed(T + E)
+    xd = torch.randn(T, H, generator=gen).to(torch.bfloat16).to(DEV)
+    gwd = (torch.randn(E, H, generator=gen) * 0.02).to(torch.bfloat16).to(DEV)
+    sgd = (torch.randn(H, generator=gen) * 0.02).to(torch.bfloat16).to(DEV) if shared else None
+    TK, sh = T * K, (T if shared else 0)
+    maxt = lib.smel_dispatch_max_tiles(TK, E, sh, 128)
+    gk = torch.arange(E + (1 if shared else 0), dtype=torch.int32, device=DEV) * 5
+
+    def run(counted):
+        f32 = lambda *s: torch.full(s, float("nan"), dtype=torch.float32, device=DEV)
+        i32 = lambda n: torch.full((n,), -7, dtype=torch.int32, device=DEV)
+        o = dict(probs=f32(T, E), topv=torch.zeros(T, K, dtype=torch.bfloat16, device=DEV), topv32=f32(T, K),
+                 topi=torch.zeros(T, K, dtype=torch.int64, device=DEV), topi32=i32(TK), sgate=f32(T),
+                 lg=torch.zeros(T, lib.smel_route_ld(E, int(shared)), dtype=torch.bfloat16, device=DEV),
+                 counts=i32(E), offsets=i32(E + 1), order=i32(TK), inv=i32(TK), tiles=i32(4 * maxt),
+                 tiles_g=i32(4 * maxt), ntiles=i32(1), err=i32(1))
+        ws = torch.randint(-1000, 1000, (max(1, lib.smel_dispatch_ws_size(TK, E)),), dtype=torch.int32, device=DEV)
+        route = [L.ptr(xd), L.ptr(gwd), L.ptr(sgd), T, H, E, K] + [L.ptr(o[k]) for k in
+                                                                   ("probs", "topv", "topv32", "topi", "topi32")] + \
+                [L.ptr(o["sgate"]) if shared else None, L.ptr(o["lg"])]
+        if counted:
+            L.call("smel_route_counted", *route, L.ptr(ws), L.stream())
+        else:
+            L.call("smel_route", *route, L.stream())
+        L.call("smel_dispatch_counted" if counted else "smel_dispatch", L.ptr(o["topi32"]), 0, T, K, E, sh, 128,
+               L.ptr(gk), *[L.ptr(o[k]) for k in ("counts", "offsets", "order", "inv", "tiles", "tiles_g", "ntiles",
+                                                  "err")], L.ptr(ws), L.stream())
+        torch.cuda.synchronize()
+        return {k: v.cpu() for k, v in o.items()}
+
+    want, got = run(False), run(True)
+    assert want["err"][0] == 0
+    for k in want:
+        if k == "sgate" and not shared:
+            continue
+        a, b = want[k], got[k]
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b) or \
+            (a.dtype.is_floating_point and torch.equal(torch.nan_to_num(a, 7.0), torch.nan_to_num(b, 7.0))), k
+
+
 # ------------------------------------------------------------------------------------------------------ dispatch
 
 
