@@ -254,6 +254,26 @@ int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
                  const int32_t* order,
                  int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act, uint16_t* out,
                  int64_t ldo, uint16_t* hsave, hipStream_t stream);
+/* The down projection's LoRA rows without a separate smel_lora_ext launch (lora_linear's x A^T, smel/lora.py:61-69,
+ * for the down LoRA of the selected / shared experts): */
+typedef struct smel_fwd_lora_rows {
+  const uint16_t* a_sel;  /* a_dn layout of the selected experts [n_sel][32][I] (smel_lora_prep), or NULL          */
+  const uint16_t* a_sh;   /* a_dn layout of the shared expert [32][I], or NULL                                     */
+  float scale_sel, scale_sh;
+  float* part;            /* [rows][parts][32] fp32, 16-B aligned; NULL: off                                         */
+  int32_t parts;          /* smel_gmm_fwd_nblocks(2 I, 1): the gate_up GEMM's column blocks                         */
+  uint16_t* ext_out;      /* [rows][32] bf16, 16-B aligned, or NULL                                                 */
+} smel_fwd_lora_rows;
+/* smel_gmm_fwd with lr: the gate_up forward (epilogue 1) writes, for the rows of SEL / SHARED tiles whose LoRA set
+ * is given, part[row][b][j] = scale * sum over column block b's columns c of h[row][c] a[j][c] (h = the bf16 SiLU-gate
+ * output it stores); the down forward (epilogue 0, ext unused) takes ext[row][j] = bf16(sum_b part[row][b][j]) as
+ * its K-extension rows and, if ext_out, stores them there (the LoRA gradients read them). */
+int smel_gmm_fwd_lr(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
+                    int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
+                    const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
+                    uint16_t* out, int64_t ldo, uint16_t* hsave, const smel_fwd_lora_rows* lr, hipStream_t stream);
+/* Column blocks of smel_gmm_fwd for R weight rows and the epilogue (host-side, no GPU call); -1 for R <= 0. */
+int64_t smel_gmm_fwd_nblocks(int64_t R, int32_t epilogue);
 
 /* ---- (A13) replaces the combine of routed_experts, smel/moe.py:248-252 (+ the shared add of :263):
  * out[t] = bf16( sum_k topv[t,k] * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Ysh[t])] ), k in fixed order, topv fp32;

@@ -56,11 +56,13 @@ struct FwdArgs {
   int a_gather, TK, topk, act;
   int N, K;   // N = w.R (weight rows), K = w.C
   int nblk;   // column blocks per tile
+  smel_fwd_lora_rows lr;   // down-LoRA rows: produced by the gate_up epilogue, taken by the down K-extension
+  bool lr_on;
 };
 
 template <int EPI, bool Q4, int NS, bool FAST>
 SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
-                       uint16_t* S2, uint16_t* S3, int* rowmap) {
+                       uint16_t* S2, uint16_t* S3, int* rowmap, uint16_t* X) {
   const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = a.K;
@@ -107,6 +109,33 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     rsz = rw;
     wo0 = fv0 ? (uint32_t)(fr0 * nk * 4096 + l * 16) : OOB;
     wo1 = fv1 ? (uint32_t)(fr1 * nk * 4096 + l * 16) : OOB;
+  }
+  // ---- down LoRA rows from the gate_up forward's per-column-block partials (LoRA tiles of the down projection):
+  // summed in block order into the bf16 tile X [128][32] before the main loop (no accumulator is live yet); the same
+  // rows in every column block of the tile, column block 0 also stores them for the LoRA gradients
+  if (EPI == 0 && a.lr_on && a.lr.part &&
+      ((kind == SMEL_KIND_SEL && ws.ext_sel) || (kind == SMEL_KIND_SHARED && ws.ext_sh))) {
+    const int P = a.lr.parts;
+    const rsrc_t rp = make_rsrc(a.lr.part + (int64_t)row0 * P * 32, (uint64_t)nrows * P * 128);
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {   // 256 threads x 8 values x 2 passes = 128 rows x 32
+      const int row = (tid >> 2) + 64 * pass, k0 = 8 * (tid & 3);
+      float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < P; ++p) {
+        const uint32_t o = row < nrows ? (uint32_t)((row * P + p) * 32 + k0) * 4 : OOB;
+        const u32x4_t x0 = ld16(rp, o), x1 = ld16(rp, o == OOB ? OOB : o + 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          v[t] += __uint_as_float(x0[t]);
+          v[4 + t] += __uint_as_float(x1[t]);
+        }
+      }
+      const u32x4_t h = u32x4_t{pack2bf(v[0], v[1]), pack2bf(v[2], v[3]), pack2bf(v[4], v[5]), pack2bf(v[6], v[7])};
+      *reinterpret_cast<u32x4_t*>(X + row * 32 + k0) = h;
+      if (nb == 0 && a.lr.ext_out && row < nrows)
+        *reinterpret_cast<u32x4_t*>(a.lr.ext_out + (int64_t)(row0 + row) * 32 + k0) = h;
+    }
+    lds_barrier();
   }
   // ---- A staging: wave-load ii of wave w fills rows 8 g .. 8 g + 7 (g = 4 w + ii) of a stage, 1 KB; lane i writes
   // physical chunk i % 8 of row 8 g + i / 8, i.e. logical chunk c = (i % 8) ^ swz(row).
@@ -263,7 +292,8 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   // 64 wide, the gate fragment (0) takes plane 0 and the up fragment (1) plane 1.
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * a.N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
-  if (a.ext && eb) {
+  const bool xrows = EPI == 0 && a.lr_on && a.lr.part;   // K-extension rows in X (filled at the tile's start)
+  if ((a.ext || xrows) && eb) {
     const bool two = (ws.flags & SMEL_WSET_EXT2) != 0;   // uniform
     const uint32_t xb = two ? 128u : 64u;                 // ext row bytes
     const rsrc_t re = make_rsrc(eb, (uint64_t)a.N * 64);
@@ -280,7 +310,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const uint32_t o = row < nrows ? (uint32_t)row * xb + 32 * hi + 16 * s : OOB;
-        const u32x4_t af = ld16(rx, o);
+        const u32x4_t af = xrows ? *reinterpret_cast<const u32x4_t*>(X + row * 32 + 16 * hi + 8 * s) : ld16(rx, o);
         const u32x4_t af1 = two ? ld16(rx, o == OOB ? OOB : o + 64) : af;
         acc[m][0] = mfma32(af, b0[s], acc[m][0]);
         acc[m][1] = mfma32(af1, b1[s], acc[m][1]);
@@ -292,6 +322,18 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   // output. Tile rows are 128 B-chunked and XOR-swizzled like the A stages (phys chunk = c ^ (row & 7)).
   __syncthreads();   // every wave is done with the ring (its loads landed, its reads returned)
   if constexpr (EPI == 1) {
+    // the down LoRA's A factor of this tile's group (SEL / SHARED with a LoRA), if the partials are wanted
+    const uint16_t* xa = nullptr;
+    float xscale = 0.f;
+    if (a.lr_on && a.lr.part) {
+      if (kind == SMEL_KIND_SEL && a.lr.a_sel) {
+        xa = a.lr.a_sel + (int64_t)idx * 32 * (a.N / 2);
+        xscale = a.lr.scale_sel;
+      } else if (kind == SMEL_KIND_SHARED && a.lr.a_sh) {
+        xa = a.lr.a_sh;
+        xscale = a.lr.scale_sh;
+      }
+    }
     // g tile [128][128] in S0 (rows 0..63) / S1, u tile in S2 / S3; column = 32 w + r32 inside the block's 128
     const int col = 32 * w + r32;
 #pragma unroll
@@ -326,6 +368,36 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
         if (a.hsave) {
           *reinterpret_cast<u32x4_t*>(a.hsave + grow * a.N + col0) = g;
           *reinterpret_cast<u32x4_t*>(a.hsave + grow * a.N + I + col0) = u;
+        }
+        if (xa)   // h replaces g in the tile (each chunk is read and written by this thread only)
+          *reinterpret_cast<u32x4_t*>((row < 64 ? S0 : S1) + e) = u32x4_t{o[0], o[1], o[2], o[3]};
+      }
+    }
+    if (xa) {
+      // partial down-LoRA projection of the tile's rows over this block's 128 columns of h:
+      // part[row][nb][j] = scale * sum_c h[row][c] a[j][c]; wave w takes rows 32 w .. 32 w + 31
+      __syncthreads();
+      if (w < NS) {
+        const rsrc_t rb = make_rsrc(xa, (uint64_t)32 * I * 2);
+        f32x16_t px = f32x16_t{};
+        const int row = 32 * w + r32;
+        const uint16_t* Hh = row < 64 ? S0 : S1;
+        const int lr_ = row & 63;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int c = 64 * kk + 32 * hi + 8 * s;   // column inside the block's 128
+            const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Hh + lr_ * 128 + 8 * ((c >> 3) ^ (row & 7)));
+            const int gc = nb * 128 + c;
+            const u32x4_t bf = ld16(rb, gc < I ? (uint32_t)(r32 * I + gc) * 2 : OOB);
+            px = mfma32(af, bf, px);
+          }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int orow = 32 * w + acc_row(r, l);
+          if (orow < nrows)
+            a.lr.part[((int64_t)(row0 + orow) * a.lr.parts + nb) * 32 + r32] = xscale * px[r];
         }
       }
     }
@@ -362,12 +434,12 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 
 template <int EPI, bool Q4, bool FAST>
 SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0,
-                          uint16_t* S1, uint16_t* S2, uint16_t* S3, int* rowmap) {
+                          uint16_t* S1, uint16_t* S2, uint16_t* S3, int* rowmap, uint16_t* X) {
   switch ((nrows + 31) >> 5) {
-    case 1: run_tile<EPI, Q4, 1, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
-    case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
-    case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
-    default: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap); break;
+    case 1: run_tile<EPI, Q4, 1, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
+    case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
+    case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
+    default: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
   }
 }
 
@@ -378,6 +450,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __attribute__((aligned(1024))) uint16_t S2[A_STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t S3[A_STAGE];
   __shared__ int rowmap[MT];
+  // the down projection's LoRA rows of a tile (bf16 [128][32]); unused by the gate_up kernel
+  __shared__ __attribute__((aligned(16))) uint16_t X[EPI == 0 ? MT * 32 : 8];
   int tile, nb;
   if (!((a.w.flags & SMEL_WSET_XCD_CHUNK) ? xcd_tile_chunk(a.n_tiles[0], a.nblk, tile, nb)
                                           : xcd_tile(a.n_tiles[0], a.nblk, tile, nb)))
@@ -389,20 +463,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4) {
     if (a.w.flags & SMEL_WSET_FAST_DQ)
-      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap);
+      run_tile_ns<EPI, true, true>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap, X);
     else
-      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap);
+      run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap, X);
   } else {
-    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap);
+    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap, X);
   }
 }
 
 }  // namespace
 
-extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
-                            int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
-                            const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
-                            int32_t act, uint16_t* out, int64_t ldo, uint16_t* hsave, hipStream_t stream) {
+extern "C" int64_t smel_gmm_fwd_nblocks(int64_t R, int32_t epilogue) {
+  if (R <= 0) return -1;
+  return epilogue == 1 ? (R / 2 + 127) / 128 : (R + 255) / 256;
+}
+
+extern "C" int smel_gmm_fwd_lr(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
+                               const int32_t* n_tiles, int64_t max_tiles, const uint16_t* A, int64_t lda,
+                               int64_t a_rows, int32_t a_gather, const int32_t* order, int64_t TK, int64_t topk,
+                               const uint16_t* ext, int32_t epilogue, int32_t act, uint16_t* out, int64_t ldo,
+                               uint16_t* hsave, const smel_fwd_lora_rows* lr, hipStream_t stream) {
   SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_fwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->C && topk > 0, SMEL_EINVAL,
                "gmm_fwd: bad sizes");
@@ -421,8 +501,18 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_fwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_fwd: A larger than 2 GiB");
+  if (lr && lr->part) {
+    SMEL_REQUIRE(epilogue == 1 ? lr->parts == smel_gmm_fwd_nblocks(w->R, 1) : lr->parts >= 1, SMEL_EINVAL,
+                 "gmm_fwd: %d LoRA-row partials per row (the gate_up GEMM's column blocks)", lr->parts);
+    SMEL_REQUIRE(((uintptr_t)lr->part % 16) == 0 && ((uintptr_t)lr->ext_out % 16) == 0, SMEL_EUNSUPPORTED,
+                 "gmm_fwd: LoRA-row partials and rows must be 16-B aligned");
+    SMEL_REQUIRE(epilogue == 1 || !(w->flags & SMEL_WSET_EXT2), SMEL_EINVAL,
+                 "gmm_fwd: the down projection's LoRA has one plane");
+  }
   if (max_tiles == 0) return 0;
   FwdArgs a;
+  a.lr_on = lr && lr->part;
+  if (a.lr_on) a.lr = *lr;
   a.w = *w;
   a.gkind = gkind;
   a.tiles = reinterpret_cast<const int4*>(tiles);
@@ -448,4 +538,12 @@ extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int3
   else
     gmm_fwd_kernel<0><<<grid, 256, 0, stream>>>(a);
   return smel::launch_status();
+}
+
+extern "C" int smel_gmm_fwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
+                            int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
+                            const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
+                            int32_t act, uint16_t* out, int64_t ldo, uint16_t* hsave, hipStream_t stream) {
+  return smel_gmm_fwd_lr(w, gkind, tiles, n_tiles, max_tiles, A, lda, a_rows, a_gather, order, TK, topk, ext,
+                         epilogue, act, out, ldo, hsave, nullptr, stream);
 }

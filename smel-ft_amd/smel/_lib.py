@@ -19,7 +19,7 @@ PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -40,6 +40,12 @@ class WgJob(ctypes.Structure):
     """smel_wg_job of include/smel_moe.h."""
     _fields_ = [("L", vp), ("Rm", vp), ("ldr", i64), ("r_rows", i64), ("r_gather", i32), ("use_w", i32), ("Q", i64),
                 ("ldl", i64), ("dest", (WgDest * 2) * 2)]
+
+
+class FwdLoraRows(ctypes.Structure):
+    """smel_fwd_lora_rows of include/smel_moe.h: the down LoRA's rows produced in the gate_up forward's epilogue."""
+    _fields_ = [("a_sel", vp), ("a_sh", vp), ("scale_sel", ctypes.c_float), ("scale_sh", ctypes.c_float),
+                ("part", vp), ("parts", i32), ("ext_out", vp)]
 
 
 class LoraSet(ctypes.Structure):
@@ -82,6 +88,9 @@ SIGNATURES = {
     "smel_lora_ext": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, vp, i64, i64, vp, vp, i64, f32, f32, vp, i64, vp]),
     "smel_gmm_fwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, i64, vp, vp]),
+    "smel_gmm_fwd_lr": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
+                              vp, i64, vp, ctypes.POINTER(FwdLoraRows), vp]),
+    "smel_gmm_fwd_nblocks": (i64, [i64, i32]),
     "smel_combine": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp]),
     "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, vp, vp, vp, vp, i64, vp, vp]),

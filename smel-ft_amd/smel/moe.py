@@ -689,14 +689,23 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     # the down GEMMs the long-tiles-first order (short tiles fill the last round)
     w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"), planes=planes)
     w_gu.flags |= L.WSET_XCD_CHUNK
-    L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_g), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
-           L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_gu_fwd")
+    # the down LoRA's rows come from the gate_up epilogue (per-column-block partials of h A_dn^T), summed and stored
+    # by the down GEMM: no separate projection launch
+    lr = None
     if any_lora:
-        ext_dn = _lora_ext(tl, actb, I, M, 0, order, TK, K, lb_ex, lb_sh, "a_dn", I, 1, M, dev, st)
+        parts = int(L.load().smel_gmm_fwd_nblocks(2 * I, 1))
+        xpart = torch.empty(M, parts, EXT, dtype=torch.float32, device=dev)
+        ext_dn = bf(M, EXT)
+        lr = L.FwdLoraRows(L.ptr(g(lb_ex, "a_dn")), L.ptr(g(lb_sh, "a_dn")), lb_ex.scale if lb_ex is not None else 0.0,
+                           lb_sh.scale if lb_sh is not None else 0.0, L.ptr(xpart), parts, L.ptr(ext_dn))
+    L.call("smel_gmm_fwd_lr", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_g), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
+           L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave),
+           ctypes.byref(lr) if lr is not None else None, st, tag="gemm_gu_fwd")
     Y = bf(M, H)
     w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
-    L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
-           L.ptr(order), TK, K, L.ptr(ext_dn), 0, _ACT[ex.act], L.ptr(Y), H, None, st, tag="gemm_dn_fwd")
+    L.call("smel_gmm_fwd_lr", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
+           L.ptr(order), TK, K, None, 0, _ACT[ex.act], L.ptr(Y), H, None, ctypes.byref(lr) if lr is not None else None,
+           st, tag="gemm_dn_fwd")
     out = bf(T, H)
     ysh = None
     if shared_rows is not None:
