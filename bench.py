@@ -323,10 +323,12 @@ def time_step(step, steps, warmup, graph):
 
 
 def breakdown_of(step, n):
-    """Per-launch milliseconds of every entry point over n extra eager steps, by HIP events on the launching stream.
-    The side-stream forks of the step run on the main stream for this (launch order kept), so each event pair
-    brackets one launch with nothing beside it: the launch's own duration, as a kernel trace shows it. (With the
-    forks on, a launch's start event also counts the wait for compute units that the forked kernels hold.)"""
+    """Per-launch milliseconds of every entry point over n extra eager steps, by HIP events on the launching stream:
+    the median over its launches (a launch whose start event waited on the host, e.g. for an allocation, would pull
+    a mean far from what a kernel trace shows). The side-stream forks of the step run on the main stream for this
+    (launch order kept), so each event pair brackets one launch with nothing beside it: the launch's own duration.
+    (With the forks on, a launch's start event also counts the wait for compute units that the forked kernels
+    hold.)"""
     from smel import _lib
     from smel import moe
     forks, moe._SIDE_ON = moe._SIDE_ON, frozenset()
@@ -338,7 +340,7 @@ def breakdown_of(step, n):
     finally:
         moe._SIDE_ON = forks
     res = tm.results()
-    return {k: round(statistics.mean(v), 4) for k, v in sorted(res.items(), key=lambda kv: -sum(kv[1]))}
+    return {k: round(statistics.median(v), 4) for k, v in sorted(res.items(), key=lambda kv: -statistics.median(kv[1]))}
 
 
 def emit(metric, tokens, args, timing, workload, extra_cfg, roof, breakdown, cpu=None, **extra):
