@@ -589,10 +589,10 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__
   if (ok)
     for (int w = q + ST_Q * ST_W; w < nwin; w += ST_Q) E = fmaxf(E, win_e[(int64_t)w * ldn + row]);
   red[q][t] = E;
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int k = 0; k < ST_Q; ++k) E = fmaxf(E, red[k][t]);
-  __syncthreads();
+  lds_barrier();
   const float mo = ok ? m[row] : -INFINITY;
   const float nE = fmaxf(mo, E);   // finite: every chunk has a valid column
   float S = 0.f;
@@ -614,7 +614,7 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const float* __restrict__
     for (int w = q + ST_Q * ST_W; w < nwin; w += ST_Q) fold(w, win_e[(int64_t)w * ldn + row], win_s[(int64_t)w * ldn + row]);
   }
   red[q][t] = S;
-  __syncthreads();
+  lds_barrier();
   if (q == 0 && ok) {
     S = 0.f;
 #pragma unroll
@@ -648,7 +648,8 @@ __global__ __launch_bounds__(256) void ce_finish_kernel(const float* __restrict_
                                                         const float* __restrict__ part, const void* __restrict__ W,
                                                         int64_t ldw, const void* __restrict__ trows,
                                                         const int64_t* __restrict__ tgt, int64_t V, int64_t H,
-                                                        float gscale, void* g, int64_t ldg, float* loss_rows) {
+                                                        float gscale, void* g, int64_t ldg, float* loss_rows,
+                                                        bool vec) {
   const int64_t row = blockIdx.x;
   const float sr = s[row];
   const int64_t t = tgt[row];
@@ -658,6 +659,29 @@ __global__ __launch_bounds__(256) void ce_finish_kernel(const float* __restrict_
   const float inv = 1.f / sr, d = ok ? td[row] : 0.f;
   const void* wsrc = trows ? trows : W;
   const int64_t wrow = trows ? row * H : (ok ? t : 0) * ldw;
+  if (DT == 0 && GT == 0 && vec) {
+    // 8 columns per thread and pass: 2 x 16-B loads of acc (and of part), one of the bf16 target row, one 16-B store
+    for (int64_t c = 8 * (int64_t)threadIdx.x; c < H; c += 8 * 256) {
+      const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(acc + row * H + c);
+      const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(acc + row * H + c + 4);
+      f32x4_t p0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, p1 = p0;
+      if (part) {
+        p0 = *reinterpret_cast<const f32x4_t*>(part + row * H + c);
+        p1 = *reinterpret_cast<const f32x4_t*>(part + row * H + c + 4);
+      }
+      const u32x4_t wv = ok ? *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(wsrc) + wrow + c)
+                            : u32x4_t{0u, 0u, 0u, 0u};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float x0 = k < 2 ? a0[2 * k] + p0[2 * k] : a1[2 * k - 4] + p1[2 * k - 4];
+        const float x1 = k < 2 ? a0[2 * k + 1] + p0[2 * k + 1] : a1[2 * k - 3] + p1[2 * k - 3];
+        o[k] = pack2bf((x0 * inv - d * bf_lo(wv[k])) * gscale, (x1 * inv - d * bf_hi(wv[k])) * gscale);
+      }
+      *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(g) + row * ldg + c) = u32x4_t{o[0], o[1], o[2], o[3]};
+    }
+    return;
+  }
   for (int64_t c = threadIdx.x; c < H; c += 256) {
     const float wv = ok ? ld_t<DT>(wsrc, wrow + c) : 0.f;
     const float v = (acc[row * H + c] + (part ? part[row * H + c] : 0.f)) * inv - d * wv;
@@ -847,9 +871,13 @@ extern "C" int smel_ce_finish(const float* m, const float* s, const float* tz, c
                "ce_finish: null pointer");
   SMEL_REQUIRE(n < INT32_MAX, SMEL_EUNSUPPORTED, "ce_finish: too many rows");
   const dim3 gr((unsigned)n), b(256);
+  // 16-byte accesses when every row of acc, part, the target rows and g starts on 16 bytes
+  const auto al16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+  const bool vec = acc && H % 8 == 0 && al16(acc) && al16(part) && al16(g) && ldg % 8 == 0 &&
+                   (trows ? al16(trows) : (al16(W) && ldw % 8 == 0));
 #define SMEL_FIN(D, G) \
   ce_finish_kernel<D, G><<<gr, b, 0, stream>>>(m, s, tz, td, acc, part, W, ldw, trows, tgt, V, H, gscale, g, ldg, \
-                                               loss_rows)
+                                               loss_rows, vec)
 #define SMEL_FIN_G(D)            \
   if (g_dtype == 0) SMEL_FIN(D, 0); \
   else if (g_dtype == 1) SMEL_FIN(D, 1); \
