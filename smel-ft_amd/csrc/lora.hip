@@ -484,31 +484,40 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
   }
 }
 
-// The multi-chunk groups: sum the partial tiles in chunk order, store like lora_wgrad_kernel. Block = one column block
-// of all jobs; it takes every group of more than one chunk.
+// The multi-chunk groups: sum the partial tiles in chunk order, store like lora_wgrad_kernel. Block = (one column
+// block of all jobs, one LoRA group); blocks of groups with at most one chunk leave at once. The chunks' loads go out
+// four chunks at a time (one memory round trip per four chunks), the sum keeps chunk order.
 __global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
   __shared__ int G0[WG_MAXG], GN[WG_MAXG], GC[WG_MAXG + 1];
-  const int qbg = blockIdx.x;
+  const int qbg = blockIdx.x, i = blockIdx.y;
   int jb = 0;
 #pragma unroll
   for (int j = 1; j < WG_MAXJ; ++j)
     if (qbg >= a.qb0[j]) jb = j;
   const smel_wg_job& J = a.job[jb];
   const int qb = qbg - a.qb0[jb];
-  const int ng = wg_table(a, G0, GN, GC);
+  wg_table(a, G0, GN, GC);
   const int tid = threadIdx.x;
-  for (int i = 0; i < ng; ++i) {   // uniform
-    const int nch = GC[i + 1] - GC[i];
-    if (nch <= 1) continue;
-    const float* tile = a.ws + ((int64_t)qbg * a.tot + GC[i]) * (32 * WG_QB);
-    f32x16_t acc;
+  const int nch = GC[i + 1] - GC[i];
+  if (nch <= 1) return;   // uniform
+  const float* tile = a.ws + ((int64_t)qbg * a.tot + GC[i]) * (32 * WG_QB);
+  f32x16_t acc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = tile[r * 256 + tid];
-    for (int cc = 1; cc < nch; ++cc)
+  for (int r = 0; r < 16; ++r) acc[r] = tile[r * 256 + tid];
+  for (int c0 = 1; c0 < nch; c0 += 4) {
+    float v[4][16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] += tile[(int64_t)cc * (32 * WG_QB) + r * 256 + tid];
-    wg_store(J, a.n_sel, i, qb * WG_QB, tid >> 6, lane_id(), acc);
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        v[u][r] = c0 + u < nch ? tile[(int64_t)(c0 + u) * (32 * WG_QB) + r * 256 + tid] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (c0 + u < nch)   // uniform
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += v[u][r];
   }
+  wg_store(J, a.n_sel, i, qb * WG_QB, tid >> 6, lane_id(), acc);
 }
 
 }  // namespace
@@ -667,6 +676,6 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   lora_wgrad_kernel<<<(unsigned)std::min<int64_t>(bound, 2 * smel::cu_count()), 256, 0, stream>>>(a);
   int st = smel::launch_status();
   if (st) return st;
-  lora_wgrad_reduce<<<(unsigned)qbs, 256, 0, stream>>>(a);
+  lora_wgrad_reduce<<<dim3((unsigned)qbs, (unsigned)n_lora), 256, 0, stream>>>(a);
   return smel::launch_status();
 }
