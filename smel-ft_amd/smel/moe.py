@@ -345,6 +345,11 @@ _SIDE_STREAMS = {}
 # 0 and 1: the layouts of both LoRA sets are one ~16 us launch, less than a fork and join of a graph costs there.
 # SMEL_SIDE_STREAMS="0,1,2" (say) picks others; a fork that is off runs its launches on the main stream, in order.
 _SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1").split(",") if v.strip())
+# SMEL_BWD_ONE_SIDE=1 (default): the router backward and the LoRA factor gradients share one side stream, forked once
+# after the gate_up LoRA projection and joined once before the dX reduce (each fork or join point of a replayed graph
+# costs the main queue several µs); 0: each on its own stream, the router backward forked right after the down
+# backward
+_BWD_ONE_SIDE = os.environ.get("SMEL_BWD_ONE_SIDE", "1") == "1"
 
 
 def _side_stream(dev, i: int) -> torch.cuda.Stream:
@@ -754,6 +759,10 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["act"]), L.ptr(t["topv"]),
            L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st, tag="gemm_dn_bwd")
+    # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
+    ext_dxa = None
+    if any_lora and _BWD_ONE_SIDE:
+        ext_dxa = _lora_ext(tl, dh, 2 * I, M, 0, order, TK, K, lb_ex, lb_sh, "bt_gu", 2 * I, planes, M, dev, st)
     # (5, side stream 0) router backward (fused layer) or d topv (routed_experts): needs only dwp, so it overlaps
     # steps (3) and (4)
     dxr = None
@@ -773,12 +782,11 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
         dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
         with side_r:
             L.call("smel_dtopv", L.ptr(dwp), nblk, L.ptr(t["inv"]), TK, L.ptr(dtopv), L.stream())
-    # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
-    ext_dxa = None
-    if any_lora:
+    if any_lora and not _BWD_ONE_SIDE:
         ext_dxa = _lora_ext(tl, dh, 2 * I, M, 0, order, TK, K, lb_ex, lb_sh, "bt_gu", 2 * I, planes, M, dev, st)
-    # (6, side stream 1) LoRA factor gradients: one launch for the four products, written into parameter-shaped fp32
-    # tensors; every operand is ready here, so it overlaps the gate_up backward
+    # (6, side stream 1, or after the router backward on stream 0) LoRA factor gradients: one launch for the four
+    # products, written into parameter-shaped fp32 tensors; every operand is ready here, so it overlaps the gate_up
+    # backward
     grads = {}
     side_w = None
     if any_lora:
@@ -791,7 +799,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
         # rows of all LoRA groups: a token routes at most min(K, n_sel) slots to selected experts, + the shared rows
         max_rows = (min(K, n_sel) * T if lb_ex is not None else 0) + (T if lb_sh is not None else 0)
         ws = _wgrad_ws(jobs, nj, groups.numel(), max_rows, dev)
-        side_w = _Fork(dev, 1)
+        side_w = side_r if _BWD_ONE_SIDE else _Fork(dev, 1)
         with side_w:
             L.call("smel_lora_wgrad", jobs, nj, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK,
                    K, L.ptr(order), L.ptr(t["topv"]), L.ptr(t["sgate"]), max_rows, L.ptr(ws), ws.numel(), L.stream(),
@@ -812,7 +820,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     dxsh = shared_split[2] if shared_split is not None else None
     L.call("smel_dx_reduce", L.ptr(dxs), L.ptr(dxr), L.ptr(t["inv"]), int(t["sgate"] is not None), L.ptr(dxsh), T,
            K, H, L.ptr(dx), st)
-    if side_w is not None:
+    if side_w is not None and side_w is not side_r:
         side_w.join()
     return dx, dtopv, grads
 
