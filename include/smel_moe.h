@@ -279,7 +279,7 @@ int64_t smel_gmm_fwd_nblocks(int64_t R, int32_t epilogue);
  * out[t] = bf16( sum_k topv[t,k] * fp32(Y[t*K+k])  [+ sgate[t] * fp32(Ysh[t])] ), k in fixed order, topv fp32;
  * the shared expert's row Ysh[t] is Y[TK+t] (the fused shared expert) when Ysh is NULL, else row t of Ysh [T][H]
  * (a shared expert of another intermediate size, run as its own GEMMs). inv [T*K] (optional, smel_dispatch's): a slot
- * with inv < 0 (an expert id out of range, dropped by the dispatch) adds nothing. */
+ * with inv < 0 (an expert id out of range, dropped by the dispatch) adds nothing. K <= 16. */
 int smel_combine(const uint16_t* Y, const float* topv, const int32_t* inv, const float* sgate, const uint16_t* Ysh,
                  int64_t T, int64_t K, int64_t H, uint16_t* out, hipStream_t stream);
 
@@ -319,7 +319,7 @@ int smel_dtopv(const float* dwp, int64_t nblk, const int32_t* inv, int64_t TK, f
 
 /* ---- dX of the layer: dx[t] = bf16( sum_k DXS[t*K+k] + [shared row] + [DXR[t]] ), fixed order, fp32; the shared row
  * (with_shared) is DXS[TK+t], or DXSH[t] when dxsh is given; slots with inv < 0 (inv optional, as in smel_combine)
- * add nothing. */
+ * add nothing. K <= 16. */
 int smel_dx_reduce(const uint16_t* dxs, const uint16_t* dxr, const int32_t* inv, int32_t with_shared,
                    const uint16_t* dxsh, int64_t T, int64_t K, int64_t H, uint16_t* dx, hipStream_t stream);
 
