@@ -301,6 +301,31 @@ int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
                  uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream);
 /* number of column blocks (dwp row width) smel_gmm_bwd uses for a given C */
 int64_t smel_gmm_bwd_nblocks(int64_t C);
+/* The gate_up backward's LoRA rows without a separate smel_lora_ext launch (the autograd of lora_gate_up's B
+ * products, smel/lora.py:72-83: DXA = s [dg B_g, du B_u] per row of a selected / shared expert with a LoRA): */
+typedef struct smel_bwd_lora_rows {
+  const uint16_t* bt_sel;  /* bt_gu layout of the selected experts [planes][n_sel][32][2 I] (smel_lora_prep), or NULL */
+  const uint16_t* bt_sh;   /* bt_gu layout of the shared expert [planes][1][32][2 I], or NULL                         */
+  float scale_sel, scale_sh;
+  int32_t n_sel;           /* selected slots of bt_sel (its plane stride)                                             */
+  int32_t planes;          /* 1 or 2, as the weight set's SMEL_WSET_EXT2                                              */
+  float* part;             /* [rows][parts][planes][32] fp32, 16-B aligned; NULL: off                                 */
+  int32_t parts;           /* smel_gmm_bwd_nblocks(I): the down backward's column blocks                              */
+} smel_bwd_lora_rows;
+/* smel_gmm_bwd with lr: the down backward (epilogue 1) writes, for the rows of SEL / SHARED tiles whose bt_* is given,
+ * part[row][b][c][j] = scale * sum over column block b's columns n of (dg[row][n] bt[c][j][n] + du[row][n]
+ * bt[c][j][I+n]) from the bf16 dg / du it stores; the gate_up backward (epilogue 0, ext NULL) takes
+ * ext[row][32 c + j] = bf16(sum_b part[row][b][c][j]) (b ascending, fp32) as its K-extension rows. */
+int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
+                    int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
+                    const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
+                    const uint16_t* hsave, const uint16_t* actsave, const float* topv, const float* sgate,
+                    uint16_t* out, int64_t ldo, float* dwp, const smel_bwd_lora_rows* lr, hipStream_t stream);
+/* The same rows as bf16 [rows][32 * planes] for the LoRA gradients: ext[row][32 c + j] = bf16(sum_b part[row][b][c][j])
+ * for the rows of SEL tiles (sel != 0) and SHARED tiles (sh != 0) of the tile list; other rows are left untouched. */
+int smel_lora_rows_sum(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,
+                       int32_t sel, int32_t sh, const float* part, int32_t parts, int32_t planes, uint16_t* ext,
+                       hipStream_t stream);
 
 /* ---- (A15) router backward (autograd of route + renorm + the shared gate, smel/moe.py:162-167, 201):
  * dtopv[t,k] = sum_j dwp[inv[t*K+k]][j]; d renorm; d gather; d softmax (probs) -> dlogits [T][ldl] bf16 with

@@ -69,6 +69,8 @@ struct BwdArgs {
   int a_gather, TK, topk, act;
   int Kd, N;   // Kd = w.R (contraction), N = w.C
   int nblk;    // column blocks per tile
+  smel_bwd_lora_rows lr;   // gate_up LoRA rows: partials produced by the down backward, taken by the gate_up backward
+  bool lr_on;
 };
 
 SMEL_DEV f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
@@ -363,10 +365,52 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
   const int planes = (ws.flags & SMEL_WSET_EXT2) ? 2 : 1;   // uniform
   const uint16_t* eb = kind == SMEL_KIND_SEL ? (ws.ext_sel ? ws.ext_sel + (int64_t)idx * planes * N * 32 : nullptr)
                                              : (kind == SMEL_KIND_SHARED ? ws.ext_sh : nullptr);
-  if (a.ext && eb) {
+  // xpart: the rows come as the down backward's per-column-block fp32 partials, summed here in block order
+  const bool xpart = EPI == 0 && a.lr_on;
+  if ((a.ext || xpart) && eb) {
     const uint32_t xb = 64u * planes;   // ext row bytes
     const rsrc_t re = make_rsrc(eb, (uint64_t)planes * N * 64);
-    const rsrc_t rx = make_rsrc(a.ext + (int64_t)row0 * (xb / 2), (uint64_t)nrows * xb);
+    const rsrc_t rx = make_rsrc(a.ext ? a.ext + (int64_t)row0 * (xb / 2) : nullptr, a.ext ? (uint64_t)nrows * xb : 0);
+    // partials: summed once per tile into a bf16 tile X [128][32 planes] in ring stage 0 (free now), every load of a
+    // thread in flight at once, then read like the ext rows
+    uint16_t* const X = reinterpret_cast<uint16_t*>(smem);
+    if (xpart) {
+      const int P = a.lr.parts;
+      const rsrc_t rp = make_rsrc(a.lr.part + (int64_t)row0 * P * planes * 32, (uint64_t)nrows * P * planes * 128);
+      __syncthreads();   // every wave's ring loads have landed and its fragment reads returned
+      const int xr = tid >> 2, xj = 8 * (tid & 3);   // rows xr and xr + 64, values xj .. xj + 7 of a plane
+      for (int c = 0; c < planes; ++c) {
+        float v[2][8] = {};
+        for (int p0 = 0; p0 < P; p0 += 2) {
+          u32x4_t x[2][2][2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const int row = xr + 64 * h, p = p0 + q;
+              const uint32_t o =
+                  (row < nrows && p < P) ? (uint32_t)(((row * P + p) * planes + c) * 128 + 4 * xj) : OOB;
+              x[h][q][0] = ld16(rp, o);
+              x[h][q][1] = ld16(rp, o == OOB ? OOB : o + 16);
+            }
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)   // p ascending; a p past P reads zeros
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                v[h][t] += __uint_as_float(x[h][q][0][t]);
+                v[h][4 + t] += __uint_as_float(x[h][q][1][t]);
+              }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<u32x4_t*>(X + (xr + 64 * h) * 32 * planes + 32 * c + xj) =
+              u32x4_t{pack2bf(v[h][0], v[h][1]), pack2bf(v[h][2], v[h][3]), pack2bf(v[h][4], v[h][5]),
+                      pack2bf(v[h][6], v[h][7])};
+      }
+      __syncthreads();
+    }
     for (int c = 0; c < planes; ++c) {
       u32x4_t b[4];
 #pragma unroll
@@ -377,7 +421,12 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
 #pragma unroll
       for (int m = 0; m < NRF; ++m) {
         const int row = m * 16 + li;
-        const u32x4_t af = ld16(rx, row < nrows ? (uint32_t)row * xb + 64 * c + 16 * kq : OOB);
+        u32x4_t af;
+        if (xpart) {
+          af = *reinterpret_cast<const u32x4_t*>(X + row * 32 * planes + 32 * c + 8 * kq);
+        } else {
+          af = ld16(rx, row < nrows ? (uint32_t)row * xb + 64 * c + 16 * kq : OOB);
+        }
 #pragma unroll
         for (int f = 0; f < 4; ++f) acc[m][f] = mfma16(af, b[f], acc[m][f]);
       }
@@ -486,6 +535,83 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       }
     }
   }
+  // ---- the gate_up backward's LoRA rows of this tile (SEL / SHARED with a LoRA): this block's partial of
+  // s [dg, du] bt^T over its columns, part[row][nb][c][j]. The K of 512 (this block's 256 dg columns, then its 256 du
+  // columns, read back from the rows just stored) goes in 4 chunks of 128 columns through LDS: the dh rows and bt rows
+  // of every chunk are loaded coalesced (16-B pieces of whole row segments) into registers at once, then per chunk
+  // wave w multiplies rows 32 w .. 32 w + 31 by them (MFMA 32x32x16, one accumulator per plane).
+  if (!a.lr_on) return;
+  const uint16_t* bt = kind == SMEL_KIND_SEL ? a.lr.bt_sel : (kind == SMEL_KIND_SHARED ? a.lr.bt_sh : nullptr);
+  if (!bt) return;   // uniform
+  const int64_t I2 = 2 * (int64_t)I;
+  const int64_t pstride = (kind == SMEL_KIND_SEL ? (int64_t)a.lr.n_sel : 1) * 32 * I2;   // one plane
+  if (kind == SMEL_KIND_SEL) bt += (int64_t)idx * 32 * I2;
+  const float sc = kind == SMEL_KIND_SEL ? a.lr.scale_sel : a.lr.scale_sh;
+  const int P = a.lr.parts, gplanes = a.lr.planes;   // the gate_up side's planes
+  constexpr int DP = 128 + 8;                         // LDS row pitch (bf16): 272 B
+  uint16_t* const D = reinterpret_cast<uint16_t*>(smem);   // dh chunk [128][DP]
+  uint16_t* const Bs = D + MT * DP;                         // bt chunk [planes][32][DP]
+  static_assert(MT * DP * 2 + 2 * 32 * DP * 2 <= smem_bytes(false), "LoRA-row chunks fit in the ring");
+  const rsrc_t rd = make_rsrc(a.out + (int64_t)row0 * a.ldo, (uint64_t)nrows * a.ldo * 2);
+  const rsrc_t rb0 = make_rsrc(bt, (uint64_t)32 * I2 * 2);
+  const rsrc_t rb1 = make_rsrc(gplanes > 1 ? bt + pstride : bt, gplanes > 1 ? (uint64_t)32 * I2 * 2 : 0);
+  const int gch = tid & 15, grow = tid >> 4;   // this thread's 16-B pieces: rows grow + 16 i, columns 8 gch ..
+  // chunk q: columns (q < 2 ? 0 : I) + nb * 256 + 128 (q & 1) + [0, 128); I is a multiple of 32, so a piece is in or out
+  auto piece_ok = [&](int q) { return nb * NB + 128 * (q & 1) + 8 * gch < I; };
+  auto piece_col = [&](int q) { return (q >= 2 ? I : 0) + nb * NB + 128 * (q & 1) + 8 * gch; };
+  // the bt rows of all 4 chunks before the barrier (they do not depend on this block's stores), the dh rows of all
+  // 4 chunks right after it: one memory round trip for the whole projection
+  u32x4_t pd[4][8], pb[4][2][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t o = piece_ok(q) ? (uint32_t)((grow + 16 * i) * I2 + piece_col(q)) * 2 : OOB;
+      pb[q][0][i] = ld16(rb0, o);
+      pb[q][1][i] = ld16(rb1, o);
+    }
+  const int h5 = l >> 5, r32 = l & 31;
+  f32x16_t px0 = f32x16_t{}, px1 = f32x16_t{};
+  __syncthreads();   // the block's dg / du stores are visible to all of its waves; the staged tile's reads are done
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = grow + 16 * i;
+      pd[q][i] = ld16(rd, piece_ok(q) && row < nrows ? (uint32_t)(row * a.ldo + piece_col(q)) * 2 : OOB);
+    }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4_t*>(D + (grow + 16 * i) * DP + 8 * gch) = pd[q][i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<u32x4_t*>(Bs + (grow + 16 * i) * DP + 8 * gch) = pb[q][0][i];
+      *reinterpret_cast<u32x4_t*>(Bs + (32 + grow + 16 * i) * DP + 8 * gch) = pb[q][1][i];
+    }
+    lds_barrier();
+    if (w < NS) {
+      const uint16_t* Ar = D + (32 * w + r32) * DP + 8 * h5;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(Ar + 16 * s);
+        px0 = mfma32(af, *reinterpret_cast<const u32x4_t*>(Bs + r32 * DP + 16 * s + 8 * h5), px0);
+        if (gplanes > 1)   // uniform
+          px1 = mfma32(af, *reinterpret_cast<const u32x4_t*>(Bs + (32 + r32) * DP + 16 * s + 8 * h5), px1);
+      }
+    }
+    lds_barrier();   // this chunk's reads are done before the next one is stored
+  }
+  if (w >= NS) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int orow = 32 * w + acc_row(r, l);
+    if (orow < nrows) {
+      float* const o = a.lr.part + (((int64_t)(row0 + orow) * P + nb) * gplanes) * 32 + r32;
+      o[0] = sc * px0[r];
+      if (gplanes > 1) o[32] = sc * px1[r];
+    }
+  }
 }
 
 template <int EPI, bool Q4, bool SZ2, bool FAST>
@@ -537,11 +663,12 @@ __global__ __launch_bounds__(256) void gmm_bwd_kernel_sz2(BwdArgs a) {
 
 extern "C" int64_t smel_gmm_bwd_nblocks(int64_t C) { return (C + NB - 1) / NB; }
 
-extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
-                            int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
-                            const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
-                            int32_t act, const uint16_t* hsave, const uint16_t* actsave, const float* topv,
-                            const float* sgate, uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
+extern "C" int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const int32_t* tiles,
+                               const int32_t* n_tiles, int64_t max_tiles, const uint16_t* A, int64_t lda,
+                               int64_t a_rows, int32_t a_gather, const int32_t* order, int64_t TK, int64_t topk,
+                               const uint16_t* ext, int32_t epilogue, int32_t act, const uint16_t* hsave,
+                               const uint16_t* actsave, const float* topv, const float* sgate, uint16_t* out,
+                               int64_t ldo, float* dwp, const smel_bwd_lora_rows* lr, hipStream_t stream) {
   SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->R && topk > 0, SMEL_EINVAL,
                "gmm_bwd: bad sizes");
@@ -563,8 +690,25 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_bwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: A larger than 2 GiB");
   SMEL_REQUIRE(w->R * w->C * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_bwd: one weight matrix larger than 2 GiB");
+  if (lr && lr->part) {
+    SMEL_REQUIRE(lr->planes == 1 || lr->planes == 2, SMEL_EINVAL, "gmm_bwd: LoRA-row planes %d", lr->planes);
+    SMEL_REQUIRE(((uintptr_t)lr->part % 16) == 0, SMEL_EUNSUPPORTED, "gmm_bwd: LoRA-row partials must be 16-B aligned");
+    if (epilogue == 1) {
+      SMEL_REQUIRE(lr->parts == smel_gmm_bwd_nblocks(w->C), SMEL_EINVAL,
+                   "gmm_bwd: %d LoRA-row partials per row (the down backward's column blocks: %lld)", lr->parts,
+                   (long long)smel_gmm_bwd_nblocks(w->C));
+      SMEL_REQUIRE(ldo >= 2 * w->C && (!lr->bt_sel || lr->n_sel > 0), SMEL_EINVAL,
+                   "gmm_bwd: LoRA rows need the dh rows [rows][2 I] and the selected slots' count");
+    } else {
+      SMEL_REQUIRE(!ext && lr->parts >= 1, SMEL_EINVAL, "gmm_bwd: LoRA-row partials replace ext (pass NULL)");
+      SMEL_REQUIRE(lr->planes == ((w->flags & SMEL_WSET_EXT2) ? 2 : 1), SMEL_EINVAL,
+                   "gmm_bwd: LoRA-row planes %d against the weight set's extension", lr->planes);
+    }
+  }
   if (max_tiles == 0) return 0;
   BwdArgs a;
+  a.lr_on = lr && lr->part;
+  if (a.lr_on) a.lr = *lr;
   a.w = *w;
   a.gkind = gkind;
   a.tiles = reinterpret_cast<const int4*>(tiles);
@@ -602,4 +746,13 @@ extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int3
       gmm_bwd_kernel<0><<<grid, 256, 0, stream>>>(a);
   }
   return smel::launch_status();
+}
+
+extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
+                            int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
+                            const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
+                            int32_t act, const uint16_t* hsave, const uint16_t* actsave, const float* topv,
+                            const float* sgate, uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
+  return smel_gmm_bwd_lr(w, gkind, tiles, n_tiles, max_tiles, A, lda, a_rows, a_gather, order, TK, topk, ext,
+                         epilogue, act, hsave, actsave, topv, sgate, out, ldo, dwp, nullptr, stream);
 }

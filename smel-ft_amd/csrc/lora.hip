@@ -520,6 +520,41 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(WgArgs a) {
   wg_store(J, a.n_sel, i, qb * WG_QB, tid >> 6, lane_id(), acc);
 }
 
+// LoRA rows from per-column-block fp32 partials (smel_gmm_bwd_lr's): ext[row][32 c + j] = bf16(sum_b part[row][b][c][j])
+// with b ascending from 0.f, the order the gate_up backward sums them in, so both see the same bf16 rows. One block
+// per tile of the list; a thread takes 8 values (two 16-B loads per partial, one 16-B store).
+__global__ __launch_bounds__(256) void lora_rows_sum_kernel(const int4* __restrict__ tiles,
+                                                            const int32_t* __restrict__ n_tiles,
+                                                            const int32_t* __restrict__ gkind, int sel, int sh,
+                                                            const float* __restrict__ part, int parts, int planes,
+                                                            uint16_t* __restrict__ ext) {
+  const int tt = blockIdx.x;
+  if (tt >= n_tiles[0]) return;
+  const int4 t = tiles[tt];
+  const int gk = gkind ? gkind[t.x] : t.w;
+  const int kind = gk >> 16;
+  if (!((kind == SMEL_KIND_SEL && sel) || (kind == SMEL_KIND_SHARED && sh))) return;
+  const int nrows = min(t.z - t.y, 128);
+  const int W = 4 * planes;   // 8-value chunks per row
+  for (int i = threadIdx.x; i < nrows * W; i += blockDim.x) {
+    const int row = i / W, ch = i - row * W;
+    const int c = ch >> 2, j0 = 8 * (ch & 3);
+    const int64_t grow = t.y + row;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < parts; ++p) {
+      const float* src = part + ((grow * parts + p) * planes + c) * 32 + j0;
+      const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(src), x1 = *reinterpret_cast<const f32x4_t*>(src + 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] += x0[q];
+        v[4 + q] += x1[q];
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(ext + grow * 32 * planes + 32 * c + j0) =
+        u32x4_t{pack2bf(v[0], v[1]), pack2bf(v[2], v[3]), pack2bf(v[4], v[5]), pack2bf(v[6], v[7])};
+  }
+}
+
 }  // namespace
 
 extern "C" int smel_lora_prep_sets(const smel_lora_set* sets, int32_t n_sets, int32_t planes, int64_t Hd,
@@ -598,6 +633,20 @@ extern "C" int smel_lora_ext(const int32_t* tiles, const int32_t* n_tiles, int64
                                                         lda, a_rows, a_gather, order, (int)TK, (int)topk, wcat_sel,
                                                         wcat_sh, (int)Kd, scale_sel, scale_sh, ext, (int)ldx,
                                                         (int)max_tiles);
+  return smel::launch_status();
+}
+
+extern "C" int smel_lora_rows_sum(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,
+                                  int32_t sel, int32_t sh, const float* part, int32_t parts, int32_t planes,
+                                  uint16_t* ext, hipStream_t stream) {
+  SMEL_REQUIRE(parts >= 1 && (planes == 1 || planes == 2) && max_tiles >= 0, SMEL_EINVAL,
+               "lora_rows_sum: parts %d, planes %d", parts, planes);
+  if (max_tiles == 0 || (!sel && !sh)) return 0;
+  SMEL_REQUIRE(tiles && n_tiles && part && ext, SMEL_EINVAL, "lora_rows_sum: null pointer");
+  SMEL_REQUIRE(((uintptr_t)part % 16) == 0 && ((uintptr_t)ext % 16) == 0, SMEL_EUNSUPPORTED,
+               "lora_rows_sum: part and ext must be 16-B aligned");
+  lora_rows_sum_kernel<<<(unsigned)max_tiles, 256, 0, stream>>>(reinterpret_cast<const int4*>(tiles), n_tiles, gkind,
+                                                               sel, sh, part, parts, planes, ext);
   return smel::launch_status();
 }
 

@@ -19,7 +19,7 @@ PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -46,6 +46,13 @@ class FwdLoraRows(ctypes.Structure):
     """smel_fwd_lora_rows of include/smel_moe.h: the down LoRA's rows produced in the gate_up forward's epilogue."""
     _fields_ = [("a_sel", vp), ("a_sh", vp), ("scale_sel", ctypes.c_float), ("scale_sh", ctypes.c_float),
                 ("part", vp), ("parts", i32), ("ext_out", vp)]
+
+
+class BwdLoraRows(ctypes.Structure):
+    """smel_bwd_lora_rows of include/smel_moe.h: the gate_up LoRA's backward rows produced in the down backward's
+    epilogue."""
+    _fields_ = [("bt_sel", vp), ("bt_sh", vp), ("scale_sel", ctypes.c_float), ("scale_sh", ctypes.c_float),
+                ("n_sel", i32), ("planes", i32), ("part", vp), ("parts", i32)]
 
 
 class LoraSet(ctypes.Structure):
@@ -94,7 +101,10 @@ SIGNATURES = {
     "smel_combine": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp]),
     "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
                            vp, vp, vp, vp, vp, i64, vp, vp]),
+    "smel_gmm_bwd_lr": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
+                              vp, vp, vp, vp, vp, i64, vp, ctypes.POINTER(BwdLoraRows), vp]),
     "smel_gmm_bwd_nblocks": (i64, [i64]),
+    "smel_lora_rows_sum": (i32, [vp, vp, i64, vp, i32, i32, vp, i32, i32, vp, vp]),
     "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp, vp, vp]),
     "smel_route_gemma4": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_gemma4_prenorm_bwd": (i32, [vp, vp, vp, vp, i64, i64, vp, vp]),

@@ -350,6 +350,10 @@ _SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1").
 # costs the main queue several µs); 0: each on its own stream, the router backward forked right after the down
 # backward
 _BWD_ONE_SIDE = os.environ.get("SMEL_BWD_ONE_SIDE", "1") == "1"
+# SMEL_BWD_LORA_ROWS=1 (default): the gate_up backward's LoRA rows come from the down backward's epilogue as
+# per-column-block partials (smel_gmm_bwd_lr), summed by the gate_up backward itself and, for the LoRA gradients, by
+# smel_lora_rows_sum on the side stream: no smel_lora_ext launch between the two GEMMs; 0: that launch
+_BWD_LORA_ROWS = os.environ.get("SMEL_BWD_LORA_ROWS", "1") == "1"
 
 
 def _side_stream(dev, i: int) -> torch.cuda.Stream:
@@ -443,6 +447,26 @@ def _lora_ext(tl, A, lda, a_rows, gather, order, TK, K, lb_ex, lb_sh, name: str,
         L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(A), lda, a_rows, gather,
                L.ptr(order), TK, K, L.ptr(w(lb_ex)), L.ptr(w(lb_sh)), Kd, s_ex, s_sh, ext.data_ptr() + 2 * EXT * c,
                EXT * planes, st)
+    return ext
+
+
+def _bwd_lora_rows(lb_ex, lb_sh, nblk: int, M: int, planes: int, dev):
+    """smel_bwd_lora_rows for the down backward (producer) and the gate_up backward (consumer), with its fp32 partial
+    buffer [M][nblk][planes][32]."""
+    part = torch.empty(M, nblk, planes, EXT, dtype=torch.float32, device=dev)
+    lr = L.BwdLoraRows(L.ptr(lb_ex.bt_gu) if lb_ex is not None else None,
+                       L.ptr(lb_sh.bt_gu) if lb_sh is not None else None,
+                       lb_ex.scale if lb_ex is not None else 0.0, lb_sh.scale if lb_sh is not None else 0.0,
+                       lb_ex.n if lb_ex is not None else 0, planes, L.ptr(part), nblk)
+    return lr, part
+
+
+def _lora_rows_sum(tl, lr, lb_ex, lb_sh, M: int, planes: int, dev, st):
+    """bf16 rows [M][32 planes] of the LoRA tiles from the partials of ``lr`` (for the LoRA gradients)."""
+    tiles, ntiles, maxt, gk = tl
+    ext = torch.empty(M, EXT * planes, dtype=torch.bfloat16, device=dev)
+    L.call("smel_lora_rows_sum", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), int(lb_ex is not None),
+           int(lb_sh is not None), lr.part, lr.parts, planes, L.ptr(ext), st, tag="smel_lora_rows")
     return ext
 
 
@@ -756,12 +780,15 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     dh = bf(M, 2 * I)
     dwp = torch.empty(M, nblk, dtype=torch.float32, device=dev)
     w_dn = _wset(ex, "dn", t["sel_dn"], sh_dn, g(lb_ex, "at_dn"), g(lb_sh, "at_dn"), t=True)
-    L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
+    # with the LoRA rows from this GEMM's epilogue: DXA = s [dg B_g, du B_u] as per-column-block partials
+    lrows = _bwd_lora_rows(lb_ex, lb_sh, nblk, M, planes, dev) if any_lora and _BWD_LORA_ROWS else None
+    lr = ctypes.byref(lrows[0]) if lrows is not None else None
+    L.call("smel_gmm_bwd_lr", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["act"]), L.ptr(t["topv"]),
-           L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), st, tag="gemm_dn_bwd")
-    # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u]
+           L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), lr, st, tag="gemm_dn_bwd")
+    # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u] (without the partials)
     ext_dxa = None
-    if any_lora and _BWD_ONE_SIDE:
+    if any_lora and _BWD_ONE_SIDE and lrows is None:
         ext_dxa = _lora_ext(tl, dh, 2 * I, M, 0, order, TK, K, lb_ex, lb_sh, "bt_gu", 2 * I, planes, M, dev, st)
     # (5, side stream 0) router backward (fused layer) or d topv (routed_experts): needs only dwp, so it overlaps
     # steps (3) and (4)
@@ -782,7 +809,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
         dtopv = torch.empty(T, K, dtype=torch.float32, device=dev)
         with side_r:
             L.call("smel_dtopv", L.ptr(dwp), nblk, L.ptr(t["inv"]), TK, L.ptr(dtopv), L.stream())
-    if any_lora and not _BWD_ONE_SIDE:
+    if any_lora and not _BWD_ONE_SIDE and lrows is None:
         ext_dxa = _lora_ext(tl, dh, 2 * I, M, 0, order, TK, K, lb_ex, lb_sh, "bt_gu", 2 * I, planes, M, dev, st)
     # (6, side stream 1, or after the router backward on stream 0) LoRA factor gradients: one launch for the four
     # products, written into parameter-shaped fp32 tensors; every operand is ready here, so it overlaps the gate_up
@@ -794,6 +821,8 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
         groups = _lora_groups(ex, lb_sh is not None, n_sel, dev)
         sets = ((c.lora_ex if lb_ex is not None else None), (c.lora_sh if lb_sh is not None else None))
         gx, gs = (_alloc_lora_grads(m, dev) for m in sets)
+        if lrows is not None:
+            ext_dxa = torch.empty(M, EXT * planes, dtype=torch.bfloat16, device=dev)   # filled on the side stream
         jobs, nj = _wgrad_jobs(H, I, (gx, gs), sets, (ext_dxa, t["x"], T, 1, 0), (t["ext_gu"], dh, M, 0, 0),
                                (ext_db, t["act"], M, 0, 1), (t["ext_dn"], dout, T, 1, 1), planes)
         # rows of all LoRA groups: a token routes at most min(K, n_sel) slots to selected experts, + the shared rows
@@ -801,6 +830,10 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
         ws = _wgrad_ws(jobs, nj, groups.numel(), max_rows, dev)
         side_w = side_r if _BWD_ONE_SIDE else _Fork(dev, 1)
         with side_w:
+            if lrows is not None:
+                L.call("smel_lora_rows_sum", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), int(lb_ex is not None),
+                       int(lb_sh is not None), L.ptr(lrows[1]), nblk, planes, L.ptr(ext_dxa), L.stream(),
+                       tag="smel_lora_rows")
             L.call("smel_lora_wgrad", jobs, nj, L.ptr(groups), groups.numel(), n_sel, L.ptr(t["offsets"]), E, T, TK,
                    K, L.ptr(order), L.ptr(t["topv"]), L.ptr(t["sgate"]), max_rows, L.ptr(ws), ws.numel(), L.stream(),
                    tag="lora_wgrad")
@@ -812,9 +845,9 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     dxs = bf(M, H)
     w_gu = _wset(ex, "gu", t["sel_gu"], sh_gu, g(lb_ex, "at_gu"), g(lb_sh, "at_gu"), t=True, planes=planes)
     w_gu.flags |= L.WSET_XCD_CHUNK
-    L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(t["tiles_g"]), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I,
-           M, 0, L.ptr(order), TK, K, L.ptr(ext_dxa), 0, _ACT[ex.act], None, None, None, None, L.ptr(dxs), H, None, st,
-           tag="gemm_gu_bwd")
+    L.call("smel_gmm_bwd_lr", ctypes.byref(w_gu), L.ptr(gk), L.ptr(t["tiles_g"]), L.ptr(ntiles), maxt, L.ptr(dh),
+           2 * I, M, 0, L.ptr(order), TK, K, None if lrows is not None else L.ptr(ext_dxa), 0, _ACT[ex.act], None, None,
+           None, None, L.ptr(dxs), H, None, lr, st, tag="gemm_gu_bwd")
     side_r.join()
     dx = bf(T, H)
     dxsh = shared_split[2] if shared_split is not None else None
@@ -1068,18 +1101,22 @@ def _dense_mlp_bwd(sv: _DenseSaved, dy, w_gu_t: PackedW, w_dn_t: PackedW, lora, 
     dh = bf(T, 2 * Is)
     dwp = torch.empty(T, nblk, dtype=torch.float32, device=dev)
     wd = _dense_wset(w_dn_t, g("at_dn"))
-    L.call("smel_gmm_bwd", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
+    lrows = _bwd_lora_rows(None, lb, nblk, T, planes, dev) if lb is not None and _BWD_LORA_ROWS else None
+    lr = ctypes.byref(lrows[0]) if lrows is not None else None
+    L.call("smel_gmm_bwd_lr", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
            None, 0, 1, L.ptr(ext_db), 1, _ACT[act_name], L.ptr(sv.hsave), L.ptr(sv.actb), None, L.ptr(row_w),
-           L.ptr(dh), 2 * Is, L.ptr(dwp), st, tag=tag + "_dn_bwd")
-    if lb is not None:
+           L.ptr(dh), 2 * Is, L.ptr(dwp), lr, st, tag=tag + "_dn_bwd")
+    if lb is not None and lrows is None:
         ext_dxa = _lora_ext(tl, dh, 2 * Is, T, 0, None, 0, 1, None, lb, "bt_gu", 2 * Is, planes, T, dev, st)
     dx = bf(T, H)
     wg = _dense_wset(w_gu_t, g("at_gu"), planes)
-    L.call("smel_gmm_bwd", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
-           0, None, 0, 1, L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H, None, st,
-           tag=tag + "_gu_bwd")
+    L.call("smel_gmm_bwd_lr", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
+           0, None, 0, 1, None if lrows is not None else L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H,
+           None, lr, st, tag=tag + "_gu_bwd")
     grads = None
     if lb is not None:
+        if lrows is not None:   # the LoRA gradients take the same rows the gate_up backward summed
+            ext_dxa = _lora_rows_sum(tl, lrows[0], None, lb, T, planes, dev, st)
         zero = torch.zeros(2, dtype=torch.int32, device=dev)     # offsets of zero experts
         groups = torch.zeros(1, dtype=torch.int32, device=dev)   # group 0 >= E = 0: rows [0, T)
         gs = _alloc_lora_grads(lora, dev)

@@ -564,6 +564,24 @@ def test_layer_parity(name):
     assert set(grads) == set(g["grads"])
 
 
+@pytest.mark.parametrize("name", ["r16", "r32", "shared_wide", "r24_mixed"])
+def test_bwd_lora_rows_against_projection(name, monkeypatch):
+    """The gate_up backward's LoRA rows from the down backward's per-column-block partials (smel_gmm_bwd_lr +
+    smel_lora_rows_sum, the default) against the separate smel_lora_ext projection of dh: the same rows up to their
+    bf16 rounding, so dX and every LoRA gradient agree far inside the bf16 bar (and both pass it against the oracle in
+    test_layer_parity)."""
+    import smel.moe as M
+    _say(f"bwd LoRA rows vs projection {name}")
+    monkeypatch.setattr(M, "_BWD_LORA_ROWS", True)
+    a = run_layer(name, seed=3)
+    monkeypatch.setattr(M, "_BWD_LORA_ROWS", False)
+    b = run_layer(name, seed=3)
+    assert torch.equal(a["y"].view(torch.int16), b["y"].view(torch.int16))
+    assert_close_bf16(a["dx"], b["dx"], "dx", rel=5e-3, cos=0.99999)
+    for k in b["grads"]:
+        assert_close_bf16(a["grads"][k], b["grads"][k], k, rel=1e-2, cos=0.99999)
+
+
 def test_layer_determinism():
     _say("determinism mid x3")
     runs = [run_layer("mid", seed=5) for _ in range(3)]
