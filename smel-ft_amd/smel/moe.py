@@ -346,9 +346,9 @@ _SIDE_STREAMS = {}
 # SMEL_SIDE_STREAMS="0,1,2" (say) picks others; a fork that is off runs its launches on the main stream, in order.
 _SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1").split(",") if v.strip())
 # SMEL_BWD_ONE_SIDE=1 (default): the router backward and the LoRA factor gradients share one side stream, forked once
-# after the gate_up LoRA projection and joined once before the dX reduce (each fork or join point of a replayed graph
-# costs the main queue several µs); 0: each on its own stream, the router backward forked right after the down
-# backward
+# after the down backward (after the gate_up LoRA projection when that is a launch of its own) and joined once before
+# the dX reduce (each fork or join point of a replayed graph costs the main queue several µs); 0: each on its own
+# stream, the router backward forked right after the down backward
 _BWD_ONE_SIDE = os.environ.get("SMEL_BWD_ONE_SIDE", "1") == "1"
 # SMEL_BWD_LORA_ROWS=1 (default): the gate_up backward's LoRA rows come from the down backward's epilogue as
 # per-column-block partials (smel_gmm_bwd_lr), summed by the gate_up backward itself and, for the LoRA gradients, by
