@@ -48,6 +48,10 @@ int main() {
   F(smel_wset, R) F(smel_wset, group) F(smel_wset, flags) F(smel_wg_dest, s_idx) F(smel_wg_dest, p0) F(smel_wg_dest, nq)
   F(smel_wg_job, ldr) F(smel_wg_job, r_gather) F(smel_wg_job, Q) F(smel_wg_job, ldl) F(smel_wg_job, dest)
   F(smel_lora_set, n) F(smel_lora_set, r) F(smel_lora_set, fwd_gu) F(smel_lora_set, at_dn)
+  printf("smel_fwd_lora_rows %zu\nsmel_bwd_lora_rows %zu\n", sizeof(smel_fwd_lora_rows), sizeof(smel_bwd_lora_rows));
+  F(smel_fwd_lora_rows, scale_sh) F(smel_fwd_lora_rows, part) F(smel_fwd_lora_rows, parts) F(smel_fwd_lora_rows, ext_out)
+  F(smel_bwd_lora_rows, scale_sh) F(smel_bwd_lora_rows, n_sel) F(smel_bwd_lora_rows, planes) F(smel_bwd_lora_rows, part)
+  F(smel_bwd_lora_rows, parts)
   return 0;
 }
 """
@@ -69,7 +73,8 @@ def test_struct_layouts_match_header(tmp_path):
     got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
                                                        text=True).stdout.splitlines())
     mirror = {"smel_wset": _lib.WSet, "smel_wg_dest": _lib.WgDest, "smel_wg_job": _lib.WgJob,
-              "smel_lora_set": _lib.LoraSet}
+              "smel_lora_set": _lib.LoraSet, "smel_fwd_lora_rows": _lib.FwdLoraRows,
+              "smel_bwd_lora_rows": _lib.BwdLoraRows}
     for key, val in got.items():
         if "." in key:
             t, f = key.split(".")
@@ -134,6 +139,23 @@ def test_host_side_rejections():
     assert L.smel_pack_int4_t(1, 1, 1, 1, 64, 128, 64, 2, 16, 16, None) == -1   # fast is 0 or 1
     assert L.smel_int4_fast_ok(None, None, 4, None, None) == -1
     assert L.smel_pack_bf16_t(1, 1, 64, 48, 64, 1, None) == -2           # C not a multiple of 32
+    # LoRA rows from GEMM epilogues: partial count other than the producing GEMM's column blocks, ext given beside the
+    # partials, a third plane
+    w = _lib.WSet()
+    w.R, w.C = 2048, 512
+    lr = _lib.BwdLoraRows(None, 16, 1.0, 1.0, 0, 1, 16, 3)
+    args = (ctypes.byref(w), None, 16, 16, 1, 16, 2048, 4, 0, None, 0, 1, None)
+    assert L.smel_gmm_bwd_lr(*args, 1, 0, 16, 16, 16, 16, 16, 1024, 16, ctypes.byref(lr), None) == -1
+    assert b"partials" in L.smel_last_error()
+    lr.parts = L.smel_gmm_bwd_nblocks(512)
+    w.R, w.C = 512, 2048
+    assert L.smel_gmm_bwd_lr(ctypes.byref(w), None, 16, 16, 1, 16, 1024, 4, 0, None, 0, 1, 16, 0, 0, None, None, None,
+                             None, 16, 2048, None, ctypes.byref(lr), None) == -1   # ext and partials together
+    assert L.smel_lora_rows_sum(16, 16, 4, None, 1, 1, 16, 2, 3, 16, None) == -1
+    fl = _lib.FwdLoraRows(None, 16, 1.0, 1.0, 16, 3, None)
+    w.R, w.C = 1024, 2048
+    assert L.smel_gmm_fwd_lr(ctypes.byref(w), None, 16, 16, 1, 16, 2048, 4, 0, None, 0, 1, None, 1, 0, 16, 512, None,
+                             ctypes.byref(fl), None) == -1   # 3 partials for the gate_up forward's 4 column blocks
 
 
 def test_product_path_does_not_reach_the_oracle():
