@@ -74,25 +74,38 @@ class MLPLoRA(_LoRASet):
         return self._deltas(())
 
 
+def _add_low_rank(y, xa, B, scale):
+    """y + scale (xa B^T), B cast to the rows' dtype. For rows given as a matrix, one addmm: the low-rank product's
+    sum, its scaling and the add round once (the reference's epilogue form); other shapes scale and add the rounded
+    product, as the reference does for them."""
+    bt = B.to(xa.dtype).t()
+    if xa.dim() == 2:
+        return torch.addmm(y, xa, bt, alpha=scale)
+    return y + scale * (xa @ bt)
+
+
 def lora_linear(x, w, A, B, scale):
     """x w^T + scale (x A^T) B^T with the LoRA factors in x's dtype (smel/lora.py:61-69)."""
-    y = F.linear(x, w)
+    y = x @ w.t()
     if A is None:
         return y
-    return torch.add(y, F.linear(F.linear(x, A.to(x.dtype)), B.to(x.dtype)), alpha=scale)
+    return _add_low_rank(y, x @ A.to(x.dtype).t(), B, scale)
 
 
 def lora_gate_up(x, w_gate_up, A_gate, B_gate, A_up, B_up, scale):
-    """(gate, up) of a gated MLP from its stacked [2I, H] weight (smel/lora.py:72-83). Both low-rank products run
-    as one: x [A_gate; A_up]^T gives the 2r-wide projection, and the block-diagonal [[B_gate, 0], [0, B_up]] maps it
-    to the stacked 2I outputs, added to the base GEMM's."""
-    h = F.linear(x, w_gate_up)
-    if A_gate is not None:
-        dt = x.dtype
-        low = F.linear(x, torch.cat((A_gate, A_up)).to(dt))
-        h = torch.add(h, F.linear(low, torch.block_diag(B_gate, B_up).to(dt)), alpha=scale)
+    """(gate, up) of a gated MLP from its stacked [2I, H] weight (smel/lora.py:72-83): one base GEMM over the stacked
+    weight and one rank-2r projection x [A_gate; A_up]^T, whose two halves go through B_gate and B_up into the gate
+    and up halves. Rows of any leading shape (flattened to a matrix for the products)."""
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
     I = w_gate_up.shape[0] // 2
-    return h[..., :I], h[..., I:]
+    base = x2 @ w_gate_up.t()
+    g, u = base[:, :I], base[:, I:]
+    if A_gate is not None:
+        r = A_gate.shape[0]
+        xa = x2 @ torch.cat((A_gate, A_up)).to(x.dtype).t()
+        g, u = _add_low_rank(g, xa[:, :r], B_gate, scale), _add_low_rank(u, xa[:, r:], B_up, scale)
+    return g.reshape(*lead, I), u.reshape(*lead, I)
 
 
 class LayerLoRA(nn.Module):

@@ -14,9 +14,11 @@ Structure here:
   * the gradient GEMM reads the head transposed ([H][V]): a dense head whose dtype is the rows' is transposed once
     and kept with the head (it is frozen); other heads (int8, or another dtype) are converted per vocabulary chunk,
     as the reference's ``rows()`` does, and that chunk is transposed;
-  * vocabulary chunks are ``vocab_chunk`` rounded up to 256 columns (the logits tile), and a pass takes
-    max(token_chunk, 4096) rows: the rows are independent, so the results are those of the reference's chunking;
-    the softmax terms of a pass take rows x chunk values of the rows' dtype (256 MB at 4096 x 32768 bf16).
+  * vocabulary chunks are ``vocab_chunk`` rounded up to 256 columns (the logits tile), and a pass takes at most
+    ``token_chunk`` rows, so token_chunk x vocab_chunk bounds its buffers as in the reference (the softmax terms of a
+    pass take rows x chunk values of the rows' dtype); a caller that leaves token_chunk at its default gets passes of
+    up to 4096 rows (256 MB of bf16 terms at vocab_chunk 32768), where the GEMMs' row tiles fill the GPU. The rows are
+    independent, so the results are those of the reference's chunking either way.
 The gradient is computed in the forward (lm_head is frozen) and handed back by the backward, as in the reference.
 """
 from __future__ import annotations
@@ -29,7 +31,26 @@ from .quant import dequant_int8_rows, quantize_int8_rows
 _DT = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}
 TILE_V = 256           # vocabulary columns of a logits tile; chunks are whole tiles
 WIN = 128              # columns of one statistics window
-ROWS_PER_PASS = 4096   # token rows of one pass at least (the GEMMs' row tiles fill the GPU from there on)
+ROWS_PER_PASS = 4096   # token rows of a pass when token_chunk is left at its default (the GEMMs fill the GPU there)
+
+
+class _DefaultTokenChunk(int):
+    """The default token_chunk of chunked_ce (1024, the reference's): a caller who left it has not bounded the rows
+    of a pass, which may then take ROWS_PER_PASS rows."""
+
+
+TOKEN_CHUNK_DEFAULT = _DefaultTokenChunk(1024)
+
+
+def _rows_per_pass(N: int, token_chunk) -> int:
+    """Token rows of one pass: at most ``token_chunk`` (it bounds a pass's buffers, the softmax terms
+    [rows][vocab_chunk] and about 12 H bytes per row), or up to ROWS_PER_PASS when the caller left the default."""
+    tc = int(token_chunk)
+    if tc <= 0:
+        raise ValueError(f"chunked_ce: token_chunk must be positive, got {tc}")
+    if isinstance(token_chunk, _DefaultTokenChunk):
+        tc = max(tc, ROWS_PER_PASS)
+    return min(N, tc)
 
 
 def _round_up(x: int, m: int) -> int:
@@ -283,10 +304,9 @@ class _ChunkedCE(torch.autograd.Function):
     written into one output during the forward and returned, times the incoming gradient, by the backward."""
 
     @staticmethod
-    def forward(ctx, h, head, tgt, denom, token_chunk, need_grad):
+    def forward(ctx, h, head, tgt, denom, rows, need_grad):
         h, tgt = _prep(h, tgt)
         N, H = h.shape
-        rows = min(N, max(int(token_chunk), ROWS_PER_PASS))
         _, vcp = head._kernel_chunks()
         grad = torch.empty_like(h) if need_grad else None
         total = torch.empty((), dtype=torch.float32, device=h.device)
@@ -310,11 +330,12 @@ class _ChunkedCE(torch.autograd.Function):
         return g, None, None, None, None, None
 
 
-def chunked_ce(h, head: LMHead, tgt, denom: float, token_chunk: int = 1024, need_grad: bool = True):
+def chunked_ce(h, head: LMHead, tgt, denom: float, token_chunk: int = TOKEN_CHUNK_DEFAULT, need_grad: bool = True):
     """sum_t CE(h_t W^T, tgt_t) / denom (smel/loss.py:149-156). h: [N, H] (final-normed, supervised rows only),
-    tgt: [N] long."""
+    tgt: [N] long. A pass over the vocabulary takes at most ``token_chunk`` rows when the caller sets it."""
     if h.shape[0] == 0:
         return h.sum() * 0.0
+    rows = _rows_per_pass(h.shape[0], token_chunk)
     grad = need_grad and h.requires_grad
     with torch.set_grad_enabled(grad and torch.is_grad_enabled()):
-        return _ChunkedCE.apply(h, head, tgt, float(denom), int(token_chunk), grad)
+        return _ChunkedCE.apply(h, head, tgt, float(denom), rows, grad)

@@ -354,6 +354,10 @@ _BWD_ONE_SIDE = os.environ.get("SMEL_BWD_ONE_SIDE", "1") == "1"
 # per-column-block partials (smel_gmm_bwd_lr), summed by the gate_up backward itself and, for the LoRA gradients, by
 # smel_lora_rows_sum on the side stream: no smel_lora_ext launch between the two GEMMs; 0: that launch
 _BWD_LORA_ROWS = os.environ.get("SMEL_BWD_LORA_ROWS", "1") == "1"
+# SMEL_FWD_LORA_ROWS=1 (default): the down LoRA's rows come from the gate_up forward's epilogue as per-column-block
+# partials (smel_gmm_fwd_lr), summed and stored by the down forward; 0: a smel_lora_ext launch over the gate_up
+# output between the two GEMMs
+_FWD_LORA_ROWS = os.environ.get("SMEL_FWD_LORA_ROWS", "1") == "1"
 
 
 def _side_stream(dev, i: int) -> torch.cuda.Stream:
@@ -721,7 +725,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     # the down LoRA's rows come from the gate_up epilogue (per-column-block partials of h A_dn^T), summed and stored
     # by the down GEMM: no separate projection launch
     lr = None
-    if any_lora:
+    if any_lora and _FWD_LORA_ROWS:
         parts = int(L.load().smel_gmm_fwd_nblocks(2 * I, 1))
         xpart = torch.empty(M, parts, EXT, dtype=torch.float32, device=dev)
         ext_dn = bf(M, EXT)
@@ -730,11 +734,13 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     L.call("smel_gmm_fwd_lr", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_g), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave),
            ctypes.byref(lr) if lr is not None else None, st, tag="gemm_gu_fwd")
+    if any_lora and lr is None:   # the down LoRA's rows as a projection launch of the gate_up output
+        ext_dn = _lora_ext(tl, actb, I, M, 0, order, TK, K, lb_ex, lb_sh, "a_dn", I, 1, M, dev, st)
     Y = bf(M, H)
     w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
     L.call("smel_gmm_fwd_lr", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
-           L.ptr(order), TK, K, None, 0, _ACT[ex.act], L.ptr(Y), H, None, ctypes.byref(lr) if lr is not None else None,
-           st, tag="gemm_dn_fwd")
+           L.ptr(order), TK, K, L.ptr(ext_dn) if lr is None else None, 0, _ACT[ex.act], L.ptr(Y), H, None,
+           ctypes.byref(lr) if lr is not None else None, st, tag="gemm_dn_fwd")
     out = bf(T, H)
     ysh = None
     if shared_rows is not None:

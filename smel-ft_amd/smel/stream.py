@@ -16,11 +16,14 @@ next ones); device memory is a fixed set of slots (no allocator churn per layer)
 from __future__ import annotations
 
 import ctypes
+import itertools
+import json
 import os
 import time
 from collections import OrderedDict
 
 import torch
+from safetensors.torch import load_file as load_safetensors
 
 from . import _lib as L
 from .moe import BF16Experts, Int4Experts, LayerExperts
@@ -51,27 +54,58 @@ class LayerWeights:
         self.idx, self.ltype, self.W, self.experts = idx, ltype, W, experts
 
 
+_EXPERT_PREFIXES = ("mlp.experts.", "experts.")   # routed-expert tensors; everything else is the dense part
+_SEL_PREFIX = "experts.sel."
+
+
+def _id_list(ids) -> list:
+    """Expert ids (list, tuple, tensor or None) as a list of Python ints."""
+    if ids is None:
+        return []
+    if isinstance(ids, torch.Tensor):
+        ids = ids.reshape(-1).tolist()
+    return [int(i) for i in ids]
+
+
+def _fused_bank(bank: dict, sel_ids):
+    """bf16 fused bank [E, 2I, H] / [E, H, I]: the frozen experts, and trainable copies of the selected rows."""
+    gu, dn = bank["mlp.experts.gate_up_proj"], bank["mlp.experts.down_proj"]
+    ids = _id_list(sel_ids)
+    if not ids:
+        return BF16Experts(gu, dn), None, None, None
+    pick = torch.tensor(ids, dtype=torch.long, device=gu.device)
+    return BF16Experts(gu, dn), sel_ids, gu.index_select(0, pick), dn.index_select(0, pick)
+
+
+def _packed_bank(bank: dict, sel_ids, frozen_dtype):
+    """Packed int4 bank ('experts.{gate_up,down}.{q,scale,zero}') with the packed block's own bf16 selection
+    ('experts.sel.*'); ``sel_ids`` overrides the block's id list."""
+    halves = {w: {} for w in ("gate_up", "down")}
+    for k, v in bank.items():
+        which, _, field = k[len("experts."):].partition(".")
+        if which in halves:
+            halves[which][field] = v
+    sel_gu, sel_dn = bank.get(_SEL_PREFIX + "gate_up"), bank.get(_SEL_PREFIX + "down")
+    if sel_gu is None:
+        return Int4Experts(halves["gate_up"], halves["down"], dtype=frozen_dtype), None, None, None
+    if sel_ids is None:
+        sel_ids = _id_list(bank.get(_SEL_PREFIX + "ids")) or None
+    return Int4Experts(halves["gate_up"], halves["down"], dtype=frozen_dtype), sel_ids, sel_gu, sel_dn
+
+
 def build_layer(idx, ltype, t: dict, sel_ids=None, group=32, frozen_dtype=torch.bfloat16, act="silu"):
-    """t: device tensors of one layer, names relative to the layer: bf16 fused experts ('mlp.experts.gate_up_proj' /
-    'down_proj') or the packed int4 bank ('experts.gate_up.q', ...) + 'experts.sel.*' (smel/stream.py:16-36)."""
-    dense = {k: v for k, v in t.items() if not k.startswith(("mlp.experts.", "experts."))}
-    if "mlp.experts.gate_up_proj" in t:
-        gu, dn = t["mlp.experts.gate_up_proj"], t["mlp.experts.down_proj"]
-        frozen = BF16Experts(gu, dn)
-        sgu = sdn = None
-        if sel_ids is not None and len(sel_ids):
-            ids = torch.as_tensor(sel_ids, device=gu.device)
-            sgu, sdn = gu[ids].clone(), dn[ids].clone()
+    """LayerWeights of one layer from its device tensors (names relative to the layer), smel/stream.py:16-36: the
+    routed experts come either as the bf16 fused bank ('mlp.experts.gate_up_proj' / 'down_proj', the selected
+    experts copied out of it) or as the packed int4 bank with its selection ('experts.*'); the rest is the dense
+    part. Without selected bf16 experts the layer has no selection."""
+    dense, bank = {}, {}
+    for k, v in t.items():
+        (bank if k.startswith(_EXPERT_PREFIXES) else dense)[k] = v
+    if "mlp.experts.gate_up_proj" in bank:
+        frozen, ids, sel_gu, sel_dn = _fused_bank(bank, sel_ids)
     else:
-        gq = {k[len("experts.gate_up."):]: v for k, v in t.items() if k.startswith("experts.gate_up.")}
-        dq = {k[len("experts.down."):]: v for k, v in t.items() if k.startswith("experts.down.")}
-        frozen = Int4Experts(gq, dq, dtype=frozen_dtype)
-        sgu, sdn = t.get("experts.sel.gate_up"), t.get("experts.sel.down")
-        if sel_ids is None and "experts.sel.ids" in t:
-            sel_ids = t["experts.sel.ids"].tolist()
-    if sgu is None:
-        sel_ids = None
-    return LayerWeights(idx, ltype, dense, LayerExperts(frozen, sel_ids, sgu, sdn, group=group, act=act))
+        frozen, ids, sel_gu, sel_dn = _packed_bank(bank, sel_ids, frozen_dtype)
+    return LayerWeights(idx, ltype, dense, LayerExperts(frozen, ids, sel_gu, sel_dn, group=group, act=act))
 
 
 def _order(names):
@@ -310,6 +344,21 @@ class PinnedSource(_StagedSource):
         return self.ltypes.get(l, "linear_attention")
 
 
+PACKED_FILE = "layer_{:02d}.safetensors"   # one file per layer of a packed block
+
+
+def _override_selection(own: dict, sel_rows, l, conv=None) -> dict:
+    """A layer's entries under a new selection: without one (``sel_rows`` None) its own entries; with one, its own
+    'experts.sel.*' entries give way to the selection's for layer l (none if the selection leaves it out). ``conv``
+    maps the selection's tensors first (e.g. to their sizes)."""
+    if sel_rows is None:
+        return own
+    new = sel_rows.get(l, {})
+    out = {k: v for k, v in own.items() if not k.startswith(_SEL_PREFIX)}
+    out.update(new if conv is None else {k: conv(v) for k, v in new.items()})
+    return out
+
+
 def _selected_rows(selection: dict, layers, ckpt) -> dict:
     """{l: the packed layer's experts.sel.* tensors} for a new selection, from the original checkpoint's fused bf16
     expert tensors (only the selected rows are read)."""
@@ -377,36 +426,44 @@ class PackedSource(_StagedSource):
         self.dir, self.d = packed_dir, dims
         self.sel_rows = None if selection is None else _selected_rows(selection, layers, ckpt)
         self.preloaded = preloaded or {}
-        self.pinned, self.pinned_gb = {}, 0.0
+        self.pinned = {}
+        used = 0
         if pin:
-            used = 0
-            for l in layers:
-                P = PinnedLayer(self._read(l))
-                if (used + P.nbytes) / 2**30 > pin_budget_gb:
-                    break
-                self.pinned[l] = P
-                self.preloaded.pop(l, None)
-                used += P.nbytes
-            self.pinned_gb = used / 2**30
+            # the longest prefix of `layers` whose tensor bytes fit the budget, decided from the files' headers (and
+            # the preloaded dicts) before any tensor is read; only those layers are then read and pinned
+            fits = itertools.takewhile(lambda lc: lc[1] / 2**30 <= pin_budget_gb,
+                                       zip(layers, itertools.accumulate(map(self._layer_bytes, layers))))
+            for l, used in list(fits):
+                self.pinned[l] = PinnedLayer(self._layer_tensors(l))
+                self.preloaded.pop(l, None)   # the pinned arena replaces the caller's host copy
+        self.pinned_gb = used / 2**30
 
-    def _path(self, l):
-        return os.path.join(self.dir, f"layer_{l:02d}.safetensors")
+    def _file(self, l) -> str:
+        return os.path.join(self.dir, PACKED_FILE.format(l))
 
-    def _read(self, l):
+    def _own_tensor_bytes(self, l) -> dict:
+        """{name: bytes} of layer l's own tensors (preloaded dict, or the safetensors header of its file)."""
         if l in self.preloaded:
-            t = self.preloaded[l]
-        else:
-            from safetensors import safe_open
-            with safe_open(self._path(l), "pt") as f:
-                t = {k: f.get_tensor(k) for k in f.keys()}
-        if self.sel_rows is None:
-            return t
-        t = {k: v for k, v in t.items() if not k.startswith("experts.sel.")}
-        t.update(self.sel_rows.get(l, {}))
-        return t
+            return {k: v.numel() * v.element_size() for k, v in self.preloaded[l].items()}
+        with open(self._file(l), "rb") as f:
+            n = int.from_bytes(f.read(8), "little")
+            head = json.loads(f.read(n))
+        return {k: e["data_offsets"][1] - e["data_offsets"][0] for k, e in head.items() if k != "__metadata__"}
+
+    def _layer_bytes(self, l) -> int:
+        sizes = _override_selection(self._own_tensor_bytes(l), self.sel_rows, l,
+                                    lambda v: v.numel() * v.element_size())
+        return sum(sizes.values())
+
+    def _layer_tensors(self, l) -> dict:
+        """Host tensors of layer l: the preloaded dict or the whole file, with a new selection's rows in place of the
+        packed block's own."""
+        own = self.preloaded[l] if l in self.preloaded else load_safetensors(self._file(l))
+        return _override_selection(own, self.sel_rows, l)
 
     def _pinned(self, l):
-        return self.pinned[l] if l in self.pinned else PinnedLayer(self._read(l))
+        P = self.pinned.get(l)
+        return P if P is not None else PinnedLayer(self._layer_tensors(l))
 
     def _ltype(self, l):
         return self.d.layer_types[l]

@@ -178,9 +178,9 @@ def test_wide_logit_range(lm, dtype):
         assert (g1.double().cpu() - g64).norm() / g64.norm() < 1e-4
 
 
-def test_several_row_passes(lm, monkeypatch):
-    """Passes of 64 rows (the pass size lowered for the test): the loss accumulates over the passes and each pass
-    writes its own gradient rows; equal to one pass over all rows."""
+def test_several_row_passes(lm):
+    """Passes of 16 rows (a caller's token_chunk bounds the rows of a pass): the loss accumulates over the passes and
+    each pass writes its own gradient rows; equal to one pass over all rows."""
     loss_mod, _ = lm
     torch.manual_seed(7)
     n, H, V = 200, 64, 1500
@@ -191,7 +191,6 @@ def test_several_row_passes(lm, monkeypatch):
     one = h.clone().requires_grad_(True)
     l_one = loss_mod.chunked_ce(one, head, tgt, denom=float(n))
     l_one.backward()
-    monkeypatch.setattr(loss_mod, "ROWS_PER_PASS", 64)
     many = h.clone().requires_grad_(True)
     l_many = loss_mod.chunked_ce(many, head, tgt, denom=float(n), token_chunk=16)
     (l_many * 2.0).backward()                                      # the incoming gradient scales the rows
@@ -199,6 +198,46 @@ def test_several_row_passes(lm, monkeypatch):
     assert torch.equal(many.grad.float(), (2.0 * one.grad.float()).bfloat16().float())
     l64, g64 = LR.full_ce(h, W, tgt, denom=float(n))
     assert abs(l_many.item() - float(l64)) / abs(float(l64)) < 1e-3
+
+
+def test_token_chunk_bounds_pass_memory(lm):
+    """token_chunk x vocab_chunk bounds a pass's scratch, as the reference promises for its peak memory: with
+    token_chunk=256 over 4096 rows, one call allocates at most one 256-row pass (softmax terms 256 x vocab_chunk
+    bf16, fp32 row state and accumulators) beyond its gradient output; left at the default, a pass takes all 4096
+    rows and its terms alone are 16 times larger. Both give the same loss and gradient."""
+    loss_mod, _ = lm
+    torch.manual_seed(9)
+    n, H, V, vc = 4096, 256, 65536, 32768
+    h = torch.randn(n, H, device="cuda").bfloat16()
+    W = (torch.randn(V, H, device="cuda") * 0.05).bfloat16()
+    tgt = torch.randint(0, V, (n,), device="cuda")
+    head = loss_mod.LMHead(weight=W, vocab_chunk=vc)
+
+    def run(**kw):
+        x = h.clone().requires_grad_(True)
+        loss_mod.chunked_ce(x, head, tgt, denom=float(n), **kw)   # the head's transposed copy is made once, here
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        loss = loss_mod.chunked_ce(x, head, tgt, denom=float(n), **kw)
+        loss.backward()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() - base, loss.detach(), x.grad
+
+    peak_small, l_small, g_small = run(token_chunk=256)
+    peak_dflt, l_dflt, g_dflt = run()
+    tc = 256
+    one_pass = tc * vc * 2 + tc * H * 4 * 3 + 2 * (vc // 128) * tc * 4 + (vc // 128) * tc + 6 * tc * 4
+    bound = one_pass + 2 * n * H * 2 + (1 << 20)    # + the gradient output and x.grad (bf16), small tensors
+    print(f"CE peak allocation: token_chunk=256 {peak_small / 2**20:.1f} MiB (bound {bound / 2**20:.1f}), default "
+          f"{peak_dflt / 2**20:.1f} MiB", flush=True)
+    assert peak_small <= bound
+    assert peak_dflt > 8 * tc * vc * 2
+    # the gradient GEMM splits its contraction by the number of row tiles of a pass, so the two pass sizes sum the
+    # fp32 partials in different orders: equal up to the last bits
+    assert abs(l_small.item() - l_dflt.item()) <= 1e-5 * abs(l_dflt.item())
+    d = (g_small.float() - g_dflt.float()).abs().max().item()
+    assert d <= 2**-7 * g_dflt.float().abs().max().item(), d
 
 
 def test_qwen_head_full_size(lm):

@@ -95,6 +95,33 @@ def test_dense_helpers_match_plain_formula():
     assert yb.dtype == torch.bfloat16 and yb.shape == (2, 5, 2 * I)
 
 
+def test_dense_helpers_bf16_round_once():
+    """bf16 rows as a matrix: the scaled LoRA term is added in the second LoRA product's epilogue (torch.addmm with
+    alpha, smel/lora.py:61-83), so it is not rounded on its own before the add. Bitwise equal to that form for both
+    helpers, and different from rounding the LoRA product first (so the check can fail)."""
+    torch.manual_seed(5)
+    T, H, I, r, s = 64, 96, 40, 8, 2.0
+    bf = torch.bfloat16
+    x = torch.randn(T, H).to(bf)
+    wgu = (torch.randn(2 * I, H) * 0.1).to(bf)
+    Ag, Au = torch.randn(r, H) * 0.1, torch.randn(r, H) * 0.1
+    Bg, Bu = torch.randn(I, r) * 0.1, torch.randn(I, r) * 0.1
+    g, u = lora_gate_up(x, wgu, Ag, Bg, Au, Bu, s)
+    base = x @ wgu.t()
+    xa = x @ torch.cat((Ag, Au)).to(bf).t()
+    g_ref = torch.addmm(base[:, :I], xa[:, :r], Bg.to(bf).t(), alpha=s)
+    u_ref = torch.addmm(base[:, I:], xa[:, r:], Bu.to(bf).t(), alpha=s)
+    assert torch.equal(g, g_ref) and torch.equal(u, u_ref)
+    y = lora_linear(x, wgu[:I], Ag, Bg, s)
+    y_ref = torch.addmm(x @ wgu[:I].t(), x @ Ag.to(bf).t(), Bg.to(bf).t(), alpha=s)
+    assert torch.equal(y, y_ref)
+    twice = torch.add(x @ wgu[:I].t(), (x @ Ag.to(bf).t()) @ Bg.to(bf).t(), alpha=s)
+    assert not torch.equal(y, twice)
+    # rows of a leading shape: the same values as the flattened matrix
+    g3, u3 = lora_gate_up(x.reshape(4, 16, H), wgu, Ag, Bg, Au, Bu, s)
+    assert torch.equal(g3.reshape(T, I), g) and torch.equal(u3.reshape(T, I), u)
+
+
 def test_block_build_and_adapter_roundtrip(tmp_path):
     """BlockLoRA.build over a selection, then an adapter folder in the reference trainer's format (config keys
     experts / r / alpha / shared_lora, tensors under the module paths) loads back equal."""
