@@ -63,6 +63,11 @@ typedef struct smel_wset {
  * XCDs takes a contiguous chunk of it, so a group's tiles run side by side on one XCD and share its L2 (its weights
  * are streamed once for all of them); without it, tile t runs on XCD t % 8 in list order. */
 #define SMEL_WSET_XCD_CHUNK 4
+/* SMEL_WSET_MERGE_SHORT (smel_gmm_fwd, gate_up projection, group-ordered tile list, int4 bank with
+ * SMEL_WSET_FAST_DQ, C a multiple of 64): the blocks of a full int4 tile also take the rows of the next tile when that is the same
+ * group's last tile of at most 32 rows (the weights are streamed and dequantized once for up to 160 rows); that
+ * tile's own blocks do nothing. */
+#define SMEL_WSET_MERGE_SHORT 8
 
 const char* smel_last_error(void);
 int smel_abi_version(void);

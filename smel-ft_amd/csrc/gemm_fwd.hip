@@ -6,7 +6,9 @@
 // smel/moe.py:58-72, 110-117, 204-211 and smel/lora.py:61-83.
 //
 // Block = 4 waves, tile = up to 128 rows of one group (4 slices of 32) x (gate_up: 32 gate + 32 up columns per wave;
-// down: 64 columns per wave). MFMA 32x32x16 bf16. Per 64-wide k-step:
+// down: 64 columns per wave); the gate_up projection of an int4 group also takes up to 160 rows (5 slices) when a
+// full tile and the group's last tile of at most 32 rows are merged (SMEL_WSET_MERGE_SHORT): the weights are then
+// streamed and dequantized once for all of the group's rows. MFMA 32x32x16 bf16. Per 64-wide k-step:
 //  * A (activation rows, gathered by token) goes global -> LDS directly (16-B LDS-DMA loads, 1 KB per wave-load, no
 //    registers), into a ring of 4 stages; each 128-B row's 16-B chunks are XOR-swizzled so the fragment reads are
 //    bank-conflict free. Every wave reads all rows of a stage.
@@ -23,22 +25,30 @@
 
 namespace {
 
-constexpr int MT = 128;
+constexpr int MT = 128;            // rows of a tile of the tile list
+constexpr int MT_MERGED = 160;     // rows of a merged gate_up tile: a full tile + a last tile of <= 32 rows
 constexpr int KT = 64;
-constexpr int A_STAGE = MT * KT;   // bf16 elements of one A stage: row r at r * KT, no padding
+// Rows an A stage holds (row r at r * KT bf16, no padding): 160 for the gate_up projection (the merged tiles; its
+// epilogue keeps the g and u tiles of 160 x 128 in the four stages), 128 for the down projection.
+constexpr int stage_rows(int epi) { return epi == 1 ? MT_MERGED : MT; }
 
 // Vector-memory operations per wave in each issue group of the main loops; the issue code below is written with
 // these counts and every wait is computed from them (vmcnt retires in issue order).
-constexpr int VM_A = A_STAGE * 2 / (4 * 1024);   // A rows of a stage: 1-KB LDS-DMA wave-loads, 4 waves
+// A rows of a stage: 1-KB LDS-DMA wave-loads of 8 rows; with 4 waves, 4 per wave cover 128 rows, 5 cover 160.
+constexpr int vm_a(int ns) { return ns > 4 ? 5 : 4; }
 constexpr int VM_Q = 2;                           // int4: one 16-B word per weight fragment, 2 fragments
-constexpr int VM_SZ = 2;                          // int4: the packed scale/zero run of 4 k-steps, per fragment
+constexpr int VM_SZ = 2;                          // int4: a scale/zero run (16 B) or pair (4 B), per fragment
 constexpr int VM_B = 2 * 4;                       // bf16: 4 substep chunks per fragment, 2 fragments
-// int4: the group of step j carries the scale/zero run iff j % 4 == 0; while step j (round position pos = j % 4)
-// computes, the groups of steps j+1 and j+2 may still be in flight
-constexpr int q4_group(int j) { return VM_Q + (j % 4 == 0 ? VM_SZ : 0) + VM_A; }
-constexpr int q4_wait(int pos) { return q4_group(pos + 1) + q4_group(pos + 2); }
+// int4, tiles of up to 4 slices: the group of step j carries the packed scale/zero run of steps j..j+3 iff j % 4 ==
+// 0; after the barrier of step j the group of step j+3 is issued; while step j (round position pos = j % 4) computes,
+// the groups of steps j+1 and j+2 may still be in flight (four sets of weight registers)
+constexpr int q4_group(int j, int vma) { return VM_Q + (j % 4 == 0 ? VM_SZ : 0) + vma; }
+constexpr int q4_wait(int pos, int vma) { return q4_group(pos + 1, vma) + q4_group(pos + 2, vma); }
+// int4, 5-slice (merged) tiles, whose accumulators leave room for three sets of weight registers only: after the
+// barrier of step j the group [q, scale/zero of step j+2 | A of step j+3] is issued. Before step j computes it needs
+// q(j) (group of step j-2) and A(j) (group of step j-3): A(j+1) and the whole group of step j-1 may still be in flight.
+constexpr int q4_wait_w2(int vma) { return vma + (VM_Q + VM_SZ + vma); }
 // bf16: issue order ... B(j+1), A(j+3): before step j only the last group, A(j+2), may be in flight
-constexpr int BF_WAIT = VM_A;
 
 struct FwdArgs {
   smel_wset w;
@@ -63,6 +73,9 @@ struct FwdArgs {
 template <int EPI, bool Q4, int NS, bool FAST>
 SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
                        uint16_t* S2, uint16_t* S3, int* rowmap, uint16_t* X) {
+  static_assert(NS * 32 <= stage_rows(EPI), "the tile's rows fit the A stages");
+  constexpr int VMA = vm_a(NS);               // A wave-loads per wave and stage
+  constexpr int BF_WAIT = VMA;                // bf16: issue order ... B(j+1), A(j+3): before step j only A(j+2)
   const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = a.K;
@@ -137,18 +150,20 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     }
     lds_barrier();
   }
-  // ---- A staging: wave-load ii of wave w fills rows 8 g .. 8 g + 7 (g = 4 w + ii) of a stage, 1 KB; lane i writes
+  // ---- A staging: wave-load ii of wave w fills rows 8 g .. 8 g + 7 (g = VMA w + ii) of a stage, 1 KB; lane i writes
   // physical chunk i % 8 of row 8 g + i / 8, i.e. logical chunk c = (i % 8) ^ swz(row).
   const rsrc_t ra = make_rsrc(a.A, (uint64_t)a.a_rows * a.lda * 2);
   const int li = tid & 63;
-  uint32_t aoff[VM_A];
-  int akc[VM_A];   // first k of this lane's chunk
+  // Tiles of up to 4 slices keep each chunk's first k (akc) for the K tail; a merged 5-slice tile exists only for K a
+  // multiple of 64 (every chunk of an in-range step is inside the row) and keeps no such registers.
+  constexpr bool TAIL = NS <= 4;
+  uint32_t aoff[VMA];
+  int akc[TAIL ? VMA : 1];   // first k of this lane's chunk
 #pragma unroll
-  for (int ii = 0; ii < VM_A; ++ii) {
-    const int g = VM_A * w + ii;
-    const int row = 8 * g + (li >> 3);
+  for (int ii = 0; ii < VMA; ++ii) {
+    const int row = 8 * (VMA * w + ii) + (li >> 3);
     const int c = (li & 7) ^ swz(row);
-    akc[ii] = 8 * c;
+    if constexpr (TAIL) akc[ii] = 8 * c;
     aoff[ii] = OOB;
     if (row < nrows) {
       const int grow = row0 + row;
@@ -160,8 +175,12 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     const int k0 = j * KT;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ii = 0; ii < VM_A; ++ii)
-      ld16_lds(ra, S + (VM_A * w + ii) * 512, (k0 + akc[ii] + 8 <= K) ? aoff[ii] + k0 * 2 : OOB);
+    for (int ii = 0; ii < VMA; ++ii) {
+      if constexpr (TAIL)
+        ld16_lds(ra, S + (VMA * w + ii) * 512, (k0 + akc[ii] + 8 <= K) ? aoff[ii] + k0 * 2 : OOB);
+      else
+        ld16_lds(ra, S + (VMA * w + ii) * 512, aoff[ii] + k0 * 2);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   // A fragment reads: lane (r32, h) of slice m, substep s reads logical chunk 4 h + s of row 32 m + r32
@@ -182,9 +201,9 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     }
   };
 
-  if constexpr (Q4) {
+  if constexpr (Q4 && NS <= 4) {
     // Group of loads for step j: q (2), then, when j % 4 == 0, the packed (scale, zero) run of steps j..j+3 (2),
-    // then A (4). Groups j+1, j+2 are in flight while step j computes; group j+3 is issued after its barrier.
+    // then A (VMA). Groups j+1, j+2 are in flight while step j computes; group j+3 is issued after its barrier.
     static_assert(VM_Q == 2 && VM_SZ == 2, "one q word and one scale/zero run per fragment, 2 fragments");
     u32x4_t q0[VM_Q], q1[VM_Q], q2[VM_Q], q3[VM_Q], szc[VM_SZ], szn[VM_SZ];
     const uint32_t wof[VM_Q] = {wo0, wo1}, sof[VM_SZ] = {so0, so1};
@@ -223,24 +242,85 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     issue(2, q2, nullptr, S2);
     // ceil(nk / 4) * 4 steps, branch-free: a step past K loads zeros and adds nothing
     for (int i = 0; i < nk; i += 4) {
-      wait_vm_lds<q4_wait(0)>();
+      wait_vm_lds<q4_wait(0, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 3, q3, nullptr, S3);
       compute(S0, q0, 0);
-      wait_vm_lds<q4_wait(1)>();
+      wait_vm_lds<q4_wait(1, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 4, q0, szn, S0);
       compute(S1, q1, 1);
-      wait_vm_lds<q4_wait(2)>();
+      wait_vm_lds<q4_wait(2, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 5, q1, nullptr, S1);
       compute(S2, q2, 2);
-      wait_vm_lds<q4_wait(3)>();
+      wait_vm_lds<q4_wait(3, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 6, q2, nullptr, S2);
       compute(S3, q3, 3);
       szc[0] = szn[0];
       szc[1] = szn[1];
+    }
+  } else if constexpr (Q4) {
+    // 5-slice (merged) tiles: 160 accumulators leave room for three sets of weight registers only, so the weights
+    // (q and the step's (scale, zero) pair of each fragment, 4 B: word j % 4 of the packed run) are loaded two steps
+    // ahead and A three. In issue order: A(0), [q/z(0) A(1)], [q/z(1) A(2)], then after the barrier of step j
+    // [q/z(j+2) A(j+3)].
+    static_assert(VM_Q == 2 && VM_SZ == 2, "one q word and one scale/zero pair per fragment, 2 fragments");
+    u32x4_t q0[VM_Q], q1[VM_Q], q2[VM_Q], q3[VM_Q];
+    uint32_t z0[VM_SZ], z1[VM_SZ], z2[VM_SZ], z3[VM_SZ];
+    const uint32_t wof[VM_Q] = {wo0, wo1}, sof[VM_SZ] = {so0, so1};
+    auto issue_w = [&](int j, u32x4_t* q, uint32_t* z) {
+      const bool in = j < nk;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int f = 0; f < VM_Q; ++f) q[f] = ld16(rw, in ? wof[f] + j * 1024 : OOB);
+#pragma unroll
+      for (int f = 0; f < VM_SZ; ++f) z[f] = ld4(rsz, in ? sof[f] + (j >> 2) * 1024 + 4 * (j & 3) : OOB);
+    };
+    const uint32_t magic = FAST ? f16_magic() : 0u;
+    auto compute = [&](const uint16_t* S, const u32x4_t* q, const uint32_t* z) {
+      const float s0 = bf_lo(z[0]), z0v = bf_hi(z[0]), s1 = bf_lo(z[1]), z1v = bf_hi(z[1]);
+      const FastSZ f0 = fast_sz(s0, z0v), f1 = fast_sz(s1, z1v);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint32_t o0[4], o1[4];
+        if constexpr (FAST) {
+          dq8f(q[0][s], f0, magic, o0);
+          dq8f(q[1][s], f1, magic, o1);
+        } else {
+          dq8(q[0][s], s0, z0v, o0);
+          dq8(q[1][s], s1, z1v, o1);
+        }
+        mma(S, s, u32x4_t{o0[0], o0[1], o0[2], o0[3]}, u32x4_t{o1[0], o1[1], o1[2], o1[3]});
+      }
+    };
+    issue_a(0, S0);
+    issue_w(0, q0, z0);
+    issue_a(1, S1);
+    issue_w(1, q1, z1);
+    issue_a(2, S2);
+    for (int i = 0; i < nk; i += 4) {
+      wait_vm_lds<q4_wait_w2(VMA)>();
+      __builtin_amdgcn_s_barrier();
+      issue_w(i + 2, q2, z2);
+      issue_a(i + 3, S3);
+      compute(S0, q0, z0);
+      wait_vm_lds<q4_wait_w2(VMA)>();
+      __builtin_amdgcn_s_barrier();
+      issue_w(i + 3, q3, z3);
+      issue_a(i + 4, S0);
+      compute(S1, q1, z1);
+      wait_vm_lds<q4_wait_w2(VMA)>();
+      __builtin_amdgcn_s_barrier();
+      issue_w(i + 4, q0, z0);
+      issue_a(i + 5, S1);
+      compute(S2, q2, z2);
+      wait_vm_lds<q4_wait_w2(VMA)>();
+      __builtin_amdgcn_s_barrier();
+      issue_w(i + 5, q1, z1);
+      issue_a(i + 6, S2);
+      compute(S3, q3, z3);
     }
   } else {
     // bf16 weights: 8 loads per fragment pair and step, one step ahead in two alternating register sets; A three
@@ -334,15 +414,19 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
         xscale = a.lr.scale_sh;
       }
     }
-    // g tile [128][128] in S0 (rows 0..63) / S1, u tile in S2 / S3; column = 32 w + r32 inside the block's 128
+    // g tile [160][128] in S0 (rows 0..HALF-1) / S1 (rows HALF..), u tile in S2 / S3 (a stage holds HALF rows of 128
+    // columns); column = 32 w + r32 inside the block's 128. Which stage a row goes to is known at compile time: HALF is
+    // a multiple of 8 and a lane's part of acc_row is below 8.
+    constexpr int HALF = stage_rows(1) / 2;
     const int col = 32 * w + r32;
 #pragma unroll
     for (int m = 0; m < NS; ++m) {
-      uint16_t* G = m < 2 ? S0 : S1;
-      uint16_t* U = m < 2 ? S2 : S3;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m * 32 + acc_row(r, l), lr = row & 63;
+        const bool lo = m * 32 + 8 * (r >> 2) < HALF;
+        uint16_t* G = lo ? S0 : S1;
+        uint16_t* U = lo ? S2 : S3;
+        const int row = m * 32 + acc_row(r, l), lr = lo ? row : row - HALF;
         const int e = lr * 128 + 8 * ((col >> 3) ^ (row & 7)) + (col & 7);
         G[e] = f2bf(acc[m][0][r]);
         U[e] = f2bf(acc[m][1][r]);
@@ -355,10 +439,11 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     const int col0 = nb * 128 + 8 * ch;
     if (col0 < I) {
       for (int row = tid >> 4; row < nrows; row += 16) {
-        const int lr = row & 63;
+        const bool lo = row < HALF;
+        const int lr = lo ? row : row - HALF;
         const int e = lr * 128 + 8 * (ch ^ (row & 7));
-        const u32x4_t g = *reinterpret_cast<const u32x4_t*>((row < 64 ? S0 : S1) + e);
-        const u32x4_t u = *reinterpret_cast<const u32x4_t*>((row < 64 ? S2 : S3) + e);
+        const u32x4_t g = *reinterpret_cast<const u32x4_t*>((lo ? S0 : S1) + e);
+        const u32x4_t u = *reinterpret_cast<const u32x4_t*>((lo ? S2 : S3) + e);
         uint32_t o[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -370,7 +455,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
           *reinterpret_cast<u32x4_t*>(a.hsave + grow * a.N + I + col0) = u;
         }
         if (xa)   // h replaces g in the tile (each chunk is read and written by this thread only)
-          *reinterpret_cast<u32x4_t*>((row < 64 ? S0 : S1) + e) = u32x4_t{o[0], o[1], o[2], o[3]};
+          *reinterpret_cast<u32x4_t*>((lo ? S0 : S1) + e) = u32x4_t{o[0], o[1], o[2], o[3]};
       }
     }
     if (xa) {
@@ -381,8 +466,8 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
         const rsrc_t rb = make_rsrc(xa, (uint64_t)32 * I * 2);
         f32x16_t px = f32x16_t{};
         const int row = 32 * w + r32;
-        const uint16_t* Hh = row < 64 ? S0 : S1;
-        const int lr_ = row & 63;
+        const uint16_t* Hh = row < HALF ? S0 : S1;
+        const int lr_ = row < HALF ? row : row - HALF;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -439,27 +524,41 @@ SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nro
     case 1: run_tile<EPI, Q4, 1, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
     case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
     case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
-    default: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
+    case 4: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
+    default:   // 5 slices: only a merged int4 tile (fast dequant form) of the gate_up projection has more rows
+      if constexpr (EPI == 1 && Q4 && FAST)
+        run_tile<EPI, Q4, 5, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X);
+      break;
   }
 }
 
 template <int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t S0[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S1[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S2[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S3[A_STAGE];
-  __shared__ int rowmap[MT];
-  // the down projection's LoRA rows of a tile (bf16 [128][32]); unused by the gate_up kernel
-  __shared__ __attribute__((aligned(16))) uint16_t X[EPI == 0 ? MT * 32 : 8];
+SMEL_DEV void gmm_fwd_body(const FwdArgs& a, uint16_t* S0, uint16_t* S1, uint16_t* S2, uint16_t* S3, int* rowmap,
+                           uint16_t* X) {
   int tile, nb;
-  if (!((a.w.flags & SMEL_WSET_XCD_CHUNK) ? xcd_tile_chunk(a.n_tiles[0], a.nblk, tile, nb)
-                                          : xcd_tile(a.n_tiles[0], a.nblk, tile, nb)))
+  const int n_t = a.n_tiles[0];
+  if (!((a.w.flags & SMEL_WSET_XCD_CHUNK) ? xcd_tile_chunk(n_t, a.nblk, tile, nb) : xcd_tile(n_t, a.nblk, tile, nb)))
     return;
   const int4 t = a.tiles[tile];
   const int gk = a.gkind ? a.gkind[t.x] : t.w;   // the tile list may carry the group kind itself
   const int kind = gk >> 16, idx = gk & 0xffff;
-  const int nrows = min(t.z - t.y, MT);
+  int row1 = t.z;
+  if (EPI == 1 && kind == SMEL_KIND_INT4 && (a.w.flags & SMEL_WSET_MERGE_SHORT) && (a.w.flags & SMEL_WSET_FAST_DQ) &&
+      (a.K & (KT - 1)) == 0) {
+    // In a group-ordered list, a group's last tile of at most MT_MERGED - MT rows right after a full tile of the same
+    // group is taken by the full tile's blocks (one weight stream and dequant for both); its own blocks exit. (Banks
+    // in the fast dequant form and K a multiple of 64 only: the 5-slice tile has no registers for the other form or
+    // for a K tail.)
+    if (t.z - t.y <= MT_MERGED - MT && tile > 0) {
+      const int4 p = a.tiles[tile - 1];
+      if (p.x == t.x && p.z == t.y && p.z - p.y == MT) return;
+    }
+    if (t.z - t.y == MT && tile + 1 < n_t) {
+      const int4 q = a.tiles[tile + 1];
+      if (q.x == t.x && q.y == t.z && q.z - q.y <= MT_MERGED - MT) row1 = q.z;
+    }
+  }
+  const int nrows = min(row1 - t.y, stage_rows(EPI));
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4) {
     if (a.w.flags & SMEL_WSET_FAST_DQ)
@@ -467,7 +566,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     else
       run_tile_ns<EPI, true, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap, X);
   } else {
-    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, nrows, nb, S0, S1, S2, S3, rowmap, X);
+    run_tile_ns<EPI, false, false>(a, kind, idx, t.y, min(nrows, MT), nb, S0, S1, S2, S3, rowmap, X);
+  }
+}
+
+// The gate_up projection (epilogue 1): four A stages of 160 rows (80 KiB, two blocks per CU), nothing else in LDS.
+// The down projection (epilogue 0): four stages of 128 rows, the output slots of the tile's rows and its LoRA rows.
+template <int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_fwd_kernel(FwdArgs a) {
+  constexpr int STAGE = stage_rows(EPI) * KT;
+  __shared__ __attribute__((aligned(1024))) uint16_t S0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S1[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S2[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t S3[STAGE];
+  if constexpr (EPI == 0) {
+    __shared__ int rowmap[MT];
+    __shared__ __attribute__((aligned(16))) uint16_t X[MT * 32];   // the down projection's LoRA rows of a tile
+    gmm_fwd_body<EPI>(a, S0, S1, S2, S3, rowmap, X);
+  } else {
+    gmm_fwd_body<EPI>(a, S0, S1, S2, S3, nullptr, nullptr);
   }
 }
 

@@ -19,7 +19,8 @@ PACK_Q4, PACK_SZ, PACK_BF16 = 0, 1, 2
 WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
-ABI_VERSION = 18
+WSET_MERGE_SHORT = 8 # smel_wset.flags: gate_up forward, a full int4 tile also takes the group's short last tile
+ABI_VERSION = 19
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 

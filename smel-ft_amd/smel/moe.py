@@ -358,6 +358,10 @@ _BWD_LORA_ROWS = os.environ.get("SMEL_BWD_LORA_ROWS", "1") == "1"
 # partials (smel_gmm_fwd_lr), summed and stored by the down forward; 0: a smel_lora_ext launch over the gate_up
 # output between the two GEMMs
 _FWD_LORA_ROWS = os.environ.get("SMEL_FWD_LORA_ROWS", "1") == "1"
+# SMEL_MERGE_SHORT=1 (default): the gate_up forward takes an int4 expert's last tile of at most 32 rows together with
+# the full tile before it (one weight stream and dequant for up to 160 rows; banks in the fast dequant form); 0: every
+# tile of the list on its own
+_MERGE_SHORT = os.environ.get("SMEL_MERGE_SHORT", "1") == "1"
 
 
 def _side_stream(dev, i: int) -> torch.cuda.Stream:
@@ -721,7 +725,7 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     # the gate_up GEMMs take the tiles in group order, a chunk per XCD (an expert's tiles share its weights in L2);
     # the down GEMMs the long-tiles-first order (short tiles fill the last round)
     w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"), planes=planes)
-    w_gu.flags |= L.WSET_XCD_CHUNK
+    w_gu.flags |= L.WSET_XCD_CHUNK | (L.WSET_MERGE_SHORT if _MERGE_SHORT else 0)
     # the down LoRA's rows come from the gate_up epilogue (per-column-block partials of h A_dn^T), summed and stored
     # by the down GEMM: no separate projection launch
     lr = None
@@ -1287,6 +1291,7 @@ class FrozenExpertsFn(torch.autograd.Function):
         dev = xs.device
         st = L.stream()
         w_gu, w_dn = _bank_wset(bank, "gu"), _bank_wset(bank, "dn")
+        w_gu.flags |= L.WSET_MERGE_SHORT if _MERGE_SHORT else 0   # the count tiles are in group order
         I = w_dn.C
         bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
         out = bf(rows, H)

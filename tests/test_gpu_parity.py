@@ -564,6 +564,26 @@ def test_layer_parity(name):
     assert set(grads) == set(g["grads"])
 
 
+@pytest.mark.parametrize("name", ["r16"])
+def test_merged_short_tiles_bitwise(name, monkeypatch):
+    """The gate_up forward's merged tiles (a full int4 tile and the expert's last tile of <= 32 rows in one block,
+    SMEL_WSET_MERGE_SHORT) accumulate every row in the same k order as the separate tiles: y, dX and the LoRA
+    gradients are bitwise equal with and without the merge. (r16: 32 experts of about 129 rows, so most experts have
+    a short last tile.)"""
+    import smel.moe as M
+    _say(f"merged short tiles {name}")
+    monkeypatch.setattr(M, "_MERGE_SHORT", True)
+    a = run_layer(name, seed=4)
+    monkeypatch.setattr(M, "_MERGE_SHORT", False)
+    b = run_layer(name, seed=4)
+    counts = torch.bincount(a["topi"].flatten(), minlength=LAYERS[name]["E"])
+    assert bool(((counts > 128) & (counts <= 160)).any()), counts   # some expert has a merged tile
+    assert torch.equal(a["y"].view(torch.int16), b["y"].view(torch.int16))
+    assert torch.equal(a["dx"].view(torch.int16), b["dx"].view(torch.int16))
+    for k in b["grads"]:
+        assert torch.equal(a["grads"][k], b["grads"][k]), k
+
+
 @pytest.mark.parametrize("name", ["r16", "r32", "shared_wide", "r24_mixed"])
 def test_bwd_lora_rows_against_projection(name, monkeypatch):
     """The gate_up backward's LoRA rows from the down backward's per-column-block partials (smel_gmm_bwd_lr +
@@ -737,6 +757,9 @@ def test_gelu_experts_parity():
     (False, "gelu_tanh", [9, 0, 12, 7, 15, 7]),
     (True, "silu", [0, 300, 1, 129, 0, 0, 64, 128]),              # tiles split at 128 rows, empty experts
     (True, "gelu_tanh", [0, 0, 0, 0, 0, 0]),                      # no rows at all
+    # full tiles merged with a last tile of <= 32 rows in the gate_up forward (160, 129, 150, 288 = 128 + 160),
+    # and not merged (161 = 128 + 33, 96)
+    (True, "silu", [160, 0, 129, 161, 288, 5, 150, 96]),
 ])
 def test_frozen_experts_fn(int4, act_name, counts):
     """FrozenExpertsFn.apply(xs, counts, bank, group, act) (smel/moe.py:120-143) on rows sorted by expert, forward
