@@ -1019,6 +1019,7 @@ class _RoutedFn(torch.autograd.Function):
         tv = topv.detach().float().contiguous()   # fp32 combine weights: the reference's topv.float() (:252)
         need = ctx.needs_input_grad[0] or ctx.needs_input_grad[1] or any(ctx.needs_input_grad[5:])
         out = _forward_pipeline(x, ex, K, tv, topi.contiguous(), topi.dtype == torch.int64, None, lora, None, need, c)
+        _ID_CHECK.record(c.tensors["err"])
         if need:
             ctx.c = c
         ctx.topv_dtype = topv.dtype
@@ -1033,23 +1034,58 @@ class _RoutedFn(torch.autograd.Function):
         return (dx, dtopv.to(ctx.topv_dtype), None, None, None, *g)
 
 
-def _check_ids(topi: torch.Tensor, E: int):
-    """Expert ids handed in by a caller must lie in [0, E), where the reference's bincount / indexing
-    (smel/moe.py:216-223) fails otherwise: checked here with one host synchronisation. Inside a HIP-graph capture
-    (no synchronisation possible) the check is skipped; the dispatch then drops a slot whose id is out of range
-    (inv = -1) and the combine, the dX reduce and the d(topv) reduction treat it as a zero row, so the output and
-    the gradients stay defined."""
-    if topi.numel() == 0 or torch.cuda.is_current_stream_capturing():
-        return
-    if bool(((topi < 0) | (topi >= E)).any()):
-        raise IndexError(f"routed_experts: expert ids must lie in [0, {E})")
+class _DeferredIdCheck:
+    """Expert ids handed in by a caller must lie in [0, E) (the reference's bincount / indexing, smel/moe.py:216-223,
+    fails otherwise, on the GPU asynchronously). The dispatch kernel checks them itself: it drops a slot whose id is
+    out of range (inv = -1; the combine, the dX reduce and the d(topv) reduction read it as a zero row, so outputs and
+    gradients stay defined) and sets bit 0 of its error word. Each eager call copies that word into pinned host memory
+    behind an event, without waiting; the next routed_experts call raises IndexError for every earlier call whose copy
+    has landed with the bit set, and check_routing_errors() waits for all of them. No call synchronises the host.
+    Under HIP-graph capture nothing is recorded (the replays drop such slots as above)."""
+
+    def __init__(self):
+        self.pending = []   # (event, pinned host word)
+
+    def record(self, err: torch.Tensor):
+        if torch.cuda.is_current_stream_capturing():
+            return
+        host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        host.copy_(err, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.pending.append((ev, host))
+
+    def poll(self, wait: bool = False):
+        done, keep = [], []
+        for ev, host in self.pending:
+            if wait:
+                ev.synchronize()
+            if wait or ev.query():
+                done.append(host)
+            else:
+                keep.append((ev, host))
+        self.pending = keep
+        if any(int(h[0]) & 1 for h in done):
+            raise IndexError("routed_experts: expert ids must lie in [0, E) (an earlier call's dispatch dropped "
+                             "slots with ids out of range)")
+
+
+_ID_CHECK = _DeferredIdCheck()
+
+
+def check_routing_errors():
+    """Wait for the id checks of earlier routed_experts calls and raise IndexError if any was given an expert id
+    outside [0, E) (such slots were dropped: they contributed zero rows)."""
+    _ID_CHECK.poll(wait=True)
 
 
 def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
-    """Weighted sum of the routed experts of every token (smel/moe.py:214-252)."""
+    """Weighted sum of the routed experts of every token (smel/moe.py:214-252). Expert ids outside [0, E) are reported
+    by the next call or check_routing_errors(), without a host synchronisation here."""
     L.require_device(x2d, topv, topi)
     _check_bank(ex)
-    _check_ids(topi, ex.E)
+    if not torch.cuda.is_current_stream_capturing():
+        _ID_CHECK.poll()
     return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
 
 

@@ -3,11 +3,14 @@ the stager of include/smel_stream.h.
 
 A layer's tensors live in one pinned host arena (``PinnedLayer``: the reference's tensor names, 256-byte aligned
 offsets, the dense gate and up projections next to each other). ``prefetch(l)`` copies the arena into a device slot
-on copy streams (chunked over two DMA queues), then, on the first copy stream, packs the frozen int4 bank and the
-selected experts into the grouped GEMMs' layouts, so the layer arrives ready to run; ``get(l)`` makes the current
-(compute) stream wait on the stage's event. The host never blocks on a copy (the reference's worker thread waits on
-every upload's event, smel/stream.py:62). The one host synchronisation is the exact-fast-dequant check of an int4
-bank, once per pinned layer on its first upload (the answer is kept with the pinned layer).
+on copy streams (chunked over two DMA queues) in copy groups: the int4 banks in chunks of BANK_CHUNK experts first,
+then the selected experts, then the rest. A pack stream turns each group into the grouped GEMMs' layouts as soon as
+its copies have landed (forward and transposed int4 layouts, the selected experts' bf16 layouts), writing into a
+second arena the slot owns, so an upload allocates nothing on the device and only the last group's packing follows
+the copy; ``get(l)`` makes the current (compute) stream wait on the stage's event. The host never blocks on a copy
+(the reference's worker thread waits on every upload's event, smel/stream.py:62). The one host synchronisation is the
+exact-fast-dequant check of an int4 bank, once per pinned layer before its first upload (the answer is kept with the
+pinned layer).
 
 Differences from the reference, by design: a slot is reused once ``max_on_gpu`` other layers were fetched after it,
 so a ``LayerWeights`` from ``get(l)`` is valid until then (the layer-major runner uses a layer before fetching the
@@ -26,11 +29,12 @@ import torch
 from safetensors.torch import load_file as load_safetensors
 
 from . import _lib as L
-from .moe import BF16Experts, Int4Experts, LayerExperts
+from .moe import BF16Experts, Int4Experts, LayerExperts, PackedW
 
 ALIGN = 256
 CHUNK_BYTES = 8 << 20
 N_COPY_STREAMS = 2
+BANK_CHUNK = 64          # experts per copy group of an int4 bank (each group is packed as soon as it has landed)
 
 
 class LayerWeights:
@@ -135,6 +139,18 @@ def arena_layout(t: dict):
     return meta, -(-off // ALIGN) * ALIGN
 
 
+def bank_geometry(meta: dict) -> dict:
+    """{'gu' | 'dn': (E, R, C, group)} of the int4 banks an arena layout holds (q [E][R][C/2], scale / zero
+    [E][R][C/group])."""
+    banks = {}
+    for which, name in (("gu", "gate_up"), ("dn", "down")):
+        q, sc = meta.get(f"experts.{name}.q"), meta.get(f"experts.{name}.scale")
+        if q is not None and sc is not None and f"experts.{name}.zero" in meta:
+            E, R, half = q[1]
+            banks[which] = (E, R, 2 * half, 2 * half // sc[1][2])
+    return banks
+
+
 class PinnedLayer:
     """One layer's tensors copied once into a pinned host arena (page-locked: the DMA engines read it directly)."""
 
@@ -146,18 +162,81 @@ class PinnedLayer:
                 self.host[off:off + nb].copy_(t[k].detach().contiguous().reshape(-1).view(torch.uint8))
         ids = t.get("experts.sel.ids")
         self.sel_ids = None if ids is None else [int(i) for i in ids.tolist()]
-        self.fast = {}   # int4 bank: {'gu' | 'dn': exact fast dequant form holds}, filled at the first upload
+        self.fast = {}   # int4 bank: {'gu' | 'dn': exact fast dequant form holds}, filled before the first upload
+        self.banks = bank_geometry(self.meta)
+
+
+_BANK_NAMES = {"gu": "gate_up", "dn": "down"}
+
+
+class _UploadPlan:
+    """How a pinned layer goes up: its copy groups (lists of (arena offset, bytes)) in order, what is packed after
+    each, and the byte layout of the packed GEMM layouts in the slot's pack arena."""
+
+    def __init__(self, P: PinnedLayer):
+        lib = L.load()
+        self.groups, self.after = [], []          # after[i]: ('bank', which, e0, e1) / ('sel',) / None
+        self.pack_at, self.pack_bytes = {}, 0     # name -> (byte offset, bytes) in the pack arena
+
+        def put(name, nb):
+            self.pack_at[name] = (self.pack_bytes, nb)
+            self.pack_bytes += -(-nb // ALIGN) * ALIGN
+
+        banked = set()
+        for which, (E, R, C, g) in P.banks.items():
+            fields = [P.meta[f"experts.{_BANK_NAMES[which]}.{f}"] for f in ("q", "scale", "zero")]
+            banked.update(f"experts.{_BANK_NAMES[which]}.{f}" for f in ("q", "scale", "zero"))
+            for e0 in range(0, E, BANK_CHUNK):
+                e1 = min(E, e0 + BANK_CHUNK)
+                self.groups.append([(off + e0 * (nb // E), (e1 - e0) * (nb // E)) for off, _, _, nb in fields])
+                self.after.append(("bank", which, e0, e1))
+            put(which + ".f.q", lib.smel_packed_bytes(L.PACK_Q4, E * R, C))
+            put(which + ".f.sz", lib.smel_packed_bytes(L.PACK_SZ, E * R, C))
+            put(which + ".t.q", lib.smel_packed_t_bytes(L.PACK_Q4, E, R, C, g))
+            put(which + ".t.sz", lib.smel_packed_t_bytes(L.PACK_SZ, E, R, C, g))
+        sel = [k for k in ("experts.sel.gate_up", "experts.sel.down") if k in P.meta]
+        if P.banks and len(sel) == 2 and P.sel_ids:
+            self.groups.append([P.meta[k][0:1] + (P.meta[k][3],) for k in sel])
+            self.after.append(("sel",))
+            banked.update(sel)
+            for k in sel:
+                n, R, C = P.meta[k][1]
+                put(k + ".f", lib.smel_packed_bytes(L.PACK_BF16, n * R, C))
+                put(k + ".t", lib.smel_packed_t_bytes(L.PACK_BF16, n, R, C, 0))
+        rest = sorted((off, nb) for k, (off, _, _, nb) in P.meta.items() if k not in banked and nb)
+        runs = []
+        for off, nb in rest:   # neighbours (up to alignment padding) go as one region
+            if runs and off - (runs[-1][0] + runs[-1][1]) < ALIGN:
+                runs[-1] = (runs[-1][0], off + nb - runs[-1][0])
+            else:
+                runs.append((off, nb))
+        if runs:
+            self.groups.append(runs)
+            self.after.append(None)
 
 
 class _Slot:
     def __init__(self, nbytes, device):
+        self.device = device
         self.arena = torch.empty(max(nbytes, ALIGN), dtype=torch.uint8, device=device)
+        self.pack = torch.empty(ALIGN, dtype=torch.uint8, device=device)   # the staged layer's packed layouts
         self.free = _Event()                 # recorded on the compute stream when the slot is given up
         self.free_used = False
-        self.done = [_Event() for _ in range(N_COPY_STREAMS)]
+        self.done = []                       # [copy group][copy stream] events, made as needed
         self.ready = _Event()
         self.layer = None
         self.LW = None
+
+    def group_events(self, n: int):
+        while len(self.done) < n:
+            self.done.append([_Event() for _ in range(N_COPY_STREAMS)])
+        return self.done[:n]
+
+    def pack_arena(self, nbytes: int) -> torch.Tensor:
+        """The pack arena, grown if a layer needs more (freed blocks are reused in the compute stream's order)."""
+        if self.pack.numel() < nbytes:
+            self.pack = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self.pack
 
 
 class _Event:
@@ -187,6 +266,7 @@ class _StagedSource:
         self.resident, self.max_on_gpu, self.group, self.act = resident, max(1, max_on_gpu), group, act
         self.slots = []                     # _Slot, in least-recently-used order at the front
         self.copy = [torch.cuda.Stream(self.device) for _ in range(N_COPY_STREAMS)]   # default priority
+        self.packer = torch.cuda.Stream(self.device)   # packs each copy group as soon as it has landed
         self.stats = {"load_s": 0.0, "wait_s": 0.0, "bytes": 0, "loads": 0}
         self.cache = {}                     # l -> LayerWeights staged (views into a slot)
         # (PinnedLayer, event after its stage): a host arena made for one upload stays referenced until its copies
@@ -223,8 +303,27 @@ class _StagedSource:
         s.layer, s.LW = None, None
         return s, False
 
+    def _fast_flags(self, P: PinnedLayer) -> dict:
+        """Whether each int4 bank of P admits the GEMMs' exact fast dequant form (smel_int4_fast_ok on its scale /
+        zero, uploaded for the check): decided once per pinned layer, before its first upload, with one host
+        synchronisation, so that the transposed layouts can be packed chunk by chunk as the copies land."""
+        if P.fast or not P.banks:
+            return P.fast
+        oks = {}
+        for which, (E, R, C, g) in P.banks.items():
+            name = _BANK_NAMES[which]
+            (so, _, _, nb), (zo, _, _, _) = P.meta[f"experts.{name}.scale"], P.meta[f"experts.{name}.zero"]
+            sz = torch.empty(2 * nb, dtype=torch.uint8, device=self.device)
+            sz[:nb].copy_(P.host[so:so + nb], non_blocking=True)
+            sz[nb:].copy_(P.host[zo:zo + nb], non_blocking=True)
+            oks[which] = torch.zeros(1, dtype=torch.int32, device=self.device)
+            L.call("smel_int4_fast_ok", L.ptr(sz), sz.data_ptr() + nb, nb // 2, L.ptr(oks[which]), L.stream())
+        P.fast = {k: bool(v.item()) for k, v in oks.items()}
+        return P.fast
+
     def prefetch(self, l):
-        """Stage layer l in a device slot (copies and packing on the copy streams; returns at once)."""
+        """Stage layer l in a device slot (copies on the copy streams, packing on the pack stream; returns at
+        once)."""
         if l in self.cache:
             return
         t0 = time.perf_counter()
@@ -232,23 +331,37 @@ class _StagedSource:
         s, hit = self._slot_for(l, P.nbytes)
         if hit:
             return
-        regions = (L.H2DRegion * 1)(L.H2DRegion(s.arena.data_ptr(), P.host.data_ptr(), P.nbytes))
+        fast = self._fast_flags(P)
+        plan = _UploadPlan(P)
+        pack = s.pack_arena(plan.pack_bytes)
         streams = (ctypes.c_void_p * N_COPY_STREAMS)(*[c.cuda_stream for c in self.copy])
-        done = (ctypes.c_void_p * N_COPY_STREAMS)(*[d.h for d in s.done])
-        # the copy streams start after work already enqueued on the current stream that may read the slot
-        L.call("smel_h2d_regions", regions, 1, CHUNK_BYTES, streams, done, N_COPY_STREAMS,
-               s.free.h if s.free_used else None)
+        events = s.group_events(len(plan.groups))
+        after = s.free.h if s.free_used else None   # queued kernels may still read the slot's previous layer
+        for regions, evs in zip(plan.groups, events):
+            arr = (L.H2DRegion * len(regions))(*[L.H2DRegion(s.arena.data_ptr() + off, P.host.data_ptr() + off, nb)
+                                                 for off, nb in regions])
+            done = (ctypes.c_void_p * N_COPY_STREAMS)(*[e.h for e in evs])
+            L.call("smel_h2d_regions", arr, len(regions), CHUNK_BYTES, streams, done, N_COPY_STREAMS, after)
+            after = None
         torch.autograd.graph.increment_version(s.arena)   # packed-layout caches keyed on the old bytes miss
         t = {k: s.arena[off:off + nb].view(dt).view(shape) for k, (off, shape, dt, nb) in P.meta.items()}
-        c0 = self.copy[0]
-        for d in s.done[1:]:
-            L.call("smel_stream_wait", c0.cuda_stream, d.h)
-        with torch.cuda.stream(c0):
+        pk = self.packer
+        if s.free_used:
+            L.call("smel_stream_wait", pk.cuda_stream, s.free.h)   # the pack arena is read by those kernels too
+        with torch.cuda.stream(pk):
             LW = build_layer(l, self._ltype(l), t, self._sel_ids(l, P), self.group, act=self.act)
-            self._pack(LW.experts, P)
-        L.call("smel_event_record", s.ready.h, c0.cuda_stream)
+            views = {k: pack[o:o + nb] for k, (o, nb) in plan.pack_at.items()}
+            for what, evs in zip(plan.after, events):
+                for e in evs:
+                    L.call("smel_stream_wait", pk.cuda_stream, e.h)
+                if what is not None and what[0] == "bank":
+                    self._pack_bank_chunk(P, s, views, fast, *what[1:])
+                elif what is not None:
+                    self._pack_selected(P, s, views)
+            self._attach(LW.experts, P, views, fast, plan)
+        L.call("smel_event_record", s.ready.h, pk.cuda_stream)
         staged = torch.cuda.Event()
-        staged.record(c0)                   # c0 has waited on every copy stream's part of this upload
+        staged.record(pk)                   # the pack stream has waited on every copy group of this upload
         self._in_flight = [(p, e) for p, e in self._in_flight if not e.query()] + [(P, staged)]
         s.layer, s.LW = l, LW
         self.cache[l] = LW
@@ -259,30 +372,56 @@ class _StagedSource:
         self.stats["loads"] += 1
 
     @staticmethod
-    def _pack(ex: LayerExperts, P: PinnedLayer):
-        """The GEMMs' packed layouts of the staged bank and selected experts, on the current (copy) stream."""
+    def _pack_bank_chunk(P: PinnedLayer, s: _Slot, views: dict, fast: dict, which: str, e0: int, e1: int):
+        """Experts [e0, e1) of an int4 bank into the forward and transposed layouts (smel_pack_int4 / _int4_t), on
+        the current (pack) stream."""
+        lib = L.load()
+        E, R, C, g = P.banks[which]
+        name, n = _BANK_NAMES[which], e1 - e0
+        q, sc, z = (P.meta[f"experts.{name}.{f}"] for f in ("q", "scale", "zero"))
+        src = [s.arena.data_ptr() + off + e0 * (nb // E) for off, _, _, nb in (q, sc, z)]
+        fq = views[which + ".f.q"].data_ptr() + lib.smel_packed_bytes(L.PACK_Q4, e0 * R, C)
+        fsz = views[which + ".f.sz"].data_ptr() + lib.smel_packed_bytes(L.PACK_SZ, e0 * R, C)
+        L.call("smel_pack_int4", *src, n * R, C, g, fq, fsz, L.stream())
+        tq = views[which + ".t.q"].data_ptr() + lib.smel_packed_t_bytes(L.PACK_Q4, e0, R, C, g)
+        tsz = views[which + ".t.sz"].data_ptr() + lib.smel_packed_t_bytes(L.PACK_SZ, e0, R, C, g)
+        L.call("smel_pack_int4_t", *src, n, R, C, g, int(fast[which]), tq, tsz, L.stream())
+
+    @staticmethod
+    def _pack_selected(P: PinnedLayer, s: _Slot, views: dict):
+        """The selected experts' bf16 gate_up / down into the forward and transposed layouts (smel_pack_bf16 /
+        _bf16_t), on the current (pack) stream."""
+        for k in ("experts.sel.gate_up", "experts.sel.down"):
+            off, (n, R, C), _, _ = P.meta[k]
+            w = s.arena.data_ptr() + off
+            L.call("smel_pack_bf16", w, n * R, C, C, views[k + ".f"].data_ptr(), L.stream())
+            L.call("smel_pack_bf16_t", w, n, R, C, C, views[k + ".t"].data_ptr(), L.stream())
+
+    @staticmethod
+    def _attach(ex: LayerExperts, P: PinnedLayer, views: dict, fast: dict, plan: _UploadPlan):
+        """Hand the packed layouts in the pack arena to the layer's expert objects (their caches), as the layouts
+        their own packing would have built."""
         fz = ex.frozen
-        if isinstance(fz, Int4Experts):
-            if P.fast:
-                fz._fast_dq = dict(P.fast)
-            for which in ("gu", "dn"):
-                P.fast[which] = fz.fast_dq(which)    # a host synchronisation only the first time
-                fz.packed(which)
-                fz.packed_t(which)
-        ex.packed_sel()
-        ex.packed_sel_t()
+        if isinstance(fz, Int4Experts) and P.banks:
+            fz._fast_dq = dict(fast)
+            fz._packed = {w: (views[w + ".f.q"], views[w + ".f.sz"].view(torch.int32)) for w in P.banks}
+            fz._packed_t = {w: (views[w + ".t.q"], views[w + ".t.sz"].view(torch.float32)) for w in P.banks}
+        if ("sel",) in plan.after and ex.sel_ids is not None and ex._slot:
+            mk = lambda k, sfx: PackedW(views[k + sfx].view(torch.bfloat16), P.meta[k][1][1], P.meta[k][1][2])
+            ex._packed_sel = (mk("experts.sel.gate_up", ".f"), mk("experts.sel.down", ".f"))
+            ex._packed_sel_t = (mk("experts.sel.gate_up", ".t"), mk("experts.sel.down", ".t"))
+        else:   # a bf16 bank, or selected experts outside the plan: their layouts are packed at first use
+            ex.packed_sel()
+            ex.packed_sel_t()
 
     @staticmethod
     def _stage_tensors(LW: LayerWeights):
-        """Every tensor of a staged layer; those made on the copy stream (packed layouts, stacked or selected
-        copies) must not be reused by the allocator before the compute stream is done with them."""
+        """Tensors of a staged layer that were allocated on the pack stream (stacked or selected copies, packs made
+        there); they must not be reused by the allocator before the compute stream is done with them. The slot
+        arenas are the compute stream's own."""
         ex = LW.experts
         out = [v for v in LW.W.values() if isinstance(v, torch.Tensor)]
         out += [v for v in (ex.sel_gate_up, ex.sel_down) if isinstance(v, torch.Tensor)]
-        fz = ex.frozen
-        for name in ("_packed", "_packed_t"):
-            for v in fz.__dict__.get(name, {}).values():
-                out += [x for x in v if isinstance(x, torch.Tensor)]
         for name in ("_packed_sel", "_packed_sel_t"):
             for p in ex.__dict__.get(name) or ():
                 out.append(p.t)
@@ -297,7 +436,7 @@ class _StagedSource:
         cur = L.stream()
         L.call("smel_stream_wait", cur, s.ready.h)
         cs = torch.cuda.current_stream(self.device)
-        for x in self._stage_tensors(s.LW):   # made on the copy stream, read on this one
+        for x in self._stage_tensors(s.LW):   # made on the pack stream, read on this one
             x.record_stream(cs)
         self.slots.remove(s)
         self.slots.append(s)

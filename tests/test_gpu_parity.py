@@ -640,10 +640,12 @@ def test_routed_experts_parity():
 
 
 def test_routed_experts_bad_ids():
-    """Expert ids outside [0, E) given to routed_experts: eager calls raise (the reference's bincount / indexing
-    fails there); under HIP-graph capture the dispatch drops those slots and the combine treats them as zero rows, so
-    the output equals the oracle's with those routing weights set to zero (no uninitialised rows are read)."""
-    from smel.moe import routed_experts
+    """Expert ids outside [0, E) given to routed_experts (the reference's bincount / indexing fails there): the call
+    itself does not synchronise; its dispatch drops those slots (zero rows: the output equals the oracle's with those
+    routing weights set to zero, no uninitialised rows are read) and the error is raised by check_routing_errors() or,
+    once the call's check has landed, by the next call. Under HIP-graph capture nothing is reported and the replays
+    drop the slots the same way."""
+    from smel.moe import check_routing_errors, routed_experts
     _say("routed_experts bad ids")
     x, ol = R.make_layer(T=96, H=128, E=8, I=64, K=2, n_sel=2, r=4, alpha=8.0, shared_inter=None, seed=8,
                          lora_b_std=0.05)
@@ -652,9 +654,25 @@ def test_routed_experts_bad_ids():
     bad = topi.clone()
     bad[3, 1], bad[40, 0], bad[77, 1] = 8, -1, 1000
     xd, tvd, bd = x.to(DEV), topv.float().to(DEV), bad.to(DEV)
+    keep = (bad >= 0) & (bad < 8)
+    tv0 = torch.where(keep, topv.float(), torch.zeros_like(topv.float()))
+    ids0 = torch.where(keep, bad, torch.zeros_like(bad))
+    yo = R.routed_experts(x.float(), tv0, ids0, ol, {n: ol.ex_lora[n].clone() for n in LORA_NAMES}, torch.float32)
+    with torch.no_grad():
+        for _ in range(4):   # calls back to back: the earlier checks may still be in flight when the next polls
+            routed_experts(xd, tvd, topi.to(DEV), ex, lora.experts)
+        check_routing_errors()
+        y_eager = routed_experts(xd, tvd, bd, ex, lora.experts)   # returns without waiting for the check
     with pytest.raises(IndexError):
+        check_routing_errors()
+    check_routing_errors()                                           # reported once
+    assert_close_bf16(y_eager.cpu(), yo, "y (eager, bad ids dropped)")
+    with torch.no_grad():
         routed_experts(xd, tvd, bd, ex, lora.experts)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()                                     # the check has landed: the next call raises
+        with pytest.raises(IndexError):
+            routed_experts(xd, tvd, topi.to(DEV), ex, lora.experts)
+    check_routing_errors()
     with torch.no_grad():
         routed_experts(xd, tvd, topi.to(DEV), ex, lora.experts)    # warm-up: packs and caches outside the capture
         torch.cuda.synchronize()
@@ -664,13 +682,9 @@ def test_routed_experts_bad_ids():
         for _ in range(2):
             g.replay()
             torch.cuda.synchronize()
-            keep = (bad >= 0) & (bad < 8)
-            tv0 = torch.where(keep, topv.float(), torch.zeros_like(topv.float()))
-            ids0 = torch.where(keep, bad, torch.zeros_like(bad))
-            leaves = {n: ol.ex_lora[n].clone() for n in LORA_NAMES}
-            yo = R.routed_experts(x.float(), tv0, ids0, ol, leaves, torch.float32)
             assert torch.isfinite(y.float()).all()
             assert_close_bf16(y.cpu(), yo, "y")
+    check_routing_errors()   # captured calls record nothing
 
 
 def test_route_api_backward():
