@@ -96,19 +96,28 @@ _PACK_CACHE: "OrderedDict" = OrderedDict()
 _PACK_CACHE_MAX = 32
 
 
-def _cached(kind: str, build, *mats: torch.Tensor):
+def _cached(kind: str, build, *mats: torch.Tensor, store: dict | None = None):
     """Packed form of per-call weights (shared expert, router, dense MLP) reused while the source tensors are
-    unchanged: keyed by storage address, version counter (bumped by any in-place write, views included), shape and
-    strides. The entry holds the sources, so their addresses cannot be reused while it lives."""
-    key = (kind,) + tuple((m.data_ptr(), m._version, tuple(m.shape), tuple(m.stride()), str(m.device)) for m in mats)
-    hit = _PACK_CACHE.get(key)
-    if hit is not None:
-        _PACK_CACHE.move_to_end(key)
-        return hit[1]
+    unchanged: keyed by storage address, shape and strides, valid while the version counters (bumped by any in-place
+    write, views included) are the ones it was built at. ``store``: the layer's own dict (LayerExperts), whose
+    entries live and die with the layer and are replaced when their sources change; without one, a process-wide LRU
+    of _PACK_CACHE_MAX entries. An entry holds its sources, so their addresses cannot be reused while it lives."""
+    key = (kind,) + tuple((m.data_ptr(), tuple(m.shape), tuple(m.stride()), str(m.device)) for m in mats)
+    ver = tuple(m._version for m in mats)
+    cache = _PACK_CACHE if store is None else store
+    hit = cache.get(key)
+    if hit is not None and hit[0] == ver:
+        if store is None:
+            _PACK_CACHE.move_to_end(key)
+        return hit[2]
     val = build()
-    _PACK_CACHE[key] = (mats, val)
-    while len(_PACK_CACHE) > _PACK_CACHE_MAX:
-        _PACK_CACHE.popitem(last=False)
+    if store is not None and hit is None and len(store) >= _PACK_CACHE_MAX:
+        store.clear()   # a layer called with ever new weight tensors keeps only the latest packs
+    cache[key] = (ver, mats, val)
+    if store is None:
+        _PACK_CACHE.move_to_end(key)
+        while len(_PACK_CACHE) > _PACK_CACHE_MAX:
+            _PACK_CACHE.popitem(last=False)
     return val
 
 
@@ -320,7 +329,7 @@ def _dense_tiles(T: int, device):
     return _dense_tiles_cache[key]
 
 
-def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> PackedW:
+def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None, store: dict | None = None) -> PackedW:
     """The weight of the router-backward GEMM (dx += dlogits . W): router rows, then the shared-gate row, as one
     [E(+1), H] matrix in the transposed layout, its contraction dim padded to a multiple of 64 (R of the result)."""
     E, H = gate_w.shape
@@ -337,7 +346,7 @@ def _router_ext_weight(gate_w: torch.Tensor, sg_w: torch.Tensor | None) -> Packe
         pw.R = Epad
         return pw
 
-    return _cached("router_t", build, *((gate_w,) if sg_w is None else (gate_w, sg_w)))
+    return _cached("router_t", build, *((gate_w,) if sg_w is None else (gate_w, sg_w)), store=store)
 
 
 _SIDE_STREAMS = {}
@@ -985,7 +994,7 @@ class _MoELayerFn(torch.autograd.Function):
                                 plan["lora_sh"] if fuse else None, plan["need_grad"], c, prep=(fork, bufs),
                                 shared_rows=shared_rows, counted_ws=dws)
         if plan["need_grad"]:
-            c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw))
+            c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw, plan["store"]))
             c.plan_lora_sh = plan["lora_sh"]
             ctx.c = c
         return out
@@ -1239,10 +1248,10 @@ def shared_mlp(x, W, lora):
     return y * torch.sigmoid(F.linear(x, W["mlp.shared_expert_gate.weight"]))
 
 
-def _shared_weights(W: dict):
+def _shared_weights(W: dict, store: dict | None = None):
     """(gate_up, down) of the shared expert packed, the shared-gate row, the shared intermediate size, and (gate_up,
     down) in the backward's transposed layout; None without a shared expert. Packs are reused while the dict's
-    tensors are unchanged."""
+    tensors are unchanged (kept in ``store``, the layer's own, when given)."""
     pre = "mlp.shared_expert."
     if pre + "gate_proj.weight" not in W and pre + "gate_up_proj.weight" not in W:
         return None
@@ -1250,14 +1259,14 @@ def _shared_weights(W: dict):
     dn = _bf16(W[pre + "down_proj.weight"])
     if gu is not None:
         gus = (_bf16(gu),)
-        pgu = _cached("f", lambda: pack_bf16(gus[0]), *gus)
-        pgu_t = _cached("t", lambda: pack_bf16_t(gus[0]), *gus)
+        pgu = _cached("f", lambda: pack_bf16(gus[0]), *gus, store=store)
+        pgu_t = _cached("t", lambda: pack_bf16_t(gus[0]), *gus, store=store)
     else:
         gus = (_bf16(W[pre + "gate_proj.weight"]), _bf16(W[pre + "up_proj.weight"]))
-        pgu = _cached("f", lambda: pack_bf16(*gus), *gus)
-        pgu_t = _cached("t", lambda: pack_bf16_t(torch.cat(gus)), *gus)
-    pdn = _cached("f", lambda: pack_bf16(dn), dn)
-    pdn_t = _cached("t", lambda: pack_bf16_t(dn), dn)
+        pgu = _cached("f", lambda: pack_bf16(*gus), *gus, store=store)
+        pgu_t = _cached("t", lambda: pack_bf16_t(torch.cat(gus)), *gus, store=store)
+    pdn = _cached("f", lambda: pack_bf16(dn), dn, store=store)
+    pdn_t = _cached("t", lambda: pack_bf16_t(dn), dn, store=store)
     return pgu, pdn, _bf16(W["mlp.shared_expert_gate.weight"].reshape(-1)), dn.shape[1], pgu_t, pdn_t
 
 
@@ -1269,12 +1278,13 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
     x = _bf16(x2d)
     lora_ex = lora_layer.experts if lora_layer is not None else None
     lora_sh = lora_layer.shared if lora_layer is not None else None
-    shared = _shared_weights(W)
+    store = ex.__dict__.setdefault("_dense_packs", {})   # the layer's shared-expert / router packs live with it
+    shared = _shared_weights(W, store)
     # a shared expert of the experts' intermediate size is fused into the expert GEMMs; another runs on its own
     split = shared is not None and shared[3] != _expert_I(ex)
     if lora_ex is not None and (ex.sel_ids is None or len(ex._slot) == 0):
         lora_ex = None
-    plan = {"ex": ex, "top_k": int(top_k), "gate_w": _bf16(W["mlp.gate.weight"]), "shared": shared,
+    plan = {"ex": ex, "top_k": int(top_k), "gate_w": _bf16(W["mlp.gate.weight"]), "shared": shared, "store": store,
             "split_shared": split, "lora_ex": lora_ex, "lora_sh": lora_sh if shared is not None else None}
     leaves = _lora_leaves(plan["lora_ex"]) + _lora_leaves(plan["lora_sh"])
     plan["need_grad"] = torch.is_grad_enabled() and (x2d.requires_grad or any(p.requires_grad for p in leaves))
