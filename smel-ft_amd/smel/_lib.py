@@ -1,4 +1,5 @@
-"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h, smel_norm.h, smel_stream.h and smel_loss.h).
+"""ctypes binding of libsmel_moe.so (the C-ABI declared in include/smel_moe.h, smel_f32.h, smel_norm.h, smel_stream.h and
+smel_loss.h).
 
 The library is the only compute path: if it is missing, or no GPU is visible, calls raise instead of falling back to
 anything else. Tensors go in as raw device pointers; every call runs on torch's current HIP stream.
@@ -20,7 +21,7 @@ WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
 WSET_MERGE_SHORT = 8 # smel_wset.flags: gate_up forward, a full int4 tile also takes the group's short last tile
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -29,6 +30,12 @@ class WSet(ctypes.Structure):
     """smel_wset of include/smel_moe.h."""
     _fields_ = [("q4", vp), ("sz4", vp), ("wb", vp), ("wsel", vp), ("wsh", vp), ("ext_sel", vp), ("ext_sh", vp),
                 ("R", i64), ("C", i64), ("group", i32), ("flags", i32)]
+
+
+class WSetF32(ctypes.Structure):
+    """smel_wset_f32 of include/smel_f32.h."""
+    _fields_ = [("q4", vp), ("scale", vp), ("zero", vp), ("wf", vp), ("wsel", vp), ("wsh", vp), ("R", i64), ("C", i64),
+                ("group", i32), ("kinds", i32), ("q4_round_bf16", i32), ("pad_", i32)]
 
 
 class WgDest(ctypes.Structure):
@@ -114,6 +121,21 @@ SIGNATURES = {
     "smel_lora_wgrad": (i32, [ctypes.POINTER(WgJob), i32, vp, i64, i64, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp,
                               i64, vp]),
     "smel_lora_wgrad_ws_floats": (i64, [ctypes.POINTER(WgJob), i32, i64, i64]),
+    # include/smel_f32.h
+    "smel_gmm_f32": (i32, [ctypes.POINTER(WSetF32), i32, vp, vp, vp, i64, vp, i64, f32, f32, vp, i64, vp]),
+    "smel_wgrad_f32": (i32, [vp, i64, vp, i64, vp, vp, i32, i64, i64, f32, vp, i64, vp]),
+    "smel_gather_rows_f32": (i32, [vp, i64, vp, i32, vp, i64, i64, vp, vp]),
+    "smel_act_gate_f32": (i32, [vp, i64, i64, i64, i32, vp, i64, vp]),
+    "smel_act_gate_bwd_f32": (i32, [vp, i64, vp, i64, i64, i64, i32, vp, i64, vp]),
+    "smel_combine_f32": (i32, [vp, vp, vp, i64, i64, i64, vp, vp]),
+    "smel_combine_bwd_f32": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp, vp]),
+    "smel_dx_reduce_f32": (i32, [vp, vp, i64, i64, i64, vp, vp]),
+    "smel_route_select_f32": (i32, [vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp]),
+    "smel_route_bwd_f32": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
+    "smel_route_prenorm_f32": (i32, [vp, vp, i64, i64, f32, f32, vp, vp, vp]),
+    "smel_route_prenorm_bwd_f32": (i32, [vp, vp, vp, vp, i64, i64, f32, vp, vp]),
+    "smel_gate_mul_f32": (i32, [vp, vp, vp, i64, i64, vp, vp]),
+    "smel_gate_mul_bwd_f32": (i32, [vp, vp, vp, i64, i64, vp, vp, vp]),
     # include/smel_norm.h
     "smel_rmsnorm_fwd": (i32, [vp, i64, i64, i64, vp, i32, f32, i32, vp, vp, vp]),
     "smel_rmsnorm_bwd": (i32, [vp, vp, i64, i64, i64, vp, i32, vp, vp, i32, vp, vp]),

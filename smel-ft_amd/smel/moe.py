@@ -26,6 +26,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib as L
+from . import moe_f32 as F32
 from .quant import dequant_int4, quantize_int4
 
 M_TILE = 128      # rows per GEMM tile (the tile list of smel_dispatch)
@@ -588,8 +589,11 @@ def _router_dx(dl: torch.Tensor, wr: PackedW, T: int, dx: torch.Tensor | None = 
 
 
 def route(x2d, gate_w, top_k):
-    """smel/moe.py:162-167 -> (probs fp32 [T,E], topv bf16 [T,K] renormalised, topi int64 [T,K])."""
+    """smel/moe.py:162-167 -> (probs fp32 [T,E], topv [T,K] renormalised in the logits' dtype, topi int64 [T,K]).
+    bf16 or fp32 activations (the fp32 path: every product an fp32 MFMA)."""
     L.require_device(x2d, gate_w)
+    if x2d.dtype == torch.float32:
+        return F32.RouteFn.apply(F32.f32(x2d), F32.f32(gate_w, "gate_w"), int(top_k))
     return _RouteFn.apply(_bf16(x2d), _bf16(gate_w), int(top_k))
 
 
@@ -640,6 +644,11 @@ def route_gemma4(h, W, top_k, eps):
     renormalised top-k x per_expert_scale, topi int64 [T,K]): weightless RMSNorm, x router.scale x H^-0.5, logits,
     softmax, top-k, renorm, scale, as HIP kernels (differentiable w.r.t. h)."""
     L.require_device(h)
+    if h.dtype == torch.float32:
+        return F32.RouteGemma4Fn.apply(F32.f32(h), F32.f32(W["router.scale"], "router.scale").reshape(-1),
+                                       F32.f32(W["router.proj.weight"], "router.proj.weight"),
+                                       F32.f32(W["router.per_expert_scale"], "router.per_expert_scale").reshape(-1),
+                                       int(top_k), float(eps))
     return _RouteGemma4Fn.apply(_bf16(h), _bf16(W["router.scale"]).reshape(-1), _bf16(W["router.proj.weight"]),
                                 _bf16(W["router.per_expert_scale"]).reshape(-1), int(top_k), float(eps))
 
@@ -1092,9 +1101,11 @@ def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
     """Weighted sum of the routed experts of every token (smel/moe.py:214-252). Expert ids outside [0, E) are reported
     by the next call or check_routing_errors(), without a host synchronisation here."""
     L.require_device(x2d, topv, topi)
-    _check_bank(ex)
     if not torch.cuda.is_current_stream_capturing():
         _ID_CHECK.poll()
+    if x2d.dtype == torch.float32:
+        return F32.RoutedFn.apply(F32.f32(x2d), topv, topi, ex, lora, _ID_CHECK.record, *_lora_leaves(lora))
+    _check_bank(ex)
     return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
 
 
@@ -1225,6 +1236,12 @@ def mlp_lora(x, w_gate, w_up, w_down, lora, act_name="silu", w_gate_up=None):
         raise ValueError(f"unknown activation {act_name}")
     L.require_device(x, w_down)
     xs = x.reshape(-1, x.shape[-1])
+    if x.dtype == torch.float32:
+        f = lambda t, n: None if t is None else F32.f32(t, n)
+        y = F32.MLPFn.apply(F32.f32(xs), f(w_gate if w_gate_up is None else None, "w_gate"),
+                            f(w_up if w_gate_up is None else None, "w_up"), f(w_down, "w_down"),
+                            f(w_gate_up, "w_gate_up"), lora, act_name, *_lora_leaves(lora))
+        return y.reshape(*x.shape[:-1], y.shape[-1])
     if w_gate_up is not None:
         gus = (_bf16(w_gate_up),)
         pgu = (_cached("f", lambda: pack_bf16(gus[0]), *gus), _cached("t", lambda: pack_bf16_t(gus[0]), *gus))
@@ -1243,8 +1260,10 @@ def shared_mlp(x, W, lora):
     """smel/moe.py:197-201: the shared expert times sigmoid(x w_sg^T). moe_forward fuses this into its grouped
     GEMMs; this stand-alone form multiplies the gate with torch ops."""
     pre = "mlp.shared_expert."
-    y = mlp_lora(x, W[pre + "gate_proj.weight"], W[pre + "up_proj.weight"], W[pre + "down_proj.weight"], lora,
+    y = mlp_lora(x, W.get(pre + "gate_proj.weight"), W.get(pre + "up_proj.weight"), W[pre + "down_proj.weight"], lora,
                  w_gate_up=W.get(pre + "gate_up_proj.weight"))
+    if x.dtype == torch.float32:   # the gate as an fp32 GEMM and a HIP kernel
+        return F32.GateAddFn.apply(y, F32.f32(x), F32.f32(W["mlp.shared_expert_gate.weight"], "shared gate"), None)
     return y * torch.sigmoid(F.linear(x, W["mlp.shared_expert_gate.weight"]))
 
 
@@ -1274,6 +1293,8 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
     """x2d [N, H] (already post-attention-normed) -> [N, H] bf16 (smel/moe.py:255-263): router, stats hook, routed
     experts and the shared expert, fused into one forward/backward pipeline."""
     L.require_device(x2d)
+    if x2d.dtype == torch.float32:
+        return _moe_forward_f32(x2d, W, ex, top_k, lora_layer, stats)
     _check_bank(ex)
     x = _bf16(x2d)
     lora_ex = lora_layer.experts if lora_layer is not None else None
@@ -1289,6 +1310,23 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
     leaves = _lora_leaves(plan["lora_ex"]) + _lora_leaves(plan["lora_sh"])
     plan["need_grad"] = torch.is_grad_enabled() and (x2d.requires_grad or any(p.requires_grad for p in leaves))
     return _MoELayerFn.apply(x, plan, stats, *leaves)
+
+
+def _moe_forward_f32(x2d, W, ex: LayerExperts, top_k: int, lora_layer, stats):
+    """moe_forward on fp32 activations, composed as the reference composes it (smel/moe.py:255-263): route, the stats
+    hook, routed_experts, and the shared expert times its gate added to the routed output (one kernel)."""
+    probs, topv, topi = route(x2d, W["mlp.gate.weight"], top_k)
+    if stats is not None:
+        stats(probs, topv, topi)
+    lora_ex = lora_layer.experts if lora_layer is not None else None
+    lora_sh = lora_layer.shared if lora_layer is not None else None
+    routed = routed_experts(x2d, topv, topi, ex, lora_ex)
+    pre = "mlp.shared_expert."
+    if pre + "down_proj.weight" not in W:
+        return routed
+    y = mlp_lora(x2d, W.get(pre + "gate_proj.weight"), W.get(pre + "up_proj.weight"), W[pre + "down_proj.weight"],
+                 lora_sh, w_gate_up=W.get(pre + "gate_up_proj.weight"))
+    return F32.GateAddFn.apply(y, F32.f32(x2d), F32.f32(W["mlp.shared_expert_gate.weight"], "shared gate"), routed)
 
 
 def _count_tiles(counts: list, device):
@@ -1327,6 +1365,14 @@ class FrozenExpertsFn(torch.autograd.Function):
         if act_name not in _ACT:
             raise ValueError(f"unknown activation {act_name}")
         L.require_device(xs)
+        ctx.plan = ctx.plan_f32 = None
+        if xs.dtype == torch.float32:
+            counts = [int(c) for c in counts]
+            if len(counts) != bank.num_experts or sum(counts) != xs.shape[0] or min(counts, default=0) < 0:
+                raise ValueError(f"FrozenExpertsFn: counts (sum {sum(counts)}, {len(counts)} experts) do not match "
+                                 f"xs rows {xs.shape[0]} / bank experts {bank.num_experts}")
+            out, ctx.plan_f32 = F32.frozen_fwd(F32.f32(xs), counts, bank, act_name)
+            return out
         _check_bank(bank)
         xs = _bf16(xs)
         counts = [int(c) for c in counts]
@@ -1356,6 +1402,9 @@ class FrozenExpertsFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy):
+        if ctx.plan_f32 is not None:
+            keep, ctx.plan_f32 = ctx.plan_f32, None
+            return F32.frozen_bwd(keep, dy), None, None, None, None
         if ctx.plan is None:
             return torch.zeros_like(dy), None, None, None, None
         bank, tiles, ntiles, maxt, gk, hsave, actb, act_name = ctx.plan

@@ -34,12 +34,14 @@ def assert_close_bf16(out, ref, name="", rel=2e-2, cos=0.9999):
     return e, m, c
 
 
-def to_device_layer(ol: R.OracleLayer, device):
-    """The oracle's layer as the drop-in API's objects on ``device``: (W dict, LayerExperts, LayerLoRA or None)."""
+def to_device_layer(ol: R.OracleLayer, device, dtype=torch.bfloat16):
+    """The oracle's layer as the drop-in API's objects on ``device``: (W dict, LayerExperts, LayerLoRA or None), the
+    floating weights in ``dtype`` (bf16, or fp32 for the fp32 path, whose int4 bank then keeps the oracle's
+    dequant dtype as Int4Experts.dtype)."""
     from smel.lora import ExpertsLoRA, LayerLoRA, MLPLoRA
     from smel.moe import BF16Experts, Int4Experts, LayerExperts
 
-    bf = lambda t: t.to(device=device, dtype=torch.bfloat16).contiguous()
+    bf = lambda t: t.to(device=device, dtype=dtype).contiguous()
     W = {"mlp.gate.weight": bf(ol.gate_w)}
     if ol.shared is not None:
         Is = ol.shared["down"].shape[1]
@@ -49,7 +51,8 @@ def to_device_layer(ol: R.OracleLayer, device):
         W["mlp.shared_expert_gate.weight"] = bf(ol.shared["gate_w"])
     if ol.int4:
         dev = lambda d: {k: v.to(device).contiguous() for k, v in d.items()}
-        bank = Int4Experts(dev(ol.frozen["gate_up"]), dev(ol.frozen["down"]))
+        bank = Int4Experts(dev(ol.frozen["gate_up"]), dev(ol.frozen["down"]),
+                           dtype=ol.deq_dtype if dtype == torch.float32 else torch.bfloat16)
     else:
         bank = BF16Experts(bf(ol.frozen["gate_up"]), bf(ol.frozen["down"]))
     if ol.sel_ids:

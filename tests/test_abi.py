@@ -41,6 +41,7 @@ PROBE = r"""
 #include <stddef.h>
 #include <stdio.h>
 #include "smel_moe.h"
+#include "smel_f32.h"
 #define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
 int main() {
   printf("smel_wset %zu\nsmel_wg_dest %zu\nsmel_wg_job %zu\nsmel_lora_set %zu\n", sizeof(smel_wset),
@@ -52,6 +53,9 @@ int main() {
   F(smel_fwd_lora_rows, scale_sh) F(smel_fwd_lora_rows, part) F(smel_fwd_lora_rows, parts) F(smel_fwd_lora_rows, ext_out)
   F(smel_bwd_lora_rows, scale_sh) F(smel_bwd_lora_rows, n_sel) F(smel_bwd_lora_rows, planes) F(smel_bwd_lora_rows, part)
   F(smel_bwd_lora_rows, parts)
+  printf("smel_wset_f32 %zu\n", sizeof(smel_wset_f32));
+  F(smel_wset_f32, wsh) F(smel_wset_f32, R) F(smel_wset_f32, C) F(smel_wset_f32, group) F(smel_wset_f32, kinds)
+  F(smel_wset_f32, q4_round_bf16)
   return 0;
 }
 """
@@ -74,7 +78,7 @@ def test_struct_layouts_match_header(tmp_path):
                                                        text=True).stdout.splitlines())
     mirror = {"smel_wset": _lib.WSet, "smel_wg_dest": _lib.WgDest, "smel_wg_job": _lib.WgJob,
               "smel_lora_set": _lib.LoraSet, "smel_fwd_lora_rows": _lib.FwdLoraRows,
-              "smel_bwd_lora_rows": _lib.BwdLoraRows}
+              "smel_bwd_lora_rows": _lib.BwdLoraRows, "smel_wset_f32": _lib.WSetF32}
     for key, val in got.items():
         if "." in key:
             t, f = key.split(".")
@@ -156,6 +160,35 @@ def test_host_side_rejections():
     w.R, w.C = 1024, 2048
     assert L.smel_gmm_fwd_lr(ctypes.byref(w), None, 16, 16, 1, 16, 2048, 4, 0, None, 0, 1, None, 1, 0, 16, 512, None,
                              ctypes.byref(fl), None) == -1   # 3 partials for the gate_up forward's 4 column blocks
+
+
+def test_f32_host_side_rejections():
+    """The fp32 path's entry points check their arguments on the host before any launch."""
+    from smel import _lib
+    L = _lib.load()
+    w = _lib.WSetF32()
+    w.R, w.C, w.kinds = 64, 128, 1 << _lib.KIND_SHARED
+    ok = (ctypes.byref(w), 0, None, 16, 16, 1, 16, 128, 1.0, 0.0, 16, 64, None)
+    assert L.smel_gmm_f32(*ok) == -1 and b"shared" in L.smel_last_error()        # no shared weights
+    w.wsh = 16
+    assert L.smel_gmm_f32(ctypes.byref(w), 0, None, 16, 16, 1, 16, 128, 1.0, 0.5, 16, 64, None) == -1   # beta
+    assert L.smel_gmm_f32(ctypes.byref(w), 2, None, 16, 16, 1, 16, 128, 1.0, 0.0, 16, 64, None) == -1   # trans
+    assert L.smel_gmm_f32(ctypes.byref(w), 0, None, 16, 16, 1, 16, 64, 1.0, 0.0, 16, 64, None) == -1    # lda < K
+    assert L.smel_gmm_f32(ctypes.byref(w), 1, None, 16, 16, 1, 16, 64, 1.0, 0.0, 16, 64, None) == -1    # ldc < N
+    w.kinds = 1 << _lib.KIND_INT4
+    assert L.smel_gmm_f32(ctypes.byref(w), 0, None, 16, 16, 1, 16, 128, 1.0, 0.0, 16, 64, None) == -1   # no q4
+    w.q4 = w.scale = w.zero = 16
+    w.group = 48                                                                                        # !| C
+    assert L.smel_gmm_f32(ctypes.byref(w), 0, None, 16, 16, 1, 16, 128, 1.0, 0.0, 16, 64, None) == -1
+    w.kinds = 1 << 5
+    assert L.smel_gmm_f32(ctypes.byref(w), 0, None, 16, 16, 1, 16, 128, 1.0, 0.0, 16, 64, None) == -1   # kinds
+    assert L.smel_wgrad_f32(16, 8, 16, 64, 16, 16, 1, 16, 64, 1.0, 16, 1024, None) == -1   # ldx < M
+    assert L.smel_wgrad_f32(16, 16, 16, 64, 16, 16, 1, 16, 64, 1.0, 16, 512, None) == -1   # c_stride < M N
+    assert L.smel_route_select_f32(16, 600, 4, 600, 8, None, 16, 16, 16, 16, None) == -2
+    assert L.smel_route_select_f32(16, 64, 4, 64, 17, None, 16, 16, 16, 16, None) == -2
+    assert L.smel_act_gate_f32(16, 64, 4, 64, 2, 16, 64, None) == -1                       # act id
+    assert L.smel_act_gate_f32(16, 100, 4, 64, 0, 16, 64, None) == -1                      # ldh < 2I
+    assert L.smel_combine_f32(16, 16, 16, 4, 65, 64, 16, None) == -1                       # K > 64
 
 
 def test_product_path_does_not_reach_the_oracle():
