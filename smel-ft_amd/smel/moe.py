@@ -535,6 +535,65 @@ def _check_bank(ex):
             _bf16(t)
 
 
+# ------------------------------------------------------------------------------------------------ shapes beyond the bf16 kernels
+
+
+def _bf16_limit(H: int, ex=None, loras=(), mlp_I: int | None = None) -> str | None:
+    """Why bf16 activations of these shapes cannot run on the bf16 kernels, or None: those take a hidden size that is
+    a multiple of 64, intermediate sizes that are multiples of 32, int4 groups that are multiples of 32 and LoRA
+    ranks up to 32. Such calls run on the fp32 kernels instead (bf16 in and out; every weight value the same, the
+    int4 dequant rounded to bf16 as here), which the reference's shapes never need (its defaults are inside)."""
+    if H % 64:
+        return f"hidden {H} is not a multiple of 64"
+    if ex is not None:
+        fz = ex.frozen if isinstance(ex, LayerExperts) else ex
+        I = (fz.dn["q"].shape[2] * 2) if isinstance(fz, Int4Experts) else fz.down.shape[2]
+        if I % 32:
+            return f"expert intermediate size {I} is not a multiple of 32"
+        if isinstance(fz, Int4Experts) and any(Int4Experts.group_of(d) % 32 for d in (fz.gu, fz.dn)):
+            return "int4 group not a multiple of 32"
+    if mlp_I is not None and mlp_I % 32:
+        return f"MLP intermediate size {mlp_I} is not a multiple of 32"
+    r = max((m.r for m in loras if m is not None), default=0)
+    if r > MAX_LORA_RANK:
+        return f"LoRA rank {r} is above {MAX_LORA_RANK}"
+    return None
+
+
+def _f32_of(t: torch.Tensor, store: dict | None = None) -> torch.Tensor:
+    """fp32 copy of a weight, reused while the source is unchanged (in ``store``, the layer's own, when given)."""
+    return _cached("f32", lambda: t.float().contiguous(), t, store=store)
+
+
+def _f32_W(W: dict, store: dict) -> dict:
+    return {k: _f32_of(v, store) if torch.is_tensor(v) and v.is_floating_point() else v for k, v in W.items()}
+
+
+def _f32_bank(fz, store: dict | None = None):
+    """The frozen bank for the fp32 kernels: an int4 bank as is, dequantized and rounded to bf16 inside the GEMM (the
+    values the bf16 kernels use); a bf16 bank as fp32 copies."""
+    if isinstance(fz, Int4Experts):
+        return _cached("f32_int4", lambda: Int4Experts(fz.gu, fz.dn, dtype=torch.bfloat16), fz.gu["q"], fz.dn["q"],
+                       store=store)
+    return _cached("f32_bank", lambda: BF16Experts(fz.gate_up.float().contiguous(), fz.down.float().contiguous()),
+                   fz.gate_up, fz.down, store=store)
+
+
+def _f32_experts(ex: LayerExperts, store: dict) -> LayerExperts:
+    """The layer's experts for the fp32 kernels (selected experts as fp32 copies), kept in ``store``."""
+    bank = _f32_bank(ex.frozen, store)
+    if ex.sel_ids is None or not ex._slot:
+        return _cached("f32_ex", lambda: LayerExperts(bank, group=ex.group, act=ex.act), *_bank_sources(ex.frozen),
+                       store=store)
+    return _cached("f32_ex", lambda: LayerExperts(bank, ex.sel_ids, ex.sel_gate_up.float().contiguous(),
+                                                  ex.sel_down.float().contiguous(), ex.group, ex.act),
+                   *_bank_sources(ex.frozen), ex.sel_gate_up, ex.sel_down, store=store)
+
+
+def _bank_sources(fz):
+    return (fz.gu["q"], fz.dn["q"]) if isinstance(fz, Int4Experts) else (fz.gate_up, fz.down)
+
+
 # ------------------------------------------------------------------------------------------------ router
 
 
@@ -594,6 +653,9 @@ def route(x2d, gate_w, top_k):
     L.require_device(x2d, gate_w)
     if x2d.dtype == torch.float32:
         return F32.RouteFn.apply(F32.f32(x2d), F32.f32(gate_w, "gate_w"), int(top_k))
+    if _bf16_limit(x2d.shape[-1]) is not None:
+        probs, topv, topi = F32.RouteFn.apply(x2d.float(), _f32_of(_bf16(gate_w)), int(top_k))
+        return probs, topv.to(x2d.dtype), topi
     return _RouteFn.apply(_bf16(x2d), _bf16(gate_w), int(top_k))
 
 
@@ -644,6 +706,10 @@ def route_gemma4(h, W, top_k, eps):
     renormalised top-k x per_expert_scale, topi int64 [T,K]): weightless RMSNorm, x router.scale x H^-0.5, logits,
     softmax, top-k, renorm, scale, as HIP kernels (differentiable w.r.t. h)."""
     L.require_device(h)
+    if h.dtype == torch.bfloat16 and _bf16_limit(h.shape[-1]) is not None:
+        return F32.RouteGemma4Fn.apply(h.float(), _f32_of(_bf16(W["router.scale"])).reshape(-1),
+                                       _f32_of(_bf16(W["router.proj.weight"])),
+                                       _f32_of(_bf16(W["router.per_expert_scale"])).reshape(-1), int(top_k), float(eps))
     if h.dtype == torch.float32:
         return F32.RouteGemma4Fn.apply(F32.f32(h), F32.f32(W["router.scale"], "router.scale").reshape(-1),
                                        F32.f32(W["router.proj.weight"], "router.proj.weight"),
@@ -1106,6 +1172,10 @@ def routed_experts(x2d, topv, topi, ex: LayerExperts, lora=None):
     if x2d.dtype == torch.float32:
         return F32.RoutedFn.apply(F32.f32(x2d), topv, topi, ex, lora, _ID_CHECK.record, *_lora_leaves(lora))
     _check_bank(ex)
+    if _bf16_limit(x2d.shape[-1], ex, (lora,)) is not None:
+        ex32 = _f32_experts(ex, ex.__dict__.setdefault("_dense_packs", {}))
+        out = F32.RoutedFn.apply(_bf16(x2d).float(), topv, topi, ex32, lora, _ID_CHECK.record, *_lora_leaves(lora))
+        return out.to(x2d.dtype)
     return _RoutedFn.apply(_bf16(x2d), topv, topi, ex, lora, *_lora_leaves(lora))
 
 
@@ -1236,12 +1306,16 @@ def mlp_lora(x, w_gate, w_up, w_down, lora, act_name="silu", w_gate_up=None):
         raise ValueError(f"unknown activation {act_name}")
     L.require_device(x, w_down)
     xs = x.reshape(-1, x.shape[-1])
+    to32 = None
     if x.dtype == torch.float32:
-        f = lambda t, n: None if t is None else F32.f32(t, n)
-        y = F32.MLPFn.apply(F32.f32(xs), f(w_gate if w_gate_up is None else None, "w_gate"),
-                            f(w_up if w_gate_up is None else None, "w_up"), f(w_down, "w_down"),
-                            f(w_gate_up, "w_gate_up"), lora, act_name, *_lora_leaves(lora))
-        return y.reshape(*x.shape[:-1], y.shape[-1])
+        to32 = lambda t, n: None if t is None else F32.f32(t, n)
+    elif _bf16_limit(x.shape[-1], None, (lora,), w_down.shape[1]) is not None:
+        to32 = lambda t, n: None if t is None else _f32_of(_bf16(t))
+    if to32 is not None:
+        y = F32.MLPFn.apply(xs.float(), to32(w_gate if w_gate_up is None else None, "w_gate"),
+                            to32(w_up if w_gate_up is None else None, "w_up"), to32(w_down, "w_down"),
+                            to32(w_gate_up, "w_gate_up"), lora, act_name, *_lora_leaves(lora))
+        return y.reshape(*x.shape[:-1], y.shape[-1]).to(x.dtype)
     if w_gate_up is not None:
         gus = (_bf16(w_gate_up),)
         pgu = (_cached("f", lambda: pack_bf16(gus[0]), *gus), _cached("t", lambda: pack_bf16_t(gus[0]), *gus))
@@ -1297,6 +1371,13 @@ def moe_forward(x2d, W, ex: LayerExperts, top_k: int, lora_layer=None, stats=Non
         return _moe_forward_f32(x2d, W, ex, top_k, lora_layer, stats)
     _check_bank(ex)
     x = _bf16(x2d)
+    sh_dn = W.get("mlp.shared_expert.down_proj.weight")
+    loras = (lora_layer.experts, lora_layer.shared) if lora_layer is not None else ()
+    if _bf16_limit(x.shape[-1], ex, loras, None if sh_dn is None else sh_dn.shape[1]) is not None:
+        store = ex.__dict__.setdefault("_dense_packs", {})
+        st = None if stats is None else (lambda p, v, i: stats(p, v.to(x.dtype), i))
+        return _moe_forward_f32(x.float(), _f32_W(W, store), _f32_experts(ex, store), top_k, lora_layer,
+                                st).to(x.dtype)
     lora_ex = lora_layer.experts if lora_layer is not None else None
     lora_sh = lora_layer.shared if lora_layer is not None else None
     store = ex.__dict__.setdefault("_dense_packs", {})   # the layer's shared-expert / router packs live with it
@@ -1366,13 +1447,18 @@ class FrozenExpertsFn(torch.autograd.Function):
             raise ValueError(f"unknown activation {act_name}")
         L.require_device(xs)
         ctx.plan = ctx.plan_f32 = None
-        if xs.dtype == torch.float32:
+        ctx.dtype = xs.dtype
+        if xs.dtype == torch.float32 or _bf16_limit(xs.shape[-1], bank) is not None:
             counts = [int(c) for c in counts]
             if len(counts) != bank.num_experts or sum(counts) != xs.shape[0] or min(counts, default=0) < 0:
                 raise ValueError(f"FrozenExpertsFn: counts (sum {sum(counts)}, {len(counts)} experts) do not match "
                                  f"xs rows {xs.shape[0]} / bank experts {bank.num_experts}")
-            out, ctx.plan_f32 = F32.frozen_fwd(F32.f32(xs), counts, bank, act_name)
-            return out
+            if xs.dtype == torch.float32:
+                out, ctx.plan_f32 = F32.frozen_fwd(F32.f32(xs), counts, bank, act_name)
+                return out
+            bank32 = _f32_bank(bank, bank.__dict__.setdefault("_f32_store", {}))
+            out, ctx.plan_f32 = F32.frozen_fwd(_bf16(xs).float(), counts, bank32, act_name)
+            return out.to(xs.dtype)
         _check_bank(bank)
         xs = _bf16(xs)
         counts = [int(c) for c in counts]
@@ -1404,7 +1490,7 @@ class FrozenExpertsFn(torch.autograd.Function):
     def backward(ctx, dy):
         if ctx.plan_f32 is not None:
             keep, ctx.plan_f32 = ctx.plan_f32, None
-            return F32.frozen_bwd(keep, dy), None, None, None, None
+            return F32.frozen_bwd(keep, dy.float()).to(ctx.dtype), None, None, None, None
         if ctx.plan is None:
             return torch.zeros_like(dy), None, None, None, None
         bank, tiles, ntiles, maxt, gk, hsave, actb, act_name = ctx.plan

@@ -336,3 +336,67 @@ def test_routed_experts_f32_bad_ids_reported():
     with pytest.raises(IndexError):
         check_routing_errors()
     check_routing_errors()   # reported once
+
+
+# ------------------------------------------------------------------------------------------------ bf16 beyond the bf16 kernels
+
+
+@pytest.mark.parametrize("case", ["rank48", "hidden200_group8", "inter100"])
+def test_bf16_layer_outside_bf16_kernel_limits(case):
+    """bf16 activations of shapes the bf16 kernels do not take (LoRA rank above 32, a hidden size that is not a
+    multiple of 64 with int4 groups of 8, an expert / shared intermediate size that is not a multiple of 32) run on
+    the fp32 kernels with bf16 in and out: y, dX and every LoRA gradient against the fp32 oracle at the bf16 bar
+    (the reference takes these shapes; its bf16 tests compare at 2e-2)."""
+    from helpers import assert_close_bf16
+    from smel.moe import moe_forward
+    _say(f"bf16 layer beyond the bf16 kernels: {case}")
+    H, I, group, r = {"rank48": (256, 128, 64, 48), "hidden200_group8": (200, 96, 8, 8),
+                      "inter100": (256, 100, 4, 16)}[case]
+    x, ol = R.make_layer(320, H, 16, I, 4, n_sel=3, r=r, shared_inter=I, group=group, seed=11, lora_b_std=0.05)
+    W, ex, lora = to_device_layer(ol, DEV)
+    gy = torch.randn(x.shape, generator=torch.Generator().manual_seed(2)).bfloat16()
+    xd = x.to(DEV).requires_grad_(True)
+    seen = {}
+    y = moe_forward(xd, W, ex, 4, lora, stats=lambda p, v, i: seen.update(v=v, i=i.clone()))
+    assert y.dtype == torch.bfloat16 and seen["v"].dtype == torch.bfloat16
+    y.backward(gy.to(DEV))
+    torch.cuda.synchronize()
+    y32, dx32, g32 = R.moe_forward_backward(x.float(), ol, 4, gy.float(), forced_topi=seen["i"].cpu(),
+                                            dtype=torch.float32)
+    e, m, c = assert_close_bf16(y.detach().float().cpu(), y32, "y")
+    _say(f"  y: rel {e:.2e} cos {c:.7f}")
+    e, m, c = assert_close_bf16(xd.grad.float().cpu(), dx32, "dx")
+    _say(f"  dx: rel {e:.2e} cos {c:.7f}")
+    for tag, mod in (("ex", lora.experts), ("sh", lora.shared)):
+        for n in LORA_NAMES:
+            e, m, c = assert_close_bf16(getattr(mod, n).grad.float().cpu(), g32[f"{tag}_{n}"], f"d_{tag}_{n}")
+            _say(f"  d_{tag}_{n}: rel {e:.2e}")
+
+
+def test_bf16_frozen_experts_and_route_hidden_200():
+    """FrozenExpertsFn and route() on bf16 rows whose hidden size (200) the bf16 kernels do not take: the fp32 kernels
+    with bf16 in and out, against the fp32 oracle at the bf16 bar; the router's ids equal the oracle's on the same
+    logits' ordering (no near-ties here)."""
+    from helpers import assert_close_bf16
+    from smel.moe import FrozenExpertsFn, route
+    _say("bf16 FrozenExpertsFn / route, hidden 200")
+    x, ol = R.make_layer(256, 200, 6, 96, 2, n_sel=0, group=8, seed=4)
+    W, ex, _ = to_device_layer(ol, DEV)
+    counts = [9, 0, 12, 7, 15, 7]
+    xs = x[:sum(counts)].bfloat16()
+    gy = torch.randn(xs.shape, generator=torch.Generator().manual_seed(3)).bfloat16()
+    xd = xs.to(DEV).requires_grad_(True)
+    out = FrozenExpertsFn.apply(xd, counts, ex.frozen, 32, "silu")
+    assert out.dtype == torch.bfloat16
+    out.backward(gy.to(DEV))
+    x32 = xs.float().requires_grad_(True)
+    ref = R._FrozenExperts.apply(x32, counts, ol, torch.float32)
+    ref.backward(gy.float())
+    assert_close_bf16(out.detach().float().cpu(), ref.detach(), "out")
+    assert_close_bf16(xd.grad.float().cpu(), x32.grad, "dx")
+    xr = x.bfloat16().to(DEV)
+    probs, topv, topi = route(xr, W["mlp.gate.weight"], 2)
+    assert topv.dtype == torch.bfloat16
+    p32, _, i32 = R.route(x.bfloat16().float(), ol.gate_w.float(), 2)
+    assert torch.equal(topi.cpu(), i32)
+    assert_close_bf16(probs.cpu(), p32, "probs", rel=1e-5)
