@@ -24,6 +24,8 @@ Other workloads of BASELINE.json (``--workload``), each printing one JSON line o
   norms  the RMSNorm family around the block (include/smel_norm.h), forward + backward at the Qwen3.6 block's
       shapes for T=4092: input norm and residual add + post-attention norm [T, 2048], q / k head norms
       [T, 16 | 2, 256] (q a strided half of q_proj's output), the gated DeltaNet output norm [T * 32, 128];
+  c3f32  the C3 layer with float32 activations and weights (the reference's fp32 models) on the fp32 kernels
+      (include/smel_f32.h), eager fwd+bwd, roofline against the dense fp32 MFMA peak;
   peaks  the achievable MFMA rate and HBM bandwidth of this GPU by kernels that do nothing else
       (include/smel_probe.h), and hipBLASLt's bf16 GEMM for comparison.
 
@@ -433,6 +435,57 @@ def run_qwen(args, dev, mode):
         cpu = cpu_baseline(x, W, ex, lora, gy, cfg, fwd_only)
     emit(METRIC if mode == "c3" else QWEN_METRICS[mode], T * nmb, args, timing, QWEN_NAMES[mode],
          {"selected_slots": S, "micro_batches": nmb}, roof, bd, cpu, **extra)
+
+
+F32_MFMA_PEAK = 157.3e12    # FLOP/s, MI355X dense fp32 MFMA
+
+
+def run_c3f32(args, dev):
+    """c3f32: the C3 layer (same shapes, routing, selected experts and LoRA) with float32 activations and float32
+    floating weights, the int4 bank of dtype fp32 (the reference's fp32 models: Int4Experts.from_bf16 of fp32
+    weights), fwd+bwd on the fp32 kernels of include/smel_f32.h; eager launches. Roofline of the longest routed-expert
+    GEMM against the dense fp32 MFMA peak."""
+    from smel.moe import Int4Experts, LayerExperts, moe_forward
+    cfg = dict(QWEN)
+    log("building the c3 layer in fp32 (int4 quantization on the GPU) ...")
+    x, W, ex, lora, gy = build_qwen_layer(dev, cfg)
+    W32 = {k: v.float().contiguous() for k, v in W.items()}
+    ex32 = LayerExperts(Int4Experts(ex.frozen.gu, ex.frozen.dn, dtype=torch.float32), ex.sel_ids,
+                        ex.sel_gate_up.float(), ex.sel_down.float(), group=32, act=cfg["act"])
+    xg = x.float().requires_grad_(True)
+    gy32 = gy.float()
+    params = list(lora.parameters())
+    seen = []
+
+    def step(stats=None):
+        for p in params:
+            p.grad = None
+        xg.grad = None
+        moe_forward(xg, W32, ex32, cfg["K"], lora, stats=stats).backward(gy32)
+
+    step(stats=lambda p, v, i: seen.append(i))
+    sel = torch.zeros(cfg["E"], dtype=torch.bool, device=dev)
+    sel[ex.sel_ids.to(dev)] = True
+    S = int(sel[seen[0]].sum())
+    timing = time_step(step, args.steps, args.warmup, False)
+    bd = breakdown_of(step, max(3, min(10, args.steps)))
+    log("per-launch ms:", json.dumps(bd))
+    T, H, I, K = cfg["T"], cfg["H"], cfg["I"], cfg["K"]
+    TK = T * K
+    flops = {"gemm_f32_ex_gu": 2 * TK * H * 2 * I, "gemm_f32_ex_dn": 2 * TK * I * H,
+             "gemm_f32_ex_dn_bwd": 2 * TK * H * I, "gemm_f32_ex_gu_bwd": 2 * TK * 2 * I * H}
+    dom = max(flops, key=lambda k: bd.get(k, 0.0))
+    ach = flops[dom] / (bd[dom] * 1e-3)
+    roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach / 1e12, 2), "peak": F32_MFMA_PEAK / 1e12,
+            "unit": "TFLOP/s", "frac": round(ach / F32_MFMA_PEAK, 4), "traffic": None, "flops_per_launch": flops[dom],
+            "avg_launch_ms": bd[dom]}
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (the oracle, fp32: 1 warmup + median of 5 full passes) ...")
+        cpu = cpu_baseline(x, W, ex, lora, gy, cfg)
+    emit("MoE layer fwd+bwd tokens/s with fp32 activations (Qwen3.6 shape, T=4092)", T, args, timing,
+         "C3 in fp32: the C3 layer with float32 activations and weights, int4 bank dequantized to fp32, fp32 MFMA",
+         {"selected_slots": S}, roof, bd, cpu, dtype="f32")
 
 
 def run_gemma(args, dev):
@@ -900,7 +953,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "norms", "stream", "quant", "ce", "peaks"),
+    ap.add_argument("--workload", choices=("c3", "c2", "c4", "c5", "c3f32", "norms", "stream", "quant", "ce", "peaks"),
                     default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph replay)")
@@ -930,6 +983,8 @@ def main():
         run_ce(args, dev)
     elif args.workload == "peaks":
         run_peaks(args, dev)
+    elif args.workload == "c3f32":
+        run_c3f32(args, dev)
     else:
         run_qwen(args, dev, args.workload)
 

@@ -31,30 +31,63 @@ SMEL_DEV void mma_step(const float* __restrict__ As, const float* __restrict__ B
 // ---------------------------------------------------------------------------------------------- weight matrices
 
 // One matrix [R][C] of a weight set: fp32 values, or the reference's int4 format dequantized as w = q s + z in fp32
-// (q s is exact in fp32, so this equals the separate product and sum), optionally rounded to bf16.
+// (q s is exact in fp32, so this equals the separate product and sum), optionally rounded to bf16. Offsets inside a
+// matrix are 32-bit (one matrix is below 2^31 elements); the group index is a shift when the group is a power of two.
 struct WMat {
   const float* f;
   const uint8_t* q;
   const uint16_t* s;
   const uint16_t* z;
-  int64_t R, C;
+  int C;
+  int gpr;      // groups per row, C / group
   int group;
+  int gshift;   // log2(group), or -1
   int rbf;
 };
 
-SMEL_DEV float w_at(const WMat& m, int64_t row, int64_t col) {
-  if (m.f) return m.f[row * m.C + col];
-  const uint32_t b = m.q[row * (m.C >> 1) + (col >> 1)];
-  const float qv = (float)((b >> (4 * (int)(col & 1))) & 0xfu);
-  const int64_t gi = row * (m.C / m.group) + col / m.group;
-  const float v = fmaf(qv, bf2f(m.s[gi]), bf2f(m.z[gi]));
+SMEL_DEV int gidx(const WMat& m, int row, int col) {
+  return row * m.gpr + (m.gshift >= 0 ? col >> m.gshift : col / m.group);
+}
+
+SMEL_DEV float dq(const WMat& m, uint32_t q, int gi) {
+  const float v = fmaf((float)q, bf2f(m.s[gi]), bf2f(m.z[gi]));
   return m.rbf ? bf2f(f2bf(v)) : v;
 }
 
+SMEL_DEV float w_at(const WMat& m, int row, int col) {
+  if (m.f) return m.f[row * m.C + col];
+  const uint32_t b = m.q[row * (m.C >> 1) + (col >> 1)];
+  return dq(m, (b >> (4 * (col & 1))) & 0xfu, gidx(m, row, col));
+}
+
+// Elements [row][col .. col + 3] (col a multiple of 4, col + 3 < C, C a multiple of 4): one 16-byte load for fp32,
+// one 16-bit load of nibbles for int4 (one scale / zero pair when the group is a multiple of 4).
+SMEL_DEV void w_quad(const WMat& m, int row, int col, float v[4]) {
+  if (m.f) {
+    const float4 x = *reinterpret_cast<const float4*>(m.f + row * m.C + col);
+    v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+    return;
+  }
+  const uint32_t qq = *reinterpret_cast<const uint16_t*>(m.q + row * (m.C >> 1) + (col >> 1));
+  if ((m.group & 3) == 0) {
+    const int gi = gidx(m, row, col);
+    const float sc = bf2f(m.s[gi]), ze = bf2f(m.z[gi]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = fmaf((float)((qq >> (4 * i)) & 0xfu), sc, ze);
+      v[i] = m.rbf ? bf2f(f2bf(x)) : x;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = dq(m, (qq >> (4 * i)) & 0xfu, gidx(m, row, col + i));
+  }
+}
+
 SMEL_DEV bool resolve(const smel_wset_f32& w, int kind, int idx, WMat& m) {
-  m.R = w.R;
-  m.C = w.C;
-  m.group = w.group;
+  m.C = (int)w.C;
+  m.group = w.group > 0 ? w.group : 1;
+  m.gpr = (int)(w.C / m.group);
+  m.gshift = (m.group & (m.group - 1)) == 0 ? __builtin_ctz((unsigned)m.group) : -1;
   m.rbf = w.q4_round_bf16;
   m.f = nullptr;
   m.q = nullptr;
@@ -64,8 +97,8 @@ SMEL_DEV bool resolve(const smel_wset_f32& w, int kind, int idx, WMat& m) {
     case SMEL_KIND_INT4:
       if (!w.q4) return false;
       m.q = w.q4 + (int64_t)idx * (n >> 1);
-      m.s = w.scale + (int64_t)idx * w.R * (w.C / w.group);
-      m.z = w.zero + (int64_t)idx * w.R * (w.C / w.group);
+      m.s = w.scale + (int64_t)idx * w.R * m.gpr;
+      m.z = w.zero + (int64_t)idx * w.R * m.gpr;
       return true;
     case SMEL_KIND_BF16: m.f = w.wf ? w.wf + (int64_t)idx * n : nullptr; break;
     case SMEL_KIND_SEL: m.f = w.wsel ? w.wsel + (int64_t)idx * n : nullptr; break;
@@ -104,6 +137,7 @@ __global__ __launch_bounds__(256) void gmm_f32_kernel(smel_wset_f32 w, const int
   // column quad t % 16
   const int am = t >> 2, akq = 4 * (t & 3);
   const int bk1 = t >> 4, bn1 = 4 * (t & 15);
+  const bool qvec = (w.C & 3) == 0 && (m.f ? VEC : true);
   for (int mr0 = r0; mr0 < r1; mr0 += FB) {
     const int mr1 = min(r1, mr0 + FB);
     float ra[4], rb[4];
@@ -116,20 +150,20 @@ __global__ __launch_bounds__(256) void gmm_f32_kernel(smel_wset_f32 w, const int
 #pragma unroll
         for (int i = 0; i < 4; ++i) ra[i] = (row < mr1 && k + i < K) ? A[row * lda + k + i] : 0.f;
       }
+      // weights: whole quads through w_quad when the matrix's rows are multiples of 4 (and, for fp32, its base
+      // 16-byte aligned: VEC), the guarded element path otherwise
       if (TRANS == 0) {   // W [N][K]: row n0 + t / 4, k quad
-        const int64_t n = n0 + am;
-        if (VEC && m.f && n < N && k + 3 < K) {
-          const float4 v = *reinterpret_cast<const float4*>(m.f + n * m.C + k);
-          rb[0] = v.x, rb[1] = v.y, rb[2] = v.z, rb[3] = v.w;
+        const int n = (int)(n0 + am), kq = (int)k;
+        if (qvec && n < N && kq + 3 < K) {
+          w_quad(m, n, kq, rb);
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) rb[i] = (n < N && k + i < K) ? w_at(m, n, k + i) : 0.f;
+          for (int i = 0; i < 4; ++i) rb[i] = (n < N && kq + i < K) ? w_at(m, n, kq + i) : 0.f;
         }
       } else {            // W [K][N]: row k0 + t / 16, column quad
-        const int64_t kk = k0 + bk1, n = n0 + bn1;
-        if (VEC && m.f && kk < K && n + 3 < N) {
-          const float4 v = *reinterpret_cast<const float4*>(m.f + kk * m.C + n);
-          rb[0] = v.x, rb[1] = v.y, rb[2] = v.z, rb[3] = v.w;
+        const int kk = (int)(k0 + bk1), n = (int)(n0 + bn1);
+        if (qvec && kk < K && n + 3 < N) {
+          w_quad(m, kk, n, rb);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) rb[i] = (kk < K && n + i < N) ? w_at(m, kk, n + i) : 0.f;
@@ -541,6 +575,7 @@ extern "C" int smel_gmm_f32(const smel_wset_f32* w, int32_t trans, const int32_t
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && max_tiles < (1 << 30), SMEL_EINVAL,
                "smel_gmm_f32: bad sizes R=%lld C=%lld max_tiles=%lld", (long long)w->R, (long long)w->C,
                (long long)max_tiles);
+  SMEL_REQUIRE(w->R * w->C < (1LL << 31), SMEL_EUNSUPPORTED, "smel_gmm_f32: one weight matrix of 2^31 elements or more");
   const int64_t N = trans ? w->C : w->R, K = trans ? w->R : w->C;
   SMEL_REQUIRE(lda >= K && ldc >= N, SMEL_EINVAL, "smel_gmm_f32: lda %lld < K %lld or ldc %lld < N %lld",
                (long long)lda, (long long)K, (long long)ldc, (long long)N);

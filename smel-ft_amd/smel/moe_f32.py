@@ -144,47 +144,48 @@ class _Saved:
     __slots__ = ("x", "h", "a", "xa_g", "xa_u", "xa_d")
 
 
-def mlp_core_fwd(x, tl, I: int, w_gu, w_dn, gu_split, lora_w, s: float, lora_w_sel: bool, act: int, need: bool):
+def mlp_core_fwd(x, tl, I: int, w_gu, w_dn, gu_split, lora_w, s: float, lora_w_sel: bool, act: int, need: bool,
+                 tag: str = "f32"):
     """The gated MLP over the rows of the tile list: h = [g | u] = x W_gu^T (+ s (x A_g^T) B_g^T, + s (x A_u^T) B_u^T),
     a = act(g) u, y = a W_dn^T (+ s (a A_d^T) B_d^T). ``w_gu`` is one weight set of 2I rows, or None with
     ``gu_split`` = (gate, up) weight sets of I rows each. ``lora_w`` = dict of fp32 factors (stacked per slot when
-    ``lora_w_sel``) or None. Returns (y, saved)."""
+    ``lora_w_sel``) or None. ``tag`` names the launches for timing. Returns (y, saved)."""
     M, H = x.shape
     dev = x.device
     e = lambda *sh: torch.empty(*sh, dtype=torch.float32, device=dev)
     h = e(M, 2 * I)
     if w_gu is not None:
-        gmm(w_gu, 0, tl, x, H, h, 2 * I, tag="gemm_f32_gu")
+        gmm(w_gu, 0, tl, x, H, h, 2 * I, tag=f"gemm_{tag}_gu")
     else:
-        gmm(gu_split[0], 0, tl, x, H, h, 2 * I, tag="gemm_f32_gu")
-        gmm(gu_split[1], 0, tl, x, H, h[:, I:], 2 * I, tag="gemm_f32_gu")
+        gmm(gu_split[0], 0, tl, x, H, h, 2 * I, tag=f"gemm_{tag}_gu")
+        gmm(gu_split[1], 0, tl, x, H, h[:, I:], 2 * I, tag=f"gemm_{tag}_gu")
     sv = _Saved()
     sv.xa_g = sv.xa_u = sv.xa_d = None
     wl = _sel if lora_w_sel else (lambda t: _dense(t))
     if lora_w is not None:
         r = lora_w["A_gate"].shape[-2]
         sv.xa_g, sv.xa_u = e(M, r), e(M, r)
-        gmm(wl(lora_w["A_gate"]), 0, tl, x, H, sv.xa_g, r, tag="lora_f32")
-        gmm(wl(lora_w["A_up"]), 0, tl, x, H, sv.xa_u, r, tag="lora_f32")
-        gmm(wl(lora_w["B_gate"]), 0, tl, sv.xa_g, r, h, 2 * I, alpha=s, beta=1.0, tag="lora_f32")
-        gmm(wl(lora_w["B_up"]), 0, tl, sv.xa_u, r, h[:, I:], 2 * I, alpha=s, beta=1.0, tag="lora_f32")
+        gmm(wl(lora_w["A_gate"]), 0, tl, x, H, sv.xa_g, r, tag=f"lora_{tag}")
+        gmm(wl(lora_w["A_up"]), 0, tl, x, H, sv.xa_u, r, tag=f"lora_{tag}")
+        gmm(wl(lora_w["B_gate"]), 0, tl, sv.xa_g, r, h, 2 * I, alpha=s, beta=1.0, tag=f"lora_{tag}")
+        gmm(wl(lora_w["B_up"]), 0, tl, sv.xa_u, r, h[:, I:], 2 * I, alpha=s, beta=1.0, tag=f"lora_{tag}")
     a = e(M, I)
-    L.call("smel_act_gate_f32", L.ptr(h), 2 * I, M, I, act, L.ptr(a), I, L.stream(), tag="act_f32")
+    L.call("smel_act_gate_f32", L.ptr(h), 2 * I, M, I, act, L.ptr(a), I, L.stream(), tag=f"act_{tag}")
     Hout = w_dn.R
     y = e(M, Hout)
-    gmm(w_dn, 0, tl, a, I, y, Hout, tag="gemm_f32_dn")
+    gmm(w_dn, 0, tl, a, I, y, Hout, tag=f"gemm_{tag}_dn")
     if lora_w is not None:
         r = lora_w["A_down"].shape[-2]
         sv.xa_d = e(M, r)
-        gmm(wl(lora_w["A_down"]), 0, tl, a, I, sv.xa_d, r, tag="lora_f32")
-        gmm(wl(lora_w["B_down"]), 0, tl, sv.xa_d, r, y, Hout, alpha=s, beta=1.0, tag="lora_f32")
+        gmm(wl(lora_w["A_down"]), 0, tl, a, I, sv.xa_d, r, tag=f"lora_{tag}")
+        gmm(wl(lora_w["B_down"]), 0, tl, sv.xa_d, r, y, Hout, alpha=s, beta=1.0, tag=f"lora_{tag}")
     if need:
         sv.x, sv.h, sv.a = x, h, a
     return y, sv
 
 
 def mlp_core_bwd(sv: _Saved, dy, tl, I: int, w_gu, w_dn, gu_split, lora_w, s: float, lora_w_sel: bool, act: int,
-                 offsets, jobs, n_jobs: int, want_grads: bool):
+                 offsets, jobs, n_jobs: int, want_grads: bool, tag: str = "f32"):
     """Backward of mlp_core_fwd: dx over the tile rows, and the LoRA factor gradients (fp32, stacked per job) when
     ``want_grads``: job j's rows are those of group jobs[j] (offsets)."""
     M, Hout = dy.shape
@@ -194,42 +195,42 @@ def mlp_core_bwd(sv: _Saved, dy, tl, I: int, w_gu, w_dn, gu_split, lora_w, s: fl
     wl = _sel if lora_w_sel else (lambda t: _dense(t))
     grads = {}
     da = e(M, I)
-    gmm(w_dn, 1, tl, dy, Hout, da, I, tag="gemm_f32_dn_bwd")
+    gmm(w_dn, 1, tl, dy, Hout, da, I, tag=f"gemm_{tag}_dn_bwd")
     if lora_w is not None:
         r = lora_w["A_down"].shape[-2]
         dz = e(M, r)
-        gmm(wl(lora_w["B_down"]), 1, tl, dy, Hout, dz, r, alpha=s, tag="lora_f32")
-        gmm(wl(lora_w["A_down"]), 1, tl, dz, r, da, I, beta=1.0, tag="lora_f32")
+        gmm(wl(lora_w["B_down"]), 1, tl, dy, Hout, dz, r, alpha=s, tag=f"lora_{tag}")
+        gmm(wl(lora_w["A_down"]), 1, tl, dz, r, da, I, beta=1.0, tag=f"lora_{tag}")
         if want_grads:
             grads["B_down"] = e(n_jobs, Hout, r)
             grads["A_down"] = e(n_jobs, r, I)
-            wgrad(dy, Hout, sv.xa_d, r, offsets, jobs, n_jobs, Hout, r, s, grads["B_down"])
-            wgrad(dz, r, sv.a, I, offsets, jobs, n_jobs, r, I, 1.0, grads["A_down"])
+            wgrad(dy, Hout, sv.xa_d, r, offsets, jobs, n_jobs, Hout, r, s, grads["B_down"], tag=f"wgrad_{tag}")
+            wgrad(dz, r, sv.a, I, offsets, jobs, n_jobs, r, I, 1.0, grads["A_down"], tag=f"wgrad_{tag}")
     dh = e(M, 2 * I)
     L.call("smel_act_gate_bwd_f32", L.ptr(sv.h), 2 * I, L.ptr(da), I, M, I, act, L.ptr(dh), 2 * I, L.stream(),
-           tag="act_f32")
+           tag=f"act_{tag}")
     dx = e(M, H)
     if w_gu is not None:
-        gmm(w_gu, 1, tl, dh, 2 * I, dx, H, tag="gemm_f32_gu_bwd")
+        gmm(w_gu, 1, tl, dh, 2 * I, dx, H, tag=f"gemm_{tag}_gu_bwd")
     else:
-        gmm(gu_split[0], 1, tl, dh, 2 * I, dx, H, tag="gemm_f32_gu_bwd")
-        gmm(gu_split[1], 1, tl, dh[:, I:], 2 * I, dx, H, beta=1.0, tag="gemm_f32_gu_bwd")
+        gmm(gu_split[0], 1, tl, dh, 2 * I, dx, H, tag=f"gemm_{tag}_gu_bwd")
+        gmm(gu_split[1], 1, tl, dh[:, I:], 2 * I, dx, H, beta=1.0, tag=f"gemm_{tag}_gu_bwd")
     if lora_w is not None:
         r = lora_w["A_gate"].shape[-2]
         dzg, dzu = e(M, r), e(M, r)
-        gmm(wl(lora_w["B_gate"]), 1, tl, dh, 2 * I, dzg, r, alpha=s, tag="lora_f32")
-        gmm(wl(lora_w["B_up"]), 1, tl, dh[:, I:], 2 * I, dzu, r, alpha=s, tag="lora_f32")
-        gmm(wl(lora_w["A_gate"]), 1, tl, dzg, r, dx, H, beta=1.0, tag="lora_f32")
-        gmm(wl(lora_w["A_up"]), 1, tl, dzu, r, dx, H, beta=1.0, tag="lora_f32")
+        gmm(wl(lora_w["B_gate"]), 1, tl, dh, 2 * I, dzg, r, alpha=s, tag=f"lora_{tag}")
+        gmm(wl(lora_w["B_up"]), 1, tl, dh[:, I:], 2 * I, dzu, r, alpha=s, tag=f"lora_{tag}")
+        gmm(wl(lora_w["A_gate"]), 1, tl, dzg, r, dx, H, beta=1.0, tag=f"lora_{tag}")
+        gmm(wl(lora_w["A_up"]), 1, tl, dzu, r, dx, H, beta=1.0, tag=f"lora_{tag}")
         if want_grads:
             for n in ("B_gate", "B_up"):
                 grads[n] = e(n_jobs, I, r)
             for n in ("A_gate", "A_up"):
                 grads[n] = e(n_jobs, r, H)
-            wgrad(dh, 2 * I, sv.xa_g, r, offsets, jobs, n_jobs, I, r, s, grads["B_gate"])
-            wgrad(dh[:, I:], 2 * I, sv.xa_u, r, offsets, jobs, n_jobs, I, r, s, grads["B_up"])
-            wgrad(dzg, r, sv.x, H, offsets, jobs, n_jobs, r, H, 1.0, grads["A_gate"])
-            wgrad(dzu, r, sv.x, H, offsets, jobs, n_jobs, r, H, 1.0, grads["A_up"])
+            wgrad(dh, 2 * I, sv.xa_g, r, offsets, jobs, n_jobs, I, r, s, grads["B_gate"], tag=f"wgrad_{tag}")
+            wgrad(dh[:, I:], 2 * I, sv.xa_u, r, offsets, jobs, n_jobs, I, r, s, grads["B_up"], tag=f"wgrad_{tag}")
+            wgrad(dzg, r, sv.x, H, offsets, jobs, n_jobs, r, H, 1.0, grads["A_gate"], tag=f"wgrad_{tag}")
+            wgrad(dzu, r, sv.x, H, offsets, jobs, n_jobs, r, H, 1.0, grads["A_up"], tag=f"wgrad_{tag}")
     return dx, grads
 
 
@@ -366,7 +367,7 @@ class RoutedFn(torch.autograd.Function):
         I = w_dn.C
         lw, s = _lora_f32(lora) if (lora is not None and has_sel) else (None, 0.0)
         need = any(ctx.needs_input_grad[i] for i in (0, 1)) or any(ctx.needs_input_grad[6:])
-        ys, sv = mlp_core_fwd(xs, tl, I, w_gu, w_dn, None, lw, s, True, _act_id(ex.act), need)
+        ys, sv = mlp_core_fwd(xs, tl, I, w_gu, w_dn, None, lw, s, True, _act_id(ex.act), need, tag="f32_ex")
         tv = topv.detach().float().contiguous()
         out = torch.empty(T, H, dtype=torch.float32, device=dev)
         L.call("smel_combine_f32", L.ptr(ys), L.ptr(tv), L.ptr(inv), T, K, H, L.ptr(out), st, tag="combine_f32")
@@ -394,7 +395,7 @@ class RoutedFn(torch.autograd.Function):
             jobs = ex.sel_ids.to(device=dev, dtype=torch.int32)
             n_jobs = int(jobs.numel())
         dxs, grads = mlp_core_bwd(sv, dys, tl, I, w_gu, w_dn, None, lw, s, True, _act_id(ex.act), offsets, jobs, n_jobs,
-                                  lw is not None)
+                                  lw is not None, tag="f32_ex")
         dx = torch.empty(T, H, dtype=torch.float32, device=dev)
         L.call("smel_dx_reduce_f32", L.ptr(dxs), L.ptr(inv), T, K, H, L.ptr(dx), L.stream(), tag="dx_reduce_f32")
         g = _grad_like(lora, grads) if lw is not None else ([None] * 6 if lora is not None else [])
@@ -422,7 +423,7 @@ class MLPFn(torch.autograd.Function):
         w_dn = _dense(w_down)
         lw, s = _lora_f32(lora) if lora is not None else (None, 0.0)
         need = ctx.needs_input_grad[0] or any(ctx.needs_input_grad[7:])
-        y, sv = mlp_core_fwd(x, tl, I, w_gu, w_dn, split, lw, s, False, _act_id(act_name), need)
+        y, sv = mlp_core_fwd(x, tl, I, w_gu, w_dn, split, lw, s, False, _act_id(act_name), need, tag="f32_mlp")
         ctx.keep = (sv, tl, offs, jobs, I, w_gu, w_dn, split, lw, s, lora, act_name,
                     (w_gate, w_up, w_down, w_gate_up)) if need else None
         return y
@@ -433,7 +434,7 @@ class MLPFn(torch.autograd.Function):
         ctx.keep = None
         dy = f32(dy, "the output gradient")
         dx, grads = mlp_core_bwd(sv, dy, tl, I, w_gu, w_dn, split, lw, s, False, _act_id(act_name), offs, jobs, 1,
-                                 lw is not None)
+                                 lw is not None, tag="f32_mlp")
         g = []
         if lora is not None:
             g = [grads[n].reshape(getattr(lora, n).shape).to(getattr(lora, n).dtype)
@@ -485,7 +486,7 @@ def frozen_fwd(xs, counts: list, bank, act_name: str):
     tl, _ = count_tiles(counts, kind, xs.device)
     w_gu, w_dn = bank_wset(bank, "gu"), bank_wset(bank, "dn")
     I = w_dn.C
-    y, sv = mlp_core_fwd(xs, tl, I, w_gu, w_dn, None, None, 0.0, False, _act_id(act_name), True)
+    y, sv = mlp_core_fwd(xs, tl, I, w_gu, w_dn, None, None, 0.0, False, _act_id(act_name), True, tag="f32_frozen")
     return y, (sv, tl, w_gu, w_dn, I, act_name, bank)
 
 
@@ -493,5 +494,5 @@ def frozen_bwd(keep, dy):
     """FrozenExpertsFn.backward (smel/moe.py:128-143) on fp32: dX of the rows (no weight gradients)."""
     sv, tl, w_gu, w_dn, I, act_name, _bank = keep
     dx, _ = mlp_core_bwd(sv, f32(dy, "the output gradient"), tl, I, w_gu, w_dn, None, None, 0.0, False,
-                         _act_id(act_name), None, None, 0, False)
+                         _act_id(act_name), None, None, 0, False, tag="f32_frozen")
     return dx
