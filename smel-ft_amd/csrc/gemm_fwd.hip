@@ -279,9 +279,16 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       for (int f = 0; f < VM_SZ; ++f) z[f] = ld4(rsz, in ? sof[f] + (j >> 2) * 1024 + 4 * (j & 3) : OOB);
     };
     const uint32_t magic = FAST ? f16_magic() : 0u;
+    // The A fragment of slice m + 1 (or of the next substep's slice 0) is read from LDS before slice m's two MFMAs
+    // run, so each read has a pair of MFMAs to land instead of being waited for at once; the fences keep the
+    // scheduler from sinking the reads back to their uses.
+    auto rd = [&](const uint16_t* S, int s, int m) {
+      return *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 32 * KT);
+    };
     auto compute = [&](const uint16_t* S, const u32x4_t* q, const uint32_t* z) {
       const float s0 = bf_lo(z[0]), z0v = bf_hi(z[0]), s1 = bf_lo(z[1]), z1v = bf_hi(z[1]);
       const FastSZ f0 = fast_sz(s0, z0v), f1 = fast_sz(s1, z1v);
+      u32x4_t a_cur = rd(S, 0, 0);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         uint32_t o0[4], o1[4];
@@ -292,7 +299,18 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
           dq8(q[0][s], s0, z0v, o0);
           dq8(q[1][s], s1, z1v, o1);
         }
-        mma(S, s, u32x4_t{o0[0], o0[1], o0[2], o0[3]}, u32x4_t{o1[0], o1[1], o1[2], o1[3]});
+        const u32x4_t b0 = u32x4_t{o0[0], o0[1], o0[2], o0[3]}, b1 = u32x4_t{o1[0], o1[1], o1[2], o1[3]};
+#pragma unroll
+        for (int m = 0; m < NS; ++m) {
+          u32x4_t a_nxt = a_cur;
+          if (m + 1 < NS) a_nxt = rd(S, s, m + 1);
+          else if (s + 1 < 4) a_nxt = rd(S, s + 1, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          acc[m][0] = mfma32(a_cur, b0, acc[m][0]);
+          acc[m][1] = mfma32(a_cur, b1, acc[m][1]);
+          __builtin_amdgcn_sched_barrier(0);
+          a_cur = a_nxt;
+        }
       }
     };
     issue_a(0, S0);
