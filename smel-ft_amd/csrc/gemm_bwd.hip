@@ -328,9 +328,27 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
           b[s][2 + fr] = ld16(rw1, in ? wo + j * 4096 + (2 * fr + s) * 1024 : OOB);
         }
     };
+    // The step's 2 NRF A-fragment reads in (substep, fragment) order through a ring of three registers, two reads
+    // ahead of the MFMAs that use them (the weights sit in registers already); the fences keep the scheduler from
+    // sinking the reads back to their uses.
     auto compute = [&](int st, u32x4_t (*b)[4]) {
+      const uint16_t* S = St(st);
+      constexpr int NR = 2 * NRF;
+      auto rd = [&](int r) {
+        return *reinterpret_cast<const u32x4_t*>(S + ard[r / NRF] + (r % NRF) * 16 * KT);
+      };
+      u32x4_t ar[3];
+      ar[0] = rd(0);
+      ar[1] = rd(1);
 #pragma unroll
-      for (int s = 0; s < 2; ++s) mma(St(st), s, b[s]);
+      for (int r = 0; r < NR; ++r) {
+        const int s = r / NRF, m = r % NRF;
+        if (r + 2 < NR) ar[(r + 2) % 3] = rd(r + 2);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) acc[m][f] = mfma16(ar[r % 3], b[s][f], acc[m][f]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
     issue_lds(0, 0, nullptr);
     issue_lds(1, 1, nullptr);

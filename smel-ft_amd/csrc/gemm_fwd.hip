@@ -192,6 +192,10 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 #pragma unroll
   for (int m = 0; m < NS; ++m) acc[m][0] = acc[m][1] = f32x16_t{};
 
+  // A fragment of slice m, substep s from a stage
+  auto rd = [&](const uint16_t* S, int s, int m) {
+    return *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 32 * KT);
+  };
   auto mma = [&](const uint16_t* S, int s, const u32x4_t& b0, const u32x4_t& b1) {
 #pragma unroll
     for (int m = 0; m < NS; ++m) {
@@ -282,9 +286,6 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     // The A fragment of slice m + 1 (or of the next substep's slice 0) is read from LDS before slice m's two MFMAs
     // run, so each read has a pair of MFMAs to land instead of being waited for at once; the fences keep the
     // scheduler from sinking the reads back to their uses.
-    auto rd = [&](const uint16_t* S, int s, int m) {
-      return *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 32 * KT);
-    };
     auto compute = [&](const uint16_t* S, const u32x4_t* q, const uint32_t* z) {
       const float s0 = bf_lo(z[0]), z0v = bf_hi(z[0]), s1 = bf_lo(z[1]), z1v = bf_hi(z[1]);
       const FastSZ f0 = fast_sz(s0, z0v), f1 = fast_sz(s1, z1v);
@@ -354,9 +355,23 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
         b[1][s] = ld16(rw, in ? wo1 + j * 4096 + s * 1024 : OOB);
       }
     };
+    // The step's 4 NS A-fragment reads in (substep, slice) order through a ring of three registers, two reads ahead of
+    // the MFMA pair that uses them (the weights sit in registers already, so nothing else delays the MFMAs); the
+    // fences keep the scheduler from sinking the reads back to their uses.
     auto compute = [&](const uint16_t* S, u32x4_t (*b)[4]) {
+      constexpr int NR = 4 * NS;
+      u32x4_t ar[3];
+      ar[0] = rd(S, 0, 0);
+      if (NR > 1) ar[1] = rd(S, 1 / NS, 1 % NS);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) mma(S, s, b[0][s], b[1][s]);
+      for (int r = 0; r < NR; ++r) {
+        const int s = r / NS, m = r % NS;
+        if (r + 2 < NR) ar[(r + 2) % 3] = rd(S, (r + 2) / NS, (r + 2) % NS);
+        __builtin_amdgcn_sched_barrier(0);
+        acc[m][0] = mfma32(ar[r % 3], b[0][s], acc[m][0]);
+        acc[m][1] = mfma32(ar[r % 3], b[1][s], acc[m][1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
     issue_a(0, S0);
     issue_a(1, S1);
