@@ -242,36 +242,47 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
         }
       };
       constexpr int H1 = (NRF + 1) / 2, HA = (H1 + 1) / 2;   // first-half row fragments, in two MFMA groups
+      constexpr int H2 = NRF - H1;                            // second-half row fragments
+      auto rda = [&](int s, int m) { return *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT); };
+      // A fragments: the first half's and the second half's in separate registers, each read about two column
+      // fragments of MFMAs before its first use (the second half during the first half's MFMAs, the next substep's
+      // first half during the second half's), so no MFMA group waits for its LDS reads
+      u32x4_t af1[H1], af2[H2 > 0 ? H2 : 1];
       unpack(Z);
       dqh(0, 0, 0);
       dqh(0, 0, 1);
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        u32x4_t af[H1];
+      for (int m = 0; m < H1; ++m) af1[m] = rda(0, m);
 #pragma unroll
-        for (int m = 0; m < H1; ++m) af[m] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
+      for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int f = 0; f < 4; ++f) {
           if (SZ2 && f == 1) unpack(Z + 128 + 16 * s);   // fragments 2, 3 are the wave's second scale/zero group
 #pragma unroll
-          for (int m = 0; m < HA; ++m) acc[m][f] = mfma16(af[m], b[f], acc[m][f]);
+          for (int m = 0; m < HA; ++m) acc[m][f] = mfma16(af1[m], b[f], acc[m][f]);
           if (f < 3) dqh(s, f + 1, 0);
+          if (f == 1) {
+#pragma unroll
+            for (int m = 0; m < H2; ++m) af2[m] = rda(s, H1 + m);
+          }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int m = HA; m < H1; ++m) acc[m][f] = mfma16(af[m], b[f], acc[m][f]);
+          for (int m = HA; m < H1; ++m) acc[m][f] = mfma16(af1[m], b[f], acc[m][f]);
           if (f < 3) dqh(s, f + 1, 1);
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int m = H1; m < NRF; ++m) af[m - H1] = *reinterpret_cast<const u32x4_t*>(S + ard[s] + m * 16 * KT);
-#pragma unroll
         for (int f = 0; f < 4; ++f) {
 #pragma unroll
-          for (int m = H1; m < NRF; ++m) acc[m][f] = mfma16(af[m - H1], b[f], acc[m][f]);
+          for (int m = 0; m < H2; ++m) acc[H1 + m][f] = mfma16(af2[m], b[f], acc[H1 + m][f]);
           if (s == 0) {   // substep 1's first fragment: b[0] is free once these MFMAs on it are issued
             if (f == 0) unpack(Z + 16);
             if (f == 1) dqh(1, 0, 0);
             if (f == 2) dqh(1, 0, 1);
+            if (f == 1) {   // substep 1's first-half A fragments (their registers' MFMAs are all issued)
+#pragma unroll
+              for (int m = 0; m < H1; ++m) af1[m] = rda(1, m);
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
