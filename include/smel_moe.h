@@ -295,15 +295,15 @@ int smel_combine(const uint16_t* Y, const float* topv, const int32_t* inv, const
  * epilogue 1: down backward, n < C = I: da = w(row) acc with w(row) = topv[p] (fp32) or sgate[t]; (g, u) = hsave[row];
  *             out[row][n] = bf16(da u act'(g)), out[row][I+n] = bf16(da act(g));
  *             dwp[row][j] = sum over column block j of acc * bf16(act(g) u)   (d row weight, reduced later in
- *             fixed order); dwp holds (rows) x smel_gmm_bwd_nblocks(C) floats; bf16(act(g) u) is read from actsave
- *             [rows][C], the forward's activation output (the down GEMM's input)
+ *             fixed order); dwp holds (rows) x smel_gmm_bwd_nblocks(C) floats; bf16(act(g) u) is recomputed from
+ *             the saved bf16 (g, u) exactly as smel_gmm_fwd's epilogue 1 computed it (the value the forward stored)
  * A rows: A[token(row)] if a_gather else A[row]; A holds a_rows rows; the GEMM K = w.R. */
 int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                  int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                  const int32_t* order,
                  int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
-                 const uint16_t* hsave, const uint16_t* actsave, const float* topv, const float* sgate,
-                 uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream);
+                 const uint16_t* hsave, const float* topv, const float* sgate, uint16_t* out, int64_t ldo,
+                 float* dwp, hipStream_t stream);
 /* number of column blocks (dwp row width) smel_gmm_bwd uses for a given C */
 int64_t smel_gmm_bwd_nblocks(int64_t C);
 /* The gate_up backward's LoRA rows without a separate smel_lora_ext launch (the autograd of lora_gate_up's B
@@ -324,8 +324,8 @@ typedef struct smel_bwd_lora_rows {
 int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                     int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                     const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue, int32_t act,
-                    const uint16_t* hsave, const uint16_t* actsave, const float* topv, const float* sgate,
-                    uint16_t* out, int64_t ldo, float* dwp, const smel_bwd_lora_rows* lr, hipStream_t stream);
+                    const uint16_t* hsave, const float* topv, const float* sgate, uint16_t* out, int64_t ldo,
+                    float* dwp, const smel_bwd_lora_rows* lr, hipStream_t stream);
 /* The same rows as bf16 [rows][32 * planes] for the LoRA gradients: ext[row][32 c + j] = bf16(sum_b part[row][b][c][j])
  * for the rows of SEL tiles (sel != 0) and SHARED tiles (sh != 0) of the tile list; other rows are left untouched. */
 int smel_lora_rows_sum(const int32_t* tiles, const int32_t* n_tiles, int64_t max_tiles, const int32_t* gkind,

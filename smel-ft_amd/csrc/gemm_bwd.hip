@@ -60,7 +60,6 @@ struct BwdArgs {
   const int32_t* order;
   const uint16_t* ext;
   const uint16_t* hsave;
-  const uint16_t* actsave;   // the forward's bf16 act(g) u rows (epilogue 1)
   const float* topv;
   const float* sgate;
   uint16_t* out;
@@ -501,25 +500,26 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
     return;
   }
   // down backward, columns n < I of dh = [dg | du]: per row, da = w(row) acc, (g, u) = hsave, dg = da u act'(g),
-  // du = da act(g), and the row's partial of sum_n acc * bf16(act(g) u) over this block's columns -> dwp.
+  // du = da act(g), and the row's partial of sum_n acc * bf16(act(g) u) over this block's columns -> dwp. The
+  // forward's activation bf16(act(g) u) is recomputed from the saved bf16 (g, u) with the forward epilogue's own
+  // operations (act_f and act_and_grad_f share the sigmoid / tanh form), so it is the value the forward stored.
   const int I = N;
   const bool cv = col0 < I;
   const float* const wmap = reinterpret_cast<const float*>(rowmap);
-  // 32 threads per row, 8 rows per pass; the saved (g, u) and act(g) u of PB passes are loaded before any of them is
-  // used, so the stores of one batch never wait for the loads of the next row.
+  // 32 threads per row, 8 rows per pass; the saved (g, u) of PB passes are loaded before any of them is used, so the
+  // stores of one batch never wait for the loads of the next row.
   constexpr int PB = 8;
   const int act = a.act;
   {
     for (int rb = tid >> 5; rb < nrows; rb += 8 * PB) {
-      u32x4_t g2s[PB], u2s[PB], a2s[PB];
+      u32x4_t g2s[PB], u2s[PB];
 #pragma unroll
       for (int p = 0; p < PB; ++p) {
         const int64_t grow = row0 + rb + 8 * p;
-        g2s[p] = u2s[p] = a2s[p] = u32x4_t{};
+        g2s[p] = u2s[p] = u32x4_t{};
         if (cv && rb + 8 * p < nrows) {
           g2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + col0);
           u2s[p] = *reinterpret_cast<const u32x4_t*>(a.hsave + grow * 2 * I + I + col0);
-          a2s[p] = *reinterpret_cast<const u32x4_t*>(a.actsave + grow * I + col0);
         }
       }
 #pragma unroll
@@ -532,23 +532,24 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
         const float wrow_ = wmap[row];
         float part = 0.f;
         if (cv) {
-          const u32x4_t g2 = g2s[p], u2 = u2s[p], a2 = a2s[p];
+          const u32x4_t g2 = g2s[p], u2 = u2s[p];
           uint32_t og[4], ou[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            float dgv[2], duv[2];
+            float dgv[2], duv[2], avl[2], dav[2], uv[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-              const float g = h ? bf_hi(g2[j]) : bf_lo(g2[j]);
-              const float u = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
+              uv[h] = h ? bf_hi(u2[j]) : bf_lo(u2[j]);
+              act_and_grad_f(h ? bf_hi(g2[j]) : bf_lo(g2[j]), act, avl[h], dav[h]);
+            }
+            const uint32_t a2 = pack2bf(avl[0] * uv[0], avl[1] * uv[1]);   // the forward's rounded activation
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
               const float acv = h ? bf_hi(av[j]) : bf_lo(av[j]);
-              float avl, dav;
-              act_and_grad_f(g, act, avl, dav);
-              const float abf = h ? bf_hi(a2[j]) : bf_lo(a2[j]);   // the forward's rounded activation
-              part += acv * abf;
+              part += acv * (h ? bf_hi(a2) : bf_lo(a2));
               const float da = wrow_ * acv;
-              dgv[h] = da * u * dav;
-              duv[h] = da * avl;
+              dgv[h] = da * uv[h] * dav[h];
+              duv[h] = da * avl[h];
             }
             og[j] = pack2bf(dgv[0], dgv[1]);
             ou[j] = pack2bf(duv[0], duv[1]);
@@ -696,8 +697,8 @@ extern "C" int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const i
                                const int32_t* n_tiles, int64_t max_tiles, const uint16_t* A, int64_t lda,
                                int64_t a_rows, int32_t a_gather, const int32_t* order, int64_t TK, int64_t topk,
                                const uint16_t* ext, int32_t epilogue, int32_t act, const uint16_t* hsave,
-                               const uint16_t* actsave, const float* topv, const float* sgate, uint16_t* out,
-                               int64_t ldo, float* dwp, const smel_bwd_lora_rows* lr, hipStream_t stream) {
+                               const float* topv, const float* sgate, uint16_t* out, int64_t ldo, float* dwp,
+                               const smel_bwd_lora_rows* lr, hipStream_t stream) {
   SMEL_REQUIRE(w && tiles && n_tiles && A && out, SMEL_EINVAL, "gmm_bwd: null pointer");
   SMEL_REQUIRE(w->R > 0 && w->C > 0 && max_tiles >= 0 && lda >= w->R && topk > 0, SMEL_EINVAL,
                "gmm_bwd: bad sizes");
@@ -708,11 +709,10 @@ extern "C" int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const i
   SMEL_REQUIRE(!w->q4 || w->sz4, SMEL_EINVAL,
                "gmm_bwd: an int4 bank needs its transposed scale/zero (smel_pack_int4_t)");
   SMEL_REQUIRE(lda % 8 == 0 && ((uintptr_t)A % 16) == 0, SMEL_EUNSUPPORTED, "gmm_bwd: A rows must be 16-B aligned");
-  SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0 &&
-                   ((uintptr_t)actsave % 16) == 0, SMEL_EUNSUPPORTED,
-               "gmm_bwd: out / hsave / actsave rows must be 16-B aligned");
-  SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && actsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
-               "gmm_bwd: epilogue %d needs hsave, actsave, dwp and topv", epilogue);
+  SMEL_REQUIRE(ldo % 8 == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)hsave % 16) == 0, SMEL_EUNSUPPORTED,
+               "gmm_bwd: out / hsave rows must be 16-B aligned");
+  SMEL_REQUIRE(epilogue == 0 || (epilogue == 1 && hsave && dwp && (topv || TK == 0)), SMEL_EINVAL,
+               "gmm_bwd: epilogue %d needs hsave, dwp and topv", epilogue);
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_bwd: gather needs order");
   SMEL_REQUIRE(!(w->flags & SMEL_WSET_EXT2) || epilogue == 0, SMEL_EINVAL,
                "gmm_bwd: a two-plane LoRA extension belongs to the gate_up backward (epilogue 0)");
@@ -748,7 +748,6 @@ extern "C" int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const i
   a.order = order;
   a.ext = ext;
   a.hsave = hsave;
-  a.actsave = epilogue == 1 ? actsave : nullptr;
   a.topv = topv;
   a.sgate = sgate;
   a.out = out;
@@ -780,8 +779,8 @@ extern "C" int smel_gmm_bwd_lr(const smel_wset* w, const int32_t* gkind, const i
 extern "C" int smel_gmm_bwd(const smel_wset* w, const int32_t* gkind, const int32_t* tiles, const int32_t* n_tiles,
                             int64_t max_tiles, const uint16_t* A, int64_t lda, int64_t a_rows, int32_t a_gather,
                             const int32_t* order, int64_t TK, int64_t topk, const uint16_t* ext, int32_t epilogue,
-                            int32_t act, const uint16_t* hsave, const uint16_t* actsave, const float* topv,
-                            const float* sgate, uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
+                            int32_t act, const uint16_t* hsave, const float* topv, const float* sgate,
+                            uint16_t* out, int64_t ldo, float* dwp, hipStream_t stream) {
   return smel_gmm_bwd_lr(w, gkind, tiles, n_tiles, max_tiles, A, lda, a_rows, a_gather, order, TK, topk, ext,
-                         epilogue, act, hsave, actsave, topv, sgate, out, ldo, dwp, nullptr, stream);
+                         epilogue, act, hsave, topv, sgate, out, ldo, dwp, nullptr, stream);
 }

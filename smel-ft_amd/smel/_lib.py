@@ -21,7 +21,7 @@ WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
 WSET_MERGE_SHORT = 8 # smel_wset.flags: gate_up forward, a full int4 tile also takes the group's short last tile
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -108,9 +108,9 @@ SIGNATURES = {
     "smel_gmm_fwd_nblocks": (i64, [i64, i32]),
     "smel_combine": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp]),
     "smel_gmm_bwd": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
-                           vp, vp, vp, vp, vp, i64, vp, vp]),
+                           vp, vp, vp, vp, i64, vp, vp]),
     "smel_gmm_bwd_lr": (i32, [ctypes.POINTER(WSet), vp, vp, vp, i64, vp, i64, i64, i32, vp, i64, i64, vp, i32, i32,
-                              vp, vp, vp, vp, vp, i64, vp, ctypes.POINTER(BwdLoraRows), vp]),
+                              vp, vp, vp, vp, i64, vp, ctypes.POINTER(BwdLoraRows), vp]),
     "smel_gmm_bwd_nblocks": (i64, [i64]),
     "smel_lora_rows_sum": (i32, [vp, vp, i64, vp, i32, i32, vp, i32, i32, vp, vp]),
     "smel_route_bwd": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp, vp, vp]),

@@ -643,7 +643,7 @@ def _router_dx(dl: torch.Tensor, wr: PackedW, T: int, dx: torch.Tensor | None = 
     w.wsh = L.ptr(wr.t)
     w.R, w.C, w.group = wr.R, H, 32
     L.call("smel_gmm_bwd", ctypes.byref(w), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dl), dl.shape[1], T, 0,
-           None, 0, 1, None, 0, 0, None, None, None, None, L.ptr(dx), H, None, L.stream(), tag="gemm_router_bwd")
+           None, 0, 1, None, 0, 0, None, None, None, L.ptr(dx), H, None, L.stream(), tag="gemm_router_bwd")
     return dx
 
 
@@ -878,8 +878,8 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     lrows = _bwd_lora_rows(lb_ex, lb_sh, nblk, M, planes, dev) if any_lora and _BWD_LORA_ROWS else None
     lr = ctypes.byref(lrows[0]) if lrows is not None else None
     L.call("smel_gmm_bwd_lr", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dout), H, T, 1,
-           L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["act"]), L.ptr(t["topv"]),
-           L.ptr(t["sgate"]), L.ptr(dh), 2 * I, L.ptr(dwp), lr, st, tag="gemm_dn_bwd")
+           L.ptr(order), TK, K, L.ptr(ext_db), 1, _ACT[ex.act], L.ptr(t["hsave"]), L.ptr(t["topv"]), L.ptr(t["sgate"]),
+           L.ptr(dh), 2 * I, L.ptr(dwp), lr, st, tag="gemm_dn_bwd")
     # (3) LoRA B^T projection of dh for the gate_up backward: DXA = s [dg B_g, du B_u] (without the partials)
     ext_dxa = None
     if any_lora and _BWD_ONE_SIDE and lrows is None:
@@ -941,7 +941,7 @@ def _backward_pipeline(c: _Ctx, dout: torch.Tensor, router=None, shared_split=No
     w_gu.flags |= L.WSET_XCD_CHUNK
     L.call("smel_gmm_bwd_lr", ctypes.byref(w_gu), L.ptr(gk), L.ptr(t["tiles_g"]), L.ptr(ntiles), maxt, L.ptr(dh),
            2 * I, M, 0, L.ptr(order), TK, K, None if lrows is not None else L.ptr(ext_dxa), 0, _ACT[ex.act], None, None,
-           None, None, L.ptr(dxs), H, None, lr, st, tag="gemm_gu_bwd")
+           None, L.ptr(dxs), H, None, lr, st, tag="gemm_gu_bwd")
     side_r.join()
     dx = bf(T, H)
     dxsh = shared_split[2] if shared_split is not None else None
@@ -1240,15 +1240,15 @@ def _dense_mlp_bwd(sv: _DenseSaved, dy, w_gu_t: PackedW, w_dn_t: PackedW, lora, 
     lrows = _bwd_lora_rows(None, lb, nblk, T, planes, dev) if lb is not None and _BWD_LORA_ROWS else None
     lr = ctypes.byref(lrows[0]) if lrows is not None else None
     L.call("smel_gmm_bwd_lr", ctypes.byref(wd), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, T, 0,
-           None, 0, 1, L.ptr(ext_db), 1, _ACT[act_name], L.ptr(sv.hsave), L.ptr(sv.actb), None, L.ptr(row_w),
-           L.ptr(dh), 2 * Is, L.ptr(dwp), lr, st, tag=tag + "_dn_bwd")
+           None, 0, 1, L.ptr(ext_db), 1, _ACT[act_name], L.ptr(sv.hsave), None, L.ptr(row_w), L.ptr(dh), 2 * Is,
+           L.ptr(dwp), lr, st, tag=tag + "_dn_bwd")
     if lb is not None and lrows is None:
         ext_dxa = _lora_ext(tl, dh, 2 * Is, T, 0, None, 0, 1, None, lb, "bt_gu", 2 * Is, planes, T, dev, st)
     dx = bf(T, H)
     wg = _dense_wset(w_gu_t, g("at_gu"), planes)
     L.call("smel_gmm_bwd_lr", ctypes.byref(wg), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * Is, T,
-           0, None, 0, 1, None if lrows is not None else L.ptr(ext_dxa), 0, 0, None, None, None, None, L.ptr(dx), H,
-           None, lr, st, tag=tag + "_gu_bwd")
+           0, None, 0, 1, None if lrows is not None else L.ptr(ext_dxa), 0, 0, None, None, None, L.ptr(dx), H, None,
+           lr, st, tag=tag + "_gu_bwd")
     grads = None
     if lb is not None:
         if lrows is not None:   # the LoRA gradients take the same rows the gate_up backward summed
@@ -1483,7 +1483,7 @@ class FrozenExpertsFn(torch.autograd.Function):
                0, None, 0, 1, None, 1, _ACT[act_name], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_frozen_gu_fwd")
         L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, rows,
                0, None, 0, 1, None, 0, _ACT[act_name], L.ptr(out), H, None, st, tag="gemm_frozen_dn_fwd")
-        ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, actb, act_name)
+        ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, act_name)
         return out
 
     @staticmethod
@@ -1493,7 +1493,7 @@ class FrozenExpertsFn(torch.autograd.Function):
             return F32.frozen_bwd(keep, dy.float()).to(ctx.dtype), None, None, None, None
         if ctx.plan is None:
             return torch.zeros_like(dy), None, None, None, None
-        bank, tiles, ntiles, maxt, gk, hsave, actb, act_name = ctx.plan
+        bank, tiles, ntiles, maxt, gk, hsave, act_name = ctx.plan
         ctx.plan = None
         dy = _bf16(dy)
         rows, H = dy.shape
@@ -1506,11 +1506,11 @@ class FrozenExpertsFn(torch.autograd.Function):
         dwp = torch.empty(rows, nblk, dtype=torch.float32, device=dev)
         ones = torch.ones(rows, dtype=torch.float32, device=dev)    # row weight 1 (no combine weight here)
         L.call("smel_gmm_bwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dy), H, rows, 0,
-               None, 0, 1, None, 1, _ACT[act_name], L.ptr(hsave), L.ptr(actb), None, L.ptr(ones), L.ptr(dh), 2 * I,
-               L.ptr(dwp), st, tag="gemm_frozen_dn_bwd")
+               None, 0, 1, None, 1, _ACT[act_name], L.ptr(hsave), None, L.ptr(ones), L.ptr(dh), 2 * I, L.ptr(dwp),
+               st, tag="gemm_frozen_dn_bwd")
         dx = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
         L.call("smel_gmm_bwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(dh), 2 * I,
-               rows, 0, None, 0, 1, None, 0, _ACT[act_name], None, None, None, None, L.ptr(dx), H, None, st,
+               rows, 0, None, 0, 1, None, 0, _ACT[act_name], None, None, None, L.ptr(dx), H, None, st,
                tag="gemm_frozen_gu_bwd")
         return dx, None, None, None, None
 

@@ -149,12 +149,12 @@ def test_host_side_rejections():
     w.R, w.C = 2048, 512
     lr = _lib.BwdLoraRows(None, 16, 1.0, 1.0, 0, 1, 16, 3)
     args = (ctypes.byref(w), None, 16, 16, 1, 16, 2048, 4, 0, None, 0, 1, None)
-    assert L.smel_gmm_bwd_lr(*args, 1, 0, 16, 16, 16, 16, 16, 1024, 16, ctypes.byref(lr), None) == -1
+    assert L.smel_gmm_bwd_lr(*args, 1, 0, 16, 16, 16, 16, 1024, 16, ctypes.byref(lr), None) == -1
     assert b"partials" in L.smel_last_error()
     lr.parts = L.smel_gmm_bwd_nblocks(512)
     w.R, w.C = 512, 2048
     assert L.smel_gmm_bwd_lr(ctypes.byref(w), None, 16, 16, 1, 16, 1024, 4, 0, None, 0, 1, 16, 0, 0, None, None, None,
-                             None, 16, 2048, None, ctypes.byref(lr), None) == -1   # ext and partials together
+                             16, 2048, None, ctypes.byref(lr), None) == -1   # ext and partials together
     assert L.smel_lora_rows_sum(16, 16, 4, None, 1, 1, 16, 2, 3, 16, None) == -1
     fl = _lib.FwdLoraRows(None, 16, 1.0, 1.0, 16, 3, None)
     w.R, w.C = 1024, 2048

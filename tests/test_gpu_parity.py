@@ -248,7 +248,7 @@ def test_gemm_dequant_bitexact(group, fast):
     tiles, nt, maxt = _count_tiles([R] * E, DEV)
     out_t = torch.empty(E * R, C, dtype=torch.bfloat16, device=DEV)
     L.call("smel_gmm_bwd", ctypes.byref(wt), L.ptr(gk), L.ptr(tiles), L.ptr(nt), maxt, L.ptr(At), R, E * R, 0,
-           L.ptr(order_t), E * R, 1, None, 0, 0, None, None, None, None, L.ptr(out_t), C, None, L.stream())
+           L.ptr(order_t), E * R, 1, None, 0, 0, None, None, None, L.ptr(out_t), C, None, L.stream())
     assert np.array_equal(_u16(out_t).reshape(E, R, C), want)
 
 
