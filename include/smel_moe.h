@@ -68,6 +68,11 @@ typedef struct smel_wset {
  * group's last tile of at most 32 rows (the weights are streamed and dequantized once for up to 160 rows); that
  * tile's own blocks do nothing. */
 #define SMEL_WSET_MERGE_SHORT 8
+/* SMEL_WSET_MERGED_LIST (smel_gmm_fwd, gate_up projection, int4 bank with SMEL_WSET_FAST_DQ, C a multiple of 64):
+ * the tile list is smel_dispatch's tiles_merged, whose int4 tiles may hold up to 160 rows (a full tile and the
+ * group's last tile of at most 32 rows); each is one tile (one weight stream and dequant), and no block idles.
+ * Without it a tile of the list has at most 128 rows (rows past 128 are not computed). */
+#define SMEL_WSET_MERGED_LIST 16
 
 const char* smel_last_error(void);
 int smel_abi_version(void);
@@ -179,11 +184,16 @@ int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scal
  * in group order. tiles_grouped (optional, [max_tiles][4]): the same tiles in group order (for SMEL_WSET_XCD_CHUNK).
  * err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
  * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
- * workspace. E <= 512. */
+ * workspace. E <= 512.
+ * merge_rows (0: off; m_tile < merge_rows <= 2 m_tile, needs gkind): also the merged list tiles_merged [max_tiles][4]
+ * (n_tiles_merged [1] of them) for the gate_up forward with SMEL_WSET_MERGED_LIST: a group of kind SMEL_KIND_INT4
+ * whose last tile has at most merge_rows - m_tile rows gets it joined to the full tile before it (one tile of up to
+ * merge_rows rows); order: those merged tiles, then the other tiles of more than m_tile / 2 rows, then the shorter
+ * ones, each part in group order. */
 int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                   int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
-                  int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t* ws,
-                  hipStream_t stream);
+                  int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err,
+                  int32_t merge_rows, int32_t* tiles_merged, int32_t* n_tiles_merged, int32_t* ws, hipStream_t stream);
 /* int32 elements of smel_dispatch's workspace (host-side, no GPU call); -1 for bad sizes. */
 int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
 /* smel_dispatch of the ids that smel_route_counted selected, with the workspace it filled: the histogram launch is
@@ -191,14 +201,16 @@ int64_t smel_dispatch_ws_size(int64_t TK, int64_t E);
 int smel_dispatch_counted(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                           int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
                           int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err,
-                          int32_t* ws, hipStream_t stream);
+                          int32_t merge_rows, int32_t* tiles_merged, int32_t* n_tiles_merged, int32_t* ws,
+                          hipStream_t stream);
 /* smel_dispatch without the workspace argument; it allocates nothing. No counterpart in the reference: it exists
  * for callers that cannot allocate device memory (code under HIP-graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). The workspace is a fixed array of smel_dispatch_noalloc_max_ws() int32 held by the library on
  * every GPU it runs on until the process ends; calls whose smel_dispatch_ws_size(T*K, E) exceeds it are rejected
  * (SMEL_EUNSUPPORTED). Every call on one GPU shares that GPU's array and each call rewrites all of the part it uses
  * before reading it, so nothing carries over between calls, but calls that overlap in time on one GPU (different
- * streams, or threads without ordering) race: order them on one stream. Results are those of smel_dispatch. */
+ * streams, or threads without ordering) race: order them on one stream. Results are those of smel_dispatch (without
+ * the merged list: merge_rows 0). */
 int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                           int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order,
                           int32_t* inv, int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err,

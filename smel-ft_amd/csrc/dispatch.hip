@@ -47,10 +47,67 @@ SMEL_DEV int block_exclusive_scan(int v, int* wsum /* [NW] LDS */, int& total) {
   return base + inc - v;
 }
 
+// Exclusive scan of three values at once over the block (the latency of one scan); tot = the block totals. wsum is
+// not reused afterwards, so there is no trailing barrier.
+struct I3 {
+  int a, b, c;
+};
+SMEL_DEV I3 block_exclusive_scan3(I3 v, I3* wsum /* [NW] LDS */, I3& tot) {
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  I3 inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int ya = __shfl_up(inc.a, o, 64), yb = __shfl_up(inc.b, o, 64), yc = __shfl_up(inc.c, o, 64);
+    if (l >= o) {
+      inc.a += ya;
+      inc.b += yb;
+      inc.c += yc;
+    }
+  }
+  if (l == 63) wsum[w] = inc;
+  lds_barrier();
+  I3 base{0, 0, 0}, t{0, 0, 0};
+  for (int j = 0; j < NW; ++j) {
+    const I3 s = wsum[j];
+    if (j < w) {
+      base.a += s.a;
+      base.b += s.b;
+      base.c += s.c;
+    }
+    t.a += s.a;
+    t.b += s.b;
+    t.c += s.c;
+  }
+  tot = t;
+  return I3{base.a + inc.a - v.a, base.b + inc.b - v.b, base.c + inc.c - v.c};
+}
+
 SMEL_DEV int id_at(const void* ids, int is64, int p) {
   return is64 ? (int)static_cast<const int64_t*>(ids)[p] : static_cast<const int32_t*>(ids)[p];
 }
 
+SMEL_DEV int tiles_of(int rows, int m_tile) { return (rows + m_tile - 1) / m_tile; }
+SMEL_DEV int long_tiles_of(int rows, int m_tile) {   // tiles of more than m_tile / 2 rows
+  const int nt = tiles_of(rows, m_tile);
+  return nt - ((nt > 0 && rows - (nt - 1) * m_tile <= m_tile / 2) ? 1 : 0);
+}
+
+// The merged tile list (tiles_m, merge_rows > m_tile), for the gate_up forward: an int4 group's last tile of at most
+// merge_rows - m_tile rows joins the full tile before it (one tile, one weight stream and dequant for both). Order:
+// the merged tiles, then the other tiles of more than m_tile / 2 rows, then the shorter ones, each part in group
+// order (the costliest tiles start first, the short ones fill the last round). A group's counts: {merged (0 or 1),
+// full or long (the tiles before the last, and the last when long), short (0 or 1)}.
+SMEL_DEV I3 merged_counts(int rows, int m_tile, int merge_rows, bool int4) {
+  const int nt = tiles_of(rows, m_tile);
+  if (nt == 0) return I3{0, 0, 0};
+  const int rem = rows - (nt - 1) * m_tile;
+  const int a = (merge_rows > m_tile && int4 && nt >= 2 && rem <= merge_rows - m_tile) ? 1 : 0;
+  const int last_long = (!a && rem > m_tile / 2) ? 1 : 0;
+  return I3{a, nt - 1 - a + last_long, (!a && !last_long) ? 1 : 0};
+}
+struct TileLds {
+  int lb[MAXE + 1], sb[MAXE + 1], mb[MAXE + 1], row0[MAXE + 1], rows[MAXE + 1], nt[MAXE + 1], gk[MAXE + 1];
+};
 // Tile list over groups 0..E-1 (+ shared group E): the tiles of more than m_tile / 2 rows first (in group order), then
 // the shorter last tiles of the groups (in group order). The grouped GEMMs start tiles in list order, so the short
 // tiles fill the last round of workgroups instead of holding long ones back. tiles_g (optional): the same tiles in
@@ -59,15 +116,16 @@ SMEL_DEV int id_at(const void* ids, int is64, int p) {
 // short tiles; n_long / n_short = the totals. The groups' values go through LDS, then thread q writes long tile q and
 // short tile q (its group found by a binary search over the first positions), so no thread loops over a large
 // group's tiles. Every thread of the block calls it (one barrier inside).
-struct TileLds {
-  int lb[MAXE + 1], sb[MAXE + 1], row0[MAXE + 1], rows[MAXE + 1], nt[MAXE + 1], gk[MAXE + 1];
-};
+// Merged list (tiles_m != nullptr): mc / mpos = this group's merged_counts and their exclusive positions, mtot the
+// totals.
 SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt, int lbase, int sbase, int n_long,
                           int n_short, int m_tile, int max_tiles, int gkv, int bad, int32_t* __restrict__ tiles,
-                          int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
+                          int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err,
+                          I3 mc, I3 mpos, I3 mtot, int32_t* __restrict__ tiles_m, int32_t* __restrict__ n_tiles_m) {
   if (tid < G) {
     t.lb[tid] = lbase;
     t.sb[tid] = sbase;
+    t.mb[tid] = mpos.b;
     t.row0[tid] = row0;
     t.rows[tid] = rows;
     t.nt[tid] = nt;
@@ -112,17 +170,33 @@ SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt
     n_tiles[0] = min(total_tiles, max_tiles);
     err[0] = bad | (total_tiles > max_tiles ? 2 : 0);
   }
-}
-SMEL_DEV int tiles_of(int rows, int m_tile) { return (rows + m_tile - 1) / m_tile; }
-SMEL_DEV int long_tiles_of(int rows, int m_tile) {   // tiles of more than m_tile / 2 rows
-  const int nt = tiles_of(rows, m_tile);
-  return nt - ((nt > 0 && rows - (nt - 1) * m_tile <= m_tile / 2) ? 1 : 0);
+  if (!tiles_m) return;   // uniform
+  auto putm = [&](int g, int y, int z, int pos) {
+    if (pos >= max_tiles) return;
+    int4 tl;
+    tl.x = g;
+    tl.y = y;
+    tl.z = z;
+    tl.w = t.gk[g];
+    reinterpret_cast<int4*>(tiles_m)[pos] = tl;
+  };
+  if (tid < G) {   // the group's merged tile and short tile (at most one of each), from its own thread
+    if (mc.a) putm(tid, row0 + (nt - 2) * m_tile, row0 + rows, mpos.a);
+    if (mc.c) putm(tid, row0 + (nt - 1) * m_tile, row0 + rows, mtot.a + mtot.b + mpos.c);
+  }
+  for (int q = tid; q < mtot.b; q += DB) {   // full / long tile i of its group
+    const int g = group_of(t.mb, q);
+    const int i = q - t.mb[g], r0 = t.row0[g];
+    putm(g, r0 + i * m_tile, min(r0 + t.rows[g], r0 + (i + 1) * m_tile), mtot.a + q);
+  }
+  if (tid == 0) n_tiles_m[0] = min(mtot.a + mtot.b + mtot.c, max_tiles);   // never longer than tiles
 }
 
 // The tile list from the offsets off_s[0..E] (LDS). Called by every thread of one block (block scans inside).
 SMEL_DEV void write_tiles(TileLds& tl, int tid, int E, int TK, int shared_rows, int m_tile, int max_tiles, int gkv,
-                          const int* off_s, int bad, int* wsum, int32_t* __restrict__ tiles,
-                          int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err) {
+                          const int* off_s, int bad, int* wsum, I3* wsum3, int32_t* __restrict__ tiles,
+                          int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err,
+                          int merge_rows, bool has_gk, int32_t* __restrict__ tiles_m, int32_t* __restrict__ n_tiles_m) {
   const int G = E + (shared_rows > 0 ? 1 : 0);
   int nt = 0, rows = 0, row0 = 0, nlong = 0;
   if (tid < G) {
@@ -134,8 +208,11 @@ SMEL_DEV void write_tiles(TileLds& tl, int tid, int E, int TK, int shared_rows, 
   int n_long, n_short;
   const int lbase = block_exclusive_scan(nlong, wsum, n_long);
   const int sbase = block_exclusive_scan(nt - nlong, wsum, n_short);
+  const I3 mc = merged_counts(rows, m_tile, tiles_m ? merge_rows : 0, has_gk && (gkv >> 16) == SMEL_KIND_INT4);
+  I3 mtot;
+  const I3 mpos = block_exclusive_scan3(mc, wsum3, mtot);
   store_tiles(tl, tid, G, rows, row0, nt, lbase, sbase, n_long, n_short, m_tile, max_tiles, gkv, bad, tiles, tiles_g,
-              n_tiles, err);
+              n_tiles, err, mc, mpos, mtot, tiles_m, n_tiles_m);
 }
 
 // (1) hist[b][e] = slots of block b routed to expert e; bad[b] = 1 if block b holds an id outside [0, E)
@@ -167,8 +244,11 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
                                                       const int32_t* __restrict__ bad, int32_t* __restrict__ counts,
                                                       int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
                                                       int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles,
-                                                      int32_t* __restrict__ err) {
+                                                      int32_t* __restrict__ err, int merge_rows,
+                                                      int32_t* __restrict__ tiles_m,
+                                                      int32_t* __restrict__ n_tiles_m) {
   __shared__ int wsum[NW];
+  __shared__ I3 wsum3[NW];
   __shared__ int off_s[MAXE + 1];
   __shared__ int bad_s;
   __shared__ int hs[HCH];
@@ -224,7 +304,8 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
   }
   if (badv) bad_s = 1;
   lds_barrier();
-  write_tiles(tl, tid, E, TK, shared_rows, m_tile, max_tiles, gkv, off_s, bad_s, wsum, tiles, tiles_g, n_tiles, err);
+  write_tiles(tl, tid, E, TK, shared_rows, m_tile, max_tiles, gkv, off_s, bad_s, wsum, wsum3, tiles, tiles_g, n_tiles,
+              err, merge_rows, gkind != nullptr, tiles_m, n_tiles_m);
 }
 
 // Stable scatter of block b's slots: order[pos] = p, inv[p] = pos (-1 for an id outside [0, E)); base(x) = the first
@@ -278,41 +359,6 @@ __global__ __launch_bounds__(1024) void dispatch_scatter(const void* __restrict_
   scatter_block(e, TK, E, b, [&](int x) { return base[b * E + x]; }, cnt, order, inv);
 }
 
-// Exclusive scan of three values at once over the block (the latency of one scan); tot = the block totals. wsum is
-// not reused afterwards, so there is no trailing barrier.
-struct I3 {
-  int a, b, c;
-};
-SMEL_DEV I3 block_exclusive_scan3(I3 v, I3* wsum /* [NW] LDS */, I3& tot) {
-  const int l = lane_id(), w = threadIdx.x >> 6;
-  I3 inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int ya = __shfl_up(inc.a, o, 64), yb = __shfl_up(inc.b, o, 64), yc = __shfl_up(inc.c, o, 64);
-    if (l >= o) {
-      inc.a += ya;
-      inc.b += yb;
-      inc.c += yc;
-    }
-  }
-  if (l == 63) wsum[w] = inc;
-  lds_barrier();
-  I3 base{0, 0, 0}, t{0, 0, 0};
-  for (int j = 0; j < NW; ++j) {
-    const I3 s = wsum[j];
-    if (j < w) {
-      base.a += s.a;
-      base.b += s.b;
-      base.c += s.c;
-    }
-    t.a += s.a;
-    t.b += s.b;
-    t.c += s.c;
-  }
-  tot = t;
-  return I3{base.a + inc.a - v.a, base.b + inc.b - v.b, base.c + inc.c - v.c};
-}
-
 // (2+3) for at most SCAN_FUSE_NB blocks, the scan and the scatter in one launch: every block folds all blocks'
 // histograms itself (the totals, and the prefix over the blocks before it, per expert) and scatters its slots; block
 // 0 also writes counts, offsets, the tile lists, n_tiles and err. No block waits for another. Order of the work: every
@@ -330,9 +376,11 @@ __global__ __launch_bounds__(1024) void dispatch_scan_scatter(const void* __rest
                                                               int32_t* __restrict__ tiles_g,
                                                               int32_t* __restrict__ n_tiles,
                                                               int32_t* __restrict__ err, int32_t* __restrict__ order,
-                                                              int32_t* __restrict__ inv) {
+                                                              int32_t* __restrict__ inv, int merge_rows,
+                                                              int32_t* __restrict__ tiles_m,
+                                                              int32_t* __restrict__ n_tiles_m) {
   __shared__ int cnt[NW * MAXE];   // per-wave counts, then per-wave first positions
-  __shared__ I3 wsum[NW];
+  __shared__ I3 wsum[NW], wsum_m[NW];
   __shared__ int bad_s;
   __shared__ TileLds tl;
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, b = blockIdx.x;
@@ -391,8 +439,11 @@ __global__ __launch_bounds__(1024) void dispatch_scan_scatter(const void* __rest
       offsets[tid] = ex.a;
     }
     if (tid == 0) offsets[E] = tot.a;
+    const I3 mc = merged_counts(rows, m_tile, tiles_m ? merge_rows : 0, gkind && (gkv >> 16) == SMEL_KIND_INT4);
+    I3 mtot;
+    const I3 mpos = block_exclusive_scan3(mc, wsum_m, mtot);
     store_tiles(tl, tid, G, rows, tid < E ? ex.a : TK, nt, ex.b, ex.c, tot.b, tot.c, m_tile, max_tiles, gkv, bad_s,
-                tiles, tiles_g, n_tiles, err);
+                tiles, tiles_g, n_tiles, err, mc, mpos, mtot, tiles_m, n_tiles_m);
   }
   // first output position of wave j's slots of expert tid
   if (tid < E) {
@@ -460,9 +511,15 @@ extern "C" int64_t smel_dispatch_ws_size(int64_t TK, int64_t E) {
 namespace {
 int dispatch_impl(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E, int64_t shared_rows,
                   int32_t m_tile, const int32_t* gkind, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* inv,
-                  int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t* ws, bool counted,
-                  hipStream_t stream) {
+                  int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t merge_rows,
+                  int32_t* tiles_merged, int32_t* n_tiles_merged, int32_t* ws, bool counted, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && shared_rows >= 0 && m_tile > 0, SMEL_EINVAL, "dispatch: bad sizes");
+  SMEL_REQUIRE(merge_rows == 0 || (merge_rows > m_tile && merge_rows <= 2 * m_tile && tiles_merged &&
+                                   n_tiles_merged && gkind),
+               SMEL_EINVAL,
+               "dispatch: a merged tile list needs m_tile < merge_rows <= 2 m_tile (got %d, m_tile %d), its outputs "
+               "and the group kinds", merge_rows, m_tile);
+  if (merge_rows == 0) tiles_merged = n_tiles_merged = nullptr;
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "dispatch: E=%lld > %d experts", (long long)E, MAXE);
   SMEL_REQUIRE(T * K < (1ll << 30), SMEL_EUNSUPPORTED, "dispatch: T*K too large");
   SMEL_REQUIRE(counts && offsets && tiles && n_tiles && err && (T == 0 || (ids && order && inv && ws)), SMEL_EINVAL,
@@ -480,11 +537,13 @@ int dispatch_impl(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, in
   if (nb > 0 && nb <= SCAN_FUSE_NB) {
     dispatch_scan_scatter<<<nb, DB, 0, stream>>>(ids, ids_are_i64 ? 1 : 0, nb, (int)TK, (int)E, (int)shared_rows,
                                                  m_tile, (int)mt, gkind, hist, bad, counts, offsets, tiles,
-                                                 tiles_grouped, n_tiles, err, order, inv);
+                                                 tiles_grouped, n_tiles, err, order, inv, merge_rows, tiles_merged,
+                                                 n_tiles_merged);
     return smel::launch_status();
   }
   dispatch_scan<<<1, DB, 0, stream>>>(nb, (int)TK, (int)E, (int)shared_rows, m_tile, (int)mt, gkind, hist, bad,
-                                      counts, offsets, tiles, tiles_grouped, n_tiles, err);
+                                      counts, offsets, tiles, tiles_grouped, n_tiles, err, merge_rows, tiles_merged,
+                                      n_tiles_merged);
   if (nb > 0) {
     const int st = smel::launch_status();
     if (st) return st;
@@ -497,18 +556,20 @@ int dispatch_impl(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, in
 extern "C" int smel_dispatch(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
                              int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
                              int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles, int32_t* tiles_grouped,
-                             int32_t* n_tiles, int32_t* err, int32_t* ws, hipStream_t stream) {
+                             int32_t* n_tiles, int32_t* err, int32_t merge_rows, int32_t* tiles_merged,
+                             int32_t* n_tiles_merged, int32_t* ws, hipStream_t stream) {
   return dispatch_impl(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
-                       tiles_grouped, n_tiles, err, ws, false, stream);
+                       tiles_grouped, n_tiles, err, merge_rows, tiles_merged, n_tiles_merged, ws, false, stream);
 }
 
 extern "C" int smel_dispatch_counted(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, int64_t E,
                                      int64_t shared_rows, int32_t m_tile, const int32_t* gkind, int32_t* counts,
                                      int32_t* offsets, int32_t* order, int32_t* inv, int32_t* tiles,
-                                     int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t* ws,
+                                     int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t merge_rows,
+                                     int32_t* tiles_merged, int32_t* n_tiles_merged, int32_t* ws,
                                      hipStream_t stream) {
   return dispatch_impl(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
-                       tiles_grouped, n_tiles, err, ws, true, stream);
+                       tiles_grouped, n_tiles, err, merge_rows, tiles_merged, n_tiles_merged, ws, true, stream);
 }
 
 extern "C" int64_t smel_dispatch_noalloc_max_ws(void) { return SCRATCH_INTS; }
@@ -526,5 +587,5 @@ extern "C" int smel_dispatch_noalloc(const void* ids, int32_t ids_are_i64, int64
   int32_t* ws = scratch_on_device();
   if (!ws) return SMEL_EINVAL;
   return smel_dispatch(ids, ids_are_i64, T, K, E, shared_rows, m_tile, gkind, counts, offsets, order, inv, tiles,
-                       tiles_grouped, n_tiles, err, ws, stream);
+                       tiles_grouped, n_tiles, err, 0, nullptr, nullptr, ws, stream);
 }

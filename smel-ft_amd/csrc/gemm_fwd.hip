@@ -576,12 +576,13 @@ SMEL_DEV void gmm_fwd_body(const FwdArgs& a, uint16_t* S0, uint16_t* S1, uint16_
   const int gk = a.gkind ? a.gkind[t.x] : t.w;   // the tile list may carry the group kind itself
   const int kind = gk >> 16, idx = gk & 0xffff;
   int row1 = t.z;
-  if (EPI == 1 && kind == SMEL_KIND_INT4 && (a.w.flags & SMEL_WSET_MERGE_SHORT) && (a.w.flags & SMEL_WSET_FAST_DQ) &&
-      (a.K & (KT - 1)) == 0) {
+  // a tile of up to 160 rows: a merged list's int4 tile (its rows beyond 128 are the group's short last tile), or a
+  // full tile that takes the next one below (group-ordered list, SMEL_WSET_MERGE_SHORT). Both need the fast dequant
+  // form and K a multiple of 64 (the 5-slice tile has no registers for the other form or for a K tail).
+  const bool five = EPI == 1 && kind == SMEL_KIND_INT4 && (a.w.flags & SMEL_WSET_FAST_DQ) && (a.K & (KT - 1)) == 0;
+  if (five && (a.w.flags & SMEL_WSET_MERGE_SHORT)) {
     // In a group-ordered list, a group's last tile of at most MT_MERGED - MT rows right after a full tile of the same
-    // group is taken by the full tile's blocks (one weight stream and dequant for both); its own blocks exit. (Banks
-    // in the fast dequant form and K a multiple of 64 only: the 5-slice tile has no registers for the other form or
-    // for a K tail.)
+    // group is taken by the full tile's blocks (one weight stream and dequant for both); its own blocks exit.
     if (t.z - t.y <= MT_MERGED - MT && tile > 0) {
       const int4 p = a.tiles[tile - 1];
       if (p.x == t.x && p.z == t.y && p.z - p.y == MT) return;
@@ -591,7 +592,8 @@ SMEL_DEV void gmm_fwd_body(const FwdArgs& a, uint16_t* S0, uint16_t* S1, uint16_
       if (q.x == t.x && q.y == t.z && q.z - q.y <= MT_MERGED - MT) row1 = q.z;
     }
   }
-  const int nrows = min(row1 - t.y, stage_rows(EPI));
+  const bool merged = five && (a.w.flags & (SMEL_WSET_MERGE_SHORT | SMEL_WSET_MERGED_LIST));
+  const int nrows = min(row1 - t.y, merged ? MT_MERGED : MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4) {
     if (a.w.flags & SMEL_WSET_FAST_DQ)
@@ -648,6 +650,11 @@ extern "C" int smel_gmm_fwd_lr(const smel_wset* w, const int32_t* gkind, const i
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
   SMEL_REQUIRE(!(w->flags & SMEL_WSET_EXT2) || epilogue == 1, SMEL_EINVAL,
                "gmm_fwd: a two-plane LoRA extension belongs to the gate_up projection (epilogue 1)");
+  SMEL_REQUIRE(!(w->flags & SMEL_WSET_MERGED_LIST) ||
+                   (epilogue == 1 && (!w->q4 || ((w->flags & SMEL_WSET_FAST_DQ) && w->C % 64 == 0))),
+               SMEL_EINVAL,
+               "gmm_fwd: a merged tile list (SMEL_WSET_MERGED_LIST) needs the gate_up projection (epilogue 1) and, for "
+               "an int4 bank, its fast dequant form and K a multiple of 64");
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_fwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_fwd: A larger than 2 GiB");

@@ -21,7 +21,8 @@ WSET_FAST_DQ = 1     # smel_wset.flags: the int4 bank passed smel_int4_fast_ok
 WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up projection has two 32-wide planes
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
 WSET_MERGE_SHORT = 8 # smel_wset.flags: gate_up forward, a full int4 tile also takes the group's short last tile
-ABI_VERSION = 21
+WSET_MERGED_LIST = 16 # smel_wset.flags: gate_up forward on smel_dispatch's merged tile list (int4 tiles up to 160 rows)
+ABI_VERSION = 22
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 
@@ -92,8 +93,9 @@ SIGNATURES = {
     "smel_route_counted": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
     "smel_route_ld": (i64, [i64, i32]),
     "smel_route_logits": (i32, [vp, i64, i64, i64, vp, vp, vp, vp, vp]),
-    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
-    "smel_dispatch_counted": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "smel_dispatch": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp]),
+    "smel_dispatch_counted": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp,
+                                    vp]),
     "smel_dispatch_ws_size": (i64, [i64, i64]),
     "smel_dispatch_max_tiles": (i64, [i64, i64, i64, i32]),
     "smel_dispatch_noalloc": (i32, [vp, i32, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),

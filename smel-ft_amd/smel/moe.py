@@ -30,6 +30,7 @@ from . import moe_f32 as F32
 from .quant import dequant_int4, quantize_int4
 
 M_TILE = 128      # rows per GEMM tile (the tile list of smel_dispatch)
+M_MERGED = 160    # rows of a merged gate_up forward tile (a full tile + an int4 expert's last tile of <= 32 rows)
 EXT = 32          # width of one plane of the LoRA K-extension
 MAX_LORA_RANK = 32
 
@@ -369,8 +370,9 @@ _BWD_LORA_ROWS = os.environ.get("SMEL_BWD_LORA_ROWS", "1") == "1"
 # output between the two GEMMs
 _FWD_LORA_ROWS = os.environ.get("SMEL_FWD_LORA_ROWS", "1") == "1"
 # SMEL_MERGE_SHORT=1 (default): the gate_up forward takes an int4 expert's last tile of at most 32 rows together with
-# the full tile before it (one weight stream and dequant for up to 160 rows; banks in the fast dequant form); 0: every
-# tile of the list on its own
+# the full tile before it (one weight stream and dequant for up to 160 rows; banks in the fast dequant form): the
+# fused layer runs it on the dispatch's merged tile list, the frozen-experts path on its group-ordered count tiles;
+# 0: every tile of the list on its own
 _MERGE_SHORT = os.environ.get("SMEL_MERGE_SHORT", "1") == "1"
 
 
@@ -776,6 +778,10 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, tiles_g, ntiles, err = i32(maxt * 4), i32(maxt * 4), i32(1), i32(1)
+    # the gate_up forward's merged tile list: an int4 expert's last tile of <= 32 rows joins its full tile
+    fz = ex.frozen
+    merge = _MERGE_SHORT and isinstance(fz, Int4Experts) and H % 64 == 0 and fz.fast_dq("gu")
+    tiles_m, ntiles_m = (i32(maxt * 4), i32(1)) if merge else (None, None)
     dws = counted_ws if counted_ws is not None else i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))
     if prep is None:   # LoRA layouts on a side stream, overlapping the dispatch
         fork = _Fork(dev, 2)
@@ -785,7 +791,8 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     gk_groups = ex.gkind(shared is not None, dev)
     L.call("smel_dispatch_counted" if counted_ws is not None else "smel_dispatch", L.ptr(topi_ids), int(ids_i64), T, K,
            E, rows_sh, M_TILE, L.ptr(gk_groups), L.ptr(counts), L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles),
-           L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err), L.ptr(dws), st, tag="smel_dispatch")
+           L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err), M_MERGED if merge else 0, L.ptr(tiles_m), L.ptr(ntiles_m),
+           L.ptr(dws), st, tag="smel_dispatch")
     gk = None   # the tile list carries each tile's group kind
     sel_gu = sel_dn = None
     if ex.sel_ids is not None and len(ex._slot):
@@ -806,10 +813,11 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
         ext_gu = _lora_ext(tl, x, H, T, 1, order, TK, K, lb_ex, lb_sh, "a_gu", H, planes, M, dev, st)
     actb = bf(M, I)
     hsave = bf(M, 2 * I) if need_grad else None
-    # the gate_up GEMMs take the tiles in group order, a chunk per XCD (an expert's tiles share its weights in L2);
-    # the down GEMMs the long-tiles-first order (short tiles fill the last round)
+    # the gate_up forward takes the merged list (tile t on XCD t % 8, the merged tiles first) or else the tiles in
+    # group order, a chunk per XCD (an expert's tiles share its weights in L2); the down GEMMs the long-tiles-first
+    # order (short tiles fill the last round)
     w_gu = _wset(ex, "gu", sel_gu, sh_gu, g(lb_ex, "fwd_gu"), g(lb_sh, "fwd_gu"), planes=planes)
-    w_gu.flags |= L.WSET_XCD_CHUNK | (L.WSET_MERGE_SHORT if _MERGE_SHORT else 0)
+    w_gu.flags |= L.WSET_MERGED_LIST if merge else L.WSET_XCD_CHUNK
     # the down LoRA's rows come from the gate_up epilogue (per-column-block partials of h A_dn^T), summed and stored
     # by the down GEMM: no separate projection launch
     lr = None
@@ -819,7 +827,8 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
         ext_dn = bf(M, EXT)
         lr = L.FwdLoraRows(L.ptr(g(lb_ex, "a_dn")), L.ptr(g(lb_sh, "a_dn")), lb_ex.scale if lb_ex is not None else 0.0,
                            lb_sh.scale if lb_sh is not None else 0.0, L.ptr(xpart), parts, L.ptr(ext_dn))
-    L.call("smel_gmm_fwd_lr", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_g), L.ptr(ntiles), maxt, L.ptr(x), H, T, 1,
+    L.call("smel_gmm_fwd_lr", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_m if merge else tiles_g),
+           L.ptr(ntiles_m if merge else ntiles), maxt, L.ptr(x), H, T, 1,
            L.ptr(order), TK, K, L.ptr(ext_gu), 1, _ACT[ex.act], L.ptr(actb), I, L.ptr(hsave),
            ctypes.byref(lr) if lr is not None else None, st, tag="gemm_gu_fwd")
     if any_lora and lr is None:   # the down LoRA's rows as a projection launch of the gate_up output

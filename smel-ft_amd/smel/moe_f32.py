@@ -352,8 +352,8 @@ class RoutedFn(torch.autograd.Function):
         gk = ex.gkind(False, dev)
         ids = topi.contiguous()
         L.call("smel_dispatch", L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, 0, M_TILE, L.ptr(gk), L.ptr(counts),
-               L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err),
-               L.ptr(ws), st, tag="dispatch_f32")
+               L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(tiles_g), L.ptr(ntiles), L.ptr(err), 0,
+               None, None, L.ptr(ws), st, tag="dispatch_f32")
         record_err(err)
         tl = (tiles, ntiles, maxt)
         xs = torch.empty(TK, H, dtype=torch.float32, device=dev)

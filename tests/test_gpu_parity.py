@@ -383,7 +383,7 @@ def test_route_counted_then_dispatch_counted(T, H, E, K, shared):
                  topi=torch.zeros(T, K, dtype=torch.int64, device=DEV), topi32=i32(TK), sgate=f32(T),
                  lg=torch.zeros(T, lib.smel_route_ld(E, int(shared)), dtype=torch.bfloat16, device=DEV),
                  counts=i32(E), offsets=i32(E + 1), order=i32(TK), inv=i32(TK), tiles=i32(4 * maxt),
-                 tiles_g=i32(4 * maxt), ntiles=i32(1), err=i32(1))
+                 tiles_g=i32(4 * maxt), ntiles=i32(1), err=i32(1), tiles_m=i32(4 * maxt), ntiles_m=i32(1))
         ws = torch.randint(-1000, 1000, (max(1, lib.smel_dispatch_ws_size(TK, E)),), dtype=torch.int32, device=DEV)
         route = [L.ptr(xd), L.ptr(gwd), L.ptr(sgd), T, H, E, K] + [L.ptr(o[k]) for k in
                                                                    ("probs", "topv", "topv32", "topi", "topi32")] + \
@@ -394,7 +394,8 @@ def test_route_counted_then_dispatch_counted(T, H, E, K, shared):
             L.call("smel_route", *route, L.stream())
         L.call("smel_dispatch_counted" if counted else "smel_dispatch", L.ptr(o["topi32"]), 0, T, K, E, sh, 128,
                L.ptr(gk), *[L.ptr(o[k]) for k in ("counts", "offsets", "order", "inv", "tiles", "tiles_g", "ntiles",
-                                                  "err")], L.ptr(ws), L.stream())
+                                                  "err")], 160, L.ptr(o["tiles_m"]), L.ptr(o["ntiles_m"]), L.ptr(ws),
+               L.stream())
         torch.cuda.synchronize()
         return {k: v.cpu() for k, v in o.items()}
 
@@ -412,20 +413,23 @@ def test_route_counted_then_dispatch_counted(T, H, E, K, shared):
 # ------------------------------------------------------------------------------------------------------ dispatch
 
 
-def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128, gkind=None):
+def _dispatch(ids, T, K, E, shared_rows=0, m_tile=128, gkind=None, merge_rows=0):
     L = _lib()
     TK = T * K
     maxt = L.load().smel_dispatch_max_tiles(TK, E, shared_rows, m_tile)
     i32 = lambda n: torch.full((n,), -7, dtype=torch.int32, device=DEV)
     counts, offsets, order, inv = i32(E), i32(E + 1), i32(max(TK, 1)), i32(max(TK, 1))
     tiles, tiles_g, ntiles, err = i32(maxt * 4), i32(maxt * 4), i32(1), i32(1)
+    tiles_m, ntiles_m = i32(maxt * 4), i32(1)
     ws = i32(max(1, L.load().smel_dispatch_ws_size(TK, E)))   # garbage-filled: the kernels must not rely on zeros
     gk = torch.tensor(gkind, dtype=torch.int32, device=DEV) if gkind is not None else None
     L.call("smel_dispatch", L.ptr(ids), int(ids.dtype == torch.int64), T, K, E, shared_rows, m_tile, L.ptr(gk),
            L.ptr(counts), L.ptr(offsets), L.ptr(order), L.ptr(inv), L.ptr(tiles), L.ptr(tiles_g), L.ptr(ntiles),
-           L.ptr(err), L.ptr(ws), L.stream())
+           L.ptr(err), merge_rows, L.ptr(tiles_m) if merge_rows else None, L.ptr(ntiles_m) if merge_rows else None,
+           L.ptr(ws), L.stream())
     out = [a.cpu().numpy() for a in (counts, offsets, order, inv, tiles, ntiles, err)]
     _dispatch.grouped = tiles_g.cpu().numpy()
+    _dispatch.merged = (tiles_m.cpu().numpy(), int(ntiles_m[0]))
     return out
 
 
@@ -441,6 +445,24 @@ def _expected_tiles(offsets, E, TK, shared_rows, m_tile, grouped=False):
     if not grouped:
         out = [t for t in out if t[2] - t[1] > m_tile // 2] + [t for t in out if t[2] - t[1] <= m_tile // 2]
     return np.array(out, dtype=np.int32).reshape(-1, 4)
+
+
+def _expected_merged(offsets, E, TK, shared_rows, m_tile, gkind, merge_rows):
+    """The merged list: an int4-kind group's (gkind >> 16 == 0) last tile of at most merge_rows - m_tile rows joins
+    the full tile before it; the merged tiles, then the other tiles of more than m_tile / 2 rows, then the shorter
+    ones, each part in group order. Written from the rule itself, tile by tile."""
+    merged, long_, short = [], [], []
+    for g in range(E + (1 if shared_rows else 0)):
+        r0 = offsets[g] if g < E else TK
+        n = (offsets[g + 1] - offsets[g]) if g < E else shared_rows
+        t = [(g, r0 + i, r0 + min(n, i + m_tile), gkind[g]) for i in range(0, n, m_tile)]
+        if len(t) >= 2 and gkind[g] >> 16 == 0 and t[-1][2] - t[-1][1] <= merge_rows - m_tile:
+            last = t.pop()
+            full = t.pop()
+            merged.append((g, full[1], last[2], gkind[g]))
+        for x in t:
+            (long_ if x[2] - x[1] > m_tile // 2 else short).append(x)
+    return np.array(merged + long_ + short, dtype=np.int32).reshape(-1, 4)
 
 
 def _zipf_topi(T, K, E, s, gen):
@@ -471,7 +493,7 @@ def test_dispatch_bitexact(T, K, E, shared, kind):
         # with int64 ids, also hand over group kinds: the tile list then carries them in its fourth field
         gkind = [(g * 7919) & 0x3ffff for g in range(E + 1)] if dt == torch.int64 else None
         counts, offsets, order, inv, tiles, ntiles, err = _dispatch(torch.from_numpy(topi).to(DEV, dt), T, K, E, sh,
-                                                                    gkind=gkind)
+                                                                    gkind=gkind, merge_rows=160 if gkind else 0)
         c0, o0, ord0, inv0 = intref.dispatch(topi, E)
         assert err[0] == 0
         assert np.array_equal(counts, c0) and np.array_equal(offsets, o0)
@@ -485,6 +507,14 @@ def test_dispatch_bitexact(T, K, E, shared, kind):
         assert ntiles[0] == len(want)
         assert np.array_equal(tiles.reshape(-1, 4)[:len(want)], want)
         assert np.array_equal(_dispatch.grouped.reshape(-1, 4)[:len(want)], want_g)
+        if gkind is not None:   # the merged list for the gate_up forward: every row in exactly one tile
+            want_m = _expected_merged(o0, E, T * K, sh, 128, np.asarray(gkind, np.int32), 160)
+            got_m, n_m = _dispatch.merged
+            assert n_m == len(want_m) and np.array_equal(got_m.reshape(-1, 4)[:n_m], want_m)
+            cover = np.zeros(T * K + sh, np.int32)
+            for _, a, b, _k in want_m:
+                cover[a:b] += 1
+            assert (cover == 1).all()
 
 
 def test_dispatch_flags_bad_ids():

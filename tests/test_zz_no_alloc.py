@@ -22,7 +22,7 @@ def _run(entry, ids, T, K, E, shared_rows, gkind):
            [L.ptr(out[k]) for k in ("counts", "offsets", "order", "inv", "tiles", "tiles_g", "ntiles", "err")]
     if entry == "smel_dispatch":
         ws = torch.empty(max(1, lib.smel_dispatch_ws_size(TK, E)), dtype=torch.int32, device=DEV)
-        L.call(entry, *args, L.ptr(ws), L.stream())
+        L.call(entry, *args, 0, None, None, L.ptr(ws), L.stream())
     else:
         L.call(entry, *args, L.stream())
     torch.cuda.synchronize()
