@@ -185,7 +185,7 @@ int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scal
  * err [1]: bit 0 set if an id is outside [0, E) (that slot is dropped, its
  * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
  * workspace. E <= 512.
- * merge_rows (0: off; m_tile < merge_rows <= 2 m_tile, needs gkind): also the merged list tiles_merged [max_tiles][4]
+ * merge_rows (0: off; m_tile < merge_rows <= 1.5 m_tile, needs gkind): also the merged list tiles_merged [max_tiles][4]
  * (n_tiles_merged [1] of them) for the gate_up forward with SMEL_WSET_MERGED_LIST: a group of kind SMEL_KIND_INT4
  * whose last tile has at most merge_rows - m_tile rows gets it joined to the full tile before it (one tile of up to
  * merge_rows rows); order: those merged tiles, then the other tiles of more than m_tile / 2 rows, then the shorter

@@ -47,39 +47,50 @@ SMEL_DEV int block_exclusive_scan(int v, int* wsum /* [NW] LDS */, int& total) {
   return base + inc - v;
 }
 
-// Exclusive scan of three values at once over the block (the latency of one scan); tot = the block totals. wsum is
-// not reused afterwards, so there is no trailing barrier.
+// Exclusive scan of N triples at once over the block (the latency of one scan); v is replaced by its exclusive
+// prefix, tot = the block totals. wsum is not reused afterwards, so there is no trailing barrier.
 struct I3 {
   int a, b, c;
 };
-SMEL_DEV I3 block_exclusive_scan3(I3 v, I3* wsum /* [NW] LDS */, I3& tot) {
+template <int N>
+SMEL_DEV void block_exclusive_scan3(I3 (&v)[N], I3 (*wsum)[N] /* [NW][N] LDS */, I3 (&tot)[N]) {
   const int l = lane_id(), w = threadIdx.x >> 6;
-  I3 inc = v;
+  I3 inc[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) inc[n] = v[n];
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int ya = __shfl_up(inc.a, o, 64), yb = __shfl_up(inc.b, o, 64), yc = __shfl_up(inc.c, o, 64);
-    if (l >= o) {
-      inc.a += ya;
-      inc.b += yb;
-      inc.c += yc;
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const int ya = __shfl_up(inc[n].a, o, 64), yb = __shfl_up(inc[n].b, o, 64), yc = __shfl_up(inc[n].c, o, 64);
+      if (l >= o) {
+        inc[n].a += ya;
+        inc[n].b += yb;
+        inc[n].c += yc;
+      }
     }
   }
-  if (l == 63) wsum[w] = inc;
+  if (l == 63)
+#pragma unroll
+    for (int n = 0; n < N; ++n) wsum[w][n] = inc[n];
   lds_barrier();
-  I3 base{0, 0, 0}, t{0, 0, 0};
-  for (int j = 0; j < NW; ++j) {
-    const I3 s = wsum[j];
-    if (j < w) {
-      base.a += s.a;
-      base.b += s.b;
-      base.c += s.c;
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    I3 base{0, 0, 0}, t{0, 0, 0};
+    for (int j = 0; j < NW; ++j) {
+      const I3 s = wsum[j][n];
+      if (j < w) {
+        base.a += s.a;
+        base.b += s.b;
+        base.c += s.c;
+      }
+      t.a += s.a;
+      t.b += s.b;
+      t.c += s.c;
     }
-    t.a += s.a;
-    t.b += s.b;
-    t.c += s.c;
+    tot[n] = t;
+    v[n] = I3{base.a + inc[n].a - v[n].a, base.b + inc[n].b - v[n].b, base.c + inc[n].c - v[n].c};
   }
-  tot = t;
-  return I3{base.a + inc.a - v.a, base.b + inc.b - v.b, base.c + inc.c - v.c};
 }
 
 SMEL_DEV int id_at(const void* ids, int is64, int p) {
@@ -106,7 +117,8 @@ SMEL_DEV I3 merged_counts(int rows, int m_tile, int merge_rows, bool int4) {
   return I3{a, nt - 1 - a + last_long, (!a && !last_long) ? 1 : 0};
 }
 struct TileLds {
-  int lb[MAXE + 1], sb[MAXE + 1], mb[MAXE + 1], row0[MAXE + 1], rows[MAXE + 1], nt[MAXE + 1], gk[MAXE + 1];
+  int lb[MAXE + 1], sb[MAXE + 1], mb[MAXE + 1], ma[MAXE + 1], row0[MAXE + 1], rows[MAXE + 1], nt[MAXE + 1],
+      gk[MAXE + 1];
 };
 // Tile list over groups 0..E-1 (+ shared group E): the tiles of more than m_tile / 2 rows first (in group order), then
 // the shorter last tiles of the groups (in group order). The grouped GEMMs start tiles in list order, so the short
@@ -126,6 +138,7 @@ SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt
     t.lb[tid] = lbase;
     t.sb[tid] = sbase;
     t.mb[tid] = mpos.b;
+    t.ma[tid] = mc.a;
     t.row0[tid] = row0;
     t.rows[tid] = rows;
     t.nt[tid] = nt;
@@ -145,7 +158,17 @@ SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt
     }
     return lo;
   };
-  auto put = [&](int g, int i, int pos) {
+  // merged list: a long tile is also the merged list's full / long tile i of its group (at mtot.a + mb[g] + i), except
+  // the one that a merged group's short last tile joins (that one the group's own thread writes)
+  auto put = [&](int g, int i, int pos, bool is_long) {
+    if (tiles_m && is_long && !(t.ma[g] && i >= t.nt[g] - 2)) {
+      const int mp = mtot.a + t.mb[g] + i;
+      if (mp < max_tiles) {
+        const int r0 = t.row0[g];
+        reinterpret_cast<int4*>(tiles_m)[mp] =
+            int4{g, r0 + i * m_tile, min(r0 + t.rows[g], r0 + (i + 1) * m_tile), t.gk[g]};
+      }
+    }
     if (pos >= max_tiles) return;
     const int r0 = t.row0[g];
     int4 tl;
@@ -159,11 +182,11 @@ SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt
   };
   for (int q = tid; q < n_long; q += DB) {
     const int g = group_of(t.lb, q);
-    put(g, q - t.lb[g], q);
+    put(g, q - t.lb[g], q, true);
   }
   for (int q = tid; q < n_short; q += DB) {   // only a group's last tile can be short
     const int g = group_of(t.sb, q);
-    put(g, t.nt[g] - 1, n_long + q);
+    put(g, t.nt[g] - 1, n_long + q, false);
   }
   if (tid == 0) {
     const int total_tiles = n_long + n_short;
@@ -184,17 +207,12 @@ SMEL_DEV void store_tiles(TileLds& t, int tid, int G, int rows, int row0, int nt
     if (mc.a) putm(tid, row0 + (nt - 2) * m_tile, row0 + rows, mpos.a);
     if (mc.c) putm(tid, row0 + (nt - 1) * m_tile, row0 + rows, mtot.a + mtot.b + mpos.c);
   }
-  for (int q = tid; q < mtot.b; q += DB) {   // full / long tile i of its group
-    const int g = group_of(t.mb, q);
-    const int i = q - t.mb[g], r0 = t.row0[g];
-    putm(g, r0 + i * m_tile, min(r0 + t.rows[g], r0 + (i + 1) * m_tile), mtot.a + q);
-  }
   if (tid == 0) n_tiles_m[0] = min(mtot.a + mtot.b + mtot.c, max_tiles);   // never longer than tiles
 }
 
 // The tile list from the offsets off_s[0..E] (LDS). Called by every thread of one block (block scans inside).
 SMEL_DEV void write_tiles(TileLds& tl, int tid, int E, int TK, int shared_rows, int m_tile, int max_tiles, int gkv,
-                          const int* off_s, int bad, int* wsum, I3* wsum3, int32_t* __restrict__ tiles,
+                          const int* off_s, int bad, int* wsum, I3 (*wsum3)[1], int32_t* __restrict__ tiles,
                           int32_t* __restrict__ tiles_g, int32_t* __restrict__ n_tiles, int32_t* __restrict__ err,
                           int merge_rows, bool has_gk, int32_t* __restrict__ tiles_m, int32_t* __restrict__ n_tiles_m) {
   const int G = E + (shared_rows > 0 ? 1 : 0);
@@ -209,10 +227,10 @@ SMEL_DEV void write_tiles(TileLds& tl, int tid, int E, int TK, int shared_rows, 
   const int lbase = block_exclusive_scan(nlong, wsum, n_long);
   const int sbase = block_exclusive_scan(nt - nlong, wsum, n_short);
   const I3 mc = merged_counts(rows, m_tile, tiles_m ? merge_rows : 0, has_gk && (gkv >> 16) == SMEL_KIND_INT4);
-  I3 mtot;
-  const I3 mpos = block_exclusive_scan3(mc, wsum3, mtot);
+  I3 mv[1] = {mc}, mtot[1];
+  block_exclusive_scan3<1>(mv, wsum3, mtot);
   store_tiles(tl, tid, G, rows, row0, nt, lbase, sbase, n_long, n_short, m_tile, max_tiles, gkv, bad, tiles, tiles_g,
-              n_tiles, err, mc, mpos, mtot, tiles_m, n_tiles_m);
+              n_tiles, err, mc, mv[0], mtot[0], tiles_m, n_tiles_m);
 }
 
 // (1) hist[b][e] = slots of block b routed to expert e; bad[b] = 1 if block b holds an id outside [0, E)
@@ -248,7 +266,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan(int nb, int TK, int E, int
                                                       int32_t* __restrict__ tiles_m,
                                                       int32_t* __restrict__ n_tiles_m) {
   __shared__ int wsum[NW];
-  __shared__ I3 wsum3[NW];
+  __shared__ I3 wsum3[NW][1];
   __shared__ int off_s[MAXE + 1];
   __shared__ int bad_s;
   __shared__ int hs[HCH];
@@ -380,7 +398,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_scatter(const void* __rest
                                                               int32_t* __restrict__ tiles_m,
                                                               int32_t* __restrict__ n_tiles_m) {
   __shared__ int cnt[NW * MAXE];   // per-wave counts, then per-wave first positions
-  __shared__ I3 wsum[NW], wsum_m[NW];
+  __shared__ I3 wsum[NW][2];
   __shared__ int bad_s;
   __shared__ TileLds tl;
   const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, b = blockIdx.x;
@@ -430,20 +448,19 @@ __global__ __launch_bounds__(1024) void dispatch_scan_scatter(const void* __rest
   }
   const int rows = tid < E ? total : (tid < G ? shared_rows : 0);
   const int nt = tiles_of(rows, m_tile), nlong = long_tiles_of(rows, m_tile);
-  I3 tot;
-  const I3 ex = block_exclusive_scan3(I3{tid < E ? total : 0, nlong, nt - nlong}, wsum, tot);   // its barrier also
-                                                                                                // completes cnt, bad_s
+  // (offsets, long tiles, short tiles) and, for the lead block's merged list, its three tile classes: one scan
+  const I3 mc = merged_counts(rows, m_tile, lead && tiles_m ? merge_rows : 0, gkind && (gkv >> 16) == SMEL_KIND_INT4);
+  I3 sv[2] = {I3{tid < E ? total : 0, nlong, nt - nlong}, mc}, stot[2];
+  block_exclusive_scan3<2>(sv, wsum, stot);   // its barrier also completes cnt, bad_s
+  const I3 ex = sv[0], tot = stot[0];
   if (lead) {
     if (tid < E) {
       counts[tid] = total;
       offsets[tid] = ex.a;
     }
     if (tid == 0) offsets[E] = tot.a;
-    const I3 mc = merged_counts(rows, m_tile, tiles_m ? merge_rows : 0, gkind && (gkv >> 16) == SMEL_KIND_INT4);
-    I3 mtot;
-    const I3 mpos = block_exclusive_scan3(mc, wsum_m, mtot);
     store_tiles(tl, tid, G, rows, tid < E ? ex.a : TK, nt, ex.b, ex.c, tot.b, tot.c, m_tile, max_tiles, gkv, bad_s,
-                tiles, tiles_g, n_tiles, err, mc, mpos, mtot, tiles_m, n_tiles_m);
+                tiles, tiles_g, n_tiles, err, mc, sv[1], stot[1], tiles_m, n_tiles_m);
   }
   // first output position of wave j's slots of expert tid
   if (tid < E) {
@@ -514,10 +531,10 @@ int dispatch_impl(const void* ids, int32_t ids_are_i64, int64_t T, int64_t K, in
                   int32_t* tiles, int32_t* tiles_grouped, int32_t* n_tiles, int32_t* err, int32_t merge_rows,
                   int32_t* tiles_merged, int32_t* n_tiles_merged, int32_t* ws, bool counted, hipStream_t stream) {
   SMEL_REQUIRE(T >= 0 && K > 0 && E > 0 && shared_rows >= 0 && m_tile > 0, SMEL_EINVAL, "dispatch: bad sizes");
-  SMEL_REQUIRE(merge_rows == 0 || (merge_rows > m_tile && merge_rows <= 2 * m_tile && tiles_merged &&
+  SMEL_REQUIRE(merge_rows == 0 || (merge_rows > m_tile && 2 * merge_rows <= 3 * m_tile && tiles_merged &&
                                    n_tiles_merged && gkind),
                SMEL_EINVAL,
-               "dispatch: a merged tile list needs m_tile < merge_rows <= 2 m_tile (got %d, m_tile %d), its outputs "
+               "dispatch: a merged tile list needs m_tile < merge_rows <= 1.5 m_tile (got %d, m_tile %d), its outputs "
                "and the group kinds", merge_rows, m_tile);
   if (merge_rows == 0) tiles_merged = n_tiles_merged = nullptr;
   SMEL_REQUIRE(E <= MAXE, SMEL_EUNSUPPORTED, "dispatch: E=%lld > %d experts", (long long)E, MAXE);

@@ -93,6 +93,19 @@ def test_host_side_rejections():
     L = _lib.load()
     assert L.smel_dispatch_max_tiles(32736, 256, 4092, 128) == (32736 + 127) // 128 + 256 + 32 + 1
     assert L.smel_dispatch_ws_size(32736, 256) == 32 * 256 + 32 and L.smel_dispatch_ws_size(0, 8) == 0
+    # dispatch: a merged tile list needs 128 < merge_rows <= 192, its outputs and the group kinds
+    d = (16, 0, 4, 2, 8, 0, 128)
+    for mr, gk, tm in ((200, 16, 16), (160, None, 16), (160, 16, None), (100, 16, 16)):
+        assert L.smel_dispatch(*d, gk, 16, 16, 16, 16, 16, 16, 16, 16, mr, tm, 16, 16, None) == -1
+        assert b"merged tile list" in L.smel_last_error()
+    # gmm_fwd: the merged list on an int4 bank without the fast dequant form, or on the down projection
+    wm = _lib.WSet()
+    wm.R, wm.C, wm.group, wm.q4, wm.sz4, wm.flags = 1024, 2048, 64, 16, 16, _lib.WSET_MERGED_LIST
+    for epi, flags in ((1, _lib.WSET_MERGED_LIST), (0, _lib.WSET_MERGED_LIST | _lib.WSET_FAST_DQ)):
+        wm.flags = flags
+        assert L.smel_gmm_fwd(ctypes.byref(wm), None, 16, 16, 1, 16, 2048, 4, 0, None, 0, 1, None, epi, 0, 16, 1024,
+                              16, None) == -1
+        assert b"merged tile list" in L.smel_last_error()
     # route: too many experts
     rc = L.smel_route(1, 1, None, 4, 64, 600, 8, 1, 1, None, 1, 1, None, 1, None)
     assert rc == -2 and b"E=600" in L.smel_last_error()
