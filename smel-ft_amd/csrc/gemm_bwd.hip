@@ -374,17 +374,17 @@ SMEL_DEV void run_tile(const BwdArgs& a, int kind, int idx, int row0, int nrows,
       __builtin_amdgcn_s_barrier();
       issue_b(i + 2, bA);
       issue_lds(i + 4, 0, nullptr);
-      compute(1, bB);
+      if (i + 1 < nk) compute(1, bB);   // steps past K: loads of zeros, no compute
       wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 3, bB);
       issue_lds(i + 5, 1, nullptr);
-      compute(2, bA);
+      if (i + 2 < nk) compute(2, bA);
       wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 4, bA);
       issue_lds(i + 6, 2, nullptr);
-      compute(3, bB);
+      if (i + 3 < nk) compute(3, bB);
     }
   }
   wait_vm<0>();   // the ring's trailing (out-of-range) loads

@@ -244,7 +244,8 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     issue(0, q0, szc, S0);
     issue(1, q1, nullptr, S1);
     issue(2, q2, nullptr, S2);
-    // ceil(nk / 4) * 4 steps, branch-free: a step past K loads zeros and adds nothing
+    // ceil(nk / 4) * 4 steps of loads and barriers (a load past K reads zeros); the computes of steps past K are
+    // skipped (uniform branches)
     for (int i = 0; i < nk; i += 4) {
       wait_vm_lds<q4_wait(0, VMA)>();
       __builtin_amdgcn_s_barrier();
@@ -253,15 +254,15 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       wait_vm_lds<q4_wait(1, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 4, q0, szn, S0);
-      compute(S1, q1, 1);
+      if (i + 1 < nk) compute(S1, q1, 1);
       wait_vm_lds<q4_wait(2, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 5, q1, nullptr, S1);
-      compute(S2, q2, 2);
+      if (i + 2 < nk) compute(S2, q2, 2);
       wait_vm_lds<q4_wait(3, VMA)>();
       __builtin_amdgcn_s_barrier();
       issue(i + 6, q2, nullptr, S2);
-      compute(S3, q3, 3);
+      if (i + 3 < nk) compute(S3, q3, 3);
       szc[0] = szn[0];
       szc[1] = szn[1];
     }
@@ -329,17 +330,17 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       __builtin_amdgcn_s_barrier();
       issue_w(i + 3, q3, z3);
       issue_a(i + 4, S0);
-      compute(S1, q1, z1);
+      if (i + 1 < nk) compute(S1, q1, z1);
       wait_vm_lds<q4_wait_w2(VMA)>();
       __builtin_amdgcn_s_barrier();
       issue_w(i + 4, q0, z0);
       issue_a(i + 5, S1);
-      compute(S2, q2, z2);
+      if (i + 2 < nk) compute(S2, q2, z2);
       wait_vm_lds<q4_wait_w2(VMA)>();
       __builtin_amdgcn_s_barrier();
       issue_w(i + 5, q1, z1);
       issue_a(i + 6, S2);
-      compute(S3, q3, z3);
+      if (i + 3 < nk) compute(S3, q3, z3);
     }
   } else {
     // bf16 weights: 8 loads per fragment pair and step, one step ahead in two alternating register sets; A three
@@ -387,17 +388,17 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
       __builtin_amdgcn_s_barrier();
       issue_b(i + 2, bA);
       issue_a(i + 4, S0);
-      compute(S1, bB);
+      if (i + 1 < nk) compute(S1, bB);   // steps past K: loads of zeros, no compute
       wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 3, bB);
       issue_a(i + 5, S1);
-      compute(S2, bA);
+      if (i + 2 < nk) compute(S2, bA);
       wait_vm_lds<BF_WAIT>();
       __builtin_amdgcn_s_barrier();
       issue_b(i + 4, bA);
       issue_a(i + 6, S2);
-      compute(S3, bB);
+      if (i + 3 < nk) compute(S3, bB);
     }
   }
   wait_vm<0>();   // the ring's trailing (out-of-range) loads
