@@ -1419,14 +1419,27 @@ def _moe_forward_f32(x2d, W, ex: LayerExperts, top_k: int, lora_layer, stats):
     return F32.GateAddFn.apply(y, F32.f32(x2d), F32.f32(W["mlp.shared_expert_gate.weight"], "shared gate"), routed)
 
 
-def _count_tiles(counts: list, device):
+def _count_tiles(counts: list, device, order: str = "group"):
     """Tile list of 128-row tiles over contiguous row groups of the given (host) sizes: rows of group e are
-    [sum(counts[:e]), +counts[e]). Returns (tiles, n_tiles, max_tiles) as the grouped GEMMs take them."""
+    [sum(counts[:e]), +counts[e]). order "group": in group order; "long": the tiles of more than 64 rows first, then
+    the short ones (as smel_dispatch's tiles); "merged": a group's last tile of at most 32 rows joined to its full
+    tile, then that merged-first, long, short order (as smel_dispatch's tiles_merged, every group of the int4 kind).
+    Returns (tiles, n_tiles, max_tiles) as the grouped GEMMs take them."""
     tl, row = [], 0
+    merged, long_, short = [], [], []
     for e, c in enumerate(counts):
-        for r0 in range(row, row + c, M_TILE):
-            tl.append((e, r0, min(row + c, r0 + M_TILE), 0))
+        t = [(e, r0, min(row + c, r0 + M_TILE), 0) for r0 in range(row, row + c, M_TILE)]
         row += c
+        if order == "group":
+            tl += t
+            continue
+        if order == "merged" and len(t) >= 2 and t[-1][2] - t[-1][1] <= M_MERGED - M_TILE:
+            last, full = t.pop(), t.pop()
+            merged.append((e, full[1], last[2], 0))
+        for x in t:
+            (long_ if x[2] - x[1] > M_TILE // 2 else short).append(x)
+    if order != "group":
+        tl = merged + long_ + short
     n = len(tl)
     t = torch.tensor(tl or [(0, 0, 0, 0)], dtype=torch.int32).reshape(-1).to(device)
     return t, torch.tensor([n], dtype=torch.int32).to(device), n
@@ -1478,18 +1491,23 @@ class FrozenExpertsFn(torch.autograd.Function):
         dev = xs.device
         st = L.stream()
         w_gu, w_dn = _bank_wset(bank, "gu"), _bank_wset(bank, "dn")
-        w_gu.flags |= L.WSET_MERGE_SHORT if _MERGE_SHORT else 0   # the count tiles are in group order
+        # the gate_up forward on the merged list (int4 banks in the fast form, H a multiple of 64), the other GEMMs on
+        # the long-first list, as in the fused layer
+        merge = _MERGE_SHORT and isinstance(bank, Int4Experts) and (w_gu.flags & L.WSET_FAST_DQ) and H % 64 == 0
+        if merge:
+            w_gu.flags |= L.WSET_MERGED_LIST
         I = w_dn.C
         bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
         out = bf(rows, H)
         ctx.plan = None
         if rows == 0:
             return out
-        tiles, ntiles, maxt = _count_tiles(counts, dev)
+        tiles, ntiles, maxt = _count_tiles(counts, dev, "long")
+        tiles_gu, ntiles_gu, maxt_gu = _count_tiles(counts, dev, "merged") if merge else (tiles, ntiles, maxt)
         gk = _bank_gkind(bank, dev)
         actb, hsave = bf(rows, I), bf(rows, 2 * I)
-        L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(xs), H, rows,
-               0, None, 0, 1, None, 1, _ACT[act_name], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_frozen_gu_fwd")
+        L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_gu), L.ptr(ntiles_gu), maxt_gu, L.ptr(xs), H,
+               rows, 0, None, 0, 1, None, 1, _ACT[act_name], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_frozen_gu_fwd")
         L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, rows,
                0, None, 0, 1, None, 0, _ACT[act_name], L.ptr(out), H, None, st, tag="gemm_frozen_dn_fwd")
         ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, act_name)
