@@ -68,8 +68,8 @@ typedef struct smel_wset {
  * group's last tile of at most 32 rows (the weights are streamed and dequantized once for up to 160 rows); that
  * tile's own blocks do nothing. */
 #define SMEL_WSET_MERGE_SHORT 8
-/* SMEL_WSET_MERGED_LIST (smel_gmm_fwd, gate_up projection, int4 bank with SMEL_WSET_FAST_DQ, C a multiple of 64):
- * the tile list is smel_dispatch's tiles_merged, whose int4 tiles may hold up to 160 rows (a full tile and the
+/* SMEL_WSET_MERGED_LIST (smel_gmm_fwd, either projection; an int4 bank needs SMEL_WSET_FAST_DQ and C a multiple of
+ * 64): the tile list is smel_dispatch's tiles_merged, whose int4 tiles may hold up to 160 rows (a full tile and the
  * group's last tile of at most 32 rows); each is one tile (one weight stream and dequant), and no block idles.
  * Without it a tile of the list has at most 128 rows (rows past 128 are not computed). */
 #define SMEL_WSET_MERGED_LIST 16
@@ -186,7 +186,7 @@ int smel_route_gemma4_prenorm_bwd(const uint16_t* h, const uint16_t* router_scal
  * inv = -1), bit 1 if the tile list overflowed max_tiles. ws [smel_dispatch_ws_size(T*K, E)] int32 is the caller's
  * workspace. E <= 512.
  * merge_rows (0: off; m_tile < merge_rows <= 1.5 m_tile, needs gkind): also the merged list tiles_merged [max_tiles][4]
- * (n_tiles_merged [1] of them) for the gate_up forward with SMEL_WSET_MERGED_LIST: a group of kind SMEL_KIND_INT4
+ * (n_tiles_merged [1] of them) for the forward GEMMs with SMEL_WSET_MERGED_LIST: a group of kind SMEL_KIND_INT4
  * whose last tile has at most merge_rows - m_tile rows gets it joined to the full tile before it (one tile of up to
  * merge_rows rows); order: those merged tiles, then the other tiles of more than m_tile / 2 rows, then the shorter
  * ones, each part in group order. */

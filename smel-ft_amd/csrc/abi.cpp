@@ -18,4 +18,4 @@ void set_error(const char* fmt, ...) {
 }  // namespace smel
 
 extern "C" const char* smel_last_error(void) { return g_msg; }
-extern "C" int smel_abi_version(void) { return 22; }
+extern "C" int smel_abi_version(void) { return 23; }

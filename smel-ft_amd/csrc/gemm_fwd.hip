@@ -6,9 +6,10 @@
 // smel/moe.py:58-72, 110-117, 204-211 and smel/lora.py:61-83.
 //
 // Block = 4 waves, tile = up to 128 rows of one group (4 slices of 32) x (gate_up: 32 gate + 32 up columns per wave;
-// down: 64 columns per wave); the gate_up projection of an int4 group also takes up to 160 rows (5 slices) when a
-// full tile and the group's last tile of at most 32 rows are merged (SMEL_WSET_MERGE_SHORT): the weights are then
-// streamed and dequantized once for all of the group's rows. MFMA 32x32x16 bf16. Per 64-wide k-step:
+// down: 64 columns per wave); a tile of an int4 group also takes up to 160 rows (5 slices) when a full tile and the
+// group's last tile of at most 32 rows are merged (SMEL_WSET_MERGED_LIST, both projections; SMEL_WSET_MERGE_SHORT,
+// gate_up only): the weights are then streamed and dequantized once for all of the group's rows. MFMA 32x32x16 bf16.
+// Per 64-wide k-step:
 //  * A (activation rows, gathered by token) goes global -> LDS directly (16-B LDS-DMA loads, 1 KB per wave-load, no
 //    registers), into a ring of 4 stages; each 128-B row's 16-B chunks are XOR-swizzled so the fragment reads are
 //    bank-conflict free. Every wave reads all rows of a stage.
@@ -26,11 +27,14 @@
 namespace {
 
 constexpr int MT = 128;            // rows of a tile of the tile list
-constexpr int MT_MERGED = 160;     // rows of a merged gate_up tile: a full tile + a last tile of <= 32 rows
+constexpr int MT_MERGED = 160;     // rows of a merged tile: a full tile + a last tile of <= 32 rows
 constexpr int KT = 64;
-// Rows an A stage holds (row r at r * KT bf16, no padding): 160 for the gate_up projection (the merged tiles; its
-// epilogue keeps the g and u tiles of 160 x 128 in the four stages), 128 for the down projection.
-constexpr int stage_rows(int epi) { return epi == 1 ? MT_MERGED : MT; }
+// An A stage holds MT_MERGED rows (row r at r * KT bf16, no padding; the four stages are contiguous). The gate_up
+// epilogue keeps the g and u tiles of 160 x 128 in them; the down epilogue its output tile. A tile of at most MT rows
+// leaves rows MT.. of every stage alone: the down projection keeps its LoRA rows (stages 0 and 1) and its rows'
+// output slots (stage 2) there.
+constexpr int STAGE = MT_MERGED * KT;   // bf16 elements of a stage
+constexpr int SPARE = MT * KT;          // first element of a stage's rows past MT
 
 // Vector-memory operations per wave in each issue group of the main loops; the issue code below is written with
 // these counts and every wait is computed from them (vmcnt retires in issue order).
@@ -73,7 +77,7 @@ struct FwdArgs {
 template <int EPI, bool Q4, int NS, bool FAST>
 SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows, int nb, uint16_t* S0, uint16_t* S1,
                        uint16_t* S2, uint16_t* S3, int* rowmap, uint16_t* X) {
-  static_assert(NS * 32 <= stage_rows(EPI), "the tile's rows fit the A stages");
+  static_assert(NS * 32 <= MT_MERGED, "the tile's rows fit the A stages");
   constexpr int VMA = vm_a(NS);               // A wave-loads per wave and stage
   constexpr int BF_WAIT = VMA;                // bf16: issue order ... B(j+1), A(j+3): before step j only A(j+2)
   const int tid = threadIdx.x, l = lane_id(), hi = l >> 5, r32 = l & 31;
@@ -83,7 +87,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
   // output slot of tile row t (thread t < MT) for the down projection, fetched now so that no load sits between the
   // epilogue's stores
   int ep_slot = 0;
-  if (EPI == 0 && tid < nrows) ep_slot = row_slot(row0 + tid, a.order, a.TK);
+  if (EPI == 0 && NS <= 4 && tid < nrows) ep_slot = row_slot(row0 + tid, a.order, a.TK);
   // ---- this wave's two 32-row weight fragments: gate/up pair for epilogue 1, two adjacent fragments else
   int n0, n1, fr0, fr1;
   bool fv0, fv1;
@@ -124,8 +128,9 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     wo1 = fv1 ? (uint32_t)(fr1 * nk * 4096 + l * 16) : OOB;
   }
   // ---- down LoRA rows from the gate_up forward's per-column-block partials (LoRA tiles of the down projection):
-  // summed in block order into the bf16 tile X [128][32] before the main loop (no accumulator is live yet); the same
-  // rows in every column block of the tile, column block 0 also stores them for the LoRA gradients
+  // summed in block order into the bf16 tile X [128][32] before the main loop (no accumulator is live yet; rows 0..63
+  // at X, rows 64..127 at X + STAGE: the spare rows of stages 0 and 1); the same rows in every column block of the
+  // tile, column block 0 also stores them for the LoRA gradients
   if (EPI == 0 && a.lr_on && a.lr.part &&
       ((kind == SMEL_KIND_SEL && ws.ext_sel) || (kind == SMEL_KIND_SHARED && ws.ext_sh))) {
     const int P = a.lr.parts;
@@ -144,7 +149,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
         }
       }
       const u32x4_t h = u32x4_t{pack2bf(v[0], v[1]), pack2bf(v[2], v[3]), pack2bf(v[4], v[5]), pack2bf(v[6], v[7])};
-      *reinterpret_cast<u32x4_t*>(X + row * 32 + k0) = h;
+      *reinterpret_cast<u32x4_t*>(X + pass * STAGE + (row & 63) * 32 + k0) = h;
       if (nb == 0 && a.lr.ext_out && row < nrows)
         *reinterpret_cast<u32x4_t*>(a.lr.ext_out + (int64_t)(row0 + row) * 32 + k0) = h;
     }
@@ -424,7 +429,9 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const uint32_t o = row < nrows ? (uint32_t)row * xb + 32 * hi + 16 * s : OOB;
-        const u32x4_t af = xrows ? *reinterpret_cast<const u32x4_t*>(X + row * 32 + 16 * hi + 8 * s) : ld16(rx, o);
+        const u32x4_t af =
+            xrows ? *reinterpret_cast<const u32x4_t*>(X + (m >> 1) * STAGE + (row & 63) * 32 + 16 * hi + 8 * s)
+                  : ld16(rx, o);
         const u32x4_t af1 = two ? ld16(rx, o == OOB ? OOB : o + 64) : af;
         acc[m][0] = mfma32(af, b0[s], acc[m][0]);
         acc[m][1] = mfma32(af1, b1[s], acc[m][1]);
@@ -451,7 +458,7 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
     // g tile [160][128] in S0 (rows 0..HALF-1) / S1 (rows HALF..), u tile in S2 / S3 (a stage holds HALF rows of 128
     // columns); column = 32 w + r32 inside the block's 128. Which stage a row goes to is known at compile time: HALF is
     // a multiple of 8 and a lane's part of acc_row is below 8.
-    constexpr int HALF = stage_rows(1) / 2;
+    constexpr int HALF = MT_MERGED / 2;
     const int col = 32 * w + r32;
 #pragma unroll
     for (int m = 0; m < NS; ++m) {
@@ -520,6 +527,44 @@ SMEL_DEV void run_tile(const FwdArgs& a, int kind, int idx, int row0, int nrows,
         }
       }
     }
+  } else if constexpr (NS == 5) {
+    // merged tile: out tile [160][256] over the four contiguous stages, row r at S0 + 256 r; column = 64 w + 32 f +
+    // r32 inside the block's 256. Thread -> (row, two 8-column chunks): 16 threads per row, 16 rows per pass; the
+    // output slots of a thread's 10 rows are loaded before the tile goes to LDS (no row table: the tile fills the LDS)
+    const int ch = tid & 15;
+    int slot[MT_MERGED / 16];
+#pragma unroll
+    for (int p = 0; p < MT_MERGED / 16; ++p) {
+      const int row = (tid >> 4) + 16 * p;
+      slot[p] = row < nrows ? row_slot(row0 + row, a.order, a.TK) : 0;
+    }
+#pragma unroll
+    for (int m = 0; m < NS; ++m) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m * 32 + acc_row(r, l);
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const int col = 64 * w + 32 * f + r32;
+          S0[row * 256 + 8 * ((col >> 3) ^ (row & 7)) + (col & 7)] = f2bf(acc[m][f][r]);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < MT_MERGED / 16; ++p) {
+      const int row = (tid >> 4) + 16 * p;
+      if (row < nrows) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int c = ch + 16 * h, col0 = nb * 256 + 8 * c;
+          if (col0 < a.N) {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(S0 + row * 256 + 8 * (c ^ (row & 7)));
+            *reinterpret_cast<u32x4_t*>(a.out + (int64_t)slot[p] * a.ldo + col0) = v;
+          }
+        }
+      }
+    }
   } else {
     // out tile [128][256]: rows 32 m .. 32 m + 31 in stage m; column = 64 w + 32 f + r32 inside the block's 256
     uint16_t* const St[4] = {S0, S1, S2, S3};
@@ -559,8 +604,8 @@ SMEL_DEV void run_tile_ns(const FwdArgs& a, int kind, int idx, int row0, int nro
     case 2: run_tile<EPI, Q4, 2, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
     case 3: run_tile<EPI, Q4, 3, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
     case 4: run_tile<EPI, Q4, 4, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X); break;
-    default:   // 5 slices: only a merged int4 tile (fast dequant form) of the gate_up projection has more rows
-      if constexpr (EPI == 1 && Q4 && FAST)
+    default:   // 5 slices: only a merged int4 tile (fast dequant form) has more rows
+      if constexpr (Q4 && FAST)
         run_tile<EPI, Q4, 5, FAST>(a, kind, idx, row0, nrows, nb, S0, S1, S2, S3, rowmap, X);
       break;
   }
@@ -578,10 +623,10 @@ SMEL_DEV void gmm_fwd_body(const FwdArgs& a, uint16_t* S0, uint16_t* S1, uint16_
   const int kind = gk >> 16, idx = gk & 0xffff;
   int row1 = t.z;
   // a tile of up to 160 rows: a merged list's int4 tile (its rows beyond 128 are the group's short last tile), or a
-  // full tile that takes the next one below (group-ordered list, SMEL_WSET_MERGE_SHORT). Both need the fast dequant
-  // form and K a multiple of 64 (the 5-slice tile has no registers for the other form or for a K tail).
-  const bool five = EPI == 1 && kind == SMEL_KIND_INT4 && (a.w.flags & SMEL_WSET_FAST_DQ) && (a.K & (KT - 1)) == 0;
-  if (five && (a.w.flags & SMEL_WSET_MERGE_SHORT)) {
+  // gate_up tile that takes the next one below (group-ordered list, SMEL_WSET_MERGE_SHORT). Both need the fast
+  // dequant form and K a multiple of 64 (the 5-slice tile has no registers for the other form or for a K tail).
+  const bool five = kind == SMEL_KIND_INT4 && (a.w.flags & SMEL_WSET_FAST_DQ) && (a.K & (KT - 1)) == 0;
+  if (EPI == 1 && five && (a.w.flags & SMEL_WSET_MERGE_SHORT)) {
     // In a group-ordered list, a group's last tile of at most MT_MERGED - MT rows right after a full tile of the same
     // group is taken by the full tile's blocks (one weight stream and dequant for both); its own blocks exit.
     if (t.z - t.y <= MT_MERGED - MT && tile > 0) {
@@ -593,7 +638,8 @@ SMEL_DEV void gmm_fwd_body(const FwdArgs& a, uint16_t* S0, uint16_t* S1, uint16_
       if (q.x == t.x && q.y == t.z && q.z - q.y <= MT_MERGED - MT) row1 = q.z;
     }
   }
-  const bool merged = five && (a.w.flags & (SMEL_WSET_MERGE_SHORT | SMEL_WSET_MERGED_LIST));
+  const bool merged = five && (a.w.flags & (EPI == 1 ? SMEL_WSET_MERGE_SHORT | SMEL_WSET_MERGED_LIST
+                                                      : SMEL_WSET_MERGED_LIST));
   const int nrows = min(row1 - t.y, merged ? MT_MERGED : MT);
   if (nrows <= 0) return;
   if (kind == SMEL_KIND_INT4) {
@@ -606,22 +652,18 @@ SMEL_DEV void gmm_fwd_body(const FwdArgs& a, uint16_t* S0, uint16_t* S1, uint16_
   }
 }
 
-// The gate_up projection (epilogue 1): four A stages of 160 rows (80 KiB, two blocks per CU), nothing else in LDS.
-// The down projection (epilogue 0): four stages of 128 rows, the output slots of the tile's rows and its LoRA rows.
+// Four contiguous A stages of 160 rows (80 KiB, two blocks per CU), nothing else in LDS. The down projection
+// (epilogue 0) keeps a tile's LoRA rows and its rows' output slots in the stages' spare rows (a tile of at most 128
+// rows; a merged tile of more is an int4 tile, without either).
 template <int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gmm_fwd_kernel(FwdArgs a) {
-  constexpr int STAGE = stage_rows(EPI) * KT;
-  __shared__ __attribute__((aligned(1024))) uint16_t S0[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S1[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S2[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t S3[STAGE];
-  if constexpr (EPI == 0) {
-    __shared__ int rowmap[MT];
-    __shared__ __attribute__((aligned(16))) uint16_t X[MT * 32];   // the down projection's LoRA rows of a tile
-    gmm_fwd_body<EPI>(a, S0, S1, S2, S3, rowmap, X);
-  } else {
-    gmm_fwd_body<EPI>(a, S0, S1, S2, S3, nullptr, nullptr);
-  }
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[4 * STAGE];
+  uint16_t* const S0 = ring;
+  if constexpr (EPI == 0)
+    gmm_fwd_body<EPI>(a, S0, S0 + STAGE, S0 + 2 * STAGE, S0 + 3 * STAGE,
+                      reinterpret_cast<int*>(S0 + 2 * STAGE + SPARE), S0 + SPARE);
+  else
+    gmm_fwd_body<EPI>(a, S0, S0 + STAGE, S0 + 2 * STAGE, S0 + 3 * STAGE, nullptr, nullptr);
 }
 
 }  // namespace
@@ -651,11 +693,10 @@ extern "C" int smel_gmm_fwd_lr(const smel_wset* w, const int32_t* gkind, const i
   SMEL_REQUIRE(epilogue == 0 || epilogue == 1, SMEL_EINVAL, "gmm_fwd: epilogue %d", epilogue);
   SMEL_REQUIRE(!(w->flags & SMEL_WSET_EXT2) || epilogue == 1, SMEL_EINVAL,
                "gmm_fwd: a two-plane LoRA extension belongs to the gate_up projection (epilogue 1)");
-  SMEL_REQUIRE(!(w->flags & SMEL_WSET_MERGED_LIST) ||
-                   (epilogue == 1 && (!w->q4 || ((w->flags & SMEL_WSET_FAST_DQ) && w->C % 64 == 0))),
+  SMEL_REQUIRE(!(w->flags & SMEL_WSET_MERGED_LIST) || !w->q4 || ((w->flags & SMEL_WSET_FAST_DQ) && w->C % 64 == 0),
                SMEL_EINVAL,
-               "gmm_fwd: a merged tile list (SMEL_WSET_MERGED_LIST) needs the gate_up projection (epilogue 1) and, for "
-               "an int4 bank, its fast dequant form and K a multiple of 64");
+               "gmm_fwd: a merged tile list (SMEL_WSET_MERGED_LIST) on an int4 bank needs its fast dequant form and K "
+               "a multiple of 64");
   SMEL_REQUIRE(!a_gather || order || TK == 0, SMEL_EINVAL, "gmm_fwd: gather needs order");
   SMEL_REQUIRE(act == 0 || act == 1, SMEL_EINVAL, "gmm_fwd: act %d", act);
   SMEL_REQUIRE(a_rows >= 0 && a_rows * lda * 2 < (1ll << 31), SMEL_EUNSUPPORTED, "gmm_fwd: A larger than 2 GiB");

@@ -22,7 +22,7 @@ WSET_EXT2 = 2        # smel_wset.flags: the LoRA K-extension of the gate_up proj
 WSET_XCD_CHUNK = 4   # smel_wset.flags: group-ordered tile list, a contiguous chunk of it per XCD
 WSET_MERGE_SHORT = 8 # smel_wset.flags: gate_up forward, a full int4 tile also takes the group's short last tile
 WSET_MERGED_LIST = 16 # smel_wset.flags: gate_up forward on smel_dispatch's merged tile list (int4 tiles up to 160 rows)
-ABI_VERSION = 22
+ABI_VERSION = 23
 
 vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 

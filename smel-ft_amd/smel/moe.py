@@ -369,10 +369,10 @@ _BWD_LORA_ROWS = os.environ.get("SMEL_BWD_LORA_ROWS", "1") == "1"
 # partials (smel_gmm_fwd_lr), summed and stored by the down forward; 0: a smel_lora_ext launch over the gate_up
 # output between the two GEMMs
 _FWD_LORA_ROWS = os.environ.get("SMEL_FWD_LORA_ROWS", "1") == "1"
-# SMEL_MERGE_SHORT=1 (default): the gate_up forward takes an int4 expert's last tile of at most 32 rows together with
-# the full tile before it (one weight stream and dequant for up to 160 rows; banks in the fast dequant form): the
-# fused layer runs it on the dispatch's merged tile list, the frozen-experts path on its group-ordered count tiles;
-# 0: every tile of the list on its own
+# SMEL_MERGE_SHORT=1 (default): the forward GEMMs take an int4 expert's last tile of at most 32 rows together with
+# the full tile before it (one weight stream and dequant for up to 160 rows; banks in the fast dequant form), on the
+# dispatch's merged tile list (the fused layer) or the merged count tiles (the frozen-experts path); 0: every tile of
+# the list on its own
 _MERGE_SHORT = os.environ.get("SMEL_MERGE_SHORT", "1") == "1"
 
 
@@ -835,7 +835,12 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
         ext_dn = _lora_ext(tl, actb, I, M, 0, order, TK, K, lb_ex, lb_sh, "a_dn", I, 1, M, dev, st)
     Y = bf(M, H)
     w_dn = _wset(ex, "dn", sel_dn, sh_dn, g(lb_ex, "fwd_dn"), g(lb_sh, "fwd_dn"))
-    L.call("smel_gmm_fwd_lr", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, M, 0,
+    # the down forward on the same merged list when its bank is in the fast form too (and I a multiple of 64)
+    merge_dn = merge and I % 64 == 0 and fz.fast_dq("dn")
+    if merge_dn:
+        w_dn.flags |= L.WSET_MERGED_LIST
+    L.call("smel_gmm_fwd_lr", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles_m if merge_dn else tiles),
+           L.ptr(ntiles_m if merge_dn else ntiles), maxt, L.ptr(actb), I, M, 0,
            L.ptr(order), TK, K, L.ptr(ext_dn) if lr is None else None, 0, _ACT[ex.act], L.ptr(Y), H, None,
            ctypes.byref(lr) if lr is not None else None, st, tag="gemm_dn_fwd")
     out = bf(T, H)
@@ -1491,12 +1496,15 @@ class FrozenExpertsFn(torch.autograd.Function):
         dev = xs.device
         st = L.stream()
         w_gu, w_dn = _bank_wset(bank, "gu"), _bank_wset(bank, "dn")
-        # the gate_up forward on the merged list (int4 banks in the fast form, H a multiple of 64), the other GEMMs on
-        # the long-first list, as in the fused layer
+        # the forward GEMMs on the merged list (int4 banks in the fast form, K a multiple of 64), the backward on the
+        # long-first list, as in the fused layer
+        I = w_dn.C
         merge = _MERGE_SHORT and isinstance(bank, Int4Experts) and (w_gu.flags & L.WSET_FAST_DQ) and H % 64 == 0
+        merge_dn = merge and (w_dn.flags & L.WSET_FAST_DQ) and I % 64 == 0
         if merge:
             w_gu.flags |= L.WSET_MERGED_LIST
-        I = w_dn.C
+        if merge_dn:
+            w_dn.flags |= L.WSET_MERGED_LIST
         bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
         out = bf(rows, H)
         ctx.plan = None
@@ -1508,8 +1516,9 @@ class FrozenExpertsFn(torch.autograd.Function):
         actb, hsave = bf(rows, I), bf(rows, 2 * I)
         L.call("smel_gmm_fwd", ctypes.byref(w_gu), L.ptr(gk), L.ptr(tiles_gu), L.ptr(ntiles_gu), maxt_gu, L.ptr(xs), H,
                rows, 0, None, 0, 1, None, 1, _ACT[act_name], L.ptr(actb), I, L.ptr(hsave), st, tag="gemm_frozen_gu_fwd")
-        L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(actb), I, rows,
-               0, None, 0, 1, None, 0, _ACT[act_name], L.ptr(out), H, None, st, tag="gemm_frozen_dn_fwd")
+        tl_dn = (tiles_gu, ntiles_gu, maxt_gu) if merge_dn else (tiles, ntiles, maxt)
+        L.call("smel_gmm_fwd", ctypes.byref(w_dn), L.ptr(gk), L.ptr(tl_dn[0]), L.ptr(tl_dn[1]), tl_dn[2], L.ptr(actb),
+               I, rows, 0, None, 0, 1, None, 0, _ACT[act_name], L.ptr(out), H, None, st, tag="gemm_frozen_dn_fwd")
         ctx.plan = (bank, tiles, ntiles, maxt, gk, hsave, act_name)
         return out
 

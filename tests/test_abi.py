@@ -98,11 +98,12 @@ def test_host_side_rejections():
     for mr, gk, tm in ((200, 16, 16), (160, None, 16), (160, 16, None), (100, 16, 16)):
         assert L.smel_dispatch(*d, gk, 16, 16, 16, 16, 16, 16, 16, 16, mr, tm, 16, 16, None) == -1
         assert b"merged tile list" in L.smel_last_error()
-    # gmm_fwd: the merged list on an int4 bank without the fast dequant form, or on the down projection
+    # gmm_fwd: the merged list on an int4 bank without the fast dequant form, or with K not a multiple of 64
     wm = _lib.WSet()
     wm.R, wm.C, wm.group, wm.q4, wm.sz4, wm.flags = 1024, 2048, 64, 16, 16, _lib.WSET_MERGED_LIST
-    for epi, flags in ((1, _lib.WSET_MERGED_LIST), (0, _lib.WSET_MERGED_LIST | _lib.WSET_FAST_DQ)):
-        wm.flags = flags
+    for epi, flags, C in ((1, _lib.WSET_MERGED_LIST, 2048), (0, _lib.WSET_MERGED_LIST, 2048),
+                          (0, _lib.WSET_MERGED_LIST | _lib.WSET_FAST_DQ, 2016)):
+        wm.flags, wm.C, wm.group = flags, C, 32 if C % 64 else 64
         assert L.smel_gmm_fwd(ctypes.byref(wm), None, 16, 16, 1, 16, 2048, 4, 0, None, 0, 1, None, epi, 0, 16, 1024,
                               16, None) == -1
         assert b"merged tile list" in L.smel_last_error()

@@ -596,10 +596,10 @@ def test_layer_parity(name):
 
 @pytest.mark.parametrize("name", ["r16"])
 def test_merged_short_tiles_bitwise(name, monkeypatch):
-    """The gate_up forward's merged tiles (a full int4 tile and the expert's last tile of <= 32 rows in one block,
-    SMEL_WSET_MERGE_SHORT) accumulate every row in the same k order as the separate tiles: y, dX and the LoRA
-    gradients are bitwise equal with and without the merge. (r16: 32 experts of about 129 rows, so most experts have
-    a short last tile.)"""
+    """The forward GEMMs' merged tiles (a full int4 tile and the expert's last tile of <= 32 rows in one block, on the
+    dispatch's merged list: the gate_up and the down projection) accumulate every row in the same k order as the
+    separate tiles: y, dX and the LoRA gradients are bitwise equal with and without the merge. (r16: 32 experts of
+    about 129 rows, so most experts have a short last tile.)"""
     import smel.moe as M
     _say(f"merged short tiles {name}")
     monkeypatch.setattr(M, "_MERGE_SHORT", True)
