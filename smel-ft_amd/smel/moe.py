@@ -361,6 +361,12 @@ _SIDE_ON = frozenset(int(v) for v in os.environ.get("SMEL_SIDE_STREAMS", "0,1").
 # the dX reduce (each fork or join point of a replayed graph costs the main queue several µs); 0: each on its own
 # stream, the router backward forked right after the down backward
 _BWD_ONE_SIDE = os.environ.get("SMEL_BWD_ONE_SIDE", "1") == "1"
+# SMEL_FWD_EXT_SIDE=1: with a fused shared expert that has a LoRA, the forward's LoRA layouts and the shared rows'
+# gate_up LoRA projection (token order: no routing needed) run on side stream 2 beside the router and the dispatch;
+# the main stream projects only the selected experts' rows after the dispatch. 0 (default): side stream 2 as
+# SMEL_SIDE_STREAMS says, and one projection launch for all LoRA rows after the dispatch (the projection's time is
+# its fixed latency, not its rows, so the split launch saves nothing on the main stream and the fork costs time)
+_FWD_EXT_SIDE = os.environ.get("SMEL_FWD_EXT_SIDE", "0") == "1"
 # SMEL_BWD_LORA_ROWS=1 (default): the gate_up backward's LoRA rows come from the down backward's epilogue as
 # per-column-block partials (smel_gmm_bwd_lr), summed by the gate_up backward itself and, for the LoRA gradients, by
 # smel_lora_rows_sum on the side stream: no smel_lora_ext launch between the two GEMMs; 0: that launch
@@ -390,9 +396,9 @@ class _Fork:
     """``with _Fork(dev, i) as s:`` launches on side stream i after the current stream's work so far; ``join()``
     makes the current (main) stream wait for everything launched there."""
 
-    def __init__(self, dev, i: int):
+    def __init__(self, dev, i: int, on: bool = None):
         self.main = torch.cuda.current_stream(dev)
-        self.side = _side_stream(dev, i) if i in _SIDE_ON else self.main
+        self.side = _side_stream(dev, i) if (i in _SIDE_ON if on is None else on) else self.main
         if self.side is not self.main:
             self.side.wait_stream(self.main)
         self._ctx = torch.cuda.stream(self.side)
@@ -451,11 +457,14 @@ _PLANE_MAJOR = ("a_gu", "bt_gu")   # layouts with a leading plane dimension (lor
 
 
 def _lora_ext(tl, A, lda, a_rows, gather, order, TK, K, lb_ex, lb_sh, name: str, Kd: int, planes: int, M: int, dev,
-              st):
+              st, ext=None, row0: int = 0):
     """ext rows [M][32 * planes] of one direction: smel_lora_ext once per plane (``name`` = the layout the rows are
-    projected on; the down side's layouts have one plane). ``tl`` = (tiles, n_tiles, max_tiles, gkind)."""
+    projected on; the down side's layouts have one plane). ``tl`` = (tiles, n_tiles, max_tiles, gkind). ``ext`` = a
+    buffer to fill instead of a new one, the tiles' row r going to its row row0 + r."""
     tiles, ntiles, maxt, gk = tl
-    ext = torch.empty(M, EXT * planes, dtype=torch.bfloat16, device=dev)
+    if ext is None:
+        ext = torch.empty(M, EXT * planes, dtype=torch.bfloat16, device=dev)
+    base = ext.data_ptr() + 2 * row0 * EXT * planes
     s_ex = lb_ex.scale if lb_ex is not None else 0.0
     s_sh = lb_sh.scale if lb_sh is not None else 0.0
     for c in range(planes):
@@ -465,9 +474,32 @@ def _lora_ext(tl, A, lda, a_rows, gather, order, TK, K, lb_ex, lb_sh, name: str,
             t = getattr(lb, name)
             return t[c] if name in _PLANE_MAJOR else t
         L.call("smel_lora_ext", L.ptr(tiles), L.ptr(ntiles), maxt, L.ptr(gk), L.ptr(A), lda, a_rows, gather,
-               L.ptr(order), TK, K, L.ptr(w(lb_ex)), L.ptr(w(lb_sh)), Kd, s_ex, s_sh, ext.data_ptr() + 2 * EXT * c,
+               L.ptr(order), TK, K, L.ptr(w(lb_ex)), L.ptr(w(lb_sh)), Kd, s_ex, s_sh, base + 2 * EXT * c,
                EXT * planes, st)
     return ext
+
+
+def _token_tiles(T: int, E: int, dev):
+    """Rows [0, T) as M_TILE-row tiles of group E with the kind SMEL_KIND_SHARED in the entry's fourth field (the
+    shared expert's rows, in token order), cached per shape: (tiles, n_tiles, max_tiles, gkind None)."""
+    cache = _token_tiles.__dict__.setdefault("cache", {})
+    key = (T, E, str(dev))
+    if key not in cache:
+        rows = [[E, r, min(r + M_TILE, T), L.KIND_SHARED << 16] for r in range(0, T, M_TILE)]
+        t = torch.tensor(rows, dtype=torch.int32).reshape(-1).to(dev)
+        cache[key] = (t, torch.tensor([len(rows)], dtype=torch.int32).to(dev), len(rows), None)
+    return cache[key]
+
+
+def _shared_lora_ext(x, K: int, E: int, bufs, dev):
+    """The gate_up LoRA projection of the fused shared expert's rows [TK, TK + T) (x in token order, no routing
+    needed) into a new ext buffer of all TK + T rows; the routed rows are filled after the dispatch."""
+    lb_ex, lb_sh = bufs
+    T, H = x.shape
+    planes = (lb_ex or lb_sh).planes
+    ext = torch.empty(T * K + T, EXT * planes, dtype=torch.bfloat16, device=dev)
+    return _lora_ext(_token_tiles(T, E, dev), x, H, T, 0, None, 0, 1, None, lb_sh, "a_gu", H, planes, T, dev,
+                     L.stream(), ext=ext, row0=T * K)
 
 
 def _bwd_lora_rows(lb_ex, lb_sh, nblk: int, M: int, planes: int, dev):
@@ -760,13 +792,14 @@ def _prep_lora(ex: LayerExperts, lora_ex, lora_sh, with_shared: bool, H: int, de
 
 
 def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool, shared, lora_ex, lora_sh,
-                      need_grad: bool, c: _Ctx, prep=None, shared_rows=None, counted_ws=None):
+                      need_grad: bool, c: _Ctx, prep=None, shared_rows=None, counted_ws=None, ext_pre=None):
     """Dispatch + expert GEMMs + combine. ``shared`` = (gate_up, down, sgate fp32 [T], gate_up^T, down^T) or None
     (packed forward and transposed layouts of the shared expert's [2I,H] / [H,I] weights). ``prep`` = (_Fork,
     (lb_ex, lb_sh)) when the LoRA layouts were launched on a side stream (joined before their first use).
     ``shared_rows`` = (sgate fp32 [T], y_shared bf16 [T, H]) adds a shared expert computed elsewhere (one whose
     intermediate size differs from the experts') to the combine. ``counted_ws`` = the dispatch workspace that
-    smel_route_counted filled for these ids (the dispatch then skips its histogram launch)."""
+    smel_route_counted filled for these ids (the dispatch then skips its histogram launch). ``ext_pre`` = the gate_up
+    LoRA rows with the shared rows already projected (_shared_lora_ext, on the fork of ``prep``)."""
     T, H = x.shape
     E = ex.E
     dev = x.device
@@ -809,7 +842,11 @@ def _forward_pipeline(x, ex: LayerExperts, K: int, topv, topi_ids, ids_i64: bool
     bf = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device=dev)
     tl = (tiles, ntiles, maxt, gk)
     ext_gu = ext_dn = None
-    if any_lora:
+    if any_lora and ext_pre is not None:   # the shared rows are done: the selected experts' rows only
+        ext_gu = ext_pre
+        if lb_ex is not None:
+            _lora_ext(tl, x, H, T, 1, order, TK, K, lb_ex, None, "a_gu", H, planes, M, dev, st, ext=ext_gu)
+    elif any_lora:
         ext_gu = _lora_ext(tl, x, H, T, 1, order, TK, K, lb_ex, lb_sh, "a_gu", H, planes, M, dev, st)
     actb = bf(M, I)
     hsave = bf(M, 2 * I) if need_grad else None
@@ -1059,9 +1096,14 @@ class _MoELayerFn(torch.autograd.Function):
         sgate = torch.empty(T, dtype=torch.float32, device=dev) if has_sh else None
         sgw = plan["shared"][2] if has_sh else None
         lg = torch.empty(T, L.load().smel_route_ld(E, int(has_sh)), dtype=torch.bfloat16, device=dev)
-        fork = _Fork(dev, 2)   # LoRA layouts overlap the router and the dispatch
+        # LoRA layouts (and the shared rows' LoRA projection) overlap the router and the dispatch
+        side_ext = _FWD_EXT_SIDE and fuse and plan["lora_sh"] is not None
+        fork = _Fork(dev, 2, on=True if side_ext else None)
+        ext_pre = None
         with fork:
             bufs = _prep_lora(plan["ex"], plan["lora_ex"], plan["lora_sh"] if fuse else None, fuse, H, dev)
+            if side_ext and bufs[1] is not None:
+                ext_pre = _shared_lora_ext(x, K, E, bufs, dev)
         # the router also counts the dispatch's per-block histograms of its picks into the dispatch workspace
         dws = torch.empty(max(1, L.load().smel_dispatch_ws_size(T * K, E)), dtype=torch.int32, device=dev)
         L.call("smel_route_counted", L.ptr(x), L.ptr(plan["gate_w"]), L.ptr(sgw), T, H, E, K, L.ptr(probs),
@@ -1081,7 +1123,7 @@ class _MoELayerFn(torch.autograd.Function):
             c.split = (sv, pgu_t, pdn_t, lsh, sgate)
         out = _forward_pipeline(x, plan["ex"], K, topv32, topi32, False, shared, plan["lora_ex"],
                                 plan["lora_sh"] if fuse else None, plan["need_grad"], c, prep=(fork, bufs),
-                                shared_rows=shared_rows, counted_ws=dws)
+                                shared_rows=shared_rows, counted_ws=dws, ext_pre=ext_pre)
         if plan["need_grad"]:
             c.router = (probs, topi32, _router_ext_weight(plan["gate_w"], sgw, plan["store"]))
             c.plan_lora_sh = plan["lora_sh"]

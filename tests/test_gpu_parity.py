@@ -614,6 +614,25 @@ def test_merged_short_tiles_bitwise(name, monkeypatch):
         assert torch.equal(a["grads"][k], b["grads"][k]), k
 
 
+@pytest.mark.parametrize("name", ["r16", "r24_mixed", "c1"])
+def test_shared_lora_rows_on_side_stream_bitwise(name, monkeypatch):
+    """The fused shared expert's gate_up LoRA rows projected on a side stream beside the router (SMEL_FWD_EXT_SIDE,
+    token-order tiles written at rows TK + t) and the selected experts' rows after the dispatch give the same rows as
+    one projection over the dispatch's tiles: y, dX and the LoRA gradients are bitwise equal. (r24_mixed: two planes;
+    c1: T = 128, a single shared tile.)"""
+    import smel.moe as M
+    _say(f"shared LoRA rows on the side stream {name}")
+    monkeypatch.setattr(M, "_FWD_EXT_SIDE", True)
+    a = run_layer(name, seed=6)
+    monkeypatch.setattr(M, "_FWD_EXT_SIDE", False)
+    b = run_layer(name, seed=6)
+    assert torch.equal(a["y"].view(torch.int16), b["y"].view(torch.int16))
+    assert torch.equal(a["dx"].view(torch.int16), b["dx"].view(torch.int16))
+    assert set(a["grads"]) == set(b["grads"]) and any(k.startswith("sh_") for k in b["grads"])
+    for k in b["grads"]:
+        assert torch.equal(a["grads"][k], b["grads"][k]), k
+
+
 @pytest.mark.parametrize("name", ["r16", "r32", "shared_wide", "r24_mixed"])
 def test_bwd_lora_rows_against_projection(name, monkeypatch):
     """The gate_up backward's LoRA rows from the down backward's per-column-block partials (smel_gmm_bwd_lr +
