@@ -156,7 +156,12 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(PrepArgs pa) {
 // (the tile list holds each tile's kind; all tile entries are loaded at once, one memory latency), then takes the
 // (LoRA tile, 32-row slice) items blockIdx.x, blockIdx.x + gridDim.x, ... A slice's 8 waves take the 64-wide k-steps
 // j = w, w + 8, ..., issuing all loads of up to XPRE of their steps before the MFMAs (one memory latency per XPRE
-// steps, not one per step); the partial sums are added in wave order through LDS.
+// steps, not one per step); the partial sums are added in wave order through LDS. The 16x16x32 MFMA layout lets four
+// lanes share a row, so each load takes 64 contiguous bytes of 16 rows (32 bytes of 32 rows with 32x32x16).
+SMEL_DEV f32x4_t mfma16x(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                 c, 0, 0, 0);
+}
 constexpr int XW = 8;
 constexpr int XPRE = 4;
 constexpr int XT_PER = 8;              // tile entries each thread scans
@@ -172,7 +177,7 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
   __shared__ float red[XW * 64 * 16];
   __shared__ int4 lt[XLT];   // the call's LoRA tiles (whole entries: no second load per item)
   __shared__ int wcnt[XT_PER][XW];
-  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
+  const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, kq = l >> 4, li = l & 15;
   // ---- the LoRA tiles of this call, in tile order
   const int nt = min(n_tiles[0], max_tiles);
   bool fl[XT_PER];
@@ -220,51 +225,68 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
     if (m * 32 >= nrows) continue;   // uniform over the block
     const uint16_t* wc = kind == SMEL_KIND_SEL ? wsel + (int64_t)idx * 32 * Kd : wsh;
     const float scale = kind == SMEL_KIND_SEL ? ssel : ssh;
-    const int row = m * 32 + r32;
+    // v_mfma_f32_16x16x32_bf16: lane (kq, i) holds row 16 fr + i of the slice and factor row 16 fc + i, k = 32 s +
+    // 8 kq + [0, 8) of each 64-wide step, so a load takes 64 contiguous bytes of 16 rows (4 lanes per row)
     const rsrc_t rb = make_rsrc(wc, (uint64_t)32 * Kd * 2);
-    uint32_t ao = OOB;
-    if (row < nrows) {
-      const int grow = t.y + row;
-      ao = (uint32_t)(a_gather ? row_token(grow, order, TK, topk) : grow) * (uint32_t)lda * 2;
+    uint32_t ao[2], bo[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int row = m * 32 + 16 * f + li;
+      ao[f] = OOB;
+      if (row < nrows) {
+        const int grow = t.y + row;
+        ao[f] = (uint32_t)(a_gather ? row_token(grow, order, TK, topk) : grow) * (uint32_t)lda * 2 + 16 * kq;
+      }
+      bo[f] = (uint32_t)(16 * f + li) * Kd * 2 + 16 * kq;
     }
-    const uint32_t bo = (uint32_t)r32 * Kd * 2;
-    f32x16_t acc = f32x16_t{};
+    f32x4_t acc[2][2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) acc[f][0] = acc[f][1] = f32x4_t{};
     for (int j0 = w; j0 < nk; j0 += XW * XPRE) {
-      u32x4_t av[XPRE][4], bv[XPRE][4];
+      u32x4_t av[XPRE][2][2], bv[XPRE][2][2];   // [step][fragment][substep]
       // the factor rows first: they do not wait for the row's token (a gathered row's address does)
 #pragma unroll
-      for (int p = 0; p < XPRE; ++p) {
-        const int kk = (j0 + XW * p) * 64 + 32 * hi;
-        const bool ok = kk + 32 <= Kd;   // Kd % 32 == 0: a lane half's 32 k are all in or all out
+      for (int p = 0; p < XPRE; ++p)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bv[p][s] = ld16(rb, ok ? bo + kk * 2 + 16 * s : OOB);
-      }
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int kk = (j0 + XW * p) * 64 + 32 * s2;
+          const bool ok = kk + 32 <= Kd;   // Kd % 32 == 0: a 32-wide substep is all in or all out
 #pragma unroll
-      for (int p = 0; p < XPRE; ++p) {
-        const int kk = (j0 + XW * p) * 64 + 32 * hi;
-        const bool ok = kk + 32 <= Kd;
+          for (int f = 0; f < 2; ++f) bv[p][f][s2] = ld16(rb, ok ? bo[f] + kk * 2 : OOB);
+        }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) av[p][s] = ld16(ra, ok ? ao + kk * 2 + 16 * s : OOB);
-      }
+      for (int p = 0; p < XPRE; ++p)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int kk = (j0 + XW * p) * 64 + 32 * s2;
+          const bool ok = kk + 32 <= Kd;
+#pragma unroll
+          for (int f = 0; f < 2; ++f) av[p][f][s2] = ld16(ra, (ok && ao[f] != OOB) ? ao[f] + kk * 2 : OOB);
+        }
       __builtin_amdgcn_sched_barrier(0);   // every load of the batch is issued before the first MFMA waits
 #pragma unroll
       for (int p = 0; p < XPRE; ++p)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc = mfma32(av[p][s], bv[p][s], acc);
-    }
+        for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[(w * 16 + r) * 64 + l] = acc[r];   // lane-contiguous: no bank conflicts
+          for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+            for (int fc = 0; fc < 2; ++fc) acc[fr][fc] = mfma16x(av[p][fr][s2], bv[p][fc][s2], acc[fr][fc]);
+    }
+    // element q = 8 fr + 4 fc + r of a lane: row 16 fr + 4 kq + r of the slice, factor row (ext column) 16 fc + i
+#pragma unroll
+    for (int q = 0; q < 16; ++q) red[(w * 16 + q) * 64 + l] = acc[q >> 3][(q >> 2) & 1][q & 3];   // lane-contiguous
     lds_barrier();
-    // wave w sums accumulator registers 2w and 2w + 1 over the waves, in wave order, and stores those rows
-    static_assert(2 * XW == 16, "two accumulator registers per wave");
+    // wave w sums elements 2w and 2w + 1 over the waves, in wave order, and stores those values
+    static_assert(2 * XW == 16, "two accumulator elements per wave");
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
-      const int r = 2 * w + rr;
-      float v = red[r * 64 + l];
+      const int q = 2 * w + rr;
+      float v = red[q * 64 + l];
 #pragma unroll
-      for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + r) * 64 + l];
-      const int orow = m * 32 + acc_row(r, l);
-      if (orow < nrows) ext[(int64_t)(t.y + orow) * ldx + r32] = f2bf(scale * v);
+      for (int ww = 1; ww < XW; ++ww) v += red[(ww * 16 + q) * 64 + l];
+      const int orow = m * 32 + 16 * (q >> 3) + 4 * kq + (q & 3);
+      if (orow < nrows) ext[(int64_t)(t.y + orow) * ldx + 16 * ((q >> 2) & 1) + li] = f2bf(scale * v);
     }
     lds_barrier();   // red is reused by the next item
   }
