@@ -348,7 +348,8 @@ SMEL_DEV int wg_table(const WgArgs& a, int* G0, int* GN, int* GC) {
 }
 
 // R[p][q] of one 32 x 32 wave tile (acc of wave w, lane l; column block q0) -> the job's destination for group i's
-// class (selected slot i, or the shared set) and p-range.
+// class (selected slot i, or the shared set) and p-range. Registers 4 j .. 4 j + 3 of a lane hold four consecutive p's,
+// so a destination with p contiguous (s_p = 1: the B factors' [out][r] layout) takes them as one 16-B store.
 SMEL_DEV void wg_store(const smel_wg_job& J, int n_sel, int i, int q0, int w, int l, const f32x16_t& acc) {
   const int q = q0 + 32 * w + (l & 31);
   if (q >= J.Q) return;
@@ -358,11 +359,18 @@ SMEL_DEV void wg_store(const smel_wg_job& J, int n_sel, int i, int q0, int w, in
   for (int h = 0; h < 2; ++h) {
     const smel_wg_dest& d = J.dest[cls][h];
     if (!d.ptr || q < d.q0 || q >= d.q0 + d.nq) continue;
+    float* const base = d.ptr + slot * d.s_idx + (int64_t)(q - d.q0) * d.s_q;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int p = acc_row(r, l);
-      if (p >= d.p0 && p < d.p0 + d.np)
-        d.ptr[slot * d.s_idx + (int64_t)(p - d.p0) * d.s_p + (int64_t)(q - d.q0) * d.s_q] = acc[r];
+    for (int j = 0; j < 4; ++j) {
+      const int p = acc_row(4 * j, l);   // p .. p + 3 in registers 4 j .. 4 j + 3
+      float* const o = base + (int64_t)(p - d.p0) * d.s_p;
+      if (d.s_p == 1 && p >= d.p0 && p + 4 <= d.p0 + d.np && ((uintptr_t)o & 15) == 0) {
+        *reinterpret_cast<f32x4_t*>(o) = f32x4_t{acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]};
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (p + t >= d.p0 && p + t < d.p0 + d.np) o[t * d.s_p] = acc[4 * j + t];
+      }
     }
   }
 }
@@ -417,20 +425,30 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     // per window of WG_WIN rows: source-row byte offset and row weight of every row, built once into LDS so that the
     // prefetched loads depend on LDS reads only (a load whose address came from a global load would make the wait for
     // it drain every load in flight, vmcnt retiring in order)
+    // a thread's WG_WIN / 256 rows: all their slot loads, then all their weight loads (two memory round trips)
     auto build = [&](int w0, int w1) {
-      for (int row = w0 + tid; row < w1; row += 256) {
-        int src = row;
-        float alpha = 1.f;
-        if (row < a.TK) {
-          const int p = a.order[row];
-          if (r_gather) src = p / a.topk;
-          if (use_w) alpha = a.topv[p];
-        } else {
-          if (r_gather) src = row - a.TK;
-          if (use_w) alpha = a.sgate[row - a.TK];
+      constexpr int BR = WG_WIN / 256;
+      int pv[BR];
+#pragma unroll
+      for (int u = 0; u < BR; ++u) {
+        const int row = w0 + tid + 256 * u;
+        pv[u] = (row < w1 && row < a.TK) ? a.order[row] : 0;
+      }
+      float al[BR];
+#pragma unroll
+      for (int u = 0; u < BR; ++u) {
+        const int row = w0 + tid + 256 * u;
+        al[u] = 1.f;
+        if (use_w && row < w1) al[u] = row < a.TK ? a.topv[pv[u]] : a.sgate[row - a.TK];
+      }
+#pragma unroll
+      for (int u = 0; u < BR; ++u) {
+        const int row = w0 + tid + 256 * u;
+        if (row < w1) {
+          const int src = !r_gather ? row : (row < a.TK ? pv[u] / a.topk : row - a.TK);
+          TOFF[row - w0] = (uint32_t)src * (uint32_t)ldr * 2;
+          TAL[row - w0] = al[u];
         }
-        TOFF[row - w0] = (uint32_t)src * (uint32_t)ldr * 2;
-        TAL[row - w0] = alpha;
       }
     };
     const uint32_t ldl2 = (uint32_t)J.ldl * 2;              // L row pitch in bytes
