@@ -293,8 +293,10 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
 }
 
 // LoRA factor gradients, all products of a backward (four, or six with two-plane gate_up operands) in one launch.
-// Item = (128-column block of a job, 512-row chunk slot of a LoRA group); persistent blocks (at most two per CU) take
-// the items that are in use, counted on the device from the group offsets. out[p][q] = sum over ALL rows of group i
+// Item = (two adjacent 128-column blocks of a job, 512-row chunk slot of a LoRA group); persistent blocks (at most
+// two per CU) take the items that are in use, counted on the device from the group offsets. An item's two column
+// blocks share its row table and run as one sequence of 64-row steps, so the second one's first loads go out during
+// the first one's last steps (an item's time is mostly its fixed latency, not its steps). out[p][q] = sum over ALL rows of group i
 // of alpha(row) L[row * ldl + p] Rm[src(row)][q], p < 32, as an MFMA GEMM with the row index as the contraction dim:
 // per 64-row step, L and Rm are staged transposed in LDS (k-pair packing: the values of rows 2j and 2j+1 share one
 // 32-bit word), then each wave multiplies the 32 x 64 L^T tile by its 64 x 32 slice of the Rm tile. The LDS tiles
@@ -313,6 +315,8 @@ struct WgArgs {
   smel_wg_job job[WG_MAXJ];
   int qb0[WG_MAXJ];            // first 128-column block of each job in the partial-tile space
   int nqb;                     // 128-column blocks of all jobs
+  int pb0[WG_MAXJ];            // first column-block pair of each job
+  int npb;                     // column-block pairs of all jobs
   int tot;                     // partial-tile slots per column block
   float* ws;                   // partial tiles [sum of column blocks][tot][32 * 128]
   const int32_t* groups;
@@ -385,15 +389,17 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
   // [GC[i], GC[i+1]), one per 512-row chunk (at least one)
   const int ng = wg_table(a, G0, GN, GC);
   const int used = GC[ng];
-  // persistent: items (column block of all jobs, chunk slot), the slots in use only
-  for (int it = blockIdx.x; it < a.nqb * used; it += gridDim.x) {   // uniform
-    const int qbg = it / used, sl = it - qbg * used;
+  // persistent: items (column-block pair of all jobs, chunk slot), the slots in use only
+  static_assert(WG_WIN == WG_CH, "one row window per chunk");
+  for (int it = blockIdx.x; it < a.npb * used; it += gridDim.x) {   // uniform
+    const int pg = it / used, sl = it - pg * used;
     int jb = 0;
 #pragma unroll
     for (int j = 1; j < WG_MAXJ; ++j)
-      if (qbg >= a.qb0[j]) jb = j;
+      if (pg >= a.pb0[j]) jb = j;
     const smel_wg_job& J = a.job[jb];
-    const int qb = qbg - a.qb0[jb];
+    const int qb = 2 * (pg - a.pb0[jb]);                                  // the pair's first column block
+    const int ncb = min(2, (int)((J.Q + WG_QB - 1) / WG_QB) - qb);        // 1 or 2
     int i = 0;
     while (GC[i + 1] <= sl) ++i;
     const int c = sl - GC[i];
@@ -406,13 +412,12 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     const int Q = (int)J.Q;
     const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
     const int kp = tid & 31, grp = tid >> 5;   // k pair, and 4 p's (L) / 16 q's (Rm) per thread
-    const int qq = q0 + 16 * grp;
-    const bool qok = qq < Q;
+    const int qq = q0 + 16 * grp;             // in the pair's first column block
     const rsrc_t rr = make_rsrc(J.Rm, (uint64_t)J.r_rows * J.ldr * 2);
     const int64_t ldr = J.ldr;
     const int r_gather = J.r_gather, use_w = J.use_w;
     const uint16_t* __restrict__ Lp = J.L;
-    f32x16_t acc = f32x16_t{};
+    f32x16_t acc0 = f32x16_t{}, acc1 = f32x16_t{};   // the pair's two column blocks
     // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights;
     // WG_PF steps are in flight (a register ring rotated by unrolling): a long group (the shared MLP's T rows) is bound
     // by the load latency, not by its few MFMAs.
@@ -453,8 +458,11 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     };
     const uint32_t ldl2 = (uint32_t)J.ldl * 2;              // L row pitch in bytes
     const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * ldl2);  // L rows [0, a1): a row past the group reads zeros
-    // branch-free: rows past the window get an out-of-range offset (zeros) and weight 0
-    auto load = [&](int k0, int w0, int w1, Raw& R) {
+    // branch-free: rows past the window, and a column block past the pair, get out-of-range offsets (zeros) and
+    // weight 0
+    auto load = [&](int k0, int w0, int w1, int cb, Raw& R) {
+      const int qc = qq + WG_QB * cb;
+      const bool qok = cb < ncb && qc < Q;
       const int ra = k0 + 2 * kp;
       const bool v0 = ra < w1, v1 = ra + 1 < w1;
       const int t0 = v0 ? ra - w0 : 0, t1 = v1 ? ra + 1 - w0 : 0;
@@ -467,8 +475,8 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
       R.lv1 = make_uint2(l1.x, l1.y);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        R.x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qq + 8 * h) * 2 : OOB);
-        R.x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qq + 8 * h) * 2 : OOB);
+        R.x0[h] = ld16(rr, qok ? o0 + (uint32_t)(qc + 8 * h) * 2 : OOB);
+        R.x1[h] = ld16(rr, qok ? o1 + (uint32_t)(qc + 8 * h) * 2 : OOB);
       }
     };
     auto stage = [&](int buf, const Raw& R) {
@@ -492,17 +500,22 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
       __syncthreads();   // the previous window's table and tiles are no longer read
       build(w0, w1);
       __syncthreads();
+      // virtual steps: v < S are column block 0's 64-row steps (S = whole rounds of WG_PF), S .. 2 S block 1's
+      const int S = (w1 - w0 + 64 * WG_PF - 1) / (64 * WG_PF) * WG_PF;
+      auto vload = [&](int v, Raw& R) {
+        const int cb = v / S;   // >= ncb past the last step: zeros
+        load(w0 + 64 * (v - cb * S), w0, w1, cb, R);
+      };
 #pragma unroll
-      for (int u = 0; u < WG_PF; ++u) load(w0 + 64 * u, w0, w1, rw[u]);
-      for (int k0 = w0; k0 < w1; k0 += 64 * WG_PF) {
-        // WG_PF steps per round, branch-free (a step past the window stages zeros and adds nothing), so the compiler's
-        // wait for a ring slot counts exactly the loads issued after it
+      for (int u = 0; u < WG_PF; ++u) vload(u, rw[u]);
+      // WG_PF steps per round, branch-free (a step past the window stages zeros and adds nothing), so the compiler's
+      // wait for a ring slot counts exactly the loads issued after it
+      auto round = [&](int v0, f32x16_t& acc) {
 #pragma unroll
         for (int u = 0; u < WG_PF; ++u) {
-          const int kk = k0 + 64 * u;
           const int buf = u & 1;
           stage(buf, rw[u]);
-          load(kk + 64 * WG_PF, w0, w1, rw[u]);   // past the window: out-of-range loads, zeros
+          vload(v0 + u + WG_PF, rw[u]);   // the next column block's first steps during this one's last round
           __syncthreads();
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
@@ -511,16 +524,23 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
             acc = mfma32(af, bfr, acc);
           }
         }
-      }
+      };
+      for (int v0 = 0; v0 < S; v0 += WG_PF) round(v0, acc0);
+      if (ncb > 1)   // uniform
+        for (int v0 = S; v0 < 2 * S; v0 += WG_PF) round(v0, acc1);
     }
-    if (nch == 1) {
-      wg_store(J, a.n_sel, i, q0, w, l, acc);
-    } else {
-      // a group of several chunks: this chunk's partial tile, summed in chunk order by lora_wgrad_reduce
-      float* tile = a.ws + ((int64_t)(a.qb0[jb] + qb) * a.tot + sl) * (32 * WG_QB);
+    auto put = [&](const f32x16_t& acc, int qbc) {
+      if (nch == 1) {
+        wg_store(J, a.n_sel, i, qbc * WG_QB, w, l, acc);
+      } else {
+        // a group of several chunks: this chunk's partial tile, summed in chunk order by lora_wgrad_reduce
+        float* tile = a.ws + ((int64_t)(a.qb0[jb] + qbc) * a.tot + sl) * (32 * WG_QB);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = acc[r];
-    }
+        for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = acc[r];
+      }
+    };
+    put(acc0, qb);
+    if (ncb > 1) put(acc1, qb + 1);
   }
 }
 
@@ -720,9 +740,10 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   WgArgs a;
   a.tot = (int)wg_tot(n_lora, max_rows);
   a.ws = ws;
-  int qbs = 0;
+  int qbs = 0, pbs = 0;
   for (int j = 0; j < WG_MAXJ; ++j) {
     a.qb0[j] = qbs;
+    a.pb0[j] = pbs;
     if (j < n_jobs) {
       const smel_wg_job& J = jobs[j];
       SMEL_REQUIRE(J.L && J.Rm && J.Q > 0, SMEL_EINVAL, "lora_wgrad: job %d: null operand or Q", j);
@@ -741,7 +762,9 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
                        SMEL_EINVAL, "lora_wgrad: job %d: destination [%d][%d] outside the 32 x Q result", j, c, h);
         }
       a.job[j] = J;
-      qbs += (int)((J.Q + WG_QB - 1) / WG_QB);
+      const int nqbj = (int)((J.Q + WG_QB - 1) / WG_QB);
+      qbs += nqbj;
+      pbs += (nqbj + 1) / 2;
     } else {
       a.job[j] = smel_wg_job{};
       a.job[j].Q = WG_QB;
@@ -749,6 +772,7 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
     }
   }
   a.nqb = qbs;
+  a.npb = pbs;
   a.groups = lora_groups;
   a.n_lora = (int)n_lora;
   a.n_sel = (int)n_sel;
@@ -760,8 +784,8 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   a.order = order;
   a.topv = topv;
   a.sgate = sgate;
-  // persistent blocks over the (column block, chunk slot) items in use: at most two per CU
-  const int64_t bound = (int64_t)qbs * a.tot;
+  // persistent blocks over the (column-block pair, chunk slot) items in use: at most two per CU
+  const int64_t bound = (int64_t)pbs * a.tot;
   lora_wgrad_kernel<<<(unsigned)std::min<int64_t>(bound, 2 * smel::cu_count()), 256, 0, stream>>>(a);
   int st = smel::launch_status();
   if (st) return st;
