@@ -293,10 +293,10 @@ __global__ __launch_bounds__(512) void lora_ext_kernel(const int4* __restrict__ 
 }
 
 // LoRA factor gradients, all products of a backward (four, or six with two-plane gate_up operands) in one launch.
-// Item = (two adjacent 128-column blocks of a job, 512-row chunk slot of a LoRA group); persistent blocks (at most
-// two per CU) take the items that are in use, counted on the device from the group offsets. An item's two column
-// blocks share its row table and run as one sequence of 64-row steps, so the second one's first loads go out during
-// the first one's last steps (an item's time is mostly its fixed latency, not its steps). out[p][q] = sum over ALL rows of group i
+// Item = (WG_CBI adjacent 128-column blocks of a job, 512-row chunk slot of a LoRA group); persistent blocks (at most
+// two per CU) take the items that are in use, counted on the device from the group offsets. An item's column blocks
+// share its row table and run as one sequence of 64-row steps, so each next one's first loads go out during the
+// previous one's last steps (an item's time is mostly its fixed latency, not its steps). out[p][q] = sum over ALL rows of group i
 // of alpha(row) L[row * ldl + p] Rm[src(row)][q], p < 32, as an MFMA GEMM with the row index as the contraction dim:
 // per 64-row step, L and Rm are staged transposed in LDS (k-pair packing: the values of rows 2j and 2j+1 share one
 // 32-bit word), then each wave multiplies the 32 x 64 L^T tile by its 64 x 32 slice of the Rm tile. The LDS tiles
@@ -310,13 +310,14 @@ constexpr int WG_CH = 512;    // rows per chunk block
 constexpr int WG_MAXG = 256;  // LoRA groups per call
 constexpr int WG_WIN = WG_CH; // rows per index window
 constexpr int WG_MAXJ = 6;    // jobs per launch (four, or six with two-plane gate_up operands)
+constexpr int WG_CBI = 4;     // adjacent column blocks per item (a divisor of the jobs' 4, 8 and 16)
 
 struct WgArgs {
   smel_wg_job job[WG_MAXJ];
   int qb0[WG_MAXJ];            // first 128-column block of each job in the partial-tile space
   int nqb;                     // 128-column blocks of all jobs
-  int pb0[WG_MAXJ];            // first column-block pair of each job
-  int npb;                     // column-block pairs of all jobs
+  int pb0[WG_MAXJ];            // first column-block group (WG_CBI blocks) of each job
+  int npb;                     // column-block groups of all jobs
   int tot;                     // partial-tile slots per column block
   float* ws;                   // partial tiles [sum of column blocks][tot][32 * 128]
   const int32_t* groups;
@@ -389,7 +390,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
   // [GC[i], GC[i+1]), one per 512-row chunk (at least one)
   const int ng = wg_table(a, G0, GN, GC);
   const int used = GC[ng];
-  // persistent: items (column-block pair of all jobs, chunk slot), the slots in use only
+  // persistent: items (column-block group of all jobs, chunk slot), the slots in use only
   static_assert(WG_WIN == WG_CH, "one row window per chunk");
   for (int it = blockIdx.x; it < a.npb * used; it += gridDim.x) {   // uniform
     const int pg = it / used, sl = it - pg * used;
@@ -398,8 +399,8 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     for (int j = 1; j < WG_MAXJ; ++j)
       if (pg >= a.pb0[j]) jb = j;
     const smel_wg_job& J = a.job[jb];
-    const int qb = 2 * (pg - a.pb0[jb]);                                  // the pair's first column block
-    const int ncb = min(2, (int)((J.Q + WG_QB - 1) / WG_QB) - qb);        // 1 or 2
+    const int qb = WG_CBI * (pg - a.pb0[jb]);                               // the item's first column block
+    const int ncb = min(WG_CBI, (int)((J.Q + WG_QB - 1) / WG_QB) - qb);     // 1 .. WG_CBI
     int i = 0;
     while (GC[i + 1] <= sl) ++i;
     const int c = sl - GC[i];
@@ -412,12 +413,14 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     const int Q = (int)J.Q;
     const int tid = threadIdx.x, l = lane_id(), w = tid >> 6, hi = l >> 5, r32 = l & 31;
     const int kp = tid & 31, grp = tid >> 5;   // k pair, and 4 p's (L) / 16 q's (Rm) per thread
-    const int qq = q0 + 16 * grp;             // in the pair's first column block
+    const int qq = q0 + 16 * grp;             // in the item's first column block
     const rsrc_t rr = make_rsrc(J.Rm, (uint64_t)J.r_rows * J.ldr * 2);
     const int64_t ldr = J.ldr;
     const int r_gather = J.r_gather, use_w = J.use_w;
     const uint16_t* __restrict__ Lp = J.L;
-    f32x16_t acc0 = f32x16_t{}, acc1 = f32x16_t{};   // the pair's two column blocks
+    f32x16_t acc[WG_CBI];   // the item's column blocks
+#pragma unroll
+    for (int cb = 0; cb < WG_CBI; ++cb) acc[cb] = f32x16_t{};
     // raw data of one step for this thread: L rows (ra, ra+1) x 4 p, Rm rows (ra, ra+1) x 16 q, the row weights;
     // WG_PF steps are in flight (a register ring rotated by unrolling): a long group (the shared MLP's T rows) is bound
     // by the load latency, not by its few MFMAs.
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
     };
     const uint32_t ldl2 = (uint32_t)J.ldl * 2;              // L row pitch in bytes
     const rsrc_t rl = make_rsrc(Lp, (uint64_t)a1 * ldl2);  // L rows [0, a1): a row past the group reads zeros
-    // branch-free: rows past the window, and a column block past the pair, get out-of-range offsets (zeros) and
+    // branch-free: rows past the window, and a column block past the item's, get out-of-range offsets (zeros) and
     // weight 0
     auto load = [&](int k0, int w0, int w1, int cb, Raw& R) {
       const int qc = qq + WG_QB * cb;
@@ -500,7 +503,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
       __syncthreads();   // the previous window's table and tiles are no longer read
       build(w0, w1);
       __syncthreads();
-      // virtual steps: v < S are column block 0's 64-row steps (S = whole rounds of WG_PF), S .. 2 S block 1's
+      // virtual steps: [cb S, (cb + 1) S) are column block cb's 64-row steps (S = whole rounds of WG_PF)
       const int S = (w1 - w0 + 64 * WG_PF - 1) / (64 * WG_PF) * WG_PF;
       auto vload = [&](int v, Raw& R) {
         const int cb = v / S;   // >= ncb past the last step: zeros
@@ -510,7 +513,7 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
       for (int u = 0; u < WG_PF; ++u) vload(u, rw[u]);
       // WG_PF steps per round, branch-free (a step past the window stages zeros and adds nothing), so the compiler's
       // wait for a ring slot counts exactly the loads issued after it
-      auto round = [&](int v0, f32x16_t& acc) {
+      auto round = [&](int v0, f32x16_t& ac) {
 #pragma unroll
         for (int u = 0; u < WG_PF; ++u) {
           const int buf = u & 1;
@@ -521,26 +524,28 @@ __global__ __launch_bounds__(256) void lora_wgrad_kernel(WgArgs a) {
           for (int s = 0; s < 4; ++s) {
             const u32x4_t af = *reinterpret_cast<const u32x4_t*>(LT[buf] + r32 * WG_S + 32 * hi + 8 * s);
             const u32x4_t bfr = *reinterpret_cast<const u32x4_t*>(RT[buf] + (32 * w + r32) * WG_S + 32 * hi + 8 * s);
-            acc = mfma32(af, bfr, acc);
+            ac = mfma32(af, bfr, ac);
           }
         }
       };
-      for (int v0 = 0; v0 < S; v0 += WG_PF) round(v0, acc0);
-      if (ncb > 1)   // uniform
-        for (int v0 = S; v0 < 2 * S; v0 += WG_PF) round(v0, acc1);
+#pragma unroll
+      for (int cb = 0; cb < WG_CBI; ++cb)
+        if (cb < ncb)   // uniform
+          for (int v0 = cb * S; v0 < (cb + 1) * S; v0 += WG_PF) round(v0, acc[cb]);
     }
-    auto put = [&](const f32x16_t& acc, int qbc) {
+    auto put = [&](const f32x16_t& ac, int qbc) {
       if (nch == 1) {
-        wg_store(J, a.n_sel, i, qbc * WG_QB, w, l, acc);
+        wg_store(J, a.n_sel, i, qbc * WG_QB, w, l, ac);
       } else {
         // a group of several chunks: this chunk's partial tile, summed in chunk order by lora_wgrad_reduce
         float* tile = a.ws + ((int64_t)(a.qb0[jb] + qbc) * a.tot + sl) * (32 * WG_QB);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = acc[r];
+        for (int r = 0; r < 16; ++r) tile[r * 256 + tid] = ac[r];
       }
     };
-    put(acc0, qb);
-    if (ncb > 1) put(acc1, qb + 1);
+#pragma unroll
+    for (int cb = 0; cb < WG_CBI; ++cb)
+      if (cb < ncb) put(acc[cb], qb + cb);
   }
 }
 
@@ -764,7 +769,7 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
       a.job[j] = J;
       const int nqbj = (int)((J.Q + WG_QB - 1) / WG_QB);
       qbs += nqbj;
-      pbs += (nqbj + 1) / 2;
+      pbs += (nqbj + WG_CBI - 1) / WG_CBI;
     } else {
       a.job[j] = smel_wg_job{};
       a.job[j].Q = WG_QB;
@@ -784,7 +789,7 @@ extern "C" int smel_lora_wgrad(const smel_wg_job* jobs, int32_t n_jobs, const in
   a.order = order;
   a.topv = topv;
   a.sgate = sgate;
-  // persistent blocks over the (column-block pair, chunk slot) items in use: at most two per CU
+  // persistent blocks over the (column-block group, chunk slot) items in use: at most two per CU
   const int64_t bound = (int64_t)pbs * a.tot;
   lora_wgrad_kernel<<<(unsigned)std::min<int64_t>(bound, 2 * smel::cu_count()), 256, 0, stream>>>(a);
   int st = smel::launch_status();
