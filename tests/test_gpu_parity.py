@@ -556,6 +556,9 @@ LAYERS = {
                       lora_b_std=0.05, r_shared=8),
     "r32_shared_split": dict(T=260, H=256, E=16, I=128, K=4, n_sel=2, r=32, alpha=32.0, shared_inter=192, group=64,
                              lora_b_std=0.05),
+    # a rank that is not a multiple of 4: the LoRA gradients' stores of ragged rank groups and unaligned rows
+    "r6": dict(T=280, H=256, E=16, I=128, K=4, n_sel=3, r=6, alpha=12.0, shared_inter=128, group=64,
+               lora_b_std=0.05),
 }
 
 
